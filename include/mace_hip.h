@@ -1,0 +1,113 @@
+/*
+ * mace_hip.h — C ABI of libmace_hip.so, the MI355X (gfx950) backend of mace_hip_kernels.
+ *
+ * The reference (Yike-Ye/mace-mps-kernels) JIT-compiles one generated Metal library per layer with
+ * torch.mps.compile_shader and calls its kernels as lib.<kernel>(tensors..., n, threads=...).  This library is the
+ * HIP replacement of that boundary: per-layer HIP source (generated in Python with the layer's coupling
+ * coefficients as literals) is compiled by hipRTC into a gfx950 code object, loaded as a module, and its kernels are
+ * launched on the caller's HIP stream.  Plain pointers and sizes only; no torch types.
+ *
+ * Conventions
+ *   - Every function returns 0 on success or a nonzero hipError_t / hiprtcResult code; mh_last_error() then holds a
+ *     message (per calling thread).
+ *   - All device pointers are caller-owned (torch allocations); the library never allocates or frees tensor memory
+ *     and never synchronises the stream.  Inputs must be contiguous fp32 / int32 in the layouts below.
+ *   - A module is bound to the device that was current when it was loaded; launching it with another device current
+ *     is an error.  Module handles are immutable after mh_module_bind, so concurrent launches are safe.
+ *
+ * Layouts (e3nn "mul_ir"), MUL channels, NINS instructions:
+ *   x   [N, X_DIM]       node features, block b at x_off[b] + u*(2l_b+1) + m
+ *   Y   [E, Y_DIM]       edge spherical harmonics
+ *   W   [E, NINS*MUL]    per-edge weights, instruction k / channel u at k*MUL + u
+ *   out [N, OUT_DIM]     instruction k output block at o_off[k] + u*(2l_k+1) + m;  out[n] = Σ_{e: recv(e)=n} TP(...)
+ *   X   [N, C, N_ELL]    symmetric-contraction input;  T [n_elem, R, C] polynomial table;  elem [N] int32
+ */
+#ifndef MACE_HIP_H
+#define MACE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mh_module mh_module;
+
+/* kernel slots a module can bind (mh_module_bind) */
+enum mh_kernel_kind {
+    MH_CONV_FWD = 0,     /* receiver rows over the receiver CSR                                   */
+    MH_CONV_BWD = 1,     /* fused d/dx, d/dW, d/dY: sender rows over the sender CSR               */
+    MH_CONV_BWD_WY = 2,  /* d/dW, d/dY only: chunks of consecutive edges, no CSR                  */
+    MH_SC_FWD = 3,       /* node rows                                                             */
+    MH_SC_BWD = 4,       /* node rows                                                             */
+    MH_NUM_KINDS = 5
+};
+
+/* flags of mh_conv_bwd */
+#define MH_WANT_GX 1
+#define MH_WANT_GWY 2
+
+/* Message of the last failing call on this thread ("" if none).  No reference counterpart (Metal errors surface
+ * from torch there). */
+const char* mh_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int mh_version(void);
+
+/* Path of the HIP runtime library this .so is bound to (must be the one torch loaded). */
+const char* mh_hip_runtime_path(void);
+
+/* hipRTC-compile `source` with space-separated `options` into a code object (malloc'ed, release with
+ * mh_free_code).  Needs no GPU.  Replaces the compile half of torch.mps.compile_shader (reference conv.py:280,
+ * symmetric.py:165). */
+int mh_compile(const char* source, const char* options, void** code, size_t* code_size);
+void mh_free_code(void* code);
+
+/* Load a code object on the current device.  Replaces the load half of torch.mps.compile_shader. */
+int mh_module_load(const void* code, size_t code_size, mh_module** out);
+int mh_module_unload(mh_module* m);
+
+/* Attach kernel `name` of the module to slot `kind` with its launch shape: `block_threads` threads per workgroup,
+ * each workgroup covering `rows_per_block` rows of the launch (receivers, senders, nodes or edges).  Replaces the
+ * threads=/group_size= launch arguments of the reference (conv.py:247, 264, 269; symmetric.py:140, 154). */
+int mh_module_bind(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block);
+
+/* Fused convolution forward: out[n] = Σ_{p in rowptr[n]..rowptr[n+1]} TP(x[senders[e]], Y[e], W[e]), e = eids[p].
+ * rowptr/eids: receiver-sorted CSR.  Replaces lib.conv_fwd (reference conv.py:109-141, launched at conv.py:247). */
+int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
+                const int32_t* eids, const int32_t* senders, float* out, int32_t N, void* stream);
+
+/* d/dx only, over the sender-sorted CSR: gx[s] = Σ_{e: sender(e)=s} ∂TP/∂x · g[receivers[e]].
+ * Replaces lib.conv_bwd_x (reference conv.py:144-176, launched at conv.py:264).  Runs the MH_CONV_BWD kernel with
+ * flags = MH_WANT_GX. */
+int mh_conv_bwd_x(mh_module* m, const float* g, const float* Y, const float* W, const int32_t* rowptr_s,
+                  const int32_t* eids_s, const int32_t* receivers, float* gx, int32_t N, void* stream);
+
+/* d/dW and d/dY per edge: gW[e, k*MUL+u] = ∂TP/∂W · g[recv(e)],  gY[e, j] = Σ_u W·∂TP/∂Y · g[recv(e)].
+ * Replaces lib.conv_bwd_wy (reference conv.py:179-222, launched at conv.py:269). */
+int mh_conv_bwd_wy(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                   const int32_t* senders, const int32_t* receivers, float* gW, float* gY, int32_t E, void* stream);
+
+/* Fused backward over the sender-sorted CSR: one pass computes any of gx (flags & MH_WANT_GX) and gW, gY
+ * (flags & MH_WANT_GWY), reading W and g once.  Outputs not wanted may be NULL.  This is the path
+ * mace_hip_kernels uses; it replaces the pair lib.conv_bwd_x + lib.conv_bwd_wy (reference conv.py:252-270). */
+int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* receivers, float* gx, float* gW,
+                float* gY, int32_t N, int32_t flags, void* stream);
+
+/* Symmetric contraction forward: out[b, off + c*M + m] = Σ_terms T[elem[b], r0+m, c] Π X[b, c, idx].
+ * Replaces lib.sc_fwd (reference symmetric.py:82-105, launched at symmetric.py:140). */
+int mh_sc_fwd(mh_module* m, const float* X, const int32_t* elem, const float* T, float* out, int32_t N,
+              void* stream);
+
+/* Symmetric contraction backward: GX[b, c, i] = Σ_terms (Σ_m T·G) ∂(Π X)/∂X_i.
+ * Replaces lib.sc_bwd (reference symmetric.py:106-131, launched at symmetric.py:154). */
+int mh_sc_bwd(mh_module* m, const float* X, const int32_t* elem, const float* T, const float* G, float* GX,
+              int32_t N, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MACE_HIP_H */

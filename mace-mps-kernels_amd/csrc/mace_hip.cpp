@@ -1,0 +1,219 @@
+// libmace_hip.so — host runtime behind include/mace_hip.h.
+//
+// hipRTC compiles per-layer generated HIP source into a gfx950 code object; the code object is loaded as a
+// hipModule on the current device; kernels are launched with hipModuleLaunchKernel on the caller's stream.  This
+// replaces torch.mps.compile_shader + lib.<kernel>(..., threads=) of the reference (conv.py:247, 264, 269, 280;
+// symmetric.py:140, 154, 165).
+//
+// The library links libamdhip64.so.7 / libhiprtc.so.7 by soname; loaded into a process that has imported torch, the
+// dynamic linker resolves them to torch's bundled copies, so modules, streams and allocations share one HIP
+// runtime.  mh_hip_runtime_path() reports which file was bound so the Python side can verify it.
+#include <dlfcn.h>
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/mace_hip.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+struct Kernel {
+    hipFunction_t fn = nullptr;
+    int block = 0;
+    int rows_per_block = 1;
+};
+
+}  // namespace
+
+struct mh_module {
+    hipModule_t mod = nullptr;
+    int device = -1;
+    Kernel k[MH_NUM_KINDS];
+};
+
+namespace {
+
+int fail(int code, const std::string& what) {
+    g_err = what;
+    return code ? code : -1;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    std::ostringstream os;
+    os << what << ": " << hipGetErrorName(e) << " (" << hipGetErrorString(e) << ")";
+    return fail(static_cast<int>(e), os.str());
+}
+
+#define MH_HIP(call)                                   \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+// Launch `kind` over `rows` rows; args are the kernel's parameters in order.
+int launch(mh_module* m, int kind, int64_t rows, void** args, void* stream, const char* what) {
+    if (!m) return fail(-1, std::string(what) + ": null module");
+    const Kernel& k = m->k[kind];
+    if (!k.fn) return fail(-1, std::string(what) + ": kernel slot not bound in this module");
+    if (rows < 0) return fail(-1, std::string(what) + ": negative size");
+    if (rows == 0) return 0;
+    int dev = -1;
+    MH_HIP(hipGetDevice(&dev));
+    if (dev != m->device) {
+        std::ostringstream os;
+        os << what << ": module was loaded on device " << m->device << " but device " << dev << " is current";
+        return fail(-1, os.str());
+    }
+    int64_t grid = (rows + k.rows_per_block - 1) / k.rows_per_block;
+    if (grid > 0x7fffffffLL) return fail(-1, std::string(what) + ": launch too large");
+    hipError_t e = hipModuleLaunchKernel(k.fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(k.block), 1, 1,
+                                         0, static_cast<hipStream_t>(stream), args, nullptr);
+    if (e != hipSuccess) return hip_fail(e, what);
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mh_last_error(void) { return g_err.c_str(); }
+
+int mh_version(void) { return 1; }
+
+const char* mh_hip_runtime_path(void) {
+    static std::string path;
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&hipModuleLaunchKernel), &info) && info.dli_fname) path = info.dli_fname;
+    return path.c_str();
+}
+
+int mh_compile(const char* source, const char* options, void** code, size_t* code_size) {
+    if (!source || !code || !code_size) return fail(-1, "mh_compile: null argument");
+    *code = nullptr;
+    *code_size = 0;
+    hiprtcProgram prog;
+    hiprtcResult r = hiprtcCreateProgram(&prog, source, "mace_hip_layer.hip", 0, nullptr, nullptr);
+    if (r != HIPRTC_SUCCESS) return fail(static_cast<int>(r), std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+    std::vector<std::string> opts;
+    if (options) {
+        std::istringstream is(options);
+        std::string o;
+        while (is >> o) opts.push_back(o);
+    }
+    std::vector<const char*> optp;
+    for (auto& o : opts) optp.push_back(o.c_str());
+    r = hiprtcCompileProgram(prog, static_cast<int>(optp.size()), optp.data());
+    size_t log_size = 0;
+    hiprtcGetProgramLogSize(prog, &log_size);
+    std::string log(log_size, '\0');
+    if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+    if (r != HIPRTC_SUCCESS) {
+        hiprtcDestroyProgram(&prog);
+        return fail(static_cast<int>(r), std::string("hiprtcCompileProgram: ") + hiprtcGetErrorString(r) + "\n" + log);
+    }
+    size_t n = 0;
+    r = hiprtcGetCodeSize(prog, &n);
+    if (r != HIPRTC_SUCCESS || n == 0) {
+        hiprtcDestroyProgram(&prog);
+        return fail(static_cast<int>(r), "hiprtcGetCodeSize failed");
+    }
+    void* buf = std::malloc(n);
+    if (!buf) {
+        hiprtcDestroyProgram(&prog);
+        return fail(-1, "mh_compile: out of host memory");
+    }
+    r = hiprtcGetCode(prog, static_cast<char*>(buf));
+    hiprtcDestroyProgram(&prog);
+    if (r != HIPRTC_SUCCESS) {
+        std::free(buf);
+        return fail(static_cast<int>(r), std::string("hiprtcGetCode: ") + hiprtcGetErrorString(r));
+    }
+    *code = buf;
+    *code_size = n;
+    return 0;
+}
+
+void mh_free_code(void* code) { std::free(code); }
+
+int mh_module_load(const void* code, size_t code_size, mh_module** out) {
+    if (!code || !code_size || !out) return fail(-1, "mh_module_load: null argument");
+    *out = nullptr;
+    mh_module* m = new mh_module();
+    hipError_t e = hipGetDevice(&m->device);
+    if (e == hipSuccess) e = hipModuleLoadData(&m->mod, code);
+    if (e != hipSuccess) {
+        delete m;
+        return hip_fail(e, "hipModuleLoadData");
+    }
+    *out = m;
+    return 0;
+}
+
+int mh_module_unload(mh_module* m) {
+    if (!m) return 0;
+    hipError_t e = m->mod ? hipModuleUnload(m->mod) : hipSuccess;
+    delete m;
+    if (e != hipSuccess) return hip_fail(e, "hipModuleUnload");
+    return 0;
+}
+
+int mh_module_bind(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block) {
+    if (!m || !name) return fail(-1, "mh_module_bind: null argument");
+    if (kind < 0 || kind >= MH_NUM_KINDS) return fail(-1, "mh_module_bind: bad kernel kind");
+    if (block_threads <= 0 || block_threads > 1024 || block_threads % 64 || rows_per_block <= 0)
+        return fail(-1, "mh_module_bind: bad launch shape");
+    hipFunction_t fn = nullptr;
+    MH_HIP(hipModuleGetFunction(&fn, m->mod, name));
+    m->k[kind].fn = fn;
+    m->k[kind].block = block_threads;
+    m->k[kind].rows_per_block = rows_per_block;
+    return 0;
+}
+
+int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
+                const int32_t* eids, const int32_t* senders, float* out, int32_t N, void* stream) {
+    void* args[] = {&x, &Y, &W, &rowptr, &eids, &senders, &out, &N};
+    return launch(m, MH_CONV_FWD, N, args, stream, "mh_conv_fwd");
+}
+
+int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* receivers, float* gx, float* gW,
+                float* gY, int32_t N, int32_t flags, void* stream) {
+    if ((flags & MH_WANT_GX) && !gx) return fail(-1, "mh_conv_bwd: gx requested but NULL");
+    if ((flags & MH_WANT_GWY) && (!gW || !gY || !x)) return fail(-1, "mh_conv_bwd: gW/gY requested but NULL");
+    if (!(flags & (MH_WANT_GX | MH_WANT_GWY))) return 0;
+    void* args[] = {&x, &g, &Y, &W, &rowptr_s, &eids_s, &receivers, &gx, &gW, &gY, &N, &flags};
+    return launch(m, MH_CONV_BWD, N, args, stream, "mh_conv_bwd");
+}
+
+int mh_conv_bwd_x(mh_module* m, const float* g, const float* Y, const float* W, const int32_t* rowptr_s,
+                  const int32_t* eids_s, const int32_t* receivers, float* gx, int32_t N, void* stream) {
+    return mh_conv_bwd(m, nullptr, g, Y, W, rowptr_s, eids_s, receivers, gx, nullptr, nullptr, N, MH_WANT_GX, stream);
+}
+
+int mh_conv_bwd_wy(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                   const int32_t* senders, const int32_t* receivers, float* gW, float* gY, int32_t E, void* stream) {
+    void* args[] = {&x, &g, &Y, &W, &senders, &receivers, &gW, &gY, &E};
+    return launch(m, MH_CONV_BWD_WY, E, args, stream, "mh_conv_bwd_wy");
+}
+
+int mh_sc_fwd(mh_module* m, const float* X, const int32_t* elem, const float* T, float* out, int32_t N,
+              void* stream) {
+    void* args[] = {&X, &elem, &T, &out, &N};
+    return launch(m, MH_SC_FWD, N, args, stream, "mh_sc_fwd");
+}
+
+int mh_sc_bwd(mh_module* m, const float* X, const int32_t* elem, const float* T, const float* G, float* GX,
+              int32_t N, void* stream) {
+    void* args[] = {&X, &elem, &T, &G, &GX, &N};
+    return launch(m, MH_SC_BWD, N, args, stream, "mh_sc_bwd");
+}
+
+}  // extern "C"

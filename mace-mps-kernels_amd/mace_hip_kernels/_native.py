@@ -1,0 +1,135 @@
+"""
+ctypes binding of ``libmace_hip.so`` (declared in ``include/mace_hip.h``).
+
+The library is built in-tree (``__graft_entry__.build()``) next to this file.  It must be loaded after torch so that
+its ``libamdhip64.so.7`` / ``libhiprtc.so.7`` dependencies resolve to the copies torch already mapped; ``load()``
+verifies that.  There is no fallback: a missing or broken library raises.
+"""
+import ctypes
+import hashlib
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, 'libmace_hip.so')
+DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
+
+MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD = range(5)
+MH_WANT_GX, MH_WANT_GWY = 1, 2
+ABI_VERSION = 1
+
+# hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
+ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
+COMPILE_OPTIONS = f'--offload-arch={ARCH} -O3 -std=c++17 -Xclang -target-feature -Xclang -packed-fp32-ops'
+
+_lib = None
+_lock = threading.Lock()
+_code_cache = {}
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int32
+_SIGS = {
+    'mh_last_error': (ctypes.c_char_p, []),
+    'mh_version': (ctypes.c_int, []),
+    'mh_hip_runtime_path': (ctypes.c_char_p, []),
+    'mh_compile': (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_P), ctypes.POINTER(ctypes.c_size_t)]),
+    'mh_free_code': (None, [_P]),
+    'mh_module_load': (ctypes.c_int, [_P, ctypes.c_size_t, ctypes.POINTER(_P)]),
+    'mh_module_unload': (ctypes.c_int, [_P]),
+    'mh_module_bind': (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.c_int]),
+    'mh_conv_fwd': (ctypes.c_int, [_P] * 8 + [_I, _P]),
+    'mh_conv_bwd_x': (ctypes.c_int, [_P] * 8 + [_I, _P]),
+    'mh_conv_bwd_wy': (ctypes.c_int, [_P] * 9 + [_I, _P]),
+    'mh_conv_bwd': (ctypes.c_int, [_P] * 11 + [_I, _I, _P]),
+    'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
+    'mh_sc_bwd': (ctypes.c_int, [_P] * 6 + [_I, _P]),
+}
+EXPORTS = tuple(_SIGS)
+
+
+def load():
+    """The bound library (loaded once).  Raises if it is missing, stale or bound to a foreign HIP runtime."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f'mace_hip_kernels: {LIB_PATH} is missing; build it with __graft_entry__.build()')
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.mh_version() != ABI_VERSION:
+            raise RuntimeError('mace_hip_kernels: libmace_hip.so ABI version mismatch; rebuild it')
+        rt = lib.mh_hip_runtime_path().decode()
+        torch_lib = os.path.realpath(os.path.join(os.path.dirname(torch.__file__), 'lib'))
+        if rt and os.path.dirname(os.path.realpath(rt)) != torch_lib:
+            raise RuntimeError(f'mace_hip_kernels: libmace_hip.so bound HIP runtime {rt}, not the one torch loaded '
+                               f'from {torch_lib}; import torch before mace_hip_kernels')
+        _lib = lib
+    return _lib
+
+
+def check(rc, what=''):
+    if rc != 0:
+        msg = load().mh_last_error().decode(errors='replace')
+        raise RuntimeError(f'mace_hip_kernels: {what} failed (code {rc}): {msg}')
+
+
+def device_header():
+    with open(DEVICE_HEADER) as f:
+        return f.read()
+
+
+def compile_source(source):
+    """hipRTC-compile ``source`` → code-object bytes (cached per process by source hash; no GPU needed)."""
+    key = hashlib.sha256((COMPILE_OPTIONS + '\0' + source).encode()).hexdigest()
+    if key in _code_cache:
+        return _code_cache[key]
+    lib = load()
+    code, size = _P(), ctypes.c_size_t()
+    check(lib.mh_compile(source.encode(), COMPILE_OPTIONS.encode(), ctypes.byref(code), ctypes.byref(size)),
+          'hipRTC compile')
+    try:
+        data = ctypes.string_at(code, size.value)
+    finally:
+        lib.mh_free_code(code)
+    _code_cache[key] = data
+    return data
+
+
+class Module:
+    """A loaded per-layer code object with its kernels bound to launch slots (owned; unloaded on deletion)."""
+
+    def __init__(self, code, kernels):
+        lib = load()
+        self._lib = lib
+        self.handle = _P()
+        self._code = code
+        buf = ctypes.create_string_buffer(code, len(code))
+        check(lib.mh_module_load(buf, len(code), ctypes.byref(self.handle)), 'module load')
+        self.device = torch.cuda.current_device()
+        for kind, (name, block, rows) in kernels.items():
+            check(lib.mh_module_bind(self.handle, kind, name.encode(), block, rows), f'bind {name}')
+
+    def __del__(self):
+        h = getattr(self, 'handle', None)
+        if h is not None and h.value and getattr(self, '_lib', None) is not None:
+            try:
+                self._lib.mh_module_unload(h)
+            except Exception:  # noqa: BLE001  (interpreter shutdown)
+                pass
+
+
+def ptr(t):
+    """Device pointer of a tensor (None → NULL)."""
+    return None if t is None else _P(t.data_ptr())
+
+
+def stream_of(t):
+    return _P(torch.cuda.current_stream(t.device).cuda_stream)

@@ -1,0 +1,527 @@
+"""
+Fused MACE interaction convolution on MI355X: gather → channel-wise ('uvu') tensor product → scatter-sum, one
+generated HIP module per e3nn ``TensorProduct`` (reference conv.py).
+
+Coefficients.  The effective coefficient of every path (Clebsch-Gordan × e3nn normalisation × path weight) is
+probed from the TensorProduct itself with unit inputs (reference conv.py:57-88) — here on a float64 CPU copy, so the
+literals baked into the kernel are exact to fp32 rounding rather than fp32-probed.
+
+Kernels (all deterministic, no atomics; one lane per channel, 64-lane wavefronts, ceil(MUL/64) waves per row):
+  * ``conv_fwd``  one workgroup per receiver n walks the receiver-sorted CSR; per edge the wave loads its W row
+    slice (coalesced), the sender's x slice, and Y[e] as wave-uniform scalars; accumulators stay in registers and
+    the [N, OUT_DIM] output is written once (reference conv.py:109-141).
+  * ``conv_bwd``  one workgroup per sender s walks the sender-sorted CSR and produces, in one pass, gx[s]
+    (reference conv.py:144-176) and gW[e], gY[e] (reference conv.py:179-222): W and g[receiver] are read once
+    instead of twice, x[s] is loaded once per sender.  gY[e, j] = Σ_u (…) is reduced over the wave by a transpose
+    reduction and over the workgroup's waves through LDS, in a fixed order.
+  * ``conv_bwd_wy`` the per-edge d/dW, d/dY kernel of the reference's C ABI (no CSR): 64 consecutive edges per
+    workgroup.
+
+Layouts are the reference's (conv.py:9-14): x [N, X_DIM] mul_ir, Y [E, Y_DIM], W [E, NINS*MUL] (instruction k,
+channel u at k*MUL+u), out [N, OUT_DIM].  ``edge_index = [sender, receiver]``.
+"""
+import copy
+import math
+import weakref
+
+import numpy as np
+import torch
+
+from . import _native
+
+WAVE = 64
+
+
+def _blocks(irreps):
+    res, off = [], 0
+    for mul, ir in irreps:
+        res.append((ir.l, mul, off))
+        off += mul * (2 * ir.l + 1)
+    return res, off
+
+
+def conv_supported(tp):
+    """(ok, reason) — whether an e3nn TensorProduct can be replaced by the fused convolution (reference conv.py:31-51).
+    """
+    try:
+        ins = tp.instructions
+        if any(i.connection_mode != 'uvu' or not i.has_weight for i in ins):
+            return False, 'only weighted uvu instructions are supported'
+        if getattr(tp, 'shared_weights', True) or getattr(tp, 'internal_weights', True):
+            return False, 'per-edge (external, unshared) weights required'
+        muls = {m for m, _ in tp.irreps_in1} | {m for m, _ in tp.irreps_out}
+        if len(muls) != 1:
+            return False, 'all node/out blocks must have the same multiplicity'
+        mul = muls.pop()
+        if mul % 32:
+            return False, f'multiplicity {mul} is not a multiple of 32'
+        if any(m != 1 for m, _ in tp.irreps_in2):
+            return False, 'edge attributes must have multiplicity 1 per l'
+        if tp.weight_numel != len(ins) * mul:
+            return False, 'unexpected weight layout'
+        if tp.irreps_in2.dim > WAVE:
+            return False, f'edge attribute dimension {tp.irreps_in2.dim} > {WAVE}'
+        if len({i.i_out for i in ins}) != len(ins):
+            return False, 'each output block must come from exactly one instruction'
+    except AttributeError as e:
+        return False, f'not an e3nn TensorProduct ({e})'
+    return True, ''
+
+
+def _probe_tp(tp):
+    """(callable, device, dtype) used for probing: a float64 CPU copy when the TP can be copied, else the TP itself."""
+    try:
+        cp = copy.deepcopy(tp).to(device='cpu', dtype=torch.float64)
+        return cp, torch.device('cpu'), torch.float64
+    except Exception:  # noqa: BLE001  (an exotic TP that cannot be copied: probe it where it lives, like the reference)
+        dev = next(iter(tp.buffers()), torch.zeros(1)).device
+        return tp, dev, torch.get_default_dtype()
+
+
+class ConvSpec:
+    """Instruction table and effective path coefficients of one 'uvu' TensorProduct (reference conv.py:54-102)."""
+
+    def __init__(self, tp, tol=1e-10):
+        ok, why = conv_supported(tp)
+        if not ok:
+            raise ValueError(why)
+        self.in1, self.x_dim = _blocks(tp.irreps_in1)
+        self.in2, self.y_dim = _blocks(tp.irreps_in2)
+        self.outb, self.out_dim = _blocks(tp.irreps_out)
+        self.mul = self.in1[0][1]
+        self.ins = [(i.i_in1, i.i_in2, i.i_out) for i in tp.instructions]
+        self.nins = len(self.ins)
+        probe, dev, dt = _probe_tp(tp)
+        self.coef = []
+        for k, (i1, i2, io) in enumerate(self.ins):
+            l1, _, o1 = self.in1[i1]
+            l2, _, o2 = self.in2[i2]
+            l3, _, o3 = self.outb[io]
+            d1, d2, d3 = 2 * l1 + 1, 2 * l2 + 1, 2 * l3 + 1
+            x1 = torch.zeros(d1 * d2, self.x_dim, device=dev, dtype=dt)
+            x2 = torch.zeros(d1 * d2, self.y_dim, device=dev, dtype=dt)
+            w = torch.zeros(d1 * d2, tp.weight_numel, device=dev, dtype=dt)
+            for a in range(d1):
+                for b in range(d2):
+                    r = a * d2 + b
+                    x1[r, o1 + a] = 1.0          # channel u = 0
+                    x2[r, o2 + b] = 1.0
+                    w[r, k * self.mul] = 1.0
+            with torch.no_grad():
+                y = probe(x1, x2, w)[:, o3:o3 + d3].double().cpu().reshape(d1, d2, d3)
+            terms = [(a, b, c, float(y[a, b, c])) for a in range(d1) for b in range(d2) for c in range(d3)
+                     if abs(float(y[a, b, c])) > tol]
+            self.coef.append(dict(k=k, l1=l1, l2=l2, l3=l3, o1=o1, o2=o2, o3=o3, d1=d1, d2=d2, d3=d3, terms=terms))
+        self.nnz = sum(len(c['terms']) for c in self.coef)
+        self.ncb = (self.mul + WAVE - 1) // WAVE
+        self.block = self.ncb * WAVE
+        self.y_pad = 1 << max(0, (self.y_dim - 1).bit_length())
+
+    def xreg(self):
+        r, idx = 0, {}
+        for b, (l, _, _) in enumerate(self.in1):
+            idx[b] = r
+            r += 2 * l + 1
+        return idx, r
+
+    def oreg(self):
+        r, idx = 0, {}
+        for c in self.coef:
+            idx[c['k']] = r
+            r += 2 * c['l3'] + 1
+        return idx, r
+
+    # ---------------------------------------------------------------------------------------- cost model
+    def flops(self):
+        """(fwd, bwd) fp32 FLOP per real edge per channel as the generated code evaluates them."""
+        nnz = self.nnz
+        pairs = sum(len({(a, c) for a, _, c, _ in co['terms']}) for co in self.coef)
+        d3 = sum(co['d3'] for co in self.coef)
+        d1 = sum(co['d1'] for co in self.coef)
+        fwd = 2 * nnz + 2 * pairs + 2 * d3
+        bwd = (2 * nnz + 2 * d1) + (2 * d1) + (4 * nnz + 2 * self.y_dim)   # h (gx), gW, gY partials
+        return fwd, bwd
+
+    def bytes(self, n_nodes, n_edges):
+        """Algorithmic HBM bytes (fwd, bwd) of one call: every tensor read or written once, 4 B per element."""
+        nw = self.nins * self.mul
+        fwd = 4 * (n_edges * (nw + self.y_dim + 2) + n_nodes * (self.x_dim + self.out_dim) + (n_nodes + 1))
+        bwd = 4 * (n_edges * (2 * nw + 2 * self.y_dim + 4) + n_nodes * (2 * self.x_dim + self.out_dim)
+                   + 2 * (n_nodes + 1))
+        return fwd, bwd
+
+
+# ------------------------------------------------------------------------------------------------- codegen
+def _lit(v):
+    """Hexadecimal fp32 literal holding exactly float32(v) (round to nearest)."""
+    return f'{float(np.float32(v)).hex()}f'
+
+
+def _sum(parts):
+    return ' + '.join(parts) if parts else '0.0f'
+
+
+def _load_y(spec, indent):
+    return [f'{indent}const float* __restrict__ ye = Y + (size_t)e * {spec.y_dim};'] + \
+           [f'{indent}const float y{j} = ye[{j}];' for j in range(spec.y_dim)]
+
+
+def _load_x(spec, indent, src='s'):
+    xi, _ = spec.xreg()
+    out = [f'{indent}const float* __restrict__ xs = x + (size_t){src} * {spec.x_dim};']
+    for b, (l, _, off) in enumerate(spec.in1):
+        d = 2 * l + 1
+        out += [f'{indent}xv[{xi[b] + m}] = xs[{off} + uc * {d} + {m}];' for m in range(d)]
+    return out
+
+
+def _load_w(spec, indent):
+    out = [f'{indent}const float* __restrict__ we = W + (size_t)e * {spec.nins * spec.mul} + uc;']
+    out += [f'{indent}const float w{k} = we[{k * spec.mul}];' for k in range(spec.nins)]
+    return out
+
+
+def _fwd_body(spec, indent):
+    """acc[o] += w_k * Σ_a x[a] * (Σ_b v·y[b])  for every output component of every instruction."""
+    xi, _ = spec.xreg()
+    oi, _ = spec.oreg()
+    L = []
+    for co in spec.coef:
+        k, i1 = co['k'], spec.ins[co['k']][0]
+        for c in range(co['d3']):
+            by_a = {}
+            for a, b, cc, v in co['terms']:
+                if cc == c:
+                    by_a.setdefault(a, []).append(f'{_lit(v)} * y{co["o2"] + b}')
+            if not by_a:
+                continue
+            t = _sum([f'xv[{xi[i1] + a}] * ({_sum(ys)})' for a, ys in sorted(by_a.items())])
+            L.append(f'{indent}acc[{oi[k] + c}] = fmaf(w{k}, {t}, acc[{oi[k] + c}]);')
+    return L
+
+
+def _bwd_body(spec, indent, with_gx, store_gw):
+    """h_a = Σ_{b,c} v·y[b]·g[c];  gx[a] += w·h_a;  gW_k = Σ_a x[a]·h_a;  P[b] += w·Σ_{a,c} v·x[a]·g[c]."""
+    xi, _ = spec.xreg()
+    oi, _ = spec.oreg()
+    L = []
+    for co in spec.coef:
+        k, i1 = co['k'], spec.ins[co['k']][0]
+        L.append(f'{indent}{{')
+        hs = []
+        for a in range(co['d1']):
+            ts = [f'{_lit(v)} * y{co["o2"] + b} * gv[{oi[k] + c}]' for aa, b, c, v in co['terms'] if aa == a]
+            if not ts:
+                continue
+            L.append(f'{indent}  const float h{a} = {_sum(ts)};')
+            hs.append(a)
+            if with_gx:
+                L.append(f'{indent}  gxa[{xi[i1] + a}] = fmaf(w{k}, h{a}, gxa[{xi[i1] + a}]);')
+        if store_gw:
+            gw = _sum([f'xv[{xi[i1] + a}] * h{a}' for a in hs])
+            L.append(f'{indent}  if (GWY && active) gwe[{k * spec.mul}] = {gw};')
+            for b in range(co['d2']):
+                ts = [f'{_lit(v)} * xv[{xi[i1] + a}] * gv[{oi[k] + c}]' for a, bb, c, v in co['terms'] if bb == b]
+                if ts:
+                    L.append(f'{indent}  P[{co["o2"] + b}] = fmaf(w{k}, {_sum(ts)}, P[{co["o2"] + b}]);')
+        L.append(f'{indent}}}')
+    return L
+
+
+def _header(spec):
+    return [_native.device_header(),
+            f'#define MUL {spec.mul}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}',
+            f'#define X_DIM {spec.x_dim}', f'#define Y_DIM {spec.y_dim}', f'#define Y_PAD {spec.y_pad}',
+            f'#define OUT_DIM {spec.out_dim}', f'#define NW {spec.nins * spec.mul}']
+
+
+def _gy_combine(indent, edge_expr):
+    """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order)."""
+    return [
+        f'{indent}__syncthreads();',
+        f'{indent}for (int q = threadIdx.x; q < cnt * Y_DIM; q += BLOCK) {{',
+        f'{indent}  const int j = q / Y_DIM, b = q - j * Y_DIM;',
+        f'{indent}  float v = 0.0f;',
+        f'{indent}  for (int w = 0; w < NCB; ++w) v += part[w][j][b];',
+        f'{indent}  gY[(size_t)({edge_expr}) * Y_DIM + b] = v;',
+        f'{indent}}}',
+        f'{indent}__syncthreads();',
+    ]
+
+
+def _gy_reduce(indent):
+    return [
+        f'{indent}for (int b = Y_DIM; b < Y_PAD; ++b) P[b] = 0.0f;',
+        f'{indent}{{ const float tot = mh_wave_transpose_sum<Y_PAD>(P);',
+        f'{indent}  const int comp = lane >> (6 - {{LOG2P}});',
+        f'{indent}  if ((lane & ((1 << (6 - {{LOG2P}})) - 1)) == 0 && comp < Y_DIM) part[wave][j][comp] = tot; }}',
+    ]
+
+
+def source(spec):
+    """HIP source of the three convolution kernels of one layer."""
+    _, nx = spec.xreg()
+    _, no = spec.oreg()
+    log2p = spec.y_pad.bit_length() - 1
+    gyr = [s.replace('{LOG2P}', str(log2p)) for s in _gy_reduce('      ')]
+    L = _header(spec)
+    # ---------------------------------------------------------------------------------------- forward
+    L += [
+        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_fwd(',
+        '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
+        '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
+        '    float* __restrict__ out, int N) {',
+        '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
+        '  if (n >= N) return;',
+        '  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1);',
+        '  const bool active = u < MUL;',
+        '  const int uc = active ? u : MUL - 1;',
+        f'  float acc[{no}];',
+        f'  for (int i = 0; i < {no}; ++i) acc[i] = 0.0f;',
+        f'  float xv[{nx}];',
+        '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
+        '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
+        '    const int cnt = min(MH_WAVE, p1 - pb);',
+        '    int my_e = 0, my_s = 0;',
+        '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }',
+        '    for (int j = 0; j < cnt; ++j) {',
+        '      const int e = mh_bcast(my_e, j), s = mh_bcast(my_s, j);',
+    ]
+    L += _load_y(spec, '      ') + _load_x(spec, '      ') + _load_w(spec, '      ') + _fwd_body(spec, '      ')
+    L += ['    }', '  }', '  if (active) {', '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
+    oi, _ = spec.oreg()
+    for co in spec.coef:
+        L += [f'    o[{co["o3"]} + u * {co["d3"]} + {c}] = acc[{oi[co["k"]] + c}];' for c in range(co['d3'])]
+    L += ['  }', '}', '']
+    # ------------------------------------------------------------------------------- fused backward
+    L += [
+        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_bwd(',
+        '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
+        '    const float* __restrict__ W, const int* __restrict__ rowptr, const int* __restrict__ eids,',
+        '    const int* __restrict__ receivers, float* __restrict__ gx, float* __restrict__ gW,',
+        '    float* __restrict__ gY, int N, int flags) {',
+        '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
+        '  const int s = mh_xcd_block(blockIdx.x, gridDim.x);',
+        '  if (s >= N) return;',
+        '  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1), wave = threadIdx.x >> 6;',
+        '  const bool active = u < MUL;',
+        '  const int uc = active ? u : MUL - 1;',
+        '  const bool GX = (flags & 1) != 0, GWY = (flags & 2) != 0;',
+        f'  float xv[{nx}];',
+        f'  for (int i = 0; i < {nx}; ++i) xv[i] = 0.0f;',
+        '  if (GWY) {',
+    ]
+    L += _load_x(spec, '    ')
+    L += [
+        '  }',
+        f'  float gxa[{nx}];',
+        f'  for (int i = 0; i < {nx}; ++i) gxa[i] = 0.0f;',
+        f'  float gv[{no}];',
+        '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
+        '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
+        '    const int cnt = min(MH_WAVE, p1 - pb);',
+        '    int my_e = 0, my_r = 0;',
+        '    if (lane < cnt) { my_e = eids[pb + lane]; my_r = receivers[my_e]; }',
+        '    for (int j = 0; j < cnt; ++j) {',
+        '      const int e = mh_bcast(my_e, j), r = mh_bcast(my_r, j);',
+    ]
+    L += _load_y(spec, '      ') + _load_w(spec, '      ')
+    L += ['      const float* __restrict__ gr = g + (size_t)r * OUT_DIM;']
+    for co in spec.coef:
+        L += [f'      gv[{oi[co["k"]] + c}] = active ? gr[{co["o3"]} + uc * {co["d3"]} + {c}] : 0.0f;'
+              for c in range(co['d3'])]
+    L += ['      float P[Y_PAD];', '      for (int b = 0; b < Y_PAD; ++b) P[b] = 0.0f;',
+          '      float* __restrict__ gwe = gW + (size_t)e * NW + uc;']
+    L += _bwd_body(spec, '      ', with_gx=True, store_gw=True)
+    L += ['      if (GWY) {'] + ['  ' + s for s in gyr] + ['      }']
+    L += ['    }', '    if (GWY) {']
+    L += _gy_combine('      ', 'eids[pb + j]')
+    L += ['    }', '  }', '  if (GX && active) {', '    float* __restrict__ gxs = gx + (size_t)s * X_DIM;']
+    xi, _ = spec.xreg()
+    for b, (l, _, off) in enumerate(spec.in1):
+        d = 2 * l + 1
+        L += [f'    gxs[{off} + u * {d} + {m}] = gxa[{xi[b] + m}];' for m in range(d)]
+    L += ['  }', '}', '']
+    # ----------------------------------------------------------------- per-edge d/dW, d/dY (no CSR)
+    L += [
+        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_bwd_wy(',
+        '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
+        '    const float* __restrict__ W, const int* __restrict__ senders, const int* __restrict__ receivers,',
+        '    float* __restrict__ gW, float* __restrict__ gY, int E) {',
+        '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
+        '  const int pb = mh_xcd_block(blockIdx.x, gridDim.x) * MH_WAVE;',
+        '  if (pb >= E) return;',
+        '  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1), wave = threadIdx.x >> 6;',
+        '  const bool active = u < MUL;',
+        '  const int uc = active ? u : MUL - 1;',
+        '  const bool GWY = true;',
+        '  const int cnt = min(MH_WAVE, E - pb);',
+        f'  float xv[{nx}];',
+        f'  float gv[{no}];',
+        '  int my_s = 0, my_r = 0;',
+        '  if (lane < cnt) { my_s = senders[pb + lane]; my_r = receivers[pb + lane]; }',
+        '  for (int j = 0; j < cnt; ++j) {',
+        '    const int e = pb + j, s = mh_bcast(my_s, j), r = mh_bcast(my_r, j);',
+    ]
+    L += _load_y(spec, '    ') + _load_x(spec, '    ') + _load_w(spec, '    ')
+    L += ['    const float* __restrict__ gr = g + (size_t)r * OUT_DIM;']
+    for co in spec.coef:
+        L += [f'    gv[{oi[co["k"]] + c}] = active ? gr[{co["o3"]} + uc * {co["d3"]} + {c}] : 0.0f;'
+              for c in range(co['d3'])]
+    L += ['    float P[Y_PAD];', '    for (int b = 0; b < Y_PAD; ++b) P[b] = 0.0f;',
+          '    float* __restrict__ gwe = gW + (size_t)e * NW + uc;']
+    L += _bwd_body(spec, '    ', with_gx=False, store_gw=True)
+    L += [s[2:] for s in gyr]
+    L += ['  }']
+    L += _gy_combine('  ', 'pb + j')
+    L += ['}', '']
+    return '\n'.join(L)
+
+
+# ------------------------------------------------------------------------------------------- graph cache
+def csr_by(index, n):
+    """Edges sorted by ``index`` → (rowptr[n+1], edge ids) as int32 (reference conv.py:229-235)."""
+    order = torch.argsort(index, stable=True)
+    counts = torch.bincount(index, minlength=n)
+    rowptr = torch.zeros(n + 1, dtype=torch.int64, device=index.device)
+    rowptr[1:] = torch.cumsum(counts, 0)
+    return rowptr.to(torch.int32), order.to(torch.int32)
+
+
+class _Graph:
+    """int32 senders/receivers and both CSRs of one edge_index, built lazily and shared by every layer of a call."""
+
+    def __init__(self, edge_index, n):
+        if edge_index.dim() != 2 or edge_index.shape[0] != 2:
+            raise ValueError(f'edge_index must be [2, E], got {tuple(edge_index.shape)}')
+        if edge_index.numel():
+            # the kernels index x, g and the CSRs with these values: reject out-of-range nodes on the host
+            lo, hi = torch.aminmax(edge_index)
+            lo, hi = int(lo), int(hi)
+            if lo < 0 or hi >= n:
+                raise ValueError(f'edge_index holds node {lo if lo < 0 else hi} outside [0, {n})')
+        self.n = n
+        self.send = edge_index[0].to(torch.int32).contiguous()
+        self.recv = edge_index[1].to(torch.int32).contiguous()
+        self._by_recv = self._by_send = None
+        self._ei = edge_index
+
+    def by_recv(self):
+        if self._by_recv is None:
+            self._by_recv = csr_by(self._ei[1], self.n)
+        return self._by_recv
+
+    def by_send(self):
+        if self._by_send is None:
+            self._by_send = csr_by(self._ei[0], self.n)
+        return self._by_send
+
+
+_graph_cache = []          # [(weakref(edge_index), version, n, _Graph)], most recent first
+_GRAPH_CACHE_SIZE = 4
+
+
+def graph_for(edge_index, n):
+    """Cached ``_Graph`` for this edge_index tensor object (invalidated by in-place modification or deletion)."""
+    ver = edge_index._version
+    for i, (ref, v, nn_, gr) in enumerate(_graph_cache):
+        if ref() is edge_index and v == ver and nn_ == n:
+            if i:
+                _graph_cache.insert(0, _graph_cache.pop(i))
+            return gr
+    gr = _Graph(edge_index, n)
+    _graph_cache.insert(0, (weakref.ref(edge_index), ver, n, gr))
+    del _graph_cache[_GRAPH_CACHE_SIZE:]
+    return gr
+
+
+def clear_graph_cache():
+    _graph_cache.clear()
+
+
+# ------------------------------------------------------------------------------------------------ autograd
+_DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
+                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+
+
+def _check_inputs(op, x, Y, W, edge_index):
+    s = op.spec
+    if x.dtype != torch.float32 or Y.dtype != torch.float32 or W.dtype != torch.float32:
+        raise TypeError('mace_hip_kernels: conv_tp expects float32 inputs')
+    if not (x.is_cuda and Y.is_cuda and W.is_cuda and edge_index.is_cuda):
+        raise RuntimeError('mace_hip_kernels: conv_tp inputs must be on the GPU')
+    E = edge_index.shape[1]
+    if x.dim() != 2 or x.shape[1] != s.x_dim:
+        raise ValueError(f'node_feats must be [N, {s.x_dim}], got {tuple(x.shape)}')
+    if Y.shape != (E, s.y_dim):
+        raise ValueError(f'edge_attrs must be [{E}, {s.y_dim}], got {tuple(Y.shape)}')
+    if W.shape != (E, s.nins * s.mul):
+        raise ValueError(f'tp_weights must be [{E}, {s.nins * s.mul}], got {tuple(W.shape)}')
+    if x.shape[0] >= 2 ** 31 or E >= 2 ** 31:
+        raise ValueError('graph too large for int32 indices')
+
+
+class _ConvFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, Y, W, edge_index, op):
+        _check_inputs(op, x, Y, W, edge_index)
+        x, Y, W = x.contiguous(), Y.contiguous(), W.contiguous()
+        n = x.shape[0]
+        gr = graph_for(edge_index, n)
+        rowptr, eids = gr.by_recv()
+        out = torch.empty(n, op.spec.out_dim, device=x.device, dtype=torch.float32)
+        lib = _native.load()
+        _native.check(lib.mh_conv_fwd(op.module.handle, _native.ptr(x), _native.ptr(Y), _native.ptr(W),
+                                      _native.ptr(rowptr), _native.ptr(eids), _native.ptr(gr.send),
+                                      _native.ptr(out), n, _native.stream_of(x)), 'conv_fwd')
+        ctx.save_for_backward(x, Y, W)
+        ctx.op, ctx.gr = op, gr
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            raise RuntimeError(_DOUBLE_BACKWARD)
+        x, Y, W = ctx.saved_tensors
+        op, gr = ctx.op, ctx.gr
+        g = g.contiguous()
+        want_x = ctx.needs_input_grad[0]
+        want_wy = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
+        gx = torch.empty_like(x) if want_x else None
+        gW = torch.empty_like(W) if want_wy else None
+        gY = torch.empty_like(Y) if want_wy else None
+        flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy else 0)
+        if flags:
+            rowptr_s, eids_s = gr.by_send()
+            lib = _native.load()
+            _native.check(lib.mh_conv_bwd(op.module.handle, _native.ptr(x), _native.ptr(g), _native.ptr(Y),
+                                          _native.ptr(W), _native.ptr(rowptr_s), _native.ptr(eids_s),
+                                          _native.ptr(gr.recv), _native.ptr(gx), _native.ptr(gW), _native.ptr(gY),
+                                          x.shape[0], flags, _native.stream_of(x)), 'conv_bwd')
+        return gx, gY, gW, None, None
+
+
+class HipConvTP(torch.nn.Module):
+    """Replacement for an interaction block's ``conv_tp`` under MACE's ``conv_fusion`` path:
+    ``forward(node_feats, edge_attrs, tp_weights, edge_index) → summed messages [N, OUT_DIM]``
+    (reference conv.py:273-285)."""
+
+    def __init__(self, tp, device=None):
+        super().__init__()
+        self.spec = ConvSpec(tp)
+        self.source = source(self.spec)
+        code = _native.compile_source(self.source)
+        dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
+        with torch.cuda.device(dev):
+            self.module = _native.Module(code, {
+                _native.MH_CONV_FWD: ('conv_fwd', self.spec.block, 1),
+                _native.MH_CONV_BWD: ('conv_bwd', self.spec.block, 1),
+                _native.MH_CONV_BWD_WY: ('conv_bwd_wy', self.spec.block, WAVE),
+            })
+        self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
+        self.instructions = tp.instructions
+        self.weight_numel = tp.weight_numel
+        self.original = [tp]          # kept (outside the module tree) so the patch can be undone
+
+    def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
+        return _ConvFn.apply(node_feats, edge_attrs, tp_weights, edge_index, self)

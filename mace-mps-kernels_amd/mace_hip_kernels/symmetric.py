@@ -1,0 +1,299 @@
+"""
+MACE ``SymmetricContraction`` as a precomputed symmetrised polynomial, evaluated by one generated HIP kernel per
+layer (reference symmetric.py).
+
+At inference the U matrices and product-basis weights are constants, so for element e, channel c and output
+component M the contraction is a polynomial in x = X[b, c, :] (n_ell = (l_max+1)^2 components):
+    out[b, c, M] = Σ_{i≤j≤k} T3 x_i x_j x_k + Σ_{i≤j} T2 x_i x_j + Σ_i T1 x_i          (correlation 3)
+The coefficients T_ν[e, c, M, i…] = Σ_p U_ν[M, i…, p] W_ν[e, p, c] are formed once in float64 on the CPU, summed over
+index permutations into sorted monomials, and monomials that vanish for every (element, channel, M) are dropped
+(reference symmetric.py:20-75).  Only U and the weights are read, so any correlation order, l_max and CG basis work.
+
+Table layout T[element][monomial × M][channel] (fp32): the 64 lanes of a wave are 64 channels of one node, so every
+coefficient row is one coalesced 256-byte load.  Monomials are evaluated in FP32 VALU with shared prefix products.
+Backward: ∂/∂x of the polynomial (first order; double backward raises).
+"""
+import itertools
+import math
+import weakref
+
+import numpy as np
+import scipy.sparse
+import torch
+
+from . import _native
+
+WAVE = 64
+LOADS_PER_FENCE = 32
+
+
+def _poly_coeffs(ct):
+    """{ν: {sorted index tuple: coefficient array [n_elem, M, C]}}, M, n_ell (reference symmetric.py:20-39)."""
+    corr = ct.correlation
+    U = {nu: getattr(ct, f'U_matrix_{nu}').detach().cpu().double().numpy() for nu in range(1, corr + 1)}
+    W = {corr: ct.weights_max.detach().cpu().double().numpy()}
+    for j, w in enumerate(ct.weights):                  # weights[0] ↔ ν = corr-1, weights[1] ↔ corr-2, …
+        W[corr - 1 - j] = w.detach().cpu().double().numpy()
+    lead = U[1].ndim - 2                                # 1 if there is an M axis (L > 0), else 0
+    M = U[1].shape[0] if lead else 1
+    n_ell = U[1].shape[-2]
+    res = {}
+    for nu in range(1, corr + 1):
+        u = U[nu] if lead else U[nu][None]
+        u = u.reshape(M, n_ell ** nu, u.shape[-1])                      # [M, ell^ν, p]
+        # Sum every index tuple into its sorted representative.  Symmetrisation is linear and U does not depend on
+        # the element, so it is applied to U before the (element-dependent) weights are contracted in.
+        tuples = list(itertools.product(range(n_ell), repeat=nu))
+        keys = sorted(set(tuple(sorted(x)) for x in tuples))
+        kid = {k: i for i, k in enumerate(keys)}
+        cols = np.array([kid[tuple(sorted(x))] for x in tuples])
+        S = scipy.sparse.csr_matrix((np.ones(len(tuples)), (cols, np.arange(len(tuples)))),
+                                    shape=(len(keys), len(tuples)))
+        u_sym = np.stack([S @ u[m] for m in range(M)])                  # [M, K, p]
+        t = np.einsum('mkp,epc->kemc', u_sym, W[nu])                    # [K, e, M, c]
+        res[nu] = {k: t[i] for i, k in enumerate(keys)}                 # [e, M, c]
+    return res, M, n_ell
+
+
+def sc_supported(sc):
+    """(ok, reason) — duck-type check of a MACE SymmetricContraction (reference symmetric.py:42-49)."""
+    try:
+        cts = list(sc.contractions)
+        for ct in cts:
+            _ = ct.correlation, ct.weights_max, ct.U_matrix_1
+    except (AttributeError, TypeError) as e:
+        return False, f'not a MACE SymmetricContraction ({e})'
+    return True, ''
+
+
+class SCSpec:
+    """Term table and coefficient table of one SymmetricContraction (reference symmetric.py:52-75)."""
+
+    def __init__(self, sc, tol=1e-12):
+        ok, why = sc_supported(sc)
+        if not ok:
+            raise ValueError(why)
+        self.blocks, rows, out_off = [], [], 0
+        self.n_ell = None
+        self.C = None
+        for ct in sc.contractions:
+            coeffs, M, n_ell = _poly_coeffs(ct)
+            if self.n_ell not in (None, n_ell):
+                raise ValueError('contractions disagree on n_ell')
+            self.n_ell = n_ell
+            terms = []
+            for nu in sorted(coeffs, reverse=True):
+                for idx, v in sorted(coeffs[nu].items()):
+                    if np.abs(v).max() <= tol:
+                        continue
+                    terms.append((idx, len(rows)))
+                    rows += [v[:, m, :] for m in range(M)]
+            C = next(iter(coeffs[1].values())).shape[2]
+            if self.C not in (None, C):
+                raise ValueError('contractions disagree on the channel count')
+            self.C = C
+            self.blocks.append(dict(M=M, terms=terms, out_off=out_off))
+            out_off += C * M
+        self.out_dim, self.nrows = out_off, len(rows)
+        self.T = torch.tensor(np.stack(rows, axis=1), dtype=torch.float32)     # [e, rows, c]
+        self.n_elem = self.T.shape[0]
+        self.n_terms = sum(len(b['terms']) for b in self.blocks)
+        self.ncb = (self.C + WAVE - 1) // WAVE
+        self.block = self.ncb * WAVE
+
+    def flops(self):
+        """(fwd, bwd) fp32 FLOP per (node, channel) as the generated code evaluates them."""
+        fwd = bwd = 0
+        for bl in self.blocks:
+            M = bl['M']
+            for idx, _ in bl['terms']:
+                deg = len(idx)
+                fwd += (deg - 1) + 2 * M
+                bwd += (2 * M - 1) + 2 * len(set(idx)) + (deg - 1)
+        return fwd, bwd
+
+    def bytes(self, n_nodes, n_elem_used):
+        fwd = 4 * (n_nodes * self.C * self.n_ell + n_nodes * self.out_dim + n_nodes
+                   + n_elem_used * self.nrows * self.C)
+        bwd = 4 * (2 * n_nodes * self.C * self.n_ell + n_nodes * self.out_dim + n_nodes
+                   + n_elem_used * self.nrows * self.C)
+        return fwd, bwd
+
+
+# ------------------------------------------------------------------------------------------------- codegen
+def _trie(spec):
+    """Prefix trie of every monomial of every contraction block: node = {'terms': [(block, r0, M)], 'kids': {i: node}}.
+    Walking it depth first evaluates each prefix product x_i·x_j·… exactly once, right before its last use."""
+    root = {'terms': [], 'kids': {}}
+    for bi, bl in enumerate(spec.blocks):
+        for idx, r0 in bl['terms']:
+            node = root
+            for i in idx:
+                node = node['kids'].setdefault(i, {'terms': [], 'kids': {}})
+            node['terms'].append((bi, r0, bl['M']))
+    return root
+
+
+def _fence(L, ind, cnt, M, live):
+    """Every LOADS_PER_FENCE coefficient loads, pass the table pointer and the live accumulators through an empty asm
+    statement.  Work before the fence must finish to produce its inputs and loads after it depend on its output, so
+    the coefficient loads (invariant, hence otherwise free to move) cannot all be hoisted to the top of the kernel,
+    where they would need hundreds of registers."""
+    cnt[0] += M
+    if cnt[0] >= LOADS_PER_FENCE:
+        cnt[0] = 0
+        ops = ', '.join(f'"+v"({v})' for v in live)
+        L.append(f'{ind}asm volatile("" : "+s"(tb), {ops}); t = tb + cc;')
+
+
+def _fwd_walk(spec, node, depth, L, ind, cnt):
+    live = [f'a{bi}_{m}' for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+    for bi, r0, M in node['terms']:
+        _fence(L, ind, cnt, M, live)
+        L += [f'{ind}a{bi}_{m} = fmaf(t[{(r0 + m) * spec.C}], p{depth}, a{bi}_{m});' for m in range(M)]
+    for i in sorted(node['kids']):
+        L.append(f'{ind}{{ const float p{depth + 1} = ' + (f'x{i};' if depth == 0 else f'p{depth} * x{i};'))
+        _fwd_walk(spec, node['kids'][i], depth + 1, L, ind + '  ', cnt)
+        L.append(f'{ind}}}')
+
+
+def _bwd_walk(spec, node, depth, L, ind, cnt):
+    """Reverse mode along the trie: G{depth} accumulates ∂out/∂p{depth}; a child p' = p·x_i passes G'·p to d_i and
+    G'·x_i to G."""
+    live = [f'd{i}' for i in range(spec.n_ell)] + [f'G{k}' for k in range(1, depth + 1)]
+    for bi, r0, M in node['terms']:
+        _fence(L, ind, cnt, M, live)
+        s = ' + '.join(f't[{(r0 + m) * spec.C}] * g{bi}_{m}' for m in range(M))
+        L.append(f'{ind}G{depth} += {s};')
+    for i in sorted(node['kids']):
+        kid = node['kids'][i]
+        L.append(f'{ind}{{ const float p{depth + 1} = ' + (f'x{i};' if depth == 0 else f'p{depth} * x{i};'))
+        L.append(f'{ind}  float G{depth + 1} = 0.0f;')
+        _bwd_walk(spec, kid, depth + 1, L, ind + '  ', cnt)
+        if depth == 0:
+            L.append(f'{ind}  d{i} += G1;')
+        else:
+            L.append(f'{ind}  d{i} = fmaf(G{depth + 1}, p{depth}, d{i});')
+            L.append(f'{ind}  G{depth} = fmaf(G{depth + 1}, x{i}, G{depth});')
+        L.append(f'{ind}}}')
+
+
+def source(spec):
+    C, R, n = spec.C, spec.nrows, spec.n_ell
+    L = [_native.device_header(),
+         f'#define C {C}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}', f'#define N_ELL {n}',
+         f'#define R {R}', f'#define OUT_DIM {spec.out_dim}']
+    head = [
+        '  const int b = mh_xcd_block(blockIdx.x, gridDim.x);',
+        '  if (b >= N) return;',
+        '  const int c = threadIdx.x;',
+        '  const bool active = c < C;',
+        '  const int cc = active ? c : C - 1;',
+        '  const float* __restrict__ xp = X + ((size_t)b * C + cc) * N_ELL;',
+    ] + [f'  const float x{i} = xp[{i}];' for i in range(n)] + [
+        '  const float* tb = T + (size_t)elem[b] * ((size_t)R * C);',
+        '  const float* t = tb + cc;',
+    ]
+    trie = _trie(spec)
+    # ------------------------------------------------------------------------------------- forward
+    L += ['extern "C" __global__ __launch_bounds__(BLOCK) void sc_fwd(const float* __restrict__ X,',
+          '    const int* __restrict__ elem, const float* __restrict__ T, float* __restrict__ out, int N) {']
+    L += head
+    for bi, bl in enumerate(spec.blocks):
+        L += [f'  float a{bi}_{m} = 0.0f;' for m in range(bl['M'])]
+    _fwd_walk(spec, trie, 0, L, '  ', [0])
+    L.append('  if (active) {')
+    for bi, bl in enumerate(spec.blocks):
+        M = bl['M']
+        L += [f'    out[(size_t)b * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{bi}_{m};' for m in range(M)]
+    L += ['  }', '}', '']
+    # ------------------------------------------------------------------------------------ backward
+    L += ['extern "C" __global__ __launch_bounds__(BLOCK) void sc_bwd(const float* __restrict__ X,',
+          '    const int* __restrict__ elem, const float* __restrict__ T, const float* __restrict__ G,',
+          '    float* __restrict__ GX, int N) {']
+    L += head
+    L += [f'  float d{i} = 0.0f;' for i in range(n)]
+    for bi, bl in enumerate(spec.blocks):
+        M = bl['M']
+        L += [f'  const float g{bi}_{m} = G[(size_t)b * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];' for m in range(M)]
+    L.append('  float G0 = 0.0f;')
+    _bwd_walk(spec, trie, 0, L, '  ', [0])
+    L += ['  (void)G0;', '  if (active) {', '    float* __restrict__ gp = GX + ((size_t)b * C + c) * N_ELL;']
+    L += [f'    gp[{i}] = d{i};' for i in range(n)]
+    L += ['  }', '}', '']
+    return '\n'.join(L)
+
+
+# ------------------------------------------------------------------------------------------------ autograd
+_DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
+                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+
+_elem_cache = []          # [(weakref(node_attrs), version, elem int32)], most recent first
+
+
+def element_index(node_attrs):
+    """argmax of the one-hot node attributes as int32, cached per node_attrs tensor (reference symmetric.py:169)."""
+    ver = node_attrs._version
+    for i, (ref, v, el) in enumerate(_elem_cache):
+        if ref() is node_attrs and v == ver:
+            return el
+    el = torch.argmax(node_attrs, dim=1).to(torch.int32).contiguous()
+    _elem_cache.insert(0, (weakref.ref(node_attrs), ver, el))
+    del _elem_cache[4:]
+    return el
+
+
+class _SCFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, elem, op):
+        s = op.spec
+        if x.dtype != torch.float32 or not x.is_cuda:
+            raise TypeError('mace_hip_kernels: symmetric contraction expects float32 GPU input')
+        if x.dim() != 3 or x.shape[1] != s.C or x.shape[2] != s.n_ell:
+            raise ValueError(f'node_feats must be [N, {s.C}, {s.n_ell}], got {tuple(x.shape)}')
+        x = x.contiguous()
+        N = x.shape[0]
+        out = torch.empty(N, s.out_dim, device=x.device, dtype=torch.float32)
+        _native.check(_native.load().mh_sc_fwd(op.module.handle, _native.ptr(x), _native.ptr(elem),
+                                               _native.ptr(op.T), _native.ptr(out), N, _native.stream_of(x)),
+                      'sc_fwd')
+        ctx.save_for_backward(x, elem)
+        ctx.op = op
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            raise RuntimeError(_DOUBLE_BACKWARD)
+        x, elem = ctx.saved_tensors
+        op = ctx.op
+        gx = torch.empty_like(x)
+        _native.check(_native.load().mh_sc_bwd(op.module.handle, _native.ptr(x), _native.ptr(elem),
+                                               _native.ptr(op.T), _native.ptr(g.contiguous()), _native.ptr(gx),
+                                               x.shape[0], _native.stream_of(x)), 'sc_bwd')
+        return gx, None, None
+
+
+class HipSymmetricContraction(torch.nn.Module):
+    """Drop-in for mace ``SymmetricContraction`` at inference: ``forward(x[N, C, n_ell], node_attrs[N, n_elem])``
+    (reference symmetric.py:158-170)."""
+
+    def __init__(self, sc, device=None):
+        super().__init__()
+        self.spec = SCSpec(sc)
+        dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
+        self.register_buffer('T', self.spec.T.to(dev).contiguous())
+        self.source = source(self.spec)
+        code = _native.compile_source(self.source)
+        with torch.cuda.device(dev):
+            self.module = _native.Module(code, {
+                _native.MH_SC_FWD: ('sc_fwd', self.spec.block, 1),
+                _native.MH_SC_BWD: ('sc_bwd', self.spec.block, 1),
+            })
+        self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
+        self.original = [sc]
+
+    def forward(self, x, y):
+        if y.shape != (x.shape[0], self.spec.n_elem):
+            raise ValueError(f'node_attrs must be [{x.shape[0]}, {self.spec.n_elem}], got {tuple(y.shape)}')
+        return _SCFn.apply(x, element_index(y), self)

@@ -1,0 +1,191 @@
+"""
+Kernel-level parity of the HIP path against the oracle (float64 CPU restatement), through the C ABI.
+
+Every case prints its name before launching.  Tolerance: fp32 kernels vs fp64 oracle, max relative error
+(normalised by the largest reference magnitude) < 2e-6 for the convolution and < 1e-5 for the symmetric contraction
+(hundreds of fp32 terms per output); determinism is bitwise.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from mace_hip_kernels import HipConvTP, HipSymmetricContraction, _native
+from mace_hip_kernels import conv as hconv
+from mace_lite import blocks as B
+from mace_lite import factory
+from mace_lite.o3 import Irreps, TensorProduct
+from oracle import conv as oconv
+from oracle import sc as osc
+
+pytestmark = pytest.mark.gpu
+CONV_TOL = 2e-6
+SC_TOL = 1e-5
+
+
+def _dev():
+    assert torch.cuda.is_available(), 'GPU test needs a GPU'
+    return torch.device('cuda:0')
+
+
+def _tp(hidden, lmax):
+    sh = Irreps.spherical_harmonics(lmax)
+    hid = Irreps(hidden)
+    target = (sh * hid.count((0, 1))).sort()[0].simplify()
+    irreps_mid, ins = B.tp_out_irreps_with_instructions(hid, sh, target)
+    return TensorProduct(hid, sh, irreps_mid, ins, shared_weights=False, internal_weights=False)
+
+
+def _graph(rng, n, e):
+    """Random multigraph with isolated nodes, self loops, and one receiver and one sender with > 64 edges."""
+    s, r = oconv.random_graph(rng, n, e)
+    r[:150] = 0                    # receiver 0: >64 edges (several CSR chunks)
+    s[150:230] = 1                 # sender 1: >64 edges
+    s[s == n - 1] = 0              # node n-1 never sends ...
+    r[r == n - 1] = 1              # ... nor receives
+    return s, r
+
+
+def _rel(got, want):
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+CONV_CASES = [('32x0e+32x1o', 2), ('128x0e', 3), ('128x0e+128x1o', 3), ('128x0e+128x1o+128x2e', 3),
+              ('64x0e', 2), ('96x0e+96x1o', 3)]
+
+
+@pytest.mark.parametrize('hidden,lmax', CONV_CASES)
+def test_conv_fwd_bwd_vs_oracle(hidden, lmax):
+    dev = _dev()
+    print(f'[case] conv {hidden} l{lmax}', flush=True)
+    tp = _tp(hidden, lmax)
+    op = HipConvTP(tp, device=dev)
+    desc = oconv.describe_tp(tp)
+    coef = oconv.path_terms(desc)
+    rng = np.random.default_rng(1)
+    n, e = 41, 700
+    s, r = _graph(rng, n, e)
+    nw = len(desc['ins']) * desc['mul']
+    x, Y, W = rng.normal(size=(n, desc['x_dim'])), rng.normal(size=(e, desc['y_dim'])), rng.normal(size=(e, nw))
+    g = rng.normal(size=(n, desc['out_dim']))
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+    xt, Yt, Wt = t(x), t(Y), t(W)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    out = op(xt, Yt, Wt, ei)
+    out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+    want = oconv.conv_fwd(desc, coef, x, Y, W, s, r, n)
+    assert _rel(out.detach().double().cpu().numpy(), want) < CONV_TOL
+    assert _rel(xt.grad.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, W, s, r, n)) < CONV_TOL
+    assert _rel(Wt.grad.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
+    assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
+    assert float(out[n - 1].abs().max()) == 0.0 and float(xt.grad[n - 1].abs().max()) == 0.0
+
+
+def test_conv_c_abi_bwd_x_and_bwd_wy():
+    """The reference-shaped entry points mh_conv_bwd_x / mh_conv_bwd_wy against the oracle and the fused kernel."""
+    dev = _dev()
+    print('[case] conv C-ABI bwd_x / bwd_wy', flush=True)
+    tp = _tp('128x0e+128x1o', 3)
+    op = HipConvTP(tp, device=dev)
+    desc = oconv.describe_tp(tp)
+    coef = oconv.path_terms(desc)
+    rng = np.random.default_rng(2)
+    n, e = 33, 500
+    s, r = _graph(rng, n, e)
+    f = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+    x, Y, W, g = (rng.normal(size=sh) for sh in ((n, desc['x_dim']), (e, desc['y_dim']), (e, 10 * 128),
+                                                  (n, desc['out_dim'])))
+    xt, Yt, Wt, gt = f(x), f(Y), f(W), f(g)
+    st, rt = torch.tensor(s, dtype=torch.int32, device=dev), torch.tensor(r, dtype=torch.int32, device=dev)
+    rowptr_s, eids_s = hconv.csr_by(torch.tensor(s, device=dev), n)
+    lib, P, st_ = _native.load(), _native.ptr, _native.stream_of(xt)
+    gx = torch.zeros_like(xt)
+    _native.check(lib.mh_conv_bwd_x(op.module.handle, P(gt), P(Yt), P(Wt), P(rowptr_s), P(eids_s), P(rt), P(gx), n,
+                                    st_), 'bwd_x')
+    gW, gY = torch.zeros_like(Wt), torch.zeros_like(Yt)
+    _native.check(lib.mh_conv_bwd_wy(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(st), P(rt), P(gW), P(gY), e,
+                                     st_), 'bwd_wy')
+    gW2, gY2, gx2 = torch.zeros_like(Wt), torch.zeros_like(Yt), torch.zeros_like(xt)
+    _native.check(lib.mh_conv_bwd(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_s), P(eids_s), P(rt),
+                                  P(gx2), P(gW2), P(gY2), n, 3, st_), 'bwd')
+    torch.cuda.synchronize()
+    assert _rel(gx.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, W, s, r, n)) < CONV_TOL
+    assert _rel(gW.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
+    assert _rel(gY.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
+    assert torch.equal(gx, gx2) and torch.equal(gW, gW2)
+    assert _rel(gY2.double().cpu().numpy(), gY.double().cpu().numpy()) < 1e-6
+
+
+def test_conv_deterministic_and_empty():
+    dev = _dev()
+    print('[case] conv determinism + empty graph', flush=True)
+    tp = _tp('128x0e+128x1o', 3)
+    op = HipConvTP(tp, device=dev)
+    rng = np.random.default_rng(3)
+    n, e = 60, 900
+    s, r = _graph(rng, n, e)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    f = lambda *sh: torch.randn(*sh, device=dev, requires_grad=True)  # noqa: E731
+    x, Y, W = f(n, 512), f(e, 16), f(e, 1280)
+    outs = []
+    for _ in range(2):
+        o = op(x, Y, W, ei)
+        gx, gY, gW = torch.autograd.grad(o.square().sum(), (x, Y, W))
+        outs.append((o.detach(), gx, gY, gW))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    # no edges at all: zero messages, zero node gradient, empty edge gradients
+    ei0 = torch.zeros(2, 0, dtype=torch.int64, device=dev)
+    Y0, W0 = f(0, 16), f(0, 1280)
+    o = op(x, Y0, W0, ei0)
+    assert o.shape == (n, 5120) and float(o.abs().max()) == 0.0
+    gx, = torch.autograd.grad(o.sum(), (x,))
+    assert float(gx.abs().max()) == 0.0
+
+
+SC_MODELS = [('32x0e+32x1o', 2, 2), ('128x0e+128x1o', 3, 3), ('64x0e', 2, 2), ('128x0e+128x1o+128x2e', 3, 3)]
+
+
+@pytest.mark.parametrize('hidden,lmax,corr', SC_MODELS)
+def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr):
+    dev = _dev()
+    model = factory.make_model(hidden, lmax, corr, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(4)
+    for li, prod in enumerate(model.products):
+        print(f'[case] sc {hidden} l{lmax} c{corr} layer {li}', flush=True)
+        sc = prod.symmetric_contractions
+        op = HipSymmetricContraction(sc, device=dev)
+        C, n_ell = op.spec.C, op.spec.n_ell
+        n = 37
+        x = rng.normal(size=(n, C, n_ell)) * 0.7
+        elem = rng.integers(0, 4, n)
+        attrs = np.eye(4)[elem]
+        g = rng.normal(size=(n, op.spec.out_dim))
+        xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
+        out = op(xt, torch.tensor(attrs, dtype=torch.float32, device=dev))
+        out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+        # oracle: dense evaluation per contraction, outputs concatenated as [b, c*M]
+        xo = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+        parts = []
+        for ct in sc.contractions:
+            U = {nu: getattr(ct, f'U_matrix_{nu}').double() for nu in range(1, ct.correlation + 1)}
+            U = {nu: (u if u.dim() == nu + 2 else u.unsqueeze(0)) for nu, u in U.items()}
+            U = {nu: u.reshape(u.shape[0], -1, u.shape[-1]) for nu, u in U.items()}
+            Wd = {ct.correlation: ct.weights_max.detach().double()}
+            for j, w in enumerate(ct.weights):
+                Wd[ct.correlation - 1 - j] = w.detach().double()
+            parts.append(osc.sc_dense(U, Wd, xo, elem).reshape(n, -1))
+        want = torch.cat(parts, dim=-1)
+        want.backward(torch.tensor(g, dtype=torch.float64))
+        assert _rel(out.detach().double().cpu().numpy(), want.detach().numpy()) < SC_TOL
+        assert _rel(xt.grad.double().cpu().numpy(), xo.grad.numpy()) < SC_TOL
+
+
+def test_library_runtime_is_torchs():
+    dev = _dev()
+    print('[case] runtime binding', flush=True)
+    lib = _native.load()
+    assert 'torch' in lib.mh_hip_runtime_path().decode()
+    assert lib.mh_version() == _native.ABI_VERSION
+    del dev

@@ -1,0 +1,140 @@
+"""
+Model-level parity of the patched MACE model (HIP kernels, fp32, GPU) against the unpatched e3nn path, mirroring the
+reference's tests (reference tests/test_kernels.py:23-85) plus the BASELINE configurations.
+
+Reference for E/F/stress: the same model unpatched, evaluated in float64 on the GPU (the e3nn path restated in plain
+PyTorch).  Tolerances: the reference's (E: 1e-5 eV/atom; F: 1e-5 relative to the largest force component;
+rotation: 1e-4 relative) and the tier's absolute ones (|dE| <= 1 meV per structure, max|dF| <= 1e-5 eV/A).
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from mace_hip_kernels import patch_model
+from mace_lite import data as D
+from mace_lite import factory
+from oracle import wigner
+
+pytestmark = pytest.mark.gpu
+E_TOL = 1e-5        # eV per atom
+F_TOL = 1e-5        # relative to the largest force component
+E_ABS = 1e-3        # eV per structure
+F_ABS = 1e-5        # eV/A
+
+
+def _dev():
+    assert torch.cuda.is_available(), 'GPU test needs a GPU'
+    return torch.device('cuda:0')
+
+
+def _to(batch, dev, dtype):
+    return {k: (v.to(dev, dtype) if torch.is_tensor(v) and v.is_floating_point() else
+                v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
+
+
+def _ef(model, batch, dev, dtype, stress=False):
+    out = model(D.fresh(_to(batch, dev, dtype)), compute_force=True, compute_stress=stress)
+    res = [out['energy'].detach().double().cpu().numpy(), out['forces'].detach().double().cpu().numpy()]
+    if stress:
+        res.append(out['stress'].detach().double().cpu().numpy())
+    return res
+
+
+def _pair(model, dev):
+    ref = copy.deepcopy(model).to(dev, torch.float64)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    report = patch_model(met, verbose=False)
+    return ref, met, report
+
+
+def _check(ref, met, batch, dev, n_atoms, stress=False):
+    r = _ef(ref, batch, dev, torch.float64, stress)
+    m = _ef(met, batch, dev, torch.float32, stress)
+    dE = np.abs(m[0] - r[0])
+    dF = np.abs(m[1] - r[1]).max()
+    assert dE.max() < E_ABS, dE
+    assert (dE / np.asarray(n_atoms)).max() < E_TOL, dE
+    assert dF / max(np.abs(r[1]).max(), 1e-3) < F_TOL, dF
+    assert dF < F_ABS, dF
+    if stress:
+        ds = np.abs(m[2] - r[2]).max()
+        assert ds / max(np.abs(r[2]).max(), 1e-6) < 1e-4, ds
+    return dE.max(), dF
+
+
+@pytest.mark.parametrize('config', list(factory.REF_CONFIGS))
+def test_matches_e3nn_all_configs(config):
+    dev = _dev()
+    hidden, lmax, corr = factory.REF_CONFIGS[config]
+    seed = 0 if not config.endswith('_b') else 7
+    ref, met, report = _pair(factory.make_model(hidden, lmax, corr, seed=seed), dev)
+    assert not report['skipped'], report['skipped']
+    assert len(report['patched']) == 4, report
+    for s in (0, 1, 2):
+        print(f'[case] {config} seed {s}', flush=True)
+        st = factory.make_structure(seed=s)
+        batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
+        dE, dF = _check(ref, met, batch, dev, [len(st)])
+        print(f'       |dE| {dE * 1e3:.4f} meV  max|dF| {dF:.2e}', flush=True)
+
+
+def test_rotation_equivariance():
+    dev = _dev()
+    print('[case] rotation equivariance', flush=True)
+    _, met, _ = _pair(factory.make_model(*factory.REF_CONFIGS['l3_corr3_fullcg']), dev)
+    st = factory.make_structure(seed=3)
+    R = wigner.random_rotation(np.random.default_rng(0))
+    b0 = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
+    b1 = D.batch_graphs([D.graph_of(st.rotated(R), 5.0)], factory.ELEMENTS_REF)
+    E0, F0 = _ef(met, b0, dev, torch.float32)
+    E1, F1 = _ef(met, b1, dev, torch.float32)
+    assert abs(E1 - E0).max() / len(st) < E_TOL
+    assert np.abs(F1 - F0 @ R.T).max() / np.abs(F0).max() < 1e-4
+
+
+def test_double_backward_raises():
+    dev = _dev()
+    print('[case] double backward guard', flush=True)
+    _, met, _ = _pair(factory.make_model(*factory.REF_CONFIGS['l3_corr3_fullcg']), dev)
+    batch = D.fresh(_to(D.batch_graphs([D.graph_of(factory.make_structure(seed=4), 5.0)], factory.ELEMENTS_REF),
+                        dev, torch.float32))
+    out = met(batch, compute_force=False, training=True)
+    with pytest.raises(RuntimeError, match='double backward'):
+        (f,) = torch.autograd.grad(out['energy'].sum(), batch['positions'], create_graph=True)
+        torch.autograd.grad(f.sum(), batch['positions'])
+
+
+def test_unsupported_block_is_skipped():
+    dev = _dev()
+    print('[case] 48-channel model: convolutions skipped', flush=True)
+    ref, met, report = _pair(factory.make_model('48x0e+48x1o', 3, 3), dev)
+    assert all('conv_tp' in n for n, _ in report['skipped']) and len(report['skipped']) == 2, report
+    assert len(report['patched']) == 2
+    st = factory.make_structure(seed=5)
+    _check(ref, met, D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF), dev, [len(st)])
+
+
+@pytest.mark.parametrize('cfg', [0, 1, 2, 3])
+def test_baseline_configs(cfg):
+    dev = _dev()
+    print(f'[case] BASELINE config {cfg}', flush=True)
+    model, batch, meta = factory.workload(cfg)
+    ref, met, report = _pair(model, dev)
+    assert not report['skipped'] and len(report['patched']) == 4, report
+    n_atoms = np.diff(batch['ptr'].numpy())
+    dE, dF = _check(ref, met, batch, dev, n_atoms, stress=(cfg == 1))
+    print(f'       {meta["name"]}: |dE| {dE * 1e3:.4f} meV  max|dF| {dF:.2e}', flush=True)
+
+
+def test_idempotent_patch_and_unpatch():
+    dev = _dev()
+    print('[case] patch idempotence / unpatch', flush=True)
+    from mace_hip_kernels import unpatch_model
+    m = factory.make_model(*factory.REF_CONFIGS['l2_corr2_scalar']).to(dev)
+    r1 = patch_model(m, verbose=False)
+    r2 = patch_model(m, verbose=False)
+    assert len(r1['patched']) == 4 and r2 == dict(patched=[], skipped=[])
+    assert len(unpatch_model(m)) == 4
+    assert not hasattr(m.interactions[0], 'conv_fusion')
