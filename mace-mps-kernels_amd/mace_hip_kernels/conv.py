@@ -22,6 +22,7 @@ channel u at k*MUL+u), out [N, OUT_DIM].  ``edge_index = [sender, receiver]``.
 """
 import copy
 import math
+import warnings
 import weakref
 
 import numpy as np
@@ -73,7 +74,9 @@ def _probe_tp(tp):
     try:
         cp = copy.deepcopy(tp).to(device='cpu', dtype=torch.float64)
         return cp, torch.device('cpu'), torch.float64
-    except Exception:  # noqa: BLE001  (an exotic TP that cannot be copied: probe it where it lives, like the reference)
+    except Exception as e:  # noqa: BLE001  (a TP that cannot be copied: probe it where it lives, like the reference)
+        warnings.warn(f'mace_hip_kernels: probing {type(tp).__name__} in its own dtype/device ({e}); path '
+                      'coefficients carry that precision')
         dev = next(iter(tp.buffers()), torch.zeros(1)).device
         return tp, dev, torch.get_default_dtype()
 
@@ -490,7 +493,9 @@ class _ConvFn(torch.autograd.Function):
         gx = torch.empty_like(x) if want_x else None
         gW = torch.empty_like(W) if want_wy else None
         gY = torch.empty_like(Y) if want_wy else None
-        flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy else 0)
+        # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
+        flags = (_native.MH_WANT_GX if want_x else 0) | \
+            (_native.MH_WANT_GWY if want_wy and W.shape[0] > 0 else 0)
         if flags:
             rowptr_s, eids_s = gr.by_send()
             lib = _native.load()

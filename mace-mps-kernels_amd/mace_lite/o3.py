@@ -76,6 +76,9 @@ class MulIr(tuple):
     def __new__(cls, mul, ir):
         return super().__new__(cls, (mul, Irrep(ir)))
 
+    def __getnewargs__(self):
+        return (self[0], self[1])
+
     @property
     def mul(self):
         return self[0]
@@ -302,13 +305,17 @@ class SphericalHarmonics(torch.nn.Module):
         for l in self._ls:
             s = 1.0 if normalization == 'component' else 1.0 / math.sqrt(2 * l + 1)
             scale += [s] * (2 * l + 1)
-        self.register_buffer('_scale', torch.tensor(scale), persistent=False)
+        self._scale = scale                   # python floats: exact in any dtype the module is cast to
+        self._scale_t = {}
 
     def forward(self, vec):
         if self.normalize:
             vec = vec / vec.norm(dim=-1, keepdim=True).clamp_min(1e-30)
         sh = _sh_component(self.lmax, vec[..., 0], vec[..., 1], vec[..., 2])
-        return sh * self._scale.to(sh.dtype)
+        key = (sh.device, sh.dtype)
+        if key not in self._scale_t:
+            self._scale_t[key] = torch.tensor(self._scale, dtype=sh.dtype, device=sh.device)
+        return sh * self._scale_t[key]
 
 
 # ------------------------------------------------------------------------------------------------ tensor products
@@ -380,12 +387,21 @@ class TensorProduct(torch.nn.Module):
             self.weight = torch.nn.Parameter(torch.randn(self.weight_numel))
         else:
             self.register_buffer('weight', torch.Tensor(), persistent=False)
+        # coupling tables are kept out of the module's buffers: they are constants of the operation, recomputed in
+        # float64 and cast per (device, dtype), so casting the model to float32 and back cannot round them
+        self._w3j_ls, self._w3j = [], {}
         for k, i in enumerate(ins):
             l1, l2, lo = self.irreps_in1[i.i_in1].ir.l, self.irreps_in2[i.i_in2].ir.l, self.irreps_out[i.i_out].ir.l
-            self.register_buffer(f'_w3j_{k}', wigner_3j(l1, l2, lo), persistent=False)
+            self._w3j_ls.append((l1, l2, lo))
 
     def __repr__(self):
         return f'TensorProduct({self.irreps_in1} x {self.irreps_in2} -> {self.irreps_out} | {len(self.instructions)} paths)'
+
+    def _coupling(self, k, like):
+        key = (like.device, like.dtype)
+        if key not in self._w3j:
+            self._w3j[key] = [wigner_3j(*ls, dtype=like.dtype, device=like.device) for ls in self._w3j_ls]
+        return self._w3j[key][k]
 
     def forward(self, x1, x2, weight=None):
         if weight is None:
@@ -407,7 +423,7 @@ class TensorProduct(torch.nn.Module):
             mi1, mi2, mo = self.irreps_in1[i.i_in1], self.irreps_in2[i.i_in2], self.irreps_out[i.i_out]
             a = x1[:, s1[i.i_in1]].reshape(z, mi1.mul, mi1.ir.dim)
             b = x2[:, s2[i.i_in2]].reshape(z, mi2.mul, mi2.ir.dim)
-            c = getattr(self, f'_w3j_{k}').to(x1.dtype)
+            c = self._coupling(k, x1)
             n = math.prod(i.path_shape) if i.has_weight else 0
             w = weight[:, woff:woff + n].reshape(weight.shape[0], *i.path_shape) if i.has_weight else None
             woff += n
