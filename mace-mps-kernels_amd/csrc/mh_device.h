@@ -23,28 +23,39 @@ __device__ __forceinline__ int mh_bcast(int v, int j) { return __builtin_amdgcn_
 // exchange step halves the number of values a lane carries, so the cost is NV-1 + log2(64/NV) shuffles instead of
 // 6*NV.  On return every lane L holds the wave total of component (L >> (6 - log2 NV)) in v[0].  The summation
 // order is fixed, so results are bitwise reproducible.
+// One step exchanges with lane ^ M: N values per lane become N/2 (lanes with bit M set keep the upper half).  The
+// recursion is resolved at compile time so every register index is a constant (a runtime index would turn the
+// array into compare/select chains).
+template <int N, int M, int NV>
+struct MhTransposeStep {
+    static __device__ __forceinline__ void run(float (&v)[NV], int lane) {
+        const bool hi = (lane & M) != 0;
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k) {
+            const float send = hi ? v[k] : v[k + N / 2];
+            const float keep = hi ? v[k + N / 2] : v[k];
+            v[k] = keep + __shfl_xor(send, M, MH_WAVE);
+        }
+        MhTransposeStep<N / 2, M / 2, NV>::run(v, lane);
+    }
+};
+
+template <int M, int NV>
+struct MhTransposeStep<1, M, NV> {
+    static __device__ __forceinline__ void run(float (&v)[NV], int lane) {
+        v[0] += __shfl_xor(v[0], M, MH_WAVE);
+        MhTransposeStep<1, M / 2, NV>::run(v, lane);
+    }
+};
+
+template <int NV>
+struct MhTransposeStep<1, 0, NV> {
+    static __device__ __forceinline__ void run(float (&)[NV], int) {}
+};
+
 template <int NV>
 __device__ __forceinline__ float mh_wave_transpose_sum(float (&v)[NV]) {
-    const int lane = threadIdx.x & (MH_WAVE - 1);
-    int n = NV;
-    int m = MH_WAVE / 2;
-#pragma unroll
-    for (int step = 0; step < 6; ++step) {
-        if (n > 1) {
-            n >>= 1;
-            const bool hi = (lane & m) != 0;
-#pragma unroll
-            for (int k = 0; k < NV / 2; ++k) {
-                if (k < n) {
-                    const float send = hi ? v[k] : v[k + n];
-                    const float keep = hi ? v[k + n] : v[k];
-                    v[k] = keep + __shfl_xor(send, m, MH_WAVE);
-                }
-            }
-        } else {
-            v[0] += __shfl_xor(v[0], m, MH_WAVE);
-        }
-        m >>= 1;
-    }
+    static_assert(NV >= 1 && NV <= MH_WAVE && (NV & (NV - 1)) == 0, "NV must be a power of two <= 64");
+    MhTransposeStep<NV, MH_WAVE / 2, NV>::run(v, threadIdx.x & (MH_WAVE - 1));
     return v[0];
 }

@@ -63,6 +63,7 @@ def patch_model(model, conv=True, symmetric=True, verbose=True):
                 skipped.append((name, why))
                 continue
             blk.conv_tp = HipConvTP(blk.conv_tp, device=dev)
+            blk.conv_tp.tag = name
             blk.conv_fusion = True
             patched.append(name)
     if symmetric:
@@ -80,6 +81,7 @@ def patch_model(model, conv=True, symmetric=True, verbose=True):
                 skipped.append((name, why))
                 continue
             prod.symmetric_contractions = HipSymmetricContraction(sc, device=dev)
+            prod.symmetric_contractions.tag = name
             patched.append(name)
     if verbose:
         for name, why in skipped:

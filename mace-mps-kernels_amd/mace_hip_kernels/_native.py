@@ -126,6 +126,44 @@ class Module:
                 pass
 
 
+class timing:
+    """Context manager: while active, every kernel launch is bracketed by two HIP events recorded on the launch
+    stream; ``.records`` collects (tag, start, end).  Off by default (no events outside this context)."""
+    active = None
+
+    def __init__(self):
+        self.records = []
+
+    def __enter__(self):
+        timing.active = self
+        return self
+
+    def __exit__(self, *exc):
+        timing.active = None
+
+    def summary(self):
+        """{tag: (launches, mean ms)} (synchronises the device)."""
+        torch.cuda.synchronize()
+        acc = {}
+        for tag, s, e in self.records:
+            n, tot = acc.get(tag, (0, 0.0))
+            acc[tag] = (n + 1, tot + s.elapsed_time(e))
+        return {k: (n, tot / n) for k, (n, tot) in acc.items()}
+
+
+def launch(tag, fn, *args):
+    """Call a C-ABI launcher, raise on a nonzero status, and time it when a ``timing`` context is active."""
+    rec = timing.active
+    if rec is None:
+        check(fn(*args), tag)
+        return
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    check(fn(*args), tag)
+    e.record()
+    rec.records.append((tag, s, e))
+
+
 def ptr(t):
     """Device pointer of a tensor (None → NULL)."""
     return None if t is None else _P(t.data_ptr())

@@ -226,7 +226,7 @@ def _bwd_body(spec, indent, with_gx, store_gw):
             for b in range(co['d2']):
                 ts = [f'{_lit(v)} * xv[{xi[i1] + a}] * gv[{oi[k] + c}]' for a, bb, c, v in co['terms'] if bb == b]
                 if ts:
-                    L.append(f'{indent}  P[{co["o2"] + b}] = fmaf(w{k}, {_sum(ts)}, P[{co["o2"] + b}]);')
+                    L.append(f'{indent}  P{co["o2"] + b} = fmaf(w{k}, {_sum(ts)}, P{co["o2"] + b});')
         L.append(f'{indent}}}')
     return L
 
@@ -252,13 +252,42 @@ def _gy_combine(indent, edge_expr):
     ]
 
 
-def _gy_reduce(indent):
-    return [
-        f'{indent}for (int b = Y_DIM; b < Y_PAD; ++b) P[b] = 0.0f;',
-        f'{indent}{{ const float tot = mh_wave_transpose_sum<Y_PAD>(P);',
-        f'{indent}  const int comp = lane >> (6 - {{LOG2P}});',
-        f'{indent}  if ((lane & ((1 << (6 - {{LOG2P}})) - 1)) == 0 && comp < Y_DIM) part[wave][j][comp] = tot; }}',
-    ]
+# Lane exchanges of the transpose reduction, one per lane bit from 5 down to 0.  Bits 5 and 4 cross 16-lane rows and
+# go through __shfl_xor (ds_bpermute); bits 3..0 stay inside a row and use DPP moves, which are plain VALU operands
+# (row_ror:8 = lane^8, row_half_mirror = lane^7, quad_perm [2,3,0,1] = lane^2, [1,0,3,2] = lane^1).  Every exchange
+# pairs lanes that differ in the current bit and agree in the higher ones, which is all the reduction needs.
+_DPP = {3: 0x128, 2: 0x141, 1: 0x4E, 0: 0xB1}
+
+
+def _dpp(v, bit):
+    return (f'__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, {v}), '
+            f'{_DPP[bit]:#x}, 0xf, 0xf, false))')
+
+
+def _xchg(v, bit):
+    return _dpp(v, bit) if bit < 4 else f'__shfl_xor({v}, {1 << bit}, MH_WAVE)'
+
+
+def _gy_reduce(indent, y_dim, y_pad):
+    """Sum P0..P{y_pad-1} over the 64 lanes (transpose reduction, fixed order); lane L ends up holding the total of
+    component L >> (6 - log2 y_pad), which lanes with zero low bits store to part[wave][j][.]."""
+    L = [f'{indent}P{b} = 0.0f;' for b in range(y_dim, y_pad)]
+    n = y_pad
+    for bit in range(5, -1, -1):
+        if n > 1:
+            half = n // 2
+            L.append(f'{indent}{{ const bool hi = (lane & {1 << bit}) != 0;')
+            for k in range(half):
+                L.append(f'{indent}  {{ const float s = hi ? P{k} : P{k + half}, q = hi ? P{k + half} : P{k};')
+                L.append(f'{indent}    P{k} = q + {_xchg("s", bit)}; }}')
+            L.append(f'{indent}}}')
+            n = half
+        else:
+            L.append(f'{indent}P0 += {_xchg("P0", bit)};')
+    shift = 6 - (y_pad.bit_length() - 1)
+    L.append(f'{indent}{{ const int comp = lane >> {shift};')
+    L.append(f'{indent}  if ((lane & {(1 << shift) - 1}) == 0 && comp < Y_DIM) part[wave][j][comp] = P0; }}')
+    return L
 
 
 def source(spec):
@@ -266,7 +295,8 @@ def source(spec):
     _, nx = spec.xreg()
     _, no = spec.oreg()
     log2p = spec.y_pad.bit_length() - 1
-    gyr = [s.replace('{LOG2P}', str(log2p)) for s in _gy_reduce('      ')]
+    gyr = _gy_reduce('      ', spec.y_dim, spec.y_pad)
+    pdecl = ' '.join(f'P{b} = 0.0f,' for b in range(spec.y_pad)).rstrip(',')
     L = _header(spec)
     # ---------------------------------------------------------------------------------------- forward
     L += [
@@ -333,7 +363,7 @@ def source(spec):
     for co in spec.coef:
         L += [f'      gv[{oi[co["k"]] + c}] = active ? gr[{co["o3"]} + uc * {co["d3"]} + {c}] : 0.0f;'
               for c in range(co['d3'])]
-    L += ['      float P[Y_PAD];', '      for (int b = 0; b < Y_PAD; ++b) P[b] = 0.0f;',
+    L += [f'      float {pdecl};',
           '      float* __restrict__ gwe = gW + (size_t)e * NW + uc;']
     L += _bwd_body(spec, '      ', with_gx=True, store_gw=True)
     L += ['      if (GWY) {'] + ['  ' + s for s in gyr] + ['      }']
@@ -371,7 +401,7 @@ def source(spec):
     for co in spec.coef:
         L += [f'    gv[{oi[co["k"]] + c}] = active ? gr[{co["o3"]} + uc * {co["d3"]} + {c}] : 0.0f;'
               for c in range(co['d3'])]
-    L += ['    float P[Y_PAD];', '    for (int b = 0; b < Y_PAD; ++b) P[b] = 0.0f;',
+    L += [f'    float {pdecl};',
           '    float* __restrict__ gwe = gW + (size_t)e * NW + uc;']
     L += _bwd_body(spec, '    ', with_gx=False, store_gw=True)
     L += [s[2:] for s in gyr]
@@ -474,9 +504,9 @@ class _ConvFn(torch.autograd.Function):
         rowptr, eids = gr.by_recv()
         out = torch.empty(n, op.spec.out_dim, device=x.device, dtype=torch.float32)
         lib = _native.load()
-        _native.check(lib.mh_conv_fwd(op.module.handle, _native.ptr(x), _native.ptr(Y), _native.ptr(W),
-                                      _native.ptr(rowptr), _native.ptr(eids), _native.ptr(gr.send),
-                                      _native.ptr(out), n, _native.stream_of(x)), 'conv_fwd')
+        _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, _native.ptr(x), _native.ptr(Y),
+                       _native.ptr(W), _native.ptr(rowptr), _native.ptr(eids), _native.ptr(gr.send),
+                       _native.ptr(out), n, _native.stream_of(x))
         ctx.save_for_backward(x, Y, W)
         ctx.op, ctx.gr = op, gr
         return out
@@ -499,10 +529,10 @@ class _ConvFn(torch.autograd.Function):
         if flags:
             rowptr_s, eids_s = gr.by_send()
             lib = _native.load()
-            _native.check(lib.mh_conv_bwd(op.module.handle, _native.ptr(x), _native.ptr(g), _native.ptr(Y),
-                                          _native.ptr(W), _native.ptr(rowptr_s), _native.ptr(eids_s),
-                                          _native.ptr(gr.recv), _native.ptr(gx), _native.ptr(gW), _native.ptr(gY),
-                                          x.shape[0], flags, _native.stream_of(x)), 'conv_bwd')
+            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, _native.ptr(x), _native.ptr(g),
+                           _native.ptr(Y), _native.ptr(W), _native.ptr(rowptr_s), _native.ptr(eids_s),
+                           _native.ptr(gr.recv), _native.ptr(gx), _native.ptr(gW), _native.ptr(gY), x.shape[0],
+                           flags, _native.stream_of(x))
         return gx, gY, gW, None, None
 
 
@@ -527,6 +557,7 @@ class HipConvTP(torch.nn.Module):
         self.instructions = tp.instructions
         self.weight_numel = tp.weight_numel
         self.original = [tp]          # kept (outside the module tree) so the patch can be undone
+        self.tag = 'conv'             # name used in launch timings (patch_model sets the module path)
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
         return _ConvFn.apply(node_feats, edge_attrs, tp_weights, edge_index, self)

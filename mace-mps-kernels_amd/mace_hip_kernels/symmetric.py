@@ -254,9 +254,8 @@ class _SCFn(torch.autograd.Function):
         x = x.contiguous()
         N = x.shape[0]
         out = torch.empty(N, s.out_dim, device=x.device, dtype=torch.float32)
-        _native.check(_native.load().mh_sc_fwd(op.module.handle, _native.ptr(x), _native.ptr(elem),
-                                               _native.ptr(op.T), _native.ptr(out), N, _native.stream_of(x)),
-                      'sc_fwd')
+        _native.launch(f'sc_fwd[{op.tag}]', _native.load().mh_sc_fwd, op.module.handle, _native.ptr(x),
+                       _native.ptr(elem), _native.ptr(op.T), _native.ptr(out), N, _native.stream_of(x))
         ctx.save_for_backward(x, elem)
         ctx.op = op
         return out
@@ -268,9 +267,9 @@ class _SCFn(torch.autograd.Function):
         x, elem = ctx.saved_tensors
         op = ctx.op
         gx = torch.empty_like(x)
-        _native.check(_native.load().mh_sc_bwd(op.module.handle, _native.ptr(x), _native.ptr(elem),
-                                               _native.ptr(op.T), _native.ptr(g.contiguous()), _native.ptr(gx),
-                                               x.shape[0], _native.stream_of(x)), 'sc_bwd')
+        _native.launch(f'sc_bwd[{op.tag}]', _native.load().mh_sc_bwd, op.module.handle, _native.ptr(x),
+                       _native.ptr(elem), _native.ptr(op.T), _native.ptr(g.contiguous()), _native.ptr(gx),
+                       x.shape[0], _native.stream_of(x))
         return gx, None, None
 
 
@@ -292,6 +291,7 @@ class HipSymmetricContraction(torch.nn.Module):
             })
         self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
         self.original = [sc]
+        self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
 
     def forward(self, x, y):
         if y.shape != (x.shape[0], self.spec.n_elem):
