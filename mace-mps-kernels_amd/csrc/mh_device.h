@@ -19,6 +19,16 @@ __device__ __forceinline__ int mh_xcd_block(int b, int nblocks) {
 // Value of `v` in lane `j` (j wave-uniform) as a scalar.
 __device__ __forceinline__ int mh_bcast(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
 
+// Load / store at a wave-uniform base pointer plus a 32-bit unsigned per-lane byte offset.  Written this way the
+// compiler keeps the 64-bit base in SGPRs and issues global_load/store with a 32-bit VGPR offset (saddr form), so
+// a gather from a different row costs scalar arithmetic only, no 64-bit VALU address computation per access.
+__device__ __forceinline__ float mh_ld(const float* __restrict__ base, unsigned boff) {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + boff);
+}
+__device__ __forceinline__ void mh_st(float* __restrict__ base, unsigned boff, float v) {
+    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + boff) = v;
+}
+
 // Sum each of NV per-lane values over the 64 lanes of the wave, NV a power of two <= 64.  Transpose reduction: every
 // exchange step halves the number of values a lane carries, so the cost is NV-1 + log2(64/NV) shuffles instead of
 // 6*NV.  On return every lane L holds the wave total of component (L >> (6 - log2 NV)) in v[0].  The summation

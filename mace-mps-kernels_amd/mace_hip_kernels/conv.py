@@ -29,6 +29,7 @@ import numpy as np
 import torch
 
 from . import _native
+from .conv_codegen import source
 
 WAVE = 64
 
@@ -152,263 +153,6 @@ class ConvSpec:
         bwd = 4 * (n_edges * (2 * nw + 2 * self.y_dim + 4) + n_nodes * (2 * self.x_dim + self.out_dim)
                    + 2 * (n_nodes + 1))
         return fwd, bwd
-
-
-# ------------------------------------------------------------------------------------------------- codegen
-def _lit(v):
-    """Hexadecimal fp32 literal holding exactly float32(v) (round to nearest)."""
-    return f'{float(np.float32(v)).hex()}f'
-
-
-def _sum(parts):
-    return ' + '.join(parts) if parts else '0.0f'
-
-
-def _load_y(spec, indent):
-    return [f'{indent}const float* __restrict__ ye = Y + (size_t)e * {spec.y_dim};'] + \
-           [f'{indent}const float y{j} = ye[{j}];' for j in range(spec.y_dim)]
-
-
-def _load_x(spec, indent, src='s'):
-    xi, _ = spec.xreg()
-    out = [f'{indent}const float* __restrict__ xs = x + (size_t){src} * {spec.x_dim};']
-    for b, (l, _, off) in enumerate(spec.in1):
-        d = 2 * l + 1
-        out += [f'{indent}xv[{xi[b] + m}] = xs[{off} + uc * {d} + {m}];' for m in range(d)]
-    return out
-
-
-def _load_w(spec, indent):
-    out = [f'{indent}const float* __restrict__ we = W + (size_t)e * {spec.nins * spec.mul} + uc;']
-    out += [f'{indent}const float w{k} = we[{k * spec.mul}];' for k in range(spec.nins)]
-    return out
-
-
-def _fwd_body(spec, indent):
-    """acc[o] += w_k * Σ_a x[a] * (Σ_b v·y[b])  for every output component of every instruction."""
-    xi, _ = spec.xreg()
-    oi, _ = spec.oreg()
-    L = []
-    for co in spec.coef:
-        k, i1 = co['k'], spec.ins[co['k']][0]
-        for c in range(co['d3']):
-            by_a = {}
-            for a, b, cc, v in co['terms']:
-                if cc == c:
-                    by_a.setdefault(a, []).append(f'{_lit(v)} * y{co["o2"] + b}')
-            if not by_a:
-                continue
-            t = _sum([f'xv[{xi[i1] + a}] * ({_sum(ys)})' for a, ys in sorted(by_a.items())])
-            L.append(f'{indent}acc[{oi[k] + c}] = fmaf(w{k}, {t}, acc[{oi[k] + c}]);')
-    return L
-
-
-def _bwd_body(spec, indent, with_gx, store_gw):
-    """h_a = Σ_{b,c} v·y[b]·g[c];  gx[a] += w·h_a;  gW_k = Σ_a x[a]·h_a;  P[b] += w·Σ_{a,c} v·x[a]·g[c]."""
-    xi, _ = spec.xreg()
-    oi, _ = spec.oreg()
-    L = []
-    for co in spec.coef:
-        k, i1 = co['k'], spec.ins[co['k']][0]
-        L.append(f'{indent}{{')
-        hs = []
-        for a in range(co['d1']):
-            ts = [f'{_lit(v)} * y{co["o2"] + b} * gv[{oi[k] + c}]' for aa, b, c, v in co['terms'] if aa == a]
-            if not ts:
-                continue
-            L.append(f'{indent}  const float h{a} = {_sum(ts)};')
-            hs.append(a)
-            if with_gx:
-                L.append(f'{indent}  gxa[{xi[i1] + a}] = fmaf(w{k}, h{a}, gxa[{xi[i1] + a}]);')
-        if store_gw:
-            gw = _sum([f'xv[{xi[i1] + a}] * h{a}' for a in hs])
-            L.append(f'{indent}  if (GWY && active) gwe[{k * spec.mul}] = {gw};')
-            for b in range(co['d2']):
-                ts = [f'{_lit(v)} * xv[{xi[i1] + a}] * gv[{oi[k] + c}]' for a, bb, c, v in co['terms'] if bb == b]
-                if ts:
-                    L.append(f'{indent}  P{co["o2"] + b} = fmaf(w{k}, {_sum(ts)}, P{co["o2"] + b});')
-        L.append(f'{indent}}}')
-    return L
-
-
-def _header(spec):
-    return [_native.device_header(),
-            f'#define MUL {spec.mul}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}',
-            f'#define X_DIM {spec.x_dim}', f'#define Y_DIM {spec.y_dim}', f'#define Y_PAD {spec.y_pad}',
-            f'#define OUT_DIM {spec.out_dim}', f'#define NW {spec.nins * spec.mul}']
-
-
-def _gy_combine(indent, edge_expr):
-    """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order)."""
-    return [
-        f'{indent}__syncthreads();',
-        f'{indent}for (int q = threadIdx.x; q < cnt * Y_DIM; q += BLOCK) {{',
-        f'{indent}  const int j = q / Y_DIM, b = q - j * Y_DIM;',
-        f'{indent}  float v = 0.0f;',
-        f'{indent}  for (int w = 0; w < NCB; ++w) v += part[w][j][b];',
-        f'{indent}  gY[(size_t)({edge_expr}) * Y_DIM + b] = v;',
-        f'{indent}}}',
-        f'{indent}__syncthreads();',
-    ]
-
-
-# Lane exchanges of the transpose reduction, one per lane bit from 5 down to 0.  Bits 5 and 4 cross 16-lane rows and
-# go through __shfl_xor (ds_bpermute); bits 3..0 stay inside a row and use DPP moves, which are plain VALU operands
-# (row_ror:8 = lane^8, row_half_mirror = lane^7, quad_perm [2,3,0,1] = lane^2, [1,0,3,2] = lane^1).  Every exchange
-# pairs lanes that differ in the current bit and agree in the higher ones, which is all the reduction needs.
-_DPP = {3: 0x128, 2: 0x141, 1: 0x4E, 0: 0xB1}
-
-
-def _dpp(v, bit):
-    return (f'__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, {v}), '
-            f'{_DPP[bit]:#x}, 0xf, 0xf, false))')
-
-
-def _xchg(v, bit):
-    return _dpp(v, bit) if bit < 4 else f'__shfl_xor({v}, {1 << bit}, MH_WAVE)'
-
-
-def _gy_reduce(indent, y_dim, y_pad):
-    """Sum P0..P{y_pad-1} over the 64 lanes (transpose reduction, fixed order); lane L ends up holding the total of
-    component L >> (6 - log2 y_pad), which lanes with zero low bits store to part[wave][j][.]."""
-    L = [f'{indent}P{b} = 0.0f;' for b in range(y_dim, y_pad)]
-    n = y_pad
-    for bit in range(5, -1, -1):
-        if n > 1:
-            half = n // 2
-            L.append(f'{indent}{{ const bool hi = (lane & {1 << bit}) != 0;')
-            for k in range(half):
-                L.append(f'{indent}  {{ const float s = hi ? P{k} : P{k + half}, q = hi ? P{k + half} : P{k};')
-                L.append(f'{indent}    P{k} = q + {_xchg("s", bit)}; }}')
-            L.append(f'{indent}}}')
-            n = half
-        else:
-            L.append(f'{indent}P0 += {_xchg("P0", bit)};')
-    shift = 6 - (y_pad.bit_length() - 1)
-    L.append(f'{indent}{{ const int comp = lane >> {shift};')
-    L.append(f'{indent}  if ((lane & {(1 << shift) - 1}) == 0 && comp < Y_DIM) part[wave][j][comp] = P0; }}')
-    return L
-
-
-def source(spec):
-    """HIP source of the three convolution kernels of one layer."""
-    _, nx = spec.xreg()
-    _, no = spec.oreg()
-    log2p = spec.y_pad.bit_length() - 1
-    gyr = _gy_reduce('      ', spec.y_dim, spec.y_pad)
-    pdecl = ' '.join(f'P{b} = 0.0f,' for b in range(spec.y_pad)).rstrip(',')
-    L = _header(spec)
-    # ---------------------------------------------------------------------------------------- forward
-    L += [
-        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_fwd(',
-        '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
-        '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
-        '    float* __restrict__ out, int N) {',
-        '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
-        '  if (n >= N) return;',
-        '  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1);',
-        '  const bool active = u < MUL;',
-        '  const int uc = active ? u : MUL - 1;',
-        f'  float acc[{no}];',
-        f'  for (int i = 0; i < {no}; ++i) acc[i] = 0.0f;',
-        f'  float xv[{nx}];',
-        '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
-        '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
-        '    const int cnt = min(MH_WAVE, p1 - pb);',
-        '    int my_e = 0, my_s = 0;',
-        '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }',
-        '    for (int j = 0; j < cnt; ++j) {',
-        '      const int e = mh_bcast(my_e, j), s = mh_bcast(my_s, j);',
-    ]
-    L += _load_y(spec, '      ') + _load_x(spec, '      ') + _load_w(spec, '      ') + _fwd_body(spec, '      ')
-    L += ['    }', '  }', '  if (active) {', '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
-    oi, _ = spec.oreg()
-    for co in spec.coef:
-        L += [f'    o[{co["o3"]} + u * {co["d3"]} + {c}] = acc[{oi[co["k"]] + c}];' for c in range(co['d3'])]
-    L += ['  }', '}', '']
-    # ------------------------------------------------------------------------------- fused backward
-    L += [
-        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_bwd(',
-        '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
-        '    const float* __restrict__ W, const int* __restrict__ rowptr, const int* __restrict__ eids,',
-        '    const int* __restrict__ receivers, float* __restrict__ gx, float* __restrict__ gW,',
-        '    float* __restrict__ gY, int N, int flags) {',
-        '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
-        '  const int s = mh_xcd_block(blockIdx.x, gridDim.x);',
-        '  if (s >= N) return;',
-        '  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1), wave = threadIdx.x >> 6;',
-        '  const bool active = u < MUL;',
-        '  const int uc = active ? u : MUL - 1;',
-        '  const bool GX = (flags & 1) != 0, GWY = (flags & 2) != 0;',
-        f'  float xv[{nx}];',
-        f'  for (int i = 0; i < {nx}; ++i) xv[i] = 0.0f;',
-        '  if (GWY) {',
-    ]
-    L += _load_x(spec, '    ')
-    L += [
-        '  }',
-        f'  float gxa[{nx}];',
-        f'  for (int i = 0; i < {nx}; ++i) gxa[i] = 0.0f;',
-        f'  float gv[{no}];',
-        '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
-        '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
-        '    const int cnt = min(MH_WAVE, p1 - pb);',
-        '    int my_e = 0, my_r = 0;',
-        '    if (lane < cnt) { my_e = eids[pb + lane]; my_r = receivers[my_e]; }',
-        '    for (int j = 0; j < cnt; ++j) {',
-        '      const int e = mh_bcast(my_e, j), r = mh_bcast(my_r, j);',
-    ]
-    L += _load_y(spec, '      ') + _load_w(spec, '      ')
-    L += ['      const float* __restrict__ gr = g + (size_t)r * OUT_DIM;']
-    for co in spec.coef:
-        L += [f'      gv[{oi[co["k"]] + c}] = active ? gr[{co["o3"]} + uc * {co["d3"]} + {c}] : 0.0f;'
-              for c in range(co['d3'])]
-    L += [f'      float {pdecl};',
-          '      float* __restrict__ gwe = gW + (size_t)e * NW + uc;']
-    L += _bwd_body(spec, '      ', with_gx=True, store_gw=True)
-    L += ['      if (GWY) {'] + ['  ' + s for s in gyr] + ['      }']
-    L += ['    }', '    if (GWY) {']
-    L += _gy_combine('      ', 'eids[pb + j]')
-    L += ['    }', '  }', '  if (GX && active) {', '    float* __restrict__ gxs = gx + (size_t)s * X_DIM;']
-    xi, _ = spec.xreg()
-    for b, (l, _, off) in enumerate(spec.in1):
-        d = 2 * l + 1
-        L += [f'    gxs[{off} + u * {d} + {m}] = gxa[{xi[b] + m}];' for m in range(d)]
-    L += ['  }', '}', '']
-    # ----------------------------------------------------------------- per-edge d/dW, d/dY (no CSR)
-    L += [
-        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_bwd_wy(',
-        '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
-        '    const float* __restrict__ W, const int* __restrict__ senders, const int* __restrict__ receivers,',
-        '    float* __restrict__ gW, float* __restrict__ gY, int E) {',
-        '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
-        '  const int pb = mh_xcd_block(blockIdx.x, gridDim.x) * MH_WAVE;',
-        '  if (pb >= E) return;',
-        '  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1), wave = threadIdx.x >> 6;',
-        '  const bool active = u < MUL;',
-        '  const int uc = active ? u : MUL - 1;',
-        '  const bool GWY = true;',
-        '  const int cnt = min(MH_WAVE, E - pb);',
-        f'  float xv[{nx}];',
-        f'  float gv[{no}];',
-        '  int my_s = 0, my_r = 0;',
-        '  if (lane < cnt) { my_s = senders[pb + lane]; my_r = receivers[pb + lane]; }',
-        '  for (int j = 0; j < cnt; ++j) {',
-        '    const int e = pb + j, s = mh_bcast(my_s, j), r = mh_bcast(my_r, j);',
-    ]
-    L += _load_y(spec, '    ') + _load_x(spec, '    ') + _load_w(spec, '    ')
-    L += ['    const float* __restrict__ gr = g + (size_t)r * OUT_DIM;']
-    for co in spec.coef:
-        L += [f'    gv[{oi[co["k"]] + c}] = active ? gr[{co["o3"]} + uc * {co["d3"]} + {c}] : 0.0f;'
-              for c in range(co['d3'])]
-    L += [f'    float {pdecl};',
-          '    float* __restrict__ gwe = gW + (size_t)e * NW + uc;']
-    L += _bwd_body(spec, '    ', with_gx=False, store_gw=True)
-    L += [s[2:] for s in gyr]
-    L += ['  }']
-    L += _gy_combine('  ', 'pb + j')
-    L += ['}', '']
-    return '\n'.join(L)
 
 
 # ------------------------------------------------------------------------------------------- graph cache
