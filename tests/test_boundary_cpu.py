@@ -1,0 +1,114 @@
+"""
+The drop-in boundary on the CPU (no GPU calls): the C-ABI library, the supports-checks and skip reasons of
+patch_model (reference __init__.py:34-79, conv.py:31-51, symmetric.py:42-49), code generation for gfx950, the graph
+cache, and the golden kernel fixtures.
+"""
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import mace_hip_kernels as mhk
+from mace_hip_kernels import _native, conv, symmetric
+from mace_lite import factory
+from mace_lite.o3 import FullyConnectedTensorProduct, TensorProduct
+from oracle import conv as oconv
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'mace_hip.h')
+GOLDEN = os.path.join(ROOT, 'tests', 'golden')
+
+
+def test_library_loads_and_exports_header_symbols():
+    lib = _native.load()
+    declared = set(re.findall(r'\b(mh_\w+)\s*\(', open(HEADER).read()))
+    assert declared == set(_native.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.mh_version() == _native.ABI_VERSION
+    assert lib.mh_last_error() is not None
+
+
+def test_compile_errors_are_reported():
+    with pytest.raises(RuntimeError, match='hipRTC compile'):
+        _native.compile_source('extern "C" __global__ void k() { this is not HIP; }')
+
+
+@pytest.mark.parametrize('hidden,lmax,corr', [('32x0e+32x1o', 2, 2), ('128x0e+128x1o', 3, 3),
+                                              ('64x0e', 2, 2), ('96x0e+96x1o', 3, 2)])
+def test_generated_kernels_compile_for_gfx950(hidden, lmax, corr):
+    m = factory.make_model(hidden, lmax, corr, elements=factory.ELEMENTS_PTCOH)
+    for blk in m.interactions:
+        code = _native.compile_source(conv.source(conv.ConvSpec(blk.conv_tp)))
+        assert code[:4] == b'\x7fELF'
+    for prod in m.products:
+        code = _native.compile_source(symmetric.source(symmetric.SCSpec(prod.symmetric_contractions)))
+        assert code[:4] == b'\x7fELF'
+
+
+def test_conv_supported_reasons():
+    m = factory.make_model('48x0e+48x1o', 3, 3)
+    ok, why = conv.conv_supported(m.interactions[1].conv_tp)
+    assert not ok and 'multiple of 32' in why
+    ok, why = conv.conv_supported(m.interactions[1].skip_tp)          # uvw, internal shared weights
+    assert not ok and 'uvu' in why
+    tp = m.interactions[1].conv_tp
+    shared = TensorProduct(tp.irreps_in1, tp.irreps_in2, tp.irreps_out,
+                           [(i.i_in1, i.i_in2, i.i_out, 'uvu', True) for i in tp.instructions])
+    ok, why = conv.conv_supported(shared)
+    assert not ok and 'per-edge' in why
+    ok, why = conv.conv_supported(object())
+    assert not ok and 'not an e3nn TensorProduct' in why
+    ok, why = conv.conv_supported(factory.make_model('32x0e+32x1o', 3, 3).interactions[1].conv_tp)
+    assert ok and why == ''
+    assert not symmetric.sc_supported(object())[0]
+    assert symmetric.sc_supported(m.products[0].symmetric_contractions) == (True, '')
+    assert isinstance(FullyConnectedTensorProduct('2x0e', '1x0e', '2x0e'), TensorProduct)
+
+
+def test_patch_model_refuses_cpu_and_float64():
+    m = factory.make_model('32x0e+32x1o', 2, 2)
+    with pytest.raises(RuntimeError, match='ROCm GPU'):
+        mhk.patch_model(m)
+    with pytest.raises(RuntimeError):
+        mhk.patch_model(m.double())
+
+
+def test_block_conv_fusion_detection():
+    m = factory.make_model('32x0e+32x1o', 2, 2)
+    assert all(mhk._block_has_conv_fusion(b) for b in m.interactions)
+    assert not mhk._block_has_conv_fusion(torch.nn.Linear(2, 2))
+
+
+def test_graph_cache_and_validation():
+    conv.clear_graph_cache()
+    ei = torch.tensor([[0, 1, 2, 2], [1, 2, 0, 1]])
+    g1 = conv.graph_for(ei, 3)
+    assert conv.graph_for(ei, 3) is g1                       # same tensor object, same version: cached
+    rp, eids = g1.by_recv()
+    assert rp.tolist() == [0, 1, 3, 4] and eids.tolist() == [2, 0, 3, 1]
+    rp, eids = g1.by_send()
+    assert rp.tolist() == [0, 1, 2, 4] and eids.tolist() == [0, 1, 2, 3]
+    ei[1, 0] = 2                                              # in-place change bumps the version
+    g2 = conv.graph_for(ei, 3)
+    assert g2 is not g1 and g2.by_recv()[0].tolist() == [0, 1, 2, 4]
+    assert conv.graph_for(ei.clone(), 3) is not g2           # a different tensor object
+    with pytest.raises(ValueError, match='outside'):
+        conv.graph_for(torch.tensor([[0, 5], [1, 0]]), 3)
+    with pytest.raises(ValueError):
+        conv.graph_for(torch.tensor([0, 1, 2]), 3)
+
+
+def test_golden_fixtures_reproduce():
+    """The oracle still produces the committed fixtures that the GPU tests compare the kernels with."""
+    g = np.load(os.path.join(GOLDEN, 'conv_small.npz'))
+    tp = factory.make_model('32x0e+32x1o', 3, 3).interactions[1].conv_tp
+    desc = oconv.describe_tp(tp)
+    coef = oconv.path_terms(desc)
+    s, r, n = g['sender'], g['receiver'], int(g['n'])
+    assert np.abs(oconv.conv_fwd(desc, coef, g['x'], g['Y'], g['W'], s, r, n) - g['out']).max() < 1e-12
+    assert np.abs(oconv.conv_bwd_x(desc, coef, g['g'], g['Y'], g['W'], s, r, n) - g['gx']).max() < 1e-12
+    assert np.abs(oconv.conv_bwd_w(desc, coef, g['x'], g['g'], g['Y'], s, r) - g['gW']).max() < 1e-12
+    assert np.abs(oconv.conv_bwd_y(desc, coef, g['x'], g['g'], g['W'], s, r) - g['gY']).max() < 1e-12

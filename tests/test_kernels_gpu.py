@@ -182,6 +182,30 @@ def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr):
         assert _rel(xt.grad.double().cpu().numpy(), xo.grad.numpy()) < SC_TOL
 
 
+def test_kernels_match_golden_fixtures():
+    """Kernels against the committed oracle fixtures (tests/golden/make_golden.py)."""
+    import os
+    dev = _dev()
+    print('[case] golden fixtures', flush=True)
+    gdir = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
+    model = factory.make_model('32x0e+32x1o', 3, 3)
+    g = np.load(os.path.join(gdir, 'conv_small.npz'))
+    op = HipConvTP(model.interactions[1].conv_tp, device=dev)
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+    xt, Yt, Wt = t(g['x']), t(g['Y']), t(g['W'])
+    out = op(xt, Yt, Wt, torch.tensor(np.stack([g['sender'], g['receiver']]), device=dev))
+    out.backward(torch.tensor(g['g'], dtype=torch.float32, device=dev))
+    for got, want in ((out, g['out']), (xt.grad, g['gx']), (Wt.grad, g['gW']), (Yt.grad, g['gY'])):
+        assert _rel(got.detach().double().cpu().numpy(), want) < CONV_TOL
+    f = np.load(os.path.join(gdir, 'sc_small.npz'))
+    op = HipSymmetricContraction(model.products[0].symmetric_contractions, device=dev)
+    xt = torch.tensor(f['x'], dtype=torch.float32, device=dev, requires_grad=True)
+    out = op(xt, torch.tensor(np.eye(4)[f['elem']], dtype=torch.float32, device=dev))
+    out.backward(torch.tensor(f['g'], dtype=torch.float32, device=dev))
+    assert _rel(out.detach().double().cpu().numpy(), f['out']) < SC_TOL
+    assert _rel(xt.grad.double().cpu().numpy(), f['gx']) < SC_TOL
+
+
 def test_library_runtime_is_torchs():
     dev = _dev()
     print('[case] runtime binding', flush=True)
