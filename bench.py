@@ -113,9 +113,77 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
                 cpu=platform.processor() or platform.machine(), seconds=round(dt * steps, 2))
 
 
+COPY_BYTES = 1 << 30          # size of the calibration copy (read 1 GiB, write 1 GiB) of --profile
+
+
+def _profile(a):
+    """Patched E+F calls only (for rocprofv3), then a plain elementwise copy of known size whose FETCH_SIZE and
+    WRITE_SIZE calibrate the counters."""
+    import torch
+    from mace_hip_kernels import patch_model
+    from mace_lite import data as D
+    from mace_lite import factory
+    dev = torch.device('cuda:0')
+    model, batch_cpu, meta = factory.workload(a.config)
+    met = model.to(dev)
+    patch_model(met, verbose=False)
+    batch = D.fresh(_to(batch_cpu, dev))
+    for _ in range(a.warmup + a.steps):
+        met(batch, compute_force=True)
+    x = torch.ones(COPY_BYTES // 4, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.mul(x, 2.0, out=y)
+    torch.cuda.synchronize()
+    _log(f'profile run done: {meta["name"]}, {a.warmup + a.steps} E+F calls, 3 x {COPY_BYTES >> 20} MiB copy')
+
+
+def _summarize(a):
+    """Markdown summary of rocprofv3 output directories (kernel stats, and FETCH_SIZE / WRITE_SIZE counters)."""
+    import csv
+    import glob
+
+    def rows(d, pattern):
+        out = []
+        for f in sorted(glob.glob(os.path.join(d, '**', pattern), recursive=True)):
+            with open(f) as fh:
+                out += list(csv.DictReader(fh))
+        return out
+
+    stats = rows(a.summarize_rocprof, '*kernel_stats.csv')
+    print('| kernel | calls | mean us | min us | max us | share of GPU time |')
+    print('|---|---:|---:|---:|---:|---:|')
+    for r in sorted(stats, key=lambda r: -float(r['TotalDurationNs']))[:a.top]:
+        print(f"| {r['Name'][:80]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} "
+              f"| {float(r['MaxNs']) / 1e3:.1f} | {float(r['Percentage']):.1f}% |")
+    for label, d, counter in (('FETCH_SIZE', a.pmc_fetch, 'FETCH_SIZE'), ('WRITE_SIZE', a.pmc_write, 'WRITE_SIZE')):
+        if not d:
+            continue
+        acc = {}
+        for r in rows(d, '*counter_collection.csv'):
+            if r.get('Counter_Name') != counter:
+                continue
+            k = r['Kernel_Name']
+            n, s = acc.get(k, (0, 0.0))
+            acc[k] = (n + 1, s + float(r['Counter_Value']))
+        print(f'\n{label} (KiB per dispatch, mean over dispatches)\n')
+        print('| kernel | dispatches | KiB per dispatch |')
+        print('|---|---:|---:|')
+        for k, (n, s) in sorted(acc.items(), key=lambda t: -t[1][1] / t[1][0]):
+            if a.filter and not any(f in k for f in a.filter.split(',')):
+                continue
+            print(f'| {k[:80]} | {n} | {s / n:.1f} |')
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--profile', action='store_true', help='patched calls + calibration copy only (for rocprofv3)')
+    ap.add_argument('--summarize-rocprof', metavar='DIR', help='print a markdown summary of rocprofv3 output and exit')
+    ap.add_argument('--pmc-fetch', metavar='DIR')
+    ap.add_argument('--pmc-write', metavar='DIR')
+    ap.add_argument('--filter', default='conv_,sc_,MulFunctor', help='kernel-name substrings kept in counter tables')
+    ap.add_argument('--top', type=int, default=30)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--config', type=int, default=2, choices=[0, 1, 2, 3])
@@ -124,6 +192,9 @@ def main():
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--no-e3nn', action='store_true')
     a = ap.parse_args()
+    if a.summarize_rocprof:
+        _summarize(a)
+        return
     if a.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py: this build runs on one GPU only (no multi-GPU path is built; batched structures would '
               'shard as independent units, see DESIGN.md). Run with --gpus 1.', file=sys.stderr)
@@ -135,6 +206,9 @@ def main():
     from mace_lite import factory
 
     assert torch.cuda.is_available(), 'bench.py needs a GPU'
+    if a.profile:
+        _profile(a)
+        return
     dev = torch.device('cuda:0')
     sync = torch.cuda.synchronize
     model, batch_cpu, meta = factory.workload(a.config)

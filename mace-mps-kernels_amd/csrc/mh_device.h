@@ -28,6 +28,14 @@ __device__ __forceinline__ float mh_ld(const float* __restrict__ base, unsigned 
 __device__ __forceinline__ void mh_st(float* __restrict__ base, unsigned boff, float v) {
     *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + boff) = v;
 }
+// Streaming (non-temporal) variants for data touched once per call (edge weights in, weight gradients out): they
+// do not displace the node rows that the edge loop gathers repeatedly from L2.
+__device__ __forceinline__ float mh_ld_nt(const float* __restrict__ base, unsigned boff) {
+    return __builtin_nontemporal_load(reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + boff));
+}
+__device__ __forceinline__ void mh_st_nt(float* __restrict__ base, unsigned boff, float v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<float*>(reinterpret_cast<char*>(base) + boff));
+}
 
 // Sum each of NV per-lane values over the 64 lanes of the wave, NV a power of two <= 64.  Transpose reduction: every
 // exchange step halves the number of values a lane carries, so the cost is NV-1 + log2(64/NV) shuffles instead of

@@ -121,6 +121,10 @@ class ConvSpec:
         self.block = self.ncb * WAVE
         self.y_pad = 1 << max(0, (self.y_dim - 1).bit_length())
 
+    def kname(self, base):
+        """Kernel symbol of this layer (shape-tagged so profiles tell the layers apart)."""
+        return f'{base}_x{self.x_dim}_o{self.out_dim}'
+
     def xreg(self):
         r, idx = 0, {}
         for b, (l, _, _) in enumerate(self.in1):
@@ -293,9 +297,9 @@ class HipConvTP(torch.nn.Module):
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
             self.module = _native.Module(code, {
-                _native.MH_CONV_FWD: ('conv_fwd', self.spec.block, 1),
-                _native.MH_CONV_BWD: ('conv_bwd', self.spec.block, 1),
-                _native.MH_CONV_BWD_WY: ('conv_bwd_wy', self.spec.block, WAVE),
+                _native.MH_CONV_FWD: (self.spec.kname('conv_fwd'), self.spec.block, 1),
+                _native.MH_CONV_BWD: (self.spec.kname('conv_bwd'), self.spec.block, 1),
+                _native.MH_CONV_BWD_WY: (self.spec.kname('conv_bwd_wy'), self.spec.block, WAVE),
             })
         self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
         self.instructions = tp.instructions

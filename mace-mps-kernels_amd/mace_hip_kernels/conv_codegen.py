@@ -29,6 +29,15 @@ def _sum(parts):
     return ' + '.join(parts) if parts else '0.0f'
 
 
+# fused backward: load each edge's inputs one iteration ahead of its use (see source())
+PIPELINE_BWD = True
+
+
+def _nxt(name):
+    """Next-stage register of a per-edge input: y3 -> yn3, w2 -> wn2, gv5 -> gvn5."""
+    return 'gvn' + name[2:] if name.startswith('gv') else name[0] + 'n' + name[1:]
+
+
 class _Gen:
     """Shared naming for the three kernels of one spec."""
 
@@ -75,6 +84,27 @@ class _Gen:
                   for c in range(d3)]
         return L
 
+    # --- software-pipelined backward: the edge's inputs are loaded one iteration ahead into the "n" stage
+    def stage_names(self):
+        s = self.s
+        return ([f'y{j}' for j in range(s.y_dim)] + [f'w{k}' for k in range(s.nins)] +
+                [f'gv{i}' for i in range(self.no)])
+
+    def ld_stage(self, ind, e, r):
+        """Issue the loads of edge (e, receiver r) into the next-stage registers yn*, wn*, gvn*."""
+        s = self.s
+        mask = '' if self.full else ' * am'
+        L = [f'{ind}{{ const float* __restrict__ ye = Y + (size_t)({e}) * Y_DIM;',
+             f'{ind}  const float* __restrict__ we = W + (size_t)({e}) * NW;',
+             f'{ind}  const float* __restrict__ gr = g + (size_t)({r}) * OUT_DIM;']
+        L += [f'{ind}  yn{j} = ye[{j}];' for j in range(s.y_dim)]
+        L += [f'{ind}  wn{k} = mh_ld(we + {k * s.mul}, ol1);' for k in range(s.nins)]
+        for co in s.coef:
+            L += [f'{ind}  gvn{self.oi[co["k"]] + c} = mh_ld(gr + {co["o3"] + c}, ol{co["d3"]}){mask};'
+                  for c in range(co['d3'])]
+        L.append(f'{ind}}}')
+        return L
+
     def fwd_body(self, ind):
         """acc[o] += w_k · Σ_a x[a] · (Σ_b v·y[b]) for every output component of every instruction."""
         L = []
@@ -109,7 +139,7 @@ class _Gen:
                 if with_gx:
                     L.append(f'{ind}  gxa{self.xi[i1] + a} = fmaf(w{k}, h{a}, gxa{self.xi[i1] + a});')
             gw = _sum([f'xv{self.xi[i1] + a} * h{a}' for a in hs])
-            st = f'mh_st(gwe + {k * s.mul}, ol1, {gw});'
+            st = f'mh_st_nt(gwe + {k * s.mul}, ol1, {gw});'       # written once, never re-read here
             L.append(f'{ind}  if (GWY) {st}' if self.full else f'{ind}  if (GWY && active) {st}')
             for b in range(co['d2']):
                 ts = [f'{_lit(v)} * xv{self.xi[i1] + a} * gv{self.oi[k] + c}'
@@ -185,7 +215,7 @@ def source(spec):
     xdecl = 'float ' + ', '.join(f'xv{i}' for i in range(nx)) + ';'
     # ------------------------------------------------------------------------------------------- forward
     L += [
-        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_fwd(',
+        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwd")}(',
         '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
         '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
         '    float* __restrict__ out, int N) {',
@@ -209,7 +239,7 @@ def source(spec):
     L += ['  }', '}', '']
     # ----------------------------------------------------------------------------------- fused backward
     L += [
-        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_bwd(',
+        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwd")}(',
         '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
         '    const float* __restrict__ W, const int* __restrict__ rowptr, const int* __restrict__ eids,',
         '    const int* __restrict__ receivers, float* __restrict__ gx, float* __restrict__ gW,',
@@ -231,10 +261,22 @@ def source(spec):
         '    const int cnt = min(MH_WAVE, p1 - pb);',
         '    int my_e = 0, my_r = 0;',
         '    if (lane < cnt) { my_e = eids[pb + lane]; my_r = receivers[my_e]; }',
-        '    for (int j = 0; j < cnt; ++j) {',
-        '      const int e = mh_bcast(my_e, j), r = mh_bcast(my_r, j);',
     ]
-    L += G.ld_y('      ') + G.ld_w('      ') + G.ld_g('      ')
+    if PIPELINE_BWD:
+        # Edge j+1's loads are issued before edge j's gW stores.  vmcnt counts loads and stores in issue order, so
+        # waiting for the next edge's inputs then never waits for the previous edge's stores.
+        names = G.stage_names()
+        L += ['    float ' + ', '.join(_nxt(n) for n in names) + ';',
+              '    int en = mh_bcast(my_e, 0), rn = mh_bcast(my_r, 0);']
+        L += G.ld_stage('    ', 'en', 'rn')
+        L += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = en, r = rn;']
+        L += [f'      const float {n} = {_nxt(n)};' for n in names]
+        L += ['      if (j + 1 < cnt) {', '        en = mh_bcast(my_e, j + 1); rn = mh_bcast(my_r, j + 1);']
+        L += G.ld_stage('        ', 'en', 'rn')
+        L += ['      }']
+    else:
+        L += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j), r = mh_bcast(my_r, j);']
+        L += G.ld_y('      ') + G.ld_w('      ') + G.ld_g('      ')
     L += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
     L += G.bwd_body('      ', with_gx=True)
     L += ['      if (GWY) {'] + ['  ' + t for t in gyr] + ['      }']
@@ -247,7 +289,7 @@ def source(spec):
     L += ['  }', '}', '']
     # --------------------------------------------------------------------- per-edge d/dW, d/dY (no CSR)
     L += [
-        'extern "C" __global__ __launch_bounds__(BLOCK) void conv_bwd_wy(',
+        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwd_wy")}(',
         '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
         '    const float* __restrict__ W, const int* __restrict__ senders, const int* __restrict__ receivers,',
         '    float* __restrict__ gW, float* __restrict__ gY, int E) {',

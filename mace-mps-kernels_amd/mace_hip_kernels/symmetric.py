@@ -101,6 +101,10 @@ class SCSpec:
         self.ncb = (self.C + WAVE - 1) // WAVE
         self.block = self.ncb * WAVE
 
+    def kname(self, base):
+        """Kernel symbol of this layer (shape-tagged so profiles tell the layers apart)."""
+        return f'{base}_c{self.C}_o{self.out_dim}_r{self.nrows}'
+
     def flops(self):
         """(fwd, bwd) fp32 FLOP per (node, channel) as the generated code evaluates them."""
         fwd = bwd = 0
@@ -196,7 +200,7 @@ def source(spec):
     ]
     trie = _trie(spec)
     # ------------------------------------------------------------------------------------- forward
-    L += ['extern "C" __global__ __launch_bounds__(BLOCK) void sc_fwd(const float* __restrict__ X,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwd")}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const float* __restrict__ T, float* __restrict__ out, int N) {']
     L += head
     for bi, bl in enumerate(spec.blocks):
@@ -208,7 +212,7 @@ def source(spec):
         L += [f'    out[(size_t)b * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{bi}_{m};' for m in range(M)]
     L += ['  }', '}', '']
     # ------------------------------------------------------------------------------------ backward
-    L += ['extern "C" __global__ __launch_bounds__(BLOCK) void sc_bwd(const float* __restrict__ X,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwd")}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const float* __restrict__ T, const float* __restrict__ G,',
           '    float* __restrict__ GX, int N) {']
     L += head
@@ -286,8 +290,8 @@ class HipSymmetricContraction(torch.nn.Module):
         code = _native.compile_source(self.source)
         with torch.cuda.device(dev):
             self.module = _native.Module(code, {
-                _native.MH_SC_FWD: ('sc_fwd', self.spec.block, 1),
-                _native.MH_SC_BWD: ('sc_bwd', self.spec.block, 1),
+                _native.MH_SC_FWD: (self.spec.kname('sc_fwd'), self.spec.block, 1),
+                _native.MH_SC_BWD: (self.spec.kname('sc_bwd'), self.spec.block, 1),
             })
         self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
         self.original = [sc]

@@ -113,7 +113,9 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
     assert _rel(gx.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, W, s, r, n)) < CONV_TOL
     assert _rel(gW.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
     assert _rel(gY.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
-    assert torch.equal(gx, gx2) and torch.equal(gW, gW2)
+    assert torch.equal(gx, gx2)                  # same kernel (fused backward), different flags: bitwise
+    # different kernels (per-edge vs fused): same formulas, possibly different fp32 contraction order
+    assert _rel(gW2.double().cpu().numpy(), gW.double().cpu().numpy()) < 1e-6
     assert _rel(gY2.double().cpu().numpy(), gY.double().cpu().numpy()) < 1e-6
 
 
