@@ -65,18 +65,18 @@ def _kernel_table(met, batch, n_real_edges, summary):
             s = m.spec
             bf, bb = s.bytes(n, n_real_edges)
             ff, fb = s.flops()
-            rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul)
-            rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul)
+            rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul, s.kname('conv_fwd'))
+            rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul, s.kname('conv_bwd'))
         elif isinstance(m, HipSymmetricContraction):
             s = m.spec
             bf, bb = s.bytes(n, n_elem_used)
             ff, fb = s.flops()
-            rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C)
-            rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C)
+            rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C, s.kname('sc_fwd'))
+            rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C, s.kname('sc_bwd'))
     out = {}
     for tag, (cnt, ms) in summary.items():
-        nbytes, flops = rows.get(tag, (0, 0))
-        out[tag] = dict(launches=cnt, ms=round(ms, 5), bytes=int(nbytes), flops=int(flops),
+        nbytes, flops, sym = rows.get(tag, (0, 0, None))
+        out[tag] = dict(symbol=sym, launches=cnt, ms=round(ms, 5), bytes=int(nbytes), flops=int(flops),
                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
                         tflops=round(flops / (ms * 1e-3) / 1e12, 2) if ms > 0 else None)
     del torch
@@ -130,10 +130,11 @@ def _profile(a):
     batch = D.fresh(_to(batch_cpu, dev))
     for _ in range(a.warmup + a.steps):
         met(batch, compute_force=True)
-    x = torch.ones(COPY_BYTES // 4, device=dev)
+    # calibration: an elementwise kernel whose name occurs nowhere in the model (reads and writes COPY_BYTES)
+    x = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
     y = torch.empty_like(x)
     for _ in range(3):
-        torch.mul(x, 2.0, out=y)
+        torch.bitwise_not(x, out=y)
     torch.cuda.synchronize()
     _log(f'profile run done: {meta["name"]}, {a.warmup + a.steps} E+F calls, 3 x {COPY_BYTES >> 20} MiB copy')
 
@@ -182,7 +183,7 @@ def main():
     ap.add_argument('--summarize-rocprof', metavar='DIR', help='print a markdown summary of rocprofv3 output and exit')
     ap.add_argument('--pmc-fetch', metavar='DIR')
     ap.add_argument('--pmc-write', metavar='DIR')
-    ap.add_argument('--filter', default='conv_,sc_,MulFunctor', help='kernel-name substrings kept in counter tables')
+    ap.add_argument('--filter', default='conv_,sc_,bitwise_not', help='kernel-name substrings kept in counter tables')
     ap.add_argument('--top', type=int, default=30)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
@@ -267,6 +268,16 @@ def main():
         cpu = _cpu_baseline(copy.deepcopy(model), batch_cpu, n_structs, a.cpu_sample, a.cpu_steps)
         _log('cpu baseline:', cpu)
 
+    # HBM traffic of the dominant kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE run of this workload
+    # (calibrated against a copy of known size); null when no such measurement exists for this config
+    traffic, traffic_src = None, None
+    tf = os.path.join(ROOT, 'profiles', f'traffic_cfg{a.config}.json')
+    if os.path.exists(tf):
+        with open(tf) as fh:
+            tj = json.load(fh)
+        rec = tj['kernels'].get(d.get('symbol') or '')
+        if rec:
+            traffic, traffic_src = int(rec['traffic_bytes']), tj['source']
     conv_total = {k: v for k, v in kern.items() if k.startswith('conv')}
     conv_bytes = sum(v['bytes'] * v['launches'] for v in conv_total.values())
     conv_ms = sum(v['ms'] * v['launches'] for v in conv_total.values())
@@ -290,7 +301,7 @@ def main():
         'ms_per_step_new_graph_tensors': round(dt_fresh * 1e3, 4),
         'conv_hbm_gbs': round(conv_bytes / (conv_ms * 1e-3) / 1e9, 1) if conv_ms else None,
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': d['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
-                     'frac': round(d['gbs'] / HBM_PEAK_GBS, 4), 'traffic': None,
+                     'frac': round(d['gbs'] / HBM_PEAK_GBS, 4), 'traffic': traffic, 'traffic_source': traffic_src,
                      'bytes_per_launch': d['bytes'], 'ms_per_launch': d['ms']},
         'kernels': kern,
         'e3nn_gpu': e3nn_res,
