@@ -41,7 +41,9 @@ enum mh_kernel_kind {
     MH_CONV_BWD_WY = 2,  /* d/dW, d/dY only: chunks of consecutive edges, no CSR                  */
     MH_SC_FWD = 3,       /* node rows                                                             */
     MH_SC_BWD = 4,       /* node rows                                                             */
-    MH_NUM_KINDS = 5
+    MH_CONV_BWD_R = 5,   /* d/dW, d/dY and per-edge dX messages: receiver rows over the receiver CSR */
+    MH_CONV_GXSUM = 6,   /* dX = sum of an edge-row array over the sender CSR: sender rows        */
+    MH_NUM_KINDS = 7
 };
 
 /* flags of mh_conv_bwd */
@@ -90,11 +92,25 @@ int mh_conv_bwd_wy(mh_module* m, const float* x, const float* g, const float* Y,
                    const int32_t* senders, const int32_t* receivers, float* gW, float* gY, int32_t E, void* stream);
 
 /* Fused backward over the sender-sorted CSR: one pass computes any of gx (flags & MH_WANT_GX) and gW, gY
- * (flags & MH_WANT_GWY), reading W and g once.  Outputs not wanted may be NULL.  This is the path
- * mace_hip_kernels uses; it replaces the pair lib.conv_bwd_x + lib.conv_bwd_wy (reference conv.py:252-270). */
+ * (flags & MH_WANT_GWY), reading W once and gathering the g row of every edge's receiver.  Outputs not wanted may
+ * be NULL.  mace_hip_kernels uses it when only gx is wanted; it replaces the pair lib.conv_bwd_x +
+ * lib.conv_bwd_wy (reference conv.py:252-270). */
 int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
                 const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* receivers, float* gx, float* gW,
                 float* gY, int32_t N, int32_t flags, void* stream);
+
+/* Backward in receiver order, the path mace_hip_kernels uses whenever gW and gY are wanted (flags must hold
+ * MH_WANT_GWY).  Kernel MH_CONV_BWD_R walks the receiver CSR (rowptr_r, eids_r, senders: the forward's), keeps
+ * g[r] in registers for the whole row and writes gW[e] and gY[e].  With MH_WANT_GX it also writes each edge's dX
+ * message work[e, :] = Σ_k W·∂TP/∂x · g[r] ([E, X_DIM] floats of caller-owned scratch), and kernel MH_CONV_GXSUM
+ * then sums them over the sender CSR (rowptr_s, eids_s) in CSR order: gx[s] = Σ_{p} work[eids_s[p], :].  No
+ * atomics; the result is deterministic.  Together the two kernels replace lib.conv_bwd_wy + lib.conv_bwd_x
+ * (reference conv.py:144-222, launched at conv.py:259-270).  Without MH_WANT_GX, rowptr_s, eids_s, gx and work
+ * may be NULL. */
+int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                     const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
+                     const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
+                     int32_t N, int32_t flags, void* stream);
 
 /* Symmetric contraction forward: out[b, off + c*M + m] = Σ_terms T[elem[b], r0+m, c] Π X[b, c, idx].
  * Replaces lib.sc_fwd (reference symmetric.py:82-105, launched at symmetric.py:140). */

@@ -16,9 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, 'libmace_hip.so')
 DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
 
-MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD = range(5)
+MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, MH_CONV_GXSUM = range(7)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -43,6 +43,7 @@ _SIGS = {
     'mh_conv_bwd_x': (ctypes.c_int, [_P] * 8 + [_I, _P]),
     'mh_conv_bwd_wy': (ctypes.c_int, [_P] * 9 + [_I, _P]),
     'mh_conv_bwd': (ctypes.c_int, [_P] * 11 + [_I, _I, _P]),
+    'mh_conv_bwd_recv': (ctypes.c_int, [_P] * 14 + [_I, _I, _P]),
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
     'mh_sc_bwd': (ctypes.c_int, [_P] * 6 + [_I, _P]),
 }
@@ -171,3 +172,27 @@ def ptr(t):
 
 def stream_of(t):
     return _P(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+# ------------------------------------------------------------------------------------------- graph capture
+# Device memory that a graph being captured reads but does not own (cached CSRs and element indices built by earlier
+# eager calls).  A captured kernel node keeps raw pointers, so whoever owns the graph must keep these objects alive:
+# ``graphs.capture`` takes them with ``take_capture_holds`` right after capture.
+_capture_holds = []
+
+
+def capturing():
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
+def hold_for_capture(obj):
+    """Register ``obj`` as read by the graph being captured on the current stream (no-op outside capture)."""
+    if capturing():
+        _capture_holds.append(obj)
+    return obj
+
+
+def take_capture_holds():
+    held = list(_capture_holds)
+    _capture_holds.clear()
+    return held

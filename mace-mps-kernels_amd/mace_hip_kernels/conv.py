@@ -29,7 +29,7 @@ import numpy as np
 import torch
 
 from . import _native
-from .conv_codegen import source
+from .conv_codegen import gxsum_block, source
 
 WAVE = 64
 
@@ -189,13 +189,21 @@ class _Graph:
 
     def by_recv(self):
         if self._by_recv is None:
+            self._check_not_capturing()
             self._by_recv = csr_by(self._ei[1], self.n)
         return self._by_recv
 
     def by_send(self):
         if self._by_send is None:
+            self._check_not_capturing()
             self._by_send = csr_by(self._ei[0], self.n)
         return self._by_send
+
+    @staticmethod
+    def _check_not_capturing():
+        if _native.capturing():
+            raise RuntimeError('mace_hip_kernels: a CSR of this graph is first needed inside a HIP graph capture; '
+                               'warm up with the same call (forward and backward) before capturing')
 
 
 _graph_cache = []          # [(weakref(edge_index), version, n, _Graph)], most recent first
@@ -209,7 +217,11 @@ def graph_for(edge_index, n):
         if ref() is edge_index and v == ver and nn_ == n:
             if i:
                 _graph_cache.insert(0, _graph_cache.pop(i))
-            return gr
+            return _native.hold_for_capture(gr)
+    if _native.capturing():
+        # building a graph validates it on the host (a synchronisation), which a capture cannot contain
+        raise RuntimeError('mace_hip_kernels: this edge_index is new inside a HIP graph capture; run the model once '
+                           'eagerly on the same tensors before capturing (mace_hip_kernels.graphs.capture does)')
     gr = _Graph(edge_index, n)
     _graph_cache.insert(0, (weakref.ref(edge_index), ver, n, gr))
     del _graph_cache[_GRAPH_CACHE_SIZE:]
@@ -242,6 +254,23 @@ def _check_inputs(op, x, Y, W, edge_index):
         raise ValueError('graph too large for int32 indices')
 
 
+def _grad_needed(ctx, i):
+    """Whether this backward pass uses the gradient of input i.  ``needs_input_grad`` is fixed at forward time; the
+    engine knows more: under ``autograd.grad(E, positions)`` the branch from the first layer's node features to
+    ``node_attrs`` is never executed, so that gradient would be computed and dropped.  e3nn's own backward ops skip
+    such outputs through the engine's output mask; here the engine is asked whether the node that receives the
+    gradient will run.  Anything it cannot answer (a leaf that is itself a requested input) counts as needed."""
+    if not ctx.needs_input_grad[i]:
+        return False
+    node = ctx.next_functions[i][0]
+    if node is None:
+        return True
+    try:
+        return bool(torch._C._will_engine_execute_node(node))
+    except (RuntimeError, AttributeError):
+        return True
+
+
 class _ConvFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, Y, W, edge_index, op):
@@ -266,21 +295,29 @@ class _ConvFn(torch.autograd.Function):
         x, Y, W = ctx.saved_tensors
         op, gr = ctx.op, ctx.gr
         g = g.contiguous()
-        want_x = ctx.needs_input_grad[0]
-        want_wy = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
+        want_x = _grad_needed(ctx, 0)
+        want_wy = _grad_needed(ctx, 1) or _grad_needed(ctx, 2)
         gx = torch.empty_like(x) if want_x else None
         gW = torch.empty_like(W) if want_wy else None
         gY = torch.empty_like(Y) if want_wy else None
         # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
         flags = (_native.MH_WANT_GX if want_x else 0) | \
             (_native.MH_WANT_GWY if want_wy and W.shape[0] > 0 else 0)
-        if flags:
+        lib = _native.load()
+        P = _native.ptr
+        if flags & _native.MH_WANT_GWY and op.bwd_recv:
+            # receiver order: g rows read once per receiver; dX goes through per-edge messages in `work`
+            rowptr_r, eids_r = gr.by_recv()
+            rowptr_s, eids_s = gr.by_send() if want_x else (None, None)
+            work = torch.empty(W.shape[0], op.spec.x_dim, device=x.device, dtype=torch.float32) if want_x else None
+            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv, op.module.handle, P(x), P(g), P(Y), P(W),
+                           P(rowptr_r), P(eids_r), P(gr.send), P(rowptr_s), P(eids_s), P(work), P(gx), P(gW), P(gY),
+                           x.shape[0], flags, _native.stream_of(x))
+        elif flags:
             rowptr_s, eids_s = gr.by_send()
-            lib = _native.load()
-            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, _native.ptr(x), _native.ptr(g),
-                           _native.ptr(Y), _native.ptr(W), _native.ptr(rowptr_s), _native.ptr(eids_s),
-                           _native.ptr(gr.recv), _native.ptr(gx), _native.ptr(gW), _native.ptr(gY), x.shape[0],
-                           flags, _native.stream_of(x))
+            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, P(x), P(g), P(Y), P(W),
+                           P(rowptr_s), P(eids_s), P(gr.recv), P(gx), P(gW), P(gY), x.shape[0], flags,
+                           _native.stream_of(x))
         return gx, gY, gW, None, None
 
 
@@ -300,12 +337,16 @@ class HipConvTP(torch.nn.Module):
                 _native.MH_CONV_FWD: (self.spec.kname('conv_fwd'), self.spec.block, 1),
                 _native.MH_CONV_BWD: (self.spec.kname('conv_bwd'), self.spec.block, 1),
                 _native.MH_CONV_BWD_WY: (self.spec.kname('conv_bwd_wy'), self.spec.block, WAVE),
+                _native.MH_CONV_BWD_R: (self.spec.kname('conv_bwdr'), self.spec.block, 1),
+                _native.MH_CONV_GXSUM: (self.spec.kname('conv_gxsum'), gxsum_block(self.spec), 1),
             })
         self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
         self.instructions = tp.instructions
         self.weight_numel = tp.weight_numel
         self.original = [tp]          # kept (outside the module tree) so the patch can be undone
         self.tag = 'conv'             # name used in launch timings (patch_model sets the module path)
+        # backward walks the receiver CSR when gW/gY are wanted (False: the sender-ordered fused kernel)
+        self.bwd_recv = True
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
         return _ConvFn.apply(node_feats, edge_attrs, tp_weights, edge_index, self)

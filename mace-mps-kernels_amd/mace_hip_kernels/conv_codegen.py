@@ -3,15 +3,25 @@ HIP source of the three interaction-convolution kernels of one layer (gfx950, wa
 with the layer's path coefficients as fp32 literals (reference conv.py:105-226 generates the Metal counterparts).
 
 Thread mapping: lane u of the workgroup is channel u (NCB = ceil(MUL/64) waves per row); a row is a receiver (forward),
-a sender (fused backward) or a chunk of 64 consecutive edges (per-edge backward).  Edge ids and their far endpoints
-are fetched 64 at a time, one per lane, and broadcast with v_readlane, so the per-edge loop issues no dependent index
-loads.  Per edge, Y[e] is wave-uniform (scalar loads); W[e], x[sender] and g[receiver] slices are 256-byte coalesced
-loads at a uniform row pointer plus a loop-invariant per-lane offset.
+a sender (fused backward) or a chunk of 64 consecutive edges (per-edge backward).  Edges are processed in chunks of
+up to 64: their ids and far endpoints are fetched one per lane and broadcast with v_readlane, so the edge loop issues
+no dependent index loads.
+
+Edge-uniform coupling products.  For instruction k the tensor product contracts the Clebsch-Gordan table with the
+edge's spherical harmonics before anything channel-dependent happens: M_k[a, c] = Σ_b C_k[a, b, c] · Y[e, o2_k + b].
+These numbers are the same for every channel, so the row kernels compute them once per chunk, cooperatively (lane j
+of the workgroup handles edge j, the pairs (k, a, c) split across the waves), into LDS; the edge loop then reads them
+as wave-uniform ds_read_b128 broadcasts.  Then
+    forward   acc[o3_k + c] += W[e, k] · Σ_a x[s, a] · M_k[a, c]
+    backward  h_a = Σ_c M_k[a, c] · g[r, o3_k + c];   gx_a += W·h_a;   gW_k = Σ_a x_a h_a;
+              gY[b] += W · Σ_{a,c} C_k[a,b,c] x_a g_c   (reduced over channels)
+instead of every wave re-deriving the uniform products per edge.
 
 Addressing: every global access is ``mh_ld(uniform_base, lane_byte_offset)`` — the base (row pointer + constant
-column) lives in SGPRs, the per-lane offset is one of a handful of loop-invariant VGPRs (u·4·d for each block
-dimension d), so no 64-bit VALU address arithmetic is emitted in the edge loop.  When MUL is a multiple of 64 every
-lane is a live channel and no lane-activity test is generated at all.
+column) is wave-uniform, the per-lane offset is one of a handful of loop-invariant registers (u·4·d for each block
+dimension d).  When MUL is a multiple of 64 every lane is a live channel and no lane-activity test is generated.
+Both row kernels issue the next edge's loads before the current edge's arithmetic and stores (vmcnt counts loads
+and stores in issue order, so waiting for the next edge's inputs never waits for earlier stores).
 """
 import numpy as np
 
@@ -29,26 +39,35 @@ def _sum(parts):
     return ' + '.join(parts) if parts else '0.0f'
 
 
-# fused backward: load each edge's inputs one iteration ahead of its use (see source())
-PIPELINE_BWD = True
-
-
-def _nxt(name):
-    """Next-stage register of a per-edge input: y3 -> yn3, w2 -> wn2, gv5 -> gvn5."""
-    return 'gvn' + name[2:] if name.startswith('gv') else name[0] + 'n' + name[1:]
+# fence the per-instruction LDS reads of the coupling products (bounds their register lifetime)
+FENCE_M = True
+# Load the W rows (read exactly once per launch) with the non-temporal cache policy.  Measured on config 2 with
+# W rotating over buffers larger than the Infinity Cache: never slower, 131 → 112 µs for the 1280-wide forward.
+W_NT = True
 
 
 class _Gen:
-    """Shared naming for the three kernels of one spec."""
+    """Shared naming and code fragments for the kernels of one spec."""
 
     def __init__(self, spec):
         self.s = spec
         self.full = spec.mul % WAVE == 0
         self.xi, self.nx = spec.xreg()
         self.oi, self.no = spec.oreg()
-        self.dims = sorted({2 * l + 1 for l, _, _ in spec.in1} | {co['d3'] for co in spec.coef})
+        self.dims = sorted({2 * l + 1 for l, _, _ in spec.in1} | {co['d3'] for co in spec.coef} | {1})
+        # coupling pairs (k, a, c) with their (b, coefficient) lists; pair p lives at Ms[edge][p]
+        self.pairs = []
+        self.pidx = {}
+        for co in spec.coef:
+            acc = {}
+            for a, b, c, v in co['terms']:
+                acc.setdefault((a, c), []).append((b, v))
+            for (a, c), bv in sorted(acc.items()):
+                self.pidx[(co['k'], a, c)] = len(self.pairs)
+                self.pairs.append((co, a, c, bv))
+        self.np = len(self.pairs)
+        self.npp = (self.np + 3) // 4 * 4
 
-    # per-lane, loop-invariant byte offsets: channel u of a block with components of dimension d starts at u*d*4
     def prelude(self):
         L = ['  const int u = threadIdx.x, lane = threadIdx.x & (MH_WAVE - 1), wave = threadIdx.x >> 6;']
         if self.full:
@@ -56,91 +75,117 @@ class _Gen:
         else:
             L += ['  const bool active = u < MUL;', '  const unsigned uc = active ? u : MUL - 1;',
                   '  const float am = active ? 1.0f : 0.0f;']
-        L += [f'  const unsigned ol{d} = uc * {4 * d}u;' for d in sorted(set(self.dims) | {1})]
+        L += [f'  const unsigned ol{d} = uc * {4 * d}u;' for d in self.dims]
+        L += ['  (void)wave; (void)lane;']
         return L
 
-    def ld_x(self, ind, src):
-        s = self.s
-        L = [f'{ind}const float* __restrict__ xs = x + (size_t){src} * X_DIM;']
-        for b, (l, _, off) in enumerate(s.in1):
+    # ---------------------------------------------------------------------------------------- loads
+    def ld_x(self, ind, src, dst='xv'):
+        L = [f'{ind}{{ const float* __restrict__ xs = x + (size_t)({src}) * X_DIM;']
+        for b, (l, _, off) in enumerate(self.s.in1):
             d = 2 * l + 1
-            L += [f'{ind}xv{self.xi[b] + m} = mh_ld(xs + {off + m}, ol{d});' for m in range(d)]
-        return L
+            L += [f'{ind}  {dst}{self.xi[b] + m} = mh_ld(xs + {off + m}, ol{d});' for m in range(d)]
+        return L + [f'{ind}}}']
 
-    def ld_y(self, ind):
+    def ld_w(self, ind, e, dst):
+        ld = 'mh_ld_nt' if W_NT else 'mh_ld'
+        return ([f'{ind}{{ const float* __restrict__ we = W + (size_t)({e}) * NW;'] +
+                [f'{ind}  {dst}{k} = {ld}(we + {k * self.s.mul}, ol1);' for k in range(self.s.nins)] + [f'{ind}}}'])
+
+    def ld_g(self, ind, r, dst):
+        mask = '' if self.full else ' * am'
+        L = [f'{ind}{{ const float* __restrict__ gr = g + (size_t)({r}) * OUT_DIM;']
+        for co in self.s.coef:
+            L += [f'{ind}  {dst}{self.oi[co["k"]] + c} = mh_ld(gr + {co["o3"] + c}, ol{co["d3"]}){mask};'
+                  for c in range(co['d3'])]
+        return L + [f'{ind}}}']
+
+    def ld_y_uniform(self, ind):
         return [f'{ind}const float* __restrict__ ye = Y + (size_t)e * Y_DIM;'] + \
                [f'{ind}const float y{j} = ye[{j}];' for j in range(self.s.y_dim)]
 
-    def ld_w(self, ind):
-        return [f'{ind}const float* __restrict__ we = W + (size_t)e * NW;'] + \
-               [f'{ind}const float w{k} = mh_ld(we + {k * self.s.mul}, ol1);' for k in range(self.s.nins)]
-
-    def ld_g(self, ind):
-        L = [f'{ind}const float* __restrict__ gr = g + (size_t)r * OUT_DIM;']
-        mask = '' if self.full else ' * am'
-        for co in self.s.coef:
-            d3 = co['d3']
-            L += [f'{ind}const float gv{self.oi[co["k"]] + c} = mh_ld(gr + {co["o3"] + c}, ol{d3}){mask};'
-                  for c in range(d3)]
-        return L
-
-    # --- software-pipelined backward: the edge's inputs are loaded one iteration ahead into the "n" stage
-    def stage_names(self):
-        s = self.s
-        return ([f'y{j}' for j in range(s.y_dim)] + [f'w{k}' for k in range(s.nins)] +
-                [f'gv{i}' for i in range(self.no)])
-
-    def ld_stage(self, ind, e, r):
-        """Issue the loads of edge (e, receiver r) into the next-stage registers yn*, wn*, gvn*."""
-        s = self.s
-        mask = '' if self.full else ' * am'
-        L = [f'{ind}{{ const float* __restrict__ ye = Y + (size_t)({e}) * Y_DIM;',
-             f'{ind}  const float* __restrict__ we = W + (size_t)({e}) * NW;',
-             f'{ind}  const float* __restrict__ gr = g + (size_t)({r}) * OUT_DIM;']
-        L += [f'{ind}  yn{j} = ye[{j}];' for j in range(s.y_dim)]
-        L += [f'{ind}  wn{k} = mh_ld(we + {k * s.mul}, ol1);' for k in range(s.nins)]
-        for co in s.coef:
-            L += [f'{ind}  gvn{self.oi[co["k"]] + c} = mh_ld(gr + {co["o3"] + c}, ol{co["d3"]}){mask};'
-                  for c in range(co['d3'])]
+    # ---------------------------------------------------------------- chunk prologue: M into LDS
+    def m_prologue(self, ind, edge_of_lane):
+        """Lane j computes edge j's coupling products; the pairs are split evenly over the NCB waves."""
+        s, ncb = self.s, self.s.ncb
+        per = (self.np + ncb - 1) // ncb
+        L = [f'{ind}if (lane < cnt) {{',
+             f'{ind}  const float* __restrict__ yl = Y + (size_t)({edge_of_lane}) * Y_DIM;']
+        L += [f'{ind}  const float q{j} = yl[{j}];' for j in range(s.y_dim)]
+        L += [f'{ind}  float* __restrict__ mrow = &Ms[lane][0];']
+        for w in range(ncb):
+            sel = self.pairs[w * per:(w + 1) * per]
+            if not sel:
+                continue
+            L.append(f'{ind}  if (wave == {w}) {{' if ncb > 1 else f'{ind}  {{')
+            for p, (co, a, c, bv) in enumerate(sel, start=w * per):
+                val = _sum([f'{_lit(v)} * q{co["o2"] + b}' for b, v in bv])
+                L.append(f'{ind}    mrow[{p}] = {val};')
+            L.append(f'{ind}  }}')
         L.append(f'{ind}}}')
+        L.append(f'{ind}__syncthreads();')
         return L
 
-    def fwd_body(self, ind):
-        """acc[o] += w_k · Σ_a x[a] · (Σ_b v·y[b]) for every output component of every instruction."""
+    def ld_m(self, ind, k):
+        """Instruction k's coupling products of the current edge from LDS (uniform address → broadcast), read right
+        before use; with FENCE_M an empty asm with a memory clobber keeps the next block's reads from being hoisted
+        (LDS loads are ordinary loads, so the clobber orders them)."""
+        qs = sorted({p // 4 for (kk, _, _), p in self.pidx.items() if kk == k})
+        L = [f'{ind}asm volatile("" ::: "memory");'] if FENCE_M else []
+        return L + [f'{ind}const float4 mq{q} = Ms4[j][{q}];' for q in qs]
+
+    def m(self, k, a, c):
+        p = self.pidx[(k, a, c)]
+        return f'mq{p // 4}.{"xyzw"[p % 4]}'
+
+    # ------------------------------------------------------------------------------- edge bodies
+    def fwd_body(self, ind, xv='xv', w='w'):
+        """acc[o] += w_k · Σ_a x_a · M_k[a, c]."""
         L = []
         for co in self.s.coef:
             k, i1 = co['k'], self.s.ins[co['k']][0]
+            L.append(f'{ind}{{')
+            L += self.ld_m(ind + '  ', k)
             for c in range(co['d3']):
-                by_a = {}
-                for a, b, cc, v in co['terms']:
-                    if cc == c:
-                        by_a.setdefault(a, []).append(f'{_lit(v)} * y{co["o2"] + b}')
-                if not by_a:
-                    continue
-                t = _sum([f'xv{self.xi[i1] + a} * ({_sum(ys)})' for a, ys in sorted(by_a.items())])
-                o = self.oi[k] + c
-                L.append(f'{ind}acc{o} = fmaf(w{k}, {t}, acc{o});')
+                ts = [f'{xv}{self.xi[i1] + a} * {self.m(k, a, c)}' for a in range(co['d1'])
+                      if (k, a, c) in self.pidx]
+                if ts:
+                    o = self.oi[k] + c
+                    L.append(f'{ind}  acc{o} = fmaf({w}{k}, {_sum(ts)}, acc{o});')
+            L.append(f'{ind}}}')
         return L
 
-    def bwd_body(self, ind, with_gx):
-        """h_a = Σ_{b,c} v·y[b]·g[c];  gx[a] += w·h_a;  gW_k = Σ_a x[a]·h_a;  P[b] += w·Σ_{a,c} v·x[a]·g[c]."""
+    def bwd_body(self, ind, with_gx, use_m, store):
+        """h_a = Σ_c M[a,c]·g_c (or Σ_{b,c} v·y_b·g_c);  gx_a += w·h_a;  gW_k = Σ_a x_a·h_a;
+        P_b += w·Σ_{a,c} v·x_a·g_c.  With ``store`` the gW row is written and P accumulated; full-wave specs write it
+        unconditionally (a store under a branch makes the wait-count pass assume it may be absent and wait for every
+        outstanding access at the next edge, stores included)."""
         s = self.s
         L = []
         for co in s.coef:
             k, i1 = co['k'], s.ins[co['k']][0]
             L.append(f'{ind}{{')
+            if use_m:
+                L += self.ld_m(ind + '  ', k)
             hs = []
             for a in range(co['d1']):
-                ts = [f'{_lit(v)} * y{co["o2"] + b} * gv{self.oi[k] + c}' for aa, b, c, v in co['terms'] if aa == a]
+                if use_m:
+                    ts = [f'{self.m(k, a, c)} * gv{self.oi[k] + c}' for c in range(co['d3']) if (k, a, c) in self.pidx]
+                else:
+                    ts = [f'{_lit(v)} * y{co["o2"] + b} * gv{self.oi[k] + c}'
+                          for aa, b, c, v in co['terms'] if aa == a]
                 if not ts:
                     continue
                 L.append(f'{ind}  const float h{a} = {_sum(ts)};')
                 hs.append(a)
                 if with_gx:
                     L.append(f'{ind}  gxa{self.xi[i1] + a} = fmaf(w{k}, h{a}, gxa{self.xi[i1] + a});')
+            if not store:
+                L.append(f'{ind}}}')
+                continue
             gw = _sum([f'xv{self.xi[i1] + a} * h{a}' for a in hs])
-            st = f'mh_st_nt(gwe + {k * s.mul}, ol1, {gw});'       # written once, never re-read here
-            L.append(f'{ind}  if (GWY) {st}' if self.full else f'{ind}  if (GWY && active) {st}')
+            st = f'mh_st_nt(gwe + {k * s.mul}, ol1, {gw});'      # written once, never re-read here
+            L.append(f'{ind}  {st}' if self.full else f'{ind}  if (active) {st}')
             for b in range(co['d2']):
                 ts = [f'{_lit(v)} * xv{self.xi[i1] + a} * gv{self.oi[k] + c}'
                       for a, bb, c, v in co['terms'] if bb == b]
@@ -189,7 +234,8 @@ def gy_reduce(indent, y_dim, y_pad):
 
 
 def _gy_combine(indent, edge_expr):
-    """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order)."""
+    """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order).  The leading
+    barrier also orders the chunk's Ms reads before the next chunk's prologue overwrites them."""
     return [
         f'{indent}__syncthreads();',
         f'{indent}for (int q = threadIdx.x; q < cnt * Y_DIM; q += BLOCK) {{',
@@ -205,35 +251,50 @@ def _gy_combine(indent, edge_expr):
 def source(spec):
     """HIP source of conv_fwd, conv_bwd (fused) and conv_bwd_wy (per edge) for one layer."""
     G = _Gen(spec)
-    nx, no = G.nx, G.no
+    nx, no, nk = G.nx, G.no, spec.nins
     gyr = gy_reduce('      ', spec.y_dim, spec.y_pad)
     pdecl = 'float ' + ', '.join(f'P{b} = 0.0f' for b in range(spec.y_pad)) + ';'
+
+    def decl(prefix, n, init=None):
+        return 'float ' + ', '.join(f'{prefix}{i}' + ('' if init is None else f' = {init}') for i in range(n)) + ';'
+
+    def copy(dst, src, n):
+        return [f'      const float {dst}{i} = {src}{i};' for i in range(n)]
+
     L = [_native.device_header(),
          f'#define MUL {spec.mul}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}',
          f'#define X_DIM {spec.x_dim}', f'#define Y_DIM {spec.y_dim}', f'#define Y_PAD {spec.y_pad}',
-         f'#define OUT_DIM {spec.out_dim}', f'#define NW {spec.nins * spec.mul}']
-    xdecl = 'float ' + ', '.join(f'xv{i}' for i in range(nx)) + ';'
+         f'#define OUT_DIM {spec.out_dim}', f'#define NW {spec.nins * spec.mul}', f'#define NPP {G.npp}']
+    ms_decl = ['  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
+               '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);']
     # ------------------------------------------------------------------------------------------- forward
     L += [
         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwd")}(',
         '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
         '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
         '    float* __restrict__ out, int N) {',
+    ] + ms_decl + [
         '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  if (n >= N) return;',
     ] + G.prelude() + [
-        '  float ' + ', '.join(f'acc{i} = 0.0f' for i in range(no)) + ';',
-        f'  {xdecl}',
+        '  ' + decl('acc', no, '0.0f'),
+        '  ' + decl('xn', nx), '  ' + decl('wn', nk),
         '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
         '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
         '    const int cnt = min(MH_WAVE, p1 - pb);',
         '    int my_e = 0, my_s = 0;',
         '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }',
-        '    for (int j = 0; j < cnt; ++j) {',
-        '      const int e = mh_bcast(my_e, j), s = mh_bcast(my_s, j);',
     ]
-    L += G.ld_y('      ') + G.ld_x('      ', 's') + G.ld_w('      ') + G.fwd_body('      ')
-    L += ['    }', '  }', '  if (active) {', '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
+    L += G.m_prologue('    ', 'my_e')
+    L += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
+    L += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
+    L += ['    }', '    for (int j = 0; j < cnt; ++j) {']
+    L += copy('xv', 'xn', nx) + copy('w', 'wn', nk)
+    L += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
+    L += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+    L += ['      }']
+    L += G.fwd_body('      ')
+    L += ['    }', '    __syncthreads();', '  }', '  if (active) {', '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
     for co in spec.coef:
         L += [f'    mh_st(o + {co["o3"] + c}, ol{co["d3"]}, acc{G.oi[co["k"]] + c});' for c in range(co['d3'])]
     L += ['  }', '}', '']
@@ -245,44 +306,51 @@ def source(spec):
         '    const int* __restrict__ receivers, float* __restrict__ gx, float* __restrict__ gW,',
         '    float* __restrict__ gY, int N, int flags) {',
         '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
+    ] + ms_decl + [
         '  const int s = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  if (s >= N) return;',
     ] + G.prelude() + [
         '  const bool GX = (flags & 1) != 0, GWY = (flags & 2) != 0;',
-        '  float ' + ', '.join(f'xv{i} = 0.0f' for i in range(nx)) + ';',
+        '  ' + decl('xv', nx, '0.0f'),
         '  if (GWY) {',
     ]
     L += G.ld_x('    ', 's')
     L += [
         '  }',
-        '  float ' + ', '.join(f'gxa{i} = 0.0f' for i in range(nx)) + ';',
+        '  ' + decl('gxa', nx, '0.0f'),
+        '  ' + decl('wn', nk), '  ' + decl('gvn', no),
         '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
-        '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
-        '    const int cnt = min(MH_WAVE, p1 - pb);',
-        '    int my_e = 0, my_r = 0;',
-        '    if (lane < cnt) { my_e = eids[pb + lane]; my_r = receivers[my_e]; }',
     ]
-    if PIPELINE_BWD:
-        # Edge j+1's loads are issued before edge j's gW stores.  vmcnt counts loads and stores in issue order, so
-        # waiting for the next edge's inputs then never waits for the previous edge's stores.
-        names = G.stage_names()
-        L += ['    float ' + ', '.join(_nxt(n) for n in names) + ';',
-              '    int en = mh_bcast(my_e, 0), rn = mh_bcast(my_r, 0);']
-        L += G.ld_stage('    ', 'en', 'rn')
-        L += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = en, r = rn;']
-        L += [f'      const float {n} = {_nxt(n)};' for n in names]
-        L += ['      if (j + 1 < cnt) {', '        en = mh_bcast(my_e, j + 1); rn = mh_bcast(my_r, j + 1);']
-        L += G.ld_stage('        ', 'en', 'rn')
-        L += ['      }']
-    else:
-        L += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j), r = mh_bcast(my_r, j);']
-        L += G.ld_y('      ') + G.ld_w('      ') + G.ld_g('      ')
-    L += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
-    L += G.bwd_body('      ', with_gx=True)
-    L += ['      if (GWY) {'] + ['  ' + t for t in gyr] + ['      }']
-    L += ['    }', '    if (GWY) {']
-    L += _gy_combine('      ', 'eids[pb + j]')
-    L += ['    }', '  }', '  if (GX && active) {', '    float* __restrict__ gxs = gx + (size_t)s * X_DIM;']
+
+    def bwd_chunks(store):
+        # The flag test sits outside the edge loop, and the next edge's loads are unconditional (the last edge of a
+        # chunk re-loads itself), so the loop has no branch around a global access: the wait for the prefetched
+        # inputs then counts only the stores issued after them instead of draining the memory queue every edge.
+        C = ['  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
+             '    const int cnt = min(MH_WAVE, p1 - pb);',
+             '    int my_e = 0, my_r = 0;',
+             '    if (lane < cnt) { my_e = eids[pb + lane]; my_r = receivers[my_e]; }']
+        C += G.m_prologue('    ', 'my_e')
+        C += ['    {', '      const int e0 = mh_bcast(my_e, 0), r0 = mh_bcast(my_r, 0);']
+        C += G.ld_w('      ', 'e0', 'wn') + G.ld_g('      ', 'r0', 'gvn')
+        C += ['    }', '    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
+        C += copy('w', 'wn', nk) + copy('gv', 'gvn', no)
+        C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
+              '        const int e1 = mh_bcast(my_e, j1), r1 = mh_bcast(my_r, j1);']
+        C += G.ld_w('        ', 'e1', 'wn') + G.ld_g('        ', 'r1', 'gvn')
+        C += ['      }']
+        if store:
+            C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
+        C += G.bwd_body('      ', with_gx=True, use_m=True, store=store)
+        if store:
+            C += gyr
+        C += ['    }']
+        C += _gy_combine('    ', 'eids[pb + j]') if store else ['    __syncthreads();']
+        return C + ['  }']
+
+    L += ['  if (GWY) {'] + ['  ' + t for t in bwd_chunks(True)] + ['  } else {']
+    L += ['  ' + t for t in bwd_chunks(False)] + ['  }']
+    L += ['  if (GX && active) {', '    float* __restrict__ gxs = gx + (size_t)s * X_DIM;']
     for b, (l, _, off) in enumerate(spec.in1):
         d = 2 * l + 1
         L += [f'    mh_st(gxs + {off + m}, ol{d}, gxa{G.xi[b] + m});' for m in range(d)]
@@ -297,19 +365,118 @@ def source(spec):
         '  const int pb = mh_xcd_block(blockIdx.x, gridDim.x) * MH_WAVE;',
         '  if (pb >= E) return;',
     ] + G.prelude() + [
-        '  const bool GWY = true;',
         '  const int cnt = min(MH_WAVE, E - pb);',
-        f'  {xdecl}',
+        '  ' + decl('xv', nx), '  ' + decl('w', nk), '  ' + decl('gv', no),
         '  int my_s = 0, my_r = 0;',
         '  if (lane < cnt) { my_s = senders[pb + lane]; my_r = receivers[pb + lane]; }',
         '  for (int j = 0; j < cnt; ++j) {',
         '    const int e = pb + j, s = mh_bcast(my_s, j), r = mh_bcast(my_r, j);',
     ]
-    L += G.ld_y('    ') + G.ld_x('    ', 's') + G.ld_w('    ') + G.ld_g('    ')
+    L += G.ld_y_uniform('    ') + G.ld_x('    ', 's') + G.ld_w('    ', 'e', 'w') + G.ld_g('    ', 'r', 'gv')
     L += [f'    {pdecl}', '    float* __restrict__ gwe = gW + (size_t)e * NW;']
-    L += G.bwd_body('    ', with_gx=False)
+    L += G.bwd_body('    ', with_gx=False, use_m=False, store=True)
     L += [t[2:] for t in gyr]
     L += ['  }']
     L += _gy_combine('  ', 'pb + j')
     L += ['}', '']
+    L += _bwd_recv(G, gyr, pdecl, decl, copy)
+    L += _gx_sum(spec)
     return '\n'.join(L)
+
+
+def _bwd_recv(G, gyr, pdecl, decl, copy):
+    """Receiver-ordered backward (rows = receivers, the forward's CSR).  g[r] is loaded once per row and stays in
+    registers; each edge gathers only x[s] (X_DIM floats) and its W row, writes its gW row and gY, and, when dX is
+    wanted, its dX message gxm[e] = Σ_k W_k·h_k (X_DIM floats), which ``conv_gxsum`` adds up per sender.  Per edge
+    this reads X_DIM + NW floats per channel block instead of the OUT_DIM-float g row the sender-ordered kernel
+    gathers."""
+    spec, nx, nk = G.s, G.nx, G.s.nins
+    L = [
+        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwdr")}(',
+        '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
+        '    const float* __restrict__ W, const int* __restrict__ rowptr, const int* __restrict__ eids,',
+        '    const int* __restrict__ senders, float* __restrict__ gW, float* __restrict__ gY,',
+        '    float* __restrict__ gxm, int N, int flags) {',
+        '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
+        '  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
+        '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);',
+        '  const int r = mh_xcd_block(blockIdx.x, gridDim.x);',
+        '  if (r >= N) return;',
+    ] + G.prelude() + [
+        '  const bool GX = (flags & 1) != 0;',
+        '  ' + decl('gv', G.no),
+    ]
+    L += G.ld_g('  ', 'r', 'gv')
+    L += ['  ' + decl('xn', nx), '  ' + decl('wn', nk),
+          '  const int p0 = rowptr[r], p1 = rowptr[r + 1];']
+
+    def chunks(msg):
+        C = ['  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
+             '    const int cnt = min(MH_WAVE, p1 - pb);',
+             '    int my_e = 0, my_s = 0;',
+             '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
+        C += G.m_prologue('    ', 'my_e')
+        C += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
+        C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
+        C += ['    }', '    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
+        C += copy('xv', 'xn', nx) + copy('w', 'wn', nk)
+        C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
+              '        const int e1 = mh_bcast(my_e, j1), s1 = mh_bcast(my_s, j1);']
+        C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+        C += ['      }']
+        C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
+        if msg:
+            C += ['      ' + decl('gxa', nx, '0.0f')]
+        C += G.bwd_body('      ', with_gx=msg, use_m=True, store=True)
+        if msg:
+            C += ['      {', '        float* __restrict__ gme = gxm + (size_t)e * X_DIM;']
+            for b, (l, _, off) in enumerate(spec.in1):
+                d = 2 * l + 1
+                st = [f'mh_st(gme + {off + m}, ol{d}, gxa{G.xi[b] + m});' for m in range(d)]
+                C += [f'        {t}' if G.full else f'        if (active) {t}' for t in st]
+            C += ['      }']
+        C += gyr
+        C += ['    }']
+        C += _gy_combine('    ', 'eids[pb + j]')
+        return C + ['  }']
+
+    L += ['  if (GX) {'] + ['  ' + t for t in chunks(True)] + ['  } else {']
+    L += ['  ' + t for t in chunks(False)] + ['  }', '}', '']
+    return L
+
+
+def gxsum_block(spec):
+    """Threads of the dX-message reduction: one float4 column each, rounded up to whole waves."""
+    return (spec.x_dim // 4 + WAVE - 1) // WAVE * WAVE
+
+
+def _gx_sum(spec):
+    """gx[s] = Σ_{e ∈ CSR_send(s)} gxm[e], summed in CSR order (deterministic); one float4 column per thread."""
+    assert spec.x_dim % 4 == 0
+    return [
+        f'extern "C" __global__ __launch_bounds__({gxsum_block(spec)}) void {spec.kname("conv_gxsum")}(',
+        '    const float* __restrict__ gxm, const int* __restrict__ rowptr, const int* __restrict__ eids,',
+        '    float* __restrict__ gx, int N) {',
+        '  const int s = mh_xcd_block(blockIdx.x, gridDim.x);',
+        '  const int t = threadIdx.x;',
+        '  if (s >= N || t >= X_DIM / 4) return;',
+        '  const float4* __restrict__ src = reinterpret_cast<const float4*>(gxm) + t;',
+        '  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);',
+        '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
+        '  int p = p0;',
+        '  for (; p + 4 <= p1; p += 4) {',
+        '    const int e0 = eids[p], e1 = eids[p + 1], e2 = eids[p + 2], e3 = eids[p + 3];',
+        '    const float4 v0 = src[(size_t)e0 * (X_DIM / 4)], v1 = src[(size_t)e1 * (X_DIM / 4)];',
+        '    const float4 v2 = src[(size_t)e2 * (X_DIM / 4)], v3 = src[(size_t)e3 * (X_DIM / 4)];',
+        '    acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;',
+        '    acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;',
+        '    acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;',
+        '    acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;',
+        '  }',
+        '  for (; p < p1; ++p) {',
+        '    const float4 v = src[(size_t)eids[p] * (X_DIM / 4)];',
+        '    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;',
+        '  }',
+        '  reinterpret_cast<float4*>(gx)[(size_t)s * (X_DIM / 4) + t] = acc;',
+        '}', '',
+    ]

@@ -240,8 +240,10 @@ def element_index(node_attrs):
     ver = node_attrs._version
     for i, (ref, v, el) in enumerate(_elem_cache):
         if ref() is node_attrs and v == ver:
-            return el
+            return _native.hold_for_capture(el)
     el = torch.argmax(node_attrs, dim=1).to(torch.int32).contiguous()
+    if _native.capturing():
+        return el              # recomputed by every replay; its memory only holds values once the graph runs
     _elem_cache.insert(0, (weakref.ref(node_attrs), ver, el))
     del _elem_cache[4:]
     return el

@@ -35,10 +35,11 @@ class _Layer(torch.nn.Module):
         self.h_in, self.var_in, self.var_out = h_in, var_in, var_out
 
     def forward(self, x):
-        x = x @ (self.weight / math.sqrt(self.h_in * self.var_in))
+        # as e3nn: hidden layers rescale after the activation; the last layer folds var_out into the weight scale
         if self.act is not None:
-            x = self.act(x)
-        return x * math.sqrt(self.var_out)
+            x = self.act(x @ (self.weight / math.sqrt(self.h_in * self.var_in)))
+            return x * math.sqrt(self.var_out)
+        return x @ (self.weight / math.sqrt(self.h_in * self.var_in / self.var_out))
 
 
 class FullyConnectedNet(torch.nn.Sequential):

@@ -419,29 +419,35 @@ class TensorProduct(torch.nn.Module):
         s1, s2 = self.irreps_in1.slices(), self.irreps_in2.slices()
         blocks = [None] * len(self.irreps_out)
         woff = 0
+        xx = {}              # outer products shared by the instructions of one input pair (e3nn's xx_dict)
         for k, i in enumerate(self.instructions):
             mi1, mi2, mo = self.irreps_in1[i.i_in1], self.irreps_in2[i.i_in2], self.irreps_out[i.i_out]
             a = x1[:, s1[i.i_in1]].reshape(z, mi1.mul, mi1.ir.dim)
             b = x2[:, s2[i.i_in2]].reshape(z, mi2.mul, mi2.ir.dim)
-            c = self._coupling(k, x1)
             n = math.prod(i.path_shape) if i.has_weight else 0
             w = weight[:, woff:woff + n].reshape(weight.shape[0], *i.path_shape) if i.has_weight else None
             woff += n
-            if i.connection_mode == 'uvu':
-                ab = torch.einsum('zui,zvj->zuvij', a, b)
-                if w is not None:
-                    out = torch.einsum('zuvij,ijk,zuv->zuk', ab, c, w.expand(z, *i.path_shape))
-                else:
-                    out = torch.einsum('zuvij,ijk->zuk', ab, c)
-            elif i.connection_mode == 'uvw':
-                ab = torch.einsum('zui,zvj->zuvij', a, b)
-                t = torch.einsum('zuvij,ijk->zuvk', ab, c)
-                if w.shape[0] == 1:
-                    out = torch.einsum('zuvk,uvw->zwk', t, w[0])
-                else:
-                    out = torch.einsum('zuvk,zuvw->zwk', t, w)
-            else:
+            if i.connection_mode not in ('uvu', 'uvw'):
                 raise NotImplementedError(i.connection_mode)
+            l1, l2 = mi1.ir.l, mi2.ir.l
+            if w is not None and (l1 == 0 or l2 == 0):
+                # e3nn's specialised code: a scalar operand makes the coupling δ/sqrt(2l+1) (1 for 0x0->0), so the
+                # Clebsch-Gordan contraction is skipped
+                t = (torch.einsum('zu,zvj->zuvj', a[..., 0], b) if l1 == 0 else
+                     torch.einsum('zui,zv->zuvi', a, b[..., 0]))
+                if l1 or l2:
+                    t = t / math.sqrt(mo.ir.dim)
+            else:
+                key = (i.i_in1, i.i_in2)
+                if key not in xx:
+                    xx[key] = torch.einsum('zui,zvj->zuvij', a, b)
+                t = torch.einsum('zuvij,ijk->zuvk', xx[key], self._coupling(k, x1))
+            if i.connection_mode == 'uvu':
+                out = t.sum(2) if w is None else torch.einsum('zuvk,zuv->zuk', t, w.expand(z, *i.path_shape))
+            elif w.shape[0] == 1:
+                out = torch.einsum('zuvk,uvw->zwk', t, w[0])
+            else:
+                out = torch.einsum('zuvk,zuvw->zwk', t, w)
             out = self._coeffs[k] * out.reshape(z, mo.dim)
             blocks[i.i_out] = out if blocks[i.i_out] is None else blocks[i.i_out] + out
         res = [blk if blk is not None else x1.new_zeros(z, mo.dim) for blk, mo in zip(blocks, self.irreps_out)]

@@ -112,3 +112,34 @@ def test_golden_fixtures_reproduce():
     assert np.abs(oconv.conv_bwd_x(desc, coef, g['g'], g['Y'], g['W'], s, r, n) - g['gx']).max() < 1e-12
     assert np.abs(oconv.conv_bwd_w(desc, coef, g['x'], g['g'], g['Y'], s, r) - g['gW']).max() < 1e-12
     assert np.abs(oconv.conv_bwd_y(desc, coef, g['x'], g['g'], g['W'], s, r) - g['gY']).max() < 1e-12
+
+
+def test_grad_needed_follows_the_engine():
+    """The backward asks the autograd engine which input gradients the current pass uses (host logic, CPU)."""
+    seen = []
+
+    class Probe(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, a, b):
+            return a * b
+
+        @staticmethod
+        def backward(ctx, g):
+            seen.append((conv._grad_needed(ctx, 0), conv._grad_needed(ctx, 1)))
+            return g, g
+
+    x, p = torch.randn(3, requires_grad=True), torch.randn(3, requires_grad=True)
+    cases = [
+        (lambda: torch.autograd.grad(Probe.apply(x * 2, p * 3).sum(), [p]), (False, True)),   # branch unused
+        (lambda: torch.autograd.grad(Probe.apply(x, p * 3).sum(), [x]), (True, False)),       # leaf is an input
+        (lambda: Probe.apply(x * 2, p * 3).sum().backward(), (True, True)),
+        (lambda: Probe.apply(torch.randn(3), p * 3).sum().backward(), (False, True)),           # no grad at all
+    ]
+    for run, want in cases:
+        seen.clear()
+        run()
+        assert seen == [want]
+    a = x * 2                                                                                    # non-leaf input
+    seen.clear()
+    torch.autograd.grad(Probe.apply(a, p * 3).sum(), [a])
+    assert seen == [(True, False)]

@@ -55,12 +55,16 @@ CONV_CASES = [('32x0e+32x1o', 2), ('128x0e', 3), ('128x0e+128x1o', 3), ('128x0e+
               ('64x0e', 2), ('96x0e+96x1o', 3)]
 
 
+@pytest.mark.parametrize('order', ['recv', 'send'])
 @pytest.mark.parametrize('hidden,lmax', CONV_CASES)
-def test_conv_fwd_bwd_vs_oracle(hidden, lmax):
+def test_conv_fwd_bwd_vs_oracle(hidden, lmax, order):
+    """Forward and all three gradients against the oracle, with the backward in receiver order (g rows read once
+    per receiver, dX through per-edge messages) and in sender order (fused kernel)."""
     dev = _dev()
-    print(f'[case] conv {hidden} l{lmax}', flush=True)
+    print(f'[case] conv {hidden} l{lmax} bwd={order}', flush=True)
     tp = _tp(hidden, lmax)
     op = HipConvTP(tp, device=dev)
+    op.bwd_recv = order == 'recv'
     desc = oconv.describe_tp(tp)
     coef = oconv.path_terms(desc)
     rng = np.random.default_rng(1)
@@ -80,6 +84,29 @@ def test_conv_fwd_bwd_vs_oracle(hidden, lmax):
     assert _rel(Wt.grad.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
     assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
     assert float(out[n - 1].abs().max()) == 0.0 and float(xt.grad[n - 1].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize('order', ['recv', 'send'])
+def test_conv_bwd_without_dx(order):
+    """x not requiring grad (the first interaction layer under forces): gW and gY only, no dX messages."""
+    dev = _dev()
+    print(f'[case] conv bwd gW/gY only bwd={order}', flush=True)
+    tp = _tp('128x0e+128x1o', 3)
+    op = HipConvTP(tp, device=dev)
+    op.bwd_recv = order == 'recv'
+    desc = oconv.describe_tp(tp)
+    coef = oconv.path_terms(desc)
+    rng = np.random.default_rng(5)
+    n, e = 29, 400
+    s, r = _graph(rng, n, e)
+    x, Y, W = (rng.normal(size=sh) for sh in ((n, desc['x_dim']), (e, desc['y_dim']), (e, 10 * 128)))
+    g = rng.normal(size=(n, desc['out_dim']))
+    xt = torch.tensor(x, dtype=torch.float32, device=dev)
+    Yt, Wt = (torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True) for a in (Y, W))
+    out = op(xt, Yt, Wt, torch.tensor(np.stack([s, r]), device=dev))
+    out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+    assert _rel(Wt.grad.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
+    assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
 
 
 def test_conv_c_abi_bwd_x_and_bwd_wy():
@@ -113,6 +140,20 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
     assert _rel(gx.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, W, s, r, n)) < CONV_TOL
     assert _rel(gW.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
     assert _rel(gY.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
+    # receiver-ordered backward through its own entry point (dX via per-edge messages)
+    rowptr_r, eids_r = hconv.csr_by(torch.tensor(r, device=dev), n)
+    gW3, gY3, gx3 = torch.zeros_like(Wt), torch.zeros_like(Yt), torch.zeros_like(xt)
+    work = torch.empty(e, desc['x_dim'], device=dev)
+    _native.check(lib.mh_conv_bwd_recv(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_r), P(eids_r), P(st),
+                                       P(rowptr_s), P(eids_s), P(work), P(gx3), P(gW3), P(gY3), n, 3, st_),
+                  'bwd_recv')
+    assert lib.mh_conv_bwd_recv(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_r), P(eids_r), P(st),
+                                None, None, None, P(gx3), P(gW3), P(gY3), n, 3, st_) != 0   # GX without scratch
+    assert b'NULL' in lib.mh_last_error()
+    torch.cuda.synchronize()
+    assert _rel(gx3.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, W, s, r, n)) < CONV_TOL
+    assert _rel(gW3.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
+    assert _rel(gY3.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
     assert torch.equal(gx, gx2)                  # same kernel (fused backward), different flags: bitwise
     # different kernels (per-edge vs fused): same formulas, possibly different fp32 contraction order
     assert _rel(gW2.double().cpu().numpy(), gW.double().cpu().numpy()) < 1e-6
