@@ -66,7 +66,8 @@ def _kernel_table(met, batch, n_real_edges, summary):
             bf, bb = s.bytes(n, n_real_edges)
             ff, fb = s.flops()
             rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul, s.kname('conv_fwd'))
-            rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul, s.kname('conv_bwd'))
+            bwd_sym = (f"{s.kname('conv_bwdr')}+{s.kname('conv_gxsum')}" if m.bwd_recv else s.kname('conv_bwd'))
+            rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul, bwd_sym)
         elif isinstance(m, HipSymmetricContraction):
             s = m.spec
             bf, bb = s.bytes(n, n_elem_used)
@@ -116,6 +117,99 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
 COPY_BYTES = 1 << 30          # size of the calibration copy (read 1 GiB, write 1 GiB) of --profile
 
 
+def _isolated(a):
+    """Each HIP kernel alone on a configuration's graph (BASELINE config 4 by default: 20,000-atom bulk Pt): conv
+    forward, conv backward in receiver order with and without dX, the sender-ordered fused backward, and the symmetric
+    contraction forward/backward, on seeded random inputs.  Edge-sized tensors rotate over enough buffers that no
+    launch finds its inputs in the 256 MB Infinity Cache.  Time = HIP events on the launch stream over K launches
+    after W warm-ups.  Prints one JSON line per kernel."""
+    import torch
+    from mace_hip_kernels import HipConvTP, HipSymmetricContraction, _native
+    from mace_hip_kernels import conv as hconv
+    from mace_lite import factory
+    dev = torch.device('cuda:0')
+    model, batch, meta = factory.workload(a.config)
+    N, E = int(batch['positions'].shape[0]), int(batch['edge_index'].shape[1])
+    n_real = int(batch.get('n_real_edges', E))
+    _log(f'isolated kernels, config {a.config} {meta["name"]}: {N} atoms, {E} edges ({n_real} real)')
+    gr = hconv.graph_for(batch['edge_index'].to(dev), N)
+    rp_r, ei_r = gr.by_recv()
+    rp_s, ei_s = gr.by_send()
+    P, lib = _native.ptr, _native.load()
+    gen = torch.Generator(device='cpu').manual_seed(5)
+
+    def rnd(*shape):
+        return torch.randn(*shape, generator=gen).to(dev)
+
+    def timed(fn, nb):
+        for i in range(a.warmup):
+            _native.check(fn(i % nb))
+        st = torch.cuda.current_stream()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(st)
+        for i in range(a.steps):
+            _native.check(fn(i % nb))
+        t1.record(st)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / a.steps
+
+    def report(name, sym, ms, nbytes, flops):
+        rec = dict(kernel=name, symbol=sym, config=meta['name'], ms=round(ms, 5), bytes=int(nbytes),
+                   flops=int(flops), gbs=round(nbytes / (ms * 1e-3) / 1e9, 1),
+                   hbm_frac=round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   tflops=round(flops / (ms * 1e-3) / 1e12, 2),
+                   valu_frac=round(flops / (ms * 1e-3) / 1e12 / FP32_NONPACKED_TFLOPS, 4))
+        print(json.dumps(rec), flush=True)
+
+    stream = _native.stream_of(torch.empty(0, device=dev))
+    for li, blk in enumerate(model.interactions):
+        op = HipConvTP(blk.conv_tp, device=dev)
+        s, h = op.spec, op.module.handle
+        nw = s.nins * s.mul
+        nb = max(1, min(4, -(-600_000_000 // (E * nw * 4))))       # rotate until > 600 MB of W is in flight
+        x, g = rnd(N, s.x_dim), rnd(N, s.out_dim)
+        Ys = [rnd(E, s.y_dim) for _ in range(nb)]
+        Ws = [rnd(E, nw) for _ in range(nb)]
+        gWs = [torch.empty(E, nw, device=dev) for _ in range(nb)]
+        gY, gx, out = torch.empty(E, s.y_dim, device=dev), torch.empty_like(x), torch.empty(N, s.out_dim, device=dev)
+        work = torch.empty(E, s.x_dim, device=dev)
+        bf, bb = s.bytes(N, n_real)
+        ff, fb = s.flops()
+        tag = f'interactions.{li}.conv_tp'
+        ms = timed(lambda i: lib.mh_conv_fwd(h, P(x), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send), P(out), N,
+                                             stream), nb)
+        report(f'conv_fwd[{tag}]', s.kname('conv_fwd'), ms, bf, ff * n_real * s.mul)
+        ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
+                                                  P(rp_s), P(ei_s), P(work), P(gx), P(gWs[i]), P(gY), N, 3, stream), nb)
+        report(f'conv_bwd[{tag}] dx+dW+dY', f"{s.kname('conv_bwdr')}+{s.kname('conv_gxsum')}", ms, bb,
+               fb * n_real * s.mul)
+        ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
+                                                  None, None, None, None, P(gWs[i]), P(gY), N, 2, stream), nb)
+        report(f'conv_bwd[{tag}] dW+dY', s.kname('conv_bwdr'), ms, bb - 4 * (N * s.x_dim + n_real * 2 + N + 1),
+               fb * n_real * s.mul)
+        ms = timed(lambda i: lib.mh_conv_bwd(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_s), P(ei_s), P(gr.recv),
+                                             P(gx), P(gWs[i]), P(gY), N, 3, stream), nb)
+        report(f'conv_bwd[{tag}] sender-ordered', s.kname('conv_bwd'), ms, bb, fb * n_real * s.mul)
+        del op, x, g, Ys, Ws, gWs, gY, gx, out, work
+        torch.cuda.empty_cache()
+    elem = batch['node_attrs'].argmax(1).to(torch.int32).to(dev)
+    n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
+    for li, prod in enumerate(model.products):
+        op = HipSymmetricContraction(prod.symmetric_contractions, device=dev)
+        s, h = op.spec, op.module.handle
+        X = rnd(N, s.C, s.n_ell) * 0.5
+        G, out, GX = rnd(N, s.out_dim), torch.empty(N, s.out_dim, device=dev), torch.empty(N, s.C, s.n_ell, device=dev)
+        bf, bb = s.bytes(N, n_elem_used)
+        ff, fb = s.flops()
+        tag = f'products.{li}.symmetric_contractions'
+        ms = timed(lambda i: lib.mh_sc_fwd(h, P(X), P(elem), P(op.T), P(out), N, stream), 1)
+        report(f'sc_fwd[{tag}]', s.kname('sc_fwd'), ms, bf, ff * N * s.C)
+        ms = timed(lambda i: lib.mh_sc_bwd(h, P(X), P(elem), P(op.T), P(G), P(GX), N, stream), 1)
+        report(f'sc_bwd[{tag}]', s.kname('sc_bwd'), ms, bb, fb * N * s.C)
+        del op
+
+
 def _profile(a):
     """Patched E+F calls only (for rocprofv3), then a plain elementwise copy of known size whose FETCH_SIZE and
     WRITE_SIZE calibrate the counters."""
@@ -151,6 +245,7 @@ def _summarize(a):
                 out += list(csv.DictReader(fh))
         return out
 
+    per = {}
     stats = rows(a.summarize_rocprof, '*kernel_stats.csv')
     print('| kernel | calls | mean us | min us | max us | share of GPU time |')
     print('|---|---:|---:|---:|---:|---:|')
@@ -174,6 +269,47 @@ def _summarize(a):
             if a.filter and not any(f in k for f in a.filter.split(',')):
                 continue
             print(f'| {k[:80]} | {n} | {s / n:.1f} |')
+        per[label] = {k: s / n for k, (n, s) in acc.items()}
+    for d in a.pmc or []:
+        # any counters: per kernel, summed over hardware instances within a dispatch, mean over dispatches
+        disp = {}
+        for r in rows(d, '*counter_collection.csv'):
+            key = (r['Kernel_Name'], r['Dispatch_Id'])
+            disp.setdefault(key, {})
+            disp[key][r['Counter_Name']] = disp[key].get(r['Counter_Name'], 0.0) + float(r['Counter_Value'])
+        kern, names = {}, []
+        for (k, _), cs in disp.items():
+            if a.filter and not any(f in k for f in a.filter.split(',')):
+                continue
+            for c, v in cs.items():
+                kern.setdefault(k, {}).setdefault(c, []).append(v)
+                if c not in names:
+                    names.append(c)
+        print(f'\ncounters of {d} (per dispatch: sum over instances, mean over dispatches)\n')
+        print('| kernel | ' + ' | '.join(names) + ' |')
+        print('|---|' + '---:|' * len(names))
+        for k in sorted(kern):
+            vals = [sum(kern[k][c]) / len(kern[k][c]) if c in kern[k] else float('nan') for c in names]
+            print(f'| {k[:60]} | ' + ' | '.join(f'{v:.4g}' for v in vals) + ' |')
+    if a.traffic_json and len(per) == 2:
+        # calibration: the COPY_BYTES bitwise_not copy of --profile reads and writes exactly COPY_BYTES
+        cal = [k for k in per['FETCH_SIZE'] if 'bitwise_not' in k]
+        if not cal:
+            raise SystemExit('no bitwise_not calibration kernel in the counter runs')
+        ff = COPY_BYTES / 1024 / per['FETCH_SIZE'][cal[0]]
+        wf = COPY_BYTES / 1024 / per['WRITE_SIZE'][cal[0]]
+        kern = {}
+        for k in per['FETCH_SIZE']:
+            if any(f in k for f in ('conv_', 'sc_')) and k in per['WRITE_SIZE']:
+                fk, wk = per['FETCH_SIZE'][k], per['WRITE_SIZE'][k]
+                kern[k] = dict(fetch_kib=round(fk, 1), write_kib=round(wk, 1), traffic_bytes=(fk * ff + wk * wf) * 1024)
+        with open(a.traffic_json, 'w') as fh:
+            json.dump(dict(source=a.traffic_source, fetch_factor=ff, write_factor=wf, kernels=kern), fh, indent=1)
+        print(f'\ncalibration: FETCH_SIZE x {ff:.3f}, WRITE_SIZE x {wf:.3f}; wrote {a.traffic_json}\n')
+        print('| kernel | FETCH_SIZE KiB | WRITE_SIZE KiB | traffic (calibrated) MB |')
+        print('|---|---:|---:|---:|')
+        for k, r in sorted(kern.items(), key=lambda t: -t[1]['traffic_bytes']):
+            print(f"| {k} | {r['fetch_kib']} | {r['write_kib']} | {r['traffic_bytes'] / 1e6:.1f} |")
 
 
 def main():
@@ -183,17 +319,26 @@ def main():
     ap.add_argument('--summarize-rocprof', metavar='DIR', help='print a markdown summary of rocprofv3 output and exit')
     ap.add_argument('--pmc-fetch', metavar='DIR')
     ap.add_argument('--pmc-write', metavar='DIR')
+    ap.add_argument('--pmc', metavar='DIR', action='append', help='counter run to tabulate per kernel (repeatable)')
+    ap.add_argument('--traffic-json', metavar='PATH', help='with both counter runs: write calibrated traffic per kernel')
+    ap.add_argument('--traffic-source', default='profiles/conv_sc_traffic_cfg2.md')
     ap.add_argument('--filter', default='conv_,sc_,bitwise_not', help='kernel-name substrings kept in counter tables')
     ap.add_argument('--top', type=int, default=30)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
-    ap.add_argument('--config', type=int, default=2, choices=[0, 1, 2, 3])
+    ap.add_argument('--config', type=int, default=None, choices=[0, 1, 2, 3, 4],
+                    help='workload (default 2; 4 with --isolated)')
+    ap.add_argument('--isolated', action='store_true', help='time each HIP kernel alone (config 4 by default)')
     ap.add_argument('--cpu-sample', type=int, default=4, help='structures in the CPU-baseline sample')
     ap.add_argument('--cpu-steps', type=int, default=2)
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--no-e3nn', action='store_true')
     ap.add_argument('--no-graph', action='store_true', help='report the eager call instead of the captured one')
     a = ap.parse_args()
+    if a.config is None:
+        a.config = 4 if a.isolated else 2
+    if a.config == 4 and not a.isolated:
+        ap.error('config 4 is an isolated-kernel workload: add --isolated')
     if a.summarize_rocprof:
         _summarize(a)
         return
@@ -210,6 +355,9 @@ def main():
     assert torch.cuda.is_available(), 'bench.py needs a GPU'
     if a.profile:
         _profile(a)
+        return
+    if a.isolated:
+        _isolated(a)
         return
     dev = torch.device('cuda:0')
     sync = torch.cuda.synchronize
@@ -309,9 +457,9 @@ def main():
     if os.path.exists(tf):
         with open(tf) as fh:
             tj = json.load(fh)
-        rec = tj['kernels'].get(d.get('symbol') or '')
-        if rec:
-            traffic, traffic_src = int(rec['traffic_bytes']), tj['source']
+        recs = [tj['kernels'][k] for k in (d.get('symbol') or '').split('+') if k in tj['kernels']]
+        if recs:
+            traffic, traffic_src = int(sum(r['traffic_bytes'] for r in recs)), tj['source']
     conv_total = {k: v for k, v in kern.items() if k.startswith('conv')}
     conv_bytes = sum(v['bytes'] * v['launches'] for v in conv_total.values())
     conv_ms = sum(v['ms'] * v['launches'] for v in conv_total.values())
