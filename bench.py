@@ -194,6 +194,7 @@ def _isolated(a):
         del op, x, g, Ys, Ws, gWs, gY, gx, out, work
         torch.cuda.empty_cache()
     elem = batch['node_attrs'].argmax(1).to(torch.int32).to(dev)
+    order = torch.argsort(elem, stable=True).to(torch.int32)
     n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
     for li, prod in enumerate(model.products):
         op = HipSymmetricContraction(prod.symmetric_contractions, device=dev)
@@ -203,10 +204,15 @@ def _isolated(a):
         bf, bb = s.bytes(N, n_elem_used)
         ff, fb = s.flops()
         tag = f'products.{li}.symmetric_contractions'
+        ms = timed(lambda i: lib.mh_sc_fwd_sorted(h, P(X), P(elem), P(order), P(op.T), P(out), N, stream), 1)
+        report(f'sc_fwd[{tag}] grouped', s.kname('sc_fwdg'), ms, bf, ff * N * s.C)
+        ms = timed(lambda i: lib.mh_sc_bwd_sorted(h, P(X), P(elem), P(order), P(op.T), P(G), P(GX), N, stream), 1)
+        report(f'sc_bwd[{tag}] grouped', s.kname('sc_bwdg'), ms, bb, fb * N * s.C)
         ms = timed(lambda i: lib.mh_sc_fwd(h, P(X), P(elem), P(op.T), P(out), N, stream), 1)
-        report(f'sc_fwd[{tag}]', s.kname('sc_fwd'), ms, bf, ff * N * s.C)
+        report(f'sc_fwd[{tag}] per-node', s.kname('sc_fwd'), ms, bf, ff * N * s.C)
         ms = timed(lambda i: lib.mh_sc_bwd(h, P(X), P(elem), P(op.T), P(G), P(GX), N, stream), 1)
-        report(f'sc_bwd[{tag}]', s.kname('sc_bwd'), ms, bb, fb * N * s.C)
+        report(f'sc_bwd[{tag}] per-node', s.kname('sc_bwd'), ms, bb, fb * N * s.C)
+        _log(f'{tag}: the model uses the {"grouped" if op.use_grouped(N, dev) else "per-node"} kernels at N = {N}')
         del op
 
 

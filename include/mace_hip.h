@@ -43,7 +43,9 @@ enum mh_kernel_kind {
     MH_SC_BWD = 4,       /* node rows                                                             */
     MH_CONV_BWD_R = 5,   /* d/dW, d/dY and per-edge dX messages: receiver rows over the receiver CSR */
     MH_CONV_GXSUM = 6,   /* dX = sum of an edge-row array over the sender CSR: sender rows        */
-    MH_NUM_KINDS = 7
+    MH_SC_FWD_G = 7,     /* groups of consecutive nodes of an element-sorted order                */
+    MH_SC_BWD_G = 8,     /* groups of consecutive nodes of an element-sorted order                */
+    MH_NUM_KINDS = 9
 };
 
 /* flags of mh_conv_bwd */
@@ -121,6 +123,17 @@ int mh_sc_fwd(mh_module* m, const float* X, const int32_t* elem, const float* T,
  * Replaces lib.sc_bwd (reference symmetric.py:106-131, launched at symmetric.py:154). */
 int mh_sc_bwd(mh_module* m, const float* X, const int32_t* elem, const float* T, const float* G, float* GX,
               int32_t N, void* stream);
+
+/* The symmetric contraction over groups of nodes: `order` [N] is a permutation of the nodes, sorted by element for
+ * speed (any permutation gives the same results).  Each workgroup takes rows_per_block consecutive entries of `order`; when they
+ * share an element every coefficient row loaded serves all of them.  Same results as mh_sc_fwd / mh_sc_bwd (the
+ * per-node arithmetic is identical).  Both replace the reference's lib.sc_fwd / lib.sc_bwd (symmetric.py:82-131,
+ * launched at symmetric.py:140, 154) with a grouping the reference does not have; bind MH_SC_FWD_G / MH_SC_BWD_G
+ * with rows_per_block = the GROUP the kernels were generated for. */
+int mh_sc_fwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     float* out, int32_t N, void* stream);
+int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     const float* G, float* GX, int32_t N, void* stream);
 
 #ifdef __cplusplus
 }

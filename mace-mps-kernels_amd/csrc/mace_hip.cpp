@@ -85,7 +85,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 2; }
+int mh_version(void) { return 3; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -232,6 +232,18 @@ int mh_sc_bwd(mh_module* m, const float* X, const int32_t* elem, const float* T,
               int32_t N, void* stream) {
     void* args[] = {&X, &elem, &T, &G, &GX, &N};
     return launch(m, MH_SC_BWD, N, args, stream, "mh_sc_bwd");
+}
+
+int mh_sc_fwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     float* out, int32_t N, void* stream) {
+    void* args[] = {&X, &elem, &order, &T, &out, &N};
+    return launch(m, MH_SC_FWD_G, N, args, stream, "mh_sc_fwd_sorted");
+}
+
+int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     const float* G, float* GX, int32_t N, void* stream) {
+    void* args[] = {&X, &elem, &order, &T, &G, &GX, &N};
+    return launch(m, MH_SC_BWD_G, N, args, stream, "mh_sc_bwd_sorted");
 }
 
 }  // extern "C"

@@ -25,6 +25,7 @@ from . import _native
 
 WAVE = 64
 LOADS_PER_FENCE = 32
+GROUP = 4              # nodes per workgroup of the element-grouped kernels
 
 
 def _poly_coeffs(ct):
@@ -138,16 +139,23 @@ def _trie(spec):
     return root
 
 
-def _fence(L, ind, cnt, M, live):
-    """Every LOADS_PER_FENCE coefficient loads, pass the table pointer and the live accumulators through an empty asm
-    statement.  Work before the fence must finish to produce its inputs and loads after it depend on its output, so
-    the coefficient loads (invariant, hence otherwise free to move) cannot all be hoisted to the top of the kernel,
-    where they would need hundreds of registers."""
+def _fence(L, ind, cnt, M, live, buffered=False):
+    """Every LOADS_PER_FENCE coefficient loads, pass the table pointer and the live accumulators through empty asm
+    statements.  Work before the fence must finish to produce their inputs and loads after it depend on their output,
+    so the coefficient loads (invariant, hence otherwise free to move) cannot all be hoisted to the top of the kernel,
+    where they would need hundreds of registers.  Volatile asm statements keep their order, so the operands are split
+    into statements of at most 16 and the table pointer (``tb``; the lane offset ``voff`` for buffer loads) goes
+    through the last one."""
     cnt[0] += M
     if cnt[0] >= LOADS_PER_FENCE:
         cnt[0] = 0
-        ops = ', '.join(f'"+v"({v})' for v in live)
-        L.append(f'{ind}asm volatile("" : "+s"(tb), {ops}); t = tb + cc;')
+        chunks = [live[i:i + 16] for i in range(0, len(live), 16)] or [[]]
+        for k, ch in enumerate(chunks):
+            last = (['"+v"(voff)' if buffered else '"+s"(tb)'] if k == len(chunks) - 1 else [])
+            ops = ', '.join([f'"+v"({v})' for v in ch] + last)
+            L.append(f'{ind}asm volatile("" : {ops});')
+        if not buffered:
+            L.append(f'{ind}t = tb + cc;')
 
 
 def _fwd_walk(spec, node, depth, L, ind, cnt):
@@ -182,49 +190,167 @@ def _bwd_walk(spec, node, depth, L, ind, cnt):
         L.append(f'{ind}}}')
 
 
-def source(spec):
+def _fwd_walk_g(spec, node, depth, L, ind, cnt, nb):
+    """The forward walk for ``nb`` nodes of one element at once: each coefficient load feeds ``nb`` FMAs (node j's
+    variables carry the prefix ``j``), in the same order as the one-node walk."""
+    live = [f'a{j}_{bi}_{m}' for j in range(nb) for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+    for bi, r0, M in node['terms']:
+        _fence(L, ind, cnt, M, live, buffered=True)
+        for m in range(M):
+            L.append(f'{ind}{{ const float tc = TLD({(r0 + m) * spec.C * 4});')
+            L += [f'{ind}  a{j}_{bi}_{m} = fmaf(tc, p{j}_{depth}, a{j}_{bi}_{m});' for j in range(nb)]
+            L.append(f'{ind}}}')
+    for i in sorted(node['kids']):
+        decl = ' '.join(f'const float p{j}_{depth + 1} = ' + (f'x{j}_{i};' if depth == 0 else f'p{j}_{depth} * x{j}_{i};')
+                        for j in range(nb))
+        L.append(f'{ind}{{ {decl}')
+        _fwd_walk_g(spec, node['kids'][i], depth + 1, L, ind + '  ', cnt, nb)
+        L.append(f'{ind}}}')
+
+
+def _bwd_walk_g(spec, node, depth, L, ind, cnt, nb):
+    """The reverse-mode walk for ``nb`` nodes of one element at once (same expressions as ``_bwd_walk`` per node)."""
+    live = [f'd{j}_{i}' for j in range(nb) for i in range(spec.n_ell)] + \
+           [f'G{j}_{k}' for j in range(nb) for k in range(1, depth + 1)]
+    for bi, r0, M in node['terms']:
+        _fence(L, ind, cnt, M, live, buffered=True)
+        L.append(f'{ind}{{ ' + ' '.join(f'const float tc{m} = TLD({(r0 + m) * spec.C * 4});' for m in range(M)))
+        for j in range(nb):
+            s_ = ' + '.join(f'tc{m} * g{j}_{bi}_{m}' for m in range(M))
+            L.append(f'{ind}  G{j}_{depth} += {s_};')
+        L.append(f'{ind}}}')
+    for i in sorted(node['kids']):
+        kid = node['kids'][i]
+        decl = ' '.join(f'const float p{j}_{depth + 1} = ' + (f'x{j}_{i};' if depth == 0 else f'p{j}_{depth} * x{j}_{i};')
+                        for j in range(nb))
+        L.append(f'{ind}{{ {decl}')
+        L.append(f'{ind}  ' + ' '.join(f'float G{j}_{depth + 1} = 0.0f;' for j in range(nb)))
+        _bwd_walk_g(spec, kid, depth + 1, L, ind + '  ', cnt, nb)
+        for j in range(nb):
+            if depth == 0:
+                L.append(f'{ind}  d{j}_{i} += G{j}_1;')
+            else:
+                L.append(f'{ind}  d{j}_{i} = fmaf(G{j}_{depth + 1}, p{j}_{depth}, d{j}_{i});')
+                L.append(f'{ind}  G{j}_{depth} = fmaf(G{j}_{depth + 1}, x{j}_{i}, G{j}_{depth});')
+        L.append(f'{ind}}}')
+
+
+def source(spec, group=None):
+    """HIP source of the per-node kernels ``sc_fwd`` / ``sc_bwd`` (one workgroup per node, the reference's launch
+    shape) and the element-grouped kernels ``sc_fwdg`` / ``sc_bwdg``: one workgroup per GROUP consecutive nodes of an
+    element-sorted order.  When the group's nodes share an element (every group but those straddling an element
+    boundary) every coefficient load feeds GROUP FMAs instead of one; other groups run the one-node body per node.
+    Per node the arithmetic is the same sequence either way."""
+    group = GROUP if group is None else group
     C, R, n = spec.C, spec.nrows, spec.n_ell
     L = [_native.device_header(),
          f'#define C {C}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}', f'#define N_ELL {n}',
-         f'#define R {R}', f'#define OUT_DIM {spec.out_dim}']
-    head = [
-        '  const int b = mh_xcd_block(blockIdx.x, gridDim.x);',
-        '  if (b >= N) return;',
-        '  const int c = threadIdx.x;',
-        '  const bool active = c < C;',
-        '  const int cc = active ? c : C - 1;',
-        '  const float* __restrict__ xp = X + ((size_t)b * C + cc) * N_ELL;',
-    ] + [f'  const float x{i} = xp[{i}];' for i in range(n)] + [
-        '  const float* tb = T + (size_t)elem[b] * ((size_t)R * C);',
-        '  const float* t = tb + cc;',
-    ]
+         f'#define R {R}', f'#define OUT_DIM {spec.out_dim}', f'#define GROUP {group}',
+         f'#define TBYTES {spec.n_elem * R * C * 4}',
+         # coefficient row loads: raw buffer loads over T at lane offset voff (VGPR) + row offset, the row offset split
+         # into a 4 KiB-aligned part (SGPR, shared by 8 consecutive rows) and the instruction's 12-bit immediate
+         '#define TLD(off) __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff + ((off) & 4095), '
+         '(off) & ~4095, 0))']
+    assert spec.n_elem * R * C * 4 < 2 ** 31, 'coefficient table too large for 32-bit buffer offsets'
     trie = _trie(spec)
-    # ------------------------------------------------------------------------------------- forward
+    lane = ['  const int c = threadIdx.x;', '  const bool active = c < C;', '  const int cc = active ? c : C - 1;',
+            '  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)T, (short)0, TBYTES, 0x00020000);']
+
+    def node_head(ind, bexpr):
+        return ([f'{ind}const int b = {bexpr};',
+                 f'{ind}const float* __restrict__ xp = X + ((size_t)b * C + cc) * N_ELL;'] +
+                [f'{ind}const float x{i} = xp[{i}];' for i in range(n)] +
+                [f'{ind}const float* tb = T + (size_t)elem[b] * ((size_t)R * C);', f'{ind}const float* t = tb + cc;'])
+
+    def fwd_one(ind):
+        B = [f'{ind}float a{bi}_{m} = 0.0f;' for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+        _fwd_walk(spec, trie, 0, B, ind, [0])
+        B.append(f'{ind}if (active) {{')
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            B += [f'{ind}  out[(size_t)b * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{bi}_{m};' for m in range(M)]
+        return B + [f'{ind}}}']
+
+    def bwd_one(ind):
+        B = [f'{ind}float d{i} = 0.0f;' for i in range(n)]
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            B += [f'{ind}const float g{bi}_{m} = G[(size_t)b * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];'
+                  for m in range(M)]
+        B.append(f'{ind}float G0 = 0.0f;')
+        _bwd_walk(spec, trie, 0, B, ind, [0])
+        B += [f'{ind}(void)G0;', f'{ind}if (active) {{',
+              f'{ind}  float* __restrict__ gp = GX + ((size_t)b * C + c) * N_ELL;']
+        B += [f'{ind}  gp[{i}] = d{i};' for i in range(n)]
+        return B + [f'{ind}}}']
+
+    def group_head():
+        H = ['  const int q0 = mh_xcd_block(blockIdx.x, gridDim.x) * GROUP;', '  if (q0 >= N) return;'] + lane
+        H.append('  const int qn = min(GROUP, N - q0);')
+        # nodes past the end repeat the last one (loaded, never stored), so every index stays in range
+        H += [f'  const int n{j} = order[q0 + min({j}, qn - 1)];' for j in range(group)]
+        H += [f'  const int e{j} = elem[n{j}];' for j in range(group)]
+        same = ' && '.join(f'e0 == e{j}' for j in range(1, group)) or 'true'
+        H += [f'  if ({same}) {{', '    int voff = (e0 * (R * C) + cc) * 4;']
+        for j in range(group):
+            H.append(f'    const float* __restrict__ xp{j} = X + ((size_t)n{j} * C + cc) * N_ELL;')
+            H += [f'    const float x{j}_{i} = xp{j}[{i}];' for i in range(n)]
+        return H
+
+    def guarded(j, lines):
+        return lines if j == 0 else [f'      if ({j} < qn) {{'] + ['  ' + x for x in lines] + ['      }']
+
+    # ------------------------------------------------------------------------------- per-node forward
     L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwd")}(const float* __restrict__ X,',
-          '    const int* __restrict__ elem, const float* __restrict__ T, float* __restrict__ out, int N) {']
-    L += head
-    for bi, bl in enumerate(spec.blocks):
-        L += [f'  float a{bi}_{m} = 0.0f;' for m in range(bl['M'])]
-    _fwd_walk(spec, trie, 0, L, '  ', [0])
-    L.append('  if (active) {')
-    for bi, bl in enumerate(spec.blocks):
-        M = bl['M']
-        L += [f'    out[(size_t)b * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{bi}_{m};' for m in range(M)]
-    L += ['  }', '}', '']
-    # ------------------------------------------------------------------------------------ backward
+          '    const int* __restrict__ elem, const float* __restrict__ T, float* __restrict__ out, int N) {',
+          '  const int bq = mh_xcd_block(blockIdx.x, gridDim.x);', '  if (bq >= N) return;'] + lane
+    L += node_head('  ', 'bq') + fwd_one('  ') + ['}', '']
+    # ------------------------------------------------------------------------------ per-node backward
     L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwd")}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const float* __restrict__ T, const float* __restrict__ G,',
-          '    float* __restrict__ GX, int N) {']
-    L += head
-    L += [f'  float d{i} = 0.0f;' for i in range(n)]
-    for bi, bl in enumerate(spec.blocks):
-        M = bl['M']
-        L += [f'  const float g{bi}_{m} = G[(size_t)b * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];' for m in range(M)]
-    L.append('  float G0 = 0.0f;')
-    _bwd_walk(spec, trie, 0, L, '  ', [0])
-    L += ['  (void)G0;', '  if (active) {', '    float* __restrict__ gp = GX + ((size_t)b * C + c) * N_ELL;']
-    L += [f'    gp[{i}] = d{i};' for i in range(n)]
-    L += ['  }', '}', '']
+          '    float* __restrict__ GX, int N) {',
+          '  const int bq = mh_xcd_block(blockIdx.x, gridDim.x);', '  if (bq >= N) return;'] + lane
+    L += node_head('  ', 'bq') + bwd_one('  ') + ['}', '']
+    # -------------------------------------------------------------------------------- grouped forward
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwdg")}(const float* __restrict__ X,',
+          '    const int* __restrict__ elem, const int* __restrict__ order, const float* __restrict__ T,',
+          '    float* __restrict__ out, int N) {']
+    L += group_head()
+    L += [f'    float a{j}_{bi}_{m} = 0.0f;' for j in range(group) for bi, bl in enumerate(spec.blocks)
+          for m in range(bl['M'])]
+    _fwd_walk_g(spec, trie, 0, L, '    ', [0], group)
+    L.append('    if (active) {')
+    for j in range(group):
+        st = []
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            st += [f'      out[(size_t)n{j} * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{j}_{bi}_{m};'
+                   for m in range(M)]
+        L += guarded(j, st)
+    L += ['    }', '  } else {', '    for (int j = 0; j < qn; ++j) {']
+    L += ['  ' + x for x in node_head('    ', 'order[q0 + j]') + fwd_one('    ')]
+    L += ['    }', '  }', '}', '']
+    # ------------------------------------------------------------------------------- grouped backward
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwdg")}(const float* __restrict__ X,',
+          '    const int* __restrict__ elem, const int* __restrict__ order, const float* __restrict__ T,',
+          '    const float* __restrict__ G, float* __restrict__ GX, int N) {']
+    L += group_head()
+    for j in range(group):
+        L += [f'    float d{j}_{i} = 0.0f;' for i in range(n)]
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'    const float g{j}_{bi}_{m} = G[(size_t)n{j} * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];'
+                  for m in range(M)]
+    L.append('    ' + ' '.join(f'float G{j}_0 = 0.0f;' for j in range(group)))
+    _bwd_walk_g(spec, trie, 0, L, '    ', [0], group)
+    L.append('    ' + ' '.join(f'(void)G{j}_0;' for j in range(group)))
+    L.append('    if (active) {')
+    for j in range(group):
+        st = [f'      GX[((size_t)n{j} * C + c) * N_ELL + {i}] = d{j}_{i};' for i in range(n)]
+        L += guarded(j, st)
+    L += ['    }', '  } else {', '    for (int j = 0; j < qn; ++j) {']
+    L += ['  ' + x for x in node_head('    ', 'order[q0 + j]') + bwd_one('    ')]
+    L += ['    }', '  }', '}', '']
     return '\n'.join(L)
 
 
@@ -232,26 +358,34 @@ def source(spec):
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
                     'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
 
-_elem_cache = []          # [(weakref(node_attrs), version, elem int32)], most recent first
+_elem_cache = []          # [(weakref(node_attrs), version, (elem int32, order int32))], most recent first
+_SIMDS = {}               # device index -> SIMD count (4 per compute unit)
+
+
+def element_order(node_attrs):
+    """(elem, order): the argmax of the one-hot node attributes as int32 (reference symmetric.py:169) and the node
+    indices stably sorted by element, which the grouped kernels walk.  Cached per node_attrs tensor."""
+    ver = node_attrs._version
+    for i, (ref, v, eo) in enumerate(_elem_cache):
+        if ref() is node_attrs and v == ver:
+            return _native.hold_for_capture(eo)
+    elem = torch.argmax(node_attrs, dim=1).to(torch.int32).contiguous()
+    order = torch.argsort(elem, stable=True).to(torch.int32).contiguous()
+    if _native.capturing():
+        return elem, order     # recomputed by every replay; its memory only holds values once the graph runs
+    _elem_cache.insert(0, (weakref.ref(node_attrs), ver, (elem, order)))
+    del _elem_cache[4:]
+    return elem, order
 
 
 def element_index(node_attrs):
-    """argmax of the one-hot node attributes as int32, cached per node_attrs tensor (reference symmetric.py:169)."""
-    ver = node_attrs._version
-    for i, (ref, v, el) in enumerate(_elem_cache):
-        if ref() is node_attrs and v == ver:
-            return _native.hold_for_capture(el)
-    el = torch.argmax(node_attrs, dim=1).to(torch.int32).contiguous()
-    if _native.capturing():
-        return el              # recomputed by every replay; its memory only holds values once the graph runs
-    _elem_cache.insert(0, (weakref.ref(node_attrs), ver, el))
-    del _elem_cache[4:]
-    return el
+    """argmax of the one-hot node attributes as int32 (reference symmetric.py:169)."""
+    return element_order(node_attrs)[0]
 
 
 class _SCFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, elem, op):
+    def forward(ctx, x, elem, order, op):
         s = op.spec
         if x.dtype != torch.float32 or not x.is_cuda:
             raise TypeError('mace_hip_kernels: symmetric contraction expects float32 GPU input')
@@ -260,9 +394,17 @@ class _SCFn(torch.autograd.Function):
         x = x.contiguous()
         N = x.shape[0]
         out = torch.empty(N, s.out_dim, device=x.device, dtype=torch.float32)
-        _native.launch(f'sc_fwd[{op.tag}]', _native.load().mh_sc_fwd, op.module.handle, _native.ptr(x),
-                       _native.ptr(elem), _native.ptr(op.T), _native.ptr(out), N, _native.stream_of(x))
-        ctx.save_for_backward(x, elem)
+        lib = _native.load()
+        grouped = op.use_grouped(N, x.device)
+        if grouped:
+            _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_sorted, op.module.handle, _native.ptr(x),
+                           _native.ptr(elem), _native.ptr(order), _native.ptr(op.T), _native.ptr(out), N,
+                           _native.stream_of(x))
+        else:
+            _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd, op.module.handle, _native.ptr(x), _native.ptr(elem),
+                           _native.ptr(op.T), _native.ptr(out), N, _native.stream_of(x))
+        ctx.save_for_backward(x, elem, order)
+        ctx.grouped = grouped
         ctx.op = op
         return out
 
@@ -270,13 +412,18 @@ class _SCFn(torch.autograd.Function):
     def backward(ctx, g):
         if torch.is_grad_enabled():          # only true under create_graph=True
             raise RuntimeError(_DOUBLE_BACKWARD)
-        x, elem = ctx.saved_tensors
+        x, elem, order = ctx.saved_tensors
         op = ctx.op
         gx = torch.empty_like(x)
-        _native.launch(f'sc_bwd[{op.tag}]', _native.load().mh_sc_bwd, op.module.handle, _native.ptr(x),
-                       _native.ptr(elem), _native.ptr(op.T), _native.ptr(g.contiguous()), _native.ptr(gx),
-                       x.shape[0], _native.stream_of(x))
-        return gx, None, None
+        lib, g = _native.load(), g.contiguous()
+        if ctx.grouped:
+            _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_sorted, op.module.handle, _native.ptr(x),
+                           _native.ptr(elem), _native.ptr(order), _native.ptr(op.T), _native.ptr(g), _native.ptr(gx),
+                           x.shape[0], _native.stream_of(x))
+        else:
+            _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd, op.module.handle, _native.ptr(x), _native.ptr(elem),
+                           _native.ptr(op.T), _native.ptr(g), _native.ptr(gx), x.shape[0], _native.stream_of(x))
+        return gx, None, None, None
 
 
 class HipSymmetricContraction(torch.nn.Module):
@@ -294,12 +441,28 @@ class HipSymmetricContraction(torch.nn.Module):
             self.module = _native.Module(code, {
                 _native.MH_SC_FWD: (self.spec.kname('sc_fwd'), self.spec.block, 1),
                 _native.MH_SC_BWD: (self.spec.kname('sc_bwd'), self.spec.block, 1),
+                _native.MH_SC_FWD_G: (self.spec.kname('sc_fwdg'), self.spec.block, GROUP),
+                _native.MH_SC_BWD_G: (self.spec.kname('sc_bwdg'), self.spec.block, GROUP),
             })
         self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
         self.original = [sc]
         self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
+        self.grouped = None           # None: by size (use_grouped); True / False: force a kernel family
+
+    def use_grouped(self, n_nodes, device):
+        """The element-grouped kernels serve GROUP nodes per workgroup, so they need GROUP times more nodes to keep
+        the GPU busy: use them when they still give at least 4 waves per SIMD (config 4's 20,000 atoms: 1.7-1.9x
+        faster than one node per workgroup; config 2's 2,533 atoms: slower)."""
+        if self.grouped is not None:
+            return bool(self.grouped)
+        key = device.index if device.index is not None else torch.cuda.current_device()
+        if key not in _SIMDS:
+            _SIMDS[key] = 4 * torch.cuda.get_device_properties(key).multi_processor_count
+        waves = -(-n_nodes // GROUP) * self.spec.ncb
+        return waves >= 4 * _SIMDS[key]
 
     def forward(self, x, y):
         if y.shape != (x.shape[0], self.spec.n_elem):
             raise ValueError(f'node_attrs must be [{x.shape[0]}, {self.spec.n_elem}], got {tuple(y.shape)}')
-        return _SCFn.apply(x, element_index(y), self)
+        elem, order = element_order(y)
+        return _SCFn.apply(x, elem, order, self)

@@ -190,15 +190,19 @@ def test_conv_deterministic_and_empty():
 SC_MODELS = [('32x0e+32x1o', 2, 2), ('128x0e+128x1o', 3, 3), ('64x0e', 2, 2), ('128x0e+128x1o+128x2e', 3, 3)]
 
 
+@pytest.mark.parametrize('grouped', [False, True])
 @pytest.mark.parametrize('hidden,lmax,corr', SC_MODELS)
-def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr):
+def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr, grouped):
+    """Both kernel families: one node per workgroup, and element-grouped (GROUP nodes per workgroup, mixed groups at
+    element boundaries, a partial last group)."""
     dev = _dev()
     model = factory.make_model(hidden, lmax, corr, elements=factory.ELEMENTS_PTCOH)
     rng = np.random.default_rng(4)
     for li, prod in enumerate(model.products):
-        print(f'[case] sc {hidden} l{lmax} c{corr} layer {li}', flush=True)
+        print(f'[case] sc {hidden} l{lmax} c{corr} layer {li} grouped={grouped}', flush=True)
         sc = prod.symmetric_contractions
         op = HipSymmetricContraction(sc, device=dev)
+        op.grouped = grouped
         C, n_ell = op.spec.C, op.spec.n_ell
         n = 37
         x = rng.normal(size=(n, C, n_ell)) * 0.7
@@ -223,6 +227,36 @@ def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr):
         want.backward(torch.tensor(g, dtype=torch.float64))
         assert _rel(out.detach().double().cpu().numpy(), want.detach().numpy()) < SC_TOL
         assert _rel(xt.grad.double().cpu().numpy(), xo.grad.numpy()) < SC_TOL
+
+
+def test_sc_grouped_matches_per_node():
+    """The element-grouped kernels (mh_sc_*_sorted) against the per-node ones (mh_sc_fwd / mh_sc_bwd, the reference's
+    launch shape): sorted order (mostly single-element groups) and a random permutation (mostly mixed groups), with a
+    node count that leaves a partial last group."""
+    dev = _dev()
+    print('[case] sc grouped vs per-node', flush=True)
+    model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    op = HipSymmetricContraction(model.products[0].symmetric_contractions, device=dev)
+    s, h = op.spec, op.module.handle
+    rng = np.random.default_rng(9)
+    n = 4 * 13 + 3
+    elem_np = rng.integers(0, 4, n)
+    f = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+    X, G = f(rng.normal(size=(n, s.C, s.n_ell)) * 0.7), f(rng.normal(size=(n, s.out_dim)))
+    elem = torch.tensor(elem_np, dtype=torch.int32, device=dev)
+    lib, P, st = _native.load(), _native.ptr, _native.stream_of(X)
+    out1, gx1 = torch.empty(n, s.out_dim, device=dev), torch.empty_like(X)
+    _native.check(lib.mh_sc_fwd(h, P(X), P(elem), P(op.T), P(out1), n, st), 'sc_fwd')
+    _native.check(lib.mh_sc_bwd(h, P(X), P(elem), P(op.T), P(G), P(gx1), n, st), 'sc_bwd')
+    sorted_order = torch.argsort(elem, stable=True).to(torch.int32)
+    perm = torch.tensor(rng.permutation(n), dtype=torch.int32, device=dev)
+    for order in (sorted_order, perm):
+        out2, gx2 = torch.full_like(out1, float('nan')), torch.full_like(gx1, float('nan'))
+        _native.check(lib.mh_sc_fwd_sorted(h, P(X), P(elem), P(order), P(op.T), P(out2), n, st), 'sc_fwd_sorted')
+        _native.check(lib.mh_sc_bwd_sorted(h, P(X), P(elem), P(order), P(op.T), P(G), P(gx2), n, st), 'sc_bwd_sorted')
+        torch.cuda.synchronize()
+        assert _rel(out2.double().cpu().numpy(), out1.double().cpu().numpy()) < 1e-6
+        assert _rel(gx2.double().cpu().numpy(), gx1.double().cpu().numpy()) < 1e-6
 
 
 def test_kernels_match_golden_fixtures():
