@@ -66,7 +66,9 @@ def _kernel_table(met, batch, n_real_edges, summary):
             bf, bb = s.bytes(n, n_real_edges)
             ff, fb = s.flops()
             rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul, s.kname('conv_fwd'))
-            bwd_sym = (f"{s.kname('conv_bwdr')}+{s.kname('conv_gxsum')}" if m.bwd_recv else s.kname('conv_bwd'))
+            # MACE's blocks pass tp_weights = W0 * cutoff, which takes the factored receiver-ordered kernel
+            bwd_sym = (f"{s.kname('conv_bwdrc' if m.fuse_cutoff else 'conv_bwdr')}+{s.kname('conv_gxsum')}"
+                       if m.bwd_recv or m.fuse_cutoff else s.kname('conv_bwd'))
             rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul, bwd_sym)
         elif isinstance(m, HipSymmetricContraction):
             s = m.spec
@@ -181,15 +183,15 @@ def _isolated(a):
                                              stream), nb)
         report(f'conv_fwd[{tag}]', s.kname('conv_fwd'), ms, bf, ff * n_real * s.mul)
         ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
-                                                  P(rp_s), P(ei_s), P(work), P(gx), P(gWs[i]), P(gY), N, 3, stream), nb)
+                                                  P(rp_s), P(ei_s), P(work), P(gx), P(gWs[i]), P(gY), None, None, N, 3, stream), nb)
         report(f'conv_bwd[{tag}] dx+dW+dY', f"{s.kname('conv_bwdr')}+{s.kname('conv_gxsum')}", ms, bb,
                fb * n_real * s.mul)
         ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
-                                                  None, None, None, None, P(gWs[i]), P(gY), N, 2, stream), nb)
+                                                  None, None, None, None, P(gWs[i]), P(gY), None, None, N, 2, stream), nb)
         report(f'conv_bwd[{tag}] dW+dY', s.kname('conv_bwdr'), ms, bb - 4 * (N * s.x_dim + n_real * 2 + N + 1),
                fb * n_real * s.mul)
         ms = timed(lambda i: lib.mh_conv_bwd(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_s), P(ei_s), P(gr.recv),
-                                             P(gx), P(gWs[i]), P(gY), N, 3, stream), nb)
+                                             P(gx), P(gWs[i]), P(gY), None, None, N, 3, stream), nb)
         report(f'conv_bwd[{tag}] sender-ordered', s.kname('conv_bwd'), ms, bb, fb * n_real * s.mul)
         del op, x, g, Ys, Ws, gWs, gY, gx, out, work
         torch.cuda.empty_cache()

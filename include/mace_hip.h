@@ -45,7 +45,8 @@ enum mh_kernel_kind {
     MH_CONV_GXSUM = 6,   /* dX = sum of an edge-row array over the sender CSR: sender rows        */
     MH_SC_FWD_G = 7,     /* groups of consecutive nodes of an element-sorted order                */
     MH_SC_BWD_G = 8,     /* groups of consecutive nodes of an element-sorted order                */
-    MH_NUM_KINDS = 9
+    MH_CONV_BWD_RC = 9,  /* MH_CONV_BWD_R with the weights factored as W0 * cutoff per edge       */
+    MH_NUM_KINDS = 10
 };
 
 /* flags of mh_conv_bwd */
@@ -108,11 +109,15 @@ int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, co
  * then sums them over the sender CSR (rowptr_s, eids_s) in CSR order: gx[s] = Σ_{p} work[eids_s[p], :].  No
  * atomics; the result is deterministic.  Together the two kernels replace lib.conv_bwd_wy + lib.conv_bwd_x
  * (reference conv.py:144-222, launched at conv.py:259-270).  Without MH_WANT_GX, rowptr_s, eids_s, gx and work
- * may be NULL. */
+ * may be NULL.
+ * Factored weights: with `cutoff` non-NULL ([E] floats) the weights are W = W0 * cutoff[e] (MACE multiplies the
+ * radial MLP output by the cutoff envelope before the convolution) and `W` must point to W0.  Then `gW` receives
+ * ∂/∂W0 = ∂/∂W * cutoff[e] and `g_cutoff` ([E]) receives ∂/∂cutoff[e] = Σ_{k,u} ∂/∂W[e,k,u] * W0[e,k,u], so the caller
+ * need not differentiate the product itself (kernel MH_CONV_BWD_RC; no reference counterpart). */
 int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
                      const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
                      const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
-                     int32_t N, int32_t flags, void* stream);
+                     const float* cutoff, float* g_cutoff, int32_t N, int32_t flags, void* stream);
 
 /* Symmetric contraction forward: out[b, off + c*M + m] = Σ_terms T[elem[b], r0+m, c] Π X[b, c, idx].
  * Replaces lib.sc_fwd (reference symmetric.py:82-105, launched at symmetric.py:140). */

@@ -85,7 +85,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 3; }
+int mh_version(void) { return 4; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -196,15 +196,23 @@ int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, co
 int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
                      const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
                      const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
-                     int32_t N, int32_t flags, void* stream) {
+                     const float* cutoff, float* g_cutoff, int32_t N, int32_t flags, void* stream) {
     if (!(flags & MH_WANT_GWY)) return fail(-1, "mh_conv_bwd_recv: flags must include MH_WANT_GWY");
     if (!x || !gW || !gY) return fail(-1, "mh_conv_bwd_recv: x, gW and gY are required");
+    if (cutoff && !g_cutoff) return fail(-1, "mh_conv_bwd_recv: cutoff given but g_cutoff is NULL");
     const bool want_gx = (flags & MH_WANT_GX) != 0;
     if (want_gx && (!gx || !work || !rowptr_s || !eids_s))
         return fail(-1, "mh_conv_bwd_recv: gx requested but gx, work or the sender CSR is NULL");
     int32_t kflags = want_gx ? 1 : 0;
-    void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags};
-    int rc = launch(m, MH_CONV_BWD_R, N, args, stream, "mh_conv_bwd_recv");
+    int rc;
+    if (cutoff) {
+        void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags, &cutoff,
+                        &g_cutoff};
+        rc = launch(m, MH_CONV_BWD_RC, N, args, stream, "mh_conv_bwd_recv (factored weights)");
+    } else {
+        void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags};
+        rc = launch(m, MH_CONV_BWD_R, N, args, stream, "mh_conv_bwd_recv");
+    }
     if (rc || !want_gx) return rc;
     const float* msg = work;
     void* args2[] = {&msg, &rowptr_s, &eids_s, &gx, &N};

@@ -271,9 +271,37 @@ def _grad_needed(ctx, i):
         return True
 
 
+def _factored_weights(W):
+    """(W0, cutoff) when ``W`` is the product ``W0 * cutoff`` that MACE forms right before the convolution
+    (``tp_weights = self.conv_tp_weights(edge_feats) * cutoff``, W0 [E, NW], cutoff [E, 1]), read from the product's
+    autograd node; otherwise None.  The backward then takes the gradients of W0 and cutoff from the kernel directly
+    and the product's own backward (a pass over [E, NW] for each factor) never runs; any other use of the product
+    still gets its gradient through that node.  Anything unexpected (no graph, other op, other shapes, a factor that
+    needs no gradient, a factor modified in place) keeps the plain path."""
+    gf = W.grad_fn
+    if gf is None or type(gf).__name__ != 'MulBackward0' or W.dim() != 2:
+        return None
+    try:
+        a, b = gf._saved_self, gf._saved_other
+    except (RuntimeError, AttributeError):
+        return None
+    if a is None or b is None:
+        return None
+    E, nw = W.shape
+    for w0, c in ((a, b), (b, a)):
+        if (isinstance(w0, torch.Tensor) and isinstance(c, torch.Tensor) and tuple(w0.shape) == (E, nw)
+                and tuple(c.shape) in ((E, 1), (E,)) and w0.dtype == torch.float32 and c.dtype == torch.float32
+                and w0.device == W.device and c.device == W.device):
+            return w0, c
+    return None
+
+
 class _ConvFn(torch.autograd.Function):
+    """Inputs (x, Y, W, W0, cut, edge_index, op).  Plain: W is the weight tensor, W0 = cut = None.  Factored:
+    W = W0 * cut is passed detached (the forward kernel reads it) and W0, cut are the differentiable inputs."""
+
     @staticmethod
-    def forward(ctx, x, Y, W, edge_index, op):
+    def forward(ctx, x, Y, W, W0, cut, edge_index, op):
         _check_inputs(op, x, Y, W, edge_index)
         x, Y, W = x.contiguous(), Y.contiguous(), W.contiguous()
         n = x.shape[0]
@@ -284,7 +312,12 @@ class _ConvFn(torch.autograd.Function):
         _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, _native.ptr(x), _native.ptr(Y),
                        _native.ptr(W), _native.ptr(rowptr), _native.ptr(eids), _native.ptr(gr.send),
                        _native.ptr(out), n, _native.stream_of(x))
-        ctx.save_for_backward(x, Y, W)
+        ctx.factored = W0 is not None
+        if ctx.factored:
+            ctx.cut_shape = cut.shape
+            ctx.save_for_backward(x, Y, W0.contiguous(), cut.reshape(-1).contiguous())
+        else:
+            ctx.save_for_backward(x, Y, W)
         ctx.op, ctx.gr = op, gr
         return out
 
@@ -292,33 +325,45 @@ class _ConvFn(torch.autograd.Function):
     def backward(ctx, g):
         if torch.is_grad_enabled():          # only true under create_graph=True
             raise RuntimeError(_DOUBLE_BACKWARD)
-        x, Y, W = ctx.saved_tensors
         op, gr = ctx.op, ctx.gr
+        if ctx.factored:
+            x, Y, W0, cut = ctx.saved_tensors
+            want_w = _grad_needed(ctx, 3) or _grad_needed(ctx, 4)
+        else:
+            x, Y, W = ctx.saved_tensors
+            W0 = cut = None
+            want_w = _grad_needed(ctx, 2)
         g = g.contiguous()
         want_x = _grad_needed(ctx, 0)
-        want_wy = _grad_needed(ctx, 1) or _grad_needed(ctx, 2)
+        want_wy = _grad_needed(ctx, 1) or want_w
+        E = Y.shape[0]
         gx = torch.empty_like(x) if want_x else None
-        gW = torch.empty_like(W) if want_wy else None
         gY = torch.empty_like(Y) if want_wy else None
+        gW = torch.empty_like(W0 if ctx.factored else W) if want_wy else None
+        gcut = torch.empty_like(cut) if want_wy and ctx.factored else None
         # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
-        flags = (_native.MH_WANT_GX if want_x else 0) | \
-            (_native.MH_WANT_GWY if want_wy and W.shape[0] > 0 else 0)
+        flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy and E > 0 else 0)
         lib = _native.load()
         P = _native.ptr
-        if flags & _native.MH_WANT_GWY and op.bwd_recv:
+        if flags & _native.MH_WANT_GWY and (op.bwd_recv or ctx.factored):
             # receiver order: g rows read once per receiver; dX goes through per-edge messages in `work`
             rowptr_r, eids_r = gr.by_recv()
             rowptr_s, eids_s = gr.by_send() if want_x else (None, None)
-            work = torch.empty(W.shape[0], op.spec.x_dim, device=x.device, dtype=torch.float32) if want_x else None
-            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv, op.module.handle, P(x), P(g), P(Y), P(W),
-                           P(rowptr_r), P(eids_r), P(gr.send), P(rowptr_s), P(eids_s), P(work), P(gx), P(gW), P(gY),
-                           x.shape[0], flags, _native.stream_of(x))
+            work = torch.empty(E, op.spec.x_dim, device=x.device, dtype=torch.float32) if want_x else None
+            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv, op.module.handle, P(x), P(g), P(Y),
+                           P(W0 if ctx.factored else W), P(rowptr_r), P(eids_r), P(gr.send), P(rowptr_s), P(eids_s),
+                           P(work), P(gx), P(gW), P(gY), P(cut), P(gcut), x.shape[0], flags, _native.stream_of(x))
         elif flags:
+            if ctx.factored:                 # dX only: the sender-ordered kernel needs the product
+                W = W0 * cut[:, None]
             rowptr_s, eids_s = gr.by_send()
             _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, P(x), P(g), P(Y), P(W),
                            P(rowptr_s), P(eids_s), P(gr.recv), P(gx), P(gW), P(gY), x.shape[0], flags,
                            _native.stream_of(x))
-        return gx, gY, gW, None, None
+        if ctx.factored:
+            gc = gcut.view(ctx.cut_shape) if gcut is not None else None
+            return gx, gY, None, gW, gc, None, None
+        return gx, gY, gW, None, None, None, None
 
 
 class HipConvTP(torch.nn.Module):
@@ -338,6 +383,7 @@ class HipConvTP(torch.nn.Module):
                 _native.MH_CONV_BWD: (self.spec.kname('conv_bwd'), self.spec.block, 1),
                 _native.MH_CONV_BWD_WY: (self.spec.kname('conv_bwd_wy'), self.spec.block, WAVE),
                 _native.MH_CONV_BWD_R: (self.spec.kname('conv_bwdr'), self.spec.block, 1),
+                _native.MH_CONV_BWD_RC: (self.spec.kname('conv_bwdrc'), self.spec.block, 1),
                 _native.MH_CONV_GXSUM: (self.spec.kname('conv_gxsum'), gxsum_block(self.spec), 1),
             })
         self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out
@@ -347,6 +393,12 @@ class HipConvTP(torch.nn.Module):
         self.tag = 'conv'             # name used in launch timings (patch_model sets the module path)
         # backward walks the receiver CSR when gW/gY are wanted (False: the sender-ordered fused kernel)
         self.bwd_recv = True
+        # differentiate MACE's tp_weights = W0 * cutoff inside the backward kernel (see _factored_weights)
+        self.fuse_cutoff = True
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
-        return _ConvFn.apply(node_feats, edge_attrs, tp_weights, edge_index, self)
+        fac = _factored_weights(tp_weights) if self.fuse_cutoff and torch.is_grad_enabled() else None
+        if fac is not None:
+            W0, cut = fac
+            return _ConvFn.apply(node_feats, edge_attrs, tp_weights.detach(), W0, cut, edge_index, self)
+        return _ConvFn.apply(node_feats, edge_attrs, tp_weights, None, None, edge_index, self)

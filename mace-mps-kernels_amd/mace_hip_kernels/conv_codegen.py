@@ -155,11 +155,12 @@ class _Gen:
             L.append(f'{ind}}}')
         return L
 
-    def bwd_body(self, ind, with_gx, use_m, store):
+    def bwd_body(self, ind, with_gx, use_m, store, cut=False):
         """h_a = Σ_c M[a,c]·g_c (or Σ_{b,c} v·y_b·g_c);  gx_a += w·h_a;  gW_k = Σ_a x_a·h_a;
         P_b += w·Σ_{a,c} v·x_a·g_c.  With ``store`` the gW row is written and P accumulated; full-wave specs write it
         unconditionally (a store under a branch makes the wait-count pass assume it may be absent and wait for every
-        outstanding access at the next edge, stores included)."""
+        outstanding access at the next edge, stores included).  With ``cut`` the weights are W = W0·c (w0{k}, ce):
+        the stored row is ∂/∂W0 = gW·c and Pc accumulates this lane's share of ∂/∂c = Σ_k gW_k·W0_k."""
         s = self.s
         L = []
         for co in s.coef:
@@ -184,6 +185,10 @@ class _Gen:
                 L.append(f'{ind}}}')
                 continue
             gw = _sum([f'xv{self.xi[i1] + a} * h{a}' for a in hs])
+            if cut:
+                L.append(f'{ind}  const float gwk = {gw};')
+                L.append(f'{ind}  Pc = fmaf(gwk, w0{k}, Pc);')
+                gw = 'gwk * ce'
             st = f'mh_st_nt(gwe + {k * s.mul}, ol1, {gw});'      # written once, never re-read here
             L.append(f'{ind}  {st}' if self.full else f'{ind}  if (active) {st}')
             for b in range(co['d2']):
@@ -233,10 +238,11 @@ def gy_reduce(indent, y_dim, y_pad):
     return L
 
 
-def _gy_combine(indent, edge_expr):
-    """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order).  The leading
-    barrier also orders the chunk's Ms reads before the next chunk's prologue overwrites them."""
-    return [
+def _gy_combine(indent, edge_expr, cut=False):
+    """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order); with ``cut``
+    also the ∂/∂c partials.  The leading barrier also orders the chunk's Ms reads before the next chunk's prologue
+    overwrites them."""
+    L = [
         f'{indent}__syncthreads();',
         f'{indent}for (int q = threadIdx.x; q < cnt * Y_DIM; q += BLOCK) {{',
         f'{indent}  const int j = q / Y_DIM, b = q - j * Y_DIM;',
@@ -244,8 +250,14 @@ def _gy_combine(indent, edge_expr):
         f'{indent}  for (int w = 0; w < NCB; ++w) v += part[w][j][b];',
         f'{indent}  gY[(size_t)({edge_expr}) * Y_DIM + b] = v;',
         f'{indent}}}',
-        f'{indent}__syncthreads();',
     ]
+    if cut:
+        L += [f'{indent}for (int j = threadIdx.x; j < cnt; j += BLOCK) {{',
+              f'{indent}  float v = 0.0f;',
+              f'{indent}  for (int w = 0; w < NCB; ++w) v += partc[w][j];',
+              f'{indent}  gcut[{edge_expr}] = v;',
+              f'{indent}}}']
+    return L + [f'{indent}__syncthreads();']
 
 
 def source(spec):
@@ -380,24 +392,32 @@ def source(spec):
     L += _gy_combine('  ', 'pb + j')
     L += ['}', '']
     L += _bwd_recv(G, gyr, pdecl, decl, copy)
+    L += _bwd_recv(G, gyr, pdecl, decl, copy, cut=True)
     L += _gx_sum(spec)
     return '\n'.join(L)
 
 
-def _bwd_recv(G, gyr, pdecl, decl, copy):
+def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
     """Receiver-ordered backward (rows = receivers, the forward's CSR).  g[r] is loaded once per row and stays in
     registers; each edge gathers only x[s] (X_DIM floats) and its W row, writes its gW row and gY, and, when dX is
     wanted, its dX message gxm[e] = Σ_k W_k·h_k (X_DIM floats), which ``conv_gxsum`` adds up per sender.  Per edge
     this reads X_DIM + NW floats per channel block instead of the OUT_DIM-float g row the sender-ordered kernel
-    gathers."""
+    gathers.
+
+    ``cut`` (kernel ``conv_bwdrc``): the weights arrive factored as W = W0·c with a per-edge scalar c (MACE's
+    ``tp_weights * cutoff``).  The kernel reads W0 and c, writes ∂/∂W0 = gW·c instead of gW, and reduces
+    ∂/∂c[e] = Σ_{k,u} gW·W0 over the channels (a butterfly over the wave, then LDS across waves, fixed order), which
+    saves the caller the separate passes over the [E, NW] tensors that differentiating the product takes."""
     spec, nx, nk = G.s, G.nx, G.s.nins
     L = [
-        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwdr")}(',
+        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwdrc" if cut else "conv_bwdr")}(',
         '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
         '    const float* __restrict__ W, const int* __restrict__ rowptr, const int* __restrict__ eids,',
         '    const int* __restrict__ senders, float* __restrict__ gW, float* __restrict__ gY,',
-        '    float* __restrict__ gxm, int N, int flags) {',
+        '    float* __restrict__ gxm, int N, int flags' +
+        (', const float* __restrict__ cutv, float* __restrict__ gcut) {' if cut else ') {'),
         '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
+    ] + (['  __shared__ float partc[NCB][MH_WAVE];'] if cut else []) + [
         '  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
         '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);',
         '  const int r = mh_xcd_block(blockIdx.x, gridDim.x);',
@@ -419,7 +439,13 @@ def _bwd_recv(G, gyr, pdecl, decl, copy):
         C += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
         C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
         C += ['    }', '    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
-        C += copy('xv', 'xn', nx) + copy('w', 'wn', nk)
+        C += copy('xv', 'xn', nx)
+        if cut:
+            C += ['      const float ce = cutv[e];'] + copy('w0', 'wn', nk)
+            C += [f'      const float w{k} = w0{k} * ce;' for k in range(nk)]
+            C += ['      float Pc = 0.0f;']
+        else:
+            C += copy('w', 'wn', nk)
         C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
               '        const int e1 = mh_bcast(my_e, j1), s1 = mh_bcast(my_s, j1);']
         C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
@@ -427,7 +453,7 @@ def _bwd_recv(G, gyr, pdecl, decl, copy):
         C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
         if msg:
             C += ['      ' + decl('gxa', nx, '0.0f')]
-        C += G.bwd_body('      ', with_gx=msg, use_m=True, store=True)
+        C += G.bwd_body('      ', with_gx=msg, use_m=True, store=True, cut=cut)
         if msg:
             C += ['      {', '        float* __restrict__ gme = gxm + (size_t)e * X_DIM;']
             for b, (l, _, off) in enumerate(spec.in1):
@@ -436,8 +462,12 @@ def _bwd_recv(G, gyr, pdecl, decl, copy):
                 C += [f'        {t}' if G.full else f'        if (active) {t}' for t in st]
             C += ['      }']
         C += gyr
+        if cut:
+            # all-reduce over the wave (every lane ends with the sum), lane 0 keeps the wave's partial
+            C += [f'      Pc += {_xchg("Pc", bit)};' for bit in range(5, -1, -1)]
+            C += ['      if (lane == 0) partc[wave][j] = Pc;']
         C += ['    }']
-        C += _gy_combine('    ', 'eids[pb + j]')
+        C += _gy_combine('    ', 'eids[pb + j]', cut=cut)
         return C + ['  }']
 
     L += ['  if (GX) {'] + ['  ' + t for t in chunks(True)] + ['  } else {']

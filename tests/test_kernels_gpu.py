@@ -109,6 +109,41 @@ def test_conv_bwd_without_dx(order):
     assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
 
 
+@pytest.mark.parametrize('want_x', [True, False])
+def test_conv_factored_cutoff_weights(want_x):
+    """tp_weights = W0 * cutoff (MACE's form): the backward kernel returns d/dW0 and d/dcutoff itself.  Against the
+    oracle: d/dW0 = gW * c, d/dc = sum_k gW * W0 (gW the oracle's d/dW), with some cutoffs exactly zero (padding)."""
+    dev = _dev()
+    print(f'[case] conv factored cutoff weights want_x={want_x}', flush=True)
+    tp = _tp('128x0e+128x1o', 3)
+    op = HipConvTP(tp, device=dev)
+    desc = oconv.describe_tp(tp)
+    coef = oconv.path_terms(desc)
+    rng = np.random.default_rng(6)
+    n, e = 41, 700
+    s, r = _graph(rng, n, e)
+    x, Y, W0 = (rng.normal(size=sh) for sh in ((n, desc['x_dim']), (e, desc['y_dim']), (e, 10 * 128)))
+    c = rng.uniform(0.0, 1.0, size=(e, 1))
+    c[::7] = 0.0
+    g = rng.normal(size=(n, desc['out_dim']))
+    t = lambda a, rg=True: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=rg)  # noqa: E731
+    xt, Yt, W0t, ct = t(x, want_x), t(Y), t(W0), t(c)
+    W = W0t * ct
+    assert hconv._factored_weights(W) is not None
+    out = op(xt, Yt, W, torch.tensor(np.stack([s, r]), device=dev))
+    out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+    Wd = (W0.astype(np.float32) * c.astype(np.float32)).astype(np.float64)     # the fp32 product the kernel reads
+    assert _rel(out.detach().double().cpu().numpy(), oconv.conv_fwd(desc, coef, x, Y, Wd, s, r, n)) < CONV_TOL
+    gW = oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)
+    assert _rel(W0t.grad.double().cpu().numpy(), gW * c) < CONV_TOL
+    assert _rel(ct.grad.double().cpu().numpy(), (gW * W0).sum(1, keepdims=True)) < CONV_TOL
+    assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, Wd, s, r)) < CONV_TOL
+    if want_x:
+        assert _rel(xt.grad.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, Wd, s, r, n)) < CONV_TOL
+    else:
+        assert xt.grad is None
+
+
 def test_conv_c_abi_bwd_x_and_bwd_wy():
     """The reference-shaped entry points mh_conv_bwd_x / mh_conv_bwd_wy against the oracle and the fused kernel."""
     dev = _dev()
@@ -145,11 +180,14 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
     gW3, gY3, gx3 = torch.zeros_like(Wt), torch.zeros_like(Yt), torch.zeros_like(xt)
     work = torch.empty(e, desc['x_dim'], device=dev)
     _native.check(lib.mh_conv_bwd_recv(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_r), P(eids_r), P(st),
-                                       P(rowptr_s), P(eids_s), P(work), P(gx3), P(gW3), P(gY3), n, 3, st_),
+                                       P(rowptr_s), P(eids_s), P(work), P(gx3), P(gW3), P(gY3), None, None, n, 3, st_),
                   'bwd_recv')
     assert lib.mh_conv_bwd_recv(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_r), P(eids_r), P(st),
-                                None, None, None, P(gx3), P(gW3), P(gY3), n, 3, st_) != 0   # GX without scratch
+                                None, None, None, P(gx3), P(gW3), P(gY3), None, None, n, 3, st_) != 0   # GX without scratch
     assert b'NULL' in lib.mh_last_error()
+    assert lib.mh_conv_bwd_recv(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_r), P(eids_r), P(st),
+                                None, None, None, None, P(gW3), P(gY3), P(Yt), None, n, 2, st_) != 0  # no g_cutoff
+    assert b'g_cutoff' in lib.mh_last_error()
     torch.cuda.synchronize()
     assert _rel(gx3.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, W, s, r, n)) < CONV_TOL
     assert _rel(gW3.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
