@@ -65,7 +65,8 @@ def _kernel_table(met, batch, n_real_edges, summary):
             s = m.spec
             bf, bb = s.bytes(n, n_real_edges)
             ff, fb = s.flops()
-            rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul, s.kname('conv_fwd'))
+            rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul,
+                                          s.kname('conv_fwdc' if m.fuse_cutoff else 'conv_fwd'))
             # MACE's blocks pass tp_weights = W0 * cutoff, which takes the factored receiver-ordered kernel
             bwd_sym = (f"{s.kname('conv_bwdrc' if m.fuse_cutoff else 'conv_bwdr')}+{s.kname('conv_gxsum')}"
                        if m.bwd_recv or m.fuse_cutoff else s.kname('conv_bwd'))

@@ -46,7 +46,8 @@ enum mh_kernel_kind {
     MH_SC_FWD_G = 7,     /* groups of consecutive nodes of an element-sorted order                */
     MH_SC_BWD_G = 8,     /* groups of consecutive nodes of an element-sorted order                */
     MH_CONV_BWD_RC = 9,  /* MH_CONV_BWD_R with the weights factored as W0 * cutoff per edge       */
-    MH_NUM_KINDS = 10
+    MH_CONV_FWD_C = 10,  /* MH_CONV_FWD skipping edges whose cutoff is 0                          */
+    MH_NUM_KINDS = 11
 };
 
 /* flags of mh_conv_bwd */
@@ -82,6 +83,13 @@ int mh_module_bind(mh_module* m, int kind, const char* name, int block_threads, 
  * rowptr/eids: receiver-sorted CSR.  Replaces lib.conv_fwd (reference conv.py:109-141, launched at conv.py:247). */
 int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
                 const int32_t* eids, const int32_t* senders, float* out, int32_t N, void* stream);
+
+/* mh_conv_fwd for weights W = W0 * cutoff[e] (W passed as the product, cutoff [E]): an edge with cutoff[e] == 0
+ * contributes exactly zero and is skipped (the padding of fixed-size graphs, and neighbour-list entries beyond the
+ * cutoff radius).  Same result as mh_conv_fwd up to the sign of zero sums.  No reference counterpart. */
+int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
+                    const int32_t* eids, const int32_t* senders, const float* cutoff, float* out, int32_t N,
+                    void* stream);
 
 /* d/dx only, over the sender-sorted CSR: gx[s] = Σ_{e: sender(e)=s} ∂TP/∂x · g[receivers[e]].
  * Replaces lib.conv_bwd_x (reference conv.py:144-176, launched at conv.py:264).  Runs the MH_CONV_BWD kernel with

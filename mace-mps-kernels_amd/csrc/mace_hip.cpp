@@ -85,7 +85,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 4; }
+int mh_version(void) { return 5; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -181,6 +181,14 @@ int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, co
                 const int32_t* eids, const int32_t* senders, float* out, int32_t N, void* stream) {
     void* args[] = {&x, &Y, &W, &rowptr, &eids, &senders, &out, &N};
     return launch(m, MH_CONV_FWD, N, args, stream, "mh_conv_fwd");
+}
+
+int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
+                    const int32_t* eids, const int32_t* senders, const float* cutoff, float* out, int32_t N,
+                    void* stream) {
+    if (!cutoff) return fail(-1, "mh_conv_fwd_cut: cutoff is NULL");
+    void* args[] = {&x, &Y, &W, &rowptr, &eids, &senders, &out, &N, &cutoff};
+    return launch(m, MH_CONV_FWD_C, N, args, stream, "mh_conv_fwd_cut");
 }
 
 int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, const float* W,

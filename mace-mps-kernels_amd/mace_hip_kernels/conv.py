@@ -309,14 +309,18 @@ class _ConvFn(torch.autograd.Function):
         rowptr, eids = gr.by_recv()
         out = torch.empty(n, op.spec.out_dim, device=x.device, dtype=torch.float32)
         lib = _native.load()
-        _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, _native.ptr(x), _native.ptr(Y),
-                       _native.ptr(W), _native.ptr(rowptr), _native.ptr(eids), _native.ptr(gr.send),
-                       _native.ptr(out), n, _native.stream_of(x))
         ctx.factored = W0 is not None
+        P = _native.ptr
         if ctx.factored:
+            cutf = cut.reshape(-1).contiguous()
+            # edges with cutoff 0 (padding, or beyond r_max in a skinned neighbour list) contribute exactly zero
+            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd_cut, op.module.handle, P(x), P(Y), P(W),
+                           P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n, _native.stream_of(x))
             ctx.cut_shape = cut.shape
-            ctx.save_for_backward(x, Y, W0.contiguous(), cut.reshape(-1).contiguous())
+            ctx.save_for_backward(x, Y, W0.contiguous(), cutf)
         else:
+            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, P(x), P(Y), P(W), P(rowptr),
+                           P(eids), P(gr.send), P(out), n, _native.stream_of(x))
             ctx.save_for_backward(x, Y, W)
         ctx.op, ctx.gr = op, gr
         return out
@@ -384,6 +388,7 @@ class HipConvTP(torch.nn.Module):
                 _native.MH_CONV_BWD_WY: (self.spec.kname('conv_bwd_wy'), self.spec.block, WAVE),
                 _native.MH_CONV_BWD_R: (self.spec.kname('conv_bwdr'), self.spec.block, 1),
                 _native.MH_CONV_BWD_RC: (self.spec.kname('conv_bwdrc'), self.spec.block, 1),
+                _native.MH_CONV_FWD_C: (self.spec.kname('conv_fwdc'), self.spec.block, 1),
                 _native.MH_CONV_GXSUM: (self.spec.kname('conv_gxsum'), gxsum_block(self.spec), 1),
             })
         self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out

@@ -280,36 +280,55 @@ def source(spec):
     ms_decl = ['  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
                '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);']
     # ------------------------------------------------------------------------------------------- forward
-    L += [
-        f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwd")}(',
-        '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
-        '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
-        '    float* __restrict__ out, int N) {',
-    ] + ms_decl + [
-        '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
-        '  if (n >= N) return;',
-    ] + G.prelude() + [
-        '  ' + decl('acc', no, '0.0f'),
-        '  ' + decl('xn', nx), '  ' + decl('wn', nk),
-        '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
-        '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
-        '    const int cnt = min(MH_WAVE, p1 - pb);',
-        '    int my_e = 0, my_s = 0;',
-        '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }',
-    ]
-    L += G.m_prologue('    ', 'my_e')
-    L += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
-    L += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
-    L += ['    }', '    for (int j = 0; j < cnt; ++j) {']
-    L += copy('xv', 'xn', nx) + copy('w', 'wn', nk)
-    L += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
-    L += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
-    L += ['      }']
-    L += G.fwd_body('      ')
-    L += ['    }', '    __syncthreads();', '  }', '  if (active) {', '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
-    for co in spec.coef:
-        L += [f'    mh_st(o + {co["o3"] + c}, ol{co["d3"]}, acc{G.oi[co["k"]] + c});' for c in range(co['d3'])]
-    L += ['  }', '}', '']
+    def fwd_kernel(cut):
+        """``cut`` (kernel ``conv_fwdc``): W = W0·c with a per-edge scalar c; an edge with c == 0 (padding, or past
+        r_max in a neighbour list with a skin) contributes exactly zero, so each chunk of 64 edges is first compacted
+        to its edges with c != 0 (ballot, then a per-wave LDS scatter by lane rank) and only those are walked.  Every
+        wave of the workgroup builds the same list, so the barriers stay uniform."""
+        F = [
+            f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwdc" if cut else "conv_fwd")}(',
+            '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
+            '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
+            '    float* __restrict__ out, int N' + (', const float* __restrict__ cutv) {' if cut else ') {'),
+        ] + ms_decl + (['  __shared__ int sidx[NCB][MH_WAVE];'] if cut else []) + [
+            '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
+            '  if (n >= N) return;',
+        ] + G.prelude() + [
+            '  ' + decl('acc', no, '0.0f'),
+            '  ' + decl('xn', nx), '  ' + decl('wn', nk),
+            '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
+            '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
+        ]
+        if cut:
+            F += ['    const int cnt0 = min(MH_WAVE, p1 - pb);',
+                  '    int my_e = 0, my_s = 0;',
+                  '    bool keep = false;',
+                  '    if (lane < cnt0) { my_e = eids[pb + lane]; keep = cutv[my_e] != 0.0f; }',
+                  '    const unsigned long long kept = __ballot(keep);',
+                  '    const int cnt = __popcll(kept);',
+                  '    if (keep) sidx[wave][__popcll(kept & ((1ull << lane) - 1ull))] = my_e;',
+                  '    if (cnt == 0) continue;',
+                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; }']
+        else:
+            F += ['    const int cnt = min(MH_WAVE, p1 - pb);',
+                  '    int my_e = 0, my_s = 0;',
+                  '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
+        F += G.m_prologue('    ', 'my_e')
+        F += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
+        F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
+        F += ['    }', '    for (int j = 0; j < cnt; ++j) {']
+        F += copy('xv', 'xn', nx) + copy('w', 'wn', nk)
+        F += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
+        F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+        F += ['      }']
+        F += G.fwd_body('      ')
+        F += ['    }', '    __syncthreads();', '  }', '  if (active) {',
+              '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
+        for co in spec.coef:
+            F += [f'    mh_st(o + {co["o3"] + c}, ol{co["d3"]}, acc{G.oi[co["k"]] + c});' for c in range(co['d3'])]
+        return F + ['  }', '}', '']
+
+    L += fwd_kernel(False) + fwd_kernel(True)
     # ----------------------------------------------------------------------------------- fused backward
     L += [
         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwd")}(',

@@ -125,6 +125,7 @@ def test_conv_factored_cutoff_weights(want_x):
     x, Y, W0 = (rng.normal(size=sh) for sh in ((n, desc['x_dim']), (e, desc['y_dim']), (e, 10 * 128)))
     c = rng.uniform(0.0, 1.0, size=(e, 1))
     c[::7] = 0.0
+    c[r == 2] = 0.0                  # a receiver whose every edge is skipped by the forward
     g = rng.normal(size=(n, desc['out_dim']))
     t = lambda a, rg=True: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=rg)  # noqa: E731
     xt, Yt, W0t, ct = t(x, want_x), t(Y), t(W0), t(c)
