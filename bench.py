@@ -177,6 +177,12 @@ def _isolated(a):
         gWs = [torch.empty(E, nw, device=dev) for _ in range(nb)]
         gY, gx, out = torch.empty(E, s.y_dim, device=dev), torch.empty_like(x), torch.empty(N, s.out_dim, device=dev)
         work = torch.empty(E, s.x_dim, device=dev)
+        # the model passes tp_weights = W0 * cutoff: cutoff in (0, 1] inside r_max, exactly 0 on padding edges
+        ei = batch['edge_index']
+        vec = batch['positions'][ei[1]] - batch['positions'][ei[0]] + batch['shifts']
+        inside = (vec.norm(dim=1) < meta['r_max']).to(dev)
+        cut = torch.where(inside, 0.1 + 0.9 * torch.rand(E, generator=gen).to(dev), torch.zeros((), device=dev))
+        gcut = torch.empty(E, device=dev)
         bf, bb = s.bytes(N, n_real)
         ff, fb = s.flops()
         tag = f'interactions.{li}.conv_tp'
@@ -192,9 +198,17 @@ def _isolated(a):
         report(f'conv_bwd[{tag}] dW+dY', s.kname('conv_bwdr'), ms, bb - 4 * (N * s.x_dim + n_real * 2 + N + 1),
                fb * n_real * s.mul)
         ms = timed(lambda i: lib.mh_conv_bwd(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_s), P(ei_s), P(gr.recv),
-                                             P(gx), P(gWs[i]), P(gY), None, None, N, 3, stream), nb)
+                                             P(gx), P(gWs[i]), P(gY), N, 3, stream), nb)
         report(f'conv_bwd[{tag}] sender-ordered', s.kname('conv_bwd'), ms, bb, fb * n_real * s.mul)
-        del op, x, g, Ys, Ws, gWs, gY, gx, out, work
+        ms = timed(lambda i: lib.mh_conv_fwd_cut(h, P(x), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send), P(cut),
+                                                 P(out), N, stream), nb)
+        report(f'conv_fwd[{tag}] factored (model path)', s.kname('conv_fwdc'), ms, bf, ff * n_real * s.mul)
+        ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
+                                                  P(rp_s), P(ei_s), P(work), P(gx), P(gWs[i]), P(gY), P(cut), P(gcut),
+                                                  N, 3, stream), nb)
+        report(f'conv_bwd[{tag}] factored dx+dW+dY (model path)', f"{s.kname('conv_bwdrc')}+{s.kname('conv_gxsum')}",
+               ms, bb, fb * n_real * s.mul)
+        del op, x, g, Ys, Ws, gWs, gY, gx, out, work, cut, gcut
         torch.cuda.empty_cache()
     elem = batch['node_attrs'].argmax(1).to(torch.int32).to(dev)
     order = torch.argsort(elem, stable=True).to(torch.int32)
