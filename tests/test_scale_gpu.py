@@ -1,0 +1,114 @@
+"""
+Parity at BASELINE config 4's full size (20,000-atom bulk Pt, 820,110 edges, hidden 128x0e+128x1o+128x2e, l_max 3,
+correlation 3), where the float64 oracle is too slow, through size-independent properties:
+
+* the convolution is linear in each of x, W and Y, so for any g:  <g, out> = <gx, x> = <gW, W> = <gY, Y>  (each
+  product of the backward is the adjoint of the forward; a dropped term, a wrong sign or a wrong index breaks it);
+* the receiver-ordered and the sender-ordered backward, and the factored-weight (W0 * cutoff) and plain paths, agree;
+* the element-grouped and the one-node-per-workgroup symmetric contraction agree.
+
+Tolerances are relative, sized for fp32 sums over ~10^8 terms: 1e-4 on the inner products, 1e-5 between kernels.
+"""
+import pytest
+import torch
+
+from mace_hip_kernels import HipConvTP, HipSymmetricContraction
+from mace_hip_kernels import conv as hconv
+from mace_lite import factory
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope='module')
+def cfg4():
+    assert torch.cuda.is_available(), 'GPU test needs a GPU'
+    model, batch, meta = factory.workload(4)
+    return model, batch, meta
+
+
+def _rel(a, b):
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def _dot(a, b):
+    return float((a.double() * b.double()).sum())
+
+
+@pytest.mark.parametrize('layer', [0, 1])
+def test_conv_adjoint_identities_full_size(cfg4, layer):
+    model, batch, meta = cfg4
+    dev = torch.device('cuda:0')
+    print(f'[case] config 4 conv layer {layer} adjoint identities', flush=True)
+    op = HipConvTP(model.interactions[layer].conv_tp, device=dev)
+    s = op.spec
+    N, E = batch['positions'].shape[0], batch['edge_index'].shape[1]
+    ei = batch['edge_index'].to(dev)
+    gen = torch.Generator(device='cpu').manual_seed(10 + layer)
+    r = lambda *sh: torch.randn(*sh, generator=gen).to(dev).requires_grad_(True)  # noqa: E731
+    x, Y, W = r(N, s.x_dim), r(E, s.y_dim), r(E, s.nins * s.mul)
+    g = torch.randn(N, s.out_dim, generator=gen).to(dev)
+    results = {}
+    for order in ('recv', 'send'):
+        op.bwd_recv = order == 'recv'
+        out = op(x, Y, W, ei)
+        gx, gY, gW = torch.autograd.grad(out, (x, Y, W), g)
+        lhs = _dot(g, out.detach())
+        for name, gr_, inp in (('x', gx, x), ('W', gW, W), ('Y', gY, Y)):
+            rhs = _dot(gr_, inp.detach())
+            print(f'  {order}: <g,out> = {lhs:.6e}  <g{name},{name}> = {rhs:.6e}', flush=True)
+            assert abs(lhs - rhs) <= 1e-4 * abs(lhs)
+        results[order] = (out.detach(), gx, gY, gW)
+        del out
+    a, b = results['recv'], results['send']
+    assert torch.equal(a[0], b[0])
+    for u, v in zip(a[1:], b[1:]):
+        assert _rel(u, v) < 1e-5
+
+
+def test_conv_factored_matches_plain_full_size(cfg4):
+    model, batch, meta = cfg4
+    dev = torch.device('cuda:0')
+    print('[case] config 4 conv layer 1 factored weights vs plain', flush=True)
+    op = HipConvTP(model.interactions[1].conv_tp, device=dev)
+    s = op.spec
+    N, E = batch['positions'].shape[0], batch['edge_index'].shape[1]
+    ei = batch['edge_index'].to(dev)
+    gen = torch.Generator(device='cpu').manual_seed(20)
+    x = torch.randn(N, s.x_dim, generator=gen).to(dev).requires_grad_(True)
+    Y = torch.randn(E, s.y_dim, generator=gen).to(dev).requires_grad_(True)
+    W0 = torch.randn(E, s.nins * s.mul, generator=gen).to(dev).requires_grad_(True)
+    c = torch.rand(E, 1, generator=gen).to(dev)
+    c[::5] = 0.0
+    c.requires_grad_(True)
+    g = torch.randn(N, s.out_dim, generator=gen).to(dev)
+    got = {}
+    for fuse in (True, False):
+        op.fuse_cutoff = fuse
+        W = W0 * c
+        assert (hconv._factored_weights(W) is not None) or not fuse
+        out = op(x, Y, W, ei)
+        got[fuse] = (out.detach(),) + torch.autograd.grad(out, (x, Y, W0, c), g)
+        del out, W
+    for u, v in zip(got[True], got[False]):
+        assert _rel(u, v) < 1e-5
+
+
+def test_sc_grouped_matches_per_node_full_size(cfg4):
+    model, batch, meta = cfg4
+    dev = torch.device('cuda:0')
+    N = batch['positions'].shape[0]
+    attrs = batch['node_attrs'].to(dev)
+    gen = torch.Generator(device='cpu').manual_seed(30)
+    for li, prod in enumerate(model.products):
+        print(f'[case] config 4 symmetric contraction {li} grouped vs per node', flush=True)
+        op = HipSymmetricContraction(prod.symmetric_contractions, device=dev)
+        assert op.use_grouped(N, dev)
+        x = (0.5 * torch.randn(N, op.spec.C, op.spec.n_ell, generator=gen)).to(dev).requires_grad_(True)
+        g = torch.randn(N, op.spec.out_dim, generator=gen).to(dev)
+        got = {}
+        for grouped in (True, False):
+            op.grouped = grouped
+            out = op(x, attrs)
+            got[grouped] = (out.detach(), torch.autograd.grad(out, x, g)[0])
+        for u, v in zip(got[True], got[False]):
+            assert _rel(u, v) < 1e-5
