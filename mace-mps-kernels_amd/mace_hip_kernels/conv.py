@@ -161,31 +161,41 @@ class ConvSpec:
 
 # ------------------------------------------------------------------------------------------- graph cache
 def csr_by(index, n):
-    """Edges sorted by ``index`` → (rowptr[n+1], edge ids) as int32 (reference conv.py:229-235)."""
+    """Edges sorted by ``index`` → (rowptr[n+1], edge ids) as int32 (reference conv.py:229-235).  Stable sort, then
+    rowptr[k] = number of keys below k by binary search of the sorted keys: device work only, no host
+    synchronisation, so it can be captured in a HIP graph."""
     order = torch.argsort(index, stable=True)
-    counts = torch.bincount(index, minlength=n)
-    rowptr = torch.zeros(n + 1, dtype=torch.int64, device=index.device)
-    rowptr[1:] = torch.cumsum(counts, 0)
+    keys = index[order]
+    rowptr = torch.searchsorted(keys, torch.arange(n + 1, device=index.device, dtype=keys.dtype))
     return rowptr.to(torch.int32), order.to(torch.int32)
 
 
 class _Graph:
-    """int32 senders/receivers and both CSRs of one edge_index, built lazily and shared by every layer of a call."""
+    """int32 senders/receivers and both CSRs of one edge_index, built lazily and shared by every layer of a call.
 
-    def __init__(self, edge_index, n):
+    ``validate=False`` (a graph first met inside a HIP graph capture, which cannot synchronise to check it): the
+    indices are clamped into [0, n) instead of checked, so a bad edge list gives wrong numbers, never an out-of-range
+    access; both CSRs are built at once, inside the capture."""
+
+    def __init__(self, edge_index, n, validate=True):
         if edge_index.dim() != 2 or edge_index.shape[0] != 2:
             raise ValueError(f'edge_index must be [2, E], got {tuple(edge_index.shape)}')
-        if edge_index.numel():
+        if validate and edge_index.numel():
             # the kernels index x, g and the CSRs with these values: reject out-of-range nodes on the host
             lo, hi = torch.aminmax(edge_index)
             lo, hi = int(lo), int(hi)
             if lo < 0 or hi >= n:
                 raise ValueError(f'edge_index holds node {lo if lo < 0 else hi} outside [0, {n})')
         self.n = n
-        self.send = edge_index[0].to(torch.int32).contiguous()
-        self.recv = edge_index[1].to(torch.int32).contiguous()
+        ei = edge_index if validate else edge_index.clamp(0, max(n - 1, 0))
+        self.send = ei[0].to(torch.int32).contiguous()
+        self.recv = ei[1].to(torch.int32).contiguous()
         self._by_recv = self._by_send = None
-        self._ei = edge_index
+        self._ei = ei
+        self._validated = validate
+        if not validate:
+            self._by_recv = csr_by(self.recv, n)
+            self._by_send = csr_by(self.send, n)
 
     def by_recv(self):
         if self._by_recv is None:
@@ -208,10 +218,21 @@ class _Graph:
 
 _graph_cache = []          # [(weakref(edge_index), version, n, _Graph)], most recent first
 _GRAPH_CACHE_SIZE = 4
+# Set by graphs.capture(rebuild_graph=True): a capture builds the graph of an edge_index it meets (clamped, no host
+# validation) instead of reusing the eager cache, so every replay rebuilds the CSRs from the tensor's contents.
+_capture_rebuild = False
+_capture_graphs = {}       # graphs built inside the current capture, by (id(edge_index), n); cleared after capture
 
 
 def graph_for(edge_index, n):
     """Cached ``_Graph`` for this edge_index tensor object (invalidated by in-place modification or deletion)."""
+    if _native.capturing() and _capture_rebuild:
+        gr = _capture_graphs.get((id(edge_index), n))
+        if gr is None or gr.src is not edge_index:
+            gr = _Graph(edge_index, n, validate=False)
+            gr.src = edge_index
+            _capture_graphs[(id(edge_index), n)] = gr
+        return _native.hold_for_capture(gr)
     ver = edge_index._version
     for i, (ref, v, nn_, gr) in enumerate(_graph_cache):
         if ref() is edge_index and v == ver and nn_ == n:
@@ -221,7 +242,8 @@ def graph_for(edge_index, n):
     if _native.capturing():
         # building a graph validates it on the host (a synchronisation), which a capture cannot contain
         raise RuntimeError('mace_hip_kernels: this edge_index is new inside a HIP graph capture; run the model once '
-                           'eagerly on the same tensors before capturing (mace_hip_kernels.graphs.capture does)')
+                           'eagerly on the same tensors before capturing (mace_hip_kernels.graphs.capture does), or '
+                           'capture with rebuild_graph=True')
     gr = _Graph(edge_index, n)
     _graph_cache.insert(0, (weakref.ref(edge_index), ver, n, gr))
     del _graph_cache[_GRAPH_CACHE_SIZE:]

@@ -14,13 +14,18 @@ skin) the whole call — forward, ``autograd.grad`` and the HIP kernels — can 
         batch['positions'].copy_(new_positions)
     out = call.replay()                                   # every kernel runs again; out['forces'] is overwritten
 
-What is frozen: the tensors of ``batch`` (their addresses and shapes) and the edge list's content — the CSRs the
-convolution kernels read are built by the eager warm-up and reused.  After a neighbour-list rebuild, capture again.
-The caller must not resize or reallocate the batch tensors while the capture is in use.
+What is frozen: the tensors of ``batch`` (their addresses and shapes).  By default the edge list's content is frozen
+too — the CSRs the convolution kernels read are built by the eager warm-up and reused; after a neighbour-list
+rebuild, capture again.  With ``rebuild_graph=True`` the captured call also rebuilds the CSRs (a stable device sort
+per direction) from the current contents of ``batch['edge_index']``, so a neighbour list of the same size (padded)
+can be copied in before each replay.  Those rebuilt graphs cannot be validated on the host inside the graph: node
+indices are clamped into range instead (a bad edge list gives wrong numbers, never a bad memory access).  The caller
+must not resize or reallocate the batch tensors while the capture is in use.
 """
 import torch
 
 from . import _native
+from . import conv as _conv
 
 __all__ = ['capture', 'CapturedCall']
 
@@ -29,7 +34,7 @@ class CapturedCall:
     """A captured model call: ``replay()`` re-runs it on the current contents of ``batch`` and returns the outputs
     (the same tensors every time, overwritten by each replay)."""
 
-    def __init__(self, model, batch, warmup=2, **kwargs):
+    def __init__(self, model, batch, warmup=2, rebuild_graph=False, **kwargs):
         if not torch.cuda.is_available():
             raise RuntimeError('HIP graph capture needs a GPU')
         self.model, self.batch, self.kwargs = model, batch, kwargs
@@ -44,10 +49,13 @@ class CapturedCall:
         torch.cuda.synchronize()
         _native.take_capture_holds()
         self.graph = torch.cuda.CUDAGraph()
+        _conv._capture_rebuild = bool(rebuild_graph)
         try:
             with torch.cuda.graph(self.graph):
                 self.out = model(batch, **kwargs)
         finally:
+            _conv._capture_rebuild = False
+            _conv._capture_graphs.clear()
             self._held = _native.take_capture_holds()     # cached device memory the graph reads
 
     def replay(self):
@@ -55,6 +63,6 @@ class CapturedCall:
         return self.out
 
 
-def capture(model, batch, warmup=2, **kwargs):
+def capture(model, batch, warmup=2, rebuild_graph=False, **kwargs):
     """Capture ``model(batch, **kwargs)`` (energy, forces, ...) as a HIP graph; see the module docstring."""
-    return CapturedCall(model, batch, warmup=warmup, **kwargs)
+    return CapturedCall(model, batch, warmup=warmup, rebuild_graph=rebuild_graph, **kwargs)

@@ -59,3 +59,39 @@ def test_captured_call_matches_eager(cfg, stress):
         prev_f = f_g
     del call
     torch.cuda.synchronize()
+
+
+def test_captured_call_rebuilds_graph():
+    """capture(rebuild_graph=True): the edge list is part of the graph's input.  Each replay gets a different padded
+    neighbour list (the structure re-jittered and its neighbours rebuilt, same atoms, same padded size) and must match
+    an eager call on that batch."""
+    assert torch.cuda.is_available(), 'GPU test needs a GPU'
+    dev = torch.device('cuda:0')
+    print('[case] graph capture with edge-list rebuild', flush=True)
+    model = copy.deepcopy(factory.make_model('32x0e+32x1o', 2, 2, elements=factory.ELEMENTS_PTCOH)).to(dev)
+    assert not patch_model(model, verbose=False)['skipped']
+    rng = np.random.default_rng(3)
+    s0 = factory.pt_slab_with_adsorbates(rng, (4, 4, 4), 15)
+    batches = []
+    for _ in range(3):
+        s = s0.copy()
+        s.positions = s.positions + rng.normal(0.0, 0.12, size=s.positions.shape)
+        batches.append(D.batch_graphs([D.graph_of(s, 5.0)], factory.ELEMENTS_PTCOH, torch.float32, 'cpu',
+                                      pad_edges_to=3200, r_max=5.0))
+    assert not torch.equal(batches[0]['edge_index'], batches[1]['edge_index'])
+    static = _gpu_batch(batches[0], dev)
+    call = capture(model, static, rebuild_graph=True, compute_force=True)
+    for rep, b in enumerate(batches[1:] + batches[:1]):
+        with torch.no_grad():
+            for k in ('positions', 'edge_index', 'shifts', 'unit_shifts'):
+                static[k].copy_(b[k].to(dev))
+        out = call.replay()
+        e_g, f_g = out['energy'].detach().clone(), out['forces'].detach().clone()
+        ref = model(D.fresh(_gpu_batch(b, dev)), compute_force=True)
+        torch.cuda.synchronize()
+        de = float((e_g - ref['energy']).abs().max())
+        df = float((f_g - ref['forces']).abs().max())
+        print(f'  replay {rep}: |dE| {de:.2e} eV  |dF| {df:.2e} eV/A', flush=True)
+        assert de <= 1e-3 and df <= 1e-5
+    del call
+    torch.cuda.synchronize()
