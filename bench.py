@@ -56,7 +56,7 @@ def _time_calls(model, batch, steps, warmup, sync):
 def _kernel_table(met, batch, n_real_edges, summary):
     """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only)."""
     import torch
-    from mace_hip_kernels import HipConvTP, HipSymmetricContraction
+    from mace_hip_kernels import HipConvTP, HipSphericalHarmonics, HipSymmetricContraction
     n = batch['positions'].shape[0]
     n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
     rows = {}
@@ -77,6 +77,11 @@ def _kernel_table(met, batch, n_real_edges, summary):
             ff, fb = s.flops()
             rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C, s.kname('sc_fwd'))
             rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C, s.kname('sc_bwd'))
+        elif isinstance(m, HipSphericalHarmonics):
+            s = m.spec                                  # every edge of the padded list is evaluated
+            bf, bb = s.bytes(batch['edge_index'].shape[1])
+            rows[f'sh_fwd[{m.tag}]'] = (bf, 0, s.kname('sh_fwd'))
+            rows[f'sh_bwd[{m.tag}]'] = (bb, 0, s.kname('sh_bwd'))
     out = {}
     for tag, (cnt, ms) in summary.items():
         nbytes, flops, sym = rows.get(tag, (0, 0, None))

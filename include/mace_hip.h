@@ -47,7 +47,9 @@ enum mh_kernel_kind {
     MH_SC_BWD_G = 8,     /* groups of consecutive nodes of an element-sorted order                */
     MH_CONV_BWD_RC = 9,  /* MH_CONV_BWD_R with the weights factored as W0 * cutoff per edge       */
     MH_CONV_FWD_C = 10,  /* MH_CONV_FWD skipping edges whose cutoff is 0                          */
-    MH_NUM_KINDS = 11
+    MH_SH_FWD = 11,      /* edge spherical harmonics: one edge per thread                         */
+    MH_SH_BWD = 12,      /* their gradient with respect to the edge vectors                       */
+    MH_NUM_KINDS = 13
 };
 
 /* flags of mh_conv_bwd */
@@ -147,6 +149,13 @@ int mh_sc_fwd_sorted(mh_module* m, const float* X, const int32_t* elem, const in
                      float* out, int32_t N, void* stream);
 int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
                      const float* G, float* GX, int32_t N, void* stream);
+
+/* Edge spherical harmonics Y[e, :] = Y_{0..l_max}(vec[e] / |vec[e]|) (vec [E, 3], Y [E, (l_max+1)^2]; e3nn's real
+ * basis, y polar axis) and their backward gvec[e] = dL/dvec[e] from gY.  The kernels are generated per (l_max,
+ * normalisation).  No reference counterpart: the reference leaves the model's edge spherical harmonics on e3nn's
+ * o3.SphericalHarmonics(normalize=True), which these replace in the model's forward (edge vectors -> edge attrs). */
+int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream);
+int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int64_t E, void* stream);
 
 #ifdef __cplusplus
 }

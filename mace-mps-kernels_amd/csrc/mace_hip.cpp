@@ -85,7 +85,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 5; }
+int mh_version(void) { return 6; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -260,6 +260,16 @@ int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const in
                      const float* G, float* GX, int32_t N, void* stream) {
     void* args[] = {&X, &elem, &order, &T, &G, &GX, &N};
     return launch(m, MH_SC_BWD_G, N, args, stream, "mh_sc_bwd_sorted");
+}
+
+int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream) {
+    void* args[] = {&vec, &Y, &E};
+    return launch(m, MH_SH_FWD, E, args, stream, "mh_sh_fwd");
+}
+
+int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int64_t E, void* stream) {
+    void* args[] = {&vec, &gY, &gvec, &E};
+    return launch(m, MH_SH_BWD, E, args, stream, "mh_sh_bwd");
 }
 
 }  // extern "C"

@@ -21,11 +21,13 @@ import warnings
 import torch
 
 from .conv import HipConvTP, conv_supported
+from .edge import HipSphericalHarmonics, sh_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
 
 __version__ = '0.1.0'
-__all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'conv_supported', 'sc_supported']
+__all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
+           'conv_supported', 'sc_supported', 'sh_supported']
 
 
 def _block_has_conv_fusion(blk):
@@ -36,9 +38,10 @@ def _block_has_conv_fusion(blk):
         return False
 
 
-def patch_model(model, conv=True, symmetric=True, verbose=True):
+def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
-    (reference __init__.py:34-79)."""
+    (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
+    edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module."""
     p = next(model.parameters())
     dev = p.device
     if dev.type != 'cuda' or torch.version.hip is None:
@@ -83,6 +86,15 @@ def patch_model(model, conv=True, symmetric=True, verbose=True):
             prod.symmetric_contractions = HipSymmetricContraction(sc, device=dev)
             prod.symmetric_contractions.tag = name
             patched.append(name)
+    if spherical_harmonics and hasattr(model, 'spherical_harmonics'):
+        sh = model.spherical_harmonics
+        if not isinstance(sh, HipSphericalHarmonics):
+            ok, why = sh_supported(sh)
+            if ok:
+                model.spherical_harmonics = HipSphericalHarmonics(sh, device=dev)
+                patched.append('spherical_harmonics')
+            else:
+                skipped.append(('spherical_harmonics', why))
     if verbose:
         for name, why in skipped:
             warnings.warn(f'mace_hip_kernels: kept e3nn for {name}: {why}')
@@ -102,4 +114,7 @@ def unpatch_model(model):
         if isinstance(getattr(prod, 'symmetric_contractions', None), HipSymmetricContraction):
             prod.symmetric_contractions = prod.symmetric_contractions.original[0]
             restored.append(f'products.{i}.symmetric_contractions')
+    if isinstance(getattr(model, 'spherical_harmonics', None), HipSphericalHarmonics):
+        model.spherical_harmonics = model.spherical_harmonics.original[0]
+        restored.append('spherical_harmonics')
     return restored

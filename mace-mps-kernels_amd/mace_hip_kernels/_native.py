@@ -17,9 +17,9 @@ LIB_PATH = os.path.join(HERE, 'libmace_hip.so')
 DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
 
 MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, MH_CONV_GXSUM, MH_SC_FWD_G, \
-    MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C = range(11)
+    MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD = range(13)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -46,6 +46,8 @@ _SIGS = {
     'mh_conv_bwd': (ctypes.c_int, [_P] * 11 + [_I, _I, _P]),
     'mh_conv_bwd_recv': (ctypes.c_int, [_P] * 16 + [_I, _I, _P]),
     'mh_conv_fwd_cut': (ctypes.c_int, [_P] * 9 + [_I, _P]),
+    'mh_sh_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int64, _P]),
+    'mh_sh_bwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
     'mh_sc_fwd_sorted': (ctypes.c_int, [_P] * 6 + [_I, _P]),
     'mh_sc_bwd_sorted': (ctypes.c_int, [_P] * 7 + [_I, _P]),
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),

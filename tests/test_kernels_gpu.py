@@ -11,13 +11,15 @@ import numpy as np
 import pytest
 import torch
 
-from mace_hip_kernels import HipConvTP, HipSymmetricContraction, _native
+from mace_hip_kernels import HipConvTP, HipSphericalHarmonics, HipSymmetricContraction, _native
 from mace_hip_kernels import conv as hconv
 from mace_lite import blocks as B
 from mace_lite import factory
+from mace_lite import o3
 from mace_lite.o3 import Irreps, TensorProduct
 from oracle import conv as oconv
 from oracle import sc as osc
+from oracle import wigner
 
 pytestmark = pytest.mark.gpu
 CONV_TOL = 2e-6
@@ -296,6 +298,74 @@ def test_sc_grouped_matches_per_node():
         torch.cuda.synchronize()
         assert _rel(out2.double().cpu().numpy(), out1.double().cpu().numpy()) < 1e-6
         assert _rel(gx2.double().cpu().numpy(), gx1.double().cpu().numpy()) < 1e-6
+
+
+SH_TOL = 5e-6        # absolute on Y (|Y| <= ~4 in component normalisation)
+
+
+@pytest.mark.parametrize('lmax,norm', [(1, 'component'), (2, 'component'), (3, 'component'), (3, 'norm')])
+def test_sh_fwd_bwd_vs_oracle(lmax, norm):
+    """Edge spherical harmonics: forward against the oracle's harmonics (fp64), backward against float64 autograd of
+    the host model's e3nn module; a ragged edge count (not a multiple of the 256-edge block), a zero vector, a
+    leading batch shape, and no edges at all."""
+    dev = _dev()
+    print(f'[case] spherical harmonics l_max {lmax} {norm}', flush=True)
+    mod = o3.SphericalHarmonics(Irreps.spherical_harmonics(lmax), normalize=True, normalization=norm)
+    op = HipSphericalHarmonics(mod, device=dev)
+    rng = np.random.default_rng(lmax)
+    e = 70001
+    v = rng.normal(size=(e, 3)) * rng.uniform(0.3, 6.0, size=(e, 1))
+    v[0] = 0.0
+    vt = torch.tensor(v, dtype=torch.float32, device=dev, requires_grad=True)
+    Y = op(vt)
+    g = rng.normal(size=(e, op.spec.dim))
+    gv, = torch.autograd.grad(Y, vt, torch.tensor(g, dtype=torch.float32, device=dev))
+    torch.cuda.synchronize()
+    vd = vt.detach().double().cpu()
+    ref = wigner.spherical_harmonics(lmax, vd.numpy()[1:]) * np.array(op.spec.scale)
+    assert np.abs(Y.detach().double().cpu().numpy()[1:] - ref).max() < SH_TOL
+    vr = vd.clone().requires_grad_(True)
+    mod64 = o3.SphericalHarmonics(Irreps.spherical_harmonics(lmax), normalize=True, normalization=norm).double()
+    Yr = mod64(vr)
+    assert np.abs(Y.detach().double().cpu().numpy() - Yr.detach().numpy()).max() < SH_TOL
+    gr, = torch.autograd.grad(Yr, vr, torch.tensor(g))
+    gv_, gr_ = gv.double().cpu().numpy(), gr.numpy()
+    assert np.abs(gv_[0] - gr_[0]).max() <= 1e-5 * np.abs(gr_[0]).max()     # zero vector: |v| clamped, ~1e30
+    assert _rel(gv_[1:], gr_[1:]) < 1e-5
+    # leading batch dimensions, and the empty edge list
+    Y2 = op(vt.detach()[:1000].reshape(10, 100, 3))
+    assert Y2.shape == (10, 100, op.spec.dim) and torch.equal(Y2.reshape(1000, -1), Y.detach()[:1000])
+    v0 = torch.zeros(0, 3, device=dev, requires_grad=True)
+    Y0 = op(v0)
+    assert Y0.shape == (0, op.spec.dim)
+    g0, = torch.autograd.grad(Y0.sum(), v0)
+    assert g0.shape == (0, 3)
+
+
+def test_sh_c_abi_and_golden():
+    """mh_sh_fwd / mh_sh_bwd through the C ABI on the committed golden vectors (tests/golden/coupling.npz), and the
+    entry points' errors for a negative edge count and an unbound module."""
+    import os
+    dev = _dev()
+    print('[case] spherical harmonics C-ABI + golden', flush=True)
+    gold = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden', 'coupling.npz'))
+    lmax = int(round(np.sqrt(gold['sh_values'].shape[1]))) - 1
+    op = HipSphericalHarmonics(o3.SphericalHarmonics(Irreps.spherical_harmonics(lmax)), device=dev)
+    v = torch.tensor(gold['sh_vectors'], dtype=torch.float32, device=dev)
+    Y = torch.empty(v.shape[0], op.spec.dim, device=dev)
+    lib, P, st = _native.load(), _native.ptr, _native.stream_of(v)
+    _native.check(lib.mh_sh_fwd(op.module.handle, P(v), P(Y), v.shape[0], st), 'sh_fwd')
+    gv = torch.empty_like(v)
+    _native.check(lib.mh_sh_bwd(op.module.handle, P(v), P(Y), P(gv), v.shape[0], st), 'sh_bwd')
+    torch.cuda.synchronize()
+    assert np.abs(Y.double().cpu().numpy() - gold['sh_values']).max() < SH_TOL
+    # d/dv of |Y(v/|v|)|^2 / 2 = 0 (|Y_l| is constant on the sphere): the backward with gY = Y gives ~0
+    assert float(gv.abs().max()) < 1e-4 * float(Y.abs().max()) / float(v.norm(dim=1).min())
+    assert lib.mh_sh_fwd(op.module.handle, P(v), P(Y), -1, st) != 0
+    assert b'negative' in lib.mh_last_error()
+    conv = HipConvTP(_tp('32x0e+32x1o', 2), device=dev)            # a module with no spherical-harmonics kernels
+    assert lib.mh_sh_fwd(conv.module.handle, P(v), P(Y), v.shape[0], st) != 0
+    assert b'not bound' in lib.mh_last_error()
 
 
 def test_kernels_match_golden_fixtures():
