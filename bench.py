@@ -56,7 +56,7 @@ def _time_calls(model, batch, steps, warmup, sync):
 def _kernel_table(met, batch, n_real_edges, summary):
     """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only)."""
     import torch
-    from mace_hip_kernels import HipConvTP, HipSphericalHarmonics, HipSymmetricContraction
+    from mace_hip_kernels import HipConvTP, HipNodeLinear, HipRadialMLP, HipSphericalHarmonics, HipSymmetricContraction
     n = batch['positions'].shape[0]
     n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
     rows = {}
@@ -82,6 +82,17 @@ def _kernel_table(met, batch, n_real_edges, summary):
             bf, bb = s.bytes(batch['edge_index'].shape[1])
             rows[f'sh_fwd[{m.tag}]'] = (bf, 0, s.kname('sh_fwd'))
             rows[f'sh_bwd[{m.tag}]'] = (bb, 0, s.kname('sh_bwd'))
+        elif isinstance(m, HipNodeLinear):
+            s = m.spec
+            bf, bb = s.bytes(n)
+            rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n), 'lin_fwd')
+            rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n), 'lin_bwd')
+        elif isinstance(m, HipRadialMLP):
+            s = m.spec                                  # every edge of the padded list is evaluated
+            E = batch['edge_index'].shape[1]
+            bf, bb = s.bytes(E)
+            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(E), 'mlp_fwd')
+            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(E), 'mlp_bwd')
     out = {}
     for tag, (cnt, ms) in summary.items():
         nbytes, flops, sym = rows.get(tag, (0, 0, None))

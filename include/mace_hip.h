@@ -49,7 +49,11 @@ enum mh_kernel_kind {
     MH_CONV_FWD_C = 10,  /* MH_CONV_FWD skipping edges whose cutoff is 0                          */
     MH_SH_FWD = 11,      /* edge spherical harmonics: one edge per thread                         */
     MH_SH_BWD = 12,      /* their gradient with respect to the edge vectors                       */
-    MH_NUM_KINDS = 13
+    MH_LIN_FWD = 13,     /* node-wise equivariant linear (optionally modulated by scalar attrs)    */
+    MH_LIN_BWD = 14,     /* its input gradient (the same map with transposed weights)              */
+    MH_MLP_FWD = 15,     /* radial MLP: per-edge weights from the edge features, 64 edges a block  */
+    MH_MLP_BWD = 16,     /* its input gradient (hidden layers recomputed)                          */
+    MH_NUM_KINDS = 17
 };
 
 /* flags of mh_conv_bwd */
@@ -80,6 +84,9 @@ int mh_module_unload(mh_module* m);
  * each workgroup covering `rows_per_block` rows of the launch (receivers, senders, nodes or edges).  Replaces the
  * threads=/group_size= launch arguments of the reference (conv.py:247, 264, 269; symmetric.py:140, 154). */
 int mh_module_bind(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block);
+/* As mh_module_bind, with a second grid dimension of grid_y workgroups (1..65535); mh_module_bind uses 1. */
+int mh_module_bind_grid(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block,
+                        int grid_y);
 
 /* Fused convolution forward: out[n] = Σ_{p in rowptr[n]..rowptr[n+1]} TP(x[senders[e]], Y[e], W[e]), e = eids[p].
  * rowptr/eids: receiver-sorted CSR.  Replaces lib.conv_fwd (reference conv.py:109-141, launched at conv.py:247). */
@@ -156,6 +163,29 @@ int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const in
  * o3.SphericalHarmonics(normalize=True), which these replace in the model's forward (edge vectors -> edge attrs). */
 int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream);
 int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int64_t E, void* stream);
+
+/* Node-wise equivariant linear out[n] = L(x[n], attrs[n]) for N nodes (x [N, Din], out [N, Dout], fp32, the e3nn
+ * irreps layout [.., u * (2l+1) + m] per block).  Without attrs (attrs NULL) it is e3nn's o3.Linear:
+ *   out[n, o, w, m] = sum_{i: irrep_i = irrep_o} sum_u x[n, i, u, m] W_io[u, w];
+ * with V scalar attrs it is the tensor product x (x) attrs over 0e attrs (MACE's skip_tp, FullyConnectedTensorProduct
+ * with node_attrs): out[n, o, w, m] = sum_i sum_{u, v} x[n, i, u, m] attrs[n, v] W_io[u, v, w], terms whose attrs are
+ * zero over a whole tile of nodes skipped.  W is the module's packed weights with the path normalisation folded in;
+ * the block layout is compiled into the module.  mh_lin_bwd computes gx from g [N, Dout] the same way with the
+ * transposed weights Wt_oi[w, v, u].  No reference counterpart: the reference leaves the model's linears and skip_tp
+ * on e3nn (o3.Linear / o3.FullyConnectedTensorProduct in the interaction and product blocks). */
+int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const float* W, float* out, int32_t N,
+               void* stream);
+int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const float* Wt, float* gx, int32_t N,
+               void* stream);
+
+/* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers
+ * h <- c_i * silu(h A_i) and a linear output layer, MACE's conv_tp_weights (an e3nn FullyConnectedNet).  Wh holds the
+ * hidden layers' weights in the module's LDS layout, Wl [n_hidden_last, n_out] the output layer's; the layer widths
+ * are compiled into the module.  mh_mlp_bwd gives gef = dL/def from gW0 = dL/dW0.  No reference counterpart: the
+ * reference leaves the radial MLP on e3nn (FullyConnectedNet in MACE's interaction blocks). */
+int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, float* W0, int64_t E, void* stream);
+int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, const float* gW0, float* gef,
+               int64_t E, void* stream);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,7 @@ struct Kernel {
     hipFunction_t fn = nullptr;
     int block = 0;
     int rows_per_block = 1;
+    int grid_y = 1;          // second grid dimension (a fixed count: output blocks of a node linear)
 };
 
 }  // namespace
@@ -73,8 +74,9 @@ int launch(mh_module* m, int kind, int64_t rows, void** args, void* stream, cons
     }
     int64_t grid = (rows + k.rows_per_block - 1) / k.rows_per_block;
     if (grid > 0x7fffffffLL) return fail(-1, std::string(what) + ": launch too large");
-    hipError_t e = hipModuleLaunchKernel(k.fn, static_cast<unsigned>(grid), 1, 1, static_cast<unsigned>(k.block), 1, 1,
-                                         0, static_cast<hipStream_t>(stream), args, nullptr);
+    hipError_t e = hipModuleLaunchKernel(k.fn, static_cast<unsigned>(grid), static_cast<unsigned>(k.grid_y), 1,
+                                         static_cast<unsigned>(k.block), 1, 1, 0, static_cast<hipStream_t>(stream), args,
+                                         nullptr);
     if (e != hipSuccess) return hip_fail(e, what);
     return 0;
 }
@@ -85,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 6; }
+int mh_version(void) { return 8; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -164,17 +166,24 @@ int mh_module_unload(mh_module* m) {
     return 0;
 }
 
-int mh_module_bind(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block) {
+int mh_module_bind_grid(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block,
+                        int grid_y) {
     if (!m || !name) return fail(-1, "mh_module_bind: null argument");
     if (kind < 0 || kind >= MH_NUM_KINDS) return fail(-1, "mh_module_bind: bad kernel kind");
-    if (block_threads <= 0 || block_threads > 1024 || block_threads % 64 || rows_per_block <= 0)
+    if (block_threads <= 0 || block_threads > 1024 || block_threads % 64 || rows_per_block <= 0 || grid_y <= 0 ||
+        grid_y > 65535)
         return fail(-1, "mh_module_bind: bad launch shape");
     hipFunction_t fn = nullptr;
     MH_HIP(hipModuleGetFunction(&fn, m->mod, name));
     m->k[kind].fn = fn;
     m->k[kind].block = block_threads;
     m->k[kind].rows_per_block = rows_per_block;
+    m->k[kind].grid_y = grid_y;
     return 0;
+}
+
+int mh_module_bind(mh_module* m, int kind, const char* name, int block_threads, int rows_per_block) {
+    return mh_module_bind_grid(m, kind, name, block_threads, rows_per_block, 1);
 }
 
 int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
@@ -270,6 +279,33 @@ int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream)
 int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int64_t E, void* stream) {
     void* args[] = {&vec, &gY, &gvec, &E};
     return launch(m, MH_SH_BWD, E, args, stream, "mh_sh_bwd");
+}
+
+int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const float* W, float* out, int32_t N,
+               void* stream) {
+    if (N > 0 && (!x || !W || !out)) return fail(-1, "mh_lin_fwd: NULL x, W or out");
+    void* args[] = {&x, &attrs, &W, &out, &N};
+    return launch(m, MH_LIN_FWD, N, args, stream, "mh_lin_fwd");
+}
+
+int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const float* Wt, float* gx, int32_t N,
+               void* stream) {
+    if (N > 0 && (!g || !Wt || !gx)) return fail(-1, "mh_lin_bwd: NULL g, Wt or gx");
+    void* args[] = {&g, &attrs, &Wt, &gx, &N};
+    return launch(m, MH_LIN_BWD, N, args, stream, "mh_lin_bwd");
+}
+
+int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, float* W0, int64_t E, void* stream) {
+    if (E > 0 && (!ef || !Wh || !Wl || !W0)) return fail(-1, "mh_mlp_fwd: NULL operand");
+    void* args[] = {&ef, &Wh, &Wl, &W0, &E};
+    return launch(m, MH_MLP_FWD, E, args, stream, "mh_mlp_fwd");
+}
+
+int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, const float* gW0, float* gef,
+               int64_t E, void* stream) {
+    if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef)) return fail(-1, "mh_mlp_bwd: NULL operand");
+    void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E};
+    return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
 }
 
 }  // extern "C"

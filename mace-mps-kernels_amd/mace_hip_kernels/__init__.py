@@ -7,7 +7,10 @@ mace_hip_kernels — MI355X (gfx950) HIP kernels for MACE inference, patched int
 Replaces, where supported (reference __init__.py:1-14):
   * each interaction block's convolution (gather → channel-wise tensor product → scatter-sum) via MACE's own
     ``conv_fusion`` hook,
-  * each product block's symmetric contraction.
+  * each product block's symmetric contraction,
+  * beyond the reference: the edge spherical harmonics, and the node-wise equivariant linears (e3nn ``o3.Linear``)
+    and scalar-attribute tensor products (``skip_tp``) with at least 16 output channels per irrep, and each
+    interaction block's radial MLP (``conv_tp_weights``).
 Everything else stays on the original e3nn / PyTorch path.  Inference only: the backward pass is first order
 (energies, forces, stress, finite-difference Hessians, MD, relaxations); double backward raises.
 
@@ -22,12 +25,17 @@ import torch
 
 from .conv import HipConvTP, conv_supported
 from .edge import HipSphericalHarmonics, sh_supported
+from .linear import HipNodeLinear, lin_supported
+from .radial import HipRadialMLP, mlp_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
 
 __version__ = '0.1.0'
 __all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
-           'conv_supported', 'sc_supported', 'sh_supported']
+           'HipNodeLinear', 'HipRadialMLP', 'conv_supported', 'sc_supported', 'sh_supported', 'lin_supported',
+           'mlp_supported']
+
+_LINEAR_CLASSES = ('Linear', 'FullyConnectedTensorProduct')
 
 
 def _block_has_conv_fusion(blk):
@@ -38,10 +46,24 @@ def _block_has_conv_fusion(blk):
         return False
 
 
-def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True):
+def _linear_candidates(model):
+    """(name, parent, attribute, module) of every e3nn Linear / FullyConnectedTensorProduct in the model."""
+    out = []
+    for pname, parent in model.named_modules():
+        for attr, mod in parent.named_children():
+            if type(mod).__name__ in _LINEAR_CLASSES and not isinstance(mod, HipNodeLinear):
+                out.append((f'{pname}.{attr}' if pname else attr, parent, attr, mod))
+    return out
+
+
+def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
+                radial_mlp=True):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
-    edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module."""
+    edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
+    node-wise e3nn linears and scalar-attribute tensor products (``skip_tp``); readout heads with fewer than 16 output
+    channels per irrep are left on e3nn without being reported (they are a negligible part of the call), and
+    ``radial_mlp`` each interaction block's radial MLP (``conv_tp_weights``, an e3nn FullyConnectedNet)."""
     p = next(model.parameters())
     dev = p.device
     if dev.type != 'cuda' or torch.version.hip is None:
@@ -95,6 +117,40 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 patched.append('spherical_harmonics')
             else:
                 skipped.append(('spherical_harmonics', why))
+    if radial_mlp:
+        for i, blk in enumerate(getattr(model, 'interactions', [])):
+            name = f'interactions.{i}.conv_tp_weights'
+            mlp = getattr(blk, 'conv_tp_weights', None)
+            if mlp is None or isinstance(mlp, HipRadialMLP):
+                continue
+            ok, why = mlp_supported(mlp)
+            if ok:
+                try:
+                    new = HipRadialMLP(mlp, device=dev)
+                except ValueError as e:
+                    ok, why = False, str(e)
+            if not ok:
+                skipped.append((name, why))
+                continue
+            new.tag = name
+            blk.conv_tp_weights = new
+            patched.append(name)
+    if linears:
+        for name, parent, attr, mod in _linear_candidates(model):
+            if any(mul < 16 for mul, _ in mod.irreps_out):
+                continue
+            ok, why = lin_supported(mod)
+            if ok:
+                try:
+                    new = HipNodeLinear(mod, device=dev)
+                except ValueError as e:            # the probed map is not the expected block structure
+                    ok, why = False, str(e)
+            if not ok:
+                skipped.append((name, why))
+                continue
+            new.tag = name
+            setattr(parent, attr, new)
+            patched.append(name)
     if verbose:
         for name, why in skipped:
             warnings.warn(f'mace_hip_kernels: kept e3nn for {name}: {why}')
@@ -117,4 +173,13 @@ def unpatch_model(model):
     if isinstance(getattr(model, 'spherical_harmonics', None), HipSphericalHarmonics):
         model.spherical_harmonics = model.spherical_harmonics.original[0]
         restored.append('spherical_harmonics')
+    for i, blk in enumerate(getattr(model, 'interactions', [])):
+        if isinstance(getattr(blk, 'conv_tp_weights', None), HipRadialMLP):
+            blk.conv_tp_weights = blk.conv_tp_weights.original[0]
+            restored.append(f'interactions.{i}.conv_tp_weights')
+    for pname, parent in list(model.named_modules()):
+        for attr, mod in list(parent.named_children()):
+            if isinstance(mod, HipNodeLinear):
+                setattr(parent, attr, mod.original[0])
+                restored.append(f'{pname}.{attr}' if pname else attr)
     return restored

@@ -17,9 +17,10 @@ LIB_PATH = os.path.join(HERE, 'libmace_hip.so')
 DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
 
 MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, MH_CONV_GXSUM, MH_SC_FWD_G, \
-    MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD = range(13)
+    MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD, MH_LIN_FWD, MH_LIN_BWD, \
+    MH_MLP_FWD, MH_MLP_BWD = range(17)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 6
+ABI_VERSION = 8
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -48,6 +49,11 @@ _SIGS = {
     'mh_conv_fwd_cut': (ctypes.c_int, [_P] * 9 + [_I, _P]),
     'mh_sh_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int64, _P]),
     'mh_sh_bwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
+    'mh_lin_fwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int, _P]),
+    'mh_lin_bwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int, _P]),
+    'mh_mlp_fwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
+    'mh_mlp_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
+    'mh_module_bind_grid': (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     'mh_sc_fwd_sorted': (ctypes.c_int, [_P] * 6 + [_I, _P]),
     'mh_sc_bwd_sorted': (ctypes.c_int, [_P] * 7 + [_I, _P]),
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
@@ -121,8 +127,9 @@ class Module:
         buf = ctypes.create_string_buffer(code, len(code))
         check(lib.mh_module_load(buf, len(code), ctypes.byref(self.handle)), 'module load')
         self.device = torch.cuda.current_device()
-        for kind, (name, block, rows) in kernels.items():
-            check(lib.mh_module_bind(self.handle, kind, name.encode(), block, rows), f'bind {name}')
+        for kind, (name, block, rows, *grid_y) in kernels.items():
+            check(lib.mh_module_bind_grid(self.handle, kind, name.encode(), block, rows, grid_y[0] if grid_y else 1),
+                  f'bind {name}')
 
     def __del__(self):
         h = getattr(self, 'handle', None)

@@ -5,13 +5,15 @@ Every case prints its name before launching.  Tolerance: fp32 kernels vs fp64 or
 (normalised by the largest reference magnitude) < 2e-6 for the convolution and < 1e-5 for the symmetric contraction
 (hundreds of fp32 terms per output); determinism is bitwise.
 """
+import copy
 import ctypes
 
 import numpy as np
 import pytest
 import torch
 
-from mace_hip_kernels import HipConvTP, HipSphericalHarmonics, HipSymmetricContraction, _native
+from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialMLP, HipSphericalHarmonics, HipSymmetricContraction,
+                              _native)
 from mace_hip_kernels import conv as hconv
 from mace_lite import blocks as B
 from mace_lite import factory
@@ -366,6 +368,154 @@ def test_sh_c_abi_and_golden():
     conv = HipConvTP(_tp('32x0e+32x1o', 2), device=dev)            # a module with no spherical-harmonics kernels
     assert lib.mh_sh_fwd(conv.module.handle, P(v), P(Y), v.shape[0], st) != 0
     assert b'not bound' in lib.mh_last_error()
+
+
+LIN_TOL = 1e-5       # relative to the largest |component| of the float64 result
+
+
+def _lin_modules():
+    """(name, module) of every patchable node linear of the config-2 and config-4 models and of a 48-channel one."""
+    from mace_hip_kernels import lin_supported
+    out = []
+    for tag, m in (('c2', factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)),
+                   ('c4', factory.make_model('128x0e+128x1o+128x2e', 3, 3, elements=factory.ELEMENTS_PTCOH)),
+                   ('c48', factory.make_model('48x0e+48x1o', 2, 2))):
+        for name, mod in m.named_modules():
+            if type(mod).__name__ in ('Linear', 'FullyConnectedTensorProduct') and lin_supported(mod)[0]:
+                out.append((f'{tag}.{name}', mod))
+    return out
+
+
+@pytest.mark.parametrize('attrs_kind', ['one_hot', 'dense'])
+def test_node_linears_vs_float64(attrs_kind):
+    """Every node linear (o3.Linear and skip_tp) of three models: forward and input gradient against float64 runs of
+    the e3nn module (autograd for the gradient), on a ragged node count; skip_tp with one-hot element attributes
+    (zero terms skipped per tile) and with dense random attributes (every term live)."""
+    dev = _dev()
+    rng = np.random.default_rng(5)
+    n = 1237
+    for name, mod in _lin_modules():
+        print(f'[case] node linear {name} attrs={attrs_kind}', flush=True)
+        op = HipNodeLinear(mod, device=dev)
+        s = op.spec
+        x = rng.normal(size=(n, s.Din))
+        a = None
+        if s.V:
+            a = (np.eye(s.V)[rng.integers(0, s.V, size=n)] if attrs_kind == 'one_hot' else rng.normal(size=(n, s.V)))
+        g = rng.normal(size=(n, s.Dout))
+        xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=s.has_bwd)
+        at = None if a is None else torch.tensor(a, dtype=torch.float32, device=dev)
+        out = op(xt, at)
+        m64 = copy.deepcopy(mod).double()
+        x64 = torch.tensor(x, requires_grad=True)
+        ref = m64(x64, torch.tensor(a)) if s.V else m64(x64)
+        assert _rel(out.detach().double().cpu().numpy(), ref.detach().numpy()) < LIN_TOL
+        if s.has_bwd:
+            gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
+            gr, = torch.autograd.grad(ref, x64, torch.tensor(g))
+            assert _rel(gx.double().cpu().numpy(), gr.numpy()) < LIN_TOL
+        if attrs_kind == 'dense':
+            continue
+        # no nodes at all, and a leading batch shape
+        x0 = torch.zeros(0, s.Din, device=dev, requires_grad=s.has_bwd)
+        o0 = op(x0, None if at is None else at[:0])
+        assert o0.shape == (0, s.Dout)
+        o2 = op(xt.detach()[:60].reshape(3, 20, s.Din), None if at is None else at[:60].reshape(3, 20, s.V))
+        assert torch.equal(o2.reshape(60, -1), out.detach()[:60])
+
+
+def test_node_linear_c_abi_and_errors():
+    """mh_lin_fwd / mh_lin_bwd through the C ABI against the module, and their errors (NULL operands, a module
+    without the kernel)."""
+    dev = _dev()
+    print('[case] node linear C-ABI', flush=True)
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    op = HipNodeLinear(m.interactions[0].skip_tp, device=dev)
+    s = op.spec
+    n = 300
+    x = torch.randn(n, s.Din, device=dev)
+    a = torch.eye(s.V, device=dev)[torch.randint(0, s.V, (n,), device=dev)]
+    out, gx = torch.empty(n, s.Dout, device=dev), torch.empty(n, s.Din, device=dev)
+    lib, P, st = _native.load(), _native.ptr, _native.stream_of(x)
+    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out), n, st), 'lin_fwd')
+    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx), n, st), 'lin_bwd')
+    torch.cuda.synchronize()
+    ref = op(x, a)
+    assert torch.equal(out, ref)
+    # <out, out> = <gx, x> for gx = L^T out
+    assert abs(_dot(gx, x) - _dot(out, out)) <= 1e-5 * abs(_dot(out, out))
+    assert lib.mh_lin_fwd(op.module.handle, None, P(a), P(op.W), P(out), n, st) != 0
+    assert b'NULL' in lib.mh_last_error()
+    conv = HipConvTP(_tp('32x0e+32x1o', 2), device=dev)
+    assert lib.mh_lin_fwd(conv.module.handle, P(x), P(a), P(op.W), P(out), n, st) != 0
+    assert b'not bound' in lib.mh_last_error()
+
+
+def _dot(a, b):
+    return float((a.double() * b.double()).sum())
+
+
+MLP_TOL = 1e-5       # relative to the largest |component| of the float64 result
+
+
+@pytest.mark.parametrize('hidden,lmax,elements', [('128x0e+128x1o', 3, 'ptcoh'), ('128x0e+128x1o+128x2e', 3, 'ptcoh'),
+                                                  ('32x0e+32x1o', 2, 'ref')])
+def test_radial_mlp_vs_float64(hidden, lmax, elements):
+    """Each interaction block's radial MLP: forward and d/d(edge features) against float64 runs of the e3nn module,
+    on a ragged edge count (not a multiple of the 64-edge block), with edge features of the model's radial
+    embedding (Bessel basis times the cutoff envelope, so rows of zeros past the cutoff) and random ones."""
+    dev = _dev()
+    el = factory.ELEMENTS_PTCOH if elements == 'ptcoh' else factory.ELEMENTS_REF
+    model = factory.make_model(hidden, lmax, 2, elements=el)
+    rng = np.random.default_rng(9)
+    e = 3001
+    r = torch.tensor(rng.uniform(0.5, 6.0, size=(e, 1)))
+    emb, _ = model.radial_embedding.double()(r)
+    for kind, ef in (('embedding', emb.numpy()), ('random', rng.normal(size=(e, emb.shape[1])))):
+        for li, blk in enumerate(model.interactions):
+            print(f'[case] radial MLP {hidden} layer {li} ({kind} features)', flush=True)
+            op = HipRadialMLP(blk.conv_tp_weights, device=dev)
+            xt = torch.tensor(ef, dtype=torch.float32, device=dev, requires_grad=True)
+            out = op(xt)
+            g = rng.normal(size=tuple(out.shape))
+            gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
+            m64 = copy.deepcopy(blk.conv_tp_weights).double()
+            x64 = torch.tensor(ef, requires_grad=True)
+            ref = m64(x64)
+            gr, = torch.autograd.grad(ref, x64, torch.tensor(g))
+            assert _rel(out.detach().double().cpu().numpy(), ref.detach().numpy()) < MLP_TOL
+            assert _rel(gx.double().cpu().numpy(), gr.numpy()) < MLP_TOL
+    # no edges, and a leading batch shape
+    op = HipRadialMLP(model.interactions[0].conv_tp_weights, device=dev)
+    x0 = torch.zeros(0, emb.shape[1], device=dev, requires_grad=True)
+    o0 = op(x0)
+    assert o0.shape == (0, op.hs[-1])
+    assert torch.autograd.grad(o0.sum(), x0)[0].shape == (0, emb.shape[1])
+    xb = torch.tensor(ef[:64], dtype=torch.float32, device=dev)
+    assert torch.equal(op(xb.reshape(4, 16, -1)).reshape(64, -1), op(xb))
+
+
+def test_radial_mlp_c_abi():
+    dev = _dev()
+    print('[case] radial MLP C-ABI', flush=True)
+    model = factory.make_model('128x0e+128x1o', 3, 2, elements=factory.ELEMENTS_PTCOH)
+    op = HipRadialMLP(model.interactions[1].conv_tp_weights, device=dev)
+    e = 200
+    x = torch.randn(e, op.hs[0], device=dev)
+    out = torch.empty(e, op.hs[-1], device=dev)
+    lib, P, st = _native.load(), _native.ptr, _native.stream_of(x)
+    _native.check(lib.mh_mlp_fwd(op.module.handle, P(x), P(op.Wh), P(op.Wl), P(out), e, st), 'mlp_fwd')
+    gx = torch.empty_like(x)
+    _native.check(lib.mh_mlp_bwd(op.module.handle, P(x), P(op.Wh), P(op.Wl), P(out), P(gx), e, st), 'mlp_bwd')
+    torch.cuda.synchronize()
+    assert torch.equal(out, op(x))
+    # the backward is the adjoint of the Jacobian: <gx, dx> = <out, J dx> for a small step dx (finite difference)
+    dx = 1e-3 * torch.randn_like(x)
+    jdx = (op(x + dx) - op(x - dx)) / 2
+    lhs, rhs = _dot(gx, dx), _dot(out, jdx)
+    assert abs(lhs - rhs) <= 1e-3 * abs(rhs)
+    assert lib.mh_mlp_fwd(op.module.handle, None, P(op.Wh), P(op.Wl), P(out), e, st) != 0
+    assert b'NULL' in lib.mh_last_error()
 
 
 def test_kernels_match_golden_fixtures():

@@ -24,6 +24,14 @@ E_ABS = 1e-3        # eV per structure
 F_ABS = 1e-5        # eV/A
 
 
+CORE = ('conv_tp', 'symmetric_contractions', 'spherical_harmonics')
+
+
+def _core(report):
+    """Patched convolutions, contractions and spherical harmonics (the rest of ``patched`` are node linears)."""
+    return [n for n in report['patched'] if n.endswith(CORE)]
+
+
 def _dev():
     assert torch.cuda.is_available(), 'GPU test needs a GPU'
     return torch.device('cuda:0')
@@ -71,7 +79,9 @@ def test_matches_e3nn_all_configs(config):
     seed = 0 if not config.endswith('_b') else 7
     ref, met, report = _pair(factory.make_model(hidden, lmax, corr, seed=seed), dev)
     assert not report['skipped'], report['skipped']
-    assert len(report['patched']) == 5 and 'spherical_harmonics' in report['patched'], report
+    assert len(_core(report)) == 5 and 'spherical_harmonics' in report['patched'], report
+    assert 'interactions.1.linear' in report['patched'] and 'interactions.0.skip_tp' in report['patched'], report
+    assert 'interactions.1.conv_tp_weights' in report['patched'], report
     for s in (0, 1, 2):
         print(f'[case] {config} seed {s}', flush=True)
         st = factory.make_structure(seed=s)
@@ -111,7 +121,7 @@ def test_unsupported_block_is_skipped():
     print('[case] 48-channel model: convolutions skipped', flush=True)
     ref, met, report = _pair(factory.make_model('48x0e+48x1o', 3, 3), dev)
     assert all('conv_tp' in n for n, _ in report['skipped']) and len(report['skipped']) == 2, report
-    assert len(report['patched']) == 3                 # both contractions and the spherical harmonics
+    assert len(_core(report)) == 3                     # both contractions and the spherical harmonics
     st = factory.make_structure(seed=5)
     _check(ref, met, D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF), dev, [len(st)])
 
@@ -122,7 +132,7 @@ def test_baseline_configs(cfg):
     print(f'[case] BASELINE config {cfg}', flush=True)
     model, batch, meta = factory.workload(cfg)
     ref, met, report = _pair(model, dev)
-    assert not report['skipped'] and len(report['patched']) == 5, report
+    assert not report['skipped'] and len(_core(report)) == 5, report
     n_atoms = np.diff(batch['ptr'].numpy())
     dE, dF = _check(ref, met, batch, dev, n_atoms, stress=(cfg == 1))
     print(f'       {meta["name"]}: |dE| {dE * 1e3:.4f} meV  max|dF| {dF:.2e}', flush=True)
@@ -135,10 +145,11 @@ def test_idempotent_patch_and_unpatch():
     m = factory.make_model(*factory.REF_CONFIGS['l2_corr2_scalar']).to(dev)
     r1 = patch_model(m, verbose=False)
     r2 = patch_model(m, verbose=False)
-    assert len(r1['patched']) == 5 and r2 == dict(patched=[], skipped=[])
-    assert len(unpatch_model(m)) == 5
+    assert len(_core(r1)) == 5 and r2 == dict(patched=[], skipped=[])
+    assert sorted(unpatch_model(m)) == sorted(r1['patched'])
     assert type(m.spherical_harmonics).__name__ == 'SphericalHarmonics'
-    r3 = patch_model(m, verbose=False, spherical_harmonics=False)
+    assert type(m.interactions[1].linear).__name__ == 'Linear'
+    r3 = patch_model(m, verbose=False, spherical_harmonics=False, linears=False, radial_mlp=False)
     assert len(r3['patched']) == 4 and 'spherical_harmonics' not in r3['patched']
     assert len(unpatch_model(m)) == 4
     assert not hasattr(m.interactions[0], 'conv_fusion')
