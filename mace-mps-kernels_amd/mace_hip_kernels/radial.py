@@ -117,154 +117,173 @@ def _lit(v):
     return f'{float(np.float32(v)).hex()}f'
 
 
+def _layout(spec):
+    """Packing constants shared by the generator and the weight packer."""
+    hs = spec.hs
+    H0, NW, HL = hs[0], hs[-1], hs[-2]
+    K0S = -(-H0 // 4)                                    # MFMA steps of the first layer (K = H0 padded to 4 K0S)
+    rows = [4 * K0S] + hs[1:-2]                          # K extent of each hidden layer
+    cols = hs[1:-1]                                      # outputs of each hidden layer
+    CHUNK = next(c for c in CHUNKS if NW % c == 0)
+    nat, tr, o1, o2 = [], [], 0, 0
+    for r, c in zip(rows, cols):
+        nat.append(o1)
+        o1 += r * (c + PAD)                              # natural [k][j + PAD]   (backward)
+        tr.append(o2)
+        o2 += c * (r + PAD)                              # transposed [j][k + PAD] (forward)
+    return dict(H0=H0, NW=NW, HL=HL, K0S=K0S, rows=rows, cols=cols, CHUNK=CHUNK, nat=nat, tr=tr, nat_size=o1,
+                tr_size=o2, chunk_fwd=CHUNK * (HL + PAD), chunk_bwd=HL * (CHUNK + PAD))
+
+
 def source(spec):
     """HIP source of ``mlp_fwd`` and ``mlp_bwd``."""
-    hs = spec.hs
-    H0, NW = hs[0], hs[-1]
-    hidden = hs[1:-1]
-    nh = len(hidden)
-    K0S = -(-H0 // 4)                                   # MFMA steps of the first layer
-    HL = hs[-2]                                         # width feeding the output layer
+    Lo = _layout(spec)
+    H0, NW, HL, K0S, CHUNK = Lo['H0'], Lo['NW'], Lo['HL'], Lo['K0S'], Lo['CHUNK']
+    rows, cols = Lo['rows'], Lo['cols']
+    nh = len(cols)
     TL = HL // 16
-    CHUNK = next(c for c in CHUNKS if NW % c == 0)
-    # LDS: hidden weights [h_in][h_out + PAD] (first layer [4 K0S][...]), then one output-layer chunk [HL][CHUNK + PAD]
-    offs, off = [], 0
-    for i in range(nh):
-        rows = 4 * K0S if i == 0 else hs[i]
-        offs.append(off)
-        off += rows * (hs[i + 1] + PAD)
-    woff_chunk = off
-    lds_floats = off + HL * (CHUNK + PAD)
     NCHK = NW // CHUNK
-    NV4 = HL * CHUNK // 4                                # float4s per chunk
-    NLD = -(-NV4 // BLOCK)                               # per thread (the last one clamped when NV4 % 256 != 0)
-    L = [_native.device_header(), 'typedef float mh_f4 __attribute__((ext_vector_type(4)));', '']
-    L += ['__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '']
+    NO = CHUNK // 16
+    lds_fwd = max(Lo['tr_size'], 2 * Lo['chunk_fwd'])
+    lds_bwd = max(Lo['nat_size'], 2 * Lo['chunk_bwd'])
+    L = [_native.device_header(), 'typedef float mh_f4 __attribute__((ext_vector_type(4)));', '',
+         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '']
 
-    # ---- shared prologue: hidden weights into LDS, this wave's 16 edges' features into registers
-    def prologue(name, with_grad):
-        P = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ ef,',
-             '    const float* __restrict__ Wh, const float* __restrict__ Wl, ' +
-             ('const float* __restrict__ gW, float* __restrict__ gef, long long E) {' if with_grad else
-              'float* __restrict__ W0, long long E) {'),
-             f'  __shared__ __align__(16) float lds[{lds_floats}];',
-             '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
-             f'  const long long e0 = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * {EDGES} + wave * 16;',
-             '  const long long ej = e0 + c16;                 // this lane\'s edge (as a B column / output row)',
-             '  const bool live = ej < E;',
-             '  const long long ejc = live ? ej : E - 1;       // clamped: every load in bounds',
-             f'  for (int f = t; f < {woff_chunk}; f += {BLOCK}) lds[f] = Wh[f];',
-             '  __syncthreads();',
-             f'  float xin[{K0S}];']
+    def head(name, args, lds):
+        return [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}({args}) {{',
+                f'  __shared__ __align__(16) float lds[{lds}];',
+                '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
+                f'  const long long e0 = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * {EDGES} + wave * 16;',
+                '  const long long ej = e0 + c16;                 // this lane\'s edge (as a B column / output row)',
+                '  const bool live = ej < E;',
+                '  const long long ejc = live ? ej : E - 1;       // clamped: every load in bounds']
+
+    def stage(src, n):
+        return [f'  for (int f = t; f < {n // 4}; f += {BLOCK})',
+                f'    reinterpret_cast<mh_f4*>(lds)[f] = reinterpret_cast<const mh_f4*>({src})[f];']
+
+    def xin():
+        P = [f'  float xin[{K0S}];']
         P += [f'  xin[{st}] = {4 * st} + q < {H0} ? ef[ejc * {H0} + {4 * st} + q] : 0.f;' for st in range(K0S)]
         return P
 
-    # output-layer weight chunks: float4 register prefetch (pre0..) and LDS store, unrolled (named registers)
-    def chunk_load(nx, ind):
+    def hidden_fwd(transposed, keep):
+        """z_i and h_i = c_i silu(z_i) for every hidden layer, A operands from LDS (transposed layout: one b128 read
+        per 4 MFMAs; natural layout: b32 reads)."""
         P = []
-        for it in range(NLD):
-            fx = f't + {it * BLOCK}' if (it + 1) * BLOCK <= NV4 else f'min(t + {it * BLOCK}, {NV4 - 1})'
-            P += [f'{ind}{{ const int f = {fx}, k = f / {CHUNK // 4}, c4 = f - k * {CHUNK // 4};',
-                  f'{ind}  pre{it} = *reinterpret_cast<const mh_f4*>(Wl + (size_t)k * {NW} + {nx} + 4 * c4); }}']
+        for i in range(nh):
+            T = cols[i] // 16
+            z = f'z{i}'
+            P.append(f'  mh_f4 {z}[{T}];')
+            for o in range(T):
+                P.append(f'  {z}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};')
+            if i == 0:
+                for st in range(K0S):
+                    for o in range(T):
+                        a = (f'lds[{Lo["tr"][0]} + ({16 * o} + c16) * {rows[0] + PAD} + {4 * st} + q]' if transposed else
+                             f'lds[{Lo["nat"][0]} + ({4 * st} + q) * {cols[0] + PAD} + {16 * o} + c16]')
+                        P.append(f'  {z}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32({a}, xin[{st}], {z}[{o}], 0, 0, 0);')
+            else:
+                Tin = cols[i - 1] // 16
+                for ti in range(Tin):
+                    if transposed:
+                        for o in range(T):
+                            P.append(f'  const mh_f4 a{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["tr"][i]} + '
+                                     f'({16 * o} + c16) * {rows[i] + PAD} + {16 * ti} + 4 * q]);')
+                    for r in range(4):
+                        for o in range(T):
+                            a = (f'a{i}_{ti}_{o}[{r}]' if transposed else
+                                 f'lds[{Lo["nat"][i]} + ({16 * ti + r} + 4 * q) * {cols[i] + PAD} + {16 * o} + c16]')
+                            P.append(f'  {z}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32({a}, h{i - 1}[{ti}][{r}], '
+                                     f'{z}[{o}], 0, 0, 0);')
+            if i < nh - 1 or keep:
+                P.append(f'  mh_f4 h{i}[{T}];')
+                for o in range(T):
+                    for r in range(4):
+                        P.append(f'  h{i}[{o}][{r}] = {_lit(spec.c[i])} * {z}[{o}][{r}] * mlp_sig({z}[{o}][{r}]);')
         return P
 
-    def chunk_store(ind):
+    def pre_load(src, nx, stride, width, ind):
+        """This thread's share of an output-layer chunk, as float4 registers pre0..: chunk element f4 index f covers
+        row f / (width / 4) and 4 columns (global row stride ``stride``)."""
+        n4 = (CHUNK * HL) // 4
         P = []
-        for it in range(NLD):
-            guard = '' if (it + 1) * BLOCK <= NV4 else f'if (t + {it * BLOCK} < {NV4}) '
-            P += [f'{ind}{guard}{{ const int f = t + {it * BLOCK}, k = f / {CHUNK // 4}, c4 = f - k * {CHUNK // 4};',
-                  f'{ind}  *reinterpret_cast<mh_f4*>(&lds[{woff_chunk} + k * {CHUNK + PAD} + 4 * c4]) = pre{it}; }}']
+        for it in range(-(-n4 // BLOCK)):
+            fx = f't + {it * BLOCK}' if (it + 1) * BLOCK <= n4 else f'min(t + {it * BLOCK}, {n4 - 1})'
+            P += [f'{ind}{{ const int f = {fx}, rr = f / {width // 4}, c4 = f - rr * {width // 4};',
+                  f'{ind}  pre{it} = *reinterpret_cast<const mh_f4*>({src} + (size_t)rr * {stride} + {nx} + 4 * c4); }}']
         return P
 
-    def mm_first(dst, T):
-        # layer 0: K = H0 in natural order (k = 4 s + q), A = W^T from LDS
-        P = [f'  mh_f4 {dst}[{T}];']
-        for o in range(T):
-            P.append(f'  {dst}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};')
-            for st in range(K0S):
-                P.append(f'  {dst}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(lds[{offs[0]} + ({4 * st} + q) * '
-                         f'{hs[1] + PAD} + {16 * o} + c16], xin[{st}], {dst}[{o}], 0, 0, 0);')
+    def pre_store(base, width, ind):
+        n4 = (CHUNK * HL) // 4
+        P = []
+        for it in range(-(-n4 // BLOCK)):
+            guard = '' if (it + 1) * BLOCK <= n4 else f'if (t + {it * BLOCK} < {n4}) '
+            P += [f'{ind}{guard}{{ const int f = t + {it * BLOCK}, rr = f / {width // 4}, c4 = f - rr * {width // 4};',
+                  f'{ind}  *reinterpret_cast<mh_f4*>(&lds[{base} + rr * {width + PAD} + 4 * c4]) = pre{it}; }}']
         return P
 
-    def mm_hidden(dst, src, T_in, T_out, base, ncol):
-        # K walks the previous tile layout: step (t, r) <-> k = 16 t + 4 q + r (unrolled here: constant indices)
-        P = [f'  mh_f4 {dst}[{T_out}];']
-        for o in range(T_out):
-            P.append(f'  {dst}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};')
-            for ti in range(T_in):
-                for r in range(4):
-                    P.append(f'  {dst}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(lds[{base} + ({16 * ti + r} + 4 * q) * '
-                             f'{ncol + PAD} + {16 * o} + c16], {src}[{ti}][{r}], {dst}[{o}], 0, 0, 0);')
-        return P
+    npre = -(-(CHUNK * HL // 4) // BLOCK)
+    pres = ', '.join(f'pre{i}' for i in range(npre))
 
-    def act(dst, src, T, c):
-        P = [f'  mh_f4 {dst}[{T}];']
-        for o in range(T):
-            for r in range(4):
-                P.append(f'  {dst}[{o}][{r}] = {_lit(c)} * {src}[{o}][{r}] * mlp_sig({src}[{o}][{r}]);')
-        return P
-
-    # ---------------------------------------------------------------- forward
-    F = prologue('mlp_fwd', False)
-    F += mm_first('z0', hidden[0] // 16) + act('h0', 'z0', hidden[0] // 16, spec.c[0])
-    for i in range(1, nh):
-        F += mm_hidden(f'z{i}', f'h{i - 1}', hidden[i - 1] // 16, hidden[i] // 16, offs[i], hidden[i])
-        F += act(f'h{i}', f'z{i}', hidden[i] // 16, spec.c[i])
+    # ------------------------------------------------------------------ forward
+    # hidden weights transposed [j][k + PAD]; output layer from WlT [NW][HL], chunks [CHUNK cols][HL + PAD]
+    F = head('mlp_fwd', 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
+             'float* __restrict__ W0, long long E', lds_fwd)
+    F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(True, True)
     hl = f'h{nh - 1}'
-    F += [f'  mh_f4 {", ".join(f"pre{it}" for it in range(NLD))};']
-    F += chunk_load('0', '  ')
-    F += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{', '    __syncthreads();']
-    F += chunk_store('    ')
-    F += ['    __syncthreads();',
-          f'    const int nx = min(ch + 1, {NCHK - 1}) * {CHUNK};      // next chunk (the last one reloads itself)']
-    F += chunk_load('nx', '    ')
-    for o in range(CHUNK // 16):
-        F.append(f'    mh_f4 acc{o} = mh_f4{{0.f, 0.f, 0.f, 0.f}};')
+    F += [f'  mh_f4 {pres};'] + pre_load('Wl', '0', HL, HL, '  ')
+    F += ['  __syncthreads();                                // every wave is done with the hidden weights']
+    F += pre_store('0', HL, '  ') + ['  __syncthreads();']
+    F += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
+          f'    const int base = (ch & 1) * {Lo["chunk_fwd"]}, nbase = {Lo["chunk_fwd"]} - base;',
+          f'    const int nx = min(ch + 1, {NCHK - 1}) * {CHUNK * HL};      // next chunk (the last one reloads itself)']
+    F += pre_load('Wl', 'nx', HL, HL, '    ')
+    F += [f'    mh_f4 acc[{NO}];']
+    F += [f'    acc[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO)]
     for ti in range(TL):
+        for o in range(NO):
+            F.append(f'    const mh_f4 a{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[base + ({16 * o} + c16) * '
+                     f'{HL + PAD} + {16 * ti} + 4 * q]);')
         for r in range(4):
-            for o in range(CHUNK // 16):
-                F.append(f'    acc{o} = __builtin_amdgcn_mfma_f32_16x16x4f32(lds[{woff_chunk} + ({16 * ti + r} + 4 * q) * '
-                         f'{CHUNK + PAD} + {16 * o} + c16], {hl}[{ti}][{r}], acc{o}, 0, 0, 0);')
+            for o in range(NO):
+                F.append(f'    acc[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a{ti}_{o}[{r}], {hl}[{ti}][{r}], acc[{o}], '
+                         '0, 0, 0);')
     F.append('    if (live) {')
-    for o in range(CHUNK // 16):
-        F.append(f'      *reinterpret_cast<mh_f4*>(W0 + ej * {NW} + ch * {CHUNK} + {16 * o} + 4 * q) = acc{o};')
-    F += ['    }',
-          '  }',
-          '}', '']
+    F += [f'      *reinterpret_cast<mh_f4*>(W0 + ej * {NW} + ch * {CHUNK} + {16 * o} + 4 * q) = acc[{o}];'
+          for o in range(NO)]
+    F += ['    }']
+    F += pre_store('nbase', HL, '    ') + ['    __syncthreads();', '  }', '}', '']
     L += F
 
-    # ---------------------------------------------------------------- backward
-    B = prologue('mlp_bwd', True)
-    B += mm_first('z0', hidden[0] // 16) + act('h0', 'z0', hidden[0] // 16, spec.c[0])
-    for i in range(1, nh):
-        B += mm_hidden(f'z{i}', f'h{i - 1}', hidden[i - 1] // 16, hidden[i] // 16, offs[i], hidden[i])
-        if i < nh - 1:
-            B += act(f'h{i}', f'z{i}', hidden[i] // 16, spec.c[i])
-    # dL/dh_last = gW @ Wl^T: the output layer's columns are the K index, streamed in chunks; the B operand is gW, one
-    # float4 per lane per 16 columns (k = 16 t + 4 q + r), the A operand Wl[h][k] from the staged chunk
-    NG = CHUNK // 16
-    B += [f'  mh_f4 dh[{TL}];']
-    B += [f'  dh[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
-    B += [f'  mh_f4 {", ".join(f"pre{it}" for it in range(NLD))};']
-    B += chunk_load('0', '  ')
-    B += [f'  mh_f4 g{ti} = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {16 * ti} + 4 * q);' for ti in range(NG)]
-    B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{', '    __syncthreads();']
-    B += chunk_store('    ')
-    B += ['    __syncthreads();', f'    const int nx = min(ch + 1, {NCHK - 1}) * {CHUNK};']
-    B += chunk_load('nx', '    ')
+    # ------------------------------------------------------------------ backward
+    # dL/dh_last = gW Wl^T first (chunks of Wl [HL][NW] as [HL][CHUNK + PAD]; gW one float4 per lane per 16 columns,
+    # K order k = 16 t + 4 q + r), then the hidden layers recomputed from the natural-layout weights and walked back
+    B = head('mlp_bwd', 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
+             'const float* __restrict__ gW, float* __restrict__ gef, long long E', lds_bwd)
+    B += [f'  mh_f4 dh[{TL}];'] + [f'  dh[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
+    B += [f'  mh_f4 {pres};'] + pre_load('Wl', '0', NW, CHUNK, '  ')
+    B += [f'  mh_f4 g{ti} = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {16 * ti} + 4 * q);' for ti in range(NO)]
+    B += pre_store('0', CHUNK, '  ') + ['  __syncthreads();']
+    B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
+          f'    const int base = (ch & 1) * {Lo["chunk_bwd"]}, nbase = {Lo["chunk_bwd"]} - base;',
+          f'    const int nx = min(ch + 1, {NCHK - 1}) * {CHUNK};']
+    B += pre_load('Wl', 'nx', NW, CHUNK, '    ')
     B += [f'    const mh_f4 gn{ti} = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + nx + {16 * ti} + 4 * q);'
-          for ti in range(NG)]
-    for ti in range(CHUNK // 16):
+          for ti in range(NO)]
+    for ti in range(NO):
+        for o in range(TL):
+            B.append(f'    const mh_f4 a{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[base + ({16 * o} + c16) * '
+                     f'{CHUNK + PAD} + {16 * ti} + 4 * q]);')
         for r in range(4):
             for o in range(TL):
-                B.append(f'    dh[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(lds[{woff_chunk} + ({16 * o} + c16) * '
-                         f'{CHUNK + PAD} + {16 * ti + r} + 4 * q], g{ti}[{r}], dh[{o}], 0, 0, 0);')
-    B += [f'    g{ti} = gn{ti};' for ti in range(NG)]
-    B += ['  }']
-    # back through the hidden layers: dz_i = dh_i * c_i * silu'(z_i); dh_{i-1} = dz_i @ A_i^T
+                B.append(f'    dh[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a{ti}_{o}[{r}], g{ti}[{r}], dh[{o}], 0, 0, 0);')
+    B += [f'    g{ti} = gn{ti};' for ti in range(NO)]
+    B += pre_store('nbase', CHUNK, '    ') + ['    __syncthreads();', '  }']
+    B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(False, False)
     cur = 'dh'
     for i in range(nh - 1, -1, -1):
-        T = hidden[i] // 16
+        T = cols[i] // 16
         for o in range(T):
             for r in range(4):
                 B += ['  {',
@@ -272,28 +291,31 @@ def source(spec):
                       f'    {cur}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
                       '  }']
         if i > 0:
-            Tp = hidden[i - 1] // 16
+            Tp = cols[i - 1] // 16
             nxt = f'dh{i - 1}'
-            # A[j][k] = A_i[j][k] (row j = input feature of layer i, k = its output): LDS rows are the input features
+            # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
             B.append(f'  mh_f4 {nxt}[{Tp}];')
-            for o in range(Tp):
-                B.append(f'  {nxt}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};')
-                for ti in range(T):
-                    for r in range(4):
-                        B.append(f'  {nxt}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(lds[{offs[i]} + ({16 * o} + c16) * '
-                                 f'{hidden[i] + PAD} + {16 * ti + r} + 4 * q], {cur}[{ti}][{r}], {nxt}[{o}], 0, 0, 0);')
+            B += [f'  {nxt}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
+            for ti in range(T):
+                for o in range(Tp):
+                    B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
+                             f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
+                for r in range(4):
+                    for o in range(Tp):
+                        B.append(f'  {nxt}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], {cur}[{ti}][{r}], '
+                                 f'{nxt}[{o}], 0, 0, 0);')
             cur = nxt
-    # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16 inputs; rows past H0 read row 0)
-    TI = -(-H0 // 16)
-    T0 = hidden[0] // 16
-    for o in range(TI):
+    # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
+    T0 = cols[0] // 16
+    for o in range(-(-H0 // 16)):
         B += ['  {',
               '    mh_f4 d = mh_f4{0.f, 0.f, 0.f, 0.f};',
-              f'    const int row = {16 * o} + c16 < {H0} ? {16 * o} + c16 : 0;']
+              f'    const int row = {16 * o} + c16 < {rows[0]} ? {16 * o} + c16 : 0;']
         for ti in range(T0):
+            B.append(f'    const mh_f4 w{ti} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][0]} + row * {cols[0] + PAD} + '
+                     f'{16 * ti} + 4 * q]);')
             for r in range(4):
-                B.append(f'    d = __builtin_amdgcn_mfma_f32_16x16x4f32(lds[{offs[0]} + row * {hidden[0] + PAD} + '
-                         f'{16 * ti + r} + 4 * q], {cur}[{ti}][{r}], d, 0, 0, 0);')
+                B.append(f'    d = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}[{ti}][{r}], d, 0, 0, 0);')
         for r in range(4):
             B.append(f'    if (live && {16 * o + r} + 4 * q < {H0}) gef[ej * {H0} + {16 * o + r} + 4 * q] = d[{r}];')
         B.append('  }')
@@ -303,16 +325,23 @@ def source(spec):
 
 
 def packed_weights(spec):
-    """(hidden weights as laid out in LDS, output-layer weights [HL, NW]) in float32."""
-    hs = spec.hs
-    K0S = -(-hs[0] // 4)
-    parts = []
+    """float32 weight buffers: {'fwd': (hidden transposed, WlT [NW, HL]), 'bwd': (hidden natural, Wl [HL, NW])}.
+    Hidden layer i is laid out as the kernel's LDS copy: natural [k][j + PAD] (the first layer's K padded to a
+    multiple of 4 with zero rows) or transposed [j][k + PAD]."""
+    Lo = _layout(spec)
+    nat = np.zeros(Lo['nat_size'])
+    tr = np.zeros(Lo['tr_size'])
     for i, A in enumerate(spec.A[:-1]):
-        rows = 4 * K0S if i == 0 else hs[i]
-        buf = np.zeros((rows, hs[i + 1] + PAD))
-        buf[:A.shape[0], :A.shape[1]] = A
-        parts.append(buf.reshape(-1))
-    return np.concatenate(parts).astype(np.float32), np.ascontiguousarray(spec.A[-1]).astype(np.float32)
+        r, c = Lo['rows'][i], Lo['cols'][i]
+        buf = np.zeros((r, c + PAD))
+        buf[:A.shape[0], :c] = A
+        nat[Lo['nat'][i]:Lo['nat'][i] + buf.size] = buf.reshape(-1)
+        bt = np.zeros((c, r + PAD))
+        bt[:, :A.shape[0]] = A.T
+        tr[Lo['tr'][i]:Lo['tr'][i] + bt.size] = bt.reshape(-1)
+    Wl = spec.A[-1]
+    return {'fwd': (tr.astype(np.float32), np.ascontiguousarray(Wl.T).astype(np.float32)),
+            'bwd': (nat.astype(np.float32), np.ascontiguousarray(Wl).astype(np.float32))}
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
@@ -332,7 +361,7 @@ class _MLPFn(torch.autograd.Function):
         E = x.shape[0]
         out = torch.empty(E, s.hs[-1], device=x.device, dtype=torch.float32)
         _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd, op.module.handle, _native.ptr(x),
-                       _native.ptr(op.Wh), _native.ptr(op.Wl), _native.ptr(out), E, _native.stream_of(x))
+                       _native.ptr(op.WhT), _native.ptr(op.WlT), _native.ptr(out), E, _native.stream_of(x))
         ctx.save_for_backward(x)
         ctx.op, ctx.lead = op, lead
         return out.reshape(*lead, s.hs[-1])
@@ -366,9 +395,9 @@ class HipRadialMLP(torch.nn.Module):
                 _native.MH_MLP_FWD: ('mlp_fwd', BLOCK, EDGES),
                 _native.MH_MLP_BWD: ('mlp_bwd', BLOCK, EDGES),
             })
-        wh, wl = packed_weights(self.spec)
-        self.register_buffer('Wh', torch.tensor(wh, device=dev), persistent=False)
-        self.register_buffer('Wl', torch.tensor(wl, device=dev), persistent=False)
+        pw = packed_weights(self.spec)
+        for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1])):
+            self.register_buffer(name, torch.tensor(arr, device=dev), persistent=False)
         self.hs = self.spec.hs
         self.original = [mod]
         self.tag = 'radial_mlp'

@@ -504,7 +504,7 @@ def test_radial_mlp_c_abi():
     x = torch.randn(e, op.hs[0], device=dev)
     out = torch.empty(e, op.hs[-1], device=dev)
     lib, P, st = _native.load(), _native.ptr, _native.stream_of(x)
-    _native.check(lib.mh_mlp_fwd(op.module.handle, P(x), P(op.Wh), P(op.Wl), P(out), e, st), 'mlp_fwd')
+    _native.check(lib.mh_mlp_fwd(op.module.handle, P(x), P(op.WhT), P(op.WlT), P(out), e, st), 'mlp_fwd')
     gx = torch.empty_like(x)
     _native.check(lib.mh_mlp_bwd(op.module.handle, P(x), P(op.Wh), P(op.Wl), P(out), P(gx), e, st), 'mlp_bwd')
     torch.cuda.synchronize()
@@ -514,7 +514,7 @@ def test_radial_mlp_c_abi():
     jdx = (op(x + dx) - op(x - dx)) / 2
     lhs, rhs = _dot(gx, dx), _dot(out, jdx)
     assert abs(lhs - rhs) <= 1e-3 * abs(rhs)
-    assert lib.mh_mlp_fwd(op.module.handle, None, P(op.Wh), P(op.Wl), P(out), e, st) != 0
+    assert lib.mh_mlp_fwd(op.module.handle, None, P(op.WhT), P(op.WlT), P(out), e, st) != 0
     assert b'NULL' in lib.mh_last_error()
 
 

@@ -20,8 +20,11 @@ def test_restated_layers_match_every_block():
         with torch.no_grad():
             ref = blk.conv_tp_weights.double()(torch.tensor(x)).numpy()
         assert np.abs(spec.apply(x) - ref).max() < 1e-12 * np.abs(ref).max()
-        wh, wl = radial.packed_weights(spec)
-        assert wl.shape == (spec.hs[-2], spec.hs[-1]) and wh.dtype == np.float32
+        pw = radial.packed_weights(spec)
+        assert pw['bwd'][1].shape == (spec.hs[-2], spec.hs[-1]) and pw['fwd'][1].shape == (spec.hs[-1], spec.hs[-2])
+        assert pw['fwd'][0].dtype == np.float32
+        # both hidden layouts hold the same numbers
+        assert np.isclose(np.abs(pw['fwd'][0]).sum(), np.abs(pw['bwd'][0]).sum(), rtol=1e-6)
 
 
 def test_unsupported_networks_are_refused():
