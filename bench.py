@@ -56,7 +56,8 @@ def _time_calls(model, batch, steps, warmup, sync):
 def _kernel_table(met, batch, n_real_edges, summary):
     """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only)."""
     import torch
-    from mace_hip_kernels import HipConvTP, HipNodeLinear, HipRadialMLP, HipSphericalHarmonics, HipSymmetricContraction
+    from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipSphericalHarmonics,
+                                  HipSymmetricContraction)
     n = batch['positions'].shape[0]
     n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
     rows = {}
@@ -87,6 +88,10 @@ def _kernel_table(met, batch, n_real_edges, summary):
             bf, bb = s.bytes(n)
             rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n), 'lin_fwd')
             rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n), 'lin_bwd')
+        elif isinstance(m, HipRadialEmbedding):
+            bf, bb = m.spec.bytes(batch['edge_index'].shape[1])
+            rows[f'emb_fwd[{m.tag}]'] = (bf, 0, 'emb_fwd')
+            rows[f'emb_bwd[{m.tag}]'] = (bb, 0, 'emb_bwd')
         elif isinstance(m, HipRadialMLP):
             s = m.spec                                  # every edge of the padded list is evaluated
             E = batch['edge_index'].shape[1]

@@ -53,7 +53,9 @@ enum mh_kernel_kind {
     MH_LIN_BWD = 14,     /* its input gradient (the same map with transposed weights)              */
     MH_MLP_FWD = 15,     /* radial MLP: per-edge weights from the edge features, 64 edges a block  */
     MH_MLP_BWD = 16,     /* its input gradient (hidden layers recomputed)                          */
-    MH_NUM_KINDS = 17
+    MH_EMB_FWD = 17,     /* radial embedding: Bessel basis x polynomial cutoff of the edge lengths */
+    MH_EMB_BWD = 18,     /* its gradient with respect to the lengths                               */
+    MH_NUM_KINDS = 19
 };
 
 /* flags of mh_conv_bwd */
@@ -186,6 +188,15 @@ int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const float* Wt
 int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, float* W0, int64_t E, void* stream);
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, const float* gW0, float* gef,
                int64_t E, void* stream);
+
+/* Radial embedding of E edge lengths (len [E]): cutoff[e] = polynomial envelope of len[e] / r_max (0 beyond r_max)
+ * and feats[e, n] = sqrt(2 / r_max) sin(w_n len[e]) / len[e] * cutoff[e] (feats [E, n_basis]); r_max, the envelope
+ * power and the w_n are compiled into the module.  mh_emb_bwd gives glen from gfeats and gcutoff (gcutoff may be
+ * NULL: no gradient reaches the cutoff).  No reference counterpart: the reference leaves MACE's
+ * RadialEmbeddingBlock (BesselBasis x PolynomialCutoff) on PyTorch. */
+int mh_emb_fwd(mh_module* m, const float* len, float* feats, float* cutoff, int64_t E, void* stream);
+int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float* gcutoff, float* glen, int64_t E,
+               void* stream);
 
 #ifdef __cplusplus
 }

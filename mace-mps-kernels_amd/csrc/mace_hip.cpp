@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 8; }
+int mh_version(void) { return 9; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -306,6 +306,19 @@ int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, 
     if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef)) return fail(-1, "mh_mlp_bwd: NULL operand");
     void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E};
     return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
+}
+
+int mh_emb_fwd(mh_module* m, const float* len, float* feats, float* cutoff, int64_t E, void* stream) {
+    if (E > 0 && (!len || !feats || !cutoff)) return fail(-1, "mh_emb_fwd: NULL operand");
+    void* args[] = {&len, &feats, &cutoff, &E};
+    return launch(m, MH_EMB_FWD, E, args, stream, "mh_emb_fwd");
+}
+
+int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float* gcutoff, float* glen, int64_t E,
+               void* stream) {
+    if (E > 0 && (!len || !gfeats || !glen)) return fail(-1, "mh_emb_bwd: NULL len, gfeats or glen");
+    void* args[] = {&len, &gfeats, &gcutoff, &glen, &E};
+    return launch(m, MH_EMB_BWD, E, args, stream, "mh_emb_bwd");
 }
 
 }  // extern "C"

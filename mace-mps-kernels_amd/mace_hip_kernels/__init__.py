@@ -10,7 +10,7 @@ Replaces, where supported (reference __init__.py:1-14):
   * each product block's symmetric contraction,
   * beyond the reference: the edge spherical harmonics, and the node-wise equivariant linears (e3nn ``o3.Linear``)
     and scalar-attribute tensor products (``skip_tp``) with at least 16 output channels per irrep, and each
-    interaction block's radial MLP (``conv_tp_weights``).
+    interaction block's radial MLP (``conv_tp_weights``), and the radial embedding of the edge lengths.
 Everything else stays on the original e3nn / PyTorch path.  Inference only: the backward pass is first order
 (energies, forces, stress, finite-difference Hessians, MD, relaxations); double backward raises.
 
@@ -27,13 +27,14 @@ from .conv import HipConvTP, conv_supported
 from .edge import HipSphericalHarmonics, sh_supported
 from .linear import HipNodeLinear, lin_supported
 from .radial import HipRadialMLP, mlp_supported
+from .embedding import HipRadialEmbedding, emb_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
 
 __version__ = '0.1.0'
 __all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
-           'HipNodeLinear', 'HipRadialMLP', 'conv_supported', 'sc_supported', 'sh_supported', 'lin_supported',
-           'mlp_supported']
+           'HipNodeLinear', 'HipRadialMLP', 'HipRadialEmbedding', 'conv_supported', 'sc_supported', 'sh_supported', 'lin_supported',
+           'mlp_supported', 'emb_supported']
 
 _LINEAR_CLASSES = ('Linear', 'FullyConnectedTensorProduct')
 
@@ -57,13 +58,14 @@ def _linear_candidates(model):
 
 
 def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
-                radial_mlp=True):
+                radial_mlp=True, radial_embedding=True):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
     edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
     node-wise e3nn linears and scalar-attribute tensor products (``skip_tp``); readout heads with fewer than 16 output
     channels per irrep are left on e3nn without being reported (they are a negligible part of the call), and
-    ``radial_mlp`` each interaction block's radial MLP (``conv_tp_weights``, an e3nn FullyConnectedNet)."""
+    ``radial_mlp`` each interaction block's radial MLP (``conv_tp_weights``, an e3nn FullyConnectedNet), and
+    ``radial_embedding`` the model's Bessel x polynomial-cutoff edge embedding."""
     p = next(model.parameters())
     dev = p.device
     if dev.type != 'cuda' or torch.version.hip is None:
@@ -117,6 +119,19 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 patched.append('spherical_harmonics')
             else:
                 skipped.append(('spherical_harmonics', why))
+    if radial_embedding and hasattr(model, 'radial_embedding'):
+        emb = model.radial_embedding
+        if not isinstance(emb, HipRadialEmbedding):
+            ok, why = emb_supported(emb)
+            if ok:
+                try:
+                    model.radial_embedding = HipRadialEmbedding(emb, device=dev)
+                except ValueError as e:
+                    ok, why = False, str(e)
+            if ok:
+                patched.append('radial_embedding')
+            else:
+                skipped.append(('radial_embedding', why))
     if radial_mlp:
         for i, blk in enumerate(getattr(model, 'interactions', [])):
             name = f'interactions.{i}.conv_tp_weights'
@@ -173,6 +188,9 @@ def unpatch_model(model):
     if isinstance(getattr(model, 'spherical_harmonics', None), HipSphericalHarmonics):
         model.spherical_harmonics = model.spherical_harmonics.original[0]
         restored.append('spherical_harmonics')
+    if isinstance(getattr(model, 'radial_embedding', None), HipRadialEmbedding):
+        model.radial_embedding = model.radial_embedding.original[0]
+        restored.append('radial_embedding')
     for i, blk in enumerate(getattr(model, 'interactions', [])):
         if isinstance(getattr(blk, 'conv_tp_weights', None), HipRadialMLP):
             blk.conv_tp_weights = blk.conv_tp_weights.original[0]

@@ -12,8 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialMLP, HipSphericalHarmonics, HipSymmetricContraction,
-                              _native)
+from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipSphericalHarmonics,
+                              HipSymmetricContraction, _native)
 from mace_hip_kernels import conv as hconv
 from mace_lite import blocks as B
 from mace_lite import factory
@@ -516,6 +516,41 @@ def test_radial_mlp_c_abi():
     assert abs(lhs - rhs) <= 1e-3 * abs(rhs)
     assert lib.mh_mlp_fwd(op.module.handle, None, P(op.WhT), P(op.WlT), P(out), e, st) != 0
     assert b'NULL' in lib.mh_last_error()
+
+
+def test_radial_embedding_vs_float64():
+    """Bessel x polynomial-cutoff embedding of the edge lengths: both outputs against the module in float64, and
+    dL/dr against float64 autograd with gradients on both outputs and on the features only; lengths on both sides of
+    r_max and exactly at it, a ragged count, a leading batch shape and no edges."""
+    dev = _dev()
+    print('[case] radial embedding', flush=True)
+    model = factory.make_model('128x0e+128x1o', 3, 2, elements=factory.ELEMENTS_PTCOH)
+    emb = model.radial_embedding
+    op = HipRadialEmbedding(emb, device=dev)
+    rng = np.random.default_rng(4)
+    e = 5001
+    r = rng.uniform(0.4, 1.3 * op.spec.r_max, size=(e, 1))
+    r[:7, 0] = op.spec.r_max
+    rt = torch.tensor(r, dtype=torch.float32, device=dev, requires_grad=True)
+    f, c = op(rt)
+    m64 = copy.deepcopy(emb).double()
+    r64 = torch.tensor(r, requires_grad=True)
+    f64, c64 = m64(r64)
+    assert _rel(f.detach().double().cpu().numpy(), f64.detach().numpy()) < 1e-5
+    assert _rel(c.detach().double().cpu().numpy(), c64.detach().numpy()) < 1e-5
+    assert float(c[:7].abs().max()) == 0.0 and float(f[:7].abs().max()) == 0.0
+    gf, gc = rng.normal(size=(e, op.spec.n)), rng.normal(size=(e, 1))
+    for with_cut in (True, False):
+        outs, outs64 = (f, c) if with_cut else (f,), (f64, c64) if with_cut else (f64,)
+        grads = (gf, gc) if with_cut else (gf,)
+        got, = torch.autograd.grad(outs, rt, [torch.tensor(g, dtype=torch.float32, device=dev) for g in grads],
+                                   retain_graph=True)
+        want, = torch.autograd.grad(outs64, r64, [torch.tensor(g) for g in grads], retain_graph=True)
+        assert _rel(got.double().cpu().numpy(), want.numpy()) < 1e-5
+    f2, c2 = op(rt.detach()[:60].reshape(3, 20, 1))
+    assert f2.shape == (3, 20, op.spec.n) and torch.equal(f2.reshape(60, -1), f.detach()[:60])
+    f0, c0 = op(torch.zeros(0, 1, device=dev))
+    assert f0.shape == (0, op.spec.n) and c0.shape == (0, 1)
 
 
 def test_kernels_match_golden_fixtures():

@@ -149,7 +149,8 @@ def test_idempotent_patch_and_unpatch():
     assert sorted(unpatch_model(m)) == sorted(r1['patched'])
     assert type(m.spherical_harmonics).__name__ == 'SphericalHarmonics'
     assert type(m.interactions[1].linear).__name__ == 'Linear'
-    r3 = patch_model(m, verbose=False, spherical_harmonics=False, linears=False, radial_mlp=False)
+    r3 = patch_model(m, verbose=False, spherical_harmonics=False, linears=False, radial_mlp=False,
+                     radial_embedding=False)
     assert len(r3['patched']) == 4 and 'spherical_harmonics' not in r3['patched']
     assert len(unpatch_model(m)) == 4
     assert not hasattr(m.interactions[0], 'conv_fusion')
