@@ -55,7 +55,9 @@ enum mh_kernel_kind {
     MH_MLP_BWD = 16,     /* its input gradient (hidden layers recomputed)                          */
     MH_EMB_FWD = 17,     /* radial embedding: Bessel basis x polynomial cutoff of the edge lengths */
     MH_EMB_BWD = 18,     /* its gradient with respect to the lengths                               */
-    MH_NUM_KINDS = 19
+    MH_PERM_FWD = 19,    /* per-node permutation irreps layout -> [mul, sum (2l+1)]                */
+    MH_PERM_BWD = 20,    /* its inverse                                                            */
+    MH_NUM_KINDS = 21
 };
 
 /* flags of mh_conv_bwd */
@@ -197,6 +199,12 @@ int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, 
 int mh_emb_fwd(mh_module* m, const float* len, float* feats, float* cutoff, int64_t E, void* stream);
 int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float* gcutoff, float* glen, int64_t E,
                void* stream);
+
+/* Per-node permutation of N rows from e3nn's irreps layout (block l at off_l, index off_l + u (2l+1) + m) to
+ * [mul, sum_l (2l+1)] (index u D + o_l + m), the block table compiled into the module; mh_perm_bwd applies the inverse
+ * (gx from gy).  No reference counterpart: the reference leaves MACE's reshape_irreps on PyTorch. */
+int mh_perm_fwd(mh_module* m, const float* x, float* y, int32_t N, void* stream);
+int mh_perm_bwd(mh_module* m, const float* gy, float* gx, int32_t N, void* stream);
 
 #ifdef __cplusplus
 }

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 9; }
+int mh_version(void) { return 10; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -319,6 +319,18 @@ int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float*
     if (E > 0 && (!len || !gfeats || !glen)) return fail(-1, "mh_emb_bwd: NULL len, gfeats or glen");
     void* args[] = {&len, &gfeats, &gcutoff, &glen, &E};
     return launch(m, MH_EMB_BWD, E, args, stream, "mh_emb_bwd");
+}
+
+int mh_perm_fwd(mh_module* m, const float* x, float* y, int32_t N, void* stream) {
+    if (N > 0 && (!x || !y)) return fail(-1, "mh_perm_fwd: NULL operand");
+    void* args[] = {&x, &y, &N};
+    return launch(m, MH_PERM_FWD, N, args, stream, "mh_perm_fwd");
+}
+
+int mh_perm_bwd(mh_module* m, const float* gy, float* gx, int32_t N, void* stream) {
+    if (N > 0 && (!gy || !gx)) return fail(-1, "mh_perm_bwd: NULL operand");
+    void* args[] = {&gy, &gx, &N};
+    return launch(m, MH_PERM_BWD, N, args, stream, "mh_perm_bwd");
 }
 
 }  // extern "C"

@@ -10,7 +10,8 @@ Replaces, where supported (reference __init__.py:1-14):
   * each product block's symmetric contraction,
   * beyond the reference: the edge spherical harmonics, and the node-wise equivariant linears (e3nn ``o3.Linear``)
     and scalar-attribute tensor products (``skip_tp``) with at least 16 output channels per irrep, and each
-    interaction block's radial MLP (``conv_tp_weights``), and the radial embedding of the edge lengths.
+    interaction block's radial MLP (``conv_tp_weights``), the radial embedding of the edge lengths, and the
+    per-node layout permutation (``reshape_irreps``) in front of each symmetric contraction.
 Everything else stays on the original e3nn / PyTorch path.  Inference only: the backward pass is first order
 (energies, forces, stress, finite-difference Hessians, MD, relaxations); double backward raises.
 
@@ -28,13 +29,14 @@ from .edge import HipSphericalHarmonics, sh_supported
 from .linear import HipNodeLinear, lin_supported
 from .radial import HipRadialMLP, mlp_supported
 from .embedding import HipRadialEmbedding, emb_supported
+from .layout import HipReshapeIrreps, reshape_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
 
 __version__ = '0.1.0'
 __all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
            'HipNodeLinear', 'HipRadialMLP', 'HipRadialEmbedding', 'conv_supported', 'sc_supported', 'sh_supported', 'lin_supported',
-           'mlp_supported', 'emb_supported']
+           'mlp_supported', 'emb_supported', 'HipReshapeIrreps', 'reshape_supported']
 
 _LINEAR_CLASSES = ('Linear', 'FullyConnectedTensorProduct')
 
@@ -58,14 +60,15 @@ def _linear_candidates(model):
 
 
 def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
-                radial_mlp=True, radial_embedding=True):
+                radial_mlp=True, radial_embedding=True, layouts=True):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
     edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
     node-wise e3nn linears and scalar-attribute tensor products (``skip_tp``); readout heads with fewer than 16 output
     channels per irrep are left on e3nn without being reported (they are a negligible part of the call), and
     ``radial_mlp`` each interaction block's radial MLP (``conv_tp_weights``, an e3nn FullyConnectedNet), and
-    ``radial_embedding`` the model's Bessel x polynomial-cutoff edge embedding."""
+    ``radial_embedding`` the model's Bessel x polynomial-cutoff edge embedding, and ``layouts`` each interaction
+    block's ``reshape`` (irreps layout -> symmetric-contraction layout)."""
     p = next(model.parameters())
     dev = p.device
     if dev.type != 'cuda' or torch.version.hip is None:
@@ -150,6 +153,19 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             new.tag = name
             blk.conv_tp_weights = new
             patched.append(name)
+    if layouts:
+        for i, blk in enumerate(getattr(model, 'interactions', [])):
+            name = f'interactions.{i}.reshape'
+            rs = getattr(blk, 'reshape', None)
+            if rs is None or isinstance(rs, HipReshapeIrreps) or type(rs).__name__ != 'reshape_irreps':
+                continue
+            ok, why = reshape_supported(rs)
+            if not ok:
+                skipped.append((name, why))
+                continue
+            blk.reshape = HipReshapeIrreps(rs, device=dev)
+            blk.reshape.tag = name
+            patched.append(name)
     if linears:
         for name, parent, attr, mod in _linear_candidates(model):
             if any(mul < 16 for mul, _ in mod.irreps_out):
@@ -192,6 +208,9 @@ def unpatch_model(model):
         model.radial_embedding = model.radial_embedding.original[0]
         restored.append('radial_embedding')
     for i, blk in enumerate(getattr(model, 'interactions', [])):
+        if isinstance(getattr(blk, 'reshape', None), HipReshapeIrreps):
+            blk.reshape = blk.reshape.original[0]
+            restored.append(f'interactions.{i}.reshape')
         if isinstance(getattr(blk, 'conv_tp_weights', None), HipRadialMLP):
             blk.conv_tp_weights = blk.conv_tp_weights.original[0]
             restored.append(f'interactions.{i}.conv_tp_weights')

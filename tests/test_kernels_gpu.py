@@ -553,6 +553,28 @@ def test_radial_embedding_vs_float64():
     assert f0.shape == (0, op.spec.n) and c0.shape == (0, 1)
 
 
+def test_reshape_irreps_is_the_module_permutation():
+    """reshape_irreps drop-in: forward and backward equal the PyTorch module bitwise (a permutation), for the
+    config-2 and config-4 layouts and a ragged node count."""
+    from mace_hip_kernels import HipReshapeIrreps
+    dev = _dev()
+    for hidden in ('128x0e+128x1o', '128x0e+128x1o+128x2e'):
+        print(f'[case] reshape_irreps {hidden}', flush=True)
+        model = factory.make_model(hidden, 3, 2, elements=factory.ELEMENTS_PTCOH)
+        rs = model.interactions[0].reshape
+        op = HipReshapeIrreps(rs, device=dev)
+        n = 1001
+        x = torch.randn(n, op.spec.dim, device=dev, requires_grad=True)
+        y = op(x)
+        y_ref = rs(x)
+        assert y.shape == y_ref.shape and torch.equal(y, y_ref)
+        g = torch.randn_like(y)
+        gx, = torch.autograd.grad(y, x, g)
+        gx_ref, = torch.autograd.grad(y_ref, x, g)
+        assert torch.equal(gx, gx_ref)
+        assert op(torch.zeros(0, op.spec.dim, device=dev)).shape == (0, op.spec.mul, op.spec.D)
+
+
 def test_kernels_match_golden_fixtures():
     """Kernels against the committed oracle fixtures (tests/golden/make_golden.py)."""
     import os

@@ -79,3 +79,16 @@ def test_generated_source_compiles():
             spec = linear.LinSpec(mod)
             assert len(_native.compile_source(linear.source(spec))) > 1000
             assert spec.has_bwd == (name != 'node_embedding.linear')
+
+
+def test_reshape_permutation_matches_the_module():
+    """The permutation table of the reshape_irreps drop-in against the PyTorch module (on an arange input the output
+    lists the source index of every element), and its HIP source compiling."""
+    from mace_hip_kernels import _native, layout
+    m = factory.make_model('128x0e+128x1o+128x2e', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    for blk in m.interactions:
+        spec = layout.ReshapeSpec(blk.reshape)
+        x = torch.arange(spec.dim, dtype=torch.float64).reshape(1, -1)
+        assert blk.reshape(x).reshape(-1).long().tolist() == spec.perm()
+        assert sorted(spec.perm()) == list(range(spec.dim))
+        assert len(_native.compile_source(layout.source(spec))) > 1000
