@@ -57,7 +57,9 @@ enum mh_kernel_kind {
     MH_EMB_BWD = 18,     /* its gradient with respect to the lengths                               */
     MH_PERM_FWD = 19,    /* per-node permutation irreps layout -> [mul, sum (2l+1)]                */
     MH_PERM_BWD = 20,    /* its inverse                                                            */
-    MH_NUM_KINDS = 21
+    MH_GEOM_FWD = 21,    /* edge vectors and lengths from positions, edge list and shifts          */
+    MH_GEOM_BWD = 22,    /* their gradient: per-atom CSR sums (one wave per atom)                  */
+    MH_NUM_KINDS = 23
 };
 
 /* flags of mh_conv_bwd */
@@ -205,6 +207,17 @@ int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float*
  * (gx from gy).  No reference counterpart: the reference leaves MACE's reshape_irreps on PyTorch. */
 int mh_perm_fwd(mh_module* m, const float* x, float* y, int32_t N, void* stream);
 int mh_perm_bwd(mh_module* m, const float* gy, float* gx, int32_t N, void* stream);
+
+/* Edge geometry: vec[e] = pos[recv[e]] - pos[send[e]] + shifts[e] and len[e] = |vec[e]| for E edges (pos [N, 3],
+ * shifts/vec [E, 3], len [E]).  mh_geom_bwd: gpos[n] = sum_{recv[e] = n} gv[e] - sum_{send[e] = n} gv[e] with
+ * gv[e] = gvec[e] + glen[e] vec[e] / len[e] (0 where len is 0), over the receiver and sender CSRs of the edge list
+ * (rowptr [N + 1], eids [E]); gshifts (may be NULL) receives gv; gvec or glen NULL count as zero.  No reference
+ * counterpart: the reference leaves MACE's get_edge_vectors_and_lengths on PyTorch. */
+int mh_geom_fwd(mh_module* m, const float* pos, const int32_t* send, const int32_t* recv, const float* shifts,
+                float* vec, float* len, int64_t E, void* stream);
+int mh_geom_bwd(mh_module* m, const float* vec, const float* len, const float* gvec, const float* glen,
+                const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s,
+                float* gpos, float* gshifts, int32_t N, void* stream);
 
 #ifdef __cplusplus
 }

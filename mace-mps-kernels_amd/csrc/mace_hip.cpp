@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 10; }
+int mh_version(void) { return 11; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -331,6 +331,22 @@ int mh_perm_bwd(mh_module* m, const float* gy, float* gx, int32_t N, void* strea
     if (N > 0 && (!gy || !gx)) return fail(-1, "mh_perm_bwd: NULL operand");
     void* args[] = {&gy, &gx, &N};
     return launch(m, MH_PERM_BWD, N, args, stream, "mh_perm_bwd");
+}
+
+int mh_geom_fwd(mh_module* m, const float* pos, const int32_t* send, const int32_t* recv, const float* shifts,
+                float* vec, float* len, int64_t E, void* stream) {
+    if (E > 0 && (!pos || !send || !recv || !shifts || !vec || !len)) return fail(-1, "mh_geom_fwd: NULL operand");
+    void* args[] = {&pos, &send, &recv, &shifts, &vec, &len, &E};
+    return launch(m, MH_GEOM_FWD, E, args, stream, "mh_geom_fwd");
+}
+
+int mh_geom_bwd(mh_module* m, const float* vec, const float* len, const float* gvec, const float* glen,
+                const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s,
+                float* gpos, float* gshifts, int32_t N, void* stream) {
+    if (N > 0 && (!vec || !len || !rowptr_r || !eids_r || !rowptr_s || !eids_s || !gpos))
+        return fail(-1, "mh_geom_bwd: NULL operand");
+    void* args[] = {&vec, &len, &gvec, &glen, &rowptr_r, &eids_r, &rowptr_s, &eids_s, &gpos, &gshifts, &N};
+    return launch(m, MH_GEOM_BWD, N, args, stream, "mh_geom_bwd");
 }
 
 }  // extern "C"

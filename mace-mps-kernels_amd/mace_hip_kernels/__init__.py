@@ -11,7 +11,8 @@ Replaces, where supported (reference __init__.py:1-14):
   * beyond the reference: the edge spherical harmonics, and the node-wise equivariant linears (e3nn ``o3.Linear``)
     and scalar-attribute tensor products (``skip_tp``) with at least 16 output channels per irrep, and each
     interaction block's radial MLP (``conv_tp_weights``), the radial embedding of the edge lengths, and the
-    per-node layout permutation (``reshape_irreps``) in front of each symmetric contraction.
+    per-node layout permutation (``reshape_irreps``) in front of each symmetric contraction, and the edge geometry
+    (``get_edge_vectors_and_lengths``, routed to the kernels while the patched model runs).
 Everything else stays on the original e3nn / PyTorch path.  Inference only: the backward pass is first order
 (energies, forces, stress, finite-difference Hessians, MD, relaxations); double backward raises.
 
@@ -32,6 +33,7 @@ from .embedding import HipRadialEmbedding, emb_supported
 from .layout import HipReshapeIrreps, reshape_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
+from . import geometry as _geometry
 
 __version__ = '0.1.0'
 __all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
@@ -60,7 +62,7 @@ def _linear_candidates(model):
 
 
 def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
-                radial_mlp=True, radial_embedding=True, layouts=True):
+                radial_mlp=True, radial_embedding=True, layouts=True, edge_geometry=True):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
     edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
@@ -68,7 +70,9 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     channels per irrep are left on e3nn without being reported (they are a negligible part of the call), and
     ``radial_mlp`` each interaction block's radial MLP (``conv_tp_weights``, an e3nn FullyConnectedNet), and
     ``radial_embedding`` the model's Bessel x polynomial-cutoff edge embedding, and ``layouts`` each interaction
-    block's ``reshape`` (irreps layout -> symmetric-contraction layout)."""
+    block's ``reshape`` (irreps layout -> symmetric-contraction layout), and ``edge_geometry`` the edge vectors and
+    lengths (MACE's ``get_edge_vectors_and_lengths`` in the model's module, taken over only while this model's forward
+    runs; other models keep the original)."""
     p = next(model.parameters())
     dev = p.device
     if dev.type != 'cuda' or torch.version.hip is None:
@@ -122,6 +126,11 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 patched.append('spherical_harmonics')
             else:
                 skipped.append(('spherical_harmonics', why))
+    if edge_geometry and not _geometry.installed(model):
+        if _geometry.install(model):
+            patched.append('edge_geometry')
+        else:
+            skipped.append(('edge_geometry', f'no {_geometry.FUNCTION} in {type(model).__module__}'))
     if radial_embedding and hasattr(model, 'radial_embedding'):
         emb = model.radial_embedding
         if not isinstance(emb, HipRadialEmbedding):
@@ -204,6 +213,8 @@ def unpatch_model(model):
     if isinstance(getattr(model, 'spherical_harmonics', None), HipSphericalHarmonics):
         model.spherical_harmonics = model.spherical_harmonics.original[0]
         restored.append('spherical_harmonics')
+    if _geometry.uninstall(model):
+        restored.append('edge_geometry')
     if isinstance(getattr(model, 'radial_embedding', None), HipRadialEmbedding):
         model.radial_embedding = model.radial_embedding.original[0]
         restored.append('radial_embedding')

@@ -18,9 +18,9 @@ DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
 
 MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, MH_CONV_GXSUM, MH_SC_FWD_G, \
     MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD, MH_LIN_FWD, MH_LIN_BWD, \
-    MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD = range(21)
+    MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD = range(23)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -57,6 +57,8 @@ _SIGS = {
     'mh_emb_bwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_perm_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int, _P]),
     'mh_perm_bwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int, _P]),
+    'mh_geom_fwd': (ctypes.c_int, [_P] * 7 + [ctypes.c_int64, _P]),
+    'mh_geom_bwd': (ctypes.c_int, [_P] * 11 + [ctypes.c_int, _P]),
     'mh_module_bind_grid': (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     'mh_sc_fwd_sorted': (ctypes.c_int, [_P] * 6 + [_I, _P]),
     'mh_sc_bwd_sorted': (ctypes.c_int, [_P] * 7 + [_I, _P]),

@@ -1,0 +1,210 @@
+"""
+Edge geometry of MACE on MI355X: vectors[e] = positions[receiver[e]] - positions[sender[e]] + shifts[e] and
+lengths[e] = |vectors[e]| (MACE's ``get_edge_vectors_and_lengths``), with the backward that forces and stress run
+through: dL/dpositions[n] = sum over edges into n of dL/dv - sum over edges out of n of dL/dv, where
+dL/dv = g_vectors + g_lengths v / |v|, and dL/dshifts = dL/dv.
+
+In PyTorch the backward of the two row gathers is an index_put with accumulation per gather (a sort of the edge
+list and a segmented sum each call).  Here the forward is one thread per edge, and the backward one wave per atom
+summing dL/dv over the receiver-sorted and sender-sorted edge lists (CSRs) that the convolution already keeps for
+the same edge_index: deterministic, no atomics, no sort.
+
+The computation is a module-level function of MACE, not a module, so ``patch_model`` routes it here through the
+model's own module namespace: the function there is wrapped once, and the wrapper only takes this path while a
+patched model's forward is running (a context variable set by that model's forward); every other caller, unpatched
+models included, keeps the original function.
+"""
+import contextvars
+import functools
+import sys
+import types
+
+import torch
+
+from . import _native
+from . import conv as _conv
+
+BLOCK = 256
+_ACTIVE = contextvars.ContextVar('mace_hip_kernels_geometry', default=False)
+FUNCTION = 'get_edge_vectors_and_lengths'
+
+_SOURCE = r'''
+#define BLOCK 256
+extern "C" __global__ __launch_bounds__(BLOCK) void geom_fwd(const float* __restrict__ pos,
+    const int* __restrict__ send, const int* __restrict__ recv, const float* __restrict__ shifts,
+    float* __restrict__ vec, float* __restrict__ len, long long E) {
+  const long long e = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * BLOCK + threadIdx.x;
+  if (e >= E) return;
+  const long long s = send[e], r = recv[e];
+  const float vx = (pos[3 * r] - pos[3 * s]) + shifts[3 * e];
+  const float vy = (pos[3 * r + 1] - pos[3 * s + 1]) + shifts[3 * e + 1];
+  const float vz = (pos[3 * r + 2] - pos[3 * s + 2]) + shifts[3 * e + 2];
+  vec[3 * e] = vx; vec[3 * e + 1] = vy; vec[3 * e + 2] = vz;
+  len[e] = sqrtf(vx * vx + vy * vy + vz * vz);
+}
+
+// dL/dv of edge e: g_vec + g_len * v / |v| (the norm's gradient is 0 at |v| = 0, as PyTorch's)
+__device__ __forceinline__ void geom_gv(const float* __restrict__ vec, const float* __restrict__ len,
+    const float* __restrict__ gvec, const float* __restrict__ glen, int e, float& gx, float& gy, float& gz) {
+  gx = gvec ? gvec[3 * e] : 0.f;
+  gy = gvec ? gvec[3 * e + 1] : 0.f;
+  gz = gvec ? gvec[3 * e + 2] : 0.f;
+  if (glen) {
+    const float l = len[e];
+    const float c = l != 0.f ? glen[e] / l : 0.f;
+    gx += c * vec[3 * e]; gy += c * vec[3 * e + 1]; gz += c * vec[3 * e + 2];
+  }
+}
+
+__device__ __forceinline__ float geom_wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// one wave per atom: the edges into it (receiver CSR) minus the edges out of it (sender CSR)
+extern "C" __global__ __launch_bounds__(BLOCK) void geom_bwd(const float* __restrict__ vec,
+    const float* __restrict__ len, const float* __restrict__ gvec, const float* __restrict__ glen,
+    const int* __restrict__ rowptr_r, const int* __restrict__ eids_r, const int* __restrict__ rowptr_s,
+    const int* __restrict__ eids_s, float* __restrict__ gpos, float* __restrict__ gshifts, int N) {
+  const int n = mh_xcd_block(blockIdx.x, gridDim.x) * (BLOCK / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  float sx = 0.f, sy = 0.f, sz = 0.f;
+  for (int k = rowptr_r[n] + lane; k < rowptr_r[n + 1]; k += 64) {
+    const int e = eids_r[k];
+    float gx, gy, gz;
+    geom_gv(vec, len, gvec, glen, e, gx, gy, gz);
+    sx += gx; sy += gy; sz += gz;
+    if (gshifts) { gshifts[3 * e] = gx; gshifts[3 * e + 1] = gy; gshifts[3 * e + 2] = gz; }
+  }
+  for (int k = rowptr_s[n] + lane; k < rowptr_s[n + 1]; k += 64) {
+    float gx, gy, gz;
+    geom_gv(vec, len, gvec, glen, eids_s[k], gx, gy, gz);
+    sx -= gx; sy -= gy; sz -= gz;
+  }
+  sx = geom_wave_sum(sx); sy = geom_wave_sum(sy); sz = geom_wave_sum(sz);
+  if (lane == 0) { gpos[3 * n] = sx; gpos[3 * n + 1] = sy; gpos[3 * n + 2] = sz; }
+}
+'''
+
+_modules = {}
+
+
+def _module(device):
+    """The geometry kernels, loaded once per device."""
+    key = torch.device(device).index
+    if key not in _modules:
+        code = _native.compile_source(_native.device_header() + _SOURCE)
+        with torch.cuda.device(device):
+            _modules[key] = _native.Module(code, {_native.MH_GEOM_FWD: ('geom_fwd', BLOCK, BLOCK),
+                                                  _native.MH_GEOM_BWD: ('geom_bwd', BLOCK, BLOCK // 64)})
+    return _modules[key]
+
+
+def source():
+    return _native.device_header() + _SOURCE
+
+
+_DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
+                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+
+
+class _GeomFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, positions, shifts, edge_index):
+        N, E = positions.shape[0], edge_index.shape[1]
+        gr = _conv.graph_for(edge_index, N)
+        p = positions.contiguous()
+        sh = shifts.contiguous()
+        vec = torch.empty(E, 3, device=p.device, dtype=torch.float32)
+        ln = torch.empty(E, 1, device=p.device, dtype=torch.float32)
+        mod = _module(p.device)
+        _native.launch('geom_fwd', _native.load().mh_geom_fwd, mod.handle, _native.ptr(p), _native.ptr(gr.send),
+                       _native.ptr(gr.recv), _native.ptr(sh), _native.ptr(vec), _native.ptr(ln), E,
+                       _native.stream_of(p))
+        ctx.save_for_backward(vec, ln)
+        ctx.gr, ctx.N = gr, N
+        return vec, ln
+
+    @staticmethod
+    def backward(ctx, gv, gl):
+        if torch.is_grad_enabled():
+            raise RuntimeError(_DOUBLE_BACKWARD)
+        vec, ln = ctx.saved_tensors
+        gr, N = ctx.gr, ctx.N
+        rp_r, ei_r = gr.by_recv()
+        rp_s, ei_s = gr.by_send()
+        gpos = torch.empty(N, 3, device=vec.device, dtype=torch.float32)
+        gsh = torch.empty_like(vec) if ctx.needs_input_grad[1] else None
+        gv = None if gv is None else gv.contiguous()
+        gl = None if gl is None else gl.contiguous()
+        mod = _module(vec.device)
+        _native.launch('geom_bwd', _native.load().mh_geom_bwd, mod.handle, _native.ptr(vec), _native.ptr(ln),
+                       _native.ptr(gv), _native.ptr(gl), _native.ptr(rp_r), _native.ptr(ei_r), _native.ptr(rp_s),
+                       _native.ptr(ei_s), _native.ptr(gpos), _native.ptr(gsh), N, _native.stream_of(vec))
+        return (gpos if ctx.needs_input_grad[0] else None), gsh, None
+
+
+def edge_vectors_and_lengths(positions, edge_index, shifts):
+    """(vectors [E, 3], lengths [E, 1]) on the GPU kernels, differentiable in positions and shifts."""
+    if positions.dtype != torch.float32 or shifts.dtype != torch.float32 or not positions.is_cuda:
+        raise TypeError('mace_hip_kernels: edge geometry expects float32 GPU positions and shifts')
+    if positions.shape[-1] != 3 or shifts.shape != (edge_index.shape[1], 3):
+        raise ValueError(f'positions [N, 3] and shifts [E, 3] expected, got {tuple(positions.shape)}, '
+                         f'{tuple(shifts.shape)}')
+    return _GeomFn.apply(positions, shifts, edge_index)
+
+
+def _supported_call(positions, edge_index, shifts):
+    return (torch.is_tensor(positions) and positions.is_cuda and positions.dtype == torch.float32
+            and positions.dim() == 2 and torch.is_tensor(shifts) and shifts.dtype == torch.float32
+            and torch.is_tensor(edge_index) and edge_index.is_cuda and edge_index.dim() == 2 and edge_index.shape[0] == 2
+            and shifts.shape == (edge_index.shape[1], 3))
+
+
+def _wrap(orig):
+    @functools.wraps(orig)
+    def get_edge_vectors_and_lengths(positions, edge_index, shifts, normalize=False, eps=1e-9):
+        if _ACTIVE.get() and _supported_call(positions, edge_index, shifts):
+            vectors, lengths = edge_vectors_and_lengths(positions, edge_index, shifts)
+            if normalize:
+                vectors = vectors / (lengths + eps)
+            return vectors, lengths
+        return orig(positions, edge_index, shifts, normalize=normalize, eps=eps) if normalize else \
+            orig(positions, edge_index, shifts)
+    get_edge_vectors_and_lengths._mh_original = orig
+    return get_edge_vectors_and_lengths
+
+
+def _forward_with_geometry(self, *args, **kwargs):
+    token = _ACTIVE.set(True)
+    try:
+        return type(self).forward(self, *args, **kwargs)
+    finally:
+        _ACTIVE.reset(token)
+
+
+def install(model):
+    """Route the model's edge geometry through the kernels; False (nothing changed) if its module has no such
+    function."""
+    mod = sys.modules.get(type(model).__module__)
+    fn = getattr(mod, FUNCTION, None) if mod is not None else None
+    if fn is None or not callable(fn):
+        return False
+    if not hasattr(fn, '_mh_original'):
+        setattr(mod, FUNCTION, _wrap(fn))
+    model.forward = types.MethodType(_forward_with_geometry, model)
+    return True
+
+
+def installed(model):
+    f = model.__dict__.get('forward')
+    return isinstance(f, types.MethodType) and f.__func__ is _forward_with_geometry
+
+
+def uninstall(model):
+    if installed(model):
+        del model.forward
+        return True
+    return False

@@ -575,6 +575,67 @@ def test_reshape_irreps_is_the_module_permutation():
         assert op(torch.zeros(0, op.spec.dim, device=dev)).shape == (0, op.spec.mul, op.spec.D)
 
 
+def test_edge_geometry_vs_float64():
+    """Edge vectors and lengths and their backward (atom CSR sums) against float64 autograd of the PyTorch gathers,
+    with gradients on vectors and lengths, on positions and shifts (the stress path), and with zero-length edges."""
+    from mace_hip_kernels import geometry
+    dev = _dev()
+    print('[case] edge geometry', flush=True)
+    rng = np.random.default_rng(8)
+    n, e = 700, 9000
+    s, r = _graph(rng, n, e)
+    s[:5] = r[:5]                                    # self edges with zero shift: zero length
+    pos = rng.normal(size=(n, 3)) * 4.0
+    sh = rng.normal(size=(e, 3))
+    sh[:5] = 0.0
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    pt = torch.tensor(pos, dtype=torch.float32, device=dev, requires_grad=True)
+    st = torch.tensor(sh, dtype=torch.float32, device=dev, requires_grad=True)
+    v, ln = geometry.edge_vectors_and_lengths(pt, ei, st)
+    p64 = torch.tensor(pos, requires_grad=True)
+    s64 = torch.tensor(sh, requires_grad=True)
+    ei64 = torch.tensor(np.stack([s, r]))
+    v64 = p64[ei64[1]] - p64[ei64[0]] + s64
+    l64 = torch.linalg.norm(v64, dim=-1, keepdim=True)
+    assert _rel(v.detach().double().cpu().numpy(), v64.detach().numpy()) < 1e-6
+    assert _rel(ln.detach().double().cpu().numpy(), l64.detach().numpy()) < 1e-6
+    gv, gl = rng.normal(size=(e, 3)), rng.normal(size=(e, 1))
+    got = torch.autograd.grad((v, ln), (pt, st), (torch.tensor(gv, dtype=torch.float32, device=dev),
+                                                  torch.tensor(gl, dtype=torch.float32, device=dev)))
+    want = torch.autograd.grad((v64, l64), (p64, s64), (torch.tensor(gv), torch.tensor(gl)))
+    for a, b in zip(got, want):
+        assert _rel(a.double().cpu().numpy(), b.numpy()) < 1e-5
+    # lengths only, positions only
+    got, = torch.autograd.grad(geometry.edge_vectors_and_lengths(pt, ei, st.detach())[1].sum(), pt)
+    want, = torch.autograd.grad(torch.linalg.norm(p64[ei64[1]] - p64[ei64[0]] + s64.detach(), dim=-1).sum(), p64)
+    assert _rel(got.double().cpu().numpy(), want.numpy()) < 1e-5
+
+
+def test_edge_geometry_only_while_a_patched_model_runs():
+    """The edge-geometry route is taken inside a patched model's forward and nowhere else: an unpatched copy of the
+    same model, run in the same process, launches no geometry kernel."""
+    from mace_hip_kernels import patch_model, unpatch_model
+    dev = _dev()
+    print('[case] edge geometry scoping', flush=True)
+    from mace_lite import data as D
+    model = factory.make_model('32x0e+32x1o', 2, 2, elements=factory.ELEMENTS_PTCOH)
+    plain = copy.deepcopy(model).to(dev)
+    patched = copy.deepcopy(model).to(dev)
+    assert 'edge_geometry' in patch_model(patched, verbose=False)['patched']
+    st = factory.make_structure(seed=1)
+    batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
+    b = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
+    for mdl, expect in ((plain, False), (patched, True), (plain, False)):
+        with _native.timing() as tm:
+            mdl(D.fresh(b), compute_force=True)
+        tags = {t for t, *_ in tm.records}
+        assert ('geom_fwd' in tags) == expect and ('geom_bwd' in tags) == expect, tags
+    assert 'edge_geometry' in unpatch_model(patched)
+    with _native.timing() as tm:
+        patched(D.fresh(b), compute_force=True)
+    assert not any(t.startswith('geom') for t, *_ in tm.records)
+
+
 def test_kernels_match_golden_fixtures():
     """Kernels against the committed oracle fixtures (tests/golden/make_golden.py)."""
     import os
