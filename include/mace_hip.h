@@ -99,9 +99,10 @@ int mh_module_bind_grid(mh_module* m, int kind, const char* name, int block_thre
 int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
                 const int32_t* eids, const int32_t* senders, float* out, int32_t N, void* stream);
 
-/* mh_conv_fwd for weights W = W0 * cutoff[e] (W passed as the product, cutoff [E]): an edge with cutoff[e] == 0
- * contributes exactly zero and is skipped (the padding of fixed-size graphs, and neighbour-list entries beyond the
- * cutoff radius).  Same result as mh_conv_fwd up to the sign of zero sums.  No reference counterpart. */
+/* mh_conv_fwd for weights W0[e] * cutoff[e] (W passed as the unscaled W0 [E, NW], cutoff [E]; the kernel scales
+ * each edge's weights in registers, so the product is never stored): an edge with cutoff[e] == 0 contributes exactly
+ * zero and is skipped (the padding of fixed-size graphs, and neighbour-list entries beyond the cutoff radius).  Same
+ * result as mh_conv_fwd on W0 * cutoff up to the sign of zero sums.  No reference counterpart. */
 int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
                     const int32_t* eids, const int32_t* senders, const float* cutoff, float* out, int32_t N,
                     void* stream);

@@ -318,14 +318,78 @@ def _factored_weights(W):
     return None
 
 
+class CutoffProduct(torch.Tensor):
+    """The product W0 * cutoff ([E, NW] * [E, 1]) that MACE forms from the radial MLP's output right before the
+    convolution, kept as its two factors: a tensor of the product's shape and dtype without storage of its own.
+    The convolution reads the factors (its kernels scale W0 by the cutoff in registers), so the product is never
+    written to or read from memory; any other operation on it computes the product first and runs on that, so
+    every other consumer sees an ordinary tensor.  Its autograd node is the product rule (``_CutoffMul``)."""
+
+    @staticmethod
+    def __new__(cls, w0, cut):
+        return torch.Tensor._make_wrapper_subclass(cls, w0.shape, dtype=w0.dtype, device=w0.device,
+                                                   requires_grad=False)
+
+    def __init__(self, w0, cut):
+        self.w0, self.cut = w0, cut
+
+    __torch_function__ = torch._C._disabled_torch_function_impl
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        def real(t):
+            return t.w0 * t.cut if isinstance(t, CutoffProduct) else t
+        args = torch.utils._pytree.tree_map(real, args)
+        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
+        return func(*args, **kwargs)
+
+
+class _CutoffMul(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, w0, cut):
+        ctx.save_for_backward(w0, cut)
+        return CutoffProduct(w0, cut)
+
+    @staticmethod
+    def backward(ctx, g):
+        w0, cut = ctx.saved_tensors
+        gw0 = g * cut if ctx.needs_input_grad[0] else None
+        gc = (g * w0).sum(-1, keepdim=True).reshape(cut.shape) if ctx.needs_input_grad[1] else None
+        return gw0, gc
+
+
+class RadialWeights(torch.Tensor):
+    """A radial MLP's output W0 [E, NW] (an ordinary tensor of this subclass) whose product with a per-edge column
+    ``W0 * cutoff`` ([E, 1], same device and dtype) is returned as a ``CutoffProduct`` instead of being computed.
+    Every other operation behaves as on a plain tensor and returns plain tensors."""
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if func in _MULS and len(args) == 2 and not kwargs:
+            a, b = args
+            if isinstance(b, RadialWeights) and not isinstance(a, RadialWeights):
+                a, b = b, a
+            if (isinstance(a, RadialWeights) and torch.is_tensor(b) and not isinstance(b, RadialWeights)
+                    and a.dim() == 2 and tuple(b.shape) == (a.shape[0], 1) and b.dtype == a.dtype
+                    and b.device == a.device and a.dtype == torch.float32):
+                return _CutoffMul.apply(a.as_subclass(torch.Tensor), b)
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+
+_MULS = {torch.Tensor.__mul__, torch.Tensor.__rmul__, torch.Tensor.mul, torch.mul}
+
+
 class _ConvFn(torch.autograd.Function):
     """Inputs (x, Y, W, W0, cut, edge_index, op).  Plain: W is the weight tensor, W0 = cut = None.  Factored:
-    W = W0 * cut is passed detached (the forward kernel reads it) and W0, cut are the differentiable inputs."""
+    W is None, W0 and cut are the differentiable inputs and the kernels form W0 * cut per edge in registers."""
 
     @staticmethod
     def forward(ctx, x, Y, W, W0, cut, edge_index, op):
-        _check_inputs(op, x, Y, W, edge_index)
-        x, Y, W = x.contiguous(), Y.contiguous(), W.contiguous()
+        _check_inputs(op, x, Y, W if W is not None else W0, edge_index)
+        x, Y = x.contiguous(), Y.contiguous()
+        W = W.contiguous() if W is not None else None
         n = x.shape[0]
         gr = graph_for(edge_index, n)
         rowptr, eids = gr.by_recv()
@@ -336,10 +400,11 @@ class _ConvFn(torch.autograd.Function):
         if ctx.factored:
             cutf = cut.reshape(-1).contiguous()
             # edges with cutoff 0 (padding, or beyond r_max in a skinned neighbour list) contribute exactly zero
-            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd_cut, op.module.handle, P(x), P(Y), P(W),
+            W0 = W0.contiguous()
+            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd_cut, op.module.handle, P(x), P(Y), P(W0),
                            P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n, _native.stream_of(x))
             ctx.cut_shape = cut.shape
-            ctx.save_for_backward(x, Y, W0.contiguous(), cutf)
+            ctx.save_for_backward(x, Y, W0, cutf)
         else:
             _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, P(x), P(Y), P(W), P(rowptr),
                            P(eids), P(gr.send), P(out), n, _native.stream_of(x))
@@ -424,8 +489,11 @@ class HipConvTP(torch.nn.Module):
         self.fuse_cutoff = True
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
+        if isinstance(tp_weights, CutoffProduct):
+            # the radial MLP's output times the cutoff, never formed: the kernels take the two factors
+            return _ConvFn.apply(node_feats, edge_attrs, None, tp_weights.w0, tp_weights.cut, edge_index, self)
         fac = _factored_weights(tp_weights) if self.fuse_cutoff and torch.is_grad_enabled() else None
         if fac is not None:
             W0, cut = fac
-            return _ConvFn.apply(node_feats, edge_attrs, tp_weights.detach(), W0, cut, edge_index, self)
+            return _ConvFn.apply(node_feats, edge_attrs, None, W0, cut, edge_index, self)
         return _ConvFn.apply(node_feats, edge_attrs, tp_weights, None, None, edge_index, self)

@@ -281,10 +281,11 @@ def source(spec):
                '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);']
     # ------------------------------------------------------------------------------------------- forward
     def fwd_kernel(cut):
-        """``cut`` (kernel ``conv_fwdc``): W = W0·c with a per-edge scalar c; an edge with c == 0 (padding, or past
-        r_max in a neighbour list with a skin) contributes exactly zero, so each chunk of 64 edges is first compacted
-        to its edges with c != 0 (ballot, then a per-wave LDS scatter by lane rank) and only those are walked.  Every
-        wave of the workgroup builds the same list, so the barriers stay uniform."""
+        """``cut`` (kernel ``conv_fwdc``): the weights are W0·c with a per-edge scalar c, read as W0 and scaled in
+        registers (the product is never formed in memory); an edge with c == 0 (padding, or past r_max in a
+        neighbour list with a skin) contributes exactly zero, so each chunk of 64 edges is first compacted to its
+        edges with c != 0 (ballot, then a per-wave LDS scatter by lane rank) and only those are walked.  Every wave
+        of the workgroup builds the same list, so the barriers stay uniform."""
         F = [
             f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwdc" if cut else "conv_fwd")}(',
             '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
@@ -308,7 +309,8 @@ def source(spec):
                   '    const int cnt = __popcll(kept);',
                   '    if (keep) sidx[wave][__popcll(kept & ((1ull << lane) - 1ull))] = my_e;',
                   '    if (cnt == 0) continue;',
-                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; }']
+                  '    float my_c = 0.0f;',
+                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e]; }']
         else:
             F += ['    const int cnt = min(MH_WAVE, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
@@ -317,7 +319,12 @@ def source(spec):
         F += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
         F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
         F += ['    }', '    for (int j = 0; j < cnt; ++j) {']
-        F += copy('xv', 'xn', nx) + copy('w', 'wn', nk)
+        F += copy('xv', 'xn', nx)
+        if cut:
+            F += ['      const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_c), j));']
+            F += [f'      const float w{k} = wn{k} * cj;' for k in range(nk)]
+        else:
+            F += copy('w', 'wn', nk)
         F += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
         F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
         F += ['      }']

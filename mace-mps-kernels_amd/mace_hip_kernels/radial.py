@@ -28,6 +28,7 @@ import numpy as np
 import torch
 
 from . import _native
+from . import conv as _conv
 
 BLOCK = 256          # 4 waves x 16 edges
 EDGES = 64           # edges per workgroup
@@ -403,4 +404,5 @@ class HipRadialMLP(torch.nn.Module):
         self.tag = 'radial_mlp'
 
     def forward(self, ef):
-        return _MLPFn.apply(ef, self)
+        # the output's product with MACE's cutoff column is handed to the convolution unformed (conv.RadialWeights)
+        return _MLPFn.apply(ef, self).as_subclass(_conv.RadialWeights)
