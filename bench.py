@@ -56,8 +56,8 @@ def _time_calls(model, batch, steps, warmup, sync):
 def _kernel_table(met, batch, n_real_edges, summary):
     """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only)."""
     import torch
-    from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipSphericalHarmonics,
-                                  HipSymmetricContraction)
+    from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipReshapeIrreps,
+                                  HipSphericalHarmonics, HipSymmetricContraction)
     n = batch['positions'].shape[0]
     n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
     rows = {}
@@ -86,18 +86,27 @@ def _kernel_table(met, batch, n_real_edges, summary):
         elif isinstance(m, HipNodeLinear):
             s = m.spec
             bf, bb = s.bytes(n)
-            rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n), 'lin_fwd')
-            rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n), 'lin_bwd')
+            rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n), s.kname('lin_fwd'))
+            rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n), s.kname('lin_bwd'))
+        elif isinstance(m, HipReshapeIrreps):
+            nb = 2 * 4 * n * m.spec.dim                 # a permutation: the rows read once and written once
+            rows[f'perm_fwd[{m.tag}]'] = (nb, 0, m.spec.kname('perm_fwd'))
+            rows[f'perm_bwd[{m.tag}]'] = (nb, 0, m.spec.kname('perm_bwd'))
         elif isinstance(m, HipRadialEmbedding):
             bf, bb = m.spec.bytes(batch['edge_index'].shape[1])
-            rows[f'emb_fwd[{m.tag}]'] = (bf, 0, 'emb_fwd')
-            rows[f'emb_bwd[{m.tag}]'] = (bb, 0, 'emb_bwd')
+            rows[f'emb_fwd[{m.tag}]'] = (bf, 0, m.spec.kname('emb_fwd'))
+            rows[f'emb_bwd[{m.tag}]'] = (bb, 0, m.spec.kname('emb_bwd'))
         elif isinstance(m, HipRadialMLP):
             s = m.spec                                  # every edge of the padded list is evaluated
             E = batch['edge_index'].shape[1]
             bf, bb = s.bytes(E)
-            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(E), 'mlp_fwd')
-            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(E), 'mlp_bwd')
+            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(E), s.kname('mlp_fwd'))
+            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(E), s.kname('mlp_bwd'))
+    # edge geometry: positions, shifts and the edge list in, vectors and lengths out; backward: vectors, lengths and
+    # their gradients plus both CSRs in, the position gradient out
+    E = batch['edge_index'].shape[1]
+    rows['geom_fwd'] = (4 * (3 * n + 3 * E + 2 * E + 3 * E + E), 0, 'geom_fwd')
+    rows['geom_bwd'] = (4 * (8 * E + 2 * (n + 1) + 2 * E + 3 * n), 0, 'geom_bwd')
     out = {}
     for tag, (cnt, ms) in summary.items():
         nbytes, flops, sym = rows.get(tag, (0, 0, None))
@@ -138,6 +147,8 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
                 cpu=platform.processor() or platform.machine(), seconds=round(dt * steps, 2))
 
 
+# symbol prefixes of this package's generated kernels
+HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_')
 COPY_BYTES = 1 << 30          # size of the calibration copy (read 1 GiB, write 1 GiB) of --profile
 
 
@@ -344,7 +355,7 @@ def _summarize(a):
         wf = COPY_BYTES / 1024 / per['WRITE_SIZE'][cal[0]]
         kern = {}
         for k in per['FETCH_SIZE']:
-            if any(f in k for f in ('conv_', 'sc_')) and k in per['WRITE_SIZE']:
+            if any(k.startswith(f) for f in HIP_KERNEL_PREFIXES) and k in per['WRITE_SIZE']:
                 fk, wk = per['FETCH_SIZE'][k], per['WRITE_SIZE'][k]
                 kern[k] = dict(fetch_kib=round(fk, 1), write_kib=round(wk, 1), traffic_bytes=(fk * ff + wk * wf) * 1024)
         with open(a.traffic_json, 'w') as fh:
@@ -365,7 +376,7 @@ def main():
     ap.add_argument('--pmc-write', metavar='DIR')
     ap.add_argument('--pmc', metavar='DIR', action='append', help='counter run to tabulate per kernel (repeatable)')
     ap.add_argument('--traffic-json', metavar='PATH', help='with both counter runs: write calibrated traffic per kernel')
-    ap.add_argument('--traffic-source', default='profiles/conv_sc_traffic_cfg2.md')
+    ap.add_argument('--traffic-source', default='profiles/kernel_traffic_cfg2.md')
     ap.add_argument('--filter', default='conv_,sc_,bitwise_not', help='kernel-name substrings kept in counter tables')
     ap.add_argument('--top', type=int, default=30)
     ap.add_argument('--steps', type=int, default=20)

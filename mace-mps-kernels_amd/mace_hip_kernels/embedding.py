@@ -75,7 +75,7 @@ class EmbSpec:
         return E * 4 * (1 + self.n + 1), E * 4 * (1 + self.n + 1 + 1)
 
     def kname(self, base):
-        return base
+        return f'{base}_n{self.n}_p{self.p}'
 
 
 def source(spec):
@@ -94,14 +94,14 @@ def source(spec):
             f'  const float env = 1.f - {_lit(c1)} * up + {_lit(c2)} * (up * u) - {_lit(c3)} * (up * u * u);',
             '  const float cut = in ? env : 0.f;']
     L = [_native.device_header(), f'#define BLOCK {BLOCK}',
-         f'extern "C" __global__ __launch_bounds__(BLOCK) void emb_fwd(const float* __restrict__ len,',
+         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("emb_fwd")}(const float* __restrict__ len,',
          '    float* __restrict__ feats, float* __restrict__ cutoff, long long E) {'] + head
     L += ['  cutoff[e] = cut;']
     for k, w in enumerate(spec.w):
         L.append(f'  feats[e * {n} + {k}] = ({_lit(spec.pref)} * sinf({_lit(w)} * x)) / x * cut;')
     L += ['}', '']
     # backward: d cut/dx = env'(u) / r_max inside the cutoff; d feat_k/dx = b_k' cut + b_k cut'
-    L += ['extern "C" __global__ __launch_bounds__(BLOCK) void emb_bwd(const float* __restrict__ len,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("emb_bwd")}(const float* __restrict__ len,',
           '    const float* __restrict__ gfeats, const float* __restrict__ gcut, float* __restrict__ glen, long long E) {']
     L += head
     L += [f'  const float denv = (-{_lit(c1 * p)} * {powu(p - 1)} + {_lit(c2 * (p + 1))} * up'
@@ -167,8 +167,8 @@ class HipRadialEmbedding(torch.nn.Module):
         code = _native.compile_source(self.source)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
-            self.module = _native.Module(code, {_native.MH_EMB_FWD: ('emb_fwd', BLOCK, BLOCK),
-                                                _native.MH_EMB_BWD: ('emb_bwd', BLOCK, BLOCK)})
+            self.module = _native.Module(code, {_native.MH_EMB_FWD: (self.spec.kname('emb_fwd'), BLOCK, BLOCK),
+                                                _native.MH_EMB_BWD: (self.spec.kname('emb_bwd'), BLOCK, BLOCK)})
         self.out_dim = self.spec.n
         self.original = [mod]
         self.tag = 'radial_embedding'

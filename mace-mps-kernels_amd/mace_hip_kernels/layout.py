@@ -34,6 +34,9 @@ class ReshapeSpec:
         self.D = sum(2 * l + 1 for _, l in self.blocks)
         self.dim = self.mul * self.D
 
+    def kname(self, base):
+        return f'{base}_m{self.mul}_d{self.D}'
+
     def perm(self):
         """src[j]: the irreps-layout index that output index j (= u D + o_l + m) reads."""
         src, o = [0] * self.dim, 0
@@ -63,7 +66,8 @@ def source(spec):
     sel.append('  }')
     body = ['  const int u = j / {D}, c = j - u * {D};'.format(D=spec.D), '  int s = 0;'] + sel
     L = [_native.device_header(), f'#define BLOCK {BLOCK}']
-    for name, rd, wr in (('perm_fwd', 'x[base + s]', 'y[base + j]'), ('perm_bwd', 'x[base + j]', 'y[base + s]')):
+    for name, rd, wr in ((spec.kname('perm_fwd'), 'x[base + s]', 'y[base + j]'),
+                         (spec.kname('perm_bwd'), 'x[base + j]', 'y[base + s]')):
         L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {name}(const float* __restrict__ x,',
               '    float* __restrict__ y, int N) {',
               f'  const int n0 = mh_xcd_block(blockIdx.x, gridDim.x) * {NODES};',
@@ -115,8 +119,8 @@ class HipReshapeIrreps(torch.nn.Module):
         code = _native.compile_source(self.source)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
-            self.module = _native.Module(code, {_native.MH_PERM_FWD: ('perm_fwd', BLOCK, NODES),
-                                                _native.MH_PERM_BWD: ('perm_bwd', BLOCK, NODES)})
+            self.module = _native.Module(code, {_native.MH_PERM_FWD: (self.spec.kname('perm_fwd'), BLOCK, NODES),
+                                                _native.MH_PERM_BWD: (self.spec.kname('perm_bwd'), BLOCK, NODES)})
         self.irreps = mod.irreps
         self.original = [mod]
         self.tag = 'reshape'

@@ -126,6 +126,10 @@ class LinSpec:
             out[:, oo:oo + mo * d] += t.reshape(x.shape[0], -1)
         return out
 
+    def kname(self, base):
+        """Kernel symbol of this module (shape-tagged so profiles tell the modules apart)."""
+        return f'{base}_i{self.Din}_o{self.Dout}' + (f'_v{self.V}' if self.V else '')
+
     def flops(self, n):
         """Multiply-adds x 2 of the dense map over n nodes (attribute terms all counted)."""
         return 2 * n * sum(w.size * (2 * self.in_blocks[i][1] + 1) for (i, o), w in self.Wio.items())
@@ -355,9 +359,9 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout):
 def source(spec):
     """HIP source of ``lin_fwd`` and ``lin_bwd`` for one module."""
     L = [_native.device_header(), 'typedef float mh_f4 __attribute__((ext_vector_type(4)));', '']
-    L += _kernel('lin_fwd', spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din, spec.Dout)
+    L += _kernel(spec.kname('lin_fwd'), spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din, spec.Dout)
     if spec.has_bwd:
-        L += _kernel('lin_bwd', spec.out_blocks, spec.in_blocks, spec.bterms, spec.V, spec.Dout, spec.Din)
+        L += _kernel(spec.kname('lin_bwd'), spec.out_blocks, spec.in_blocks, spec.bterms, spec.V, spec.Dout, spec.Din)
     return '\n'.join(L)
 
 
@@ -430,9 +434,9 @@ class HipNodeLinear(torch.nn.Module):
         code = _native.compile_source(self.source)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
-            kernels = {_native.MH_LIN_FWD: ('lin_fwd', BLOCK, _tiles(s.out_blocks), len(_grid_y(s.out_blocks)))}
+            kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK, _tiles(s.out_blocks), len(_grid_y(s.out_blocks)))}
             if s.has_bwd:
-                kernels[_native.MH_LIN_BWD] = ('lin_bwd', BLOCK, _tiles(s.in_blocks), len(_grid_y(s.in_blocks)))
+                kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK, _tiles(s.in_blocks), len(_grid_y(s.in_blocks)))
             self.module = _native.Module(code, kernels)
         self.register_buffer('W', torch.tensor(s.W, dtype=torch.float32, device=dev), persistent=False)
         self.register_buffer('Wt', torch.tensor(s.Wt, dtype=torch.float32, device=dev), persistent=False)

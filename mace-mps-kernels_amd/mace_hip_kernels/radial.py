@@ -100,6 +100,10 @@ class MLPSpec:
             h = c * z / (1.0 + np.exp(-z))
         return h @ self.A[-1]
 
+    def kname(self, base):
+        """Kernel symbol of this network (layer widths in the name, so profiles tell the blocks apart)."""
+        return f'{base}_' + 'x'.join(str(h) for h in self.hs)
+
     def flops(self, E):
         return 2 * E * sum(a * b for a, b in zip(self.hs, self.hs[1:]))
 
@@ -229,7 +233,7 @@ def source(spec):
 
     # ------------------------------------------------------------------ forward
     # hidden weights transposed [j][k + PAD]; output layer from WlT [NW][HL], chunks [CHUNK cols][HL + PAD]
-    F = head('mlp_fwd', 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
+    F = head(spec.kname('mlp_fwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
              'float* __restrict__ W0, long long E', lds_fwd)
     F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(True, True)
     hl = f'h{nh - 1}'
@@ -260,7 +264,7 @@ def source(spec):
     # ------------------------------------------------------------------ backward
     # dL/dh_last = gW Wl^T first (chunks of Wl [HL][NW] as [HL][CHUNK + PAD]; gW one float4 per lane per 16 columns,
     # K order k = 16 t + 4 q + r), then the hidden layers recomputed from the natural-layout weights and walked back
-    B = head('mlp_bwd', 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
+    B = head(spec.kname('mlp_bwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
              'const float* __restrict__ gW, float* __restrict__ gef, long long E', lds_bwd)
     B += [f'  mh_f4 dh[{TL}];'] + [f'  dh[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
     B += [f'  mh_f4 {pres};'] + pre_load('Wl', '0', NW, CHUNK, '  ')
@@ -393,8 +397,8 @@ class HipRadialMLP(torch.nn.Module):
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
             self.module = _native.Module(code, {
-                _native.MH_MLP_FWD: ('mlp_fwd', BLOCK, EDGES),
-                _native.MH_MLP_BWD: ('mlp_bwd', BLOCK, EDGES),
+                _native.MH_MLP_FWD: (self.spec.kname('mlp_fwd'), BLOCK, EDGES),
+                _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), BLOCK, EDGES),
             })
         pw = packed_weights(self.spec)
         for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1])):
