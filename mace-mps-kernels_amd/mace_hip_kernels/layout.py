@@ -3,8 +3,8 @@ MACE's ``reshape_irreps`` on MI355X: the per-node permutation from e3nn's irreps
 (channel-major inside each irrep block: index off_l + u (2l+1) + m) to the symmetric contraction's layout
 [N, mul, sum_l (2l+1)] (index u * D + o_l + m, D = sum_l (2l+1)).  In PyTorch it is a slice, a reshape and a
 concatenation per block, and its backward a zero-filled full-size tensor per slice; here each direction is one
-kernel: every thread moves one element of a node's row (coalesced on the written side, a gather inside the same
-row on the read side), and the backward applies the inverse permutation.
+kernel: a workgroup copies four node rows into LDS (coalesced), then writes the permuted rows (coalesced), the
+gather happening in LDS; the backward applies the inverse permutation the same way.
 """
 import torch
 
@@ -19,6 +19,8 @@ def reshape_supported(mod):
         muls = {mul for mul, _ in mod.irreps}
         if len(muls) != 1:
             return False, 'blocks of different multiplicities'
+        if muls.pop() % 4:
+            return False, 'multiplicity not a multiple of 4'
     except (AttributeError, TypeError) as e:
         return False, f'not a reshape_irreps module ({e})'
     return True, ''
@@ -52,31 +54,65 @@ class ReshapeSpec:
 
 
 def source(spec):
-    # src(j): u = j / D, c = j % D; the block holding column c gives (offset, dimension, column start)
+    """Each workgroup moves NODES whole rows: a coalesced copy of the rows into LDS, then a coalesced write of the
+    permuted rows (the gather happens in LDS)."""
     conds, off, o = [], 0, 0
     for mul, l in spec.blocks:
         d = 2 * l + 1
         conds.append((o + d, off, d, o))
         off += mul * d
         o += d
-    sel = []
-    for k, (end, boff, d, o0) in enumerate(conds):
-        kw = 'if' if k == 0 else '} else if'
-        sel.append(f'  {kw} (c < {end}) {{ s = {boff} + u * {d} + (c - {o0}); ')
-    sel.append('  }')
-    body = ['  const int u = j / {D}, c = j - u * {D};'.format(D=spec.D), '  int s = 0;'] + sel
+
+    def src_of(ind):
+        # forward: SC-layout index j (u = j / D, column c inside the block of dimension d) reads irreps index s
+        L = [f'{ind}const int u = j / {spec.D}, c = j - u * {spec.D};', f'{ind}int s = 0;']
+        for k, (end, boff, d, o0) in enumerate(conds):
+            kw = 'if' if k == 0 else '} else if'
+            L.append(f'{ind}{kw} (c < {end}) {{ s = {boff} + u * {d} + (c - {o0});')
+        L.append(f'{ind}}}')
+        return L
+
+    def inv_of(ind):
+        # backward: irreps index j (block at offset boff, dimension d: u = (j - boff) / d) reads SC index s
+        L = [f'{ind}int s = 0;']
+        for k, (end, boff, d, o0) in enumerate(conds):
+            kw = 'if' if k == 0 else '} else if'
+            bend = boff + spec.mul * d
+            L.append(f'{ind}{kw} (j < {bend}) {{ const int u = (j - {boff}) / {d}; '
+                     f's = u * {spec.D} + {o0} + (j - {boff} - u * {d});')
+        L.append(f'{ind}}}')
+        return L
+
+    n4 = NODES * spec.dim // 4                       # float4s per workgroup
+    it = -(-n4 // BLOCK)
     L = [_native.device_header(), f'#define BLOCK {BLOCK}']
-    for name, rd, wr in ((spec.kname('perm_fwd'), 'x[base + s]', 'y[base + j]'),
-                         (spec.kname('perm_bwd'), 'x[base + j]', 'y[base + s]')):
+    for name, fwd in ((spec.kname('perm_fwd'), True), (spec.kname('perm_bwd'), False)):
         L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {name}(const float* __restrict__ x,',
               '    float* __restrict__ y, int N) {',
+              f'  __shared__ __align__(16) float rows[{NODES * spec.dim}];',
               f'  const int n0 = mh_xcd_block(blockIdx.x, gridDim.x) * {NODES};',
-              f'  for (int f = threadIdx.x; f < {NODES * spec.dim}; f += BLOCK) {{',
-              f'    const int nl = f / {spec.dim}, j = f - nl * {spec.dim};',
-              '    if (n0 + nl >= N) break;',
-              f'    const size_t base = (size_t)(n0 + nl) * {spec.dim};']
-        L += ['  ' + b for b in body]
-        L += [f'    {wr} = {rd};', '  }', '}', '']
+              f'  const int nn = min({NODES}, N - n0), m4 = nn * {spec.dim // 4};',
+              f'  const size_t base = (size_t)n0 * {spec.dim};',
+              '  const float4* __restrict__ xs = reinterpret_cast<const float4*>(x + base);',
+              '  float4* __restrict__ ys = reinterpret_cast<float4*>(y + base);',
+              '  float4 v[%d];' % it,
+              '#pragma unroll',
+              f'  for (int i = 0; i < {it}; ++i) {{ const int f = threadIdx.x + i * BLOCK; v[i] = xs[min(f, m4 - 1)]; }}',
+              '#pragma unroll',
+              f'  for (int i = 0; i < {it}; ++i) {{ const int f = threadIdx.x + i * BLOCK;',
+              '    if (f < m4) reinterpret_cast<float4*>(rows)[f] = v[i]; }',
+              '  __syncthreads();',
+              '  for (int g = threadIdx.x; g < m4; g += BLOCK) {',
+              f'    const int nl = g / {spec.dim // 4}, j0 = 4 * (g - nl * {spec.dim // 4});',
+              '    float o[4];',
+              '#pragma unroll',
+              '    for (int e = 0; e < 4; ++e) {',
+              '      const int j = j0 + e;']
+        L += src_of('      ') if fwd else inv_of('      ')
+        L += [f'      o[e] = rows[nl * {spec.dim} + s];',
+              '    }',
+              '    ys[g] = make_float4(o[0], o[1], o[2], o[3]);',
+              '  }', '}', '']
     return '\n'.join(L)
 
 

@@ -11,9 +11,9 @@ with a == 1 (V = 1 term) for the linear and a = node_attrs for skip_tp.  On the 
 dozen launches each (slices, einsums through batched GEMMs, path-weight multiplies, a concatenation) and their
 backward about as many again, each materialising a full-size tensor.  Here each direction is ONE launch of a
 generated kernel: per output block, a GEMM with rows = (node, m) pairs, columns = output channels w, and
-K = (input block, u, v), on the fp32 matrix cores (v_mfma_f32_16x16x4f32).  A workgroup (4 waves) owns 16 // d whole
-nodes (<= 16 rows, one MFMA row tile) and 64 output channels, and its waves split the K loop (many small
-workgroups: the node counts of a batch are a few thousand, and the chip has 256 CUs).  Attribute terms v whose
+K = (input block, u, v), on the fp32 matrix cores (v_mfma_f32_16x16x4f32).  A tile is 16 // d whole nodes (<= 16
+rows, one MFMA row tile) and 64 output channels (small tiles: the node counts of a batch are a few thousand, and
+the chip has 256 CUs); long K loops run one tile per wave, short ones split K over a workgroup's waves.  Attribute terms v whose
 a[n, v] is zero for every node of the tile are skipped (a one-hot element encoding leaves only the tile's species),
 which is exact: they add 0.
 
@@ -32,7 +32,8 @@ import torch
 from . import _native
 
 KC = 32              # K chunk (input channels u of one attribute v) loaded per step of a wave
-BLOCK = 256          # 4 waves, splitting the K loop of one 16-row tile
+BLOCK = 256          # 4 waves, one 16-row tile each
+WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of a workgroup tile: one MFMA row tile
 MAXMUL = 512         # largest multiplicity of a block
 
@@ -195,164 +196,224 @@ def _grid_y(blocks):
     return [(o, cg) for o, (mo, *_) in enumerate(blocks) for cg in range(mo // _cw(mo))]
 
 
-def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout):
-    """HIP source of one direction.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x
-    the node tile: TN = 16 // d whole nodes, i.e. <= 16 rows (node, m) — one MFMA row tile.
+def _tiles_mode(terms_o, in_blocks, V):
+    """One tile per wave with the whole K loop (long K: the pipeline hides the load latency), or one tile per
+    workgroup with K split over the waves (short K, or attribute terms: more waves in flight)."""
+    return V == 0 and sum(-(-in_blocks[i][0] // KC) for i, _ in terms_o) >= 8
 
-    The four waves split K: the chunk sequence c = (active attribute v, 32 input channels) of each term is dealt
-    round-robin to the waves, and each wave loads its operands straight into registers in the MFMA lane layout
-    (16x16x4: lane (i, kq) = (lane % 16, lane / 16) holds A[i][4s + kq] and B[4s + kq][16 ct + i]), the next chunk
-    in flight while the current one is multiplied.  No LDS and no barrier in the K loop; the four partial tiles are
-    summed through LDS at the end and written back node by node (each node's CW * d outputs are contiguous)."""
+
+def _nodes_per_group(terms_o, in_blocks, V, l):
+    tn = ROWS // (2 * l + 1)
+    return WAVES * tn if (terms_o and _tiles_mode(terms_o, in_blocks, V)) else tn
+
+
+def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH):
+    """Register loads of chunk c of term i: A (x, times the attribute) and B (weights) in MFMA lane layout.
+
+    K order inside a chunk: lane group kq takes k = k0 + 8 kq + st at step st, so a lane's 8 values of x are
+    consecutive (two float4 loads for scalars); column order inside a group of 16 columns: lane c16 takes the CT
+    adjacent columns CT c16 + ct (one vector load of W per step)."""
     VV = max(V, 1)
+    vsel = f'vlist[1 + c / {NCH}]' if V else '0'
+    vecx = D == 1 and Din % 4 == 0 and oi % 4 == 0 and mi % 8 == 0
+    wt = {4: 'float4', 2: 'float2', 1: 'float'}[CT]
+    L = [f'__device__ __forceinline__ void {fn}_ld{i}(const float* __restrict__ x, const float* __restrict__ attr,',
+         '    const float* __restrict__ W, const int* __restrict__ vlist, int n0, int col0, int anl, int am,',
+         f'    int q, int c16, int c, float (&ra)[{KC // 4}], float (&rb)[{KC // 4}][{CT}]) {{',
+         f'  const int v = {vsel}, k0 = (c % {NCH}) * {KC} + 8 * q;',
+         '  (void)v; (void)vlist; (void)attr;',
+         f'  const float* __restrict__ xr = x + (size_t)(n0 + anl) * {Din} + {oi} + am;']
+    if V:
+        L.append(f'  const float s = attr[(size_t)(n0 + anl) * {V} + v];')
+    if vecx:
+        # mi % 8 == 0: the lane's 8 channels are all in range or all out of range
+        L += [f'  const bool okx = k0 < {mi};',
+              f'  const float4* __restrict__ xv = reinterpret_cast<const float4*>(xr + (okx ? k0 : 0));',
+              '  const float4 x0 = xv[0], x1 = xv[1];',
+              '  const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};']
+    L += ['#pragma unroll',
+          f'  for (int st = 0; st < {KC // 4}; ++st) {{',
+          '    const int k = k0 + st;',
+          f'    const bool ok = k < {mi};',
+          f'    const int kc = ok ? k : {mi - 1};      // every load in bounds and unconditional']
+    if vecx:
+        L.append(f'    ra[st] = okx ? xs[st]{" * s" if V else ""} : 0.f;')
+    else:
+        L += [f'    const float xa = xr[kc * {D}];',
+              f'    ra[st] = ok ? xa{" * s" if V else ""} : 0.f;']
+    L += [f'    const {wt} wv = *reinterpret_cast<const {wt}*>(W + {woff} + ((size_t)kc * {VV} + v) * {mo} + col0'
+          f' + {CT} * c16);']
+    comps = ['x', 'y', 'z', 'w'][:CT] if CT > 1 else [None]
+    for ct, cmp in enumerate(comps):
+        L.append(f'    rb[st][{ct}] = ok ? wv{"." + cmp if cmp else ""} : 0.f;')
+    L += ['  }', '}', '']
+    return L
+
+
+def _kloop(ld, CT, first, step, count, ind):
+    """Pipelined K loop over `count` chunks first, first + step, ...: two register sets, unrolled by two so every
+    array index is a constant and no branch separates a prefetch from the MFMAs that use it (the compiler would sink
+    the loads past it); every prefetch is unconditional (clamped to the last chunk)."""
+    mm = ['#pragma unroll',
+          f'{ind}  for (int st = 0; st < {KC // 4}; ++st) {{',
+          '#pragma unroll',
+          f'{ind}    for (int ct = 0; ct < {CT}; ++ct)',
+          f'{ind}      acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(raX[st], rbX[st][ct], acc[ct], 0, 0, 0);',
+          f'{ind}  }}']
+    L = [f'{ind}float ra0[{KC // 4}], rb0[{KC // 4}][{CT}], ra1[{KC // 4}], rb1[{KC // 4}][{CT}];',
+         f'{ind}const int nw = {count}, last = {first} + (nw - 1) * {step};',
+         f'{ind}if (nw > 0) {ld}, {first}, ra0, rb0);',
+         f'{ind}int c = {first};',
+         f'{ind}for (int p = 0; p < nw / 2; ++p, c += {2 * step}) {{',
+         f'{ind}  {ld}, min(c + {step}, last), ra1, rb1);',
+         f'{ind}  __builtin_amdgcn_sched_barrier(0);']
+    L += [l.replace('raX', 'ra0').replace('rbX', 'rb0') for l in mm]
+    L += [f'{ind}  {ld}, min(c + {2 * step}, last), ra0, rb0);',
+          f'{ind}  __builtin_amdgcn_sched_barrier(0);']
+    L += [l.replace('raX', 'ra1').replace('rbX', 'rb1') for l in mm]
+    L += [f'{ind}}}', f'{ind}if (nw & 1) {{']
+    L += [l.replace('raX', 'ra0').replace('rbX', 'rb0') for l in mm]
+    L += [f'{ind}}}']
+    return L
+
+
+def _mask(V, first, count):
+    """The workgroup's list of attributes that are nonzero somewhere in its nodes (vlist[0] = count)."""
     VW = (V + 31) // 32
+    return [f'  if (t < {VW}) amask[t] = 0u;',
+            '  __syncthreads();',
+            f'  for (int f = t; f < {count} * {V}; f += {BLOCK}) {{',
+            f'    if (attr[(size_t){first} * {V} + f] != 0.f) {{ const int v = f % {V}; '
+            'atomicOr(&amask[v >> 5], 1u << (v & 31)); }',
+            '  }',
+            '  __syncthreads();',
+            '  if (t == 0) {',
+            '    int c = 0;',
+            f'    for (int w = 0; w < {VW}; ++w) {{',
+            '      unsigned b = amask[w];',
+            '      while (b) { vlist[1 + c++] = w * 32 + __builtin_ctz(b); b &= b - 1u; }',
+            '    }',
+            '    vlist[0] = c;',
+            '  }',
+            '  __syncthreads();',
+            '  const int nact = vlist[0];']
+
+
+def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout):
+    """HIP source of one direction.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x a
+    group of nodes.  A tile is TN = 16 // d whole nodes, i.e. <= 16 rows (node, m) — one MFMA row tile — and CW
+    channels.  Each block runs in one of two modes (``_tiles_mode``):
+
+    * one tile per wave, WAVES tiles per workgroup, each wave running the whole K loop for its tile and storing it
+      from the result registers (no LDS, no barrier in the loop);
+    * one tile per workgroup, its waves splitting K (chunks dealt round-robin) and the four partial tiles summed
+      through LDS, then written node by node (each node's CW * d outputs are contiguous).
+
+    K is walked in chunks c = (active attribute v, 32 input channels); operands are loaded straight into registers
+    in the MFMA lane layout (16x16x4: lane (i, kq) = (lane % 16, lane / 16) holds A[i][4s + kq] and B[4s + kq][16 ct
+    + i]) with the next chunk in flight."""
     fns, cases = [], []
     for o, (mo, l, oo, _) in enumerate(out_blocks):
         D = 2 * l + 1
         TN = ROWS // D
-        R = TN * D
         CW = _cw(mo)
         CT = CW // 16
         fn = f'{name}_b{o}'
+        tiles = bool(terms[o]) and _tiles_mode(terms[o], in_blocks, V)
+        G = WAVES * TN if tiles else TN                       # nodes per workgroup
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
-             '    const float* __restrict__ W, float* __restrict__ out, int N, int tile, int cg, float* __restrict__ red,',
+             '    const float* __restrict__ W, float* __restrict__ out, int N, int group, int cg, float* __restrict__ red,',
              '    unsigned* __restrict__ amask, int* __restrict__ vlist) {',
-             f'  const int n0 = tile * {TN};',
-             '  if (n0 >= N) return;',
-             f'  const int nn = min({TN}, N - n0);',
+             f'  const int g0 = group * {G};                 // first node of the workgroup',
+             '  if (g0 >= N) return;',
+             f'  const int ng = min({G}, N - g0);',
              f'  const int t = threadIdx.x, col0 = cg * {CW};']
         if not terms[o]:
-            L += [f'  for (int f = t; f < nn * {CW * D}; f += {BLOCK}) {{',
+            L += [f'  for (int f = t; f < ng * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D};',
-                  f'    out[(size_t)(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
+                  f'    out[(size_t)(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
                   '  }', '}', '']
             fns += L
             cases.append((o, fn))
             continue
-        L += ['  const int wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
-              # the lane's A row (node, m); rows past the tile read row 0 (their outputs are never stored)
-              f'  const int arow = c16 < nn * {D} ? c16 : 0;',
+        L += ['  const int wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;']
+        if tiles:
+            L += [f'  const int n0 = g0 + wave * {TN};                      // this wave\'s tile',
+                  '  const bool wlive = n0 < N;',
+                  f'  const int nn = wlive ? min({TN}, N - n0) : 0;',
+                  '  const int nb = wlive ? n0 : g0;                        // load base: always a valid node']
+        else:
+            L += ['  const int n0 = g0, nn = ng, nb = g0;', '  const bool wlive = true;']
+        # the lane's A row (node, m); rows past the tile read row 0 (their outputs are never stored)
+        L += [f'  const int arow = c16 < nn * {D} ? c16 : 0;',
               f'  const int anl = arow / {D}, am = arow - anl * {D};',
               f'  mh_f4 acc[{CT}];',
               '#pragma unroll',
               f'  for (int c = 0; c < {CT}; ++c) acc[c] = mh_f4{{0.f, 0.f, 0.f, 0.f}};']
         if V:
-            L += [f'  if (t < {VW}) amask[t] = 0u;',
-                  '  __syncthreads();',
-                  f'  for (int f = t; f < nn * {V}; f += {BLOCK}) {{',
-                  f'    if (attr[(size_t)n0 * {V} + f] != 0.f) {{ const int v = f % {V}; '
-                  'atomicOr(&amask[v >> 5], 1u << (v & 31)); }',
-                  '  }',
-                  '  __syncthreads();',
-                  '  if (t == 0) {',
-                  '    int c = 0;',
-                  f'    for (int w = 0; w < {VW}; ++w) {{',
-                  '      unsigned b = amask[w];',
-                  '      while (b) { vlist[1 + c++] = w * 32 + __builtin_ctz(b); b &= b - 1u; }',
-                  '    }',
-                  '    vlist[0] = c;',
-                  '  }',
-                  '  __syncthreads();',
-                  '  const int nact = vlist[0];']
+            L += _mask(V, 'g0', 'ng')
         for (i, woff) in terms[o]:
             mi, li, oi, _ = in_blocks[i]
             assert li == l
             NCH = -(-mi // KC)
             nchunks = f'nact * {NCH}' if V else f'{NCH}'
-            vsel = f'vlist[1 + c / {NCH}]' if V else '0'
-            # K order inside a chunk: lane group kq takes k = k0 + 8 kq + st at step st, so a lane's 8 values of x
-            # are consecutive (two float4 loads for scalars); column order inside the group: lane c16 takes the CT
-            # adjacent columns CT c16 + ct (one vector load of W per step)
-            vecx = D == 1 and Din % 4 == 0 and oi % 4 == 0 and mi % 8 == 0
-            wt = {4: 'float4', 2: 'float2', 1: 'float'}[CT]
-            L1 = [f'__device__ __forceinline__ void {fn}_ld{i}(const float* __restrict__ x, const float* __restrict__ attr,',
-                  '    const float* __restrict__ W, const int* __restrict__ vlist, int n0, int col0, int anl, int am,',
-                  f'    int q, int c16, int c, float (&ra)[{KC // 4}], float (&rb)[{KC // 4}][{CT}]) {{',
-                  f'  const int v = {vsel}, k0 = (c % {NCH}) * {KC} + 8 * q;',
-                  '  (void)v; (void)vlist; (void)attr;',
-                  f'  const float* __restrict__ xr = x + (size_t)(n0 + anl) * {Din} + {oi} + am;']
-            if V:
-                L1.append(f'  const float s = attr[(size_t)(n0 + anl) * {V} + v];')
-            if vecx:
-                # mi % 8 == 0: the lane's 8 channels are all in range or all out of range
-                L1 += [f'  const bool okx = k0 < {mi};',
-                       f'  const float4* __restrict__ xv = reinterpret_cast<const float4*>(xr + (okx ? k0 : 0));',
-                       '  const float4 x0 = xv[0], x1 = xv[1];',
-                       '  const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};']
-            L1 += ['#pragma unroll',
-                   f'  for (int st = 0; st < {KC // 4}; ++st) {{',
-                   '    const int k = k0 + st;',
-                   f'    const bool ok = k < {mi};',
-                   f'    const int kc = ok ? k : {mi - 1};      // every load in bounds and unconditional']
-            if vecx:
-                L1.append(f'    ra[st] = okx ? xs[st]{" * s" if V else ""} : 0.f;')
+            fns += _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH)
+            ld = f'{fn}_ld{i}(x, attr, W, vlist, nb, col0, anl, am, q, c16'
+            if tiles:
+                L += ['  if (wlive) {', f'    const int nch = {nchunks};']
+                L += _kloop(ld, CT, '0', 1, 'nch', '    ')
             else:
-                L1 += [f'    const float xa = xr[kc * {D}];',
-                       f'    ra[st] = ok ? xa{" * s" if V else ""} : 0.f;']
-            L1 += [f'    const {wt} wv = *reinterpret_cast<const {wt}*>(W + {woff} + ((size_t)kc * {VV} + v) * {mo} + col0'
-                   f' + {CT} * c16);']
-            comps = ['x', 'y', 'z', 'w'][:CT] if CT > 1 else [None]
-            for ct, cmp in enumerate(comps):
-                L1.append(f'    rb[st][{ct}] = ok ? wv{"." + cmp if cmp else ""} : 0.f;')
-            L1 += ['  }', '}', '']
-            fns += L1
-            ld = f'{fn}_ld{i}(x, attr, W, vlist, n0, col0, anl, am, q, c16'
-            mm = ['#pragma unroll',
-                  f'      for (int st = 0; st < {KC // 4}; ++st) {{',
+                L += ['  {', f'    const int nch = {nchunks};']
+                L += _kloop(ld, CT, 'wave', WAVES, 'wave < nch ? (nch - wave + 3) / 4 : 0', '    ')
+            L += ['  }']
+        if tiles:
+            # the tile straight from the result registers: lane (c16, q) holds rows 4q + r, columns CT c16 + ct
+            L += ['  if (wlive) {',
                   '#pragma unroll',
-                  f'        for (int ct = 0; ct < {CT}; ++ct)',
-                  '          acc[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(raX[st], rbX[st][ct], acc[ct], 0, 0, 0);',
-                  '      }']
-            # two register sets, the loop unrolled by two so that every array index is a constant, and no branch
-            # between a prefetch and the MFMAs that use it (the compiler would sink the loads past it)
-            L += ['  {',
-                  f'    float ra0[{KC // 4}], rb0[{KC // 4}][{CT}], ra1[{KC // 4}], rb1[{KC // 4}][{CT}];',
-                  f'    const int nch = {nchunks};',
-                  '    const int nw = wave < nch ? (nch - wave + 3) / 4 : 0;     // chunks wave, wave + 4, ...',
-                  f'    if (nw > 0) {ld}, wave, ra0, rb0);',
-                  '    int c = wave;',
-                  '    for (int p = 0; p < nw / 2; ++p, c += 8) {',
-                  f'      {ld}, min(c + 4, nch - 1), ra1, rb1);',
-                  '      __builtin_amdgcn_sched_barrier(0);']
-            L += [l.replace('raX', 'ra0').replace('rbX', 'rb0') for l in mm]
-            L += [f'      {ld}, min(c + 8, nch - 1), ra0, rb0);',
-                  '      __builtin_amdgcn_sched_barrier(0);']
-            L += [l.replace('raX', 'ra1').replace('rbX', 'rb1') for l in mm]
-            L += ['    }',
-                  '    if (nw & 1) {']
-            L += [l.replace('raX', 'ra0').replace('rbX', 'rb0') for l in mm]
-            L += ['    }',
-                  '  }']
-        # sum of the four waves' partial tiles, then coalesced per-node stores
-        L += ['  __syncthreads();',
-              '#pragma unroll',
-              f'  for (int ct = 0; ct < {CT}; ++ct)',
-              '#pragma unroll',
-              '    for (int r = 0; r < 4; ++r)',
-              f'      red[(wave * 16 + q * 4 + r) * {CW} + {CT} * c16 + ct] = acc[ct][r];',
-              '  __syncthreads();',
-              f'  for (int f = t; f < nn * {CW * D}; f += {BLOCK}) {{',
-              f'    const int nl = f / {CW * D}, j = f - nl * {CW * D}, cc = j / {D}, m = j - cc * {D};',
-              f'    const int row = nl * {D} + m;',
-              f'    out[(size_t)(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = (red[row * {CW} + cc] + red[(16 + row) * {CW} + cc])',
-              f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]);',
-              '  }',
-              '}', '']
+                  '    for (int r = 0; r < 4; ++r) {',
+                  '      const int row = 4 * q + r;',
+                  f'      if (row < nn * {D}) {{']
+            if D == 1 and CT == 4 and Dout % 4 == 0 and oo % 4 == 0:
+                L += [f'        *reinterpret_cast<float4*>(out + (size_t)(n0 + row) * {Dout} + {oo} + col0 + 4 * c16) =',
+                      '            make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);']
+            else:
+                L += [f'        const int nl = row / {D}, m = row - nl * {D};',
+                      f'        float* __restrict__ o = out + (size_t)(n0 + nl) * {Dout} + {oo} + m;']
+                L += [f'        o[(col0 + {CT} * c16 + {ct}) * {D}] = acc[{ct}][r];' for ct in range(CT)]
+            L += ['      }', '    }', '  }', '}', '']
+        else:
+            # sum of the four waves' partial tiles, then coalesced per-node stores
+            L += ['  __syncthreads();',
+                  '#pragma unroll',
+                  f'  for (int ct = 0; ct < {CT}; ++ct)',
+                  '#pragma unroll',
+                  '    for (int r = 0; r < 4; ++r)',
+                  f'      red[(wave * 16 + q * 4 + r) * {CW} + {CT} * c16 + ct] = acc[ct][r];',
+                  '  __syncthreads();',
+                  f'  for (int f = t; f < nn * {CW * D}; f += {BLOCK}) {{',
+                  f'    const int nl = f / {CW * D}, j = f - nl * {CW * D}, cc = j / {D}, m = j - cc * {D};',
+                  f'    const int row = nl * {D} + m;',
+                  f'    out[(size_t)(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = (red[row * {CW} + cc] + '
+                  f'red[(16 + row) * {CW} + cc])',
+                  f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]);',
+                  '  }',
+                  '}', '']
         fns += L
         cases.append((o, fn))
     gy = _grid_y(out_blocks)
     cw_max = max(_cw(mo) for mo, *_ in out_blocks)
+    VW = (V + 31) // 32
     sw = ['  switch (blockIdx.y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, tile, {cg}, red, amask, vlist); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist); break;')
     sw += ['    default: break;', '  }']
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const float* __restrict__ W, float* __restrict__ out, int N) {',
          f'  __shared__ float red[{4 * 16 * cw_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];',
-         '  const int tile = blockIdx.x;'] + sw + ['}', '']
+         '  const int group = blockIdx.x;'] + sw + ['}', '']
     return fns + K
 
 
@@ -365,8 +426,10 @@ def source(spec):
     return '\n'.join(L)
 
 
-def _tiles(blocks):
-    return min(ROWS // (2 * l + 1) for _, l, *_ in blocks)
+def _tiles(blocks, terms, in_blocks, V):
+    """Nodes per workgroup of the launch (its rows per block): the smallest over the output blocks; blocks with more
+    nodes per workgroup leave their trailing workgroups idle."""
+    return min(_nodes_per_group(terms[o], in_blocks, V, l) for o, (_, l, *_) in enumerate(blocks))
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
@@ -434,9 +497,12 @@ class HipNodeLinear(torch.nn.Module):
         code = _native.compile_source(self.source)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
-            kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK, _tiles(s.out_blocks), len(_grid_y(s.out_blocks)))}
+            kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK, _tiles(s.out_blocks, s.terms, s.in_blocks, s.V),
+                                            len(_grid_y(s.out_blocks)))}
             if s.has_bwd:
-                kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK, _tiles(s.in_blocks), len(_grid_y(s.in_blocks)))
+                kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK,
+                                               _tiles(s.in_blocks, s.bterms, s.out_blocks, s.V),
+                                               len(_grid_y(s.in_blocks)))
             self.module = _native.Module(code, kernels)
         self.register_buffer('W', torch.tensor(s.W, dtype=torch.float32, device=dev), persistent=False)
         self.register_buffer('Wt', torch.tensor(s.Wt, dtype=torch.float32, device=dev), persistent=False)
