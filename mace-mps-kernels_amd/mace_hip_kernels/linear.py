@@ -35,7 +35,6 @@ KC = 32              # K chunk (input channels u of one attribute v) loaded per 
 BLOCK = 256          # 4 waves, one 16-row tile each
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of a workgroup tile: one MFMA row tile
-MAXMUL = 512         # largest multiplicity of a block
 
 
 def _blocks(irreps):
@@ -61,8 +60,8 @@ def lin_supported(mod):
         return False, 'not an e3nn Linear or tensor product'
     try:
         outs = mod.irreps_out
-        if any(mul % 16 or mul > MAXMUL for mul, _ in outs):
-            return False, f'output multiplicities must be multiples of 16 (<= {MAXMUL})'
+        if any(mul % 16 for mul, _ in outs):
+            return False, 'output multiplicities must be multiples of 16'
         ins = mod.irreps_in1 if kind == 'attrs' else mod.irreps_in
         if any(2 * ir.l + 1 > ROWS for _, ir in list(ins) + list(outs)):
             return False, 'irrep too large'
@@ -110,7 +109,7 @@ class LinSpec:
         self.Wio = Wio
         # the backward writes the input blocks with the same tiling: their multiplicities must tile too (a module
         # whose input never needs a gradient, like the node embedding of one-hot attributes, can do without)
-        self.has_bwd = all(m % 16 == 0 and m <= MAXMUL for m, *_ in self.in_blocks)
+        self.has_bwd = all(m % 16 == 0 for m, *_ in self.in_blocks)
 
     def apply(self, x, a=None):
         """float64 numpy application of the probed map (the patch-time structure check)."""

@@ -403,6 +403,9 @@ def test_node_linears_vs_float64(attrs_kind):
         if s.V:
             a = (np.eye(s.V)[rng.integers(0, s.V, size=n)] if attrs_kind == 'one_hot' else rng.normal(size=(n, s.V)))
         g = rng.normal(size=(n, s.Dout))
+        # every module whose input carries a gradient in the model has the backward kernel (the node embedding of
+        # one-hot attributes is the one without)
+        assert s.has_bwd == (not name.endswith('node_embedding.linear')), name
         xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=s.has_bwd)
         at = None if a is None else torch.tensor(a, dtype=torch.float32, device=dev)
         out = op(xt, at)
