@@ -187,11 +187,15 @@ int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const float* Wt
 
 /* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers
  * h <- c_i * silu(h A_i) and a linear output layer, MACE's conv_tp_weights (an e3nn FullyConnectedNet).  Wh holds the
- * hidden layers' weights in the module's LDS layout, Wl [n_hidden_last, n_out] the output layer's; the layer widths
- * are compiled into the module.  mh_mlp_bwd gives gef = dL/def from gW0 = dL/dW0.  No reference counterpart: the
- * reference leaves the radial MLP on e3nn (FullyConnectedNet in MACE's interaction blocks). */
-int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, float* W0, int64_t E, void* stream);
-int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, const float* gW0, float* gef,
+ * hidden layers' fp32 weights in the module's LDS layout; Wl the output layer [n_hidden_last, n_out] split exactly
+ * into three bf16 parts (bit patterns), cut into chunks of 32 columns (the last zero-padded): for mh_mlp_fwd
+ * [chunk][part][column][hidden] with the hidden index in the kernel's MFMA operand order, for mh_mlp_bwd
+ * [chunk][part][hidden][column].  The layer widths are compiled into the module.  mh_mlp_bwd gives gef = dL/def from
+ * gW0 = dL/dW0.  No reference counterpart: the reference leaves the radial MLP on e3nn (FullyConnectedNet in MACE's
+ * interaction blocks). */
+int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E,
+               void* stream);
+int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream);
 
 /* Radial embedding of E edge lengths (len [E]): cutoff[e] = polynomial envelope of len[e] / r_max (0 beyond r_max)

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 11; }
+int mh_version(void) { return 12; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -295,13 +295,13 @@ int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const float* Wt
     return launch(m, MH_LIN_BWD, N, args, stream, "mh_lin_bwd");
 }
 
-int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, float* W0, int64_t E, void* stream) {
+int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E, void* stream) {
     if (E > 0 && (!ef || !Wh || !Wl || !W0)) return fail(-1, "mh_mlp_fwd: NULL operand");
     void* args[] = {&ef, &Wh, &Wl, &W0, &E};
     return launch(m, MH_MLP_FWD, E, args, stream, "mh_mlp_fwd");
 }
 
-int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const float* Wl, const float* gW0, float* gef,
+int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream) {
     if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef)) return fail(-1, "mh_mlp_bwd: NULL operand");
     void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E};

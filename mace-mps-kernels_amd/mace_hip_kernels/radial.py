@@ -5,16 +5,21 @@ The radial MLP of MACE's interaction blocks on MI355X: a drop-in for ``conv_tp_w
 
 On the GPU the e3nn module is a chain of GEMMs and elementwise launches (a matmul, the normalised SiLU and its
 rescale per layer) whose backward adds as many again, every intermediate an [E, 64] tensor, and whose last GEMM
-(64 -> weight_numel, e.g. 1280) is most of the arithmetic.  Here each direction is ONE kernel on the fp32 matrix
-cores (v_mfma_f32_16x16x4f32):
+(64 -> weight_numel, e.g. 1280) is most of the arithmetic.  Here each direction is ONE kernel on the matrix
+cores, the hidden layers in fp32 (v_mfma_f32_16x16x4f32) and the wide output layer at fp32 accuracy on the bf16
+units (v_mfma_f32_16x16x32_bf16, 2.7x the fp32 rate per K):
 
 * a wave owns 16 edges and computes every layer for them with the transposed product out^T = W^T h^T, so that an
   MFMA result tile leaves lane (edge j = lane % 16, q = lane / 16) holding features 16 t + 4 q + r (r = 0..3) of
   its edge — which is exactly the operand layout the next layer's MFMA needs if that layer walks its K index in the
   order k = 16 t + 4 q + r.  Hidden activations never leave registers;
 * the hidden layers' weights sit in LDS for the whole workgroup (4 waves, 64 edges); the last layer's weights are
-  streamed through LDS 64 output columns at a time, the next chunk loaded into registers while the current one is
+  streamed through LDS 32 output columns at a time, the next chunk loaded into registers while the current one is
   multiplied, and each result tile is stored as one float4 per lane (16 consecutive bytes of an edge's row);
+* the output layer splits both fp32 operands exactly into three bf16 parts (v = hi + mid + lo, by truncation; the
+  weights once on the host, the activations and dL/dW0 in registers) and sums the six leading partial products
+  hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi on the bf16 MFMA with fp32 accumulation; the dropped terms are below
+  2^-24 of each product, so the result is as accurate as an fp32 dot product;
 * the backward recomputes the hidden layers from the edge features (cheaper than storing [E, 64] activations),
   forms dL/dh = dL/dW0 W_last^T over the streamed weight chunks, and walks back through the SiLUs to dL/d(edge
   features).
@@ -32,7 +37,9 @@ from . import conv as _conv
 
 BLOCK = 256          # 4 waves x 16 edges
 EDGES = 64           # edges per workgroup
-CHUNKS = (64, 32, 16)  # output columns of the last layer staged per LDS round (the largest that divides the width)
+CH = 32              # output columns of the last layer per LDS chunk
+NSPLIT = 3           # bf16 parts per fp32 weight (exact split)
+BPAD = 8             # bf16 row padding of a chunk (keeps 16-byte reads aligned, spreads banks)
 PAD = 4              # LDS row padding (floats): the 4 lane groups of a fragment land on different banks
 
 
@@ -51,6 +58,8 @@ def mlp_supported(mod):
             return False, f'{hs[0]} input features (> 64)'
         if any(h % 16 or h > 128 for h in hs[1:-1]):
             return False, 'hidden widths must be multiples of 16 (<= 128)'
+        if hs[-2] % 32:
+            return False, f'last hidden width {hs[-2]} is not a multiple of 32'
         if hs[-1] % 16:
             return False, f'output width {hs[-1]} is not a multiple of 16'
         for l in layers[:-1]:
@@ -123,40 +132,95 @@ def _lit(v):
 
 
 def _layout(spec):
-    """Packing constants shared by the generator and the weight packer."""
+    """Packing constants shared by the generator and the weight packer (float offsets for the fp32 hidden weights,
+    bf16 offsets for the output layer's chunks)."""
     hs = spec.hs
     H0, NW, HL = hs[0], hs[-1], hs[-2]
     K0S = -(-H0 // 4)                                    # MFMA steps of the first layer (K = H0 padded to 4 K0S)
     rows = [4 * K0S] + hs[1:-2]                          # K extent of each hidden layer
     cols = hs[1:-1]                                      # outputs of each hidden layer
-    CHUNK = next(c for c in CHUNKS if NW % c == 0)
     nat, tr, o1, o2 = [], [], 0, 0
     for r, c in zip(rows, cols):
         nat.append(o1)
         o1 += r * (c + PAD)                              # natural [k][j + PAD]   (backward)
         tr.append(o2)
         o2 += c * (r + PAD)                              # transposed [j][k + PAD] (forward)
-    return dict(H0=H0, NW=NW, HL=HL, K0S=K0S, rows=rows, cols=cols, CHUNK=CHUNK, nat=nat, tr=tr, nat_size=o1,
-                tr_size=o2, chunk_fwd=CHUNK * (HL + PAD), chunk_bwd=HL * (CHUNK + PAD))
+    RSF = HL + BPAD                                      # bf16 row of a forward chunk: one output column, K = HL
+    RSB = CH + BPAD                                      # bf16 row of a backward chunk: one hidden feature, K = CH
+    return dict(H0=H0, NW=NW, HL=HL, K0S=K0S, rows=rows, cols=cols, nat=nat, tr=tr, nat_size=o1, tr_size=o2,
+                RSF=RSF, RSB=RSB, chunk_fwd=NSPLIT * CH * RSF, chunk_bwd=NSPLIT * HL * RSB)
+
+
+def _kperm(HL):
+    """Forward K order of the output layer: position 32 s + 8 q + 4 t + r holds hidden feature 32 s + 16 t + 4 q + r,
+    so the eight bf16 operands of lane group q at step s are one 16-byte read, and they pair with that lane's hidden
+    activations h[2 s + t][r] (the fp32 MFMA result layout of the last hidden layer)."""
+    perm = np.zeros(HL, dtype=np.int64)
+    for s in range(HL // 32):
+        for q in range(4):
+            for t in range(2):
+                for r in range(4):
+                    perm[32 * s + 8 * q + 4 * t + r] = 32 * s + 16 * t + 4 * q + r
+    return perm
+
+
+def bf16_split3(a):
+    """Exact three-way split of float32 values into bf16 parts (uint16 bit patterns): a = hi + mid + lo exactly
+    (truncation at every step leaves at most 16, then 8, significant bits)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    hi = a.view(np.uint32) & np.uint32(0xFFFF0000)
+    r1 = (a - hi.view(np.float32)).astype(np.float32)
+    mid = r1.view(np.uint32) & np.uint32(0xFFFF0000)
+    r2 = (r1 - mid.view(np.float32)).astype(np.float32)
+    lo = r2.view(np.uint32)
+    assert not np.any(lo & np.uint32(0xFFFF)), 'bf16 split not exact'
+    return [(x >> np.uint32(16)).astype(np.uint16) for x in (hi, mid, lo)]
 
 
 def source(spec):
     """HIP source of ``mlp_fwd`` and ``mlp_bwd``."""
     Lo = _layout(spec)
-    H0, NW, HL, K0S, CHUNK = Lo['H0'], Lo['NW'], Lo['HL'], Lo['K0S'], Lo['CHUNK']
+    H0, NW, HL, K0S = Lo['H0'], Lo['NW'], Lo['HL'], Lo['K0S']
     rows, cols = Lo['rows'], Lo['cols']
+    RSF, RSB = Lo['RSF'], Lo['RSB']
     nh = len(cols)
     TL = HL // 16
-    NCHK = NW // CHUNK
-    NO = CHUNK // 16
-    lds_fwd = max(Lo['tr_size'], 2 * Lo['chunk_fwd'])
-    lds_bwd = max(Lo['nat_size'], 2 * Lo['chunk_bwd'])
-    L = [_native.device_header(), 'typedef float mh_f4 __attribute__((ext_vector_type(4)));', '',
-         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '']
+    S = HL // 32                                         # K steps of the forward output layer
+    NCHK = -(-NW // CH)                                  # the last chunk may hold 16 zero columns past NW
+    TAIL = NW % CH != 0
+    NO = CH // 16
+    lds_fwd = max(Lo['tr_size'], Lo['chunk_fwd'])        # floats; a bf16 chunk of n elements takes n / 2 floats
+    lds_bwd = max(Lo['nat_size'], Lo['chunk_bwd'])
+    L = [_native.device_header(),
+         'typedef float mh_f4 __attribute__((ext_vector_type(4)));',
+         'typedef __bf16 mh_bf8 __attribute__((ext_vector_type(8)));',
+         'typedef unsigned int mh_u4 __attribute__((ext_vector_type(4)));', '',
+         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '',
+         '// exact split of eight floats into three bf16 parts each (v = hi + mid + lo), as three bf16x8 operands',
+         '__device__ __forceinline__ void mh_split8(const float (&v)[8], mh_bf8 (&s)[3]) {',
+         '  unsigned p[3][4];',
+         '#pragma unroll',
+         '  for (int j = 0; j < 8; j += 2) {',
+         '    unsigned b[2][3];',
+         '#pragma unroll',
+         '    for (int e = 0; e < 2; ++e) {',
+         '      const unsigned hb = __float_as_uint(v[j + e]) & 0xFFFF0000u;',
+         '      const float r1 = v[j + e] - __uint_as_float(hb);',
+         '      const unsigned mb = __float_as_uint(r1) & 0xFFFF0000u;',
+         '      const float r2 = r1 - __uint_as_float(mb);',
+         '      b[e][0] = hb >> 16; b[e][1] = mb >> 16; b[e][2] = __float_as_uint(r2) >> 16;',
+         '    }',
+         '#pragma unroll',
+         '    for (int k = 0; k < 3; ++k) p[k][j / 2] = b[0][k] | (b[1][k] << 16);',
+         '  }',
+         '#pragma unroll',
+         '  for (int k = 0; k < 3; ++k) s[k] = __builtin_bit_cast(mh_bf8, mh_u4{p[k][0], p[k][1], p[k][2], p[k][3]});',
+         '}', '']
 
     def head(name, args, lds):
         return [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}({args}) {{',
                 f'  __shared__ __align__(16) float lds[{lds}];',
+                '  unsigned short* __restrict__ ldsb = reinterpret_cast<unsigned short*>(lds);',
                 '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
                 f'  const long long e0 = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * {EDGES} + wave * 16;',
                 '  const long long ej = e0 + c16;                 // this lane\'s edge (as a B column / output row)',
@@ -173,8 +237,8 @@ def source(spec):
         return P
 
     def hidden_fwd(transposed, keep):
-        """z_i and h_i = c_i silu(z_i) for every hidden layer, A operands from LDS (transposed layout: one b128 read
-        per 4 MFMAs; natural layout: b32 reads)."""
+        """z_i and h_i = c_i silu(z_i) for every hidden layer on the fp32 MFMA, A operands from LDS (transposed
+        layout: one b128 read per 4 MFMAs; natural layout: b32 reads)."""
         P = []
         for i in range(nh):
             T = cols[i] // 16
@@ -208,85 +272,115 @@ def source(spec):
                         P.append(f'  h{i}[{o}][{r}] = {_lit(spec.c[i])} * {z}[{o}][{r}] * mlp_sig({z}[{o}][{r}]);')
         return P
 
-    def pre_load(src, nx, stride, width, ind):
-        """This thread's share of an output-layer chunk, as float4 registers pre0..: chunk element f4 index f covers
-        row f / (width / 4) and 4 columns (global row stride ``stride``)."""
-        n4 = (CHUNK * HL) // 4
-        P = []
-        for it in range(-(-n4 // BLOCK)):
-            fx = f't + {it * BLOCK}' if (it + 1) * BLOCK <= n4 else f'min(t + {it * BLOCK}, {n4 - 1})'
-            P += [f'{ind}{{ const int f = {fx}, rr = f / {width // 4}, c4 = f - rr * {width // 4};',
-                  f'{ind}  pre{it} = *reinterpret_cast<const mh_f4*>({src} + (size_t)rr * {stride} + {nx} + 4 * c4); }}']
-        return P
 
-    def pre_store(base, width, ind):
-        n4 = (CHUNK * HL) // 4
+    def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None):
+        """Load (store_base None) or store this thread's 16-byte pieces of a bf16 chunk: piece f is part p, row rr,
+        8-element group c8 of a [3][nrows][row_elems] block at element offset nx_elems of ``src``; in LDS the rows
+        are ``rs`` elements apart."""
+        per_row = row_elems // 8
+        total = NSPLIT * nrows * per_row
         P = []
-        for it in range(-(-n4 // BLOCK)):
-            guard = '' if (it + 1) * BLOCK <= n4 else f'if (t + {it * BLOCK} < {n4}) '
-            P += [f'{ind}{guard}{{ const int f = t + {it * BLOCK}, rr = f / {width // 4}, c4 = f - rr * {width // 4};',
-                  f'{ind}  *reinterpret_cast<mh_f4*>(&lds[{base} + rr * {width + PAD} + 4 * c4]) = pre{it}; }}']
-        return P
+        for it in range(-(-total // BLOCK)):
+            exact = (it + 1) * BLOCK <= total
+            fx = f't + {it * BLOCK}' if exact else f'min(t + {it * BLOCK}, {total - 1})'
+            idx = [f'{ind}{{ const int f = {fx}, p = f / {nrows * per_row}, rem = f - p * {nrows * per_row},',
+                   f'{ind}      rr = rem / {per_row}, c8 = rem - rr * {per_row};']
+            if store_base is None:
+                P += idx + [f'{ind}  pre{it} = *reinterpret_cast<const mh_u4*>({src} + (size_t){nx_elems} + '
+                            f'(size_t)f * 8); }}']
+            else:
+                guard = '' if exact else f'if (t + {it * BLOCK} < {total}) '
+                P += idx + [f'{ind}  {guard}*reinterpret_cast<mh_u4*>(&ldsb[{store_base} + p * {nrows * rs} + rr * {rs} + '
+                            f'8 * c8]) = pre{it}; }}']
+        return P, -(-total // BLOCK)
 
-    npre = -(-(CHUNK * HL // 4) // BLOCK)
-    pres = ', '.join(f'pre{i}' for i in range(npre))
+    PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
 
     # ------------------------------------------------------------------ forward
-    # hidden weights transposed [j][k + PAD]; output layer from WlT [NW][HL], chunks [CHUNK cols][HL + PAD]
-    F = head(spec.kname('mlp_fwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
-             'float* __restrict__ W0, long long E', lds_fwd)
+    # hidden weights transposed [j][k + PAD] in fp32; the output layer as bf16 chunks of CH columns x HL (K in the
+    # _kperm order), three parts each, double-buffered in LDS (the hidden weights' space is reused once they are done)
+    F = head(spec.kname('mlp_fwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
+             'const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E', lds_fwd)
     F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(True, True)
     hl = f'h{nh - 1}'
-    F += [f'  mh_f4 {pres};'] + pre_load('Wl', '0', HL, HL, '  ')
+    # the last hidden layer's activations as bf16 operands: step s, lane group q: features 32 s + 16 t + 4 q + r
+    F += [f'  mh_bf8 hb[{S}][3];']
+    for st in range(S):
+        F += [f'  {{ const float v[8] = {{{", ".join(f"{hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
+              f'    mh_split8(v, hb[{st}]); }}']
+    ld0, npre = chunk_io('Wl', 0, HL, RSF, CH, '  ')
+    F += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
     F += ['  __syncthreads();                                // every wave is done with the hidden weights']
-    F += pre_store('0', HL, '  ') + ['  __syncthreads();']
+    st0, _ = chunk_io('Wl', 0, HL, RSF, CH, '  ', store_base='0')
+    F += st0 + ['  __syncthreads();']
     F += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
           f'    const int base = (ch & 1) * {Lo["chunk_fwd"]}, nbase = {Lo["chunk_fwd"]} - base;',
-          f'    const int nx = min(ch + 1, {NCHK - 1}) * {CHUNK * HL};      // next chunk (the last one reloads itself)']
-    F += pre_load('Wl', 'nx', HL, HL, '    ')
-    F += [f'    mh_f4 acc[{NO}];']
-    F += [f'    acc[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO)]
-    for ti in range(TL):
+          f'    const size_t nx = (size_t)min(ch + 1, {NCHK - 1}) * {NSPLIT * CH * HL};']
+    ldn, _ = chunk_io('Wl', 'nx', HL, RSF, CH, '    ')
+    F += ldn + ['    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
+    F += [f'    mh_f4 acc[{NO}][2];']
+    F += [f'    acc[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO) for j in range(2)]
+    for st in range(S):
         for o in range(NO):
-            F.append(f'    const mh_f4 a{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[base + ({16 * o} + c16) * '
-                     f'{HL + PAD} + {16 * ti} + 4 * q]);')
-        for r in range(4):
+            F += [f'    mh_bf8 a{st}_{o}[3];']
+            F += [f'    a{st}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * CH * RSF} + ({16 * o} + c16) * '
+                  f'{RSF} + {32 * st} + 8 * q]);' for p in range(3)]
+        for k, (pa, pb) in enumerate(PAIRS):
             for o in range(NO):
-                F.append(f'    acc[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a{ti}_{o}[{r}], {hl}[{ti}][{r}], acc[{o}], '
-                         '0, 0, 0);')
+                F.append(f'    acc[{o}][{k & 1}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{st}_{o}[{pa}], hb[{st}][{pb}], '
+                         f'acc[{o}][{k & 1}], 0, 0, 0);')
     F.append('    if (live) {')
-    F += [f'      *reinterpret_cast<mh_f4*>(W0 + ej * {NW} + ch * {CHUNK} + {16 * o} + 4 * q) = acc[{o}];'
-          for o in range(NO)]
+    for o in range(NO):
+        guard = f'if (ch < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
+        F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + ej * {NW} + ch * {CH} + {16 * o} + 4 * q) = '
+              f'acc[{o}][0] + acc[{o}][1];']
     F += ['    }']
-    F += pre_store('nbase', HL, '    ') + ['    __syncthreads();', '  }', '}', '']
+    stn, _ = chunk_io('Wl', 0, HL, RSF, CH, '    ', store_base='nbase')
+    F += stn + ['    __syncthreads();', '  }', '}', '']
     L += F
 
     # ------------------------------------------------------------------ backward
-    # dL/dh_last = gW Wl^T first (chunks of Wl [HL][NW] as [HL][CHUNK + PAD]; gW one float4 per lane per 16 columns,
-    # K order k = 16 t + 4 q + r), then the hidden layers recomputed from the natural-layout weights and walked back
-    B = head(spec.kname('mlp_bwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, const float* __restrict__ Wl, '
-             'const float* __restrict__ gW, float* __restrict__ gef, long long E', lds_bwd)
-    B += [f'  mh_f4 dh[{TL}];'] + [f'  dh[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
-    B += [f'  mh_f4 {pres};'] + pre_load('Wl', '0', NW, CHUNK, '  ')
-    B += [f'  mh_f4 g{ti} = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {16 * ti} + 4 * q);' for ti in range(NO)]
-    B += pre_store('0', CHUNK, '  ') + ['  __syncthreads();']
+    # dL/dh_last = gW Wl^T first: K = the output columns, one bf16 step of 32 per chunk (lane group q: columns
+    # 8 q .. 8 q + 7, two float4 loads of gW split into three bf16 parts); chunks of Wl [HL][CH] as bf16 rows of
+    # CH + BPAD.  Then the hidden layers recomputed from the natural-layout fp32 weights and walked back.
+    B = head(spec.kname('mlp_bwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
+             'const unsigned short* __restrict__ Wl, const float* __restrict__ gW, float* __restrict__ gef, long long E',
+             lds_bwd)
+    B += [f'  mh_f4 dh[{TL}][2];'] + [f'  dh[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL) for j in range(2)]
+    ld0, npre = chunk_io('Wl', 0, CH, RSB, HL, '  ')
+    B += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
+    # columns past NW (the zero-padded tail of the last chunk) read a valid column and are zeroed
+    gcol = (lambda c: f'min({c} + 8 * q, {NW - 8})') if TAIL else (lambda c: f'{c} + 8 * q')
+    gok = (lambda c: f' if ({c} + 8 * q >= {NW}) {{ g0 = mh_f4{{0.f, 0.f, 0.f, 0.f}}; g1 = g0; }}') if TAIL else (lambda c: '')
+    B += [f'  mh_f4 g0 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol("0")});',
+          f'  mh_f4 g1 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol("0")} + 4);']
+    st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0')
+    B += st0 + ['  __syncthreads();']
     B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
           f'    const int base = (ch & 1) * {Lo["chunk_bwd"]}, nbase = {Lo["chunk_bwd"]} - base;',
-          f'    const int nx = min(ch + 1, {NCHK - 1}) * {CHUNK};']
-    B += pre_load('Wl', 'nx', NW, CHUNK, '    ')
-    B += [f'    const mh_f4 gn{ti} = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + nx + {16 * ti} + 4 * q);'
-          for ti in range(NO)]
-    for ti in range(NO):
+          f'    const int nc = min(ch + 1, {NCHK - 1});',
+          f'    const size_t nx = (size_t)nc * {NSPLIT * HL * CH};']
+    ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ')
+    B += ldn
+    B += [f'    const mh_f4 gn0 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol(f"nc * {CH}")});',
+          f'    const mh_f4 gn1 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol(f"nc * {CH}")} + 4);',
+          '    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs',
+          '    mh_bf8 gb[3];' + gok(f'ch * {CH}'),
+          '    { const float v[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]}; mh_split8(v, gb); }']
+    for o in range(TL):
+        B += [f'    mh_bf8 a{o}[3];']
+        B += [f'    a{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * HL * RSB} + ({16 * o} + c16) * {RSB} + '
+              f'8 * q]);' for p in range(3)]
+    for k, (pa, pb) in enumerate(PAIRS):
         for o in range(TL):
-            B.append(f'    const mh_f4 a{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[base + ({16 * o} + c16) * '
-                     f'{CHUNK + PAD} + {16 * ti} + 4 * q]);')
-        for r in range(4):
-            for o in range(TL):
-                B.append(f'    dh[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a{ti}_{o}[{r}], g{ti}[{r}], dh[{o}], 0, 0, 0);')
-    B += [f'    g{ti} = gn{ti};' for ti in range(NO)]
-    B += pre_store('nbase', CHUNK, '    ') + ['    __syncthreads();', '  }']
+            B.append(f'    dh[{o}][{k & 1}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{o}[{pa}], gb[{pb}], dh[{o}][{k & 1}], '
+                     '0, 0, 0);')
+    B += ['    g0 = gn0; g1 = gn1;']
+    stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase')
+    B += stn + ['    __syncthreads();', '  }']
+    B += [f'  mh_f4 dhs[{TL}];'] + [f'  dhs[{o}] = dh[{o}][0] + dh[{o}][1];' for o in range(TL)]
     B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(False, False)
-    cur = 'dh'
+    cur = 'dhs'
     for i in range(nh - 1, -1, -1):
         T = cols[i] // 16
         for o in range(T):
@@ -330,9 +424,11 @@ def source(spec):
 
 
 def packed_weights(spec):
-    """float32 weight buffers: {'fwd': (hidden transposed, WlT [NW, HL]), 'bwd': (hidden natural, Wl [HL, NW])}.
-    Hidden layer i is laid out as the kernel's LDS copy: natural [k][j + PAD] (the first layer's K padded to a
-    multiple of 4 with zero rows) or transposed [j][k + PAD]."""
+    """Weight buffers: {'fwd': (hidden transposed fp32, output layer bf16 chunks), 'bwd': (hidden natural fp32,
+    output layer bf16 chunks)}.  Hidden layer i is laid out as the kernel's LDS copy: natural [k][j + PAD] (the first
+    layer's K padded to a multiple of 4 with zero rows) or transposed [j][k + PAD].  The output layer W [HL, NW] is
+    split exactly into three bf16 parts (uint16 bit patterns) and cut into chunks of CH columns: forward
+    [NW / CH][3][CH][HL] with K in the ``_kperm`` order, backward [NW / CH][3][HL][CH]."""
     Lo = _layout(spec)
     nat = np.zeros(Lo['nat_size'])
     tr = np.zeros(Lo['tr_size'])
@@ -344,9 +440,16 @@ def packed_weights(spec):
         bt = np.zeros((c, r + PAD))
         bt[:, :A.shape[0]] = A.T
         tr[Lo['tr'][i]:Lo['tr'][i] + bt.size] = bt.reshape(-1)
-    Wl = spec.A[-1]
-    return {'fwd': (tr.astype(np.float32), np.ascontiguousarray(Wl.T).astype(np.float32)),
-            'bwd': (nat.astype(np.float32), np.ascontiguousarray(Wl).astype(np.float32))}
+    HL, NW = spec.A[-1].shape
+    Wl = np.zeros((HL, -(-NW // CH) * CH), dtype=np.float32)  # zero columns up to a whole chunk
+    Wl[:, :NW] = spec.A[-1]
+    NW = Wl.shape[1]
+    parts = bf16_split3(Wl)
+    perm = _kperm(HL)
+    fwd = np.stack([p.reshape(HL, NW // CH, CH).transpose(1, 2, 0)[:, :, perm] for p in parts], axis=1)
+    bwd = np.stack([p.reshape(HL, NW // CH, CH).transpose(1, 0, 2) for p in parts], axis=1)
+    return {'fwd': (tr.astype(np.float32), np.ascontiguousarray(fwd).reshape(-1)),
+            'bwd': (nat.astype(np.float32), np.ascontiguousarray(bwd).reshape(-1))}
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
@@ -402,7 +505,9 @@ class HipRadialMLP(torch.nn.Module):
             })
         pw = packed_weights(self.spec)
         for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1])):
-            self.register_buffer(name, torch.tensor(arr, device=dev), persistent=False)
+            # the bf16 parts travel as int16 bit patterns (the kernels read them as raw 16-bit words)
+            arr = arr.view(np.int16) if arr.dtype == np.uint16 else arr
+            self.register_buffer(name, torch.from_numpy(np.ascontiguousarray(arr)).to(dev), persistent=False)
         self.hs = self.spec.hs
         self.original = [mod]
         self.tag = 'radial_mlp'

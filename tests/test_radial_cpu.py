@@ -21,15 +21,68 @@ def test_restated_layers_match_every_block():
             ref = blk.conv_tp_weights.double()(torch.tensor(x)).numpy()
         assert np.abs(spec.apply(x) - ref).max() < 1e-12 * np.abs(ref).max()
         pw = radial.packed_weights(spec)
-        assert pw['bwd'][1].shape == (spec.hs[-2], spec.hs[-1]) and pw['fwd'][1].shape == (spec.hs[-1], spec.hs[-2])
         assert pw['fwd'][0].dtype == np.float32
         # both hidden layouts hold the same numbers
         assert np.isclose(np.abs(pw['fwd'][0]).sum(), np.abs(pw['bwd'][0]).sum(), rtol=1e-6)
+        # both output-layer layouts rebuild the float32 weights exactly from their three bf16 parts
+        want = spec.A[-1].astype(np.float32)
+        assert np.array_equal(_unpack(pw['fwd'][1], spec, fwd=True), want)
+        assert np.array_equal(_unpack(pw['bwd'][1], spec, fwd=False), want)
+
+
+def _bf16(u16):
+    return (u16.astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def _unpack(buf, spec, fwd):
+    """Sum of the three bf16 parts of a packed output layer, back in [HL, NW] order (the forward layout walks K in
+    the MFMA-operand order 32 s + 8 q + 4 t + r <-> hidden feature 32 s + 16 t + 4 q + r)."""
+    HL, NW = spec.A[-1].shape
+    CH = radial.CH
+    nch = -(-NW // CH)
+    if fwd:
+        p = buf.reshape(nch, 3, CH, HL)
+        w = _bf16(p[:, 0]) + _bf16(p[:, 1]) + _bf16(p[:, 2])          # exact: the parts do not overlap
+        out = np.zeros((HL, nch * CH), dtype=np.float32)
+        for pos in range(HL):
+            s_, rem = divmod(pos, 32)
+            q, j = divmod(rem, 8)
+            t, r = divmod(j, 4)
+            out[32 * s_ + 16 * t + 4 * q + r] = w[:, :, pos].reshape(-1)
+    else:
+        p = buf.reshape(nch, 3, HL, CH)
+        w = _bf16(p[:, 0]) + _bf16(p[:, 1]) + _bf16(p[:, 2])
+        out = w.transpose(1, 0, 2).reshape(HL, nch * CH)
+    assert not np.any(out[:, NW:]), 'padding columns must be zero'
+    return out[:, :NW]
+
+
+def test_bf16_split_is_exact_and_six_products_reach_fp32_accuracy():
+    """The output layer's arithmetic, restated in numpy: each fp32 operand split exactly into three bf16 parts, the
+    six leading partial products summed.  Against a float64 dot product the error must be at the level of an fp32
+    dot product; dropping one of the six (a planted mistake) must show up."""
+    rng = np.random.default_rng(5)
+    a = (rng.normal(size=(200, 64)) * np.exp(rng.normal(size=(200, 64)))).astype(np.float32)
+    b = rng.normal(size=(64,)).astype(np.float32)
+    pa, pb = radial.bf16_split3(a), radial.bf16_split3(b)
+    assert np.array_equal(_bf16(pa[0]) + _bf16(pa[1]) + _bf16(pa[2]), a)
+    for x in pa:        # every part is a bf16 value: no bits below the top 16
+        assert x.dtype == np.uint16
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+
+    def dot(pairs):
+        return sum(_bf16(pa[i]).astype(np.float64) @ _bf16(pb[j]).astype(np.float64) for i, j in pairs)
+    six = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
+    assert (np.abs(dot(six) - exact) / scale).max() < 2 ** -22
+    assert (np.abs(dot(six[:3] + six[4:]) - exact) / scale).max() > 2 ** -20      # hi*lo dropped
 
 
 def test_unsupported_networks_are_refused():
     assert not radial.mlp_supported(enn.FullyConnectedNet([8, 64, 100], torch.nn.functional.silu))[0]   # output
     assert not radial.mlp_supported(enn.FullyConnectedNet([8, 40, 128], torch.nn.functional.silu))[0]   # hidden
+    assert not radial.mlp_supported(enn.FullyConnectedNet([8, 48, 128], torch.nn.functional.silu))[0]   # last hidden
+    assert radial.mlp_supported(enn.FullyConnectedNet([8, 64, 144], torch.nn.functional.silu))[0]       # 16 mod 32
     assert not radial.mlp_supported(enn.FullyConnectedNet([8, 64, 128], torch.tanh))[0]                 # activation
     assert not radial.mlp_supported(enn.FullyConnectedNet([8, 128]))[0]                                 # no hidden
     assert radial.mlp_supported(enn.FullyConnectedNet([8, 64, 64, 128], torch.nn.functional.silu))[0]
@@ -44,8 +97,8 @@ def test_mismatched_module_is_rejected():
         radial.MLPSpec(Scaled([8, 64, 64, 128], torch.nn.functional.silu))
 
 
-def test_generated_source_compiles():
+@pytest.mark.parametrize('widths', [[8, 64, 64, 64, 1280], [8, 64, 64, 144]])
+def test_generated_source_compiles(widths):
     from mace_hip_kernels import _native
-    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
-    spec = radial.MLPSpec(m.interactions[1].conv_tp_weights)
+    spec = radial.MLPSpec(enn.FullyConnectedNet(widths, torch.nn.functional.silu))
     assert len(_native.compile_source(radial.source(spec))) > 1000
