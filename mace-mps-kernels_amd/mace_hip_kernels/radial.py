@@ -14,8 +14,10 @@ units (v_mfma_f32_16x16x32_bf16, 2.7x the fp32 rate per K):
   its edge — which is exactly the operand layout the next layer's MFMA needs if that layer walks its K index in the
   order k = 16 t + 4 q + r.  Hidden activations never leave registers;
 * the hidden layers' weights sit in LDS for the whole workgroup (4 waves, 64 edges); the last layer's weights are
-  streamed through LDS 32 output columns at a time, the next chunk loaded into registers while the current one is
-  multiplied, and each result tile is stored as one float4 per lane (16 consecutive bytes of an edge's row);
+  streamed through LDS 32 output columns at a time, the next PREFETCH chunks in flight in registers while the
+  current one is multiplied, and each result tile is stored as one float4 per lane (16 consecutive bytes of an
+  edge's row); in the forward each wave owns NB_FWD = 2 tiles of 16 edges, so every LDS weight fragment feeds two
+  MFMAs;
 * the output layer splits both fp32 operands exactly into three bf16 parts (v = hi + mid + lo, by truncation; the
   weights once on the host, the activations and dL/dW0 in registers) and sums the six leading partial products
   hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi on the bf16 MFMA with fp32 accumulation; the dropped terms are below
@@ -35,9 +37,13 @@ import torch
 from . import _native
 from . import conv as _conv
 
-BLOCK = 256          # 4 waves x 16 edges
-EDGES = 64           # edges per workgroup
-CH = 32              # output columns of the last layer per LDS chunk
+BLOCK = 256          # 4 waves
+NB_FWD = 2           # 16-edge tiles per wave in the forward (each LDS weight fragment feeds NB_FWD MFMAs)
+NB_BWD = 1           # and in the backward
+GW_DIST = 2          # chunks of dL/dW0 in flight ahead of the one being multiplied (backward)
+PREFETCH = 2         # output-layer weight chunks in flight ahead of the one being multiplied
+CH_FWD = 32          # output columns of the last layer per LDS chunk, forward (a multiple of 32)
+CH_BWD = 32          # and backward (a multiple of 32: one bf16 MFMA K step per 32 columns)
 NSPLIT = 3           # bf16 parts per fp32 weight (exact split)
 BPAD = 8             # bf16 row padding of a chunk (keeps 16-byte reads aligned, spreads banks)
 PAD = 4              # LDS row padding (floats): the 4 lane groups of a fragment land on different banks
@@ -146,9 +152,9 @@ def _layout(spec):
         tr.append(o2)
         o2 += c * (r + PAD)                              # transposed [j][k + PAD] (forward)
     RSF = HL + BPAD                                      # bf16 row of a forward chunk: one output column, K = HL
-    RSB = CH + BPAD                                      # bf16 row of a backward chunk: one hidden feature, K = CH
+    RSB = CH_BWD + BPAD                                  # bf16 row of a backward chunk: one hidden feature, K = CH_BWD
     return dict(H0=H0, NW=NW, HL=HL, K0S=K0S, rows=rows, cols=cols, nat=nat, tr=tr, nat_size=o1, tr_size=o2,
-                RSF=RSF, RSB=RSB, chunk_fwd=NSPLIT * CH * RSF, chunk_bwd=NSPLIT * HL * RSB)
+                RSF=RSF, RSB=RSB, chunk_fwd=NSPLIT * CH_FWD * RSF, chunk_bwd=NSPLIT * HL * RSB)
 
 
 def _kperm(HL):
@@ -186,7 +192,8 @@ def source(spec):
     nh = len(cols)
     TL = HL // 16
     S = HL // 32                                         # K steps of the forward output layer
-    NCHK = -(-NW // CH)                                  # the last chunk may hold 16 zero columns past NW
+    CH = CH_FWD
+    NCHK = -(-NW // CH)                                  # the last chunk may hold zero columns past NW
     TAIL = NW % CH != 0
     NO = CH // 16
     lds_fwd = max(Lo['tr_size'], Lo['chunk_fwd'])        # floats; a bf16 chunk of n elements takes n / 2 floats
@@ -217,41 +224,54 @@ def source(spec):
          '  for (int k = 0; k < 3; ++k) s[k] = __builtin_bit_cast(mh_bf8, mh_u4{p[k][0], p[k][1], p[k][2], p[k][3]});',
          '}', '']
 
-    def head(name, args, lds):
-        return [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}({args}) {{',
-                f'  __shared__ __align__(16) float lds[{lds}];',
-                '  unsigned short* __restrict__ ldsb = reinterpret_cast<unsigned short*>(lds);',
-                '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
-                f'  const long long e0 = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * {EDGES} + wave * 16;',
-                '  const long long ej = e0 + c16;                 // this lane\'s edge (as a B column / output row)',
-                '  const bool live = ej < E;',
-                '  const long long ejc = live ? ej : E - 1;       // clamped: every load in bounds']
-
-    def stage(src, n):
-        return [f'  for (int f = t; f < {n // 4}; f += {BLOCK})',
-                f'    reinterpret_cast<mh_f4*>(lds)[f] = reinterpret_cast<const mh_f4*>({src})[f];']
-
-    def xin():
-        P = [f'  float xin[{K0S}];']
-        P += [f'  xin[{st}] = {4 * st} + q < {H0} ? ef[ejc * {H0} + {4 * st} + q] : 0.f;' for st in range(K0S)]
+    def head(name, args, lds, nb, waves=BLOCK // 64):
+        P = [f'extern "C" __global__ __launch_bounds__({64 * waves}) void {name}({args}) {{',
+             f'  __shared__ __align__(16) float lds[{lds}];',
+             '  unsigned short* __restrict__ ldsb = reinterpret_cast<unsigned short*>(lds);',
+             '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
+             '  (void)ldsb; (void)lane;',
+             f'  const long long e0 = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * {16 * nb * waves} + wave * {16 * nb};']
+        for b in range(nb):      # edge tile b of this wave: this lane's edge as a B column / output row
+            P += [f'  const long long ej{b} = e0 + {16 * b} + c16;',
+                  f'  const bool live{b} = ej{b} < E;',
+                  f'  const long long ejc{b} = live{b} ? ej{b} : E - 1;      // clamped: every load in bounds']
         return P
 
-    def hidden_fwd(transposed, keep):
+    def stage(src, n, nthreads=BLOCK):
+        """Copy n floats to the start of LDS: every thread issues all of its loads before its first LDS write (a
+        rolled copy loop waits out one L2 round trip per iteration)."""
+        it = -(-(n // 4) // nthreads)
+        P = [f'  mh_f4 {", ".join(f"sg{i}" for i in range(it))};']
+        P += [f'  sg{i} = reinterpret_cast<const mh_f4*>({src})[min(t + {i * nthreads}, {n // 4 - 1})];' for i in range(it)]
+        P += [f'  {"" if (i + 1) * nthreads <= n // 4 else f"if (t + {i * nthreads} < {n // 4}) "}'
+              f'reinterpret_cast<mh_f4*>(lds)[t + {i * nthreads}] = sg{i};' for i in range(it)]
+        return P
+
+    def xin(nb):
+        P = []
+        for b in range(nb):
+            P += [f'  float xin{b}[{K0S}];']
+            P += [f'  xin{b}[{st}] = {4 * st} + q < {H0} ? ef[ejc{b} * {H0} + {4 * st} + q] : 0.f;' for st in range(K0S)]
+        return P
+
+    def hidden_fwd(transposed, keep, nb):
         """z_i and h_i = c_i silu(z_i) for every hidden layer on the fp32 MFMA, A operands from LDS (transposed
-        layout: one b128 read per 4 MFMAs; natural layout: b32 reads)."""
+        layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for the nb edge tiles."""
         P = []
         for i in range(nh):
             T = cols[i] // 16
-            z = f'z{i}'
-            P.append(f'  mh_f4 {z}[{T}];')
-            for o in range(T):
-                P.append(f'  {z}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};')
+            for b in range(nb):
+                P.append(f'  mh_f4 z{i}_{b}[{T}];')
+                P += [f'  z{i}_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(T)]
             if i == 0:
                 for st in range(K0S):
                     for o in range(T):
                         a = (f'lds[{Lo["tr"][0]} + ({16 * o} + c16) * {rows[0] + PAD} + {4 * st} + q]' if transposed else
                              f'lds[{Lo["nat"][0]} + ({4 * st} + q) * {cols[0] + PAD} + {16 * o} + c16]')
-                        P.append(f'  {z}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32({a}, xin[{st}], {z}[{o}], 0, 0, 0);')
+                        P.append(f'  {{ const float a = {a};')
+                        P += [f'    z0_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xin{b}[{st}], z0_{b}[{o}], 0, 0, 0);'
+                              for b in range(nb)]
+                        P.append('  }')
             else:
                 Tin = cols[i - 1] // 16
                 for ti in range(Tin):
@@ -263,17 +283,20 @@ def source(spec):
                         for o in range(T):
                             a = (f'a{i}_{ti}_{o}[{r}]' if transposed else
                                  f'lds[{Lo["nat"][i]} + ({16 * ti + r} + 4 * q) * {cols[i] + PAD} + {16 * o} + c16]')
-                            P.append(f'  {z}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32({a}, h{i - 1}[{ti}][{r}], '
-                                     f'{z}[{o}], 0, 0, 0);')
+                            P.append(f'  {{ const float a = {a};')
+                            P += [f'    z{i}_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h{i - 1}_{b}[{ti}][{r}], '
+                                  f'z{i}_{b}[{o}], 0, 0, 0);' for b in range(nb)]
+                            P.append('  }')
             if i < nh - 1 or keep:
-                P.append(f'  mh_f4 h{i}[{T}];')
-                for o in range(T):
-                    for r in range(4):
-                        P.append(f'  h{i}[{o}][{r}] = {_lit(spec.c[i])} * {z}[{o}][{r}] * mlp_sig({z}[{o}][{r}]);')
+                for b in range(nb):
+                    P.append(f'  mh_f4 h{i}_{b}[{T}];')
+                    for o in range(T):
+                        for r in range(4):
+                            P.append(f'  h{i}_{b}[{o}][{r}] = {_lit(spec.c[i])} * z{i}_{b}[{o}][{r}] * '
+                                     f'mlp_sig(z{i}_{b}[{o}][{r}]);')
         return P
 
-
-    def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None):
+    def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None, reg='pre'):
         """Load (store_base None) or store this thread's 16-byte pieces of a bf16 chunk: piece f is part p, row rr,
         8-element group c8 of a [3][nrows][row_elems] block at element offset nx_elems of ``src``; in LDS the rows
         are ``rs`` elements apart."""
@@ -286,12 +309,12 @@ def source(spec):
             idx = [f'{ind}{{ const int f = {fx}, p = f / {nrows * per_row}, rem = f - p * {nrows * per_row},',
                    f'{ind}      rr = rem / {per_row}, c8 = rem - rr * {per_row};']
             if store_base is None:
-                P += idx + [f'{ind}  pre{it} = *reinterpret_cast<const mh_u4*>({src} + (size_t){nx_elems} + '
+                P += idx + [f'{ind}  {reg}{it} = *reinterpret_cast<const mh_u4*>({src} + (size_t){nx_elems} + '
                             f'(size_t)f * 8); }}']
             else:
                 guard = '' if exact else f'if (t + {it * BLOCK} < {total}) '
                 P += idx + [f'{ind}  {guard}*reinterpret_cast<mh_u4*>(&ldsb[{store_base} + p * {nrows * rs} + rr * {rs} + '
-                            f'8 * c8]) = pre{it}; }}']
+                            f'8 * c8]) = {reg}{it}; }}']
         return P, -(-total // BLOCK)
 
     PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
@@ -299,61 +322,99 @@ def source(spec):
     # ------------------------------------------------------------------ forward
     # hidden weights transposed [j][k + PAD] in fp32; the output layer as bf16 chunks of CH columns x HL (K in the
     # _kperm order), three parts each, double-buffered in LDS (the hidden weights' space is reused once they are done)
+    nb = NB_FWD
+    ncf = 2 if nb == 1 else 1                            # accumulator chains per result tile
     F = head(spec.kname('mlp_fwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
-             'const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E', lds_fwd)
-    F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(True, True)
-    hl = f'h{nh - 1}'
+             'const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E', lds_fwd, nb)
+    F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(nb) + hidden_fwd(True, True, nb)
     # the last hidden layer's activations as bf16 operands: step s, lane group q: features 32 s + 16 t + 4 q + r
-    F += [f'  mh_bf8 hb[{S}][3];']
-    for st in range(S):
-        F += [f'  {{ const float v[8] = {{{", ".join(f"{hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
-              f'    mh_split8(v, hb[{st}]); }}']
-    ld0, npre = chunk_io('Wl', 0, HL, RSF, CH, '  ')
-    F += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
+    for b in range(nb):
+        hl = f'h{nh - 1}_{b}'
+        F += [f'  mh_bf8 hb{b}[{S}][3];']
+        for st in range(S):
+            F += [f'  {{ const float v[8] = {{{", ".join(f"{hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
+                  f'    mh_split8(v, hb{b}[{st}]); }}']
+    # weight chunks in flight: register set j holds chunk c + PD while chunk c is multiplied (the loop is unrolled PD
+    # times so the sets have fixed names; chunks past the last, when PD does not divide the count, are computed from
+    # the last chunk's weights and not stored)
+    PD = PREFETCH
+    NCHP = -(-NCHK // PD) * PD
+    npre = -(-(NSPLIT * CH * HL // 8) // BLOCK)
+    for j in range(PD):
+        F += [f'  mh_u4 {", ".join(f"pre{j}_{i}" for i in range(npre))};']
+        F += chunk_io('Wl', f'{min(j, NCHK - 1) * NSPLIT * CH * HL}', HL, RSF, CH, '  ', reg=f'pre{j}_')[0]
     F += ['  __syncthreads();                                // every wave is done with the hidden weights']
-    st0, _ = chunk_io('Wl', 0, HL, RSF, CH, '  ', store_base='0')
-    F += st0 + ['  __syncthreads();']
-    F += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
-          f'    const int base = (ch & 1) * {Lo["chunk_fwd"]}, nbase = {Lo["chunk_fwd"]} - base;',
-          f'    const size_t nx = (size_t)min(ch + 1, {NCHK - 1}) * {NSPLIT * CH * HL};']
-    ldn, _ = chunk_io('Wl', 'nx', HL, RSF, CH, '    ')
-    F += ldn + ['    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
-    F += [f'    mh_f4 acc[{NO}][2];']
-    F += [f'    acc[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO) for j in range(2)]
-    for st in range(S):
-        for o in range(NO):
-            F += [f'    mh_bf8 a{st}_{o}[3];']
-            F += [f'    a{st}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * CH * RSF} + ({16 * o} + c16) * '
-                  f'{RSF} + {32 * st} + 8 * q]);' for p in range(3)]
-        for k, (pa, pb) in enumerate(PAIRS):
+    F += chunk_io('Wl', 0, HL, RSF, CH, '  ', store_base='0', reg='pre0_')[0] + ['  __syncthreads();']
+    F += [f'  for (int ch = 0; ch < {NCHP}; ch += {PD}) {{']
+    for j in range(PD):
+        c = f'(ch + {j})' if j else 'ch'
+        F += ['  {',
+              f'    const int c = {c}, base = (c & 1) * {Lo["chunk_fwd"]}, nbase = {Lo["chunk_fwd"]} - base;',
+              f'    const size_t nx = (size_t)min(c + {PD}, {NCHK - 1}) * {NSPLIT * CH * HL};']
+        F += chunk_io('Wl', 'nx', HL, RSF, CH, '    ', reg=f'pre{j}_')[0]
+        F += ['    __builtin_amdgcn_sched_barrier(0);            // the loads go out before the MFMAs']
+        for b in range(nb):
+            F += [f'    mh_f4 acc{b}[{NO}][{ncf}];']
+            F += [f'    acc{b}[{o}][{jj}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO) for jj in range(ncf)]
+        for st in range(S):
             for o in range(NO):
-                F.append(f'    acc[{o}][{k & 1}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{st}_{o}[{pa}], hb[{st}][{pb}], '
-                         f'acc[{o}][{k & 1}], 0, 0, 0);')
-    F.append('    if (live) {')
-    for o in range(NO):
-        guard = f'if (ch < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
-        F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + ej * {NW} + ch * {CH} + {16 * o} + 4 * q) = '
-              f'acc[{o}][0] + acc[{o}][1];']
-    F += ['    }']
-    stn, _ = chunk_io('Wl', 0, HL, RSF, CH, '    ', store_base='nbase')
-    F += stn + ['    __syncthreads();', '  }', '}', '']
+                F += [f'    mh_bf8 a{st}_{o}[3];']
+                F += [f'    a{st}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * CH * RSF} + ({16 * o} + c16) '
+                      f'* {RSF} + {32 * st} + 8 * q]);' for p in range(3)]
+            for k, (pa, pb) in enumerate(PAIRS):
+                for o in range(NO):
+                    for b in range(nb):
+                        a = f'acc{b}[{o}][{k % ncf}]'
+                        F.append(f'    {a} = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{st}_{o}[{pa}], hb{b}[{st}][{pb}], '
+                                 f'{a}, 0, 0, 0);')
+        # chunk c + 1 goes to LDS before chunk c's results go out: vmcnt counts loads and stores in issue order, so
+        # waiting for the prefetch then never waits for stores (they drain during the next chunk's MFMAs)
+        F += chunk_io('Wl', 0, HL, RSF, CH, '    ', store_base='nbase', reg=f'pre{(j + 1) % PD}_')[0]
+        F += ['    __builtin_amdgcn_sched_barrier(0);']
+        for b in range(nb):
+            F.append(f'    if (live{b}{f" && c < {NCHK}" if NCHP > NCHK else ""}) {{')
+            for o in range(NO):
+                guard = f'if (c < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
+                val = ' + '.join(f'acc{b}[{o}][{jj}]' for jj in range(ncf))
+                F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + ej{b} * {NW} + c * {CH} + {16 * o} + 4 * q) = {val};']
+            F += ['    }']
+        F += ['    __syncthreads();', '  }']
+    F += ['  }', '}', '']
     L += F
 
     # ------------------------------------------------------------------ backward
     # dL/dh_last = gW Wl^T first: K = the output columns, one bf16 step of 32 per chunk (lane group q: columns
     # 8 q .. 8 q + 7, two float4 loads of gW split into three bf16 parts); chunks of Wl [HL][CH] as bf16 rows of
     # CH + BPAD.  Then the hidden layers recomputed from the natural-layout fp32 weights and walked back.
+    nb = NB_BWD
+    ncb = 2 if nb == 1 else 1
+    CH = CH_BWD
+    KS = CH // 32                                        # bf16 K steps per chunk
+    NCHK = -(-NW // CH)
+    TAIL = NW % CH != 0
     B = head(spec.kname('mlp_bwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
              'const unsigned short* __restrict__ Wl, const float* __restrict__ gW, float* __restrict__ gef, long long E',
-             lds_bwd)
-    B += [f'  mh_f4 dh[{TL}][2];'] + [f'  dh[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL) for j in range(2)]
+             lds_bwd, nb)
+    for b in range(nb):
+        B += [f'  mh_f4 dh{b}[{TL}][{ncb}];'] + [f'  dh{b}[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};'
+                                                for o in range(TL) for j in range(ncb)]
     ld0, npre = chunk_io('Wl', 0, CH, RSB, HL, '  ')
     B += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
     # columns past NW (the zero-padded tail of the last chunk) read a valid column and are zeroed
     gcol = (lambda c: f'min({c} + 8 * q, {NW - 8})') if TAIL else (lambda c: f'{c} + 8 * q')
-    gok = (lambda c: f' if ({c} + 8 * q >= {NW}) {{ g0 = mh_f4{{0.f, 0.f, 0.f, 0.f}}; g1 = g0; }}') if TAIL else (lambda c: '')
-    B += [f'  mh_f4 g0 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol("0")});',
-          f'  mh_f4 g1 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol("0")} + 4);']
+
+    def gload(dst, c, b, decl):
+        """dL/dW0 of edge tile b, columns c + 32 ks + 8 q .. + 7 for each K step ks, into dst_ks_{0,1}"""
+        P = []
+        for ks in range(KS):
+            col = gcol(f'{c} + {32 * ks}')
+            P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col});',
+                  f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col} + 4);']
+        return P
+    # dL/dW0 of chunk ch + d sits in g{d}_* (d = 0 .. GW_DIST - 1) while chunk ch is multiplied
+    for b in range(nb):
+        for d in range(GW_DIST):
+            B += gload(f'g{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
     st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0')
     B += st0 + ['  __syncthreads();']
     B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
@@ -362,61 +423,83 @@ def source(spec):
           f'    const size_t nx = (size_t)nc * {NSPLIT * HL * CH};']
     ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ')
     B += ldn
-    B += [f'    const mh_f4 gn0 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol(f"nc * {CH}")});',
-          f'    const mh_f4 gn1 = *reinterpret_cast<const mh_f4*>(gW + ejc * {NW} + {gcol(f"nc * {CH}")} + 4);',
-          '    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs',
-          '    mh_bf8 gb[3];' + gok(f'ch * {CH}'),
-          '    { const float v[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]}; mh_split8(v, gb); }']
-    for o in range(TL):
-        B += [f'    mh_bf8 a{o}[3];']
-        B += [f'    a{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * HL * RSB} + ({16 * o} + c16) * {RSB} + '
-              f'8 * q]);' for p in range(3)]
-    for k, (pa, pb) in enumerate(PAIRS):
+    B += [f'    const int gc = min(ch + {GW_DIST}, {NCHK - 1}) * {CH};']
+    for b in range(nb):
+        B += gload('gn', 'gc', b, '    const mh_f4 ')
+    B += ['    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
+    for ks in range(KS):
+        for b in range(nb):
+            v = f'g0_{ks}'
+            zero = (f' if (ch * {CH} + {32 * ks} + 8 * q >= {NW}) {{ {v}_0_{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}}; '
+                    f'{v}_1_{b} = {v}_0_{b}; }}' if TAIL else '')
+            B += [f'    mh_bf8 gb{ks}_{b}[3];' + zero,
+                  f'    {{ const float v[8] = {{{", ".join(f"{v}_{h}_{b}[{i}]" for h in range(2) for i in range(4))}}}; '
+                  f'mh_split8(v, gb{ks}_{b}); }}']
         for o in range(TL):
-            B.append(f'    dh[{o}][{k & 1}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{o}[{pa}], gb[{pb}], dh[{o}][{k & 1}], '
-                     '0, 0, 0);')
-    B += ['    g0 = gn0; g1 = gn1;']
+            B += [f'    mh_bf8 a{ks}_{o}[3];']
+            B += [f'    a{ks}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * HL * RSB} + ({16 * o} + c16) * '
+                  f'{RSB} + {32 * ks} + 8 * q]);' for p in range(3)]
+        for k, (pa, pb) in enumerate(PAIRS):
+            for o in range(TL):
+                for b in range(nb):
+                    c = f'dh{b}[{o}][{k % ncb}]'
+                    B.append(f'    {c} = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{ks}_{o}[{pa}], gb{ks}_{b}[{pb}], {c}, '
+                             '0, 0, 0);')
+    for b in range(nb):
+        for ks in range(KS):
+            for h in range(2):
+                for d in range(GW_DIST - 1):
+                    B += [f'    g{d}_{ks}_{h}_{b} = g{d + 1}_{ks}_{h}_{b};']
+                B += [f'    g{GW_DIST - 1}_{ks}_{h}_{b} = gn_{ks}_{h}_{b};']
     stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase')
     B += stn + ['    __syncthreads();', '  }']
-    B += [f'  mh_f4 dhs[{TL}];'] + [f'  dhs[{o}] = dh[{o}][0] + dh[{o}][1];' for o in range(TL)]
-    B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin() + hidden_fwd(False, False)
-    cur = 'dhs'
+    for b in range(nb):
+        B += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = ' + ' + '.join(f'dh{b}[{o}][{j}]' for j in range(ncb)) + ';'
+                                           for o in range(TL)]
+    B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin(nb) + hidden_fwd(False, False, nb)
+    cur = 'dhs_'
     for i in range(nh - 1, -1, -1):
         T = cols[i] // 16
-        for o in range(T):
-            for r in range(4):
-                B += ['  {',
-                      f'    const float z = z{i}[{o}][{r}], s = mlp_sig(z);',
-                      f'    {cur}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
-                      '  }']
+        for b in range(nb):
+            for o in range(T):
+                for r in range(4):
+                    B += ['  {',
+                          f'    const float z = z{i}_{b}[{o}][{r}], s = mlp_sig(z);',
+                          f'    {cur}{b}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
+                          '  }']
         if i > 0:
             Tp = cols[i - 1] // 16
-            nxt = f'dh{i - 1}'
+            nxt = f'dh{i - 1}_'
             # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
-            B.append(f'  mh_f4 {nxt}[{Tp}];')
-            B += [f'  {nxt}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
+            for b in range(nb):
+                B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
+                B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
             for ti in range(T):
                 for o in range(Tp):
                     B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
                              f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
                 for r in range(4):
                     for o in range(Tp):
-                        B.append(f'  {nxt}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], {cur}[{ti}][{r}], '
-                                 f'{nxt}[{o}], 0, 0, 0);')
+                        for b in range(nb):
+                            B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
+                                     f'{cur}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
             cur = nxt
     # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
     T0 = cols[0] // 16
     for o in range(-(-H0 // 16)):
         B += ['  {',
-              '    mh_f4 d = mh_f4{0.f, 0.f, 0.f, 0.f};',
               f'    const int row = {16 * o} + c16 < {rows[0]} ? {16 * o} + c16 : 0;']
+        B += [f'    mh_f4 d{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for b in range(nb)]
         for ti in range(T0):
             B.append(f'    const mh_f4 w{ti} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][0]} + row * {cols[0] + PAD} + '
                      f'{16 * ti} + 4 * q]);')
             for r in range(4):
-                B.append(f'    d = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}[{ti}][{r}], d, 0, 0, 0);')
-        for r in range(4):
-            B.append(f'    if (live && {16 * o + r} + 4 * q < {H0}) gef[ej * {H0} + {16 * o + r} + 4 * q] = d[{r}];')
+                B += [f'    d{b} = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}{b}[{ti}][{r}], d{b}, 0, 0, 0);'
+                      for b in range(nb)]
+        for b in range(nb):
+            for r in range(4):
+                B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[ej{b} * {H0} + {16 * o + r} + 4 * q] = '
+                         f'd{b}[{r}];')
         B.append('  }')
     B += ['}', '']
     L += B
@@ -427,8 +510,8 @@ def packed_weights(spec):
     """Weight buffers: {'fwd': (hidden transposed fp32, output layer bf16 chunks), 'bwd': (hidden natural fp32,
     output layer bf16 chunks)}.  Hidden layer i is laid out as the kernel's LDS copy: natural [k][j + PAD] (the first
     layer's K padded to a multiple of 4 with zero rows) or transposed [j][k + PAD].  The output layer W [HL, NW] is
-    split exactly into three bf16 parts (uint16 bit patterns) and cut into chunks of CH columns: forward
-    [NW / CH][3][CH][HL] with K in the ``_kperm`` order, backward [NW / CH][3][HL][CH]."""
+    split exactly into three bf16 parts (uint16 bit patterns) and cut into chunks of CH_FWD / CH_BWD columns (the last
+    zero-padded): forward [chunk][3][CH_FWD][HL] with K in the ``_kperm`` order, backward [chunk][3][HL][CH_BWD]."""
     Lo = _layout(spec)
     nat = np.zeros(Lo['nat_size'])
     tr = np.zeros(Lo['tr_size'])
@@ -441,13 +524,16 @@ def packed_weights(spec):
         bt[:, :A.shape[0]] = A.T
         tr[Lo['tr'][i]:Lo['tr'][i] + bt.size] = bt.reshape(-1)
     HL, NW = spec.A[-1].shape
-    Wl = np.zeros((HL, -(-NW // CH) * CH), dtype=np.float32)  # zero columns up to a whole chunk
-    Wl[:, :NW] = spec.A[-1]
-    NW = Wl.shape[1]
-    parts = bf16_split3(Wl)
+
+    def padded(CH):                                          # zero columns up to a whole chunk
+        w = np.zeros((HL, -(-NW // CH) * CH), dtype=np.float32)
+        w[:, :NW] = spec.A[-1]
+        return bf16_split3(w), w.shape[1] // CH
     perm = _kperm(HL)
-    fwd = np.stack([p.reshape(HL, NW // CH, CH).transpose(1, 2, 0)[:, :, perm] for p in parts], axis=1)
-    bwd = np.stack([p.reshape(HL, NW // CH, CH).transpose(1, 0, 2) for p in parts], axis=1)
+    parts, n = padded(CH_FWD)
+    fwd = np.stack([p.reshape(HL, n, CH_FWD).transpose(1, 2, 0)[:, :, perm] for p in parts], axis=1)
+    parts, n = padded(CH_BWD)
+    bwd = np.stack([p.reshape(HL, n, CH_BWD).transpose(1, 0, 2) for p in parts], axis=1)
     return {'fwd': (tr.astype(np.float32), np.ascontiguousarray(fwd).reshape(-1)),
             'bwd': (nat.astype(np.float32), np.ascontiguousarray(bwd).reshape(-1))}
 
@@ -500,8 +586,8 @@ class HipRadialMLP(torch.nn.Module):
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
             self.module = _native.Module(code, {
-                _native.MH_MLP_FWD: (self.spec.kname('mlp_fwd'), BLOCK, EDGES),
-                _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), BLOCK, EDGES),
+                _native.MH_MLP_FWD: (self.spec.kname('mlp_fwd'), BLOCK, 64 * NB_FWD),
+                _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), BLOCK, 64 * NB_BWD),
             })
         pw = packed_weights(self.spec)
         for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1])):

@@ -38,10 +38,10 @@ def _unpack(buf, spec, fwd):
     """Sum of the three bf16 parts of a packed output layer, back in [HL, NW] order (the forward layout walks K in
     the MFMA-operand order 32 s + 8 q + 4 t + r <-> hidden feature 32 s + 16 t + 4 q + r)."""
     HL, NW = spec.A[-1].shape
-    CH = radial.CH
+    CH = radial.CH_FWD if fwd else radial.CH_BWD
     nch = -(-NW // CH)
     if fwd:
-        p = buf.reshape(nch, 3, CH, HL)
+        p = np.ascontiguousarray(buf).reshape(nch, 3, CH, HL)
         w = _bf16(p[:, 0]) + _bf16(p[:, 1]) + _bf16(p[:, 2])          # exact: the parts do not overlap
         out = np.zeros((HL, nch * CH), dtype=np.float32)
         for pos in range(HL):
