@@ -176,13 +176,18 @@ int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int6
  *   out[n, o, w, m] = sum_{i: irrep_i = irrep_o} sum_u x[n, i, u, m] W_io[u, w];
  * with V scalar attrs it is the tensor product x (x) attrs over 0e attrs (MACE's skip_tp, FullyConnectedTensorProduct
  * with node_attrs): out[n, o, w, m] = sum_i sum_{u, v} x[n, i, u, m] attrs[n, v] W_io[u, v, w], terms whose attrs are
- * zero over a whole tile of nodes skipped.  W is the module's packed weights with the path normalisation folded in;
- * the block layout is compiled into the module.  mh_lin_bwd computes gx from g [N, Dout] the same way with the
- * transposed weights Wt_oi[w, v, u].  No reference counterpart: the reference leaves the model's linears and skip_tp
- * on e3nn (o3.Linear / o3.FullyConnectedTensorProduct in the interaction and product blocks). */
-int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const float* W, float* out, int32_t N,
+ * zero over a whole tile of nodes skipped.  W holds the module's weights (path normalisation folded in) in the layout
+ * of the module's kernel family: for the bf16 family (attribute-free maps with >= 1024 outputs) each fp32 value split
+ * exactly into three bf16 parts (uint16 bit patterns) in streaming order — per output block, column group of up to
+ * 64 channels, input block and chunk of 32 input channels, a [part][column][channel] slice; for the fp32 family the
+ * float32 blocks W_io[u, v, w] one after another.  The block layout, family and offsets are compiled into the module
+ * (attrs must not be NULL for a module with attributes).  mh_lin_bwd computes gx
+ * from g [N, Dout] the same way with the transposed weights Wt_oi[w, v, u].  No reference counterpart: the
+ * reference leaves the model's linears and skip_tp on e3nn (o3.Linear / o3.FullyConnectedTensorProduct in the
+ * interaction and product blocks). */
+int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, int32_t N,
                void* stream);
-int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const float* Wt, float* gx, int32_t N,
+int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, int32_t N,
                void* stream);
 
 /* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers

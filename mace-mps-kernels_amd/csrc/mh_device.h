@@ -77,3 +77,34 @@ __device__ __forceinline__ float mh_wave_transpose_sum(float (&v)[NV]) {
     MhTransposeStep<NV, MH_WAVE / 2, NV>::run(v, threadIdx.x & (MH_WAVE - 1));
     return v[0];
 }
+
+// fp32 at fp32 accuracy on the bf16 matrix cores: a float splits exactly into three bf16 parts v = hi + mid + lo
+// (truncation at every step: hi keeps the top 8 significant bits, mid the next 8, lo the last 8), and a product
+// a·b is then the sum of the six partial products hi·hi, hi·mid, mid·hi, hi·lo, mid·mid, lo·hi up to terms below
+// 2^-24 of |a·b| — as accurate as an fp32 multiply.  mh_split8 splits eight floats into the three bf16x8 MFMA
+// operands (v_mfma_f32_16x16x32_bf16 takes eight K values per lane).
+typedef float mh_f4 __attribute__((ext_vector_type(4)));
+typedef __bf16 mh_bf8 __attribute__((ext_vector_type(8)));
+typedef unsigned int mh_u4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void mh_split8(const float (&v)[8], mh_bf8 (&s)[3]) {
+    unsigned p[3][4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        unsigned b[2][3];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const unsigned hb = __float_as_uint(v[j + e]) & 0xFFFF0000u;
+            const float r1 = v[j + e] - __uint_as_float(hb);
+            const unsigned mb = __float_as_uint(r1) & 0xFFFF0000u;
+            const float r2 = r1 - __uint_as_float(mb);
+            b[e][0] = hb >> 16;
+            b[e][1] = mb >> 16;
+            b[e][2] = __float_as_uint(r2) >> 16;
+        }
+#pragma unroll
+        for (int k = 0; k < 3; ++k) p[k][j / 2] = b[0][k] | (b[1][k] << 16);
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s[k] = __builtin_bit_cast(mh_bf8, mh_u4{p[k][0], p[k][1], p[k][2], p[k][3]});
+}

@@ -31,10 +31,13 @@ import torch
 
 from . import _native
 
-KC = 32              # K chunk (input channels u of one attribute v) loaded per step of a wave
-BLOCK = 256          # 4 waves, one 16-row tile each
+KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
+BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
-ROWS = 16            # rows (node, m) of a workgroup tile: one MFMA row tile
+ROWS = 16            # rows (node, m) of an MFMA row tile
+NT = 2               # row tiles per wave: each LDS weight fragment feeds NT MFMAs
+XPAD = 4             # floats of padding per LDS row of staged inputs
+WPAD = 8             # bf16 of padding per LDS row of staged weights
 
 
 def _blocks(irreps):
@@ -107,6 +110,10 @@ class LinSpec:
         self.W = np.concatenate(fw) if fw else np.zeros(4)
         self.Wt = np.concatenate(bw) if bw else np.zeros(4)
         self.Wio = Wio
+        # what the kernels stream: exact bf16 splits in chunk order (forward: W_io; backward: its transpose)
+        self.pack_fwd = pack(self.out_blocks, self.terms, self.in_blocks, Wio, self.V)
+        self.pack_bwd = pack(self.in_blocks, self.bterms, self.out_blocks,
+                             {(o, i): np.ascontiguousarray(w.transpose(2, 1, 0)) for (i, o), w in Wio.items()}, self.V)
         # the backward writes the input blocks with the same tiling: their multiplicities must tile too (a module
         # whose input never needs a gradient, like the node embedding of one-hot attributes, can do without)
         self.has_bwd = all(m % 16 == 0 for m, *_ in self.in_blocks)
@@ -186,7 +193,7 @@ def _probe(mod, spec):
 
 
 def _cw(mo):
-    """Columns per workgroup: 64 (4 MFMA column tiles per wave) where the multiplicity allows."""
+    """Columns per workgroup: 64 (4 MFMA column tiles) where the multiplicity allows."""
     return 64 if mo % 64 == 0 else 32 if mo % 32 == 0 else 16
 
 
@@ -194,6 +201,255 @@ def _grid_y(blocks):
     """(block, column group) pairs of one direction, in blockIdx.y order."""
     return [(o, cg) for o, (mo, *_) in enumerate(blocks) for cg in range(mo // _cw(mo))]
 
+
+def _group(l):
+    """(nodes per row tile, nodes per workgroup) for output irreps of degree l: a tile is 16 // (2l + 1) whole
+    nodes (<= 16 rows (node, m)), each wave holds NT tiles."""
+    tn = ROWS // (2 * l + 1)
+    return tn, WAVES * NT * tn
+
+
+def _nodes_per_launch_group(blocks):
+    """Nodes per workgroup of the launch: the smallest over the output blocks (blocks with more nodes per workgroup
+    leave their trailing workgroups idle)."""
+    return min(_group(l)[1] for _, l, *_ in blocks)
+
+
+def pack(blocks, terms, in_blocks, wmats, V):
+    """The weights of one direction as the kernel streams them: for output block o, column group cg (CW columns),
+    term (input block i), attribute v and chunk uc of 32 input channels, the [32, CW] slice of W_io[u, v, w]
+    (rows past mul_i zero) split exactly into three bf16 parts and stored [part][column][k] (uint16 bit patterns).
+    Returns (flat array, {(o, cg): element offset}, {o: [element offset of each term within a column group]})."""
+    from .radial import bf16_split3
+    VV = max(V, 1)
+    out, base, toffs, off = [], {}, {}, 0
+    for o, (mo, l, oo, _) in enumerate(blocks):
+        CW = _cw(mo)
+        offs, t = [], 0
+        for i, _ in terms[o]:
+            offs.append(t)
+            t += VV * -(-in_blocks[i][0] // KC) * 3 * CW * KC
+        toffs[o] = offs
+        for cg in range(mo // CW):
+            base[(o, cg)] = off
+            for i, _ in terms[o]:
+                w = wmats[(i, o)]                                   # [mi, VV, mo]
+                mi = w.shape[0]
+                for v in range(VV):
+                    for uc in range(-(-mi // KC)):
+                        blk = np.zeros((KC, CW), dtype=np.float32)
+                        rows = w[uc * KC:(uc + 1) * KC, v, cg * CW:(cg + 1) * CW]
+                        blk[:rows.shape[0]] = rows
+                        out += [p.T.reshape(-1) for p in bf16_split3(blk)]
+                        off += 3 * CW * KC
+    flat = np.concatenate(out) if out else np.zeros(8, dtype=np.uint16)
+    return flat, base, toffs
+
+
+def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
+    """HIP source of one direction.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x a
+    group of nodes: four waves of NT row tiles, a row tile being 16 // d whole nodes (<= 16 rows (node, m)).
+
+    K is walked in chunks of 32 input channels of one (input block, attribute v) term.  Per chunk the workgroup
+    stages, double-buffered in LDS, the chunk's inputs of its nodes (coalesced float4 loads, transposed to rows
+    (node, m) x 32 channels) and the chunk's weights (the host's exact three-way bf16 split, [part][column][k]);
+    the next chunk's loads are in flight in registers meanwhile.  Each wave splits its rows into bf16 parts (times
+    the attribute a[n, v] for skip_tp) and sums the six leading partial products on v_mfma_f32_16x16x32_bf16 (fp32
+    accuracy, 2.7x the fp32 matrix rate per K).  Attribute terms v whose a[n, v] is zero on every node of the
+    workgroup are skipped (exact: they add 0).  The result tile goes through LDS and out as coalesced float4 rows
+    (a node's CW d outputs of a block are contiguous)."""
+    fns, cases, lds_max = [], [], 0
+    VV = max(V, 1)
+    for o, (mo, l, oo, _) in enumerate(out_blocks):
+        D = 2 * l + 1
+        TN, G = _group(l)
+        CW = _cw(mo)
+        CT = CW // 16
+        fn = f'{name}_b{o}'
+        L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
+             '    const unsigned short* __restrict__ W, float* __restrict__ out, int N, int group, int cg,',
+             '    float* __restrict__ lds, unsigned* __restrict__ amask, int* __restrict__ vlist) {',
+             f'  const int g0 = group * {G};                 // first node of the workgroup',
+             '  if (g0 >= N) return;',
+             f'  const int ng = min({G}, N - g0);',
+             f'  const int t = threadIdx.x, col0 = cg * {CW};']
+        if not terms[o]:
+            L += [f'  for (int f = t; f < ng * {CW * D}; f += {BLOCK}) {{',
+                  f'    const int nl = f / {CW * D}, j = f - nl * {CW * D};',
+                  f'    out[(size_t)(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
+                  '  }', '}', '']
+            fns += L
+            cases.append((o, fn))
+            continue
+        XS = KC + XPAD                               # floats per staged input row (node, m)
+        WS = KC + WPAD                               # bf16 per staged weight row (column)
+        XR = G * D                                   # staged input rows
+        XB = XR * XS                                 # floats per input buffer
+        WB = 3 * CW * WS // 2                        # floats per weight buffer
+        lds = max(2 * (XB + WB), G * CW * D)
+        lds_max = max(lds_max, lds)
+        NXP = G * KC * D // 4                        # float4 pieces of a chunk's inputs
+        NWP = 3 * CW * KC // 8                       # 16-byte pieces of a chunk's weights
+        ix, iw = -(-NXP // BLOCK), -(-NWP // BLOCK)
+        L += ['  const int wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
+              '  (void)lane;']
+        if V:
+            L += _mask(V, 'g0', 'ng')
+        else:
+            L += ['  const int nact = 1;']
+        # chunk c -> term ti (compile-time boundaries scaled by nact), attribute v, channel chunk uc
+        nchs = [-(-in_blocks[i][0] // KC) for i, _ in terms[o]]
+        L += [f'  const int nch = nact * {sum(nchs)};',
+              f'  const unsigned short* __restrict__ Wg = W + {base[(o, 0)]} + (size_t)cg * '
+              f'{toffs[o][-1] + VV * nchs[-1] * 3 * CW * KC};']
+        L += ['  auto where = [&](int c, int& oi, int& mi, int& uc, int& v, int& wo) {',
+              '    int r = c;']
+        for k, ((i, _), nc) in enumerate(zip(terms[o], nchs)):
+            mi_, _, oi_, _ = in_blocks[i]
+            last = k == len(terms[o]) - 1
+            cond = 'true' if last else f'r < nact * {nc}'
+            L += [f'    if ({cond}) {{',
+                  f'      const int vv = r / {nc};',
+                  f'      uc = r - vv * {nc}; oi = {oi_}; mi = {mi_};',
+                  f'      v = {"vlist[1 + vv]" if V else "0"};',
+                  f'      wo = {toffs[o][k]} + (v * {nc} + uc) * {3 * CW * KC};',
+                  '      return;',
+                  '    }']
+            if not last:
+                L.append(f'    r -= nact * {nc};')
+        L += ['  };']
+        # staging: thread piece it of the inputs is node nl = f / (8 D), float4 e = f % (8 D) of the node's run of
+        # 32 d floats (channel-major, component-minor, as in e3nn's layout)
+        L += [f'  mh_f4 {", ".join(f"px{k}" for k in range(ix))};',
+              f'  mh_u4 {", ".join(f"pw{k}" for k in range(iw))};',
+              '  auto load = [&](int c) {',
+              '    int oi, mi, uc, v, wo;',
+              '    where(c, oi, mi, uc, v, wo);',
+              '    (void)v;']
+        # float4 loads where every input block of this output block starts and ends on a 16-byte boundary (a
+        # one-hot node embedding with, say, 89 elements does not): else four scalar loads
+        vec = Din % 4 == 0 and all(in_blocks[i][2] % 4 == 0 and in_blocks[i][0] * D % 4 == 0 for i, _ in terms[o])
+        for k in range(ix):
+            fx = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NXP else f'min(t + {k * BLOCK}, {NXP - 1})'
+            L += [f'    {{ const int f = {fx}, nl = f / {8 * D}, e = f - nl * {8 * D};',
+                  '      const int n = min(g0 + nl, N - 1);',
+                  f'      const float* __restrict__ xr = x + (size_t)n * {Din} + oi;']
+            if vec:     # past the block: any valid input (its weights are zero)
+                L += [f'      px{k} = *reinterpret_cast<const mh_f4*>(xr + min(uc * {KC * D} + 4 * e, mi * {D} - 4)); }}']
+            else:
+                L += [f'      px{k}[{j}] = xr[min(uc * {KC * D} + 4 * e + {j}, mi * {D} - 1)];' for j in range(4)]
+                L[-1] += ' }'
+        for k in range(iw):
+            fw = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NWP else f'min(t + {k * BLOCK}, {NWP - 1})'
+            L += [f'    pw{k} = *reinterpret_cast<const mh_u4*>(Wg + wo + (size_t)({fw}) * 8);']
+        L += ['  };',
+              '  auto store = [&](int buf) {',
+              f'    float* __restrict__ xs = lds + buf * {XB};',
+              f'    unsigned short* __restrict__ ws = reinterpret_cast<unsigned short*>(lds + {2 * XB} + buf * {WB});']
+        for k in range(ix):
+            guard = '' if (k + 1) * BLOCK <= NXP else f'if (t + {k * BLOCK} < {NXP}) '
+            L += [f'    {guard}{{ const int f = t + {k * BLOCK}, nl = f / {8 * D}, e = f - nl * {8 * D};']
+            if D == 1:
+                L += [f'      *reinterpret_cast<mh_f4*>(xs + nl * {XS} + 4 * e) = px{k}; }}']
+            else:
+                L += ['#pragma unroll',
+                      '      for (int j = 0; j < 4; ++j) {',
+                      f'        const int idx = 4 * e + j, u = idx / {D}, m = idx - u * {D};',
+                      f'        xs[(nl * {D} + m) * {XS} + u] = px{k}[j];',
+                      '      } }']
+        for k in range(iw):
+            guard = '' if (k + 1) * BLOCK <= NWP else f'if (t + {k * BLOCK} < {NWP}) '
+            L += [f'    {guard}{{ const int f = t + {k * BLOCK}, row = f / {KC // 8}, k8 = f - row * {KC // 8};',
+                  f'      *reinterpret_cast<mh_u4*>(ws + row * {WS} + 8 * k8) = pw{k}; }}']
+        L += ['  };']
+        # the lane's A rows: row c16 of each of its tiles (rows past the tile's nodes read row 0; never stored)
+        for tt in range(NT):
+            L += [f'  const int xr{tt} = {(tt) * TN * D} + wave * {NT * TN * D} + (c16 < {TN * D} ? c16 : 0);']
+            if V:
+                L += [f'  const int an{tt} = min(g0 + xr{tt} / {D}, N - 1);']
+        L += [f'  mh_f4 acc[{NT}][{CT}];',
+              '#pragma unroll',
+              f'  for (int a = 0; a < {NT}; ++a)',
+              '#pragma unroll',
+              f'    for (int b = 0; b < {CT}; ++b) acc[a][b] = mh_f4{{0.f, 0.f, 0.f, 0.f}};',
+              '  load(0);',
+              '  store(0);',
+              '  __syncthreads();',
+              '  for (int c = 0; c < nch; ++c) {',
+              '    load(min(c + 1, nch - 1));',
+              '    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs',
+              f'    const float* __restrict__ xs = lds + (c & 1) * {XB};',
+              f'    const unsigned short* __restrict__ ws = reinterpret_cast<const unsigned short*>(lds + {2 * XB} + '
+              f'(c & 1) * {WB});']
+        if V:
+            L += ['    int oi_, mi_, uc_, v, wo_;', '    where(c, oi_, mi_, uc_, v, wo_);']
+        for tt in range(NT):
+            L += [f'    mh_bf8 a{tt}[3];',
+                  '    {',
+                  f'      const mh_f4 lo = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q);',
+                  f'      const mh_f4 hi = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q + 4);']
+            if V:
+                L += [f'      const float s = attr[(size_t)an{tt} * {V} + v];',
+                      '      const float v8[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, '
+                      'hi[2] * s, hi[3] * s};']
+            else:
+                L += ['      const float v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};']
+            L += [f'      mh_split8(v8, a{tt});', '    }']
+        PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
+        for ct in range(CT):
+            L += [f'    {{ mh_bf8 b[3];']
+            L += [f'      b[{p}] = *reinterpret_cast<const mh_bf8*>(ws + ({p * CW + 16 * ct} + c16) * {WS} + 8 * q);'
+                  for p in range(3)]
+            for pa, pb in PAIRS:
+                for tt in range(NT):
+                    L.append(f'      acc[{tt}][{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{tt}[{pa}], b[{pb}], '
+                             f'acc[{tt}][{ct}], 0, 0, 0);')
+            L += ['    }']
+        L += ['    store((c + 1) & 1);',
+              '    __syncthreads();',
+              '  }']
+        # epilogue: lane (c16, q) holds rows 4q + r, column 16 ct + c16 of each tile -> LDS [node][column][m] ->
+        # coalesced float4 rows of CW d floats per node
+        L += ['#pragma unroll',
+              f'  for (int tt = 0; tt < {NT}; ++tt)',
+              '#pragma unroll',
+              '    for (int r = 0; r < 4; ++r) {',
+              '      const int row = 4 * q + r;',
+              f'      if (row < {TN * D}) {{',
+              f'        const int rr = tt * {TN * D} + wave * {NT * TN * D} + row, nl = rr / {D}, m = rr - nl * {D};',
+              '#pragma unroll',
+              f'        for (int ct = 0; ct < {CT}; ++ct)',
+              f'          lds[(nl * {CW} + 16 * ct + c16) * {D} + m] = acc[tt][ct][r];',
+              '      }',
+              '    }',
+              '  __syncthreads();',
+              f'  for (int f = t; f < ng * {CW * D // 4}; f += {BLOCK}) {{',
+              f'    const int nl = f / {CW * D // 4}, j = f - nl * {CW * D // 4};',
+              f'    *reinterpret_cast<mh_f4*>(out + (size_t)(g0 + nl) * {Dout} + {oo} + col0 * {D} + 4 * j) = '
+              f'*reinterpret_cast<const mh_f4*>(lds + nl * {CW * D} + 4 * j);',
+              '  }',
+              '}', '']
+        fns += L
+        cases.append((o, fn))
+    gy = _grid_y(out_blocks)
+    VW = (V + 31) // 32
+    sw = ['  switch (blockIdx.y) {']
+    for y, (o, cg) in enumerate(gy):
+        fn = dict(cases)[o]
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist); break;')
+    sw += ['    default: break;', '  }']
+    lds_max = max(lds_max, 4)
+    K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
+         '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N) {',
+         f'  __shared__ __align__(16) float lds[{lds_max}];',
+         f'  __shared__ unsigned amask[{max(VW, 1)}];',
+         f'  __shared__ int vlist[{V + 1}];',
+         '  (void)amask; (void)vlist;',
+         '  const int group = blockIdx.x;'] + sw + ['}', '']
+    return fns + K
+
+
+# ---------------------------------------------------------------- the fp32 family (short K, attribute terms)
 
 def _tiles_mode(terms_o, in_blocks, V):
     """One tile per wave with the whole K loop (long K: the pipeline hides the load latency), or one tile per
@@ -276,30 +532,8 @@ def _kloop(ld, CT, first, step, count, ind):
     return L
 
 
-def _mask(V, first, count):
-    """The workgroup's list of attributes that are nonzero somewhere in its nodes (vlist[0] = count)."""
-    VW = (V + 31) // 32
-    return [f'  if (t < {VW}) amask[t] = 0u;',
-            '  __syncthreads();',
-            f'  for (int f = t; f < {count} * {V}; f += {BLOCK}) {{',
-            f'    if (attr[(size_t){first} * {V} + f] != 0.f) {{ const int v = f % {V}; '
-            'atomicOr(&amask[v >> 5], 1u << (v & 31)); }',
-            '  }',
-            '  __syncthreads();',
-            '  if (t == 0) {',
-            '    int c = 0;',
-            f'    for (int w = 0; w < {VW}; ++w) {{',
-            '      unsigned b = amask[w];',
-            '      while (b) { vlist[1 + c++] = w * 32 + __builtin_ctz(b); b &= b - 1u; }',
-            '    }',
-            '    vlist[0] = c;',
-            '  }',
-            '  __syncthreads();',
-            '  const int nact = vlist[0];']
-
-
-def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout):
-    """HIP source of one direction.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x a
+def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
+    """HIP source of one direction on the fp32 matrix cores.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x a
     group of nodes.  A tile is TN = 16 // d whole nodes, i.e. <= 16 rows (node, m) — one MFMA row tile — and CW
     channels.  Each block runs in one of two modes (``_tiles_mode``):
 
@@ -416,19 +650,59 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout):
     return fns + K
 
 
-def source(spec):
-    """HIP source of ``lin_fwd`` and ``lin_bwd`` for one module."""
-    L = [_native.device_header(), 'typedef float mh_f4 __attribute__((ext_vector_type(4)));', '']
-    L += _kernel(spec.kname('lin_fwd'), spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din, spec.Dout)
-    if spec.has_bwd:
-        L += _kernel(spec.kname('lin_bwd'), spec.out_blocks, spec.in_blocks, spec.bterms, spec.V, spec.Dout, spec.Din)
-    return '\n'.join(L)
-
-
-def _tiles(blocks, terms, in_blocks, V):
+def _f32_nodes_per_launch_group(blocks, terms, in_blocks, V):
     """Nodes per workgroup of the launch (its rows per block): the smallest over the output blocks; blocks with more
     nodes per workgroup leave their trailing workgroups idle."""
     return min(_nodes_per_group(terms[o], in_blocks, V, l) for o, (_, l, *_) in enumerate(blocks))
+
+
+def _mask(V, first, count):
+    """The workgroup's list of attributes that are nonzero somewhere in its nodes (vlist[0] = count)."""
+    VW = (V + 31) // 32
+    return [f'  if (t < {VW}) amask[t] = 0u;',
+            '  __syncthreads();',
+            f'  for (int f = t; f < {count} * {V}; f += {BLOCK}) {{',
+            f'    if (attr[(size_t){first} * {V} + f] != 0.f) {{ const int v = f % {V}; '
+            'atomicOr(&amask[v >> 5], 1u << (v & 31)); }',
+            '  }',
+            '  __syncthreads();',
+            '  if (t == 0) {',
+            '    int c = 0;',
+            f'    for (int w = 0; w < {VW}; ++w) {{',
+            '      unsigned b = amask[w];',
+            '      while (b) { vlist[1 + c++] = w * 32 + __builtin_ctz(b); b &= b - 1u; }',
+            '    }',
+            '    vlist[0] = c;',
+            '  }',
+            '  __syncthreads();',
+            '  const int nact = vlist[0];']
+
+
+def use_bf16(spec, backward=False):
+    """Which kernel family a direction gets: the bf16x6 LDS-staged one for attribute-free maps with at least 1024
+    outputs (MACE's interaction linears: long K over many irreps blocks, every weight chunk shared by a workgroup's
+    eight row tiles); the fp32 one with per-wave register pipelines otherwise (short K and scalar-only blocks, whose
+    few workgroups and short chunk chains favour it, and skip_tp's attribute terms)."""
+    return spec.V == 0 and (spec.Din if backward else spec.Dout) >= 1024
+
+
+def source(spec):
+    """HIP source of ``lin_fwd`` and ``lin_bwd`` for one module."""
+    L = [_native.device_header(), '']
+    if use_bf16(spec):
+        L += _kernel(spec.kname('lin_fwd'), spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din, spec.Dout,
+                     spec.pack_fwd[1], spec.pack_fwd[2])
+    else:
+        L += _kernel_f32(spec.kname('lin_fwd'), spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din,
+                         spec.Dout)
+    if spec.has_bwd:
+        if use_bf16(spec, backward=True):
+            L += _kernel(spec.kname('lin_bwd'), spec.out_blocks, spec.in_blocks, spec.bterms, spec.V, spec.Dout,
+                         spec.Din, spec.pack_bwd[1], spec.pack_bwd[2])
+        else:
+            L += _kernel_f32(spec.kname('lin_bwd'), spec.out_blocks, spec.in_blocks, spec.bterms, spec.V, spec.Dout,
+                             spec.Din)
+    return '\n'.join(L)
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
@@ -496,15 +770,21 @@ class HipNodeLinear(torch.nn.Module):
         code = _native.compile_source(self.source)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
-            kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK, _tiles(s.out_blocks, s.terms, s.in_blocks, s.V),
+            def group(blocks, terms, in_blocks, bf16):
+                return (_nodes_per_launch_group(blocks) if bf16 else
+                        _f32_nodes_per_launch_group(blocks, terms, in_blocks, s.V))
+            kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK,
+                                            group(s.out_blocks, s.terms, s.in_blocks, use_bf16(s)),
                                             len(_grid_y(s.out_blocks)))}
             if s.has_bwd:
                 kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK,
-                                               _tiles(s.in_blocks, s.bterms, s.out_blocks, s.V),
+                                               group(s.in_blocks, s.bterms, s.out_blocks, use_bf16(s, True)),
                                                len(_grid_y(s.in_blocks)))
             self.module = _native.Module(code, kernels)
-        self.register_buffer('W', torch.tensor(s.W, dtype=torch.float32, device=dev), persistent=False)
-        self.register_buffer('Wt', torch.tensor(s.Wt, dtype=torch.float32, device=dev), persistent=False)
+        # the bf16 family reads its weights as bf16 parts (int16 bit patterns), the fp32 family as float32
+        for name, bf16, pk, w in (('W', use_bf16(s), s.pack_fwd[0], s.W), ('Wt', use_bf16(s, True), s.pack_bwd[0], s.Wt)):
+            buf = torch.from_numpy(pk.view(np.int16)) if bf16 else torch.tensor(w, dtype=torch.float32)
+            self.register_buffer(name, buf.to(dev), persistent=False)
         for k in ('irreps_in', 'irreps_in1', 'irreps_in2', 'irreps_out'):
             if hasattr(mod, k):
                 setattr(self, k, getattr(mod, k))

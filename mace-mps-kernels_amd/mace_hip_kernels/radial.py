@@ -199,30 +199,7 @@ def source(spec):
     lds_fwd = max(Lo['tr_size'], Lo['chunk_fwd'])        # floats; a bf16 chunk of n elements takes n / 2 floats
     lds_bwd = max(Lo['nat_size'], Lo['chunk_bwd'])
     L = [_native.device_header(),
-         'typedef float mh_f4 __attribute__((ext_vector_type(4)));',
-         'typedef __bf16 mh_bf8 __attribute__((ext_vector_type(8)));',
-         'typedef unsigned int mh_u4 __attribute__((ext_vector_type(4)));', '',
-         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '',
-         '// exact split of eight floats into three bf16 parts each (v = hi + mid + lo), as three bf16x8 operands',
-         '__device__ __forceinline__ void mh_split8(const float (&v)[8], mh_bf8 (&s)[3]) {',
-         '  unsigned p[3][4];',
-         '#pragma unroll',
-         '  for (int j = 0; j < 8; j += 2) {',
-         '    unsigned b[2][3];',
-         '#pragma unroll',
-         '    for (int e = 0; e < 2; ++e) {',
-         '      const unsigned hb = __float_as_uint(v[j + e]) & 0xFFFF0000u;',
-         '      const float r1 = v[j + e] - __uint_as_float(hb);',
-         '      const unsigned mb = __float_as_uint(r1) & 0xFFFF0000u;',
-         '      const float r2 = r1 - __uint_as_float(mb);',
-         '      b[e][0] = hb >> 16; b[e][1] = mb >> 16; b[e][2] = __float_as_uint(r2) >> 16;',
-         '    }',
-         '#pragma unroll',
-         '    for (int k = 0; k < 3; ++k) p[k][j / 2] = b[0][k] | (b[1][k] << 16);',
-         '  }',
-         '#pragma unroll',
-         '  for (int k = 0; k < 3; ++k) s[k] = __builtin_bit_cast(mh_bf8, mh_u4{p[k][0], p[k][1], p[k][2], p[k][3]});',
-         '}', '']
+         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '']
 
     def head(name, args, lds, nb, waves=BLOCK // 64):
         P = [f'extern "C" __global__ __launch_bounds__({64 * waves}) void {name}({args}) {{',
