@@ -440,7 +440,9 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     sw += ['    default: break;', '  }']
     lds_max = max(lds_max, 4)
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
-         '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N) {',
+         '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N,',
+         '    const int* __restrict__ order) {',
+         '  (void)order;                                  // attribute-free: node order does not matter',
          f'  __shared__ __align__(16) float lds[{lds_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];',
@@ -473,13 +475,15 @@ def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH):
     vecx = D == 1 and Din % 4 == 0 and oi % 4 == 0 and mi % 8 == 0
     wt = {4: 'float4', 2: 'float2', 1: 'float'}[CT]
     L = [f'__device__ __forceinline__ void {fn}_ld{i}(const float* __restrict__ x, const float* __restrict__ attr,',
-         '    const float* __restrict__ W, const int* __restrict__ vlist, int n0, int col0, int anl, int am,',
+         '    const float* __restrict__ W, const int* __restrict__ vlist, const int* __restrict__ order, int n0, int col0,',
+         '    int anl, int am,'
          f'    int q, int c16, int c, float (&ra)[{KC // 4}], float (&rb)[{KC // 4}][{CT}]) {{',
          f'  const int v = {vsel}, k0 = (c % {NCH}) * {KC} + 8 * q;',
-         '  (void)v; (void)vlist; (void)attr;',
-         f'  const float* __restrict__ xr = x + (size_t)(n0 + anl) * {Din} + {oi} + am;']
+         '  (void)v; (void)vlist; (void)attr; (void)order;',
+         f'  const int nr = {"order ? order[n0 + anl] : " if V else ""}n0 + anl;   // the row\'s node',
+         f'  const float* __restrict__ xr = x + (size_t)nr * {Din} + {oi} + am;']
     if V:
-        L.append(f'  const float s = attr[(size_t)(n0 + anl) * {V} + v];')
+        L.append(f'  const float s = attr[(size_t)nr * {V} + v];')
     if vecx:
         # mi % 8 == 0: the lane's 8 channels are all in range or all out of range
         L += [f'  const bool okx = k0 < {mi};',
@@ -556,7 +560,9 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
         G = WAVES * TN if tiles else TN                       # nodes per workgroup
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const float* __restrict__ W, float* __restrict__ out, int N, int group, int cg, float* __restrict__ red,',
-             '    unsigned* __restrict__ amask, int* __restrict__ vlist) {',
+             '    unsigned* __restrict__ amask, int* __restrict__ vlist, const int* __restrict__ order) {',
+             f'  auto nd = [&](int i) {{ return {"order ? order[i] : " if V else ""}i; }};   // node of position i',
+             '  (void)order;',
              f'  const int g0 = group * {G};                 // first node of the workgroup',
              '  if (g0 >= N) return;',
              f'  const int ng = min({G}, N - g0);',
@@ -564,7 +570,7 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
         if not terms[o]:
             L += [f'  for (int f = t; f < ng * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D};',
-                  f'    out[(size_t)(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
+                  f'    out[(size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
                   '  }', '}', '']
             fns += L
             cases.append((o, fn))
@@ -584,14 +590,14 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
               '#pragma unroll',
               f'  for (int c = 0; c < {CT}; ++c) acc[c] = mh_f4{{0.f, 0.f, 0.f, 0.f}};']
         if V:
-            L += _mask(V, 'g0', 'ng')
+            L += _mask(V, 'g0', 'ng', ordered=True)
         for (i, woff) in terms[o]:
             mi, li, oi, _ = in_blocks[i]
             assert li == l
             NCH = -(-mi // KC)
             nchunks = f'nact * {NCH}' if V else f'{NCH}'
             fns += _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH)
-            ld = f'{fn}_ld{i}(x, attr, W, vlist, nb, col0, anl, am, q, c16'
+            ld = f'{fn}_ld{i}(x, attr, W, vlist, order, nb, col0, anl, am, q, c16'
             if tiles:
                 L += ['  if (wlive) {', f'    const int nch = {nchunks};']
                 L += _kloop(ld, CT, '0', 1, 'nch', '    ')
@@ -607,11 +613,11 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
                   '      const int row = 4 * q + r;',
                   f'      if (row < nn * {D}) {{']
             if D == 1 and CT == 4 and Dout % 4 == 0 and oo % 4 == 0:
-                L += [f'        *reinterpret_cast<float4*>(out + (size_t)(n0 + row) * {Dout} + {oo} + col0 + 4 * c16) =',
+                L += [f'        *reinterpret_cast<float4*>(out + (size_t)nd(n0 + row) * {Dout} + {oo} + col0 + 4 * c16) =',
                       '            make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);']
             else:
                 L += [f'        const int nl = row / {D}, m = row - nl * {D};',
-                      f'        float* __restrict__ o = out + (size_t)(n0 + nl) * {Dout} + {oo} + m;']
+                      f'        float* __restrict__ o = out + (size_t)nd(n0 + nl) * {Dout} + {oo} + m;']
                 L += [f'        o[(col0 + {CT} * c16 + {ct}) * {D}] = acc[{ct}][r];' for ct in range(CT)]
             L += ['      }', '    }', '  }', '}', '']
         else:
@@ -626,7 +632,7 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
                   f'  for (int f = t; f < nn * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D}, cc = j / {D}, m = j - cc * {D};',
                   f'    const int row = nl * {D} + m;',
-                  f'    out[(size_t)(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = (red[row * {CW} + cc] + '
+                  f'    out[(size_t)nd(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = (red[row * {CW} + cc] + '
                   f'red[(16 + row) * {CW} + cc])',
                   f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]);',
                   '  }',
@@ -639,10 +645,11 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
     sw = ['  switch (blockIdx.y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order); break;')
     sw += ['    default: break;', '  }']
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
-         '    const float* __restrict__ attr, const float* __restrict__ W, float* __restrict__ out, int N) {',
+         '    const float* __restrict__ attr, const float* __restrict__ W, float* __restrict__ out, int N,',
+         '    const int* __restrict__ order) {',
          f'  __shared__ float red[{4 * 16 * cw_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];',
@@ -656,13 +663,15 @@ def _f32_nodes_per_launch_group(blocks, terms, in_blocks, V):
     return min(_nodes_per_group(terms[o], in_blocks, V, l) for o, (_, l, *_) in enumerate(blocks))
 
 
-def _mask(V, first, count):
-    """The workgroup's list of attributes that are nonzero somewhere in its nodes (vlist[0] = count)."""
+def _mask(V, first, count, ordered=False):
+    """The workgroup's list of attributes that are nonzero somewhere in its nodes (vlist[0] = count); with
+    ``ordered`` position i of the workgroup is node nd(i)."""
     VW = (V + 31) // 32
+    row = f'(size_t)nd({first} + f / {V}) * {V} + f % {V}' if ordered else f'(size_t){first} * {V} + f'
     return [f'  if (t < {VW}) amask[t] = 0u;',
             '  __syncthreads();',
             f'  for (int f = t; f < {count} * {V}; f += {BLOCK}) {{',
-            f'    if (attr[(size_t){first} * {V} + f] != 0.f) {{ const int v = f % {V}; '
+            f'    if (attr[{row}] != 0.f) {{ const int v = f % {V}; '
             'atomicOr(&amask[v >> 5], 1u << (v & 31)); }',
             '  }',
             '  __syncthreads();',
@@ -705,6 +714,20 @@ def source(spec):
     return '\n'.join(L)
 
 
+_ORDER = [None, None]     # (key, order) of the last attribute tensor seen
+
+
+def node_order(attrs):
+    """int32 permutation of the nodes sorted by species (argmax of the attributes), cached for the attribute tensor
+    most recently seen (MACE's one-hot node_attrs are shared by every skip_tp of a call).  The results do not depend
+    on it, so a stale cache entry (reused memory with the same shape) costs speed only."""
+    key = (attrs.data_ptr(), attrs.shape, attrs._version, attrs.device)
+    if _ORDER[0] != key:
+        _ORDER[1] = torch.argsort(attrs.argmax(1), stable=True).to(torch.int32)
+        _ORDER[0] = key
+    return _ORDER[1]
+
+
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
                     'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
 
@@ -731,9 +754,12 @@ class _LinFn(torch.autograd.Function):
                 raise TypeError('node attributes must be float32 on the input\'s device')
             a2 = attrs.reshape(-1, s.V).contiguous()
         out = torch.empty(N, s.Dout, device=x.device, dtype=torch.float32)
+        order = node_order(a2) if a2 is not None and N > 0 else None
         _native.launch(f'lin_fwd[{op.tag}]', _native.load().mh_lin_fwd, op.module.handle, _native.ptr(x2),
-                       _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), N, _native.stream_of(x2))
-        ctx.save_for_backward(a2) if a2 is not None else ctx.save_for_backward()
+                       _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), _native.ptr(order), N,
+                       _native.stream_of(x2))
+        if a2 is not None:
+            ctx.save_for_backward(a2, order)
         ctx.op, ctx.lead, ctx.N = op, lead, N
         return out.reshape(*lead, s.Dout)
 
@@ -750,11 +776,12 @@ class _LinFn(torch.autograd.Function):
         if not s.has_bwd:
             raise NotImplementedError(f'mace_hip_kernels: {op.tag} has input multiplicities that the backward kernel '
                                       'does not tile (multiples of 16 needed)')
-        a2 = ctx.saved_tensors[0] if ctx.saved_tensors else None
+        a2, order = ctx.saved_tensors if ctx.saved_tensors else (None, None)
         g2 = g.reshape(-1, s.Dout).contiguous()
         gx = torch.empty(ctx.N, s.Din, device=g.device, dtype=torch.float32)
         _native.launch(f'lin_bwd[{op.tag}]', _native.load().mh_lin_bwd, op.module.handle, _native.ptr(g2),
-                       _native.ptr(a2), _native.ptr(op.Wt), _native.ptr(gx), ctx.N, _native.stream_of(g2))
+                       _native.ptr(a2), _native.ptr(op.Wt), _native.ptr(gx), _native.ptr(order), ctx.N,
+                       _native.stream_of(g2))
         return gx.reshape(*ctx.lead, s.Din), None, None
 
 

@@ -440,17 +440,24 @@ def test_node_linear_c_abi_and_errors():
     a = torch.eye(s.V, device=dev)[torch.randint(0, s.V, (n,), device=dev)]
     out, gx = torch.empty(n, s.Dout, device=dev), torch.empty(n, s.Din, device=dev)
     lib, P, st = _native.load(), _native.ptr, _native.stream_of(x)
-    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out), n, st), 'lin_fwd')
-    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx), n, st), 'lin_bwd')
+    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out), None, n, st), 'lin_fwd')
+    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx), None, n, st), 'lin_bwd')
     torch.cuda.synchronize()
     ref = op(x, a)
     assert torch.equal(out, ref)
     # <out, out> = <gx, x> for gx = L^T out
     assert abs(_dot(gx, x) - _dot(out, out)) <= 1e-5 * abs(_dot(out, out))
-    assert lib.mh_lin_fwd(op.module.handle, None, P(a), P(op.W), P(out), n, st) != 0
+    # the node order is a walking order only: any permutation gives the same numbers (zero terms add exactly 0)
+    perm = torch.randperm(n, device=dev).to(torch.int32)
+    out_p, gx_p = torch.empty_like(out), torch.empty_like(gx)
+    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out_p), P(perm), n, st), 'lin_fwd')
+    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx_p), P(perm), n, st), 'lin_bwd')
+    torch.cuda.synchronize()
+    assert torch.equal(out_p, out) and torch.equal(gx_p, gx)
+    assert lib.mh_lin_fwd(op.module.handle, None, P(a), P(op.W), P(out), None, n, st) != 0
     assert b'NULL' in lib.mh_last_error()
     conv = HipConvTP(_tp('32x0e+32x1o', 2), device=dev)
-    assert lib.mh_lin_fwd(conv.module.handle, P(x), P(a), P(op.W), P(out), n, st) != 0
+    assert lib.mh_lin_fwd(conv.module.handle, P(x), P(a), P(op.W), P(out), None, n, st) != 0
     assert b'not bound' in lib.mh_last_error()
 
 
