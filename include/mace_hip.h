@@ -175,31 +175,31 @@ int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int6
  * irreps layout [.., u * (2l+1) + m] per block).  Without attrs (attrs NULL) it is e3nn's o3.Linear:
  *   out[n, o, w, m] = sum_{i: irrep_i = irrep_o} sum_u x[n, i, u, m] W_io[u, w];
  * with V scalar attrs it is the tensor product x (x) attrs over 0e attrs (MACE's skip_tp, FullyConnectedTensorProduct
- * with node_attrs): out[n, o, w, m] = sum_i sum_{u, v} x[n, i, u, m] attrs[n, v] W_io[u, v, w], terms whose attrs are
- * zero over a whole tile of nodes skipped.  W holds the module's weights (path normalisation folded in) in the layout
- * of the module's kernel family: for the bf16 family (attribute-free maps with >= 1024 outputs) each fp32 value split
- * exactly into three bf16 parts (uint16 bit patterns) in streaming order — per output block, column group of up to
- * 64 channels, input block and chunk of 32 input channels, a [part][column][channel] slice; for the fp32 family the
- * float32 blocks W_io[u, v, w] one after another.  The block layout, family and offsets are compiled into the module
- * (attrs must not be NULL for a module with attributes).  order (NULL: identity) is an optional permutation of the
- * N nodes in which the kernels walk them — the results do not depend on it; sorting the nodes by species (the one-hot
- * attrs' argmax) lets a workgroup skip every attribute term but one.  mh_lin_bwd computes gx
- * from g [N, Dout] the same way with the transposed weights Wt_oi[w, v, u].  No reference counterpart: the
- * reference leaves the model's linears and skip_tp on e3nn (o3.Linear / o3.FullyConnectedTensorProduct in the
- * interaction and product blocks). */
+ * with node_attrs):
+ *   out[n, o, w, m] = sum_i sum_{u, v} x[n, i, u, m] attrs[n, v] W_io[u, v, w],
+ * terms whose attrs are zero over a whole tile of nodes skipped.  W holds the module's weights (path normalisation folded in) in the layout of the module's kernel
+ * family: for the bf16 family (attribute-free maps with >= 1024 outputs) each fp32 value split exactly into three
+ * bf16 parts (uint16 bit patterns) in streaming order — per output block, column group of up to 64 channels, input
+ * block and chunk of 32 input channels, a [part][channel / 8][column][8] slice; for the fp32 family the float32
+ * blocks W_io[u, v, w] one after another.  The block layout, family and offsets are compiled into the module (attrs
+ * must not be NULL for a module with attributes).  order (NULL: identity) is an optional permutation of the N nodes
+ * in which the kernels walk them — the results do not depend on it; sorting the nodes by species (the one-hot
+ * attrs' argmax) lets a workgroup skip every attribute term but one.  mh_lin_bwd computes gx from g [N, Dout] the
+ * same way with the transposed weights Wt_oi[w, v, u].  No reference counterpart: the reference leaves the model's
+ * linears and skip_tp on e3nn (o3.Linear / o3.FullyConnectedTensorProduct in the interaction and product blocks). */
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
                int32_t N, void* stream);
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,
                int32_t N, void* stream);
 
-/* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers
- * h <- c_i * silu(h A_i) and a linear output layer, MACE's conv_tp_weights (an e3nn FullyConnectedNet).  Wh holds the
- * hidden layers' fp32 weights in the module's LDS layout; Wl the output layer [n_hidden_last, n_out] split exactly
- * into three bf16 parts (bit patterns), cut into chunks of 32 columns (the last zero-padded): for mh_mlp_fwd
- * [chunk][part][column][hidden] with the hidden index in the kernel's MFMA operand order, for mh_mlp_bwd
- * [chunk][part][hidden][column].  The layer widths are compiled into the module.  mh_mlp_bwd gives gef = dL/def from
- * gW0 = dL/dW0.  No reference counterpart: the reference leaves the radial MLP on e3nn (FullyConnectedNet in MACE's
- * interaction blocks). */
+/* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers h <- c_i *
+ * silu(h A_i) and a linear output layer, MACE's conv_tp_weights (an e3nn FullyConnectedNet).  Wh holds the hidden
+ * layers' fp32 weights in the module's LDS layout; Wl the output layer [n_hidden_last, n_out] split exactly into
+ * three bf16 parts (bit patterns), cut into chunks of 32 columns (the last zero-padded): for mh_mlp_fwd
+ * [chunk][part][hidden / 8][column][8] with the hidden index in the kernel's MFMA operand order, for mh_mlp_bwd
+ * [chunk][part][column / 8][hidden][8] (HipRadialMLP packs both).  The layer widths are compiled into the module.
+ * mh_mlp_bwd gives gef = dL/def from gW0 = dL/dW0.  No reference counterpart: the reference leaves the radial MLP
+ * on e3nn (FullyConnectedNet in MACE's interaction blocks). */
 int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E,
                void* stream);
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,

@@ -218,7 +218,8 @@ def _nodes_per_launch_group(blocks):
 def pack(blocks, terms, in_blocks, wmats, V):
     """The weights of one direction as the kernel streams them: for output block o, column group cg (CW columns),
     term (input block i), attribute v and chunk uc of 32 input channels, the [32, CW] slice of W_io[u, v, w]
-    (rows past mul_i zero) split exactly into three bf16 parts and stored [part][column][k] (uint16 bit patterns).
+    (rows past mul_i zero) split exactly into three bf16 parts and stored [part][k / 8][column][8] (uint16 bit
+    patterns).
     Returns (flat array, {(o, cg): element offset}, {o: [element offset of each term within a column group]})."""
     from .radial import bf16_split3
     VV = max(V, 1)
@@ -240,7 +241,9 @@ def pack(blocks, terms, in_blocks, wmats, V):
                         blk = np.zeros((KC, CW), dtype=np.float32)
                         rows = w[uc * KC:(uc + 1) * KC, v, cg * CW:(cg + 1) * CW]
                         blk[:rows.shape[0]] = rows
-                        out += [p.T.reshape(-1) for p in bf16_split3(blk)]
+                        # [part][k / 8][column][8]: columns innermost, so the eight lanes of an LDS write phase
+                        # hit eight different rows of the staged chunk (conflict-free)
+                        out += [p.T.reshape(CW, KC // 8, 8).transpose(1, 0, 2).reshape(-1) for p in bf16_split3(blk)]
                         off += 3 * CW * KC
     flat = np.concatenate(out) if out else np.zeros(8, dtype=np.uint16)
     return flat, base, toffs
@@ -359,8 +362,9 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                       '      } }']
         for k in range(iw):
             guard = '' if (k + 1) * BLOCK <= NWP else f'if (t + {k * BLOCK} < {NWP}) '
-            L += [f'    {guard}{{ const int f = t + {k * BLOCK}, row = f / {KC // 8}, k8 = f - row * {KC // 8};',
-                  f'      *reinterpret_cast<mh_u4*>(ws + row * {WS} + 8 * k8) = pw{k}; }}']
+            L += [f'    {guard}{{ const int f = t + {k * BLOCK}, p = f / {CW * KC // 8}, r = f - p * {CW * KC // 8},',
+                  f'        k8 = r / {CW}, col = r - k8 * {CW};',
+                  f'      *reinterpret_cast<mh_u4*>(ws + (p * {CW} + col) * {WS} + 8 * k8) = pw{k}; }}']
         L += ['  };']
         # the lane's A rows: row c16 of each of its tiles (rows past the tile's nodes read row 0; never stored)
         for tt in range(NT):

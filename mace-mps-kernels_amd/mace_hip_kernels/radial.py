@@ -274,9 +274,10 @@ def source(spec):
         return P
 
     def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None, reg='pre'):
-        """Load (store_base None) or store this thread's 16-byte pieces of a bf16 chunk: piece f is part p, row rr,
-        8-element group c8 of a [3][nrows][row_elems] block at element offset nx_elems of ``src``; in LDS the rows
-        are ``rs`` elements apart."""
+        """Load (store_base None) or store this thread's 16-byte pieces of a bf16 chunk: piece f is part p, 8-element
+        group c8, row rr of a [3][row_elems / 8][nrows][8] block at element offset nx_elems of ``src`` (rows
+        innermost, so the eight lanes of one LDS write phase hit eight different rows: conflict-free for any row
+        stride that is 4 words mod 8 banks); in LDS the rows are ``rs`` elements apart."""
         per_row = row_elems // 8
         total = NSPLIT * nrows * per_row
         P = []
@@ -284,7 +285,7 @@ def source(spec):
             exact = (it + 1) * BLOCK <= total
             fx = f't + {it * BLOCK}' if exact else f'min(t + {it * BLOCK}, {total - 1})'
             idx = [f'{ind}{{ const int f = {fx}, p = f / {nrows * per_row}, rem = f - p * {nrows * per_row},',
-                   f'{ind}      rr = rem / {per_row}, c8 = rem - rr * {per_row};']
+                   f'{ind}      c8 = rem / {nrows}, rr = rem - c8 * {nrows};']
             if store_base is None:
                 P += idx + [f'{ind}  {reg}{it} = *reinterpret_cast<const mh_u4*>({src} + (size_t){nx_elems} + '
                             f'(size_t)f * 8); }}']
@@ -488,7 +489,8 @@ def packed_weights(spec):
     output layer bf16 chunks)}.  Hidden layer i is laid out as the kernel's LDS copy: natural [k][j + PAD] (the first
     layer's K padded to a multiple of 4 with zero rows) or transposed [j][k + PAD].  The output layer W [HL, NW] is
     split exactly into three bf16 parts (uint16 bit patterns) and cut into chunks of CH_FWD / CH_BWD columns (the last
-    zero-padded): forward [chunk][3][CH_FWD][HL] with K in the ``_kperm`` order, backward [chunk][3][HL][CH_BWD]."""
+    zero-padded): forward [chunk][3][HL / 8][CH_FWD][8] with K in the ``_kperm`` order, backward
+    [chunk][3][CH_BWD / 8][HL][8] (16-byte groups of a row, rows innermost)."""
     Lo = _layout(spec)
     nat = np.zeros(Lo['nat_size'])
     tr = np.zeros(Lo['tr_size'])
@@ -509,8 +511,10 @@ def packed_weights(spec):
     perm = _kperm(HL)
     parts, n = padded(CH_FWD)
     fwd = np.stack([p.reshape(HL, n, CH_FWD).transpose(1, 2, 0)[:, :, perm] for p in parts], axis=1)
+    fwd = fwd.reshape(n, 3, CH_FWD, HL // 8, 8).transpose(0, 1, 3, 2, 4)        # rows innermost (see chunk_io)
     parts, n = padded(CH_BWD)
     bwd = np.stack([p.reshape(HL, n, CH_BWD).transpose(1, 0, 2) for p in parts], axis=1)
+    bwd = bwd.reshape(n, 3, HL, CH_BWD // 8, 8).transpose(0, 1, 3, 2, 4)
     return {'fwd': (tr.astype(np.float32), np.ascontiguousarray(fwd).reshape(-1)),
             'bwd': (nat.astype(np.float32), np.ascontiguousarray(bwd).reshape(-1))}
 

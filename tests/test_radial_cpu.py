@@ -41,7 +41,7 @@ def _unpack(buf, spec, fwd):
     CH = radial.CH_FWD if fwd else radial.CH_BWD
     nch = -(-NW // CH)
     if fwd:
-        p = np.ascontiguousarray(buf).reshape(nch, 3, CH, HL)
+        p = buf.reshape(nch, 3, HL // 8, CH, 8).transpose(0, 1, 3, 2, 4).reshape(nch, 3, CH, HL)
         w = _bf16(p[:, 0]) + _bf16(p[:, 1]) + _bf16(p[:, 2])          # exact: the parts do not overlap
         out = np.zeros((HL, nch * CH), dtype=np.float32)
         for pos in range(HL):
@@ -50,7 +50,7 @@ def _unpack(buf, spec, fwd):
             t, r = divmod(j, 4)
             out[32 * s_ + 16 * t + 4 * q + r] = w[:, :, pos].reshape(-1)
     else:
-        p = buf.reshape(nch, 3, HL, CH)
+        p = buf.reshape(nch, 3, CH // 8, HL, 8).transpose(0, 1, 3, 2, 4).reshape(nch, 3, HL, CH)
         w = _bf16(p[:, 0]) + _bf16(p[:, 1]) + _bf16(p[:, 2])
         out = w.transpose(1, 0, 2).reshape(HL, nch * CH)
     assert not np.any(out[:, NW:]), 'padding columns must be zero'
