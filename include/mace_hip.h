@@ -184,13 +184,14 @@ int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int6
  * blocks W_io[u, v, w] one after another.  The block layout, family and offsets are compiled into the module (attrs
  * must not be NULL for a module with attributes).  order (NULL: identity) is an optional permutation of the N nodes
  * in which the kernels walk them — the results do not depend on it; sorting the nodes by species (the one-hot
- * attrs' argmax) lets a workgroup skip every attribute term but one.  mh_lin_bwd computes gx from g [N, Dout] the
+ * attrs' argmax) lets a workgroup skip every attribute term but one.  Outputs are scaled by alpha (1 for the plain
+ * map; MACE divides the interaction linear's output by avg_num_neighbors).  mh_lin_bwd computes gx from g [N, Dout] the
  * same way with the transposed weights Wt_oi[w, v, u].  No reference counterpart: the reference leaves the model's
  * linears and skip_tp on e3nn (o3.Linear / o3.FullyConnectedTensorProduct in the interaction and product blocks). */
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
-               int32_t N, void* stream);
+               float alpha, int32_t N, void* stream);
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,
-               int32_t N, void* stream);
+               float alpha, int32_t N, void* stream);
 
 /* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers h <- c_i *
  * silu(h A_i) and a linear output layer, MACE's conv_tp_weights (an e3nn FullyConnectedNet).  Wh holds the hidden

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 14; }
+int mh_version(void) { return 15; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -282,16 +282,16 @@ int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int6
 }
 
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
-               int32_t N, void* stream) {
+               float alpha, int32_t N, void* stream) {
     if (N > 0 && (!x || !W || !out)) return fail(-1, "mh_lin_fwd: NULL x, W or out");
-    void* args[] = {&x, &attrs, &W, &out, &N, &order};
+    void* args[] = {&x, &attrs, &W, &out, &N, &order, &alpha};
     return launch(m, MH_LIN_FWD, N, args, stream, "mh_lin_fwd");
 }
 
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,
-               int32_t N, void* stream) {
+               float alpha, int32_t N, void* stream) {
     if (N > 0 && (!g || !Wt || !gx)) return fail(-1, "mh_lin_bwd: NULL g, Wt or gx");
-    void* args[] = {&g, &attrs, &Wt, &gx, &N, &order};
+    void* args[] = {&g, &attrs, &Wt, &gx, &N, &order, &alpha};
     return launch(m, MH_LIN_BWD, N, args, stream, "mh_lin_bwd");
 }
 

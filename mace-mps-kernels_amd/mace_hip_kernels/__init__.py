@@ -189,6 +189,11 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 skipped.append((name, why))
                 continue
             new.tag = name
+            # MACE's interaction blocks divide the post-convolution linear's output by avg_num_neighbors
+            # (message = self.linear(message) / self.avg_num_neighbors): the division is folded into the kernels
+            avg = getattr(parent, 'avg_num_neighbors', None)
+            if attr == 'linear' and hasattr(parent, 'conv_tp') and isinstance(avg, (int, float)) and avg:
+                new.div_hint = float(avg)
             setattr(parent, attr, new)
             patched.append(name)
     if verbose:

@@ -20,7 +20,7 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD, MH_LIN_FWD, MH_LIN_BWD, \
     MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD = range(23)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -49,8 +49,8 @@ _SIGS = {
     'mh_conv_fwd_cut': (ctypes.c_int, [_P] * 9 + [_I, _P]),
     'mh_sh_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int64, _P]),
     'mh_sh_bwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
-    'mh_lin_fwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_int, _P]),
-    'mh_lin_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_int, _P]),
+    'mh_lin_fwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, ctypes.c_int, _P]),
+    'mh_lin_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, ctypes.c_int, _P]),
     'mh_mlp_fwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_mlp_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
     'mh_emb_fwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),

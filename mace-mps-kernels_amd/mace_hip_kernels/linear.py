@@ -271,7 +271,8 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         fn = f'{name}_b{o}'
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const unsigned short* __restrict__ W, float* __restrict__ out, int N, int group, int cg,',
-             '    float* __restrict__ lds, unsigned* __restrict__ amask, int* __restrict__ vlist) {',
+             '    float* __restrict__ lds, unsigned* __restrict__ amask, int* __restrict__ vlist, float alpha) {',
+             '  (void)alpha;',
              f'  const int g0 = group * {G};                 // first node of the workgroup',
              '  if (g0 >= N) return;',
              f'  const int ng = min({G}, N - g0);',
@@ -423,7 +424,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
               f'        const int rr = tt * {TN * D} + wave * {NT * TN * D} + row, nl = rr / {D}, m = rr - nl * {D};',
               '#pragma unroll',
               f'        for (int ct = 0; ct < {CT}; ++ct)',
-              f'          lds[(nl * {CW} + 16 * ct + c16) * {D} + m] = acc[tt][ct][r];',
+              f'          lds[(nl * {CW} + 16 * ct + c16) * {D} + m] = alpha * acc[tt][ct][r];',
               '      }',
               '    }',
               '  __syncthreads();',
@@ -440,12 +441,12 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     sw = ['  switch (blockIdx.y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha); break;')
     sw += ['    default: break;', '  }']
     lds_max = max(lds_max, 4)
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N,',
-         '    const int* __restrict__ order) {',
+         '    const int* __restrict__ order, float alpha) {',
          '  (void)order;                                  // attribute-free: node order does not matter',
          f'  __shared__ __align__(16) float lds[{lds_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
@@ -564,7 +565,8 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
         G = WAVES * TN if tiles else TN                       # nodes per workgroup
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const float* __restrict__ W, float* __restrict__ out, int N, int group, int cg, float* __restrict__ red,',
-             '    unsigned* __restrict__ amask, int* __restrict__ vlist, const int* __restrict__ order) {',
+             '    unsigned* __restrict__ amask, int* __restrict__ vlist, const int* __restrict__ order, float alpha) {',
+             '  (void)alpha;',
              f'  auto nd = [&](int i) {{ return {"order ? order[i] : " if V else ""}i; }};   // node of position i',
              '  (void)order;',
              f'  const int g0 = group * {G};                 // first node of the workgroup',
@@ -618,11 +620,11 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
                   f'      if (row < nn * {D}) {{']
             if D == 1 and CT == 4 and Dout % 4 == 0 and oo % 4 == 0:
                 L += [f'        *reinterpret_cast<float4*>(out + (size_t)nd(n0 + row) * {Dout} + {oo} + col0 + 4 * c16) =',
-                      '            make_float4(acc[0][r], acc[1][r], acc[2][r], acc[3][r]);']
+                      '            make_float4(alpha * acc[0][r], alpha * acc[1][r], alpha * acc[2][r], alpha * acc[3][r]);']
             else:
                 L += [f'        const int nl = row / {D}, m = row - nl * {D};',
                       f'        float* __restrict__ o = out + (size_t)nd(n0 + nl) * {Dout} + {oo} + m;']
-                L += [f'        o[(col0 + {CT} * c16 + {ct}) * {D}] = acc[{ct}][r];' for ct in range(CT)]
+                L += [f'        o[(col0 + {CT} * c16 + {ct}) * {D}] = alpha * acc[{ct}][r];' for ct in range(CT)]
             L += ['      }', '    }', '  }', '}', '']
         else:
             # sum of the four waves' partial tiles, then coalesced per-node stores
@@ -636,9 +638,9 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
                   f'  for (int f = t; f < nn * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D}, cc = j / {D}, m = j - cc * {D};',
                   f'    const int row = nl * {D} + m;',
-                  f'    out[(size_t)nd(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = (red[row * {CW} + cc] + '
+                  f'    out[(size_t)nd(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = alpha * ((red[row * {CW} + cc] + '
                   f'red[(16 + row) * {CW} + cc])',
-                  f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]);',
+                  f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]));',
                   '  }',
                   '}', '']
         fns += L
@@ -649,11 +651,11 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
     sw = ['  switch (blockIdx.y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order, alpha); break;')
     sw += ['    default: break;', '  }']
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const float* __restrict__ W, float* __restrict__ out, int N,',
-         '    const int* __restrict__ order) {',
+         '    const int* __restrict__ order, float alpha) {',
          f'  __shared__ float red[{4 * 16 * cw_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];',
@@ -738,7 +740,7 @@ _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. 
 
 class _LinFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, attrs, op):
+    def forward(ctx, x, attrs, op, scale=1.0):
         s = op.spec
         if x.dtype != torch.float32 or not x.is_cuda:
             raise TypeError('mace_hip_kernels: node linears expect float32 GPU input')
@@ -760,11 +762,11 @@ class _LinFn(torch.autograd.Function):
         out = torch.empty(N, s.Dout, device=x.device, dtype=torch.float32)
         order = node_order(a2) if a2 is not None and N > 0 else None
         _native.launch(f'lin_fwd[{op.tag}]', _native.load().mh_lin_fwd, op.module.handle, _native.ptr(x2),
-                       _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), _native.ptr(order), N,
+                       _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), _native.ptr(order), scale, N,
                        _native.stream_of(x2))
         if a2 is not None:
             ctx.save_for_backward(a2, order)
-        ctx.op, ctx.lead, ctx.N = op, lead, N
+        ctx.op, ctx.lead, ctx.N, ctx.scale = op, lead, N, scale
         return out.reshape(*lead, s.Dout)
 
     @staticmethod
@@ -774,7 +776,7 @@ class _LinFn(torch.autograd.Function):
         # node attributes are data (MACE's one-hot element encoding): no gradient flows to them, as in the
         # symmetric contraction
         if not ctx.needs_input_grad[0]:
-            return None, None, None
+            return None, None, None, None
         op = ctx.op
         s = op.spec
         if not s.has_bwd:
@@ -784,9 +786,9 @@ class _LinFn(torch.autograd.Function):
         g2 = g.reshape(-1, s.Dout).contiguous()
         gx = torch.empty(ctx.N, s.Din, device=g.device, dtype=torch.float32)
         _native.launch(f'lin_bwd[{op.tag}]', _native.load().mh_lin_bwd, op.module.handle, _native.ptr(g2),
-                       _native.ptr(a2), _native.ptr(op.Wt), _native.ptr(gx), _native.ptr(order), ctx.N,
-                       _native.stream_of(g2))
-        return gx.reshape(*ctx.lead, s.Din), None, None
+                       _native.ptr(a2), _native.ptr(op.Wt), _native.ptr(gx), _native.ptr(order), ctx.scale,
+                       ctx.N, _native.stream_of(g2))
+        return gx.reshape(*ctx.lead, s.Din), None, None, None
 
 
 class HipNodeLinear(torch.nn.Module):
@@ -821,9 +823,58 @@ class HipNodeLinear(torch.nn.Module):
                 setattr(self, k, getattr(mod, k))
         self.original = [mod]
         self.tag = 'linear'
+        # set by patch_model when the caller divides the output by a constant: forward then returns a PendingLinear
+        self.div_hint = None
 
     def forward(self, x, attrs=None):
         if self.spec.V == 0 and attrs is not None:
             raise TypeError('this linear takes no node attributes')
+        if self.div_hint is not None and x.dtype == torch.float32:
+            return PendingLinear(x, attrs, self)
         return _LinFn.apply(x, attrs, self)
+
+
+_DIVS = {torch.Tensor.__truediv__, torch.Tensor.div, torch.div, torch.true_divide}
+
+
+class PendingLinear(torch.Tensor):
+    """The output of a node linear whose caller is known to divide it by a constant (MACE's interaction blocks:
+    ``self.linear(message) / self.avg_num_neighbors``), not yet computed: a tensor of the output's shape and dtype
+    without storage.  Dividing it by a Python number launches the kernel with the reciprocal folded into its stores
+    (and the backward's), so no division kernel runs in either direction; any other use computes the plain output
+    first and runs on that, so every other consumer sees an ordinary tensor."""
+
+    @staticmethod
+    def __new__(cls, x, attrs, op):
+        return torch.Tensor._make_wrapper_subclass(cls, (*x.shape[:-1], op.spec.Dout), dtype=x.dtype, device=x.device,
+                                                   requires_grad=False)
+
+    def __init__(self, x, attrs, op):
+        self.x, self.attrs, self.op = x, attrs, op
+
+    def value(self, scale=1.0):
+        return _LinFn.apply(self.x, self.attrs, self.op, scale)
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        if (func in _DIVS and len(args) == 2 and not kwargs and isinstance(args[0], PendingLinear)
+                and isinstance(args[1], (int, float)) and not isinstance(args[1], bool) and args[1] != 0):
+            return args[0].value(1.0 / float(args[1]))
+
+        def real(t):
+            return t.value() if isinstance(t, PendingLinear) else t
+        args = torch.utils._pytree.tree_map(real, args)
+        kwargs = torch.utils._pytree.tree_map(real, kwargs)
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        # reached only by code that bypasses __torch_function__: compute the plain output and run on it
+        def real(t):
+            return t.value() if isinstance(t, PendingLinear) else t
+        args = torch.utils._pytree.tree_map(real, args)
+        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
+        return func(*args, **kwargs)
 

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipSphericalHarmonics,
-                              HipSymmetricContraction, _native)
+                              HipSymmetricContraction, _native, patch_model)
 from mace_hip_kernels import conv as hconv
 from mace_lite import blocks as B
 from mace_lite import factory
@@ -440,8 +440,8 @@ def test_node_linear_c_abi_and_errors():
     a = torch.eye(s.V, device=dev)[torch.randint(0, s.V, (n,), device=dev)]
     out, gx = torch.empty(n, s.Dout, device=dev), torch.empty(n, s.Din, device=dev)
     lib, P, st = _native.load(), _native.ptr, _native.stream_of(x)
-    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out), None, n, st), 'lin_fwd')
-    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx), None, n, st), 'lin_bwd')
+    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out), None, 1.0, n, st), 'lin_fwd')
+    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx), None, 1.0, n, st), 'lin_bwd')
     torch.cuda.synchronize()
     ref = op(x, a)
     assert torch.equal(out, ref)
@@ -450,15 +450,49 @@ def test_node_linear_c_abi_and_errors():
     # the node order is a walking order only: any permutation gives the same numbers (zero terms add exactly 0)
     perm = torch.randperm(n, device=dev).to(torch.int32)
     out_p, gx_p = torch.empty_like(out), torch.empty_like(gx)
-    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out_p), P(perm), n, st), 'lin_fwd')
-    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx_p), P(perm), n, st), 'lin_bwd')
+    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out_p), P(perm), 1.0, n, st), 'lin_fwd')
+    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx_p), P(perm), 1.0, n, st), 'lin_bwd')
     torch.cuda.synchronize()
     assert torch.equal(out_p, out) and torch.equal(gx_p, gx)
-    assert lib.mh_lin_fwd(op.module.handle, None, P(a), P(op.W), P(out), None, n, st) != 0
+    # alpha scales every output (a power of two: exactly)
+    _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(out_p), None, 0.25, n, st), 'lin_fwd')
+    _native.check(lib.mh_lin_bwd(op.module.handle, P(out), P(a), P(op.Wt), P(gx_p), None, 0.25, n, st), 'lin_bwd')
+    torch.cuda.synchronize()
+    assert torch.equal(out_p, 0.25 * out) and torch.equal(gx_p, 0.25 * gx)
+    assert lib.mh_lin_fwd(op.module.handle, None, P(a), P(op.W), P(out), None, 1.0, n, st) != 0
     assert b'NULL' in lib.mh_last_error()
     conv = HipConvTP(_tp('32x0e+32x1o', 2), device=dev)
-    assert lib.mh_lin_fwd(conv.module.handle, P(x), P(a), P(op.W), P(out), None, n, st) != 0
+    assert lib.mh_lin_fwd(conv.module.handle, P(x), P(a), P(op.W), P(out), None, 1.0, n, st) != 0
     assert b'not bound' in lib.mh_last_error()
+
+
+def test_linear_division_folded():
+    """The interaction linear's output divided by avg_num_neighbors (MACE's block code) is computed with the division
+    folded into the kernels: same values and input gradient as dividing the plain output, and any other use of the
+    pending output sees the plain output."""
+    dev = _dev()
+    print('[case] folded avg_num_neighbors division', flush=True)
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    mod = m.interactions[1].linear
+    op = HipNodeLinear(mod, device=dev)
+    n = 777
+    x = torch.randn(n, op.spec.Din, device=dev, requires_grad=True)
+    g = torch.randn(n, op.spec.Dout, device=dev)
+    ref = op(x) / 20.0
+    gref, = torch.autograd.grad(ref, x, g)
+    op.div_hint = 20.0
+    pend = op(x)
+    assert type(pend).__name__ == 'PendingLinear' and pend.shape == (n, op.spec.Dout)
+    got = pend / 20.0
+    assert type(got) is torch.Tensor
+    ggot, = torch.autograd.grad(got, x, g)
+    assert torch.allclose(got, ref, rtol=1e-6, atol=1e-6 * float(ref.abs().max()))
+    assert torch.allclose(ggot, gref, rtol=1e-6, atol=1e-6 * float(gref.abs().max()))
+    other = op(x) + 1.0                                   # not a division: the plain output
+    assert torch.equal(other, ref * 20.0 + 1.0) or torch.allclose(other, ref * 20.0 + 1.0, rtol=1e-6, atol=1e-5)
+    # the patched model folds it for both interaction blocks
+    rep = patch_model(copy.deepcopy(m).to(dev), verbose=False)
+    assert 'interactions.1.linear' in rep['patched']
 
 
 def _dot(a, b):
