@@ -59,7 +59,11 @@ enum mh_kernel_kind {
     MH_PERM_BWD = 20,    /* its inverse                                                            */
     MH_GEOM_FWD = 21,    /* edge vectors and lengths from positions, edge list and shifts          */
     MH_GEOM_BWD = 22,    /* their gradient: per-atom CSR sums (one wave per atom)                  */
-    MH_NUM_KINDS = 23
+    MH_SC_FWD_I = 23,    /* MH_SC_FWD reading x in e3nn's irreps layout                            */
+    MH_SC_BWD_I = 24,    /* MH_SC_BWD reading x and writing its gradient in the irreps layout      */
+    MH_SC_FWD_GI = 25,   /* MH_SC_FWD_G in the irreps layout                                       */
+    MH_SC_BWD_GI = 26,   /* MH_SC_BWD_G in the irreps layout                                       */
+    MH_NUM_KINDS = 27
 };
 
 /* flags of mh_conv_bwd */
@@ -162,6 +166,18 @@ int mh_sc_bwd(mh_module* m, const float* X, const int32_t* elem, const float* T,
 int mh_sc_fwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
                      float* out, int32_t N, void* stream);
 int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     const float* G, float* GX, int32_t N, void* stream);
+
+/* The symmetric contraction on x in e3nn's irreps layout X [N, sum_k C d_k] (block k of dimension d_k = 2l+1 holds
+ * channel c's components at C o_k + c d_k + m, o_k the sum of the earlier d) instead of [N, C, n_ell]: the tensor
+ * MACE passes through reshape_irreps, read and differentiated in place, so that permutation never runs; GX comes
+ * back in the same layout.  order NULL: one node per workgroup (kernels MH_SC_FWD_I / MH_SC_BWD_I, rows_per_block
+ * 1); else as mh_sc_fwd_sorted / mh_sc_bwd_sorted (MH_SC_FWD_GI / MH_SC_BWD_GI).  Same results as the [N, C, n_ell]
+ * entry points on the permuted input.  No reference counterpart: the reference reshapes first (MACE's
+ * reshape_irreps) and launches lib.sc_fwd / lib.sc_bwd on the result (symmetric.py:140, 154). */
+int mh_sc_fwd_irreps(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     float* out, int32_t N, void* stream);
+int mh_sc_bwd_irreps(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
                      const float* G, float* GX, int32_t N, void* stream);
 
 /* Edge spherical harmonics Y[e, :] = Y_{0..l_max}(vec[e] / |vec[e]|) (vec [E, 3], Y [E, (l_max+1)^2]; e3nn's real

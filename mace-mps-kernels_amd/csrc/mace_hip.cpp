@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 15; }
+int mh_version(void) { return 16; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -269,6 +269,26 @@ int mh_sc_bwd_sorted(mh_module* m, const float* X, const int32_t* elem, const in
                      const float* G, float* GX, int32_t N, void* stream) {
     void* args[] = {&X, &elem, &order, &T, &G, &GX, &N};
     return launch(m, MH_SC_BWD_G, N, args, stream, "mh_sc_bwd_sorted");
+}
+
+int mh_sc_fwd_irreps(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     float* out, int32_t N, void* stream) {
+    if (!order) {
+        void* args[] = {&X, &elem, &T, &out, &N};
+        return launch(m, MH_SC_FWD_I, N, args, stream, "mh_sc_fwd_irreps");
+    }
+    void* args[] = {&X, &elem, &order, &T, &out, &N};
+    return launch(m, MH_SC_FWD_GI, N, args, stream, "mh_sc_fwd_irreps");
+}
+
+int mh_sc_bwd_irreps(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
+                     const float* G, float* GX, int32_t N, void* stream) {
+    if (!order) {
+        void* args[] = {&X, &elem, &T, &G, &GX, &N};
+        return launch(m, MH_SC_BWD_I, N, args, stream, "mh_sc_bwd_irreps");
+    }
+    void* args[] = {&X, &elem, &order, &T, &G, &GX, &N};
+    return launch(m, MH_SC_BWD_GI, N, args, stream, "mh_sc_bwd_irreps");
 }
 
 int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream) {

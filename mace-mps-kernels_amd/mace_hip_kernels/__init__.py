@@ -175,6 +175,13 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             blk.reshape = HipReshapeIrreps(rs, device=dev)
             blk.reshape.tag = name
             patched.append(name)
+            # MACE passes interaction i's reshaped message straight to product i's symmetric contraction; a patched
+            # one reads the irreps layout itself, so the reshape is left unformed (formed only for other consumers)
+            prods = getattr(model, 'products', None)
+            sc = getattr(prods[i], 'symmetric_contractions', None) if prods is not None and i < len(prods) else None
+            if isinstance(sc, HipSymmetricContraction) and sc.spec.dims == [2 * l + 1 for _, l in
+                                                                             blk.reshape.spec.blocks]:
+                blk.reshape.fuse = True
     if linears:
         for name, parent, attr, mod in _linear_candidates(model):
             if any(mul < 16 for mul, _ in mod.irreps_out):

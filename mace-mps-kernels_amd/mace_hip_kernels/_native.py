@@ -18,9 +18,10 @@ DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
 
 MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, MH_CONV_GXSUM, MH_SC_FWD_G, \
     MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD, MH_LIN_FWD, MH_LIN_BWD, \
-    MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD = range(23)
+    MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD, \
+    MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI = range(27)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -61,6 +62,8 @@ _SIGS = {
     'mh_geom_bwd': (ctypes.c_int, [_P] * 11 + [ctypes.c_int, _P]),
     'mh_module_bind_grid': (ctypes.c_int, [_P, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     'mh_sc_fwd_sorted': (ctypes.c_int, [_P] * 6 + [_I, _P]),
+    'mh_sc_fwd_irreps': (ctypes.c_int, [_P] * 6 + [_I, _P]),
+    'mh_sc_bwd_irreps': (ctypes.c_int, [_P] * 7 + [_I, _P]),
     'mh_sc_bwd_sorted': (ctypes.c_int, [_P] * 7 + [_I, _P]),
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
     'mh_sc_bwd': (ctypes.c_int, [_P] * 6 + [_I, _P]),

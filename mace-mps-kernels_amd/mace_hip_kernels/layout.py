@@ -160,6 +160,50 @@ class HipReshapeIrreps(torch.nn.Module):
         self.irreps = mod.irreps
         self.original = [mod]
         self.tag = 'reshape'
+        # set by patch_model when the only consumer is a patched symmetric contraction, which can read the irreps
+        # layout itself: forward then returns a PendingReshape
+        self.fuse = False
 
     def forward(self, x):
+        if self.fuse and torch.is_tensor(x) and x.dim() == 2 and x.dtype == torch.float32:
+            return PendingReshape(x, self)
         return _PermFn.apply(x, self)
+
+
+class PendingReshape(torch.Tensor):
+    """MACE's reshape_irreps of x ([N, mul, sum (2l+1)]), not yet formed: a tensor of that shape and dtype without
+    storage.  A patched symmetric contraction asks for the irreps-layout source (``irreps_source``) and reads it in
+    place, so the permutation never runs in either direction; any other use forms the reshaped tensor first (the
+    permutation kernel) and runs on that, so every other consumer sees an ordinary tensor."""
+
+    @staticmethod
+    def __new__(cls, x, op):
+        return torch.Tensor._make_wrapper_subclass(cls, (x.shape[0], op.spec.mul, op.spec.D), dtype=x.dtype,
+                                                   device=x.device, requires_grad=False)
+
+    def __init__(self, x, op):
+        self.src, self.op = x, op
+
+    def irreps_source(self, dims):
+        """The irreps-layout tensor if its blocks have the component dimensions ``dims``, else None."""
+        return self.src if [2 * l + 1 for _, l in self.op.spec.blocks] == list(dims) else None
+
+    def value(self):
+        return _PermFn.apply(self.src, self.op)
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        def real(t):
+            return t.value() if isinstance(t, PendingReshape) else t
+        args = torch.utils._pytree.tree_map(real, args)
+        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+    @classmethod
+    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
+        def real(t):
+            return t.value() if isinstance(t, PendingReshape) else t
+        args = torch.utils._pytree.tree_map(real, args)
+        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
+        return func(*args, **kwargs)

@@ -101,6 +101,15 @@ class SCSpec:
         self.n_terms = sum(len(b['terms']) for b in self.blocks)
         self.ncb = (self.C + WAVE - 1) // WAVE
         self.block = self.ncb * WAVE
+        # component blocks of x in e3nn's irreps layout (the input before MACE's reshape_irreps): block k of
+        # dimension d_k holds channel c's components at C o_k + c d_k + m, o_k = sum of the earlier d
+        self.dims = None
+        try:
+            ir = [(mul, 2 * r.l + 1) for mul, r in sc.irreps_in]
+            if all(mul == self.C for mul, _ in ir) and sum(d for _, d in ir) == self.n_ell:
+                self.dims = [d for _, d in ir]
+        except (AttributeError, TypeError):
+            pass
 
     def kname(self, base):
         """Kernel symbol of this layer (shape-tagged so profiles tell the layers apart)."""
@@ -235,14 +244,29 @@ def _bwd_walk_g(spec, node, depth, L, ind, cnt, nb):
         L.append(f'{ind}}}')
 
 
-def source(spec, group=None):
+def _source_layout(spec, group=None, irreps=False):
     """HIP source of the per-node kernels ``sc_fwd`` / ``sc_bwd`` (one workgroup per node, the reference's launch
     shape) and the element-grouped kernels ``sc_fwdg`` / ``sc_bwdg``: one workgroup per GROUP consecutive nodes of an
     element-sorted order.  When the group's nodes share an element (every group but those straddling an element
     boundary) every coefficient load feeds GROUP FMAs instead of one; other groups run the one-node body per node.
-    Per node the arithmetic is the same sequence either way."""
+    Per node the arithmetic is the same sequence either way.  With ``irreps`` the same four kernels (names ending
+    in ``i``) read x and write its gradient in e3nn's irreps layout [N, sum C (2l+1)] (MACE's reshape_irreps input),
+    so that permutation never runs."""
     group = GROUP if group is None else group
     C, R, n = spec.C, spec.nrows, spec.n_ell
+    sfx = 'i' if irreps else ''
+    if irreps:
+        comp, o = [], 0
+        for d in spec.dims:
+            comp += [(o, d, m) for m in range(d)]
+            o += d
+
+    def xidx(node, i, ch):
+        """Index of component i of channel ch of node `node` in X (and GX)."""
+        if not irreps:
+            return f'((size_t)({node}) * C + {ch}) * N_ELL + {i}'
+        ok, d, m = comp[i]
+        return f'(size_t)({node}) * (C * N_ELL) + {C * ok} + {ch} * {d} + {m}'
     L = [_native.device_header(),
          f'#define C {C}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}', f'#define N_ELL {n}',
          f'#define R {R}', f'#define OUT_DIM {spec.out_dim}', f'#define GROUP {group}',
@@ -257,9 +281,8 @@ def source(spec, group=None):
             '  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)T, (short)0, TBYTES, 0x00020000);']
 
     def node_head(ind, bexpr):
-        return ([f'{ind}const int b = {bexpr};',
-                 f'{ind}const float* __restrict__ xp = X + ((size_t)b * C + cc) * N_ELL;'] +
-                [f'{ind}const float x{i} = xp[{i}];' for i in range(n)] +
+        return ([f'{ind}const int b = {bexpr};'] +
+                [f'{ind}const float x{i} = X[{xidx("b", i, "cc")}];' for i in range(n)] +
                 [f'{ind}const float* tb = T + (size_t)elem[b] * ((size_t)R * C);', f'{ind}const float* t = tb + cc;'])
 
     def fwd_one(ind):
@@ -279,9 +302,8 @@ def source(spec, group=None):
                   for m in range(M)]
         B.append(f'{ind}float G0 = 0.0f;')
         _bwd_walk(spec, trie, 0, B, ind, [0])
-        B += [f'{ind}(void)G0;', f'{ind}if (active) {{',
-              f'{ind}  float* __restrict__ gp = GX + ((size_t)b * C + c) * N_ELL;']
-        B += [f'{ind}  gp[{i}] = d{i};' for i in range(n)]
+        B += [f'{ind}(void)G0;', f'{ind}if (active) {{']
+        B += [f'{ind}  GX[{xidx("b", i, "c")}] = d{i};' for i in range(n)]
         return B + [f'{ind}}}']
 
     def group_head():
@@ -293,26 +315,25 @@ def source(spec, group=None):
         same = ' && '.join(f'e0 == e{j}' for j in range(1, group)) or 'true'
         H += [f'  if ({same}) {{', '    int voff = (e0 * (R * C) + cc) * 4;']
         for j in range(group):
-            H.append(f'    const float* __restrict__ xp{j} = X + ((size_t)n{j} * C + cc) * N_ELL;')
-            H += [f'    const float x{j}_{i} = xp{j}[{i}];' for i in range(n)]
+            H += [f'    const float x{j}_{i} = X[{xidx(f"n{j}", i, "cc")}];' for i in range(n)]
         return H
 
     def guarded(j, lines):
         return lines if j == 0 else [f'      if ({j} < qn) {{'] + ['  ' + x for x in lines] + ['      }']
 
     # ------------------------------------------------------------------------------- per-node forward
-    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwd")}(const float* __restrict__ X,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwd" + sfx)}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const float* __restrict__ T, float* __restrict__ out, int N) {',
           '  const int bq = mh_xcd_block(blockIdx.x, gridDim.x);', '  if (bq >= N) return;'] + lane
     L += node_head('  ', 'bq') + fwd_one('  ') + ['}', '']
     # ------------------------------------------------------------------------------ per-node backward
-    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwd")}(const float* __restrict__ X,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwd" + sfx)}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const float* __restrict__ T, const float* __restrict__ G,',
           '    float* __restrict__ GX, int N) {',
           '  const int bq = mh_xcd_block(blockIdx.x, gridDim.x);', '  if (bq >= N) return;'] + lane
     L += node_head('  ', 'bq') + bwd_one('  ') + ['}', '']
     # -------------------------------------------------------------------------------- grouped forward
-    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwdg")}(const float* __restrict__ X,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwdg" + sfx)}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const int* __restrict__ order, const float* __restrict__ T,',
           '    float* __restrict__ out, int N) {']
     L += group_head()
@@ -331,7 +352,7 @@ def source(spec, group=None):
     L += ['  ' + x for x in node_head('    ', 'order[q0 + j]') + fwd_one('    ')]
     L += ['    }', '  }', '}', '']
     # ------------------------------------------------------------------------------- grouped backward
-    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwdg")}(const float* __restrict__ X,',
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwdg" + sfx)}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const int* __restrict__ order, const float* __restrict__ T,',
           '    const float* __restrict__ G, float* __restrict__ GX, int N) {']
     L += group_head()
@@ -346,12 +367,22 @@ def source(spec, group=None):
     L.append('    ' + ' '.join(f'(void)G{j}_0;' for j in range(group)))
     L.append('    if (active) {')
     for j in range(group):
-        st = [f'      GX[((size_t)n{j} * C + c) * N_ELL + {i}] = d{j}_{i};' for i in range(n)]
+        st = [f'      GX[{xidx(f"n{j}", i, "c")}] = d{j}_{i};' for i in range(n)]
         L += guarded(j, st)
     L += ['    }', '  } else {', '    for (int j = 0; j < qn; ++j) {']
     L += ['  ' + x for x in node_head('    ', 'order[q0 + j]') + bwd_one('    ')]
     L += ['    }', '  }', '}', '']
     return '\n'.join(L)
+
+
+def source(spec, group=None):
+    """HIP source of one layer's module: the four kernels on the [N, C, n_ell] layout and, when the input irreps
+    are known, the same four on e3nn's irreps layout (one shared header)."""
+    src = _source_layout(spec, group)
+    if spec.dims is not None:
+        alt = _source_layout(spec, group, irreps=True)
+        src += '\n' + alt[alt.index('extern "C"'):]
+    return src
 
 
 # ------------------------------------------------------------------------------------------------ autograd
@@ -426,6 +457,40 @@ class _SCFn(torch.autograd.Function):
         return gx, None, None, None
 
 
+class _SCIrrepsFn(torch.autograd.Function):
+    """The contraction on x in e3nn's irreps layout [N, C n_ell] (the kernels with the ``i`` suffix); the gradient
+    comes back in that layout."""
+
+    @staticmethod
+    def forward(ctx, x, elem, order, op):
+        s = op.spec
+        if x.dtype != torch.float32 or not x.is_cuda or x.dim() != 2 or x.shape[1] != s.C * s.n_ell:
+            raise ValueError(f'expected float32 GPU input [N, {s.C * s.n_ell}], got {tuple(x.shape)}')
+        x = x.contiguous()
+        N = x.shape[0]
+        out = torch.empty(N, s.out_dim, device=x.device, dtype=torch.float32)
+        grouped = op.use_grouped(N, x.device)
+        _native.launch(f'sc_fwd[{op.tag}]', _native.load().mh_sc_fwd_irreps, op.module.handle, _native.ptr(x),
+                       _native.ptr(elem), _native.ptr(order) if grouped else None, _native.ptr(op.T),
+                       _native.ptr(out), N, _native.stream_of(x))
+        ctx.save_for_backward(x, elem, order)
+        ctx.grouped, ctx.op = grouped, op
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        if torch.is_grad_enabled():
+            raise RuntimeError(_DOUBLE_BACKWARD)
+        x, elem, order = ctx.saved_tensors
+        op = ctx.op
+        gx = torch.empty_like(x)
+        g = g.contiguous()
+        _native.launch(f'sc_bwd[{op.tag}]', _native.load().mh_sc_bwd_irreps, op.module.handle, _native.ptr(x),
+                       _native.ptr(elem), _native.ptr(order) if ctx.grouped else None, _native.ptr(op.T),
+                       _native.ptr(g), _native.ptr(gx), x.shape[0], _native.stream_of(x))
+        return gx, None, None, None
+
+
 class HipSymmetricContraction(torch.nn.Module):
     """Drop-in for mace ``SymmetricContraction`` at inference: ``forward(x[N, C, n_ell], node_attrs[N, n_elem])``
     (reference symmetric.py:158-170)."""
@@ -438,12 +503,20 @@ class HipSymmetricContraction(torch.nn.Module):
         self.source = source(self.spec)
         code = _native.compile_source(self.source)
         with torch.cuda.device(dev):
-            self.module = _native.Module(code, {
+            kinds = {
                 _native.MH_SC_FWD: (self.spec.kname('sc_fwd'), self.spec.block, 1),
                 _native.MH_SC_BWD: (self.spec.kname('sc_bwd'), self.spec.block, 1),
                 _native.MH_SC_FWD_G: (self.spec.kname('sc_fwdg'), self.spec.block, GROUP),
                 _native.MH_SC_BWD_G: (self.spec.kname('sc_bwdg'), self.spec.block, GROUP),
-            })
+            }
+            if self.spec.dims is not None:
+                kinds.update({
+                    _native.MH_SC_FWD_I: (self.spec.kname('sc_fwdi'), self.spec.block, 1),
+                    _native.MH_SC_BWD_I: (self.spec.kname('sc_bwdi'), self.spec.block, 1),
+                    _native.MH_SC_FWD_GI: (self.spec.kname('sc_fwdgi'), self.spec.block, GROUP),
+                    _native.MH_SC_BWD_GI: (self.spec.kname('sc_bwdgi'), self.spec.block, GROUP),
+                })
+            self.module = _native.Module(code, kinds)
         self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
         self.original = [sc]
         self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
@@ -465,4 +538,8 @@ class HipSymmetricContraction(torch.nn.Module):
         if y.shape != (x.shape[0], self.spec.n_elem):
             raise ValueError(f'node_attrs must be [{x.shape[0]}, {self.spec.n_elem}], got {tuple(y.shape)}')
         elem, order = element_order(y)
+        src = getattr(x, 'irreps_source', None)
+        if src is not None and self.spec.dims is not None and src(self.spec.dims) is not None:
+            # x is MACE's reshape_irreps of a tensor in e3nn's layout, not yet formed: read that tensor directly
+            return _SCIrrepsFn.apply(src(self.spec.dims), elem, order, self)
         return _SCFn.apply(x, elem, order, self)

@@ -619,6 +619,49 @@ def test_reshape_irreps_is_the_module_permutation():
         assert op(torch.zeros(0, op.spec.dim, device=dev)).shape == (0, op.spec.mul, op.spec.D)
 
 
+@pytest.mark.parametrize('grouped', [False, True])
+def test_sc_reads_the_irreps_layout(grouped):
+    """The symmetric contraction on MACE's reshape_irreps left unformed (PendingReshape): it reads the irreps-layout
+    tensor itself and returns its gradient in that layout.  Output and input gradient equal the reshape-then-contract
+    path bitwise (the same arithmetic on the same numbers), per node and element-grouped, through the module and the
+    C ABI; another consumer of the pending reshape sees the reshaped tensor."""
+    from mace_hip_kernels import HipReshapeIrreps
+    from mace_hip_kernels.layout import PendingReshape
+    from mace_hip_kernels.symmetric import element_order
+    dev = _dev()
+    for hidden in ('128x0e+128x1o', '128x0e+128x1o+128x2e'):
+        print(f'[case] SC on the irreps layout {hidden} grouped={grouped}', flush=True)
+        model = factory.make_model(hidden, 3, 3, elements=factory.ELEMENTS_PTCOH)
+        rs = HipReshapeIrreps(model.interactions[1].reshape, device=dev)
+        sc = HipSymmetricContraction(model.products[1].symmetric_contractions, device=dev)
+        sc.grouped = grouped
+        n = 1237
+        rng = np.random.default_rng(3)
+        x = torch.randn(n, rs.spec.dim, device=dev, requires_grad=True)
+        attrs = torch.tensor(np.eye(4)[rng.integers(0, 4, size=n)], dtype=torch.float32, device=dev)
+        ref = sc(rs(x), attrs)
+        g = torch.randn_like(ref)
+        gref, = torch.autograd.grad(ref, x, g)
+        rs.fuse = True
+        pend = rs(x)
+        assert isinstance(pend, PendingReshape) and pend.shape == (n, rs.spec.mul, rs.spec.D)
+        out = sc(pend, attrs)
+        gx, = torch.autograd.grad(out, x, g)
+        assert torch.equal(out, ref) and torch.equal(gx, gref)
+        assert torch.equal(rs(x) * 1.0, rs.original[0](x))          # any other use: the reshaped tensor
+        # the C ABI entry point on the same input
+        elem, order = element_order(attrs)
+        lib, P, st = _native.load(), _native.ptr, _native.stream_of(x)
+        o2, g2 = torch.empty_like(ref), torch.empty_like(x)
+        ordp = P(order) if grouped else None
+        xd = x.detach().contiguous()
+        _native.check(lib.mh_sc_fwd_irreps(sc.module.handle, P(xd), P(elem), ordp, P(sc.T), P(o2), n, st), 'sc_fwd_i')
+        _native.check(lib.mh_sc_bwd_irreps(sc.module.handle, P(xd), P(elem), ordp, P(sc.T), P(g.contiguous()), P(g2),
+                                           n, st), 'sc_bwd_i')
+        torch.cuda.synchronize()
+        assert torch.equal(o2, ref) and torch.equal(g2, gref)
+
+
 def test_edge_geometry_vs_float64():
     """Edge vectors and lengths and their backward (atom CSR sums) against float64 autograd of the PyTorch gathers,
     with gradients on vectors and lengths, on positions and shifts (the stress path), and with zero-length edges."""
