@@ -9,6 +9,7 @@ gather happening in LDS; the backward applies the inverse permutation the same w
 import torch
 
 from . import _native
+from .pending import Pending
 
 BLOCK = 256
 NODES = 4            # nodes per workgroup
@@ -170,16 +171,14 @@ class HipReshapeIrreps(torch.nn.Module):
         return _PermFn.apply(x, self)
 
 
-class PendingReshape(torch.Tensor):
-    """MACE's reshape_irreps of x ([N, mul, sum (2l+1)]), not yet formed: a tensor of that shape and dtype without
-    storage.  A patched symmetric contraction asks for the irreps-layout source (``irreps_source``) and reads it in
-    place, so the permutation never runs in either direction; any other use forms the reshaped tensor first (the
-    permutation kernel) and runs on that, so every other consumer sees an ordinary tensor."""
+class PendingReshape(Pending):
+    """MACE's reshape_irreps of x ([N, mul, sum (2l+1)]), not yet formed.  A patched symmetric contraction asks for
+    the irreps-layout source (``irreps_source``) and reads it in place, so the permutation never runs in either
+    direction; any other use forms the reshaped tensor first (the permutation kernel)."""
 
     @staticmethod
     def __new__(cls, x, op):
-        return torch.Tensor._make_wrapper_subclass(cls, (x.shape[0], op.spec.mul, op.spec.D), dtype=x.dtype,
-                                                   device=x.device, requires_grad=False)
+        return Pending.__new__(cls, (x.shape[0], op.spec.mul, op.spec.D), x)
 
     def __init__(self, x, op):
         self.src, self.op = x, op
@@ -190,20 +189,3 @@ class PendingReshape(torch.Tensor):
 
     def value(self):
         return _PermFn.apply(self.src, self.op)
-
-    @classmethod
-    def __torch_function__(cls, func, types, args=(), kwargs=None):
-        def real(t):
-            return t.value() if isinstance(t, PendingReshape) else t
-        args = torch.utils._pytree.tree_map(real, args)
-        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
-        with torch._C.DisableTorchFunctionSubclass():
-            return func(*args, **kwargs)
-
-    @classmethod
-    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
-        def real(t):
-            return t.value() if isinstance(t, PendingReshape) else t
-        args = torch.utils._pytree.tree_map(real, args)
-        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
-        return func(*args, **kwargs)

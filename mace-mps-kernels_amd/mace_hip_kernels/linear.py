@@ -30,6 +30,7 @@ import numpy as np
 import torch
 
 from . import _native
+from .pending import Pending
 
 KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
 BLOCK = 256          # 4 waves
@@ -837,17 +838,15 @@ class HipNodeLinear(torch.nn.Module):
 _DIVS = {torch.Tensor.__truediv__, torch.Tensor.div, torch.div, torch.true_divide}
 
 
-class PendingLinear(torch.Tensor):
+class PendingLinear(Pending):
     """The output of a node linear whose caller is known to divide it by a constant (MACE's interaction blocks:
-    ``self.linear(message) / self.avg_num_neighbors``), not yet computed: a tensor of the output's shape and dtype
-    without storage.  Dividing it by a Python number launches the kernel with the reciprocal folded into its stores
-    (and the backward's), so no division kernel runs in either direction; any other use computes the plain output
-    first and runs on that, so every other consumer sees an ordinary tensor."""
+    ``self.linear(message) / self.avg_num_neighbors``), not yet computed.  Dividing it by a Python number launches the
+    kernel with the reciprocal folded into its stores (and the backward's), so no division kernel runs in either
+    direction; any other use computes the plain output first."""
 
     @staticmethod
     def __new__(cls, x, attrs, op):
-        return torch.Tensor._make_wrapper_subclass(cls, (*x.shape[:-1], op.spec.Dout), dtype=x.dtype, device=x.device,
-                                                   requires_grad=False)
+        return Pending.__new__(cls, (*x.shape[:-1], op.spec.Dout), x)
 
     def __init__(self, x, attrs, op):
         self.x, self.attrs, self.op = x, attrs, op
@@ -856,25 +855,9 @@ class PendingLinear(torch.Tensor):
         return _LinFn.apply(self.x, self.attrs, self.op, scale)
 
     @classmethod
-    def __torch_function__(cls, func, types, args=(), kwargs=None):
-        kwargs = kwargs or {}
+    def intercept(cls, func, args, kwargs):
         if (func in _DIVS and len(args) == 2 and not kwargs and isinstance(args[0], PendingLinear)
                 and isinstance(args[1], (int, float)) and not isinstance(args[1], bool) and args[1] != 0):
             return args[0].value(1.0 / float(args[1]))
-
-        def real(t):
-            return t.value() if isinstance(t, PendingLinear) else t
-        args = torch.utils._pytree.tree_map(real, args)
-        kwargs = torch.utils._pytree.tree_map(real, kwargs)
-        with torch._C.DisableTorchFunctionSubclass():
-            return func(*args, **kwargs)
-
-    @classmethod
-    def __torch_dispatch__(cls, func, types, args=(), kwargs=None):
-        # reached only by code that bypasses __torch_function__: compute the plain output and run on it
-        def real(t):
-            return t.value() if isinstance(t, PendingLinear) else t
-        args = torch.utils._pytree.tree_map(real, args)
-        kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
-        return func(*args, **kwargs)
+        return NotImplemented
 
