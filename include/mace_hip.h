@@ -63,7 +63,9 @@ enum mh_kernel_kind {
     MH_SC_BWD_I = 24,    /* MH_SC_BWD reading x and writing its gradient in the irreps layout      */
     MH_SC_FWD_GI = 25,   /* MH_SC_FWD_G in the irreps layout                                       */
     MH_SC_BWD_GI = 26,   /* MH_SC_BWD_G in the irreps layout                                       */
-    MH_NUM_KINDS = 27
+    MH_READOUT_FWD = 27, /* readout head: per-node energy from the node features, 16 nodes a block  */
+    MH_READOUT_BWD = 28, /* its input gradient                                                     */
+    MH_NUM_KINDS = 29
 };
 
 /* flags of mh_conv_bwd */
@@ -208,6 +210,14 @@ int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, 
                float alpha, int32_t N, void* stream);
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,
                float alpha, int32_t N, void* stream);
+
+/* Readout head e[n] = R(x[n]) for N nodes (x [N, D], e [N], fp32): MACE's LinearReadoutBlock (e = x_s . w) or
+ * NonLinearReadoutBlock (e = w2 . (c silu(x_s W1))), x_s the scalar (0e) block of the node features; the weights,
+ * the activation constant and the block offset are compiled into the module.  mh_readout_bwd gives gx = dL/dx
+ * (the whole row, zeros outside the scalar block) from g = dL/de.  No reference counterpart: the reference leaves
+ * MACE's readout heads on e3nn. */
+int mh_readout_fwd(mh_module* m, const float* x, float* e, int64_t N, void* stream);
+int mh_readout_bwd(mh_module* m, const float* x, const float* g, float* gx, int64_t N, void* stream);
 
 /* Radial MLP W0[e] = MLP(ef[e]) for E edges (ef [E, n_basis], W0 [E, n_out], fp32): bias-free layers h <- c_i *
  * silu(h A_i) and a linear output layer, MACE's conv_tp_weights (an e3nn FullyConnectedNet).  Wh holds the hidden

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 16; }
+int mh_version(void) { return 17; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -313,6 +313,18 @@ int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt,
     if (N > 0 && (!g || !Wt || !gx)) return fail(-1, "mh_lin_bwd: NULL g, Wt or gx");
     void* args[] = {&g, &attrs, &Wt, &gx, &N, &order, &alpha};
     return launch(m, MH_LIN_BWD, N, args, stream, "mh_lin_bwd");
+}
+
+int mh_readout_fwd(mh_module* m, const float* x, float* e, int64_t N, void* stream) {
+    if (N > 0 && (!x || !e)) return fail(-1, "mh_readout_fwd: NULL operand");
+    void* args[] = {&x, &e, &N};
+    return launch(m, MH_READOUT_FWD, N, args, stream, "mh_readout_fwd");
+}
+
+int mh_readout_bwd(mh_module* m, const float* x, const float* g, float* gx, int64_t N, void* stream) {
+    if (N > 0 && (!x || !g || !gx)) return fail(-1, "mh_readout_bwd: NULL operand");
+    void* args[] = {&x, &g, &gx, &N};
+    return launch(m, MH_READOUT_BWD, N, args, stream, "mh_readout_bwd");
 }
 
 int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E, void* stream) {

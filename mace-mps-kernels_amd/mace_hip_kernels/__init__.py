@@ -21,6 +21,7 @@ The kernels are generated per layer with the layer's coefficients as literals, c
 be loaded, ``patch_model`` raises: there is no CPU or eager fallback.
 """
 import inspect
+import itertools
 import warnings
 
 import torch
@@ -31,6 +32,7 @@ from .linear import HipNodeLinear, lin_supported
 from .radial import HipRadialMLP, mlp_supported
 from .embedding import HipRadialEmbedding, emb_supported
 from .layout import HipReshapeIrreps, reshape_supported
+from .readout import HipReadout, readout_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
 from . import geometry as _geometry
@@ -38,7 +40,8 @@ from . import geometry as _geometry
 __version__ = '0.1.0'
 __all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
            'HipNodeLinear', 'HipRadialMLP', 'HipRadialEmbedding', 'conv_supported', 'sc_supported', 'sh_supported', 'lin_supported',
-           'mlp_supported', 'emb_supported', 'HipReshapeIrreps', 'reshape_supported']
+           'mlp_supported', 'emb_supported', 'HipReshapeIrreps', 'reshape_supported', 'HipReadout',
+           'readout_supported']
 
 _LINEAR_CLASSES = ('Linear', 'FullyConnectedTensorProduct')
 
@@ -62,18 +65,23 @@ def _linear_candidates(model):
 
 
 def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
-                radial_mlp=True, radial_embedding=True, layouts=True, edge_geometry=True):
+                radial_mlp=True, radial_embedding=True, layouts=True, edge_geometry=True, readouts=True):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
     edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
-    node-wise e3nn linears and scalar-attribute tensor products (``skip_tp``); readout heads with fewer than 16 output
-    channels per irrep are left on e3nn without being reported (they are a negligible part of the call), and
+    node-wise e3nn linears and scalar-attribute tensor products (``skip_tp``; linears with fewer than 16 output channels
+    per irrep, such as a readout head's last layer when ``readouts`` is off, are left on e3nn without being reported),
+    and
     ``radial_mlp`` each interaction block's radial MLP (``conv_tp_weights``, an e3nn FullyConnectedNet), and
     ``radial_embedding`` the model's Bessel x polynomial-cutoff edge embedding, and ``layouts`` each interaction
     block's ``reshape`` (irreps layout -> symmetric-contraction layout), and ``edge_geometry`` the edge vectors and
     lengths (MACE's ``get_edge_vectors_and_lengths`` in the model's module, taken over only while this model's forward
-    runs; other models keep the original)."""
-    p = next(model.parameters())
+    runs; other models keep the original), and ``readouts`` the per-interaction readout heads (``LinearReadoutBlock``,
+    ``NonLinearReadoutBlock``) as one kernel per direction each."""
+    # a fully patched model may hold no parameters any more (the drop-ins keep their weights as buffers)
+    p = next((t for t in itertools.chain(model.parameters(), model.buffers()) if t.is_floating_point()), None)
+    if p is None:
+        raise RuntimeError('model has no floating-point parameters or buffers')
     dev = p.device
     if dev.type != 'cuda' or torch.version.hip is None:
         raise RuntimeError(f'model must be on a ROCm GPU device (found {dev})')
@@ -182,6 +190,23 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             if isinstance(sc, HipSymmetricContraction) and sc.spec.dims == [2 * l + 1 for _, l in
                                                                              blk.reshape.spec.blocks]:
                 blk.reshape.fuse = True
+    if readouts:                          # before the linears: a head's own linears go with it
+        for i, ro in enumerate(getattr(model, 'readouts', [])):
+            name = f'readouts.{i}'
+            if isinstance(ro, HipReadout):
+                continue
+            ok, why = readout_supported(ro)
+            if ok:
+                try:
+                    new = HipReadout(ro, device=dev)
+                except ValueError as e:
+                    ok, why = False, str(e)
+            if not ok:
+                skipped.append((name, why))
+                continue
+            new.tag = name
+            model.readouts[i] = new
+            patched.append(name)
     if linears:
         for name, parent, attr, mod in _linear_candidates(model):
             if any(mul < 16 for mul, _ in mod.irreps_out):
@@ -237,6 +262,10 @@ def unpatch_model(model):
         if isinstance(getattr(blk, 'conv_tp_weights', None), HipRadialMLP):
             blk.conv_tp_weights = blk.conv_tp_weights.original[0]
             restored.append(f'interactions.{i}.conv_tp_weights')
+    for i, ro in enumerate(getattr(model, 'readouts', [])):
+        if isinstance(ro, HipReadout):
+            model.readouts[i] = ro.original[0]
+            restored.append(f'readouts.{i}')
     for pname, parent in list(model.named_modules()):
         for attr, mod in list(parent.named_children()):
             if isinstance(mod, HipNodeLinear):

@@ -19,9 +19,9 @@ DEVICE_HEADER = os.path.join(os.path.dirname(HERE), 'csrc', 'mh_device.h')
 MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, MH_CONV_GXSUM, MH_SC_FWD_G, \
     MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD, MH_LIN_FWD, MH_LIN_BWD, \
     MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD, \
-    MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI = range(27)
+    MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI, MH_READOUT_FWD, MH_READOUT_BWD = range(29)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -52,6 +52,8 @@ _SIGS = {
     'mh_sh_bwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
     'mh_lin_fwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, ctypes.c_int, _P]),
     'mh_lin_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, ctypes.c_int, _P]),
+    'mh_readout_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int64, _P]),
+    'mh_readout_bwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
     'mh_mlp_fwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_mlp_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
     'mh_emb_fwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),

@@ -662,6 +662,42 @@ def test_sc_reads_the_irreps_layout(grouped):
         assert torch.equal(o2, ref) and torch.equal(g2, gref)
 
 
+def test_readout_heads_vs_float64():
+    """Both readout heads (linear on 128x0e+128x1o, SiLU MLP on 128x0e) of the config-2 model and of a 48-channel
+    model: energies and input gradients against float64 runs of the e3nn modules on a ragged node count; the C ABI
+    entry points equal the module."""
+    from mace_hip_kernels import HipReadout
+    dev = _dev()
+    rng = np.random.default_rng(4)
+    for hidden in ('128x0e+128x1o', '48x0e+48x1o'):
+        m = factory.make_model(hidden, 3, 3, elements=factory.ELEMENTS_PTCOH)
+        for i, ro in enumerate(m.readouts):
+            print(f'[case] readout {hidden} {i}', flush=True)
+            op = HipReadout(ro, device=dev)
+            n = 1237
+            x = rng.normal(size=(n, op.spec.Din))
+            g = rng.normal(size=(n, 1))
+            xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
+            out = op(xt)
+            gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
+            m64 = copy.deepcopy(ro).double()
+            x64 = torch.tensor(x, requires_grad=True)
+            ref = m64(x64)
+            gref, = torch.autograd.grad(ref, x64, torch.tensor(g))
+            assert out.shape == (n, 1)
+            assert _rel(out.detach().double().cpu().numpy(), ref.detach().numpy()) < 1e-5
+            assert _rel(gx.double().cpu().numpy(), gref.numpy()) < 1e-5
+            lib, P, st = _native.load(), _native.ptr, _native.stream_of(xt)
+            o2, g2 = torch.empty(n, device=dev), torch.empty_like(xt)
+            gg = torch.tensor(g[:, 0], dtype=torch.float32, device=dev)
+            xd = xt.detach()
+            _native.check(lib.mh_readout_fwd(op.module.handle, P(xd), P(o2), n, st), 'ro_fwd')
+            _native.check(lib.mh_readout_bwd(op.module.handle, P(xd), P(gg), P(g2), n, st), 'ro_bwd')
+            torch.cuda.synchronize()
+            assert torch.equal(o2, out.detach()[:, 0]) and torch.equal(g2, gx)
+            assert op(torch.zeros(0, op.spec.Din, device=dev)).shape == (0, 1)
+
+
 def test_edge_geometry_vs_float64():
     """Edge vectors and lengths and their backward (atom CSR sums) against float64 autograd of the PyTorch gathers,
     with gradients on vectors and lengths, on positions and shifts (the stress path), and with zero-length edges."""

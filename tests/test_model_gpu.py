@@ -150,7 +150,7 @@ def test_idempotent_patch_and_unpatch():
     assert type(m.spherical_harmonics).__name__ == 'SphericalHarmonics'
     assert type(m.interactions[1].linear).__name__ == 'Linear'
     r3 = patch_model(m, verbose=False, spherical_harmonics=False, linears=False, radial_mlp=False,
-                     radial_embedding=False, layouts=False, edge_geometry=False)
+                     radial_embedding=False, layouts=False, edge_geometry=False, readouts=False)
     assert len(r3['patched']) == 4 and 'spherical_harmonics' not in r3['patched']
     assert len(unpatch_model(m)) == 4
     assert not hasattr(m.interactions[0], 'conv_fusion')
