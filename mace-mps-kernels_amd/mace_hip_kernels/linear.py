@@ -272,8 +272,10 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         fn = f'{name}_b{o}'
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const unsigned short* __restrict__ W, float* __restrict__ out, int N, int group, int cg,',
-             '    float* __restrict__ lds, unsigned* __restrict__ amask, int* __restrict__ vlist, float alpha) {',
-             '  (void)alpha;',
+             '    float* __restrict__ lds, unsigned* __restrict__ amask, int* __restrict__ vlist, float alpha,',
+             '    const int* __restrict__ order) {',
+             f'  auto nd = [&](int i) {{ return {"order ? order[i] : " if V else ""}i; }};   // node of position i',
+             '  (void)alpha; (void)order;',
              f'  const int g0 = group * {G};                 // first node of the workgroup',
              '  if (g0 >= N) return;',
              f'  const int ng = min({G}, N - g0);',
@@ -281,7 +283,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         if not terms[o]:
             L += [f'  for (int f = t; f < ng * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D};',
-                  f'    out[(size_t)(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
+                  f'    out[(size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
                   '  }', '}', '']
             fns += L
             cases.append((o, fn))
@@ -299,7 +301,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         L += ['  const int wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
               '  (void)lane;']
         if V:
-            L += _mask(V, 'g0', 'ng')
+            L += _mask(V, 'g0', 'ng', ordered=True)
         else:
             L += ['  const int nact = 1;']
         # chunk c -> term ti (compile-time boundaries scaled by nact), attribute v, channel chunk uc
@@ -337,7 +339,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         for k in range(ix):
             fx = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NXP else f'min(t + {k * BLOCK}, {NXP - 1})'
             L += [f'    {{ const int f = {fx}, nl = f / {8 * D}, e = f - nl * {8 * D};',
-                  '      const int n = min(g0 + nl, N - 1);',
+                  '      const int n = nd(min(g0 + nl, N - 1));',
                   f'      const float* __restrict__ xr = x + (size_t)n * {Din} + oi;']
             if vec:     # past the block: any valid input (its weights are zero)
                 L += [f'      px{k} = *reinterpret_cast<const mh_f4*>(xr + min(uc * {KC * D} + 4 * e, mi * {D} - 4)); }}']
@@ -372,7 +374,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         for tt in range(NT):
             L += [f'  const int xr{tt} = {(tt) * TN * D} + wave * {NT * TN * D} + (c16 < {TN * D} ? c16 : 0);']
             if V:
-                L += [f'  const int an{tt} = min(g0 + xr{tt} / {D}, N - 1);']
+                L += [f'  const int an{tt} = nd(min(g0 + xr{tt} / {D}, N - 1));']
         L += [f'  mh_f4 acc[{NT}][{CT}];',
               '#pragma unroll',
               f'  for (int a = 0; a < {NT}; ++a)',
@@ -431,7 +433,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
               '  __syncthreads();',
               f'  for (int f = t; f < ng * {CW * D // 4}; f += {BLOCK}) {{',
               f'    const int nl = f / {CW * D // 4}, j = f - nl * {CW * D // 4};',
-              f'    *reinterpret_cast<mh_f4*>(out + (size_t)(g0 + nl) * {Dout} + {oo} + col0 * {D} + 4 * j) = '
+              f'    *reinterpret_cast<mh_f4*>(out + (size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + 4 * j) = '
               f'*reinterpret_cast<const mh_f4*>(lds + nl * {CW * D} + 4 * j);',
               '  }',
               '}', '']
@@ -442,13 +444,13 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     sw = ['  switch (blockIdx.y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha, order); break;')
     sw += ['    default: break;', '  }']
     lds_max = max(lds_max, 4)
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N,',
          '    const int* __restrict__ order, float alpha) {',
-         '  (void)order;                                  // attribute-free: node order does not matter',
+         '  (void)order;',
          f'  __shared__ __align__(16) float lds[{lds_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];',
@@ -698,7 +700,8 @@ def use_bf16(spec, backward=False):
     """Which kernel family a direction gets: the bf16x6 LDS-staged one for attribute-free maps with at least 1024
     outputs (MACE's interaction linears: long K over many irreps blocks, every weight chunk shared by a workgroup's
     eight row tiles); the fp32 one with per-wave register pipelines otherwise (short K and scalar-only blocks, whose
-    few workgroups and short chunk chains favour it, and skip_tp's attribute terms)."""
+    few workgroups and short chunk chains favour it, and skip_tp's attribute terms: measured no faster on the bf16
+    family, which supports them too)."""
     return spec.V == 0 and (spec.Din if backward else spec.Dout) >= 1024
 
 

@@ -427,6 +427,33 @@ def test_node_linears_vs_float64(attrs_kind):
         assert torch.equal(o2.reshape(60, -1), out.detach()[:60])
 
 
+def test_skip_tp_on_both_families(monkeypatch):
+    """skip_tp (attribute terms, species-ordered nodes) generated by the bf16 family as well as the fp32 family it
+    normally gets: both against float64, forward and input gradient."""
+    from mace_hip_kernels import linear as hlin
+    dev = _dev()
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    mod = m.interactions[0].skip_tp
+    rng = np.random.default_rng(9)
+    n = 1001
+    x = rng.normal(size=(n, hlin.LinSpec(mod).Din))
+    a = np.eye(4)[rng.integers(0, 4, size=n)]
+    g = rng.normal(size=(n, hlin.LinSpec(mod).Dout))
+    m64 = copy.deepcopy(mod).double()
+    x64 = torch.tensor(x, requires_grad=True)
+    ref = m64(x64, torch.tensor(a))
+    gref, = torch.autograd.grad(ref, x64, torch.tensor(g))
+    for fam in ('fp32', 'bf16'):
+        print(f'[case] skip_tp on the {fam} family', flush=True)
+        monkeypatch.setattr(hlin, 'use_bf16', lambda spec, backward=False, f=fam: f == 'bf16')
+        op = HipNodeLinear(mod, device=dev)
+        xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
+        out = op(xt, torch.tensor(a, dtype=torch.float32, device=dev))
+        gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
+        assert _rel(out.detach().double().cpu().numpy(), ref.detach().numpy()) < LIN_TOL
+        assert _rel(gx.double().cpu().numpy(), gref.numpy()) < LIN_TOL
+
+
 def test_node_linear_c_abi_and_errors():
     """mh_lin_fwd / mh_lin_bwd through the C ABI against the module, and their errors (NULL operands, a module
     without the kernel)."""
