@@ -42,6 +42,7 @@ NB_FWD = 2           # 16-edge tiles per wave in the forward (each LDS weight fr
 NB_BWD = 1           # and in the backward
 GW_DIST = 2          # chunks of dL/dW0 in flight ahead of the one being multiplied (backward)
 PREFETCH = 2         # output-layer weight chunks in flight ahead of the one being multiplied
+HIDDEN_TILES_BWD = 1 # edge tiles whose hidden layers the backward recomputes together (register pressure)
 CH_FWD = 32          # output columns of the last layer per LDS chunk, forward (a multiple of 32)
 CH_BWD = 32          # and backward (a multiple of 32: one bf16 MFMA K step per 32 columns)
 NSPLIT = 3           # bf16 parts per fp32 weight (exact split)
@@ -224,20 +225,20 @@ def source(spec):
               f'reinterpret_cast<mh_f4*>(lds)[t + {i * nthreads}] = sg{i};' for i in range(it)]
         return P
 
-    def xin(nb):
+    def xin(tiles):
         P = []
-        for b in range(nb):
+        for b in tiles:
             P += [f'  float xin{b}[{K0S}];']
             P += [f'  xin{b}[{st}] = {4 * st} + q < {H0} ? ef[ejc{b} * {H0} + {4 * st} + q] : 0.f;' for st in range(K0S)]
         return P
 
-    def hidden_fwd(transposed, keep, nb):
+    def hidden_fwd(transposed, keep, tiles):
         """z_i and h_i = c_i silu(z_i) for every hidden layer on the fp32 MFMA, A operands from LDS (transposed
-        layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for the nb edge tiles."""
+        layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for every edge tile in ``tiles``."""
         P = []
         for i in range(nh):
             T = cols[i] // 16
-            for b in range(nb):
+            for b in tiles:
                 P.append(f'  mh_f4 z{i}_{b}[{T}];')
                 P += [f'  z{i}_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(T)]
             if i == 0:
@@ -247,7 +248,7 @@ def source(spec):
                              f'lds[{Lo["nat"][0]} + ({4 * st} + q) * {cols[0] + PAD} + {16 * o} + c16]')
                         P.append(f'  {{ const float a = {a};')
                         P += [f'    z0_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xin{b}[{st}], z0_{b}[{o}], 0, 0, 0);'
-                              for b in range(nb)]
+                              for b in tiles]
                         P.append('  }')
             else:
                 Tin = cols[i - 1] // 16
@@ -262,10 +263,10 @@ def source(spec):
                                  f'lds[{Lo["nat"][i]} + ({16 * ti + r} + 4 * q) * {cols[i] + PAD} + {16 * o} + c16]')
                             P.append(f'  {{ const float a = {a};')
                             P += [f'    z{i}_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h{i - 1}_{b}[{ti}][{r}], '
-                                  f'z{i}_{b}[{o}], 0, 0, 0);' for b in range(nb)]
+                                  f'z{i}_{b}[{o}], 0, 0, 0);' for b in tiles]
                             P.append('  }')
             if i < nh - 1 or keep:
-                for b in range(nb):
+                for b in tiles:
                     P.append(f'  mh_f4 h{i}_{b}[{T}];')
                     for o in range(T):
                         for r in range(4):
@@ -304,7 +305,7 @@ def source(spec):
     ncf = 2 if nb == 1 else 1                            # accumulator chains per result tile
     F = head(spec.kname('mlp_fwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
              'const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E', lds_fwd, nb)
-    F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(nb) + hidden_fwd(True, True, nb)
+    F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(nb)) + hidden_fwd(True, True, range(nb))
     # the last hidden layer's activations as bf16 operands: step s, lane group q: features 32 s + 16 t + 4 q + r
     for b in range(nb):
         hl = f'h{nh - 1}_{b}'
@@ -434,51 +435,57 @@ def source(spec):
     for b in range(nb):
         B += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = ' + ' + '.join(f'dh{b}[{o}][{j}]' for j in range(ncb)) + ';'
                                            for o in range(TL)]
-    B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin(nb) + hidden_fwd(False, False, nb)
-    cur = 'dhs_'
-    for i in range(nh - 1, -1, -1):
-        T = cols[i] // 16
-        for b in range(nb):
-            for o in range(T):
-                for r in range(4):
-                    B += ['  {',
-                          f'    const float z = z{i}_{b}[{o}][{r}], s = mlp_sig(z);',
-                          f'    {cur}{b}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
-                          '  }']
-        if i > 0:
-            Tp = cols[i - 1] // 16
-            nxt = f'dh{i - 1}_'
-            # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
-            for b in range(nb):
-                B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
-                B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
-            for ti in range(T):
-                for o in range(Tp):
-                    B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
-                             f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
-                for r in range(4):
+    # the hidden layers recomputed and walked back HIDDEN_TILES_BWD edge tiles at a time (each group in a scope of
+    # its own, so the registers of its activations are free for the next)
+    B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();']
+    for g0 in range(0, nb, HIDDEN_TILES_BWD):
+        grp = range(g0, min(nb, g0 + HIDDEN_TILES_BWD))
+        B += ['  {'] + xin(grp) + hidden_fwd(False, False, grp)
+        cur = 'dhs_'
+        for i in range(nh - 1, -1, -1):
+            T = cols[i] // 16
+            for b in grp:
+                for o in range(T):
+                    for r in range(4):
+                        B += ['  {',
+                              f'    const float z = z{i}_{b}[{o}][{r}], s = mlp_sig(z);',
+                              f'    {cur}{b}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
+                              '  }']
+            if i > 0:
+                Tp = cols[i - 1] // 16
+                nxt = f'dh{i - 1}_'
+                # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
+                for b in grp:
+                    B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
+                    B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
+                for ti in range(T):
                     for o in range(Tp):
-                        for b in range(nb):
-                            B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
-                                     f'{cur}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
-            cur = nxt
-    # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
-    T0 = cols[0] // 16
-    for o in range(-(-H0 // 16)):
-        B += ['  {',
-              f'    const int row = {16 * o} + c16 < {rows[0]} ? {16 * o} + c16 : 0;']
-        B += [f'    mh_f4 d{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for b in range(nb)]
-        for ti in range(T0):
-            B.append(f'    const mh_f4 w{ti} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][0]} + row * {cols[0] + PAD} + '
-                     f'{16 * ti} + 4 * q]);')
-            for r in range(4):
-                B += [f'    d{b} = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}{b}[{ti}][{r}], d{b}, 0, 0, 0);'
-                      for b in range(nb)]
-        for b in range(nb):
-            for r in range(4):
-                B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[ej{b} * {H0} + {16 * o + r} + 4 * q] = '
-                         f'd{b}[{r}];')
-        B.append('  }')
+                        B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
+                                 f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
+                    for r in range(4):
+                        for o in range(Tp):
+                            for b in grp:
+                                B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
+                                         f'{cur}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
+                cur = nxt
+        # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
+        T0 = cols[0] // 16
+        for o in range(-(-H0 // 16)):
+            B += ['  {',
+                  f'    const int row = {16 * o} + c16 < {rows[0]} ? {16 * o} + c16 : 0;']
+            B += [f'    mh_f4 d{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for b in grp]
+            for ti in range(T0):
+                B.append(f'    const mh_f4 w{ti} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][0]} + row * '
+                         f'{cols[0] + PAD} + {16 * ti} + 4 * q]);')
+                for r in range(4):
+                    B += [f'    d{b} = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}{b}[{ti}][{r}], d{b}, 0, 0, 0);'
+                          for b in grp]
+            for b in grp:
+                for r in range(4):
+                    B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[ej{b} * {H0} + {16 * o + r} + 4 * q] = '
+                             f'd{b}[{r}];')
+            B.append('  }')
+        B += ['  }', '  __builtin_amdgcn_sched_barrier(0);       // one group finished before the next starts']
     B += ['}', '']
     L += B
     return '\n'.join(L)
