@@ -56,8 +56,8 @@ def _time_calls(model, batch, steps, warmup, sync):
 def _kernel_table(met, batch, n_real_edges, summary):
     """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only)."""
     import torch
-    from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipReshapeIrreps,
-                                  HipSphericalHarmonics, HipSymmetricContraction)
+    from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipReadout,
+                                  HipReshapeIrreps, HipSphericalHarmonics, HipSymmetricContraction)
     n = batch['positions'].shape[0]
     n_elem_used = int((batch['node_attrs'].sum(0) > 0).sum())
     rows = {}
@@ -76,8 +76,9 @@ def _kernel_table(met, batch, n_real_edges, summary):
             s = m.spec
             bf, bb = s.bytes(n, n_elem_used)
             ff, fb = s.flops()
-            rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C, s.kname('sc_fwd'))
-            rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C, s.kname('sc_bwd'))
+            sfx = 'i' if m.last_layout == 'irreps' else ''      # fed by an unformed reshape_irreps
+            rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C, s.kname('sc_fwd' + sfx))
+            rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C, s.kname('sc_bwd' + sfx))
         elif isinstance(m, HipSphericalHarmonics):
             s = m.spec                                  # every edge of the padded list is evaluated
             bf, bb = s.bytes(batch['edge_index'].shape[1])
@@ -96,6 +97,10 @@ def _kernel_table(met, batch, n_real_edges, summary):
             bf, bb = m.spec.bytes(batch['edge_index'].shape[1])
             rows[f'emb_fwd[{m.tag}]'] = (bf, 0, m.spec.kname('emb_fwd'))
             rows[f'emb_bwd[{m.tag}]'] = (bb, 0, m.spec.kname('emb_bwd'))
+        elif isinstance(m, HipReadout):
+            bf, bb = m.spec.bytes(n)
+            rows[f'ro_fwd[{m.tag}]'] = (bf, 0, m.spec.kname('ro_fwd'))
+            rows[f'ro_bwd[{m.tag}]'] = (bb, 0, m.spec.kname('ro_bwd'))
         elif isinstance(m, HipRadialMLP):
             s = m.spec                                  # every edge of the padded list is evaluated
             E = batch['edge_index'].shape[1]
@@ -148,7 +153,7 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
 
 
 # symbol prefixes of this package's generated kernels
-HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_')
+HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_', 'ro_')
 COPY_BYTES = 1 << 30          # size of the calibration copy (read 1 GiB, write 1 GiB) of --profile
 
 

@@ -521,6 +521,7 @@ class HipSymmetricContraction(torch.nn.Module):
         self.original = [sc]
         self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
         self.grouped = None           # None: by size (use_grouped); True / False: force a kernel family
+        self.last_layout = None       # input layout of the last call: 'mace' [N, C, n_ell] or 'irreps'
 
     def use_grouped(self, n_nodes, device):
         """The element-grouped kernels serve GROUP nodes per workgroup, so they need GROUP times more nodes to keep
@@ -541,5 +542,7 @@ class HipSymmetricContraction(torch.nn.Module):
         src = getattr(x, 'irreps_source', None)
         if src is not None and self.spec.dims is not None and src(self.spec.dims) is not None:
             # x is MACE's reshape_irreps of a tensor in e3nn's layout, not yet formed: read that tensor directly
+            self.last_layout = 'irreps'
             return _SCIrrepsFn.apply(src(self.spec.dims), elem, order, self)
+        self.last_layout = 'mace'
         return _SCFn.apply(x, elem, order, self)
