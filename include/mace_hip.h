@@ -65,7 +65,11 @@ enum mh_kernel_kind {
     MH_SC_BWD_GI = 26,   /* MH_SC_BWD_G in the irreps layout                                       */
     MH_READOUT_FWD = 27, /* readout head: per-node energy from the node features, 16 nodes a block  */
     MH_READOUT_BWD = 28, /* its input gradient                                                     */
-    MH_NUM_KINDS = 29
+    MH_SC_JVP = 29,      /* symmetric contraction: directional derivative of the output, node rows */
+    MH_SC_BWD2 = 30,     /* directional derivative of the x-gradient (a Hessian-vector product)     */
+    MH_SC_JVP_I = 31,    /* MH_SC_JVP in the irreps layout                                          */
+    MH_SC_BWD2_I = 32,   /* MH_SC_BWD2 in the irreps layout                                         */
+    MH_NUM_KINDS = 33
 };
 
 /* flags of mh_conv_bwd */
@@ -181,6 +185,20 @@ int mh_sc_fwd_irreps(mh_module* m, const float* X, const int32_t* elem, const in
                      float* out, int32_t N, void* stream);
 int mh_sc_bwd_irreps(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
                      const float* G, float* GX, int32_t N, void* stream);
+
+/* Second derivatives of the symmetric contraction, behind a double backward.  With P(X) the contraction of
+ * mh_sc_fwd and V a direction in the layout of X:
+ *   mh_sc_jvp:  out = d/de P(X + eV) at e = 0 (the forward-mode derivative; [N, out_dim] like mh_sc_fwd), which is
+ *               the gradient of <V, dL/dX> with respect to G;
+ *   mh_sc_bwd2: GX = d/de (dP/dX(X + eV))^T G at e = 0 (a Hessian-vector product of <G, P>), the gradient of
+ *               <V, dL/dX> with respect to X.
+ * layout 0: X, V, GX as [N, C, n_ell] (kernels MH_SC_JVP / MH_SC_BWD2); 1: e3nn's irreps layout as in
+ * mh_sc_fwd_irreps (MH_SC_JVP_I / MH_SC_BWD2_I).  One node per workgroup (rows_per_block 1).  No reference
+ * counterpart: the reference raises on a double backward (symmetric.py:147-149). */
+int mh_sc_jvp(mh_module* m, const float* X, const float* V, const int32_t* elem, const float* T, float* out,
+              int32_t N, int32_t layout, void* stream);
+int mh_sc_bwd2(mh_module* m, const float* X, const float* V, const int32_t* elem, const float* T, const float* G,
+               float* GX, int32_t N, int32_t layout, void* stream);
 
 /* Edge spherical harmonics Y[e, :] = Y_{0..l_max}(vec[e] / |vec[e]|) (vec [E, 3], Y [E, (l_max+1)^2]; e3nn's real
  * basis, y polar axis) and their backward gvec[e] = dL/dvec[e] from gY.  The kernels are generated per (l_max,

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 17; }
+int mh_version(void) { return 18; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -289,6 +289,20 @@ int mh_sc_bwd_irreps(mh_module* m, const float* X, const int32_t* elem, const in
     }
     void* args[] = {&X, &elem, &order, &T, &G, &GX, &N};
     return launch(m, MH_SC_BWD_GI, N, args, stream, "mh_sc_bwd_irreps");
+}
+
+int mh_sc_jvp(mh_module* m, const float* X, const float* V, const int32_t* elem, const float* T, float* out,
+              int32_t N, int32_t layout, void* stream) {
+    if (layout != 0 && layout != 1) return fail(-1, "mh_sc_jvp: layout must be 0 or 1");
+    void* args[] = {&X, &V, &elem, &T, &out, &N};
+    return launch(m, layout ? MH_SC_JVP_I : MH_SC_JVP, N, args, stream, "mh_sc_jvp");
+}
+
+int mh_sc_bwd2(mh_module* m, const float* X, const float* V, const int32_t* elem, const float* T, const float* G,
+               float* GX, int32_t N, int32_t layout, void* stream) {
+    if (layout != 0 && layout != 1) return fail(-1, "mh_sc_bwd2: layout must be 0 or 1");
+    void* args[] = {&X, &V, &elem, &T, &G, &GX, &N};
+    return launch(m, layout ? MH_SC_BWD2_I : MH_SC_BWD2, N, args, stream, "mh_sc_bwd2");
 }
 
 int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream) {

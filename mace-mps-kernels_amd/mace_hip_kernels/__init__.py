@@ -65,7 +65,8 @@ def _linear_candidates(model):
 
 
 def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
-                radial_mlp=True, radial_embedding=True, layouts=True, edge_geometry=True, readouts=True):
+                radial_mlp=True, radial_embedding=True, layouts=True, edge_geometry=True, readouts=True,
+                double_backward=False):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
     edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
@@ -77,7 +78,15 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     block's ``reshape`` (irreps layout -> symmetric-contraction layout), and ``edge_geometry`` the edge vectors and
     lengths (MACE's ``get_edge_vectors_and_lengths`` in the model's module, taken over only while this model's forward
     runs; other models keep the original), and ``readouts`` the per-interaction readout heads (``LinearReadoutBlock``,
-    ``NonLinearReadoutBlock``) as one kernel per direction each."""
+    ``NonLinearReadoutBlock``) as one kernel per direction each.
+
+    ``double_backward`` (default off, as in the reference, where a backward under ``create_graph=True`` raises)
+    makes the patched modules' gradients differentiable once more, for second derivatives with respect to the
+    inputs: Hessian-vector products and force constants, or force and stress terms of a loss differentiated with
+    respect to parameters the patch leaves on e3nn.  The convolution, symmetric contraction, linears, layout change
+    and linear readout heads take it; the modules without second-order kernels (spherical harmonics, edge geometry,
+    radial embedding and MLP, SiLU readout heads) are then left on e3nn and reported in ``skipped``.  The patched
+    modules hold their weights as constants: no gradient reaches those weights, with or without it."""
     # a fully patched model may hold no parameters any more (the drop-ins keep their weights as buffers)
     p = next((t for t in itertools.chain(model.parameters(), model.buffers()) if t.is_floating_point()), None)
     if p is None:
@@ -125,6 +134,16 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             prod.symmetric_contractions = HipSymmetricContraction(sc, device=dev)
             prod.symmetric_contractions.tag = name
             patched.append(name)
+    no2 = 'no second-order kernels (patched with double_backward=True)'
+    if double_backward:
+        for flag, name, present in ((spherical_harmonics, 'spherical_harmonics', hasattr(model, 'spherical_harmonics')),
+                                    (edge_geometry, 'edge_geometry', True),
+                                    (radial_embedding, 'radial_embedding', hasattr(model, 'radial_embedding'))):
+            if flag and present:
+                skipped.append((name, no2))
+        if radial_mlp:
+            skipped += [(f'interactions.{i}.conv_tp_weights', no2) for i in range(len(getattr(model, 'interactions', [])))]
+        spherical_harmonics = edge_geometry = radial_embedding = radial_mlp = False
     if spherical_harmonics and hasattr(model, 'spherical_harmonics'):
         sh = model.spherical_harmonics
         if not isinstance(sh, HipSphericalHarmonics):
@@ -199,6 +218,7 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             if ok:
                 try:
                     new = HipReadout(ro, device=dev)
+                    new.double_backward = double_backward      # ValueError for a SiLU head
                 except ValueError as e:
                     ok, why = False, str(e)
             if not ok:
@@ -228,6 +248,14 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 new.div_hint = float(avg)
             setattr(parent, attr, new)
             patched.append(name)
+    if double_backward:                   # including modules patched by an earlier call
+        for mod in model.modules():
+            if isinstance(mod, (HipConvTP, HipSymmetricContraction, HipNodeLinear, HipReshapeIrreps)):
+                mod.double_backward = True
+                if isinstance(mod, HipSymmetricContraction):
+                    mod.second_module()   # compiled now rather than inside the first double backward
+            elif isinstance(mod, HipReadout) and mod.spec.kind == 'linear':
+                mod.double_backward = True
     if verbose:
         for name, why in skipped:
             warnings.warn(f'mace_hip_kernels: kept e3nn for {name}: {why}')

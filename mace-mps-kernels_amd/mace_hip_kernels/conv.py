@@ -256,7 +256,8 @@ def clear_graph_cache():
 
 # ------------------------------------------------------------------------------------------------ autograd
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
 
 
 def _check_inputs(op, x, Y, W, edge_index):
@@ -381,6 +382,37 @@ class RadialWeights(torch.Tensor):
 _MULS = {torch.Tensor.__mul__, torch.Tensor.__rmul__, torch.Tensor.mul, torch.mul}
 
 
+def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy):
+    """First-order gradients (gx, gY, gW or gW0, gcut) of <g, conv(x, Y, W)> for contiguous operands, by the
+    kernels; W = W0 * cut (cut flat [E]) when W is None.  Entries not wanted are None."""
+    factored = W is None
+    E = Y.shape[0]
+    gx = torch.empty_like(x) if want_x else None
+    gY = torch.empty_like(Y) if want_wy else None
+    gW = torch.empty_like(W0 if factored else W) if want_wy else None
+    gcut = torch.empty_like(cut) if want_wy and factored else None
+    # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
+    flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy and E > 0 else 0)
+    lib = _native.load()
+    P = _native.ptr
+    if flags & _native.MH_WANT_GWY and (op.bwd_recv or factored):
+        # receiver order: g rows read once per receiver; dX goes through per-edge messages in `work`
+        rowptr_r, eids_r = gr.by_recv()
+        rowptr_s, eids_s = gr.by_send() if want_x else (None, None)
+        work = torch.empty(E, op.spec.x_dim, device=x.device, dtype=torch.float32) if want_x else None
+        _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv, op.module.handle, P(x), P(g), P(Y),
+                       P(W0 if factored else W), P(rowptr_r), P(eids_r), P(gr.send), P(rowptr_s), P(eids_s),
+                       P(work), P(gx), P(gW), P(gY), P(cut), P(gcut), x.shape[0], flags, _native.stream_of(x))
+    elif flags:
+        if factored:                     # dX only: the sender-ordered kernel needs the product
+            W = W0 * cut[:, None]
+        rowptr_s, eids_s = gr.by_send()
+        _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, P(x), P(g), P(Y), P(W),
+                       P(rowptr_s), P(eids_s), P(gr.recv), P(gx), P(gW), P(gY), x.shape[0], flags,
+                       _native.stream_of(x))
+    return gx, gY, gW, gcut
+
+
 class _ConvFn(torch.autograd.Function):
     """Inputs (x, Y, W, W0, cut, edge_index, op).  Plain: W is the weight tensor, W0 = cut = None.  Factored:
     W is None, W0 and cut are the differentiable inputs and the kernels form W0 * cut per edge in registers."""
@@ -388,8 +420,7 @@ class _ConvFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, Y, W, W0, cut, edge_index, op):
         _check_inputs(op, x, Y, W if W is not None else W0, edge_index)
-        x, Y = x.contiguous(), Y.contiguous()
-        W = W.contiguous() if W is not None else None
+        xc, Yc = x.contiguous(), Y.contiguous()
         n = x.shape[0]
         gr = graph_for(edge_index, n)
         rowptr, eids = gr.by_recv()
@@ -397,64 +428,110 @@ class _ConvFn(torch.autograd.Function):
         lib = _native.load()
         ctx.factored = W0 is not None
         P = _native.ptr
+        # the inputs themselves are saved (contiguous copies are made again in backward if needed): a double
+        # backward differentiates through them
         if ctx.factored:
             cutf = cut.reshape(-1).contiguous()
             # edges with cutoff 0 (padding, or beyond r_max in a skinned neighbour list) contribute exactly zero
-            W0 = W0.contiguous()
-            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd_cut, op.module.handle, P(x), P(Y), P(W0),
-                           P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n, _native.stream_of(x))
+            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd_cut, op.module.handle, P(xc), P(Yc),
+                           P(W0.contiguous()), P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n,
+                           _native.stream_of(x))
             ctx.cut_shape = cut.shape
-            ctx.save_for_backward(x, Y, W0, cutf)
+            ctx.save_for_backward(x, Y, W0, cut, edge_index)
         else:
-            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, P(x), P(Y), P(W), P(rowptr),
-                           P(eids), P(gr.send), P(out), n, _native.stream_of(x))
-            ctx.save_for_backward(x, Y, W)
+            _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, P(xc), P(Yc), P(W.contiguous()),
+                           P(rowptr), P(eids), P(gr.send), P(out), n, _native.stream_of(x))
+            ctx.save_for_backward(x, Y, W, edge_index)
         ctx.op, ctx.gr = op, gr
         return out
 
     @staticmethod
     def backward(ctx, g):
-        if torch.is_grad_enabled():          # only true under create_graph=True
-            raise RuntimeError(_DOUBLE_BACKWARD)
         op, gr = ctx.op, ctx.gr
         if ctx.factored:
-            x, Y, W0, cut = ctx.saved_tensors
-            want_w = _grad_needed(ctx, 3) or _grad_needed(ctx, 4)
+            x, Y, W0, cut, edge_index = ctx.saved_tensors
+            want_w0, want_cut = _grad_needed(ctx, 3), _grad_needed(ctx, 4)
+            want_w = want_w0 or want_cut
         else:
-            x, Y, W = ctx.saved_tensors
-            W0 = cut = None
+            x, Y, W, edge_index = ctx.saved_tensors
             want_w = _grad_needed(ctx, 2)
-        g = g.contiguous()
-        want_x = _grad_needed(ctx, 0)
-        want_wy = _grad_needed(ctx, 1) or want_w
-        E = Y.shape[0]
-        gx = torch.empty_like(x) if want_x else None
-        gY = torch.empty_like(Y) if want_wy else None
-        gW = torch.empty_like(W0 if ctx.factored else W) if want_wy else None
-        gcut = torch.empty_like(cut) if want_wy and ctx.factored else None
-        # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
-        flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy and E > 0 else 0)
-        lib = _native.load()
-        P = _native.ptr
-        if flags & _native.MH_WANT_GWY and (op.bwd_recv or ctx.factored):
-            # receiver order: g rows read once per receiver; dX goes through per-edge messages in `work`
-            rowptr_r, eids_r = gr.by_recv()
-            rowptr_s, eids_s = gr.by_send() if want_x else (None, None)
-            work = torch.empty(E, op.spec.x_dim, device=x.device, dtype=torch.float32) if want_x else None
-            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv, op.module.handle, P(x), P(g), P(Y),
-                           P(W0 if ctx.factored else W), P(rowptr_r), P(eids_r), P(gr.send), P(rowptr_s), P(eids_s),
-                           P(work), P(gx), P(gW), P(gY), P(cut), P(gcut), x.shape[0], flags, _native.stream_of(x))
-        elif flags:
-            if ctx.factored:                 # dX only: the sender-ordered kernel needs the product
-                W = W0 * cut[:, None]
-            rowptr_s, eids_s = gr.by_send()
-            _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, P(x), P(g), P(Y), P(W),
-                           P(rowptr_s), P(eids_s), P(gr.recv), P(gx), P(gW), P(gY), x.shape[0], flags,
-                           _native.stream_of(x))
+        want_x, want_y = _grad_needed(ctx, 0), _grad_needed(ctx, 1)
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            # the gradients as a differentiable function of (g, x, Y, W); the product W0 * cut and its rule are
+            # ordinary torch operations here
+            if ctx.factored:
+                c2 = cut.reshape(-1, 1)
+                W = W0 * c2
+            gx, gY, gW = _ConvAdjFn.apply(g, x, Y, W, edge_index, op, gr, (want_x, want_y, want_w))
+            if ctx.factored:
+                gW0 = gW * c2 if want_w0 else None
+                gc = (gW * W0).sum(-1).reshape(ctx.cut_shape) if want_cut else None
+                return gx, gY, None, gW0, gc, None, None
+            return gx, gY, gW, None, None, None, None
+        xc, Yc, gc_ = x.contiguous(), Y.contiguous(), g.contiguous()
         if ctx.factored:
-            gc = gcut.view(ctx.cut_shape) if gcut is not None else None
-            return gx, gY, None, gW, gc, None, None
+            gx, gY, gW, gcut = _conv_grads(op, gr, gc_, xc, Yc, None, W0.contiguous(), cut.reshape(-1).contiguous(),
+                                           want_x, want_y or want_w)
+            return gx, gY, None, gW, gcut.view(ctx.cut_shape) if gcut is not None else None, None, None
+        gx, gY, gW, _ = _conv_grads(op, gr, gc_, xc, Yc, W.contiguous(), None, None, want_x, want_y or want_w)
         return gx, gY, gW, None, None, None, None
+
+
+class _ConvAdjFn(torch.autograd.Function):
+    """(gx, gY, gW): the first-order gradients of <g, conv(x, Y, W)> as a differentiable function of (g, x, Y, W),
+    for a double backward.  The convolution is linear in each of x, Y and W, so each second derivative is a
+    first-order quantity with one argument replaced by the incoming direction: with (ggx, ggY, ggW) the gradients
+    arriving for (gx, gY, gW),
+        d/dg = conv(ggx, Y, W) + conv(x, ggY, W) + conv(x, Y, ggW),
+        d/dx = gx(g; ggY, W) + gx(g; Y, ggW),  d/dY = gY(g; ggx, W) + gY(g; x, ggW),  d/dW = gW(g; ggx, Y) + gW(g; x, ggY),
+    computed by the same kernels (through this function and _ConvFn again, so higher orders follow).  ``want``
+    (x, Y, W) says which gradients to form; the others are returned as None."""
+
+    @staticmethod
+    def forward(ctx, g, x, Y, W, edge_index, op, gr, want):
+        want_x, want_y, want_w = want
+        gx, gY, gW, _ = _conv_grads(op, gr, g.contiguous(), x.contiguous(), Y.contiguous(), W.contiguous(), None,
+                                    None, want_x, want_y or want_w)
+        ctx.save_for_backward(g, x, Y, W, edge_index)
+        ctx.op, ctx.gr = op, gr
+        return gx if want_x else None, gY if want_y else None, gW if want_w else None
+
+    @staticmethod
+    def backward(ctx, ggx, ggY, ggW):
+        g, x, Y, W, edge_index = ctx.saved_tensors
+        op, gr = ctx.op, ctx.gr
+        need_g, need_x, need_y, need_w = (_grad_needed(ctx, i) for i in range(4))
+        acc = [None, None, None, None]
+
+        def add(i, t):
+            if t is not None:
+                acc[i] = t if acc[i] is None else acc[i] + t
+
+        def conv(a, b, c):
+            return _ConvFn.apply(a, b, c, None, None, edge_index, op)
+
+        if need_g:
+            if ggx is not None:
+                add(0, conv(ggx, Y, W))
+            if ggY is not None:
+                add(0, conv(x, ggY, W))
+            if ggW is not None:
+                add(0, conv(x, Y, ggW))
+        if ggY is not None and (need_x or need_w):            # Y -> ggY: gradients for x and W
+            a, _, c = _ConvAdjFn.apply(g, x, ggY, W, edge_index, op, gr, (need_x, False, need_w))
+            add(1, a)
+            add(3, c)
+        if ggW is not None and (need_x or need_y):            # W -> ggW: gradients for x and Y
+            a, b, _ = _ConvAdjFn.apply(g, x, Y, ggW, edge_index, op, gr, (need_x, need_y, False))
+            add(1, a)
+            add(2, b)
+        if ggx is not None and (need_y or need_w):            # x -> ggx: gradients for Y and W
+            _, b, c = _ConvAdjFn.apply(g, ggx, Y, W, edge_index, op, gr, (False, need_y, need_w))
+            add(2, b)
+            add(3, c)
+        return acc[0], acc[1], acc[2], acc[3], None, None, None, None
 
 
 class HipConvTP(torch.nn.Module):
@@ -487,6 +564,9 @@ class HipConvTP(torch.nn.Module):
         self.bwd_recv = True
         # differentiate MACE's tp_weights = W0 * cutoff inside the backward kernel (see _factored_weights)
         self.fuse_cutoff = True
+        # a backward under create_graph=True: raise (the reference's behaviour) unless this is set, in which case
+        # the gradients are differentiable again (_ConvAdjFn)
+        self.double_backward = False
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
         if isinstance(tp_weights, CutoffProduct):

@@ -135,15 +135,35 @@ class _PermFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g):
-        if torch.is_grad_enabled():
-            raise RuntimeError('mace_hip_kernels: double backward (create_graph=True) is not supported by the HIP '
-                               'kernels; use the unpatched e3nn model for that')
         op = ctx.op
-        g = g.contiguous()
-        gx = torch.empty(g.shape[0], op.spec.dim, device=g.device, dtype=torch.float32)
-        _native.launch(f'perm_bwd[{op.tag}]', _native.load().mh_perm_bwd, op.module.handle, _native.ptr(g),
-                       _native.ptr(gx), g.shape[0], _native.stream_of(g))
-        return gx, None
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError('mace_hip_kernels: double backward (create_graph=True) is not enabled for this '
+                                   'HIP module; patch with patch_model(model, double_backward=True)')
+            return _PermAdjFn.apply(g, op), None
+        return _perm_bwd(op, g), None
+
+
+def _perm_bwd(op, g):
+    g = g.contiguous()
+    gx = torch.empty(g.shape[0], op.spec.dim, device=g.device, dtype=torch.float32)
+    _native.launch(f'perm_bwd[{op.tag}]', _native.load().mh_perm_bwd, op.module.handle, _native.ptr(g),
+                   _native.ptr(gx), g.shape[0], _native.stream_of(g))
+    return gx
+
+
+class _PermAdjFn(torch.autograd.Function):
+    """The inverse permutation as a differentiable function of g (a double backward): its gradient is the forward
+    permutation."""
+
+    @staticmethod
+    def forward(ctx, g, op):
+        ctx.op = op
+        return _perm_bwd(op, g)
+
+    @staticmethod
+    def backward(ctx, ggx):
+        return _PermFn.apply(ggx, ctx.op), None
 
 
 class HipReshapeIrreps(torch.nn.Module):
@@ -161,6 +181,9 @@ class HipReshapeIrreps(torch.nn.Module):
         self.irreps = mod.irreps
         self.original = [mod]
         self.tag = 'reshape'
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; the map is
+        # linear, so its double backward is the forward map again
+        self.double_backward = False
         # set by patch_model when the only consumer is a patched symmetric contraction, which can read the irreps
         # layout itself: forward then returns a PendingReshape
         self.fuse = False

@@ -739,7 +739,8 @@ def node_order(attrs):
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
 
 
 class _LinFn(torch.autograd.Function):
@@ -775,24 +776,49 @@ class _LinFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
         # node attributes are data (MACE's one-hot element encoding): no gradient flows to them, as in the
         # symmetric contraction
         if not ctx.needs_input_grad[0]:
             return None, None, None, None
         op = ctx.op
-        s = op.spec
-        if not s.has_bwd:
-            raise NotImplementedError(f'mace_hip_kernels: {op.tag} has input multiplicities that the backward kernel '
-                                      'does not tile (multiples of 16 needed)')
         a2, order = ctx.saved_tensors if ctx.saved_tensors else (None, None)
-        g2 = g.reshape(-1, s.Dout).contiguous()
-        gx = torch.empty(ctx.N, s.Din, device=g.device, dtype=torch.float32)
-        _native.launch(f'lin_bwd[{op.tag}]', _native.load().mh_lin_bwd, op.module.handle, _native.ptr(g2),
-                       _native.ptr(a2), _native.ptr(op.Wt), _native.ptr(gx), _native.ptr(order), ctx.scale,
-                       ctx.N, _native.stream_of(g2))
-        return gx.reshape(*ctx.lead, s.Din), None, None, None
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            return _LinAdjFn.apply(g, a2, order, op, ctx.scale, ctx.lead), None, None, None
+        return _lin_bwd(op, g, a2, order, ctx.scale, ctx.lead), None, None, None
+
+
+def _lin_bwd(op, g, a2, order, scale, lead):
+    """The input gradient L^T g [*lead, Din] of g [*lead, Dout] by the backward kernel."""
+    s = op.spec
+    if not s.has_bwd:
+        raise NotImplementedError(f'mace_hip_kernels: {op.tag} has input multiplicities that the backward kernel '
+                                  'does not tile (multiples of 16 needed)')
+    g2 = g.reshape(-1, s.Dout).contiguous()
+    N = g2.shape[0]
+    gx = torch.empty(N, s.Din, device=g.device, dtype=torch.float32)
+    _native.launch(f'lin_bwd[{op.tag}]', _native.load().mh_lin_bwd, op.module.handle, _native.ptr(g2),
+                   _native.ptr(a2), _native.ptr(op.Wt), _native.ptr(gx), _native.ptr(order), scale, N,
+                   _native.stream_of(g2))
+    return gx.reshape(*lead, s.Din)
+
+
+class _LinAdjFn(torch.autograd.Function):
+    """gx = L^T g as a function of g, for a double backward.  The map is linear in x, so gx does not depend on x and
+    d<ggx, L^T g>/dg = L ggx: the forward map again (through _LinFn, so higher orders follow)."""
+
+    @staticmethod
+    def forward(ctx, g, a2, order, op, scale, lead):
+        ctx.save_for_backward(a2)
+        ctx.op, ctx.scale, ctx.lead = op, scale, lead
+        return _lin_bwd(op, g, a2, order, scale, lead)
+
+    @staticmethod
+    def backward(ctx, ggx):
+        a2, = ctx.saved_tensors
+        attrs = a2.reshape(*ctx.lead, a2.shape[-1]) if a2 is not None else None
+        return _LinFn.apply(ggx, attrs, ctx.op, ctx.scale), None, None, None, None, None
 
 
 class HipNodeLinear(torch.nn.Module):
@@ -827,6 +853,9 @@ class HipNodeLinear(torch.nn.Module):
                 setattr(self, k, getattr(mod, k))
         self.original = [mod]
         self.tag = 'linear'
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; the map is
+        # linear, so its double backward is the forward map again
+        self.double_backward = False
         # set by patch_model when the caller divides the output by a constant: forward then returns a PendingLinear
         self.div_hint = None
 

@@ -527,7 +527,8 @@ def packed_weights(spec):
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+                    'autograd Hessian) is not supported by this HIP module; patch_model(model, '
+                    'double_backward=True) leaves it on e3nn')
 
 
 class _MLPFn(torch.autograd.Function):

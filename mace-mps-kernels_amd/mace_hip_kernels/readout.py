@@ -233,7 +233,8 @@ def source(spec):
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
 
 
 class _ReadoutFn(torch.autograd.Function):
@@ -256,15 +257,36 @@ class _ReadoutFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
         x2, = ctx.saved_tensors
         op = ctx.op
-        g2 = g.reshape(-1).contiguous()
-        gx = torch.empty_like(x2)
-        _native.launch(f'ro_bwd[{op.tag}]', _native.load().mh_readout_bwd, op.module.handle, _native.ptr(x2),
-                       _native.ptr(g2), _native.ptr(gx), x2.shape[0], _native.stream_of(x2))
-        return gx.reshape(*ctx.lead, op.spec.Din), None
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            return _ReadoutAdjFn.apply(g, x2, op, ctx.lead), None
+        return _readout_bwd(op, x2, g, ctx.lead), None
+
+
+def _readout_bwd(op, x2, g, lead):
+    g2 = g.reshape(-1).contiguous()
+    gx = torch.empty_like(x2)
+    _native.launch(f'ro_bwd[{op.tag}]', _native.load().mh_readout_bwd, op.module.handle, _native.ptr(x2),
+                   _native.ptr(g2), _native.ptr(gx), x2.shape[0], _native.stream_of(x2))
+    return gx.reshape(*lead, op.spec.Din)
+
+
+class _ReadoutAdjFn(torch.autograd.Function):
+    """The linear head's input gradient g w^T as a function of g, for a double backward: it does not depend on x,
+    and d<ggx, g w^T>/dg = ggx w, the head itself (through _ReadoutFn, so higher orders follow).  Only linear heads
+    (``HipReadout.double_backward`` is refused for the SiLU heads)."""
+
+    @staticmethod
+    def forward(ctx, g, x2, op, lead):
+        ctx.op = op
+        return _readout_bwd(op, x2, g, lead)
+
+    @staticmethod
+    def backward(ctx, ggx):
+        return _ReadoutFn.apply(ggx, ctx.op), None, None, None
 
 
 class HipReadout(torch.nn.Module):
@@ -282,6 +304,18 @@ class HipReadout(torch.nn.Module):
                 _native.MH_READOUT_BWD: (self.spec.kname('ro_bwd'), BLOCK, BLOCK // LANES)})
         self.original = [mod]
         self.tag = 'readout'
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; linear heads only
+        self._double_backward = False
+
+    @property
+    def double_backward(self):
+        return self._double_backward
+
+    @double_backward.setter
+    def double_backward(self, on):
+        if on and self.spec.kind != 'linear':
+            raise ValueError('mace_hip_kernels: only linear readout heads have a double backward')
+        self._double_backward = bool(on)
 
     def forward(self, x, heads=None):
         return _ReadoutFn.apply(x, self)

@@ -11,7 +11,8 @@ index permutations into sorted monomials, and monomials that vanish for every (e
 
 Table layout T[element][monomial × M][channel] (fp32): the 64 lanes of a wave are 64 channels of one node, so every
 coefficient row is one coalesced 256-byte load.  Monomials are evaluated in FP32 VALU with shared prefix products.
-Backward: ∂/∂x of the polynomial (first order; double backward raises).
+Backward: ∂/∂x of the polynomial.  A double backward raises unless enabled (``double_backward``); then two more
+kernels give the forward-mode derivative and the Hessian-vector product of the same polynomial.
 """
 import itertools
 import math
@@ -199,6 +200,51 @@ def _bwd_walk(spec, node, depth, L, ind, cnt):
         L.append(f'{ind}}}')
 
 
+def _prefix(depth, i, L, ind):
+    """Open the scope of the child x_i: prefix product p and its tangent q along V (p' = p x_i, q' = q x_i + p v_i)."""
+    if depth == 0:
+        L.append(f'{ind}{{ const float p1 = x{i}; const float q1 = v{i};')
+    else:
+        L.append(f'{ind}{{ const float p{depth + 1} = p{depth} * x{i}; '
+                 f'const float q{depth + 1} = fmaf(q{depth}, x{i}, p{depth} * v{i});')
+
+
+def _jvp_walk(spec, node, depth, L, ind, cnt):
+    """Forward mode along the trie: each term adds coefficient × (tangent of its monomial along V)."""
+    live = [f'a{bi}_{m}' for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+    if depth > 0:                 # a constant term has no tangent
+        for bi, r0, M in node['terms']:
+            _fence(L, ind, cnt, M, live)
+            L += [f'{ind}a{bi}_{m} = fmaf(t[{(r0 + m) * spec.C}], q{depth}, a{bi}_{m});' for m in range(M)]
+    for i in sorted(node['kids']):
+        _prefix(depth, i, L, ind)
+        _jvp_walk(spec, node['kids'][i], depth + 1, L, ind + '  ', cnt)
+        L.append(f'{ind}}}')
+
+
+def _bwd2_walk(spec, node, depth, L, ind, cnt):
+    """The reverse-mode walk of ``_bwd_walk`` with x carried as x + εv: G{depth} is ∂<g,out>/∂p{depth} as before and
+    H{depth} its ε part; the ε part of every d_i update goes to h_i, which ends as the directional derivative of the
+    gradient along V (terms contribute to G only: coefficients and g do not depend on x)."""
+    live = ([f'h{i}' for i in range(spec.n_ell)] + [f'G{k}' for k in range(1, depth + 1)]
+            + [f'H{k}' for k in range(1, depth + 1)])
+    for bi, r0, M in node['terms']:
+        _fence(L, ind, cnt, M, live)
+        s = ' + '.join(f't[{(r0 + m) * spec.C}] * g{bi}_{m}' for m in range(M))
+        L.append(f'{ind}G{depth} += {s};')
+    for i in sorted(node['kids']):
+        _prefix(depth, i, L, ind)
+        L.append(f'{ind}  float G{depth + 1} = 0.0f; float H{depth + 1} = 0.0f;')
+        _bwd2_walk(spec, node['kids'][i], depth + 1, L, ind + '  ', cnt)
+        if depth == 0:
+            L.append(f'{ind}  h{i} += H1;')
+        else:
+            L.append(f'{ind}  h{i} = fmaf(H{depth + 1}, p{depth}, fmaf(G{depth + 1}, q{depth}, h{i}));')
+            L.append(f'{ind}  G{depth} = fmaf(G{depth + 1}, x{i}, G{depth});')
+            L.append(f'{ind}  H{depth} = fmaf(H{depth + 1}, x{i}, fmaf(G{depth + 1}, v{i}, H{depth}));')
+        L.append(f'{ind}}}')
+
+
 def _fwd_walk_g(spec, node, depth, L, ind, cnt, nb):
     """The forward walk for ``nb`` nodes of one element at once: each coefficient load feeds ``nb`` FMAs (node j's
     variables carry the prefix ``j``), in the same order as the one-node walk."""
@@ -244,14 +290,15 @@ def _bwd_walk_g(spec, node, depth, L, ind, cnt, nb):
         L.append(f'{ind}}}')
 
 
-def _source_layout(spec, group=None, irreps=False):
+def _source_layout(spec, group=None, irreps=False, second=False):
     """HIP source of the per-node kernels ``sc_fwd`` / ``sc_bwd`` (one workgroup per node, the reference's launch
     shape) and the element-grouped kernels ``sc_fwdg`` / ``sc_bwdg``: one workgroup per GROUP consecutive nodes of an
     element-sorted order.  When the group's nodes share an element (every group but those straddling an element
     boundary) every coefficient load feeds GROUP FMAs instead of one; other groups run the one-node body per node.
     Per node the arithmetic is the same sequence either way.  With ``irreps`` the same four kernels (names ending
     in ``i``) read x and write its gradient in e3nn's irreps layout [N, sum C (2l+1)] (MACE's reshape_irreps input),
-    so that permutation never runs."""
+    so that permutation never runs.  With ``second`` the module holds instead the two second-order kernels
+    ``sc_jvp`` / ``sc_bwd2`` (one node per workgroup) behind a double backward."""
     group = GROUP if group is None else group
     C, R, n = spec.C, spec.nrows, spec.n_ell
     sfx = 'i' if irreps else ''
@@ -321,6 +368,38 @@ def _source_layout(spec, group=None, irreps=False):
     def guarded(j, lines):
         return lines if j == 0 else [f'      if ({j} < qn) {{'] + ['  ' + x for x in lines] + ['      }']
 
+    if second:
+        vload = lambda ind: [f'{ind}const float v{i} = V[{xidx("b", i, "cc")}];' for i in range(n)]  # noqa: E731
+        # forward-mode derivative: out = d/dε P(X + εV)
+        L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_jvp" + sfx)}(const float* __restrict__ X,',
+              '    const float* __restrict__ V, const int* __restrict__ elem, const float* __restrict__ T,',
+              '    float* __restrict__ out, int N) {',
+              '  const int bq = mh_xcd_block(blockIdx.x, gridDim.x);', '  if (bq >= N) return;'] + lane
+        L += node_head('  ', 'bq') + vload('  ')
+        L += [f'  float a{bi}_{m} = 0.0f;' for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+        _jvp_walk(spec, trie, 0, L, '  ', [0])
+        L.append('  if (active) {')
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'    out[(size_t)b * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{bi}_{m};' for m in range(M)]
+        L += ['  }', '}', '']
+        # directional derivative of the gradient: GX = d/dε ∂<G, P>/∂X at X + εV
+        L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_bwd2" + sfx)}(const float* __restrict__ X,',
+              '    const float* __restrict__ V, const int* __restrict__ elem, const float* __restrict__ T,',
+              '    const float* __restrict__ G, float* __restrict__ GX, int N) {',
+              '  const int bq = mh_xcd_block(blockIdx.x, gridDim.x);', '  if (bq >= N) return;'] + lane
+        L += node_head('  ', 'bq') + vload('  ')
+        L += [f'  float h{i} = 0.0f;' for i in range(n)]
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'  const float g{bi}_{m} = G[(size_t)b * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];'
+                  for m in range(M)]
+        L.append('  float G0 = 0.0f;')
+        _bwd2_walk(spec, trie, 0, L, '  ', [0])
+        L += ['  (void)G0;', '  if (active) {']
+        L += [f'    GX[{xidx("b", i, "c")}] = h{i};' for i in range(n)]
+        L += ['  }', '}', '']
+        return '\n'.join(L)
     # ------------------------------------------------------------------------------- per-node forward
     L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sc_fwd" + sfx)}(const float* __restrict__ X,',
           '    const int* __restrict__ elem, const float* __restrict__ T, float* __restrict__ out, int N) {',
@@ -375,6 +454,17 @@ def _source_layout(spec, group=None, irreps=False):
     return '\n'.join(L)
 
 
+def source_second(spec):
+    """HIP source of the second-order module: ``sc_jvp`` / ``sc_bwd2`` on the [N, C, n_ell] layout and, when the
+    input irreps are known, on e3nn's irreps layout (``sc_jvpi`` / ``sc_bwd2i``).  Compiled only for a double
+    backward."""
+    src = _source_layout(spec, second=True)
+    if spec.dims is not None:
+        alt = _source_layout(spec, irreps=True, second=True)
+        src += '\n' + alt[alt.index('extern "C"'):]
+    return src
+
+
 def source(spec, group=None):
     """HIP source of one layer's module: the four kernels on the [N, C, n_ell] layout and, when the input irreps
     are known, the same four on e3nn's irreps layout (one shared header)."""
@@ -387,7 +477,8 @@ def source(spec, group=None):
 
 # ------------------------------------------------------------------------------------------------ autograd
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by the HIP kernels; use the unpatched e3nn model for that')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
 
 _elem_cache = []          # [(weakref(node_attrs), version, (elem int32, order int32))], most recent first
 _SIMDS = {}               # device index -> SIMD count (4 per compute unit)
@@ -414,6 +505,51 @@ def element_index(node_attrs):
     return element_order(node_attrs)[0]
 
 
+def _sc_fwd(op, layout, grouped, x, elem, order):
+    """Launch the contraction on contiguous x in ``layout`` ('mace' [N, C, n_ell] or 'irreps' [N, C n_ell])."""
+    N = x.shape[0]
+    out = torch.empty(N, op.spec.out_dim, device=x.device, dtype=torch.float32)
+    lib, P = _native.load(), _native.ptr
+    if layout == 'irreps':
+        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_irreps, op.module.handle, P(x), P(elem),
+                       P(order) if grouped else None, P(op.T), P(out), N, _native.stream_of(x))
+    elif grouped:
+        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_sorted, op.module.handle, P(x), P(elem), P(order),
+                       P(op.T), P(out), N, _native.stream_of(x))
+    else:
+        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd, op.module.handle, P(x), P(elem), P(op.T), P(out), N,
+                       _native.stream_of(x))
+    return out
+
+
+def _sc_bwd(op, layout, grouped, x, elem, order, g):
+    """Launch the contraction's x-gradient for contiguous x and g; the gradient has x's layout."""
+    gx = torch.empty_like(x)
+    lib, P = _native.load(), _native.ptr
+    if layout == 'irreps':
+        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_irreps, op.module.handle, P(x), P(elem),
+                       P(order) if grouped else None, P(op.T), P(g), P(gx), x.shape[0], _native.stream_of(x))
+    elif grouped:
+        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_sorted, op.module.handle, P(x), P(elem), P(order),
+                       P(op.T), P(g), P(gx), x.shape[0], _native.stream_of(x))
+    else:
+        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd, op.module.handle, P(x), P(elem), P(op.T), P(g), P(gx),
+                       x.shape[0], _native.stream_of(x))
+    return gx
+
+
+def _sc_backward(ctx, g):
+    """Shared backward of the two layouts' functions: the first-order kernel, or under create_graph (only then is
+    grad mode on here) the same gradient as a differentiable function of (g, x) when the module allows it."""
+    x, elem, order = ctx.saved_tensors
+    op = ctx.op
+    if torch.is_grad_enabled():
+        if not op.double_backward:
+            raise RuntimeError(_DOUBLE_BACKWARD)
+        return _SCAdjFn.apply(g, x, elem, order, op, ctx.layout, ctx.grouped), None, None, None
+    return _sc_bwd(op, ctx.layout, ctx.grouped, x.contiguous(), elem, order, g.contiguous()), None, None, None
+
+
 class _SCFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, elem, order, op):
@@ -422,39 +558,13 @@ class _SCFn(torch.autograd.Function):
             raise TypeError('mace_hip_kernels: symmetric contraction expects float32 GPU input')
         if x.dim() != 3 or x.shape[1] != s.C or x.shape[2] != s.n_ell:
             raise ValueError(f'node_feats must be [N, {s.C}, {s.n_ell}], got {tuple(x.shape)}')
-        x = x.contiguous()
-        N = x.shape[0]
-        out = torch.empty(N, s.out_dim, device=x.device, dtype=torch.float32)
-        lib = _native.load()
-        grouped = op.use_grouped(N, x.device)
-        if grouped:
-            _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_sorted, op.module.handle, _native.ptr(x),
-                           _native.ptr(elem), _native.ptr(order), _native.ptr(op.T), _native.ptr(out), N,
-                           _native.stream_of(x))
-        else:
-            _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd, op.module.handle, _native.ptr(x), _native.ptr(elem),
-                           _native.ptr(op.T), _native.ptr(out), N, _native.stream_of(x))
-        ctx.save_for_backward(x, elem, order)
-        ctx.grouped = grouped
-        ctx.op = op
+        grouped = op.use_grouped(x.shape[0], x.device)
+        out = _sc_fwd(op, 'mace', grouped, x.contiguous(), elem, order)
+        ctx.save_for_backward(x, elem, order)     # the input itself: a double backward differentiates through it
+        ctx.grouped, ctx.op, ctx.layout = grouped, op, 'mace'
         return out
 
-    @staticmethod
-    def backward(ctx, g):
-        if torch.is_grad_enabled():          # only true under create_graph=True
-            raise RuntimeError(_DOUBLE_BACKWARD)
-        x, elem, order = ctx.saved_tensors
-        op = ctx.op
-        gx = torch.empty_like(x)
-        lib, g = _native.load(), g.contiguous()
-        if ctx.grouped:
-            _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_sorted, op.module.handle, _native.ptr(x),
-                           _native.ptr(elem), _native.ptr(order), _native.ptr(op.T), _native.ptr(g), _native.ptr(gx),
-                           x.shape[0], _native.stream_of(x))
-        else:
-            _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd, op.module.handle, _native.ptr(x), _native.ptr(elem),
-                           _native.ptr(op.T), _native.ptr(g), _native.ptr(gx), x.shape[0], _native.stream_of(x))
-        return gx, None, None, None
+    backward = staticmethod(_sc_backward)
 
 
 class _SCIrrepsFn(torch.autograd.Function):
@@ -466,29 +576,46 @@ class _SCIrrepsFn(torch.autograd.Function):
         s = op.spec
         if x.dtype != torch.float32 or not x.is_cuda or x.dim() != 2 or x.shape[1] != s.C * s.n_ell:
             raise ValueError(f'expected float32 GPU input [N, {s.C * s.n_ell}], got {tuple(x.shape)}')
-        x = x.contiguous()
-        N = x.shape[0]
-        out = torch.empty(N, s.out_dim, device=x.device, dtype=torch.float32)
-        grouped = op.use_grouped(N, x.device)
-        _native.launch(f'sc_fwd[{op.tag}]', _native.load().mh_sc_fwd_irreps, op.module.handle, _native.ptr(x),
-                       _native.ptr(elem), _native.ptr(order) if grouped else None, _native.ptr(op.T),
-                       _native.ptr(out), N, _native.stream_of(x))
+        grouped = op.use_grouped(x.shape[0], x.device)
+        out = _sc_fwd(op, 'irreps', grouped, x.contiguous(), elem, order)
         ctx.save_for_backward(x, elem, order)
-        ctx.grouped, ctx.op = grouped, op
+        ctx.grouped, ctx.op, ctx.layout = grouped, op, 'irreps'
         return out
 
+    backward = staticmethod(_sc_backward)
+
+
+class _SCAdjFn(torch.autograd.Function):
+    """gx = (∂P/∂x)^T g as a function of (g, x), which a double backward differentiates: with ggx the incoming
+    gradient, d<ggx, gx>/dg is the forward-mode derivative of P along ggx (``mh_sc_jvp``) and d<ggx, gx>/dx the
+    Hessian-vector product of <g, P> (``mh_sc_bwd2``).  Third derivatives are not provided."""
+
     @staticmethod
-    def backward(ctx, g):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
-        x, elem, order = ctx.saved_tensors
+    def forward(ctx, g, x, elem, order, op, layout, grouped):
+        gx = _sc_bwd(op, layout, grouped, x.contiguous(), elem, order, g.contiguous())
+        ctx.save_for_backward(g, x, elem)
+        ctx.op, ctx.layout = op, layout
+        return gx
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggx):
+        g, x, elem = ctx.saved_tensors
         op = ctx.op
-        gx = torch.empty_like(x)
-        g = g.contiguous()
-        _native.launch(f'sc_bwd[{op.tag}]', _native.load().mh_sc_bwd_irreps, op.module.handle, _native.ptr(x),
-                       _native.ptr(elem), _native.ptr(order) if ctx.grouped else None, _native.ptr(op.T),
-                       _native.ptr(g), _native.ptr(gx), x.shape[0], _native.stream_of(x))
-        return gx, None, None, None
+        m = op.second_module()
+        lay = 1 if ctx.layout == 'irreps' else 0
+        x, v, g = x.contiguous(), ggx.contiguous(), g.contiguous()
+        lib, P, N = _native.load(), _native.ptr, x.shape[0]
+        gg = gx = None
+        if ctx.needs_input_grad[0]:
+            gg = torch.empty(N, op.spec.out_dim, device=x.device, dtype=torch.float32)
+            _native.launch(f'sc_jvp[{op.tag}]', lib.mh_sc_jvp, m.handle, P(x), P(v), P(elem), P(op.T), P(gg), N,
+                           lay, _native.stream_of(x))
+        if ctx.needs_input_grad[1]:
+            gx = torch.empty_like(x)
+            _native.launch(f'sc_bwd2[{op.tag}]', lib.mh_sc_bwd2, m.handle, P(x), P(v), P(elem), P(op.T), P(g),
+                           P(gx), N, lay, _native.stream_of(x))
+        return gg, gx, None, None, None, None, None
 
 
 class HipSymmetricContraction(torch.nn.Module):
@@ -522,6 +649,24 @@ class HipSymmetricContraction(torch.nn.Module):
         self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
         self.grouped = None           # None: by size (use_grouped); True / False: force a kernel family
         self.last_layout = None       # input layout of the last call: 'mace' [N, C, n_ell] or 'irreps'
+        # a backward under create_graph=True: raise (the reference's behaviour) unless this is set, in which case
+        # the gradient is differentiable once more through the second-order kernels (second_module)
+        self.double_backward = False
+        self._second = None
+
+    def second_module(self):
+        """The module of the second-order kernels (``sc_jvp``, ``sc_bwd2``), compiled on first use."""
+        if self._second is None:
+            s = self.spec
+            code = _native.compile_source(source_second(s))
+            kinds = {_native.MH_SC_JVP: (s.kname('sc_jvp'), s.block, 1),
+                     _native.MH_SC_BWD2: (s.kname('sc_bwd2'), s.block, 1)}
+            if s.dims is not None:
+                kinds.update({_native.MH_SC_JVP_I: (s.kname('sc_jvpi'), s.block, 1),
+                              _native.MH_SC_BWD2_I: (s.kname('sc_bwd2i'), s.block, 1)})
+            with torch.cuda.device(self.T.device):
+                self._second = _native.Module(code, kinds)
+        return self._second
 
     def use_grouped(self, n_nodes, device):
         """The element-grouped kernels serve GROUP nodes per workgroup, so they need GROUP times more nodes to keep

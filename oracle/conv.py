@@ -9,9 +9,11 @@ Restates, in float64 numpy, with coupling tables built from ``oracle.wigner`` (n
   * ``conv_fwd`` / ``conv_bwd_x`` / ``conv_bwd_w`` / ``conv_bwd_y``
                        the per-term formulas of the reference's three kernels (conv.py:109-141, 144-176, 179-222);
   * ``csr_by``         the receiver/sender CSR (conv.py:229-235) with numpy's stable argsort.
+  * ``conv_double_bwd`` the second derivatives of <g, out> as first-order formulas with substituted arguments.
 
 Pinned by (tests/test_oracle_conv.py): fused forward == unfused forward on random graphs; each backward formula ==
-central finite differences of the unfused forward; probed coefficients == path_terms; path (0e ⊗ l → l) is
+central finite differences of the unfused forward; conv_double_bwd == central
+finite differences of the first-order formulas; probed coefficients == path_terms; path (0e ⊗ l → l) is
 δ/√(2l+1)·√(2l+1) = identity; CSR == brute-force grouping.
 """
 import math
@@ -133,6 +135,24 @@ def conv_bwd_y(desc, coef, x, g, W, sender, receiver):
         for a, b, c, v in co['terms']:
             gY[:, o2 + b] += (v * w * x[sender][:, o1 + u * d1 + a] * g[receiver][:, o3 + u * d3 + c]).sum(1)
     return gY
+
+
+def conv_double_bwd(desc, coef, x, Y, W, g, ggx, ggY, ggW, sender, receiver, n):
+    """Gradients of s = <ggx, gx> + <ggY, gY> + <ggW, gW> (gx, gY, gW the first-order gradients of <g, out>) with
+    respect to (g, x, Y, W).  The product is linear in each of x, Y, W, so every term is a first-order formula with
+    one argument replaced by a direction: d s/d g = out(ggx, Y, W) + out(x, ggY, W) + out(x, Y, ggW), and e.g.
+    d s/d x = gx(g; ggY, W) + gx(g; Y, ggW) (the second derivatives the reference's backward guard refuses,
+    conv.py:254-256).  Any direction may be None (zero)."""
+    z = lambda a, shape: np.zeros(shape) if a is None else a             # noqa: E731
+    E = len(sender)
+    ggx, ggY, ggW = z(ggx, x.shape), z(ggY, Y.shape), z(ggW, W.shape)
+    f = lambda xx, yy, ww: conv_fwd(desc, coef, xx, yy, ww, sender, receiver, n)    # noqa: E731
+    gg = f(ggx, Y, W) + f(x, ggY, W) + f(x, Y, ggW)
+    gx = conv_bwd_x(desc, coef, g, ggY, W, sender, receiver, n) + conv_bwd_x(desc, coef, g, Y, ggW, sender, receiver, n)
+    gY = conv_bwd_y(desc, coef, ggx, g, W, sender, receiver) + conv_bwd_y(desc, coef, x, g, ggW, sender, receiver)
+    gW = conv_bwd_w(desc, coef, ggx, g, Y, sender, receiver) + conv_bwd_w(desc, coef, x, g, ggY, sender, receiver)
+    assert gY.shape == (E, desc['y_dim'])
+    return gg, gx, gY, gW
 
 
 def csr_by(index, n):

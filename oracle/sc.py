@@ -9,11 +9,14 @@ Restates in float64:
   * ``poly_table``     the symmetrised monomial table (reference symmetric.py:20-39): for every sorted index tuple,
                        the sum of U·W over all distinct orderings, by explicit permutation enumeration;
   * ``poly_eval``      evaluation of such a table and its derivative (reference symmetric.py:82-131).
+  * ``poly_jvp`` / ``poly_grad_jvp``  directional derivatives of the output and of the gradient (the second
+                       derivatives behind a double backward).
   * ``u_equivariance_error``  residual of the intertwiner identity of a U matrix under a random rotation, with the
                        rotation's representation taken from ``oracle.wigner``'s spherical harmonics.
 
 Pinned by (tests/test_oracle_sc.py): sc_dense == MACE's nested contraction on random U/W (a different evaluation
-order of the same sum); poly_eval(poly_table) == sc_dense; poly_eval derivative == autograd of sc_dense; U matrices
+order of the same sum); poly_eval(poly_table) == sc_dense; poly_eval derivative == autograd of sc_dense;
+poly_jvp == forward-mode autograd of sc_dense; poly_grad_jvp == double backward of sc_dense in torch; U matrices
 satisfy the intertwiner identity and have full column rank.
 """
 import itertools
@@ -87,6 +90,48 @@ def poly_grad(table, x, elem, g):
                 if q != pos:
                     rest = rest * x[:, :, j]
             gx[:, :, i] += s * rest
+    return gx
+
+
+def poly_jvp(table, x, elem, v):
+    """Directional derivative of poly_eval's output along v [b, c, n]: Σ over monomials and factor positions of the
+    coefficient times v at that position times the other factors.  It is the gradient of <ggx, poly_grad(g)> with
+    respect to g for ggx = v, which the reference's backward guard refuses (symmetric.py:147-149)."""
+    x, v = np.asarray(x, dtype=np.float64), np.asarray(v, dtype=np.float64)
+    elem = np.asarray(elem)
+    b, c, n = x.shape
+    M = next(iter(table.values())).shape[1]
+    out = np.zeros((b, c, M))
+    for key, coef in table.items():
+        dmono = np.zeros((b, c))
+        for pos, i in enumerate(key):
+            t = v[:, :, i].copy()
+            for q, j in enumerate(key):
+                if q != pos:
+                    t = t * x[:, :, j]
+            dmono += t
+        out += coef[elem].transpose(0, 2, 1) * dmono[:, :, None]
+    return out
+
+
+def poly_grad_jvp(table, x, elem, g, v):
+    """Directional derivative of poly_grad(x, g) along x + εv: for each monomial and each ordered pair of distinct
+    factor positions (p, q), the coefficient·g sum times v at q times the remaining factors, added at position p.
+    It is the gradient of <v, poly_grad(g)> with respect to x (a Hessian-vector product of <g, out>)."""
+    x, v = np.asarray(x, dtype=np.float64), np.asarray(v, dtype=np.float64)
+    elem = np.asarray(elem)
+    gx = np.zeros_like(x)
+    for key, coef in table.items():
+        s = (coef[elem].transpose(0, 2, 1) * g).sum(-1)                       # [b, c]
+        for p, i in enumerate(key):
+            for q in range(len(key)):
+                if q == p:
+                    continue
+                t = s * v[:, :, key[q]]
+                for r, j in enumerate(key):
+                    if r not in (p, q):
+                        t = t * x[:, :, j]
+                gx[:, :, i] += t
     return gx
 
 

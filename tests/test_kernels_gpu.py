@@ -786,6 +786,165 @@ def test_edge_geometry_only_while_a_patched_model_runs():
     assert not any(t.startswith('geom') for t, *_ in tm.records)
 
 
+@pytest.mark.parametrize('factored', [False, True])
+def test_conv_double_backward_vs_oracle(factored):
+    """Second derivatives through the convolution (patched with double_backward): the first-order gradients taken
+    with create_graph, contracted with random directions, and differentiated again with respect to g and every
+    input.  Against the oracle's conv_double_bwd (first-order formulas with substituted arguments, pinned by finite
+    differences).  Factored: the weights are W0 * cutoff (some cutoffs 0), which the convolution reads as its two
+    factors; the oracle side applies the product rule by hand."""
+    dev = _dev()
+    print(f'[case] conv double backward factored={factored}', flush=True)
+    tp = _tp('32x0e+32x1o', 2)
+    op = HipConvTP(tp, device=dev)
+    op.double_backward = True
+    desc = oconv.describe_tp(tp)
+    coef = oconv.path_terms(desc)
+    rng = np.random.default_rng(11)
+    n, e = 23, 300
+    s, r = _graph(rng, n, e)
+    nw = len(desc['ins']) * desc['mul']
+    x, Y, g = rng.normal(size=(n, desc['x_dim'])), rng.normal(size=(e, desc['y_dim'])), rng.normal(size=(n, desc['out_dim']))
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    xt, Yt, gt = t(x), t(Y), t(g)
+    if factored:
+        W0, cut = rng.normal(size=(e, nw)), rng.uniform(0.1, 1.0, size=(e, 1))
+        cut[::7] = 0.0
+        W0t, ct = t(W0), t(cut)
+        ins, Wt = (xt, Yt, W0t, ct), W0t * ct
+    else:
+        W = rng.normal(size=(e, nw))
+        Wt = t(W)
+        ins = (xt, Yt, Wt)
+    out = op(xt, Yt, Wt, ei)
+    firsts = torch.autograd.grad(out, ins, gt, create_graph=True)
+    dirs = [rng.normal(size=f.shape) for f in firsts]
+    sval = sum((f * torch.tensor(d, dtype=torch.float32, device=dev)).sum() for f, d in zip(firsts, dirs))
+    seconds = torch.autograd.grad(sval, (gt,) + ins)
+    if factored:
+        ggx, ggY, ggW0, ggc = dirs
+        og, ox, oY, oW = oconv.conv_double_bwd(desc, coef, x, Y, W0 * cut, g, ggx, ggY, ggW0 * cut + ggc * W0, s, r, n)
+        A = oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)
+        want = [og, ox, oY, oW * cut + ggc * A, (oW * W0).sum(1, keepdims=True) + (ggW0 * A).sum(1, keepdims=True)]
+    else:
+        want = oconv.conv_double_bwd(desc, coef, x, Y, W, g, *dirs, s, r, n)
+    for i, (got, w) in enumerate(zip(seconds, want)):
+        assert _rel(got.double().cpu().numpy(), w) < 1e-5, i
+    # the module as patched by default refuses, with the reference's message
+    op.double_backward = False
+    out = op(xt, Yt, Wt, ei)
+    with pytest.raises(RuntimeError, match='double backward'):
+        torch.autograd.grad(out, ins, gt, create_graph=True)
+
+
+def _sc_oracle_tables(sc):
+    tabs = []
+    for ct in sc.contractions:
+        U = {}
+        for nu in range(1, ct.correlation + 1):
+            u = getattr(ct, f'U_matrix_{nu}').double()
+            u = u if u.dim() == nu + 2 else u.unsqueeze(0)
+            U[nu] = u.reshape(u.shape[0], -1, u.shape[-1]).numpy()
+        Wd = {ct.correlation: ct.weights_max.detach().double().numpy()}
+        for j, w in enumerate(ct.weights):
+            Wd[ct.correlation - 1 - j] = w.detach().double().numpy()
+        tabs.append(osc.poly_table(U, Wd))
+    return tabs
+
+
+@pytest.mark.parametrize('layout', ['mace', 'irreps'])
+def test_sc_double_backward_vs_oracle(layout):
+    """Second derivatives through the symmetric contraction (the sc_jvp / sc_bwd2 kernels): d<v, gx>/dg and
+    d<v, gx>/dx against the oracle's directional derivatives, both layers of the config-2 model, on x as
+    [N, C, n_ell] and in e3nn's irreps layout; the C ABI's layout argument is checked on the host."""
+    from mace_hip_kernels import symmetric as hsym
+    dev = _dev()
+    model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(6)
+    for li, prod in enumerate(model.products):
+        print(f'[case] sc double backward layer {li} layout={layout}', flush=True)
+        sc = prod.symmetric_contractions
+        op = HipSymmetricContraction(sc, device=dev)
+        op.double_backward = True
+        sp = op.spec
+        n = 29
+        x, v = rng.normal(size=(n, sp.C, sp.n_ell)) * 0.7, rng.normal(size=(n, sp.C, sp.n_ell))
+        elem_np = rng.integers(0, 4, n)
+        g = rng.normal(size=(n, sp.out_dim))
+        attrs = torch.tensor(np.eye(4)[elem_np], dtype=torch.float32, device=dev)
+
+        def irreps(a):
+            parts, o = [], 0
+            for d in sp.dims:
+                parts.append(a[:, :, o:o + d].reshape(n, -1))
+                o += d
+            return np.concatenate(parts, axis=1)
+        lay = (lambda a: a) if layout == 'mace' else irreps
+        t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+        xt, gt = t(lay(x)), t(g)
+        if layout == 'mace':
+            out = op(xt, attrs)
+        else:
+            elem, order = hsym.element_order(attrs)
+            out = hsym._SCIrrepsFn.apply(xt, elem, order, op)
+        gx, = torch.autograd.grad(out, xt, gt, create_graph=True)
+        d_g, d_x = torch.autograd.grad((gx * torch.tensor(lay(v), dtype=torch.float32, device=dev)).sum(), (gt, xt))
+        want_g, want_x, off = [], np.zeros_like(x), 0
+        for tab in _sc_oracle_tables(sc):
+            M = next(iter(tab.values())).shape[1]
+            want_g.append(osc.poly_jvp(tab, x, elem_np, v).reshape(n, -1))
+            want_x += osc.poly_grad_jvp(tab, x, elem_np, g[:, off:off + sp.C * M].reshape(n, sp.C, M), v)
+            off += sp.C * M
+        assert _rel(d_g.double().cpu().numpy(), np.concatenate(want_g, axis=1)) < SC_TOL
+        assert _rel(d_x.double().cpu().numpy(), lay(want_x)) < SC_TOL
+    lib = _native.load()
+    m2 = op.second_module()
+    assert lib.mh_sc_jvp(m2.handle, None, None, None, None, None, 0, 2, None) != 0
+    assert b'layout' in lib.mh_last_error()
+
+
+def test_linear_double_backward():
+    """Node linears (o3.Linear and skip_tp) patched with double_backward: the input gradient does not depend on x,
+    and its derivative with respect to g along v is the map applied to v (checked against float64 runs of the
+    e3nn module); a linear readout head likewise."""
+    from mace_hip_kernels import HipReadout
+    dev = _dev()
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(8)
+    n = 301
+    for name in ('interactions.1.linear', 'interactions.0.skip_tp', 'products.0.linear'):
+        print(f'[case] linear double backward {name}', flush=True)
+        mod = m.get_submodule(name)
+        op = HipNodeLinear(mod, device=dev)
+        op.double_backward = True
+        s = op.spec
+        a = np.eye(s.V)[rng.integers(0, s.V, size=n)] if s.V else None
+        at = None if a is None else torch.tensor(a, dtype=torch.float32, device=dev)
+        xt = torch.tensor(rng.normal(size=(n, s.Din)), dtype=torch.float32, device=dev, requires_grad=True)
+        gt = torch.tensor(rng.normal(size=(n, s.Dout)), dtype=torch.float32, device=dev, requires_grad=True)
+        v = rng.normal(size=(n, s.Din))
+        gx, = torch.autograd.grad(op(xt, at), xt, gt, create_graph=True)
+        d_g, d_x = torch.autograd.grad((gx * torch.tensor(v, dtype=torch.float32, device=dev)).sum(), (gt, xt),
+                                       allow_unused=True)
+        m64 = copy.deepcopy(mod).double()
+        want = m64(torch.tensor(v), torch.tensor(a)) if s.V else m64(torch.tensor(v))
+        assert d_x is None
+        assert _rel(d_g.double().cpu().numpy(), want.detach().numpy()) < LIN_TOL
+    print('[case] linear readout double backward', flush=True)
+    ro = HipReadout(m.readouts[0], device=dev)
+    ro.double_backward = True
+    with pytest.raises(ValueError):
+        HipReadout(m.readouts[1], device=dev).double_backward = True
+    xt = torch.tensor(rng.normal(size=(n, ro.spec.Din)), dtype=torch.float32, device=dev, requires_grad=True)
+    gt = torch.tensor(rng.normal(size=(n, 1)), dtype=torch.float32, device=dev, requires_grad=True)
+    v = rng.normal(size=(n, ro.spec.Din))
+    gx, = torch.autograd.grad(ro(xt), xt, gt, create_graph=True)
+    d_g, = torch.autograd.grad((gx * torch.tensor(v, dtype=torch.float32, device=dev)).sum(), gt)
+    want = copy.deepcopy(m.readouts[0]).double()(torch.tensor(v))
+    assert _rel(d_g.double().cpu().numpy(), want.detach().numpy()) < LIN_TOL
+
+
 def test_kernels_match_golden_fixtures():
     """Kernels against the committed oracle fixtures (tests/golden/make_golden.py)."""
     import os

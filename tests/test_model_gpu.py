@@ -116,6 +116,48 @@ def test_double_backward_raises():
         torch.autograd.grad(f.sum(), batch['positions'])
 
 
+@pytest.mark.parametrize('config', ['l3_corr3_fullcg', 'l3_corr3_l2hidden'])
+def test_double_backward_hessian_and_force_loss(config):
+    """patch_model(double_backward=True): the convolutions, contractions, linears, layout changes and linear readout
+    heads differentiate twice; the modules without second-order kernels stay on e3nn and are reported.  Against the
+    unpatched model in float64: (1) a Hessian-vector product of the energy with respect to the positions,
+    d(F·v)/dx; (2) the gradients, with respect to every parameter the patch leaves in place, of a loss on energy
+    and forces computed with create_graph (MACE's training=True).  Tolerance: 1e-4 relative to the largest
+    reference component."""
+    dev = _dev()
+    print(f'[case] double backward {config}', flush=True)
+    model = factory.make_model(*factory.REF_CONFIGS[config])
+    ref = copy.deepcopy(model).to(dev, torch.float64)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    report = patch_model(met, verbose=False, double_backward=True)
+    core = _core(report)                             # convolutions and contractions; SH left on e3nn
+    assert core and not any(n.endswith('spherical_harmonics') for n in core), report
+    skipped = dict(report['skipped'])
+    assert 'double_backward' in skipped['spherical_harmonics'] and 'interactions.0.conv_tp_weights' in skipped
+    st = factory.make_structure(seed=4)
+    batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
+    v = np.random.default_rng(0).normal(size=(len(st), 3))
+    hv, grads = [], []
+    for m, dt in ((ref, torch.float64), (met, torch.float32)):
+        b = D.fresh(_to(batch, dev, dt))
+        out = m(b, compute_force=False, training=True)
+        f, = torch.autograd.grad(-out['energy'].sum(), b['positions'], create_graph=True)
+        h, = torch.autograd.grad((f * torch.tensor(v, dtype=dt, device=dev)).sum(), b['positions'])
+        hv.append(h.double().cpu().numpy())
+        m.zero_grad()
+        b = D.fresh(_to(batch, dev, dt))
+        out = m(b, compute_force=True, training=True)
+        loss = (out['energy'] ** 2).sum() + (out['forces'] ** 2).sum()
+        loss.backward()
+        grads.append({k: p.grad.double().cpu().numpy() for k, p in m.named_parameters() if p.grad is not None})
+    assert np.abs(hv[1] - hv[0]).max() < 1e-4 * np.abs(hv[0]).max()
+    common = sorted(set(grads[0]) & set(grads[1]))
+    assert any('conv_tp_weights' in k for k in common), common
+    for k in common:
+        scale = max(np.abs(grads[0][k]).max(), 1e-8)
+        assert np.abs(grads[1][k] - grads[0][k]).max() < 1e-4 * scale, k
+
+
 def test_unsupported_block_is_skipped():
     dev = _dev()
     print('[case] 48-channel model: convolutions skipped', flush=True)

@@ -112,6 +112,38 @@ def test_scalar_path_is_identity():
         assert all(abs(v - 1.0) < 1e-14 for *_, v in co['terms'])
 
 
+def test_double_backward_equals_finite_differences():
+    """conv_double_bwd (first-order formulas with substituted arguments) against central differences of
+    s = <ggx, gx> + <ggY, gY> + <ggW, gW> in each of g, x, Y, W, with the first-order formulas themselves pinned
+    against the unfused forward above.  s is linear in each argument, so differences are exact up to rounding."""
+    desc = oconv.describe_tp(_tp('2x0e+2x1o', 2))
+    coef = oconv.path_terms(desc)
+    rng = np.random.default_rng(5)
+    n, e = 4, 9
+    s, r, x, Y, W, g = _inputs(desc, rng, n, e)
+    ggx, ggY, ggW = rng.normal(size=x.shape), rng.normal(size=Y.shape), rng.normal(size=W.shape)
+
+    def sfun(g_, x_, Y_, W_):
+        return ((ggx * oconv.conv_bwd_x(desc, coef, g_, Y_, W_, s, r, n)).sum()
+                + (ggY * oconv.conv_bwd_y(desc, coef, x_, g_, W_, s, r)).sum()
+                + (ggW * oconv.conv_bwd_w(desc, coef, x_, g_, Y_, s, r)).sum())
+
+    args = [g, x, Y, W]
+    got = oconv.conv_double_bwd(desc, coef, x, Y, W, g, ggx, ggY, ggW, s, r, n)
+    h = 1e-3
+    for which, want_shape in enumerate((g.shape, x.shape, Y.shape, W.shape)):
+        fd = np.zeros(want_shape)
+        for idx in np.ndindex(want_shape):
+            p, m = [a.copy() for a in args], [a.copy() for a in args]
+            p[which][idx] += h
+            m[which][idx] -= h
+            fd[idx] = (sfun(*p) - sfun(*m)) / (2 * h)
+        assert np.abs(got[which] - fd).max() < 1e-8 * max(1.0, np.abs(fd).max()), which
+    # a direction left out (None) is a zero direction
+    part = oconv.conv_double_bwd(desc, coef, x, Y, W, g, ggx, None, None, s, r, n)
+    assert np.abs(part[1]).max() == 0.0 and np.abs(part[0]).max() > 0
+
+
 def test_planted_mistakes_are_caught():
     desc = oconv.describe_tp(_tp('4x0e+4x1o', 3))
     coef = oconv.path_terms(desc)

@@ -4,6 +4,7 @@ Pins of the symmetric-contraction oracle (CPU, float64).
 * dense Σ_ν U_ν·W_ν·x^⊗ν (oracle.sc.sc_dense) == MACE's nested contraction (mace_lite Contraction): two evaluation
   orders of the same polynomial;
 * the symmetrised monomial table evaluated as a polynomial == sc_dense, and its derivative == autograd of sc_dense;
+* the table's directional derivatives (output and gradient) == forward-mode and double-backward autograd of sc_dense;
 * the product's SCSpec table (what the kernel reads) == the oracle's table, term by term;
 * every U matrix satisfies the intertwiner identity U(D x, …, D x) = D_L U(x, …, x) with D from the spherical
   harmonics, and has full column rank; a planted mistake (one M row of U negated) breaks the identity.
@@ -71,6 +72,34 @@ def test_symmetrised_table_and_gradient(irreps_in, irrep_out, corr):
     g = rng.normal(size=dense.shape)
     dense.backward(torch.tensor(g))
     assert np.abs(osc.poly_grad(table, x, elem, g) - xt.grad.numpy()).max() < 1e-10
+
+
+@pytest.mark.parametrize('irreps_in,irrep_out,corr', CASES[:2] + CASES[3:4])
+def test_second_derivatives_equal_autograd(irreps_in, irrep_out, corr):
+    """poly_jvp == forward-mode derivative of sc_dense (torch.func.jvp); poly_grad_jvp == the x-gradient of
+    <v, d<g, out>/dx> by double backward through sc_dense.  A planted mistake (the pair loop of poly_grad_jvp
+    run over p == q too, i.e. a squared factor's second derivative counted with the wrong multiplicity) fails."""
+    ct = _contraction(irreps_in, irrep_out, corr)
+    rng = np.random.default_rng(2)
+    C, n = ct.num_features, Irreps(irreps_in).dim // ct.num_features
+    x, v = rng.normal(size=(6, C, n)), rng.normal(size=(6, C, n))
+    elem = rng.integers(0, 3, 6)
+    U, W = _uw(ct)
+    table = osc.poly_table({k: u.numpy() for k, u in U.items()}, {k: w.numpy() for k, w in W.items()})
+    _, tangent = torch.func.jvp(lambda t: osc.sc_dense(U, W, t, elem), (torch.tensor(x),), (torch.tensor(v),))
+    assert np.abs(osc.poly_jvp(table, x, elem, v) - tangent.numpy()).max() < 1e-10
+    g = rng.normal(size=tangent.shape)
+    xt = torch.tensor(x, requires_grad=True)
+    gx, = torch.autograd.grad(osc.sc_dense(U, W, xt, elem), xt, torch.tensor(g), create_graph=True)
+    hv, = torch.autograd.grad((gx * torch.tensor(v)).sum(), xt)
+    got = osc.poly_grad_jvp(table, x, elem, g, v)
+    assert np.abs(got - hv.numpy()).max() < 1e-10 * max(1.0, float(hv.abs().max()))
+    # planted: square terms counted once more (pairs p == q included with the factor itself as direction)
+    bad = got.copy()
+    key = max((k for k in table if len(set(k)) < len(k)), key=lambda k: np.abs(table[k]).max())
+    s_ = (table[key][elem].transpose(0, 2, 1) * g).sum(-1)
+    bad[:, :, key[0]] += s_ * v[:, :, key[0]]
+    assert np.abs(bad - hv.numpy()).max() > 1e-6
 
 
 def test_product_table_equals_oracle_table():
