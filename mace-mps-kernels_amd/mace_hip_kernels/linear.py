@@ -115,9 +115,9 @@ class LinSpec:
         self.pack_fwd = pack(self.out_blocks, self.terms, self.in_blocks, Wio, self.V)
         self.pack_bwd = pack(self.in_blocks, self.bterms, self.out_blocks,
                              {(o, i): np.ascontiguousarray(w.transpose(2, 1, 0)) for (i, o), w in Wio.items()}, self.V)
-        # the backward writes the input blocks with the same tiling: their multiplicities must tile too (a module
-        # whose input never needs a gradient, like the node embedding of one-hot attributes, can do without)
-        self.has_bwd = all(m % 16 == 0 for m, *_ in self.in_blocks)
+        # the tiled backward writes the input blocks with the same tiling: their multiplicities must tile too; the
+        # others (the node embedding of one-hot element attributes) get a plain one-thread-per-value backward
+        self.tiled_bwd = all(m % 16 == 0 for m, *_ in self.in_blocks)
 
     def apply(self, x, a=None):
         """float64 numpy application of the probed map (the patch-time structure check)."""
@@ -705,6 +705,53 @@ def use_bf16(spec, backward=False):
     return spec.V == 0 and (spec.Din if backward else spec.Dout) >= 1024
 
 
+SCALAR_BLOCK = 256
+
+
+def _scalar_nodes(spec):
+    """Nodes per workgroup of the plain backward (one thread per input value)."""
+    return max(1, SCALAR_BLOCK // spec.Din)
+
+
+def _kernel_scalar_bwd(spec):
+    """``lin_bwd`` for a module whose input multiplicities do not tile (the node embedding: one input per element):
+    one thread per (node, input value), reading the fp32 transposed weights Wt_io [mul_o, V', mul_i] directly,
+        gx[n, i, u, m] = alpha sum_o sum_w g[n, o, w, m] (sum_v attrs[n, v]) Wt_io[w, v, u].
+    Nothing here is on the energy-and-forces path (the engine never asks for this gradient there); a loss that
+    backpropagates into the one-hot attributes, as ``loss.backward()`` does, needs it."""
+    NB, VV = _scalar_nodes(spec), max(spec.V, 1)
+    L = [f'extern "C" __global__ __launch_bounds__({SCALAR_BLOCK}) void {spec.kname("lin_bwd")}('
+         'const float* __restrict__ g,',
+         '    const float* __restrict__ attrs, const float* __restrict__ Wt, float* __restrict__ gx, int N,',
+         '    const int* __restrict__ order, float alpha) {',
+         '  (void)order;',
+         f'  const int q0 = blockIdx.x * {NB};',
+         f'  for (int idx = threadIdx.x; idx < {NB * spec.Din}; idx += {SCALAR_BLOCK}) {{',
+         f'    const int n = q0 + idx / {spec.Din}, k = idx % {spec.Din};',
+         '    if (n >= N) break;',
+         f'    const float* gr = g + (size_t)n * {spec.Dout};',
+         '    float acc = 0.0f;']
+    for i, (mi, li, oi, _) in enumerate(spec.in_blocks):
+        d = 2 * li + 1
+        L += [f'    if (k >= {oi} && k < {oi + mi * d}) {{', f'      const int u = (k - {oi}) / {d}, m = (k - {oi}) % {d};']
+        for o, woff in spec.bterms[i]:
+            mo, lo, oo, _ = spec.out_blocks[o]
+            assert lo == li
+            if spec.V:
+                L += [f'      for (int w = 0; w < {mo}; ++w) {{',
+                      f'        const float gv = gr[{oo} + w * {d} + m];',
+                      f'        for (int v = 0; v < {spec.V}; ++v)',
+                      f'          acc = fmaf(gv * attrs[(size_t)n * {spec.V} + v], Wt[{woff} + (w * {VV} + v) * {mi} + u], '
+                      'acc);',
+                      '      }']
+            else:
+                L += [f'      for (int w = 0; w < {mo}; ++w)',
+                      f'        acc = fmaf(gr[{oo} + w * {d} + m], Wt[{woff} + w * {mi} + u], acc);']
+        L.append('    }')
+    L += [f'    gx[(size_t)n * {spec.Din} + k] = alpha * acc;', '  }', '}', '']
+    return L
+
+
 def source(spec):
     """HIP source of ``lin_fwd`` and ``lin_bwd`` for one module."""
     L = [_native.device_header(), '']
@@ -714,7 +761,9 @@ def source(spec):
     else:
         L += _kernel_f32(spec.kname('lin_fwd'), spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din,
                          spec.Dout)
-    if spec.has_bwd:
+    if not spec.tiled_bwd:
+        L += _kernel_scalar_bwd(spec)
+    else:
         if use_bf16(spec, backward=True):
             L += _kernel(spec.kname('lin_bwd'), spec.out_blocks, spec.in_blocks, spec.bterms, spec.V, spec.Dout,
                          spec.Din, spec.pack_bwd[1], spec.pack_bwd[2])
@@ -792,9 +841,6 @@ class _LinFn(torch.autograd.Function):
 def _lin_bwd(op, g, a2, order, scale, lead):
     """The input gradient L^T g [*lead, Din] of g [*lead, Dout] by the backward kernel."""
     s = op.spec
-    if not s.has_bwd:
-        raise NotImplementedError(f'mace_hip_kernels: {op.tag} has input multiplicities that the backward kernel '
-                                  'does not tile (multiples of 16 needed)')
     g2 = g.reshape(-1, s.Dout).contiguous()
     N = g2.shape[0]
     gx = torch.empty(N, s.Din, device=g.device, dtype=torch.float32)
@@ -839,13 +885,16 @@ class HipNodeLinear(torch.nn.Module):
             kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK,
                                             group(s.out_blocks, s.terms, s.in_blocks, use_bf16(s)),
                                             len(_grid_y(s.out_blocks)))}
-            if s.has_bwd:
+            if s.tiled_bwd:
                 kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK,
                                                group(s.in_blocks, s.bterms, s.out_blocks, use_bf16(s, True)),
                                                len(_grid_y(s.in_blocks)))
+            else:
+                kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), SCALAR_BLOCK, _scalar_nodes(s))
             self.module = _native.Module(code, kernels)
         # the bf16 family reads its weights as bf16 parts (int16 bit patterns), the fp32 family as float32
-        for name, bf16, pk, w in (('W', use_bf16(s), s.pack_fwd[0], s.W), ('Wt', use_bf16(s, True), s.pack_bwd[0], s.Wt)):
+        for name, bf16, pk, w in (('W', use_bf16(s), s.pack_fwd[0], s.W),
+                                  ('Wt', use_bf16(s, True) and s.tiled_bwd, s.pack_bwd[0], s.Wt)):
             buf = torch.from_numpy(pk.view(np.int16)) if bf16 else torch.tensor(w, dtype=torch.float32)
             self.register_buffer(name, buf.to(dev), persistent=False)
         for k in ('irreps_in', 'irreps_in1', 'irreps_in2', 'irreps_out'):

@@ -403,24 +403,23 @@ def test_node_linears_vs_float64(attrs_kind):
         if s.V:
             a = (np.eye(s.V)[rng.integers(0, s.V, size=n)] if attrs_kind == 'one_hot' else rng.normal(size=(n, s.V)))
         g = rng.normal(size=(n, s.Dout))
-        # every module whose input carries a gradient in the model has the backward kernel (the node embedding of
-        # one-hot attributes is the one without)
-        assert s.has_bwd == (not name.endswith('node_embedding.linear')), name
-        xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=s.has_bwd)
+        # every module but the node embedding of one-hot attributes has the tiled backward; that one has the plain
+        # one-thread-per-value kernel
+        assert s.tiled_bwd == (not name.endswith('node_embedding.linear')), name
+        xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
         at = None if a is None else torch.tensor(a, dtype=torch.float32, device=dev)
         out = op(xt, at)
         m64 = copy.deepcopy(mod).double()
         x64 = torch.tensor(x, requires_grad=True)
         ref = m64(x64, torch.tensor(a)) if s.V else m64(x64)
         assert _rel(out.detach().double().cpu().numpy(), ref.detach().numpy()) < LIN_TOL
-        if s.has_bwd:
-            gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
-            gr, = torch.autograd.grad(ref, x64, torch.tensor(g))
-            assert _rel(gx.double().cpu().numpy(), gr.numpy()) < LIN_TOL
+        gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
+        gr, = torch.autograd.grad(ref, x64, torch.tensor(g))
+        assert _rel(gx.double().cpu().numpy(), gr.numpy()) < LIN_TOL
         if attrs_kind == 'dense':
             continue
         # no nodes at all, and a leading batch shape
-        x0 = torch.zeros(0, s.Din, device=dev, requires_grad=s.has_bwd)
+        x0 = torch.zeros(0, s.Din, device=dev, requires_grad=True)
         o0 = op(x0, None if at is None else at[:0])
         assert o0.shape == (0, s.Dout)
         o2 = op(xt.detach()[:60].reshape(3, 20, s.Din), None if at is None else at[:60].reshape(3, 20, s.V))

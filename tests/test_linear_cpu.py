@@ -78,7 +78,7 @@ def test_generated_source_compiles():
         if name in ('interactions.1.linear', 'interactions.0.skip_tp', 'node_embedding.linear'):
             spec = linear.LinSpec(mod)
             assert len(_native.compile_source(linear.source(spec))) > 1000
-            assert spec.has_bwd == (name != 'node_embedding.linear')
+            assert spec.tiled_bwd == (name != 'node_embedding.linear')
 
 
 def test_reshape_permutation_matches_the_module():
