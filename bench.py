@@ -10,6 +10,7 @@ padded to 6,000 edges each), with every input already resident in HBM.  Timing f
 
 The JSON line also reports, all measured in this run:
   * ``e3nn_gpu``       the same model unpatched (the e3nn path restated in PyTorch) on the same GPU, and the speed-up;
+  * ``double_backward`` a force-loss step (second derivatives) patched with double_backward=True vs unpatched;
   * ``kernels``        per-kernel mean duration from HIP events recorded around each launch on its stream, during a
                        second (instrumented) pass of K calls, with algorithmic bytes/FLOPs, GB/s and TFLOP/s;
   * ``roofline``       the dominant kernel (largest total time per call) against the HBM roofline;
@@ -51,6 +52,25 @@ def _time_calls(model, batch, steps, warmup, sync):
         out = model(batch, compute_force=True)
     sync()
     return (time.perf_counter() - t0) / steps, out
+
+
+def _time_train(model, batch, steps, warmup, sync):
+    """Seconds per force-loss step: E and F with create_graph (MACE's training=True), the loss E^2 + |F|^2, and its
+    backward into the parameters, which differentiates the force computation (a double backward)."""
+    from mace_lite import data as D
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        out = model(D.fresh(batch), compute_force=True, training=True)
+        ((out['energy'] ** 2).sum() + (out['forces'] ** 2).sum()).backward()
+    for _ in range(warmup):
+        step()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    sync()
+    return (time.perf_counter() - t0) / steps
 
 
 def _kernel_table(met, batch, n_real_edges, summary):
@@ -393,6 +413,7 @@ def main():
     ap.add_argument('--cpu-steps', type=int, default=2)
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--no-e3nn', action='store_true')
+    ap.add_argument('--no-double-backward', action='store_true', help='skip the force-loss step timing')
     ap.add_argument('--no-graph', action='store_true', help='report the eager call instead of the captured one')
     a = ap.parse_args()
     if a.config is None:
@@ -503,6 +524,20 @@ def main():
         e3nn_res = dict(ms_per_call=round(dt_ref * 1e3, 3), calls_per_s=round(1.0 / dt_ref, 3),
                         speedup=round(dt_ref / dt, 2), speedup_eager=round(dt_ref / dt_eager, 2))
         _log(f'e3nn path on GPU: {dt_ref * 1e3:.3f} ms per call (x{dt_ref / dt:.1f})')
+
+    # force-loss step (second derivatives) with patch_model(double_backward=True), against the unpatched model
+    dbl = None
+    if not a.no_double_backward:
+        met2 = copy.deepcopy(model).to(dev)
+        rep2 = patch_model(met2, verbose=False, double_backward=True)
+        dt_tr = _time_train(met2, batch, max(3, a.steps // 4), 2, sync)
+        dbl = dict(step='E,F with create_graph; loss E^2+|F|^2; backward to parameters',
+                   patched=sorted(rep2['patched']), ms_per_step=round(dt_tr * 1e3, 3))
+        del met2
+        if not a.no_e3nn:
+            dt_tr_ref = _time_train(e3nn, batch, 2, 1, sync)
+            dbl.update(e3nn_ms_per_step=round(dt_tr_ref * 1e3, 3), speedup=round(dt_tr_ref / dt_tr, 2))
+        _log('double backward:', dbl)
     del e3nn
 
     cpu = None
@@ -550,6 +585,7 @@ def main():
                      'bytes_per_launch': d['bytes'], 'ms_per_launch': d['ms']},
         'kernels': kern,
         'e3nn_gpu': e3nn_res,
+        'double_backward': dbl,
         'parity': {'max_abs_dE_eV': dE, 'max_abs_dF_eV_per_A': dF},
         'cpu_baseline': cpu,
     }
