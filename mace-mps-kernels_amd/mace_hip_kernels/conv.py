@@ -459,16 +459,13 @@ class _ConvFn(torch.autograd.Function):
         if torch.is_grad_enabled():          # only true under create_graph=True
             if not op.double_backward:
                 raise RuntimeError(_DOUBLE_BACKWARD)
-            # the gradients as a differentiable function of (g, x, Y, W); the product W0 * cut and its rule are
-            # ordinary torch operations here
+            # the gradients as a differentiable function of (g, x, Y, W or W0 and cut)
             if ctx.factored:
-                c2 = cut.reshape(-1, 1)
-                W = W0 * c2
-            gx, gY, gW = _ConvAdjFn.apply(g, x, Y, W, edge_index, op, gr, (want_x, want_y, want_w))
-            if ctx.factored:
-                gW0 = gW * c2 if want_w0 else None
-                gc = (gW * W0).sum(-1).reshape(ctx.cut_shape) if want_cut else None
+                gx, gY, gW0, gc = _ConvAdjFn.apply(g, x, Y, None, W0, cut, edge_index, op, gr,
+                                                   (want_x, want_y, want_w0, want_cut))
                 return gx, gY, None, gW0, gc, None, None
+            gx, gY, gW, _ = _ConvAdjFn.apply(g, x, Y, W, None, None, edge_index, op, gr,
+                                             (want_x, want_y, want_w, False))
             return gx, gY, gW, None, None, None, None
         xc, Yc, gc_ = x.contiguous(), Y.contiguous(), g.contiguous()
         if ctx.factored:
@@ -480,58 +477,62 @@ class _ConvFn(torch.autograd.Function):
 
 
 class _ConvAdjFn(torch.autograd.Function):
-    """(gx, gY, gW): the first-order gradients of <g, conv(x, Y, W)> as a differentiable function of (g, x, Y, W),
-    for a double backward.  The convolution is linear in each of x, Y and W, so each second derivative is a
-    first-order quantity with one argument replaced by the incoming direction: with (ggx, ggY, ggW) the gradients
-    arriving for (gx, gY, gW),
+    """The first-order gradients of <g, conv(x, Y, W)> as a differentiable function of (g, x, Y, W), for a double
+    backward; with factored weights W = W0 * cut the inputs are (g, x, Y, W0, cut) and the outputs (gx, gY, gW0,
+    gcut).  The convolution is linear in each of x, Y and W (in each of x, Y, W0 and cut), so each second
+    derivative is a first-order quantity with one argument replaced by the direction arriving for it: with
+    (ggx, ggY, ggW) the gradients arriving for (gx, gY, gW),
         d/dg = conv(ggx, Y, W) + conv(x, ggY, W) + conv(x, Y, ggW),
         d/dx = gx(g; ggY, W) + gx(g; Y, ggW),  d/dY = gY(g; ggx, W) + gY(g; x, ggW),  d/dW = gW(g; ggx, Y) + gW(g; x, ggY),
-    computed by the same kernels (through this function and _ConvFn again, so higher orders follow).  ``want``
-    (x, Y, W) says which gradients to form; the others are returned as None."""
+    and likewise over four arguments when factored (e.g. d/dW0 gains gW(g; x, Y) * ggcut, the gradient of
+    <ggcut, gcut>).  Every term is one call of the same kernels (through this function and _ConvFn again, so higher
+    orders follow); factored, W0 * cut is never formed.  ``want`` (x, Y, W or W0, cut) says which gradients to
+    form; the others are returned as None."""
 
     @staticmethod
-    def forward(ctx, g, x, Y, W, edge_index, op, gr, want):
-        want_x, want_y, want_w = want
-        gx, gY, gW, _ = _conv_grads(op, gr, g.contiguous(), x.contiguous(), Y.contiguous(), W.contiguous(), None,
-                                    None, want_x, want_y or want_w)
-        ctx.save_for_backward(g, x, Y, W, edge_index)
-        ctx.op, ctx.gr = op, gr
-        return gx if want_x else None, gY if want_y else None, gW if want_w else None
+    def forward(ctx, g, x, Y, W, W0, cut, edge_index, op, gr, want):
+        wx, wy, ww, wc = want
+        factored = W is None
+        gx, gY, gW, gc = _conv_grads(op, gr, g.contiguous(), x.contiguous(), Y.contiguous(),
+                                     None if factored else W.contiguous(), W0.contiguous() if factored else None,
+                                     cut.reshape(-1).contiguous() if factored else None, wx, wy or ww or wc)
+        ctx.save_for_backward(g, x, Y, W, W0, cut, edge_index)
+        ctx.factored, ctx.op, ctx.gr = factored, op, gr
+        return (gx if wx else None, gY if wy else None, gW if ww else None,
+                gc.view(cut.shape) if wc and gc is not None else None)
 
     @staticmethod
-    def backward(ctx, ggx, ggY, ggW):
-        g, x, Y, W, edge_index = ctx.saved_tensors
+    def backward(ctx, ggx, ggY, ggW, ggc):
+        g, x, Y, W, W0, cut, edge_index = ctx.saved_tensors
         op, gr = ctx.op, ctx.gr
-        need_g, need_x, need_y, need_w = (_grad_needed(ctx, i) for i in range(4))
-        acc = [None, None, None, None]
+        need = [_grad_needed(ctx, i) for i in range(6)]          # g, x, Y, W, W0, cut
+        if ctx.factored:
+            args, dirs, slot = [x, Y, W0, cut], [ggx, ggY, ggW, ggc], [1, 2, 4, 5]
+        else:
+            args, dirs, slot = [x, Y, W], [ggx, ggY, ggW], [1, 2, 3]
+        acc = [None] * 6
 
         def add(i, t):
             if t is not None:
                 acc[i] = t if acc[i] is None else acc[i] + t
 
-        def conv(a, b, c):
-            return _ConvFn.apply(a, b, c, None, None, edge_index, op)
+        def split(a):                        # argument list -> (x, Y, W, W0, cut)
+            return (a[0], a[1], None, a[2], a[3]) if ctx.factored else (a[0], a[1], a[2], None, None)
 
-        if need_g:
-            if ggx is not None:
-                add(0, conv(ggx, Y, W))
-            if ggY is not None:
-                add(0, conv(x, ggY, W))
-            if ggW is not None:
-                add(0, conv(x, Y, ggW))
-        if ggY is not None and (need_x or need_w):            # Y -> ggY: gradients for x and W
-            a, _, c = _ConvAdjFn.apply(g, x, ggY, W, edge_index, op, gr, (need_x, False, need_w))
-            add(1, a)
-            add(3, c)
-        if ggW is not None and (need_x or need_y):            # W -> ggW: gradients for x and Y
-            a, b, _ = _ConvAdjFn.apply(g, x, Y, ggW, edge_index, op, gr, (need_x, need_y, False))
-            add(1, a)
-            add(2, b)
-        if ggx is not None and (need_y or need_w):            # x -> ggx: gradients for Y and W
-            _, b, c = _ConvAdjFn.apply(g, ggx, Y, W, edge_index, op, gr, (False, need_y, need_w))
-            add(2, b)
-            add(3, c)
-        return acc[0], acc[1], acc[2], acc[3], None, None, None, None
+        for j, d in enumerate(dirs):
+            if d is None:
+                continue
+            a = list(args)
+            a[j] = d
+            if need[0]:
+                add(0, _ConvFn.apply(*split(a), edge_index, op))
+            want = [need[slot[k]] and k != j for k in range(len(args))]
+            if any(want):
+                res = _ConvAdjFn.apply(g, *split(a), edge_index, op, gr, tuple(want + [False] * (4 - len(want))))
+                for k in range(len(args)):
+                    if k != j:
+                        add(slot[k], res[k])
+        return acc[0], acc[1], acc[2], acc[3], acc[4], acc[5], None, None, None, None
 
 
 class HipConvTP(torch.nn.Module):
