@@ -300,8 +300,12 @@ def _profile(a):
     dev = torch.device('cuda:0')
     model, batch_cpu, meta = factory.workload(a.config)
     met = model.to(dev)
-    patch_model(met, verbose=False)
+    patch_model(met, verbose=False, double_backward=a.profile_train)
     batch = D.fresh(_to(batch_cpu, dev))
+    if a.profile_train:                 # force-loss steps instead (second derivatives)
+        _time_train(met, batch, a.steps, a.warmup, torch.cuda.synchronize)
+        _log(f'profile run done: {meta["name"]}, {a.warmup + a.steps} force-loss steps')
+        return
     for _ in range(a.warmup + a.steps):
         met(batch, compute_force=True)
     # calibration: an elementwise kernel whose name occurs nowhere in the model (reads and writes COPY_BYTES)
@@ -396,6 +400,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--profile', action='store_true', help='patched calls + calibration copy only (for rocprofv3)')
+    ap.add_argument('--profile-train', action='store_true',
+                    help='with --profile: force-loss steps (patched with double_backward) instead of E+F calls')
     ap.add_argument('--summarize-rocprof', metavar='DIR', help='print a markdown summary of rocprofv3 output and exit')
     ap.add_argument('--pmc-fetch', metavar='DIR')
     ap.add_argument('--pmc-write', metavar='DIR')
