@@ -69,7 +69,12 @@ enum mh_kernel_kind {
     MH_SC_BWD2 = 30,     /* directional derivative of the x-gradient (a Hessian-vector product)     */
     MH_SC_JVP_I = 31,    /* MH_SC_JVP in the irreps layout                                          */
     MH_SC_BWD2_I = 32,   /* MH_SC_BWD2 in the irreps layout                                         */
-    MH_NUM_KINDS = 33
+    MH_CSR_FILL = 33,    /* graph build: zero the per-node counters (grid y = the two index rows)   */
+    MH_CSR_COUNT = 34,   /* int32 copy of the indices (clamped, flagged) and per-node edge counts   */
+    MH_CSR_SCAN = 35,    /* rowptr = exclusive scan of the counts (one workgroup per index row)     */
+    MH_CSR_SCATTER = 36, /* each edge into its node's segment (any order)                           */
+    MH_CSR_RANK = 37,    /* each segment's edges in increasing edge order                           */
+    MH_NUM_KINDS = 38
 };
 
 /* flags of mh_conv_bwd */
@@ -199,6 +204,18 @@ int mh_sc_jvp(mh_module* m, const float* X, const float* V, const int32_t* elem,
               int32_t N, int32_t layout, void* stream);
 int mh_sc_bwd2(mh_module* m, const float* X, const float* V, const int32_t* elem, const float* T, const float* G,
                float* GX, int32_t N, int32_t layout, void* stream);
+
+/* Both CSRs of an edge list in one call: edge_index [2, E] int64 (row 0 senders, row 1 receivers, contiguous) over
+ * n nodes.  Writes keys [2, E] int32 (the indices, clamped into [0, n)), rowptr [2, n + 1] int32 and eids [2, E] int32:
+ * row r lists the edges grouped by index r, node k's edges at eids[r, rowptr[r, k] .. rowptr[r, k + 1]) in
+ * increasing edge order (what a stable sort by the index gives).  *bad is set to 1 when an index was outside [0, n)
+ * and 0 otherwise.  work: 4 (n + 1) + 2 E int32 of caller-owned scratch.  Device work only (no host
+ * synchronisation, no memset), so it can be captured in a HIP graph; results do not depend on the order in which
+ * atomics land.  Bind MH_CSR_FILL / _COUNT / _SCATTER / _RANK with 256 threads and rows_per_block 256, MH_CSR_SCAN
+ * with 1024 threads and rows_per_block 1, all with grid y = 2 (mh_module_bind_grid).  Replaces the reference's
+ * csr_by (conv.py:229-235: a stable argsort per CSR and per layer, then a count). */
+int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys, int32_t* rowptr,
+                   int32_t* eids, int32_t* work, int32_t* bad, void* stream);
 
 /* Edge spherical harmonics Y[e, :] = Y_{0..l_max}(vec[e] / |vec[e]|) (vec [E, 3], Y [E, (l_max+1)^2]; e3nn's real
  * basis, y polar axis) and their backward gvec[e] = dL/dvec[e] from gY.  The kernels are generated per (l_max,

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 18; }
+int mh_version(void) { return 19; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -303,6 +303,36 @@ int mh_sc_bwd2(mh_module* m, const float* X, const float* V, const int32_t* elem
     if (layout != 0 && layout != 1) return fail(-1, "mh_sc_bwd2: layout must be 0 or 1");
     void* args[] = {&X, &V, &elem, &T, &G, &GX, &N};
     return launch(m, layout ? MH_SC_BWD2_I : MH_SC_BWD2, N, args, stream, "mh_sc_bwd2");
+}
+
+int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys, int32_t* rowptr,
+                   int32_t* eids, int32_t* work, int32_t* bad, void* stream) {
+    if (E < 0 || n < 0 || E >= 0x7fffffffLL || n >= 0x7fffffff) return fail(-1, "mh_graph_build: bad sizes");
+    if (E > 0 && n == 0) return fail(-1, "mh_graph_build: edges over zero nodes");
+    if (!rowptr || !work || !bad || (E > 0 && (!edge_index || !keys || !eids)))
+        return fail(-1, "mh_graph_build: NULL operand");
+    int32_t* cnt = work;                         // [2, n + 1]
+    int32_t* cursor = work + 2 * (int64_t)(n + 1);   // [2, n + 1]
+    int32_t* tmp = work + 4 * (int64_t)(n + 1);      // [2, E]
+    int rc;
+    {
+        void* args[] = {&cnt, &bad, &n};
+        if ((rc = launch(m, MH_CSR_FILL, (int64_t)n + 1, args, stream, "mh_graph_build"))) return rc;
+    }
+    {
+        void* args[] = {&edge_index, &keys, &cnt, &bad, &E, &n};
+        if ((rc = launch(m, MH_CSR_COUNT, E, args, stream, "mh_graph_build"))) return rc;
+    }
+    {
+        void* args[] = {&cnt, &rowptr, &cursor, &n};
+        if ((rc = launch(m, MH_CSR_SCAN, 1, args, stream, "mh_graph_build"))) return rc;
+    }
+    {
+        void* args[] = {&keys, &cursor, &tmp, &E, &n};
+        if ((rc = launch(m, MH_CSR_SCATTER, E, args, stream, "mh_graph_build"))) return rc;
+    }
+    void* args[] = {&keys, &rowptr, &tmp, &eids, &E, &n};
+    return launch(m, MH_CSR_RANK, E, args, stream, "mh_graph_build");
 }
 
 int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream) {

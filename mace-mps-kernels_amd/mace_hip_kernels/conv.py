@@ -160,60 +160,152 @@ class ConvSpec:
 
 
 # ------------------------------------------------------------------------------------------- graph cache
-def csr_by(index, n):
-    """Edges sorted by ``index`` → (rowptr[n+1], edge ids) as int32 (reference conv.py:229-235).  Stable sort, then
-    rowptr[k] = number of keys below k by binary search of the sorted keys: device work only, no host
-    synchronisation, so it can be captured in a HIP graph."""
-    order = torch.argsort(index, stable=True)
-    keys = index[order]
-    rowptr = torch.searchsorted(keys, torch.arange(n + 1, device=index.device, dtype=keys.dtype))
-    return rowptr.to(torch.int32), order.to(torch.int32)
+def graph_source():
+    """HIP source of the graph-build kernels behind ``mh_graph_build`` (both CSRs of an edge list, device work only).
+    Each kernel handles one index row per grid row (blockIdx.y: 0 senders, 1 receivers).  Segments are filled in
+    whatever order the atomics land and then ordered by edge id, so the result is what a stable sort by the index
+    gives (reference conv.py:229-235) and never depends on timing.  Ordering a segment of L edges costs L^2 reads
+    (each edge counts the smaller ids in its segment): ~40 per segment for MACE graphs."""
+    return _native.device_header() + r"""
+extern "C" __global__ __launch_bounds__(256) void csr_fill(int* __restrict__ cnt, int* __restrict__ bad, int n) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i <= n) cnt[(long long)blockIdx.y * (n + 1) + i] = 0;
+  if (i == 0 && blockIdx.y == 0) bad[0] = 0;
+}
+
+extern "C" __global__ __launch_bounds__(256) void csr_count(const long long* __restrict__ index, int* __restrict__ keys,
+    int* __restrict__ cnt, int* __restrict__ bad, long long E, int n) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= E) return;
+  const long long r = blockIdx.y;
+  long long k = index[r * E + e];
+  if (k < 0 || k >= n) {                  // flagged for the caller; clamped so that nothing reads out of range
+    atomicOr(bad, 1);
+    k = k < 0 ? 0 : n - 1;
+  }
+  keys[r * E + e] = (int)k;
+  atomicAdd(&cnt[r * (n + 1) + k], 1);
+}
+
+extern "C" __global__ __launch_bounds__(1024) void csr_scan(const int* __restrict__ cnt, int* __restrict__ rowptr,
+    int* __restrict__ cursor, int n) {
+  const long long r = blockIdx.y;
+  __shared__ int s[1024];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (long long base = 0; base <= n; base += 1024) {
+    const long long i = base + threadIdx.x;
+    const int v = i < n ? cnt[r * (n + 1) + i] : 0;
+    s[threadIdx.x] = v;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {       // inclusive scan of the chunk
+      const int t = threadIdx.x >= off ? s[threadIdx.x - off] : 0;
+      __syncthreads();
+      s[threadIdx.x] += t;
+      __syncthreads();
+    }
+    const int excl = carry + s[threadIdx.x] - v;
+    if (i <= n) {
+      rowptr[r * (n + 1) + i] = excl;
+      cursor[r * (n + 1) + i] = excl;
+    }
+    __syncthreads();
+    if (threadIdx.x == 1023) carry += s[1023];
+    __syncthreads();
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void csr_scatter(const int* __restrict__ keys, int* __restrict__ cursor,
+    int* __restrict__ tmp, long long E, int n) {
+  const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (e >= E) return;
+  const long long r = blockIdx.y;
+  const int pos = atomicAdd(&cursor[r * (n + 1) + keys[r * E + e]], 1);
+  tmp[r * E + pos] = (int)e;
+}
+
+extern "C" __global__ __launch_bounds__(256) void csr_rank(const int* __restrict__ keys, const int* __restrict__ rowptr,
+    const int* __restrict__ tmp, int* __restrict__ eids, long long E, int n) {
+  const long long p = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (p >= E) return;
+  const long long r = blockIdx.y;
+  const int e = tmp[r * E + p];
+  const int k = keys[r * E + e];
+  const int b = rowptr[r * (n + 1) + k], t = rowptr[r * (n + 1) + k + 1];
+  int rank = 0;
+  for (int q = b; q < t; ++q) rank += tmp[r * E + q] < e;
+  eids[r * E + b + rank] = e;
+}
+"""
+
+
+_GRAPH_MODULES = {}        # device index -> module of the graph-build kernels
+
+
+def _graph_module(device):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    m = _GRAPH_MODULES.get(idx)
+    if m is None:
+        code = _native.compile_source(graph_source())
+        with torch.cuda.device(idx):
+            m = _native.Module(code, {_native.MH_CSR_FILL: ('csr_fill', 256, 256, 2),
+                                      _native.MH_CSR_COUNT: ('csr_count', 256, 256, 2),
+                                      _native.MH_CSR_SCAN: ('csr_scan', 1024, 1, 2),
+                                      _native.MH_CSR_SCATTER: ('csr_scatter', 256, 256, 2),
+                                      _native.MH_CSR_RANK: ('csr_rank', 256, 256, 2)})
+        _GRAPH_MODULES[idx] = m
+    return m
+
+
+def build_graph(edge_index, n):
+    """(keys [2, E], rowptr [2, n + 1], eids [2, E], bad [1]) of an edge list on the GPU (``mh_graph_build``): the
+    int32 senders and receivers clamped into [0, n), both CSRs, and a flag set when an index was out of range."""
+    ei = edge_index if edge_index.dtype == torch.int64 else edge_index.to(torch.int64)
+    ei = ei.contiguous()
+    E = ei.shape[1]
+    if E > 0 and n == 0:
+        raise ValueError('edge_index has edges but there are no nodes')
+    if E >= 2 ** 31 or n >= 2 ** 31 - 1:
+        raise ValueError('graph too large for int32 indices')
+    dev = ei.device
+    keys = torch.empty(2, E, device=dev, dtype=torch.int32)
+    rowptr = torch.empty(2, n + 1, device=dev, dtype=torch.int32)
+    eids = torch.empty(2, E, device=dev, dtype=torch.int32)
+    work = torch.empty(4 * (n + 1) + 2 * E, device=dev, dtype=torch.int32)
+    bad = torch.empty(1, device=dev, dtype=torch.int32)
+    P = _native.ptr
+    _native.launch('graph_build', _native.load().mh_graph_build, _graph_module(dev).handle, P(ei), E, n, P(keys),
+                   P(rowptr), P(eids), P(work), P(bad), _native.stream_of(ei))
+    return keys, rowptr, eids, bad
 
 
 class _Graph:
-    """int32 senders/receivers and both CSRs of one edge_index, built lazily and shared by every layer of a call.
+    """int32 senders/receivers and both CSRs of one edge_index (``build_graph``), shared by every layer of a call.
 
-    ``validate=False`` (a graph first met inside a HIP graph capture, which cannot synchronise to check it): the
-    indices are clamped into [0, n) instead of checked, so a bad edge list gives wrong numbers, never an out-of-range
-    access; both CSRs are built at once, inside the capture."""
+    ``validate=False`` (a graph first met inside a HIP graph capture, which cannot synchronise to check it): out of
+    range indices are clamped into [0, n) without a check, so a bad edge list gives wrong numbers, never an
+    out-of-range access."""
 
     def __init__(self, edge_index, n, validate=True):
         if edge_index.dim() != 2 or edge_index.shape[0] != 2:
             raise ValueError(f'edge_index must be [2, E], got {tuple(edge_index.shape)}')
-        if validate and edge_index.numel():
-            # the kernels index x, g and the CSRs with these values: reject out-of-range nodes on the host
-            lo, hi = torch.aminmax(edge_index)
-            lo, hi = int(lo), int(hi)
-            if lo < 0 or hi >= n:
-                raise ValueError(f'edge_index holds node {lo if lo < 0 else hi} outside [0, {n})')
         self.n = n
-        ei = edge_index if validate else edge_index.clamp(0, max(n - 1, 0))
-        self.send = ei[0].to(torch.int32).contiguous()
-        self.recv = ei[1].to(torch.int32).contiguous()
-        self._by_recv = self._by_send = None
-        self._ei = ei
-        self._validated = validate
-        if not validate:
-            self._by_recv = csr_by(self.recv, n)
-            self._by_send = csr_by(self.send, n)
+        keys, rowptr, eids, bad = build_graph(edge_index, n)
+        if validate and edge_index.shape[1] and int(bad.item()):
+            # the kernels index x, g and the CSRs with these values: out-of-range nodes are an error
+            lo, hi = (int(v) for v in torch.aminmax(edge_index))
+            raise ValueError(f'edge_index holds node {lo if lo < 0 else hi} outside [0, {n})')
+        self.send, self.recv = keys[0], keys[1]
+        self._by_send = (rowptr[0], eids[0])
+        self._by_recv = (rowptr[1], eids[1])
+        self._keep = (keys, rowptr, eids)
 
     def by_recv(self):
-        if self._by_recv is None:
-            self._check_not_capturing()
-            self._by_recv = csr_by(self._ei[1], self.n)
         return self._by_recv
 
     def by_send(self):
-        if self._by_send is None:
-            self._check_not_capturing()
-            self._by_send = csr_by(self._ei[0], self.n)
         return self._by_send
-
-    @staticmethod
-    def _check_not_capturing():
-        if _native.capturing():
-            raise RuntimeError('mace_hip_kernels: a CSR of this graph is first needed inside a HIP graph capture; '
-                               'warm up with the same call (forward and backward) before capturing')
 
 
 _graph_cache = []          # [(weakref(edge_index), version, n, _Graph)], most recent first

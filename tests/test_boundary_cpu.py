@@ -82,7 +82,19 @@ def test_block_conv_fusion_detection():
     assert not mhk._block_has_conv_fusion(torch.nn.Linear(2, 2))
 
 
-def test_graph_cache_and_validation():
+def _oracle_build(edge_index, n):
+    """CPU stand-in for the GPU graph build (conv.build_graph) from the oracle's CSR, so that the cache and
+    validation logic around it runs here; the GPU build itself is checked against the same oracle on the GPU."""
+    ei = edge_index.to(torch.int64)
+    bad = torch.tensor([int(bool(((ei < 0) | (ei >= n)).any()))], dtype=torch.int32)
+    k = ei.clamp(0, max(n - 1, 0)).to(torch.int32)
+    rows = [oconv.csr_by(k[r].numpy(), n) for r in range(2)]
+    return (k, torch.stack([torch.tensor(rp) for rp, _ in rows]), torch.stack([torch.tensor(e) for _, e in rows]),
+            bad)
+
+
+def test_graph_cache_and_validation(monkeypatch):
+    monkeypatch.setattr(conv, 'build_graph', _oracle_build)
     conv.clear_graph_cache()
     ei = torch.tensor([[0, 1, 2, 2], [1, 2, 0, 1]])
     g1 = conv.graph_for(ei, 3)
@@ -99,6 +111,10 @@ def test_graph_cache_and_validation():
         conv.graph_for(torch.tensor([[0, 5], [1, 0]]), 3)
     with pytest.raises(ValueError):
         conv.graph_for(torch.tensor([0, 1, 2]), 3)
+
+
+def test_graph_build_source_compiles():
+    assert _native.compile_source(conv.graph_source())[:4] == b'\x7fELF'
 
 
 def test_golden_fixtures_reproduce():

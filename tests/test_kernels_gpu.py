@@ -165,7 +165,8 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
                                                   (n, desc['out_dim'])))
     xt, Yt, Wt, gt = f(x), f(Y), f(W), f(g)
     st, rt = torch.tensor(s, dtype=torch.int32, device=dev), torch.tensor(r, dtype=torch.int32, device=dev)
-    rowptr_s, eids_s = hconv.csr_by(torch.tensor(s, device=dev), n)
+    _, rowptr2, eids2, _ = hconv.build_graph(torch.tensor(np.stack([s, r]), device=dev), n)
+    rowptr_s, eids_s = rowptr2[0], eids2[0]
     lib, P, st_ = _native.load(), _native.ptr, _native.stream_of(xt)
     gx = torch.zeros_like(xt)
     _native.check(lib.mh_conv_bwd_x(op.module.handle, P(gt), P(Yt), P(Wt), P(rowptr_s), P(eids_s), P(rt), P(gx), n,
@@ -181,7 +182,7 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
     assert _rel(gW.double().cpu().numpy(), oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)) < CONV_TOL
     assert _rel(gY.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
     # receiver-ordered backward through its own entry point (dX via per-edge messages)
-    rowptr_r, eids_r = hconv.csr_by(torch.tensor(r, device=dev), n)
+    rowptr_r, eids_r = rowptr2[1], eids2[1]
     gW3, gY3, gx3 = torch.zeros_like(Wt), torch.zeros_like(Yt), torch.zeros_like(xt)
     work = torch.empty(e, desc['x_dim'], device=dev)
     _native.check(lib.mh_conv_bwd_recv(op.module.handle, P(xt), P(gt), P(Yt), P(Wt), P(rowptr_r), P(eids_r), P(st),
@@ -201,6 +202,41 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
     # different kernels (per-edge vs fused): same formulas, possibly different fp32 contraction order
     assert _rel(gW2.double().cpu().numpy(), gW.double().cpu().numpy()) < 1e-6
     assert _rel(gY2.double().cpu().numpy(), gY.double().cpu().numpy()) < 1e-6
+
+
+def test_graph_build_vs_oracle():
+    """Both CSRs of an edge list built on the GPU (mh_graph_build) against the oracle's stable-argsort CSR: random
+    multigraphs with isolated nodes, a node with 300 edges, one node, no edges; bitwise the same on a second run;
+    out-of-range indices flagged (and rejected by the graph cache) or, unvalidated, clamped."""
+    dev = _dev()
+    rng = np.random.default_rng(12)
+    cases = [(37, 900), (2533, 96000), (1, 5), (50, 0), (5000, 300)]
+    for n, e in cases:
+        print(f'[case] graph build n={n} e={e}', flush=True)
+        s, r = (rng.integers(0, n, e) for _ in range(2))
+        if e >= 900:
+            r[:300] = n // 2                     # a long segment
+        ei = torch.tensor(np.stack([s, r]), device=dev)
+        keys, rowptr, eids, bad = hconv.build_graph(ei, n)
+        keys2, rowptr2, eids2, _ = hconv.build_graph(ei, n)
+        torch.cuda.synchronize()
+        assert int(bad.item()) == 0
+        for row, idx in enumerate((s, r)):
+            rp_o, ei_o = oconv.csr_by(idx, n)
+            assert np.array_equal(rowptr[row].cpu().numpy(), rp_o), (n, e, row)
+            assert np.array_equal(eids[row].cpu().numpy(), ei_o), (n, e, row)
+            assert np.array_equal(keys[row].cpu().numpy(), idx)
+        assert torch.equal(rowptr, rowptr2) and torch.equal(eids, eids2) and torch.equal(keys, keys2)
+    print('[case] graph build out of range', flush=True)
+    ei = torch.tensor([[0, 1, 7, 2], [1, -1, 0, 2]], device=dev)
+    keys, rowptr, eids, bad = hconv.build_graph(ei, 3)
+    assert int(bad.item()) == 1 and keys.min() >= 0 and keys.max() <= 2
+    with pytest.raises(ValueError, match='outside'):
+        hconv._Graph(ei, 3)
+    gr = hconv._Graph(ei, 3, validate=False)
+    assert gr.send.tolist() == [0, 1, 2, 2] and gr.recv.tolist() == [1, 0, 0, 2]
+    with pytest.raises(ValueError):
+        hconv.build_graph(ei, 0)
 
 
 def test_conv_deterministic_and_empty():
