@@ -30,6 +30,7 @@ import numpy as np
 import torch
 
 from . import _native
+from .symmetric import element_order
 from .pending import Pending
 
 KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
@@ -814,7 +815,10 @@ class _LinFn(torch.autograd.Function):
                 raise TypeError('node attributes must be float32 on the input\'s device')
             a2 = attrs.reshape(-1, s.V).contiguous()
         out = torch.empty(N, s.Dout, device=x.device, dtype=torch.float32)
-        order = node_order(a2) if a2 is not None and N > 0 else None
+        order = None
+        if a2 is not None and N > 0:
+            # MACE's node_attrs is also what the symmetric contraction sorts by element: share that order
+            order = element_order(attrs)[1] if attrs.dim() == 2 else node_order(a2)
         _native.launch(f'lin_fwd[{op.tag}]', _native.load().mh_lin_fwd, op.module.handle, _native.ptr(x2),
                        _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), _native.ptr(order), scale, N,
                        _native.stream_of(x2))
