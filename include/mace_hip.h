@@ -74,7 +74,11 @@ enum mh_kernel_kind {
     MH_CSR_SCAN = 35,    /* rowptr = exclusive scan of the counts (one workgroup per index row)     */
     MH_CSR_SCATTER = 36, /* each edge into its node's segment (any order)                           */
     MH_CSR_RANK = 37,    /* each segment's edges in increasing edge order                           */
-    MH_NUM_KINDS = 38
+    MH_SH_JVP = 38,      /* edge spherical harmonics: derivative along a direction of the vectors   */
+    MH_SH_BWD2 = 39,     /* derivative of their vector gradient along that direction                */
+    MH_EMB_JVP = 40,     /* radial embedding: derivative along a direction of the lengths           */
+    MH_EMB_BWD2 = 41,    /* derivative of its length gradient along that direction                  */
+    MH_NUM_KINDS = 42
 };
 
 /* flags of mh_conv_bwd */
@@ -223,6 +227,24 @@ int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n
  * o3.SphericalHarmonics(normalize=True), which these replace in the model's forward (edge vectors -> edge attrs). */
 int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream);
 int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int64_t E, void* stream);
+
+/* Second derivatives of the edge spherical harmonics, behind a double backward (dvec [E, 3] a direction):
+ * mh_sh_jvp writes dY = (dY/dvec) dvec [E, (l_max+1)^2], the gradient of <dvec, dL/dvec> with respect to gY;
+ * mh_sh_bwd2 writes the derivative of mh_sh_bwd's gvec along dvec for the given gY (a Hessian-vector product of
+ * <gY, Y>), the gradient of <dvec, dL/dvec> with respect to vec.  The first-order statements run on dual numbers.
+ * Bind MH_SH_JVP / MH_SH_BWD2 with 256 threads and 256 edges per block.  No reference counterpart (the reference
+ * leaves the harmonics on e3nn and raises on a double backward). */
+int mh_sh_jvp(mh_module* m, const float* vec, const float* dvec, float* dY, int64_t E, void* stream);
+int mh_sh_bwd2(mh_module* m, const float* vec, const float* dvec, const float* gY, float* gvec, int64_t E,
+               void* stream);
+
+/* The same for the radial embedding (dlen [E] a direction of the lengths): mh_emb_jvp writes the derivatives of the
+ * features [E, n] and of the cutoff [E] along dlen; mh_emb_bwd2 the derivative of mh_emb_bwd's glen along dlen for
+ * the given gfeats and gcutoff (gcutoff may be NULL).  Bind MH_EMB_JVP / MH_EMB_BWD2 like MH_EMB_*. */
+int mh_emb_jvp(mh_module* m, const float* len, const float* dlen, float* dfeats, float* dcutoff, int64_t E,
+               void* stream);
+int mh_emb_bwd2(mh_module* m, const float* len, const float* dlen, const float* gfeats, const float* gcutoff,
+                float* glen, int64_t E, void* stream);
 
 /* Node-wise equivariant linear out[n] = L(x[n], attrs[n]) for N nodes (x [N, Din], out [N, Dout], fp32, the e3nn
  * irreps layout [.., u * (2l+1) + m] per block).  Without attrs (attrs NULL) it is e3nn's o3.Linear:

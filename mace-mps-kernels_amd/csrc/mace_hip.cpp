@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 19; }
+int mh_version(void) { return 20; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -343,6 +343,33 @@ int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream)
 int mh_sh_bwd(mh_module* m, const float* vec, const float* gY, float* gvec, int64_t E, void* stream) {
     void* args[] = {&vec, &gY, &gvec, &E};
     return launch(m, MH_SH_BWD, E, args, stream, "mh_sh_bwd");
+}
+
+int mh_sh_jvp(mh_module* m, const float* vec, const float* dvec, float* dY, int64_t E, void* stream) {
+    if (E > 0 && (!vec || !dvec || !dY)) return fail(-1, "mh_sh_jvp: NULL operand");
+    void* args[] = {&vec, &dvec, &dY, &E};
+    return launch(m, MH_SH_JVP, E, args, stream, "mh_sh_jvp");
+}
+
+int mh_sh_bwd2(mh_module* m, const float* vec, const float* dvec, const float* gY, float* gvec, int64_t E,
+               void* stream) {
+    if (E > 0 && (!vec || !dvec || !gY || !gvec)) return fail(-1, "mh_sh_bwd2: NULL operand");
+    void* args[] = {&vec, &dvec, &gY, &gvec, &E};
+    return launch(m, MH_SH_BWD2, E, args, stream, "mh_sh_bwd2");
+}
+
+int mh_emb_jvp(mh_module* m, const float* len, const float* dlen, float* dfeats, float* dcutoff, int64_t E,
+               void* stream) {
+    if (E > 0 && (!len || !dlen || !dfeats || !dcutoff)) return fail(-1, "mh_emb_jvp: NULL operand");
+    void* args[] = {&len, &dlen, &dfeats, &dcutoff, &E};
+    return launch(m, MH_EMB_JVP, E, args, stream, "mh_emb_jvp");
+}
+
+int mh_emb_bwd2(mh_module* m, const float* len, const float* dlen, const float* gfeats, const float* gcutoff,
+                float* glen, int64_t E, void* stream) {
+    if (E > 0 && (!len || !dlen || !gfeats || !glen)) return fail(-1, "mh_emb_bwd2: NULL operand");
+    void* args[] = {&len, &dlen, &gfeats, &gcutoff, &glen, &E};
+    return launch(m, MH_EMB_BWD2, E, args, stream, "mh_emb_bwd2");
 }
 
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,

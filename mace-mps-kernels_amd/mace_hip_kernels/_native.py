@@ -8,6 +8,7 @@ verifies that.  There is no fallback: a missing or broken library raises.
 import ctypes
 import hashlib
 import os
+import re
 import threading
 
 import torch
@@ -20,9 +21,10 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_SC_BWD_G, MH_CONV_BWD_RC, MH_CONV_FWD_C, MH_SH_FWD, MH_SH_BWD, MH_LIN_FWD, MH_LIN_BWD, \
     MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD, \
     MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI, MH_READOUT_FWD, MH_READOUT_BWD, MH_SC_JVP, MH_SC_BWD2, \
-    MH_SC_JVP_I, MH_SC_BWD2_I, MH_CSR_FILL, MH_CSR_COUNT, MH_CSR_SCAN, MH_CSR_SCATTER, MH_CSR_RANK = range(38)
+    MH_SC_JVP_I, MH_SC_BWD2_I, MH_CSR_FILL, MH_CSR_COUNT, MH_CSR_SCAN, MH_CSR_SCATTER, MH_CSR_RANK, MH_SH_JVP, \
+    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2 = range(42)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -71,6 +73,10 @@ _SIGS = {
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
     'mh_sc_jvp': (ctypes.c_int, [_P] * 6 + [_I, _I, _P]),
     'mh_graph_build': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 5),
+    'mh_sh_jvp': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
+    'mh_sh_bwd2': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
+    'mh_emb_jvp': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
+    'mh_emb_bwd2': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
     'mh_sc_bwd2': (ctypes.c_int, [_P] * 7 + [_I, _I, _P]),
     'mh_sc_bwd': (ctypes.c_int, [_P] * 6 + [_I, _P]),
 }
@@ -112,6 +118,17 @@ def check(rc, what=''):
 def device_header():
     with open(DEVICE_HEADER) as f:
         return f.read()
+
+
+def dual_header():
+    """Forward-mode dual numbers (``mh_dual``) for the second-order kernels."""
+    with open(os.path.join(os.path.dirname(DEVICE_HEADER), 'mh_dual.h')) as f:
+        return f.read()
+
+
+def dualize(lines):
+    """C statements with every ``float`` declared as ``mh_dual`` (the same arithmetic carried on dual numbers)."""
+    return [re.sub(r'\bfloat\b', 'mh_dual', l) for l in lines]
 
 
 def compile_source(source):

@@ -171,9 +171,44 @@ def source(spec):
     return '\n'.join(L)
 
 
+def source_second(spec):
+    """HIP source of the second-order kernels behind a double backward: the statements of ``sh_fwd`` / ``sh_bwd`` on
+    dual numbers (``mh_dual``) with the edge vectors carrying a direction dv.  ``sh_jvp`` writes dY = (dY/dv) dv;
+    ``sh_bwd2`` writes the derivative of the vector gradient along dv for a fixed gY (a Hessian-vector product of
+    <gY, Y>)."""
+    m = math_lines(spec)
+    ind = lambda lines: ['  ' + l for l in lines]  # noqa: E731
+    head = ['  const long long e = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * BLOCK + threadIdx.x;',
+            '  if (e >= E) return;',
+            '  const mh_dual vx(vec[3 * e], dv[3 * e]), vy(vec[3 * e + 1], dv[3 * e + 1]), '
+            'vz(vec[3 * e + 2], dv[3 * e + 2]);'] + ind(_native.dualize(m['head']))
+    L = [_native.device_header(), _native.dual_header(), f'#define BLOCK {BLOCK}', f'#define DIM {spec.dim}']
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sh_jvp")}(',
+          '    const float* __restrict__ vec, const float* __restrict__ dv, float* __restrict__ dY, long long E) {']
+    L += head + ind(_native.dualize(m['fwd']))
+    L += ['  float* __restrict__ ye = dY + e * DIM;'] + [f'  ye[{c}] = Y{c}.d;' for c in range(spec.dim)] + ['}', '']
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("sh_bwd2")}(',
+          '    const float* __restrict__ vec, const float* __restrict__ dv, const float* __restrict__ gY,',
+          '    float* __restrict__ gv, long long E) {']
+    L += head
+    L += ['  const float* __restrict__ ge = gY + e * DIM;'] + [f'  const float g{c} = ge[{c}];' for c in range(spec.dim)]
+    L += ind(_native.dualize(m['bwd']))
+    L += ['  gv[3 * e] = ox.d; gv[3 * e + 1] = oy.d; gv[3 * e + 2] = oz.d;', '}', '']
+    return '\n'.join(L)
+
+
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by this HIP module; patch_model(model, '
-                    'double_backward=True) leaves it on e3nn')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
+
+
+def _sh_bwd(op, vec, g):
+    v = vec.reshape(-1, 3).contiguous()
+    g = g.reshape(-1, op.spec.dim).contiguous()
+    gv = torch.empty_like(v)
+    _native.launch(f'sh_bwd[{op.tag}]', _native.load().mh_sh_bwd, op.module.handle, _native.ptr(v), _native.ptr(g),
+                   _native.ptr(gv), v.shape[0], _native.stream_of(v))
+    return gv.reshape(vec.shape)
 
 
 class _SHFn(torch.autograd.Function):
@@ -189,21 +224,53 @@ class _SHFn(torch.autograd.Function):
         out = torch.empty(E, op.spec.dim, device=v.device, dtype=torch.float32)
         _native.launch(f'sh_fwd[{op.tag}]', _native.load().mh_sh_fwd, op.module.handle, _native.ptr(v),
                        _native.ptr(out), E, _native.stream_of(v))
-        ctx.save_for_backward(v)
-        ctx.op, ctx.lead = op, lead
+        ctx.save_for_backward(vec)           # the input itself: a double backward differentiates through it
+        ctx.op = op
         return out.reshape(*lead, op.spec.dim)
 
     @staticmethod
     def backward(ctx, g):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
-        v, = ctx.saved_tensors
+        vec, = ctx.saved_tensors
         op = ctx.op
-        g = g.reshape(-1, op.spec.dim).contiguous()
-        gv = torch.empty_like(v)
-        _native.launch(f'sh_bwd[{op.tag}]', _native.load().mh_sh_bwd, op.module.handle, _native.ptr(v),
-                       _native.ptr(g), _native.ptr(gv), v.shape[0], _native.stream_of(v))
-        return gv.reshape(*ctx.lead, 3), None
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            return _SHAdjFn.apply(g, vec, op), None
+        return _sh_bwd(op, vec, g), None
+
+
+class _SHAdjFn(torch.autograd.Function):
+    """dL/dv = (dY/dv)^T gY as a function of (gY, v), for a double backward: with ggv the incoming gradient,
+    d<ggv, dL/dv>/dgY = (dY/dv) ggv (``sh_jvp``) and d<ggv, dL/dv>/dv the Hessian-vector product (``sh_bwd2``).
+    Third derivatives are not provided."""
+
+    @staticmethod
+    def forward(ctx, g, vec, op):
+        ctx.save_for_backward(g, vec)
+        ctx.op = op
+        return _sh_bwd(op, vec, g)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggv):
+        g, vec = ctx.saved_tensors
+        op = ctx.op
+        m = op.second_module()
+        v = vec.reshape(-1, 3).contiguous()
+        dv = ggv.reshape(-1, 3).contiguous()
+        E, P, lib = v.shape[0], _native.ptr, _native.load()
+        gg = gv = None
+        if ctx.needs_input_grad[0]:
+            gg = torch.empty(E, op.spec.dim, device=v.device, dtype=torch.float32)
+            _native.launch(f'sh_jvp[{op.tag}]', lib.mh_sh_jvp, m.handle, P(v), P(dv), P(gg), E, _native.stream_of(v))
+            gg = gg.reshape(g.shape)
+        if ctx.needs_input_grad[1]:
+            g2 = g.reshape(-1, op.spec.dim).contiguous()
+            gv = torch.empty_like(v)
+            _native.launch(f'sh_bwd2[{op.tag}]', lib.mh_sh_bwd2, m.handle, P(v), P(dv), P(g2), P(gv), E,
+                           _native.stream_of(v))
+            gv = gv.reshape(vec.shape)
+        return gg, gv, None
 
 
 class HipSphericalHarmonics(torch.nn.Module):
@@ -215,6 +282,7 @@ class HipSphericalHarmonics(torch.nn.Module):
         self.source = source(self.spec)
         code = _native.compile_source(self.source)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
+        self._device = dev
         with torch.cuda.device(dev):
             self.module = _native.Module(code, {
                 _native.MH_SH_FWD: (self.spec.kname('sh_fwd'), BLOCK, BLOCK),
@@ -224,6 +292,20 @@ class HipSphericalHarmonics(torch.nn.Module):
         self.normalize, self.normalization = mod.normalize, mod.normalization
         self.original = [mod]
         self.tag = 'spherical_harmonics'
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; then the
+        # gradient is differentiable once more through the second-order kernels (second_module)
+        self.double_backward = False
+        self._second = None
+
+    def second_module(self):
+        """The module of the second-order kernels (``sh_jvp``, ``sh_bwd2``), compiled on first use."""
+        if self._second is None:
+            code = _native.compile_source(source_second(self.spec))
+            with torch.cuda.device(self._device):
+                self._second = _native.Module(code, {
+                    _native.MH_SH_JVP: (self.spec.kname('sh_jvp'), BLOCK, BLOCK),
+                    _native.MH_SH_BWD2: (self.spec.kname('sh_bwd2'), BLOCK, BLOCK)})
+        return self._second
 
     def forward(self, vec):
         return _SHFn.apply(vec, self)

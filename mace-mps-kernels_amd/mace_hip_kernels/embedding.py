@@ -78,51 +78,90 @@ class EmbSpec:
         return f'{base}_n{self.n}_p{self.p}'
 
 
-def source(spec):
+def math_lines(spec):
+    """The per-edge arithmetic as plain C statements of the length ``x``: ``head`` defines the envelope ``cut``,
+    ``fwd`` the features ``f0..f{n-1}``, ``bwd`` (reading ``gfeats`` and ``gcut`` at edge ``e``) ``acc`` = dL/dx."""
     p, n = spec.p, spec.n
     c1, c2, c3 = (p + 1.0) * (p + 2.0) / 2.0, p * (p + 2.0), p * (p + 1.0) / 2.0
 
     def powu(k):
         return ' * '.join(['u'] * k) if k > 0 else '1.f'
 
+    head = [f'const float u = x / {_lit(spec.r_max)};',
+            f'const float up = {powu(p)};',
+            f'const bool in = x < {_lit(spec.r_max)};',
+            f'const float env = 1.f - {_lit(c1)} * up + {_lit(c2)} * (up * u) - {_lit(c3)} * (up * u * u);',
+            'const float cut = in ? env : 0.f;']
+    fwd = [f'const float f{k} = ({_lit(spec.pref)} * sinf({_lit(w)} * x)) / x * cut;' for k, w in enumerate(spec.w)]
+    # d cut/dx = env'(u) / r_max inside the cutoff; d feat_k/dx = b_k' cut + b_k cut'
+    bwd = [f'const float denv = (-{_lit(c1 * p)} * {powu(p - 1)} + {_lit(c2 * (p + 1))} * up'
+           f' - {_lit(c3 * (p + 2))} * (up * u)) / {_lit(spec.r_max)};',
+           'const float dcut = in ? denv : 0.f;',
+           'const float ix = 1.f / x;',
+           'float acc = gcut ? gcut[e] * dcut : 0.f;']
+    for k, w in enumerate(spec.w):
+        bwd += ['{',
+                f'  const float s = sinf({_lit(w)} * x), c = cosf({_lit(w)} * x);',
+                f'  const float b = {_lit(spec.pref)} * s * ix;',
+                f'  const float db = {_lit(spec.pref)} * ({_lit(w)} * c - s * ix) * ix;',
+                f'  acc += gfeats[e * {n} + {k}] * (db * cut + b * dcut);',
+                '}']
+    return dict(head=head, fwd=fwd, bwd=bwd)
+
+
+def source(spec):
+    n = spec.n
+    m = math_lines(spec)
+    ind = lambda lines: ['  ' + l for l in lines]  # noqa: E731
     head = ['  const long long e = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * BLOCK + threadIdx.x;',
             '  if (e >= E) return;',
-            '  const float x = len[e];',
-            f'  const float u = x / {_lit(spec.r_max)};',
-            f'  const float up = {powu(p)};',
-            f'  const bool in = x < {_lit(spec.r_max)};',
-            f'  const float env = 1.f - {_lit(c1)} * up + {_lit(c2)} * (up * u) - {_lit(c3)} * (up * u * u);',
-            '  const float cut = in ? env : 0.f;']
+            '  const float x = len[e];'] + ind(m['head'])
     L = [_native.device_header(), f'#define BLOCK {BLOCK}',
          f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("emb_fwd")}(const float* __restrict__ len,',
          '    float* __restrict__ feats, float* __restrict__ cutoff, long long E) {'] + head
-    L += ['  cutoff[e] = cut;']
-    for k, w in enumerate(spec.w):
-        L.append(f'  feats[e * {n} + {k}] = ({_lit(spec.pref)} * sinf({_lit(w)} * x)) / x * cut;')
-    L += ['}', '']
-    # backward: d cut/dx = env'(u) / r_max inside the cutoff; d feat_k/dx = b_k' cut + b_k cut'
+    L += ['  cutoff[e] = cut;'] + ind(m['fwd']) + [f'  feats[e * {n} + {k}] = f{k};' for k in range(n)] + ['}', '']
     L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("emb_bwd")}(const float* __restrict__ len,',
           '    const float* __restrict__ gfeats, const float* __restrict__ gcut, float* __restrict__ glen, long long E) {']
-    L += head
-    L += [f'  const float denv = (-{_lit(c1 * p)} * {powu(p - 1)} + {_lit(c2 * (p + 1))} * up'
-          f' - {_lit(c3 * (p + 2))} * (up * u)) / {_lit(spec.r_max)};',
-          '  const float dcut = in ? denv : 0.f;',
-          '  const float ix = 1.f / x;',
-          '  float acc = gcut ? gcut[e] * dcut : 0.f;']
-    for k, w in enumerate(spec.w):
-        L += ['  {',
-              f'    const float s = sinf({_lit(w)} * x), c = cosf({_lit(w)} * x);',
-              f'    const float b = {_lit(spec.pref)} * s * ix;',
-              f'    const float db = {_lit(spec.pref)} * ({_lit(w)} * c - s * ix) * ix;',
-              f'    acc += gfeats[e * {n} + {k}] * (db * cut + b * dcut);',
-              '  }']
-    L += ['  glen[e] = acc;', '}', '']
+    L += head + ind(m['bwd']) + ['  glen[e] = acc;', '}', '']
+    return '\n'.join(L)
+
+
+def source_second(spec):
+    """HIP source of the second-order kernels behind a double backward: the statements of ``emb_fwd`` / ``emb_bwd``
+    on dual numbers with the lengths carrying a direction dl.  ``emb_jvp`` writes (d feats, d cut) = their
+    derivatives times dl; ``emb_bwd2`` writes the derivative of dL/dx along dl for fixed incoming gradients."""
+    n = spec.n
+    m = math_lines(spec)
+    ind = lambda lines: ['  ' + l for l in lines]  # noqa: E731
+    head = ['  const long long e = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * BLOCK + threadIdx.x;',
+            '  if (e >= E) return;',
+            '  const mh_dual x(len[e], dl[e]);'] + ind(_native.dualize(m['head']))
+    L = [_native.device_header(), _native.dual_header(), f'#define BLOCK {BLOCK}',
+         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("emb_jvp")}(const float* __restrict__ len,',
+         '    const float* __restrict__ dl, float* __restrict__ dfeats, float* __restrict__ dcutoff, long long E) {']
+    L += head + ['  dcutoff[e] = cut.d;'] + ind(_native.dualize(m['fwd']))
+    L += [f'  dfeats[e * {n} + {k}] = f{k}.d;' for k in range(n)] + ['}', '']
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("emb_bwd2")}(const float* __restrict__ len,',
+          '    const float* __restrict__ dl, const float* __restrict__ gfeats, const float* __restrict__ gcut,',
+          '    float* __restrict__ glen, long long E) {']
+    L += head + ind(_native.dualize(m['bwd'])) + ['  glen[e] = acc.d;', '}', '']
     return '\n'.join(L)
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by this HIP module; patch_model(model, '
-                    'double_backward=True) leaves it on e3nn')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
+
+
+def _emb_bwd(op, lengths, gf, gc):
+    r = lengths.reshape(-1).contiguous()
+    E = r.shape[0]
+    gf = torch.zeros(E, op.spec.n, device=r.device) if gf is None else gf.reshape(E, op.spec.n).contiguous()
+    gc = None if gc is None else gc.reshape(E).contiguous()
+    gr = torch.empty_like(r)
+    _native.launch(f'emb_bwd[{op.tag}]', _native.load().mh_emb_bwd, op.module.handle, _native.ptr(r),
+                   _native.ptr(gf), _native.ptr(gc), _native.ptr(gr), E, _native.stream_of(r))
+    return gr.reshape(lengths.shape)
 
 
 class _EmbFn(torch.autograd.Function):
@@ -139,23 +178,57 @@ class _EmbFn(torch.autograd.Function):
         cut = torch.empty(E, 1, device=r.device, dtype=torch.float32)
         _native.launch(f'emb_fwd[{op.tag}]', _native.load().mh_emb_fwd, op.module.handle, _native.ptr(r),
                        _native.ptr(feats), _native.ptr(cut), E, _native.stream_of(r))
-        ctx.save_for_backward(r)
-        ctx.op, ctx.lead = op, lead
+        ctx.save_for_backward(lengths)       # the input itself: a double backward differentiates through it
+        ctx.op = op
         return feats.reshape(*lead, op.spec.n), cut.reshape(*lead, 1)
 
     @staticmethod
     def backward(ctx, gf, gc):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
-        r, = ctx.saved_tensors
+        lengths, = ctx.saved_tensors
         op = ctx.op
-        E = r.shape[0]
-        gf = torch.zeros(E, op.spec.n, device=r.device) if gf is None else gf.reshape(E, op.spec.n).contiguous()
-        gc = None if gc is None else gc.reshape(E).contiguous()
-        gr = torch.empty_like(r)
-        _native.launch(f'emb_bwd[{op.tag}]', _native.load().mh_emb_bwd, op.module.handle, _native.ptr(r),
-                       _native.ptr(gf), _native.ptr(gc), _native.ptr(gr), E, _native.stream_of(r))
-        return gr.reshape(*ctx.lead, 1), None
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            return _EmbAdjFn.apply(gf, gc, lengths, op), None
+        return _emb_bwd(op, lengths, gf, gc), None
+
+
+class _EmbAdjFn(torch.autograd.Function):
+    """dL/dx = sum_k gf_k f_k'(x) + gc cut'(x) as a function of (gf, gc, x), for a double backward: with ggx the
+    incoming gradient, d<ggx, dL/dx>/d(gf, gc) = (f'(x), cut'(x)) ggx (``emb_jvp``) and d<ggx, dL/dx>/dx =
+    (sum_k gf_k f_k''(x) + gc cut''(x)) ggx (``emb_bwd2``).  Third derivatives are not provided."""
+
+    @staticmethod
+    def forward(ctx, gf, gc, lengths, op):
+        ctx.save_for_backward(gf, gc, lengths)
+        ctx.op = op
+        return _emb_bwd(op, lengths, gf, gc)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggx):
+        gf, gc, lengths = ctx.saved_tensors
+        op = ctx.op
+        m = op.second_module()
+        r = lengths.reshape(-1).contiguous()
+        dl = ggx.reshape(-1).contiguous()
+        E, n, P, lib = r.shape[0], op.spec.n, _native.ptr, _native.load()
+        d_gf = d_gc = d_x = None
+        if ctx.needs_input_grad[0] or ctx.needs_input_grad[1]:
+            df = torch.empty(E, n, device=r.device, dtype=torch.float32)
+            dc = torch.empty(E, device=r.device, dtype=torch.float32)
+            _native.launch(f'emb_jvp[{op.tag}]', lib.mh_emb_jvp, m.handle, P(r), P(dl), P(df), P(dc), E,
+                           _native.stream_of(r))
+            d_gf = df.reshape(gf.shape) if ctx.needs_input_grad[0] else None
+            d_gc = dc.reshape(gc.shape) if ctx.needs_input_grad[1] else None
+        if ctx.needs_input_grad[2]:
+            gf2 = torch.zeros(E, n, device=r.device) if gf is None else gf.reshape(E, n).contiguous()
+            gc2 = None if gc is None else gc.reshape(E).contiguous()
+            gx = torch.empty_like(r)
+            _native.launch(f'emb_bwd2[{op.tag}]', lib.mh_emb_bwd2, m.handle, P(r), P(dl), P(gf2), P(gc2), P(gx), E,
+                           _native.stream_of(r))
+            d_x = gx.reshape(lengths.shape)
+        return d_gf, d_gc, d_x, None
 
 
 class HipRadialEmbedding(torch.nn.Module):
@@ -173,6 +246,21 @@ class HipRadialEmbedding(torch.nn.Module):
         self.out_dim = self.spec.n
         self.original = [mod]
         self.tag = 'radial_embedding'
+        self._device = dev
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; then the
+        # gradient is differentiable once more through the second-order kernels (second_module)
+        self.double_backward = False
+        self._second = None
+
+    def second_module(self):
+        """The module of the second-order kernels (``emb_jvp``, ``emb_bwd2``), compiled on first use."""
+        if self._second is None:
+            code = _native.compile_source(source_second(self.spec))
+            with torch.cuda.device(self._device):
+                self._second = _native.Module(code, {
+                    _native.MH_EMB_JVP: (self.spec.kname('emb_jvp'), BLOCK, BLOCK),
+                    _native.MH_EMB_BWD2: (self.spec.kname('emb_bwd2'), BLOCK, BLOCK)})
+        return self._second
 
     def forward(self, edge_lengths, *args, **kwargs):
         return _EmbFn.apply(edge_lengths, self)

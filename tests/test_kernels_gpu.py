@@ -980,6 +980,49 @@ def test_linear_double_backward():
     assert _rel(d_g.double().cpu().numpy(), want.detach().numpy()) < LIN_TOL
 
 
+def test_sh_and_embedding_double_backward():
+    """The spherical harmonics' and radial embedding's second derivatives on the GPU (sh_jvp / sh_bwd2, emb_jvp /
+    emb_bwd2): d<v, dL/dinput>/d(incoming gradients) and /d(input) against float64 double backward of the e3nn
+    modules, lengths on both sides of r_max; relative error < 1e-5 (2e-5 for the embedding's Hessian term)."""
+    from mace_hip_kernels import HipRadialEmbedding, HipSphericalHarmonics
+    dev = _dev()
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(14)
+    n = 3001
+    print('[case] SH double backward', flush=True)
+    op = HipSphericalHarmonics(m.spherical_harmonics, device=dev)
+    op.double_backward = True
+    v = rng.normal(size=(n, 3)) * rng.uniform(0.5, 5.0, size=(n, 1))
+    dv, g = rng.normal(size=(n, 3)), rng.normal(size=(n, op.spec.dim))
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+    vt, gt = t(v), t(g)
+    gv, = torch.autograd.grad(op(vt), vt, gt, create_graph=True)
+    d_g, d_v = torch.autograd.grad((gv * torch.tensor(dv, dtype=torch.float32, device=dev)).sum(), (gt, vt))
+    m64 = copy.deepcopy(m.spherical_harmonics).double()
+    v64, g64 = torch.tensor(v, requires_grad=True), torch.tensor(g, requires_grad=True)
+    gv64, = torch.autograd.grad(m64(v64), v64, g64, create_graph=True)
+    w_g, w_v = torch.autograd.grad((gv64 * torch.tensor(dv)).sum(), (g64, v64))
+    assert _rel(d_g.double().cpu().numpy(), w_g.numpy()) < 1e-5
+    assert _rel(d_v.double().cpu().numpy(), w_v.numpy()) < 1e-5
+    print('[case] radial embedding double backward', flush=True)
+    op = HipRadialEmbedding(m.radial_embedding, device=dev)
+    op.double_backward = True
+    r = rng.uniform(0.7, 6.0, size=(n, 1))
+    dl, gf, gc = rng.normal(size=(n, 1)), rng.normal(size=(n, op.spec.n)), rng.normal(size=(n, 1))
+    rt, gft, gct = t(r), t(gf), t(gc)
+    f, c = op(rt)
+    gr, = torch.autograd.grad((f, c), rt, (gft, gct), create_graph=True)
+    d_f, d_c, d_r = torch.autograd.grad((gr * torch.tensor(dl, dtype=torch.float32, device=dev)).sum(), (gft, gct, rt))
+    e64 = copy.deepcopy(m.radial_embedding).double()
+    r64, gf64, gc64 = (torch.tensor(a, requires_grad=True) for a in (r, gf, gc))
+    f64, c64 = e64(r64)
+    gr64, = torch.autograd.grad((f64, c64), r64, (gf64, gc64), create_graph=True)
+    w_f, w_c, w_r = torch.autograd.grad((gr64 * torch.tensor(dl)).sum(), (gf64, gc64, r64))
+    assert _rel(d_f.double().cpu().numpy(), w_f.numpy()) < 1e-5
+    assert _rel(d_c.double().cpu().numpy(), w_c.numpy()) < 1e-5
+    assert _rel(d_r.double().cpu().numpy(), w_r.numpy()) < 2e-5
+
+
 def test_kernels_match_golden_fixtures():
     """Kernels against the committed oracle fixtures (tests/golden/make_golden.py)."""
     import os
