@@ -78,7 +78,8 @@ enum mh_kernel_kind {
     MH_SH_BWD2 = 39,     /* derivative of their vector gradient along that direction                */
     MH_EMB_JVP = 40,     /* radial embedding: derivative along a direction of the lengths           */
     MH_EMB_BWD2 = 41,    /* derivative of its length gradient along that direction                  */
-    MH_NUM_KINDS = 42
+    MH_GEOM_JVP = 42,    /* edge geometry, behind a double backward: per-edge second-order terms     */
+    MH_NUM_KINDS = 43
 };
 
 /* flags of mh_conv_bwd */
@@ -245,6 +246,15 @@ int mh_emb_jvp(mh_module* m, const float* len, const float* dlen, float* dfeats,
                void* stream);
 int mh_emb_bwd2(mh_module* m, const float* len, const float* dlen, const float* gfeats, const float* gcutoff,
                 float* glen, int64_t E, void* stream);
+
+/* Second derivatives of the edge geometry, behind a double backward.  With d_e = ggpos[recv[e]] - ggpos[send[e]]
+ * + ggshifts[e] (either may be NULL: zero) and u = vec / |vec|: dgvec = d, dglen = u.d, and h = glen (d - u (u.d)) /
+ * |vec| (0 at |vec| = 0; glen NULL: 0), which mh_geom_bwd (h as gvec, glen NULL) sums onto the atoms and shifts.
+ * Bind MH_GEOM_JVP with 256 threads and 256 edges per block.  No reference counterpart (MACE's
+ * get_edge_vectors_and_lengths runs on PyTorch, and the reference raises on a double backward). */
+int mh_geom_jvp(mh_module* m, const float* vec, const float* len, const float* ggpos, const float* ggshifts,
+                const int32_t* send, const int32_t* recv, const float* glen, float* dgvec, float* dglen, float* h,
+                int64_t E, void* stream);
 
 /* Node-wise equivariant linear out[n] = L(x[n], attrs[n]) for N nodes (x [N, Din], out [N, Dout], fp32, the e3nn
  * irreps layout [.., u * (2l+1) + m] per block).  Without attrs (attrs NULL) it is e3nn's o3.Linear:

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 20; }
+int mh_version(void) { return 21; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -370,6 +370,14 @@ int mh_emb_bwd2(mh_module* m, const float* len, const float* dlen, const float* 
     if (E > 0 && (!len || !dlen || !gfeats || !glen)) return fail(-1, "mh_emb_bwd2: NULL operand");
     void* args[] = {&len, &dlen, &gfeats, &gcutoff, &glen, &E};
     return launch(m, MH_EMB_BWD2, E, args, stream, "mh_emb_bwd2");
+}
+
+int mh_geom_jvp(mh_module* m, const float* vec, const float* len, const float* ggpos, const float* ggshifts,
+                const int32_t* send, const int32_t* recv, const float* glen, float* dgvec, float* dglen, float* h,
+                int64_t E, void* stream) {
+    if (E > 0 && (!vec || !len || !send || !recv || !dgvec || !dglen || !h)) return fail(-1, "mh_geom_jvp: NULL operand");
+    void* args[] = {&vec, &len, &ggpos, &ggshifts, &send, &recv, &glen, &dgvec, &dglen, &h, &E};
+    return launch(m, MH_GEOM_JVP, E, args, stream, "mh_geom_jvp");
 }
 
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,

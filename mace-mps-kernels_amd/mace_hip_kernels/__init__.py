@@ -83,9 +83,8 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     ``double_backward`` (default off, as in the reference, where a backward under ``create_graph=True`` raises)
     makes the patched modules' gradients differentiable once more, for second derivatives with respect to the
     inputs: Hessian-vector products and force constants, or force and stress terms of a loss differentiated with
-    respect to parameters the patch leaves on e3nn.  The convolution, symmetric contraction, linears, layout change,
-    spherical harmonics, radial embedding and linear readout heads take it; the modules without second-order kernels
-    (edge geometry, radial MLP, SiLU readout heads) are then left on e3nn and reported in ``skipped``.  The patched
+    respect to parameters the patch leaves on e3nn.  Every drop-in takes it except the radial MLPs and the SiLU
+    readout heads, which have no second-order kernels and are then left on e3nn and reported in ``skipped``.  The patched
     modules hold their weights as constants: no gradient reaches those weights, with or without it."""
     # a fully patched model may hold no parameters any more (the drop-ins keep their weights as buffers)
     p = next((t for t in itertools.chain(model.parameters(), model.buffers()) if t.is_floating_point()), None)
@@ -136,11 +135,9 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             patched.append(name)
     no2 = 'no second-order kernels (patched with double_backward=True)'
     if double_backward:
-        if edge_geometry:
-            skipped.append(('edge_geometry', no2))
         if radial_mlp:
             skipped += [(f'interactions.{i}.conv_tp_weights', no2) for i in range(len(getattr(model, 'interactions', [])))]
-        edge_geometry = radial_mlp = False
+        radial_mlp = False
     if spherical_harmonics and hasattr(model, 'spherical_harmonics'):
         sh = model.spherical_harmonics
         if not isinstance(sh, HipSphericalHarmonics):
@@ -246,6 +243,8 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             setattr(parent, attr, new)
             patched.append(name)
     if double_backward:                   # including modules patched by an earlier call
+        if _geometry.installed(model):
+            model._mh_geometry_double_backward = True
         for mod in model.modules():
             if isinstance(mod, (HipConvTP, HipSymmetricContraction, HipNodeLinear, HipReshapeIrreps,
                                 HipSphericalHarmonics, HipRadialEmbedding)):

@@ -86,6 +86,31 @@ extern "C" __global__ __launch_bounds__(BLOCK) void geom_bwd(const float* __rest
   sx = geom_wave_sum(sx); sy = geom_wave_sum(sy); sz = geom_wave_sum(sz);
   if (lane == 0) { gpos[3 * n] = sx; gpos[3 * n + 1] = sy; gpos[3 * n + 2] = sz; }
 }
+
+// Second derivatives behind a double backward.  With d = ggpos[r] - ggpos[s] + ggshifts[e] the direction that the
+// incoming gradients give edge e's vector and u = v / |v|: d/dg_vec = d, d/dg_len = u.d, and the part that goes
+// back through v (and from there to the atoms, through geom_bwd) h = g_len (d - u (u.d)) / |v| (0 at |v| = 0).
+extern "C" __global__ __launch_bounds__(BLOCK) void geom_jvp(const float* __restrict__ vec,
+    const float* __restrict__ len, const float* __restrict__ ggpos, const float* __restrict__ ggshifts,
+    const int* __restrict__ send, const int* __restrict__ recv, const float* __restrict__ glen,
+    float* __restrict__ dgvec, float* __restrict__ dglen, float* __restrict__ h, long long E) {
+  const long long e = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * BLOCK + threadIdx.x;
+  if (e >= E) return;
+  float dx = 0.f, dy = 0.f, dz = 0.f;
+  if (ggpos) {
+    const long long s = send[e], r = recv[e];
+    dx = ggpos[3 * r] - ggpos[3 * s]; dy = ggpos[3 * r + 1] - ggpos[3 * s + 1]; dz = ggpos[3 * r + 2] - ggpos[3 * s + 2];
+  }
+  if (ggshifts) { dx += ggshifts[3 * e]; dy += ggshifts[3 * e + 1]; dz += ggshifts[3 * e + 2]; }
+  dgvec[3 * e] = dx; dgvec[3 * e + 1] = dy; dgvec[3 * e + 2] = dz;
+  const float l = len[e];
+  const float il = l != 0.f ? 1.f / l : 0.f;
+  const float ux = vec[3 * e] * il, uy = vec[3 * e + 1] * il, uz = vec[3 * e + 2] * il;
+  const float ud = ux * dx + uy * dy + uz * dz;
+  dglen[e] = ud;
+  const float c = glen ? glen[e] * il : 0.f;
+  h[3 * e] = c * (dx - ux * ud); h[3 * e + 1] = c * (dy - uy * ud); h[3 * e + 2] = c * (dz - uz * ud);
+}
 '''
 
 _modules = {}
@@ -98,7 +123,8 @@ def _module(device):
         code = _native.compile_source(_native.device_header() + _SOURCE)
         with torch.cuda.device(device):
             _modules[key] = _native.Module(code, {_native.MH_GEOM_FWD: ('geom_fwd', BLOCK, BLOCK),
-                                                  _native.MH_GEOM_BWD: ('geom_bwd', BLOCK, BLOCK // 64)})
+                                                  _native.MH_GEOM_BWD: ('geom_bwd', BLOCK, BLOCK // 64),
+                                                  _native.MH_GEOM_JVP: ('geom_jvp', BLOCK, BLOCK)})
     return _modules[key]
 
 
@@ -107,13 +133,27 @@ def source():
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by this HIP module; patch_model(model, '
-                    'double_backward=True) leaves it on e3nn')
+                    'autograd Hessian) is not enabled for the edge geometry; patch with '
+                    'patch_model(model, double_backward=True)')
+
+
+def _geom_bwd(vec, ln, gv, gl, gr, N, want_shifts):
+    rp_r, ei_r = gr.by_recv()
+    rp_s, ei_s = gr.by_send()
+    gpos = torch.empty(N, 3, device=vec.device, dtype=torch.float32)
+    gsh = torch.empty_like(vec) if want_shifts else None
+    gv = None if gv is None else gv.contiguous()
+    gl = None if gl is None else gl.contiguous()
+    mod = _module(vec.device)
+    _native.launch('geom_bwd', _native.load().mh_geom_bwd, mod.handle, _native.ptr(vec), _native.ptr(ln),
+                   _native.ptr(gv), _native.ptr(gl), _native.ptr(rp_r), _native.ptr(ei_r), _native.ptr(rp_s),
+                   _native.ptr(ei_s), _native.ptr(gpos), _native.ptr(gsh), N, _native.stream_of(vec))
+    return gpos, gsh
 
 
 class _GeomFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, positions, shifts, edge_index):
+    def forward(ctx, positions, shifts, edge_index, double_backward=False):
         N, E = positions.shape[0], edge_index.shape[1]
         gr = _conv.graph_for(edge_index, N)
         p = positions.contiguous()
@@ -124,27 +164,55 @@ class _GeomFn(torch.autograd.Function):
         _native.launch('geom_fwd', _native.load().mh_geom_fwd, mod.handle, _native.ptr(p), _native.ptr(gr.send),
                        _native.ptr(gr.recv), _native.ptr(sh), _native.ptr(vec), _native.ptr(ln), E,
                        _native.stream_of(p))
-        ctx.save_for_backward(vec, ln)
-        ctx.gr, ctx.N = gr, N
+        ctx.save_for_backward(positions, shifts, vec, ln)
+        ctx.gr, ctx.N, ctx.double_backward = gr, N, double_backward
         return vec, ln
 
     @staticmethod
     def backward(ctx, gv, gl):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
-        vec, ln = ctx.saved_tensors
-        gr, N = ctx.gr, ctx.N
-        rp_r, ei_r = gr.by_recv()
-        rp_s, ei_s = gr.by_send()
-        gpos = torch.empty(N, 3, device=vec.device, dtype=torch.float32)
-        gsh = torch.empty_like(vec) if ctx.needs_input_grad[1] else None
-        gv = None if gv is None else gv.contiguous()
-        gl = None if gl is None else gl.contiguous()
-        mod = _module(vec.device)
-        _native.launch('geom_bwd', _native.load().mh_geom_bwd, mod.handle, _native.ptr(vec), _native.ptr(ln),
-                       _native.ptr(gv), _native.ptr(gl), _native.ptr(rp_r), _native.ptr(ei_r), _native.ptr(rp_s),
-                       _native.ptr(ei_s), _native.ptr(gpos), _native.ptr(gsh), N, _native.stream_of(vec))
-        return (gpos if ctx.needs_input_grad[0] else None), gsh, None
+        positions, shifts, vec, ln = ctx.saved_tensors
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not ctx.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            gpos, gsh = _GeomAdjFn.apply(gv, gl, positions, shifts, vec.detach(), ln.detach(), ctx.gr, ctx.N,
+                                         ctx.needs_input_grad[1])
+        else:
+            gpos, gsh = _geom_bwd(vec, ln, gv, gl, ctx.gr, ctx.N, ctx.needs_input_grad[1])
+        return (gpos if ctx.needs_input_grad[0] else None), gsh, None, None
+
+
+class _GeomAdjFn(torch.autograd.Function):
+    """(dL/dpositions, dL/dshifts) as a function of (g_vec, g_len, positions, shifts), for a double backward (see
+    ``geom_jvp``): the incoming gradients become a direction d per edge; d/dg_vec = d, d/dg_len = u.d, and the
+    curvature of |v| gives h per edge, summed onto the atoms (and the shifts) by the first-order kernel.  Third
+    derivatives are not provided."""
+
+    @staticmethod
+    def forward(ctx, gv, gl, positions, shifts, vec, ln, gr, N, want_shifts):
+        ctx.save_for_backward(gl, vec, ln)
+        ctx.gr, ctx.N = gr, N
+        return _geom_bwd(vec, ln, gv, gl, gr, N, want_shifts)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggpos, ggsh):
+        gl, vec, ln = ctx.saved_tensors
+        gr, N, E = ctx.gr, ctx.N, vec.shape[0]
+        P = _native.ptr
+        ggpos = None if ggpos is None else ggpos.contiguous()
+        ggsh = None if ggsh is None else ggsh.contiguous()
+        glc = None if gl is None else gl.contiguous()
+        dgv = torch.empty(E, 3, device=vec.device, dtype=torch.float32)
+        dgl = torch.empty(E, 1, device=vec.device, dtype=torch.float32)
+        h = torch.empty(E, 3, device=vec.device, dtype=torch.float32)
+        _native.launch('geom_jvp', _native.load().mh_geom_jvp, _module(vec.device).handle, P(vec), P(ln), P(ggpos),
+                       P(ggsh), P(gr.send), P(gr.recv), P(glc), P(dgv), P(dgl), P(h), E, _native.stream_of(vec))
+        need = ctx.needs_input_grad
+        gpos = gsh = None
+        if need[2] or need[3]:
+            gpos, gsh = _geom_bwd(vec, ln, h, None, gr, N, need[3])
+        return (dgv if need[0] else None, dgl if need[1] else None, gpos if need[2] else None, gsh,
+                None, None, None, None, None)
 
 
 def edge_vectors_and_lengths(positions, edge_index, shifts):
@@ -154,7 +222,7 @@ def edge_vectors_and_lengths(positions, edge_index, shifts):
     if positions.shape[-1] != 3 or shifts.shape != (edge_index.shape[1], 3):
         raise ValueError(f'positions [N, 3] and shifts [E, 3] expected, got {tuple(positions.shape)}, '
                          f'{tuple(shifts.shape)}')
-    return _GeomFn.apply(positions, shifts, edge_index)
+    return _GeomFn.apply(positions, shifts, edge_index, _ACTIVE.get() == 'double_backward')
 
 
 def _supported_call(positions, edge_index, shifts):
@@ -179,7 +247,7 @@ def _wrap(orig):
 
 
 def _forward_with_geometry(self, *args, **kwargs):
-    token = _ACTIVE.set(True)
+    token = _ACTIVE.set('double_backward' if getattr(self, '_mh_geometry_double_backward', False) else True)
     try:
         return type(self).forward(self, *args, **kwargs)
     finally:
@@ -205,6 +273,7 @@ def installed(model):
 
 
 def uninstall(model):
+    model.__dict__.pop('_mh_geometry_double_backward', None)
     if installed(model):
         del model.forward
         return True

@@ -1023,6 +1023,43 @@ def test_sh_and_embedding_double_backward():
     assert _rel(d_r.double().cpu().numpy(), w_r.numpy()) < 2e-5
 
 
+def test_edge_geometry_double_backward():
+    """The edge geometry's second derivatives (geom_jvp + the first-order atom sums), with shifts and zero-length
+    edges absent: d<(ggpos, ggshifts), (dL/dpos, dL/dshifts)>/d(g_vec, g_len, positions, shifts) against float64
+    double backward of the plain PyTorch expressions; relative error < 1e-5."""
+    from mace_hip_kernels import geometry as geo
+    dev = _dev()
+    print('[case] edge geometry double backward', flush=True)
+    rng = np.random.default_rng(15)
+    n, e = 61, 900
+    s, r = _graph(rng, n, e)
+    keep = s != r
+    s, r = s[keep], r[keep]
+    e = len(s)
+    pos, sh = rng.normal(size=(n, 3)) * 3.0, rng.normal(size=(e, 3))
+    gv, gl = rng.normal(size=(e, 3)), rng.normal(size=(e, 1))
+    ggp, ggs = rng.normal(size=(n, 3)), rng.normal(size=(e, 3))
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+    pt, st, gvt, glt = t(pos), t(sh), t(gv), t(gl)
+    vec, ln = geo._GeomFn.apply(pt, st, ei, True)
+    gp, gs = torch.autograd.grad((vec, ln), (pt, st), (gvt, glt), create_graph=True)
+    sval = (gp * torch.tensor(ggp, dtype=torch.float32, device=dev)).sum() + \
+        (gs * torch.tensor(ggs, dtype=torch.float32, device=dev)).sum()
+    got = torch.autograd.grad(sval, (gvt, glt, pt, st))
+    p64, s64, gv64, gl64 = (torch.tensor(a, requires_grad=True) for a in (pos, sh, gv, gl))
+    v64 = p64[torch.tensor(r)] - p64[torch.tensor(s)] + s64
+    l64 = torch.linalg.norm(v64, dim=-1, keepdim=True)
+    gp64, gs64 = torch.autograd.grad((v64, l64), (p64, s64), (gv64, gl64), create_graph=True)
+    want = torch.autograd.grad((gp64 * torch.tensor(ggp)).sum() + (gs64 * torch.tensor(ggs)).sum(),
+                               (gv64, gl64, p64, s64))
+    for i, (a, w) in enumerate(zip(got, want)):
+        assert _rel(a.double().cpu().numpy(), w.numpy()) < 1e-5, i
+    vec, ln = geo._GeomFn.apply(pt, st, ei, False)
+    with pytest.raises(RuntimeError, match='double backward'):
+        torch.autograd.grad((vec, ln), (pt, st), (gvt, glt), create_graph=True)
+
+
 def test_kernels_match_golden_fixtures():
     """Kernels against the committed oracle fixtures (tests/golden/make_golden.py)."""
     import os

@@ -118,9 +118,8 @@ def test_double_backward_raises():
 
 @pytest.mark.parametrize('config', ['l3_corr3_fullcg', 'l3_corr3_l2hidden'])
 def test_double_backward_hessian_and_force_loss(config):
-    """patch_model(double_backward=True): the convolutions, contractions, linears, layout changes, spherical
-    harmonics, radial embedding and linear readout heads differentiate twice; the modules without second-order
-    kernels stay on e3nn and are reported.  Against the
+    """patch_model(double_backward=True): every drop-in but the radial MLPs and SiLU readout heads differentiates
+    twice (those stay on e3nn and are reported).  Against the
     unpatched model in float64: (1) a Hessian-vector product of the energy with respect to the positions,
     d(F·v)/dx; (2) the gradients, with respect to every parameter the patch leaves in place, of a loss on energy
     and forces computed with create_graph (MACE's training=True).  Tolerance: 1e-4 relative to the largest
@@ -133,8 +132,9 @@ def test_double_backward_hessian_and_force_loss(config):
     report = patch_model(met, verbose=False, double_backward=True)
     assert 'spherical_harmonics' in report['patched'] and 'radial_embedding' in report['patched'], report
     assert any(n.endswith('conv_tp') for n in report['patched']), report
+    assert 'edge_geometry' in report['patched'], report
     skipped = dict(report['skipped'])                # the drop-ins without second-order kernels
-    assert 'double_backward' in skipped['edge_geometry'] and 'interactions.0.conv_tp_weights' in skipped
+    assert 'double_backward' in skipped['interactions.0.conv_tp_weights'], skipped
     st = factory.make_structure(seed=4)
     batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
     v = np.random.default_rng(0).normal(size=(len(st), 3))
