@@ -77,7 +77,7 @@ _SIGS = {
     'mh_sh_bwd2': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_emb_jvp': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_emb_bwd2': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
-    'mh_geom_jvp': (ctypes.c_int, [_P] * 10 + [ctypes.c_int64, _P]),
+    'mh_geom_jvp': (ctypes.c_int, [_P] * 11 + [ctypes.c_int64, _P]),
     'mh_sc_bwd2': (ctypes.c_int, [_P] * 7 + [_I, _I, _P]),
     'mh_sc_bwd': (ctypes.c_int, [_P] * 6 + [_I, _P]),
 }
