@@ -31,6 +31,29 @@ def test_library_loads_and_exports_header_symbols():
     assert lib.mh_last_error() is not None
 
 
+def test_c_abi_rejects_bad_arguments_before_any_launch():
+    """Argument errors of the entry points come back as a status and a message, checked before anything reaches the
+    GPU (so this runs without one)."""
+    lib = _native.load()
+    cases = [
+        (lambda: lib.mh_graph_build(None, None, 5, 0, None, None, None, None, None, None), 'zero nodes'),
+        (lambda: lib.mh_graph_build(None, None, 5, 3, None, None, None, None, None, None), 'NULL'),
+        (lambda: lib.mh_graph_build(None, None, -1, 3, None, None, None, None, None, None), 'bad sizes'),
+        (lambda: lib.mh_sc_jvp(None, None, None, None, None, None, 4, 2, None), 'layout'),
+        (lambda: lib.mh_sc_bwd2(None, None, None, None, None, None, None, 4, 7, None), 'layout'),
+        (lambda: lib.mh_sh_jvp(None, None, None, None, 10, None), 'NULL'),
+        (lambda: lib.mh_sh_bwd2(None, None, None, None, None, 10, None), 'NULL'),
+        (lambda: lib.mh_emb_jvp(None, None, None, None, None, 10, None), 'NULL'),
+        (lambda: lib.mh_emb_bwd2(None, None, None, None, None, None, 10, None), 'NULL'),
+        (lambda: lib.mh_geom_jvp(None, *([None] * 10), 10, None), 'NULL'),
+        (lambda: lib.mh_lin_fwd(None, None, None, None, None, None, 1.0, 10, None), 'NULL'),
+        (lambda: lib.mh_readout_bwd(None, None, None, None, 10, None), 'NULL'),
+    ]
+    for call, msg in cases:
+        assert call() != 0
+        assert msg in lib.mh_last_error().decode(), (msg, lib.mh_last_error())
+
+
 def test_compile_errors_are_reported():
     with pytest.raises(RuntimeError, match='hipRTC compile'):
         _native.compile_source('extern "C" __global__ void k() { this is not HIP; }')
