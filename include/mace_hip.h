@@ -79,7 +79,9 @@ enum mh_kernel_kind {
     MH_EMB_JVP = 40,     /* radial embedding: derivative along a direction of the lengths           */
     MH_EMB_BWD2 = 41,    /* derivative of its length gradient along that direction                  */
     MH_GEOM_JVP = 42,    /* edge geometry, behind a double backward: per-edge second-order terms     */
-    MH_NUM_KINDS = 43
+    MH_READOUT_JVP = 43, /* SiLU readout head: derivative of the energy along a direction of x       */
+    MH_READOUT_BWD2 = 44,/* derivative of its input gradient along that direction                   */
+    MH_NUM_KINDS = 45
 };
 
 /* flags of mh_conv_bwd */
@@ -255,6 +257,13 @@ int mh_emb_bwd2(mh_module* m, const float* len, const float* dlen, const float* 
 int mh_geom_jvp(mh_module* m, const float* vec, const float* len, const float* ggpos, const float* ggshifts,
                 const int32_t* send, const int32_t* recv, const float* glen, float* dgvec, float* dglen, float* h,
                 int64_t E, void* stream);
+
+/* Second derivatives of a SiLU readout head, behind a double backward (v [N, Din] a direction of x): mh_readout_jvp
+ * writes de = (de/dx) v [N]; mh_readout_bwd2 the derivative of mh_readout_bwd's gx along v for the given g [N]
+ * (zeros outside the scalar block).  One thread per node; bind MH_READOUT_JVP / MH_READOUT_BWD2 with 256 threads
+ * and 256 nodes per block.  No reference counterpart (the readouts stay on PyTorch there). */
+int mh_readout_jvp(mh_module* m, const float* x, const float* v, float* de, int64_t N, void* stream);
+int mh_readout_bwd2(mh_module* m, const float* x, const float* v, const float* g, float* gx, int64_t N, void* stream);
 
 /* Node-wise equivariant linear out[n] = L(x[n], attrs[n]) for N nodes (x [N, Din], out [N, Dout], fp32, the e3nn
  * irreps layout [.., u * (2l+1) + m] per block).  Without attrs (attrs NULL) it is e3nn's o3.Linear:

@@ -87,7 +87,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 21; }
+int mh_version(void) { return 22; }
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -378,6 +378,18 @@ int mh_geom_jvp(mh_module* m, const float* vec, const float* len, const float* g
     if (E > 0 && (!vec || !len || !send || !recv || !dgvec || !dglen || !h)) return fail(-1, "mh_geom_jvp: NULL operand");
     void* args[] = {&vec, &len, &ggpos, &ggshifts, &send, &recv, &glen, &dgvec, &dglen, &h, &E};
     return launch(m, MH_GEOM_JVP, E, args, stream, "mh_geom_jvp");
+}
+
+int mh_readout_jvp(mh_module* m, const float* x, const float* v, float* de, int64_t N, void* stream) {
+    if (N > 0 && (!x || !v || !de)) return fail(-1, "mh_readout_jvp: NULL operand");
+    void* args[] = {&x, &v, &de, &N};
+    return launch(m, MH_READOUT_JVP, N, args, stream, "mh_readout_jvp");
+}
+
+int mh_readout_bwd2(mh_module* m, const float* x, const float* v, const float* g, float* gx, int64_t N, void* stream) {
+    if (N > 0 && (!x || !v || !g || !gx)) return fail(-1, "mh_readout_bwd2: NULL operand");
+    void* args[] = {&x, &v, &g, &gx, &N};
+    return launch(m, MH_READOUT_BWD2, N, args, stream, "mh_readout_bwd2");
 }
 
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,

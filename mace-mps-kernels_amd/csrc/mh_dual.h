@@ -42,3 +42,4 @@ MH_HD inline mh_dual sqrtf(mh_dual a) {
 MH_HD inline mh_dual fmaxf(mh_dual a, float c) { return a.v >= c ? a : mh_dual(c); }
 MH_HD inline mh_dual sinf(mh_dual a) { return mh_dual(sinf(a.v), cosf(a.v) * a.d); }
 MH_HD inline mh_dual cosf(mh_dual a) { return mh_dual(cosf(a.v), -sinf(a.v) * a.d); }
+MH_HD inline mh_dual expf(mh_dual a) { const float e = expf(a.v); return mh_dual(e, e * a.d); }

@@ -83,8 +83,8 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     ``double_backward`` (default off, as in the reference, where a backward under ``create_graph=True`` raises)
     makes the patched modules' gradients differentiable once more, for second derivatives with respect to the
     inputs: Hessian-vector products and force constants, or force and stress terms of a loss differentiated with
-    respect to parameters the patch leaves on e3nn.  Every drop-in takes it except the radial MLPs and the SiLU
-    readout heads, which have no second-order kernels and are then left on e3nn and reported in ``skipped``.  The patched
+    respect to parameters the patch leaves on e3nn.  Every drop-in takes it except the radial MLPs, which have no
+    second-order kernels and are then left on e3nn and reported in ``skipped``.  The patched
     modules hold their weights as constants: no gradient reaches those weights, with or without it."""
     # a fully patched model may hold no parameters any more (the drop-ins keep their weights as buffers)
     p = next((t for t in itertools.chain(model.parameters(), model.buffers()) if t.is_floating_point()), None)
@@ -212,7 +212,6 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             if ok:
                 try:
                     new = HipReadout(ro, device=dev)
-                    new.double_backward = double_backward      # ValueError for a SiLU head
                 except ValueError as e:
                     ok, why = False, str(e)
             if not ok:
@@ -247,12 +246,10 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             model._mh_geometry_double_backward = True
         for mod in model.modules():
             if isinstance(mod, (HipConvTP, HipSymmetricContraction, HipNodeLinear, HipReshapeIrreps,
-                                HipSphericalHarmonics, HipRadialEmbedding)):
+                                HipSphericalHarmonics, HipRadialEmbedding, HipReadout)):
                 mod.double_backward = True
                 if hasattr(mod, 'second_module'):
                     mod.second_module()   # compiled now rather than inside the first double backward
-            elif isinstance(mod, HipReadout) and mod.spec.kind == 'linear':
-                mod.double_backward = True
     if verbose:
         for name, why in skipped:
             warnings.warn(f'mace_hip_kernels: kept e3nn for {name}: {why}')

@@ -22,9 +22,9 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD, \
     MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI, MH_READOUT_FWD, MH_READOUT_BWD, MH_SC_JVP, MH_SC_BWD2, \
     MH_SC_JVP_I, MH_SC_BWD2_I, MH_CSR_FILL, MH_CSR_COUNT, MH_CSR_SCAN, MH_CSR_SCATTER, MH_CSR_RANK, MH_SH_JVP, \
-    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP = range(43)
+    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2 = range(45)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 21
+ABI_VERSION = 22
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -78,6 +78,8 @@ _SIGS = {
     'mh_emb_jvp': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_emb_bwd2': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
     'mh_geom_jvp': (ctypes.c_int, [_P] * 11 + [ctypes.c_int64, _P]),
+    'mh_readout_jvp': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
+    'mh_readout_bwd2': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_sc_bwd2': (ctypes.c_int, [_P] * 7 + [_I, _I, _P]),
     'mh_sc_bwd': (ctypes.c_int, [_P] * 6 + [_I, _P]),
 }

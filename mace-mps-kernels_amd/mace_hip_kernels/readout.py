@@ -232,6 +232,50 @@ def source(spec):
     return '\n'.join(L)
 
 
+def source_second(spec):
+    """HIP source of the SiLU head's second-order kernels behind a double backward (one thread per node, plain
+    loops, dual numbers): ``ro_jvp`` writes de = (de/dx) v, ``ro_bwd2`` the derivative of the input gradient along v
+    for a given dL/de (a Hessian-vector product of g e(x)), zeros outside the scalar block.  The head is
+        z_j = sum_k x_k W1[k, j],  e = sum_j w2_j c z_j sigmoid(z_j)."""
+    assert spec.kind == 'mlp'
+    C0, o0, Din, H = spec.C0, spec.o0, spec.Din, spec.H
+    c = _lit(spec.c)
+    L = [_native.device_header(), _native.dual_header(), _table('ro_w1', spec.W1), _table('ro_w2', spec.w2), '']
+    head = ['  const long long n = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * BLOCK2 + threadIdx.x;',
+            '  if (n >= N) return;',
+            f'  const float* __restrict__ xr = x + n * {Din} + {o0};',
+            f'  const float* __restrict__ vr = v + n * {Din} + {o0};',
+            f'  mh_dual z[{H}];',
+            f'  for (int j = 0; j < {H}; ++j) z[j] = mh_dual(0.f);',
+            f'  for (int k = 0; k < {C0}; ++k) {{',
+            '    const mh_dual xk(xr[k], vr[k]);',
+            f'    for (int j = 0; j < {H}; ++j) z[j] += xk * ro_w1[k * {H} + j];',
+            '  }']
+    L += ['#define BLOCK2 256',
+          f'extern "C" __global__ __launch_bounds__(BLOCK2) void {spec.kname("ro_jvp")}(const float* __restrict__ x,',
+          '    const float* __restrict__ v, float* __restrict__ de, long long N) {'] + head
+    L += ['  mh_dual e(0.f);',
+          f'  for (int j = 0; j < {H}; ++j) e += ro_w2[j] * ({c} * z[j] * (1.f / (1.f + expf(-z[j]))));',
+          '  de[n] = e.d;', '}', '']
+    L += [f'extern "C" __global__ __launch_bounds__(BLOCK2) void {spec.kname("ro_bwd2")}(const float* __restrict__ x,',
+          '    const float* __restrict__ v, const float* __restrict__ g, float* __restrict__ gx, long long N) {'] + head
+    L += ['  const float gn = g[n];',
+          f'  mh_dual q[{H}];',
+          f'  for (int j = 0; j < {H}; ++j) {{',
+          '    const mh_dual sg = 1.f / (1.f + expf(-z[j]));',
+          f'    q[j] = gn * ro_w2[j] * {c} * (sg * (1.f + z[j] * (1.f - sg)));',
+          '  }',
+          f'  float* __restrict__ gr = gx + n * {Din};',
+          f'  for (int k = 0; k < {C0}; ++k) {{',
+          '    mh_dual a(0.f);',
+          f'    for (int j = 0; j < {H}; ++j) a += q[j] * ro_w1[k * {H} + j];',
+          f'    gr[{o0} + k] = a.d;',
+          '  }',
+          f'  for (int k = 0; k < {Din - C0}; ++k) gr[k < {o0} ? k : k + {C0}] = 0.f;',
+          '}', '']
+    return '\n'.join(L)
+
+
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
                     'autograd Hessian) is not enabled for this HIP module; patch with '
                     'patch_model(model, double_backward=True)')
@@ -251,42 +295,79 @@ class _ReadoutFn(torch.autograd.Function):
         out = torch.empty(N, 1, device=x.device, dtype=torch.float32)
         _native.launch(f'ro_fwd[{op.tag}]', _native.load().mh_readout_fwd, op.module.handle, _native.ptr(x2),
                        _native.ptr(out), N, _native.stream_of(x2))
-        ctx.save_for_backward(x2)
-        ctx.op, ctx.lead = op, lead
+        ctx.save_for_backward(x)             # the input itself: a double backward differentiates through it
+        ctx.op = op
         return out.reshape(*lead, 1)
 
     @staticmethod
     def backward(ctx, g):
-        x2, = ctx.saved_tensors
+        x, = ctx.saved_tensors
         op = ctx.op
         if torch.is_grad_enabled():          # only true under create_graph=True
             if not op.double_backward:
                 raise RuntimeError(_DOUBLE_BACKWARD)
-            return _ReadoutAdjFn.apply(g, x2, op, ctx.lead), None
-        return _readout_bwd(op, x2, g, ctx.lead), None
+            if op.spec.kind == 'linear':
+                return _ReadoutAdjFn.apply(g, x.detach(), op), None
+            return _ReadoutMLPAdjFn.apply(g, x, op), None
+        return _readout_bwd(op, x, g), None
 
 
-def _readout_bwd(op, x2, g, lead):
+def _readout_bwd(op, x, g):
+    x2 = x.reshape(-1, op.spec.Din).contiguous()
     g2 = g.reshape(-1).contiguous()
     gx = torch.empty_like(x2)
     _native.launch(f'ro_bwd[{op.tag}]', _native.load().mh_readout_bwd, op.module.handle, _native.ptr(x2),
                    _native.ptr(g2), _native.ptr(gx), x2.shape[0], _native.stream_of(x2))
-    return gx.reshape(*lead, op.spec.Din)
+    return gx.reshape(x.shape)
 
 
 class _ReadoutAdjFn(torch.autograd.Function):
     """The linear head's input gradient g w^T as a function of g, for a double backward: it does not depend on x,
-    and d<ggx, g w^T>/dg = ggx w, the head itself (through _ReadoutFn, so higher orders follow).  Only linear heads
-    (``HipReadout.double_backward`` is refused for the SiLU heads)."""
+    and d<ggx, g w^T>/dg = ggx w, the head itself (through _ReadoutFn, so higher orders follow)."""
 
     @staticmethod
-    def forward(ctx, g, x2, op, lead):
+    def forward(ctx, g, x, op):
         ctx.op = op
-        return _readout_bwd(op, x2, g, lead)
+        return _readout_bwd(op, x, g)
 
     @staticmethod
     def backward(ctx, ggx):
-        return _ReadoutFn.apply(ggx, ctx.op), None, None, None
+        return _ReadoutFn.apply(ggx, ctx.op), None, None
+
+
+class _ReadoutMLPAdjFn(torch.autograd.Function):
+    """The SiLU head's input gradient as a function of (g, x), for a double backward: with ggx the incoming
+    gradient, d<ggx, dL/dx>/dg = (de/dx) ggx (``ro_jvp``) and d<ggx, dL/dx>/dx the Hessian-vector product
+    (``ro_bwd2``).  Third derivatives are not provided."""
+
+    @staticmethod
+    def forward(ctx, g, x, op):
+        ctx.save_for_backward(g, x)
+        ctx.op = op
+        return _readout_bwd(op, x, g)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggx):
+        g, x = ctx.saved_tensors
+        op = ctx.op
+        m = op.second_module()
+        x2 = x.reshape(-1, op.spec.Din).contiguous()
+        v2 = ggx.reshape(-1, op.spec.Din).contiguous()
+        N, P, lib = x2.shape[0], _native.ptr, _native.load()
+        dg = dx = None
+        if ctx.needs_input_grad[0]:
+            de = torch.empty(N, device=x2.device, dtype=torch.float32)
+            _native.launch(f'ro_jvp[{op.tag}]', lib.mh_readout_jvp, m.handle, P(x2), P(v2), P(de), N,
+                           _native.stream_of(x2))
+            dg = de.reshape(g.shape)
+        if ctx.needs_input_grad[1]:
+            g2 = g.reshape(-1).contiguous()
+            gx = torch.empty_like(x2)
+            _native.launch(f'ro_bwd2[{op.tag}]', lib.mh_readout_bwd2, m.handle, P(x2), P(v2), P(g2), P(gx), N,
+                           _native.stream_of(x2))
+            dx = gx.reshape(x.shape)
+        return dg, dx, None
 
 
 class HipReadout(torch.nn.Module):
@@ -304,18 +385,23 @@ class HipReadout(torch.nn.Module):
                 _native.MH_READOUT_BWD: (self.spec.kname('ro_bwd'), BLOCK, BLOCK // LANES)})
         self.original = [mod]
         self.tag = 'readout'
-        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; linear heads only
-        self._double_backward = False
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set
+        self.double_backward = False
+        self._device = dev
+        self._second = None
 
-    @property
-    def double_backward(self):
-        return self._double_backward
-
-    @double_backward.setter
-    def double_backward(self, on):
-        if on and self.spec.kind != 'linear':
-            raise ValueError('mace_hip_kernels: only linear readout heads have a double backward')
-        self._double_backward = bool(on)
+    def second_module(self):
+        """The SiLU head's second-order kernels (``ro_jvp``, ``ro_bwd2``), compiled on first use; a linear head
+        needs none (its double backward is the head itself)."""
+        if self.spec.kind == 'linear':
+            return None
+        if self._second is None:
+            code = _native.compile_source(source_second(self.spec))
+            with torch.cuda.device(self._device):
+                self._second = _native.Module(code, {
+                    _native.MH_READOUT_JVP: (self.spec.kname('ro_jvp'), 256, 256),
+                    _native.MH_READOUT_BWD2: (self.spec.kname('ro_bwd2'), 256, 256)})
+        return self._second
 
     def forward(self, x, heads=None):
         return _ReadoutFn.apply(x, self)

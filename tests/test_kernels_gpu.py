@@ -942,7 +942,8 @@ def test_sc_double_backward_vs_oracle(layout):
 def test_linear_double_backward():
     """Node linears (o3.Linear and skip_tp) patched with double_backward: the input gradient does not depend on x,
     and its derivative with respect to g along v is the map applied to v (checked against float64 runs of the
-    e3nn module); a linear readout head likewise."""
+    e3nn module); the readout heads likewise (the SiLU head's second-order kernels against float64 double
+    backward)."""
     from mace_hip_kernels import HipReadout
     dev = _dev()
     m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
@@ -966,11 +967,23 @@ def test_linear_double_backward():
         want = m64(torch.tensor(v), torch.tensor(a)) if s.V else m64(torch.tensor(v))
         assert d_x is None
         assert _rel(d_g.double().cpu().numpy(), want.detach().numpy()) < LIN_TOL
+    print('[case] SiLU readout double backward', flush=True)
+    ro = HipReadout(m.readouts[1], device=dev)
+    ro.double_backward = True
+    xt = torch.tensor(rng.normal(size=(n, ro.spec.Din)), dtype=torch.float32, device=dev, requires_grad=True)
+    gt = torch.tensor(rng.normal(size=(n, 1)), dtype=torch.float32, device=dev, requires_grad=True)
+    v = rng.normal(size=(n, ro.spec.Din))
+    gx, = torch.autograd.grad(ro(xt), xt, gt, create_graph=True)
+    d_g, d_x = torch.autograd.grad((gx * torch.tensor(v, dtype=torch.float32, device=dev)).sum(), (gt, xt))
+    r64 = copy.deepcopy(m.readouts[1]).double()
+    x64, g64 = xt.detach().double().cpu().requires_grad_(True), gt.detach().double().cpu().requires_grad_(True)
+    gx64, = torch.autograd.grad(r64(x64), x64, g64, create_graph=True)
+    w_g, w_x = torch.autograd.grad((gx64 * torch.tensor(v)).sum(), (g64, x64))
+    assert _rel(d_g.double().cpu().numpy(), w_g.numpy()) < LIN_TOL
+    assert _rel(d_x.double().cpu().numpy(), w_x.numpy()) < LIN_TOL
     print('[case] linear readout double backward', flush=True)
     ro = HipReadout(m.readouts[0], device=dev)
     ro.double_backward = True
-    with pytest.raises(ValueError):
-        HipReadout(m.readouts[1], device=dev).double_backward = True
     xt = torch.tensor(rng.normal(size=(n, ro.spec.Din)), dtype=torch.float32, device=dev, requires_grad=True)
     gt = torch.tensor(rng.normal(size=(n, 1)), dtype=torch.float32, device=dev, requires_grad=True)
     v = rng.normal(size=(n, ro.spec.Din))

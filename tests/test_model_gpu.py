@@ -118,8 +118,8 @@ def test_double_backward_raises():
 
 @pytest.mark.parametrize('config', ['l3_corr3_fullcg', 'l3_corr3_l2hidden'])
 def test_double_backward_hessian_and_force_loss(config):
-    """patch_model(double_backward=True): every drop-in but the radial MLPs and SiLU readout heads differentiates
-    twice (those stay on e3nn and are reported).  Against the
+    """patch_model(double_backward=True): every drop-in but the radial MLPs differentiates twice (those stay on e3nn
+    and are reported).  Against the
     unpatched model in float64: (1) a Hessian-vector product of the energy with respect to the positions,
     d(F·v)/dx; (2) the gradients, with respect to every parameter the patch leaves in place, of a loss on energy
     and forces computed with create_graph (MACE's training=True).  Tolerance: 1e-4 relative to the largest
@@ -133,6 +133,7 @@ def test_double_backward_hessian_and_force_loss(config):
     assert 'spherical_harmonics' in report['patched'] and 'radial_embedding' in report['patched'], report
     assert any(n.endswith('conv_tp') for n in report['patched']), report
     assert 'edge_geometry' in report['patched'], report
+    assert not any('double_backward' in why and not n.endswith('conv_tp_weights') for n, why in report['skipped'])
     skipped = dict(report['skipped'])                # the drop-ins without second-order kernels
     assert 'double_backward' in skipped['interactions.0.conv_tp_weights'], skipped
     st = factory.make_structure(seed=4)
