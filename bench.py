@@ -73,8 +73,9 @@ def _time_train(model, batch, steps, warmup, sync):
     return (time.perf_counter() - t0) / steps
 
 
-def _kernel_table(met, batch, n_real_edges, summary):
-    """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only)."""
+def _kernel_table(met, batch, n_real_edges, summary, symbols):
+    """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only); ``symbols`` are the kernels each
+    tag's launches ran, as the C ABI's launch log recorded them."""
     import torch
     from mace_hip_kernels import (HipConvTP, HipNodeLinear, HipRadialEmbedding, HipRadialMLP, HipReadout,
                                   HipReshapeIrreps, HipSphericalHarmonics, HipSymmetricContraction)
@@ -86,60 +87,68 @@ def _kernel_table(met, batch, n_real_edges, summary):
             s = m.spec
             bf, bb = s.bytes(n, n_real_edges)
             ff, fb = s.flops()
-            rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul,
-                                          s.kname('conv_fwdc' if m.fuse_cutoff else 'conv_fwd'))
-            # MACE's blocks pass tp_weights = W0 * cutoff, which takes the factored receiver-ordered kernel
-            bwd_sym = (f"{s.kname('conv_bwdrc' if m.fuse_cutoff else 'conv_bwdr')}+{s.kname('conv_gxsum')}"
-                       if m.bwd_recv or m.fuse_cutoff else s.kname('conv_bwd'))
-            rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul, bwd_sym)
+            rows[f'conv_fwd[{m.tag}]'] = (bf, ff * n_real_edges * s.mul)
+            rows[f'conv_bwd[{m.tag}]'] = (bb, fb * n_real_edges * s.mul)
         elif isinstance(m, HipSymmetricContraction):
             s = m.spec
             bf, bb = s.bytes(n, n_elem_used)
             ff, fb = s.flops()
-            sfx = 'i' if m.last_layout == 'irreps' else ''      # fed by an unformed reshape_irreps
-            rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C, s.kname('sc_fwd' + sfx))
-            rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C, s.kname('sc_bwd' + sfx))
+            rows[f'sc_fwd[{m.tag}]'] = (bf, ff * n * s.C)
+            rows[f'sc_bwd[{m.tag}]'] = (bb, fb * n * s.C)
         elif isinstance(m, HipSphericalHarmonics):
             s = m.spec                                  # every edge of the padded list is evaluated
             bf, bb = s.bytes(batch['edge_index'].shape[1])
-            rows[f'sh_fwd[{m.tag}]'] = (bf, 0, s.kname('sh_fwd'))
-            rows[f'sh_bwd[{m.tag}]'] = (bb, 0, s.kname('sh_bwd'))
+            rows[f'sh_fwd[{m.tag}]'] = (bf, 0)
+            rows[f'sh_bwd[{m.tag}]'] = (bb, 0)
         elif isinstance(m, HipNodeLinear):
             s = m.spec
             bf, bb = s.bytes(n)
-            rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n), s.kname('lin_fwd'))
-            rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n), s.kname('lin_bwd'))
+            rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n))
+            rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n))
         elif isinstance(m, HipReshapeIrreps):
             nb = 2 * 4 * n * m.spec.dim                 # a permutation: the rows read once and written once
-            rows[f'perm_fwd[{m.tag}]'] = (nb, 0, m.spec.kname('perm_fwd'))
-            rows[f'perm_bwd[{m.tag}]'] = (nb, 0, m.spec.kname('perm_bwd'))
+            rows[f'perm_fwd[{m.tag}]'] = (nb, 0)
+            rows[f'perm_bwd[{m.tag}]'] = (nb, 0)
         elif isinstance(m, HipRadialEmbedding):
             bf, bb = m.spec.bytes(batch['edge_index'].shape[1])
-            rows[f'emb_fwd[{m.tag}]'] = (bf, 0, m.spec.kname('emb_fwd'))
-            rows[f'emb_bwd[{m.tag}]'] = (bb, 0, m.spec.kname('emb_bwd'))
+            rows[f'emb_fwd[{m.tag}]'] = (bf, 0)
+            rows[f'emb_bwd[{m.tag}]'] = (bb, 0)
         elif isinstance(m, HipReadout):
             bf, bb = m.spec.bytes(n)
-            rows[f'ro_fwd[{m.tag}]'] = (bf, 0, m.spec.kname('ro_fwd'))
-            rows[f'ro_bwd[{m.tag}]'] = (bb, 0, m.spec.kname('ro_bwd'))
+            rows[f'ro_fwd[{m.tag}]'] = (bf, 0)
+            rows[f'ro_bwd[{m.tag}]'] = (bb, 0)
         elif isinstance(m, HipRadialMLP):
             s = m.spec                                  # every edge of the padded list is evaluated
             E = batch['edge_index'].shape[1]
             bf, bb = s.bytes(E)
-            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(E), s.kname('mlp_fwd'))
-            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(E), s.kname('mlp_bwd'))
+            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(E))
+            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(E))
     # edge geometry: positions, shifts and the edge list in, vectors and lengths out; backward: vectors, lengths and
     # their gradients plus both CSRs in, the position gradient out
     E = batch['edge_index'].shape[1]
-    rows['geom_fwd'] = (4 * (3 * n + 3 * E + 2 * E + 3 * E + E), 0, 'geom_fwd')
-    rows['geom_bwd'] = (4 * (8 * E + 2 * (n + 1) + 2 * E + 3 * n), 0, 'geom_bwd')
+    rows['geom_fwd'] = (4 * (3 * n + 3 * E + 2 * E + 3 * E + E), 0)
+    rows['geom_bwd'] = (4 * (8 * E + 2 * (n + 1) + 2 * E + 3 * n), 0)
     out = {}
     for tag, (cnt, ms) in summary.items():
-        nbytes, flops, sym = rows.get(tag, (0, 0, None))
-        out[tag] = dict(symbol=sym, launches=cnt, ms=round(ms, 5), bytes=int(nbytes), flops=int(flops),
+        nbytes, flops = rows.get(tag, (0, 0))
+        out[tag] = dict(symbol='+'.join(symbols.get(tag, [])) or None, launches=cnt, ms=round(ms, 5),
+                        bytes=int(nbytes), flops=int(flops),
                         gbs=round(nbytes / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
                         tflops=round(flops / (ms * 1e-3) / 1e12, 2) if ms > 0 else None)
     del torch
     return out
+
+
+def _cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), else the platform's machine string."""
+    try:
+        with open('/proc/cpuinfo') as fh:
+            for line in fh:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
@@ -169,7 +178,7 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
                 sample=f'unpatched e3nn-path restatement (mace_lite, fp32, torch CPU, {cores} threads) on {k} of '
                        f'the {n_structs} structures ({n_at} atoms, {int(keep.sum())} edges), {steps} timed calls '
                        f'after 1 warm-up, scaled x{n_structs / k:g} to one batch call',
-                cpu=platform.processor() or platform.machine(), seconds=round(dt * steps, 2))
+                cpu=_cpu_model(), seconds=round(dt * steps, 2))
 
 
 # symbol prefixes of this package's generated kernels
@@ -518,7 +527,7 @@ def main():
     with _native.timing() as tm:
         for _ in range(a.steps):
             met(batch, compute_force=True)
-    kern = _kernel_table(met, batch, n_real, tm.summary())
+    kern = _kernel_table(met, batch, n_real, tm.summary(), tm.symbols)
     per_call = {k: v['ms'] * v['launches'] / a.steps for k, v in kern.items()}
     dom = max(per_call, key=per_call.get)
     d = kern[dom]

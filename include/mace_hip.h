@@ -81,7 +81,8 @@ enum mh_kernel_kind {
     MH_GEOM_JVP = 42,    /* edge geometry, behind a double backward: per-edge second-order terms     */
     MH_READOUT_JVP = 43, /* SiLU readout head: derivative of the energy along a direction of x       */
     MH_READOUT_BWD2 = 44,/* derivative of its input gradient along that direction                   */
-    MH_NUM_KINDS = 45
+    MH_CSR_SORT = 45,    /* graph build: sort each segment longer than the counting kernel handles  */
+    MH_NUM_KINDS = 46
 };
 
 /* flags of mh_conv_bwd */
@@ -94,6 +95,15 @@ const char* mh_last_error(void);
 
 /* ABI version of this header (bumped on any signature change). */
 int mh_version(void);
+
+/* Launch log of the calling thread, for profiling and tests that check which kernels ran: while enabled, every
+ * successful launch appends the symbol bound to the launched slot.  mh_launch_log(1) enables it, mh_launch_log(0)
+ * disables and clears it; both return the previous state.  mh_launch_log_take copies the names, each followed by
+ * ';', oldest first, into buf (NUL-terminated) and clears the log when it fitted; it returns the log's length (call
+ * with buf NULL to size the buffer).  No reference counterpart (Metal kernels are named in the reference's own
+ * source). */
+int mh_launch_log(int enable);
+size_t mh_launch_log_take(char* buf, size_t len);
 
 /* Path of the HIP runtime library this .so is bound to (must be the one torch loaded). */
 const char* mh_hip_runtime_path(void);
@@ -219,7 +229,8 @@ int mh_sc_bwd2(mh_module* m, const float* X, const float* V, const int32_t* elem
  * and 0 otherwise.  work: 4 (n + 1) + 2 E int32 of caller-owned scratch.  Device work only (no host
  * synchronisation, no memset), so it can be captured in a HIP graph; results do not depend on the order in which
  * atomics land.  Bind MH_CSR_FILL / _COUNT / _SCATTER / _RANK with 256 threads and rows_per_block 256, MH_CSR_SCAN
- * with 1024 threads and rows_per_block 1, all with grid y = 2 (mh_module_bind_grid).  Replaces the reference's
+ * with 1024 threads and rows_per_block 1, MH_CSR_SORT with 256 threads and rows_per_block 1 (one workgroup per node),
+ * all with grid y = 2 (mh_module_bind_grid).  Replaces the reference's
  * csr_by (conv.py:229-235: a stable argsort per CSR and per layer, then a count). */
 int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys, int32_t* rowptr,
                    int32_t* eids, int32_t* work, int32_t* bad, void* stream);

@@ -23,9 +23,12 @@
 namespace {
 
 thread_local std::string g_err;
+thread_local bool g_log_on = false;      // launch log (mh_launch_log): bound names of the kernels launched
+thread_local std::string g_log;
 
 struct Kernel {
     hipFunction_t fn = nullptr;
+    std::string name;                      // the symbol bound to this slot
     int block = 0;
     int rows_per_block = 1;
     int grid_y = 1;          // second grid dimension (a fixed count: output blocks of a node linear)
@@ -78,6 +81,10 @@ int launch(mh_module* m, int kind, int64_t rows, void** args, void* stream, cons
                                          static_cast<unsigned>(k.block), 1, 1, 0, static_cast<hipStream_t>(stream), args,
                                          nullptr);
     if (e != hipSuccess) return hip_fail(e, what);
+    if (g_log_on) {
+        g_log += k.name;
+        g_log += ';';
+    }
     return 0;
 }
 
@@ -87,7 +94,25 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 22; }
+int mh_version(void) { return 23; }
+
+int mh_launch_log(int enable) {
+    const int was = g_log_on ? 1 : 0;
+    g_log_on = enable != 0;
+    if (!g_log_on) g_log.clear();
+    return was;
+}
+
+size_t mh_launch_log_take(char* buf, size_t len) {
+    const size_t n = g_log.size();
+    if (buf && len) {
+        const size_t c = n < len - 1 ? n : len - 1;
+        std::memcpy(buf, g_log.data(), c);
+        buf[c] = '\0';
+        if (c == n) g_log.clear();
+    }
+    return n;
+}
 
 const char* mh_hip_runtime_path(void) {
     static std::string path;
@@ -176,6 +201,7 @@ int mh_module_bind_grid(mh_module* m, int kind, const char* name, int block_thre
     hipFunction_t fn = nullptr;
     MH_HIP(hipModuleGetFunction(&fn, m->mod, name));
     m->k[kind].fn = fn;
+    m->k[kind].name = name;
     m->k[kind].block = block_threads;
     m->k[kind].rows_per_block = rows_per_block;
     m->k[kind].grid_y = grid_y;
@@ -330,6 +356,10 @@ int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n
     {
         void* args[] = {&keys, &cursor, &tmp, &E, &n};
         if ((rc = launch(m, MH_CSR_SCATTER, E, args, stream, "mh_graph_build"))) return rc;
+    }
+    {
+        void* args[] = {&rowptr, &tmp, &E, &n};
+        if ((rc = launch(m, MH_CSR_SORT, n, args, stream, "mh_graph_build"))) return rc;
     }
     void* args[] = {&keys, &rowptr, &tmp, &eids, &E, &n};
     return launch(m, MH_CSR_RANK, E, args, stream, "mh_graph_build");

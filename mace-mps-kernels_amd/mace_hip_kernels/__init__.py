@@ -135,8 +135,15 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             patched.append(name)
     no2 = 'no second-order kernels (patched with double_backward=True)'
     if double_backward:
-        if radial_mlp:
-            skipped += [(f'interactions.{i}.conv_tp_weights', no2) for i in range(len(getattr(model, 'interactions', [])))]
+        # a radial MLP an earlier call replaced goes back to e3nn: its kernels have no differentiable backward
+        for i, blk in enumerate(getattr(model, 'interactions', [])):
+            mlp = getattr(blk, 'conv_tp_weights', None)
+            restored = isinstance(mlp, HipRadialMLP)
+            if restored:
+                blk.conv_tp_weights = mlp.original[0]
+            if radial_mlp or restored:
+                skipped.append((f'interactions.{i}.conv_tp_weights',
+                                no2 + ('; the e3nn module an earlier patch replaced is restored' if restored else '')))
         radial_mlp = False
     if spherical_harmonics and hasattr(model, 'spherical_harmonics'):
         sh = model.spherical_harmonics

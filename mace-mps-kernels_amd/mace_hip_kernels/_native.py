@@ -22,9 +22,9 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD, \
     MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI, MH_READOUT_FWD, MH_READOUT_BWD, MH_SC_JVP, MH_SC_BWD2, \
     MH_SC_JVP_I, MH_SC_BWD2_I, MH_CSR_FILL, MH_CSR_COUNT, MH_CSR_SCAN, MH_CSR_SCATTER, MH_CSR_RANK, MH_SH_JVP, \
-    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2 = range(45)
+    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2, MH_CSR_SORT = range(46)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 22
+ABI_VERSION = 23
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -72,7 +72,9 @@ _SIGS = {
     'mh_sc_bwd_sorted': (ctypes.c_int, [_P] * 7 + [_I, _P]),
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
     'mh_sc_jvp': (ctypes.c_int, [_P] * 6 + [_I, _I, _P]),
-    'mh_graph_build': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 5),
+    'mh_graph_build': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 6),
+    'mh_launch_log': (ctypes.c_int, [ctypes.c_int]),
+    'mh_launch_log_take': (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
     'mh_sh_jvp': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
     'mh_sh_bwd2': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_emb_jvp': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
@@ -175,20 +177,34 @@ class Module:
                 pass
 
 
+def launch_log_take():
+    """Symbols of the kernels launched on this thread since the last call, oldest first (the C ABI's launch log)."""
+    lib = load()
+    n = lib.mh_launch_log_take(None, 0)
+    buf = ctypes.create_string_buffer(n + 1)
+    lib.mh_launch_log_take(buf, n + 1)
+    return [s for s in buf.value.decode().split(';') if s]
+
+
 class timing:
     """Context manager: while active, every kernel launch is bracketed by two HIP events recorded on the launch
-    stream; ``.records`` collects (tag, start, end).  Off by default (no events outside this context)."""
+    stream; ``.records`` collects (tag, start, end) and ``.symbols`` maps each tag to the kernel symbols its launches
+    ran, as the C ABI's launch log recorded them.  Off by default (no events outside this context)."""
     active = None
 
     def __init__(self):
         self.records = []
+        self.symbols = {}
 
     def __enter__(self):
         timing.active = self
+        self._was = load().mh_launch_log(1)
+        launch_log_take()
         return self
 
     def __exit__(self, *exc):
         timing.active = None
+        load().mh_launch_log(self._was)
 
     def summary(self):
         """{tag: (launches, mean ms)} (synchronises the device)."""
@@ -211,6 +227,10 @@ def launch(tag, fn, *args):
     check(fn(*args), tag)
     e.record()
     rec.records.append((tag, s, e))
+    syms = rec.symbols.setdefault(tag, [])
+    for name in launch_log_take():
+        if name not in syms:
+            syms.append(name)
 
 
 def ptr(t):

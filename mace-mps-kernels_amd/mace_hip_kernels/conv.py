@@ -164,9 +164,12 @@ def graph_source():
     """HIP source of the graph-build kernels behind ``mh_graph_build`` (both CSRs of an edge list, device work only).
     Each kernel handles one index row per grid row (blockIdx.y: 0 senders, 1 receivers).  Segments are filled in
     whatever order the atomics land and then ordered by edge id, so the result is what a stable sort by the index
-    gives (reference conv.py:229-235) and never depends on timing.  Ordering a segment of L edges costs L^2 reads
-    (each edge counts the smaller ids in its segment): ~40 per segment for MACE graphs."""
-    return _native.device_header() + r"""
+    gives (reference conv.py:229-235) and never depends on timing.  A segment of at most RANK_MAX edges is ordered by
+    counting (each edge counts the smaller ids in its segment, L reads per edge: ~40 for MACE graphs); a longer one
+    (a hub node, or padding edges all sent to one node) is sorted in place by one workgroup (``csr_sort_long``: a
+    bitonic network of ascending comparators, so comparators that reach past the segment's end are simply skipped,
+    O(L log^2 L) work, in LDS up to SORT_LDS edges) and then copied."""
+    return _native.device_header() + f"#define RANK_MAX {RANK_MAX}\n#define SORT_LDS {SORT_LDS}\n" + r"""
 extern "C" __global__ __launch_bounds__(256) void csr_fill(int* __restrict__ cnt, int* __restrict__ bad, int n) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   if (i <= n) cnt[(long long)blockIdx.y * (n + 1) + i] = 0;
@@ -233,13 +236,62 @@ extern "C" __global__ __launch_bounds__(256) void csr_rank(const int* __restrict
   const int e = tmp[r * E + p];
   const int k = keys[r * E + e];
   const int b = rowptr[r * (n + 1) + k], t = rowptr[r * (n + 1) + k + 1];
+  if (t - b > RANK_MAX) {                 // sorted in place by csr_sort_long
+    eids[r * E + p] = e;
+    return;
+  }
   int rank = 0;
   for (int q = b; q < t; ++q) rank += tmp[r * E + q] < e;
   eids[r * E + b + rank] = e;
 }
+
+// Comparator c of step (k, j) of an ascending-only bitonic network over P = 2^m slots: lo has bit j clear; the first
+// step of stage k pairs lo with its mirror image lo ^ (k - 1), the others with lo | j.  Every comparator puts the
+// smaller value at the lower index, so slots past the segment's end behave as +infinity and their comparators are
+// skipped.
+__device__ __forceinline__ void csr_cmp_pair(int c, int k, int j, int& lo, int& hi) {
+  lo = ((c & ~(j - 1)) << 1) | (c & (j - 1));
+  hi = j == (k >> 1) ? (lo ^ (k - 1)) : (lo | j);
+}
+
+extern "C" __global__ __launch_bounds__(256) void csr_sort_long(const int* __restrict__ rowptr,
+    int* __restrict__ tmp, long long E, int n) {
+  const int node = blockIdx.x;
+  if (node >= n) return;
+  const long long r = blockIdx.y;
+  const int b = rowptr[r * (n + 1) + node], L = rowptr[r * (n + 1) + node + 1] - b;
+  if (L <= RANK_MAX) return;
+  int P = 1;
+  while (P < L) P <<= 1;
+  int* __restrict__ seg = tmp + r * E + b;
+  __shared__ int s[SORT_LDS];
+  const bool in_lds = P <= SORT_LDS;
+  int* a = in_lds ? s : seg;
+  if (in_lds) {
+    for (int i = threadIdx.x; i < L; i += 256) s[i] = seg[i];
+    __syncthreads();
+  }
+  for (int k = 2; k <= P; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int c = threadIdx.x; c < (P >> 1); c += 256) {
+        int lo, hi;
+        csr_cmp_pair(c, k, j, lo, hi);
+        if (hi < L) {
+          const int x = a[lo], y = a[hi];
+          if (x > y) { a[lo] = y; a[hi] = x; }
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (in_lds)
+    for (int i = threadIdx.x; i < L; i += 256) seg[i] = s[i];
+}
 """
 
 
+RANK_MAX = 128             # longest segment ordered by counting in csr_rank; longer ones by csr_sort_long
+SORT_LDS = 8192            # longest segment csr_sort_long sorts in LDS (longer: in place in global memory)
 _GRAPH_MODULES = {}        # device index -> module of the graph-build kernels
 
 
@@ -253,7 +305,8 @@ def _graph_module(device):
                                       _native.MH_CSR_COUNT: ('csr_count', 256, 256, 2),
                                       _native.MH_CSR_SCAN: ('csr_scan', 1024, 1, 2),
                                       _native.MH_CSR_SCATTER: ('csr_scatter', 256, 256, 2),
-                                      _native.MH_CSR_RANK: ('csr_rank', 256, 256, 2)})
+                                      _native.MH_CSR_RANK: ('csr_rank', 256, 256, 2),
+                                      _native.MH_CSR_SORT: ('csr_sort_long', 256, 1, 2)})
         _GRAPH_MODULES[idx] = m
     return m
 

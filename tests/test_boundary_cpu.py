@@ -3,6 +3,7 @@ The drop-in boundary on the CPU (no GPU calls): the C-ABI library, the supports-
 patch_model (reference __init__.py:34-79, conv.py:31-51, symmetric.py:42-49), code generation for gfx950, the graph
 cache, and the golden kernel fixtures.
 """
+import ctypes
 import os
 import re
 
@@ -29,6 +30,53 @@ def test_library_loads_and_exports_header_symbols():
         assert hasattr(lib, name), name
     assert lib.mh_version() == _native.ABI_VERSION
     assert lib.mh_last_error() is not None
+
+
+_CTYPE_OF = {
+    'int': ctypes.c_int, 'int32_t': ctypes.c_int32, 'int64_t': ctypes.c_int64, 'size_t': ctypes.c_size_t,
+    'float': ctypes.c_float,
+}
+
+
+def _header_prototypes():
+    """{name: [parameter C type]} of every function declared in include/mace_hip.h."""
+    text = re.sub(r'/\*.*?\*/', ' ', open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r'\b(mh_\w+)\s*\(([^()]*)\)\s*;', text):
+        params = [p.strip() for p in m.group(2).split(',') if p.strip() and p.strip() != 'void']
+        types = []
+        for p in params:
+            p = re.sub(r'\s+', ' ', p)
+            if '*' in p:
+                types.append('ptr')
+            else:
+                types.append(p.rsplit(' ', 1)[0].replace('const ', '').strip())
+        out[m.group(1)] = types
+    return out
+
+
+def test_ctypes_signatures_match_the_header():
+    """Every ctypes binding has the header's arity, and each scalar parameter the header's width (a missing trailing
+    argument or an int32 bound as int64 would still "work" through ctypes' default conversions)."""
+    protos = _header_prototypes()
+    assert set(protos) == set(_native.EXPORTS)
+    for name, (_, argtypes) in _native._SIGS.items():
+        want = protos[name]
+        assert len(argtypes) == len(want), (name, len(argtypes), len(want))
+        for i, (ct, c) in enumerate(zip(argtypes, want)):
+            if c == 'ptr':
+                assert ct is ctypes.c_void_p or ct is ctypes.c_char_p or issubclass(ct, ctypes._Pointer), (name, i, ct)
+            else:
+                assert ctypes.sizeof(ct) == ctypes.sizeof(_CTYPE_OF[c]), (name, i, ct, c)
+                assert (ct is ctypes.c_float) == (c == 'float'), (name, i, ct, c)
+
+
+def test_launch_log_is_off_by_default_and_clears():
+    lib = _native.load()
+    assert lib.mh_launch_log(1) == 0
+    assert _native.launch_log_take() == []
+    assert lib.mh_launch_log(0) == 1
+    assert lib.mh_launch_log_take(None, 0) == 0
 
 
 def test_c_abi_rejects_bad_arguments_before_any_launch():

@@ -56,7 +56,7 @@ def _rel(got, want):
 
 
 CONV_CASES = [('32x0e+32x1o', 2), ('128x0e', 3), ('128x0e+128x1o', 3), ('128x0e+128x1o+128x2e', 3),
-              ('64x0e', 2), ('96x0e+96x1o', 3)]
+              ('64x0e', 2), ('96x0e+96x1o', 3), ('32x0e', 2)]
 
 
 @pytest.mark.parametrize('order', ['recv', 'send'])
@@ -206,16 +206,22 @@ def test_conv_c_abi_bwd_x_and_bwd_wy():
 
 def test_graph_build_vs_oracle():
     """Both CSRs of an edge list built on the GPU (mh_graph_build) against the oracle's stable-argsort CSR: random
-    multigraphs with isolated nodes, a node with 300 edges, one node, no edges; bitwise the same on a second run;
-    out-of-range indices flagged (and rejected by the graph cache) or, unvalidated, clamped."""
+    multigraphs with isolated nodes, a node with 300 edges, one node, no edges, hub nodes of 129, 5,000 and 20,000
+    edges (segments past the counting kernel's limit, sorted in LDS and in global memory); bitwise the same on a
+    second run; out-of-range indices flagged (and rejected by the graph cache) or, unvalidated, clamped."""
     dev = _dev()
     rng = np.random.default_rng(12)
-    cases = [(37, 900), (2533, 96000), (1, 5), (50, 0), (5000, 300)]
+    cases = [(37, 900), (2533, 96000), (1, 5), (50, 0), (5000, 300), (3000, 60000)]
     for n, e in cases:
         print(f'[case] graph build n={n} e={e}', flush=True)
         s, r = (rng.integers(0, n, e) for _ in range(2))
         if e >= 900:
             r[:300] = n // 2                     # a long segment
+        if e == 60000:                           # hubs, edge ids of each hub scattered over the list
+            hub = rng.permutation(e)
+            r[hub[:20000]] = 7
+            s[hub[20000:25000]] = 11
+            s[hub[25000:25129]] = 12
         ei = torch.tensor(np.stack([s, r]), device=dev)
         keys, rowptr, eids, bad = hconv.build_graph(ei, n)
         keys2, rowptr2, eids2, _ = hconv.build_graph(ei, n)
@@ -306,6 +312,53 @@ def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr, grouped):
         want.backward(torch.tensor(g, dtype=torch.float64))
         assert _rel(out.detach().double().cpu().numpy(), want.detach().numpy()) < SC_TOL
         assert _rel(xt.grad.double().cpu().numpy(), xo.grad.numpy()) < SC_TOL
+
+
+@pytest.mark.parametrize('redundant', [0, 2])
+def test_sc_basis_independent(redundant):
+    """The kernels see a contraction only through sum_p U W: every contraction of the product rewritten in another
+    path basis (a random well-conditioned change of basis, or a redundant one with extra paths; tests/test_oracle_sc
+    ``rebased``, in float64) gives the outputs and input gradients of the original, in both kernel families, and
+    both match the oracle on the original U and W."""
+    from test_oracle_sc import rebased
+    dev = _dev()
+    model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(8)
+    for li, prod in enumerate(model.products):
+        sc = copy.deepcopy(prod.symmetric_contractions).double()
+        sc2 = copy.deepcopy(sc)
+        for i, ct in enumerate(sc2.contractions):
+            sc2.contractions[i] = rebased(ct, seed=10 + i, redundant=redundant)
+        n = 41
+        elem = rng.integers(0, 4, n)
+        attrs = torch.tensor(np.eye(4)[elem], dtype=torch.float32, device=dev)
+        for grouped in (False, True):
+            print(f'[case] sc basis change layer {li} redundant={redundant} grouped={grouped}', flush=True)
+            res = []
+            for mod in (sc, sc2):
+                op = HipSymmetricContraction(mod, device=dev)
+                op.grouped = grouped
+                x = rng.normal(size=(n, op.spec.C, op.spec.n_ell)) * 0.7 if not res else res[0][0]
+                g = rng.normal(size=(n, op.spec.out_dim)) if not res else res[0][1]
+                xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
+                out = op(xt, attrs)
+                out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+                res.append((x, g, out.detach().double().cpu().numpy(), xt.grad.double().cpu().numpy()))
+            (x, g, o1, g1), (_, _, o2, g2) = res
+            assert _rel(o2, o1) < SC_TOL and _rel(g2, g1) < SC_TOL
+            xo = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+            parts = []
+            for ct in sc.contractions:
+                U = {nu: getattr(ct, f'U_matrix_{nu}').double() for nu in range(1, ct.correlation + 1)}
+                U = {nu: (u if u.dim() == nu + 2 else u.unsqueeze(0)) for nu, u in U.items()}
+                U = {nu: u.reshape(u.shape[0], -1, u.shape[-1]) for nu, u in U.items()}
+                Wd = {ct.correlation: ct.weights_max.detach().double()}
+                for j, w in enumerate(ct.weights):
+                    Wd[ct.correlation - 1 - j] = w.detach().double()
+                parts.append(osc.sc_dense(U, Wd, xo, elem).reshape(n, -1))
+            want = torch.cat(parts, dim=-1)
+            want.backward(torch.tensor(g, dtype=torch.float64))
+            assert _rel(o2, want.detach().numpy()) < SC_TOL and _rel(g2, xo.grad.numpy()) < SC_TOL
 
 
 def test_sc_grouped_matches_per_node():

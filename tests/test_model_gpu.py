@@ -160,6 +160,78 @@ def test_double_backward_hessian_and_force_loss(config):
         assert np.abs(grads[1][k] - grads[0][k]).max() < 1e-4 * scale, k
 
 
+def _loss_grads(m, batch, dev, dt, stress):
+    """Parameter gradients of E^2 + |F|^2 (+ |stress|^2) computed with create_graph (MACE's training=True)."""
+    m.zero_grad()
+    b = D.fresh(_to(batch, dev, dt))
+    out = m(b, compute_force=True, compute_stress=stress, training=True)
+    loss = (out['energy'] ** 2).sum() + (out['forces'] ** 2).sum()
+    if stress:
+        loss = loss + (out['stress'] ** 2).sum()
+    loss.backward()
+    return {k: p.grad.double().cpu().numpy() for k, p in m.named_parameters() if p.grad is not None}
+
+
+def test_double_backward_upgrade_and_stress_loss():
+    """patch_model(m) and then patch_model(m, double_backward=True): the radial MLPs the first call replaced go back
+    to e3nn (reported as such), every other drop-in differentiates twice, and a loss on energy, forces and stress
+    (the edge geometry's second-order shifts path) has the parameter gradients of the unpatched model in float64,
+    1e-4 relative to the largest reference component."""
+    dev = _dev()
+    print('[case] double backward after a first-order patch, stress loss', flush=True)
+    model = factory.make_model(*factory.REF_CONFIGS['l3_corr3_fullcg'])
+    ref = copy.deepcopy(model).to(dev, torch.float64)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    first = patch_model(met, verbose=False)
+    assert 'interactions.0.conv_tp_weights' in first['patched'], first
+    report = patch_model(met, verbose=False, double_backward=True)
+    skipped = dict(report['skipped'])
+    assert 'restored' in skipped['interactions.0.conv_tp_weights'], skipped
+    assert type(met.interactions[0].conv_tp_weights).__name__ != 'HipRadialMLP'
+    batch = D.batch_graphs([D.graph_of(factory.make_structure(seed=6), 5.0)], factory.ELEMENTS_REF)
+    g_ref, g_met = (_loss_grads(m, batch, dev, dt, stress=True) for m, dt in ((ref, torch.float64),
+                                                                              (met, torch.float32)))
+    common = sorted(set(g_ref) & set(g_met))
+    assert any('conv_tp_weights' in k for k in common), common
+    for k in common:
+        scale = max(np.abs(g_ref[k]).max(), 1e-8)
+        assert np.abs(g_met[k] - g_ref[k]).max() < 1e-4 * scale, k
+
+
+def test_patched_model_launches_the_fast_paths():
+    """The kernels an E+F call of the patched model runs, read from the C ABI's launch log (no assumption about which
+    path a module takes): the factored convolution kernels (W0 * cutoff never formed: conv_fwdc, conv_bwdrc), layer
+    1's backward without dX (no conv_gxsum for it: the engine never asks for the first layer's node-feature
+    gradient), the symmetric contraction reading e3nn's irreps layout (sc_*i: reshape_irreps left unformed, so no
+    permutation kernel), and every other drop-in's kernels."""
+    from mace_hip_kernels import _native
+    dev = _dev()
+    print('[case] kernels launched by the patched model (config 1)', flush=True)
+    model, batch, _ = factory.workload(1)
+    met = copy.deepcopy(model).to(dev)
+    patch_model(met, verbose=False)
+    met(D.fresh(_to(batch, dev, torch.float32)), compute_force=True)          # graph and element order cached
+    b = D.fresh(_to(batch, dev, torch.float32))
+    with _native.timing() as tm:
+        met(b, compute_force=True)
+    torch.cuda.synchronize()
+    sym = {tag: names for tag, names in tm.symbols.items()}
+    flat = [n for names in sym.values() for n in names]
+    assert sym['conv_fwd[interactions.0.conv_tp]'] == ['conv_fwdc_x128_o2048'], sym
+    assert sym['conv_fwd[interactions.1.conv_tp]'] == ['conv_fwdc_x512_o5120'], sym
+    assert sym['conv_bwd[interactions.0.conv_tp]'] == ['conv_bwdrc_x128_o2048'], sym
+    assert sym['conv_bwd[interactions.1.conv_tp]'] == ['conv_bwdrc_x512_o5120', 'conv_gxsum_x512_o5120'], sym
+    for i in range(2):
+        names = sym[f'sc_fwd[products.{i}.symmetric_contractions]'] + \
+            sym[f'sc_bwd[products.{i}.symmetric_contractions]']
+        assert len(names) == 2 and all(n.startswith(('sc_fwdi_', 'sc_bwdi_', 'sc_fwdgi_', 'sc_bwdgi_'))
+                                       for n in names), names
+    for prefix in ('mlp_fwd_', 'mlp_bwd_', 'sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_', 'geom_fwd', 'geom_bwd',
+                   'lin_fwd_', 'lin_bwd_', 'ro_fwd_', 'ro_bwd_'):
+        assert any(n.startswith(prefix) for n in flat), (prefix, flat)
+    assert not any(n.startswith(('perm_', 'conv_fwd_', 'conv_bwd_', 'conv_bwdr_')) for n in flat), flat
+
+
 def test_unsupported_block_is_skipped():
     dev = _dev()
     print('[case] 48-channel model: convolutions skipped', flush=True)

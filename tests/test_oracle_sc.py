@@ -7,8 +7,13 @@ Pins of the symmetric-contraction oracle (CPU, float64).
 * the table's directional derivatives (output and gradient) == forward-mode and double-backward autograd of sc_dense;
 * the product's SCSpec table (what the kernel reads) == the oracle's table, term by term;
 * every U matrix satisfies the intertwiner identity U(D x, …, D x) = D_L U(x, …, x) with D from the spherical
-  harmonics, and has full column rank; a planted mistake (one M row of U negated) breaks the identity.
+  harmonics, and has full column rank; a planted mistake (one M row of U negated) breaks the identity;
+* the table depends on the path basis only through Σ_p U·W: a contraction rewritten in another basis (U' = U·Q,
+  W' = Q⁻¹·W for a random well-conditioned Q per correlation order, or a redundant basis with extra paths) gives the
+  same SCSpec table, the same module output, and a planted inconsistent change (W left unrotated) does not.
 """
+import copy
+
 import numpy as np
 import pytest
 import torch
@@ -143,3 +148,57 @@ def test_u_matrix_intertwiner_and_rank(l_out, nu):
         bad = u.copy()
         bad[0] *= -1
         assert osc.u_equivariance_error(bad, [0, 1, 2], l_out, nu, rng) > 1e-3
+
+
+def rebased(ct, seed, redundant=0, consistent=True):
+    """A copy of a Contraction in another path basis with the same polynomial: per correlation order ν,
+    U_ν' = U_ν·A and W_ν' = B·W_ν with A·B = I on the old paths.  redundant = 0: A = Q, B = Q⁻¹ for a random
+    orthogonal Q times column scales in [0.5, 2] (condition number <= 4); redundant = k: A = [Q | R] adds k paths
+    (a basis with linearly dependent columns, as the full CG basis has), B = [Q⁻¹(W - R·Z); Z] for random R, Z.
+    ``consistent=False`` leaves W unchanged (a planted mistake)."""
+    rng = np.random.default_rng(seed)
+    cr = copy.deepcopy(ct)
+    with torch.no_grad():
+        for nu in range(1, ct.correlation + 1):
+            u = getattr(cr, f'U_matrix_{nu}')
+            p = u.shape[-1]
+            q, _ = np.linalg.qr(rng.normal(size=(p, p)))
+            Q = torch.tensor(q * rng.uniform(0.5, 2.0, size=p), dtype=u.dtype)
+            R = torch.tensor(rng.normal(size=(p, redundant)), dtype=u.dtype)
+            A = torch.cat([Q, R], dim=1)                                   # [p, p + k]
+            j = None if nu == ct.correlation else ct.correlation - 1 - nu
+            w = cr.weights_max if j is None else cr.weights[j]
+            Z = torch.tensor(rng.normal(size=(w.shape[0], redundant, w.shape[2])), dtype=w.dtype) / max(p, 1)
+            wn = torch.cat([torch.einsum('pq,eqc->epc', torch.linalg.inv(Q), w - torch.einsum('pk,ekc->epc', R, Z)),
+                            Z], dim=1) if consistent else torch.cat([w, Z], dim=1)
+            cr.register_buffer(f'U_matrix_{nu}', torch.einsum('...p,pq->...q', u, A).contiguous())
+            if j is None:
+                cr.weights_max = torch.nn.Parameter(wn)
+            else:
+                cr.weights[j] = torch.nn.Parameter(wn)
+    return cr
+
+
+@pytest.mark.parametrize('redundant', [0, 3])
+@pytest.mark.parametrize('irreps_in,irrep_out,corr', CASES[:3])
+def test_table_is_basis_independent(irreps_in, irrep_out, corr, redundant):
+    ct = _contraction(irreps_in, irrep_out, corr)
+    cr = rebased(ct, seed=5, redundant=redundant)
+    assert cr.U_tensors(corr).shape[-1] == ct.U_tensors(corr).shape[-1] + redundant
+
+    class SC(torch.nn.Module):
+        def __init__(self, c):
+            super().__init__()
+            self.contractions = torch.nn.ModuleList([c])
+
+    a, b = SCSpec(SC(ct)), SCSpec(SC(cr))
+    assert [t for t, _ in a.blocks[0]['terms']] == [t for t, _ in b.blocks[0]['terms']]
+    assert torch.abs(a.T - b.T).max() <= 1e-6 * float(a.T.abs().max())
+    rng = np.random.default_rng(1)
+    C, n = ct.num_features, Irreps(irreps_in).dim // ct.num_features
+    x = torch.tensor(rng.normal(size=(9, C, n)))
+    y = torch.tensor(np.eye(3)[rng.integers(0, 3, 9)])
+    want = ct(x, y)
+    assert torch.abs(cr(x, y) - want).max() < 1e-10 * max(1.0, float(want.abs().max()))
+    bad = SCSpec(SC(rebased(ct, seed=5, redundant=redundant, consistent=False)))
+    assert torch.abs(bad.T - a.T).max() > 1e-3 * float(a.T.abs().max())
