@@ -96,8 +96,9 @@ const char* mh_last_error(void);
 /* ABI version of this header (bumped on any signature change). */
 int mh_version(void);
 
-/* Launch log of the calling thread, for profiling and tests that check which kernels ran: while enabled, every
- * successful launch appends the symbol bound to the launched slot.  mh_launch_log(1) enables it, mh_launch_log(0)
+/* Launch log of the process, for profiling and tests that check which kernels ran: while enabled, every successful
+ * launch, from any thread (autograd runs backward passes on threads of its own), appends the symbol bound to the
+ * launched slot.  mh_launch_log(1) enables it, mh_launch_log(0)
  * disables and clears it; both return the previous state.  mh_launch_log_take copies the names, each followed by
  * ';', oldest first, into buf (NUL-terminated) and clears the log when it fitted; it returns the log's length (call
  * with buf NULL to size the buffer).  No reference counterpart (Metal kernels are named in the reference's own

@@ -14,6 +14,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <sstream>
 #include <string>
 #include <vector>
@@ -23,8 +24,11 @@
 namespace {
 
 thread_local std::string g_err;
-thread_local bool g_log_on = false;      // launch log (mh_launch_log): bound names of the kernels launched
-thread_local std::string g_log;
+// launch log (mh_launch_log): bound names of the kernels launched by any thread of the process (the autograd
+// engine runs backward passes on threads of its own)
+std::mutex g_log_mu;
+bool g_log_on = false;
+std::string g_log;
 
 struct Kernel {
     hipFunction_t fn = nullptr;
@@ -81,9 +85,12 @@ int launch(mh_module* m, int kind, int64_t rows, void** args, void* stream, cons
                                          static_cast<unsigned>(k.block), 1, 1, 0, static_cast<hipStream_t>(stream), args,
                                          nullptr);
     if (e != hipSuccess) return hip_fail(e, what);
-    if (g_log_on) {
-        g_log += k.name;
-        g_log += ';';
+    {
+        std::lock_guard<std::mutex> lock(g_log_mu);
+        if (g_log_on) {
+            g_log += k.name;
+            g_log += ';';
+        }
     }
     return 0;
 }
@@ -97,6 +104,7 @@ const char* mh_last_error(void) { return g_err.c_str(); }
 int mh_version(void) { return 23; }
 
 int mh_launch_log(int enable) {
+    std::lock_guard<std::mutex> lock(g_log_mu);
     const int was = g_log_on ? 1 : 0;
     g_log_on = enable != 0;
     if (!g_log_on) g_log.clear();
@@ -104,6 +112,7 @@ int mh_launch_log(int enable) {
 }
 
 size_t mh_launch_log_take(char* buf, size_t len) {
+    std::lock_guard<std::mutex> lock(g_log_mu);
     const size_t n = g_log.size();
     if (buf && len) {
         const size_t c = n < len - 1 ? n : len - 1;

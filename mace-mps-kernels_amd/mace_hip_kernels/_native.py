@@ -178,7 +178,7 @@ class Module:
 
 
 def launch_log_take():
-    """Symbols of the kernels launched on this thread since the last call, oldest first (the C ABI's launch log)."""
+    """Symbols of the kernels launched since the last call, oldest first (the C ABI's launch log)."""
     lib = load()
     n = lib.mh_launch_log_take(None, 0)
     buf = ctypes.create_string_buffer(n + 1)
