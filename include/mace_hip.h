@@ -236,6 +236,17 @@ int mh_sc_bwd2(mh_module* m, const float* X, const float* V, const int32_t* elem
 int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys, int32_t* rowptr,
                    int32_t* eids, int32_t* work, int32_t* bad, void* stream);
 
+/* mh_graph_build for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation): the same arguments but `work`, with the same results, calling no hipMalloc / hipFree.  The
+ * scratch is a device array the library owns, MH_GRAPH_SCRATCH_INTS int32 (16 MiB) per GPU, held until the process
+ * ends; a call whose 4 (n + 1) + 2 E exceeds it returns an error without launching anything.  Every call on a GPU
+ * uses that GPU's one array (the kernels clear what must start at zero), so calls that overlap on one GPU (two
+ * streams, two threads) race and must be ordered by the caller.  No counterpart in the reference (whose csr_by
+ * allocates through torch, conv.py:229-235); it is for the callers that cannot allocate. */
+#define MH_GRAPH_SCRATCH_INTS (4 << 20)
+int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys,
+                           int32_t* rowptr, int32_t* eids, int32_t* bad, void* stream);
+
 /* Edge spherical harmonics Y[e, :] = Y_{0..l_max}(vec[e] / |vec[e]|) (vec [E, 3], Y [E, (l_max+1)^2]; e3nn's real
  * basis, y polar axis) and their backward gvec[e] = dL/dvec[e] from gY.  The kernels are generated per (l_max,
  * normalisation).  No reference counterpart: the reference leaves the model's edge spherical harmonics on e3nn's

@@ -374,6 +374,57 @@ int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n
     return launch(m, MH_CSR_RANK, E, args, stream, "mh_graph_build");
 }
 
+}  // extern "C"
+
+// ------------------------------------------------------------------------------- allocation-free graph build
+// Scratch of mh_graph_build_noalloc: the graph build's per-node counters and cursors and its per-edge staging
+// (4 (n + 1) + 2 E int32) in device memory the library owns, so that the call allocates nothing.  Each GPU the
+// library runs on holds its own copy until the process ends.  Host code never passes `scratch` itself (in host code
+// the name is a stand-in, not a device address): it passes the address hipGetSymbolAddress reports for the current
+// device, looked up once per device.
+static __device__ __align__(256) int32_t scratch[MH_GRAPH_SCRATCH_INTS];
+
+namespace {
+
+std::mutex g_scratch_mu;
+std::vector<int32_t*> g_scratch_ptr;       // per device ordinal: scratch's device address, null until looked up
+
+int scratch_of_current_device(int32_t** out) {
+    int dev = -1;
+    MH_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (static_cast<int>(g_scratch_ptr.size()) <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        MH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(-1, "mh_graph_build_noalloc: hipGetSymbolAddress gave a null scratch address");
+        g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys,
+                           int32_t* rowptr, int32_t* eids, int32_t* bad, void* stream) {
+    if (E < 0 || n < 0 || E >= 0x7fffffffLL || n >= 0x7fffffff)
+        return fail(-1, "mh_graph_build_noalloc: bad sizes");
+    const int64_t need = 4 * (static_cast<int64_t>(n) + 1) + 2 * E;
+    if (need > MH_GRAPH_SCRATCH_INTS) {
+        std::ostringstream os;
+        os << "mh_graph_build_noalloc: " << E << " edges over " << n << " nodes need " << need
+           << " int32 of scratch, more than the " << MH_GRAPH_SCRATCH_INTS
+           << " the library holds (use mh_graph_build with a caller-owned work buffer)";
+        return fail(-1, os.str());
+    }
+    int32_t* work = nullptr;
+    if (int rc = scratch_of_current_device(&work)) return rc;
+    return mh_graph_build(m, edge_index, E, n, keys, rowptr, eids, work, bad, stream);
+}
+
 int mh_sh_fwd(mh_module* m, const float* vec, float* Y, int64_t E, void* stream) {
     void* args[] = {&vec, &Y, &E};
     return launch(m, MH_SH_FWD, E, args, stream, "mh_sh_fwd");

@@ -73,6 +73,7 @@ _SIGS = {
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
     'mh_sc_jvp': (ctypes.c_int, [_P] * 6 + [_I, _I, _P]),
     'mh_graph_build': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 6),
+    'mh_graph_build_noalloc': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 5),
     'mh_launch_log': (ctypes.c_int, [ctypes.c_int]),
     'mh_launch_log_take': (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
     'mh_sh_jvp': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),

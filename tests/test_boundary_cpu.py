@@ -87,6 +87,8 @@ def test_c_abi_rejects_bad_arguments_before_any_launch():
         (lambda: lib.mh_graph_build(None, None, 5, 0, None, None, None, None, None, None), 'zero nodes'),
         (lambda: lib.mh_graph_build(None, None, 5, 3, None, None, None, None, None, None), 'NULL'),
         (lambda: lib.mh_graph_build(None, None, -1, 3, None, None, None, None, None, None), 'bad sizes'),
+        (lambda: lib.mh_graph_build_noalloc(None, None, 3_000_000, 1000, None, None, None, None, None), 'scratch'),
+        (lambda: lib.mh_graph_build_noalloc(None, None, -4, 1000, None, None, None, None, None), 'bad sizes'),
         (lambda: lib.mh_sc_jvp(None, None, None, None, None, None, 4, 2, None), 'layout'),
         (lambda: lib.mh_sc_bwd2(None, None, None, None, None, None, None, 4, 7, None), 'layout'),
         (lambda: lib.mh_sh_jvp(None, None, None, None, 10, None), 'NULL'),
