@@ -194,7 +194,7 @@ def _isolated(a):
     after W warm-ups.  Prints one JSON line per kernel."""
     import torch
     from mace_hip_kernels import HipConvTP, HipSymmetricContraction, _native
-    from mace_hip_kernels import conv as hconv
+    from mace_hip_kernels import conv as hconv, radial
     from mace_lite import factory
     dev = torch.device('cuda:0')
     model, batch, meta = factory.workload(a.config)
@@ -274,6 +274,10 @@ def _isolated(a):
                                                   N, 3, stream), nb)
         report(f'conv_bwd[{tag}] factored dx+dW+dY (model path)', f"{s.kname('conv_bwdrc')}+{s.kname('conv_gxsum')}",
                ms, bb, fb * n_real * s.mul)
+        if radial.mlp_supported(blk.conv_tp_weights)[0]:
+            _isolated_radial(a, timed, report, blk, op, li, dict(x=x, g=g, Ys=Ys, Ws=Ws, gWs=gWs, gY=gY, gx=gx,
+                                                                   out=out, work=work, cut=cut, gcut=gcut), nb,
+                             (N, E, n_real, gr, rp_r, ei_r, rp_s, ei_s, stream), rnd)
         del op, x, g, Ys, Ws, gWs, gY, gx, out, work, cut, gcut
         torch.cuda.empty_cache()
     elem = batch['node_attrs'].argmax(1).to(torch.int32).to(dev)
@@ -297,6 +301,60 @@ def _isolated(a):
         report(f'sc_bwd[{tag}] per-node', s.kname('sc_bwd'), ms, bb, fb * N * s.C)
         _log(f'{tag}: the model uses the {"grouped" if op.use_grouped(N, dev) else "per-node"} kernels at N = {N}')
         del op
+
+
+def _isolated_radial(a, timed, report, blk, op, li, t, nb, graph, rnd):
+    """The radial MLP's kernels of one interaction block alone, and the fused alternative (fuse_radial: the MLP's
+    output layer inside the convolution, conv_mlp.py) on the same inputs, the MLP forward + factored convolution
+    forward against mlp_hid + conv_fwdm, and conv_bwdrc + mlp_bwd against conv_bwdm + mlp_hidb."""
+    import torch
+    from mace_hip_kernels import HipRadialMLP, _native
+    N, E, n_real, gr, rp_r, ei_r, rp_s, ei_s, stream = graph
+    P, lib = _native.ptr, _native.load()
+    dev = t['x'].device
+    mlp = HipRadialMLP(blk.conv_tp_weights, device=dev)
+    s, sm = op.spec, mlp.spec
+    nw, nbas = s.nins * s.mul, sm.hs[0]
+    tag = f'interactions.{li}.conv_tp_weights'
+    efs = [rnd(E, nbas) for _ in range(nb)]
+    gef = torch.empty(E, nbas, device=dev)
+    ms = timed(lambda i: lib.mh_mlp_fwd(mlp.module.handle, P(efs[i]), P(mlp.WhT), P(mlp.WlT), P(t['Ws'][i]), E,
+                                        stream), nb)
+    report(f'mlp_fwd[{tag}]', sm.kname('mlp_fwd'), ms, sm.bytes(E)[0], sm.flops(E))
+    ms = timed(lambda i: lib.mh_mlp_bwd(mlp.module.handle, P(efs[i]), P(mlp.Wh), P(mlp.Wl), P(t['gWs'][i]),
+                                        P(gef), E, stream), nb)
+    report(f'mlp_bwd[{tag}]', sm.kname('mlp_bwd'), ms, sm.bytes(E)[1], 2 * sm.flops(E))
+    ok, why = op.attach_mlp(mlp)
+    if not ok:
+        _log(f'{tag}: no fused kernels ({why})')
+        return
+    fc = op.fused
+    hb = [torch.empty(E, fc.spec.S * 3 * 32, device=dev, dtype=torch.int16) for _ in range(nb)]
+    gyp = torch.empty(fc.spec.nct, E, fc.yp, device=dev)
+    ghp = torch.empty(fc.spec.nct, E, fc.spec.HL, device=dev)
+    h_bytes = 2 * E * fc.spec.S * 3 * 32
+    ms = timed(lambda i: lib.mh_mlp_hid(mlp.module.handle, P(efs[i]), P(mlp.WhT), P(t['cut']), P(hb[i]), E, stream),
+               nb)
+    report(f'mlp_hid[{tag}] (fuse_radial)', sm.kname('mlp_hid'), ms, 4 * E * (nbas + 1) + h_bytes, 0)
+    bf, bb = s.bytes(N, n_real)
+    ff, fb = s.flops()
+    ctag = f'interactions.{li}.conv_tp'
+    ms = timed(lambda i: lib.mh_conv_fwd_mlp(fc.module.handle, P(t['x']), P(t['Ys'][i]), P(hb[i]), P(t['cut']),
+                                             P(rp_r), P(ei_r), P(gr.send), P(fc.Wf), P(t['out']), N, stream), nb)
+    report(f'conv_fwd[{ctag}] fuse_radial', fc.spec.kname('conv_fwdm'), ms, bf - 4 * n_real * nw + h_bytes + 4 * E,
+           ff * n_real * s.mul)
+    flags = _native.MH_WANT_GX if li else 0
+    ms = timed(lambda i: lib.mh_conv_bwd_mlp(fc.module.handle, P(t['x']), P(t['g']), P(t['Ys'][i]), P(hb[i]),
+                                             P(t['cut']), P(ei_r), P(gr.recv), P(gr.send), P(rp_s), P(ei_s), P(fc.Wf),
+                                             P(fc.Wb), P(t['work']), P(t['gx']), P(gyp), P(ghp), P(t['gY']), E, N,
+                                             flags, stream), nb)
+    report(f'conv_bwd[{ctag}] fuse_radial{" dx" if li else ""}', fc.spec.kname('conv_bwdm'), ms,
+           bb - 8 * n_real * nw + h_bytes + 4 * E * fc.spec.nct * (fc.yp + fc.spec.HL), fb * n_real * s.mul)
+    ms = timed(lambda i: lib.mh_mlp_hid_bwd(mlp.module.handle, P(efs[i]), P(mlp.Wh), P(ghp), fc.spec.nct,
+                                            P(t['cut']), P(gef), P(t['gcut']), E, stream), nb)
+    report(f'mlp_bwd[{tag}] (fuse_radial)', sm.kname('mlp_hidb'), ms,
+           4 * E * (2 * nbas + 2) + 4 * E * fc.spec.nct * fc.spec.HL, 0)
+    op.detach_mlp()
 
 
 def _profile(a):
@@ -430,6 +488,8 @@ def main():
     ap.add_argument('--no-e3nn', action='store_true')
     ap.add_argument('--no-double-backward', action='store_true', help='skip the force-loss step timing')
     ap.add_argument('--no-graph', action='store_true', help='report the eager call instead of the captured one')
+    ap.add_argument('--fuse-radial', action='store_true',
+                    help="patch_model(fuse_radial=True): the radial MLP's output layer inside the convolution")
     a = ap.parse_args()
     if a.config is None:
         a.config = 4 if a.isolated else 2
@@ -465,7 +525,7 @@ def main():
          f'{batch["edge_index"].shape[1]} edges ({n_real} real), {n_structs} structures')
 
     met = copy.deepcopy(model).to(dev)
-    report = patch_model(met, verbose=False)
+    report = patch_model(met, verbose=False, fuse_radial=a.fuse_radial)
     assert not report['skipped'], report
     _log('patched:', report['patched'])
 
@@ -591,6 +651,7 @@ def main():
                    'correlation': 3},
         'structures_per_s': round(n_structs / dt, 2),
         'timed_call': 'captured HIP graph replay' if dt_graph is not None else 'eager',
+        'fuse_radial': a.fuse_radial,
         'ms_per_step_eager': round(dt_eager * 1e3, 4),
         'ms_per_step_new_graph_tensors': round(dt_fresh * 1e3, 4),
         'graph_replay_check': graph_check,

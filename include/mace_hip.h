@@ -82,7 +82,12 @@ enum mh_kernel_kind {
     MH_READOUT_JVP = 43, /* SiLU readout head: derivative of the energy along a direction of x       */
     MH_READOUT_BWD2 = 44,/* derivative of its input gradient along that direction                   */
     MH_CSR_SORT = 45,    /* graph build: sort each segment longer than the counting kernel handles  */
-    MH_NUM_KINDS = 46
+    MH_MLP_HID = 46,     /* radial MLP's hidden layers only: last hidden activations h [E, HL]      */
+    MH_MLP_HIDB = 47,    /* their backward from the fused convolution's partial dL/d(c h)           */
+    MH_CONV_FWD_M = 48,  /* convolution forward with the MLP's output layer fused (grid_y: tiles)  */
+    MH_CONV_BWD_M = 49,  /* its backward: dX messages, gY and dL/d(c h) partials (grid_y: tiles)   */
+    MH_CONV_GYSUM = 50,  /* gY = sum of the fused backward's per-channel-tile partials             */
+    MH_NUM_KINDS = 51
 };
 
 /* flags of mh_conv_bwd */
@@ -330,6 +335,41 @@ int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* W
                void* stream);
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream);
+
+/* The convolution with the radial MLP's output layer inside it (no reference counterpart: the reference streams the
+ * materialised weights, W [E, NINS*MUL], through lib.conv_fwd and writes their gradient in lib.conv_bwd_wy,
+ * conv.py:127, 203-209).  MACE's tp_weights = MLP(ef) * cutoff with the MLP's last layer A [HL, NINS*MUL] linear, so
+ * W[e] = cutoff[e] * h[e] A with h [E, HL] the last hidden activations: the kernels read c*h and form W on the matrix
+ * cores per edge tile, at fp32 accuracy (exact three-way bf16 splits of c*h and A, six partial products).
+ *   mh_mlp_hid:       hc = cutoff * h from the MLP's hidden layers (module of radial.source, Wh the forward's hidden
+ *                     weights), as the convolutions' MFMA operand: [E][HL / 32][3 bf16 parts][4][8] uint16, K position
+ *                     8 q + t of step s holding feature 32 s + 16 (t / 4) + 4 q + t % 4;
+ *   mh_conv_fwd_mlp:  out as mh_conv_fwd_cut on W = hc A (edges with cutoff == 0 skipped); Wf = A packed per channel
+ *                     tile with its rows in hc's K order (conv_mlp.FusedSpec.pack_fwd).  Bind MH_CONV_FWD_M with rows_per_block = the
+ *                     receivers per workgroup and grid_y = channel tiles x instruction groups: the grid is grid_y
+ *                     times ceil(N / rows_per_block) workgroups;
+ *   mh_conv_bwd_mlp:  from g [N, OUT_DIM]: gY [E, Y_DIM], gx (flags & MH_WANT_GX: dX messages in work [E, X_DIM],
+ *                     summed over the sender CSR) and the per-channel-tile partials of dL/d(cutoff * h),
+ *                     gh_parts [NCT, E, HL] (gY_parts [NCT, E, Y_DIM rounded up to 4] is scratch); Wb = A packed for
+ *                     the transposed product (conv_mlp.pack_bwd).  eids_r / receivers / senders: the receiver CSR's
+ *                     edge order and the int32 edge endpoints.  Bind MH_CONV_BWD_M with rows_per_block = waves per
+ *                     workgroup and grid_y = NCT (the channel tiles), MH_CONV_GYSUM with 256 threads and 256 edges per
+ *                     block, MH_CONV_GXSUM as for mh_conv_bwd_recv;
+ *   mh_mlp_hid_bwd:   gcut[e] = sum_j P[e, j] h[e, j] and gef = dL/def through the hidden layers with dL/dh = cutoff P,
+ *                     P the sum of the nparts slices of gparts [nparts, E, HL] (Wh the backward's hidden weights).
+ * All sums run in a fixed order: results are bitwise repeatable. */
+int mh_mlp_hid(mh_module* m, const float* ef, const float* Wh, const float* cutoff, uint16_t* hc, int64_t E,
+               void* stream);
+int mh_mlp_hid_bwd(mh_module* m, const float* ef, const float* Wh, const float* gparts, int32_t nparts,
+                   const float* cutoff, float* gef, float* gcut, int64_t E, void* stream);
+int mh_conv_fwd_mlp(mh_module* m, const float* x, const float* Y, const uint16_t* h, const float* cutoff,
+                    const int32_t* rowptr, const int32_t* eids, const int32_t* senders, const uint16_t* Wf, float* out,
+                    int32_t N, void* stream);
+int mh_conv_bwd_mlp(mh_module* m, const float* x, const float* g, const float* Y, const uint16_t* h,
+                    const float* cutoff, const int32_t* eids_r, const int32_t* receivers, const int32_t* senders,
+                    const int32_t* rowptr_s, const int32_t* eids_s, const uint16_t* Wf, const uint16_t* Wb,
+                    float* work, float* gx, float* gY_parts, float* gh_parts, float* gY, int32_t E, int32_t N,
+                    int32_t flags, void* stream);
 
 /* Radial embedding of E edge lengths (len [E]): cutoff[e] = polynomial envelope of len[e] / r_max (0 beyond r_max)
  * and feats[e, n] = sqrt(2 / r_max) sin(w_n len[e]) / len[e] * cutoff[e] (feats [E, n_basis]); r_max, the envelope

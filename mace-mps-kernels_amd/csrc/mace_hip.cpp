@@ -95,13 +95,50 @@ int launch(mh_module* m, int kind, int64_t rows, void** args, void* stream, cons
     return 0;
 }
 
+// Launch `kind` on an explicit 1-D grid of `blocks` workgroups (kernels that size their own grid).
+int launch_blocks(mh_module* m, int kind, int64_t blocks, void** args, void* stream, const char* what) {
+    if (!m) return fail(-1, std::string(what) + ": null module");
+    const Kernel& k = m->k[kind];
+    if (!k.fn) return fail(-1, std::string(what) + ": kernel slot not bound in this module");
+    if (blocks <= 0) return 0;
+    if (blocks > 0x7fffffffLL) return fail(-1, std::string(what) + ": launch too large");
+    int dev = -1;
+    MH_HIP(hipGetDevice(&dev));
+    if (dev != m->device) {
+        std::ostringstream os;
+        os << what << ": module was loaded on device " << m->device << " but device " << dev << " is current";
+        return fail(-1, os.str());
+    }
+    hipError_t e = hipModuleLaunchKernel(k.fn, static_cast<unsigned>(blocks), 1, 1, static_cast<unsigned>(k.block), 1,
+                                         1, 0, static_cast<hipStream_t>(stream), args, nullptr);
+    if (e != hipSuccess) return hip_fail(e, what);
+    {
+        std::lock_guard<std::mutex> lock(g_log_mu);
+        if (g_log_on) {
+            g_log += k.name;
+            g_log += ';';
+        }
+    }
+    return 0;
+}
+
+// Workgroups of `kind` that fit on the whole device at once (occupancy x compute units), at least 1.
+int resident_blocks(mh_module* m, int kind, int* out) {
+    const Kernel& k = m->k[kind];
+    int per_cu = 0, cus = 0;
+    MH_HIP(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k.fn, k.block, 0));
+    MH_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->device));
+    *out = per_cu * cus > 0 ? per_cu * cus : 1;
+    return 0;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 23; }
+int mh_version(void) { return 24; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -519,6 +556,72 @@ int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* W
     if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef)) return fail(-1, "mh_mlp_bwd: NULL operand");
     void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E};
     return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
+}
+
+int mh_mlp_hid(mh_module* m, const float* ef, const float* Wh, const float* cutoff, uint16_t* hc, int64_t E,
+               void* stream) {
+    if (E > 0 && (!ef || !Wh || !cutoff || !hc)) return fail(-1, "mh_mlp_hid: NULL operand");
+    void* args[] = {&ef, &Wh, &cutoff, &hc, &E};
+    return launch(m, MH_MLP_HID, E, args, stream, "mh_mlp_hid");
+}
+
+int mh_mlp_hid_bwd(mh_module* m, const float* ef, const float* Wh, const float* gparts, int32_t nparts,
+                   const float* cutoff, float* gef, float* gcut, int64_t E, void* stream) {
+    if (E > 0 && (!ef || !Wh || !gparts || !cutoff || !gef || !gcut)) return fail(-1, "mh_mlp_hid_bwd: NULL operand");
+    if (nparts < 1) return fail(-1, "mh_mlp_hid_bwd: nparts must be at least 1");
+    void* args[] = {&ef, &Wh, &gparts, &nparts, &cutoff, &gef, &gcut, &E};
+    return launch(m, MH_MLP_HIDB, E, args, stream, "mh_mlp_hid_bwd");
+}
+
+int mh_conv_fwd_mlp(mh_module* m, const float* x, const float* Y, const uint16_t* h, const float* cutoff,
+                    const int32_t* rowptr, const int32_t* eids, const int32_t* senders, const uint16_t* Wf, float* out,
+                    int32_t N, void* stream) {
+    if (!m) return fail(-1, "mh_conv_fwd_mlp: null module");
+    if (N < 0) return fail(-1, "mh_conv_fwd_mlp: negative size");
+    if (N > 0 && (!x || !Y || !h || !cutoff || !rowptr || !eids || !senders || !Wf || !out))
+        return fail(-1, "mh_conv_fwd_mlp: NULL operand");
+    const Kernel& k = m->k[MH_CONV_FWD_M];
+    const int64_t blocks = static_cast<int64_t>(k.grid_y) * ((N + k.rows_per_block - 1) / k.rows_per_block);
+    void* args[] = {&x, &Y, &h, &cutoff, &rowptr, &eids, &senders, &Wf, &out, &N};
+    return launch_blocks(m, MH_CONV_FWD_M, blocks, args, stream, "mh_conv_fwd_mlp");
+}
+
+int mh_conv_bwd_mlp(mh_module* m, const float* x, const float* g, const float* Y, const uint16_t* h,
+                    const float* cutoff, const int32_t* eids_r, const int32_t* receivers, const int32_t* senders,
+                    const int32_t* rowptr_s, const int32_t* eids_s, const uint16_t* Wf, const uint16_t* Wb,
+                    float* work, float* gx, float* gY_parts, float* gh_parts, float* gY, int32_t E, int32_t N,
+                    int32_t flags, void* stream) {
+    if (!m) return fail(-1, "mh_conv_bwd_mlp: null module");
+    if (E < 0 || N < 0) return fail(-1, "mh_conv_bwd_mlp: negative size");
+    const bool want_gx = (flags & MH_WANT_GX) != 0;
+    if (E > 0 && (!x || !g || !Y || !h || !cutoff || !eids_r || !receivers || !senders || !Wf || !Wb || !gY_parts ||
+                  !gh_parts || !gY))
+        return fail(-1, "mh_conv_bwd_mlp: NULL operand");
+    if (want_gx && (!gx || (E > 0 && !work) || !rowptr_s || !eids_s))
+        return fail(-1, "mh_conv_bwd_mlp: gx requested but gx, work or the sender CSR is NULL");
+    const Kernel& k = m->k[MH_CONV_BWD_M];
+    if (!k.fn) return fail(-1, "mh_conv_bwd_mlp: kernel slot not bound in this module");
+    int rc;
+    if (E > 0) {
+        int resident = 1;
+        if ((rc = resident_blocks(m, MH_CONV_BWD_M, &resident))) return rc;
+        const int64_t tiles = (E + 15) / 16;
+        const int64_t per_tile = k.grid_y;                    // channel tiles
+        int64_t ngrp = resident / per_tile;
+        const int64_t need = (tiles + k.rows_per_block - 1) / k.rows_per_block;
+        if (ngrp > need) ngrp = need;
+        if (ngrp < 1) ngrp = 1;
+        int32_t ng = static_cast<int32_t>(ngrp), kflags = want_gx ? 1 : 0;
+        void* args[] = {&x, &g, &Y, &h, &cutoff, &eids_r, &receivers, &senders, &Wf, &Wb, &work, &gY_parts,
+                        &gh_parts, &E, &kflags, &ng};
+        if ((rc = launch_blocks(m, MH_CONV_BWD_M, per_tile * ngrp, args, stream, "mh_conv_bwd_mlp"))) return rc;
+        void* args2[] = {&gY_parts, &gY, &E};
+        if ((rc = launch(m, MH_CONV_GYSUM, E, args2, stream, "mh_conv_bwd_mlp (gY sum)"))) return rc;
+    }
+    if (!want_gx) return 0;
+    const float* msg = work;
+    void* args3[] = {&msg, &rowptr_s, &eids_s, &gx, &N};
+    return launch(m, MH_CONV_GXSUM, N, args3, stream, "mh_conv_bwd_mlp (dX sum)");
 }
 
 int mh_emb_fwd(mh_module* m, const float* len, float* feats, float* cutoff, int64_t E, void* stream) {

@@ -66,7 +66,7 @@ def _linear_candidates(model):
 
 def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmonics=True, linears=True,
                 radial_mlp=True, radial_embedding=True, layouts=True, edge_geometry=True, readouts=True,
-                double_backward=False):
+                double_backward=False, fuse_radial=False):
     """Swap supported ops for HIP kernels, in place.  Returns ``{'patched': [...], 'skipped': [(name, reason)]}``
     (reference __init__.py:34-79).  Beyond the reference's two ops, ``spherical_harmonics`` also replaces the model's
     edge spherical harmonics (``model.spherical_harmonics``) when it is a supported e3nn module, and ``linears`` the
@@ -79,6 +79,12 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     lengths (MACE's ``get_edge_vectors_and_lengths`` in the model's module, taken over only while this model's forward
     runs; other models keep the original), and ``readouts`` the per-interaction readout heads (``LinearReadoutBlock``,
     ``NonLinearReadoutBlock``) as one kernel per direction each.
+
+    ``fuse_radial`` (default off; with both the convolution and its radial MLP patched): the convolution forms its
+    per-edge weights cutoff * MLP(edge_feats) inside its kernels from the MLP's last hidden activations, so the
+    weights and their gradient are never stored (HipConvTP.attach_mlp).  Off, the MLP's kernels write the weights and
+    the convolution reads them, which measures faster on MI355X for the benchmark models: the fused kernels save the
+    weights' HBM round trip but spend more on the VALU than the round trip costs.
 
     ``double_backward`` (default off, as in the reference, where a backward under ``create_graph=True`` raises)
     makes the patched modules' gradients differentiable once more, for second derivatives with respect to the
@@ -141,6 +147,8 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             restored = isinstance(mlp, HipRadialMLP)
             if restored:
                 blk.conv_tp_weights = mlp.original[0]
+                if isinstance(getattr(blk, 'conv_tp', None), HipConvTP):
+                    blk.conv_tp.detach_mlp()
             if radial_mlp or restored:
                 skipped.append((f'interactions.{i}.conv_tp_weights',
                                 no2 + ('; the e3nn module an earlier patch replaced is restored' if restored else '')))
@@ -190,6 +198,12 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             new.tag = name
             blk.conv_tp_weights = new
             patched.append(name)
+    if fuse_radial and not double_backward:
+        for blk in getattr(model, 'interactions', []):
+            cv, mlp = getattr(blk, 'conv_tp', None), getattr(blk, 'conv_tp_weights', None)
+            if isinstance(cv, HipConvTP) and isinstance(mlp, HipRadialMLP) and cv.fused_mlp() is not mlp:
+                ok, _ = cv.attach_mlp(mlp)
+                mlp.fuse = ok
     if layouts:
         for i, blk in enumerate(getattr(model, 'interactions', [])):
             name = f'interactions.{i}.reshape'
@@ -289,6 +303,7 @@ def unpatch_model(model):
             blk.reshape = blk.reshape.original[0]
             restored.append(f'interactions.{i}.reshape')
         if isinstance(getattr(blk, 'conv_tp_weights', None), HipRadialMLP):
+            blk.conv_tp_weights.fuse = False
             blk.conv_tp_weights = blk.conv_tp_weights.original[0]
             restored.append(f'interactions.{i}.conv_tp_weights')
     for i, ro in enumerate(getattr(model, 'readouts', [])):

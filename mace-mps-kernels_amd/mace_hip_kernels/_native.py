@@ -22,9 +22,10 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_MLP_FWD, MH_MLP_BWD, MH_EMB_FWD, MH_EMB_BWD, MH_PERM_FWD, MH_PERM_BWD, MH_GEOM_FWD, MH_GEOM_BWD, \
     MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI, MH_READOUT_FWD, MH_READOUT_BWD, MH_SC_JVP, MH_SC_BWD2, \
     MH_SC_JVP_I, MH_SC_BWD2_I, MH_CSR_FILL, MH_CSR_COUNT, MH_CSR_SCAN, MH_CSR_SCATTER, MH_CSR_RANK, MH_SH_JVP, \
-    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2, MH_CSR_SORT = range(46)
+    MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2, MH_CSR_SORT, MH_MLP_HID, \
+    MH_MLP_HIDB, MH_CONV_FWD_M, MH_CONV_BWD_M, MH_CONV_GYSUM = range(51)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 23
+ABI_VERSION = 24
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -74,6 +75,10 @@ _SIGS = {
     'mh_sc_jvp': (ctypes.c_int, [_P] * 6 + [_I, _I, _P]),
     'mh_graph_build': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 6),
     'mh_graph_build_noalloc': (ctypes.c_int, [_P, _P, ctypes.c_int64, _I] + [_P] * 5),
+    'mh_mlp_hid': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
+    'mh_mlp_hid_bwd': (ctypes.c_int, [_P] * 4 + [_I] + [_P] * 3 + [ctypes.c_int64, _P]),
+    'mh_conv_fwd_mlp': (ctypes.c_int, [_P] * 10 + [_I, _P]),
+    'mh_conv_bwd_mlp': (ctypes.c_int, [_P] * 18 + [_I, _I, _I, _P]),
     'mh_launch_log': (ctypes.c_int, [ctypes.c_int]),
     'mh_launch_log_take': (ctypes.c_size_t, [ctypes.c_char_p, ctypes.c_size_t]),
     'mh_sh_jvp': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),

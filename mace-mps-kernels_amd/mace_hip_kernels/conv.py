@@ -713,8 +713,34 @@ class HipConvTP(torch.nn.Module):
         # a backward under create_graph=True: raise (the reference's behaviour) unless this is set, in which case
         # the gradients are differentiable again (_ConvAdjFn)
         self.double_backward = False
+        # the radial MLP whose output layer the fused kernels carry (attach_mlp), and those kernels
+        self.fused = None
+        self._fused_mlp = []
+
+    def attach_mlp(self, mlp):
+        """Form this convolution's weights inside its kernels from ``mlp``'s (a HipRadialMLP) last hidden
+        activations: compiles the fused kernels and packs the MLP's output layer for them.  (ok, reason)."""
+        from .conv_mlp import FusedConv, fused_supported
+        ok, why = fused_supported(self.spec, mlp.spec)
+        if not ok:
+            return False, why
+        self.fused = FusedConv(self.spec, mlp.spec, mlp.WhT.device)
+        self._fused_mlp = [mlp]                 # a plain list: the MLP stays a module of its own block only
+        return True, ''
+
+    def detach_mlp(self):
+        self.fused, self._fused_mlp = None, []
+
+    def fused_mlp(self):
+        return self._fused_mlp[0] if self._fused_mlp else None
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
+        from .conv_mlp import ConvMLPFn, FusedWeights
+        if isinstance(tp_weights, FusedWeights):
+            if self.fused is not None and tp_weights.mlp is self.fused_mlp():
+                # W = cutoff * MLP(edge_feats) formed inside the kernels: neither W nor its gradient is stored
+                return ConvMLPFn.apply(node_feats, edge_attrs, tp_weights.ef, tp_weights.cut, edge_index, self)
+            tp_weights = tp_weights.value()
         if isinstance(tp_weights, CutoffProduct):
             # the radial MLP's output times the cutoff, never formed: the kernels take the two factors
             return _ConvFn.apply(node_feats, edge_attrs, None, tp_weights.w0, tp_weights.cut, edge_index, self)

@@ -361,6 +361,55 @@ def source(spec):
     F += ['  }', '}', '']
     L += F
 
+    def walk_back(grp, cur):
+        """Lines walking dL/dh_last (in ``cur``{b}) back through the hidden layers (recomputed z's in scope) to
+        dL/d(edge features), stored to gef."""
+        B = []
+        for i in range(nh - 1, -1, -1):
+            T = cols[i] // 16
+            for b in grp:
+                for o in range(T):
+                    for r in range(4):
+                        B += ['  {',
+                              f'    const float z = z{i}_{b}[{o}][{r}], s = mlp_sig(z);',
+                              f'    {cur}{b}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
+                              '  }']
+            if i > 0:
+                Tp = cols[i - 1] // 16
+                nxt = f'dh{i - 1}_'
+                # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
+                for b in grp:
+                    B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
+                    B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
+                for ti in range(T):
+                    for o in range(Tp):
+                        B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
+                                 f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
+                    for r in range(4):
+                        for o in range(Tp):
+                            for b in grp:
+                                B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
+                                         f'{cur}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
+                cur = nxt
+        # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
+        T0 = cols[0] // 16
+        for o in range(-(-H0 // 16)):
+            B += ['  {',
+                  f'    const int row = {16 * o} + c16 < {rows[0]} ? {16 * o} + c16 : 0;']
+            B += [f'    mh_f4 d{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for b in grp]
+            for ti in range(T0):
+                B.append(f'    const mh_f4 w{ti} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][0]} + row * '
+                         f'{cols[0] + PAD} + {16 * ti} + 4 * q]);')
+                for r in range(4):
+                    B += [f'    d{b} = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}{b}[{ti}][{r}], d{b}, 0, 0, 0);'
+                          for b in grp]
+            for b in grp:
+                for r in range(4):
+                    B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[ej{b} * {H0} + {16 * o + r} + 4 * q] = '
+                             f'd{b}[{r}];')
+            B.append('  }')
+        return B
+
     # ------------------------------------------------------------------ backward
     # dL/dh_last = gW Wl^T first: K = the output columns, one bf16 step of 32 per chunk (lane group q: columns
     # 8 q .. 8 q + 7, two float4 loads of gW split into three bf16 parts); chunks of Wl [HL][CH] as bf16 rows of
@@ -441,53 +490,55 @@ def source(spec):
     for g0 in range(0, nb, HIDDEN_TILES_BWD):
         grp = range(g0, min(nb, g0 + HIDDEN_TILES_BWD))
         B += ['  {'] + xin(grp) + hidden_fwd(False, False, grp)
-        cur = 'dhs_'
-        for i in range(nh - 1, -1, -1):
-            T = cols[i] // 16
-            for b in grp:
-                for o in range(T):
-                    for r in range(4):
-                        B += ['  {',
-                              f'    const float z = z{i}_{b}[{o}][{r}], s = mlp_sig(z);',
-                              f'    {cur}{b}[{o}][{r}] *= {_lit(spec.c[i])} * s * (1.f + z * (1.f - s));',
-                              '  }']
-            if i > 0:
-                Tp = cols[i - 1] // 16
-                nxt = f'dh{i - 1}_'
-                # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
-                for b in grp:
-                    B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
-                    B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
-                for ti in range(T):
-                    for o in range(Tp):
-                        B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
-                                 f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
-                    for r in range(4):
-                        for o in range(Tp):
-                            for b in grp:
-                                B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
-                                         f'{cur}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
-                cur = nxt
-        # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
-        T0 = cols[0] // 16
-        for o in range(-(-H0 // 16)):
-            B += ['  {',
-                  f'    const int row = {16 * o} + c16 < {rows[0]} ? {16 * o} + c16 : 0;']
-            B += [f'    mh_f4 d{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for b in grp]
-            for ti in range(T0):
-                B.append(f'    const mh_f4 w{ti} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][0]} + row * '
-                         f'{cols[0] + PAD} + {16 * ti} + 4 * q]);')
-                for r in range(4):
-                    B += [f'    d{b} = __builtin_amdgcn_mfma_f32_16x16x4f32(w{ti}[{r}], {cur}{b}[{ti}][{r}], d{b}, 0, 0, 0);'
-                          for b in grp]
-            for b in grp:
-                for r in range(4):
-                    B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[ej{b} * {H0} + {16 * o + r} + 4 * q] = '
-                             f'd{b}[{r}];')
-            B.append('  }')
+        B += walk_back(grp, 'dhs_')
         B += ['  }', '  __builtin_amdgcn_sched_barrier(0);       // one group finished before the next starts']
     B += ['}', '']
     L += B
+
+    # ------------------------------------------------------------------ hidden layers only (fused convolution)
+    # mlp_hid: cutoff * the last hidden activations, c h, as the fused convolution's MFMA operand: for each K step s
+    # of 32 and lane group q, the eight values at K positions 8 q .. 8 q + 7 (features 32 s + 16 t + 4 q + r, the
+    # _kperm order, which is this lane's own MFMA result layout) split exactly into three bf16 parts:
+    # hc [E][S][3][4][8] uint16.  mlp_hidb: from the sum of the convolution's partial dL/d(c h) (np_ slices
+    # [E, HL] in natural feature order, summed in order), dL/dcutoff = sum_j P h and dL/d(edge features) through the
+    # hidden layers with dL/dh = c P
+    H = head(spec.kname('mlp_hid'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
+             'const float* __restrict__ cutv, unsigned short* __restrict__ hc, long long E', Lo['tr_size'], NB_FWD)
+    H += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(NB_FWD)) + hidden_fwd(True, True, range(NB_FWD))
+    for b in range(NB_FWD):
+        hl = f'h{nh - 1}_{b}'
+        H += [f'  if (live{b}) {{', f'    const float cb = cutv[ej{b}];']
+        for st in range(S):
+            H += [f'    {{ const float v[8] = {{{", ".join(f"cb * {hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
+                  '      mh_bf8 sp[3];',
+                  '      mh_split8(v, sp);',
+                  f'      mh_bf8* __restrict__ dst = reinterpret_cast<mh_bf8*>(hc) + (ej{b} * {S} + {st}) * 12 + q;']
+            H += [f'      dst[{4 * p}] = sp[{p}];' for p in range(3)]
+            H += ['    }']
+        H.append('  }')
+    L += H + ['}', '']
+    grp = range(NB_BWD)
+    H = head(spec.kname('mlp_hidb'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
+             'const float* __restrict__ gp, int np_, const float* __restrict__ cutv, float* __restrict__ gef, '
+             'float* __restrict__ gcut, long long E', Lo['nat_size'], NB_BWD)
+    H += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin(grp) + hidden_fwd(False, False, grp)
+    for b in grp:
+        H += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
+        H += ['  for (int pp = 0; pp < np_; ++pp) {',
+              f'    const float* __restrict__ gr = gp + ((size_t)pp * E + ejc{b}) * {HL} + 4 * q;']
+        H += [f'    dhs_{b}[{o}] += *reinterpret_cast<const mh_f4*>(gr + {16 * o});' for o in range(TL)]
+        H += ['  }', '  {', '    float gc = 0.f;']
+        for o in range(TL):
+            for r in range(4):
+                H.append(f'    {{ const float z = z{nh - 1}_{b}[{o}][{r}]; '
+                         f'gc = fmaf(dhs_{b}[{o}][{r}], {_lit(spec.c[nh - 1])} * z * mlp_sig(z), gc); }}')
+        H += ['    gc += __shfl_xor(gc, 16, 64);', '    gc += __shfl_xor(gc, 32, 64);',
+              f'    if (live{b} && q == 0) gcut[ej{b}] = gc;',
+              f'    const float cb = cutv[ejc{b}];']
+        H += [f'    dhs_{b}[{o}] *= cb;' for o in range(TL)]
+        H += ['  }']
+    H += walk_back(grp, 'dhs_')
+    L += H + ['}', '']
     return '\n'.join(L)
 
 
@@ -577,6 +628,8 @@ class HipRadialMLP(torch.nn.Module):
             self.module = _native.Module(code, {
                 _native.MH_MLP_FWD: (self.spec.kname('mlp_fwd'), BLOCK, 64 * NB_FWD),
                 _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), BLOCK, 64 * NB_BWD),
+                _native.MH_MLP_HID: (self.spec.kname('mlp_hid'), BLOCK, 64 * NB_FWD),
+                _native.MH_MLP_HIDB: (self.spec.kname('mlp_hidb'), BLOCK, 64 * NB_BWD),
             })
         pw = packed_weights(self.spec)
         for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1])):
@@ -586,7 +639,13 @@ class HipRadialMLP(torch.nn.Module):
         self.hs = self.spec.hs
         self.original = [mod]
         self.tag = 'radial_mlp'
+        # set by patch_model when the convolution fed by this MLP forms its weights itself (HipConvTP.attach_mlp):
+        # the output is then returned unformed
+        self.fuse = False
 
     def forward(self, ef):
+        if self.fuse and ef.dim() == 2 and ef.shape[1] == self.spec.hs[0]:
+            from .conv_mlp import PendingRadial
+            return PendingRadial((ef.shape[0], self.spec.hs[-1]), ef, ef, self)
         # the output's product with MACE's cutoff column is handed to the convolution unformed (conv.RadialWeights)
         return _MLPFn.apply(ef, self).as_subclass(_conv.RadialWeights)

@@ -149,6 +149,64 @@ def test_conv_factored_cutoff_weights(want_x):
         assert xt.grad is None
 
 
+FUSED_TOL = 1e-5      # the MLP's fp32 hidden layers and the fp32-accurate output layer add ~1e-6 to the conv's error
+
+
+@pytest.mark.parametrize('hidden,lmax,want_x', [('128x0e+128x1o', 3, True), ('128x0e+128x1o', 3, False),
+                                                ('32x0e+32x1o', 2, True), ('96x0e+96x1o', 3, True)])
+def test_conv_mlp_fused_vs_oracle(hidden, lmax, want_x):
+    """The convolution with the radial MLP's output layer inside it (W = cutoff * MLP(ef) formed by the kernels,
+    never stored) against the oracle's convolution on W from a float64 copy of the MLP: output, and the gradients
+    of x, Y, the edge features (the oracle's dL/dW times the cutoff, through float64 autograd of the MLP) and the
+    cutoff (sum over k of dL/dW * W0).  Both layers of each model; some cutoffs exactly zero, a receiver whose every
+    edge has zero cutoff, rows longer than 64 edges, isolated nodes."""
+    from mace_hip_kernels.conv_mlp import FusedWeights
+    dev = _dev()
+    model = factory.make_model(hidden, lmax, 3, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(17)
+    for li, blk in enumerate(model.interactions):
+        print(f'[case] fused conv+MLP {hidden} l{lmax} layer {li} want_x={want_x}', flush=True)
+        op = HipConvTP(blk.conv_tp, device=dev)
+        mlp = HipRadialMLP(blk.conv_tp_weights, device=dev)
+        ok, why = op.attach_mlp(mlp)
+        assert ok, why
+        mlp.fuse = True
+        desc = oconv.describe_tp(blk.conv_tp)
+        coef = oconv.path_terms(desc)
+        n, e = 43, 900
+        s, r = _graph(rng, n, e)
+        x, Y = rng.normal(size=(n, desc['x_dim'])), rng.normal(size=(e, desc['y_dim']))
+        ef = rng.normal(size=(e, mlp.spec.hs[0]))
+        c = rng.uniform(0.0, 1.0, size=(e, 1))
+        c[::7] = 0.0
+        c[r == 2] = 0.0
+        g = rng.normal(size=(n, desc['out_dim']))
+        t = lambda a, rg=True: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=rg)  # noqa: E731
+        xt, Yt, eft, ct = t(x, want_x), t(Y), t(ef), t(c)
+        W = mlp(eft) * ct
+        assert isinstance(W, FusedWeights)
+        out = op(xt, Yt, W, torch.tensor(np.stack([s, r]), device=dev))
+        out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+        m64 = copy.deepcopy(blk.conv_tp_weights).to(torch.float64)
+        ef64 = torch.tensor(ef, requires_grad=True)
+        W0 = m64(ef64)
+        W0n = W0.detach().numpy()
+        Wd = W0n * c
+        assert _rel(out.detach().double().cpu().numpy(), oconv.conv_fwd(desc, coef, x, Y, Wd, s, r, n)) < FUSED_TOL
+        gW = oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)
+        W0.backward(torch.tensor(gW * c))
+        assert _rel(eft.grad.double().cpu().numpy(), ef64.grad.numpy()) < FUSED_TOL
+        assert _rel(ct.grad.double().cpu().numpy(), (gW * W0n).sum(1, keepdims=True)) < FUSED_TOL
+        assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, Wd, s, r)) < FUSED_TOL
+        if want_x:
+            assert _rel(xt.grad.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, Wd, s, r, n)) < FUSED_TOL
+        else:
+            assert xt.grad is None
+        # bitwise repeatable
+        out2 = op(xt, Yt, mlp(eft) * ct, torch.tensor(np.stack([s, r]), device=dev))
+        assert torch.equal(out, out2)
+
+
 def test_conv_c_abi_bwd_x_and_bwd_wy():
     """The reference-shaped entry points mh_conv_bwd_x / mh_conv_bwd_wy against the oracle and the fused kernel."""
     dev = _dev()

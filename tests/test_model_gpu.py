@@ -90,6 +90,27 @@ def test_matches_e3nn_all_configs(config):
         print(f'       |dE| {dE * 1e3:.4f} meV  max|dF| {dF:.2e}', flush=True)
 
 
+@pytest.mark.parametrize('config', list(factory.REF_CONFIGS))
+def test_fused_radial_matches_e3nn(config):
+    """fuse_radial=True: every interaction block whose convolution and radial MLP the fused kernels take runs the MLP's
+    output layer inside the convolution; energies and forces stay within the unfused path's tolerances."""
+    dev = _dev()
+    hidden, lmax, corr = factory.REF_CONFIGS[config]
+    model = factory.make_model(hidden, lmax, corr)
+    ref = copy.deepcopy(model).to(dev, torch.float64)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    patch_model(met, verbose=False, fuse_radial=True)
+    fused = [blk.conv_tp.fused_mlp() is blk.conv_tp_weights for blk in met.interactions]
+    if not any(fused):
+        pytest.skip(f'{config}: no block takes the fused kernels')
+    for s in (0, 1):
+        print(f'[case] fused radial {config} seed {s} blocks {fused}', flush=True)
+        st = factory.make_structure(seed=s)
+        batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
+        dE, dF = _check(ref, met, batch, dev, [len(st)])
+        print(f'       |dE| {dE * 1e3:.4f} meV  max|dF| {dF:.2e}', flush=True)
+
+
 def test_rotation_equivariance():
     dev = _dev()
     print('[case] rotation equivariance', flush=True)
@@ -198,18 +219,22 @@ def test_double_backward_upgrade_and_stress_loss():
         assert np.abs(g_met[k] - g_ref[k]).max() < 1e-4 * scale, k
 
 
-def test_patched_model_launches_the_fast_paths():
+@pytest.mark.parametrize('fuse', [False, True])
+def test_patched_model_launches_the_fast_paths(fuse):
     """The kernels an E+F call of the patched model runs, read from the C ABI's launch log (no assumption about which
-    path a module takes): the factored convolution kernels (W0 * cutoff never formed: conv_fwdc, conv_bwdrc), layer
-    1's backward without dX (no conv_gxsum for it: the engine never asks for the first layer's node-feature
-    gradient), the symmetric contraction reading e3nn's irreps layout (sc_*i: reshape_irreps left unformed, so no
-    permutation kernel), and every other drop-in's kernels."""
+    path a module takes).  Default: the factored convolution kernels (W0 * cutoff never formed: conv_fwdc,
+    conv_bwdrc) after the radial MLP's kernels (mlp_fwd, mlp_bwd).  fuse_radial: the convolutions with the radial
+    MLP's output layer inside (conv_fwdm, conv_bwdm: the per-edge weights and their gradient never stored; the MLPs
+    run their hidden layers only, mlp_hid / mlp_hidb).  Both: layer 1's backward without dX (no conv_gxsum for it:
+    the engine never asks for the first layer's node-feature gradient), the symmetric contraction reading e3nn's
+    irreps layout (sc_*i: reshape_irreps left unformed, so no permutation kernel), and every other drop-in's
+    kernels."""
     from mace_hip_kernels import _native
     dev = _dev()
-    print('[case] kernels launched by the patched model (config 1)', flush=True)
+    print(f'[case] kernels launched by the patched model (config 1, fuse_radial={fuse})', flush=True)
     model, batch, _ = factory.workload(1)
     met = copy.deepcopy(model).to(dev)
-    patch_model(met, verbose=False)
+    patch_model(met, verbose=False, fuse_radial=fuse)
     met(D.fresh(_to(batch, dev, torch.float32)), compute_force=True)          # graph and element order cached
     b = D.fresh(_to(batch, dev, torch.float32))
     with _native.timing() as tm:
@@ -217,19 +242,34 @@ def test_patched_model_launches_the_fast_paths():
     torch.cuda.synchronize()
     sym = {tag: names for tag, names in tm.symbols.items()}
     flat = [n for names in sym.values() for n in names]
-    assert sym['conv_fwd[interactions.0.conv_tp]'] == ['conv_fwdc_x128_o2048'], sym
-    assert sym['conv_fwd[interactions.1.conv_tp]'] == ['conv_fwdc_x512_o5120'], sym
-    assert sym['conv_bwd[interactions.0.conv_tp]'] == ['conv_bwdrc_x128_o2048'], sym
-    assert sym['conv_bwd[interactions.1.conv_tp]'] == ['conv_bwdrc_x512_o5120', 'conv_gxsum_x512_o5120'], sym
+    if fuse:
+        assert sym['conv_fwd[interactions.0.conv_tp]'] == ['conv_fwdm_x128_o2048_h64'], sym
+        assert sym['conv_fwd[interactions.1.conv_tp]'] == ['conv_fwdm_x512_o5120_h64'], sym
+        assert sym['conv_bwd[interactions.0.conv_tp]'] == ['conv_bwdm_x128_o2048_h64',
+                                                            'conv_gysum_x128_o2048_h64'], sym
+        assert sym['conv_bwd[interactions.1.conv_tp]'] == ['conv_bwdm_x512_o5120_h64', 'conv_gysum_x512_o5120_h64',
+                                                            'conv_gxsum_x512_o5120'], sym
+        for i in range(2):
+            assert sym[f'mlp_hid[interactions.{i}.conv_tp_weights]'][0].startswith('mlp_hid_'), sym
+            assert sym[f'mlp_bwd[interactions.{i}.conv_tp_weights]'][0].startswith('mlp_hidb_'), sym
+        banned = ('conv_fwdc_', 'conv_bwdr', 'mlp_fwd_', 'mlp_bwd_')
+    else:
+        assert sym['conv_fwd[interactions.0.conv_tp]'] == ['conv_fwdc_x128_o2048'], sym
+        assert sym['conv_fwd[interactions.1.conv_tp]'] == ['conv_fwdc_x512_o5120'], sym
+        assert sym['conv_bwd[interactions.0.conv_tp]'] == ['conv_bwdrc_x128_o2048'], sym
+        assert sym['conv_bwd[interactions.1.conv_tp]'] == ['conv_bwdrc_x512_o5120', 'conv_gxsum_x512_o5120'], sym
+        for prefix in ('mlp_fwd_', 'mlp_bwd_'):
+            assert any(n.startswith(prefix) for n in flat), (prefix, flat)
+        banned = ('conv_fwdm_', 'conv_bwdm_', 'mlp_hid')
     for i in range(2):
         names = sym[f'sc_fwd[products.{i}.symmetric_contractions]'] + \
             sym[f'sc_bwd[products.{i}.symmetric_contractions]']
         assert len(names) == 2 and all(n.startswith(('sc_fwdi_', 'sc_bwdi_', 'sc_fwdgi_', 'sc_bwdgi_'))
                                        for n in names), names
-    for prefix in ('mlp_fwd_', 'mlp_bwd_', 'sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_', 'geom_fwd', 'geom_bwd',
-                   'lin_fwd_', 'lin_bwd_', 'ro_fwd_', 'ro_bwd_'):
+    for prefix in ('sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_', 'geom_fwd', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
+                   'ro_fwd_', 'ro_bwd_'):
         assert any(n.startswith(prefix) for n in flat), (prefix, flat)
-    assert not any(n.startswith(('perm_', 'conv_fwd_', 'conv_bwd_', 'conv_bwdr_')) for n in flat), flat
+    assert not any(n.startswith(('perm_', 'conv_fwd_', 'conv_bwd_') + banned) for n in flat), flat
 
 
 def test_unsupported_block_is_skipped():

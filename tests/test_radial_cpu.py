@@ -102,3 +102,47 @@ def test_generated_source_compiles(widths):
     from mace_hip_kernels import _native
     spec = radial.MLPSpec(enn.FullyConnectedNet(widths, torch.nn.functional.silu))
     assert len(_native.compile_source(radial.source(spec))) > 1000
+
+
+def test_fused_output_layer_packing():
+    """The fused convolution's two packings of the MLP's output layer A [HL, NINS·MUL] (conv_mlp.FusedSpec.pack_fwd,
+    conv_mlp.pack_bwd): summing the three bf16 parts at every documented (lane, position) gives float32(A) back
+    exactly (forward: K position 8 q + t of step s is hidden feature 32 s + 16 (t / 4) + 4 q + t % 4), every element of
+    A appears (forward) and the padding of an odd instruction count is zero (backward)."""
+    from mace_hip_kernels import conv as hconv, conv_mlp, radial
+    from mace_lite import factory
+    for hidden, lmax in (('128x0e+128x1o', 3), ('32x0e+32x1o', 2)):
+        m = factory.make_model(hidden, lmax, 3, elements=factory.ELEMENTS_PTCOH)
+        for blk in m.interactions:
+            cs, ms = hconv.ConvSpec(blk.conv_tp), radial.MLPSpec(blk.conv_tp_weights)
+            fs = conv_mlp.FusedSpec(cs, ms)
+            A = np.asarray(ms.A[-1], dtype=np.float32).astype(np.float64)
+            HL, mul, nk = fs.HL, cs.mul, len(fs.korder)
+
+            def val(parts_u16):
+                return sum((p.astype(np.uint32) << 16).view(np.float32).astype(np.float64) for p in parts_u16)
+            f = fs.pack_fwd().reshape(fs.nct, nk, fs.S, 3, 64, 8)
+            seen = np.zeros_like(A, dtype=bool)
+            for ct in range(fs.nct):
+                for ki, k in enumerate(fs.korder):
+                    for s in range(fs.S):
+                        for lane in range(64):
+                            q, i16 = divmod(lane, 16)
+                            rows = 32 * s + 16 * (np.arange(8) // 4) + 4 * q + np.arange(8) % 4
+                            col = k * mul + 16 * ct + i16
+                            got = val([f[ct, ki, s, p, lane] for p in range(3)])
+                            assert np.array_equal(got, A[rows, col])
+                            seen[rows, col] = True
+            assert seen.all()
+            b = conv_mlp.pack_bwd(fs).reshape(fs.nct, (nk + 1) // 2, 3, HL // 16, 64, 8)
+            for ct in range(fs.nct):
+                for kp in range((nk + 1) // 2):
+                    for mt in range(HL // 16):
+                        for lane in range(64):
+                            q, i16 = divmod(lane, 16)
+                            got = val([b[ct, kp, p, mt, lane] for p in range(3)])
+                            for t in range(2):
+                                ki = 2 * kp + t
+                                want = (A[16 * mt + i16, fs.korder[ki] * mul + 16 * ct + 4 * q + np.arange(4)]
+                                        if ki < nk else np.zeros(4))
+                                assert np.array_equal(got[4 * t:4 * t + 4], want)
