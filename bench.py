@@ -195,6 +195,7 @@ def _isolated(a):
     import torch
     from mace_hip_kernels import HipConvTP, HipSymmetricContraction, _native
     from mace_hip_kernels import conv as hconv, radial
+    from mace_hip_kernels import symmetric as hsym
     from mace_lite import factory
     dev = torch.device('cuda:0')
     model, batch, meta = factory.workload(a.config)
@@ -299,7 +300,14 @@ def _isolated(a):
         report(f'sc_fwd[{tag}] per-node', s.kname('sc_fwd'), ms, bf, ff * N * s.C)
         ms = timed(lambda i: lib.mh_sc_bwd(h, P(X), P(elem), P(op.T), P(G), P(GX), N, stream), 1)
         report(f'sc_bwd[{tag}] per-node', s.kname('sc_bwd'), ms, bb, fb * N * s.C)
-        _log(f'{tag}: the model uses the {"grouped" if op.use_grouped(N, dev) else "per-node"} kernels at N = {N}')
+        slots = hsym.group_slots(batch['node_attrs'].to(dev))
+        ms = timed(lambda i: lib.mh_sc_fwd_staged(h, P(X), P(slots), slots.numel(), P(elem), P(op.TS), P(out), N, 0,
+                                                  stream), 1)
+        report(f'sc_fwd[{tag}] LDS-staged', s.kname('sc_fwds'), ms, bf, ff * N * s.C)
+        ms = timed(lambda i: lib.mh_sc_bwd_staged(h, P(X), P(slots), slots.numel(), P(elem), P(op.TS), P(G), P(GX),
+                                                  N, 0, stream), 1)
+        report(f'sc_bwd[{tag}] LDS-staged', s.kname('sc_bwds'), ms, bb, fb * N * s.C)
+        _log(f'{tag}: the model uses the {op.kernel_family(N, dev)} kernels at N = {N}')
         del op
 
 

@@ -87,7 +87,11 @@ enum mh_kernel_kind {
     MH_CONV_FWD_M = 48,  /* convolution forward with the MLP's output layer fused (grid_y: tiles)  */
     MH_CONV_BWD_M = 49,  /* its backward: dX messages, gY and dL/d(c h) partials (grid_y: tiles)   */
     MH_CONV_GYSUM = 50,  /* gY = sum of the fused backward's per-channel-tile partials             */
-    MH_NUM_KINDS = 51
+    MH_SC_FWD_S = 51,    /* symmetric contraction, coefficient rows staged in LDS (grid_y: blocks)  */
+    MH_SC_BWD_S = 52,    /* its x-gradient                                                          */
+    MH_SC_FWD_SI = 53,   /* MH_SC_FWD_S in the irreps layout                                        */
+    MH_SC_BWD_SI = 54,   /* MH_SC_BWD_S in the irreps layout                                        */
+    MH_NUM_KINDS = 55
 };
 
 /* flags of mh_conv_bwd */
@@ -213,6 +217,21 @@ int mh_sc_fwd_irreps(mh_module* m, const float* X, const int32_t* elem, const in
                      float* out, int32_t N, void* stream);
 int mh_sc_bwd_irreps(mh_module* m, const float* X, const int32_t* elem, const int32_t* order, const float* T,
                      const float* G, float* GX, int32_t N, void* stream);
+
+/* The symmetric contraction with the element's coefficient table streamed through LDS: each workgroup takes
+ * rows_per_block consecutive entries of `slots` [nslots] (node ids, -1 for an empty slot; every group of
+ * rows_per_block entries holds nodes of one element and starts with a node, or is empty from its first entry on,
+ * which ends the workgroup at once) and one 64-channel block (grid_y).  TS is the table in the staged layout
+ * (rows in the kernel's walk order, chunk by chunk, symmetric.pack_staged), copied to LDS once per workgroup, so
+ * every coefficient read from L2 serves all nodes of the group.  layout 0: X, GX as [N, C, n_ell] (MH_SC_FWD_S /
+ * MH_SC_BWD_S); 1: e3nn's irreps layout as in mh_sc_fwd_irreps (MH_SC_FWD_SI / MH_SC_BWD_SI).  nslots must be a
+ * multiple of rows_per_block.  Same results as mh_sc_fwd / mh_sc_bwd up to fp32 rounding of the same per-node
+ * sums.  Replace the reference's lib.sc_fwd / lib.sc_bwd (symmetric.py:82-131, launched at symmetric.py:140, 154)
+ * with the per-element tables in LDS, as its kernels intend (symmetric.py:91, 98, 101). */
+int mh_sc_fwd_staged(mh_module* m, const float* X, const int32_t* slots, int32_t nslots, const int32_t* elem,
+                     const float* TS, float* out, int32_t N, int32_t layout, void* stream);
+int mh_sc_bwd_staged(mh_module* m, const float* X, const int32_t* slots, int32_t nslots, const int32_t* elem,
+                     const float* TS, const float* G, float* GX, int32_t N, int32_t layout, void* stream);
 
 /* Second derivatives of the symmetric contraction, behind a double backward.  With P(X) the contraction of
  * mh_sc_fwd and V a direction in the layout of X:

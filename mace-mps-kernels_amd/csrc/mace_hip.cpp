@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 24; }
+int mh_version(void) { return 25; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -361,6 +361,28 @@ int mh_sc_bwd_irreps(mh_module* m, const float* X, const int32_t* elem, const in
     }
     void* args[] = {&X, &elem, &order, &T, &G, &GX, &N};
     return launch(m, MH_SC_BWD_GI, N, args, stream, "mh_sc_bwd_irreps");
+}
+
+int mh_sc_fwd_staged(mh_module* m, const float* X, const int32_t* slots, int32_t nslots, const int32_t* elem,
+                     const float* TS, float* out, int32_t N, int32_t layout, void* stream) {
+    if (layout != 0 && layout != 1) return fail(-1, "mh_sc_fwd_staged: layout must be 0 or 1");
+    const int kind = layout ? MH_SC_FWD_SI : MH_SC_FWD_S;
+    if (m && m->k[kind].fn && nslots % m->k[kind].rows_per_block != 0)
+        return fail(-1, "mh_sc_fwd_staged: nslots must be a multiple of the workgroup's slot count");
+    if (N <= 0) return 0;
+    void* args[] = {&X, &slots, &elem, &TS, &out, &N};
+    return launch(m, kind, nslots, args, stream, "mh_sc_fwd_staged");
+}
+
+int mh_sc_bwd_staged(mh_module* m, const float* X, const int32_t* slots, int32_t nslots, const int32_t* elem,
+                     const float* TS, const float* G, float* GX, int32_t N, int32_t layout, void* stream) {
+    if (layout != 0 && layout != 1) return fail(-1, "mh_sc_bwd_staged: layout must be 0 or 1");
+    const int kind = layout ? MH_SC_BWD_SI : MH_SC_BWD_S;
+    if (m && m->k[kind].fn && nslots % m->k[kind].rows_per_block != 0)
+        return fail(-1, "mh_sc_bwd_staged: nslots must be a multiple of the workgroup's slot count");
+    if (N <= 0) return 0;
+    void* args[] = {&X, &slots, &elem, &TS, &G, &GX, &N};
+    return launch(m, kind, nslots, args, stream, "mh_sc_bwd_staged");
 }
 
 int mh_sc_jvp(mh_module* m, const float* X, const float* V, const int32_t* elem, const float* T, float* out,

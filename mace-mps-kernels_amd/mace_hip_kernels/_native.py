@@ -23,9 +23,10 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_SC_FWD_I, MH_SC_BWD_I, MH_SC_FWD_GI, MH_SC_BWD_GI, MH_READOUT_FWD, MH_READOUT_BWD, MH_SC_JVP, MH_SC_BWD2, \
     MH_SC_JVP_I, MH_SC_BWD2_I, MH_CSR_FILL, MH_CSR_COUNT, MH_CSR_SCAN, MH_CSR_SCATTER, MH_CSR_RANK, MH_SH_JVP, \
     MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2, MH_CSR_SORT, MH_MLP_HID, \
-    MH_MLP_HIDB, MH_CONV_FWD_M, MH_CONV_BWD_M, MH_CONV_GYSUM = range(51)
+    MH_MLP_HIDB, MH_CONV_FWD_M, MH_CONV_BWD_M, MH_CONV_GYSUM, MH_SC_FWD_S, MH_SC_BWD_S, MH_SC_FWD_SI, \
+    MH_SC_BWD_SI = range(55)
 MH_WANT_GX, MH_WANT_GWY = 1, 2
-ABI_VERSION = 24
+ABI_VERSION = 25
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -70,6 +71,8 @@ _SIGS = {
     'mh_sc_fwd_sorted': (ctypes.c_int, [_P] * 6 + [_I, _P]),
     'mh_sc_fwd_irreps': (ctypes.c_int, [_P] * 6 + [_I, _P]),
     'mh_sc_bwd_irreps': (ctypes.c_int, [_P] * 7 + [_I, _P]),
+    'mh_sc_fwd_staged': (ctypes.c_int, [_P] * 3 + [_I] + [_P] * 3 + [_I, _I, _P]),
+    'mh_sc_bwd_staged': (ctypes.c_int, [_P] * 3 + [_I] + [_P] * 4 + [_I, _I, _P]),
     'mh_sc_bwd_sorted': (ctypes.c_int, [_P] * 7 + [_I, _P]),
     'mh_sc_fwd': (ctypes.c_int, [_P] * 5 + [_I, _P]),
     'mh_sc_jvp': (ctypes.c_int, [_P] * 6 + [_I, _I, _P]),

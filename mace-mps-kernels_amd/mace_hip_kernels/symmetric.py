@@ -290,6 +290,236 @@ def _bwd_walk_g(spec, node, depth, L, ind, cnt, nb):
         L.append(f'{ind}}}')
 
 
+# ------------------------------------------------------------------------------- LDS-staged kernels
+STAGE_WAVES = 4        # waves per workgroup of the staged kernels (one channel block, nodes of one element)
+STAGE_NPW = 2          # nodes per wave: every coefficient read from LDS feeds STAGE_NPW FMAs
+STAGE_ROWS = 64        # coefficient rows per LDS chunk; two chunks resident (double buffer)
+STAGE_FENCE = 32       # rows between anti-hoisting fences in the staged walk (0: none)
+SLOT_GROUP = STAGE_WAVES * STAGE_NPW     # node slots per workgroup of the staged kernels
+
+
+def walk_rows(spec):
+    """Table rows in the order the trie walk reads them: at every trie node its terms' M rows, then its children in
+    index order (the forward and the backward walk read in the same order)."""
+    out = []
+
+    def rec(node):
+        for _, r0, M in node['terms']:
+            out.extend(range(r0, r0 + M))
+        for i in sorted(node['kids']):
+            rec(node['kids'][i])
+    rec(_trie(spec))
+    assert sorted(out) == list(range(spec.nrows))
+    return out
+
+
+def stage_chunks(spec, cr=None):
+    cr = STAGE_ROWS if cr is None else cr
+    return -(-spec.nrows // cr)
+
+
+def pack_staged(spec, cr=None):
+    """The coefficient table for the staged kernels: rows in walk order, per (element, 64-channel block) a
+    contiguous run of chunks of ``cr`` rows; inside a chunk, lane l's four consecutive rows r..r+3 of channel
+    64 cb + l are one 16-byte quad: [n_elem][ncb][chunks · cr / 4][64][4] float32 (zero-padded rows and channels).
+    A chunk is then one contiguous block that the workgroup copies to LDS as is, and one ds_read_b128 gives a lane
+    four rows."""
+    cr = STAGE_ROWS if cr is None else cr
+    T = spec.T.numpy()                                       # [e, R, C]
+    ne, R, C = T.shape
+    RP = stage_chunks(spec, cr) * cr
+    buf = np.zeros((ne, RP, spec.ncb * WAVE), dtype=np.float32)
+    buf[:, :R, :C] = T[:, walk_rows(spec), :]
+    buf = buf.reshape(ne, RP // 4, 4, spec.ncb, WAVE)        # [e][quad][row in quad][cb][lane]
+    return np.ascontiguousarray(buf.transpose(0, 3, 1, 4, 2))  # [e][cb][quad][lane][row in quad]
+
+
+class _Stage:
+    """Coefficient reads of a staged walk.  Walk position w (row ``walk_rows[w]``) is read from LDS buffer
+    (w // cr) % 2; every fourth position loads the lane's next quad.  Entering chunk k >= 1 stores the staged
+    registers (chunk k, loaded from global memory during chunk k - 1) into buffer k % 2, whose previous chunk k - 2
+    every wave finished before the last barrier, then waits at the workgroup barrier and issues the global loads of
+    chunk k + 1."""
+
+    def __init__(self, spec, cr, fence):
+        self.pos = {r: w for w, r in enumerate(walk_rows(spec))}
+        self.cr, self.fence, self.nchunk = cr, fence, stage_chunks(spec, cr)
+        self.nst = cr // 16                   # 16-byte staging registers per thread (256 threads per chunk copy)
+        self.sb = cr // 4 * WAVE              # quads per chunk
+        self.next, self.since = 0, 0
+
+    def copy_in(self, k, ind):
+        return [f'{ind}sg{v} = src[{k * self.sb} + t + {256 * v}];' for v in range(self.nst)]
+
+    def store(self, k, ind):
+        return [f'{ind}sl[{(k % 2) * self.sb} + t + {256 * v}] = sg{v};' for v in range(self.nst)]
+
+    def prologue(self, ind):
+        L = [f'{ind}mh_f4 ' + ', '.join(f'sg{v}' for v in range(self.nst)) + ';', f'{ind}mh_f4 tq;']
+        L += self.copy_in(0, ind) + self.store(0, ind)
+        if self.nchunk > 1:
+            L += self.copy_in(1, ind)
+        return L + [f'{ind}__syncthreads();']
+
+    def row(self, r, L, ind, live):
+        w = self.pos[r]
+        assert w == self.next, (w, self.next)
+        self.next += 1
+        k = w // self.cr
+        if w and w % self.cr == 0:
+            L += self.store(k, ind) + [f'{ind}__syncthreads();']
+            if k + 1 < self.nchunk:
+                L += self.copy_in(k + 1, ind)
+        if w % 4 == 0:
+            self.since += 4
+            if self.fence and self.since >= self.fence:
+                self.since = 0
+                chunks = [live[i:i + 16] for i in range(0, len(live), 16)] or [[]]
+                for ci, ch in enumerate(chunks):
+                    ops = ', '.join([f'"+v"({v})' for v in ch] + (['"+v"(lo)'] if ci == len(chunks) - 1 else []))
+                    L.append(f'{ind}asm volatile("" : {ops});')
+            L.append(f'{ind}tq = sl[{(k % 2) * self.sb + (w % self.cr) // 4 * WAVE} + lo];')
+        return f'tq[{w % 4}]'
+
+
+def _fwd_walk_s(spec, node, depth, L, ind, st, nb):
+    """The forward walk for ``nb`` nodes of one element with coefficients from LDS (same expressions per node as
+    ``_fwd_walk``)."""
+    live = [f'a{j}_{bi}_{m}' for j in range(nb) for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+    for bi, r0, M in node['terms']:
+        for m in range(M):
+            e = st.row(r0 + m, L, ind, live)
+            L.append(f'{ind}{{ const float tc = {e};')
+            L += [f'{ind}  a{j}_{bi}_{m} = fmaf(tc, p{j}_{depth}, a{j}_{bi}_{m});' for j in range(nb)]
+            L.append(f'{ind}}}')
+    for i in sorted(node['kids']):
+        decl = ' '.join(f'const float p{j}_{depth + 1} = ' + (f'x{j}_{i};' if depth == 0 else f'p{j}_{depth} * x{j}_{i};')
+                        for j in range(nb))
+        L.append(f'{ind}{{ {decl}')
+        _fwd_walk_s(spec, node['kids'][i], depth + 1, L, ind + '  ', st, nb)
+        L.append(f'{ind}}}')
+
+
+def _bwd_walk_s(spec, node, depth, L, ind, st, nb):
+    """The reverse-mode walk for ``nb`` nodes of one element with coefficients from LDS (same expressions per node
+    as ``_bwd_walk``)."""
+    live = [f'd{j}_{i}' for j in range(nb) for i in range(spec.n_ell)] + \
+           [f'G{j}_{k}' for j in range(nb) for k in range(1, depth + 1)]
+    for bi, r0, M in node['terms']:
+        L.append(f'{ind}{{')
+        for m in range(M):
+            e = st.row(r0 + m, L, ind + '  ', live)
+            L.append(f'{ind}  const float tc{m} = {e};')
+        for j in range(nb):
+            s_ = ' + '.join(f'tc{m} * g{j}_{bi}_{m}' for m in range(M))
+            L.append(f'{ind}  G{j}_{depth} += {s_};')
+        L.append(f'{ind}}}')
+    for i in sorted(node['kids']):
+        kid = node['kids'][i]
+        decl = ' '.join(f'const float p{j}_{depth + 1} = ' + (f'x{j}_{i};' if depth == 0 else f'p{j}_{depth} * x{j}_{i};')
+                        for j in range(nb))
+        L.append(f'{ind}{{ {decl}')
+        L.append(f'{ind}  ' + ' '.join(f'float G{j}_{depth + 1} = 0.0f;' for j in range(nb)))
+        _bwd_walk_s(spec, kid, depth + 1, L, ind + '  ', st, nb)
+        for j in range(nb):
+            if depth == 0:
+                L.append(f'{ind}  d{j}_{i} += G{j}_1;')
+            else:
+                L.append(f'{ind}  d{j}_{i} = fmaf(G{j}_{depth + 1}, p{j}_{depth}, d{j}_{i});')
+                L.append(f'{ind}  G{j}_{depth} = fmaf(G{j}_{depth + 1}, x{j}_{i}, G{j}_{depth});')
+        L.append(f'{ind}}}')
+
+
+def _source_staged(spec, irreps=False, npw=None, cr=None, fence=None):
+    """HIP source of the LDS-staged kernels ``sc_fwds`` / ``sc_bwds`` (``i`` suffix: x and its gradient in e3nn's
+    irreps layout).  Workgroup = STAGE_WAVES waves on one 64-channel block (blockIdx.y) and SLOT_GROUP consecutive
+    slots of the element-grouped node list (``group_slots``: every group holds nodes of one element; -1 marks an
+    empty slot).  The element's coefficient rows stream through LDS in chunks of ``cr`` rows, copied once per
+    workgroup, so each row read from L2 serves every node of the workgroup and each LDS read npw nodes of a wave.
+    Per node the arithmetic is the one-node kernels' sequence."""
+    npw = STAGE_NPW if npw is None else npw
+    cr = STAGE_ROWS if cr is None else cr
+    fence = STAGE_FENCE if fence is None else fence
+    assert cr % 16 == 0
+    C, n = spec.C, spec.n_ell
+    sfx = 'i' if irreps else ''
+    slots = STAGE_WAVES * npw
+    comp = []
+    if irreps:
+        o = 0
+        for d in spec.dims:
+            comp += [(o, d, m) for m in range(d)]
+            o += d
+
+    def xidx(node, i, ch):
+        if not irreps:
+            return f'((size_t)({node}) * C + {ch}) * N_ELL + {i}'
+        ok, d, m = comp[i]
+        return f'(size_t)({node}) * (C * N_ELL) + {C * ok} + {ch} * {d} + {m}'
+    nchunk = stage_chunks(spec, cr)
+    sb = cr // 4 * WAVE
+    L = [_native.device_header(),
+         f'#define C {C}', f'#define NCB {spec.ncb}', f'#define N_ELL {n}', f'#define OUT_DIM {spec.out_dim}',
+         f'#define SLOTS {slots}', f'#define CHUNK_QUADS {sb}', f'#define NCHUNK {nchunk}']
+
+    def head(name, extra_args):
+        H = [f'extern "C" __global__ __launch_bounds__({STAGE_WAVES * WAVE}) void {spec.kname(name + sfx)}('
+             'const float* __restrict__ X,',
+             '    const int* __restrict__ slots, const int* __restrict__ elem, const float* __restrict__ TS,',
+             f'    {extra_args}, int N) {{',
+             '  __shared__ mh_f4 sl[2 * CHUNK_QUADS];',
+             '  const int t = threadIdx.x, wv = t >> 6;',
+             '  int lo = t & 63;',
+             '  const int q0 = blockIdx.x * SLOTS;',
+             '  const int s0 = slots[q0];',
+             '  if (s0 < 0) return;                       // past the last group (uniform over the workgroup)',
+             '  const int c = blockIdx.y * 64 + lo;',
+             '  const bool active = c < C;',
+             '  const int cc = active ? c : C - 1;',
+             '  const mh_f4* __restrict__ src = reinterpret_cast<const mh_f4*>(TS) +',
+             '      (size_t)(elem[s0] * NCB + blockIdx.y) * (NCHUNK * CHUNK_QUADS);']
+        for j in range(npw):
+            H += [f'  const int m{j} = slots[q0 + wv * {npw} + {j}];',
+                  f'  const int n{j} = m{j} >= 0 ? m{j} : s0;             // empty slot: compute on s0, store nothing']
+            H += [f'  const float x{j}_{i} = X[{xidx(f"n{j}", i, "cc")}];' for i in range(n)]
+        return H
+
+    # forward
+    st = _Stage(spec, cr, fence)
+    L += head('sc_fwds', 'float* __restrict__ out')
+    L += st.prologue('  ')
+    L += [f'  float a{j}_{bi}_{m} = 0.0f;' for j in range(npw) for bi, bl in enumerate(spec.blocks)
+          for m in range(bl['M'])]
+    _fwd_walk_s(spec, _trie(spec), 0, L, '  ', st, npw)
+    for j in range(npw):
+        L.append(f'  if (active && m{j} >= 0) {{')
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'    out[(size_t)n{j} * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{j}_{bi}_{m};'
+                  for m in range(M)]
+        L.append('  }')
+    L += ['}', '']
+    # backward
+    st = _Stage(spec, cr, fence)
+    L += head('sc_bwds', 'const float* __restrict__ G, float* __restrict__ GX')
+    for j in range(npw):
+        L += [f'  float d{j}_{i} = 0.0f;' for i in range(n)]
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'  const float g{j}_{bi}_{m} = G[(size_t)n{j} * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];'
+                  for m in range(M)]
+    L += st.prologue('  ')
+    L.append('  ' + ' '.join(f'float G{j}_0 = 0.0f;' for j in range(npw)))
+    _bwd_walk_s(spec, _trie(spec), 0, L, '  ', st, npw)
+    L.append('  ' + ' '.join(f'(void)G{j}_0;' for j in range(npw)))
+    for j in range(npw):
+        L.append(f'  if (active && m{j} >= 0) {{')
+        L += [f'    GX[{xidx(f"n{j}", i, "c")}] = d{j}_{i};' for i in range(n)]
+        L.append('  }')
+    L += ['}', '']
+    return '\n'.join(L)
+
+
 def _source_layout(spec, group=None, irreps=False, second=False):
     """HIP source of the per-node kernels ``sc_fwd`` / ``sc_bwd`` (one workgroup per node, the reference's launch
     shape) and the element-grouped kernels ``sc_fwdg`` / ``sc_bwdg``: one workgroup per GROUP consecutive nodes of an
@@ -466,12 +696,16 @@ def source_second(spec):
 
 
 def source(spec, group=None):
-    """HIP source of one layer's module: the four kernels on the [N, C, n_ell] layout and, when the input irreps
-    are known, the same four on e3nn's irreps layout (one shared header)."""
+    """HIP source of one layer's module: the six kernels on the [N, C, n_ell] layout (per node, element-grouped,
+    LDS-staged; forward and backward) and, when the input irreps are known, the same six on e3nn's irreps layout
+    (one shared header)."""
     src = _source_layout(spec, group)
-    if spec.dims is not None:
-        alt = _source_layout(spec, group, irreps=True)
-        src += '\n' + alt[alt.index('extern "C"'):]
+    for irreps in ((False, True) if spec.dims is not None else (False,)):
+        if irreps:
+            alt = _source_layout(spec, group, irreps=True)
+            src += '\n' + alt[alt.index('extern "C"'):]
+        st = _source_staged(spec, irreps=irreps)
+        src += '\n' + st[st.index('#define SLOTS'):]
     return src
 
 
@@ -500,68 +734,107 @@ def element_order(node_attrs):
     return elem, order
 
 
+_slot_cache = []          # [(weakref(node_attrs), version, slots int32)], most recent first
+
+
+def group_slots(node_attrs):
+    """Node slots of the staged kernels: the element-sorted node order with every element's run padded with -1 to a
+    multiple of SLOT_GROUP, so that each workgroup's SLOT_GROUP slots hold nodes of one element, and -1 up to the
+    fixed length ceil(N / SLOT_GROUP) SLOT_GROUP + n_elem SLOT_GROUP (an upper bound for any element mix, so the
+    launch size needs no device-to-host copy).  Device ops only; cached per node_attrs tensor."""
+    ver = node_attrs._version
+    for ref, v, sl in _slot_cache:
+        if ref() is node_attrs and v == ver:
+            return _native.hold_for_capture(sl)
+    elem, order = element_order(node_attrs)
+    n, ne, gs = elem.numel(), node_attrs.shape[1], SLOT_GROUP
+    dev = elem.device
+    el = elem.long()
+    cnt = torch.zeros(ne, dtype=torch.int64, device=dev).scatter_add_(0, el, torch.ones_like(el))
+    run = (cnt + gs - 1) // gs * gs
+    start, pstart = torch.cumsum(cnt, 0) - cnt, torch.cumsum(run, 0) - run
+    es = el[order.long()]                                   # element of each sorted position
+    pos = pstart[es] + torch.arange(n, device=dev) - start[es]
+    slots = torch.full((-(-n // gs) * gs + ne * gs,), -1, dtype=torch.int32, device=dev)
+    slots.scatter_(0, pos, order)
+    if _native.capturing():
+        return slots
+    _slot_cache.insert(0, (weakref.ref(node_attrs), ver, slots))
+    del _slot_cache[4:]
+    return slots
+
+
 def element_index(node_attrs):
     """argmax of the one-hot node attributes as int32 (reference symmetric.py:169)."""
     return element_order(node_attrs)[0]
 
 
-def _sc_fwd(op, layout, grouped, x, elem, order):
-    """Launch the contraction on contiguous x in ``layout`` ('mace' [N, C, n_ell] or 'irreps' [N, C n_ell])."""
+def _sc_fwd(op, layout, kind, x, elem, order, slots):
+    """Launch the contraction on contiguous x in ``layout`` ('mace' [N, C, n_ell] or 'irreps' [N, C n_ell]) with
+    the kernel family ``kind`` ('node', 'grouped' or 'staged')."""
     N = x.shape[0]
     out = torch.empty(N, op.spec.out_dim, device=x.device, dtype=torch.float32)
     lib, P = _native.load(), _native.ptr
-    if layout == 'irreps':
+    st = _native.stream_of(x)
+    if kind == 'staged':
+        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_staged, op.module.handle, P(x), P(slots), slots.numel(),
+                       P(elem), P(op.TS), P(out), N, int(layout == 'irreps'), st)
+    elif layout == 'irreps':
         _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_irreps, op.module.handle, P(x), P(elem),
-                       P(order) if grouped else None, P(op.T), P(out), N, _native.stream_of(x))
-    elif grouped:
+                       P(order) if kind == 'grouped' else None, P(op.T), P(out), N, st)
+    elif kind == 'grouped':
         _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_sorted, op.module.handle, P(x), P(elem), P(order),
-                       P(op.T), P(out), N, _native.stream_of(x))
+                       P(op.T), P(out), N, st)
     else:
-        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd, op.module.handle, P(x), P(elem), P(op.T), P(out), N,
-                       _native.stream_of(x))
+        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd, op.module.handle, P(x), P(elem), P(op.T), P(out), N, st)
     return out
 
 
-def _sc_bwd(op, layout, grouped, x, elem, order, g):
+def _sc_bwd(op, layout, kind, x, elem, order, slots, g):
     """Launch the contraction's x-gradient for contiguous x and g; the gradient has x's layout."""
     gx = torch.empty_like(x)
     lib, P = _native.load(), _native.ptr
-    if layout == 'irreps':
+    st, N = _native.stream_of(x), x.shape[0]
+    if kind == 'staged':
+        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_staged, op.module.handle, P(x), P(slots), slots.numel(),
+                       P(elem), P(op.TS), P(g), P(gx), N, int(layout == 'irreps'), st)
+    elif layout == 'irreps':
         _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_irreps, op.module.handle, P(x), P(elem),
-                       P(order) if grouped else None, P(op.T), P(g), P(gx), x.shape[0], _native.stream_of(x))
-    elif grouped:
+                       P(order) if kind == 'grouped' else None, P(op.T), P(g), P(gx), N, st)
+    elif kind == 'grouped':
         _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_sorted, op.module.handle, P(x), P(elem), P(order),
-                       P(op.T), P(g), P(gx), x.shape[0], _native.stream_of(x))
+                       P(op.T), P(g), P(gx), N, st)
     else:
-        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd, op.module.handle, P(x), P(elem), P(op.T), P(g), P(gx),
-                       x.shape[0], _native.stream_of(x))
+        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd, op.module.handle, P(x), P(elem), P(op.T), P(g), P(gx), N,
+                       st)
     return gx
 
 
 def _sc_backward(ctx, g):
     """Shared backward of the two layouts' functions: the first-order kernel, or under create_graph (only then is
     grad mode on here) the same gradient as a differentiable function of (g, x) when the module allows it."""
-    x, elem, order = ctx.saved_tensors
+    x, elem, order, slots = ctx.saved_tensors
     op = ctx.op
     if torch.is_grad_enabled():
         if not op.double_backward:
             raise RuntimeError(_DOUBLE_BACKWARD)
-        return _SCAdjFn.apply(g, x, elem, order, op, ctx.layout, ctx.grouped), None, None, None
-    return _sc_bwd(op, ctx.layout, ctx.grouped, x.contiguous(), elem, order, g.contiguous()), None, None, None
+        return _SCAdjFn.apply(g, x, elem, order, slots, op, ctx.layout, ctx.kind), None, None, None, None
+    return (_sc_bwd(op, ctx.layout, ctx.kind, x.contiguous(), elem, order, slots, g.contiguous()),
+            None, None, None, None)
 
 
 class _SCFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, elem, order, op):
+    def forward(ctx, x, elem, order, slots, op):
         s = op.spec
         if x.dtype != torch.float32 or not x.is_cuda:
             raise TypeError('mace_hip_kernels: symmetric contraction expects float32 GPU input')
         if x.dim() != 3 or x.shape[1] != s.C or x.shape[2] != s.n_ell:
             raise ValueError(f'node_feats must be [N, {s.C}, {s.n_ell}], got {tuple(x.shape)}')
-        grouped = op.use_grouped(x.shape[0], x.device)
-        out = _sc_fwd(op, 'mace', grouped, x.contiguous(), elem, order)
-        ctx.save_for_backward(x, elem, order)     # the input itself: a double backward differentiates through it
-        ctx.grouped, ctx.op, ctx.layout = grouped, op, 'mace'
+        kind = op.kernel_family(x.shape[0], x.device)
+        out = _sc_fwd(op, 'mace', kind, x.contiguous(), elem, order, slots)
+        ctx.save_for_backward(x, elem, order, slots)     # the input itself: a double backward differentiates it
+        ctx.kind, ctx.op, ctx.layout = kind, op, 'mace'
         return out
 
     backward = staticmethod(_sc_backward)
@@ -572,14 +845,14 @@ class _SCIrrepsFn(torch.autograd.Function):
     comes back in that layout."""
 
     @staticmethod
-    def forward(ctx, x, elem, order, op):
+    def forward(ctx, x, elem, order, slots, op):
         s = op.spec
         if x.dtype != torch.float32 or not x.is_cuda or x.dim() != 2 or x.shape[1] != s.C * s.n_ell:
             raise ValueError(f'expected float32 GPU input [N, {s.C * s.n_ell}], got {tuple(x.shape)}')
-        grouped = op.use_grouped(x.shape[0], x.device)
-        out = _sc_fwd(op, 'irreps', grouped, x.contiguous(), elem, order)
-        ctx.save_for_backward(x, elem, order)
-        ctx.grouped, ctx.op, ctx.layout = grouped, op, 'irreps'
+        kind = op.kernel_family(x.shape[0], x.device)
+        out = _sc_fwd(op, 'irreps', kind, x.contiguous(), elem, order, slots)
+        ctx.save_for_backward(x, elem, order, slots)
+        ctx.kind, ctx.op, ctx.layout = kind, op, 'irreps'
         return out
 
     backward = staticmethod(_sc_backward)
@@ -591,8 +864,8 @@ class _SCAdjFn(torch.autograd.Function):
     Hessian-vector product of <g, P> (``mh_sc_bwd2``).  Third derivatives are not provided."""
 
     @staticmethod
-    def forward(ctx, g, x, elem, order, op, layout, grouped):
-        gx = _sc_bwd(op, layout, grouped, x.contiguous(), elem, order, g.contiguous())
+    def forward(ctx, g, x, elem, order, slots, op, layout, kind):
+        gx = _sc_bwd(op, layout, kind, x.contiguous(), elem, order, slots, g.contiguous())
         ctx.save_for_backward(g, x, elem)
         ctx.op, ctx.layout = op, layout
         return gx
@@ -615,7 +888,7 @@ class _SCAdjFn(torch.autograd.Function):
             gx = torch.empty_like(x)
             _native.launch(f'sc_bwd2[{op.tag}]', lib.mh_sc_bwd2, m.handle, P(x), P(v), P(elem), P(op.T), P(g),
                            P(gx), N, lay, _native.stream_of(x))
-        return gg, gx, None, None, None, None, None
+        return gg, gx, None, None, None, None, None, None
 
 
 class HipSymmetricContraction(torch.nn.Module):
@@ -627,14 +900,18 @@ class HipSymmetricContraction(torch.nn.Module):
         self.spec = SCSpec(sc)
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         self.register_buffer('T', self.spec.T.to(dev).contiguous())
+        self.register_buffer('TS', torch.from_numpy(pack_staged(self.spec)).to(dev))
         self.source = source(self.spec)
         code = _native.compile_source(self.source)
         with torch.cuda.device(dev):
+            sw, ncb = STAGE_WAVES * WAVE, self.spec.ncb
             kinds = {
                 _native.MH_SC_FWD: (self.spec.kname('sc_fwd'), self.spec.block, 1),
                 _native.MH_SC_BWD: (self.spec.kname('sc_bwd'), self.spec.block, 1),
                 _native.MH_SC_FWD_G: (self.spec.kname('sc_fwdg'), self.spec.block, GROUP),
                 _native.MH_SC_BWD_G: (self.spec.kname('sc_bwdg'), self.spec.block, GROUP),
+                _native.MH_SC_FWD_S: (self.spec.kname('sc_fwds'), sw, SLOT_GROUP, ncb),
+                _native.MH_SC_BWD_S: (self.spec.kname('sc_bwds'), sw, SLOT_GROUP, ncb),
             }
             if self.spec.dims is not None:
                 kinds.update({
@@ -642,12 +919,15 @@ class HipSymmetricContraction(torch.nn.Module):
                     _native.MH_SC_BWD_I: (self.spec.kname('sc_bwdi'), self.spec.block, 1),
                     _native.MH_SC_FWD_GI: (self.spec.kname('sc_fwdgi'), self.spec.block, GROUP),
                     _native.MH_SC_BWD_GI: (self.spec.kname('sc_bwdgi'), self.spec.block, GROUP),
+                    _native.MH_SC_FWD_SI: (self.spec.kname('sc_fwdsi'), sw, SLOT_GROUP, ncb),
+                    _native.MH_SC_BWD_SI: (self.spec.kname('sc_bwdsi'), sw, SLOT_GROUP, ncb),
                 })
             self.module = _native.Module(code, kinds)
         self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
         self.original = [sc]
         self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
-        self.grouped = None           # None: by size (use_grouped); True / False: force a kernel family
+        self.grouped = None           # True / False: force the grouped / per-node global-memory kernels
+        self.staged = None            # None: by size (kernel_family); True: force the LDS-staged kernels
         self.last_layout = None       # input layout of the last call: 'mace' [N, C, n_ell] or 'irreps'
         # a backward under create_graph=True: raise (the reference's behaviour) unless this is set, in which case
         # the gradient is differentiable once more through the second-order kernels (second_module)
@@ -680,14 +960,27 @@ class HipSymmetricContraction(torch.nn.Module):
         waves = -(-n_nodes // GROUP) * self.spec.ncb
         return waves >= 4 * _SIMDS[key]
 
+    def kernel_family(self, n_nodes, device):
+        """'staged' (coefficient rows through LDS, SLOT_GROUP nodes of one element per workgroup), 'grouped' or
+        'node' (coefficients from global memory): ``staged`` / ``grouped`` force a family (``staged`` False: the
+        global-memory family that ``use_grouped`` picks), else the staged kernels."""
+        if self.staged:
+            return 'staged'
+        if self.grouped is not None:
+            return 'grouped' if self.grouped else 'node'
+        if self.staged is False:
+            return 'grouped' if self.use_grouped(n_nodes, device) else 'node'
+        return 'staged'
+
     def forward(self, x, y):
         if y.shape != (x.shape[0], self.spec.n_elem):
             raise ValueError(f'node_attrs must be [{x.shape[0]}, {self.spec.n_elem}], got {tuple(y.shape)}')
         elem, order = element_order(y)
+        slots = group_slots(y) if self.kernel_family(x.shape[0], x.device) == 'staged' else None
         src = getattr(x, 'irreps_source', None)
         if src is not None and self.spec.dims is not None and src(self.spec.dims) is not None:
             # x is MACE's reshape_irreps of a tensor in e3nn's layout, not yet formed: read that tensor directly
             self.last_layout = 'irreps'
-            return _SCIrrepsFn.apply(src(self.spec.dims), elem, order, self)
+            return _SCIrrepsFn.apply(src(self.spec.dims), elem, order, slots, self)
         self.last_layout = 'mace'
-        return _SCFn.apply(x, elem, order, self)
+        return _SCFn.apply(x, elem, order, slots, self)

@@ -333,19 +333,28 @@ def test_conv_deterministic_and_empty():
 SC_MODELS = [('32x0e+32x1o', 2, 2), ('128x0e+128x1o', 3, 3), ('64x0e', 2, 2), ('128x0e+128x1o+128x2e', 3, 3)]
 
 
-@pytest.mark.parametrize('grouped', [False, True])
+SC_FAMILIES = ['node', 'grouped', 'staged']
+
+
+def _family(op, fam):
+    """Force a kernel family of a HipSymmetricContraction."""
+    op.staged, op.grouped = (True, None) if fam == 'staged' else (False, fam == 'grouped')
+    return op
+
+
+@pytest.mark.parametrize('family', SC_FAMILIES)
 @pytest.mark.parametrize('hidden,lmax,corr', SC_MODELS)
-def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr, grouped):
-    """Both kernel families: one node per workgroup, and element-grouped (GROUP nodes per workgroup, mixed groups at
-    element boundaries, a partial last group)."""
+def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr, family):
+    """Every kernel family: one node per workgroup; element-grouped (GROUP nodes per workgroup, mixed groups at
+    element boundaries, a partial last group); LDS-staged (SLOT_GROUP slots of one element per workgroup, padded
+    element runs, coefficient rows through LDS in chunks)."""
     dev = _dev()
     model = factory.make_model(hidden, lmax, corr, elements=factory.ELEMENTS_PTCOH)
     rng = np.random.default_rng(4)
     for li, prod in enumerate(model.products):
-        print(f'[case] sc {hidden} l{lmax} c{corr} layer {li} grouped={grouped}', flush=True)
+        print(f'[case] sc {hidden} l{lmax} c{corr} layer {li} family={family}', flush=True)
         sc = prod.symmetric_contractions
-        op = HipSymmetricContraction(sc, device=dev)
-        op.grouped = grouped
+        op = _family(HipSymmetricContraction(sc, device=dev), family)
         C, n_ell = op.spec.C, op.spec.n_ell
         n = 37
         x = rng.normal(size=(n, C, n_ell)) * 0.7
@@ -376,8 +385,8 @@ def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr, grouped):
 def test_sc_basis_independent(redundant):
     """The kernels see a contraction only through sum_p U W: every contraction of the product rewritten in another
     path basis (a random well-conditioned change of basis, or a redundant one with extra paths; tests/test_oracle_sc
-    ``rebased``, in float64) gives the outputs and input gradients of the original, in both kernel families, and
-    both match the oracle on the original U and W."""
+    ``rebased``, in float64) gives the outputs and input gradients of the original, in every kernel family, and
+    all match the oracle on the original U and W."""
     from test_oracle_sc import rebased
     dev = _dev()
     model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
@@ -390,12 +399,11 @@ def test_sc_basis_independent(redundant):
         n = 41
         elem = rng.integers(0, 4, n)
         attrs = torch.tensor(np.eye(4)[elem], dtype=torch.float32, device=dev)
-        for grouped in (False, True):
-            print(f'[case] sc basis change layer {li} redundant={redundant} grouped={grouped}', flush=True)
+        for family in SC_FAMILIES:
+            print(f'[case] sc basis change layer {li} redundant={redundant} family={family}', flush=True)
             res = []
             for mod in (sc, sc2):
-                op = HipSymmetricContraction(mod, device=dev)
-                op.grouped = grouped
+                op = _family(HipSymmetricContraction(mod, device=dev), family)
                 x = rng.normal(size=(n, op.spec.C, op.spec.n_ell)) * 0.7 if not res else res[0][0]
                 g = rng.normal(size=(n, op.spec.out_dim)) if not res else res[0][1]
                 xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
@@ -447,6 +455,54 @@ def test_sc_grouped_matches_per_node():
         torch.cuda.synchronize()
         assert _rel(out2.double().cpu().numpy(), out1.double().cpu().numpy()) < 1e-6
         assert _rel(gx2.double().cpu().numpy(), gx1.double().cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize('layout', [0, 1])
+def test_sc_staged_matches_per_node(layout):
+    """The LDS-staged kernels (mh_sc_fwd_staged / mh_sc_bwd_staged) against the per-node ones through the C ABI:
+    element runs of every length mod SLOT_GROUP (a single-node element, a run of exactly SLOT_GROUP, a long run
+    with a partial last group), an element with no nodes, both layouts, and slots from group_slots; then a second,
+    smaller call on the same module."""
+    from mace_hip_kernels import symmetric as hsym
+    dev = _dev()
+    model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    for li, prod in enumerate(model.products):
+        op = HipSymmetricContraction(prod.symmetric_contractions, device=dev)
+        s, h = op.spec, op.module.handle
+        rng = np.random.default_rng(20 + li)
+        gs = hsym.SLOT_GROUP
+        for counts in ([1, gs, 3 * gs + 5, 0], [2, 0, 1, 1]):
+            print(f'[case] sc staged vs per-node layer {li} layout {layout} counts {counts}', flush=True)
+            elem_np = rng.permutation(np.repeat(np.arange(4), counts))
+            n = elem_np.size
+            f = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+            X, G = f(rng.normal(size=(n, s.C, s.n_ell)) * 0.7), f(rng.normal(size=(n, s.out_dim)))
+            attrs = f(np.eye(4)[elem_np])
+            elem = torch.tensor(elem_np, dtype=torch.int32, device=dev)
+            slots = hsym.group_slots(attrs)
+            Xl = X
+            if layout:        # e3nn's irreps layout: block k of dimension d holds channel c at C o_k + c d + m
+                parts, o = [], 0
+                for d in s.dims:
+                    parts.append(X[:, :, o:o + d].reshape(n, -1))
+                    o += d
+                Xl = torch.cat(parts, dim=1).contiguous()
+            lib, P, st = _native.load(), _native.ptr, _native.stream_of(X)
+            out1, gx1 = torch.empty(n, s.out_dim, device=dev), torch.empty_like(Xl)
+            _native.check(lib.mh_sc_fwd_irreps(h, P(Xl), P(elem), None, P(op.T), P(out1), n, st) if layout else
+                          lib.mh_sc_fwd(h, P(X), P(elem), P(op.T), P(out1), n, st), 'sc_fwd')
+            _native.check(lib.mh_sc_bwd_irreps(h, P(Xl), P(elem), None, P(op.T), P(G), P(gx1), n, st) if layout else
+                          lib.mh_sc_bwd(h, P(X), P(elem), P(op.T), P(G), P(gx1), n, st), 'sc_bwd')
+            out2, gx2 = torch.full_like(out1, float('nan')), torch.full_like(gx1, float('nan'))
+            _native.check(lib.mh_sc_fwd_staged(h, P(Xl), P(slots), slots.numel(), P(elem), P(op.TS), P(out2), n,
+                                               layout, st), 'sc_fwd_staged')
+            _native.check(lib.mh_sc_bwd_staged(h, P(Xl), P(slots), slots.numel(), P(elem), P(op.TS), P(G), P(gx2),
+                                               n, layout, st), 'sc_bwd_staged')
+            torch.cuda.synchronize()
+            assert _rel(out2.double().cpu().numpy(), out1.double().cpu().numpy()) < 1e-6
+            assert _rel(gx2.double().cpu().numpy(), gx1.double().cpu().numpy()) < 1e-6
+        bad = lib.mh_sc_fwd_staged(h, P(Xl), P(slots), slots.numel() - 1, P(elem), P(op.TS), P(out2), n, layout, st)
+        assert bad != 0 and b'multiple' in lib.mh_last_error()
 
 
 SH_TOL = 5e-6        # absolute on Y (|Y| <= ~4 in component normalisation)
@@ -1033,7 +1089,7 @@ def test_sc_double_backward_vs_oracle(layout):
             out = op(xt, attrs)
         else:
             elem, order = hsym.element_order(attrs)
-            out = hsym._SCIrrepsFn.apply(xt, elem, order, op)
+            out = hsym._SCIrrepsFn.apply(xt, elem, order, hsym.group_slots(attrs), op)
         gx, = torch.autograd.grad(out, xt, gt, create_graph=True)
         d_g, d_x = torch.autograd.grad((gx * torch.tensor(lay(v), dtype=torch.float32, device=dev)).sum(), (gt, xt))
         want_g, want_x, off = [], np.zeros_like(x), 0
