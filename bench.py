@@ -406,6 +406,12 @@ def _summarize(a):
 
     per = {}
     stats = rows(a.summarize_rocprof, '*kernel_stats.csv')
+    if stats:
+        tot = sum(float(r['TotalDurationNs']) for r in stats)
+        cal = sum(float(r['TotalDurationNs']) for r in stats if 'bitwise_not' in r['Name'])
+        own = sum(float(r['TotalDurationNs']) for r in stats if r['Name'].startswith(HIP_KERNEL_PREFIXES))
+        print(f'GPU time over all dispatches: {tot / 1e6:.3f} ms ({cal / 1e6:.3f} ms calibration copies, '
+              f'{own / 1e6:.3f} ms in this package\'s kernels)\n')
     print('| kernel | calls | mean us | min us | max us | share of GPU time |')
     print('|---|---:|---:|---:|---:|---:|')
     for r in sorted(stats, key=lambda r: -float(r['TotalDurationNs']))[:a.top]:

@@ -294,7 +294,7 @@ def _bwd_walk_g(spec, node, depth, L, ind, cnt, nb):
 STAGE_WAVES = 4        # waves per workgroup of the staged kernels (one channel block, nodes of one element)
 STAGE_NPW = 2          # nodes per wave: every coefficient read from LDS feeds STAGE_NPW FMAs
 STAGE_ROWS = 64        # coefficient rows per LDS chunk; two chunks resident (double buffer)
-STAGE_FENCE = 32       # rows between anti-hoisting fences in the staged walk (0: none)
+STAGE_FENCE = 64       # rows between anti-hoisting fences in the staged walk (0: none; spills)
 SLOT_GROUP = STAGE_WAVES * STAGE_NPW     # node slots per workgroup of the staged kernels
 
 
