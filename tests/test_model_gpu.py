@@ -226,9 +226,9 @@ def test_patched_model_launches_the_fast_paths(fuse):
     conv_bwdrc) after the radial MLP's kernels (mlp_fwd, mlp_bwd).  fuse_radial: the convolutions with the radial
     MLP's output layer inside (conv_fwdm, conv_bwdm: the per-edge weights and their gradient never stored; the MLPs
     run their hidden layers only, mlp_hid / mlp_hidb).  Both: layer 1's backward without dX (no conv_gxsum for it:
-    the engine never asks for the first layer's node-feature gradient), the symmetric contraction reading e3nn's
-    irreps layout (sc_*i: reshape_irreps left unformed, so no permutation kernel), and every other drop-in's
-    kernels."""
+    the engine never asks for the first layer's node-feature gradient), the symmetric contraction's LDS-staged
+    kernels reading e3nn's irreps layout (sc_fwdsi / sc_bwdsi: reshape_irreps left unformed, so no permutation
+    kernel), and every other drop-in's kernels."""
     from mace_hip_kernels import _native
     dev = _dev()
     print(f'[case] kernels launched by the patched model (config 1, fuse_radial={fuse})', flush=True)
@@ -264,8 +264,7 @@ def test_patched_model_launches_the_fast_paths(fuse):
     for i in range(2):
         names = sym[f'sc_fwd[products.{i}.symmetric_contractions]'] + \
             sym[f'sc_bwd[products.{i}.symmetric_contractions]']
-        assert len(names) == 2 and all(n.startswith(('sc_fwdi_', 'sc_bwdi_', 'sc_fwdgi_', 'sc_bwdgi_'))
-                                       for n in names), names
+        assert [n.split('_c')[0] for n in names] == ['sc_fwdsi', 'sc_bwdsi'], names    # LDS-staged, irreps layout
     for prefix in ('sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_', 'geom_fwd', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
                    'ro_fwd_', 'ro_bwd_'):
         assert any(n.startswith(prefix) for n in flat), (prefix, flat)
