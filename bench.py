@@ -244,11 +244,12 @@ def _isolated(a):
         gWs = [torch.empty(E, nw, device=dev) for _ in range(nb)]
         gY, gx, out = torch.empty(E, s.y_dim, device=dev), torch.empty_like(x), torch.empty(N, s.out_dim, device=dev)
         work = torch.empty(E, s.x_dim, device=dev)
-        # the model passes tp_weights = W0 * cutoff: cutoff in (0, 1] inside r_max, exactly 0 on padding edges
+        # the model passes tp_weights = W0 * cutoff: cutoff in (0, 1] inside r_max, -0.0 past it (the patched
+        # radial embedding's mark of edges outside the envelope's support: config 2's padding edges)
         ei = batch['edge_index']
         vec = batch['positions'][ei[1]] - batch['positions'][ei[0]] + batch['shifts']
         inside = (vec.norm(dim=1) < meta['r_max']).to(dev)
-        cut = torch.where(inside, 0.1 + 0.9 * torch.rand(E, generator=gen).to(dev), torch.zeros((), device=dev))
+        cut = torch.where(inside, 0.1 + 0.9 * torch.rand(E, generator=gen).to(dev), torch.full((), -0.0, device=dev))
         gcut = torch.empty(E, device=dev)
         bf, bb = s.bytes(N, n_real)
         ff, fb = s.flops()
@@ -273,8 +274,18 @@ def _isolated(a):
         ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
                                                   P(rp_s), P(ei_s), P(work), P(gx), P(gWs[i]), P(gY), P(cut), P(gcut),
                                                   N, 3, stream), nb)
-        report(f'conv_bwd[{tag}] factored dx+dW+dY (model path)', f"{s.kname('conv_bwdrc')}+{s.kname('conv_gxsum')}",
+        report(f'conv_bwd[{tag}] factored dx+dW+dY, every edge walked', f"{s.kname('conv_bwdrc')}+{s.kname('conv_gxsum')}",
                ms, bb, fb * n_real * s.mul)
+        ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
+                                                  P(rp_s), P(ei_s), P(work), P(gx), P(gWs[i]), P(gY), P(cut), P(gcut),
+                                                  N, 3 | _native.MH_CUT_MASKED, stream), nb)
+        report(f'conv_bwd[{tag}] factored dx+dW+dY, masked edges skipped (model path)',
+               f"{s.kname('conv_bwdrc')}+{s.kname('conv_gxsum')}", ms, bb, fb * n_real * s.mul)
+        ms = timed(lambda i: lib.mh_conv_bwd_recv(h, P(x), P(g), P(Ys[i]), P(Ws[i]), P(rp_r), P(ei_r), P(gr.send),
+                                                  None, None, None, None, P(gWs[i]), P(gY), P(cut), P(gcut),
+                                                  N, 2 | _native.MH_CUT_MASKED, stream), nb)
+        report(f'conv_bwd[{tag}] factored dW+dY, masked edges skipped (model path, layer 1)', s.kname('conv_bwdrc'),
+               ms, bb - 4 * (N * s.x_dim + n_real * 2 + N + 1), fb * n_real * s.mul)
         if radial.mlp_supported(blk.conv_tp_weights)[0]:
             _isolated_radial(a, timed, report, blk, op, li, dict(x=x, g=g, Ys=Ys, Ws=Ws, gWs=gWs, gY=gY, gx=gx,
                                                                    out=out, work=work, cut=cut, gcut=gcut), nb,
@@ -565,6 +576,42 @@ def main():
     del fresh
     _log(f'patched, new graph tensors every call: {dt_fresh * 1e3:.3f} ms per E+F call')
 
+    # MD-like step: positions moved, the neighbour list rebuilt on the GPU into the same fixed-size padded layout
+    # (mace_hip_kernels.neighbours), then E+F on the new graph; no host synchronisation inside the step
+    md = None
+    st = factory.structures(a.config)
+    if st['pad_edges_to'] is not None:
+        from mace_hip_kernels import neighbours as hnl
+        pbc = torch.tensor([[bool(v) for v in s_.pbc] for s_ in st['structures']], device=dev)
+        mb = D.fresh(batch)
+        base = mb['positions'].detach().clone()
+        kick = [0.01 * torch.randn(base.shape, generator=torch.Generator().manual_seed(20 + k)).to(dev)
+                for k in range(a.steps)]
+
+        def md_step(k):
+            mb['positions'] = base + kick[k % len(kick)]
+            nl = hnl.update_batch(mb, st['r_max'], pbc=pbc, pad_edges_to=st['pad_edges_to'])
+            met(mb, compute_force=True)
+            return nl
+        for k in range(a.warmup):
+            md_step(k)
+        sync()
+        t0 = time.perf_counter()
+        for k in range(a.steps):
+            nl = md_step(k)
+        sync()
+        dt_md = (time.perf_counter() - t0) / a.steps
+        nl.check()
+        with _native.timing() as tm_nl:
+            for k in range(a.steps):
+                hnl.update_batch(mb, st['r_max'], pbc=pbc, pad_edges_to=st['pad_edges_to'])
+        nl_ms = tm_nl.summary().get('neighbour_list', (0, 0.0))[1]
+        md = dict(step='positions moved (0.01 A Gaussian), neighbour list rebuilt on the GPU (padded to '
+                       f"{st['pad_edges_to']} edges per structure), E+F (eager)",
+                  ms_per_step=round(dt_md * 1e3, 4), neighbour_list_ms=round(nl_ms, 4))
+        _log('MD-like step:', md)
+        del mb, kick
+
     # the same call captured as a HIP graph (mace_hip_kernels.graphs) and replayed: identical kernels, no per-launch
     # host cost.  Checked against an eager call on perturbed positions before it is timed.
     dt_graph, graph_check = None, None
@@ -602,6 +649,18 @@ def main():
         for _ in range(a.steps):
             met(batch, compute_force=True)
     kern = _kernel_table(met, batch, n_real, tm.summary(), tm.symbols)
+    # the convolutions' backward with every edge walked (skip_masked off: padding edges read and written like any
+    # other), for comparison with the model path that skips the edges outside the cutoff
+    from mace_hip_kernels import HipConvTP
+    convs = [m_ for m_ in met.modules() if isinstance(m_, HipConvTP)]
+    for m_ in convs:
+        m_.skip_masked = False
+    with _native.timing() as tm_all:
+        for _ in range(a.steps):
+            met(batch, compute_force=True)
+    for m_ in convs:
+        m_.skip_masked = True
+    conv_all_edges = {k: round(v[1], 5) for k, v in tm_all.summary().items() if k.startswith('conv_bwd')}
     per_call = {k: v['ms'] * v['launches'] / a.steps for k, v in kern.items()}
     dom = max(per_call, key=per_call.get)
     d = kern[dom]
@@ -668,6 +727,8 @@ def main():
         'fuse_radial': a.fuse_radial,
         'ms_per_step_eager': round(dt_eager * 1e3, 4),
         'ms_per_step_new_graph_tensors': round(dt_fresh * 1e3, 4),
+        'md_step': md,
+        'conv_bwd_ms_every_edge_walked': conv_all_edges,
         'graph_replay_check': graph_check,
         'conv_hbm_gbs': round(conv_bytes / (conv_ms * 1e-3) / 1e9, 1) if conv_ms else None,
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': d['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

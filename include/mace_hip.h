@@ -91,12 +91,26 @@ enum mh_kernel_kind {
     MH_SC_BWD_S = 52,    /* its x-gradient                                                          */
     MH_SC_FWD_SI = 53,   /* MH_SC_FWD_S in the irreps layout                                        */
     MH_SC_BWD_SI = 54,   /* MH_SC_BWD_S in the irreps layout                                        */
-    MH_NUM_KINDS = 55
+    MH_NL_SETUP = 55,    /* neighbour list: per-structure bounding box, images, bin grid            */
+    MH_NL_ZERO = 56,     /* zero an int32 array                                                     */
+    MH_NL_BINS = 57,     /* each atom's bin, per-bin counts                                         */
+    MH_NL_SCAN = 58,     /* bin offsets (one workgroup)                                             */
+    MH_NL_PLACE = 59,    /* atoms into their bins                                                   */
+    MH_NL_COUNT = 60,    /* edges per sender (one wave per sender)                                  */
+    MH_NL_OFFSETS = 61,  /* edges per structure, each sender's segment start (one workgroup)        */
+    MH_NL_FILL = 62,     /* edges of each sender, ordered, and its padding (one wave per sender)    */
+    MH_SPECIES_ORDER = 63, /* element index, stable element order and contraction slots (one workgroup) */
+    MH_MLP_JVP = 64,     /* radial MLP: derivative of its output along a direction of the features  */
+    MH_MLP_BWD2 = 65,    /* derivative of its feature gradient along that direction                 */
+    MH_NUM_KINDS = 66
 };
 
 /* flags of mh_conv_bwd */
 #define MH_WANT_GX 1
 #define MH_WANT_GWY 2
+/* flag of mh_conv_bwd_recv (factored weights only): cutoff[e] == -0.0 exactly marks an edge outside the cutoff
+ * envelope's support, where the envelope's derivative is zero */
+#define MH_CUT_MASKED 4
 
 /* Message of the last failing call on this thread ("" if none).  No reference counterpart (Metal errors surface
  * from torch there). */
@@ -179,7 +193,12 @@ int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, co
  * Factored weights: with `cutoff` non-NULL ([E] floats) the weights are W = W0 * cutoff[e] (MACE multiplies the
  * radial MLP output by the cutoff envelope before the convolution) and `W` must point to W0.  Then `gW` receives
  * ∂/∂W0 = ∂/∂W * cutoff[e] and `g_cutoff` ([E]) receives ∂/∂cutoff[e] = Σ_{k,u} ∂/∂W[e,k,u] * W0[e,k,u], so the caller
- * need not differentiate the product itself (kernel MH_CONV_BWD_RC; no reference counterpart). */
+ * need not differentiate the product itself (kernel MH_CONV_BWD_RC; no reference counterpart).
+ * With MH_CUT_MASKED in `flags` (factored weights only) an edge whose cutoff is -0.0 exactly is taken to lie outside
+ * the envelope's support (mace_hip_kernels' radial embedding writes -0.0 there, where the envelope's derivative is
+ * zero): its gW, gY and g_cutoff rows are written as zeros without reading W0 or x, and it has no dX message.  Only
+ * g_cutoff differs from the unmasked call (it is the exact partial derivative there), and only where whatever
+ * produced the cutoff multiplies it by a zero derivative. */
 int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
                      const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
                      const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
@@ -271,6 +290,39 @@ int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n
 int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys,
                            int32_t* rowptr, int32_t* eids, int32_t* bad, void* stream);
 
+/* Neighbour list of a batch of B structures (atoms ptr[b] .. ptr[b + 1] of pos [N, 3] float64, cell [B, 3, 3]
+ * float64 with the lattice vectors as rows, pbc [B, 3] int32): every (sender i, receiver j, unit shift o) with
+ * |pos[j] + o cell - pos[i]| < r_max (float64, no fused multiply-add), o over the translations ceil(r_max / h_k)
+ * deep along each periodic direction (h_k the spacing of lattice planes k), without (i, i, 0); ordered by sender,
+ * then receiver, then o (lexicographic).  e_pad > 0: structure b's edges fill [b e_pad, (b + 1) e_pad) (e_total =
+ * B e_pad), each sender's real edges followed by its share of padding edges (self-loops with unit shift (0, 0, kz),
+ * kz = ceil((r_max + 1) / |c_2|), spread round-robin over the structure's atoms); a structure with more edges fills
+ * its e_pad slots with e_pad of them.  e_pad == 0: the edges back to back, e_total their number.  Outputs: edge_index [2, e_total]
+ * int64 (row 0 senders, row 1 receivers), unit_shifts and shifts (= unit_shifts cell) [e_total, 3] as float64
+ * (out_f64) or float32, n_edges [B] int32 = each structure's real edge count (above e_pad when it overflowed; -1
+ * when it needs padding and cannot have any: no atoms, or c_2 = 0; its slots then hold zero-length self-loops).
+ * edge_index NULL: only n_edges (size the exact layout with it, then call again).  work: caller-owned device scratch
+ * of mh_neighbour_list_work_size(B, N, e_total) bytes.  Device work only (no host synchronisation, no memset), so a
+ * padded build can be captured in a HIP graph; deterministic.  Bind MH_NL_SETUP with 256 threads and rows_per_block
+ * 1, MH_NL_ZERO / _BINS / _PLACE with 256 and 256, MH_NL_SCAN / _OFFSETS with 1024 and 1, MH_NL_COUNT / _FILL with
+ * 256 and 4 (a wave per sender).  No reference counterpart: the reference takes MACE's host-built graphs and
+ * recommends fixed-size padded ones for long runs (README.md:77-78); this builds them on the GPU. */
+size_t mh_neighbour_list_work_size(int32_t B, int32_t N, int64_t e_total);
+int mh_neighbour_list(mh_module* m, const double* pos, const double* cell, const int32_t* pbc, const int64_t* ptr,
+                      int32_t B, int32_t N, double r_max, int64_t e_pad, int64_t e_total, int64_t* edge_index,
+                      void* unit_shifts, void* shifts, int32_t out_f64, int32_t* n_edges, void* work, void* stream);
+
+/* The species order of N nodes from one-hot attributes attrs [N, ne] float32 (ne <= MH_SPECIES_MAX_ELEM): elem [N]
+ * int32 = the first maximum of each row (torch.argmax; reference symmetric.py:169), order [N] int32 = the nodes
+ * stably sorted by elem, slots [nslots] int32 = that order with each element's run padded with -1 to a multiple of
+ * `group`, then -1 (nslots >= ceil(N / group) group + ne group: the symmetric contraction's staged kernels walk
+ * `group` slots of one element per workgroup).  One workgroup (bind MH_SPECIES_ORDER with 1024 threads, rows_per_block
+ * 1); deterministic, no host synchronisation.  No reference counterpart (the reference takes argmax per call and has
+ * no grouped kernels). */
+#define MH_SPECIES_MAX_ELEM 128
+int mh_species_order(mh_module* m, const float* attrs, int32_t N, int32_t ne, int32_t* elem, int32_t* order,
+                     int32_t* slots, int32_t nslots, int32_t group, void* stream);
+
 /* Edge spherical harmonics Y[e, :] = Y_{0..l_max}(vec[e] / |vec[e]|) (vec [E, 3], Y [E, (l_max+1)^2]; e3nn's real
  * basis, y polar axis) and their backward gvec[e] = dL/dvec[e] from gY.  The kernels are generated per (l_max,
  * normalisation).  No reference counterpart: the reference leaves the model's edge spherical harmonics on e3nn's
@@ -354,6 +406,19 @@ int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* W
                void* stream);
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream);
+
+/* Second derivatives of the radial MLP, behind a double backward (ev [E, n_basis] a direction of the features):
+ * mh_mlp_jvp writes dW0 = (dW0/def) ev [E, n_out], the gradient of <ev, dL/def> with respect to gW0; mh_mlp_bwd2
+ * writes the derivative of mh_mlp_bwd's gef along ev for the given gW0 (the Hessian-vector product
+ * sum_k gW0_k d^2 W0_k / def^2 ev), the gradient of <ev, dL/def> with respect to ef.  The first-order kernels run on
+ * dual numbers (each hidden layer carries a tangent; the output layer is the same bf16 three-part product); the
+ * weights are packed as for mh_mlp_fwd (mh_mlp_jvp) and mh_mlp_bwd (mh_mlp_bwd2).  Bind MH_MLP_JVP with 256 threads
+ * and 64 edges per block, MH_MLP_BWD2 with 256 and 64.  No reference counterpart (the reference leaves the MLP on
+ * e3nn and raises on a double backward). */
+int mh_mlp_jvp(mh_module* m, const float* ef, const float* ev, const float* Wh, const uint16_t* Wl, float* dW0,
+               int64_t E, void* stream);
+int mh_mlp_bwd2(mh_module* m, const float* ef, const float* ev, const float* Wh, const uint16_t* Wl, const float* gW0,
+                float* gev, int64_t E, void* stream);
 
 /* The convolution with the radial MLP's output layer inside it (no reference counterpart: the reference streams the
  * materialised weights, W [E, NINS*MUL], through lib.conv_fwd and writes their gradient in lib.conv_bwd_wy,

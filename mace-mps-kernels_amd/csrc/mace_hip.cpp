@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 25; }
+int mh_version(void) { return 29; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -289,10 +289,12 @@ int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* 
     if (!(flags & MH_WANT_GWY)) return fail(-1, "mh_conv_bwd_recv: flags must include MH_WANT_GWY");
     if (!x || !gW || !gY) return fail(-1, "mh_conv_bwd_recv: x, gW and gY are required");
     if (cutoff && !g_cutoff) return fail(-1, "mh_conv_bwd_recv: cutoff given but g_cutoff is NULL");
+    const bool masked = (flags & MH_CUT_MASKED) != 0;
+    if (masked && !cutoff) return fail(-1, "mh_conv_bwd_recv: MH_CUT_MASKED needs the factored form (cutoff)");
     const bool want_gx = (flags & MH_WANT_GX) != 0;
     if (want_gx && (!gx || !work || !rowptr_s || !eids_s))
         return fail(-1, "mh_conv_bwd_recv: gx requested but gx, work or the sender CSR is NULL");
-    int32_t kflags = want_gx ? 1 : 0;
+    int32_t kflags = (want_gx ? 1 : 0) | (masked ? 2 : 0);
     int rc;
     if (cutoff) {
         void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags, &cutoff,
@@ -304,7 +306,8 @@ int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* 
     }
     if (rc || !want_gx) return rc;
     const float* msg = work;
-    void* args2[] = {&msg, &rowptr_s, &eids_s, &gx, &N};
+    const float* mask = masked ? cutoff : nullptr;      // masked edges wrote no message
+    void* args2[] = {&msg, &rowptr_s, &eids_s, &gx, &N, &mask};
     return launch(m, MH_CONV_GXSUM, N, args2, stream, "mh_conv_bwd_recv (dX sum)");
 }
 
@@ -431,6 +434,123 @@ int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n
     }
     void* args[] = {&keys, &rowptr, &tmp, &eids, &E, &n};
     return launch(m, MH_CSR_RANK, E, args, stream, "mh_graph_build");
+}
+
+namespace {
+
+// Byte offsets of the neighbour list's scratch arrays (each 256-byte aligned).
+struct NLWork {
+    size_t prmd, prmi, abin, bcnt, bstart, cursor, binned, cnt, start, tot, keys, total;
+};
+
+NLWork nl_work(int64_t B, int64_t N, int64_t e_total) {
+    NLWork w{};
+    size_t off = 0;
+    auto take = [&off](size_t bytes) {
+        const size_t at = off;
+        off += (bytes + 255) / 256 * 256;
+        return at;
+    };
+    const int64_t nbins = N + B + 1;
+    w.prmd = take(16 * 8 * B);
+    w.prmi = take(16 * 4 * B);
+    w.abin = take(4 * N);
+    w.bcnt = take(4 * nbins);
+    w.bstart = take(4 * nbins);
+    w.cursor = take(4 * nbins);
+    w.binned = take(4 * N);
+    w.cnt = take(8 * N);
+    w.start = take(8 * N);
+    w.tot = take(8 * B);
+    w.keys = take(8 * (e_total > 0 ? e_total : 0));
+    w.total = off;
+    return w;
+}
+
+}  // namespace
+
+size_t mh_neighbour_list_work_size(int32_t B, int32_t N, int64_t e_total) {
+    if (B < 0 || N < 0 || e_total < 0) return 0;
+    return nl_work(B, N, e_total).total;
+}
+
+int mh_neighbour_list(mh_module* m, const double* pos, const double* cell, const int32_t* pbc, const int64_t* ptr,
+                      int32_t B, int32_t N, double r_max, int64_t e_pad, int64_t e_total, int64_t* edge_index,
+                      void* unit_shifts, void* shifts, int32_t out_f64, int32_t* n_edges, void* work, void* stream) {
+    if (B < 0 || N < 0 || e_pad < 0 || e_total < 0 || static_cast<int64_t>(N) + B + 1 >= 0x7fffffffLL)
+        return fail(-1, "mh_neighbour_list: bad sizes");
+    if (!(r_max > 0.0) || r_max > 1e300) return fail(-1, "mh_neighbour_list: r_max must be positive and finite");
+    if (e_pad > 0 && e_total != static_cast<int64_t>(B) * e_pad)
+        return fail(-1, "mh_neighbour_list: with e_pad > 0, e_total must be B * e_pad");
+    if (B == 0) return 0;
+    if (!cell || !pbc || !ptr || !n_edges || !work || (N > 0 && !pos))
+        return fail(-1, "mh_neighbour_list: NULL operand");
+    if (edge_index && e_total > 0 && (!unit_shifts || !shifts))
+        return fail(-1, "mh_neighbour_list: edge_index given without unit_shifts / shifts");
+    const NLWork w = nl_work(B, N, e_total);
+    char* base = static_cast<char*>(work);
+    double* prmd = reinterpret_cast<double*>(base + w.prmd);
+    int32_t* prmi = reinterpret_cast<int32_t*>(base + w.prmi);
+    int32_t* abin = reinterpret_cast<int32_t*>(base + w.abin);
+    int32_t* bcnt = reinterpret_cast<int32_t*>(base + w.bcnt);
+    int32_t* bstart = reinterpret_cast<int32_t*>(base + w.bstart);
+    int32_t* cursor = reinterpret_cast<int32_t*>(base + w.cursor);
+    int32_t* binned = reinterpret_cast<int32_t*>(base + w.binned);
+    int64_t* cnt = reinterpret_cast<int64_t*>(base + w.cnt);
+    int64_t* start = reinterpret_cast<int64_t*>(base + w.start);
+    int64_t* tot = reinterpret_cast<int64_t*>(base + w.tot);
+    int64_t* keys = reinterpret_cast<int64_t*>(base + w.keys);
+    const int32_t nbins = N + B;
+    int64_t nzero = static_cast<int64_t>(nbins) + 1;
+    const char* what = "mh_neighbour_list";
+    int rc;
+    {
+        void* args[] = {&pos, &cell, &pbc, &ptr, &B, &r_max, &prmd, &prmi};
+        if ((rc = launch(m, MH_NL_SETUP, B, args, stream, what))) return rc;
+    }
+    {
+        void* args[] = {&bcnt, &nzero};
+        if ((rc = launch(m, MH_NL_ZERO, nzero, args, stream, what))) return rc;
+    }
+    {
+        void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &abin, &bcnt};
+        if ((rc = launch(m, MH_NL_BINS, N, args, stream, what))) return rc;
+    }
+    {
+        int32_t nb = nbins;
+        void* args[] = {&bcnt, &bstart, &cursor, &nb};
+        if ((rc = launch(m, MH_NL_SCAN, 1, args, stream, what))) return rc;
+    }
+    {
+        void* args[] = {&abin, &cursor, &binned, &N};
+        if ((rc = launch(m, MH_NL_PLACE, N, args, stream, what))) return rc;
+    }
+    {
+        void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &bstart, &binned, &r_max, &cnt};
+        if ((rc = launch(m, MH_NL_COUNT, N, args, stream, what))) return rc;
+    }
+    {
+        int64_t* ei = e_total > 0 ? edge_index : nullptr;
+        void* args[] = {&ptr, &B, &N, &prmi, &cnt, &e_pad, &e_total, &start, &tot, &n_edges, &ei, &unit_shifts,
+                        &shifts, &out_f64};
+        if ((rc = launch(m, MH_NL_OFFSETS, 1, args, stream, what))) return rc;
+    }
+    if (!edge_index || e_total == 0) return 0;
+    void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &bstart, &binned, &r_max, &cnt, &start, &tot, &e_pad,
+                    &e_total, &keys, &edge_index, &unit_shifts, &shifts, &out_f64};
+    return launch(m, MH_NL_FILL, N, args, stream, what);
+}
+
+int mh_species_order(mh_module* m, const float* attrs, int32_t N, int32_t ne, int32_t* elem, int32_t* order,
+                     int32_t* slots, int32_t nslots, int32_t group, void* stream) {
+    if (N < 0 || ne < 1 || ne > MH_SPECIES_MAX_ELEM || group < 1)
+        return fail(-1, "mh_species_order: bad sizes (1 <= ne <= MH_SPECIES_MAX_ELEM, group >= 1)");
+    const int64_t need = (static_cast<int64_t>(N) + group - 1) / group * group + static_cast<int64_t>(ne) * group;
+    if (nslots < need) return fail(-1, "mh_species_order: nslots < ceil(N / group) group + ne group");
+    if (N > 0 && (!attrs || !elem || !order)) return fail(-1, "mh_species_order: NULL operand");
+    if (nslots > 0 && !slots) return fail(-1, "mh_species_order: NULL slots");
+    void* args[] = {&attrs, &N, &ne, &elem, &order, &slots, &nslots, &group};
+    return launch(m, MH_SPECIES_ORDER, 1, args, stream, "mh_species_order");
 }
 
 }  // extern "C"
@@ -580,6 +700,20 @@ int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* W
     return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
 }
 
+int mh_mlp_jvp(mh_module* m, const float* ef, const float* ev, const float* Wh, const uint16_t* Wl, float* dW0,
+               int64_t E, void* stream) {
+    if (E > 0 && (!ef || !ev || !Wh || !Wl || !dW0)) return fail(-1, "mh_mlp_jvp: NULL operand");
+    void* args[] = {&ef, &ev, &Wh, &Wl, &dW0, &E};
+    return launch(m, MH_MLP_JVP, E, args, stream, "mh_mlp_jvp");
+}
+
+int mh_mlp_bwd2(mh_module* m, const float* ef, const float* ev, const float* Wh, const uint16_t* Wl, const float* gW0,
+                float* gev, int64_t E, void* stream) {
+    if (E > 0 && (!ef || !ev || !Wh || !Wl || !gW0 || !gev)) return fail(-1, "mh_mlp_bwd2: NULL operand");
+    void* args[] = {&ef, &ev, &Wh, &Wl, &gW0, &gev, &E};
+    return launch(m, MH_MLP_BWD2, E, args, stream, "mh_mlp_bwd2");
+}
+
 int mh_mlp_hid(mh_module* m, const float* ef, const float* Wh, const float* cutoff, uint16_t* hc, int64_t E,
                void* stream) {
     if (E > 0 && (!ef || !Wh || !cutoff || !hc)) return fail(-1, "mh_mlp_hid: NULL operand");
@@ -642,7 +776,8 @@ int mh_conv_bwd_mlp(mh_module* m, const float* x, const float* g, const float* Y
     }
     if (!want_gx) return 0;
     const float* msg = work;
-    void* args3[] = {&msg, &rowptr_s, &eids_s, &gx, &N};
+    const float* mask = nullptr;
+    void* args3[] = {&msg, &rowptr_s, &eids_s, &gx, &N, &mask};
     return launch(m, MH_CONV_GXSUM, N, args3, stream, "mh_conv_bwd_mlp (dX sum)");
 }
 

@@ -36,12 +36,14 @@ from .readout import HipReadout, readout_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
 from . import geometry as _geometry
+from .conv import check_graphs
+from .neighbours import NeighbourList, neighbour_list, update_batch
 
 __version__ = '0.1.0'
 __all__ = ['patch_model', 'unpatch_model', 'HipConvTP', 'HipSymmetricContraction', 'HipSphericalHarmonics',
            'HipNodeLinear', 'HipRadialMLP', 'HipRadialEmbedding', 'conv_supported', 'sc_supported', 'sh_supported', 'lin_supported',
            'mlp_supported', 'emb_supported', 'HipReshapeIrreps', 'reshape_supported', 'HipReadout',
-           'readout_supported']
+           'readout_supported', 'neighbour_list', 'update_batch', 'NeighbourList', 'check_graphs']
 
 _LINEAR_CLASSES = ('Linear', 'FullyConnectedTensorProduct')
 

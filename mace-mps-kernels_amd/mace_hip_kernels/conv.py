@@ -28,7 +28,7 @@ import weakref
 import numpy as np
 import torch
 
-from . import _native
+from . import _native, neighbours
 from .conv_codegen import gxsum_block, source
 
 WAVE = 64
@@ -333,22 +333,57 @@ def build_graph(edge_index, n):
     return keys, rowptr, eids, bad
 
 
+# How a new edge_index is checked for nodes outside [0, n).  The graph build clamps such indices (so no kernel ever
+# reads out of range) and sets a device flag.  'deferred': the flag is copied to pinned host memory behind the build
+# and read when that copy has landed, at the next graph lookup or at check_graphs(); no host synchronisation.
+# 'sync': the flag is read at once (one device-to-host synchronisation per new edge_index).  Edge lists made by
+# mace_hip_kernels.neighbours are in range by construction and are not checked.
+GRAPH_CHECK = 'deferred'
+_pending_checks = []       # [(pinned int32 [1], event, shape, n)] of edge lists whose flag has not been read
+
+
+def check_graphs(block=True):
+    """Read the out-of-range flags of the edge lists built since the last check (``block``: wait for them; else
+    only those already available) and raise ValueError if any edge_index held a node outside [0, n)."""
+    keep, bad = [], None
+    for item in _pending_checks:
+        flag, ev, shape, n = item
+        if not block and not ev.query():
+            keep.append(item)
+            continue
+        ev.synchronize()
+        if int(flag[0]) and bad is None:
+            bad = (shape, n)
+    _pending_checks[:] = keep
+    if bad is not None:
+        raise ValueError(f'an edge_index of shape {bad[0]} given to a patched convolution held nodes outside '
+                         f'[0, {bad[1]}); that call clamped them (its results are wrong)')
+
+
 class _Graph:
     """int32 senders/receivers and both CSRs of one edge_index (``build_graph``), shared by every layer of a call.
 
-    ``validate=False`` (a graph first met inside a HIP graph capture, which cannot synchronise to check it): out of
-    range indices are clamped into [0, n) without a check, so a bad edge list gives wrong numbers, never an
-    out-of-range access."""
+    Out-of-range indices are clamped into [0, n), so a bad edge list gives wrong numbers, never an out-of-range
+    access; ``validate`` reports them (see GRAPH_CHECK).  ``validate=False`` (a graph first met inside a HIP graph
+    capture, which can neither synchronise nor record the check): no report."""
 
     def __init__(self, edge_index, n, validate=True):
         if edge_index.dim() != 2 or edge_index.shape[0] != 2:
             raise ValueError(f'edge_index must be [2, E], got {tuple(edge_index.shape)}')
         self.n = n
         keys, rowptr, eids, bad = build_graph(edge_index, n)
-        if validate and edge_index.shape[1] and int(bad.item()):
-            # the kernels index x, g and the CSRs with these values: out-of-range nodes are an error
-            lo, hi = (int(v) for v in torch.aminmax(edge_index))
-            raise ValueError(f'edge_index holds node {lo if lo < 0 else hi} outside [0, {n})')
+        if validate and edge_index.shape[1] and not neighbours.built_here(edge_index, n):
+            if GRAPH_CHECK == 'sync':
+                if int(bad.item()):
+                    # the kernels index x, g and the CSRs with these values: out-of-range nodes are an error
+                    lo, hi = (int(v) for v in torch.aminmax(edge_index))
+                    raise ValueError(f'edge_index holds node {lo if lo < 0 else hi} outside [0, {n})')
+            else:
+                flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+                flag.copy_(bad, non_blocking=True)
+                ev = torch.cuda.Event()
+                ev.record()
+                _pending_checks.append((flag, ev, tuple(edge_index.shape), n))
         self.send, self.recv = keys[0], keys[1]
         self._by_send = (rowptr[0], eids[0])
         self._by_recv = (rowptr[1], eids[1])
@@ -371,6 +406,8 @@ _capture_graphs = {}       # graphs built inside the current capture, by (id(edg
 
 def graph_for(edge_index, n):
     """Cached ``_Graph`` for this edge_index tensor object (invalidated by in-place modification or deletion)."""
+    if _pending_checks and not _native.capturing():
+        check_graphs(block=False)
     if _native.capturing() and _capture_rebuild:
         gr = _capture_graphs.get((id(edge_index), n))
         if gr is None or gr.src is not edge_index:
@@ -527,9 +564,17 @@ class RadialWeights(torch.Tensor):
 _MULS = {torch.Tensor.__mul__, torch.Tensor.__rmul__, torch.Tensor.mul, torch.mul}
 
 
-def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy):
+def _support_masked(cut):
+    """Whether ``cut`` is a patched radial embedding's cutoff, unmodified since: -0.0 then marks exactly the edges
+    outside the envelope's support, where the envelope's derivative is zero."""
+    return getattr(cut, '_mh_support_mask', None) == cut._version
+
+
+def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False):
     """First-order gradients (gx, gY, gW or gW0, gcut) of <g, conv(x, Y, W)> for contiguous operands, by the
-    kernels; W = W0 * cut (cut flat [E]) when W is None.  Entries not wanted are None."""
+    kernels; W = W0 * cut (cut flat [E]) when W is None.  Entries not wanted are None.  ``masked`` (factored only):
+    edges with cut == -0.0 lie outside the cutoff envelope's support, and their gradients, gcut included, are zero
+    (the envelope's derivative there is zero, so gcut's true value there never matters to its producer)."""
     factored = W is None
     E = Y.shape[0]
     gx = torch.empty_like(x) if want_x else None
@@ -538,6 +583,8 @@ def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy):
     gcut = torch.empty_like(cut) if want_wy and factored else None
     # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
     flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy and E > 0 else 0)
+    if masked and factored and flags & _native.MH_WANT_GWY:
+        flags |= _native.MH_CUT_MASKED
     lib = _native.load()
     P = _native.ptr
     if flags & _native.MH_WANT_GWY and (op.bwd_recv or factored):
@@ -582,6 +629,7 @@ class _ConvFn(torch.autograd.Function):
                            P(W0.contiguous()), P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n,
                            _native.stream_of(x))
             ctx.cut_shape = cut.shape
+            ctx.masked = _support_masked(cut)
             ctx.save_for_backward(x, Y, W0, cut, edge_index)
         else:
             _native.launch(f'conv_fwd[{op.tag}]', lib.mh_conv_fwd, op.module.handle, P(xc), P(Yc), P(W.contiguous()),
@@ -615,7 +663,7 @@ class _ConvFn(torch.autograd.Function):
         xc, Yc, gc_ = x.contiguous(), Y.contiguous(), g.contiguous()
         if ctx.factored:
             gx, gY, gW, gcut = _conv_grads(op, gr, gc_, xc, Yc, None, W0.contiguous(), cut.reshape(-1).contiguous(),
-                                           want_x, want_y or want_w)
+                                           want_x, want_y or want_w, masked=ctx.masked and op.skip_masked)
             return gx, gY, None, gW, gcut.view(ctx.cut_shape) if gcut is not None else None, None, None
         gx, gY, gW, _ = _conv_grads(op, gr, gc_, xc, Yc, W.contiguous(), None, None, want_x, want_y or want_w)
         return gx, gY, gW, None, None, None, None
@@ -710,6 +758,9 @@ class HipConvTP(torch.nn.Module):
         self.bwd_recv = True
         # differentiate MACE's tp_weights = W0 * cutoff inside the backward kernel (see _factored_weights)
         self.fuse_cutoff = True
+        # first-order backward: skip edges outside the cutoff's support when the cutoff comes unmodified from a
+        # patched radial embedding (MH_CUT_MASKED)
+        self.skip_masked = True
         # a backward under create_graph=True: raise (the reference's behaviour) unless this is set, in which case
         # the gradients are differentiable again (_ConvAdjFn)
         self.double_backward = False

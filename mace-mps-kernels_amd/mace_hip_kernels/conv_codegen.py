@@ -433,7 +433,13 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
     ``cut`` (kernel ``conv_bwdrc``): the weights arrive factored as W = W0·c with a per-edge scalar c (MACE's
     ``tp_weights * cutoff``).  The kernel reads W0 and c, writes ∂/∂W0 = gW·c instead of gW, and reduces
     ∂/∂c[e] = Σ_{k,u} gW·W0 over the channels (a butterfly over the wave, then LDS across waves, fixed order), which
-    saves the caller the separate passes over the [E, NW] tensors that differentiating the product takes."""
+    saves the caller the separate passes over the [E, NW] tensors that differentiating the product takes.
+
+    Masked edges (``cut`` with flags bit 1): c = -0.0 exactly marks an edge outside the envelope's support, where the
+    envelope's derivative is zero (padding edges, edges past r_max).  There W = 0, so ∂/∂W0 = gW·c, gY and the dX
+    message are zero, and ∂/∂c is multiplied by a zero derivative wherever it goes: the kernel writes zero ∂/∂W0,
+    gY and ∂/∂c rows for such an edge without reading W0 or x, writes no dX message (``conv_gxsum`` skips the edge
+    too), and walks only the other edges of each chunk (compacted by lane rank, as in ``conv_fwdc``)."""
     spec, nx, nk = G.s, G.nx, G.s.nins
     L = [
         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwdrc" if cut else "conv_bwdr")}(',
@@ -443,13 +449,14 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         '    float* __restrict__ gxm, int N, int flags' +
         (', const float* __restrict__ cutv, float* __restrict__ gcut) {' if cut else ') {'),
         '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
-    ] + (['  __shared__ float partc[NCB][MH_WAVE];'] if cut else []) + [
+    ] + (['  __shared__ float partc[NCB][MH_WAVE];', '  __shared__ int sidx[NCB][MH_WAVE];'] if cut else []) + [
         '  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
         '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);',
         '  const int r = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  if (r >= N) return;',
     ] + G.prelude() + [
         '  const bool GX = (flags & 1) != 0;',
+    ] + (['  const bool MASKED = (flags & 2) != 0;'] if cut else []) + [
         '  ' + decl('gv', G.no),
     ]
     L += G.ld_g('  ', 'r', 'gv')
@@ -457,10 +464,38 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
           '  const int p0 = rowptr[r], p1 = rowptr[r + 1];']
 
     def chunks(msg):
-        C = ['  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
-             '    const int cnt = min(MH_WAVE, p1 - pb);',
-             '    int my_e = 0, my_s = 0;',
-             '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
+        C = ['  for (int pb = p0; pb < p1; pb += MH_WAVE) {']
+        if cut:
+            # every wave reads the same edges and cutoffs, so ballots, counts and the `continue` are uniform over
+            # the workgroup and the barriers below stay matched
+            C += ['    const int cnt0 = min(MH_WAVE, p1 - pb);',
+                  '    int my_e = 0, my_s = 0;',
+                  '    bool keep = false;',
+                  '    if (lane < cnt0) {',
+                  '      my_e = eids[pb + lane];',
+                  '      keep = !(MASKED && __float_as_uint(cutv[my_e]) == 0x80000000u);',
+                  '    }',
+                  '    const unsigned long long kept = __ballot(keep);',
+                  '    const unsigned long long drop = __ballot(lane < cnt0 && !keep);',
+                  '    const int cnt = __popcll(kept);',
+                  '    if (keep) sidx[wave][__popcll(kept & ((1ull << lane) - 1ull))] = my_e;',
+                  '    for (unsigned long long d = drop; d; d &= d - 1ull) {',
+                  '      const int ez = mh_bcast(my_e, __builtin_ctzll(d));',
+                  '      float* __restrict__ gz = gW + (size_t)ez * NW;']
+            st = [f'mh_st_nt(gz + {k * spec.mul}, ol1, 0.0f);' for k in range(nk)]
+            C += [f'      {t}' if G.full else f'      if (active) {t}' for t in st]
+            C += ['      if (wave == 0) {',
+                  '        if (lane < Y_DIM) gY[(size_t)ez * Y_DIM + lane] = 0.0f;',
+                  '        if (lane == 0) gcut[ez] = 0.0f;',
+                  '      }',
+                  '    }',
+                  '    if (cnt == 0) continue;',
+                  '    my_e = 0;',
+                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; }']
+        else:
+            C += ['    const int cnt = min(MH_WAVE, p1 - pb);',
+                  '    int my_e = 0, my_s = 0;',
+                  '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
         C += G.m_prologue('    ', 'my_e')
         C += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
         C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
@@ -493,7 +528,7 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
             C += [f'      Pc += {_xchg("Pc", bit)};' for bit in range(5, -1, -1)]
             C += ['      if (lane == 0) partc[wave][j] = Pc;']
         C += ['    }']
-        C += _gy_combine('    ', 'eids[pb + j]', cut=cut)
+        C += _gy_combine('    ', 'sidx[0][j]' if cut else 'eids[pb + j]', cut=cut)
         return C + ['  }']
 
     L += ['  if (GX) {'] + ['  ' + t for t in chunks(True)] + ['  } else {']
@@ -507,31 +542,54 @@ def gxsum_block(spec):
 
 
 def _gx_sum(spec):
-    """gx[s] = Σ_{e ∈ CSR_send(s)} gxm[e], summed in CSR order (deterministic); one float4 column per thread."""
+    """gx[s] = Σ_{e ∈ CSR_send(s)} gxm[e], summed in CSR order (deterministic); one float4 column per thread.
+    ``mask`` non-NULL: edges whose mask value is -0.0 exactly have no message (``conv_bwdrc`` with masked edges
+    writes none; it would be zero) and are skipped, which leaves every sum unchanged."""
     assert spec.x_dim % 4 == 0
     return [
         f'extern "C" __global__ __launch_bounds__({gxsum_block(spec)}) void {spec.kname("conv_gxsum")}(',
         '    const float* __restrict__ gxm, const int* __restrict__ rowptr, const int* __restrict__ eids,',
-        '    float* __restrict__ gx, int N) {',
+        '    float* __restrict__ gx, int N, const float* __restrict__ mask) {',
         '  const int s = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  const int t = threadIdx.x;',
         '  if (s >= N || t >= X_DIM / 4) return;',
         '  const float4* __restrict__ src = reinterpret_cast<const float4*>(gxm) + t;',
-        '  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);',
+        '  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);',
+        '  float4 acc = z;',
         '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
         '  int p = p0;',
-        '  for (; p + 4 <= p1; p += 4) {',
-        '    const int e0 = eids[p], e1 = eids[p + 1], e2 = eids[p + 2], e3 = eids[p + 3];',
-        '    const float4 v0 = src[(size_t)e0 * (X_DIM / 4)], v1 = src[(size_t)e1 * (X_DIM / 4)];',
-        '    const float4 v2 = src[(size_t)e2 * (X_DIM / 4)], v3 = src[(size_t)e3 * (X_DIM / 4)];',
-        '    acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;',
-        '    acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;',
-        '    acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;',
-        '    acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;',
-        '  }',
-        '  for (; p < p1; ++p) {',
-        '    const float4 v = src[(size_t)eids[p] * (X_DIM / 4)];',
-        '    acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;',
+        '  if (mask) {',
+        '    for (; p + 4 <= p1; p += 4) {',
+        '      const int e0 = eids[p], e1 = eids[p + 1], e2 = eids[p + 2], e3 = eids[p + 3];',
+        '      const bool k0 = __float_as_uint(mask[e0]) != 0x80000000u, k1 = __float_as_uint(mask[e1]) != 0x80000000u;',
+        '      const bool k2 = __float_as_uint(mask[e2]) != 0x80000000u, k3 = __float_as_uint(mask[e3]) != 0x80000000u;',
+        '      const float4 v0 = k0 ? src[(size_t)e0 * (X_DIM / 4)] : z, v1 = k1 ? src[(size_t)e1 * (X_DIM / 4)] : z;',
+        '      const float4 v2 = k2 ? src[(size_t)e2 * (X_DIM / 4)] : z, v3 = k3 ? src[(size_t)e3 * (X_DIM / 4)] : z;',
+        '      if (k0) { acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w; }',
+        '      if (k1) { acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w; }',
+        '      if (k2) { acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w; }',
+        '      if (k3) { acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w; }',
+        '    }',
+        '    for (; p < p1; ++p) {',
+        '      const int e = eids[p];',
+        '      if (__float_as_uint(mask[e]) == 0x80000000u) continue;',
+        '      const float4 v = src[(size_t)e * (X_DIM / 4)];',
+        '      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;',
+        '    }',
+        '  } else {',
+        '    for (; p + 4 <= p1; p += 4) {',
+        '      const int e0 = eids[p], e1 = eids[p + 1], e2 = eids[p + 2], e3 = eids[p + 3];',
+        '      const float4 v0 = src[(size_t)e0 * (X_DIM / 4)], v1 = src[(size_t)e1 * (X_DIM / 4)];',
+        '      const float4 v2 = src[(size_t)e2 * (X_DIM / 4)], v3 = src[(size_t)e3 * (X_DIM / 4)];',
+        '      acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;',
+        '      acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;',
+        '      acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;',
+        '      acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;',
+        '    }',
+        '    for (; p < p1; ++p) {',
+        '      const float4 v = src[(size_t)eids[p] * (X_DIM / 4)];',
+        '      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;',
+        '    }',
         '  }',
         '  reinterpret_cast<float4*>(gx)[(size_t)s * (X_DIM / 4) + t] = acc;',
         '}', '',

@@ -91,7 +91,7 @@ def math_lines(spec):
             f'const float up = {powu(p)};',
             f'const bool in = x < {_lit(spec.r_max)};',
             f'const float env = 1.f - {_lit(c1)} * up + {_lit(c2)} * (up * u) - {_lit(c3)} * (up * u * u);',
-            'const float cut = in ? env : 0.f;']
+            'const float cut = in ? env : -0.f;']           # -0.0: outside the support (see HipRadialEmbedding)
     fwd = [f'const float f{k} = ({_lit(spec.pref)} * sinf({_lit(w)} * x)) / x * cut;' for k, w in enumerate(spec.w)]
     # d cut/dx = env'(u) / r_max inside the cutoff; d feat_k/dx = b_k' cut + b_k cut'
     bwd = [f'const float denv = (-{_lit(c1 * p)} * {powu(p - 1)} + {_lit(c2 * (p + 1))} * up'
@@ -263,5 +263,10 @@ class HipRadialEmbedding(torch.nn.Module):
         return self._second
 
     def forward(self, edge_lengths, *args, **kwargs):
-        return _EmbFn.apply(edge_lengths, self)
+        feats, cut = _EmbFn.apply(edge_lengths, self)
+        # The cutoff is -0.0 exactly where r >= r_max (outside the envelope's support, where its derivative is zero)
+        # and nonzero or +0.0 elsewhere; a patched convolution that receives this tensor unmodified (same version)
+        # skips such edges in its backward (MH_CUT_MASKED).
+        cut._mh_support_mask = cut._version
+        return feats, cut
 

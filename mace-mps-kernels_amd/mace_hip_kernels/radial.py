@@ -40,6 +40,7 @@ from . import conv as _conv
 BLOCK = 256          # 4 waves
 NB_FWD = 2           # 16-edge tiles per wave in the forward (each LDS weight fragment feeds NB_FWD MFMAs)
 NB_BWD = 1           # and in the backward
+NB_JVP = 1           # and in the forward-mode derivative (twice the hidden registers of the forward)
 GW_DIST = 2          # chunks of dL/dW0 in flight ahead of the one being multiplied (backward)
 PREFETCH = 2         # output-layer weight chunks in flight ahead of the one being multiplied
 HIDDEN_TILES_BWD = 1 # edge tiles whose hidden layers the backward recomputes together (register pressure)
@@ -185,7 +186,24 @@ def bf16_split3(a):
 
 
 def source(spec):
-    """HIP source of ``mlp_fwd`` and ``mlp_bwd``."""
+    """HIP source of ``mlp_fwd`` and ``mlp_bwd`` (and the fused convolution's ``mlp_hid`` / ``mlp_hidb``)."""
+    return _source(spec, second=False)
+
+
+def source_second(spec):
+    """HIP source of the second-order kernels behind a double backward (compiled on first use):
+    ``mlp_jvp``  the forward on dual numbers, edge features ef + eps v: the eps part of the output, dW0 = J(ef) v
+                 (every hidden layer carries a tangent, h' = c silu'(z) z', and the output layer multiplies the last
+                 hidden layer's tangent);
+    ``mlp_bwd2`` the backward on the same dual numbers with dL/dW0 held real: the eps part of dL/d(edge features),
+                 the Hessian-vector product sum_k gW_k d^2 W0_k / def^2 v (walking back, g_z = g_h h'(z) gains the
+                 tangent g_h' h'(z) + g_h h''(z) z').
+    Both keep the first-order kernels' structure: hidden layers on the fp32 MFMA, the output layer at fp32 accuracy on
+    the bf16 MFMA."""
+    return _source(spec, second=True)
+
+
+def _source(spec, second):
     Lo = _layout(spec)
     H0, NW, HL, K0S = Lo['H0'], Lo['NW'], Lo['HL'], Lo['K0S']
     rows, cols = Lo['rows'], Lo['cols']
@@ -201,6 +219,12 @@ def source(spec):
     lds_bwd = max(Lo['nat_size'], Lo['chunk_bwd'])
     L = [_native.device_header(),
          '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '']
+    if second:
+        # h = c z s(z) (s the logistic function): h' = c s (1 + z (1 - s)), h'' = c s (1 - s) (2 + z (1 - 2 s))
+        L += ['__device__ __forceinline__ float mlp_d1(float z) { const float s = mlp_sig(z); '
+              'return s * (1.f + z * (1.f - s)); }',
+              '__device__ __forceinline__ float mlp_d2(float z) { const float s = mlp_sig(z); '
+              'return s * (1.f - s) * (2.f + z * (1.f - 2.f * s)); }', '']
 
     def head(name, args, lds, nb, waves=BLOCK // 64):
         P = [f'extern "C" __global__ __launch_bounds__({64 * waves}) void {name}({args}) {{',
@@ -225,30 +249,35 @@ def source(spec):
               f'reinterpret_cast<mh_f4*>(lds)[t + {i * nthreads}] = sg{i};' for i in range(it)]
         return P
 
-    def xin(tiles):
+    def xin(tiles, src='ef', name='xin'):
         P = []
         for b in tiles:
-            P += [f'  float xin{b}[{K0S}];']
-            P += [f'  xin{b}[{st}] = {4 * st} + q < {H0} ? ef[ejc{b} * {H0} + {4 * st} + q] : 0.f;' for st in range(K0S)]
+            P += [f'  float {name}{b}[{K0S}];']
+            P += [f'  {name}{b}[{st}] = {4 * st} + q < {H0} ? {src}[ejc{b} * {H0} + {4 * st} + q] : 0.f;'
+                  for st in range(K0S)]
         return P
 
-    def hidden_fwd(transposed, keep, tiles):
+    def hidden_fwd(transposed, keep, tiles, dual=False, keep_t=False):
         """z_i and h_i = c_i silu(z_i) for every hidden layer on the fp32 MFMA, A operands from LDS (transposed
-        layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for every edge tile in ``tiles``."""
+        layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for every edge tile in
+        ``tiles``.  ``dual``: also the tangents zt_i (the same A operands applied to the input tangent xv / the
+        previous layer's ht) and ht_i = c_i silu'(z_i) zt_i (the last layer's with ``keep_t``)."""
         P = []
+        chains = [('z', 'xin', 'h')] + ([('zt', 'xv', 'ht')] if dual else [])
         for i in range(nh):
             T = cols[i] // 16
-            for b in tiles:
-                P.append(f'  mh_f4 z{i}_{b}[{T}];')
-                P += [f'  z{i}_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(T)]
+            for zn, _, _ in chains:
+                for b in tiles:
+                    P.append(f'  mh_f4 {zn}{i}_{b}[{T}];')
+                    P += [f'  {zn}{i}_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(T)]
             if i == 0:
                 for st in range(K0S):
                     for o in range(T):
                         a = (f'lds[{Lo["tr"][0]} + ({16 * o} + c16) * {rows[0] + PAD} + {4 * st} + q]' if transposed else
                              f'lds[{Lo["nat"][0]} + ({4 * st} + q) * {cols[0] + PAD} + {16 * o} + c16]')
                         P.append(f'  {{ const float a = {a};')
-                        P += [f'    z0_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, xin{b}[{st}], z0_{b}[{o}], 0, 0, 0);'
-                              for b in tiles]
+                        P += [f'    {zn}0_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, {xn}{b}[{st}], {zn}0_{b}[{o}], '
+                              f'0, 0, 0);' for zn, xn, _ in chains for b in tiles]
                         P.append('  }')
             else:
                 Tin = cols[i - 1] // 16
@@ -262,8 +291,8 @@ def source(spec):
                             a = (f'a{i}_{ti}_{o}[{r}]' if transposed else
                                  f'lds[{Lo["nat"][i]} + ({16 * ti + r} + 4 * q) * {cols[i] + PAD} + {16 * o} + c16]')
                             P.append(f'  {{ const float a = {a};')
-                            P += [f'    z{i}_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, h{i - 1}_{b}[{ti}][{r}], '
-                                  f'z{i}_{b}[{o}], 0, 0, 0);' for b in tiles]
+                            P += [f'    {zn}{i}_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, {hn}{i - 1}_{b}[{ti}][{r}], '
+                                  f'{zn}{i}_{b}[{o}], 0, 0, 0);' for zn, _, hn in chains for b in tiles]
                             P.append('  }')
             if i < nh - 1 or keep:
                 for b in tiles:
@@ -272,6 +301,13 @@ def source(spec):
                         for r in range(4):
                             P.append(f'  h{i}_{b}[{o}][{r}] = {_lit(spec.c[i])} * z{i}_{b}[{o}][{r}] * '
                                      f'mlp_sig(z{i}_{b}[{o}][{r}]);')
+            if dual and (i < nh - 1 or keep_t):
+                for b in tiles:
+                    P.append(f'  mh_f4 ht{i}_{b}[{T}];')
+                    for o in range(T):
+                        for r in range(4):
+                            P.append(f'  ht{i}_{b}[{o}][{r}] = {_lit(spec.c[i])} * mlp_d1(z{i}_{b}[{o}][{r}]) * '
+                                     f'zt{i}_{b}[{o}][{r}];')
         return P
 
     def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None, reg='pre'):
@@ -299,74 +335,96 @@ def source(spec):
     PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
 
     # ------------------------------------------------------------------ forward
-    # hidden weights transposed [j][k + PAD] in fp32; the output layer as bf16 chunks of CH columns x HL (K in the
-    # _kperm order), three parts each, double-buffered in LDS (the hidden weights' space is reused once they are done)
-    nb = NB_FWD
-    ncf = 2 if nb == 1 else 1                            # accumulator chains per result tile
-    F = head(spec.kname('mlp_fwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
-             'const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E', lds_fwd, nb)
-    F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(nb)) + hidden_fwd(True, True, range(nb))
-    # the last hidden layer's activations as bf16 operands: step s, lane group q: features 32 s + 16 t + 4 q + r
-    for b in range(nb):
-        hl = f'h{nh - 1}_{b}'
-        F += [f'  mh_bf8 hb{b}[{S}][3];']
-        for st in range(S):
-            F += [f'  {{ const float v[8] = {{{", ".join(f"{hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
-                  f'    mh_split8(v, hb{b}[{st}]); }}']
-    # weight chunks in flight: register set j holds chunk c + PD while chunk c is multiplied (the loop is unrolled PD
-    # times so the sets have fixed names; chunks past the last, when PD does not divide the count, are computed from
-    # the last chunk's weights and not stored)
-    PD = PREFETCH
-    NCHP = -(-NCHK // PD) * PD
-    npre = -(-(NSPLIT * CH * HL // 8) // BLOCK)
-    for j in range(PD):
-        F += [f'  mh_u4 {", ".join(f"pre{j}_{i}" for i in range(npre))};']
-        F += chunk_io('Wl', f'{min(j, NCHK - 1) * NSPLIT * CH * HL}', HL, RSF, CH, '  ', reg=f'pre{j}_')[0]
-    F += ['  __syncthreads();                                // every wave is done with the hidden weights']
-    F += chunk_io('Wl', 0, HL, RSF, CH, '  ', store_base='0', reg='pre0_')[0] + ['  __syncthreads();']
-    F += [f'  for (int ch = 0; ch < {NCHP}; ch += {PD}) {{']
-    for j in range(PD):
-        c = f'(ch + {j})' if j else 'ch'
-        F += ['  {',
-              f'    const int c = {c}, base = (c & 1) * {Lo["chunk_fwd"]}, nbase = {Lo["chunk_fwd"]} - base;',
-              f'    const size_t nx = (size_t)min(c + {PD}, {NCHK - 1}) * {NSPLIT * CH * HL};']
-        F += chunk_io('Wl', 'nx', HL, RSF, CH, '    ', reg=f'pre{j}_')[0]
-        F += ['    __builtin_amdgcn_sched_barrier(0);            // the loads go out before the MFMAs']
+    def fwd_kernel(name, tangent):
+        """The forward (``tangent``: the JVP: edge features ef + eps ev, the eps part of the output)."""
+        # hidden weights transposed [j][k + PAD] in fp32; the output layer as bf16 chunks of CH columns x HL (K in the
+        # _kperm order), three parts each, double-buffered in LDS (the hidden weights' space is reused once they are done)
+        nb = NB_JVP if tangent else NB_FWD
+        ncf = 2 if nb == 1 else 1                            # accumulator chains per result tile
+        F = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if tangent else '') +
+                 'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E',
+                 lds_fwd, nb)
+        F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(nb))
+        if tangent:
+            F += xin(range(nb), 'ev', 'xv') + hidden_fwd(True, False, range(nb), dual=True, keep_t=True)
+        else:
+            F += hidden_fwd(True, True, range(nb))
+        # the last hidden layer's activations (tangent: their tangents) as bf16 operands: step s, lane group q: features
+        # 32 s + 16 t + 4 q + r
         for b in range(nb):
-            F += [f'    mh_f4 acc{b}[{NO}][{ncf}];']
-            F += [f'    acc{b}[{o}][{jj}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO) for jj in range(ncf)]
-        for st in range(S):
-            for o in range(NO):
-                F += [f'    mh_bf8 a{st}_{o}[3];']
-                F += [f'    a{st}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * CH * RSF} + ({16 * o} + c16) '
-                      f'* {RSF} + {32 * st} + 8 * q]);' for p in range(3)]
-            for k, (pa, pb) in enumerate(PAIRS):
+            hl = f'ht{nh - 1}_{b}' if tangent else f'h{nh - 1}_{b}'
+            F += [f'  mh_bf8 hb{b}[{S}][3];']
+            for st in range(S):
+                F += [f'  {{ const float v[8] = {{{", ".join(f"{hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
+                      f'    mh_split8(v, hb{b}[{st}]); }}']
+        # weight chunks in flight: register set j holds chunk c + PD while chunk c is multiplied (the loop is unrolled PD
+        # times so the sets have fixed names; chunks past the last, when PD does not divide the count, are computed from
+        # the last chunk's weights and not stored)
+        PD = PREFETCH
+        NCHP = -(-NCHK // PD) * PD
+        npre = -(-(NSPLIT * CH * HL // 8) // BLOCK)
+        for j in range(PD):
+            F += [f'  mh_u4 {", ".join(f"pre{j}_{i}" for i in range(npre))};']
+            F += chunk_io('Wl', f'{min(j, NCHK - 1) * NSPLIT * CH * HL}', HL, RSF, CH, '  ', reg=f'pre{j}_')[0]
+        F += ['  __syncthreads();                                // every wave is done with the hidden weights']
+        F += chunk_io('Wl', 0, HL, RSF, CH, '  ', store_base='0', reg='pre0_')[0] + ['  __syncthreads();']
+        F += [f'  for (int ch = 0; ch < {NCHP}; ch += {PD}) {{']
+        for j in range(PD):
+            c = f'(ch + {j})' if j else 'ch'
+            F += ['  {',
+                  f'    const int c = {c}, base = (c & 1) * {Lo["chunk_fwd"]}, nbase = {Lo["chunk_fwd"]} - base;',
+                  f'    const size_t nx = (size_t)min(c + {PD}, {NCHK - 1}) * {NSPLIT * CH * HL};']
+            F += chunk_io('Wl', 'nx', HL, RSF, CH, '    ', reg=f'pre{j}_')[0]
+            F += ['    __builtin_amdgcn_sched_barrier(0);            // the loads go out before the MFMAs']
+            for b in range(nb):
+                F += [f'    mh_f4 acc{b}[{NO}][{ncf}];']
+                F += [f'    acc{b}[{o}][{jj}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(NO) for jj in range(ncf)]
+            for st in range(S):
                 for o in range(NO):
-                    for b in range(nb):
-                        a = f'acc{b}[{o}][{k % ncf}]'
-                        F.append(f'    {a} = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{st}_{o}[{pa}], hb{b}[{st}][{pb}], '
-                                 f'{a}, 0, 0, 0);')
-        # chunk c + 1 goes to LDS before chunk c's results go out: vmcnt counts loads and stores in issue order, so
-        # waiting for the prefetch then never waits for stores (they drain during the next chunk's MFMAs)
-        F += chunk_io('Wl', 0, HL, RSF, CH, '    ', store_base='nbase', reg=f'pre{(j + 1) % PD}_')[0]
-        F += ['    __builtin_amdgcn_sched_barrier(0);']
-        for b in range(nb):
-            F.append(f'    if (live{b}{f" && c < {NCHK}" if NCHP > NCHK else ""}) {{')
-            for o in range(NO):
-                guard = f'if (c < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
-                val = ' + '.join(f'acc{b}[{o}][{jj}]' for jj in range(ncf))
-                F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + ej{b} * {NW} + c * {CH} + {16 * o} + 4 * q) = {val};']
-            F += ['    }']
-        F += ['    __syncthreads();', '  }']
-    F += ['  }', '}', '']
-    L += F
+                    F += [f'    mh_bf8 a{st}_{o}[3];']
+                    F += [f'    a{st}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * CH * RSF} + ({16 * o} + c16) '
+                          f'* {RSF} + {32 * st} + 8 * q]);' for p in range(3)]
+                for k, (pa, pb) in enumerate(PAIRS):
+                    for o in range(NO):
+                        for b in range(nb):
+                            a = f'acc{b}[{o}][{k % ncf}]'
+                            F.append(f'    {a} = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{st}_{o}[{pa}], hb{b}[{st}][{pb}], '
+                                     f'{a}, 0, 0, 0);')
+            # chunk c + 1 goes to LDS before chunk c's results go out: vmcnt counts loads and stores in issue order, so
+            # waiting for the prefetch then never waits for stores (they drain during the next chunk's MFMAs)
+            F += chunk_io('Wl', 0, HL, RSF, CH, '    ', store_base='nbase', reg=f'pre{(j + 1) % PD}_')[0]
+            F += ['    __builtin_amdgcn_sched_barrier(0);']
+            for b in range(nb):
+                F.append(f'    if (live{b}{f" && c < {NCHK}" if NCHP > NCHK else ""}) {{')
+                for o in range(NO):
+                    guard = f'if (c < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
+                    val = ' + '.join(f'acc{b}[{o}][{jj}]' for jj in range(ncf))
+                    F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + ej{b} * {NW} + c * {CH} + {16 * o} + 4 * q) = {val};']
+                F += ['    }']
+            F += ['    __syncthreads();', '  }']
+        F += ['  }', '}', '']
+        return F
 
-    def walk_back(grp, cur):
+
+    def walk_back(grp, cur, dual=False):
         """Lines walking dL/dh_last (in ``cur``{b}) back through the hidden layers (recomputed z's in scope) to
-        dL/d(edge features), stored to gef."""
+        dL/d(edge features), stored to gef.  ``dual``: the recomputed layers carry tangents zt (dL/dh_last does not):
+        the walk carries the tangent of the gradient too, g_z' = g_h' h'(z) + g_h h''(z) z', and gef receives the
+        tangent of dL/d(edge features) instead."""
         B = []
+        curt = None
         for i in range(nh - 1, -1, -1):
             T = cols[i] // 16
+            if dual:
+                nt = f'dht{i}_'
+                for b in grp:
+                    B.append(f'  mh_f4 {nt}{b}[{T}];')
+                    for o in range(T):
+                        for r in range(4):
+                            prev = f'{curt}{b}[{o}][{r}] * mlp_d1(z) + ' if curt else ''
+                            B.append(f'  {{ const float z = z{i}_{b}[{o}][{r}]; {nt}{b}[{o}][{r}] = {_lit(spec.c[i])} * '
+                                     f'({prev}{cur}{b}[{o}][{r}] * mlp_d2(z) * zt{i}_{b}[{o}][{r}]); }}')
+                curt = nt
             for b in grp:
                 for o in range(T):
                     for r in range(4):
@@ -376,21 +434,27 @@ def source(spec):
                               '  }']
             if i > 0:
                 Tp = cols[i - 1] // 16
-                nxt = f'dh{i - 1}_'
+                chains = [(cur, f'dh{i - 1}_')] + ([(curt, f'dhu{i - 1}_')] if dual else [])
                 # row j of layer i's natural weights = its input feature j: A[j][k] = W_i[j][k], one b128 per 4 steps
-                for b in grp:
-                    B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
-                    B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
+                for _, nxt in chains:
+                    for b in grp:
+                        B.append(f'  mh_f4 {nxt}{b}[{Tp}];')
+                        B += [f'  {nxt}{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(Tp)]
                 for ti in range(T):
                     for o in range(Tp):
                         B.append(f'  const mh_f4 b{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["nat"][i]} + '
                                  f'({16 * o} + c16) * {cols[i] + PAD} + {16 * ti} + 4 * q]);')
                     for r in range(4):
                         for o in range(Tp):
-                            for b in grp:
-                                B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
-                                         f'{cur}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
-                cur = nxt
+                            for src, nxt in chains:
+                                for b in grp:
+                                    B.append(f'  {nxt}{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(b{i}_{ti}_{o}[{r}], '
+                                             f'{src}{b}[{ti}][{r}], {nxt}{b}[{o}], 0, 0, 0);')
+                cur = chains[0][1]
+                if dual:
+                    curt = chains[1][1]
+        if dual:
+            cur = curt
         # dL/d(edge features): rows = the H0 inputs (one 16-row tile per 16; rows past the padded K read row 0)
         T0 = cols[0] // 16
         for o in range(-(-H0 // 16)):
@@ -411,134 +475,149 @@ def source(spec):
         return B
 
     # ------------------------------------------------------------------ backward
-    # dL/dh_last = gW Wl^T first: K = the output columns, one bf16 step of 32 per chunk (lane group q: columns
-    # 8 q .. 8 q + 7, two float4 loads of gW split into three bf16 parts); chunks of Wl [HL][CH] as bf16 rows of
-    # CH + BPAD.  Then the hidden layers recomputed from the natural-layout fp32 weights and walked back.
-    nb = NB_BWD
-    ncb = 2 if nb == 1 else 1
-    CH = CH_BWD
-    KS = CH // 32                                        # bf16 K steps per chunk
-    NCHK = -(-NW // CH)
-    TAIL = NW % CH != 0
-    B = head(spec.kname('mlp_bwd'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
-             'const unsigned short* __restrict__ Wl, const float* __restrict__ gW, float* __restrict__ gef, long long E',
-             lds_bwd, nb)
-    for b in range(nb):
-        B += [f'  mh_f4 dh{b}[{TL}][{ncb}];'] + [f'  dh{b}[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};'
-                                                for o in range(TL) for j in range(ncb)]
-    ld0, npre = chunk_io('Wl', 0, CH, RSB, HL, '  ')
-    B += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
-    # columns past NW (the zero-padded tail of the last chunk) read a valid column and are zeroed
-    gcol = (lambda c: f'min({c} + 8 * q, {NW - 8})') if TAIL else (lambda c: f'{c} + 8 * q')
-
-    def gload(dst, c, b, decl):
-        """dL/dW0 of edge tile b, columns c + 32 ks + 8 q .. + 7 for each K step ks, into dst_ks_{0,1}"""
-        P = []
-        for ks in range(KS):
-            col = gcol(f'{c} + {32 * ks}')
-            P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col});',
-                  f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col} + 4);']
-        return P
-    # dL/dW0 of chunk ch + d sits in g{d}_* (d = 0 .. GW_DIST - 1) while chunk ch is multiplied
-    for b in range(nb):
-        for d in range(GW_DIST):
-            B += gload(f'g{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
-    st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0')
-    B += st0 + ['  __syncthreads();']
-    B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
-          f'    const int base = (ch & 1) * {Lo["chunk_bwd"]}, nbase = {Lo["chunk_bwd"]} - base;',
-          f'    const int nc = min(ch + 1, {NCHK - 1});',
-          f'    const size_t nx = (size_t)nc * {NSPLIT * HL * CH};']
-    ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ')
-    B += ldn
-    B += [f'    const int gc = min(ch + {GW_DIST}, {NCHK - 1}) * {CH};']
-    for b in range(nb):
-        B += gload('gn', 'gc', b, '    const mh_f4 ')
-    B += ['    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
-    for ks in range(KS):
+    def bwd_kernel(name, dual):
+        """The backward (``dual``: the Hessian-vector product along ev)."""
+        # dL/dh_last = gW Wl^T first: K = the output columns, one bf16 step of 32 per chunk (lane group q: columns
+        # 8 q .. 8 q + 7, two float4 loads of gW split into three bf16 parts); chunks of Wl [HL][CH] as bf16 rows of
+        # CH + BPAD.  Then the hidden layers recomputed from the natural-layout fp32 weights and walked back.
+        nb = NB_BWD
+        ncb = 2 if nb == 1 else 1
+        CH = CH_BWD
+        KS = CH // 32                                        # bf16 K steps per chunk
+        NCHK = -(-NW // CH)
+        TAIL = NW % CH != 0
+        B = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if dual else '') +
+                 'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, const float* __restrict__ gW, '
+                 'float* __restrict__ gef, long long E', lds_bwd, nb)
         for b in range(nb):
-            v = f'g0_{ks}'
-            zero = (f' if (ch * {CH} + {32 * ks} + 8 * q >= {NW}) {{ {v}_0_{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}}; '
-                    f'{v}_1_{b} = {v}_0_{b}; }}' if TAIL else '')
-            B += [f'    mh_bf8 gb{ks}_{b}[3];' + zero,
-                  f'    {{ const float v[8] = {{{", ".join(f"{v}_{h}_{b}[{i}]" for h in range(2) for i in range(4))}}}; '
-                  f'mh_split8(v, gb{ks}_{b}); }}']
-        for o in range(TL):
-            B += [f'    mh_bf8 a{ks}_{o}[3];']
-            B += [f'    a{ks}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * HL * RSB} + ({16 * o} + c16) * '
-                  f'{RSB} + {32 * ks} + 8 * q]);' for p in range(3)]
-        for k, (pa, pb) in enumerate(PAIRS):
-            for o in range(TL):
-                for b in range(nb):
-                    c = f'dh{b}[{o}][{k % ncb}]'
-                    B.append(f'    {c} = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{ks}_{o}[{pa}], gb{ks}_{b}[{pb}], {c}, '
-                             '0, 0, 0);')
-    for b in range(nb):
-        for ks in range(KS):
-            for h in range(2):
-                for d in range(GW_DIST - 1):
-                    B += [f'    g{d}_{ks}_{h}_{b} = g{d + 1}_{ks}_{h}_{b};']
-                B += [f'    g{GW_DIST - 1}_{ks}_{h}_{b} = gn_{ks}_{h}_{b};']
-    stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase')
-    B += stn + ['    __syncthreads();', '  }']
-    for b in range(nb):
-        B += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = ' + ' + '.join(f'dh{b}[{o}][{j}]' for j in range(ncb)) + ';'
-                                           for o in range(TL)]
-    # the hidden layers recomputed and walked back HIDDEN_TILES_BWD edge tiles at a time (each group in a scope of
-    # its own, so the registers of its activations are free for the next)
-    B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();']
-    for g0 in range(0, nb, HIDDEN_TILES_BWD):
-        grp = range(g0, min(nb, g0 + HIDDEN_TILES_BWD))
-        B += ['  {'] + xin(grp) + hidden_fwd(False, False, grp)
-        B += walk_back(grp, 'dhs_')
-        B += ['  }', '  __builtin_amdgcn_sched_barrier(0);       // one group finished before the next starts']
-    B += ['}', '']
-    L += B
+            B += [f'  mh_f4 dh{b}[{TL}][{ncb}];'] + [f'  dh{b}[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};'
+                                                    for o in range(TL) for j in range(ncb)]
+        ld0, npre = chunk_io('Wl', 0, CH, RSB, HL, '  ')
+        B += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
+        # columns past NW (the zero-padded tail of the last chunk) read a valid column and are zeroed
+        gcol = (lambda c: f'min({c} + 8 * q, {NW - 8})') if TAIL else (lambda c: f'{c} + 8 * q')
 
-    # ------------------------------------------------------------------ hidden layers only (fused convolution)
-    # mlp_hid: cutoff * the last hidden activations, c h, as the fused convolution's MFMA operand: for each K step s
-    # of 32 and lane group q, the eight values at K positions 8 q .. 8 q + 7 (features 32 s + 16 t + 4 q + r, the
-    # _kperm order, which is this lane's own MFMA result layout) split exactly into three bf16 parts:
-    # hc [E][S][3][4][8] uint16.  mlp_hidb: from the sum of the convolution's partial dL/d(c h) (np_ slices
-    # [E, HL] in natural feature order, summed in order), dL/dcutoff = sum_j P h and dL/d(edge features) through the
-    # hidden layers with dL/dh = c P
-    H = head(spec.kname('mlp_hid'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
-             'const float* __restrict__ cutv, unsigned short* __restrict__ hc, long long E', Lo['tr_size'], NB_FWD)
-    H += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(NB_FWD)) + hidden_fwd(True, True, range(NB_FWD))
-    for b in range(NB_FWD):
-        hl = f'h{nh - 1}_{b}'
-        H += [f'  if (live{b}) {{', f'    const float cb = cutv[ej{b}];']
-        for st in range(S):
-            H += [f'    {{ const float v[8] = {{{", ".join(f"cb * {hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
-                  '      mh_bf8 sp[3];',
-                  '      mh_split8(v, sp);',
-                  f'      mh_bf8* __restrict__ dst = reinterpret_cast<mh_bf8*>(hc) + (ej{b} * {S} + {st}) * 12 + q;']
-            H += [f'      dst[{4 * p}] = sp[{p}];' for p in range(3)]
-            H += ['    }']
-        H.append('  }')
-    L += H + ['}', '']
-    grp = range(NB_BWD)
-    H = head(spec.kname('mlp_hidb'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
-             'const float* __restrict__ gp, int np_, const float* __restrict__ cutv, float* __restrict__ gef, '
-             'float* __restrict__ gcut, long long E', Lo['nat_size'], NB_BWD)
-    H += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin(grp) + hidden_fwd(False, False, grp)
-    for b in grp:
-        H += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
-        H += ['  for (int pp = 0; pp < np_; ++pp) {',
-              f'    const float* __restrict__ gr = gp + ((size_t)pp * E + ejc{b}) * {HL} + 4 * q;']
-        H += [f'    dhs_{b}[{o}] += *reinterpret_cast<const mh_f4*>(gr + {16 * o});' for o in range(TL)]
-        H += ['  }', '  {', '    float gc = 0.f;']
-        for o in range(TL):
-            for r in range(4):
-                H.append(f'    {{ const float z = z{nh - 1}_{b}[{o}][{r}]; '
-                         f'gc = fmaf(dhs_{b}[{o}][{r}], {_lit(spec.c[nh - 1])} * z * mlp_sig(z), gc); }}')
-        H += ['    gc += __shfl_xor(gc, 16, 64);', '    gc += __shfl_xor(gc, 32, 64);',
-              f'    if (live{b} && q == 0) gcut[ej{b}] = gc;',
-              f'    const float cb = cutv[ejc{b}];']
-        H += [f'    dhs_{b}[{o}] *= cb;' for o in range(TL)]
-        H += ['  }']
-    H += walk_back(grp, 'dhs_')
-    L += H + ['}', '']
+        def gload(dst, c, b, decl):
+            """dL/dW0 of edge tile b, columns c + 32 ks + 8 q .. + 7 for each K step ks, into dst_ks_{0,1}"""
+            P = []
+            for ks in range(KS):
+                col = gcol(f'{c} + {32 * ks}')
+                P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col});',
+                      f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col} + 4);']
+            return P
+        # dL/dW0 of chunk ch + d sits in g{d}_* (d = 0 .. GW_DIST - 1) while chunk ch is multiplied
+        for b in range(nb):
+            for d in range(GW_DIST):
+                B += gload(f'g{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
+        st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0')
+        B += st0 + ['  __syncthreads();']
+        B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
+              f'    const int base = (ch & 1) * {Lo["chunk_bwd"]}, nbase = {Lo["chunk_bwd"]} - base;',
+              f'    const int nc = min(ch + 1, {NCHK - 1});',
+              f'    const size_t nx = (size_t)nc * {NSPLIT * HL * CH};']
+        ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ')
+        B += ldn
+        B += [f'    const int gc = min(ch + {GW_DIST}, {NCHK - 1}) * {CH};']
+        for b in range(nb):
+            B += gload('gn', 'gc', b, '    const mh_f4 ')
+        B += ['    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
+        for ks in range(KS):
+            for b in range(nb):
+                v = f'g0_{ks}'
+                zero = (f' if (ch * {CH} + {32 * ks} + 8 * q >= {NW}) {{ {v}_0_{b} = mh_f4{{0.f, 0.f, 0.f, 0.f}}; '
+                        f'{v}_1_{b} = {v}_0_{b}; }}' if TAIL else '')
+                B += [f'    mh_bf8 gb{ks}_{b}[3];' + zero,
+                      f'    {{ const float v[8] = {{{", ".join(f"{v}_{h}_{b}[{i}]" for h in range(2) for i in range(4))}}}; '
+                      f'mh_split8(v, gb{ks}_{b}); }}']
+            for o in range(TL):
+                B += [f'    mh_bf8 a{ks}_{o}[3];']
+                B += [f'    a{ks}_{o}[{p}] = *reinterpret_cast<const mh_bf8*>(&ldsb[base + {p * HL * RSB} + ({16 * o} + c16) * '
+                      f'{RSB} + {32 * ks} + 8 * q]);' for p in range(3)]
+            for k, (pa, pb) in enumerate(PAIRS):
+                for o in range(TL):
+                    for b in range(nb):
+                        c = f'dh{b}[{o}][{k % ncb}]'
+                        B.append(f'    {c} = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{ks}_{o}[{pa}], gb{ks}_{b}[{pb}], {c}, '
+                                 '0, 0, 0);')
+        for b in range(nb):
+            for ks in range(KS):
+                for h in range(2):
+                    for d in range(GW_DIST - 1):
+                        B += [f'    g{d}_{ks}_{h}_{b} = g{d + 1}_{ks}_{h}_{b};']
+                    B += [f'    g{GW_DIST - 1}_{ks}_{h}_{b} = gn_{ks}_{h}_{b};']
+        stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase')
+        B += stn + ['    __syncthreads();', '  }']
+        for b in range(nb):
+            B += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = ' + ' + '.join(f'dh{b}[{o}][{j}]' for j in range(ncb)) + ';'
+                                               for o in range(TL)]
+        # the hidden layers recomputed and walked back HIDDEN_TILES_BWD edge tiles at a time (each group in a scope of
+        # its own, so the registers of its activations are free for the next)
+        B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();']
+        for g0 in range(0, nb, HIDDEN_TILES_BWD):
+            grp = range(g0, min(nb, g0 + HIDDEN_TILES_BWD))
+            B += ['  {'] + xin(grp)
+            if dual:
+                B += xin(grp, 'ev', 'xv') + hidden_fwd(False, False, grp, dual=True)
+            else:
+                B += hidden_fwd(False, False, grp)
+            B += walk_back(grp, 'dhs_', dual=dual)
+            B += ['  }', '  __builtin_amdgcn_sched_barrier(0);       // one group finished before the next starts']
+        B += ['}', '']
+        return B
+
+    def hidden_only():
+        """mlp_hid / mlp_hidb, the fused convolution's MLP kernels."""
+
+        # ------------------------------------------------------------------ hidden layers only (fused convolution)
+        # mlp_hid: cutoff * the last hidden activations, c h, as the fused convolution's MFMA operand: for each K step s
+        # of 32 and lane group q, the eight values at K positions 8 q .. 8 q + 7 (features 32 s + 16 t + 4 q + r, the
+        # _kperm order, which is this lane's own MFMA result layout) split exactly into three bf16 parts:
+        # hc [E][S][3][4][8] uint16.  mlp_hidb: from the sum of the convolution's partial dL/d(c h) (np_ slices
+        # [E, HL] in natural feature order, summed in order), dL/dcutoff = sum_j P h and dL/d(edge features) through the
+        # hidden layers with dL/dh = c P
+        H = head(spec.kname('mlp_hid'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
+                 'const float* __restrict__ cutv, unsigned short* __restrict__ hc, long long E', Lo['tr_size'], NB_FWD)
+        H += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(NB_FWD)) + hidden_fwd(True, True, range(NB_FWD))
+        for b in range(NB_FWD):
+            hl = f'h{nh - 1}_{b}'
+            H += [f'  if (live{b}) {{', f'    const float cb = cutv[ej{b}];']
+            for st in range(S):
+                H += [f'    {{ const float v[8] = {{{", ".join(f"cb * {hl}[{2 * st + tt}][{r}]" for tt in range(2) for r in range(4))}}};',
+                      '      mh_bf8 sp[3];',
+                      '      mh_split8(v, sp);',
+                      f'      mh_bf8* __restrict__ dst = reinterpret_cast<mh_bf8*>(hc) + (ej{b} * {S} + {st}) * 12 + q;']
+                H += [f'      dst[{4 * p}] = sp[{p}];' for p in range(3)]
+                H += ['    }']
+            H.append('  }')
+        L.extend(H + ['}', ''])
+        grp = range(NB_BWD)
+        H = head(spec.kname('mlp_hidb'), 'const float* __restrict__ ef, const float* __restrict__ Wh, '
+                 'const float* __restrict__ gp, int np_, const float* __restrict__ cutv, float* __restrict__ gef, '
+                 'float* __restrict__ gcut, long long E', Lo['nat_size'], NB_BWD)
+        H += stage('Wh', Lo['nat_size']) + ['  __syncthreads();'] + xin(grp) + hidden_fwd(False, False, grp)
+        for b in grp:
+            H += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for o in range(TL)]
+            H += ['  for (int pp = 0; pp < np_; ++pp) {',
+                  f'    const float* __restrict__ gr = gp + ((size_t)pp * E + ejc{b}) * {HL} + 4 * q;']
+            H += [f'    dhs_{b}[{o}] += *reinterpret_cast<const mh_f4*>(gr + {16 * o});' for o in range(TL)]
+            H += ['  }', '  {', '    float gc = 0.f;']
+            for o in range(TL):
+                for r in range(4):
+                    H.append(f'    {{ const float z = z{nh - 1}_{b}[{o}][{r}]; '
+                             f'gc = fmaf(dhs_{b}[{o}][{r}], {_lit(spec.c[nh - 1])} * z * mlp_sig(z), gc); }}')
+            H += ['    gc += __shfl_xor(gc, 16, 64);', '    gc += __shfl_xor(gc, 32, 64);',
+                  f'    if (live{b} && q == 0) gcut[ej{b}] = gc;',
+                  f'    const float cb = cutv[ejc{b}];']
+            H += [f'    dhs_{b}[{o}] *= cb;' for o in range(TL)]
+            H += ['  }']
+        H += walk_back(grp, 'dhs_')
+        L.extend(H + ['}', ''])
+
+    if second:
+        L += fwd_kernel(spec.kname('mlp_jvp'), True) + bwd_kernel(spec.kname('mlp_bwd2'), True)
+    else:
+        L += fwd_kernel(spec.kname('mlp_fwd'), False) + bwd_kernel(spec.kname('mlp_bwd'), False)
+        hidden_only()
     return '\n'.join(L)
 
 

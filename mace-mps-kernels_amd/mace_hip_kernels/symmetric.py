@@ -22,7 +22,7 @@ import numpy as np
 import scipy.sparse
 import torch
 
-from . import _native
+from . import _native, species
 
 WAVE = 64
 LOADS_PER_FENCE = 32
@@ -714,54 +714,37 @@ _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. 
                     'autograd Hessian) is not enabled for this HIP module; patch with '
                     'patch_model(model, double_backward=True)')
 
-_elem_cache = []          # [(weakref(node_attrs), version, (elem int32, order int32))], most recent first
+_elem_cache = []          # [(weakref(node_attrs), version, (elem, order, slots) int32)], most recent first
 _SIMDS = {}               # device index -> SIMD count (4 per compute unit)
+
+
+def _species(node_attrs):
+    """(elem, order, slots) of a node_attrs tensor (``species.species_order``, one launch), cached per tensor."""
+    ver = node_attrs._version
+    for ref, v, eos in _elem_cache:
+        if ref() is node_attrs and v == ver:
+            return _native.hold_for_capture(eos)
+    eos = species.species_order(node_attrs, SLOT_GROUP)
+    if _native.capturing():
+        return eos             # recomputed by every replay; its memory only holds values once the graph runs
+    _elem_cache.insert(0, (weakref.ref(node_attrs), ver, eos))
+    del _elem_cache[4:]
+    return eos
 
 
 def element_order(node_attrs):
     """(elem, order): the argmax of the one-hot node attributes as int32 (reference symmetric.py:169) and the node
     indices stably sorted by element, which the grouped kernels walk.  Cached per node_attrs tensor."""
-    ver = node_attrs._version
-    for i, (ref, v, eo) in enumerate(_elem_cache):
-        if ref() is node_attrs and v == ver:
-            return _native.hold_for_capture(eo)
-    elem = torch.argmax(node_attrs, dim=1).to(torch.int32).contiguous()
-    order = torch.argsort(elem, stable=True).to(torch.int32).contiguous()
-    if _native.capturing():
-        return elem, order     # recomputed by every replay; its memory only holds values once the graph runs
-    _elem_cache.insert(0, (weakref.ref(node_attrs), ver, (elem, order)))
-    del _elem_cache[4:]
+    elem, order, _ = _species(node_attrs)
     return elem, order
-
-
-_slot_cache = []          # [(weakref(node_attrs), version, slots int32)], most recent first
 
 
 def group_slots(node_attrs):
     """Node slots of the staged kernels: the element-sorted node order with every element's run padded with -1 to a
     multiple of SLOT_GROUP, so that each workgroup's SLOT_GROUP slots hold nodes of one element, and -1 up to the
     fixed length ceil(N / SLOT_GROUP) SLOT_GROUP + n_elem SLOT_GROUP (an upper bound for any element mix, so the
-    launch size needs no device-to-host copy).  Device ops only; cached per node_attrs tensor."""
-    ver = node_attrs._version
-    for ref, v, sl in _slot_cache:
-        if ref() is node_attrs and v == ver:
-            return _native.hold_for_capture(sl)
-    elem, order = element_order(node_attrs)
-    n, ne, gs = elem.numel(), node_attrs.shape[1], SLOT_GROUP
-    dev = elem.device
-    el = elem.long()
-    cnt = torch.zeros(ne, dtype=torch.int64, device=dev).scatter_add_(0, el, torch.ones_like(el))
-    run = (cnt + gs - 1) // gs * gs
-    start, pstart = torch.cumsum(cnt, 0) - cnt, torch.cumsum(run, 0) - run
-    es = el[order.long()]                                   # element of each sorted position
-    pos = pstart[es] + torch.arange(n, device=dev) - start[es]
-    slots = torch.full((-(-n // gs) * gs + ne * gs,), -1, dtype=torch.int32, device=dev)
-    slots.scatter_(0, pos, order)
-    if _native.capturing():
-        return slots
-    _slot_cache.insert(0, (weakref.ref(node_attrs), ver, slots))
-    del _slot_cache[4:]
-    return slots
+    launch size needs no device-to-host copy).  Cached per node_attrs tensor, computed with element_order."""
+    return _species(node_attrs)[2]
 
 
 def element_index(node_attrs):

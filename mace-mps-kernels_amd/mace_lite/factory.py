@@ -65,31 +65,26 @@ def pt_slab_with_adsorbates(rng, size, n_ads, sigma=0.05, vacuum=12.0, min_dist=
 
 
 # ------------------------------------------------------------------------------------------------- workloads
-def workload(cfg, seed=0, dtype=torch.float32, device='cpu'):
-    """(model, batch, meta) for BASELINE configuration ``cfg`` (0–4)."""
+def structures(cfg, seed=0):
+    """The structures of BASELINE configuration ``cfg`` (0-4) and how they are batched: dict(structures, r_max,
+    pad_edges_to (None: exact graphs), elements (the one-hot table), name, extra meta)."""
     rng = np.random.default_rng(1000 + seed)
     if cfg == 0:
-        model = make_model('32x0e+32x1o', 2, 2, elements=ELEMENTS_PTCOH, dtype=dtype)
         s = pt_slab_with_adsorbates(rng, (4, 4, 4), 15)
-        graphs = [D.graph_of(s, 5.0)]
-        batch = D.batch_graphs(graphs, ELEMENTS_PTCOH, dtype, device)
-        return model, batch, dict(name='cfg0_32ch_l2c2_79atoms', r_max=5.0)
-    if cfg in (1, 2):
-        model = make_model('128x0e+128x1o', 3, 3, elements=ELEMENTS_PTCOH, dtype=dtype)
-        if cfg == 1:
-            s = pt_slab_with_adsorbates(rng, (5, 5, 5), 35)
-            batch = D.batch_graphs([D.graph_of(s, 5.0)], ELEMENTS_PTCOH, dtype, device)
-            return model, batch, dict(name='cfg1_128ch_l3c3_160atoms', r_max=5.0)
+        return dict(structures=[s], r_max=5.0, pad_edges_to=None, elements=ELEMENTS_PTCOH,
+                    name='cfg0_32ch_l2c2_79atoms', meta={})
+    if cfg == 1:
+        s = pt_slab_with_adsorbates(rng, (5, 5, 5), 35)
+        return dict(structures=[s], r_max=5.0, pad_edges_to=None, elements=ELEMENTS_PTCOH,
+                    name='cfg1_128ch_l3c3_160atoms', meta={})
+    if cfg == 2:
         # 6x5x4 Pt block (120 atoms) with 20-61 adsorbates on both faces: 4.3k-5.9k edges per slab (mean ~5k), so
         # every graph fits the fixed 6,000-edge padding
         counts = rng.integers(140, 182, size=16)
-        graphs = [D.graph_of(pt_slab_with_adsorbates(rng, (6, 5, 4), int(c) - 120, both_sides=True), 5.0)
-                  for c in counts]
-        batch = D.batch_graphs(graphs, ELEMENTS_PTCOH, dtype, device, pad_edges_to=6000, r_max=5.0)
-        return model, batch, dict(name='cfg2_128ch_l3c3_batch16_pad6000', r_max=5.0, atom_counts=counts.tolist())
+        structs = [pt_slab_with_adsorbates(rng, (6, 5, 4), int(c) - 120, both_sides=True) for c in counts]
+        return dict(structures=structs, r_max=5.0, pad_edges_to=6000, elements=ELEMENTS_PTCOH,
+                    name='cfg2_128ch_l3c3_batch16_pad6000', meta=dict(atom_counts=counts.tolist()))
     if cfg == 3:
-        elements = list(range(1, 90))
-        model = make_model('128x0e+128x1o', 3, 3, r_max=6.0, elements=elements, dtype=dtype)
         mols = [D.MOLECULES[k] for k in ('CO', 'OH', 'NH', 'H')]
         slabs = [
             D.cubic_crystal(D.fcc_basis('Au'), 4.08, (3, 3, 2), vacuum=12.0, pbc=(True, True, False)),
@@ -103,13 +98,30 @@ def workload(cfg, seed=0, dtype=torch.float32, device='cpu'):
         ]
         structs = [D.jitter(D.add_molecules(s, rng, int(rng.integers(3, 8)), mols, min_dist=1.4), rng, 0.03)
                    for s in slabs]
-        graphs = [D.graph_of(s, 6.0) for s in structs]
-        batch = D.batch_graphs(graphs, elements, dtype, device)
-        return model, batch, dict(name='cfg3_89elem_128ch_l3c3_8slabs', r_max=6.0,
-                                  atom_counts=[len(s) for s in structs])
+        return dict(structures=structs, r_max=6.0, pad_edges_to=None, elements=list(range(1, 90)),
+                    name='cfg3_89elem_128ch_l3c3_8slabs', meta=dict(atom_counts=[len(s) for s in structs]))
     if cfg == 4:
-        model = make_model('128x0e+128x1o+128x2e', 3, 3, elements=ELEMENTS_PTCOH, dtype=dtype)
         s = D.jitter(D.cubic_crystal(D.fcc_basis('Pt'), 3.92, (25, 25, 8)), rng, 0.08)
-        batch = D.batch_graphs([D.graph_of(s, 5.0)], ELEMENTS_PTCOH, dtype, device)
-        return model, batch, dict(name='cfg4_bulkPt_20000atoms', r_max=5.0)
+        return dict(structures=[s], r_max=5.0, pad_edges_to=None, elements=ELEMENTS_PTCOH,
+                    name='cfg4_bulkPt_20000atoms', meta={})
     raise ValueError(cfg)
+
+
+def batch_of(st, dtype=torch.float32, device='cpu'):
+    """MACE batch dict of a ``structures`` record (host neighbour lists, the configuration's padding)."""
+    graphs = [D.graph_of(s, st['r_max']) for s in st['structures']]
+    return D.batch_graphs(graphs, st['elements'], dtype, device, pad_edges_to=st['pad_edges_to'], r_max=st['r_max'])
+
+
+def workload(cfg, seed=0, dtype=torch.float32, device='cpu'):
+    """(model, batch, meta) for BASELINE configuration ``cfg`` (0-4)."""
+    st = structures(cfg, seed)
+    if cfg == 0:
+        model = make_model('32x0e+32x1o', 2, 2, elements=ELEMENTS_PTCOH, dtype=dtype)
+    elif cfg in (1, 2):
+        model = make_model('128x0e+128x1o', 3, 3, elements=ELEMENTS_PTCOH, dtype=dtype)
+    elif cfg == 3:
+        model = make_model('128x0e+128x1o', 3, 3, r_max=6.0, elements=list(range(1, 90)), dtype=dtype)
+    else:
+        model = make_model('128x0e+128x1o+128x2e', 3, 3, elements=ELEMENTS_PTCOH, dtype=dtype)
+    return model, batch_of(st, dtype, device), dict(name=st['name'], r_max=st['r_max'], **st['meta'])

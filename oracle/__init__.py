@@ -14,6 +14,8 @@ Modules and what each restates (reference file:line):
                 144-176 d/dx, 179-222 d/dW and d/dY), plus the CSR builder (conv.py:229-235).
   * ``sc``      the symmetric contraction: dense Σ_ν U_ν·W_ν·x^⊗ν evaluation (the math of symmetric.py:1-13), the
                 symmetrised polynomial table (symmetric.py:20-75) and its evaluation/derivative (symmetric.py:82-131).
+  * ``neighbours`` the graph the convolution's CSRs are built from (conv.py:229-235): the periodic neighbour list in
+                MACE's edge convention and the fixed-size padded layout the reference recommends (README.md:77-78).
 
 Which check pins which function is listed in each module's docstring.
 """

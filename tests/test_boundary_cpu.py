@@ -34,7 +34,7 @@ def test_library_loads_and_exports_header_symbols():
 
 _CTYPE_OF = {
     'int': ctypes.c_int, 'int32_t': ctypes.c_int32, 'int64_t': ctypes.c_int64, 'size_t': ctypes.c_size_t,
-    'float': ctypes.c_float,
+    'float': ctypes.c_float, 'double': ctypes.c_double,
 }
 
 
@@ -69,6 +69,7 @@ def test_ctypes_signatures_match_the_header():
             else:
                 assert ctypes.sizeof(ct) == ctypes.sizeof(_CTYPE_OF[c]), (name, i, ct, c)
                 assert (ct is ctypes.c_float) == (c == 'float'), (name, i, ct, c)
+                assert (ct is ctypes.c_double) == (c == 'double'), (name, i, ct, c)
 
 
 def test_launch_log_is_off_by_default_and_clears():
@@ -167,7 +168,10 @@ def _oracle_build(edge_index, n):
 
 
 def test_graph_cache_and_validation(monkeypatch):
+    """Cache and out-of-range report (the synchronous check; the deferred one reads a pinned copy of the flag behind
+    a HIP event and is covered on the GPU, tests/test_neighbours_gpu.py)."""
     monkeypatch.setattr(conv, 'build_graph', _oracle_build)
+    monkeypatch.setattr(conv, 'GRAPH_CHECK', 'sync')
     conv.clear_graph_cache()
     ei = torch.tensor([[0, 1, 2, 2], [1, 2, 0, 1]])
     g1 = conv.graph_for(ei, 3)
@@ -188,6 +192,50 @@ def test_graph_cache_and_validation(monkeypatch):
 
 def test_graph_build_source_compiles():
     assert _native.compile_source(conv.graph_source())[:4] == b'\x7fELF'
+
+
+def test_neighbour_and_species_sources_compile():
+    from mace_hip_kernels import neighbours, species
+    assert _native.compile_source(neighbours.source())[:4] == b'\x7fELF'
+    assert _native.compile_source(species.source())[:4] == b'\x7fELF'
+
+
+def test_neighbour_list_work_size_and_argument_checks():
+    """The scratch layout grows with atoms, structures and edges; bad arguments fail before any launch."""
+    lib = _native.load()
+    a, b = lib.mh_neighbour_list_work_size(1, 100, 0), lib.mh_neighbour_list_work_size(1, 100, 5000)
+    assert 0 < a < b and b - a >= 8 * 5000 and lib.mh_neighbour_list_work_size(-1, 0, 0) == 0
+    cases = [
+        ((None, None, None, None, None, 2, 10, 5.0, 100, 150, None, None, None, 0, None, None, None), 'B \\* e_pad'),
+        ((None, None, None, None, None, 2, 10, -1.0, 0, 0, None, None, None, 0, None, None, None), 'r_max'),
+        ((None, None, None, None, None, 2, 10, 5.0, 0, 0, None, None, None, 0, None, None, None), 'NULL'),
+        ((None, None, None, None, None, -1, 10, 5.0, 0, 0, None, None, None, 0, None, None, None), 'bad sizes'),
+    ]
+    for args, msg in cases:
+        assert lib.mh_neighbour_list(*args) != 0
+        assert re.search(msg, lib.mh_last_error().decode()), lib.mh_last_error()
+    assert lib.mh_species_order(None, None, 10, 200, None, None, None, 0, 8, None) != 0
+    assert b'ne <=' in lib.mh_last_error()
+    assert lib.mh_species_order(None, None, 10, 4, None, None, None, 8, 8, None) != 0
+    assert b'nslots' in lib.mh_last_error()
+
+
+def test_species_order_fallback_on_large_tables():
+    """More elements than the kernel's LDS tables: the torch expressions (they run on the CPU too)."""
+    from mace_hip_kernels import species
+    rng = np.random.default_rng(0)
+    n, ne, group = 300, 150, 8
+    idx = rng.integers(0, ne, n)
+    a = torch.zeros(n, ne)
+    a[torch.arange(n), torch.from_numpy(idx)] = 1.0
+    elem, order, slots = species.species_order(a, group)
+    assert torch.equal(elem.long(), torch.from_numpy(idx)) and torch.equal(order.long(), torch.argsort(elem, stable=True))
+    assert slots.numel() == species.slot_count(n, ne, group)
+    live = slots[slots >= 0]
+    assert torch.equal(live, order)                               # the runs in element order, -1 between them
+    starts = (torch.nonzero(slots >= 0).reshape(-1))
+    run_elem = elem[slots[starts].long()]
+    assert bool((starts[1:][run_elem[1:] != run_elem[:-1]] % group == 0).all())
 
 
 def test_golden_fixtures_reproduce():

@@ -113,12 +113,16 @@ def test_conv_bwd_without_dx(order):
     assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, W, s, r)) < CONV_TOL
 
 
+@pytest.mark.parametrize('masked', [False, True])
 @pytest.mark.parametrize('want_x', [True, False])
-def test_conv_factored_cutoff_weights(want_x):
+def test_conv_factored_cutoff_weights(want_x, masked):
     """tp_weights = W0 * cutoff (MACE's form): the backward kernel returns d/dW0 and d/dcutoff itself.  Against the
-    oracle: d/dW0 = gW * c, d/dc = sum_k gW * W0 (gW the oracle's d/dW), with some cutoffs exactly zero (padding)."""
+    oracle: d/dW0 = gW * c, d/dc = sum_k gW * W0 (gW the oracle's d/dW), with some cutoffs exactly zero (padding).
+    ``masked``: the cutoff is marked as a patched radial embedding's (-0.0 outside the envelope's support), and
+    every third edge holds -0.0: the backward skips those edges (MH_CUT_MASKED), so d/dcutoff is 0 there while
+    +0.0 edges keep the exact partial; every other gradient equals the unmasked call's."""
     dev = _dev()
-    print(f'[case] conv factored cutoff weights want_x={want_x}', flush=True)
+    print(f'[case] conv factored cutoff weights want_x={want_x} masked={masked}', flush=True)
     tp = _tp('128x0e+128x1o', 3)
     op = HipConvTP(tp, device=dev)
     desc = oconv.describe_tp(tp)
@@ -130,23 +134,48 @@ def test_conv_factored_cutoff_weights(want_x):
     c = rng.uniform(0.0, 1.0, size=(e, 1))
     c[::7] = 0.0
     c[r == 2] = 0.0                  # a receiver whose every edge is skipped by the forward
+    neg = np.zeros(e, dtype=bool)
+    if masked:
+        neg[1::3] = True
+        neg[r == 3] = True           # a receiver whose every edge is masked
+        c[neg] = -0.0
     g = rng.normal(size=(n, desc['out_dim']))
     t = lambda a, rg=True: torch.tensor(a, dtype=torch.float32, device=dev, requires_grad=rg)  # noqa: E731
-    xt, Yt, W0t, ct = t(x, want_x), t(Y), t(W0), t(c)
-    W = W0t * ct
-    assert hconv._factored_weights(W) is not None
-    out = op(xt, Yt, W, torch.tensor(np.stack([s, r]), device=dev))
-    out.backward(torch.tensor(g, dtype=torch.float32, device=dev))
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    gt = torch.tensor(g, dtype=torch.float32, device=dev)
+
+    def run(mark):
+        xt, Yt, W0t, ct = t(x, want_x), t(Y), t(W0), t(c)
+        if mark:
+            ct._mh_support_mask = ct._version
+        W = W0t * ct
+        assert hconv._factored_weights(W) is not None
+        with _native.timing() as tm:
+            out = op(xt, Yt, W, ei)
+            out.backward(gt)
+        assert tm.symbols['conv_bwd[conv]'][0].startswith('conv_bwdrc_'), tm.symbols
+        return out, xt, Yt, W0t, ct
+
+    out, xt, Yt, W0t, ct = run(masked)
+    assert (torch.signbit(ct.detach()).cpu().numpy()[:, 0] == neg).all()
     Wd = (W0.astype(np.float32) * c.astype(np.float32)).astype(np.float64)     # the fp32 product the kernel reads
     assert _rel(out.detach().double().cpu().numpy(), oconv.conv_fwd(desc, coef, x, Y, Wd, s, r, n)) < CONV_TOL
     gW = oconv.conv_bwd_w(desc, coef, x, g, Y, s, r)
     assert _rel(W0t.grad.double().cpu().numpy(), gW * c) < CONV_TOL
-    assert _rel(ct.grad.double().cpu().numpy(), (gW * W0).sum(1, keepdims=True)) < CONV_TOL
+    gc_want = (gW * W0).sum(1, keepdims=True)
+    gc_want[neg] = 0.0
+    assert _rel(ct.grad.double().cpu().numpy(), gc_want) < CONV_TOL
     assert _rel(Yt.grad.double().cpu().numpy(), oconv.conv_bwd_y(desc, coef, x, g, Wd, s, r)) < CONV_TOL
     if want_x:
         assert _rel(xt.grad.double().cpu().numpy(), oconv.conv_bwd_x(desc, coef, g, Y, Wd, s, r, n)) < CONV_TOL
     else:
         assert xt.grad is None
+    if masked:                       # the skipped edges change nothing but d/dcutoff there
+        out_u, xu, Yu, W0u, cu = run(False)
+        assert torch.equal(out, out_u) and torch.equal(Yt.grad, Yu.grad) and torch.equal(W0t.grad, W0u.grad)
+        assert torch.equal(ct.grad[~torch.from_numpy(neg).to(dev)], cu.grad[~torch.from_numpy(neg).to(dev)])
+        if want_x:
+            assert torch.equal(xt.grad, xu.grad)
 
 
 FUSED_TOL = 1e-5      # the MLP's fp32 hidden layers and the fp32-accurate output layer add ~1e-6 to the conv's error
@@ -266,7 +295,7 @@ def test_graph_build_vs_oracle():
     """Both CSRs of an edge list built on the GPU (mh_graph_build) against the oracle's stable-argsort CSR: random
     multigraphs with isolated nodes, a node with 300 edges, one node, no edges, hub nodes of 129, 5,000 and 20,000
     edges (segments past the counting kernel's limit, sorted in LDS and in global memory); bitwise the same on a
-    second run; out-of-range indices flagged (and rejected by the graph cache) or, unvalidated, clamped."""
+    second run; out-of-range indices flagged (and reported by the graph cache's check) or, unvalidated, clamped."""
     dev = _dev()
     rng = np.random.default_rng(12)
     cases = [(37, 900), (2533, 96000), (1, 5), (50, 0), (5000, 300), (3000, 60000)]
@@ -295,8 +324,10 @@ def test_graph_build_vs_oracle():
     ei = torch.tensor([[0, 1, 7, 2], [1, -1, 0, 2]], device=dev)
     keys, rowptr, eids, bad = hconv.build_graph(ei, 3)
     assert int(bad.item()) == 1 and keys.min() >= 0 and keys.max() <= 2
+    hconv.check_graphs()
+    hconv._Graph(ei, 3)                          # reported by the next check (GRAPH_CHECK 'deferred')
     with pytest.raises(ValueError, match='outside'):
-        hconv._Graph(ei, 3)
+        hconv.check_graphs()
     gr = hconv._Graph(ei, 3, validate=False)
     assert gr.send.tolist() == [0, 1, 2, 2] and gr.recv.tolist() == [1, 0, 0, 2]
     with pytest.raises(ValueError):

@@ -220,7 +220,7 @@ def test_double_backward_upgrade_and_stress_loss():
 
 
 @pytest.mark.parametrize('fuse', [False, True])
-def test_patched_model_launches_the_fast_paths(fuse):
+def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
     """The kernels an E+F call of the patched model runs, read from the C ABI's launch log (no assumption about which
     path a module takes).  Default: the factored convolution kernels (W0 * cutoff never formed: conv_fwdc,
     conv_bwdrc) after the radial MLP's kernels (mlp_fwd, mlp_bwd).  fuse_radial: the convolutions with the radial
@@ -237,9 +237,18 @@ def test_patched_model_launches_the_fast_paths(fuse):
     patch_model(met, verbose=False, fuse_radial=fuse)
     met(D.fresh(_to(batch, dev, torch.float32)), compute_force=True)          # graph and element order cached
     b = D.fresh(_to(batch, dev, torch.float32))
+    from mace_hip_kernels import conv as hconv
+    masked, first_order = [], hconv._conv_grads
+
+    def spy(*args, **kw):
+        masked.append(kw.get('masked', False))
+        return first_order(*args, **kw)
+    monkeypatch.setattr(hconv, '_conv_grads', spy)
     with _native.timing() as tm:
         met(b, compute_force=True)
     torch.cuda.synchronize()
+    # both convolutions' backward skips the edges outside the cutoff (the patched radial embedding's -0.0 marks)
+    assert masked == ([] if fuse else [True, True]), masked
     sym = {tag: names for tag, names in tm.symbols.items()}
     flat = [n for names in sym.values() for n in names]
     if fuse:
