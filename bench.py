@@ -43,26 +43,30 @@ def _to(batch, dev):
     return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
 
 
-def _time_calls(model, batch, steps, warmup, sync):
+def _time_calls(model, batch, steps, warmup, sync, **kw):
+    kw = kw or dict(compute_force=True)
     for _ in range(warmup):
-        model(batch, compute_force=True)
+        model(batch, **kw)
     sync()
     t0 = time.perf_counter()
     for _ in range(steps):
-        out = model(batch, compute_force=True)
+        out = model(batch, **kw)
     sync()
     return (time.perf_counter() - t0) / steps, out
 
 
 def _time_train(model, batch, steps, warmup, sync):
     """Seconds per force-loss step: E and F with create_graph (MACE's training=True), the loss E^2 + |F|^2, and its
-    backward into the parameters, which differentiates the force computation (a double backward)."""
+    gradient with respect to the positions, which differentiates the force computation (a double backward).  No
+    parameter gradients are formed (the patched modules hold their weights as constants), so the patched and
+    unpatched models do the same work."""
+    import torch
     from mace_lite import data as D
 
     def step():
-        model.zero_grad(set_to_none=True)
-        out = model(D.fresh(batch), compute_force=True, training=True)
-        ((out['energy'] ** 2).sum() + (out['forces'] ** 2).sum()).backward()
+        b = D.fresh(batch)
+        out = model(b, compute_force=True, training=True)
+        torch.autograd.grad((out['energy'] ** 2).sum() + (out['forces'] ** 2).sum(), b['positions'])
     for _ in range(warmup):
         step()
     sync()
@@ -151,7 +155,7 @@ def _cpu_model():
     return platform.processor() or platform.machine()
 
 
-def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
+def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, **kw):
     """Unpatched e3nn-path restatement on the host CPU over the first ``sample`` structures of the batch."""
     import torch
     from mace_lite import data as D
@@ -168,10 +172,11 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps):
         'unit_shifts': batch_cpu['unit_shifts'][keep].clone(), 'cell': batch_cpu['cell'][:3 * k].clone(),
         'batch': batch_cpu['batch'][:n_at].clone(), 'ptr': ptr[:k + 1].clone(),
     }
-    model(D.fresh(sub), compute_force=True)                      # warm-up
+    kw = kw or dict(compute_force=True)
+    model(D.fresh(sub), **kw)                                     # warm-up
     t0 = time.perf_counter()
     for _ in range(steps):
-        model(D.fresh(sub), compute_force=True)
+        model(D.fresh(sub), **kw)
     dt = (time.perf_counter() - t0) / steps
     per_call = dt * n_structs / k                                 # scaled to the full batch
     return dict(value=round(1.0 / per_call, 5), unit='E+F calls/s', cores=cores, kind='port',
@@ -393,7 +398,7 @@ def _profile(a):
         _log(f'profile run done: {meta["name"]}, {a.warmup + a.steps} force-loss steps')
         return
     for _ in range(a.warmup + a.steps):
-        met(batch, compute_force=True)
+        met(batch, compute_force=True, compute_stress=(a.config == 1))
     # calibration: an elementwise kernel whose name occurs nowhere in the model (reads and writes COPY_BYTES)
     x = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device=dev)
     y = torch.empty_like(x)
@@ -513,6 +518,7 @@ def main():
     ap.add_argument('--no-e3nn', action='store_true')
     ap.add_argument('--no-double-backward', action='store_true', help='skip the force-loss step timing')
     ap.add_argument('--no-graph', action='store_true', help='report the eager call instead of the captured one')
+    ap.add_argument('--no-sweep', action='store_true', help='skip the batch 1/4/16 E+F timings (config 2)')
     ap.add_argument('--fuse-radial', action='store_true',
                     help="patch_model(fuse_radial=True): the radial MLP's output layer inside the convolution")
     a = ap.parse_args()
@@ -542,6 +548,8 @@ def main():
         return
     dev = torch.device('cuda:0')
     sync = torch.cuda.synchronize
+    # config 1 is the reference's energy + forces + stress workload; the others are energy + forces
+    kw = dict(compute_force=True, compute_stress=(a.config == 1))
     model, batch_cpu, meta = factory.workload(a.config)
     n_structs = batch_cpu['ptr'].numel() - 1
     n_real = int(batch_cpu['n_real_edges'])
@@ -556,13 +564,13 @@ def main():
 
     # agreement with the unpatched path (fp32, same GPU) on this workload
     e3nn = copy.deepcopy(model).to(dev)
-    o_ref = e3nn(D.fresh(batch), compute_force=True)
-    o_met = met(D.fresh(batch), compute_force=True)
+    o_ref = e3nn(D.fresh(batch), **kw)
+    o_met = met(D.fresh(batch), **kw)
     dE = float((o_met['energy'] - o_ref['energy']).abs().max())
     dF = float((o_met['forces'] - o_ref['forces']).abs().max())
     _log(f'max|dE| {dE * 1e3:.4f} meV  max|dF| {dF:.2e} eV/A (patched vs unpatched, fp32, GPU)')
 
-    dt, _ = _time_calls(met, batch, a.steps, a.warmup, sync)
+    dt, _ = _time_calls(met, batch, a.steps, a.warmup, sync, **kw)
     _log(f'patched: {dt * 1e3:.3f} ms per E+F call')
     # every call on a new edge_index / node_attrs tensor (as in MD or a relaxation): CSRs and element index rebuilt
     fresh = [dict(batch, edge_index=batch['edge_index'].clone(), node_attrs=batch['node_attrs'].clone())
@@ -570,7 +578,7 @@ def main():
     sync()
     t0 = time.perf_counter()
     for b in fresh:
-        met(b, compute_force=True)
+        met(b, **kw)
     sync()
     dt_fresh = (time.perf_counter() - t0) / a.steps
     del fresh
@@ -591,7 +599,7 @@ def main():
         def md_step(k):
             mb['positions'] = base + kick[k % len(kick)]
             nl = hnl.update_batch(mb, st['r_max'], pbc=pbc, pad_edges_to=st['pad_edges_to'])
-            met(mb, compute_force=True)
+            met(mb, **kw)
             return nl
         for k in range(a.warmup):
             md_step(k)
@@ -606,9 +614,28 @@ def main():
             for k in range(a.steps):
                 hnl.update_batch(mb, st['r_max'], pbc=pbc, pad_edges_to=st['pad_edges_to'])
         nl_ms = tm_nl.summary().get('neighbour_list', (0, 0.0))[1]
+        # the same step captured whole (graphs.capture with neighbours): positions copied in, one replay
+        from mace_hip_kernels.graphs import capture
+        cb = D.fresh(batch)
+        step = capture(met, cb, neighbours=dict(r_max=st['r_max'], pbc=pbc, pad_edges_to=st['pad_edges_to']), **kw)
+        for k in range(a.warmup):
+            with torch.no_grad():
+                cb['positions'].copy_(base + kick[k % len(kick)])
+            step.replay()
+        sync()
+        t0 = time.perf_counter()
+        for k in range(a.steps):
+            with torch.no_grad():
+                cb['positions'].copy_(base + kick[k % len(kick)])
+            step.replay()
+        sync()
+        dt_md_graph = (time.perf_counter() - t0) / a.steps
+        step.neighbour_list.check()
+        del step, cb
         md = dict(step='positions moved (0.01 A Gaussian), neighbour list rebuilt on the GPU (padded to '
-                       f"{st['pad_edges_to']} edges per structure), E+F (eager)",
-                  ms_per_step=round(dt_md * 1e3, 4), neighbour_list_ms=round(nl_ms, 4))
+                       f"{st['pad_edges_to']} edges per structure), E+F",
+                  ms_per_step_eager=round(dt_md * 1e3, 4), ms_per_step_captured=round(dt_md_graph * 1e3, 4),
+                  neighbour_list_ms=round(nl_ms, 4))
         _log('MD-like step:', md)
         del mb, kick
 
@@ -618,13 +645,13 @@ def main():
     if not a.no_graph:
         from mace_hip_kernels.graphs import capture
         gbatch = D.fresh(batch)
-        call = capture(met, gbatch, compute_force=True)
+        call = capture(met, gbatch, **kw)
         base = gbatch['positions'].detach().clone()
         gen = torch.Generator(device='cpu').manual_seed(11)
         with torch.no_grad():
             gbatch['positions'].copy_(base + 0.02 * torch.randn(base.shape, generator=gen).to(base))
         out_g = call.replay()
-        ref = met(D.fresh(gbatch), compute_force=True)
+        ref = met(D.fresh(gbatch), **kw)
         graph_check = {'max_abs_dE_eV': float((out_g['energy'] - ref['energy']).abs().max()),
                        'max_abs_dF_eV_per_A': float((out_g['forces'] - ref['forces']).abs().max())}
         assert graph_check['max_abs_dE_eV'] <= 1e-3 and graph_check['max_abs_dF_eV_per_A'] <= 1e-5, graph_check
@@ -647,7 +674,7 @@ def main():
 
     with _native.timing() as tm:
         for _ in range(a.steps):
-            met(batch, compute_force=True)
+            met(batch, **kw)
     kern = _kernel_table(met, batch, n_real, tm.summary(), tm.symbols)
     # the convolutions' backward with every edge walked (skip_masked off: padding edges read and written like any
     # other), for comparison with the model path that skips the edges outside the cutoff
@@ -657,10 +684,20 @@ def main():
         m_.skip_masked = False
     with _native.timing() as tm_all:
         for _ in range(a.steps):
-            met(batch, compute_force=True)
+            met(batch, **kw)
     for m_ in convs:
         m_.skip_masked = True
     conv_all_edges = {k: round(v[1], 5) for k, v in tm_all.summary().items() if k.startswith('conv_bwd')}
+    # per-op forward + backward ms per call, the reference's per-op rows (its README.md:60-62: convolution layers 1
+    # and 2, symmetric contractions 1 and 2, measured on config 1's structure)
+    per_op = {}
+    for i in range(len(model.interactions)):
+        for key, tag in ((f'conv_layer{i + 1}', f'interactions.{i}.conv_tp'),
+                         (f'symmetric_contraction{i + 1}', f'products.{i}.symmetric_contractions')):
+            op = key.split('_')[0] if key.startswith('conv') else 'sc'
+            rows = [kern.get(f'{op}_{d}[{tag}]') for d in ('fwd', 'bwd')]
+            if all(rows):
+                per_op[key + '_fwd_bwd_ms'] = round(sum(r['ms'] for r in rows), 4)
     per_call = {k: v['ms'] * v['launches'] / a.steps for k, v in kern.items()}
     dom = max(per_call, key=per_call.get)
     d = kern[dom]
@@ -668,7 +705,7 @@ def main():
 
     e3nn_res = None
     if not a.no_e3nn:
-        dt_ref, _ = _time_calls(e3nn, batch, max(3, a.steps // 4), 2, sync)
+        dt_ref, _ = _time_calls(e3nn, batch, max(3, a.steps // 4), 2, sync, **kw)
         e3nn_res = dict(ms_per_call=round(dt_ref * 1e3, 3), calls_per_s=round(1.0 / dt_ref, 3),
                         speedup=round(dt_ref / dt, 2), speedup_eager=round(dt_ref / dt_eager, 2))
         _log(f'e3nn path on GPU: {dt_ref * 1e3:.3f} ms per call (x{dt_ref / dt:.1f})')
@@ -679,7 +716,8 @@ def main():
         met2 = copy.deepcopy(model).to(dev)
         rep2 = patch_model(met2, verbose=False, double_backward=True)
         dt_tr = _time_train(met2, batch, max(3, a.steps // 4), 2, sync)
-        dbl = dict(step='E,F with create_graph; loss E^2+|F|^2; backward to parameters',
+        dbl = dict(step='E,F with create_graph; loss E^2+|F|^2; its gradient with respect to the positions (no '
+                        'parameter gradients in either model)',
                    patched=sorted(rep2['patched']), ms_per_step=round(dt_tr * 1e3, 3))
         del met2
         if not a.no_e3nn:
@@ -690,7 +728,7 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        cpu = _cpu_baseline(copy.deepcopy(model), batch_cpu, n_structs, a.cpu_sample, a.cpu_steps)
+        cpu = _cpu_baseline(copy.deepcopy(model), batch_cpu, n_structs, a.cpu_sample, a.cpu_steps, **kw)
         _log('cpu baseline:', cpu)
 
     # HBM traffic of the dominant kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE run of this workload
@@ -703,6 +741,35 @@ def main():
         recs = [tj['kernels'][k] for k in (d.get('symbol') or '').split('+') if k in tj['kernels']]
         if recs:
             traffic, traffic_src = int(sum(r['traffic_bytes'] for r in recs)), tj['source']
+    # E+F at batch 1, 4 and 16 of config 2's structures (the reference's benchmarks/bench.py batches, its
+    # README.md:64): captured and eager, and the unpatched model on the same GPU, per call and per structure
+    sweep = None
+    if a.config == 2 and not a.no_sweep:
+        from mace_hip_kernels.graphs import capture
+        st2 = factory.structures(2)
+        sweep = {}
+        for nb in (1, 4, 16):
+            bb = D.fresh(_to(factory.batch_of(dict(st2, structures=st2['structures'][:nb])), dev))
+            t_eager, _ = _time_calls(met, bb, a.steps, a.warmup, sync, **kw)
+            call = capture(met, D.fresh(bb), **kw)
+            for _ in range(a.warmup):
+                call.replay()
+            sync()
+            t0 = time.perf_counter()
+            for _ in range(a.steps):
+                call.replay()
+            sync()
+            t_graph = (time.perf_counter() - t0) / a.steps
+            del call
+            rec = dict(structures=nb, atoms=int(bb['positions'].shape[0]), ms_per_call=round(t_graph * 1e3, 4),
+                       ms_per_structure=round(t_graph * 1e3 / nb, 4), ms_per_call_eager=round(t_eager * 1e3, 4))
+            if not a.no_e3nn:
+                e3 = copy.deepcopy(model).to(dev)
+                t_ref, _ = _time_calls(e3, bb, 3, 1, sync, **kw)
+                rec.update(e3nn_ms_per_structure=round(t_ref * 1e3 / nb, 4), speedup=round(t_ref / t_graph, 2))
+                del e3
+            sweep[f'batch{nb}'] = rec
+            _log(f'batch {nb}:', rec)
     conv_total = {k: v for k, v in kern.items() if k.startswith('conv')}
     conv_bytes = sum(v['bytes'] * v['launches'] for v in conv_total.values())
     conv_ms = sum(v['ms'] * v['launches'] for v in conv_total.values())
@@ -720,14 +787,19 @@ def main():
         'dtype': 'f32',
         'data': 'synthetic (seeded structures, random-init weights)',
         'config': {'workload': meta['name'], 'structures': n_structs, 'atoms': int(batch['positions'].shape[0]),
-                   'edges': int(batch['edge_index'].shape[1]), 'real_edges': n_real, 'channels': 128, 'l_max': 3,
-                   'correlation': 3},
+                   'edges': int(batch['edge_index'].shape[1]), 'real_edges': n_real, 'channels': meta['channels'],
+                   'l_max': meta['l_max'], 'correlation': meta['correlation']},
         'structures_per_s': round(n_structs / dt, 2),
         'timed_call': 'captured HIP graph replay' if dt_graph is not None else 'eager',
         'fuse_radial': a.fuse_radial,
         'ms_per_step_eager': round(dt_eager * 1e3, 4),
         'ms_per_step_new_graph_tensors': round(dt_fresh * 1e3, 4),
         'md_step': md,
+        'per_op_fwd_bwd_ms': per_op,
+        'per_op_reference_m4pro_metal_ms': ({'conv_layer1': 1.2, 'conv_layer2': 2.2, 'symmetric_contraction1': 0.42,
+                                             'symmetric_contraction2': 0.07} if a.config == 1 else None),
+        'batch_sweep': sweep,
+        'calls': 'energy + forces + stress' if kw['compute_stress'] else 'energy + forces',
         'conv_bwd_ms_every_edge_walked': conv_all_edges,
         'graph_replay_check': graph_check,
         'conv_hbm_gbs': round(conv_bytes / (conv_ms * 1e-3) / 1e9, 1) if conv_ms else None,

@@ -102,7 +102,8 @@ enum mh_kernel_kind {
     MH_SPECIES_ORDER = 63, /* element index, stable element order and contraction slots (one workgroup) */
     MH_MLP_JVP = 64,     /* radial MLP: derivative of its output along a direction of the features  */
     MH_MLP_BWD2 = 65,    /* derivative of its feature gradient along that direction                 */
-    MH_NUM_KINDS = 66
+    MH_GEOM_SEGSUM = 66, /* per-structure sums of 3x3 rows (the stress displacement's gather backward) */
+    MH_NUM_KINDS = 67
 };
 
 /* flags of mh_conv_bwd */
@@ -356,6 +357,14 @@ int mh_emb_bwd2(mh_module* m, const float* len, const float* dlen, const float* 
 int mh_geom_jvp(mh_module* m, const float* vec, const float* len, const float* ggpos, const float* ggshifts,
                 const int32_t* send, const int32_t* recv, const float* glen, float* dgvec, float* dglen, float* h,
                 int64_t E, void* stream);
+
+/* Per-structure sums of 3x3 rows, out[b] = sum of g[row] over the rows of segment b: perm[seg[b]] ..
+ * perm[seg[b + 1] - 1] (perm [M] int32), or rows seg[b] .. seg[b + 1] - 1 with perm NULL (seg [B + 1] int64, g [M, 9],
+ * out [B, 9]).  The backward of MACE's per-structure gathers in get_symmetric_displacement (the symmetric strain by
+ * atom, the strained cell by edge: segments from the batch's ptr and the sender CSR).  One workgroup per structure
+ * (bind MH_GEOM_SEGSUM with 256 threads and rows_per_block 1); fixed summation order.  No reference counterpart. */
+int mh_geom_segsum(mh_module* m, const float* g, const int32_t* perm, const int64_t* seg, float* out, int32_t B,
+                   void* stream);
 
 /* Second derivatives of a SiLU readout head, behind a double backward (v [N, Din] a direction of x): mh_readout_jvp
  * writes de = (de/dx) v [N]; mh_readout_bwd2 the derivative of mh_readout_bwd's gx along v for the given g [N]

@@ -91,9 +91,9 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     ``double_backward`` (default off, as in the reference, where a backward under ``create_graph=True`` raises)
     makes the patched modules' gradients differentiable once more, for second derivatives with respect to the
     inputs: Hessian-vector products and force constants, or force and stress terms of a loss differentiated with
-    respect to parameters the patch leaves on e3nn.  Every drop-in takes it except the radial MLPs, which have no
-    second-order kernels and are then left on e3nn and reported in ``skipped``.  The patched
-    modules hold their weights as constants: no gradient reaches those weights, with or without it."""
+    respect to the positions (or to parameters the patch leaves on e3nn: ``radial_mlp=False`` keeps the radial MLPs'
+    weights trainable).  Every drop-in takes it (fuse_radial does not: its fused kernels have no second-order form).
+    The patched modules hold their weights as constants: no gradient reaches those weights, with or without it."""
     # a fully patched model may hold no parameters any more (the drop-ins keep their weights as buffers)
     p = next((t for t in itertools.chain(model.parameters(), model.buffers()) if t.is_floating_point()), None)
     if p is None:
@@ -141,20 +141,15 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             prod.symmetric_contractions = HipSymmetricContraction(sc, device=dev)
             prod.symmetric_contractions.tag = name
             patched.append(name)
-    no2 = 'no second-order kernels (patched with double_backward=True)'
     if double_backward:
-        # a radial MLP an earlier call replaced goes back to e3nn: its kernels have no differentiable backward
-        for i, blk in enumerate(getattr(model, 'interactions', [])):
-            mlp = getattr(blk, 'conv_tp_weights', None)
-            restored = isinstance(mlp, HipRadialMLP)
-            if restored:
-                blk.conv_tp_weights = mlp.original[0]
-                if isinstance(getattr(blk, 'conv_tp', None), HipConvTP):
-                    blk.conv_tp.detach_mlp()
-            if radial_mlp or restored:
-                skipped.append((f'interactions.{i}.conv_tp_weights',
-                                no2 + ('; the e3nn module an earlier patch replaced is restored' if restored else '')))
-        radial_mlp = False
+        # convolutions an earlier call fused with their radial MLP (fuse_radial) go back to the two-kernel path:
+        # the fused kernels have no second-order form
+        for blk in getattr(model, 'interactions', []):
+            cv, mlp = getattr(blk, 'conv_tp', None), getattr(blk, 'conv_tp_weights', None)
+            if isinstance(cv, HipConvTP) and cv.fused_mlp() is not None:
+                cv.detach_mlp()
+            if isinstance(mlp, HipRadialMLP):
+                mlp.fuse = False
     if spherical_harmonics and hasattr(model, 'spherical_harmonics'):
         sh = model.spherical_harmonics
         if not isinstance(sh, HipSphericalHarmonics):
@@ -269,7 +264,7 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             model._mh_geometry_double_backward = True
         for mod in model.modules():
             if isinstance(mod, (HipConvTP, HipSymmetricContraction, HipNodeLinear, HipReshapeIrreps,
-                                HipSphericalHarmonics, HipRadialEmbedding, HipReadout)):
+                                HipSphericalHarmonics, HipRadialEmbedding, HipReadout, HipRadialMLP)):
                 mod.double_backward = True
                 if hasattr(mod, 'second_module'):
                     mod.second_module()   # compiled now rather than inside the first double backward

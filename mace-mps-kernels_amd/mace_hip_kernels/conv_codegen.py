@@ -44,6 +44,11 @@ FENCE_M = True
 # Load the W rows (read exactly once per launch) with the non-temporal cache policy.  Measured on config 2 with
 # W rotating over buffers larger than the Infinity Cache: never slower, 131 → 112 µs for the 1280-wide forward.
 W_NT = True
+# Edges whose x and W slices the receiver-ordered backward has in flight ahead of the one being computed (1 or 2).
+# Measured on config 2 (isolated, layer 2): 290.7 us with one edge ahead, 295.7 us with two.
+BWD_PREFETCH = 1
+# The factored backward's per-edge cutoff: broadcast from a per-chunk register (True) or loaded per edge (False).
+BWD_CUT_BCAST = True
 
 
 class _Gen:
@@ -460,8 +465,10 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         '  ' + decl('gv', G.no),
     ]
     L += G.ld_g('  ', 'r', 'gv')
-    L += ['  ' + decl('xn', nx), '  ' + decl('wn', nk),
-          '  const int p0 = rowptr[r], p1 = rowptr[r + 1];']
+    L += ['  ' + decl('xn', nx), '  ' + decl('wn', nk)]
+    if BWD_PREFETCH > 1:
+        L += ['  ' + decl('xm', nx), '  ' + decl('wm', nk)]
+    L += ['  const int p0 = rowptr[r], p1 = rowptr[r + 1];']
 
     def chunks(msg):
         C = ['  for (int pb = p0; pb < p1; pb += MH_WAVE) {']
@@ -491,7 +498,8 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
                   '    }',
                   '    if (cnt == 0) continue;',
                   '    my_e = 0;',
-                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; }']
+                  '    float my_c = 0.0f;                  // the cutoff of lane j\'s edge, broadcast per edge below',
+                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e]; }']
         else:
             C += ['    const int cnt = min(MH_WAVE, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
@@ -499,18 +507,32 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         C += G.m_prologue('    ', 'my_e')
         C += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
         C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
-        C += ['    }', '    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
+        C += ['    }']
+        if BWD_PREFETCH > 1:          # edge 1 (or the last edge again) one stage further out
+            C += ['    {', '      const int e1 = mh_bcast(my_e, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
+            C += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'e1', 'wm')
+            C += ['    }']
+        C += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
         C += copy('xv', 'xn', nx)
         if cut:
-            C += ['      const float ce = cutv[e];'] + copy('w0', 'wn', nk)
+            C += ['      const float ce = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_c), j));'
+                  if BWD_CUT_BCAST else '      const float ce = cutv[e];']
+            C += copy('w0', 'wn', nk)
             C += [f'      const float w{k} = w0{k} * ce;' for k in range(nk)]
             C += ['      float Pc = 0.0f;']
         else:
             C += copy('w', 'wn', nk)
-        C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
-              '        const int e1 = mh_bcast(my_e, j1), s1 = mh_bcast(my_s, j1);']
-        C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
-        C += ['      }']
+        if BWD_PREFETCH > 1:
+            C += [f'      xn{i} = xm{i};' for i in range(nx)] + [f'      wn{k} = wm{k};' for k in range(nk)]
+            C += ['      {', '        const int j2 = min(j + 2, cnt - 1);',
+                  '        const int e2 = mh_bcast(my_e, j2), s2 = mh_bcast(my_s, j2);']
+            C += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'e2', 'wm')
+            C += ['      }']
+        else:
+            C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
+                  '        const int e1 = mh_bcast(my_e, j1), s1 = mh_bcast(my_s, j1);']
+            C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+            C += ['      }']
         C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
         if msg:
             C += ['      ' + decl('gxa', nx, '0.0f')]

@@ -21,11 +21,21 @@ per direction) from the current contents of ``batch['edge_index']``, so a neighb
 can be copied in before each replay.  Those rebuilt graphs cannot be validated on the host inside the graph: node
 indices are clamped into range instead (a bad edge list gives wrong numbers, never a bad memory access).  The caller
 must not resize or reallocate the batch tensors while the capture is in use.
+
+A molecular-dynamics step can be captured whole: with ``neighbours=dict(r_max=..., pbc=<[B, 3] bool GPU tensor>,
+pad_edges_to=...)`` every replay first rebuilds the neighbour list on the GPU from the current positions
+(``mace_hip_kernels.neighbours``, the fixed-size padded layout), then the graph's CSRs, then runs the call:
+
+    step = capture(model, batch, neighbours=dict(r_max=5.0, pbc=pbc, pad_edges_to=6000), compute_force=True)
+    batch['positions'].copy_(new_positions)
+    out = step.replay()                                   # neighbour list, CSRs, energy and forces
+    step.neighbour_list.check()                           # (synchronises) every structure fitted its padding
 """
 import torch
 
 from . import _native
 from . import conv as _conv
+from .neighbours import update_batch
 
 __all__ = ['capture', 'CapturedCall']
 
@@ -34,17 +44,31 @@ class CapturedCall:
     """A captured model call: ``replay()`` re-runs it on the current contents of ``batch`` and returns the outputs
     (the same tensors every time, overwritten by each replay)."""
 
-    def __init__(self, model, batch, warmup=2, rebuild_graph=False, **kwargs):
+    def __init__(self, model, batch, warmup=2, rebuild_graph=False, neighbours=None, **kwargs):
         if not torch.cuda.is_available():
             raise RuntimeError('HIP graph capture needs a GPU')
         self.model, self.batch, self.kwargs = model, batch, kwargs
+        self.neighbour_list = None
+        if neighbours is not None:
+            pbc = neighbours.get('pbc')
+            if not (torch.is_tensor(pbc) and pbc.is_cuda):
+                raise ValueError('neighbours: pbc must be a [B, 3] GPU tensor (a host copy cannot be captured)')
+            if neighbours.get('pad_edges_to') is None:
+                raise ValueError('neighbours: pad_edges_to is required (the layout must not depend on the positions)')
+            rebuild_graph = True
+
+        def call():
+            if neighbours is not None:
+                self.neighbour_list = update_batch(batch, neighbours['r_max'], pbc=neighbours['pbc'],
+                                                   pad_edges_to=neighbours['pad_edges_to'])
+            return model(batch, **kwargs)
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             # builds and caches the CSRs and element indices the capture will read; the caching allocator also
             # settles its pools off the capture stream
             for _ in range(max(1, warmup)):
-                model(batch, **kwargs)
+                call()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         _native.take_capture_holds()
@@ -52,7 +76,7 @@ class CapturedCall:
         _conv._capture_rebuild = bool(rebuild_graph)
         try:
             with torch.cuda.graph(self.graph):
-                self.out = model(batch, **kwargs)
+                self.out = call()
         finally:
             _conv._capture_rebuild = False
             _conv._capture_graphs.clear()
@@ -63,6 +87,7 @@ class CapturedCall:
         return self.out
 
 
-def capture(model, batch, warmup=2, rebuild_graph=False, **kwargs):
-    """Capture ``model(batch, **kwargs)`` (energy, forces, ...) as a HIP graph; see the module docstring."""
-    return CapturedCall(model, batch, warmup=warmup, rebuild_graph=rebuild_graph, **kwargs)
+def capture(model, batch, warmup=2, rebuild_graph=False, neighbours=None, **kwargs):
+    """Capture ``model(batch, **kwargs)`` (energy, forces, ...) as a HIP graph, with ``neighbours`` preceded by a GPU
+    neighbour-list rebuild into ``batch``; see the module docstring."""
+    return CapturedCall(model, batch, warmup=warmup, rebuild_graph=rebuild_graph, neighbours=neighbours, **kwargs)

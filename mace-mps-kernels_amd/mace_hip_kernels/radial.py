@@ -27,7 +27,8 @@ units (v_mfma_f32_16x16x32_bf16, 2.7x the fp32 rate per K):
   features).
 
 Weights are read from the module when it is patched and checked against it in float64; there are no weight
-gradients (inference, like the other drop-ins).
+gradients (inference, like the other drop-ins).  Behind a double backward the second-order kernels (``mlp_jvp``,
+``mlp_bwd2``, ``source_second``) differentiate the backward once more.
 """
 import math
 
@@ -657,8 +658,17 @@ def packed_weights(spec):
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
-                    'autograd Hessian) is not supported by this HIP module; patch_model(model, '
-                    'double_backward=True) leaves it on e3nn')
+                    'autograd Hessian) is not enabled for this HIP module; patch with '
+                    'patch_model(model, double_backward=True)')
+
+
+def _mlp_bwd(op, ef, g):
+    """dL/d(edge features) [E, n_basis] from dL/dW0 (contiguous 2-D operands)."""
+    gx = torch.empty_like(ef)
+    _native.launch(f'mlp_bwd[{op.tag}]', _native.load().mh_mlp_bwd, op.module.handle, _native.ptr(ef),
+                   _native.ptr(op.Wh), _native.ptr(op.Wl), _native.ptr(g), _native.ptr(gx), ef.shape[0],
+                   _native.stream_of(ef))
+    return gx
 
 
 class _MLPFn(torch.autograd.Function):
@@ -675,23 +685,59 @@ class _MLPFn(torch.autograd.Function):
         out = torch.empty(E, s.hs[-1], device=x.device, dtype=torch.float32)
         _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd, op.module.handle, _native.ptr(x),
                        _native.ptr(op.WhT), _native.ptr(op.WlT), _native.ptr(out), E, _native.stream_of(x))
-        ctx.save_for_backward(x)
+        ctx.save_for_backward(ef)            # the input itself: a double backward differentiates through it
         ctx.op, ctx.lead = op, lead
         return out.reshape(*lead, s.hs[-1])
 
     @staticmethod
     def backward(ctx, g):
-        if torch.is_grad_enabled():
-            raise RuntimeError(_DOUBLE_BACKWARD)
-        x, = ctx.saved_tensors
+        ef, = ctx.saved_tensors
         op = ctx.op
         s = op.spec
-        g2 = g.reshape(-1, s.hs[-1]).contiguous()
-        gx = torch.empty_like(x)
-        _native.launch(f'mlp_bwd[{op.tag}]', _native.load().mh_mlp_bwd, op.module.handle, _native.ptr(x),
-                       _native.ptr(op.Wh), _native.ptr(op.Wl), _native.ptr(g2), _native.ptr(gx), x.shape[0],
-                       _native.stream_of(x))
+        if torch.is_grad_enabled():          # only true under create_graph=True
+            if not op.double_backward:
+                raise RuntimeError(_DOUBLE_BACKWARD)
+            return _MLPAdjFn.apply(g, ef, op), None
+        x = ef.reshape(-1, s.hs[0]).contiguous()
+        gx = _mlp_bwd(op, x, g.reshape(-1, s.hs[-1]).contiguous())
         return gx.reshape(*ctx.lead, s.hs[0]), None
+
+
+class _MLPAdjFn(torch.autograd.Function):
+    """dL/def = J(ef)^T g as a function of (g, ef), for a double backward: with ggx the gradient arriving for dL/def,
+    d<ggx, J^T g>/dg = J(ef) ggx (``mlp_jvp``) and d<ggx, J^T g>/def = sum_k g_k d^2 W0_k/def^2 ggx (``mlp_bwd2``).
+    Third derivatives are not provided."""
+
+    @staticmethod
+    def forward(ctx, g, ef, op):
+        s = op.spec
+        ctx.save_for_backward(g, ef)
+        ctx.op = op
+        x = ef.reshape(-1, s.hs[0]).contiguous()
+        return _mlp_bwd(op, x, g.reshape(-1, s.hs[-1]).contiguous()).reshape(ef.shape)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, ggx):
+        g, ef = ctx.saved_tensors
+        op = ctx.op
+        s = op.spec
+        m = op.second_module()
+        x = ef.reshape(-1, s.hs[0]).contiguous()
+        v = ggx.reshape(-1, s.hs[0]).contiguous()
+        E, P, lib, st = x.shape[0], _native.ptr, _native.load(), _native.stream_of(x)
+        d_g = d_ef = None
+        if ctx.needs_input_grad[0]:
+            dW = torch.empty(E, s.hs[-1], device=x.device, dtype=torch.float32)
+            _native.launch(f'mlp_jvp[{op.tag}]', lib.mh_mlp_jvp, m.handle, P(x), P(v), P(op.WhT), P(op.WlT), P(dW), E,
+                           st)
+            d_g = dW.reshape(g.shape)
+        if ctx.needs_input_grad[1]:
+            gv = torch.empty_like(x)
+            _native.launch(f'mlp_bwd2[{op.tag}]', lib.mh_mlp_bwd2, m.handle, P(x), P(v), P(op.Wh), P(op.Wl),
+                           P(g.reshape(-1, s.hs[-1]).contiguous()), P(gv), E, st)
+            d_ef = gv.reshape(ef.shape)
+        return d_g, d_ef, None
 
 
 class HipRadialMLP(torch.nn.Module):
@@ -718,9 +764,24 @@ class HipRadialMLP(torch.nn.Module):
         self.hs = self.spec.hs
         self.original = [mod]
         self.tag = 'radial_mlp'
+        self._device = dev
+        # a backward under create_graph=True raises (the reference's behaviour) unless this is set; then the
+        # gradient is differentiable once more through the second-order kernels (second_module)
+        self.double_backward = False
+        self._second = None
         # set by patch_model when the convolution fed by this MLP forms its weights itself (HipConvTP.attach_mlp):
         # the output is then returned unformed
         self.fuse = False
+
+    def second_module(self):
+        """The module of the second-order kernels (``mlp_jvp``, ``mlp_bwd2``), compiled on first use."""
+        if self._second is None:
+            code = _native.compile_source(source_second(self.spec))
+            with torch.cuda.device(self._device):
+                self._second = _native.Module(code, {
+                    _native.MH_MLP_JVP: (self.spec.kname('mlp_jvp'), BLOCK, 64 * NB_JVP),
+                    _native.MH_MLP_BWD2: (self.spec.kname('mlp_bwd2'), BLOCK, 64 * NB_BWD)})
+        return self._second
 
     def forward(self, ef):
         if self.fuse and ef.dim() == 2 and ef.shape[1] == self.spec.hs[0]:

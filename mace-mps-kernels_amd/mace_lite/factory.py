@@ -116,12 +116,9 @@ def batch_of(st, dtype=torch.float32, device='cpu'):
 def workload(cfg, seed=0, dtype=torch.float32, device='cpu'):
     """(model, batch, meta) for BASELINE configuration ``cfg`` (0-4)."""
     st = structures(cfg, seed)
-    if cfg == 0:
-        model = make_model('32x0e+32x1o', 2, 2, elements=ELEMENTS_PTCOH, dtype=dtype)
-    elif cfg in (1, 2):
-        model = make_model('128x0e+128x1o', 3, 3, elements=ELEMENTS_PTCOH, dtype=dtype)
-    elif cfg == 3:
-        model = make_model('128x0e+128x1o', 3, 3, r_max=6.0, elements=list(range(1, 90)), dtype=dtype)
-    else:
-        model = make_model('128x0e+128x1o+128x2e', 3, 3, elements=ELEMENTS_PTCOH, dtype=dtype)
-    return model, batch_of(st, dtype, device), dict(name=st['name'], r_max=st['r_max'], **st['meta'])
+    hidden, lmax, corr = {0: ('32x0e+32x1o', 2, 2), 1: ('128x0e+128x1o', 3, 3), 2: ('128x0e+128x1o', 3, 3),
+                          3: ('128x0e+128x1o', 3, 3), 4: ('128x0e+128x1o+128x2e', 3, 3)}[cfg]
+    model = make_model(hidden, lmax, corr, r_max=st['r_max'], elements=st['elements'], dtype=dtype)
+    return model, batch_of(st, dtype, device), dict(name=st['name'], r_max=st['r_max'], hidden=hidden,
+                                                    channels=int(hidden.split('x')[0]), l_max=lmax, correlation=corr,
+                                                    **st['meta'])

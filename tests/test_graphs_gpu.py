@@ -95,3 +95,49 @@ def test_captured_call_rebuilds_graph():
         assert de <= 1e-3 and df <= 1e-5
     del call
     torch.cuda.synchronize()
+
+
+def test_captured_md_step_with_gpu_neighbour_list():
+    """capture(neighbours=...): every replay rebuilds the padded neighbour list on the GPU from the current positions,
+    then the CSRs, then E+F.  The positions move by up to ~0.15 A between replays (edges enter and leave the cutoff);
+    each replay's edge list equals an eager GPU build on the same positions, and its energies and forces an eager
+    call on that graph."""
+    from mace_hip_kernels import neighbour_list
+    assert torch.cuda.is_available(), 'GPU test needs a GPU'
+    dev = torch.device('cuda:0')
+    print('[case] captured MD step: GPU neighbour list + E+F', flush=True)
+    model, batch_cpu, meta = factory.workload(2)
+    model = copy.deepcopy(model).to(dev)
+    assert not patch_model(model, verbose=False)['skipped']
+    st = factory.structures(2)
+    pbc = torch.tensor([[bool(v) for v in s.pbc] for s in st['structures']], device=dev)
+    batch = D.fresh(_gpu_batch(batch_cpu, dev))
+    base = batch['positions'].detach().clone()
+    step = capture(model, batch, neighbours=dict(r_max=5.0, pbc=pbc, pad_edges_to=6000), compute_force=True)
+    rng = np.random.default_rng(11)
+    prev = None
+    for rep in range(3):
+        new = base + torch.tensor(rng.normal(0.0, 0.05, size=tuple(base.shape)), dtype=base.dtype, device=dev)
+        with torch.no_grad():
+            batch['positions'].copy_(new)
+        out = step.replay()
+        e_g, f_g = out['energy'].detach().clone(), out['forces'].detach().clone()
+        ei_g = batch['edge_index'].clone()
+        step.neighbour_list.check()
+        nl = neighbour_list(new, batch['cell'], batch['ptr'], 5.0, pbc=pbc, pad_edges_to=6000)
+        assert torch.equal(ei_g, nl.edge_index) and torch.equal(batch['shifts'], nl.shifts)
+        if prev is not None:
+            assert not torch.equal(ei_g, prev)          # the graph changed with the positions
+        prev = ei_g
+        ref_batch = D.fresh(batch)
+        ref_batch['positions'] = new.clone()
+        ref_batch['edge_index'], ref_batch['shifts'] = nl.edge_index, nl.shifts
+        ref_batch['unit_shifts'] = nl.unit_shifts
+        ref = model(ref_batch, compute_force=True)
+        torch.cuda.synchronize()
+        de = float((e_g - ref['energy']).abs().max())
+        df = float((f_g - ref['forces']).abs().max())
+        print(f'  replay {rep}: |dE| {de:.2e} eV  |dF| {df:.2e} eV/A', flush=True)
+        assert de <= 1e-3 and df <= 1e-5
+    del step
+    torch.cuda.synchronize()

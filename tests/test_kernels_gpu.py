@@ -799,6 +799,38 @@ def test_radial_mlp_vs_float64(hidden, lmax, elements):
     assert torch.equal(op(xb.reshape(4, 16, -1)).reshape(64, -1), op(xb))
 
 
+@pytest.mark.parametrize('hidden,lmax', [('128x0e+128x1o', 3), ('32x0e+32x1o', 2)])
+def test_radial_mlp_double_backward_vs_float64(hidden, lmax):
+    """The radial MLP's second derivatives (mlp_jvp, mlp_bwd2 behind patch's double backward) against float64
+    autograd of the e3nn module: for the loss <u, dL/def> with dL/def = J(ef)^T g, the gradients with respect to g
+    (J u, the forward-mode derivative) and to ef (the Hessian-vector product sum_k g_k d^2 W0_k/def^2 u), on a
+    ragged edge count, embedding-like and random features."""
+    dev = _dev()
+    model = factory.make_model(hidden, lmax, 2, elements=factory.ELEMENTS_PTCOH)
+    rng = np.random.default_rng(19)
+    e = 1999
+    r = torch.tensor(rng.uniform(0.5, 6.0, size=(e, 1)))
+    emb, _ = model.radial_embedding.double()(r)
+    for kind, ef in (('embedding', emb.numpy()), ('random', rng.normal(size=(e, emb.shape[1])))):
+        for li, blk in enumerate(model.interactions):
+            print(f'[case] radial MLP double backward {hidden} layer {li} ({kind} features)', flush=True)
+            op = HipRadialMLP(blk.conv_tp_weights, device=dev)
+            op.double_backward = True
+            nw = op.hs[-1]
+            g, u = rng.normal(size=(e, nw)), rng.normal(size=ef.shape)
+            res = []
+            for dt, m in ((torch.float32, op), (torch.float64, copy.deepcopy(blk.conv_tp_weights).double().to(dev))):
+                xt = torch.tensor(ef, dtype=dt, device=dev, requires_grad=True)
+                gt = torch.tensor(g, dtype=dt, device=dev, requires_grad=True)
+                out = m(xt)
+                gx, = torch.autograd.grad(out, xt, gt, create_graph=True)
+                d_g, d_x = torch.autograd.grad((gx * torch.tensor(u, dtype=dt, device=dev)).sum(), (gt, xt))
+                res.append((gx.detach().double().cpu().numpy(), d_g.double().cpu().numpy(),
+                            d_x.double().cpu().numpy()))
+            for got, want in zip(*res):
+                assert _rel(got, want) < MLP_TOL
+
+
 def test_radial_mlp_c_abi():
     dev = _dev()
     print('[case] radial MLP C-ABI', flush=True)

@@ -137,67 +137,73 @@ def test_double_backward_raises():
         torch.autograd.grad(f.sum(), batch['positions'])
 
 
-@pytest.mark.parametrize('config', ['l3_corr3_fullcg', 'l3_corr3_l2hidden'])
-def test_double_backward_hessian_and_force_loss(config):
-    """patch_model(double_backward=True): every drop-in but the radial MLPs differentiates twice (those stay on e3nn
-    and are reported).  Against the
-    unpatched model in float64: (1) a Hessian-vector product of the energy with respect to the positions,
-    d(F·v)/dx; (2) the gradients, with respect to every parameter the patch leaves in place, of a loss on energy
-    and forces computed with create_graph (MACE's training=True).  Tolerance: 1e-4 relative to the largest
-    reference component."""
-    dev = _dev()
-    print(f'[case] double backward {config}', flush=True)
-    model = factory.make_model(*factory.REF_CONFIGS[config])
-    ref = copy.deepcopy(model).to(dev, torch.float64)
-    met = copy.deepcopy(model).to(dev, torch.float32)
-    report = patch_model(met, verbose=False, double_backward=True)
-    assert 'spherical_harmonics' in report['patched'] and 'radial_embedding' in report['patched'], report
-    assert any(n.endswith('conv_tp') for n in report['patched']), report
-    assert 'edge_geometry' in report['patched'], report
-    assert not any('double_backward' in why and not n.endswith('conv_tp_weights') for n, why in report['skipped'])
-    skipped = dict(report['skipped'])                # the drop-ins without second-order kernels
-    assert 'double_backward' in skipped['interactions.0.conv_tp_weights'], skipped
-    st = factory.make_structure(seed=4)
-    batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
-    v = np.random.default_rng(0).normal(size=(len(st), 3))
-    hv, grads = [], []
-    for m, dt in ((ref, torch.float64), (met, torch.float32)):
-        b = D.fresh(_to(batch, dev, dt))
-        out = m(b, compute_force=False, training=True)
-        f, = torch.autograd.grad(-out['energy'].sum(), b['positions'], create_graph=True)
-        h, = torch.autograd.grad((f * torch.tensor(v, dtype=dt, device=dev)).sum(), b['positions'])
-        hv.append(h.double().cpu().numpy())
-        m.zero_grad()
-        b = D.fresh(_to(batch, dev, dt))
-        out = m(b, compute_force=True, training=True)
-        loss = (out['energy'] ** 2).sum() + (out['forces'] ** 2).sum()
-        loss.backward()
-        grads.append({k: p.grad.double().cpu().numpy() for k, p in m.named_parameters() if p.grad is not None})
-    assert np.abs(hv[1] - hv[0]).max() < 1e-4 * np.abs(hv[0]).max()
-    common = sorted(set(grads[0]) & set(grads[1]))
-    assert any('conv_tp_weights' in k for k in common), common
-    for k in common:
-        scale = max(np.abs(grads[0][k]).max(), 1e-8)
-        assert np.abs(grads[1][k] - grads[0][k]).max() < 1e-4 * scale, k
-
-
-def _loss_grads(m, batch, dev, dt, stress):
-    """Parameter gradients of E^2 + |F|^2 (+ |stress|^2) computed with create_graph (MACE's training=True)."""
+def _force_loss(m, batch, dev, dt, stress=False, wrt_positions=False):
+    """E^2 + |F|^2 (+ |stress|^2) computed with create_graph (MACE's training=True), differentiated with respect to
+    the positions (``wrt_positions``) or to every parameter that has a gradient."""
     m.zero_grad()
     b = D.fresh(_to(batch, dev, dt))
     out = m(b, compute_force=True, compute_stress=stress, training=True)
     loss = (out['energy'] ** 2).sum() + (out['forces'] ** 2).sum()
     if stress:
         loss = loss + (out['stress'] ** 2).sum()
+    if wrt_positions:
+        g, = torch.autograd.grad(loss, b['positions'])
+        return {'positions': g.double().cpu().numpy()}
     loss.backward()
     return {k: p.grad.double().cpu().numpy() for k, p in m.named_parameters() if p.grad is not None}
 
 
+def _close(got, want, tol=1e-4):
+    for k in want:
+        scale = max(np.abs(want[k]).max(), 1e-8)
+        assert np.abs(got[k] - want[k]).max() < tol * scale, k
+
+
+@pytest.mark.parametrize('config,mlp', [('l3_corr3_fullcg', 'hip'), ('l3_corr3_l2hidden', 'hip'),
+                                        ('l3_corr3_fullcg', 'e3nn')])
+def test_double_backward_hessian_and_force_loss(config, mlp):
+    """patch_model(double_backward=True): every drop-in differentiates twice, the radial MLPs through their
+    second-order kernels (``mlp='e3nn'``: radial_mlp=False keeps them on e3nn, their weights trainable).  Against
+    the unpatched model in float64: (1) a Hessian-vector product of the energy with respect to the positions,
+    d(F·v)/dx; (2) the gradient of a loss on energy and forces computed with create_graph (MACE's training=True)
+    with respect to the positions, and, with the MLPs on e3nn, with respect to their weights.  Tolerance: 1e-4
+    relative to the largest reference component."""
+    dev = _dev()
+    print(f'[case] double backward {config} radial MLP on {mlp}', flush=True)
+    model = factory.make_model(*factory.REF_CONFIGS[config])
+    ref = copy.deepcopy(model).to(dev, torch.float64)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    report = patch_model(met, verbose=False, double_backward=True, radial_mlp=(mlp == 'hip'))
+    assert 'spherical_harmonics' in report['patched'] and 'radial_embedding' in report['patched'], report
+    assert any(n.endswith('conv_tp') for n in report['patched']), report
+    assert 'edge_geometry' in report['patched'], report
+    assert not report['skipped'], report
+    assert ('interactions.0.conv_tp_weights' in report['patched']) == (mlp == 'hip'), report
+    st = factory.make_structure(seed=4)
+    batch = D.batch_graphs([D.graph_of(st, 5.0)], factory.ELEMENTS_REF)
+    v = np.random.default_rng(0).normal(size=(len(st), 3))
+    hv = []
+    for m, dt in ((ref, torch.float64), (met, torch.float32)):
+        b = D.fresh(_to(batch, dev, dt))
+        out = m(b, compute_force=False, training=True)
+        f, = torch.autograd.grad(-out['energy'].sum(), b['positions'], create_graph=True)
+        h, = torch.autograd.grad((f * torch.tensor(v, dtype=dt, device=dev)).sum(), b['positions'])
+        hv.append(h.double().cpu().numpy())
+    assert np.abs(hv[1] - hv[0]).max() < 1e-4 * np.abs(hv[0]).max()
+    _close(_force_loss(met, batch, dev, torch.float32, wrt_positions=True),
+           _force_loss(ref, batch, dev, torch.float64, wrt_positions=True))
+    if mlp == 'e3nn':
+        g_ref, g_met = _force_loss(ref, batch, dev, torch.float64), _force_loss(met, batch, dev, torch.float32)
+        common = sorted(set(g_ref) & set(g_met))
+        assert any('conv_tp_weights' in k for k in common), common
+        _close(g_met, {k: g_ref[k] for k in common})
+
+
 def test_double_backward_upgrade_and_stress_loss():
-    """patch_model(m) and then patch_model(m, double_backward=True): the radial MLPs the first call replaced go back
-    to e3nn (reported as such), every other drop-in differentiates twice, and a loss on energy, forces and stress
-    (the edge geometry's second-order shifts path) has the parameter gradients of the unpatched model in float64,
-    1e-4 relative to the largest reference component."""
+    """patch_model(m) and then patch_model(m, double_backward=True): the drop-ins the first call made (radial MLPs
+    included) differentiate twice, and a loss on energy, forces and stress (the edge geometry's second-order shifts
+    path) has the position gradient of the unpatched model in float64, 1e-4 relative to the largest reference
+    component."""
     dev = _dev()
     print('[case] double backward after a first-order patch, stress loss', flush=True)
     model = factory.make_model(*factory.REF_CONFIGS['l3_corr3_fullcg'])
@@ -206,17 +212,12 @@ def test_double_backward_upgrade_and_stress_loss():
     first = patch_model(met, verbose=False)
     assert 'interactions.0.conv_tp_weights' in first['patched'], first
     report = patch_model(met, verbose=False, double_backward=True)
-    skipped = dict(report['skipped'])
-    assert 'restored' in skipped['interactions.0.conv_tp_weights'], skipped
-    assert type(met.interactions[0].conv_tp_weights).__name__ != 'HipRadialMLP'
+    assert not report['skipped'], report
+    assert type(met.interactions[0].conv_tp_weights).__name__ == 'HipRadialMLP'
+    assert met.interactions[0].conv_tp_weights.double_backward
     batch = D.batch_graphs([D.graph_of(factory.make_structure(seed=6), 5.0)], factory.ELEMENTS_REF)
-    g_ref, g_met = (_loss_grads(m, batch, dev, dt, stress=True) for m, dt in ((ref, torch.float64),
-                                                                              (met, torch.float32)))
-    common = sorted(set(g_ref) & set(g_met))
-    assert any('conv_tp_weights' in k for k in common), common
-    for k in common:
-        scale = max(np.abs(g_ref[k]).max(), 1e-8)
-        assert np.abs(g_met[k] - g_ref[k]).max() < 1e-4 * scale, k
+    _close(_force_loss(met, batch, dev, torch.float32, stress=True, wrt_positions=True),
+           _force_loss(ref, batch, dev, torch.float64, stress=True, wrt_positions=True))
 
 
 @pytest.mark.parametrize('fuse', [False, True])
@@ -278,6 +279,23 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
                    'ro_fwd_', 'ro_bwd_'):
         assert any(n.startswith(prefix) for n in flat), (prefix, flat)
     assert not any(n.startswith(('perm_', 'conv_fwd_', 'conv_bwd_') + banned) for n in flat), flat
+
+
+def test_stress_path_segmented_sums():
+    """E+F+stress of the patched model (config 1, one structure): the stress displacement's per-structure gathers
+    are differentiated by the segmented-sum kernel (two launches: atoms and edges), and energy, forces and stress
+    match the unpatched model in float64."""
+    from mace_hip_kernels import _native
+    dev = _dev()
+    print('[case] stress displacement through segmented sums (config 1)', flush=True)
+    model, batch, _ = factory.workload(1)
+    ref, met, _ = _pair(model, dev)
+    met(D.fresh(_to(batch, dev, torch.float32)), compute_force=True, compute_stress=True)
+    with _native.timing() as tm:
+        met(D.fresh(_to(batch, dev, torch.float32)), compute_force=True, compute_stress=True)
+    torch.cuda.synchronize()
+    assert tm.symbols.get('geom_segsum') == ['geom_segsum'] and tm.summary()['geom_segsum'][0] == 2, tm.symbols
+    _check(ref, met, batch, dev, np.diff(batch['ptr'].numpy()), stress=True)
 
 
 def test_unsupported_block_is_skipped():
