@@ -103,7 +103,8 @@ enum mh_kernel_kind {
     MH_MLP_JVP = 64,     /* radial MLP: derivative of its output along a direction of the features  */
     MH_MLP_BWD2 = 65,    /* derivative of its feature gradient along that direction                 */
     MH_GEOM_SEGSUM = 66, /* per-structure sums of 3x3 rows (the stress displacement's gather backward) */
-    MH_NUM_KINDS = 67
+    MH_NL_BASES = 67,    /* neighbour list: each structure's first edge slot (one workgroup)        */
+    MH_NUM_KINDS = 68
 };
 
 /* flags of mh_conv_bwd */
@@ -305,9 +306,10 @@ int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, i
  * edge_index NULL: only n_edges (size the exact layout with it, then call again).  work: caller-owned device scratch
  * of mh_neighbour_list_work_size(B, N, e_total) bytes.  Device work only (no host synchronisation, no memset), so a
  * padded build can be captured in a HIP graph; deterministic.  Bind MH_NL_SETUP with 256 threads and rows_per_block
- * 1, MH_NL_ZERO / _BINS / _PLACE with 256 and 256, MH_NL_SCAN / _OFFSETS with 1024 and 1, MH_NL_COUNT / _FILL with
- * 256 and 4 (a wave per sender).  No reference counterpart: the reference takes MACE's host-built graphs and
- * recommends fixed-size padded ones for long runs (README.md:77-78); this builds them on the GPU. */
+ * 1, MH_NL_ZERO / _BINS / _PLACE with 256 and 256, MH_NL_SCAN / _OFFSETS / _BASES with 1024 and 1 (MH_NL_OFFSETS
+ * runs one workgroup per structure), MH_NL_COUNT / _FILL with 256 and 4 (a wave per sender).  No reference
+ * counterpart: the reference takes MACE's host-built graphs and recommends fixed-size padded ones for long runs
+ * (README.md:77-78); this builds them on the GPU. */
 size_t mh_neighbour_list_work_size(int32_t B, int32_t N, int64_t e_total);
 int mh_neighbour_list(mh_module* m, const double* pos, const double* cell, const int32_t* pbc, const int64_t* ptr,
                       int32_t B, int32_t N, double r_max, int64_t e_pad, int64_t e_total, int64_t* edge_index,

@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 30; }
+int mh_version(void) { return 31; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -440,7 +440,7 @@ namespace {
 
 // Byte offsets of the neighbour list's scratch arrays (each 256-byte aligned).
 struct NLWork {
-    size_t prmd, prmi, abin, bcnt, bstart, cursor, binned, cnt, start, tot, keys, total;
+    size_t prmd, prmi, abin, bcnt, bstart, cursor, pbin, cnt, start, tot, sbase, keys, total;
 };
 
 NLWork nl_work(int64_t B, int64_t N, int64_t e_total) {
@@ -458,10 +458,11 @@ NLWork nl_work(int64_t B, int64_t N, int64_t e_total) {
     w.bcnt = take(4 * nbins);
     w.bstart = take(4 * nbins);
     w.cursor = take(4 * nbins);
-    w.binned = take(4 * N);
+    w.pbin = take(32 * N);
     w.cnt = take(8 * N);
     w.start = take(8 * N);
     w.tot = take(8 * B);
+    w.sbase = take(8 * B);
     w.keys = take(8 * (e_total > 0 ? e_total : 0));
     w.total = off;
     return w;
@@ -495,10 +496,11 @@ int mh_neighbour_list(mh_module* m, const double* pos, const double* cell, const
     int32_t* bcnt = reinterpret_cast<int32_t*>(base + w.bcnt);
     int32_t* bstart = reinterpret_cast<int32_t*>(base + w.bstart);
     int32_t* cursor = reinterpret_cast<int32_t*>(base + w.cursor);
-    int32_t* binned = reinterpret_cast<int32_t*>(base + w.binned);
+    double* pbin = reinterpret_cast<double*>(base + w.pbin);
     int64_t* cnt = reinterpret_cast<int64_t*>(base + w.cnt);
     int64_t* start = reinterpret_cast<int64_t*>(base + w.start);
     int64_t* tot = reinterpret_cast<int64_t*>(base + w.tot);
+    int64_t* sbase = reinterpret_cast<int64_t*>(base + w.sbase);
     int64_t* keys = reinterpret_cast<int64_t*>(base + w.keys);
     const int32_t nbins = N + B;
     int64_t nzero = static_cast<int64_t>(nbins) + 1;
@@ -522,21 +524,25 @@ int mh_neighbour_list(mh_module* m, const double* pos, const double* cell, const
         if ((rc = launch(m, MH_NL_SCAN, 1, args, stream, what))) return rc;
     }
     {
-        void* args[] = {&abin, &cursor, &binned, &N};
+        void* args[] = {&pos, &abin, &cursor, &pbin, &N};
         if ((rc = launch(m, MH_NL_PLACE, N, args, stream, what))) return rc;
     }
     {
-        void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &bstart, &binned, &r_max, &cnt};
+        void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &bstart, &pbin, &r_max, &cnt};
         if ((rc = launch(m, MH_NL_COUNT, N, args, stream, what))) return rc;
     }
     {
         int64_t* ei = e_total > 0 ? edge_index : nullptr;
         void* args[] = {&ptr, &B, &N, &prmi, &cnt, &e_pad, &e_total, &start, &tot, &n_edges, &ei, &unit_shifts,
                         &shifts, &out_f64};
-        if ((rc = launch(m, MH_NL_OFFSETS, 1, args, stream, what))) return rc;
+        if ((rc = launch(m, MH_NL_OFFSETS, B, args, stream, what))) return rc;
     }
     if (!edge_index || e_total == 0) return 0;
-    void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &bstart, &binned, &r_max, &cnt, &start, &tot, &e_pad,
+    {
+        void* args[] = {&tot, &B, &e_pad, &sbase};
+        if ((rc = launch(m, MH_NL_BASES, 1, args, stream, what))) return rc;
+    }
+    void* args[] = {&pos, &ptr, &B, &N, &prmd, &prmi, &bstart, &pbin, &r_max, &cnt, &start, &tot, &sbase, &e_pad,
                     &e_total, &keys, &edge_index, &unit_shifts, &shifts, &out_f64};
     return launch(m, MH_NL_FILL, N, args, stream, what);
 }

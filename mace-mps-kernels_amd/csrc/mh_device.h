@@ -19,6 +19,32 @@ __device__ __forceinline__ int mh_xcd_block(int b, int nblocks) {
 // Value of `v` in lane `j` (j wave-uniform) as a scalar.
 __device__ __forceinline__ int mh_bcast(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
 
+// Exclusive prefix sum of v over the workgroup (NW waves of 64, every thread calling), in a fixed order: an inclusive
+// scan inside each wave by shuffles, then the wave totals (through LDS `wsum`, NW entries) added in wave order.
+// `total` receives the workgroup's sum.  Two barriers; `wsum` may be reused after the call.
+template <typename T, int NW>
+__device__ __forceinline__ T mh_block_excl_scan(T v, T& total, T* wsum) {
+    const int lane = threadIdx.x & (MH_WAVE - 1), wave = threadIdx.x >> 6;
+    T inc = v;
+#pragma unroll
+    for (int off = 1; off < MH_WAVE; off <<= 1) {
+        const T t = __shfl_up(inc, off, MH_WAVE);
+        if (lane >= off) inc += t;
+    }
+    if (lane == MH_WAVE - 1) wsum[wave] = inc;
+    __syncthreads();
+    T before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const T sw = wsum[w];
+        before += w < wave ? sw : T(0);
+        all += sw;
+    }
+    __syncthreads();
+    total = all;
+    return before + inc - v;
+}
+
 // Load / store at a wave-uniform base pointer plus a 32-bit unsigned per-lane byte offset.  Written this way the
 // compiler keeps the 64-bit base in SGPRs and issues global_load/store with a 32-bit VGPR offset (saddr form), so
 // a gather from a different row costs scalar arithmetic only, no 64-bit VALU address computation per access.

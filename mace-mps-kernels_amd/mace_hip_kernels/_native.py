@@ -25,9 +25,9 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_SH_BWD2, MH_EMB_JVP, MH_EMB_BWD2, MH_GEOM_JVP, MH_READOUT_JVP, MH_READOUT_BWD2, MH_CSR_SORT, MH_MLP_HID, \
     MH_MLP_HIDB, MH_CONV_FWD_M, MH_CONV_BWD_M, MH_CONV_GYSUM, MH_SC_FWD_S, MH_SC_BWD_S, MH_SC_FWD_SI, \
     MH_SC_BWD_SI, MH_NL_SETUP, MH_NL_ZERO, MH_NL_BINS, MH_NL_SCAN, MH_NL_PLACE, MH_NL_COUNT, MH_NL_OFFSETS, \
-    MH_NL_FILL, MH_SPECIES_ORDER, MH_MLP_JVP, MH_MLP_BWD2, MH_GEOM_SEGSUM = range(67)
+    MH_NL_FILL, MH_SPECIES_ORDER, MH_MLP_JVP, MH_MLP_BWD2, MH_GEOM_SEGSUM, MH_NL_BASES = range(68)
 MH_WANT_GX, MH_WANT_GWY, MH_CUT_MASKED = 1, 2, 4
-ABI_VERSION = 30
+ABI_VERSION = 31
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')

@@ -193,29 +193,18 @@ extern "C" __global__ __launch_bounds__(256) void csr_count(const long long* __r
 extern "C" __global__ __launch_bounds__(1024) void csr_scan(const int* __restrict__ cnt, int* __restrict__ rowptr,
     int* __restrict__ cursor, int n) {
   const long long r = blockIdx.y;
-  __shared__ int s[1024];
-  __shared__ int carry;
-  if (threadIdx.x == 0) carry = 0;
-  __syncthreads();
+  __shared__ int wsum[16];
+  int carry = 0;
   for (long long base = 0; base <= n; base += 1024) {
     const long long i = base + threadIdx.x;
     const int v = i < n ? cnt[r * (n + 1) + i] : 0;
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {       // inclusive scan of the chunk
-      const int t = threadIdx.x >= off ? s[threadIdx.x - off] : 0;
-      __syncthreads();
-      s[threadIdx.x] += t;
-      __syncthreads();
-    }
-    const int excl = carry + s[threadIdx.x] - v;
+    int total;
+    const int excl = carry + mh_block_excl_scan<int, 16>(v, total, wsum);
     if (i <= n) {
       rowptr[r * (n + 1) + i] = excl;
       cursor[r * (n + 1) + i] = excl;
     }
-    __syncthreads();
-    if (threadIdx.x == 1023) carry += s[1023];
-    __syncthreads();
+    carry += total;
   }
 }
 

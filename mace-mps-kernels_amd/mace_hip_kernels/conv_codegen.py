@@ -566,7 +566,9 @@ def gxsum_block(spec):
 def _gx_sum(spec):
     """gx[s] = Σ_{e ∈ CSR_send(s)} gxm[e], summed in CSR order (deterministic); one float4 column per thread.
     ``mask`` non-NULL: edges whose mask value is -0.0 exactly have no message (``conv_bwdrc`` with masked edges
-    writes none; it would be zero) and are skipped, which leaves every sum unchanged."""
+    writes none; it would be zero) and are left out, which leaves every sum unchanged.  Their rows are still loaded
+    (in bounds, contents unset) alongside the mask, and dropped by a select: waiting for the mask before issuing the
+    message loads would add a dependent L2 round trip per group of four edges."""
     assert spec.x_dim % 4 == 0
     return [
         f'extern "C" __global__ __launch_bounds__({gxsum_block(spec)}) void {spec.kname("conv_gxsum")}(',
@@ -583,20 +585,20 @@ def _gx_sum(spec):
         '  if (mask) {',
         '    for (; p + 4 <= p1; p += 4) {',
         '      const int e0 = eids[p], e1 = eids[p + 1], e2 = eids[p + 2], e3 = eids[p + 3];',
+        '      const float4 v0 = src[(size_t)e0 * (X_DIM / 4)], v1 = src[(size_t)e1 * (X_DIM / 4)];',
+        '      const float4 v2 = src[(size_t)e2 * (X_DIM / 4)], v3 = src[(size_t)e3 * (X_DIM / 4)];',
         '      const bool k0 = __float_as_uint(mask[e0]) != 0x80000000u, k1 = __float_as_uint(mask[e1]) != 0x80000000u;',
         '      const bool k2 = __float_as_uint(mask[e2]) != 0x80000000u, k3 = __float_as_uint(mask[e3]) != 0x80000000u;',
-        '      const float4 v0 = k0 ? src[(size_t)e0 * (X_DIM / 4)] : z, v1 = k1 ? src[(size_t)e1 * (X_DIM / 4)] : z;',
-        '      const float4 v2 = k2 ? src[(size_t)e2 * (X_DIM / 4)] : z, v3 = k3 ? src[(size_t)e3 * (X_DIM / 4)] : z;',
-        '      if (k0) { acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w; }',
-        '      if (k1) { acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w; }',
-        '      if (k2) { acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w; }',
-        '      if (k3) { acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w; }',
+        '      acc.x += k0 ? v0.x : 0.0f; acc.y += k0 ? v0.y : 0.0f; acc.z += k0 ? v0.z : 0.0f; acc.w += k0 ? v0.w : 0.0f;',
+        '      acc.x += k1 ? v1.x : 0.0f; acc.y += k1 ? v1.y : 0.0f; acc.z += k1 ? v1.z : 0.0f; acc.w += k1 ? v1.w : 0.0f;',
+        '      acc.x += k2 ? v2.x : 0.0f; acc.y += k2 ? v2.y : 0.0f; acc.z += k2 ? v2.z : 0.0f; acc.w += k2 ? v2.w : 0.0f;',
+        '      acc.x += k3 ? v3.x : 0.0f; acc.y += k3 ? v3.y : 0.0f; acc.z += k3 ? v3.z : 0.0f; acc.w += k3 ? v3.w : 0.0f;',
         '    }',
         '    for (; p < p1; ++p) {',
         '      const int e = eids[p];',
-        '      if (__float_as_uint(mask[e]) == 0x80000000u) continue;',
         '      const float4 v = src[(size_t)e * (X_DIM / 4)];',
-        '      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;',
+        '      const bool k = __float_as_uint(mask[e]) != 0x80000000u;',
+        '      acc.x += k ? v.x : 0.0f; acc.y += k ? v.y : 0.0f; acc.z += k ? v.z : 0.0f; acc.w += k ? v.w : 0.0f;',
         '    }',
         '  } else {',
         '    for (; p + 4 <= p1; p += 4) {',

@@ -16,15 +16,17 @@ The build is one C-ABI call (``mh_neighbour_list``), device work only:
   nl_setup    one workgroup per structure: bounding box of its atoms, periodic image depth, a cell grid of bins at
               least r_max wide (at most n + 1 bins);
   nl_zero, nl_bins, nl_scan, nl_place
-              atoms counted into bins, bin offsets by a one-workgroup scan, atoms placed (a counting sort);
+              atoms counted into bins, bin offsets by a one-workgroup scan, atoms placed (a counting sort) as
+              (x, y, z, index) quads in bin order;
   nl_count    one wave per sender: for each image, the bins within r_max of the sender's image-shifted position are
               walked 64 candidates at a time (the bins of one grid column are contiguous, so each column is one
               range); the distance test is in float64 with no fused multiply-add, as the host computes it;
-  nl_offsets  one workgroup: per-structure edge counts (``n_edges``), padding shares, and each sender's segment start
-              in the padded (or exact) layout;
+  nl_offsets  one workgroup per structure: its edge count (``n_edges``), padding shares, and each sender's segment
+              start within the structure; nl_bases: each structure's first slot (b P padded, a prefix of the edge
+              counts exact);
   nl_fill     one wave per sender: the same walk writes each hit's key (receiver, image) into the sender's segment,
-              the segment is ordered by key (each key's rank = the number of smaller keys), and the edges and their
-              padding are written.
+              the segment is ordered by key (each key's rank = the number of smaller keys, counted in LDS), and the
+              edges and their padding are written.
 No host synchronisation and no allocation inside the call, so a padded build can be captured in a HIP graph.  A
 structure with more than ``pad_edges_to`` real edges fills its slots with a subset of its edges (in range, ordered)
 and reports its true count in ``n_edges`` (``NeighbourList.check()`` raises on it).  Without padding the edge count
@@ -39,6 +41,7 @@ from . import _native
 WAVE = 64
 SENDERS_PER_BLOCK = 4          # waves per workgroup of nl_count / nl_fill, one sender each
 NL_EPS = 1e-6                  # Å of slack in the bin ranges (bins only prune; the distance test is exact)
+LDS_KEYS = 256                 # a sender's keys ranked from LDS up to this many (longer segments from L2)
 
 
 def source():
@@ -46,6 +49,7 @@ def source():
     return _native.device_header() + f"""
 #define NL_SPB {SENDERS_PER_BLOCK}
 #define NL_EPS {NL_EPS!r}
+#define NL_LDS_KEYS {LDS_KEYS}
 """ + r"""
 #pragma clang fp contract(off)
 // per-structure parameters: prmd [B][16] doubles (lo[3], bs[3], cell rows c[9]); prmi [B][16] ints (nb[3], reps[3],
@@ -170,44 +174,40 @@ extern "C" __global__ __launch_bounds__(256) void nl_bins(const double* __restri
 
 extern "C" __global__ __launch_bounds__(1024) void nl_scan(const int* __restrict__ cnt, int* __restrict__ start,
     int* __restrict__ cursor, int n) {
-  __shared__ int s[1024];
-  __shared__ int carry;
-  if (threadIdx.x == 0) carry = 0;
-  __syncthreads();
+  __shared__ int wsum[16];
+  int carry = 0;
   for (long long base = 0; base <= n; base += 1024) {
     const long long i = base + threadIdx.x;
     const int v = i < n ? cnt[i] : 0;
-    s[threadIdx.x] = v;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int t = threadIdx.x >= off ? s[threadIdx.x - off] : 0;
-      __syncthreads();
-      s[threadIdx.x] += t;
-      __syncthreads();
-    }
+    int total;
+    const int ex = mh_block_excl_scan<int, 16>(v, total, wsum);
     if (i <= n) {
-      start[i] = carry + s[threadIdx.x] - v;
-      cursor[i] = carry + s[threadIdx.x] - v;
+      start[i] = carry + ex;
+      cursor[i] = carry + ex;
     }
-    __syncthreads();
-    if (threadIdx.x == 1023) carry += s[1023];
-    __syncthreads();
+    carry += total;
   }
 }
 
-extern "C" __global__ __launch_bounds__(256) void nl_place(const int* __restrict__ abin, int* __restrict__ cursor,
-    int* __restrict__ binned, int N) {
+// Each atom into its bin: slot p of the bin order gets (x, y, z, atom index) as four doubles, so a candidate walk
+// reads one 32-byte quad per candidate with no dependent index load.
+extern "C" __global__ __launch_bounds__(256) void nl_place(const double* __restrict__ pos,
+    const int* __restrict__ abin, int* __restrict__ cursor, double* __restrict__ pbin, int N) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   if (i >= N) return;
-  binned[atomicAdd(&cursor[abin[i]], 1)] = (int)i;
+  const long long p = atomicAdd(&cursor[abin[i]], 1);
+  pbin[4 * p] = pos[3 * i];
+  pbin[4 * p + 1] = pos[3 * i + 1];
+  pbin[4 * p + 2] = pos[3 * i + 2];
+  pbin[4 * p + 3] = (double)i;
 }
 
 // Walk sender i's candidates (one wave; every lane returns the same count).  FILL: write the key
 // (receiver - n0) * nimg + image of each hit at keys[kpos + k] for k in hit order, where kpos + k < klim.
 template <bool FILL>
 __device__ long long nl_walk(long long i, int b, const double* __restrict__ pos, const double* __restrict__ prmd,
-    const int* __restrict__ prmi, const int* __restrict__ bstart, const int* __restrict__ binned, double r_max,
-    long long* __restrict__ keys, long long kpos, long long klim) {
+    const int* __restrict__ prmi, const int* __restrict__ bstart, const double* __restrict__ pbin, double r_max,
+    long long* keys, long long kpos, long long klim) {
   const int lane = threadIdx.x & (MH_WAVE - 1);
   const double* P = prmd + NL_PD * (long long)b;
   const int* I = prmi + NL_PI * (long long)b;
@@ -244,10 +244,12 @@ __device__ long long nl_walk(long long i, int b, const double* __restrict__ pos,
           bool hit = false;
           int j = 0;
           if (t < t_last) {
-            j = binned[t];
-            const double dx = (pos[3 * (long long)j] + sx) - pix;
-            const double dy = (pos[3 * (long long)j + 1] + sy) - piy;
-            const double dz = (pos[3 * (long long)j + 2] + sz) - piz;
+            const double2 a = reinterpret_cast<const double2*>(pbin)[2 * (long long)t];
+            const double2 c = reinterpret_cast<const double2*>(pbin)[2 * (long long)t + 1];
+            j = (int)c.y;
+            const double dx = (a.x + sx) - pix;
+            const double dy = (a.y + sy) - piy;
+            const double dz = (c.x + sz) - piz;
             const double d2 = (dx * dx + dy * dy) + dz * dz;
             hit = sqrt(d2) < r_max && !(j == i && o == ozero);
           }
@@ -266,108 +268,118 @@ __device__ long long nl_walk(long long i, int b, const double* __restrict__ pos,
 
 extern "C" __global__ __launch_bounds__(MH_WAVE * NL_SPB) void nl_count(const double* __restrict__ pos,
     const long long* __restrict__ ptr, int B, int N, const double* __restrict__ prmd, const int* __restrict__ prmi,
-    const int* __restrict__ bstart, const int* __restrict__ binned, double r_max, long long* __restrict__ cnt) {
+    const int* __restrict__ bstart, const double* __restrict__ pbin, double r_max, long long* __restrict__ cnt) {
   const long long i = (long long)blockIdx.x * NL_SPB + (threadIdx.x >> 6);
   if (i >= N) return;                        // whole waves
   const int b = nl_struct_of(ptr, B, i);
-  const long long h = nl_walk<false>(i, b, pos, prmd, prmi, bstart, binned, r_max, nullptr, 0, 0);
+  const long long h = nl_walk<false>(i, b, pos, prmd, prmi, bstart, pbin, r_max, nullptr, 0, 0);
   if ((threadIdx.x & (MH_WAVE - 1)) == 0) cnt[i] = h;
 }
 
-// One workgroup: per structure the edge count n_edges[b] (its real edges, even past e_pad) and each sender's
-// segment start: b * e_pad + the exclusive prefix of (hits + padding share) over the structure's senders (e_pad > 0),
-// or the running prefix of hits over the whole batch (e_pad == 0).  A structure that needs padding but cannot have
-// any (no atoms, or a zero third lattice vector) gets n_edges[b] = -1; an atomless one's slots are filled with
-// zero-length self-loops of a neighbouring atom (their length makes the model's result NaN, never an index fault).
+// One workgroup per structure b: its edge count n_edges[b] (its real edges, even past e_pad) and each sender's
+// segment start relative to the structure's first slot: the exclusive prefix of (hits + padding share) over the
+// structure's senders.  A structure that needs padding but cannot have any (no atoms, or a zero third lattice vector)
+// gets n_edges[b] = -1; an atomless one's slots are filled with zero-length self-loops of a neighbouring atom (their
+// length makes the model's result NaN, never an index fault).
 extern "C" __global__ __launch_bounds__(1024) void nl_offsets(const long long* __restrict__ ptr, int B, int N,
     const int* __restrict__ prmi, const long long* __restrict__ cnt, long long e_pad, long long e_total,
     long long* __restrict__ start, long long* __restrict__ tot, int* __restrict__ n_edges,
     long long* __restrict__ edge_index, void* __restrict__ ushift, void* __restrict__ shift, int f64) {
-  __shared__ long long s[1024];
-  __shared__ long long carry;
-  const int t = threadIdx.x;
-  long long run = 0;                         // exact layout: edges of the structures before b
-  for (int b = 0; b < B; ++b) {
-    const long long n0 = ptr[b], n1 = ptr[b + 1], n = n1 - n0;
-    long long part = 0;
-    for (long long i = n0 + t; i < n1; i += 1024) part += cnt[i];
-    s[t] = part;
-    __syncthreads();
-    for (int w = 512; w > 0; w >>= 1) {
-      if (t < w) s[t] += s[t + w];
-      __syncthreads();
-    }
-    const long long total = s[0];
-    __syncthreads();
-    const long long extra = e_pad > 0 && total < e_pad ? e_pad - total : 0;
-    const bool unpaddable = extra > 0 && (n == 0 || prmi[NL_PI * (long long)b + 10] == 0);
-    if (t == 0) {
-      tot[b] = total;
-      n_edges[b] = unpaddable ? -1 : (total < 0x7fffffffLL ? (int)total : 0x7fffffff);
-      carry = e_pad > 0 ? (long long)b * e_pad : run;
-    }
-    if (n == 0 && extra > 0 && edge_index && N > 0) {
-      const long long a = n0 < N ? n0 : N - 1;
-      for (long long p = t; p < e_pad; p += 1024) {
-        const long long e = (long long)b * e_pad + p;
-        edge_index[e] = a;
-        edge_index[e_total + e] = a;
-        for (int k = 0; k < 3; ++k) {
-          if (f64) { ((double*)ushift)[3 * e + k] = 0.0; ((double*)shift)[3 * e + k] = 0.0; }
-          else { ((float*)ushift)[3 * e + k] = 0.0f; ((float*)shift)[3 * e + k] = 0.0f; }
-        }
+  __shared__ long long wsum[16];
+  const int t = threadIdx.x, b = blockIdx.x;
+  if (b >= B) return;
+  const long long n0 = ptr[b], n1 = ptr[b + 1], n = n1 - n0;
+  long long part = 0;
+  for (long long i = n0 + t; i < n1; i += 1024) part += cnt[i];
+  long long total;
+  mh_block_excl_scan<long long, 16>(part, total, wsum);
+  const long long extra = e_pad > 0 && total < e_pad ? e_pad - total : 0;
+  const bool unpaddable = extra > 0 && (n == 0 || prmi[NL_PI * (long long)b + 10] == 0);
+  if (t == 0) {
+    tot[b] = total;
+    n_edges[b] = unpaddable ? -1 : (total < 0x7fffffffLL ? (int)total : 0x7fffffff);
+  }
+  if (n == 0 && extra > 0 && edge_index && N > 0) {
+    const long long a = n0 < N ? n0 : N - 1;
+    for (long long p = t; p < e_pad; p += 1024) {
+      const long long e = (long long)b * e_pad + p;
+      edge_index[e] = a;
+      edge_index[e_total + e] = a;
+      for (int k = 0; k < 3; ++k) {
+        if (f64) { ((double*)ushift)[3 * e + k] = 0.0; ((double*)shift)[3 * e + k] = 0.0; }
+        else { ((float*)ushift)[3 * e + k] = 0.0f; ((float*)shift)[3 * e + k] = 0.0f; }
       }
     }
-    __syncthreads();
-    for (long long base = n0; base < n1; base += 1024) {
-      const long long i = base + t;
-      long long v = 0;
-      if (i < n1) {
-        const long long il = i - n0;
-        v = cnt[i] + (extra > 0 ? extra / n + (il < extra % n ? 1 : 0) : 0);
-      }
-      s[t] = v;
-      __syncthreads();
-      for (int off = 1; off < 1024; off <<= 1) {
-        const long long a = t >= off ? s[t - off] : 0;
-        __syncthreads();
-        s[t] += a;
-        __syncthreads();
-      }
-      if (i < n1) start[i] = carry + s[t] - v;
-      __syncthreads();
-      if (t == 1023) carry += s[1023];
-      __syncthreads();
+  }
+  long long carry = 0;
+  for (long long base = n0; base < n1; base += 1024) {
+    const long long i = base + t;
+    long long v = 0;
+    if (i < n1) {
+      const long long il = i - n0;
+      v = cnt[i] + (extra > 0 ? extra / n + (il < extra % n ? 1 : 0) : 0);
     }
-    run += total;
+    long long chunk;
+    const long long ex = mh_block_excl_scan<long long, 16>(v, chunk, wsum);
+    if (i < n1) start[i] = carry + ex;
+    carry += chunk;
+  }
+}
+
+// The first slot of each structure: b * e_pad (padded layout) or the running total of the edge counts of the
+// structures before b (exact layout), one workgroup.
+extern "C" __global__ __launch_bounds__(1024) void nl_bases(const long long* __restrict__ tot, int B, long long e_pad,
+    long long* __restrict__ sbase) {
+  __shared__ long long wsum[16];
+  long long carry = 0;
+  for (long long b0 = 0; b0 < B; b0 += 1024) {
+    const long long b = b0 + threadIdx.x;
+    const long long v = b < B ? tot[b] : 0;
+    long long chunk;
+    const long long ex = mh_block_excl_scan<long long, 16>(v, chunk, wsum);
+    if (b < B) sbase[b] = e_pad > 0 ? b * e_pad : carry + ex;
+    carry += chunk;
   }
 }
 
 extern "C" __global__ __launch_bounds__(MH_WAVE * NL_SPB) void nl_fill(const double* __restrict__ pos,
     const long long* __restrict__ ptr, int B, int N, const double* __restrict__ prmd, const int* __restrict__ prmi,
-    const int* __restrict__ bstart, const int* __restrict__ binned, double r_max, const long long* __restrict__ cnt,
-    const long long* __restrict__ start, const long long* __restrict__ tot, long long e_pad, long long e_total,
-    long long* __restrict__ keys, long long* __restrict__ edge_index, void* __restrict__ ushift,
+    const int* __restrict__ bstart, const double* __restrict__ pbin, double r_max, const long long* __restrict__ cnt,
+    const long long* __restrict__ start, const long long* __restrict__ tot, const long long* __restrict__ sbase,
+    long long e_pad, long long e_total, long long* __restrict__ keys, long long* __restrict__ edge_index,
+    void* __restrict__ ushift,
     void* __restrict__ shift, int f64) {
   const long long i = (long long)blockIdx.x * NL_SPB + (threadIdx.x >> 6);
   if (i >= N) return;                        // whole waves
   const int lane = threadIdx.x & (MH_WAVE - 1);
   const int b = nl_struct_of(ptr, B, i);
-  const long long kpos = start[i];
+  const long long kpos = sbase[b] + start[i];
   const long long klim = e_pad > 0 ? (long long)b * e_pad + e_pad : e_total;
-  nl_walk<true>(i, b, pos, prmd, prmi, bstart, binned, r_max, keys, kpos, klim);
-  __threadfence();                           // this wave's key stores before its loads below
+  const long long h = cnt[i];
+  const long long L = kpos >= klim ? 0 : (h < klim - kpos ? h : klim - kpos);
+  // the walk writes the keys of a segment of up to NL_LDS_KEYS edges into this wave's LDS region (h is known from
+  // the count pass), a longer segment's into global memory; the ranking below reads them back from there
+  __shared__ long long skeys[NL_SPB][NL_LDS_KEYS];
+  const bool in_lds = L <= NL_LDS_KEYS;
+  long long* sk = skeys[threadIdx.x >> 6];
+  if (in_lds) {
+    nl_walk<true>(i, b, pos, prmd, prmi, bstart, pbin, r_max, sk, 0, L);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  } else {
+    nl_walk<true>(i, b, pos, prmd, prmi, bstart, pbin, r_max, keys, kpos, klim);
+    __threadfence();                         // this wave's key stores before its loads below
+  }
+  const long long* kk = in_lds ? sk : keys + kpos;
   const double* P = prmd + NL_PD * (long long)b;
   const int* I = prmi + NL_PI * (long long)b;
   const long long n0 = I[6], n = I[7];
   const int nimg = I[8], r0 = I[3], r1 = I[4], r2 = I[5], kz = I[10];
   const int ny = 2 * r1 + 1, nz = 2 * r2 + 1;
-  const long long h = cnt[i];
-  const long long L = kpos >= klim ? 0 : (h < klim - kpos ? h : klim - kpos);
   for (long long p = lane; p < L; p += MH_WAVE) {
-    const long long kp = keys[kpos + p];
+    const long long kp = kk[p];
     long long rank = 0;
-    for (long long q = 0; q < L; ++q) rank += keys[kpos + q] < kp;
+    for (long long q = 0; q < L; ++q) rank += kk[q] < kp;
     const long long e = kpos + rank;
     const int o = (int)(kp % nimg);
     const double oi = (double)(o / (ny * nz) - r0), oj = (double)((o / nz) % ny - r1), ok = (double)(o % nz - r2);
@@ -411,12 +423,13 @@ def _module(device):
         code = _native.compile_source(source())
         with torch.cuda.device(idx):
             m = _native.Module(code, {_native.MH_NL_SETUP: ('nl_setup', 256, 1),
+                                      _native.MH_NL_BASES: ('nl_bases', 1024, 1),
                                       _native.MH_NL_ZERO: ('nl_zero', 256, 256),
                                       _native.MH_NL_BINS: ('nl_bins', 256, 256),
                                       _native.MH_NL_SCAN: ('nl_scan', 1024, 1),
                                       _native.MH_NL_PLACE: ('nl_place', 256, 256),
                                       _native.MH_NL_COUNT: ('nl_count', WAVE * SENDERS_PER_BLOCK, SENDERS_PER_BLOCK),
-                                      _native.MH_NL_OFFSETS: ('nl_offsets', 1024, 1),
+                                      _native.MH_NL_OFFSETS: ('nl_offsets', 1024, 1),  # one workgroup per structure
                                       _native.MH_NL_FILL: ('nl_fill', WAVE * SENDERS_PER_BLOCK, SENDERS_PER_BLOCK)})
         _MODULES[idx] = m
     return m
