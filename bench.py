@@ -155,8 +155,9 @@ def _cpu_model():
     return platform.processor() or platform.machine()
 
 
-def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, **kw):
-    """Unpatched e3nn-path restatement on the host CPU over the first ``sample`` structures of the batch."""
+def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, min_seconds=10.0, **kw):
+    """Unpatched e3nn-path restatement on the host CPU over the first ``sample`` structures of the batch: at least
+    ``steps`` timed calls and at least ``min_seconds`` of them (a bounded sample of ~10 s of CPU work)."""
     import torch
     from mace_lite import data as D
     cores = len(os.sched_getaffinity(0))
@@ -175,8 +176,11 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, **kw):
     kw = kw or dict(compute_force=True)
     model(D.fresh(sub), **kw)                                     # warm-up
     t0 = time.perf_counter()
-    for _ in range(steps):
+    done = 0
+    while done < steps or time.perf_counter() - t0 < min_seconds:
         model(D.fresh(sub), **kw)
+        done += 1
+    steps = done
     dt = (time.perf_counter() - t0) / steps
     per_call = dt * n_structs / k                                 # scaled to the full batch
     return dict(value=round(1.0 / per_call, 5), unit='E+F calls/s', cores=cores, kind='port',
@@ -187,7 +191,7 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, **kw):
 
 
 # symbol prefixes of this package's generated kernels
-HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_', 'ro_')
+HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_', 'ro_', 'nl_', 'csr_', 'species_')
 COPY_BYTES = 1 << 30          # size of the calibration copy (read 1 GiB, write 1 GiB) of --profile
 
 
@@ -381,6 +385,46 @@ def _isolated_radial(a, timed, report, blk, op, li, t, nb, graph, rnd):
     op.detach_mlp()
 
 
+def _neighbour_lists(a):
+    """GPU neighbour-list builds (mace_hip_kernels.neighbours) on a configuration's structures: ms per build from
+    HIP events over K builds after W warm-ups, in the configuration's layout (config 2: padded to 6,000 edges per
+    structure; the others exact, whose one edge-count read-back is inside the timed build), checked against the
+    host cKDTree builder, which is timed beside it.  One JSON line."""
+    import numpy as np
+    import torch
+    from mace_hip_kernels import neighbour_list
+    from mace_lite import data as D
+    from mace_lite import factory
+    dev = torch.device('cuda:0')
+    st = factory.structures(a.config)
+    ss, r_max, pad = st['structures'], st['r_max'], st['pad_edges_to']
+    pos = torch.tensor(np.concatenate([s_.positions for s_ in ss]), dtype=torch.float64, device=dev)
+    cell = torch.tensor(np.stack([s_.cell for s_ in ss]), dtype=torch.float64, device=dev)
+    pbc = torch.tensor([[bool(v) for v in s_.pbc] for s_ in ss], device=dev)
+    ptr = torch.tensor(np.concatenate([[0], np.cumsum([len(s_) for s_ in ss])]), dtype=torch.int64, device=dev)
+    for _ in range(a.warmup):
+        nl = neighbour_list(pos, cell, ptr, r_max, pbc=pbc, pad_edges_to=pad, dtype=torch.float32)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(a.steps):
+        nl = neighbour_list(pos, cell, ptr, r_max, pbc=pbc, pad_edges_to=pad, dtype=torch.float32)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / a.steps
+    nl.check()
+    t_host = time.perf_counter()
+    ref = D.batch_graphs([D.graph_of(s_, r_max) for s_ in ss], st['elements'], torch.float32, 'cpu',
+                         pad_edges_to=pad, r_max=r_max)
+    t_host = time.perf_counter() - t_host
+    same = bool(torch.equal(nl.edge_index.cpu(), ref['edge_index']) and torch.equal(nl.shifts.cpu(), ref['shifts']))
+    print(json.dumps(dict(workload=st['name'], atoms=int(pos.shape[0]), structures=len(ss),
+                          edges=int(nl.edge_index.shape[1]), real_edges=int(nl.n_edges.sum()), layout=(
+                              f'padded to {pad} per structure' if pad else 'exact'),
+                          gpu_ms_per_build=round(ms, 4), host_ckdtree_ms=round(t_host * 1e3, 2),
+                          equal_to_host_builder=same)), flush=True)
+
+
 def _profile(a):
     """Patched E+F calls only (for rocprofv3), then a plain elementwise copy of known size whose FETCH_SIZE and
     WRITE_SIZE calibrate the counters."""
@@ -513,18 +557,21 @@ def main():
                     help='workload (default 2; 4 with --isolated)')
     ap.add_argument('--isolated', action='store_true', help='time each HIP kernel alone (config 4 by default)')
     ap.add_argument('--cpu-sample', type=int, default=4, help='structures in the CPU-baseline sample')
-    ap.add_argument('--cpu-steps', type=int, default=2)
+    ap.add_argument('--cpu-steps', type=int, default=2, help='at least this many timed CPU-baseline calls')
+    ap.add_argument('--cpu-seconds', type=float, default=10.0, help='and at least this many seconds of them')
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--no-e3nn', action='store_true')
     ap.add_argument('--no-double-backward', action='store_true', help='skip the force-loss step timing')
     ap.add_argument('--no-graph', action='store_true', help='report the eager call instead of the captured one')
     ap.add_argument('--no-sweep', action='store_true', help='skip the batch 1/4/16 E+F timings (config 2)')
+    ap.add_argument('--neighbour-list', action='store_true',
+                    help='time the GPU neighbour list on the configuration (default 2) against the host builder')
     ap.add_argument('--fuse-radial', action='store_true',
                     help="patch_model(fuse_radial=True): the radial MLP's output layer inside the convolution")
     a = ap.parse_args()
     if a.config is None:
         a.config = 4 if a.isolated else 2
-    if a.config == 4 and not a.isolated:
+    if a.config == 4 and not (a.isolated or a.neighbour_list):
         ap.error('config 4 is an isolated-kernel workload: add --isolated')
     if a.summarize_rocprof:
         _summarize(a)
@@ -542,6 +589,9 @@ def main():
     assert torch.cuda.is_available(), 'bench.py needs a GPU'
     if a.profile:
         _profile(a)
+        return
+    if a.neighbour_list:
+        _neighbour_lists(a)
         return
     if a.isolated:
         _isolated(a)
@@ -728,7 +778,8 @@ def main():
 
     cpu = None
     if not a.no_cpu:
-        cpu = _cpu_baseline(copy.deepcopy(model), batch_cpu, n_structs, a.cpu_sample, a.cpu_steps, **kw)
+        cpu = _cpu_baseline(copy.deepcopy(model), batch_cpu, n_structs, a.cpu_sample, a.cpu_steps,
+                            min_seconds=a.cpu_seconds, **kw)
         _log('cpu baseline:', cpu)
 
     # HBM traffic of the dominant kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE run of this workload

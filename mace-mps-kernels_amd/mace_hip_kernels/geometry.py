@@ -315,12 +315,15 @@ def symmetric_displacement(positions, unit_shifts, cell, edge_index, num_graphs,
     displacement.requires_grad_(True)
     sym = 0.5 * (displacement + displacement.transpose(-1, -2))
     seg_atoms = ptr.to(torch.int64).contiguous()
-    positions = positions + torch.einsum('be,bec->bc', positions, _GraphGather.apply(sym, batch, None, seg_atoms))
+    # row vector times a 3x3 matrix per row, as a broadcast product and a sum over three terms: the einsum / matmul
+    # of MACE's expression become batched GEMMs of 3x3 blocks on the GPU (hipBLASLt launches of tens of us each)
+    positions = positions + (positions.unsqueeze(-1) * _GraphGather.apply(sym, batch, None, seg_atoms)).sum(-2)
     cell = cell.view(-1, 3, 3)
-    cell = cell + torch.matmul(cell, sym)
+    cell = cell + (cell.unsqueeze(-1) * sym.unsqueeze(-3)).sum(-2)
     rp_s, ei_s = _conv.graph_for(edge_index, n).by_send()
     seg_edges = rp_s.to(torch.int64)[seg_atoms].contiguous()
-    shifts = torch.einsum('be,bec->bc', unit_shifts, _GraphGather.apply(cell, batch[sender], ei_s, seg_edges))
+    cells = _GraphGather.apply(cell, batch[sender], ei_s, seg_edges)
+    shifts = (unit_shifts.unsqueeze(-1) * cells).sum(-2)
     return positions, shifts, displacement
 
 

@@ -1,9 +1,9 @@
 """
 One patched model call captured as a HIP graph.
 
-An energy+forces call of MACE issues about a thousand small launches from Python (linears, radial MLP, spherical
-harmonics, scatter, autograd), so at the sizes of a batch of ~160-atom structures it is bound by host launch cost,
-not by the GPU.  For a fixed graph (fixed atoms and edge list, as with padded batches or an MD neighbour list with a
+An energy+forces call of the patched MACE model still issues about 150 launches from Python (the HIP kernels plus
+PyTorch's scatter, sums and autograd bookkeeping); unpatched it issues about a thousand, and at the sizes of a batch
+of ~160-atom structures such a call is bound by host launch cost, not by the GPU.  For a fixed graph (fixed atoms and edge list, as with padded batches or an MD neighbour list with a
 skin) the whole call — forward, ``autograd.grad`` and the HIP kernels — can be captured once and replayed:
 
     from mace_hip_kernels import patch_model
@@ -16,8 +16,8 @@ skin) the whole call — forward, ``autograd.grad`` and the HIP kernels — can 
 
 What is frozen: the tensors of ``batch`` (their addresses and shapes).  By default the edge list's content is frozen
 too — the CSRs the convolution kernels read are built by the eager warm-up and reused; after a neighbour-list
-rebuild, capture again.  With ``rebuild_graph=True`` the captured call also rebuilds the CSRs (a stable device sort
-per direction) from the current contents of ``batch['edge_index']``, so a neighbour list of the same size (padded)
+rebuild, capture again.  With ``rebuild_graph=True`` the captured call also rebuilds the CSRs (``mh_graph_build``: a
+counting sort per direction) from the current contents of ``batch['edge_index']``, so a neighbour list of the same size (padded)
 can be copied in before each replay.  Those rebuilt graphs cannot be validated on the host inside the graph: node
 indices are clamped into range instead (a bad edge list gives wrong numbers, never a bad memory access).  The caller
 must not resize or reallocate the batch tensors while the capture is in use.
