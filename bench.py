@@ -191,7 +191,7 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, min_seconds=10.0, 
 
 
 # symbol prefixes of this package's generated kernels
-HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_', 'ro_', 'nl_', 'csr_', 'species_')
+HIP_KERNEL_PREFIXES = ('conv_', 'sc_', 'lin_', 'mlp_', 'emb_', 'sh_', 'perm_', 'geom_', 'ro_', 'nl_', 'csr_', 'species_', 'edge_')
 COPY_BYTES = 1 << 30          # size of the calibration copy (read 1 GiB, write 1 GiB) of --profile
 
 
@@ -738,6 +738,29 @@ def main():
     for m_ in convs:
         m_.skip_masked = True
     conv_all_edges = {k: round(v[1], 5) for k, v in tm_all.summary().items() if k.startswith('conv_bwd')}
+    # the captured call with each radial MLP as an autograd node of its own (W0 and dL/dW0 for every edge, zero rows
+    # included), for comparison with the model path that runs the MLP inside the convolution's node
+    sep_ms = None
+    deferred = [(m_, m_.deferred_mlp()) for m_ in convs if m_.deferred_mlp() is not None]
+    if deferred and not a.no_graph:
+        from mace_hip_kernels.graphs import capture
+        for m_, mlp_ in deferred:
+            m_.defer_mlp(None)
+            mlp_.fuse = False
+        sb = D.fresh(batch)
+        call = capture(met, sb, **kw)
+        for _ in range(a.warmup):
+            call.replay()
+        sync()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            call.replay()
+        sync()
+        sep_ms = round((time.perf_counter() - t0) / a.steps * 1e3, 4)
+        del call, sb
+        for m_, mlp_ in deferred:
+            m_.defer_mlp(mlp_)
+            mlp_.fuse = True
     # per-op forward + backward ms per call, the reference's per-op rows (its README.md:60-62: convolution layers 1
     # and 2, symmetric contractions 1 and 2, measured on config 1's structure)
     per_op = {}
@@ -852,6 +875,7 @@ def main():
         'batch_sweep': sweep,
         'calls': 'energy + forces + stress' if kw['compute_stress'] else 'energy + forces',
         'conv_bwd_ms_every_edge_walked': conv_all_edges,
+        'ms_per_step_mlp_as_separate_node': sep_ms,
         'graph_replay_check': graph_check,
         'conv_hbm_gbs': round(conv_bytes / (conv_ms * 1e-3) / 1e9, 1) if conv_ms else None,
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': d['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',

@@ -104,7 +104,9 @@ enum mh_kernel_kind {
     MH_MLP_BWD2 = 65,    /* derivative of its feature gradient along that direction                 */
     MH_GEOM_SEGSUM = 66, /* per-structure sums of 3x3 rows (the stress displacement's gather backward) */
     MH_NL_BASES = 67,    /* neighbour list: each structure's first edge slot (one workgroup)        */
-    MH_NUM_KINDS = 68
+    MH_EDGE_COUNT = 68,  /* edge compaction: kept edges per workgroup of 4096                       */
+    MH_EDGE_PLACE = 69,  /* edge compaction: the row list                                           */
+    MH_NUM_KINDS = 70
 };
 
 /* flags of mh_conv_bwd */
@@ -113,6 +115,8 @@ enum mh_kernel_kind {
 /* flag of mh_conv_bwd_recv (factored weights only): cutoff[e] == -0.0 exactly marks an edge outside the cutoff
  * envelope's support, where the envelope's derivative is zero */
 #define MH_CUT_MASKED 4
+/* with MH_CUT_MASKED: the masked edges' gW rows are left unwritten (not zeroed) */
+#define MH_CUT_NOZERO 8
 
 /* Message of the last failing call on this thread ("" if none).  No reference counterpart (Metal errors surface
  * from torch there). */
@@ -200,7 +204,8 @@ int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, co
  * the envelope's support (mace_hip_kernels' radial embedding writes -0.0 there, where the envelope's derivative is
  * zero): its gW, gY and g_cutoff rows are written as zeros without reading W0 or x, and it has no dX message.  Only
  * g_cutoff differs from the unmasked call (it is the exact partial derivative there), and only where whatever
- * produced the cutoff multiplies it by a zero derivative. */
+ * produced the cutoff multiplies it by a zero derivative.  MH_CUT_NOZERO as well: the masked edges' gW rows are
+ * not written at all (for a caller whose consumer of gW skips them, as mh_mlp_bwd_rows does). */
 int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
                      const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
                      const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
@@ -417,6 +422,25 @@ int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* W
                void* stream);
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream);
+/* The same over a row list: slot i < count[0] computes edge rows[i] (W0 row, or gef row from the gW0 row); the
+ * edges of the slots from count[0] to E - 1 are not computed: mh_mlp_fwd_rows leaves their W0 rows unwritten and
+ * mh_mlp_bwd_rows writes zero gef rows for them without reading their gW0 rows.  rows [E] int32 is a permutation
+ * of 0 .. E - 1 and count [1] int32 lives on the device (both from mh_edge_compact: the edges inside the cutoff's
+ * support first), so no host synchronisation is needed; rows and count both NULL is mh_mlp_fwd / mh_mlp_bwd.  No
+ * reference counterpart. */
+int mh_mlp_fwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E,
+                    const int32_t* rows, const int32_t* count, void* stream);
+int mh_mlp_bwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
+                    int64_t E, const int32_t* rows, const int32_t* count, void* stream);
+
+/* The edge rows of a cutoff column (cutoff [E] fp32): rows [E] int32 = the edges whose cutoff is not -0.0 exactly
+ * (inside the cutoff envelope's support, as mace_hip_kernels' radial embedding marks it), in increasing order, then
+ * the others; count [1] int32 = how many are inside.  work: device scratch of mh_edge_compact_work_size(E) bytes.
+ * Module of conv.graph_source(); bind MH_EDGE_COUNT and MH_EDGE_PLACE with 1024 threads and 4096 edges per block.
+ * Deterministic (no atomics), device work only.  No reference counterpart (the reference has no edge masks). */
+size_t mh_edge_compact_work_size(int64_t E);
+int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows, int32_t* count, void* work,
+                    void* stream);
 
 /* Second derivatives of the radial MLP, behind a double backward (ev [E, n_basis] a direction of the features):
  * mh_mlp_jvp writes dW0 = (dW0/def) ev [E, n_out], the gradient of <ev, dL/def> with respect to gW0; mh_mlp_bwd2

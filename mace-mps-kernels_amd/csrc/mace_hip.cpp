@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 31; }
+int mh_version(void) { return 32; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -291,10 +291,12 @@ int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* 
     if (cutoff && !g_cutoff) return fail(-1, "mh_conv_bwd_recv: cutoff given but g_cutoff is NULL");
     const bool masked = (flags & MH_CUT_MASKED) != 0;
     if (masked && !cutoff) return fail(-1, "mh_conv_bwd_recv: MH_CUT_MASKED needs the factored form (cutoff)");
+    const bool nozero = (flags & MH_CUT_NOZERO) != 0;
+    if (nozero && !masked) return fail(-1, "mh_conv_bwd_recv: MH_CUT_NOZERO needs MH_CUT_MASKED");
     const bool want_gx = (flags & MH_WANT_GX) != 0;
     if (want_gx && (!gx || !work || !rowptr_s || !eids_s))
         return fail(-1, "mh_conv_bwd_recv: gx requested but gx, work or the sender CSR is NULL");
-    int32_t kflags = (want_gx ? 1 : 0) | (masked ? 2 : 0);
+    int32_t kflags = (want_gx ? 1 : 0) | (masked ? 2 : 0) | (nozero ? 4 : 0);
     int rc;
     if (cutoff) {
         void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags, &cutoff,
@@ -701,17 +703,47 @@ int mh_readout_bwd(mh_module* m, const float* x, const float* g, float* gx, int6
     return launch(m, MH_READOUT_BWD, N, args, stream, "mh_readout_bwd");
 }
 
-int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E, void* stream) {
+int mh_mlp_fwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E,
+                    const int32_t* rows, const int32_t* count, void* stream) {
     if (E > 0 && (!ef || !Wh || !Wl || !W0)) return fail(-1, "mh_mlp_fwd: NULL operand");
-    void* args[] = {&ef, &Wh, &Wl, &W0, &E};
+    if ((rows == nullptr) != (count == nullptr)) return fail(-1, "mh_mlp_fwd_rows: rows and count go together");
+    void* args[] = {&ef, &Wh, &Wl, &W0, &E, &rows, &count};
     return launch(m, MH_MLP_FWD, E, args, stream, "mh_mlp_fwd");
+}
+
+int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E, void* stream) {
+    return mh_mlp_fwd_rows(m, ef, Wh, Wl, W0, E, nullptr, nullptr, stream);
+}
+
+int mh_mlp_bwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
+                    int64_t E, const int32_t* rows, const int32_t* count, void* stream) {
+    if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef)) return fail(-1, "mh_mlp_bwd: NULL operand");
+    if ((rows == nullptr) != (count == nullptr)) return fail(-1, "mh_mlp_bwd_rows: rows and count go together");
+    void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E, &rows, &count};
+    return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
 }
 
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream) {
-    if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef)) return fail(-1, "mh_mlp_bwd: NULL operand");
-    void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E};
-    return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
+    return mh_mlp_bwd_rows(m, ef, Wh, Wl, gW0, gef, E, nullptr, nullptr, stream);
+}
+
+size_t mh_edge_compact_work_size(int64_t E) {
+    const int64_t nb = E > 0 ? (E + 4095) / 4096 : 1;
+    return (size_t)nb * sizeof(int32_t);
+}
+
+int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows, int32_t* count, void* work,
+                    void* stream) {
+    if (E < 0 || E >= 0x7fffffffLL) return fail(-1, "mh_edge_compact: bad edge count");
+    if (!count || !work || (E > 0 && (!cutoff || !rows))) return fail(-1, "mh_edge_compact: NULL operand");
+    int32_t nb = (int32_t)(E > 0 ? (E + 4095) / 4096 : 1);       // one workgroup also for E == 0: count = 0
+    int32_t* bc = static_cast<int32_t*>(work);
+    void* a1[] = {&cutoff, &E, &bc};
+    int rc = launch_blocks(m, MH_EDGE_COUNT, nb, a1, stream, "mh_edge_compact");
+    if (rc) return rc;
+    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count};
+    return launch_blocks(m, MH_EDGE_PLACE, nb, a2, stream, "mh_edge_compact");
 }
 
 int mh_mlp_jvp(mh_module* m, const float* ef, const float* ev, const float* Wh, const uint16_t* Wl, float* dW0,

@@ -13,8 +13,10 @@ Replaces, where supported (reference __init__.py:1-14):
     interaction block's radial MLP (``conv_tp_weights``), the radial embedding of the edge lengths, and the
     per-node layout permutation (``reshape_irreps``) in front of each symmetric contraction, and the edge geometry
     (``get_edge_vectors_and_lengths``, routed to the kernels while the patched model runs).
-Everything else stays on the original e3nn / PyTorch path.  Inference only: the backward pass is first order
-(energies, forces, stress, finite-difference Hessians, MD, relaxations); double backward raises.
+Everything else stays on the original e3nn / PyTorch path.  The backward pass is first order by default
+(energies, forces, stress, MD, relaxations) and a double backward raises, as in the reference;
+``patch_model(model, double_backward=True)`` makes every drop-in differentiable once more (force-loss gradients,
+Hessian-vector products).  The graph itself can be built on the GPU (``neighbour_list``).
 
 The kernels are generated per layer with the layer's coefficients as literals, compiled by hipRTC through
 ``libmace_hip.so`` (C ABI in include/mace_hip.h) and launched on torch's current HIP stream.  If that library cannot
@@ -35,6 +37,7 @@ from .layout import HipReshapeIrreps, reshape_supported
 from .readout import HipReadout, readout_supported
 from .symmetric import HipSymmetricContraction, sc_supported
 from . import _native
+from . import conv as _conv
 from . import geometry as _geometry
 from .conv import check_graphs
 from .neighbours import NeighbourList, neighbour_list, update_batch
@@ -86,7 +89,10 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     per-edge weights cutoff * MLP(edge_feats) inside its kernels from the MLP's last hidden activations, so the
     weights and their gradient are never stored (HipConvTP.attach_mlp).  Off, the MLP's kernels write the weights and
     the convolution reads them, which measures faster on MI355X for the benchmark models: the fused kernels save the
-    weights' HBM round trip but spend more on the VALU than the round trip costs.
+    weights' HBM round trip but spend more on the VALU than the round trip costs.  The MLP's kernels then run inside
+    the convolution's autograd node (HipConvTP.defer_mlp; ``conv.DEFER_RADIAL``), so that both skip the rows of the
+    edges outside the cutoff's support (padding edges, edges past r_max) whenever the cutoff comes unmodified from
+    the patched radial embedding.
 
     ``double_backward`` (default off, as in the reference, where a backward under ``create_graph=True`` raises)
     makes the patched modules' gradients differentiable once more, for second derivatives with respect to the
@@ -146,8 +152,10 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
         # the fused kernels have no second-order form
         for blk in getattr(model, 'interactions', []):
             cv, mlp = getattr(blk, 'conv_tp', None), getattr(blk, 'conv_tp_weights', None)
-            if isinstance(cv, HipConvTP) and cv.fused_mlp() is not None:
-                cv.detach_mlp()
+            if isinstance(cv, HipConvTP):
+                if cv.fused_mlp() is not None:
+                    cv.detach_mlp()
+                cv.defer_mlp(None)
             if isinstance(mlp, HipRadialMLP):
                 mlp.fuse = False
     if spherical_harmonics and hasattr(model, 'spherical_harmonics'):
@@ -201,6 +209,14 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             if isinstance(cv, HipConvTP) and isinstance(mlp, HipRadialMLP) and cv.fused_mlp() is not mlp:
                 ok, _ = cv.attach_mlp(mlp)
                 mlp.fuse = ok
+    if not double_backward and _conv.DEFER_RADIAL:
+        # every other convolution runs its radial MLP's kernels inside its own autograd node (the MLP's output
+        # handed over unformed), so that both skip the edges outside the cutoff's support
+        for blk in getattr(model, 'interactions', []):
+            cv, mlp = getattr(blk, 'conv_tp', None), getattr(blk, 'conv_tp_weights', None)
+            if isinstance(cv, HipConvTP) and isinstance(mlp, HipRadialMLP) and cv.fused_mlp() is None:
+                cv.defer_mlp(mlp)
+                mlp.fuse = True
     if layouts:
         for i, blk in enumerate(getattr(model, 'interactions', [])):
             name = f'interactions.{i}.reshape'

@@ -276,10 +276,53 @@ extern "C" __global__ __launch_bounds__(256) void csr_sort_long(const int* __res
   if (in_lds)
     for (int i = threadIdx.x; i < L; i += 256) seg[i] = s[i];
 }
+
+// Edge rows of a masked cutoff (mh_edge_compact): the edges whose cutoff is not -0.0 (inside the cutoff envelope's
+// support) in increasing order from the front, the others from the back, and their number.  Workgroups of
+// EC_EDGES edges (1024 threads x 4): edge_count writes each workgroup's count of kept edges, edge_place adds the
+// counts of the workgroups before its own and places its edges by a block scan.  No atomics: the order is fixed.
+#define EC_EDGES 4096
+__device__ __forceinline__ int ec_keep(const float* __restrict__ cut, long long e, long long E) {
+  return e < E && __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
+}
+
+extern "C" __global__ __launch_bounds__(1024) void edge_count(const float* __restrict__ cut, long long E,
+    int* __restrict__ bc) {
+  __shared__ int wsum[16];
+  const long long e0 = (long long)blockIdx.x * EC_EDGES + 4 * threadIdx.x;
+  int c = 0;
+  for (int k = 0; k < 4; ++k) c += ec_keep(cut, e0 + k, E);
+  int total;
+  mh_block_excl_scan<int, 16>(c, total, wsum);
+  if (threadIdx.x == 0) bc[blockIdx.x] = total;
+}
+
+extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __restrict__ cut, long long E,
+    const int* __restrict__ bc, int nb, int* __restrict__ rows, int* __restrict__ count) {
+  __shared__ int wsum[16];
+  const int b = blockIdx.x;
+  int part = 0;                           // kept edges of the workgroups before this one
+  for (int j = threadIdx.x; j < b; j += 1024) part += bc[j];
+  int off;
+  mh_block_excl_scan<int, 16>(part, off, wsum);
+  const long long e0 = (long long)b * EC_EDGES + 4 * threadIdx.x;
+  int kk[4], c = 0;
+  for (int k = 0; k < 4; ++k) { kk[k] = ec_keep(cut, e0 + k, E); c += kk[k]; }
+  int mine;
+  long long p = off + mh_block_excl_scan<int, 16>(c, mine, wsum);    // kept edges before e0
+  for (int k = 0; k < 4; ++k) {
+    const long long e = e0 + k;
+    if (e >= E) break;
+    if (kk[k]) rows[p++] = (int)e;
+    else rows[E - 1 - (e - p)] = (int)e;  // e - p dropped edges come before e
+  }
+  if (b == nb - 1 && threadIdx.x == 0) count[0] = off + mine;
+}
 """
 
 
 RANK_MAX = 128             # longest segment ordered by counting in csr_rank; longer ones by csr_sort_long
+EC_EDGES = 4096            # edges per workgroup of mh_edge_compact's kernels (fixed in graph_source)
 SORT_LDS = 8192            # longest segment csr_sort_long sorts in LDS (longer: in place in global memory)
 _GRAPH_MODULES = {}        # device index -> module of the graph-build kernels
 
@@ -295,7 +338,9 @@ def _graph_module(device):
                                       _native.MH_CSR_SCAN: ('csr_scan', 1024, 1, 2),
                                       _native.MH_CSR_SCATTER: ('csr_scatter', 256, 256, 2),
                                       _native.MH_CSR_RANK: ('csr_rank', 256, 256, 2),
-                                      _native.MH_CSR_SORT: ('csr_sort_long', 256, 1, 2)})
+                                      _native.MH_CSR_SORT: ('csr_sort_long', 256, 1, 2),
+                                      _native.MH_EDGE_COUNT: ('edge_count', 1024, EC_EDGES),
+                                      _native.MH_EDGE_PLACE: ('edge_place', 1024, EC_EDGES)})
         _GRAPH_MODULES[idx] = m
     return m
 
@@ -553,17 +598,43 @@ class RadialWeights(torch.Tensor):
 _MULS = {torch.Tensor.__mul__, torch.Tensor.__rmul__, torch.Tensor.mul, torch.mul}
 
 
+EDGE_COMPACT_MIN = 16384   # fewer edges: the radial MLP walks every edge (compacting costs two launches)
+# patch_model runs each patched convolution's patched radial MLP inside the convolution's autograd node
+# (HipConvTP.defer_mlp, conv_mlp.ConvRadialFn) unless double_backward or fuse_radial asks otherwise
+DEFER_RADIAL = True
+
+
+def support_rows(cut):
+    """(rows int32 [E], count int32 [1]) of a cutoff column (``mh_edge_compact``): the edges inside the cutoff's
+    support (cutoff not -0.0) in increasing order, then the others; count[0] = how many are inside.  Cached on the
+    tensor for its current version, so the interaction layers sharing MACE's cutoff compact it once per call."""
+    c = getattr(cut, '_mh_rows', None)
+    if c is not None and c[0] == cut._version:
+        return c[1], c[2]
+    flat = cut.reshape(-1).contiguous()
+    E = flat.shape[0]
+    lib, P = _native.load(), _native.ptr
+    rows = torch.empty(E, dtype=torch.int32, device=cut.device)
+    count = torch.empty(1, dtype=torch.int32, device=cut.device)
+    work = torch.empty(-(-lib.mh_edge_compact_work_size(E) // 4), dtype=torch.int32, device=cut.device)
+    _native.launch('edge_compact', lib.mh_edge_compact, _graph_module(cut.device).handle, P(flat), E, P(rows),
+                   P(count), P(work), _native.stream_of(flat))
+    cut._mh_rows = (cut._version, rows, count)
+    return rows, count
+
+
 def _support_masked(cut):
     """Whether ``cut`` is a patched radial embedding's cutoff, unmodified since: -0.0 then marks exactly the edges
     outside the envelope's support, where the envelope's derivative is zero."""
     return getattr(cut, '_mh_support_mask', None) == cut._version
 
 
-def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False):
+def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False, nozero=False):
     """First-order gradients (gx, gY, gW or gW0, gcut) of <g, conv(x, Y, W)> for contiguous operands, by the
     kernels; W = W0 * cut (cut flat [E]) when W is None.  Entries not wanted are None.  ``masked`` (factored only):
     edges with cut == -0.0 lie outside the cutoff envelope's support, and their gradients, gcut included, are zero
-    (the envelope's derivative there is zero, so gcut's true value there never matters to its producer)."""
+    (the envelope's derivative there is zero, so gcut's true value there never matters to its producer).
+    ``nozero`` (with ``masked``): those edges' gW0 rows are left unset, for a consumer that skips them."""
     factored = W is None
     E = Y.shape[0]
     gx = torch.empty_like(x) if want_x else None
@@ -573,7 +644,7 @@ def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False):
     # with no edges gW and gY are empty (NULL data pointers): nothing to compute for them
     flags = (_native.MH_WANT_GX if want_x else 0) | (_native.MH_WANT_GWY if want_wy and E > 0 else 0)
     if masked and factored and flags & _native.MH_WANT_GWY:
-        flags |= _native.MH_CUT_MASKED
+        flags |= _native.MH_CUT_MASKED | (_native.MH_CUT_NOZERO if nozero else 0)
     lib = _native.load()
     P = _native.ptr
     if flags & _native.MH_WANT_GWY and (op.bwd_recv or factored):
@@ -756,6 +827,8 @@ class HipConvTP(torch.nn.Module):
         # the radial MLP whose output layer the fused kernels carry (attach_mlp), and those kernels
         self.fused = None
         self._fused_mlp = []
+        # the radial MLP run inside this convolution's autograd node (defer_mlp: conv_mlp.ConvRadialFn)
+        self._deferred_mlp = []
 
     def attach_mlp(self, mlp):
         """Form this convolution's weights inside its kernels from ``mlp``'s (a HipRadialMLP) last hidden
@@ -771,15 +844,27 @@ class HipConvTP(torch.nn.Module):
     def detach_mlp(self):
         self.fused, self._fused_mlp = None, []
 
+    def defer_mlp(self, mlp):
+        """Run ``mlp`` (the HipRadialMLP producing this convolution's weights, its output handed over unformed) in
+        this convolution's autograd node, so that W0 and dL/dW0 stay inside it and the edges outside the cutoff's
+        support are skipped by both modules' kernels (``conv_mlp.ConvRadialFn``).  None detaches it."""
+        self._deferred_mlp = [mlp] if mlp is not None else []
+
+    def deferred_mlp(self):
+        return self._deferred_mlp[0] if self._deferred_mlp else None
+
     def fused_mlp(self):
         return self._fused_mlp[0] if self._fused_mlp else None
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
-        from .conv_mlp import ConvMLPFn, FusedWeights
+        from .conv_mlp import ConvMLPFn, ConvRadialFn, FusedWeights
         if isinstance(tp_weights, FusedWeights):
             if self.fused is not None and tp_weights.mlp is self.fused_mlp():
                 # W = cutoff * MLP(edge_feats) formed inside the kernels: neither W nor its gradient is stored
                 return ConvMLPFn.apply(node_feats, edge_attrs, tp_weights.ef, tp_weights.cut, edge_index, self)
+            if tp_weights.mlp is self.deferred_mlp():
+                # the MLP's kernels and this convolution's in one node: rows outside the cutoff's support skipped
+                return ConvRadialFn.apply(node_feats, edge_attrs, tp_weights.ef, tp_weights.cut, edge_index, self)
             tp_weights = tp_weights.value()
         if isinstance(tp_weights, CutoffProduct):
             # the radial MLP's output times the cutoff, never formed: the kernels take the two factors

@@ -444,7 +444,9 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
     envelope's derivative is zero (padding edges, edges past r_max).  There W = 0, so ∂/∂W0 = gW·c, gY and the dX
     message are zero, and ∂/∂c is multiplied by a zero derivative wherever it goes: the kernel writes zero ∂/∂W0,
     gY and ∂/∂c rows for such an edge without reading W0 or x, writes no dX message (``conv_gxsum`` skips the edge
-    too), and walks only the other edges of each chunk (compacted by lane rank, as in ``conv_fwdc``)."""
+    too), and walks only the other edges of each chunk (compacted by lane rank, as in ``conv_fwdc``).  With flags
+    bit 2 as well the zero ∂/∂W0 rows are not written either: for a caller whose only consumer of ∂/∂W0 (the radial
+    MLP's backward) skips the masked rows itself."""
     spec, nx, nk = G.s, G.nx, G.s.nins
     L = [
         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwdrc" if cut else "conv_bwdr")}(',
@@ -461,7 +463,8 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         '  if (r >= N) return;',
     ] + G.prelude() + [
         '  const bool GX = (flags & 1) != 0;',
-    ] + (['  const bool MASKED = (flags & 2) != 0;'] if cut else []) + [
+    ] + (['  const bool MASKED = (flags & 2) != 0;',
+          '  const bool ZROWS = (flags & 4) == 0;     // write the zero gW rows of masked edges'] if cut else []) + [
         '  ' + decl('gv', G.no),
     ]
     L += G.ld_g('  ', 'r', 'gv')
@@ -490,7 +493,7 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
                   '      const int ez = mh_bcast(my_e, __builtin_ctzll(d));',
                   '      float* __restrict__ gz = gW + (size_t)ez * NW;']
             st = [f'mh_st_nt(gz + {k * spec.mul}, ol1, 0.0f);' for k in range(nk)]
-            C += [f'      {t}' if G.full else f'      if (active) {t}' for t in st]
+            C += ['      if (ZROWS) {'] + [f'        {t}' if G.full else f'        if (active) {t}' for t in st] + ['      }']
             C += ['      if (wave == 0) {',
                   '        if (lane < Y_DIM) gY[(size_t)ez * Y_DIM + lane] = 0.0f;',
                   '        if (lane == 0) gcut[ez] = 0.0f;',

@@ -645,3 +645,73 @@ class ConvMLPFn(torch.autograd.Function):
                        fc.spec.nct, P(cut), P(gef), P(gcut), E, stream)
         ef_shape, cut_shape = ctx.shapes
         return gx, gY, gef.view(ef_shape), gcut.view(cut_shape), None, None
+
+
+class ConvRadialFn(torch.autograd.Function):
+    """out = conv(x, Y, W0 * cut) with W0 = MLP(ef) formed by the radial MLP's own kernels inside this one autograd
+    node (``HipConvTP.defer_mlp``).  Inputs (x, Y, ef, cut, edge_index, conv op); gradients for x, Y, ef and cut.
+
+    W0 and dL/dW0 never leave the node, so when the cutoff comes unmodified from the patched radial embedding (an
+    edge outside the envelope's support marked -0.0) and the graph has at least ``conv.EDGE_COMPACT_MIN`` edges,
+    neither is formed for those edges: the edges inside the support are listed first (``conv.support_rows``), the
+    MLP computes and stores W0 rows for them only (the convolution never reads the others: their cutoff is 0), the
+    convolution's backward skips the others without writing their dL/dW0 rows (MH_CUT_NOZERO), and the MLP's
+    backward reads only the listed rows and writes zero dL/d(edge features) rows for the rest.  Every result equals
+    the separate modules' (the MLP's output times a zero cutoff contributes nothing, and its gradient there is
+    zero).  No double backward: the two-kernel modules take that (``patch_model(double_backward=True)``)."""
+
+    @staticmethod
+    def forward(ctx, x, Y, ef, cut, edge_index, op):
+        from . import conv as C
+        from .radial import mlp_forward
+        mlp = op.deferred_mlp()
+        s = op.spec
+        if any(t.dtype != torch.float32 for t in (x, Y, ef, cut)):
+            raise TypeError('mace_hip_kernels: conv_tp expects float32 inputs')
+        if not all(t.is_cuda for t in (x, Y, ef, cut, edge_index)):
+            raise RuntimeError('mace_hip_kernels: conv_tp inputs must be on the GPU')
+        E, n = Y.shape[0], x.shape[0]
+        if x.dim() != 2 or x.shape[1] != s.x_dim or Y.shape != (edge_index.shape[1], s.y_dim):
+            raise ValueError(f'node_feats [N, {s.x_dim}] and edge_attrs [E, {s.y_dim}] expected, got '
+                             f'{tuple(x.shape)}, {tuple(Y.shape)}')
+        if ef.shape[-1] != mlp.spec.hs[0] or ef.numel() != E * mlp.spec.hs[0] or cut.numel() != E:
+            raise ValueError('edge features and cutoff must have one row per edge')
+        if n >= 2 ** 31 or E >= 2 ** 31:
+            raise ValueError('graph too large for int32 indices')
+        masked = C._support_masked(cut) and op.skip_masked
+        xc, Yc = x.contiguous(), Y.contiguous()
+        efc, cutf = ef.reshape(E, -1).contiguous(), cut.reshape(-1).contiguous()
+        rows = count = None
+        if masked and E >= C.EDGE_COMPACT_MIN:
+            rows, count = C.support_rows(cut)
+        W0 = mlp_forward(mlp, efc, rows, count)
+        gr = C.graph_for(edge_index, n)
+        rowptr, eids = gr.by_recv()
+        out = torch.empty(n, s.out_dim, device=x.device, dtype=torch.float32)
+        P = _native.ptr
+        # edges with cutoff 0 contribute exactly zero and are not read (so the rows the MLP left unset never are)
+        _native.launch(f'conv_fwd[{op.tag}]', _native.load().mh_conv_fwd_cut, op.module.handle, P(xc), P(Yc), P(W0),
+                       P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n, _native.stream_of(x))
+        ctx.save_for_backward(xc, Yc, efc, cutf)
+        ctx.W0, ctx.rows, ctx.count, ctx.masked = W0, rows, count, masked
+        ctx.op, ctx.gr, ctx.shapes = op, gr, (ef.shape, cut.shape)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        from . import conv as C
+        from .radial import _mlp_bwd
+        if torch.is_grad_enabled():
+            raise RuntimeError(_DOUBLE_BACKWARD)
+        x, Y, ef, cut = ctx.saved_tensors
+        op, gr = ctx.op, ctx.gr
+        want_x, want_y, want_ef, want_cut = (C._grad_needed(ctx, i) for i in range(4))
+        if not (want_x or want_y or want_ef or want_cut):
+            return None, None, None, None, None, None
+        compact = ctx.rows is not None
+        gx, gY, gW0, gcut = C._conv_grads(op, gr, g.contiguous(), x, Y, None, ctx.W0, cut, want_x,
+                                          want_y or want_ef or want_cut, masked=ctx.masked, nozero=compact)
+        gef = _mlp_bwd(op.deferred_mlp(), ef, gW0, ctx.rows, ctx.count) if want_ef else None
+        ef_shape, cut_shape = ctx.shapes
+        return (gx, gY if want_y else None, gef.view(ef_shape) if gef is not None else None,
+                gcut.view(cut_shape) if want_cut else None, None, None)

@@ -227,17 +227,47 @@ def _source(spec, second):
               '__device__ __forceinline__ float mlp_d2(float z) { const float s = mlp_sig(z); '
               'return s * (1.f - s) * (2.f + z * (1.f - 2.f * s)); }', '']
 
-    def head(name, args, lds, nb, waves=BLOCK // 64):
+    def head(name, args, lds, nb, waves=BLOCK // 64, indexed=False):
+        """Kernel prologue: edge slot ej{b} of this lane in tile b (live{b}: a slot < E).  ``indexed``: two more
+        arguments, ``rows`` (NULL, or the edge of each slot) and ``count`` (NULL, or the number of slots to compute:
+        the rest are not computed, and a backward writes zero gradient rows for their edges); rowc{b} is the edge of
+        slot ej{b} (clamped into range) and do{b} whether it is computed."""
+        if indexed:
+            args += ', const int* __restrict__ rows, const int* __restrict__ count'
+        # an indexed kernel computes the slots below count only: they go round-robin over the XCDs (blockIdx order),
+        # so that every XCD gets its share however many slots are computed
+        blk = 'blockIdx.x' if indexed else 'mh_xcd_block(blockIdx.x, gridDim.x)'
         P = [f'extern "C" __global__ __launch_bounds__({64 * waves}) void {name}({args}) {{',
              f'  __shared__ __align__(16) float lds[{lds}];',
              '  unsigned short* __restrict__ ldsb = reinterpret_cast<unsigned short*>(lds);',
              '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
              '  (void)ldsb; (void)lane;',
-             f'  const long long e0 = (long long)mh_xcd_block(blockIdx.x, gridDim.x) * {16 * nb * waves} + wave * {16 * nb};']
+             f'  const long long e0 = (long long){blk} * {16 * nb * waves} + wave * {16 * nb};']
         for b in range(nb):      # edge tile b of this wave: this lane's edge as a B column / output row
             P += [f'  const long long ej{b} = e0 + {16 * b} + c16;',
                   f'  const bool live{b} = ej{b} < E;',
                   f'  const long long ejc{b} = live{b} ? ej{b} : E - 1;      // clamped: every load in bounds']
+        if indexed:
+            P += ['  const long long ncount = count ? (long long)count[0] : E;']
+            P += [f'  const long long rowc{b} = rows ? (long long)rows[ejc{b}] : ejc{b};' for b in range(nb)]
+            P += [f'  const bool do{b} = live{b} && ej{b} < ncount;' for b in range(nb)]
+        else:
+            P += [f'  const long long rowc{b} = ejc{b};' for b in range(nb)]
+            P += [f'  const bool do{b} = live{b};' for b in range(nb)]
+        return P
+
+    def skip_block(nb, zero_rows, waves=BLOCK // 64):
+        """An indexed kernel's workgroup whose slots all lie past ``count`` computes nothing (uniform: before any
+        barrier); a backward writes zero dL/d(edge features) rows for the edges of its slots."""
+        span = 16 * nb * waves
+        P = [f'  const long long slot0 = (long long)blockIdx.x * {span};',
+             '  if (slot0 >= ncount) {']
+        if zero_rows:
+            P += [f'    for (int k = t; k < {span * H0}; k += {64 * waves}) {{',
+                  f'      const long long sl = slot0 + k / {H0};',
+                  f'      if (sl < E) gef[(rows ? (long long)rows[sl] : sl) * {H0} + k % {H0}] = 0.f;',
+                  '    }']
+        P += ['    return;', '  }']
         return P
 
     def stage(src, n, nthreads=BLOCK):
@@ -254,7 +284,7 @@ def _source(spec, second):
         P = []
         for b in tiles:
             P += [f'  float {name}{b}[{K0S}];']
-            P += [f'  {name}{b}[{st}] = {4 * st} + q < {H0} ? {src}[ejc{b} * {H0} + {4 * st} + q] : 0.f;'
+            P += [f'  {name}{b}[{st}] = {4 * st} + q < {H0} ? {src}[rowc{b} * {H0} + {4 * st} + q] : 0.f;'
                   for st in range(K0S)]
         return P
 
@@ -344,7 +374,9 @@ def _source(spec, second):
         ncf = 2 if nb == 1 else 1                            # accumulator chains per result tile
         F = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if tangent else '') +
                  'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E',
-                 lds_fwd, nb)
+                 lds_fwd, nb, indexed=not tangent)
+        if not tangent:
+            F += skip_block(nb, zero_rows=False)
         F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(nb))
         if tangent:
             F += xin(range(nb), 'ev', 'xv') + hidden_fwd(True, False, range(nb), dual=True, keep_t=True)
@@ -396,11 +428,11 @@ def _source(spec, second):
             F += chunk_io('Wl', 0, HL, RSF, CH, '    ', store_base='nbase', reg=f'pre{(j + 1) % PD}_')[0]
             F += ['    __builtin_amdgcn_sched_barrier(0);']
             for b in range(nb):
-                F.append(f'    if (live{b}{f" && c < {NCHK}" if NCHP > NCHK else ""}) {{')
+                F.append(f'    if (do{b}{f" && c < {NCHK}" if NCHP > NCHK else ""}) {{')
                 for o in range(NO):
                     guard = f'if (c < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
                     val = ' + '.join(f'acc{b}[{o}][{jj}]' for jj in range(ncf))
-                    F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + ej{b} * {NW} + c * {CH} + {16 * o} + 4 * q) = {val};']
+                    F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + rowc{b} * {NW} + c * {CH} + {16 * o} + 4 * q) = {val};']
                 F += ['    }']
             F += ['    __syncthreads();', '  }']
         F += ['  }', '}', '']
@@ -470,8 +502,8 @@ def _source(spec, second):
                           for b in grp]
             for b in grp:
                 for r in range(4):
-                    B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[ej{b} * {H0} + {16 * o + r} + 4 * q] = '
-                             f'd{b}[{r}];')
+                    B.append(f'    if (live{b} && {16 * o + r} + 4 * q < {H0}) gef[rowc{b} * {H0} + {16 * o + r} + 4 * q] = '
+                             f'do{b} ? d{b}[{r}] : 0.f;')
             B.append('  }')
         return B
 
@@ -489,7 +521,9 @@ def _source(spec, second):
         TAIL = NW % CH != 0
         B = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if dual else '') +
                  'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, const float* __restrict__ gW, '
-                 'float* __restrict__ gef, long long E', lds_bwd, nb)
+                 'float* __restrict__ gef, long long E', lds_bwd, nb, indexed=not dual)
+        if not dual:
+            B += skip_block(nb, zero_rows=True)
         for b in range(nb):
             B += [f'  mh_f4 dh{b}[{TL}][{ncb}];'] + [f'  dh{b}[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};'
                                                     for o in range(TL) for j in range(ncb)]
@@ -503,8 +537,8 @@ def _source(spec, second):
             P = []
             for ks in range(KS):
                 col = gcol(f'{c} + {32 * ks}')
-                P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col});',
-                      f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + ejc{b} * {NW} + {col} + 4);']
+                P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + rowc{b} * {NW} + {col});',
+                      f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + rowc{b} * {NW} + {col} + 4);']
             return P
         # dL/dW0 of chunk ch + d sits in g{d}_* (d = 0 .. GW_DIST - 1) while chunk ch is multiplied
         for b in range(nb):
@@ -662,13 +696,25 @@ _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. 
                     'patch_model(model, double_backward=True)')
 
 
-def _mlp_bwd(op, ef, g):
-    """dL/d(edge features) [E, n_basis] from dL/dW0 (contiguous 2-D operands)."""
+def _mlp_bwd(op, ef, g, rows=None, count=None):
+    """dL/d(edge features) [E, n_basis] from dL/dW0 (contiguous 2-D operands).  With a row list (``rows``,
+    ``count`` from ``conv.support_rows``) only the first count[0] listed edges are computed; the others get zero rows
+    and their dL/dW0 rows are not read."""
     gx = torch.empty_like(ef)
-    _native.launch(f'mlp_bwd[{op.tag}]', _native.load().mh_mlp_bwd, op.module.handle, _native.ptr(ef),
-                   _native.ptr(op.Wh), _native.ptr(op.Wl), _native.ptr(g), _native.ptr(gx), ef.shape[0],
-                   _native.stream_of(ef))
+    P = _native.ptr
+    _native.launch(f'mlp_bwd[{op.tag}]', _native.load().mh_mlp_bwd_rows, op.module.handle, P(ef), P(op.Wh), P(op.Wl),
+                   P(g), P(gx), ef.shape[0], P(rows), P(count), _native.stream_of(ef))
     return gx
+
+
+def mlp_forward(op, ef, rows=None, count=None):
+    """W0 = MLP(ef) [E, n_out] (ef contiguous [E, n_basis]); with a row list only the first count[0] listed edges'
+    rows are computed and written (the other rows of W0 are left unset)."""
+    out = torch.empty(ef.shape[0], op.spec.hs[-1], device=ef.device, dtype=torch.float32)
+    P = _native.ptr
+    _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd_rows, op.module.handle, P(ef), P(op.WhT),
+                   P(op.WlT), P(out), ef.shape[0], P(rows), P(count), _native.stream_of(ef))
+    return out
 
 
 class _MLPFn(torch.autograd.Function):
@@ -680,11 +726,7 @@ class _MLPFn(torch.autograd.Function):
         if ef.shape[-1] != s.hs[0]:
             raise ValueError(f'expected [..., {s.hs[0]}] edge features, got {tuple(ef.shape)}')
         lead = ef.shape[:-1]
-        x = ef.reshape(-1, s.hs[0]).contiguous()
-        E = x.shape[0]
-        out = torch.empty(E, s.hs[-1], device=x.device, dtype=torch.float32)
-        _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd, op.module.handle, _native.ptr(x),
-                       _native.ptr(op.WhT), _native.ptr(op.WlT), _native.ptr(out), E, _native.stream_of(x))
+        out = mlp_forward(op, ef.reshape(-1, s.hs[0]).contiguous())
         ctx.save_for_backward(ef)            # the input itself: a double backward differentiates through it
         ctx.op, ctx.lead = op, lead
         return out.reshape(*lead, s.hs[-1])

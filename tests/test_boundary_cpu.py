@@ -220,6 +220,27 @@ def test_neighbour_list_work_size_and_argument_checks():
     assert b'nslots' in lib.mh_last_error()
 
 
+def test_edge_compaction_and_row_list_argument_checks():
+    """mh_edge_compact's scratch is one int32 per 4096 edges (one for none); bad arguments and a row list without
+    its count fail before any launch."""
+    lib = _native.load()
+    assert [lib.mh_edge_compact_work_size(e) for e in (0, 1, 4096, 4097, 100000)] == [4, 4, 4, 8, 100]
+    P = ctypes.c_void_p
+    assert lib.mh_edge_compact(None, None, -1, None, None, None, None) != 0
+    assert b'bad edge count' in lib.mh_last_error()
+    assert lib.mh_edge_compact(None, None, 10, None, P(8), P(8), None) != 0
+    assert b'NULL' in lib.mh_last_error()
+    assert lib.mh_edge_compact(None, P(8), 10, P(8), P(8), P(8), None) != 0
+    assert b'null module' in lib.mh_last_error()
+    assert lib.mh_mlp_fwd_rows(None, P(8), P(8), P(8), P(8), 10, P(8), None, None) != 0
+    assert b'go together' in lib.mh_last_error()
+    assert lib.mh_mlp_bwd_rows(None, P(8), P(8), P(8), P(8), P(8), 10, None, P(8), None) != 0
+    assert b'go together' in lib.mh_last_error()
+    assert lib.mh_conv_bwd_recv(None, P(8), P(8), P(8), P(8), None, None, None, None, None, None, None, P(8), P(8),
+                                P(8), P(8), 10, _native.MH_WANT_GWY | _native.MH_CUT_NOZERO, None) != 0
+    assert b'MH_CUT_NOZERO needs MH_CUT_MASKED' in lib.mh_last_error()
+
+
 def test_species_order_fallback_on_large_tables():
     """More elements than the kernel's LDS tables: the torch expressions (they run on the CPU too)."""
     from mace_hip_kernels import species

@@ -1,0 +1,134 @@
+"""
+The radial MLP run inside the convolution's autograd node (``HipConvTP.defer_mlp``, ``conv_mlp.ConvRadialFn``, the
+patched model's default) against the two modules run separately, and the edge compaction behind it
+(``mh_edge_compact``) against numpy.  With the cutoff marked as the patched radial embedding's (-0.0 outside the
+envelope's support), the deferred node lists the edges inside the support first, the MLP computes W0 rows for those
+only, the convolution's backward leaves the other dL/dW0 rows unwritten (MH_CUT_NOZERO) and the MLP's backward
+writes zero dL/d(edge features) rows there: every output and gradient must equal the separate modules' bitwise.
+"""
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from mace_hip_kernels import HipConvTP, HipRadialMLP, _native, patch_model
+from mace_hip_kernels import conv as hconv
+from mace_hip_kernels.conv_mlp import FusedWeights
+from mace_lite import data as D
+from mace_lite import factory
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev():
+    assert torch.cuda.is_available(), 'GPU test needs a GPU'
+    return torch.device('cuda:0')
+
+
+@pytest.mark.parametrize('E', [0, 1, 4095, 4096, 4097, 100003])
+def test_edge_compact_vs_numpy(E):
+    dev = _dev()
+    print(f'[case] edge compaction E={E}', flush=True)
+    rng = np.random.default_rng(E + 1)
+    c = rng.uniform(0.0, 1.0, size=E).astype(np.float32)
+    c[rng.uniform(size=E) < 0.3] = -0.0
+    c[rng.uniform(size=E) < 0.05] = 0.0          # +0.0 is inside the support: only -0.0 marks an edge outside
+    if E > 9000:
+        c[4096:8192] = -0.0                      # one compaction workgroup wholly outside
+    ct = torch.tensor(c, device=dev)
+    rows, count = hconv.support_rows(ct)
+    keep = ~(np.signbit(c) & (c == 0))
+    K = int(keep.sum())
+    assert int(count.item()) == K
+    got = rows.cpu().numpy()
+    assert np.array_equal(got[:K], np.nonzero(keep)[0])
+    assert np.array_equal(np.sort(got[K:]), np.nonzero(~keep)[0])
+    again = hconv.support_rows(ct)               # cached for the tensor's version
+    assert again[0] is rows
+
+
+def _modules(dev):
+    model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    blk = model.interactions[1]
+    return HipConvTP(blk.conv_tp, device=dev), HipRadialMLP(blk.conv_tp_weights, device=dev)
+
+
+@pytest.mark.parametrize('E,marked,want_x', [(40000, True, True), (40000, True, False), (40000, False, True),
+                                             (3000, True, True)])
+def test_deferred_mlp_equals_separate_modules(E, marked, want_x):
+    dev = _dev()
+    print(f'[case] deferred radial MLP E={E} marked={marked} want_x={want_x}', flush=True)
+    op, mlp = _modules(dev)
+    rng = np.random.default_rng(3)
+    n = max(64, E // 30)
+    s = rng.integers(0, n, size=E)
+    r = rng.integers(0, n, size=E)
+    c = rng.uniform(0.05, 1.0, size=(E, 1)).astype(np.float32)
+    out_mask = rng.uniform(size=E) < 0.2
+    if E > 30000:
+        out_mask[12000:17000] = True             # whole MLP workgroups and compaction workgroups outside
+    c[out_mask] = -0.0
+    x = rng.normal(size=(n, op.spec.x_dim)).astype(np.float32)
+    Y = rng.normal(size=(E, op.spec.y_dim)).astype(np.float32)
+    ef = rng.normal(size=(E, mlp.spec.hs[0])).astype(np.float32)
+    g = torch.tensor(rng.normal(size=(n, op.spec.out_dim)).astype(np.float32), device=dev)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+
+    def run(deferred):
+        op.defer_mlp(mlp if deferred else None)
+        mlp.fuse = deferred
+        t = lambda a, rg=True: torch.tensor(a, device=dev, requires_grad=rg)  # noqa: E731
+        xt, Yt, eft, ct = t(x, want_x), t(Y), t(ef), t(c)
+        if marked:
+            ct._mh_support_mask = ct._version
+        W = mlp(eft) * ct
+        assert isinstance(W, FusedWeights) == deferred
+        with _native.timing() as tm:
+            out = op(xt, Yt, W, ei)
+            out.backward(g)
+        torch.cuda.synchronize()
+        return out.detach(), xt.grad, Yt.grad, eft.grad, ct.grad, tm.symbols
+
+    try:
+        sep = run(False)
+        dfr = run(True)
+    finally:
+        op.defer_mlp(None)
+        mlp.fuse = False
+    names = ('out', 'gx', 'gY', 'gef', 'gcut')
+    for nm, a, b in zip(names, sep[:5], dfr[:5]):
+        if nm == 'gx' and not want_x:
+            assert a is None and b is None
+            continue
+        assert torch.equal(a, b), (nm, float((a - b).abs().max()))
+    compacted = 'edge_compact' in dfr[5]
+    assert compacted == (marked and E >= hconv.EDGE_COMPACT_MIN), dfr[5]
+    for tag in ('mlp_fwd[radial_mlp]', 'mlp_bwd[radial_mlp]', 'conv_fwd[conv]', 'conv_bwd[conv]'):
+        assert tag in dfr[5], (tag, dfr[5])
+    if marked:                                   # the masked edges' gradients are exact zeros
+        m = torch.from_numpy(out_mask).to(dev)
+        assert not dfr[3][m].any() and not dfr[4][m].any()
+
+
+def test_patched_model_defers_and_matches(monkeypatch):
+    """config 2 (padded: 18% of the edges outside the cutoff): the patched model with the MLPs inside the
+    convolutions' nodes (the default) against the same model with them as separate nodes: E and F equal."""
+    dev = _dev()
+    print('[case] patched model, deferred radial MLP vs separate (config 2)', flush=True)
+    model, batch, _ = factory.workload(2)
+    b = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
+    outs = []
+    for defer in (False, True):
+        monkeypatch.setattr(hconv, 'DEFER_RADIAL', defer)
+        m = copy.deepcopy(model).to(dev)
+        patch_model(m, verbose=False)
+        assert all((blk.conv_tp.deferred_mlp() is not None) == defer for blk in m.interactions)
+        with _native.timing() as tm:
+            o = m(D.fresh(b), compute_force=True)
+        torch.cuda.synchronize()
+        assert ('edge_compact' in tm.symbols) == defer, tm.symbols
+        outs.append((o['energy'].detach(), o['forces'].detach()))
+    (e0, f0), (e1, f1) = outs
+    assert float((e0 - e1).abs().max()) <= 1e-5 and float((f0 - f1).abs().max()) <= 1e-6
+    print(f'[case] forces bitwise equal: {torch.equal(f0, f1)}', flush=True)
