@@ -49,6 +49,14 @@ W_NT = True
 BWD_PREFETCH = 1
 # The factored backward's per-edge cutoff: broadcast from a per-chunk register (True) or loaded per edge (False).
 BWD_CUT_BCAST = True
+# Fence the factored backward's ∂/∂c accumulator after every instruction: the per-instruction gW values are then
+# not scheduled together, 173 -> 155 VGPRs for the 1280-wide layer (3 waves per SIMD instead of 2; config 2,
+# layer 2 backward 241 -> 230 us).
+BWD_PC_FENCE = True
+# Receiver-ordered backward with two channel waves: the waves' gY and ∂/∂c partials meet in one LDS plane by
+# atomic adds (0 + a + b = 0 + b + a exactly, so the result does not depend on their order), halving that buffer
+# (config 2, layer 1 backward 84 -> 77 us; layer 2's LDS then fits 6 workgroups per CU).
+GY_LDS_ATOMIC = True
 
 
 class _Gen:
@@ -192,7 +200,7 @@ class _Gen:
             gw = _sum([f'xv{self.xi[i1] + a} * h{a}' for a in hs])
             if cut:
                 L.append(f'{ind}  const float gwk = {gw};')
-                L.append(f'{ind}  Pc = fmaf(gwk, w0{k}, Pc);')
+                L.append(f'{ind}  Pc = fmaf(gwk, w0{k}, Pc);' + (' asm volatile("" : "+v"(Pc));' if BWD_PC_FENCE else ''))
                 gw = 'gwk * ce'
             st = f'mh_st_nt(gwe + {k * s.mul}, ol1, {gw});'      # written once, never re-read here
             L.append(f'{ind}  {st}' if self.full else f'{ind}  if (active) {st}')
@@ -221,7 +229,7 @@ def _xchg(v, bit):
     return _dpp(v, bit) if bit < 4 else f'__shfl_xor({v}, {1 << bit}, MH_WAVE)'
 
 
-def gy_reduce(indent, y_dim, y_pad):
+def gy_reduce(indent, y_dim, y_pad, atomic=False):
     """Sum P0..P{y_pad-1} over the 64 lanes (transpose reduction, fixed order); lane L ends up holding the total of
     component L >> (6 - log2 y_pad), which lanes with zero low bits store to part[wave][j][.]."""
     L = [f'{indent}P{b} = 0.0f;' for b in range(y_dim, y_pad)]
@@ -239,11 +247,12 @@ def gy_reduce(indent, y_dim, y_pad):
             L.append(f'{indent}P0 += {_xchg("P0", bit)};')
     shift = 6 - (y_pad.bit_length() - 1)
     L.append(f'{indent}{{ const int comp = lane >> {shift};')
-    L.append(f'{indent}  if ((lane & {(1 << shift) - 1}) == 0 && comp < Y_DIM) part[wave][j][comp] = P0; }}')
+    dst = 'atomicAdd(&part[j][comp], P0)' if atomic else 'part[wave][j][comp] = P0'
+    L.append(f'{indent}  if ((lane & {(1 << shift) - 1}) == 0 && comp < Y_DIM) {dst}; }}')
     return L
 
 
-def _gy_combine(indent, edge_expr, cut=False):
+def _gy_combine(indent, edge_expr, cut=False, atomic=False):
     """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order); with ``cut``
     also the ∂/∂c partials.  The leading barrier also orders the chunk's Ms reads before the next chunk's prologue
     overwrites them."""
@@ -251,16 +260,21 @@ def _gy_combine(indent, edge_expr, cut=False):
         f'{indent}__syncthreads();',
         f'{indent}for (int q = threadIdx.x; q < cnt * Y_DIM; q += BLOCK) {{',
         f'{indent}  const int j = q / Y_DIM, b = q - j * Y_DIM;',
+    ] + ([
+        f'{indent}  const float v = part[j][b];',
+        f'{indent}  part[j][b] = 0.0f;                    // zero again for the next chunk\'s atomic adds',
+    ] if atomic else [
         f'{indent}  float v = 0.0f;',
         f'{indent}  for (int w = 0; w < NCB; ++w) v += part[w][j][b];',
+    ]) + [
         f'{indent}  gY[(size_t)({edge_expr}) * Y_DIM + b] = v;',
         f'{indent}}}',
     ]
     if cut:
-        L += [f'{indent}for (int j = threadIdx.x; j < cnt; j += BLOCK) {{',
-              f'{indent}  float v = 0.0f;',
-              f'{indent}  for (int w = 0; w < NCB; ++w) v += partc[w][j];',
-              f'{indent}  gcut[{edge_expr}] = v;',
+        L += [f'{indent}for (int j = threadIdx.x; j < cnt; j += BLOCK) {{']
+        L += ([f'{indent}  const float v = partc[j];', f'{indent}  partc[j] = 0.0f;'] if atomic else
+              [f'{indent}  float v = 0.0f;', f'{indent}  for (int w = 0; w < NCB; ++w) v += partc[w][j];'])
+        L += [f'{indent}  gcut[{edge_expr}] = v;',
               f'{indent}}}']
     return L + [f'{indent}__syncthreads();']
 
@@ -448,6 +462,9 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
     bit 2 as well the zero ∂/∂W0 rows are not written either: for a caller whose only consumer of ∂/∂W0 (the radial
     MLP's backward) skips the masked rows itself."""
     spec, nx, nk = G.s, G.nx, G.s.nins
+    atomic = GY_LDS_ATOMIC and spec.ncb == 2
+    if atomic:
+        gyr = gy_reduce('      ', spec.y_dim, spec.y_pad, atomic=True)
     L = [
         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwdrc" if cut else "conv_bwdr")}(',
         '    const float* __restrict__ x, const float* __restrict__ g, const float* __restrict__ Y,',
@@ -455,13 +472,18 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         '    const int* __restrict__ senders, float* __restrict__ gW, float* __restrict__ gY,',
         '    float* __restrict__ gxm, int N, int flags' +
         (', const float* __restrict__ cutv, float* __restrict__ gcut) {' if cut else ') {'),
-        '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
-    ] + (['  __shared__ float partc[NCB][MH_WAVE];', '  __shared__ int sidx[NCB][MH_WAVE];'] if cut else []) + [
+        '  __shared__ float part[MH_WAVE][Y_PAD];' if atomic else '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
+    ] + ((['  __shared__ float partc[MH_WAVE];'] if atomic else ['  __shared__ float partc[NCB][MH_WAVE];']) +
+         ['  __shared__ int sidx[NCB][MH_WAVE];'] if cut else []) + [
         '  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
         '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);',
         '  const int r = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  if (r >= N) return;',
-    ] + G.prelude() + [
+    ] + ([
+        '  for (int q = threadIdx.x; q < MH_WAVE * Y_PAD; q += BLOCK) (&part[0][0])[q] = 0.0f;',
+    ] + (['  for (int q = threadIdx.x; q < MH_WAVE; q += BLOCK) partc[q] = 0.0f;'] if cut else []) + [
+        '  __syncthreads();',
+    ] if atomic else []) + G.prelude() + [
         '  const bool GX = (flags & 1) != 0;',
     ] + (['  const bool MASKED = (flags & 2) != 0;',
           '  const bool ZROWS = (flags & 4) == 0;     // write the zero gW rows of masked edges'] if cut else []) + [
@@ -551,9 +573,9 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         if cut:
             # all-reduce over the wave (every lane ends with the sum), lane 0 keeps the wave's partial
             C += [f'      Pc += {_xchg("Pc", bit)};' for bit in range(5, -1, -1)]
-            C += ['      if (lane == 0) partc[wave][j] = Pc;']
+            C += ['      if (lane == 0) atomicAdd(&partc[j], Pc);' if atomic else '      if (lane == 0) partc[wave][j] = Pc;']
         C += ['    }']
-        C += _gy_combine('    ', 'sidx[0][j]' if cut else 'eids[pb + j]', cut=cut)
+        C += _gy_combine('    ', 'sidx[0][j]' if cut else 'eids[pb + j]', cut=cut, atomic=atomic)
         return C + ['  }']
 
     L += ['  if (GX) {'] + ['  ' + t for t in chunks(True)] + ['  } else {']
