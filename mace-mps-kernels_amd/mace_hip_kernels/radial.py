@@ -234,21 +234,27 @@ def _source(spec, second):
         slot ej{b} (clamped into range) and do{b} whether it is computed."""
         if indexed:
             args += ', const int* __restrict__ rows, const int* __restrict__ count'
-        # an indexed kernel computes the slots below count only: they go round-robin over the XCDs (blockIdx order),
-        # so that every XCD gets its share however many slots are computed
-        blk = 'blockIdx.x' if indexed else 'mh_xcd_block(blockIdx.x, gridDim.x)'
+        span = 16 * nb * waves
         P = [f'extern "C" __global__ __launch_bounds__({64 * waves}) void {name}({args}) {{',
              f'  __shared__ __align__(16) float lds[{lds}];',
              '  unsigned short* __restrict__ ldsb = reinterpret_cast<unsigned short*>(lds);',
              '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
-             '  (void)ldsb; (void)lane;',
-             f'  const long long e0 = (long long){blk} * {16 * nb * waves} + wave * {16 * nb};']
+             '  (void)ldsb; (void)lane;']
+        if indexed:
+            # the workgroups' worth of computed slots (nact) go to the first nact hardware workgroups, which the
+            # dispatcher spreads round-robin over the XCDs, in one contiguous range of slots per XCD (mh_xcd_block
+            # over nact); the other workgroups take the remaining slots in order (none computed)
+            P += ['  const long long ncount = count ? (long long)count[0] : E;',
+                  f'  const int nact = (int)((ncount + {span - 1}) / {span});',
+                  '  const long long blk = (int)blockIdx.x < nact ? mh_xcd_block(blockIdx.x, nact) : blockIdx.x;']
+        else:
+            P += ['  const long long blk = mh_xcd_block(blockIdx.x, gridDim.x);']
+        P += [f'  const long long e0 = blk * {span} + wave * {16 * nb};']
         for b in range(nb):      # edge tile b of this wave: this lane's edge as a B column / output row
             P += [f'  const long long ej{b} = e0 + {16 * b} + c16;',
                   f'  const bool live{b} = ej{b} < E;',
                   f'  const long long ejc{b} = live{b} ? ej{b} : E - 1;      // clamped: every load in bounds']
         if indexed:
-            P += ['  const long long ncount = count ? (long long)count[0] : E;']
             P += [f'  const long long rowc{b} = rows ? (long long)rows[ejc{b}] : ejc{b};' for b in range(nb)]
             P += [f'  const bool do{b} = live{b} && ej{b} < ncount;' for b in range(nb)]
         else:
@@ -260,7 +266,7 @@ def _source(spec, second):
         """An indexed kernel's workgroup whose slots all lie past ``count`` computes nothing (uniform: before any
         barrier); a backward writes zero dL/d(edge features) rows for the edges of its slots."""
         span = 16 * nb * waves
-        P = [f'  const long long slot0 = (long long)blockIdx.x * {span};',
+        P = [f'  const long long slot0 = blk * {span};',
              '  if (slot0 >= ncount) {']
         if zero_rows:
             P += [f'    for (int k = t; k < {span * H0}; k += {64 * waves}) {{',
