@@ -106,7 +106,8 @@ enum mh_kernel_kind {
     MH_NL_BASES = 67,    /* neighbour list: each structure's first edge slot (one workgroup)        */
     MH_EDGE_COUNT = 68,  /* edge compaction: kept edges per workgroup of 4096                       */
     MH_EDGE_PLACE = 69,  /* edge compaction: the row list                                           */
-    MH_NUM_KINDS = 70
+    MH_GEOM_SEGSUM1 = 70, /* per-structure sums of one column (MACE's energy sums)                  */
+    MH_NUM_KINDS = 71
 };
 
 /* flags of mh_conv_bwd */
@@ -372,6 +373,11 @@ int mh_geom_jvp(mh_module* m, const float* vec, const float* len, const float* g
  * (bind MH_GEOM_SEGSUM with 256 threads and rows_per_block 1); fixed summation order.  No reference counterpart. */
 int mh_geom_segsum(mh_module* m, const float* g, const int32_t* perm, const int64_t* seg, float* out, int32_t B,
                    void* stream);
+/* The same for one column, out[b] = sum of g[seg[b]] .. g[seg[b + 1] - 1] (g [M], seg [B + 1] int64, out [B]):
+ * MACE's per-structure energy sums (scatter_sum of the node energies by the sorted batch vector), deterministic
+ * where an atomic index_add is not.  Bind MH_GEOM_SEGSUM1 with 256 threads and rows_per_block 1.  No reference
+ * counterpart. */
+int mh_geom_segsum1(mh_module* m, const float* g, const int64_t* seg, float* out, int32_t B, void* stream);
 
 /* Second derivatives of a SiLU readout head, behind a double backward (v [N, Din] a direction of x): mh_readout_jvp
  * writes de = (de/dx) v [N]; mh_readout_bwd2 the derivative of mh_readout_bwd's gx along v for the given g [N]

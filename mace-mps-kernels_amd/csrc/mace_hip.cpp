@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 32; }
+int mh_version(void) { return 33; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -663,6 +663,13 @@ int mh_geom_segsum(mh_module* m, const float* g, const int32_t* perm, const int6
     if (B > 0 && (!g || !seg || !out)) return fail(-1, "mh_geom_segsum: NULL operand");
     void* args[] = {&g, &perm, &seg, &out, &B};
     return launch(m, MH_GEOM_SEGSUM, B, args, stream, "mh_geom_segsum");
+}
+
+int mh_geom_segsum1(mh_module* m, const float* g, const int64_t* seg, float* out, int32_t B, void* stream) {
+    if (B < 0) return fail(-1, "mh_geom_segsum1: negative structure count");
+    if (B > 0 && (!g || !seg || !out)) return fail(-1, "mh_geom_segsum1: NULL operand");
+    void* args[] = {&g, &seg, &out, &B};
+    return launch(m, MH_GEOM_SEGSUM1, B, args, stream, "mh_geom_segsum1");
 }
 
 int mh_readout_jvp(mh_module* m, const float* x, const float* v, float* de, int64_t N, void* stream) {

@@ -16,13 +16,19 @@ atom and edge carries the same index and the two take ~1.9 ms of a 2.6 ms E+F+st
 and their backward is a segmented sum per structure (``geom_segsum``; atoms by the batch's ptr, edges by the sender
 CSR), one workgroup per structure in a fixed order.
 
-Both computations are module-level functions of MACE, not modules, so ``patch_model`` routes them here through the
+MACE's per-structure energy sums (``scatter_sum`` of the node energies by the batch vector) are an index_add with
+float atomics in PyTorch (~9 us each on config 2's 16 structures, and the summation order varies from run to run);
+here they are a segmented sum over the batch's ptr (``geom_segsum1``), deterministic, taken when the index is the
+batch vector of the running forward itself.
+
+These computations are module-level functions of MACE, not modules, so ``patch_model`` routes them here through the
 model's own module namespace: the functions there are wrapped once, and the wrappers only take this path while a
 patched model's forward is running (a context variable set by that model's forward, which also carries the batch's
-ptr); every other caller, unpatched models included, keeps the original functions.
+batch vector and ptr); every other caller, unpatched models included, keeps the original functions.
 """
 import contextvars
 import functools
+import inspect
 import sys
 import types
 
@@ -34,8 +40,10 @@ from . import conv as _conv
 BLOCK = 256
 _ACTIVE = contextvars.ContextVar('mace_hip_kernels_geometry', default=False)
 _PTR = contextvars.ContextVar('mace_hip_kernels_geometry_ptr', default=None)   # the batch's ptr during a forward
+_BATCH = contextvars.ContextVar('mace_hip_kernels_geometry_batch', default=None)  # the batch vector, likewise
 FUNCTION = 'get_edge_vectors_and_lengths'
 DISPLACEMENT = 'get_symmetric_displacement'
+SCATTER = 'scatter_sum'
 
 _SOURCE = r'''
 #define BLOCK 256
@@ -147,6 +155,24 @@ extern "C" __global__ __launch_bounds__(BLOCK) void geom_segsum(const float* __r
   }
   if (threadIdx.x < SEG_K) out[(long long)b * SEG_K + threadIdx.x] = red[threadIdx.x][0];
 }
+
+// The same for one column (MACE's per-structure energy sums): out[b] = sum of g[seg[b]] .. g[seg[b + 1] - 1].
+extern "C" __global__ __launch_bounds__(BLOCK) void geom_segsum1(const float* __restrict__ g,
+    const long long* __restrict__ seg, float* __restrict__ out, int B) {
+  const int b = blockIdx.x;
+  if (b >= B) return;
+  const long long lo = seg[b], hi = seg[b + 1];
+  float acc = 0.f;
+  for (long long r = lo + threadIdx.x; r < hi; r += BLOCK) acc += g[r];
+  __shared__ float red[BLOCK];
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = BLOCK / 2; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[b] = red[0];
+}
 '''
 
 _modules = {}
@@ -161,7 +187,8 @@ def _module(device):
             _modules[key] = _native.Module(code, {_native.MH_GEOM_FWD: ('geom_fwd', BLOCK, BLOCK),
                                                   _native.MH_GEOM_BWD: ('geom_bwd', BLOCK, BLOCK // 64),
                                                   _native.MH_GEOM_JVP: ('geom_jvp', BLOCK, BLOCK),
-                                                  _native.MH_GEOM_SEGSUM: ('geom_segsum', BLOCK, 1)})
+                                                  _native.MH_GEOM_SEGSUM: ('geom_segsum', BLOCK, 1),
+                                                  _native.MH_GEOM_SEGSUM1: ('geom_segsum1', BLOCK, 1)})
     return _modules[key]
 
 
@@ -303,6 +330,46 @@ class _GraphSegSum(torch.autograd.Function):
         return _GraphGather.apply(gg, index, perm, seg), None, None, None, None
 
 
+def _segsum1(src, seg, B):
+    out = torch.empty(B, device=src.device, dtype=torch.float32)
+    _native.launch('geom_segsum1', _native.load().mh_geom_segsum1, _module(src.device).handle, _native.ptr(src),
+                   _native.ptr(seg), _native.ptr(out), B, _native.stream_of(src))
+    return out
+
+
+class _StructureSum(torch.autograd.Function):
+    """out[b] = sum of src over structure b's atoms (rows ptr[b] .. ptr[b + 1] - 1 of the sorted batch); the backward
+    is the gather g[batch] (_StructureGather), whose own backward is this sum again, so higher orders follow."""
+
+    @staticmethod
+    def forward(ctx, src, batch, seg):
+        ctx.save_for_backward(batch, seg)
+        return _segsum1(src.contiguous(), seg, seg.shape[0] - 1)
+
+    @staticmethod
+    def backward(ctx, g):
+        batch, seg = ctx.saved_tensors
+        return _StructureGather.apply(g, batch, seg), None, None
+
+
+class _StructureGather(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, g, batch, seg):
+        ctx.save_for_backward(batch, seg)
+        return g.index_select(0, batch)
+
+    @staticmethod
+    def backward(ctx, gg):
+        batch, seg = ctx.saved_tensors
+        return _StructureSum.apply(gg, batch, seg), None, None
+
+
+def structure_sum(src, batch, ptr):
+    """Per-structure sums [B] of per-atom values src [N] (float32, GPU) for a sorted batch vector with offsets ptr
+    [B + 1]: MACE's ``scatter_sum(src, batch, dim=0, dim_size=B)``, as segmented sums in a fixed order."""
+    return _StructureSum.apply(src, batch, ptr.to(torch.int64).contiguous())
+
+
 def symmetric_displacement(positions, unit_shifts, cell, edge_index, num_graphs, batch, ptr):
     """MACE's ``get_symmetric_displacement`` (positions and shifts under a symmetric strain of each structure's cell,
     for the virials and the stress) with its two per-structure gathers, sym[batch] over the atoms and
@@ -367,13 +434,44 @@ def _wrap_displacement(orig):
     return get_symmetric_displacement
 
 
+def _wrap_scatter(orig):
+    try:
+        sig = inspect.signature(orig)
+    except (TypeError, ValueError):
+        sig = None
+
+    @functools.wraps(orig)
+    def scatter_sum(src, index, *args, **kwargs):
+        bp = _BATCH.get()
+        if _ACTIVE.get() and bp is not None and sig is not None and index is bp[0]:
+            try:
+                ba = sig.bind(src, index, *args, **kwargs)
+            except TypeError:
+                ba = None
+            if ba is not None:
+                ba.apply_defaults()
+                a = ba.arguments
+                batch, ptr = bp
+                if (a.get('out') is None and a.get('dim') in (0, -1) and torch.is_tensor(src) and src.dim() == 1
+                        and src.is_cuda and src.dtype == torch.float32 and src.shape[0] == batch.shape[0]
+                        and torch.is_tensor(ptr) and ptr.is_cuda and ptr.dim() == 1
+                        and a.get('dim_size') == ptr.shape[0] - 1 and a.get('reduce', 'sum') == 'sum'):
+                    return structure_sum(src, batch, ptr)
+        return orig(src, index, *args, **kwargs)
+    scatter_sum._mh_original = orig
+    return scatter_sum
+
+
 def _forward_with_geometry(self, *args, **kwargs):
     token = _ACTIVE.set('double_backward' if getattr(self, '_mh_geometry_double_backward', False) else True)
     data = args[0] if args else kwargs.get('data')
     token_ptr = _PTR.set(data.get('ptr') if isinstance(data, dict) else None)
+    b = data.get('batch') if isinstance(data, dict) else None
+    token_batch = _BATCH.set((b, data.get('ptr')) if torch.is_tensor(b) and b.dim() == 1 else None)
     try:
         return type(self).forward(self, *args, **kwargs)
     finally:
+        _BATCH.reset(token_batch)
         _PTR.reset(token_ptr)
         _ACTIVE.reset(token)
 
@@ -390,6 +488,9 @@ def install(model):
     disp = getattr(mod, DISPLACEMENT, None)
     if callable(disp) and not hasattr(disp, '_mh_original'):
         setattr(mod, DISPLACEMENT, _wrap_displacement(disp))
+    sc = getattr(mod, SCATTER, None)
+    if callable(sc) and not hasattr(sc, '_mh_original'):
+        setattr(mod, SCATTER, _wrap_scatter(sc))
     model.forward = types.MethodType(_forward_with_geometry, model)
     return True
 

@@ -1051,6 +1051,41 @@ def test_edge_geometry_only_while_a_patched_model_runs():
     assert not any(t.startswith('geom') for t, *_ in tm.records)
 
 
+def test_structure_energy_sums():
+    """MACE's per-structure energy sums as segmented sums over ptr (geometry.structure_sum, geom_segsum1): against
+    float64 index_add with an empty structure and one of more than 256 atoms, the backward (a gather) and its own
+    backward; in a patched model both sums take this path, and two calls give bitwise-equal energies."""
+    from mace_hip_kernels import geometry, patch_model
+    from mace_lite import data as D
+    dev = _dev()
+    print('[case] per-structure energy sums', flush=True)
+    counts = [3, 0, 300, 1, 57]
+    ptr = torch.tensor(np.concatenate([[0], np.cumsum(counts)]), device=dev)
+    batch = torch.repeat_interleave(torch.arange(len(counts), device=dev), torch.tensor(counts, device=dev))
+    src = torch.randn(int(ptr[-1]), device=dev, dtype=torch.float32, requires_grad=True)
+    out = geometry.structure_sum(src, batch, ptr)
+    want = torch.zeros(len(counts), dtype=torch.float64, device=dev).index_add_(0, batch, src.detach().double())
+    assert float((out.double() - want).abs().max()) <= 1e-5 * float(want.abs().max())
+    assert float(out[1]) == 0.0
+    w = torch.randn(len(counts), device=dev, requires_grad=True)
+    g, = torch.autograd.grad((out * w).sum(), src, create_graph=True)
+    assert torch.equal(g.detach(), w.detach()[batch])
+    v = torch.randn_like(src)
+    gw, = torch.autograd.grad((g * v).sum(), w)                   # d/dw of <v, w[batch]> = per-structure sums of v
+    want_gw = torch.zeros(len(counts), dtype=torch.float64, device=dev).index_add_(0, batch, v.double())
+    assert float((gw.double() - want_gw).abs().max()) <= 1e-5 * float(want_gw.abs().max())
+    model, b, _ = factory.workload(2)
+    met = model.to(dev)
+    patch_model(met, verbose=False)
+    b = {k: (t.to(dev) if torch.is_tensor(t) else t) for k, t in b.items()}
+    es = []
+    for _ in range(2):
+        with _native.timing() as tm:
+            es.append(met(D.fresh(b), compute_force=True)['energy'].detach())
+        assert tm.summary()['geom_segsum1'][0] == 2, tm.symbols
+    assert torch.equal(es[0], es[1])
+
+
 @pytest.mark.parametrize('factored', [False, True])
 def test_conv_double_backward_vs_oracle(factored):
     """Second derivatives through the convolution (patched with double_backward): the first-order gradients taken
