@@ -57,6 +57,10 @@ BWD_PC_FENCE = True
 # atomic adds (0 + a + b = 0 + b + a exactly, so the result does not depend on their order), halving that buffer
 # (config 2, layer 1 backward 84 -> 77 us; layer 2's LDS then fits 6 workgroups per CU).
 GY_LDS_ATOMIC = True
+# Edges per chunk of the receiver-ordered kernels (conv_fwd/fwdc, conv_bwdr/bwdrc): 64 (one per lane), or 32 when
+# a 64-edge chunk's coupling products would take more than CHUNK_LDS bytes of LDS (config 4's 17-instruction
+# layer: 48 KB, 1.5 waves per SIMD; at 32 edges 24 KB).  Lanes 32-63 then sit out the chunk prologue only.
+CHUNK_LDS = 24576
 
 
 class _Gen:
@@ -252,6 +256,11 @@ def gy_reduce(indent, y_dim, y_pad, atomic=False):
     return L
 
 
+def chunk_edges(npp):
+    """Edges per chunk of the receiver-ordered kernels for npp coupling products per edge."""
+    return WAVE if WAVE * npp * 4 <= CHUNK_LDS else WAVE // 2
+
+
 def _gy_combine(indent, edge_expr, cut=False, atomic=False):
     """Sum the per-wave gY partials of the current chunk held in LDS and write gY rows (fixed order); with ``cut``
     also the ∂/∂c partials.  The leading barrier also orders the chunk's Ms reads before the next chunk's prologue
@@ -295,9 +304,12 @@ def source(spec):
     L = [_native.device_header(),
          f'#define MUL {spec.mul}', f'#define NCB {spec.ncb}', f'#define BLOCK {spec.block}',
          f'#define X_DIM {spec.x_dim}', f'#define Y_DIM {spec.y_dim}', f'#define Y_PAD {spec.y_pad}',
-         f'#define OUT_DIM {spec.out_dim}', f'#define NW {spec.nins * spec.mul}', f'#define NPP {G.npp}']
+         f'#define OUT_DIM {spec.out_dim}', f'#define NW {spec.nins * spec.mul}', f'#define NPP {G.npp}',
+         f'#define CHUNK {chunk_edges(G.npp)}']
     ms_decl = ['  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
                '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);']
+    ms_decl_c = ['  __shared__ float4 Ms4[CHUNK][NPP / 4];',
+                 '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);']
     # ------------------------------------------------------------------------------------------- forward
     def fwd_kernel(cut):
         """``cut`` (kernel ``conv_fwdc``): the weights are W0·c with a per-edge scalar c, read as W0 and scaled in
@@ -310,17 +322,17 @@ def source(spec):
             '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
             '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
             '    float* __restrict__ out, int N' + (', const float* __restrict__ cutv) {' if cut else ') {'),
-        ] + ms_decl + (['  __shared__ int sidx[NCB][MH_WAVE];'] if cut else []) + [
+        ] + ms_decl_c + (['  __shared__ int sidx[NCB][CHUNK];'] if cut else []) + [
             '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
             '  if (n >= N) return;',
         ] + G.prelude() + [
             '  ' + decl('acc', no, '0.0f'),
             '  ' + decl('xn', nx), '  ' + decl('wn', nk),
             '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
-            '  for (int pb = p0; pb < p1; pb += MH_WAVE) {',
+            '  for (int pb = p0; pb < p1; pb += CHUNK) {',
         ]
         if cut:
-            F += ['    const int cnt0 = min(MH_WAVE, p1 - pb);',
+            F += ['    const int cnt0 = min(CHUNK, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
                   '    bool keep = false;',
                   '    if (lane < cnt0) { my_e = eids[pb + lane]; keep = cutv[my_e] != 0.0f; }',
@@ -331,7 +343,7 @@ def source(spec):
                   '    float my_c = 0.0f;',
                   '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e]; }']
         else:
-            F += ['    const int cnt = min(MH_WAVE, p1 - pb);',
+            F += ['    const int cnt = min(CHUNK, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
                   '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
         F += G.m_prologue('    ', 'my_e')
@@ -472,16 +484,16 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         '    const int* __restrict__ senders, float* __restrict__ gW, float* __restrict__ gY,',
         '    float* __restrict__ gxm, int N, int flags' +
         (', const float* __restrict__ cutv, float* __restrict__ gcut) {' if cut else ') {'),
-        '  __shared__ float part[MH_WAVE][Y_PAD];' if atomic else '  __shared__ float part[NCB][MH_WAVE][Y_PAD];',
-    ] + ((['  __shared__ float partc[MH_WAVE];'] if atomic else ['  __shared__ float partc[NCB][MH_WAVE];']) +
-         ['  __shared__ int sidx[NCB][MH_WAVE];'] if cut else []) + [
-        '  __shared__ float4 Ms4[MH_WAVE][NPP / 4];',
+        '  __shared__ float part[CHUNK][Y_PAD];' if atomic else '  __shared__ float part[NCB][CHUNK][Y_PAD];',
+    ] + ((['  __shared__ float partc[CHUNK];'] if atomic else ['  __shared__ float partc[NCB][CHUNK];']) +
+         ['  __shared__ int sidx[NCB][CHUNK];'] if cut else []) + [
+        '  __shared__ float4 Ms4[CHUNK][NPP / 4];',
         '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);',
         '  const int r = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  if (r >= N) return;',
     ] + ([
-        '  for (int q = threadIdx.x; q < MH_WAVE * Y_PAD; q += BLOCK) (&part[0][0])[q] = 0.0f;',
-    ] + (['  for (int q = threadIdx.x; q < MH_WAVE; q += BLOCK) partc[q] = 0.0f;'] if cut else []) + [
+        '  for (int q = threadIdx.x; q < CHUNK * Y_PAD; q += BLOCK) (&part[0][0])[q] = 0.0f;',
+    ] + (['  for (int q = threadIdx.x; q < CHUNK; q += BLOCK) partc[q] = 0.0f;'] if cut else []) + [
         '  __syncthreads();',
     ] if atomic else []) + G.prelude() + [
         '  const bool GX = (flags & 1) != 0;',
@@ -496,11 +508,11 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
     L += ['  const int p0 = rowptr[r], p1 = rowptr[r + 1];']
 
     def chunks(msg):
-        C = ['  for (int pb = p0; pb < p1; pb += MH_WAVE) {']
+        C = ['  for (int pb = p0; pb < p1; pb += CHUNK) {']
         if cut:
             # every wave reads the same edges and cutoffs, so ballots, counts and the `continue` are uniform over
             # the workgroup and the barriers below stay matched
-            C += ['    const int cnt0 = min(MH_WAVE, p1 - pb);',
+            C += ['    const int cnt0 = min(CHUNK, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
                   '    bool keep = false;',
                   '    if (lane < cnt0) {',
@@ -526,7 +538,7 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
                   '    float my_c = 0.0f;                  // the cutoff of lane j\'s edge, broadcast per edge below',
                   '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e]; }']
         else:
-            C += ['    const int cnt = min(MH_WAVE, p1 - pb);',
+            C += ['    const int cnt = min(CHUNK, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
                   '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
         C += G.m_prologue('    ', 'my_e')

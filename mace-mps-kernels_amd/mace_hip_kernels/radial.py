@@ -50,6 +50,11 @@ CH_BWD = 32          # and backward (a multiple of 32: one bf16 MFMA K step per 
 NSPLIT = 3           # bf16 parts per fp32 weight (exact split)
 BPAD = 8             # bf16 row padding of a chunk (keeps 16-byte reads aligned, spreads banks)
 PAD = 4              # LDS row padding (floats): the 4 lane groups of a fragment land on different banks
+# Waves per SIMD the forward and backward are compiled for (amdgpu_waves_per_eu; None: the compiler's choice).
+# Left to itself the compiler gives mlp_fwd 172 VGPRs + 48 AGPRs (2 waves per SIMD); asked for 3 it fits in 138
+# VGPRs without spills, mlp_bwd in 154.
+WAVES_FWD = 3
+WAVES_BWD = 3
 
 
 def _layers(mod):
@@ -227,7 +232,7 @@ def _source(spec, second):
               '__device__ __forceinline__ float mlp_d2(float z) { const float s = mlp_sig(z); '
               'return s * (1.f - s) * (2.f + z * (1.f - 2.f * s)); }', '']
 
-    def head(name, args, lds, nb, waves=BLOCK // 64, indexed=False):
+    def head(name, args, lds, nb, waves=BLOCK // 64, indexed=False, wpe=None):
         """Kernel prologue: edge slot ej{b} of this lane in tile b (live{b}: a slot < E).  ``indexed``: two more
         arguments, ``rows`` (NULL, or the edge of each slot) and ``count`` (NULL, or the number of slots to compute:
         the rest are not computed, and a backward writes zero gradient rows for their edges); rowc{b} is the edge of
@@ -235,7 +240,8 @@ def _source(spec, second):
         if indexed:
             args += ', const int* __restrict__ rows, const int* __restrict__ count'
         span = 16 * nb * waves
-        P = [f'extern "C" __global__ __launch_bounds__({64 * waves}) void {name}({args}) {{',
+        occ = f' __attribute__((amdgpu_waves_per_eu({wpe})))' if wpe else ''
+        P = [f'extern "C" __global__ __launch_bounds__({64 * waves}){occ} void {name}({args}) {{',
              f'  __shared__ __align__(16) float lds[{lds}];',
              '  unsigned short* __restrict__ ldsb = reinterpret_cast<unsigned short*>(lds);',
              '  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
@@ -380,7 +386,7 @@ def _source(spec, second):
         ncf = 2 if nb == 1 else 1                            # accumulator chains per result tile
         F = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if tangent else '') +
                  'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, float* __restrict__ W0, long long E',
-                 lds_fwd, nb, indexed=not tangent)
+                 lds_fwd, nb, indexed=not tangent, wpe=None if tangent else WAVES_FWD)
         if not tangent:
             F += skip_block(nb, zero_rows=False)
         F += stage('Wh', Lo['tr_size']) + ['  __syncthreads();'] + xin(range(nb))
@@ -527,7 +533,7 @@ def _source(spec, second):
         TAIL = NW % CH != 0
         B = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if dual else '') +
                  'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, const float* __restrict__ gW, '
-                 'float* __restrict__ gef, long long E', lds_bwd, nb, indexed=not dual)
+                 'float* __restrict__ gef, long long E', lds_bwd, nb, indexed=not dual, wpe=None if dual else WAVES_BWD)
         if not dual:
             B += skip_block(nb, zero_rows=True)
         for b in range(nb):

@@ -114,23 +114,26 @@ def test_conv_bwd_without_dx(order):
 
 
 @pytest.mark.parametrize('masked', [False, True])
-@pytest.mark.parametrize('want_x', [True, False])
-def test_conv_factored_cutoff_weights(want_x, masked):
+@pytest.mark.parametrize('want_x,hidden', [(True, '128x0e+128x1o'), (False, '128x0e+128x1o'),
+                                           (True, '128x0e+128x1o+128x2e')])
+def test_conv_factored_cutoff_weights(want_x, hidden, masked):
     """tp_weights = W0 * cutoff (MACE's form): the backward kernel returns d/dW0 and d/dcutoff itself.  Against the
     oracle: d/dW0 = gW * c, d/dc = sum_k gW * W0 (gW the oracle's d/dW), with some cutoffs exactly zero (padding).
     ``masked``: the cutoff is marked as a patched radial embedding's (-0.0 outside the envelope's support), and
     every third edge holds -0.0: the backward skips those edges (MH_CUT_MASKED), so d/dcutoff is 0 there while
-    +0.0 edges keep the exact partial; every other gradient equals the unmasked call's."""
+    +0.0 edges keep the exact partial; every other gradient equals the unmasked call's.  The 17-instruction layer
+    (l = 0, 1, 2 features) walks its receivers in chunks of 32 edges instead of 64 (its coupling products would
+    not fit the LDS budget at 64)."""
     dev = _dev()
-    print(f'[case] conv factored cutoff weights want_x={want_x} masked={masked}', flush=True)
-    tp = _tp('128x0e+128x1o', 3)
+    print(f'[case] conv factored cutoff weights want_x={want_x} hidden={hidden} masked={masked}', flush=True)
+    tp = _tp(hidden, 3)
     op = HipConvTP(tp, device=dev)
     desc = oconv.describe_tp(tp)
     coef = oconv.path_terms(desc)
     rng = np.random.default_rng(6)
     n, e = 41, 700
     s, r = _graph(rng, n, e)
-    x, Y, W0 = (rng.normal(size=sh) for sh in ((n, desc['x_dim']), (e, desc['y_dim']), (e, 10 * 128)))
+    x, Y, W0 = (rng.normal(size=sh) for sh in ((n, desc['x_dim']), (e, desc['y_dim']), (e, op.spec.nins * 128)))
     c = rng.uniform(0.0, 1.0, size=(e, 1))
     c[::7] = 0.0
     c[r == 2] = 0.0                  # a receiver whose every edge is skipped by the forward
