@@ -38,6 +38,7 @@ BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of an MFMA row tile
 NT = 2               # row tiles per wave: each LDS weight fragment feeds NT MFMAs
+PREFETCH_BF16 = 2    # chunks whose global loads are in flight ahead of the one being multiplied (1 or 2), bf16 family
 XPAD = 4             # floats of padding per LDS row of staged inputs
 WPAD = 8             # bf16 of padding per LDS row of staged weights
 
@@ -328,49 +329,50 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         L += ['  };']
         # staging: thread piece it of the inputs is node nl = f / (8 D), float4 e = f % (8 D) of the node's run of
         # 32 d floats (channel-major, component-minor, as in e3nn's layout)
-        L += [f'  mh_f4 {", ".join(f"px{k}" for k in range(ix))};',
-              f'  mh_u4 {", ".join(f"pw{k}" for k in range(iw))};',
-              '  auto load = [&](int c) {',
-              '    int oi, mi, uc, v, wo;',
-              '    where(c, oi, mi, uc, v, wo);',
-              '    (void)v;']
-        # float4 loads where every input block of this output block starts and ends on a 16-byte boundary (a
-        # one-hot node embedding with, say, 89 elements does not): else four scalar loads
-        vec = Din % 4 == 0 and all(in_blocks[i][2] % 4 == 0 and in_blocks[i][0] * D % 4 == 0 for i, _ in terms[o])
-        for k in range(ix):
-            fx = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NXP else f'min(t + {k * BLOCK}, {NXP - 1})'
-            L += [f'    {{ const int f = {fx}, nl = f / {8 * D}, e = f - nl * {8 * D};',
-                  '      const int n = nd(min(g0 + nl, N - 1));',
-                  f'      const float* __restrict__ xr = x + (size_t)n * {Din} + oi;']
-            if vec:     # past the block: any valid input (its weights are zero)
-                L += [f'      px{k} = *reinterpret_cast<const mh_f4*>(xr + min(uc * {KC * D} + 4 * e, mi * {D} - 4)); }}']
-            else:
-                L += [f'      px{k}[{j}] = xr[min(uc * {KC * D} + 4 * e + {j}, mi * {D} - 1)];' for j in range(4)]
-                L[-1] += ' }'
-        for k in range(iw):
-            fw = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NWP else f'min(t + {k * BLOCK}, {NWP - 1})'
-            L += [f'    pw{k} = *reinterpret_cast<const mh_u4*>(Wg + wo + (size_t)({fw}) * 8);']
-        L += ['  };',
-              '  auto store = [&](int buf) {',
-              f'    float* __restrict__ xs = lds + buf * {XB};',
-              f'    unsigned short* __restrict__ ws = reinterpret_cast<unsigned short*>(lds + {2 * XB} + buf * {WB});']
-        for k in range(ix):
-            guard = '' if (k + 1) * BLOCK <= NXP else f'if (t + {k * BLOCK} < {NXP}) '
-            L += [f'    {guard}{{ const int f = t + {k * BLOCK}, nl = f / {8 * D}, e = f - nl * {8 * D};']
-            if D == 1:
-                L += [f'      *reinterpret_cast<mh_f4*>(xs + nl * {XS} + 4 * e) = px{k}; }}']
-            else:
-                L += ['#pragma unroll',
-                      '      for (int j = 0; j < 4; ++j) {',
-                      f'        const int idx = 4 * e + j, u = idx / {D}, m = idx - u * {D};',
-                      f'        xs[(nl * {D} + m) * {XS} + u] = px{k}[j];',
-                      '      } }']
-        for k in range(iw):
-            guard = '' if (k + 1) * BLOCK <= NWP else f'if (t + {k * BLOCK} < {NWP}) '
-            L += [f'    {guard}{{ const int f = t + {k * BLOCK}, p = f / {CW * KC // 8}, r = f - p * {CW * KC // 8},',
-                  f'        k8 = r / {CW}, col = r - k8 * {CW};',
-                  f'      *reinterpret_cast<mh_u4*>(ws + (p * {CW} + col) * {WS} + 8 * k8) = pw{k}; }}']
-        L += ['  };']
+        for S in (['A', 'B'] if PREFETCH_BF16 == 2 else ['']):
+            L += [f'  mh_f4 {", ".join(f"px{S}{k}" for k in range(ix))};',
+                  f'  mh_u4 {", ".join(f"pw{S}{k}" for k in range(iw))};',
+                  f'  auto load{S} = [&](int c) {{',
+                  '    int oi, mi, uc, v, wo;',
+                  '    where(c, oi, mi, uc, v, wo);',
+                  '    (void)v;']
+            # float4 loads where every input block of this output block starts and ends on a 16-byte boundary (a
+            # one-hot node embedding with, say, 89 elements does not): else four scalar loads
+            vec = Din % 4 == 0 and all(in_blocks[i][2] % 4 == 0 and in_blocks[i][0] * D % 4 == 0 for i, _ in terms[o])
+            for k in range(ix):
+                fx = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NXP else f'min(t + {k * BLOCK}, {NXP - 1})'
+                L += [f'    {{ const int f = {fx}, nl = f / {8 * D}, e = f - nl * {8 * D};',
+                      '      const int n = nd(min(g0 + nl, N - 1));',
+                      f'      const float* __restrict__ xr = x + (size_t)n * {Din} + oi;']
+                if vec:     # past the block: any valid input (its weights are zero)
+                    L += [f'      px{S}{k} = *reinterpret_cast<const mh_f4*>(xr + min(uc * {KC * D} + 4 * e, mi * {D} - 4)); }}']
+                else:
+                    L += [f'      px{S}{k}[{j}] = xr[min(uc * {KC * D} + 4 * e + {j}, mi * {D} - 1)];' for j in range(4)]
+                    L[-1] += ' }'
+            for k in range(iw):
+                fw = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NWP else f'min(t + {k * BLOCK}, {NWP - 1})'
+                L += [f'    pw{S}{k} = *reinterpret_cast<const mh_u4*>(Wg + wo + (size_t)({fw}) * 8);']
+            L += ['  };',
+                  f'  auto store{S} = [&](int buf) {{',
+                  f'    float* __restrict__ xs = lds + buf * {XB};',
+                  f'    unsigned short* __restrict__ ws = reinterpret_cast<unsigned short*>(lds + {2 * XB} + buf * {WB});']
+            for k in range(ix):
+                guard = '' if (k + 1) * BLOCK <= NXP else f'if (t + {k * BLOCK} < {NXP}) '
+                L += [f'    {guard}{{ const int f = t + {k * BLOCK}, nl = f / {8 * D}, e = f - nl * {8 * D};']
+                if D == 1:
+                    L += [f'      *reinterpret_cast<mh_f4*>(xs + nl * {XS} + 4 * e) = px{S}{k}; }}']
+                else:
+                    L += ['#pragma unroll',
+                          '      for (int j = 0; j < 4; ++j) {',
+                          f'        const int idx = 4 * e + j, u = idx / {D}, m = idx - u * {D};',
+                          f'        xs[(nl * {D} + m) * {XS} + u] = px{S}{k}[j];',
+                          '      } }']
+            for k in range(iw):
+                guard = '' if (k + 1) * BLOCK <= NWP else f'if (t + {k * BLOCK} < {NWP}) '
+                L += [f'    {guard}{{ const int f = t + {k * BLOCK}, p = f / {CW * KC // 8}, r = f - p * {CW * KC // 8},',
+                      f'        k8 = r / {CW}, col = r - k8 * {CW};',
+                      f'      *reinterpret_cast<mh_u4*>(ws + (p * {CW} + col) * {WS} + 8 * k8) = pw{S}{k}; }}']
+            L += ['  };']
         # the lane's A rows: row c16 of each of its tiles (rows past the tile's nodes read row 0; never stored)
         for tt in range(NT):
             L += [f'  const int xr{tt} = {(tt) * TN * D} + wave * {NT * TN * D} + (c16 < {TN * D} ? c16 : 0);']
@@ -381,42 +383,66 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
               f'  for (int a = 0; a < {NT}; ++a)',
               '#pragma unroll',
               f'    for (int b = 0; b < {CT}; ++b) acc[a][b] = mh_f4{{0.f, 0.f, 0.f, 0.f}};',
-              '  load(0);',
-              '  store(0);',
-              '  __syncthreads();',
-              '  for (int c = 0; c < nch; ++c) {',
-              '    load(min(c + 1, nch - 1));',
-              '    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs',
-              f'    const float* __restrict__ xs = lds + (c & 1) * {XB};',
-              f'    const unsigned short* __restrict__ ws = reinterpret_cast<const unsigned short*>(lds + {2 * XB} + '
-              f'(c & 1) * {WB});']
-        if V:
-            L += ['    int oi_, mi_, uc_, v, wo_;', '    where(c, oi_, mi_, uc_, v, wo_);']
+]
+
+        def body(cc, buf):
+            """The MFMAs of chunk ``cc`` from LDS buffer ``buf`` (xs / ws scoped to it)."""
+            B = ['    {',
+                 f'    const float* __restrict__ xs = lds + ({buf}) * {XB};',
+                 f'    const unsigned short* __restrict__ ws = reinterpret_cast<const unsigned short*>(lds + {2 * XB} + '
+                 f'({buf}) * {WB});']
+            if V:
+                B += ['    int oi_, mi_, uc_, v, wo_;', f'    where({cc}, oi_, mi_, uc_, v, wo_);']
+            return B + BODY + ['    }']
+
+        BODY = []
         for tt in range(NT):
-            L += [f'    mh_bf8 a{tt}[3];',
+            BODY += [f'    mh_bf8 a{tt}[3];',
                   '    {',
                   f'      const mh_f4 lo = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q);',
                   f'      const mh_f4 hi = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q + 4);']
             if V:
-                L += [f'      const float s = attr[(size_t)an{tt} * {V} + v];',
+                BODY += [f'      const float s = attr[(size_t)an{tt} * {V} + v];',
                       '      const float v8[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, '
                       'hi[2] * s, hi[3] * s};']
             else:
-                L += ['      const float v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};']
-            L += [f'      mh_split8(v8, a{tt});', '    }']
+                BODY += ['      const float v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};']
+            BODY += [f'      mh_split8(v8, a{tt});', '    }']
         PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
         for ct in range(CT):
-            L += [f'    {{ mh_bf8 b[3];']
-            L += [f'      b[{p}] = *reinterpret_cast<const mh_bf8*>(ws + ({p * CW + 16 * ct} + c16) * {WS} + 8 * q);'
+            BODY += [f'    {{ mh_bf8 b[3];']
+            BODY += [f'      b[{p}] = *reinterpret_cast<const mh_bf8*>(ws + ({p * CW + 16 * ct} + c16) * {WS} + 8 * q);'
                   for p in range(3)]
             for pa, pb in PAIRS:
                 for tt in range(NT):
-                    L.append(f'      acc[{tt}][{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{tt}[{pa}], b[{pb}], '
+                    BODY.append(f'      acc[{tt}][{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{tt}[{pa}], b[{pb}], '
                              f'acc[{tt}][{ct}], 0, 0, 0);')
-            L += ['    }']
-        L += ['    store((c + 1) & 1);',
-              '    __syncthreads();',
-              '  }']
+            BODY += ['    }']
+        if PREFETCH_BF16 == 2:
+            # two register sets: chunk c + 1's loads (set B) were issued a whole chunk before they are stored to LDS
+            L += ['  loadA(0);', '  loadB(min(1, nch - 1));', '  storeA(0);', '  __syncthreads();',
+                  '  for (int c = 0; c < nch; c += 2) {',
+                  '    loadA(min(c + 2, nch - 1));',
+                  '    __builtin_amdgcn_sched_barrier(0);            // chunk c + 2\'s loads go out before the MFMAs']
+            L += body('c', '0')
+            L += ['    storeB(1);',
+                  '    __syncthreads();',
+                  '    if (c + 1 >= nch) break;',
+                  '    loadB(min(c + 3, nch - 1));',
+                  '    __builtin_amdgcn_sched_barrier(0);']
+            L += body('c + 1', '1')
+            L += ['    storeA(0);',
+                  '    __syncthreads();',
+                  '  }']
+        else:
+            L += ['  load(0);', '  store(0);', '  __syncthreads();',
+                  '  for (int c = 0; c < nch; ++c) {',
+                  '    load(min(c + 1, nch - 1));',
+                  '    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
+            L += body('c', '(c & 1)')
+            L += ['    store((c + 1) & 1);',
+                  '    __syncthreads();',
+                  '  }']
         # epilogue: lane (c16, q) holds rows 4q + r, column 16 ct + c16 of each tile -> LDS [node][column][m] ->
         # coalesced float4 rows of CW d floats per node
         L += ['#pragma unroll',
@@ -448,7 +474,10 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha, order); break;')
     sw += ['    default: break;', '  }']
     lds_max = max(lds_max, 4)
-    K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
+    # two workgroups per CU fit the LDS; keep the registers within two waves per SIMD as well (the second prefetch
+    # register set would otherwise push the count past 256 and halve the occupancy)
+    occ = ' __attribute__((amdgpu_waves_per_eu(2)))' if PREFETCH_BF16 == 2 else ''
+    K = [f'extern "C" __global__ __launch_bounds__({BLOCK}){occ} void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N,',
          '    const int* __restrict__ order, float alpha) {',
          '  (void)order;',
