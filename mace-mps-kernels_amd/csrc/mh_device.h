@@ -19,6 +19,12 @@ __device__ __forceinline__ int mh_xcd_block(int b, int nblocks) {
 // Value of `v` in lane `j` (j wave-uniform) as a scalar.
 __device__ __forceinline__ int mh_bcast(int v, int j) { return __builtin_amdgcn_readlane(v, j); }
 
+// index of the k-th set bit (k from 0) of a wave-uniform mask
+__device__ __forceinline__ int mh_kth_bit(unsigned m, int k) {
+  for (; k > 0; --k) m &= m - 1u;
+  return __builtin_ctz(m);
+}
+
 // Exclusive prefix sum of v over the workgroup (NW waves of 64, every thread calling), in a fixed order: an inclusive
 // scan inside each wave by shuffles, then the wave totals (through LDS `wsum`, NW entries) added in wave order.
 // `total` receives the workgroup's sum.  Two barriers; `wsum` may be reused after the call.

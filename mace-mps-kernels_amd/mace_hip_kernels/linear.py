@@ -38,7 +38,8 @@ BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of an MFMA row tile
 NT = 2               # row tiles per wave: each LDS weight fragment feeds NT MFMAs
-PREFETCH_BF16 = 2    # chunks whose global loads are in flight ahead of the one being multiplied (1 or 2), bf16 family
+NT_ATTRS = 1         # the same for skip_tp (attribute terms), bf16 family: one tile per wave, twice the workgroups
+PREFETCH_BF16 = 2    # chunks whose global loads are in flight ahead of the one being multiplied (1, 2 or 4), bf16 family
 XPAD = 4             # floats of padding per LDS row of staged inputs
 WPAD = 8             # bf16 of padding per LDS row of staged weights
 
@@ -205,17 +206,24 @@ def _grid_y(blocks):
     return [(o, cg) for o, (mo, *_) in enumerate(blocks) for cg in range(mo // _cw(mo))]
 
 
-def _group(l):
+def _tiles(V):
+    """Row tiles per wave of the bf16 family: NT, or NT_ATTRS for attribute terms (skip_tp).  Measured on config 2's
+    2048 -> 2048 x 4-element skip_tp: 37.9 us with two tiles per wave, 28.3 us with one (more workgroups hide the
+    attribute-mask prologue); the attribute-free linears are within noise of each other at one or two."""
+    return NT_ATTRS if V else NT
+
+
+def _group(l, nt=NT):
     """(nodes per row tile, nodes per workgroup) for output irreps of degree l: a tile is 16 // (2l + 1) whole
-    nodes (<= 16 rows (node, m)), each wave holds NT tiles."""
+    nodes (<= 16 rows (node, m)), each wave holds nt tiles."""
     tn = ROWS // (2 * l + 1)
-    return tn, WAVES * NT * tn
+    return tn, WAVES * nt * tn
 
 
-def _nodes_per_launch_group(blocks):
+def _nodes_per_launch_group(blocks, nt=NT):
     """Nodes per workgroup of the launch: the smallest over the output blocks (blocks with more nodes per workgroup
     leave their trailing workgroups idle)."""
-    return min(_group(l)[1] for _, l, *_ in blocks)
+    return min(_group(l, nt)[1] for _, l, *_ in blocks)
 
 
 def pack(blocks, terms, in_blocks, wmats, V):
@@ -266,9 +274,10 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     (a node's CW d outputs of a block are contiguous)."""
     fns, cases, lds_max = [], [], 0
     VV = max(V, 1)
+    NT = _tiles(V)
     for o, (mo, l, oo, _) in enumerate(out_blocks):
         D = 2 * l + 1
-        TN, G = _group(l)
+        TN, G = _group(l, NT)
         CW = _cw(mo)
         CT = CW // 16
         fn = f'{name}_b{o}'
@@ -295,7 +304,11 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         XR = G * D                                   # staged input rows
         XB = XR * XS                                 # floats per input buffer
         WB = 3 * CW * WS // 2                        # floats per weight buffer
-        lds = max(2 * (XB + WB), G * CW * D)
+        # attribute values a[n, v] of each thread's rows for the staged chunk (skip_tp): loaded with the chunk's other
+        # operands and passed through LDS, so the MFMA body never waits on a global load
+        SOFF = 2 * (XB + WB)
+        SB = NT * BLOCK if V else 0                  # floats per attribute buffer
+        lds = max(SOFF + 2 * SB, G * CW * D)
         lds_max = max(lds_max, lds)
         NXP = G * KC * D // 4                        # float4 pieces of a chunk's inputs
         NWP = 3 * CW * KC // 8                       # 16-byte pieces of a chunk's weights
@@ -303,7 +316,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         L += ['  const int wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
               '  (void)lane;']
         if V:
-            L += _mask(V, 'g0', 'ng', ordered=True)
+            L += _mask_wave(V, 'g0', 'ng') if V <= 32 else _mask(V, 'g0', 'ng', ordered=True)
         else:
             L += ['  const int nact = 1;']
         # chunk c -> term ti (compile-time boundaries scaled by nact), attribute v, channel chunk uc
@@ -320,7 +333,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
             L += [f'    if ({cond}) {{',
                   f'      const int vv = r / {nc};',
                   f'      uc = r - vv * {nc}; oi = {oi_}; mi = {mi_};',
-                  f'      v = {"vlist[1 + vv]" if V else "0"};',
+                  f'      v = {("mh_kth_bit(amw, vv)" if V <= 32 else "vlist[1 + vv]") if V else "0"};',
                   f'      wo = {toffs[o][k]} + (v * {nc} + uc) * {3 * CW * KC};',
                   '      return;',
                   '    }']
@@ -329,21 +342,36 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         L += ['  };']
         # staging: thread piece it of the inputs is node nl = f / (8 D), float4 e = f % (8 D) of the node's run of
         # 32 d floats (channel-major, component-minor, as in e3nn's layout)
-        for S in (['A', 'B'] if PREFETCH_BF16 == 2 else ['']):
+        # the lane's A rows: row c16 of each of its tiles (rows past the tile's nodes read row 0; never stored)
+        for tt in range(NT):
+            L += [f'  const int xr{tt} = {(tt) * TN * D} + wave * {NT * TN * D} + (c16 < {TN * D} ? c16 : 0);']
+            if V:
+                L += [f'  const int an{tt} = nd(min(g0 + xr{tt} / {D}, N - 1));']
+        # node of each of the thread's input pieces, once (the chunk loop's loads then depend on no index load;
+        # kept out of the loaders, whose order[] loads the compiler cannot hoist past the LDS stores)
+        for k in range(ix):
+            fx = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NXP else f'min(t + {k * BLOCK}, {NXP - 1})'
+            L += [f'  const int xn{k} = nd(min(g0 + ({fx}) / {8 * D}, N - 1));']
+        SETS = 'ABCD'[:PREFETCH_BF16] if PREFETCH_BF16 > 1 else ['']
+        for S in SETS:
             L += [f'  mh_f4 {", ".join(f"px{S}{k}" for k in range(ix))};',
-                  f'  mh_u4 {", ".join(f"pw{S}{k}" for k in range(iw))};',
-                  f'  auto load{S} = [&](int c) {{',
+                  f'  mh_u4 {", ".join(f"pw{S}{k}" for k in range(iw))};']
+            if V:
+                L += [f'  float {", ".join(f"ps{S}{tt}" for tt in range(NT))};']
+            L += [f'  auto load{S} = [&](int c) {{',
                   '    int oi, mi, uc, v, wo;',
                   '    where(c, oi, mi, uc, v, wo);',
                   '    (void)v;']
+            if V:
+                L += [f'    ps{S}{tt} = attr[(size_t)an{tt} * {V} + v];' for tt in range(NT)]
             # float4 loads where every input block of this output block starts and ends on a 16-byte boundary (a
             # one-hot node embedding with, say, 89 elements does not): else four scalar loads
             vec = Din % 4 == 0 and all(in_blocks[i][2] % 4 == 0 and in_blocks[i][0] * D % 4 == 0 for i, _ in terms[o])
             for k in range(ix):
                 fx = f't + {k * BLOCK}' if (k + 1) * BLOCK <= NXP else f'min(t + {k * BLOCK}, {NXP - 1})'
                 L += [f'    {{ const int f = {fx}, nl = f / {8 * D}, e = f - nl * {8 * D};',
-                      '      const int n = nd(min(g0 + nl, N - 1));',
-                      f'      const float* __restrict__ xr = x + (size_t)n * {Din} + oi;']
+                      '      (void)nl;',
+                      f'      const float* __restrict__ xr = x + (size_t)xn{k} * {Din} + oi;']
                 if vec:     # past the block: any valid input (its weights are zero)
                     L += [f'      px{S}{k} = *reinterpret_cast<const mh_f4*>(xr + min(uc * {KC * D} + 4 * e, mi * {D} - 4)); }}']
                 else:
@@ -356,6 +384,8 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                   f'  auto store{S} = [&](int buf) {{',
                   f'    float* __restrict__ xs = lds + buf * {XB};',
                   f'    unsigned short* __restrict__ ws = reinterpret_cast<unsigned short*>(lds + {2 * XB} + buf * {WB});']
+            if V:
+                L += [f'    lds[{SOFF} + buf * {SB} + {tt * BLOCK} + t] = ps{S}{tt};' for tt in range(NT)]
             for k in range(ix):
                 guard = '' if (k + 1) * BLOCK <= NXP else f'if (t + {k * BLOCK} < {NXP}) '
                 L += [f'    {guard}{{ const int f = t + {k * BLOCK}, nl = f / {8 * D}, e = f - nl * {8 * D};']
@@ -373,11 +403,6 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                       f'        k8 = r / {CW}, col = r - k8 * {CW};',
                       f'      *reinterpret_cast<mh_u4*>(ws + (p * {CW} + col) * {WS} + 8 * k8) = pw{S}{k}; }}']
             L += ['  };']
-        # the lane's A rows: row c16 of each of its tiles (rows past the tile's nodes read row 0; never stored)
-        for tt in range(NT):
-            L += [f'  const int xr{tt} = {(tt) * TN * D} + wave * {NT * TN * D} + (c16 < {TN * D} ? c16 : 0);']
-            if V:
-                L += [f'  const int an{tt} = nd(min(g0 + xr{tt} / {D}, N - 1));']
         L += [f'  mh_f4 acc[{NT}][{CT}];',
               '#pragma unroll',
               f'  for (int a = 0; a < {NT}; ++a)',
@@ -392,7 +417,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                  f'    const unsigned short* __restrict__ ws = reinterpret_cast<const unsigned short*>(lds + {2 * XB} + '
                  f'({buf}) * {WB});']
             if V:
-                B += ['    int oi_, mi_, uc_, v, wo_;', f'    where({cc}, oi_, mi_, uc_, v, wo_);']
+                B += [f'    const float* __restrict__ ss = lds + {SOFF} + ({buf}) * {SB};']
             return B + BODY + ['    }']
 
         BODY = []
@@ -402,7 +427,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                   f'      const mh_f4 lo = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q);',
                   f'      const mh_f4 hi = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q + 4);']
             if V:
-                BODY += [f'      const float s = attr[(size_t)an{tt} * {V} + v];',
+                BODY += [f'      const float s = ss[{tt * BLOCK} + t];',
                       '      const float v8[8] = {lo[0] * s, lo[1] * s, lo[2] * s, lo[3] * s, hi[0] * s, hi[1] * s, '
                       'hi[2] * s, hi[3] * s};']
             else:
@@ -418,22 +443,22 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                     BODY.append(f'      acc[{tt}][{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{tt}[{pa}], b[{pb}], '
                              f'acc[{tt}][{ct}], 0, 0, 0);')
             BODY += ['    }']
-        if PREFETCH_BF16 == 2:
-            # two register sets: chunk c + 1's loads (set B) were issued a whole chunk before they are stored to LDS
-            L += ['  loadA(0);', '  loadB(min(1, nch - 1));', '  storeA(0);', '  __syncthreads();',
-                  '  for (int c = 0; c < nch; c += 2) {',
-                  '    loadA(min(c + 2, nch - 1));',
-                  '    __builtin_amdgcn_sched_barrier(0);            // chunk c + 2\'s loads go out before the MFMAs']
-            L += body('c', '0')
-            L += ['    storeB(1);',
-                  '    __syncthreads();',
-                  '    if (c + 1 >= nch) break;',
-                  '    loadB(min(c + 3, nch - 1));',
-                  '    __builtin_amdgcn_sched_barrier(0);']
-            L += body('c + 1', '1')
-            L += ['    storeA(0);',
-                  '    __syncthreads();',
-                  '  }']
+        if PREFETCH_BF16 > 1:
+            # P register sets (a ring): chunk c's loads go into set c mod P a whole P - 1 chunks before they are stored
+            # to LDS buffer c mod 2 (P even, so both indices are compile-time constants in the loop unrolled by P)
+            P = PREFETCH_BF16
+            L += [f'  load{SETS[k]}(min({k}, nch - 1));' for k in range(P)]
+            L += [f'  store{SETS[0]}(0);', '  __syncthreads();',
+                  f'  for (int c = 0; c < nch; c += {P}) {{']
+            for k in range(P):
+                L += [f'    load{SETS[k]}(min(c + {k + P}, nch - 1));',
+                      '    __builtin_amdgcn_sched_barrier(0);            // these loads go out before the MFMAs']
+                L += body(f'c + {k}', f'{k % 2}')
+                L += [f'    store{SETS[(k + 1) % P]}({(k + 1) % 2});',
+                      '    __syncthreads();']
+                if k < P - 1:
+                    L += [f'    if (c + {k + 1} >= nch) break;']
+            L += ['  }']
         else:
             L += ['  load(0);', '  store(0);', '  __syncthreads();',
                   '  for (int c = 0; c < nch; ++c) {',
@@ -476,7 +501,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     lds_max = max(lds_max, 4)
     # two workgroups per CU fit the LDS; keep the registers within two waves per SIMD as well (the second prefetch
     # register set would otherwise push the count past 256 and halve the occupancy)
-    occ = ' __attribute__((amdgpu_waves_per_eu(2)))' if PREFETCH_BF16 == 2 else ''
+    occ = ' __attribute__((amdgpu_waves_per_eu(2)))' if PREFETCH_BF16 > 1 else ''
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}){occ} void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N,',
          '    const int* __restrict__ order, float alpha) {',
@@ -702,6 +727,20 @@ def _f32_nodes_per_launch_group(blocks, terms, in_blocks, V):
     return min(_nodes_per_group(terms[o], in_blocks, V, l) for o, (_, l, *_) in enumerate(blocks))
 
 
+def _mask_wave(V, first, count):
+    """The workgroup's attributes that are nonzero somewhere in its nodes (species-ordered positions), as a bit mask
+    ``amw`` (V <= 32) that every wave builds by itself: each lane tests a share of the (node, attribute) pairs and
+    the wave ORs the lanes' bits together, so there is no LDS, atomic or barrier before the first chunk's loads.
+    ``nact`` is the number of live attributes and ``mh_kth_bit(amw, k)`` the k-th of them."""
+    return [f'  unsigned amb = 0u;',
+            f'  for (int f = lane; f < {count} * {V}; f += 64)',
+            f'    if (attr[(size_t)nd({first} + f / {V}) * {V} + f % {V}] != 0.f) amb |= 1u << (f % {V});',
+            '#pragma unroll',
+            '  for (int b = 1; b < 64; b <<= 1) amb |= (unsigned)__shfl_xor((int)amb, b, 64);',
+            '  const unsigned amw = __builtin_amdgcn_readfirstlane(amb);',
+            '  const int nact = __popc(amw);']
+
+
 def _mask(V, first, count, ordered=False):
     """The workgroup's list of attributes that are nonzero somewhere in its nodes (vlist[0] = count); with
     ``ordered`` position i of the workgroup is node nd(i)."""
@@ -727,12 +766,12 @@ def _mask(V, first, count, ordered=False):
 
 
 def use_bf16(spec, backward=False):
-    """Which kernel family a direction gets: the bf16x6 LDS-staged one for attribute-free maps with at least 1024
-    outputs (MACE's interaction linears: long K over many irreps blocks, every weight chunk shared by a workgroup's
-    eight row tiles); the fp32 one with per-wave register pipelines otherwise (short K and scalar-only blocks, whose
-    few workgroups and short chunk chains favour it, and skip_tp's attribute terms: measured no faster on the bf16
-    family, which supports them too)."""
-    return spec.V == 0 and (spec.Din if backward else spec.Dout) >= 1024
+    """Which kernel family a direction gets: the bf16x6 LDS-staged one for maps with at least 1024 outputs (MACE's
+    interaction linears, and the first layer's 2048-wide skip_tp: 40.5 -> 28.3 us per direction on config 2, with
+    each chunk's attribute values prefetched alongside its operands and one row tile per wave); the fp32 one with
+    per-wave register pipelines otherwise (short K and scalar-only blocks, whose few workgroups and short chunk
+    chains favour it)."""
+    return (spec.Din if backward else spec.Dout) >= 1024
 
 
 SCALAR_BLOCK = 256
@@ -913,7 +952,7 @@ class HipNodeLinear(torch.nn.Module):
         dev = torch.device(device) if device is not None else torch.device('cuda', torch.cuda.current_device())
         with torch.cuda.device(dev):
             def group(blocks, terms, in_blocks, bf16):
-                return (_nodes_per_launch_group(blocks) if bf16 else
+                return (_nodes_per_launch_group(blocks, _tiles(s.V)) if bf16 else
                         _f32_nodes_per_launch_group(blocks, terms, in_blocks, s.V))
             kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK,
                                             group(s.out_blocks, s.terms, s.in_blocks, use_bf16(s)),

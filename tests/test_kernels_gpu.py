@@ -664,8 +664,8 @@ def test_node_linears_vs_float64(attrs_kind):
 
 
 def test_skip_tp_on_both_families(monkeypatch):
-    """skip_tp (attribute terms, species-ordered nodes) generated by the bf16 family as well as the fp32 family it
-    normally gets: both against float64, forward and input gradient."""
+    """skip_tp (attribute terms, species-ordered nodes) generated by the bf16 family (what a 2048-wide skip_tp gets)
+    and by the fp32 family (what the narrow ones get): both against float64, forward and input gradient."""
     from mace_hip_kernels import linear as hlin
     dev = _dev()
     m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
