@@ -83,7 +83,9 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     block's ``reshape`` (irreps layout -> symmetric-contraction layout), and ``edge_geometry`` the edge vectors and
     lengths (MACE's ``get_edge_vectors_and_lengths`` in the model's module, taken over only while this model's forward
     runs; other models keep the original), and ``readouts`` the per-interaction readout heads (``LinearReadoutBlock``,
-    ``NonLinearReadoutBlock``) as one kernel per direction each.
+    ``NonLinearReadoutBlock``) as one kernel per direction each.  With ``linears``, an interaction block that applies
+    its ``skip_tp`` to ``linear(message) / avg_num_neighbors`` (MACE's first block) runs the two maps as one launch of
+    their composition per direction (``HipNodeLinear.compose_after``).
 
     ``fuse_radial`` (default off; with both the convolution and its radial MLP patched): the convolution forms its
     per-edge weights cutoff * MLP(edge_feats) inside its kernels from the MLP's last hidden activations, so the
@@ -275,6 +277,13 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 new.div_hint = float(avg)
             setattr(parent, attr, new)
             patched.append(name)
+        # an interaction block whose skip_tp consumes linear(message) / avg_num_neighbors (MACE's first block) runs
+        # the two maps as one composed launch; a block that applies skip_tp elsewhere never triggers it
+        for blk in getattr(model, 'interactions', []):
+            lin, skp = getattr(blk, 'linear', None), getattr(blk, 'skip_tp', None)
+            if (isinstance(lin, HipNodeLinear) and isinstance(skp, HipNodeLinear) and lin.div_hint is not None
+                    and not skp._composed and lin.spec.V == 0 and lin.spec.out_blocks == skp.spec.in_blocks):
+                skp.compose_after(lin)
     if double_backward:                   # including modules patched by an earlier call
         if _geometry.installed(model):
             model._mh_geometry_double_backward = True

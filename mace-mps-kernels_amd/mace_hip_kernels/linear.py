@@ -100,7 +100,33 @@ class LinSpec:
         self.in_blocks, self.Din = _blocks(ins)
         self.out_blocks, self.Dout = _blocks(mod.irreps_out)
         self.V = sum(m for m, _ in mod.irreps_in2) if self.kind == 'attrs' else 0
-        Wio = _probe(mod, self)
+        self.suffix = ''
+        self._build(_probe(mod, self))
+
+    @classmethod
+    def compose(cls, first, second):
+        """The spec of ``second`` applied to the output of ``first`` (an attribute-free linear): per input block i,
+        output block o and attribute v, W_io = sum_j W1_ij W2_jo[v] over the blocks j between them, formed in
+        float64 from the two probed maps (MACE's first interaction block: skip_tp(linear(message)), whose middle
+        tensor then never exists)."""
+        if first.V or first.out_blocks != second.in_blocks:
+            raise ValueError('maps do not compose: the first must be attribute-free with the second\'s input blocks')
+        self = cls.__new__(cls)
+        self.kind = second.kind
+        self.in_blocks, self.Din = first.in_blocks, first.Din
+        self.out_blocks, self.Dout = second.out_blocks, second.Dout
+        self.V = second.V
+        self.suffix = 'c'
+        Wio = {}
+        for (i, j), w1 in first.Wio.items():
+            for (jj, o), w2 in second.Wio.items():
+                if jj == j:
+                    w = np.einsum('ut,tvw->uvw', w1[:, 0, :], w2)
+                    Wio[(i, o)] = Wio[(i, o)] + w if (i, o) in Wio else w
+        self._build(Wio)
+        return self
+
+    def _build(self, Wio):
         self.terms = {o: [] for o in range(len(self.out_blocks))}
         self.bterms = {i: [] for i in range(len(self.in_blocks))}
         fw, bw, fo, bo = [], [], 0, 0
@@ -139,7 +165,7 @@ class LinSpec:
 
     def kname(self, base):
         """Kernel symbol of this module (shape-tagged so profiles tell the modules apart)."""
-        return f'{base}_i{self.Din}_o{self.Dout}' + (f'_v{self.V}' if self.V else '')
+        return f'{base}_i{self.Din}_o{self.Dout}' + (f'_v{self.V}' if self.V else '') + self.suffix
 
     def flops(self, n):
         """Multiply-adds x 2 of the dense map over n nodes (attribute terms all counted)."""
@@ -943,9 +969,9 @@ class HipNodeLinear(torch.nn.Module):
     """Drop-in for an e3nn ``o3.Linear`` (``forward(x)``) or a scalar-attribute ``FullyConnectedTensorProduct``
     (``forward(x, node_attrs)``), at inference (weights read at patch time; no weight gradients)."""
 
-    def __init__(self, mod, device=None):
+    def __init__(self, mod, device=None, spec=None):
         super().__init__()
-        self.spec = LinSpec(mod)
+        self.spec = LinSpec(mod) if spec is None else spec
         s = self.spec
         self.source = source(s)
         code = _native.compile_source(self.source)
@@ -979,10 +1005,34 @@ class HipNodeLinear(torch.nn.Module):
         self.double_backward = False
         # set by patch_model when the caller divides the output by a constant: forward then returns a PendingLinear
         self.div_hint = None
+        # set by compose_after: the linear whose scaled output this module consumes (its output is then left
+        # pending through the division) and the composed map that runs instead of the two
+        self.compose_into = None
+        self.compose_from = None
+        self._composed = []
+
+    def compose_after(self, first):
+        """Consume ``first``'s output in composed form: when this module is called on the pending output of
+        ``first`` divided by a constant (MACE's first interaction block: ``skip_tp(linear(message) / avg)``), one
+        launch of the composed map (``LinSpec.compose``) on ``first``'s input replaces both launches, in the forward
+        and in the backward.  Any other use of ``first``'s output forms it as usual."""
+        spec = LinSpec.compose(first.spec, self.spec)
+        dev = self.W.device
+        op = HipNodeLinear(self.original[0], device=dev, spec=spec)
+        op.tag = f'{first.tag}+{self.tag}'
+        self._composed = [op]                  # a plain list: not a submodule (unpatch and .modules() skip it)
+        # plain attributes, not submodule registrations (nn.Module.__setattr__ would register the other module)
+        object.__setattr__(self, 'compose_from', first)
+        object.__setattr__(first, 'compose_into', self)
 
     def forward(self, x, attrs=None):
         if self.spec.V == 0 and attrs is not None:
             raise TypeError('this linear takes no node attributes')
+        if (isinstance(x, PendingLinear) and self._composed and x.op is self.compose_from
+                and x.attrs is None and x.x.dtype == torch.float32):
+            op = self._composed[0]
+            op.double_backward = self.double_backward
+            return _LinFn.apply(x.x, attrs, op, x.scale)
         if self.div_hint is not None and x.dtype == torch.float32:
             return PendingLinear(x, attrs, self)
         return _LinFn.apply(x, attrs, self)
@@ -993,24 +1043,30 @@ _DIVS = {torch.Tensor.__truediv__, torch.Tensor.div, torch.div, torch.true_divid
 
 class PendingLinear(Pending):
     """The output of a node linear whose caller is known to divide it by a constant (MACE's interaction blocks:
-    ``self.linear(message) / self.avg_num_neighbors``), not yet computed.  Dividing it by a Python number launches the
-    kernel with the reciprocal folded into its stores (and the backward's), so no division kernel runs in either
-    direction; any other use computes the plain output first."""
+    ``self.linear(message) / self.avg_num_neighbors``), times ``scale``, not yet computed.  Dividing it by a Python
+    number launches the kernel with the reciprocal folded into its stores (and the backward's), so no division
+    kernel runs in either direction; when a patched module consumes the quotient in composed form
+    (``HipNodeLinear.compose_after``) the quotient stays pending for it.  Any other use computes the plain output
+    first."""
 
     @staticmethod
-    def __new__(cls, x, attrs, op):
+    def __new__(cls, x, attrs, op, scale=1.0):
         return Pending.__new__(cls, (*x.shape[:-1], op.spec.Dout), x)
 
-    def __init__(self, x, attrs, op):
-        self.x, self.attrs, self.op = x, attrs, op
+    def __init__(self, x, attrs, op, scale=1.0):
+        self.x, self.attrs, self.op, self.scale = x, attrs, op, scale
 
-    def value(self, scale=1.0):
-        return _LinFn.apply(self.x, self.attrs, self.op, scale)
+    def value(self):
+        return _LinFn.apply(self.x, self.attrs, self.op, self.scale)
 
     @classmethod
     def intercept(cls, func, args, kwargs):
         if (func in _DIVS and len(args) == 2 and not kwargs and isinstance(args[0], PendingLinear)
                 and isinstance(args[1], (int, float)) and not isinstance(args[1], bool) and args[1] != 0):
-            return args[0].value(1.0 / float(args[1]))
+            p = args[0]
+            scale = p.scale / float(args[1])
+            if p.op.compose_into is not None:
+                return PendingLinear(p.x, p.attrs, p.op, scale)
+            return _LinFn.apply(p.x, p.attrs, p.op, scale)
         return NotImplemented
 

@@ -690,6 +690,49 @@ def test_skip_tp_on_both_families(monkeypatch):
         assert _rel(gx.double().cpu().numpy(), gref.numpy()) < LIN_TOL
 
 
+def test_composed_linear_then_skip_tp():
+    """MACE's first block, skip_tp(linear(x) / avg, attrs), as one composed launch per direction (compose_after):
+    output and input gradient against float64 e3nn; any other use of the quotient forms it as usual."""
+    from mace_hip_kernels import linear as hlin
+    dev = _dev()
+    print('[case] composed linear + skip_tp', flush=True)
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    blk = m.interactions[0]
+    lin, skp = HipNodeLinear(blk.linear, device=dev), HipNodeLinear(blk.skip_tp, device=dev)
+    lin.div_hint, avg = 7.5, 7.5
+    skp.compose_after(lin)
+    rng = np.random.default_rng(11)
+    n = 1001
+    x = rng.normal(size=(n, lin.spec.Din))
+    a = np.eye(4)[rng.integers(0, 4, size=n)]
+    g = rng.normal(size=(n, skp.spec.Dout))
+    x64 = torch.tensor(x, requires_grad=True)
+    ref = blk.skip_tp.double()(blk.linear.double()(x64) / avg, torch.tensor(a))
+    gref, = torch.autograd.grad(ref, x64, torch.tensor(g))
+    xt = torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)
+    at = torch.tensor(a, dtype=torch.float32, device=dev)
+    q = lin(xt) / avg
+    assert isinstance(q, hlin.PendingLinear) and q.shape == (n, lin.spec.Dout)
+    with _native.timing() as tm:
+        out = skp(q, at)
+        gx, = torch.autograd.grad(out, xt, torch.tensor(g, dtype=torch.float32, device=dev))
+    torch.cuda.synchronize()
+    lins = {k: v for k, v in tm.symbols.items() if k.startswith('lin_')}      # (and the element order)
+    assert lins == {'lin_fwd[linear+linear]': ['lin_fwd_i2048_o2048_v4c'],
+                    'lin_bwd[linear+linear]': ['lin_bwd_i2048_o2048_v4c']}, tm.symbols
+    assert _rel(out.detach().double().cpu().numpy(), ref.detach().numpy()) < LIN_TOL
+    assert _rel(gx.double().cpu().numpy(), gref.numpy()) < LIN_TOL
+    # another consumer of the quotient gets the plain tensor: the linear's kernel with the division folded in
+    q2 = lin(xt) / avg
+    plain = q2 * 1.0
+    with torch.no_grad():
+        ref_q = (blk.linear.double()(torch.tensor(x)) / avg).numpy()
+    assert _rel(plain.detach().double().cpu().numpy(), ref_q) < LIN_TOL
+    # the same skip_tp module on a plain tensor takes its own map
+    out2 = skp(torch.tensor(ref_q, dtype=torch.float32, device=dev), at)
+    assert _rel(out2.detach().double().cpu().numpy(), ref.detach().numpy()) < LIN_TOL
+
+
 def test_node_linear_c_abi_and_errors():
     """mh_lin_fwd / mh_lin_bwd through the C ABI against the module, and their errors (NULL operands, a module
     without the kernel)."""

@@ -46,6 +46,30 @@ def test_probed_weights_reproduce_every_module():
     assert seen >= 9
 
 
+def test_composed_map_is_the_two_maps_in_a_row():
+    """LinSpec.compose (MACE's first block: skip_tp applied to the interaction linear's output) against the two e3nn
+    modules run one after the other in float64, and the composed kname; maps that do not chain are refused."""
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    blk = m.interactions[0]
+    lin, skp = linear.LinSpec(blk.linear), linear.LinSpec(blk.skip_tp)
+    comp = linear.LinSpec.compose(lin, skp)
+    assert comp.V == skp.V and comp.Din == lin.Din and comp.Dout == skp.Dout
+    assert comp.kname('lin_fwd') == skp.kname('lin_fwd') + 'c'
+    rng = np.random.default_rng(3)
+    x, a = rng.normal(size=(6, lin.Din)), rng.normal(size=(6, skp.V))
+    with torch.no_grad():
+        ref = blk.skip_tp.double()(blk.linear.double()(torch.tensor(x)), torch.tensor(a)).numpy()
+    assert np.abs(comp.apply(x, a) - ref).max() < 1e-12 * np.abs(ref).max()
+    # a planted mistake in the composition (one middle block left out) must show
+    broken = dict(comp.Wio)
+    broken.pop(sorted(broken)[-1])
+    bad = linear.LinSpec.compose(lin, skp)
+    bad.Wio = broken
+    assert np.abs(bad.apply(x, a) - ref).max() > 1e-3 * np.abs(ref).max()
+    with pytest.raises(ValueError, match='do not compose'):
+        linear.LinSpec.compose(skp, skp)
+
+
 class _MixesComponents(o3.Linear):
     """A planted mistake: an o3.Linear whose output also mixes the m components of its 1o block."""
 

@@ -275,6 +275,11 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
         names = sym[f'sc_fwd[products.{i}.symmetric_contractions]'] + \
             sym[f'sc_bwd[products.{i}.symmetric_contractions]']
         assert [n.split('_c')[0] for n in names] == ['sc_fwdsi', 'sc_bwdsi'], names    # LDS-staged, irreps layout
+    # the first block's skip_tp(linear(message) / avg) runs as one composed map in each direction
+    comp = 'interactions.0.linear+interactions.0.skip_tp'
+    assert sym[f'lin_fwd[{comp}]'] == ['lin_fwd_i2048_o2048_v4c'], sym
+    assert sym[f'lin_bwd[{comp}]'] == ['lin_bwd_i2048_o2048_v4c'], sym
+    assert not any(k.endswith(('[interactions.0.linear]', '[interactions.0.skip_tp]')) for k in sym), sym
     for prefix in ('sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_', 'geom_fwd', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
                    'ro_fwd_', 'ro_bwd_'):
         assert any(n.startswith(prefix) for n in flat), (prefix, flat)
