@@ -44,6 +44,9 @@ FENCE_M = True
 # Load the W rows (read exactly once per launch) with the non-temporal cache policy.  Measured on config 2 with
 # W rotating over buffers larger than the Infinity Cache: never slower, 131 → 112 µs for the 1280-wide forward.
 W_NT = True
+# Store the gW (or ∂/∂W0) rows with the non-temporal policy (written once here; the radial MLP's backward reads
+# them next).  Measured on config 2's captured E+F call: cacheable stores made it 25 us slower.
+GW_NT = True
 # Edges whose x and W slices the receiver-ordered backward has in flight ahead of the one being computed (1 or 2).
 # Measured on config 2 (isolated, layer 2): 290.7 us with one edge ahead, 295.7 us with two.
 BWD_PREFETCH = 1
@@ -206,7 +209,7 @@ class _Gen:
                 L.append(f'{ind}  const float gwk = {gw};')
                 L.append(f'{ind}  Pc = fmaf(gwk, w0{k}, Pc);' + (' asm volatile("" : "+v"(Pc));' if BWD_PC_FENCE else ''))
                 gw = 'gwk * ce'
-            st = f'mh_st_nt(gwe + {k * s.mul}, ol1, {gw});'      # written once, never re-read here
+            st = f'{"mh_st_nt" if GW_NT else "mh_st"}(gwe + {k * s.mul}, ol1, {gw});'
             L.append(f'{ind}  {st}' if self.full else f'{ind}  if (active) {st}')
             for b in range(co['d2']):
                 ts = [f'{_lit(v)} * xv{self.xi[i1] + a} * gv{self.oi[k] + c}'

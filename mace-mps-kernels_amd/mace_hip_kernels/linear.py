@@ -37,8 +37,8 @@ KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one 
 BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of an MFMA row tile
-NT = 2               # row tiles per wave: each LDS weight fragment feeds NT MFMAs
-NT_ATTRS = 1         # the same for skip_tp (attribute terms), bf16 family: one tile per wave, twice the workgroups
+NT = 1               # row tiles per wave, bf16 family: each LDS weight fragment feeds NT MFMAs
+NT_ATTRS = 1         # the same for skip_tp (attribute terms)
 PREFETCH_BF16 = 2    # chunks whose global loads are in flight ahead of the one being multiplied (1, 2 or 4), bf16 family
 XPAD = 4             # floats of padding per LDS row of staged inputs
 WPAD = 8             # bf16 of padding per LDS row of staged weights
@@ -233,9 +233,10 @@ def _grid_y(blocks):
 
 
 def _tiles(V):
-    """Row tiles per wave of the bf16 family: NT, or NT_ATTRS for attribute terms (skip_tp).  Measured on config 2's
-    2048 -> 2048 x 4-element skip_tp: 37.9 us with two tiles per wave, 28.3 us with one (more workgroups hide the
-    attribute-mask prologue); the attribute-free linears are within noise of each other at one or two."""
+    """Row tiles per wave of the bf16 family: NT, or NT_ATTRS for attribute terms (skip_tp).  Measured on config 2:
+    the 2048 -> 2048 x 4-element skip_tp takes 37.9 us with two tiles per wave and 28.3 us with one (twice the
+    workgroups hide the attribute-mask prologue); the captured E+F call is 5 us faster with one tile per wave for
+    the attribute-free linears as well."""
     return NT_ATTRS if V else NT
 
 

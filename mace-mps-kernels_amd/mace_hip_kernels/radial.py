@@ -48,6 +48,9 @@ HIDDEN_TILES_BWD = 1 # edge tiles whose hidden layers the backward recomputes to
 CH_FWD = 32          # output columns of the last layer per LDS chunk, forward (a multiple of 32)
 CH_BWD = 32          # and backward (a multiple of 32: one bf16 MFMA K step per 32 columns)
 NSPLIT = 3           # bf16 parts per fp32 weight (exact split)
+# Store the forward's W0 rows with the non-temporal policy.  The convolution reads them next, partly from the caches:
+# measured on config 2's captured E+F call, non-temporal stores made it 42 us slower.
+W0_NT = False
 BPAD = 8             # bf16 row padding of a chunk (keeps 16-byte reads aligned, spreads banks)
 PAD = 4              # LDS row padding (floats): the 4 lane groups of a fragment land on different banks
 # Waves per SIMD the forward and backward are compiled for (amdgpu_waves_per_eu; None: the compiler's choice).
@@ -444,7 +447,9 @@ def _source(spec, second):
                 for o in range(NO):
                     guard = f'if (c < {NCHK - 1}) ' if TAIL and 16 * (o + 1) > NW % CH else ''
                     val = ' + '.join(f'acc{b}[{o}][{jj}]' for jj in range(ncf))
-                    F += [f'      {guard}*reinterpret_cast<mh_f4*>(W0 + rowc{b} * {NW} + c * {CH} + {16 * o} + 4 * q) = {val};']
+                    dst = f'reinterpret_cast<mh_f4*>(W0 + rowc{b} * {NW} + c * {CH} + {16 * o} + 4 * q)'
+                    F += [f'      {guard}__builtin_nontemporal_store({val}, {dst});' if W0_NT else
+                          f'      {guard}*{dst} = {val};']
                 F += ['    }']
             F += ['    __syncthreads();', '  }']
         F += ['  }', '}', '']
