@@ -47,6 +47,9 @@ W_NT = True
 # Store the gW (or ∂/∂W0) rows with the non-temporal policy (written once here; the radial MLP's backward reads
 # them next).  Measured on config 2's captured E+F call: cacheable stores made it 25 us slower.
 GW_NT = True
+# Edges whose x and W slices the forward kernels have in flight ahead of the one being computed (1 or 2).
+# Measured on config 2's captured E+F call: two ahead (unconditional, clamped loads) was 9 us slower.
+FWD_PREFETCH = 1
 # Edges whose x and W slices the receiver-ordered backward has in flight ahead of the one being computed (1 or 2).
 # Measured on config 2 (isolated, layer 2): 290.7 us with one edge ahead, 295.7 us with two.
 BWD_PREFETCH = 1
@@ -331,6 +334,7 @@ def source(spec):
         ] + G.prelude() + [
             '  ' + decl('acc', no, '0.0f'),
             '  ' + decl('xn', nx), '  ' + decl('wn', nk),
+        ] + (['  ' + decl('xm', nx), '  ' + decl('wm', nk)] if FWD_PREFETCH > 1 else []) + [
             '  const int p0 = rowptr[n], p1 = rowptr[n + 1];',
             '  for (int pb = p0; pb < p1; pb += CHUNK) {',
         ]
@@ -352,16 +356,29 @@ def source(spec):
         F += G.m_prologue('    ', 'my_e')
         F += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
         F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
-        F += ['    }', '    for (int j = 0; j < cnt; ++j) {']
+        F += ['    }']
+        if FWD_PREFETCH > 1:          # edge 1 (or the last edge again) one stage further out
+            F += ['    {', '      const int e1 = mh_bcast(my_e, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
+            F += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'e1', 'wm')
+            F += ['    }']
+        F += ['    for (int j = 0; j < cnt; ++j) {']
         F += copy('xv', 'xn', nx)
         if cut:
             F += ['      const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_c), j));']
             F += [f'      const float w{k} = wn{k} * cj;' for k in range(nk)]
         else:
             F += copy('w', 'wn', nk)
-        F += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
-        F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
-        F += ['      }']
+        if FWD_PREFETCH > 1:
+            # unconditional (the last edges re-load themselves): no branch around the loads
+            F += [f'      xn{i} = xm{i};' for i in range(nx)] + [f'      wn{k} = wm{k};' for k in range(nk)]
+            F += ['      {', '        const int j2 = min(j + 2, cnt - 1);',
+                  '        const int e2 = mh_bcast(my_e, j2), s2 = mh_bcast(my_s, j2);']
+            F += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'e2', 'wm')
+            F += ['      }']
+        else:
+            F += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
+            F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+            F += ['      }']
         F += G.fwd_body('      ')
         F += ['    }', '    __syncthreads();', '  }', '  if (active) {',
               '    float* __restrict__ o = out + (size_t)n * OUT_DIM;']
