@@ -107,7 +107,8 @@ enum mh_kernel_kind {
     MH_EDGE_COUNT = 68,  /* edge compaction: kept edges per workgroup of 4096                       */
     MH_EDGE_PLACE = 69,  /* edge compaction: the row list                                           */
     MH_GEOM_SEGSUM1 = 70, /* per-structure sums of one column (MACE's energy sums)                  */
-    MH_NUM_KINDS = 71
+    MH_EDGE_PAIR = 71,   /* shared radial-MLP rows of an edge and its reverse                         */
+    MH_NUM_KINDS = 72
 };
 
 /* flags of mh_conv_bwd */
@@ -169,6 +170,11 @@ int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, co
 int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
                     const int32_t* eids, const int32_t* senders, const float* cutoff, float* out, int32_t N,
                     void* stream);
+/* mh_conv_fwd_cut with edge e's W0 row read at row wrow[e] of W (wrow [E] int32 on the device; NULL: row e), so
+ * that edges with equal radial-MLP rows can share one (mh_edge_pairs).  No reference counterpart. */
+int mh_conv_fwd_cut_rows(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
+                         const int32_t* eids, const int32_t* senders, const float* cutoff, const int32_t* wrow,
+                         float* out, int32_t N, void* stream);
 
 /* d/dx only, over the sender-sorted CSR: gx[s] = Σ_{e: sender(e)=s} ∂TP/∂x · g[receivers[e]].
  * Replaces lib.conv_bwd_x (reference conv.py:144-176, launched at conv.py:264).  Runs the MH_CONV_BWD kernel with
@@ -211,6 +217,13 @@ int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* 
                      const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
                      const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
                      const float* cutoff, float* g_cutoff, int32_t N, int32_t flags, void* stream);
+/* mh_conv_bwd_recv with factored weights whose W0 rows are read at wrow[e] (as mh_conv_fwd_cut_rows; NULL: row e).
+ * gW stays per edge: row e receives ∂/∂W0 of edge e.  No reference counterpart. */
+int mh_conv_bwd_recv_rows(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                          const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
+                          const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
+                          const float* cutoff, float* g_cutoff, const int32_t* wrow, int32_t N, int32_t flags,
+                          void* stream);
 
 /* Symmetric contraction forward: out[b, off + c*M + m] = Σ_terms T[elem[b], r0+m, c] Π X[b, c, idx].
  * Replaces lib.sc_fwd (reference symmetric.py:82-105, launched at symmetric.py:140). */
@@ -447,6 +460,22 @@ int mh_mlp_bwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16
 size_t mh_edge_compact_work_size(int64_t E);
 int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows, int32_t* count, void* work,
                     void* stream);
+
+/* Radial-MLP rows shared between an edge and its reverse.  ef [E, nf] fp32 are the MLP's input rows, cutoff [E] as
+ * for mh_edge_compact, the receiver CSR (rowptr_r, eids_r) and sender CSR (rowptr_s, eids_s) of the graph and the
+ * int32 senders / receivers of every edge (mh_graph_build).  For an edge e = s -> r inside the support with r < s,
+ * the first edge r -> s into s (in CSR order) that is inside the support and whose ef row equals e's bit for bit
+ * gives e's W0 row: wrow[e] = that edge (equal inputs give bitwise-equal MLP rows); every other edge has
+ * wrow[e] = e.  rows [E] int32 lists the edges that need a row of their own (inside the support and not mapped to
+ * a partner) in increasing order, then the others; count [1] = how many need one (mh_mlp_fwd_rows takes rows and
+ * count as they are).  work: mh_edge_pairs_work_size(E) bytes of device scratch.  Module of conv.graph_source();
+ * bind MH_EDGE_PAIR with 256 threads and 4 nodes per block, MH_EDGE_COUNT and MH_EDGE_PLACE as for
+ * mh_edge_compact.  Deterministic, no atomics, device work only.  No reference counterpart. */
+size_t mh_edge_pairs_work_size(int64_t E);
+int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff, const int32_t* rowptr_r,
+                  const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* senders,
+                  const int32_t* receivers, int32_t N, int64_t E, int32_t* wrow, int32_t* rows, int32_t* count,
+                  void* work, void* stream);
 
 /* Second derivatives of the radial MLP, behind a double backward (ev [E, n_basis] a direction of the features):
  * mh_mlp_jvp writes dW0 = (dW0/def) ev [E, n_out], the gradient of <ev, dL/def> with respect to gW0; mh_mlp_bwd2

@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 33; }
+int mh_version(void) { return 34; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -264,12 +264,18 @@ int mh_conv_fwd(mh_module* m, const float* x, const float* Y, const float* W, co
     return launch(m, MH_CONV_FWD, N, args, stream, "mh_conv_fwd");
 }
 
+int mh_conv_fwd_cut_rows(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
+                         const int32_t* eids, const int32_t* senders, const float* cutoff, const int32_t* wrow,
+                         float* out, int32_t N, void* stream) {
+    if (!cutoff) return fail(-1, "mh_conv_fwd_cut: cutoff is NULL");
+    void* args[] = {&x, &Y, &W, &rowptr, &eids, &senders, &out, &N, &cutoff, &wrow};
+    return launch(m, MH_CONV_FWD_C, N, args, stream, "mh_conv_fwd_cut");
+}
+
 int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
                     const int32_t* eids, const int32_t* senders, const float* cutoff, float* out, int32_t N,
                     void* stream) {
-    if (!cutoff) return fail(-1, "mh_conv_fwd_cut: cutoff is NULL");
-    void* args[] = {&x, &Y, &W, &rowptr, &eids, &senders, &out, &N, &cutoff};
-    return launch(m, MH_CONV_FWD_C, N, args, stream, "mh_conv_fwd_cut");
+    return mh_conv_fwd_cut_rows(m, x, Y, W, rowptr, eids, senders, cutoff, nullptr, out, N, stream);
 }
 
 int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
@@ -282,10 +288,12 @@ int mh_conv_bwd(mh_module* m, const float* x, const float* g, const float* Y, co
     return launch(m, MH_CONV_BWD, N, args, stream, "mh_conv_bwd");
 }
 
-int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
-                     const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
-                     const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
-                     const float* cutoff, float* g_cutoff, int32_t N, int32_t flags, void* stream) {
+int mh_conv_bwd_recv_rows(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                          const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
+                          const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
+                          const float* cutoff, float* g_cutoff, const int32_t* wrow, int32_t N, int32_t flags,
+                          void* stream) {
+    if (wrow && !cutoff) return fail(-1, "mh_conv_bwd_recv: a W0 row map needs the factored form (cutoff)");
     if (!(flags & MH_WANT_GWY)) return fail(-1, "mh_conv_bwd_recv: flags must include MH_WANT_GWY");
     if (!x || !gW || !gY) return fail(-1, "mh_conv_bwd_recv: x, gW and gY are required");
     if (cutoff && !g_cutoff) return fail(-1, "mh_conv_bwd_recv: cutoff given but g_cutoff is NULL");
@@ -300,7 +308,7 @@ int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* 
     int rc;
     if (cutoff) {
         void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags, &cutoff,
-                        &g_cutoff};
+                        &g_cutoff, &wrow};
         rc = launch(m, MH_CONV_BWD_RC, N, args, stream, "mh_conv_bwd_recv (factored weights)");
     } else {
         void* args[] = {&x, &g, &Y, &W, &rowptr_r, &eids_r, &senders, &gW, &gY, &work, &N, &kflags};
@@ -311,6 +319,14 @@ int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* 
     const float* mask = masked ? cutoff : nullptr;      // masked edges wrote no message
     void* args2[] = {&msg, &rowptr_s, &eids_s, &gx, &N, &mask};
     return launch(m, MH_CONV_GXSUM, N, args2, stream, "mh_conv_bwd_recv (dX sum)");
+}
+
+int mh_conv_bwd_recv(mh_module* m, const float* x, const float* g, const float* Y, const float* W,
+                     const int32_t* rowptr_r, const int32_t* eids_r, const int32_t* senders,
+                     const int32_t* rowptr_s, const int32_t* eids_s, float* work, float* gx, float* gW, float* gY,
+                     const float* cutoff, float* g_cutoff, int32_t N, int32_t flags, void* stream) {
+    return mh_conv_bwd_recv_rows(m, x, g, Y, W, rowptr_r, eids_r, senders, rowptr_s, eids_s, work, gx, gW, gY,
+                                 cutoff, g_cutoff, nullptr, N, flags, stream);
 }
 
 int mh_conv_bwd_x(mh_module* m, const float* g, const float* Y, const float* W, const int32_t* rowptr_s,
@@ -746,11 +762,42 @@ int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows,
     if (!count || !work || (E > 0 && (!cutoff || !rows))) return fail(-1, "mh_edge_compact: NULL operand");
     int32_t nb = (int32_t)(E > 0 ? (E + 4095) / 4096 : 1);       // one workgroup also for E == 0: count = 0
     int32_t* bc = static_cast<int32_t*>(work);
-    void* a1[] = {&cutoff, &E, &bc};
+    const int32_t* kv = nullptr;                                    // kept: the cutoff is not -0.0
+    void* a1[] = {&cutoff, &E, &bc, &kv};
     int rc = launch_blocks(m, MH_EDGE_COUNT, nb, a1, stream, "mh_edge_compact");
     if (rc) return rc;
-    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count};
+    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count, &kv};
     return launch_blocks(m, MH_EDGE_PLACE, nb, a2, stream, "mh_edge_compact");
+}
+
+size_t mh_edge_pairs_work_size(int64_t E) {
+    return (size_t)(E > 0 ? E : 0) * sizeof(int32_t) + mh_edge_compact_work_size(E);
+}
+
+int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff, const int32_t* rowptr_r,
+                  const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* senders,
+                  const int32_t* receivers, int32_t N, int64_t E, int32_t* wrow, int32_t* rows, int32_t* count,
+                  void* work, void* stream) {
+    if (E < 0 || E >= 0x7fffffffLL || N < 0) return fail(-1, "mh_edge_pairs: bad size");
+    if (nf < 1) return fail(-1, "mh_edge_pairs: nf must be at least 1");
+    if (!count || !work || (E > 0 && (!ef || !cutoff || !rowptr_r || !eids_r || !rowptr_s || !eids_s || !senders ||
+                                      !receivers || !wrow || !rows)))
+        return fail(-1, "mh_edge_pairs: NULL operand");
+    int32_t* keep = static_cast<int32_t*>(work);
+    int32_t* bc = keep + (E > 0 ? E : 0);
+    if (N > 0) {
+        void* a0[] = {&ef, &nf, &cutoff, &rowptr_r, &eids_r, &rowptr_s, &eids_s, &senders, &receivers, &N, &wrow,
+                      &keep};
+        int rc = launch(m, MH_EDGE_PAIR, N, a0, stream, "mh_edge_pairs");
+        if (rc) return rc;
+    }
+    int32_t nb = (int32_t)(E > 0 ? (E + 4095) / 4096 : 1);
+    const int32_t* kv = keep;
+    void* a1[] = {&cutoff, &E, &bc, &kv};
+    int rc = launch_blocks(m, MH_EDGE_COUNT, nb, a1, stream, "mh_edge_pairs");
+    if (rc) return rc;
+    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count, &kv};
+    return launch_blocks(m, MH_EDGE_PLACE, nb, a2, stream, "mh_edge_pairs");
 }
 
 int mh_mlp_jvp(mh_module* m, const float* ef, const float* ev, const float* Wh, const uint16_t* Wl, float* dW0,

@@ -281,24 +281,28 @@ extern "C" __global__ __launch_bounds__(256) void csr_sort_long(const int* __res
 // support) in increasing order from the front, the others from the back, and their number.  Workgroups of
 // EC_EDGES edges (1024 threads x 4): edge_count writes each workgroup's count of kept edges, edge_place adds the
 // counts of the workgroups before its own and places its edges by a block scan.  No atomics: the order is fixed.
+// With a flag array kv the kept edges are those whose flag is set instead (mh_edge_pairs).
 #define EC_EDGES 4096
-__device__ __forceinline__ int ec_keep(const float* __restrict__ cut, long long e, long long E) {
-  return e < E && __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
+__device__ __forceinline__ int ec_keep(const float* __restrict__ cut, const int* __restrict__ kv, long long e,
+                                       long long E) {
+  if (e >= E) return 0;
+  if (kv) return kv[e] != 0 ? 1 : 0;
+  return __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
 }
 
 extern "C" __global__ __launch_bounds__(1024) void edge_count(const float* __restrict__ cut, long long E,
-    int* __restrict__ bc) {
+    int* __restrict__ bc, const int* __restrict__ kv) {
   __shared__ int wsum[16];
   const long long e0 = (long long)blockIdx.x * EC_EDGES + 4 * threadIdx.x;
   int c = 0;
-  for (int k = 0; k < 4; ++k) c += ec_keep(cut, e0 + k, E);
+  for (int k = 0; k < 4; ++k) c += ec_keep(cut, kv, e0 + k, E);
   int total;
   mh_block_excl_scan<int, 16>(c, total, wsum);
   if (threadIdx.x == 0) bc[blockIdx.x] = total;
 }
 
 extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __restrict__ cut, long long E,
-    const int* __restrict__ bc, int nb, int* __restrict__ rows, int* __restrict__ count) {
+    const int* __restrict__ bc, int nb, int* __restrict__ rows, int* __restrict__ count, const int* __restrict__ kv) {
   __shared__ int wsum[16];
   const int b = blockIdx.x;
   int part = 0;                           // kept edges of the workgroups before this one
@@ -307,7 +311,7 @@ extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __res
   mh_block_excl_scan<int, 16>(part, off, wsum);
   const long long e0 = (long long)b * EC_EDGES + 4 * threadIdx.x;
   int kk[4], c = 0;
-  for (int k = 0; k < 4; ++k) { kk[k] = ec_keep(cut, e0 + k, E); c += kk[k]; }
+  for (int k = 0; k < 4; ++k) { kk[k] = ec_keep(cut, kv, e0 + k, E); c += kk[k]; }
   int mine;
   long long p = off + mh_block_excl_scan<int, 16>(c, mine, wsum);    // kept edges before e0
   for (int k = 0; k < 4; ++k) {
@@ -317,6 +321,65 @@ extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __res
     else rows[E - 1 - (e - p)] = (int)e;  // e - p dropped edges come before e
   }
   if (b == nb - 1 && threadIdx.x == 0) count[0] = off + mine;
+}
+
+// Shared radial-MLP rows between an edge and its reverse (mh_edge_pairs).  The MLP's output row is a function of
+// the edge's feature row alone, so two edges whose feature rows are bitwise equal have bitwise-equal W0 rows.  For
+// an edge e = (s -> r) inside the cutoff's support with r < s, the edges r -> s into s (MACE's neighbour lists hold
+// the reverse of every edge, at the same length) are searched for one inside the support whose feature row equals
+// e's bit for bit; the first in CSR order becomes e's W0 row (wrow[e]) and e needs no row of its own (keep[e] = 0).
+// Every other edge inside the support keeps its own row.  A partner always keeps its own row (its sender is the
+// smaller endpoint), so every row read through wrow is computed.  One wave per node s: the edges out of s one per
+// lane, the edges into s 64 at a time in registers, scanned by readlane.  Deterministic; no atomics.
+extern "C" __global__ __launch_bounds__(256) void edge_pair(const float* __restrict__ ef, int nf,
+    const float* __restrict__ cut, const int* __restrict__ rowptr_r, const int* __restrict__ eids_r,
+    const int* __restrict__ rowptr_s, const int* __restrict__ eids_s, const int* __restrict__ senders,
+    const int* __restrict__ receivers, int N, int* __restrict__ wrow, int* __restrict__ keep) {
+  const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (s >= N) return;
+  const int a0 = rowptr_r[s], a1 = rowptr_r[s + 1];     // edges into s
+  const int b0 = rowptr_s[s], b1 = rowptr_s[s + 1];     // edges out of s
+  for (int pb = b0; pb < b1; pb += 64) {
+    const int p = pb + lane;
+    int e = 0, r = 0, w = 0, kp = 0;
+    bool look = false;
+    if (p < b1) {
+      e = eids_s[p];
+      r = receivers[e];
+      w = e;
+      kp = __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
+      look = kp && r < s;
+    }
+    // Each round finds, per looking lane, the first edge from r into s at CSR position >= from (registers and
+    // readlane only), then checks that candidate's cutoff and feature row with one round of loads; a lane whose
+    // candidate differs resumes after it (another image of the same pair), one with none stops.
+    int from = a0;
+    while (__any(look)) {
+      int cand = -1;
+      for (int qb = a0; qb < a1; qb += 64) {
+        int is = -1;
+        if (qb + lane < a1) is = senders[eids_r[qb + lane]];
+        const int nq = min(64, a1 - qb);
+        for (int q = 0; q < nq; ++q) {
+          const int s2 = __builtin_amdgcn_readlane(is, q);
+          if (look && cand < 0 && s2 == r && qb + q >= from) cand = qb + q;
+        }
+      }
+      if (look) {
+        if (cand < 0) {
+          look = false;
+        } else {
+          const int e2 = eids_r[cand];
+          bool same = __float_as_uint(cut[e2]) != 0x80000000u;
+          for (int f = 0; f < nf; ++f)
+            same = same && __float_as_uint(ef[(size_t)e * nf + f]) == __float_as_uint(ef[(size_t)e2 * nf + f]);
+          if (same) { w = e2; kp = 0; look = false; }
+          else from = cand + 1;
+        }
+      }
+    }
+    if (p < b1) { wrow[e] = w; keep[e] = kp; }
+  }
 }
 """
 
@@ -340,7 +403,8 @@ def _graph_module(device):
                                       _native.MH_CSR_RANK: ('csr_rank', 256, 256, 2),
                                       _native.MH_CSR_SORT: ('csr_sort_long', 256, 1, 2),
                                       _native.MH_EDGE_COUNT: ('edge_count', 1024, EC_EDGES),
-                                      _native.MH_EDGE_PLACE: ('edge_place', 1024, EC_EDGES)})
+                                      _native.MH_EDGE_PLACE: ('edge_place', 1024, EC_EDGES),
+                                      _native.MH_EDGE_PAIR: ('edge_pair', 256, 4)})
         _GRAPH_MODULES[idx] = m
     return m
 
@@ -623,18 +687,51 @@ def support_rows(cut):
     return rows, count
 
 
+# the deferred radial MLP computes one W0 row per pair of an edge and its reverse when their feature rows are equal
+# (support_pairs); off, one row per edge inside the cutoff's support
+PAIR_RADIAL = True
+
+
+def support_pairs(ef, cut, gr):
+    """(wrow int32 [E], rows int32 [E], count int32 [1]) of ``mh_edge_pairs`` for the MLP input rows ``ef`` [E, nf],
+    the cutoff column ``cut`` and the graph ``gr`` (both CSRs): edge e reads its W0 row at wrow[e], and rows[:count]
+    lists the edges whose rows the MLP computes (inside the cutoff's support, not mapped to a reverse edge with an
+    equal feature row).  Cached on the cutoff tensor for its version, the features' storage and version and the
+    graph, so both interaction layers (which share MACE's edge features and cutoff) pair the edges once per call."""
+    key = (cut._version, ef.data_ptr(), ef._version, gr)
+    c = getattr(cut, '_mh_pairs', None)
+    if c is not None and c[0] == key:
+        return c[1], c[2], c[3]
+    E = cut.numel()
+    efc = ef.reshape(E, -1).contiguous()
+    cutf = cut.reshape(-1).contiguous()
+    dev = cut.device
+    lib, P = _native.load(), _native.ptr
+    wrow = torch.empty(E, dtype=torch.int32, device=dev)
+    rows = torch.empty(E, dtype=torch.int32, device=dev)
+    count = torch.empty(1, dtype=torch.int32, device=dev)
+    work = torch.empty(-(-lib.mh_edge_pairs_work_size(E) // 4), dtype=torch.int32, device=dev)
+    (rowptr_r, eids_r), (rowptr_s, eids_s) = gr.by_recv(), gr.by_send()
+    _native.launch('edge_pairs', lib.mh_edge_pairs, _graph_module(dev).handle, P(efc), efc.shape[1], P(cutf),
+                   P(rowptr_r), P(eids_r), P(rowptr_s), P(eids_s), P(gr.send), P(gr.recv), gr.n, E, P(wrow), P(rows),
+                   P(count), P(work), _native.stream_of(cutf))
+    cut._mh_pairs = (key, wrow, rows, count, efc)           # (efc keeps the keyed storage alive)
+    return wrow, rows, count
+
+
 def _support_masked(cut):
     """Whether ``cut`` is a patched radial embedding's cutoff, unmodified since: -0.0 then marks exactly the edges
     outside the envelope's support, where the envelope's derivative is zero."""
     return getattr(cut, '_mh_support_mask', None) == cut._version
 
 
-def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False, nozero=False):
+def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False, nozero=False, wrow=None):
     """First-order gradients (gx, gY, gW or gW0, gcut) of <g, conv(x, Y, W)> for contiguous operands, by the
     kernels; W = W0 * cut (cut flat [E]) when W is None.  Entries not wanted are None.  ``masked`` (factored only):
     edges with cut == -0.0 lie outside the cutoff envelope's support, and their gradients, gcut included, are zero
     (the envelope's derivative there is zero, so gcut's true value there never matters to its producer).
-    ``nozero`` (with ``masked``): those edges' gW0 rows are left unset, for a consumer that skips them."""
+    ``nozero`` (with ``masked``): those edges' gW0 rows are left unset, for a consumer that skips them.  ``wrow``
+    (factored only): edge e's W0 row is row wrow[e] (support_pairs); gW0 stays one row per edge."""
     factored = W is None
     E = Y.shape[0]
     gx = torch.empty_like(x) if want_x else None
@@ -652,12 +749,15 @@ def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False, noze
         rowptr_r, eids_r = gr.by_recv()
         rowptr_s, eids_s = gr.by_send() if want_x else (None, None)
         work = torch.empty(E, op.spec.x_dim, device=x.device, dtype=torch.float32) if want_x else None
-        _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv, op.module.handle, P(x), P(g), P(Y),
+        _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd_recv_rows, op.module.handle, P(x), P(g), P(Y),
                        P(W0 if factored else W), P(rowptr_r), P(eids_r), P(gr.send), P(rowptr_s), P(eids_s),
-                       P(work), P(gx), P(gW), P(gY), P(cut), P(gcut), x.shape[0], flags, _native.stream_of(x))
+                       P(work), P(gx), P(gW), P(gY), P(cut), P(gcut), P(wrow), x.shape[0], flags,
+                       _native.stream_of(x))
     elif flags:
         if factored:                     # dX only: the sender-ordered kernel needs the product
-            W = W0 * cut[:, None]
+            # rows of edges with a zero cutoff may be unset (a row-listed MLP skips them): exact zeros there
+            c = cut[:, None]
+            W = torch.where(c == 0, torch.zeros((), device=c.device), (W0 if wrow is None else W0[wrow.long()]) * c)
         rowptr_s, eids_s = gr.by_send()
         _native.launch(f'conv_bwd[{op.tag}]', lib.mh_conv_bwd, op.module.handle, P(x), P(g), P(Y), P(W),
                        P(rowptr_s), P(eids_s), P(gr.recv), P(gx), P(gW), P(gY), x.shape[0], flags,

@@ -327,7 +327,8 @@ def source(spec):
             f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwdc" if cut else "conv_fwd")}(',
             '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
             '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
-            '    float* __restrict__ out, int N' + (', const float* __restrict__ cutv) {' if cut else ') {'),
+            '    float* __restrict__ out, int N' + (', const float* __restrict__ cutv, const int* __restrict__ wrow) {'
+                                                   if cut else ') {'),
         ] + ms_decl_c + (['  __shared__ int sidx[NCB][CHUNK];'] if cut else []) + [
             '  const int n = mh_xcd_block(blockIdx.x, gridDim.x);',
             '  if (n >= N) return;',
@@ -348,18 +349,23 @@ def source(spec):
                   '    if (keep) sidx[wave][__popcll(kept & ((1ull << lane) - 1ull))] = my_e;',
                   '    if (cnt == 0) continue;',
                   '    float my_c = 0.0f;',
-                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e]; }']
+                  '    int my_w = 0;                       // the W0 row of lane j\'s edge (its own, or wrow[e])',
+                  '    if (lane < cnt) {',
+                  '      my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e];',
+                  '      my_w = wrow ? wrow[my_e] : my_e;',
+                  '    }']
         else:
             F += ['    const int cnt = min(CHUNK, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
-                  '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
+                  '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }',
+                  '    const int my_w = my_e;']
         F += G.m_prologue('    ', 'my_e')
-        F += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
-        F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
+        F += ['    {', '      const int er0 = mh_bcast(my_w, 0), s0 = mh_bcast(my_s, 0);']
+        F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'er0', 'wn')
         F += ['    }']
         if FWD_PREFETCH > 1:          # edge 1 (or the last edge again) one stage further out
-            F += ['    {', '      const int e1 = mh_bcast(my_e, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
-            F += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'e1', 'wm')
+            F += ['    {', '      const int er1 = mh_bcast(my_w, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
+            F += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'er1', 'wm')
             F += ['    }']
         F += ['    for (int j = 0; j < cnt; ++j) {']
         F += copy('xv', 'xn', nx)
@@ -372,12 +378,12 @@ def source(spec):
             # unconditional (the last edges re-load themselves): no branch around the loads
             F += [f'      xn{i} = xm{i};' for i in range(nx)] + [f'      wn{k} = wm{k};' for k in range(nk)]
             F += ['      {', '        const int j2 = min(j + 2, cnt - 1);',
-                  '        const int e2 = mh_bcast(my_e, j2), s2 = mh_bcast(my_s, j2);']
-            F += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'e2', 'wm')
+                  '        const int er2 = mh_bcast(my_w, j2), s2 = mh_bcast(my_s, j2);']
+            F += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'er2', 'wm')
             F += ['      }']
         else:
-            F += ['      if (j + 1 < cnt) {', '        const int e1 = mh_bcast(my_e, j + 1), s1 = mh_bcast(my_s, j + 1);']
-            F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+            F += ['      if (j + 1 < cnt) {', '        const int er1 = mh_bcast(my_w, j + 1), s1 = mh_bcast(my_s, j + 1);']
+            F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'er1', 'wn')
             F += ['      }']
         F += G.fwd_body('      ')
         F += ['    }', '    __syncthreads();', '  }', '  if (active) {',
@@ -503,7 +509,8 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         '    const float* __restrict__ W, const int* __restrict__ rowptr, const int* __restrict__ eids,',
         '    const int* __restrict__ senders, float* __restrict__ gW, float* __restrict__ gY,',
         '    float* __restrict__ gxm, int N, int flags' +
-        (', const float* __restrict__ cutv, float* __restrict__ gcut) {' if cut else ') {'),
+        (', const float* __restrict__ cutv, float* __restrict__ gcut, const int* __restrict__ wrow) {'
+         if cut else ') {'),
         '  __shared__ float part[CHUNK][Y_PAD];' if atomic else '  __shared__ float part[NCB][CHUNK][Y_PAD];',
     ] + ((['  __shared__ float partc[CHUNK];'] if atomic else ['  __shared__ float partc[NCB][CHUNK];']) +
          ['  __shared__ int sidx[NCB][CHUNK];'] if cut else []) + [
@@ -556,18 +563,23 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
                   '    if (cnt == 0) continue;',
                   '    my_e = 0;',
                   '    float my_c = 0.0f;                  // the cutoff of lane j\'s edge, broadcast per edge below',
-                  '    if (lane < cnt) { my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e]; }']
+                  '    int my_w = 0;                       // the W0 row of lane j\'s edge (its own, or wrow[e])',
+                  '    if (lane < cnt) {',
+                  '      my_e = sidx[wave][lane]; my_s = senders[my_e]; my_c = cutv[my_e];',
+                  '      my_w = wrow ? wrow[my_e] : my_e;',
+                  '    }']
         else:
             C += ['    const int cnt = min(CHUNK, p1 - pb);',
                   '    int my_e = 0, my_s = 0;',
-                  '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }']
+                  '    if (lane < cnt) { my_e = eids[pb + lane]; my_s = senders[my_e]; }',
+                  '    const int my_w = my_e;']
         C += G.m_prologue('    ', 'my_e')
-        C += ['    {', '      const int e0 = mh_bcast(my_e, 0), s0 = mh_bcast(my_s, 0);']
-        C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'e0', 'wn')
+        C += ['    {', '      const int er0 = mh_bcast(my_w, 0), s0 = mh_bcast(my_s, 0);']
+        C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'er0', 'wn')
         C += ['    }']
         if BWD_PREFETCH > 1:          # edge 1 (or the last edge again) one stage further out
-            C += ['    {', '      const int e1 = mh_bcast(my_e, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
-            C += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'e1', 'wm')
+            C += ['    {', '      const int er1 = mh_bcast(my_w, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
+            C += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'er1', 'wm')
             C += ['    }']
         C += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
         C += copy('xv', 'xn', nx)
@@ -582,13 +594,13 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
         if BWD_PREFETCH > 1:
             C += [f'      xn{i} = xm{i};' for i in range(nx)] + [f'      wn{k} = wm{k};' for k in range(nk)]
             C += ['      {', '        const int j2 = min(j + 2, cnt - 1);',
-                  '        const int e2 = mh_bcast(my_e, j2), s2 = mh_bcast(my_s, j2);']
-            C += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'e2', 'wm')
+                  '        const int er2 = mh_bcast(my_w, j2), s2 = mh_bcast(my_s, j2);']
+            C += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'er2', 'wm')
             C += ['      }']
         else:
             C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
-                  '        const int e1 = mh_bcast(my_e, j1), s1 = mh_bcast(my_s, j1);']
-            C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'e1', 'wn')
+                  '        const int er1 = mh_bcast(my_w, j1), s1 = mh_bcast(my_s, j1);']
+            C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'er1', 'wn')
             C += ['      }']
         C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
         if msg:

@@ -658,7 +658,12 @@ class ConvRadialFn(torch.autograd.Function):
     convolution's backward skips the others without writing their dL/dW0 rows (MH_CUT_NOZERO), and the MLP's
     backward reads only the listed rows and writes zero dL/d(edge features) rows for the rest.  Every result equals
     the separate modules' (the MLP's output times a zero cutoff contributes nothing, and its gradient there is
-    zero).  No double backward: the two-kernel modules take that (``patch_model(double_backward=True)``)."""
+    zero).  With ``conv.PAIR_RADIAL`` the MLP's forward computes one W0 row per edge and its reverse when their
+    feature rows are bitwise equal (``conv.support_pairs``; MACE's neighbour lists hold both directions at the same
+    length, and the MLP row is a function of the feature row alone), and the convolution reads each edge's row
+    through the pairing's row map: the forward's work and W0 stores halve, every value stays bitwise the same, and
+    the backward is unchanged (one dL/dW0 row per edge).  No double backward: the two-kernel modules take that
+    (``patch_model(double_backward=True)``)."""
 
     @staticmethod
     def forward(ctx, x, Y, ef, cut, edge_index, op):
@@ -681,19 +686,26 @@ class ConvRadialFn(torch.autograd.Function):
         masked = C._support_masked(cut) and op.skip_masked
         xc, Yc = x.contiguous(), Y.contiguous()
         efc, cutf = ef.reshape(E, -1).contiguous(), cut.reshape(-1).contiguous()
-        rows = count = None
+        rows = count = wrow = None
+        gr = C.graph_for(edge_index, n)
         if masked and E >= C.EDGE_COMPACT_MIN:
             rows, count = C.support_rows(cut)
-        W0 = mlp_forward(mlp, efc, rows, count)
-        gr = C.graph_for(edge_index, n)
+            if C.PAIR_RADIAL:
+                wrow, frows, fcount = C.support_pairs(efc, cut, gr)
+            else:
+                frows, fcount = rows, count
+            W0 = mlp_forward(mlp, efc, frows, fcount)
+        else:
+            W0 = mlp_forward(mlp, efc, None, None)
         rowptr, eids = gr.by_recv()
         out = torch.empty(n, s.out_dim, device=x.device, dtype=torch.float32)
         P = _native.ptr
-        # edges with cutoff 0 contribute exactly zero and are not read (so the rows the MLP left unset never are)
-        _native.launch(f'conv_fwd[{op.tag}]', _native.load().mh_conv_fwd_cut, op.module.handle, P(xc), P(Yc), P(W0),
-                       P(rowptr), P(eids), P(gr.send), P(cutf), P(out), n, _native.stream_of(x))
+        # edges with cutoff 0 contribute exactly zero and are not read (so the rows the MLP left unset never are);
+        # with wrow an edge reads the W0 row of its reverse when their feature rows are equal
+        _native.launch(f'conv_fwd[{op.tag}]', _native.load().mh_conv_fwd_cut_rows, op.module.handle, P(xc), P(Yc),
+                       P(W0), P(rowptr), P(eids), P(gr.send), P(cutf), P(wrow), P(out), n, _native.stream_of(x))
         ctx.save_for_backward(xc, Yc, efc, cutf)
-        ctx.W0, ctx.rows, ctx.count, ctx.masked = W0, rows, count, masked
+        ctx.W0, ctx.rows, ctx.count, ctx.masked, ctx.wrow = W0, rows, count, masked, wrow
         ctx.op, ctx.gr, ctx.shapes = op, gr, (ef.shape, cut.shape)
         return out
 
@@ -710,7 +722,9 @@ class ConvRadialFn(torch.autograd.Function):
             return None, None, None, None, None, None
         compact = ctx.rows is not None
         gx, gY, gW0, gcut = C._conv_grads(op, gr, g.contiguous(), x, Y, None, ctx.W0, cut, want_x,
-                                          want_y or want_ef or want_cut, masked=ctx.masked, nozero=compact)
+                                          want_y or want_ef or want_cut, masked=ctx.masked, nozero=compact,
+                                          wrow=ctx.wrow)
+        # per edge: every edge inside the support has its own dL/dW0 row, whatever row its W0 came from
         gef = _mlp_bwd(op.deferred_mlp(), ef, gW0, ctx.rows, ctx.count) if want_ef else None
         ef_shape, cut_shape = ctx.shapes
         return (gx, gY if want_y else None, gef.view(ef_shape) if gef is not None else None,

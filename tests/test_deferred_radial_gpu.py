@@ -132,3 +132,121 @@ def test_patched_model_defers_and_matches(monkeypatch):
     (e0, f0), (e1, f1) = outs
     assert float((e0 - e1).abs().max()) <= 1e-5 and float((f0 - f1).abs().max()) <= 1e-6
     print(f'[case] forces bitwise equal: {torch.equal(f0, f1)}', flush=True)
+
+
+def _pair_graph(rng, n, m, nf):
+    """A graph holding both directions of m node pairs with equal feature rows (as a neighbour list does), plus
+    self-loops, reverse edges whose rows differ in one bit, a second image of some pairs at the same length, and
+    edges outside the cutoff's support (-0.0).  Edge ids shuffled."""
+    a = rng.integers(0, n, size=m)
+    b = rng.integers(0, n, size=m)
+    f = rng.normal(size=(m, nf)).astype(np.float32)
+    s = np.concatenate([a, b, a[:m // 8]])
+    r = np.concatenate([b, a, b[:m // 8]])
+    ef = np.concatenate([f, f, f[:m // 8]])
+    flip = rng.uniform(size=m) < 0.1                 # the reverse row differs by one bit: no sharing
+    ef[m:2 * m][flip, 0] = np.nextafter(ef[m:2 * m][flip, 0], np.float32(np.inf))
+    c = rng.uniform(0.05, 1.0, size=len(s)).astype(np.float32)
+    c[rng.uniform(size=len(s)) < 0.1] = -0.0
+    perm = rng.permutation(len(s))
+    return s[perm], r[perm], ef[perm], c[perm]
+
+
+def _pairs_numpy(s, r, ef, c):
+    """The pairing's definition: an edge s -> r inside the support with r < s takes the W0 row of the first edge
+    r -> s (by edge id) inside the support whose feature row is bitwise equal; every other edge keeps its own."""
+    E = len(s)
+    inside = ~(np.signbit(c) & (c == 0))
+    bits = ef.view(np.uint32)
+    wrow, keep = np.arange(E), inside.copy()
+    for e in range(E):
+        if inside[e] and r[e] < s[e]:
+            for e2 in np.nonzero((s == r[e]) & (r == s[e]) & inside)[0]:
+                if np.array_equal(bits[e2], bits[e]):
+                    wrow[e], keep[e] = e2, False
+                    break
+    return wrow, keep
+
+
+@pytest.mark.parametrize('n,m', [(50, 3000), (400, 20000)])
+def test_edge_pairs_vs_definition(n, m):
+    dev = _dev()
+    print(f'[case] edge pairs n={n} m={m}', flush=True)
+    rng = np.random.default_rng(n)
+    s, r, ef, c = _pair_graph(rng, n, m, 8)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    gr = hconv.graph_for(ei, n)
+    eft, ct = torch.tensor(ef, device=dev), torch.tensor(c, device=dev)
+    wrow, rows, count = hconv.support_pairs(eft, ct, gr)
+    want_w, keep = _pairs_numpy(s, r, ef, c)
+    assert np.array_equal(wrow.cpu().numpy(), want_w)
+    K = int(keep.sum())
+    assert int(count.item()) == K and K < int((~(np.signbit(c) & (c == 0))).sum())
+    got = rows.cpu().numpy()
+    assert np.array_equal(got[:K], np.nonzero(keep)[0])
+    assert np.array_equal(np.sort(got[K:]), np.nonzero(~keep)[0])
+    # every row read through the map is one the MLP computes
+    assert keep[want_w[~(np.signbit(c) & (c == 0))]].all()
+    assert hconv.support_pairs(eft, ct, gr)[0] is wrow          # cached for the tensor's version and graph
+
+
+@pytest.mark.parametrize('want_x', [True, False])
+def test_paired_rows_equal_unpaired_bitwise(monkeypatch, want_x):
+    """ConvRadialFn with the W0 rows of reverse edges shared (conv.PAIR_RADIAL) against one row per edge: every
+    output and gradient bitwise equal, and the MLP's forward computes fewer rows."""
+    dev = _dev()
+    print(f'[case] paired radial rows want_x={want_x}', flush=True)
+    op, mlp = _modules(dev)
+    rng = np.random.default_rng(7)
+    n = 900
+    s, r, ef, c = _pair_graph(rng, n, 20000, mlp.spec.hs[0])
+    E = len(s)
+    x = rng.normal(size=(n, op.spec.x_dim)).astype(np.float32)
+    Y = rng.normal(size=(E, op.spec.y_dim)).astype(np.float32)
+    g = torch.tensor(rng.normal(size=(n, op.spec.out_dim)).astype(np.float32), device=dev)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+
+    def run(paired):
+        monkeypatch.setattr(hconv, 'PAIR_RADIAL', paired)
+        op.defer_mlp(mlp)
+        mlp.fuse = True
+        t = lambda a, rg=True: torch.tensor(a, device=dev, requires_grad=rg)  # noqa: E731
+        xt, Yt, eft, ct = t(x, want_x), t(Y), t(ef), t(c[:, None])
+        ct._mh_support_mask = ct._version
+        with _native.timing() as tm:
+            out = op(xt, Yt, mlp(eft) * ct, ei)
+            out.backward(g)
+        torch.cuda.synchronize()
+        return out.detach(), xt.grad, Yt.grad, eft.grad, ct.grad, tm.symbols
+
+    try:
+        one = run(False)
+        two = run(True)
+    finally:
+        op.defer_mlp(None)
+        mlp.fuse = False
+    for nm, a, b in zip(('out', 'gx', 'gY', 'gef', 'gcut'), one[:5], two[:5]):
+        if nm == 'gx' and not want_x:
+            assert a is None and b is None
+            continue
+        assert torch.equal(a, b), (nm, float((a - b).abs().max()))
+    assert 'edge_pairs' in two[5] and 'edge_pairs' not in one[5], two[5]
+
+
+def test_patched_model_pairs_bitwise(monkeypatch):
+    """config 2 (a neighbour list holding both directions of every pair): E and F with the radial MLP rows of
+    reverse edges shared equal the unshared ones bit for bit."""
+    dev = _dev()
+    print('[case] patched model, paired radial rows (config 2)', flush=True)
+    model, batch, _ = factory.workload(2)
+    b = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
+    outs = []
+    for paired in (False, True):
+        monkeypatch.setattr(hconv, 'PAIR_RADIAL', paired)
+        m = copy.deepcopy(model).to(dev)
+        patch_model(m, verbose=False)
+        o = m(D.fresh(b), compute_force=True)
+        torch.cuda.synchronize()
+        outs.append((o['energy'].detach(), o['forces'].detach()))
+    (e0, f0), (e1, f1) = outs
+    assert torch.equal(e0, e1) and torch.equal(f0, f1), (float((e0 - e1).abs().max()), float((f0 - f1).abs().max()))
