@@ -105,10 +105,11 @@ def _kernel_table(met, batch, n_real_edges, summary, symbols):
             rows[f'sh_fwd[{m.tag}]'] = (bf, 0)
             rows[f'sh_bwd[{m.tag}]'] = (bb, 0)
         elif isinstance(m, HipNodeLinear):
-            s = m.spec
-            bf, bb = s.bytes(n)
-            rows[f'lin_fwd[{m.tag}]'] = (bf, s.flops(n))
-            rows[f'lin_bwd[{m.tag}]'] = (bb, s.flops(n))
+            for op in [m] + list(m._composed):       # (the composed map of a first block's linear and skip_tp)
+                s = op.spec
+                bf, bb = s.bytes(n)
+                rows[f'lin_fwd[{op.tag}]'] = (bf, s.flops(n))
+                rows[f'lin_bwd[{op.tag}]'] = (bb, s.flops(n))
         elif isinstance(m, HipReshapeIrreps):
             nb = 2 * 4 * n * m.spec.dim                 # a permutation: the rows read once and written once
             rows[f'perm_fwd[{m.tag}]'] = (nb, 0)
@@ -122,11 +123,17 @@ def _kernel_table(met, batch, n_real_edges, summary, symbols):
             rows[f'ro_fwd[{m.tag}]'] = (bf, 0)
             rows[f'ro_bwd[{m.tag}]'] = (bb, 0)
         elif isinstance(m, HipRadialMLP):
-            s = m.spec                                  # every edge of the padded list is evaluated
+            # the rows the forward computed (a row list: the edges inside the cutoff's support, or of those one per
+            # edge and its reverse; without one every edge of the padded list) and the backward's (the support)
+            s = m.spec
             E = batch['edge_index'].shape[1]
-            bf, bb = s.bytes(E)
-            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(E))
-            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(E))
+            last = getattr(m, 'last_rows', E)
+            ef_rows = int(last.item()) if torch.is_tensor(last) else int(last)
+            eb_rows = n_real_edges if torch.is_tensor(last) else E
+            bf, _ = s.bytes(ef_rows)
+            _, bb = s.bytes(eb_rows)
+            rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(ef_rows))
+            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(eb_rows))
     # edge geometry: positions, shifts and the edge list in, vectors and lengths out; backward: vectors, lengths and
     # their gradients plus both CSRs in, the position gradient out
     E = batch['edge_index'].shape[1]

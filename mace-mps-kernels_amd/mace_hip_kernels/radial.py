@@ -731,6 +731,7 @@ def mlp_forward(op, ef, rows=None, count=None):
     P = _native.ptr
     _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd_rows, op.module.handle, P(ef), P(op.WhT),
                    P(op.WlT), P(out), ef.shape[0], P(rows), P(count), _native.stream_of(ef))
+    op.last_rows = count if count is not None else ef.shape[0]     # rows computed: device count or all
     return out
 
 
