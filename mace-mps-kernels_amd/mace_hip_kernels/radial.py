@@ -39,7 +39,7 @@ from . import _native
 from . import conv as _conv
 
 BLOCK = 256          # 4 waves
-NB_FWD = 2           # 16-edge tiles per wave in the forward (each LDS weight fragment feeds NB_FWD MFMAs)
+NB_FWD = 1           # 16-edge tiles per wave in the forward (each LDS weight fragment feeds NB_FWD MFMAs)
 NB_BWD = 1           # and in the backward
 NB_JVP = 1           # and in the forward-mode derivative (twice the hidden registers of the forward)
 GW_DIST = 2          # chunks of dL/dW0 in flight ahead of the one being multiplied (backward)
