@@ -468,14 +468,16 @@ int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows,
  * gives e's W0 row: wrow[e] = that edge (equal inputs give bitwise-equal MLP rows); every other edge has
  * wrow[e] = e.  rows [E] int32 lists the edges that need a row of their own (inside the support and not mapped to
  * a partner) in increasing order, then the others; count [1] = how many need one (mh_mlp_fwd_rows takes rows and
- * count as they are).  work: mh_edge_pairs_work_size(E) bytes of device scratch.  Module of conv.graph_source();
- * bind MH_EDGE_PAIR with 256 threads and 4 nodes per block, MH_EDGE_COUNT and MH_EDGE_PLACE as for
- * mh_edge_compact.  Deterministic, no atomics, device work only.  No reference counterpart. */
+ * count as they are).  srows / scount receive, from the same pass, what mh_edge_compact gives for the cutoff (the
+ * edges inside the support first: mh_mlp_bwd_rows's list).  work: mh_edge_pairs_work_size(E) bytes of device
+ * scratch.  Module of conv.graph_source(); bind MH_EDGE_PAIR with 256 threads and 4 nodes per block, MH_EDGE_COUNT
+ * and MH_EDGE_PLACE as for mh_edge_compact.  Deterministic, no atomics, device work only.  No reference
+ * counterpart. */
 size_t mh_edge_pairs_work_size(int64_t E);
 int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff, const int32_t* rowptr_r,
                   const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* senders,
                   const int32_t* receivers, int32_t N, int64_t E, int32_t* wrow, int32_t* rows, int32_t* count,
-                  void* work, void* stream);
+                  int32_t* srows, int32_t* scount, void* work, void* stream);
 
 /* Second derivatives of the radial MLP, behind a double backward (ev [E, n_basis] a direction of the features):
  * mh_mlp_jvp writes dW0 = (dW0/def) ev [E, n_out], the gradient of <ev, dL/def> with respect to gW0; mh_mlp_bwd2

@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 34; }
+int mh_version(void) { return 35; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -762,26 +762,29 @@ int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows,
     if (!count || !work || (E > 0 && (!cutoff || !rows))) return fail(-1, "mh_edge_compact: NULL operand");
     int32_t nb = (int32_t)(E > 0 ? (E + 4095) / 4096 : 1);       // one workgroup also for E == 0: count = 0
     int32_t* bc = static_cast<int32_t*>(work);
-    const int32_t* kv = nullptr;                                    // kept: the cutoff is not -0.0
+    const int32_t* kv = nullptr;                                    // one list: the cutoff is not -0.0
+    int32_t* rows2 = nullptr;
+    int32_t* count2 = nullptr;
     void* a1[] = {&cutoff, &E, &bc, &kv};
     int rc = launch_blocks(m, MH_EDGE_COUNT, nb, a1, stream, "mh_edge_compact");
     if (rc) return rc;
-    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count, &kv};
+    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count, &kv, &rows2, &count2};
     return launch_blocks(m, MH_EDGE_PLACE, nb, a2, stream, "mh_edge_compact");
 }
 
 size_t mh_edge_pairs_work_size(int64_t E) {
-    return (size_t)(E > 0 ? E : 0) * sizeof(int32_t) + mh_edge_compact_work_size(E);
+    return (size_t)(E > 0 ? E : 0) * sizeof(int32_t) + 2 * mh_edge_compact_work_size(E);
 }
 
 int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff, const int32_t* rowptr_r,
                   const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* senders,
                   const int32_t* receivers, int32_t N, int64_t E, int32_t* wrow, int32_t* rows, int32_t* count,
-                  void* work, void* stream) {
+                  int32_t* srows, int32_t* scount, void* work, void* stream) {
     if (E < 0 || E >= 0x7fffffffLL || N < 0) return fail(-1, "mh_edge_pairs: bad size");
     if (nf < 1) return fail(-1, "mh_edge_pairs: nf must be at least 1");
-    if (!count || !work || (E > 0 && (!ef || !cutoff || !rowptr_r || !eids_r || !rowptr_s || !eids_s || !senders ||
-                                      !receivers || !wrow || !rows)))
+    if (!count || !scount || !work ||
+        (E > 0 && (!ef || !cutoff || !rowptr_r || !eids_r || !rowptr_s || !eids_s || !senders || !receivers ||
+                   !wrow || !rows || !srows)))
         return fail(-1, "mh_edge_pairs: NULL operand");
     int32_t* keep = static_cast<int32_t*>(work);
     int32_t* bc = keep + (E > 0 ? E : 0);
@@ -791,12 +794,13 @@ int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff
         int rc = launch(m, MH_EDGE_PAIR, N, a0, stream, "mh_edge_pairs");
         if (rc) return rc;
     }
+    // one counting pass and one placing pass build both lists: the support (srows) and the pair flags (rows)
     int32_t nb = (int32_t)(E > 0 ? (E + 4095) / 4096 : 1);
     const int32_t* kv = keep;
     void* a1[] = {&cutoff, &E, &bc, &kv};
     int rc = launch_blocks(m, MH_EDGE_COUNT, nb, a1, stream, "mh_edge_pairs");
     if (rc) return rc;
-    void* a2[] = {&cutoff, &E, &bc, &nb, &rows, &count, &kv};
+    void* a2[] = {&cutoff, &E, &bc, &nb, &srows, &scount, &kv, &rows, &count};
     return launch_blocks(m, MH_EDGE_PLACE, nb, a2, stream, "mh_edge_pairs");
 }
 

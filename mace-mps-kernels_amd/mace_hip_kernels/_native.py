@@ -28,7 +28,7 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_NL_FILL, MH_SPECIES_ORDER, MH_MLP_JVP, MH_MLP_BWD2, MH_GEOM_SEGSUM, MH_NL_BASES, MH_EDGE_COUNT, \
     MH_EDGE_PLACE, MH_GEOM_SEGSUM1, MH_EDGE_PAIR = range(72)
 MH_WANT_GX, MH_WANT_GWY, MH_CUT_MASKED, MH_CUT_NOZERO = 1, 2, 4, 8
-ABI_VERSION = 34
+ABI_VERSION = 35
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -71,7 +71,7 @@ _SIGS = {
     'mh_geom_segsum1': (ctypes.c_int, [_P, _P, _P, _P, _I, _P]),
     'mh_edge_compact': (ctypes.c_int, [_P, _P, ctypes.c_int64, _P, _P, _P, _P]),
     'mh_edge_pairs_work_size': (ctypes.c_size_t, [ctypes.c_int64]),
-    'mh_edge_pairs': (ctypes.c_int, [_P, _P, _I] + [_P] * 7 + [_I, ctypes.c_int64] + [_P] * 5),
+    'mh_edge_pairs': (ctypes.c_int, [_P, _P, _I] + [_P] * 7 + [_I, ctypes.c_int64] + [_P] * 7),
     'mh_emb_fwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
     'mh_emb_bwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_perm_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int, _P]),

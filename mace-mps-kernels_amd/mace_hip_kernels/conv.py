@@ -281,37 +281,44 @@ extern "C" __global__ __launch_bounds__(256) void csr_sort_long(const int* __res
 // support) in increasing order from the front, the others from the back, and their number.  Workgroups of
 // EC_EDGES edges (1024 threads x 4): edge_count writes each workgroup's count of kept edges, edge_place adds the
 // counts of the workgroups before its own and places its edges by a block scan.  No atomics: the order is fixed.
-// With a flag array kv the kept edges are those whose flag is set instead (mh_edge_pairs).
+// With a flag array kv (mh_edge_pairs) a second list is built in the same pass: rows2 / count2 hold the edges whose
+// flag is set, in the same arrangement (per-workgroup counts of both lists in bc[0 .. nb) and bc[nb .. 2 nb)).
 #define EC_EDGES 4096
-__device__ __forceinline__ int ec_keep(const float* __restrict__ cut, const int* __restrict__ kv, long long e,
-                                       long long E) {
-  if (e >= E) return 0;
-  if (kv) return kv[e] != 0 ? 1 : 0;
-  return __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
+__device__ __forceinline__ int ec_keep(const float* __restrict__ cut, long long e, long long E) {
+  return e < E && __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
+}
+__device__ __forceinline__ int ec_flag(const int* __restrict__ kv, long long e, long long E) {
+  return e < E && kv[e] != 0 ? 1 : 0;
 }
 
 extern "C" __global__ __launch_bounds__(1024) void edge_count(const float* __restrict__ cut, long long E,
     int* __restrict__ bc, const int* __restrict__ kv) {
   __shared__ int wsum[16];
   const long long e0 = (long long)blockIdx.x * EC_EDGES + 4 * threadIdx.x;
-  int c = 0;
-  for (int k = 0; k < 4; ++k) c += ec_keep(cut, kv, e0 + k, E);
+  int c = 0, c2 = 0;
+  for (int k = 0; k < 4; ++k) c += ec_keep(cut, e0 + k, E);
+  if (kv)
+    for (int k = 0; k < 4; ++k) c2 += ec_flag(kv, e0 + k, E);
   int total;
   mh_block_excl_scan<int, 16>(c, total, wsum);
   if (threadIdx.x == 0) bc[blockIdx.x] = total;
+  if (kv) {                               // (uniform: the same pointer for every thread)
+    __syncthreads();                      // wsum reused
+    mh_block_excl_scan<int, 16>(c2, total, wsum);
+    if (threadIdx.x == 0) bc[gridDim.x + blockIdx.x] = total;
+  }
 }
 
-extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __restrict__ cut, long long E,
-    const int* __restrict__ bc, int nb, int* __restrict__ rows, int* __restrict__ count, const int* __restrict__ kv) {
-  __shared__ int wsum[16];
+// Place one list: kept edges in increasing order from the front, the others from the back.
+__device__ __forceinline__ void ec_place(const int (&kk)[4], long long e0, long long E, const int* __restrict__ bcl,
+    int nb, int* __restrict__ rows, int* __restrict__ count, int* wsum) {
   const int b = blockIdx.x;
   int part = 0;                           // kept edges of the workgroups before this one
-  for (int j = threadIdx.x; j < b; j += 1024) part += bc[j];
+  for (int j = threadIdx.x; j < b; j += 1024) part += bcl[j];
   int off;
   mh_block_excl_scan<int, 16>(part, off, wsum);
-  const long long e0 = (long long)b * EC_EDGES + 4 * threadIdx.x;
-  int kk[4], c = 0;
-  for (int k = 0; k < 4; ++k) { kk[k] = ec_keep(cut, kv, e0 + k, E); c += kk[k]; }
+  __syncthreads();                        // wsum reused
+  const int c = kk[0] + kk[1] + kk[2] + kk[3];
   int mine;
   long long p = off + mh_block_excl_scan<int, 16>(c, mine, wsum);    // kept edges before e0
   for (int k = 0; k < 4; ++k) {
@@ -321,6 +328,21 @@ extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __res
     else rows[E - 1 - (e - p)] = (int)e;  // e - p dropped edges come before e
   }
   if (b == nb - 1 && threadIdx.x == 0) count[0] = off + mine;
+}
+
+extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __restrict__ cut, long long E,
+    const int* __restrict__ bc, int nb, int* __restrict__ rows, int* __restrict__ count, const int* __restrict__ kv,
+    int* __restrict__ rows2, int* __restrict__ count2) {
+  __shared__ int wsum[16];
+  const long long e0 = (long long)blockIdx.x * EC_EDGES + 4 * threadIdx.x;
+  int kk[4];
+  for (int k = 0; k < 4; ++k) kk[k] = ec_keep(cut, e0 + k, E);
+  ec_place(kk, e0, E, bc, nb, rows, count, wsum);
+  if (kv) {
+    __syncthreads();
+    for (int k = 0; k < 4; ++k) kk[k] = ec_flag(kv, e0 + k, E);
+    ec_place(kk, e0, E, bc + nb, nb, rows2, count2, wsum);
+  }
 }
 
 // Shared radial-MLP rows between an edge and its reverse (mh_edge_pairs).  The MLP's output row is a function of
@@ -697,7 +719,8 @@ def support_pairs(ef, cut, gr):
     the cutoff column ``cut`` and the graph ``gr`` (both CSRs): edge e reads its W0 row at wrow[e], and rows[:count]
     lists the edges whose rows the MLP computes (inside the cutoff's support, not mapped to a reverse edge with an
     equal feature row).  Cached on the cutoff tensor for its version, the features' storage and version and the
-    graph, so both interaction layers (which share MACE's edge features and cutoff) pair the edges once per call."""
+    graph, so both interaction layers (which share MACE's edge features and cutoff) pair the edges once per call;
+    the same launch also fills ``support_rows``'s cache for the cutoff."""
     key = (cut._version, ef.data_ptr(), ef._version, gr)
     c = getattr(cut, '_mh_pairs', None)
     if c is not None and c[0] == key:
@@ -710,12 +733,15 @@ def support_pairs(ef, cut, gr):
     wrow = torch.empty(E, dtype=torch.int32, device=dev)
     rows = torch.empty(E, dtype=torch.int32, device=dev)
     count = torch.empty(1, dtype=torch.int32, device=dev)
+    srows = torch.empty(E, dtype=torch.int32, device=dev)
+    scount = torch.empty(1, dtype=torch.int32, device=dev)
     work = torch.empty(-(-lib.mh_edge_pairs_work_size(E) // 4), dtype=torch.int32, device=dev)
     (rowptr_r, eids_r), (rowptr_s, eids_s) = gr.by_recv(), gr.by_send()
     _native.launch('edge_pairs', lib.mh_edge_pairs, _graph_module(dev).handle, P(efc), efc.shape[1], P(cutf),
                    P(rowptr_r), P(eids_r), P(rowptr_s), P(eids_s), P(gr.send), P(gr.recv), gr.n, E, P(wrow), P(rows),
-                   P(count), P(work), _native.stream_of(cutf))
+                   P(count), P(srows), P(scount), P(work), _native.stream_of(cutf))
     cut._mh_pairs = (key, wrow, rows, count, efc)           # (efc keeps the keyed storage alive)
+    cut._mh_rows = (cut._version, srows, scount)            # the support list came from the same pass
     return wrow, rows, count
 
 

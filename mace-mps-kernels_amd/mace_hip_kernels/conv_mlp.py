@@ -689,10 +689,10 @@ class ConvRadialFn(torch.autograd.Function):
         rows = count = wrow = None
         gr = C.graph_for(edge_index, n)
         if masked and E >= C.EDGE_COMPACT_MIN:
-            rows, count = C.support_rows(cut)
-            if C.PAIR_RADIAL:
+            if C.PAIR_RADIAL:                       # (also lists the support: support_rows is then cached)
                 wrow, frows, fcount = C.support_pairs(efc, cut, gr)
-            else:
+            rows, count = C.support_rows(cut)
+            if not C.PAIR_RADIAL:
                 frows, fcount = rows, count
             W0 = mlp_forward(mlp, efc, frows, fcount)
         else:

@@ -102,7 +102,7 @@ def test_deferred_mlp_equals_separate_modules(E, marked, want_x):
             assert a is None and b is None
             continue
         assert torch.equal(a, b), (nm, float((a - b).abs().max()))
-    compacted = 'edge_compact' in dfr[5]
+    compacted = 'edge_compact' in dfr[5] or 'edge_pairs' in dfr[5]     # (pairing lists the support as well)
     assert compacted == (marked and E >= hconv.EDGE_COMPACT_MIN), dfr[5]
     for tag in ('mlp_fwd[radial_mlp]', 'mlp_bwd[radial_mlp]', 'conv_fwd[conv]', 'conv_bwd[conv]'):
         assert tag in dfr[5], (tag, dfr[5])
@@ -127,7 +127,7 @@ def test_patched_model_defers_and_matches(monkeypatch):
         with _native.timing() as tm:
             o = m(D.fresh(b), compute_force=True)
         torch.cuda.synchronize()
-        assert ('edge_compact' in tm.symbols) == defer, tm.symbols
+        assert ('edge_compact' in tm.symbols or 'edge_pairs' in tm.symbols) == defer, tm.symbols
         outs.append((o['energy'].detach(), o['forces'].detach()))
     (e0, f0), (e1, f1) = outs
     assert float((e0 - e1).abs().max()) <= 1e-5 and float((f0 - f1).abs().max()) <= 1e-6
@@ -188,6 +188,15 @@ def test_edge_pairs_vs_definition(n, m):
     # every row read through the map is one the MLP computes
     assert keep[want_w[~(np.signbit(c) & (c == 0))]].all()
     assert hconv.support_pairs(eft, ct, gr)[0] is wrow          # cached for the tensor's version and graph
+    # the same pass listed the support (mh_edge_compact's list): cached for the cutoff, no launch
+    inside = ~(np.signbit(c) & (c == 0))
+    with _native.timing() as tm:
+        srows, scount = hconv.support_rows(ct)
+    assert not tm.symbols, tm.symbols
+    S = int(inside.sum())
+    assert int(scount.item()) == S
+    got = srows.cpu().numpy()
+    assert np.array_equal(got[:S], np.nonzero(inside)[0]) and np.array_equal(np.sort(got[S:]), np.nonzero(~inside)[0])
 
 
 @pytest.mark.parametrize('want_x', [True, False])
