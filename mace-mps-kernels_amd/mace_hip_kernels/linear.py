@@ -34,6 +34,7 @@ from .symmetric import element_order
 from .pending import Pending
 
 KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
+CW_BF16 = 64         # output columns per workgroup of the bf16 family (64 or 128)
 BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of an MFMA row tile
@@ -222,14 +223,18 @@ def _probe(mod, spec):
     return Wio
 
 
-def _cw(mo):
-    """Columns per workgroup: 64 (4 MFMA column tiles) where the multiplicity allows."""
-    return 64 if mo % 64 == 0 else 32 if mo % 32 == 0 else 16
+def _cw(mo, cmax=64):
+    """Columns per workgroup: up to cmax (the fp32 family 64, i.e. 4 MFMA column tiles; the bf16 family CW_BF16)
+    where the multiplicity allows."""
+    for c in (128, 64, 32):
+        if c <= cmax and mo % c == 0:
+            return c
+    return 16
 
 
-def _grid_y(blocks):
+def _grid_y(blocks, cmax=64):
     """(block, column group) pairs of one direction, in blockIdx.y order."""
-    return [(o, cg) for o, (mo, *_) in enumerate(blocks) for cg in range(mo // _cw(mo))]
+    return [(o, cg) for o, (mo, *_) in enumerate(blocks) for cg in range(mo // _cw(mo, cmax))]
 
 
 def _tiles(V):
@@ -263,7 +268,7 @@ def pack(blocks, terms, in_blocks, wmats, V):
     VV = max(V, 1)
     out, base, toffs, off = [], {}, {}, 0
     for o, (mo, l, oo, _) in enumerate(blocks):
-        CW = _cw(mo)
+        CW = _cw(mo, CW_BF16)
         offs, t = [], 0
         for i, _ in terms[o]:
             offs.append(t)
@@ -305,7 +310,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     for o, (mo, l, oo, _) in enumerate(out_blocks):
         D = 2 * l + 1
         TN, G = _group(l, NT)
-        CW = _cw(mo)
+        CW = _cw(mo, CW_BF16)
         CT = CW // 16
         fn = f'{name}_b{o}'
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
@@ -518,7 +523,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
               '}', '']
         fns += L
         cases.append((o, fn))
-    gy = _grid_y(out_blocks)
+    gy = _grid_y(out_blocks, CW_BF16)
     VW = (V + 31) // 32
     sw = ['  switch (blockIdx.y) {']
     for y, (o, cg) in enumerate(gy):
@@ -983,11 +988,11 @@ class HipNodeLinear(torch.nn.Module):
                         _f32_nodes_per_launch_group(blocks, terms, in_blocks, s.V))
             kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK,
                                             group(s.out_blocks, s.terms, s.in_blocks, use_bf16(s)),
-                                            len(_grid_y(s.out_blocks)))}
+                                            len(_grid_y(s.out_blocks, CW_BF16 if use_bf16(s) else 64)))}
             if s.tiled_bwd:
                 kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK,
                                                group(s.in_blocks, s.bterms, s.out_blocks, use_bf16(s, True)),
-                                               len(_grid_y(s.in_blocks)))
+                                               len(_grid_y(s.in_blocks, CW_BF16 if use_bf16(s, True) else 64)))
             else:
                 kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), SCALAR_BLOCK, _scalar_nodes(s))
             self.module = _native.Module(code, kernels)
