@@ -108,7 +108,8 @@ enum mh_kernel_kind {
     MH_EDGE_PLACE = 69,  /* edge compaction: the row list                                           */
     MH_GEOM_SEGSUM1 = 70, /* per-structure sums of one column (MACE's energy sums)                  */
     MH_EDGE_PAIR = 71,   /* shared radial-MLP rows of an edge and its reverse                         */
-    MH_NUM_KINDS = 72
+    MH_CONV_FWD_CR = 72, /* conv fwd, W0 * cutoff with W0 rows through a row map (cacheable loads)     */
+    MH_NUM_KINDS = 73
 };
 
 /* flags of mh_conv_bwd */
@@ -171,7 +172,9 @@ int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W
                     const int32_t* eids, const int32_t* senders, const float* cutoff, float* out, int32_t N,
                     void* stream);
 /* mh_conv_fwd_cut with edge e's W0 row read at row wrow[e] of W (wrow [E] int32 on the device; NULL: row e), so
- * that edges with equal radial-MLP rows can share one (mh_edge_pairs).  No reference counterpart. */
+ * that edges with equal radial-MLP rows can share one (mh_edge_pairs).  With a row map it launches MH_CONV_FWD_CR
+ * (the same kernel with cacheable W0 loads: a shared row is read twice), without one MH_CONV_FWD_C.  No reference
+ * counterpart. */
 int mh_conv_fwd_cut_rows(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,
                          const int32_t* eids, const int32_t* senders, const float* cutoff, const int32_t* wrow,
                          float* out, int32_t N, void* stream);

@@ -138,7 +138,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 35; }
+int mh_version(void) { return 36; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -269,7 +269,8 @@ int mh_conv_fwd_cut_rows(mh_module* m, const float* x, const float* Y, const flo
                          float* out, int32_t N, void* stream) {
     if (!cutoff) return fail(-1, "mh_conv_fwd_cut: cutoff is NULL");
     void* args[] = {&x, &Y, &W, &rowptr, &eids, &senders, &out, &N, &cutoff, &wrow};
-    return launch(m, MH_CONV_FWD_C, N, args, stream, "mh_conv_fwd_cut");
+    // a row map: the kernel variant whose W0 loads are cacheable (shared rows are read twice)
+    return launch(m, wrow ? MH_CONV_FWD_CR : MH_CONV_FWD_C, N, args, stream, "mh_conv_fwd_cut");
 }
 
 int mh_conv_fwd_cut(mh_module* m, const float* x, const float* Y, const float* W, const int32_t* rowptr,

@@ -933,6 +933,7 @@ class HipConvTP(torch.nn.Module):
                 _native.MH_CONV_BWD_R: (self.spec.kname('conv_bwdr'), self.spec.block, 1),
                 _native.MH_CONV_BWD_RC: (self.spec.kname('conv_bwdrc'), self.spec.block, 1),
                 _native.MH_CONV_FWD_C: (self.spec.kname('conv_fwdc'), self.spec.block, 1),
+                _native.MH_CONV_FWD_CR: (self.spec.kname('conv_fwdcr'), self.spec.block, 1),
                 _native.MH_CONV_GXSUM: (self.spec.kname('conv_gxsum'), gxsum_block(self.spec), 1),
             })
         self.irreps_in1, self.irreps_in2, self.irreps_out = tp.irreps_in1, tp.irreps_in2, tp.irreps_out

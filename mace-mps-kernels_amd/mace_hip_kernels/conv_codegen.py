@@ -41,9 +41,15 @@ def _sum(parts):
 
 # fence the per-instruction LDS reads of the coupling products (bounds their register lifetime)
 FENCE_M = True
-# Load the W rows (read exactly once per launch) with the non-temporal cache policy.  Measured on config 2 with
-# W rotating over buffers larger than the Infinity Cache: never slower, 131 → 112 µs for the 1280-wide forward.
+# Load policy of the W (or W0) rows.  Read once per launch (the forward and backward kernels without a row map):
+# non-temporal, never slower once W is not cache-resident (131 -> 112 us for the 1280-wide forward with W rotating
+# over buffers larger than the Infinity Cache).  Read through a row map (conv_fwdcr: the radial MLP's rows shared
+# between an edge and its reverse, each row read twice per launch): cacheable, so the second read finds the row in
+# the caches (config 2 captured E+F -25 us, config 3 -18 us).  The receiver-ordered backward with a row map showed no
+# difference either way and keeps the non-temporal policy.
 W_NT = True
+W_NT_ROWS = False
+W_NT_BWD = True
 # Store the gW (or ∂/∂W0) rows with the non-temporal policy (written once here; the radial MLP's backward reads
 # them next).  Measured on config 2's captured E+F call: cacheable stores made it 25 us slower.
 GW_NT = True
@@ -110,8 +116,8 @@ class _Gen:
             L += [f'{ind}  {dst}{self.xi[b] + m} = mh_ld(xs + {off + m}, ol{d});' for m in range(d)]
         return L + [f'{ind}}}']
 
-    def ld_w(self, ind, e, dst):
-        ld = 'mh_ld_nt' if W_NT else 'mh_ld'
+    def ld_w(self, ind, e, dst, nt):
+        ld = 'mh_ld_nt' if nt else 'mh_ld'
         return ([f'{ind}{{ const float* __restrict__ we = W + (size_t)({e}) * NW;'] +
                 [f'{ind}  {dst}{k} = {ld}(we + {k * self.s.mul}, ol1);' for k in range(self.s.nins)] + [f'{ind}}}'])
 
@@ -317,14 +323,15 @@ def source(spec):
     ms_decl_c = ['  __shared__ float4 Ms4[CHUNK][NPP / 4];',
                  '  float (*Ms)[NPP] = reinterpret_cast<float (*)[NPP]>(Ms4);']
     # ------------------------------------------------------------------------------------------- forward
-    def fwd_kernel(cut):
+    def fwd_kernel(cut, rows=False):
         """``cut`` (kernel ``conv_fwdc``): the weights are W0·c with a per-edge scalar c, read as W0 and scaled in
         registers (the product is never formed in memory); an edge with c == 0 (padding, or past r_max in a
         neighbour list with a skin) contributes exactly zero, so each chunk of 64 edges is first compacted to its
         edges with c != 0 (ballot, then a per-wave LDS scatter by lane rank) and only those are walked.  Every wave
         of the workgroup builds the same list, so the barriers stay uniform."""
         F = [
-            f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_fwdc" if cut else "conv_fwd")}(',
+            f'extern "C" __global__ __launch_bounds__(BLOCK) void '
+            f'{spec.kname(("conv_fwdcr" if rows else "conv_fwdc") if cut else "conv_fwd")}(',
             '    const float* __restrict__ x, const float* __restrict__ Y, const float* __restrict__ W,',
             '    const int* __restrict__ rowptr, const int* __restrict__ eids, const int* __restrict__ senders,',
             '    float* __restrict__ out, int N' + (', const float* __restrict__ cutv, const int* __restrict__ wrow) {'
@@ -361,11 +368,11 @@ def source(spec):
                   '    const int my_w = my_e;']
         F += G.m_prologue('    ', 'my_e')
         F += ['    {', '      const int er0 = mh_bcast(my_w, 0), s0 = mh_bcast(my_s, 0);']
-        F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'er0', 'wn')
+        F += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'er0', 'wn', W_NT_ROWS if rows else W_NT)
         F += ['    }']
         if FWD_PREFETCH > 1:          # edge 1 (or the last edge again) one stage further out
             F += ['    {', '      const int er1 = mh_bcast(my_w, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
-            F += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'er1', 'wm')
+            F += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'er1', 'wm', W_NT_ROWS if rows else W_NT)
             F += ['    }']
         F += ['    for (int j = 0; j < cnt; ++j) {']
         F += copy('xv', 'xn', nx)
@@ -379,11 +386,11 @@ def source(spec):
             F += [f'      xn{i} = xm{i};' for i in range(nx)] + [f'      wn{k} = wm{k};' for k in range(nk)]
             F += ['      {', '        const int j2 = min(j + 2, cnt - 1);',
                   '        const int er2 = mh_bcast(my_w, j2), s2 = mh_bcast(my_s, j2);']
-            F += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'er2', 'wm')
+            F += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'er2', 'wm', W_NT_ROWS if rows else W_NT)
             F += ['      }']
         else:
             F += ['      if (j + 1 < cnt) {', '        const int er1 = mh_bcast(my_w, j + 1), s1 = mh_bcast(my_s, j + 1);']
-            F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'er1', 'wn')
+            F += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'er1', 'wn', W_NT_ROWS if rows else W_NT)
             F += ['      }']
         F += G.fwd_body('      ')
         F += ['    }', '    __syncthreads();', '  }', '  if (active) {',
@@ -392,7 +399,7 @@ def source(spec):
             F += [f'    mh_st(o + {co["o3"] + c}, ol{co["d3"]}, acc{G.oi[co["k"]] + c});' for c in range(co['d3'])]
         return F + ['  }', '}', '']
 
-    L += fwd_kernel(False) + fwd_kernel(True)
+    L += fwd_kernel(False) + fwd_kernel(True) + fwd_kernel(True, rows=True)
     # ----------------------------------------------------------------------------------- fused backward
     L += [
         f'extern "C" __global__ __launch_bounds__(BLOCK) void {spec.kname("conv_bwd")}(',
@@ -427,12 +434,12 @@ def source(spec):
              '    if (lane < cnt) { my_e = eids[pb + lane]; my_r = receivers[my_e]; }']
         C += G.m_prologue('    ', 'my_e')
         C += ['    {', '      const int e0 = mh_bcast(my_e, 0), r0 = mh_bcast(my_r, 0);']
-        C += G.ld_w('      ', 'e0', 'wn') + G.ld_g('      ', 'r0', 'gvn')
+        C += G.ld_w('      ', 'e0', 'wn', W_NT_BWD) + G.ld_g('      ', 'r0', 'gvn')
         C += ['    }', '    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
         C += copy('w', 'wn', nk) + copy('gv', 'gvn', no)
         C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
               '        const int e1 = mh_bcast(my_e, j1), r1 = mh_bcast(my_r, j1);']
-        C += G.ld_w('        ', 'e1', 'wn') + G.ld_g('        ', 'r1', 'gvn')
+        C += G.ld_w('        ', 'e1', 'wn', W_NT_BWD) + G.ld_g('        ', 'r1', 'gvn')
         C += ['      }']
         if store:
             C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
@@ -467,7 +474,7 @@ def source(spec):
         '  for (int j = 0; j < cnt; ++j) {',
         '    const int e = pb + j, s = mh_bcast(my_s, j), r = mh_bcast(my_r, j);',
     ]
-    L += G.ld_y_uniform('    ') + G.ld_x('    ', 's') + G.ld_w('    ', 'e', 'w') + G.ld_g('    ', 'r', 'gv')
+    L += G.ld_y_uniform('    ') + G.ld_x('    ', 's') + G.ld_w('    ', 'e', 'w', W_NT_BWD) + G.ld_g('    ', 'r', 'gv')
     L += [f'    {pdecl}', '    float* __restrict__ gwe = gW + (size_t)e * NW;']
     L += G.bwd_body('    ', with_gx=False, use_m=False, store=True)
     L += [t[2:] for t in gyr]
@@ -575,11 +582,11 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
                   '    const int my_w = my_e;']
         C += G.m_prologue('    ', 'my_e')
         C += ['    {', '      const int er0 = mh_bcast(my_w, 0), s0 = mh_bcast(my_s, 0);']
-        C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'er0', 'wn')
+        C += G.ld_x('      ', 's0', 'xn') + G.ld_w('      ', 'er0', 'wn', W_NT_BWD)
         C += ['    }']
         if BWD_PREFETCH > 1:          # edge 1 (or the last edge again) one stage further out
             C += ['    {', '      const int er1 = mh_bcast(my_w, min(1, cnt - 1)), s1 = mh_bcast(my_s, min(1, cnt - 1));']
-            C += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'er1', 'wm')
+            C += G.ld_x('      ', 's1', 'xm') + G.ld_w('      ', 'er1', 'wm', W_NT_BWD)
             C += ['    }']
         C += ['    for (int j = 0; j < cnt; ++j) {', '      const int e = mh_bcast(my_e, j);']
         C += copy('xv', 'xn', nx)
@@ -595,12 +602,12 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
             C += [f'      xn{i} = xm{i};' for i in range(nx)] + [f'      wn{k} = wm{k};' for k in range(nk)]
             C += ['      {', '        const int j2 = min(j + 2, cnt - 1);',
                   '        const int er2 = mh_bcast(my_w, j2), s2 = mh_bcast(my_s, j2);']
-            C += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'er2', 'wm')
+            C += G.ld_x('        ', 's2', 'xm') + G.ld_w('        ', 'er2', 'wm', W_NT_BWD)
             C += ['      }']
         else:
             C += ['      {', '        const int j1 = min(j + 1, cnt - 1);',
                   '        const int er1 = mh_bcast(my_w, j1), s1 = mh_bcast(my_s, j1);']
-            C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'er1', 'wn')
+            C += G.ld_x('        ', 's1', 'xn') + G.ld_w('        ', 'er1', 'wn', W_NT_BWD)
             C += ['      }']
         C += [f'      {pdecl}', '      float* __restrict__ gwe = gW + (size_t)e * NW;']
         if msg:
