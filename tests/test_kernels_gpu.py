@@ -239,6 +239,58 @@ def test_conv_mlp_fused_vs_oracle(hidden, lmax, want_x):
         assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize('hidden', ['128x0e', '128x0e+128x1o'])
+def test_conv_row_map_entry_points(hidden):
+    """mh_conv_fwd_cut_rows / mh_conv_bwd_recv_rows (W0 rows read through a row map, the shared radial-MLP rows of
+    an edge and its reverse) through the C ABI: bitwise equal to mh_conv_fwd_cut / mh_conv_bwd_recv run on the
+    gathered rows W0[wrow], forward and every gradient (dL/dW0 one row per edge), with the masked-edge flags the
+    model uses; and a NULL map is the identity."""
+    dev = _dev()
+    print(f'[case] conv row map {hidden}', flush=True)
+    op = HipConvTP(_tp(hidden, 3), device=dev)
+    spec = op.spec
+    rng = np.random.default_rng(21)
+    n, e, P = 57, 900, 333
+    s, r = _graph(rng, n, e)
+    f32 = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+    x, Y = f32(rng.normal(size=(n, spec.x_dim))), f32(rng.normal(size=(e, spec.y_dim)))
+    W0 = f32(rng.normal(size=(P, spec.nins * spec.mul)))
+    wrow = torch.tensor(rng.integers(0, P, size=e), dtype=torch.int32, device=dev)
+    c = rng.uniform(0.0, 1.0, size=e).astype(np.float32)
+    c[::5] = -0.0                                       # outside the support: skipped by both directions
+    c[1::11] = 0.0
+    cut = f32(c)
+    g = f32(rng.normal(size=(n, spec.out_dim)))
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    gr = hconv.graph_for(ei, n)
+    (rp_r, ei_r), (rp_s, ei_s) = gr.by_recv(), gr.by_send()
+    lib, Pp, st = _native.load(), _native.ptr, _native.stream_of(x)
+    Wg = W0[wrow.long()].contiguous()                   # the rows each edge reads, gathered
+    flags = _native.MH_WANT_GX | _native.MH_WANT_GWY | _native.MH_CUT_MASKED
+
+    def run(W, m):
+        out = torch.empty(n, spec.out_dim, device=dev)
+        gx, gY, gW = torch.empty_like(x), torch.empty_like(Y), torch.zeros(e, spec.nins * spec.mul, device=dev)
+        gc, work = torch.empty_like(cut), torch.empty(e, spec.x_dim, device=dev)
+        _native.check(lib.mh_conv_fwd_cut_rows(op.module.handle, Pp(x), Pp(Y), Pp(W), Pp(rp_r), Pp(ei_r),
+                                               Pp(gr.send), Pp(cut), Pp(m), Pp(out), n, st), 'fwd_cut_rows')
+        _native.check(lib.mh_conv_bwd_recv_rows(op.module.handle, Pp(x), Pp(g), Pp(Y), Pp(W), Pp(rp_r), Pp(ei_r),
+                                                Pp(gr.send), Pp(rp_s), Pp(ei_s), Pp(work), Pp(gx), Pp(gW), Pp(gY),
+                                                Pp(cut), Pp(gc), Pp(m), n, flags, st), 'bwd_recv_rows')
+        torch.cuda.synchronize()
+        return out, gx, gY, gW, gc
+
+    mapped, gathered = run(W0, wrow), run(Wg, None)
+    for nm, a, b in zip(('out', 'gx', 'gY', 'gW0', 'gcut'), mapped, gathered):
+        assert torch.equal(a, b), (nm, float((a - b).abs().max()))
+    assert gathered[0].abs().max() > 0 and gathered[3].abs().max() > 0
+    # the row map without a cutoff is refused before any launch
+    gx, gY, gW = torch.empty_like(x), torch.empty_like(Y), torch.empty(e, spec.nins * spec.mul, device=dev)
+    assert lib.mh_conv_bwd_recv_rows(op.module.handle, Pp(x), Pp(g), Pp(Y), Pp(W0), Pp(rp_r), Pp(ei_r), Pp(gr.send),
+                                     None, None, None, None, Pp(gW), Pp(gY), None, None, Pp(wrow), n,
+                                     _native.MH_WANT_GWY, st) != 0
+
+
 def test_conv_c_abi_bwd_x_and_bwd_wy():
     """The reference-shaped entry points mh_conv_bwd_x / mh_conv_bwd_wy against the oracle and the fused kernel."""
     dev = _dev()
