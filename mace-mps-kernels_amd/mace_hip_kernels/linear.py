@@ -35,6 +35,8 @@ from .pending import Pending
 
 KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
 CW_BF16 = 64         # output columns per workgroup of the bf16 family (64 or 128)
+BF16_MIN_OUT = 1024  # outputs (inputs, backward) from which a direction runs on the bf16 family (the config-2 call
+                     # measured 2 us slower with the 512-wide maps on it, 4 us with every map)
 BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of an MFMA row tile
@@ -803,7 +805,7 @@ def use_bf16(spec, backward=False):
     each chunk's attribute values prefetched alongside its operands and one row tile per wave); the fp32 one with
     per-wave register pipelines otherwise (short K and scalar-only blocks, whose few workgroups and short chunk
     chains favour it)."""
-    return (spec.Din if backward else spec.Dout) >= 1024
+    return (spec.Din if backward else spec.Dout) >= BF16_MIN_OUT
 
 
 SCALAR_BLOCK = 256
