@@ -16,8 +16,8 @@ units (v_mfma_f32_16x16x32_bf16, 2.7x the fp32 rate per K):
 * the hidden layers' weights sit in LDS for the whole workgroup (4 waves, 64 edges); the last layer's weights are
   streamed through LDS 32 output columns at a time, the next PREFETCH chunks in flight in registers while the
   current one is multiplied, and each result tile is stored as one float4 per lane (16 consecutive bytes of an
-  edge's row); in the forward each wave owns NB_FWD = 2 tiles of 16 edges, so every LDS weight fragment feeds two
-  MFMAs;
+  edge's row); each wave owns NB_FWD tiles of 16 edges in the forward (every LDS weight fragment feeds NB_FWD
+  MFMAs), NB_BWD in the backward (one each: measured fastest, also with two for the 512-output layer-1 MLP alone);
 * the output layer splits both fp32 operands exactly into three bf16 parts (v = hi + mid + lo, by truncation; the
   weights once on the host, the activations and dL/dW0 in registers) and sums the six leading partial products
   hi*hi, hi*mid, mid*hi, hi*lo, mid*mid, lo*hi on the bf16 MFMA with fp32 accumulation; the dropped terms are below
