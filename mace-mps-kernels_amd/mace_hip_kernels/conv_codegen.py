@@ -53,6 +53,9 @@ W_NT_BWD = True
 # Store the gW (or ∂/∂W0) rows with the non-temporal policy (written once here; the radial MLP's backward reads
 # them next).  Measured on config 2's captured E+F call: cacheable stores made it 25 us slower.
 GW_NT = True
+# ... except for layers with at most this many weights per edge: their dL/dW0 rows (config 2 layer 1: 161 MB) fit
+# the Infinity Cache, where the MLP backward reads them next (captured call -3 us)
+GW_CACHE_NW = 512
 # Edges whose x and W slices the forward kernels have in flight ahead of the one being computed (1 or 2).
 # Measured on config 2's captured E+F call: two ahead (unconditional, clamped loads) was 9 us slower.
 FWD_PREFETCH = 1
@@ -218,7 +221,8 @@ class _Gen:
                 L.append(f'{ind}  const float gwk = {gw};')
                 L.append(f'{ind}  Pc = fmaf(gwk, w0{k}, Pc);' + (' asm volatile("" : "+v"(Pc));' if BWD_PC_FENCE else ''))
                 gw = 'gwk * ce'
-            st = f'{"mh_st_nt" if GW_NT else "mh_st"}(gwe + {k * s.mul}, ol1, {gw});'
+            gw_nt = GW_NT and s.nins * s.mul > GW_CACHE_NW
+            st = f'{"mh_st_nt" if gw_nt else "mh_st"}(gwe + {k * s.mul}, ol1, {gw});'
             L.append(f'{ind}  {st}' if self.full else f'{ind}  if (active) {st}')
             for b in range(co['d2']):
                 ts = [f'{_lit(v)} * xv{self.xi[i1] + a} * gv{self.oi[k] + c}'
