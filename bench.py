@@ -77,6 +77,62 @@ def _time_train(model, batch, steps, warmup, sync):
     return (time.perf_counter() - t0) / steps
 
 
+def _config1_record(steps, warmup, sync):
+    """The reference's own measured rows (its README.md:60-63: conv layers 1 and 2 and symmetric contractions 1 and 2
+    forward + backward, and one E+F call, on one ~160-atom slab), on BASELINE config 1's structure and model, with
+    stress as the reference's calculator computes it: per-op ms from HIP events on the launch stream inside the eager
+    call, the whole call captured and eager, the unpatched model on the same GPU, and the agreement with it."""
+    import copy
+    import torch
+    from mace_hip_kernels import _native, patch_model
+    from mace_hip_kernels.graphs import capture
+    from mace_lite import data as D
+    from mace_lite import factory
+    dev = torch.device('cuda:0')
+    kw = dict(compute_force=True, compute_stress=True)
+    model, batch_cpu, meta = factory.workload(1)
+    batch = D.fresh(_to(batch_cpu, dev))
+    met = copy.deepcopy(model).to(dev)
+    report = patch_model(met, verbose=False)
+    assert not report['skipped'], report
+    ref = copy.deepcopy(model).to(dev)
+    o_ref, o_met = ref(D.fresh(batch), **kw), met(D.fresh(batch), **kw)
+    parity = {'max_abs_dE_eV': float((o_met['energy'] - o_ref['energy']).abs().max()),
+              'max_abs_dF_eV_per_A': float((o_met['forces'] - o_ref['forces']).abs().max()),
+              'max_abs_dstress_eV_per_A3': float((o_met['stress'] - o_ref['stress']).abs().max())}
+    t_eager, _ = _time_calls(met, batch, steps, warmup, sync, **kw)
+    call = capture(met, D.fresh(batch), **kw)
+    for _ in range(warmup):
+        call.replay()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        call.replay()
+    sync()
+    t_graph = (time.perf_counter() - t0) / steps
+    del call
+    with _native.timing() as tm:
+        for _ in range(steps):
+            met(batch, **kw)
+    summ = tm.summary()
+    per_op = {}
+    for i in range(len(model.interactions)):
+        for key, tag in ((f'conv_layer{i + 1}', f'interactions.{i}.conv_tp'),
+                         (f'symmetric_contraction{i + 1}', f'products.{i}.symmetric_contractions')):
+            op = 'conv' if key.startswith('conv') else 'sc'
+            rows = [summ.get(f'{op}_{d}[{tag}]') for d in ('fwd', 'bwd')]
+            if all(rows):
+                per_op[key] = round(sum(r[1] for r in rows), 4)
+    t_ref, _ = _time_calls(ref, batch, 3, 1, sync, **kw)
+    return dict(workload=meta['name'], atoms=int(batch['positions'].shape[0]), edges=int(batch['edge_index'].shape[1]),
+                calls='energy + forces + stress', per_op_fwd_bwd_ms=per_op,
+                per_op_reference_m4pro_metal_ms={'conv_layer1': 1.2, 'conv_layer2': 2.2,
+                                                 'symmetric_contraction1': 0.42, 'symmetric_contraction2': 0.07},
+                ms_per_call_captured=round(t_graph * 1e3, 4), ms_per_call_eager=round(t_eager * 1e3, 4),
+                reference_m4pro_metal_ms_per_call='13-17 (E+F, one structure)',
+                e3nn_gpu_ms_per_call=round(t_ref * 1e3, 3), speedup=round(t_ref / t_graph, 1), parity=parity)
+
+
 def _kernel_table(met, batch, n_real_edges, summary, symbols):
     """Per-kernel timings joined with algorithmic bytes and FLOPs (real edges only); ``symbols`` are the kernels each
     tag's launches ran, as the C ABI's launch log recorded them."""
@@ -190,11 +246,13 @@ def _cpu_baseline(model, batch_cpu, n_structs, sample, steps, min_seconds=10.0, 
     steps = done
     dt = (time.perf_counter() - t0) / steps
     per_call = dt * n_structs / k                                 # scaled to the full batch
+    what = (f'the full batch of {n_structs} structures' if k == n_structs else
+            f'{k} of the {n_structs} structures, scaled x{n_structs / k:g} to one batch call')
     return dict(value=round(1.0 / per_call, 5), unit='E+F calls/s', cores=cores, kind='port',
-                sample=f'unpatched e3nn-path restatement (mace_lite, fp32, torch CPU, {cores} threads) on {k} of '
-                       f'the {n_structs} structures ({n_at} atoms, {int(keep.sum())} edges), {steps} timed calls '
-                       f'after 1 warm-up, scaled x{n_structs / k:g} to one batch call',
-                cpu=_cpu_model(), seconds=round(dt * steps, 2))
+                sample=f'unpatched e3nn-path restatement (mace_lite, fp32, torch CPU, {cores} threads) on {what} '
+                       f'({n_at} atoms, {int(keep.sum())} edges): {steps} timed calls after 1 warm-up',
+                cpu=f'{_cpu_model()}, {os.cpu_count()} logical CPUs on the host, {cores} in this process\'s affinity',
+                seconds=round(dt * steps, 2))
 
 
 # symbol prefixes of this package's generated kernels
@@ -563,7 +621,7 @@ def main():
     ap.add_argument('--config', type=int, default=None, choices=[0, 1, 2, 3, 4],
                     help='workload (default 2; 4 with --isolated)')
     ap.add_argument('--isolated', action='store_true', help='time each HIP kernel alone (config 4 by default)')
-    ap.add_argument('--cpu-sample', type=int, default=4, help='structures in the CPU-baseline sample')
+    ap.add_argument('--cpu-sample', type=int, default=16, help='structures in the CPU-baseline sample')
     ap.add_argument('--cpu-steps', type=int, default=2, help='at least this many timed CPU-baseline calls')
     ap.add_argument('--cpu-seconds', type=float, default=10.0, help='and at least this many seconds of them')
     ap.add_argument('--no-cpu', action='store_true')
@@ -571,6 +629,8 @@ def main():
     ap.add_argument('--no-double-backward', action='store_true', help='skip the force-loss step timing')
     ap.add_argument('--no-graph', action='store_true', help='report the eager call instead of the captured one')
     ap.add_argument('--no-sweep', action='store_true', help='skip the batch 1/4/16 E+F timings (config 2)')
+    ap.add_argument('--no-cfg1', action='store_true',
+                    help="skip config 1's per-op and E+F+stress record (in a config-2 run)")
     ap.add_argument('--neighbour-list', action='store_true',
                     help='time the GPU neighbour list on the configuration (default 2) against the host builder')
     ap.add_argument('--fuse-radial', action='store_true',
@@ -687,7 +747,7 @@ def main():
             step.replay()
         sync()
         dt_md_graph = (time.perf_counter() - t0) / a.steps
-        step.neighbour_list.check()
+        step.check()
         del step, cb
         md = dict(step='positions moved (0.01 A Gaussian), neighbour list rebuilt on the GPU (padded to '
                        f"{st['pad_edges_to']} edges per structure), E+F",
@@ -782,6 +842,11 @@ def main():
     dom = max(per_call, key=per_call.get)
     d = kern[dom]
     _log('kernels:', json.dumps(kern))
+    # the reference's per-op rows on its own ~160-atom structure (config 1), in the same run as the headline
+    cfg1 = None
+    if a.config == 2 and not a.no_cfg1:
+        cfg1 = _config1_record(a.steps, a.warmup, sync)
+        _log('config 1:', json.dumps(cfg1))
 
     e3nn_res = None
     if not a.no_e3nn:
@@ -888,7 +953,8 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': dom, 'achieved': d['gbs'], 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': round(d['gbs'] / HBM_PEAK_GBS, 4), 'traffic': traffic, 'traffic_source': traffic_src,
                      'bytes_per_launch': d['bytes'], 'ms_per_launch': d['ms']},
-        'kernels': kern,
+        'top_kernels_ms_per_call': {k: round(v, 4) for k, v in sorted(per_call.items(), key=lambda t: -t[1])[:12]},
+        'config1': cfg1,
         'e3nn_gpu': e3nn_res,
         'double_backward': dbl,
         'parity': {'max_abs_dE_eV': dE, 'max_abs_dF_eV_per_A': dF},

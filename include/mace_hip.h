@@ -308,8 +308,9 @@ int mh_graph_build(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n
  * scratch is a device array the library owns, MH_GRAPH_SCRATCH_INTS int32 (16 MiB) per GPU, held until the process
  * ends; a call whose 4 (n + 1) + 2 E exceeds it returns an error without launching anything.  Every call on a GPU
  * uses that GPU's one array (the kernels clear what must start at zero), so calls that overlap on one GPU (two
- * streams, two threads) race and must be ordered by the caller.  No counterpart in the reference (whose csr_by
- * allocates through torch, conv.py:229-235); it is for the callers that cannot allocate. */
+ * streams, two threads) race and must be ordered by the caller.  The array used is that of the stream's device, which
+ * must be the module's (else an error).  No counterpart in the reference; it is for the callers that cannot
+ * allocate. */
 #define MH_GRAPH_SCRATCH_INTS (4 << 20)
 int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, int32_t n, int32_t* keys,
                            int32_t* rowptr, int32_t* eids, int32_t* bad, void* stream);

@@ -593,14 +593,19 @@ namespace {
 std::mutex g_scratch_mu;
 std::vector<int32_t*> g_scratch_ptr;       // per device ordinal: scratch's device address, null until looked up
 
-int scratch_of_current_device(int32_t** out) {
-    int dev = -1;
-    MH_HIP(hipGetDevice(&dev));
+// scratch's address on device `dev`, looked up (with `dev` made current for the lookup) on first use
+int scratch_of_device(int dev, int32_t** out) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (dev < 0) return fail(-1, "mh_graph_build_noalloc: bad device ordinal");
     if (static_cast<int>(g_scratch_ptr.size()) <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
     if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        MH_HIP(hipGetDevice(&cur));
+        if (cur != dev) MH_HIP(hipSetDevice(dev));
         void* p = nullptr;
-        MH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) MH_HIP(hipSetDevice(cur));
+        if (e != hipSuccess) return hip_fail(e, "mh_graph_build_noalloc: hipGetSymbolAddress");
         if (!p) return fail(-1, "mh_graph_build_noalloc: hipGetSymbolAddress gave a null scratch address");
         g_scratch_ptr[dev] = static_cast<int32_t*>(p);
     }
@@ -624,8 +629,17 @@ int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, i
            << " the library holds (use mh_graph_build with a caller-owned work buffer)";
         return fail(-1, os.str());
     }
+    if (!m) return fail(-1, "mh_graph_build_noalloc: NULL module");
+    // the scratch of the GPU the work is queued on: the stream's device, which must be the module's
+    int dev = -1;
+    MH_HIP(hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev));
+    if (dev != m->device) {
+        std::ostringstream os;
+        os << "mh_graph_build_noalloc: the stream is on device " << dev << ", the module on device " << m->device;
+        return fail(-1, os.str());
+    }
     int32_t* work = nullptr;
-    if (int rc = scratch_of_current_device(&work)) return rc;
+    if (int rc = scratch_of_device(dev, &work)) return rc;
     return mh_graph_build(m, edge_index, E, n, keys, rowptr, eids, work, bad, stream);
 }
 

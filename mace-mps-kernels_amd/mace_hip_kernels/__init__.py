@@ -101,7 +101,8 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     inputs: Hessian-vector products and force constants, or force and stress terms of a loss differentiated with
     respect to the positions (or to parameters the patch leaves on e3nn: ``radial_mlp=False`` keeps the radial MLPs'
     weights trainable).  Every drop-in takes it (fuse_radial does not: its fused kernels have no second-order form).
-    The patched modules hold their weights as constants: no gradient reaches those weights, with or without it."""
+    The patched modules hold their weights as constants: no gradient reaches those weights, with or without it; a
+    model patched in training mode with such parameters gets a warning naming them."""
     # a fully patched model may hold no parameters any more (the drop-ins keep their weights as buffers)
     p = next((t for t in itertools.chain(model.parameters(), model.buffers()) if t.is_floating_point()), None)
     if p is None:
@@ -112,6 +113,7 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     if p.dtype != torch.float32:
         raise RuntimeError('float32 models only')
     _native.load()                        # fail loudly before touching the model
+    trainable = [n for n, t in model.named_parameters() if t.requires_grad]
     patched, skipped = [], []
     if conv:
         for i, blk in enumerate(getattr(model, 'interactions', [])):
@@ -296,6 +298,15 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
     if verbose:
         for name, why in skipped:
             warnings.warn(f'mace_hip_kernels: kept e3nn for {name}: {why}')
+    if model.training:
+        # the drop-ins hold their weights as constants: a training step (an energy loss, or a force loss under
+        # double_backward) would silently leave these parameters unchanged
+        kept = {n for n, t in model.named_parameters() if t.requires_grad}
+        frozen = sorted({n.rsplit('.', 1)[0] for n in trainable if n not in kept})
+        if frozen:
+            warnings.warn(f'mace_hip_kernels: the model is in training mode, and the parameters of {frozen} are now '
+                          f'constants of the HIP drop-ins (no gradient reaches them); patch for inference (model.eval()), '
+                          f'or keep modules to be trained on e3nn (e.g. radial_mlp=False, linears=False)')
     return dict(patched=patched, skipped=skipped)
 
 

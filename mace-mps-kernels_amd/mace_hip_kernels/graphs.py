@@ -29,13 +29,23 @@ pad_edges_to=...)`` every replay first rebuilds the neighbour list on the GPU fr
     step = capture(model, batch, neighbours=dict(r_max=5.0, pbc=pbc, pad_edges_to=6000), compute_force=True)
     batch['positions'].copy_(new_positions)
     out = step.replay()                                   # neighbour list, CSRs, energy and forces
-    step.neighbour_list.check()                           # (synchronises) every structure fitted its padding
+    step.check()                                          # (synchronises) every structure fitted its padding
+
+Each replay of such a step copies the per-structure edge counts to pinned host memory behind an event; the next
+replay reads the copies that have landed, without waiting, and raises ValueError for a structure that outgrew
+``pad_edges_to`` (its graph then held only a subset of its edges) or could not be padded or searched (n_edges -1).
+``check()`` waits for every copy.  So a bad step is reported one replay late at the latest, and no replay
+synchronises.
 """
+import collections
+
 import torch
 
 from . import _native
 from . import conv as _conv
-from .neighbours import update_batch
+from .neighbours import raise_incomplete, update_batch
+
+PENDING_COUNTS = 4         # edge-count copies in flight before a replay waits for the oldest
 
 __all__ = ['capture', 'CapturedCall']
 
@@ -49,6 +59,9 @@ class CapturedCall:
             raise RuntimeError('HIP graph capture needs a GPU')
         self.model, self.batch, self.kwargs = model, batch, kwargs
         self.neighbour_list = None
+        self._pad = neighbours.get('pad_edges_to') if neighbours is not None else None
+        self._counts = collections.deque()           # (pinned int32 [B], event) of replays not yet checked
+        self._free = []                              # pinned buffers whose counts were checked
         if neighbours is not None:
             pbc = neighbours.get('pbc')
             if not (torch.is_tensor(pbc) and pbc.is_cuda):
@@ -71,6 +84,8 @@ class CapturedCall:
                 call()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
+        if self.neighbour_list is not None:
+            self.neighbour_list.check()              # the warm-up's graph (synchronised above)
         _native.take_capture_holds()
         self.graph = torch.cuda.CUDAGraph()
         _conv._capture_rebuild = bool(rebuild_graph)
@@ -83,8 +98,33 @@ class CapturedCall:
             self._held = _native.take_capture_holds()     # cached device memory the graph reads
 
     def replay(self):
+        self._check_counts(block=len(self._counts) >= PENDING_COUNTS)
         self.graph.replay()
+        if self.neighbour_list is not None:
+            n = self.neighbour_list.n_edges
+            buf = self._free.pop() if self._free else torch.empty(n.shape, dtype=n.dtype, pin_memory=True)
+            buf.copy_(n, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record()
+            self._counts.append((buf, ev))
         return self.out
+
+    def _check_counts(self, block):
+        """Read the edge counts of earlier replays whose copies have landed (``block``: wait for the oldest first)
+        and raise for an incomplete graph."""
+        while self._counts and (block or self._counts[0][1].query()):
+            buf, ev = self._counts.popleft()
+            ev.synchronize()
+            block = False
+            self._free.append(buf)
+            raise_incomplete(buf, self._pad)
+
+    def check(self):
+        """Wait for the edge counts of every replay so far and raise ValueError if a structure's neighbour list was
+        incomplete (a no-op without ``neighbours``)."""
+        while self._counts:
+            self._check_counts(block=True)
+        return self
 
 
 def capture(model, batch, warmup=2, rebuild_graph=False, neighbours=None, **kwargs):

@@ -3,10 +3,12 @@ Periodic neighbour lists of a batch of structures on the GPU, in MACE's edge con
 padded layout the reference recommends for long runs (reference README.md:77-78: "long runs should use fixed-size
 (padded) graphs").
 
-An edge (sender i, receiver j, unit shift o) exists when |pos[j] + o @ cell - pos[i]| < r_max, o ranges over the
-lattice translations reps_k = ceil(r_max / h_k) deep along each periodic direction k (h_k the distance between
-lattice planes), and (i, i, 0) is excluded.  Edges are ordered by (sender, receiver, image), the image index
-enumerating o lexicographically; with ``pad_edges_to = P`` structure b owns edges [b P, (b + 1) P) and every sender's
+An edge (sender i, receiver j, unit shift o) exists when |pos[j] + o @ cell - pos[i]| < r_max and (i, i, 0) is
+excluded.  The search covers the lattice translations reps_k = max(ceil(r_max / h_k), floor(r_max / h_k + span_k))
+deep along each periodic direction k (h_k the distance between lattice planes, span_k the range of the structure's
+fractional coordinates along k), which holds every such edge also for atoms outside the cell (unwrapped MD
+coordinates); more than 64 translations are not searched, and the structure is reported (``n_edges`` -1).
+Edges are ordered by (sender, receiver, image), the image index enumerating o lexicographically; with ``pad_edges_to = P`` structure b owns edges [b P, (b + 1) P) and every sender's
 real edges are followed by its share of padding edges (self-loops shifted (0, 0, kz) cells, kz = ceil((r_max + 1) /
 |c_2|), so the cutoff is exactly zero on them), the padding edges spread round-robin over the structure's atoms.
 That is exactly the host builder ``mace_lite.data.neighbour_list`` + ``batch_graphs(pad_edges_to=P)`` (scipy cKDTree
@@ -53,7 +55,7 @@ def source():
 """ + r"""
 #pragma clang fp contract(off)
 // per-structure parameters: prmd [B][16] doubles (lo[3], bs[3], cell rows c[9]); prmi [B][16] ints (nb[3], reps[3],
-// n0, n, nimg, bin0, kz)
+// n0, n, nimg, bin0, kz, cut)
 #define NL_PD 16
 #define NL_PI 16
 
@@ -72,47 +74,62 @@ extern "C" __global__ __launch_bounds__(256) void nl_setup(const double* __restr
   const int b = blockIdx.x;
   if (b >= B) return;
   const long long n0 = ptr[b], n1 = ptr[b + 1];
-  __shared__ double red[6][256];
-  double lo0 = 1e300, lo1 = 1e300, lo2 = 1e300, hi0 = -1e300, hi1 = -1e300, hi2 = -1e300;
+  const double* c = cell + 9 * (long long)b;
+  // g_k = c_{k+1} x c_{k+2}: the fractional coordinate of x along lattice vector k is (x . g_k) / det
+  double g[3][3];
+  for (int k = 0; k < 3; ++k) {
+    const double* a = c + 3 * ((k + 1) % 3);
+    const double* d = c + 3 * ((k + 2) % 3);
+    g[k][0] = a[1] * d[2] - a[2] * d[1];
+    g[k][1] = a[2] * d[0] - a[0] * d[2];
+    g[k][2] = a[0] * d[1] - a[1] * d[0];
+  }
+  const double det = c[0] * g[0][0] + c[1] * g[0][1] + c[2] * g[0][2];
+  const double vol = fabs(det);
+  // per thread, over its atoms: minima (red rows 0-5: x, y, z, then the three fractional coordinates), maxima (6-11)
+  __shared__ double red[12][256];
+  double lo[6], hi[6];
+  for (int k = 0; k < 6; ++k) { lo[k] = 1e300; hi[k] = -1e300; }
   for (long long i = n0 + threadIdx.x; i < n1; i += 256) {
-    const double x = pos[3 * i], y = pos[3 * i + 1], z = pos[3 * i + 2];
-    lo0 = fmin(lo0, x); lo1 = fmin(lo1, y); lo2 = fmin(lo2, z);
-    hi0 = fmax(hi0, x); hi1 = fmax(hi1, y); hi2 = fmax(hi2, z);
+    const double x[3] = {pos[3 * i], pos[3 * i + 1], pos[3 * i + 2]};
+    for (int k = 0; k < 3; ++k) {
+      const double f = (x[0] * g[k][0] + x[1] * g[k][1] + x[2] * g[k][2]) / det;
+      lo[k] = fmin(lo[k], x[k]); hi[k] = fmax(hi[k], x[k]);
+      lo[3 + k] = fmin(lo[3 + k], f); hi[3 + k] = fmax(hi[3 + k], f);
+    }
   }
   const int t = threadIdx.x;
-  red[0][t] = lo0; red[1][t] = lo1; red[2][t] = lo2; red[3][t] = hi0; red[4][t] = hi1; red[5][t] = hi2;
+  for (int k = 0; k < 6; ++k) { red[k][t] = lo[k]; red[6 + k][t] = hi[k]; }
   __syncthreads();
   for (int s = 128; s > 0; s >>= 1) {
     if (t < s) {
-      for (int k = 0; k < 3; ++k) {
+      for (int k = 0; k < 6; ++k) {
         red[k][t] = fmin(red[k][t], red[k][t + s]);
-        red[3 + k][t] = fmax(red[3 + k][t], red[3 + k][t + s]);
+        red[6 + k][t] = fmax(red[6 + k][t], red[6 + k][t + s]);
       }
     }
     __syncthreads();
   }
   if (t != 0) return;
   const long long n = n1 - n0;
-  const double* c = cell + 9 * (long long)b;
-  double lo[3], ext[3];
+  double blo[3], ext[3];
   for (int k = 0; k < 3; ++k) {
-    lo[k] = n > 0 && red[k][0] <= red[3 + k][0] ? red[k][0] : 0.0;
-    ext[k] = n > 0 && red[k][0] <= red[3 + k][0] ? red[3 + k][0] - red[k][0] : 0.0;
+    blo[k] = n > 0 && red[k][0] <= red[6 + k][0] ? red[k][0] : 0.0;
+    ext[k] = n > 0 && red[k][0] <= red[6 + k][0] ? red[6 + k][0] - red[k][0] : 0.0;
   }
-  // images: reps_k = ceil(r_max / h_k) along periodic k, h_k = |det| / |c_{k+1} x c_{k+2}|
-  const double det = c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
-                     c[2] * (c[3] * c[7] - c[4] * c[6]);
-  const double vol = fabs(det);
-  int reps[3];
+  // images along periodic k: an edge needs |o_k + f_j,k - f_i,k| < r_max / h_k (h_k = |det| / |g_k|, the spacing of
+  // lattice planes k), so |o_k| <= floor(r_max / h_k + span_k), span_k the range of the structure's fractional
+  // coordinates along k.  For atoms inside the cell (span_k < 1) that is at most ceil(r_max / h_k), which is used
+  // then; atoms further apart (unwrapped coordinates) widen the search.  Beyond 64 translations the search is cut
+  // and the structure is flagged (prmi[11]; n_edges -1).
+  int reps[3], cut = 0;
   long long nimg = 1;
   for (int k = 0; k < 3; ++k) {
-    const double* a = c + 3 * ((k + 1) % 3);
-    const double* d = c + 3 * ((k + 2) % 3);
-    const double cx = a[1] * d[2] - a[2] * d[1], cy = a[2] * d[0] - a[0] * d[2], cz = a[0] * d[1] - a[1] * d[0];
-    const double h = vol / sqrt(cx * cx + cy * cy + cz * cz);
-    double rk = pbc[3 * b + k] ? ceil(r_max / h) : 0.0;
+    const double h = vol / sqrt(g[k][0] * g[k][0] + g[k][1] * g[k][1] + g[k][2] * g[k][2]);
+    const double span = n > 0 && red[3 + k][0] <= red[9 + k][0] ? red[9 + k][0] - red[3 + k][0] : 0.0;
+    double rk = pbc[3 * b + k] ? fmax(ceil(r_max / h), floor(r_max / h + span + 1e-9)) : 0.0;
     if (!(rk >= 0.0)) rk = 0.0;               // a degenerate (zero-volume) cell has no lattice translations
-    if (rk > 64.0) rk = 64.0;
+    if (rk > 64.0) { rk = 64.0; cut = 1; }
     reps[k] = (int)rk;
     nimg *= 2 * reps[k] + 1;
   }
@@ -130,7 +147,7 @@ extern "C" __global__ __launch_bounds__(256) void nl_setup(const double* __restr
   double* P = prmd + NL_PD * (long long)b;
   int* I = prmi + NL_PI * (long long)b;
   for (int k = 0; k < 3; ++k) {
-    P[k] = lo[k];
+    P[k] = blo[k];
     P[3 + k] = fmax(ext[k] / (double)nb[k], cw);
     I[k] = (int)nb[k];
     I[3 + k] = reps[k];
@@ -143,6 +160,7 @@ extern "C" __global__ __launch_bounds__(256) void nl_setup(const double* __restr
   I[9] = (int)(n0 + b);                      // this structure's bins: [n0 + b, n0 + b + n + 1)
   const double kz = ceil((r_max + 1.0) / c2);
   I[10] = kz >= 1.0 && kz < 1e9 ? (int)kz : 0;   // padding shift; 0: none exists (c_2 zero), flagged if needed
+  I[11] = cut;                                    // 1: the image search was cut at 64 translations
 }
 
 extern "C" __global__ __launch_bounds__(256) void nl_zero(int* __restrict__ a, long long n) {
@@ -278,9 +296,10 @@ extern "C" __global__ __launch_bounds__(MH_WAVE * NL_SPB) void nl_count(const do
 
 // One workgroup per structure b: its edge count n_edges[b] (its real edges, even past e_pad) and each sender's
 // segment start relative to the structure's first slot: the exclusive prefix of (hits + padding share) over the
-// structure's senders.  A structure that needs padding but cannot have any (no atoms, or a zero third lattice vector)
-// gets n_edges[b] = -1; an atomless one's slots are filled with zero-length self-loops of a neighbouring atom (their
-// length makes the model's result NaN, never an index fault).
+// structure's senders.  A structure that needs padding but cannot have any (no atoms, or a zero third lattice vector),
+// or whose image search was cut (more than 64 translations along a lattice direction), gets n_edges[b] = -1; an
+// atomless one's slots are filled with zero-length self-loops of a neighbouring atom (their length makes the model's
+// result NaN, never an index fault).
 extern "C" __global__ __launch_bounds__(1024) void nl_offsets(const long long* __restrict__ ptr, int B, int N,
     const int* __restrict__ prmi, const long long* __restrict__ cnt, long long e_pad, long long e_total,
     long long* __restrict__ start, long long* __restrict__ tot, int* __restrict__ n_edges,
@@ -295,9 +314,10 @@ extern "C" __global__ __launch_bounds__(1024) void nl_offsets(const long long* _
   mh_block_excl_scan<long long, 16>(part, total, wsum);
   const long long extra = e_pad > 0 && total < e_pad ? e_pad - total : 0;
   const bool unpaddable = extra > 0 && (n == 0 || prmi[NL_PI * (long long)b + 10] == 0);
+  const bool cut = prmi[NL_PI * (long long)b + 11] != 0;
   if (t == 0) {
     tot[b] = total;
-    n_edges[b] = unpaddable ? -1 : (total < 0x7fffffffLL ? (int)total : 0x7fffffff);
+    n_edges[b] = unpaddable || cut ? -1 : (total < 0x7fffffffLL ? (int)total : 0x7fffffff);
   }
   if (n == 0 && extra > 0 && edge_index && N > 0) {
     const long long a = n0 < N ? n0 : N - 1;
@@ -463,19 +483,33 @@ class NeighbourList:
         self.n_edges, self.pad_edges_to = n_edges, pad_edges_to
 
     def overflowed(self):
-        """Structures whose graph does not fit the padding (synchronises): more real edges than ``pad_edges_to``,
-        or padding needed where none can be placed (no atoms, or a zero third lattice vector: n_edges -1)."""
-        if self.pad_edges_to is None:
-            return []
-        return torch.nonzero((self.n_edges > self.pad_edges_to) | (self.n_edges < 0)).reshape(-1).tolist()
+        """Structures whose graph is incomplete (synchronises): more real edges than ``pad_edges_to``, or n_edges -1:
+        padding needed where none can be placed (no atoms, or a zero third lattice vector), or an image search cut
+        at 64 lattice translations (atoms spread over about that many cells)."""
+        return incomplete(self.n_edges.cpu(), self.pad_edges_to)
 
     def check(self):
-        bad = self.overflowed()
-        if bad:
-            raise ValueError(f'neighbour list: structures {bad} do not fit pad_edges_to={self.pad_edges_to} '
-                             f'(real edges {self.n_edges[bad].tolist()}; -1: no atoms or no third lattice vector '
-                             f'to shift padding along); rebuild with a larger padding')
+        raise_incomplete(self.n_edges.cpu(), self.pad_edges_to)
         return self
+
+
+def incomplete(counts, pad_edges_to):
+    """Indices of the structures whose host-side edge ``counts`` (``NeighbourList.n_edges`` copied to the host) show
+    an incomplete graph: -1, or more real edges than ``pad_edges_to``."""
+    bad = counts < 0
+    if pad_edges_to is not None:
+        bad = bad | (counts > pad_edges_to)
+    return torch.nonzero(bad).reshape(-1).tolist()
+
+
+def raise_incomplete(counts, pad_edges_to):
+    """ValueError naming the incomplete structures of ``counts`` (see ``incomplete``), if any."""
+    bad = incomplete(counts, pad_edges_to)
+    if bad:
+        raise ValueError(f'neighbour list: structures {bad} do not fit pad_edges_to={pad_edges_to} or are incomplete '
+                         f'(real edges {counts[bad].tolist()}; -1: no atoms or no third lattice vector to '
+                         f'shift padding along, or atoms spread over more than 64 cells); rebuild with a larger '
+                         f'padding or wrapped positions')
 
 
 def _work_bytes(B, N, e_total):
@@ -518,7 +552,12 @@ def neighbour_list(positions, cell, ptr, r_max, pbc=(True, True, True), pad_edge
         work = torch.empty(_work_bytes(B, N, 0), dtype=torch.uint8, device=dev)
         _native.launch('neighbour_list', lib.mh_neighbour_list, m.handle, P(pos), P(cl), P(pb), P(pt), B, N,
                        float(r_max), 0, 0, None, None, None, f64, P(n_edges), P(work), st)
-        e_total = int(n_edges.to(torch.int64).sum())                         # the one synchronisation
+        counts = n_edges.cpu()                                               # the one synchronisation
+        if bool((counts < 0).any()):
+            raise ValueError(f'neighbour list: structures {torch.nonzero(counts < 0).reshape(-1).tolist()} need more '
+                             f'than 64 lattice translations along a periodic direction (atoms spread over that many '
+                             f'cells); wrap the positions into the cell')
+        e_total = int(counts.to(torch.int64).sum())
         e_pad = 0
     else:
         e_pad = int(pad_edges_to)

@@ -164,13 +164,17 @@ def neighbour_list(s, r_max):
     shift excluded; sorted by (sender, receiver, shift)."""
     pos, cell = s.positions, s.cell
     n = len(pos)
-    # number of images needed along each periodic lattice direction: r_max / (distance between lattice planes)
+    # images needed along each periodic lattice direction k: |o_k + f_j - f_i| < r_max / h_k (h_k the distance between
+    # lattice planes, f the fractional coordinate along k), so floor(r_max / h_k + span of f) deep; ceil(r_max / h_k)
+    # for atoms inside the cell
     vol = abs(np.linalg.det(cell))
+    frac = pos @ np.linalg.inv(cell) if n and any(s.pbc) and vol > 0 else np.zeros((0, 3))
     reps = []
     for k in range(3):
         if s.pbc[k]:
             h = vol / np.linalg.norm(np.cross(cell[(k + 1) % 3], cell[(k + 2) % 3]))
-            reps.append(int(np.ceil(r_max / h)))
+            span = float(frac[:, k].max() - frac[:, k].min()) if len(frac) else 0.0
+            reps.append(int(max(np.ceil(r_max / h), np.floor(r_max / h + span + 1e-9))))
         else:
             reps.append(0)
     offs = np.array([(i, j, k) for i in range(-reps[0], reps[0] + 1) for j in range(-reps[1], reps[1] + 1)

@@ -7,8 +7,9 @@ recommends fixed-size padded graphs for long runs (reference README.md:77-78); i
 list per call (conv.py:229-235).  This restates, by brute force in float64 numpy, the graph such a builder hands the
 model, in MACE's convention:
   * ``neighbour_list``  every (sender i, receiver j, unit shift o) with |pos[j] + o @ cell - pos[i]| < r_max over
-                        the lattice translations ceil(r_max / h_k) deep along each periodic direction (h_k the spacing
-                        of lattice planes k), without (i, i, 0); sorted by (i, j, image index of o);
+                        the lattice translations that can hold one (``image_depth``: ceil(r_max / h_k) deep along
+                        each periodic direction for atoms inside the cell, h_k the spacing of lattice planes k;
+                        deeper for atoms outside it), without (i, i, 0); sorted by (i, j, o lexicographically);
   * ``pad_graph``       the fixed-size layout of one structure: P - E padding self-loops with unit shift (0, 0, kz),
                         kz = ceil((r_max + 1) / |c_2|), one per atom round-robin, each after its sender's real edges.
 
@@ -21,14 +22,20 @@ layouts whose every sender segment is sorted and whose padding edges lie exactly
 import numpy as np
 
 
-def image_depth(cell, pbc, r_max):
-    """Translations per lattice direction: ceil(r_max / h_k) for periodic k (h_k = |det| / |c_{k+1} x c_{k+2}|)."""
+def image_depth(cell, pbc, r_max, pos=None):
+    """Translations per lattice direction that hold every edge: along periodic k an edge needs
+    |o_k + f_j,k - f_i,k| < r_max / h_k (h_k = |det| / |c_{k+1} x c_{k+2}|, f the fractional coordinates), so
+    |o_k| <= floor(r_max / h_k + span_k) with span_k the range of f_k over the atoms ``pos``; at least
+    ceil(r_max / h_k), the depth for atoms inside the cell."""
     vol = abs(np.linalg.det(cell))
+    frac = None if pos is None or len(pos) == 0 or not any(pbc) or vol == 0 else \
+        np.asarray(pos, np.float64) @ np.linalg.inv(cell)
     reps = []
     for k in range(3):
         if pbc[k]:
             h = vol / np.linalg.norm(np.cross(cell[(k + 1) % 3], cell[(k + 2) % 3]))
-            reps.append(int(np.ceil(r_max / h)))
+            span = 0.0 if frac is None else float(frac[:, k].max() - frac[:, k].min())
+            reps.append(int(max(np.ceil(r_max / h), np.floor(r_max / h + span + 1e-9))))
         else:
             reps.append(0)
     return reps
@@ -39,7 +46,7 @@ def neighbour_list(pos, cell, pbc, r_max):
     pos = np.asarray(pos, dtype=np.float64)
     cell = np.asarray(cell, dtype=np.float64)
     n = len(pos)
-    reps = image_depth(cell, pbc, r_max)
+    reps = image_depth(cell, pbc, r_max, pos)
     snd, rcv, ush = [], [], []
     offs = [(a, b, c) for a in range(-reps[0], reps[0] + 1) for b in range(-reps[1], reps[1] + 1)
             for c in range(-reps[2], reps[2] + 1)]

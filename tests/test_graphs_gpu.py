@@ -123,7 +123,7 @@ def test_captured_md_step_with_gpu_neighbour_list():
         out = step.replay()
         e_g, f_g = out['energy'].detach().clone(), out['forces'].detach().clone()
         ei_g = batch['edge_index'].clone()
-        step.neighbour_list.check()
+        step.check()
         nl = neighbour_list(new, batch['cell'], batch['ptr'], 5.0, pbc=pbc, pad_edges_to=6000)
         assert torch.equal(ei_g, nl.edge_index) and torch.equal(batch['shifts'], nl.shifts)
         if prev is not None:
@@ -139,5 +139,24 @@ def test_captured_md_step_with_gpu_neighbour_list():
         df = float((f_g - ref['forces']).abs().max())
         print(f'  replay {rep}: |dE| {de:.2e} eV  |dF| {df:.2e} eV/A', flush=True)
         assert de <= 1e-3 and df <= 1e-5
+    # the atoms pressed together (positions scaled by 0.8 about the origin) outgrow the 6,000-edge padding: the replay
+    # itself raises nothing, the next replay (or check()) reports the structures from the counts its copy brought back
+    print('[case] captured MD step: overflow reported one replay late', flush=True)
+    with torch.no_grad():
+        batch['positions'].copy_(base * 0.8)
+    step.replay()
+    with pytest.raises(ValueError, match='incomplete'):
+        step.check()
+    with torch.no_grad():
+        batch['positions'].copy_(base)
+    step.replay()
+    step.check()
+    with torch.no_grad():
+        batch['positions'].copy_(base * 0.8)
+    step.replay()
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match='incomplete'):
+        step.replay()
+    step.check()
     del step
     torch.cuda.synchronize()

@@ -341,3 +341,28 @@ def test_idempotent_patch_and_unpatch():
     assert len(r3['patched']) == 4 and 'spherical_harmonics' not in r3['patched']
     assert len(unpatch_model(m)) == 4
     assert not hasattr(m.interactions[0], 'conv_fusion')
+
+
+def test_training_mode_patch_warns_about_frozen_parameters():
+    """The drop-ins hold their weights as constants: patching a model in training mode names the parameters that no
+    gradient will reach; the same model in eval mode patches silently, and leaving the radial MLPs and linears on
+    e3nn keeps their parameters trainable (not named)."""
+    import warnings
+    dev = _dev()
+    print('[case] training-mode patch warning', flush=True)
+    m = factory.make_model(*factory.REF_CONFIGS['l2_corr2_scalar']).to(dev).train()
+    with pytest.warns(UserWarning, match='training mode') as rec:
+        patch_model(m, verbose=False)
+    text = ' '.join(str(w.message) for w in rec)
+    assert 'conv_tp_weights' in text and 'linear' in text
+    m = factory.make_model(*factory.REF_CONFIGS['l2_corr2_scalar']).to(dev).eval()
+    with warnings.catch_warnings(record=True) as rec:
+        warnings.simplefilter('always')
+        patch_model(m, verbose=False)
+    assert not any('training mode' in str(w.message) for w in rec)
+    m = factory.make_model(*factory.REF_CONFIGS['l2_corr2_scalar']).to(dev).train()
+    with pytest.warns(UserWarning, match='training mode') as rec:
+        patch_model(m, verbose=False, radial_mlp=False, linears=False, readouts=False)
+    text = ' '.join(str(w.message) for w in rec if 'training mode' in str(w.message))
+    assert 'conv_tp_weights' not in text and 'interactions.0.linear' not in text
+    assert all(t.requires_grad for n, t in m.named_parameters() if 'conv_tp_weights' in n)

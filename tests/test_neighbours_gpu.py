@@ -69,6 +69,48 @@ def test_equals_host_builder(cfg):
         _compare(nl, ref, ref['n_real_edges'])
 
 
+@pytest.mark.parametrize('cfg', [0, 2])
+def test_unwrapped_atoms_equal_host_builder(cfg):
+    """Atoms moved by up to two cells along each periodic direction (unwrapped MD coordinates): the image search
+    widens with the span of the fractional coordinates, and the list equals the host builder's on the moved atoms
+    (itself equal to the wrapped list with shifted images, tests/test_oracle_neighbours.py)."""
+    dev = _dev()
+    st = factory.structures(cfg)
+    r_max, pad = st['r_max'], st['pad_edges_to']
+    rng = np.random.default_rng(5)
+    moved = []
+    for s in st['structures'][:4]:
+        m = rng.integers(-2, 3, size=(len(s), 3)) * np.asarray(s.pbc, dtype=np.int64)
+        moved.append(D.Structure(s.numbers, s.positions + m @ s.cell, s.cell, s.pbc))
+    for layout in (pad, None):
+        print(f'[case] neighbour list config {cfg} unwrapped, pad={layout}', flush=True)
+        ref = _host_batch(moved, r_max, layout, torch.float64)
+        pos, cell, pbc, ptr = _inputs(moved, dev)
+        nl = neighbour_list(pos, cell, ptr, r_max, pbc=pbc, pad_edges_to=layout, dtype=torch.float64)
+        _compare(nl, ref, ref['n_real_edges'])
+        assert nl.overflowed() == []
+
+
+def test_image_search_cut_is_reported():
+    """An atom 70 cells away along the one periodic direction of a 2.5 A cell needs 72 translations: the search stops
+    at 64, the structure reports n_edges -1 (padded layout: check() raises), and the exact layout raises."""
+    dev = _dev()
+    cell = np.eye(3) * 2.5
+    far = D.Structure(np.array([78, 78]), np.array([[0.0, 0.0, 0.0], [70 * 2.5 + 1.0, 0.0, 0.0]]), cell,
+                      (True, False, False))
+    near = D.Structure(np.array([78, 78]), np.array([[0.0, 0.0, 0.0], [1.0, 0.0, 0.0]]), cell, (True, False, False))
+    pos, cel, pbc, ptr = _inputs([near, far], dev)
+    print('[case] neighbour list image search cut, padded', flush=True)
+    nl = neighbour_list(pos, cel, ptr, 5.0, pbc=pbc, pad_edges_to=64, dtype=torch.float64)
+    assert nl.n_edges.cpu().tolist()[1] == -1 and nl.n_edges.cpu().tolist()[0] > 0
+    assert nl.overflowed() == [1]
+    with pytest.raises(ValueError, match='64 cells'):
+        nl.check()
+    print('[case] neighbour list image search cut, exact', flush=True)
+    with pytest.raises(ValueError, match='64 lattice translations'):
+        neighbour_list(pos, cel, ptr, 5.0, pbc=pbc, pad_edges_to=None, dtype=torch.float64)
+
+
 def test_overflow_and_unpaddable_reported():
     dev = _dev()
     st = factory.structures(2)

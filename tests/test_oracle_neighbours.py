@@ -87,3 +87,39 @@ def test_padded_layout_equals_batch_graphs():
     vec = pos[b['edge_index'][1]] - pos[b['edge_index'][0]] + b['shifts'].double().numpy()
     pad = (b['edge_index'][0] == b['edge_index'][1]).numpy() & (np.abs(b['unit_shifts'].numpy()).sum(1) > 0)
     assert pad.sum() == 3 * 6000 - b['n_real_edges'] and (np.linalg.norm(vec[pad], axis=1) > 5.0).all()
+
+
+def _unwrapped(s, seed, depth=2):
+    """The structure with every atom moved by a random lattice vector of up to ``depth`` cells along each periodic
+    direction (as in unwrapped MD coordinates), and the moves m [n, 3]."""
+    rng = np.random.default_rng(seed)
+    m = rng.integers(-depth, depth + 1, size=(len(s), 3)) * np.asarray(s.pbc, dtype=np.int64)
+    return D.Structure(s.numbers, s.positions + m @ s.cell, s.cell, s.pbc), m
+
+
+@pytest.mark.parametrize('cfg', [0, 2])
+def test_unwrapped_atoms_keep_every_edge(cfg):
+    """Moving atom i by the lattice vector m_i maps edge (i, j, o) to (i, j, o + m_i - m_j) and nothing else: the
+    oracle and the host builder on the moved atoms give exactly the wrapped list with shifted images, in the same
+    order.  The depth of atoms inside the cell, ceil(r_max / h_k), loses edges here (the planted mistake)."""
+    st = factory.structures(cfg)
+    r_max = st['r_max']
+    for k, s in enumerate(st['structures'][:2]):
+        snd, rcv, ush = onl.neighbour_list(s.positions, s.cell, s.pbc, r_max)
+        u, m = _unwrapped(s, seed=10 + k)
+        want = (snd, rcv, ush + m[snd] - m[rcv])
+        assert _same(onl.neighbour_list(u.positions, u.cell, u.pbc, r_max), want)
+        assert _same(_host(u, r_max), want)
+        shallow = onl.image_depth(s.cell, s.pbc, r_max)
+        assert any(d > w for d, w in zip(onl.image_depth(u.cell, u.pbc, r_max, u.positions), shallow))
+        assert np.any(np.abs(want[2]).max(axis=0) > np.array(shallow))
+
+
+def test_depth_of_atoms_inside_the_cell_is_the_plane_spacing_bound():
+    """For atoms within one cell's span (config 2's slabs: fractional coordinates within -0.006 .. 0.98) the depth is
+    exactly ceil(r_max / h_k): no search beyond what wrapped atoms need."""
+    st = factory.structures(2)
+    s = st['structures'][0]
+    frac = s.positions @ np.linalg.inv(s.cell)
+    assert (frac.max(axis=0) - frac.min(axis=0) < 1.0).all()
+    assert onl.image_depth(s.cell, s.pbc, st['r_max'], s.positions) == onl.image_depth(s.cell, s.pbc, st['r_max'])

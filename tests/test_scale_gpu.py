@@ -5,7 +5,7 @@ correlation 3), where the float64 oracle is too slow, through size-independent p
 * the convolution is linear in each of x, W and Y, so for any g:  <g, out> = <gx, x> = <gW, W> = <gY, Y>  (each
   product of the backward is the adjoint of the forward; a dropped term, a wrong sign or a wrong index breaks it);
 * the receiver-ordered and the sender-ordered backward, and the factored-weight (W0 * cutoff) and plain paths, agree;
-* the element-grouped and the one-node-per-workgroup symmetric contraction agree.
+* the LDS-staged and the element-grouped symmetric contraction agree with the one-node-per-workgroup kernels.
 
 Tolerances are relative, sized for fp32 sums over ~10^8 terms: 1e-4 on the inner products, 1e-5 between kernels.
 """
@@ -93,25 +93,33 @@ def test_conv_factored_matches_plain_full_size(cfg4):
         assert _rel(u, v) < 1e-5
 
 
-def test_sc_grouped_matches_per_node_full_size(cfg4):
+def test_sc_families_match_per_node_full_size(cfg4):
+    """The three symmetric-contraction families at N = 20,000: the LDS-staged kernels (what the patched model
+    launches at this size) and the element-grouped ones against one node per workgroup (itself against the oracle
+    at small sizes), outputs and input gradients."""
     model, batch, meta = cfg4
     dev = torch.device('cuda:0')
     N = batch['positions'].shape[0]
     attrs = batch['node_attrs'].to(dev)
     gen = torch.Generator(device='cpu').manual_seed(30)
     for li, prod in enumerate(model.products):
-        print(f'[case] config 4 symmetric contraction {li} grouped vs per node', flush=True)
         op = HipSymmetricContraction(prod.symmetric_contractions, device=dev)
         assert op.use_grouped(N, dev)
+        assert op.kernel_family(N, dev) == 'staged'
         x = (0.5 * torch.randn(N, op.spec.C, op.spec.n_ell, generator=gen)).to(dev).requires_grad_(True)
         g = torch.randn(N, op.spec.out_dim, generator=gen).to(dev)
         got = {}
-        for grouped in (True, False):
-            op.grouped = grouped
+        for fam, (staged, grouped) in (('staged', (True, None)), ('grouped', (False, True)),
+                                       ('node', (False, False))):
+            print(f'[case] config 4 symmetric contraction {li}: {fam} kernels', flush=True)
+            op.staged, op.grouped = staged, grouped
+            assert op.kernel_family(N, dev) == fam
             out = op(x, attrs)
-            got[grouped] = (out.detach(), torch.autograd.grad(out, x, g)[0])
-        for u, v in zip(got[True], got[False]):
-            assert _rel(u, v) < 1e-5
+            got[fam] = (out.detach(), torch.autograd.grad(out, x, g)[0])
+            del out
+        for fam in ('staged', 'grouped'):
+            for u, v in zip(got[fam], got['node']):
+                assert _rel(u, v) < 1e-5, fam
 
 
 def test_patched_model_full_size(cfg4):
