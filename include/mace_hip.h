@@ -109,7 +109,9 @@ enum mh_kernel_kind {
     MH_GEOM_SEGSUM1 = 70, /* per-structure sums of one column (MACE's energy sums)                  */
     MH_EDGE_PAIR = 71,   /* shared radial-MLP rows of an edge and its reverse                         */
     MH_CONV_FWD_CR = 72, /* conv fwd, W0 * cutoff with W0 rows through a row map (cacheable loads)     */
-    MH_NUM_KINDS = 73
+    MH_MLP_H3 = 73,      /* radial MLP: last hidden activations of the listed rows, h3 [slot][HL]       */
+    MH_MLP_OUT = 74,     /* its output layer, weight-stationary: persistent waves over 16-edge tiles    */
+    MH_NUM_KINDS = 75
 };
 
 /* flags of mh_conv_bwd */
@@ -453,6 +455,18 @@ int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* W
  * reference counterpart. */
 int mh_mlp_fwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E,
                     const int32_t* rows, const int32_t* count, void* stream);
+/* mh_mlp_fwd_rows with the output layer weight-stationary (what the patched model runs): MH_MLP_H3 writes the last
+ * hidden activations of slot i < count[0] to h3 [E, HL] (fp32, slot order, features in the output layer's K order;
+ * caller-owned scratch), then MH_MLP_OUT
+ * runs a persistent grid of 4-wave workgroups; every wave keeps one block of 64 output columns of the bf16x3-split
+ * output layer in registers (Wo, packed [ncb][4][HL / 32][3][64 lanes][8] bf16), the four waves of a workgroup take
+ * four consecutive blocks and share each 16-slot tile of their XCD's share through LDS, storing W0 row rows[i] (rows
+ * and count NULL: every slot, row = slot).  WhT: the hidden layers' transposed weights of mh_mlp_fwd.  ncb: the
+ * number of 64-column blocks the module was generated for (the grid is sized so that every workgroup keeps one group
+ * of four blocks).  Bind MH_MLP_H3 with 256 threads and 64 slots per block, MH_MLP_OUT with 256 threads.  Same
+ * results as mh_mlp_fwd_rows to fp32 rounding; no atomics.  No reference counterpart. */
+int mh_mlp_fwd_ws(mh_module* m, const float* ef, const float* WhT, const uint16_t* Wo, float* h3, float* W0,
+                  int64_t E, const int32_t* rows, const int32_t* count, int32_t ncb, void* stream);
 int mh_mlp_bwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                     int64_t E, const int32_t* rows, const int32_t* count, void* stream);
 

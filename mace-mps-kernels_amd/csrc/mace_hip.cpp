@@ -14,6 +14,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
 #include <sstream>
 #include <string>
@@ -138,7 +139,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 36; }
+int mh_version(void) { return 37; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -747,6 +748,26 @@ int mh_mlp_fwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16
     if ((rows == nullptr) != (count == nullptr)) return fail(-1, "mh_mlp_fwd_rows: rows and count go together");
     void* args[] = {&ef, &Wh, &Wl, &W0, &E, &rows, &count};
     return launch(m, MH_MLP_FWD, E, args, stream, "mh_mlp_fwd");
+}
+
+int mh_mlp_fwd_ws(mh_module* m, const float* ef, const float* WhT, const uint16_t* Wo, float* h3, float* W0,
+                  int64_t E, const int32_t* rows, const int32_t* count, int32_t ncb, void* stream) {
+    if (E > 0 && (!ef || !WhT || !Wo || !h3 || !W0)) return fail(-1, "mh_mlp_fwd_ws: NULL operand");
+    if ((rows == nullptr) != (count == nullptr)) return fail(-1, "mh_mlp_fwd_ws: rows and count go together");
+    if (ncb < 1) return fail(-1, "mh_mlp_fwd_ws: ncb must be positive");
+    if (E <= 0) return 0;
+    if (!m) return fail(-1, "mh_mlp_fwd_ws: null module");
+    void* a1[] = {&ef, &WhT, &h3, &E, &rows, &count};
+    if (int rc = launch(m, MH_MLP_H3, E, a1, stream, "mh_mlp_fwd_ws (hidden layers)")) return rc;
+    // persistent grid: 8 equal per-XCD shares of workgroups (blocks go round-robin over the XCDs), each share a
+    // multiple of the ncg = ceil(ncb / 4) column groups, about as many as are resident at once
+    if (!m->k[MH_MLP_OUT].fn) return fail(-1, "mh_mlp_fwd_ws: kernel slot MH_MLP_OUT not bound in this module");
+    int res = 0;
+    if (int rc = resident_blocks(m, MH_MLP_OUT, &res)) return rc;
+    const int ncg = (ncb + 3) / 4;
+    const int per_xcd = std::max(ncg, (res / 8) / ncg * ncg);
+    void* a2[] = {&h3, &Wo, &W0, &E, &rows, &count};
+    return launch_blocks(m, MH_MLP_OUT, 8LL * per_xcd, a2, stream, "mh_mlp_fwd_ws (output layer)");
 }
 
 int mh_mlp_fwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, float* W0, int64_t E, void* stream) {

@@ -26,9 +26,9 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_MLP_HIDB, MH_CONV_FWD_M, MH_CONV_BWD_M, MH_CONV_GYSUM, MH_SC_FWD_S, MH_SC_BWD_S, MH_SC_FWD_SI, \
     MH_SC_BWD_SI, MH_NL_SETUP, MH_NL_ZERO, MH_NL_BINS, MH_NL_SCAN, MH_NL_PLACE, MH_NL_COUNT, MH_NL_OFFSETS, \
     MH_NL_FILL, MH_SPECIES_ORDER, MH_MLP_JVP, MH_MLP_BWD2, MH_GEOM_SEGSUM, MH_NL_BASES, MH_EDGE_COUNT, \
-    MH_EDGE_PLACE, MH_GEOM_SEGSUM1, MH_EDGE_PAIR, MH_CONV_FWD_CR = range(73)
+    MH_EDGE_PLACE, MH_GEOM_SEGSUM1, MH_EDGE_PAIR, MH_CONV_FWD_CR, MH_MLP_H3, MH_MLP_OUT = range(75)
 MH_WANT_GX, MH_WANT_GWY, MH_CUT_MASKED, MH_CUT_NOZERO = 1, 2, 4, 8
-ABI_VERSION = 36
+ABI_VERSION = 37
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -66,6 +66,7 @@ _SIGS = {
     'mh_mlp_fwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),
     'mh_mlp_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P]),
     'mh_mlp_fwd_rows': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P, _P, _P]),
+    'mh_mlp_fwd_ws': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P, _P, ctypes.c_int32, _P]),
     'mh_mlp_bwd_rows': (ctypes.c_int, [_P] * 6 + [ctypes.c_int64, _P, _P, _P]),
     'mh_edge_compact_work_size': (ctypes.c_size_t, [ctypes.c_int64]),
     'mh_geom_segsum1': (ctypes.c_int, [_P, _P, _P, _P, _I, _P]),

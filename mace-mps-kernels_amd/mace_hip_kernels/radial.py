@@ -51,13 +51,29 @@ NSPLIT = 3           # bf16 parts per fp32 weight (exact split)
 # Store the forward's W0 rows with the non-temporal policy.  The convolution reads them next, partly from the caches:
 # measured on config 2's captured E+F call, non-temporal stores made it 42 us slower.
 W0_NT = False
-BPAD = 8             # bf16 row padding of a chunk (keeps 16-byte reads aligned, spreads banks)
-PAD = 4              # LDS row padding (floats): the 4 lane groups of a fragment land on different banks
+# LDS row paddings.  An MFMA operand fragment is read as one 16-byte ds_read_b128 per lane at row (lane % 16), word
+# offset 4 (lane / 16) within the row; on gfx950 such reads run at the full LDS rate when the row length is 8 mod 16
+# words, and about 17% slower for other lengths that are multiples of 4 (an in-bounds sweep of row lengths 12 .. 84
+# words).  Scalar reads of 64 lanes (column c16 + 16 q of a row-major block) want the row length 4 mod 16 instead.
+BPAD = 16            # bf16 row padding of a chunk: rows of 64 + 16 (forward) and 32 + 16 (backward) bf16 = 40 / 24 words
+PAD = 4              # fp32 row padding of the hidden layers' natural layout (scalar reads, rows of 64 + 4 words)
+TPAD = 8             # and of their transposed layout (16-byte reads, rows of 64 + 8 words), from the second layer on
+TPAD0 = 4            # the first layer's transposed rows (K = the padded input width, scalar reads: 8 + 4 words)
 # Waves per SIMD the forward and backward are compiled for (amdgpu_waves_per_eu; None: the compiler's choice).
 # Left to itself the compiler gives mlp_fwd 172 VGPRs + 48 AGPRs (2 waves per SIMD); asked for 3 it fits in 138
 # VGPRs without spills, mlp_bwd in 154.
 WAVES_FWD = 3
 WAVES_BWD = 3
+# The forward as two kernels (mh_mlp_fwd_ws): the hidden layers of the listed rows into an [E, HL] scratch (mlp_h3),
+# then the output layer weight-stationary (mlp_out): a persistent grid whose waves each keep one block of WS_COLS
+# output columns of the split output layer in registers and walk the 16-edge tiles of their XCD's share, four waves
+# (four blocks) sharing each tile's activations through LDS.  False: the single-kernel forward (mlp_fwd), whose workgroups stream the whole output layer
+# through LDS for every 64 edges.
+WS_FWD = True
+WS_MIN_COLS = 1024   # ... for output layers at least this wide (config 2: layer 2's 1280 columns 84.8 -> 76.5 us in the
+                     # E+F call; layer 1's 512 columns 39.5 -> 43.3 us, so the single kernel stays there)
+WS_COLS = 64         # output columns per wave of mlp_out (4 MFMA column tiles: 96 VGPRs of split weights)
+WS_WAVES = 3         # waves per SIMD mlp_out is compiled for
 
 
 def _layers(mod):
@@ -157,15 +173,20 @@ def _layout(spec):
     rows = [4 * K0S] + hs[1:-2]                          # K extent of each hidden layer
     cols = hs[1:-1]                                      # outputs of each hidden layer
     nat, tr, o1, o2 = [], [], 0, 0
-    for r, c in zip(rows, cols):
+    for i, (r, c) in enumerate(zip(rows, cols)):
         nat.append(o1)
         o1 += r * (c + PAD)                              # natural [k][j + PAD]   (backward)
         tr.append(o2)
-        o2 += c * (r + PAD)                              # transposed [j][k + PAD] (forward)
+        o2 += c * (r + _tpad(i))                         # transposed [j][k + TPAD] (forward)
     RSF = HL + BPAD                                      # bf16 row of a forward chunk: one output column, K = HL
     RSB = CH_BWD + BPAD                                  # bf16 row of a backward chunk: one hidden feature, K = CH_BWD
     return dict(H0=H0, NW=NW, HL=HL, K0S=K0S, rows=rows, cols=cols, nat=nat, tr=tr, nat_size=o1, tr_size=o2,
                 RSF=RSF, RSB=RSB, chunk_fwd=NSPLIT * CH_FWD * RSF, chunk_bwd=NSPLIT * HL * RSB)
+
+
+def _tpad(i):
+    """Row padding (floats) of hidden layer i's transposed LDS layout."""
+    return TPAD0 if i == 0 else TPAD
 
 
 def _kperm(HL):
@@ -227,7 +248,11 @@ def _source(spec, second):
     lds_fwd = max(Lo['tr_size'], Lo['chunk_fwd'])        # floats; a bf16 chunk of n elements takes n / 2 floats
     lds_bwd = max(Lo['nat_size'], Lo['chunk_bwd'])
     L = [_native.device_header(),
-         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }', '']
+         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }',
+         '// the logistic function on the hardware exp2 and reciprocal (about 1e-7 relative error; -z large: rcp(inf) = 0)',
+         '__device__ __forceinline__ float mlp_sigf(float z) {',
+         '  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * z));',
+         '}', '']
     if second:
         # h = c z s(z) (s the logistic function): h' = c s (1 + z (1 - s)), h'' = c s (1 - s) (2 + z (1 - 2 s))
         L += ['__device__ __forceinline__ float mlp_d1(float z) { const float s = mlp_sig(z); '
@@ -303,7 +328,7 @@ def _source(spec, second):
                   for st in range(K0S)]
         return P
 
-    def hidden_fwd(transposed, keep, tiles, dual=False, keep_t=False):
+    def hidden_fwd(transposed, keep, tiles, dual=False, keep_t=False, sig='mlp_sig'):
         """z_i and h_i = c_i silu(z_i) for every hidden layer on the fp32 MFMA, A operands from LDS (transposed
         layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for every edge tile in
         ``tiles``.  ``dual``: also the tangents zt_i (the same A operands applied to the input tangent xv / the
@@ -319,7 +344,7 @@ def _source(spec, second):
             if i == 0:
                 for st in range(K0S):
                     for o in range(T):
-                        a = (f'lds[{Lo["tr"][0]} + ({16 * o} + c16) * {rows[0] + PAD} + {4 * st} + q]' if transposed else
+                        a = (f'lds[{Lo["tr"][0]} + ({16 * o} + c16) * {rows[0] + _tpad(0)} + {4 * st} + q]' if transposed else
                              f'lds[{Lo["nat"][0]} + ({4 * st} + q) * {cols[0] + PAD} + {16 * o} + c16]')
                         P.append(f'  {{ const float a = {a};')
                         P += [f'    {zn}0_{b}[{o}] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, {xn}{b}[{st}], {zn}0_{b}[{o}], '
@@ -331,7 +356,7 @@ def _source(spec, second):
                     if transposed:
                         for o in range(T):
                             P.append(f'  const mh_f4 a{i}_{ti}_{o} = *reinterpret_cast<const mh_f4*>(&lds[{Lo["tr"][i]} + '
-                                     f'({16 * o} + c16) * {rows[i] + PAD} + {16 * ti} + 4 * q]);')
+                                     f'({16 * o} + c16) * {rows[i] + _tpad(i)} + {16 * ti} + 4 * q]);')
                     for r in range(4):
                         for o in range(T):
                             a = (f'a{i}_{ti}_{o}[{r}]' if transposed else
@@ -346,7 +371,7 @@ def _source(spec, second):
                     for o in range(T):
                         for r in range(4):
                             P.append(f'  h{i}_{b}[{o}][{r}] = {_lit(spec.c[i])} * z{i}_{b}[{o}][{r}] * '
-                                     f'mlp_sig(z{i}_{b}[{o}][{r}]);')
+                                     f'{sig}(z{i}_{b}[{o}][{r}]);')
             if dual and (i < nh - 1 or keep_t):
                 for b in tiles:
                     P.append(f'  mh_f4 ht{i}_{b}[{T}];')
@@ -665,18 +690,161 @@ def _source(spec, second):
         H += walk_back(grp, 'dhs_')
         L.extend(H + ['}', ''])
 
+    def h3_kernel(name):
+        """mlp_h3: slot i < count (edge rows[i]): the last hidden activations (SiLU on the hardware exp2 and
+        reciprocal, within about 1e-7 of the exact activation), fp32, into h3 [E][HL] at row i with
+        the features in the output layer's K order (_kperm: position 32 s + 8 q + 4 t + r holds feature
+        32 s + 16 t + 4 q + r, which is what lane group q holds after the last hidden layer: two float4 stores per K
+        step of 32)."""
+        H = head(name, 'const float* __restrict__ ef, const float* __restrict__ Wh, float* __restrict__ h3, long long E',
+                 Lo['tr_size'], 1, indexed=True)
+        H += skip_block(1, zero_rows=False)
+        H += xin(range(1))                   # the row's features are loaded while the weights are staged
+        H += stage('Wh', Lo['tr_size']) + ['  __syncthreads();']
+        H += hidden_fwd(True, True, range(1), sig='mlp_sigf')
+        H += ['  if (do0) {']
+        H += [f'    *reinterpret_cast<mh_f4*>(h3 + ej0 * {HL} + {32 * st + 4 * tt} + 8 * q) = h{nh - 1}_0[{2 * st + tt}];'
+              for st in range(S) for tt in range(2)]
+        H += ['  }', '}', '']
+        return H
+
+    def out_kernel(name):
+        """mlp_out: the output layer over h3, weight-stationary.  A workgroup is 4 waves on 4 consecutive 64-column
+        blocks (a column group of 256 columns); each wave keeps its block of the split output layer in registers for
+        the whole launch.  The 16-slot tiles are cut into eight contiguous shares, one per XCD (the dispatcher sends
+        workgroup b to XCD b % 8), and the XCD's workgroups split its tiles between them: with G workgroups on the XCD
+        (the host makes G a multiple of the NCG column groups), workgroup g takes column group g % NCG and tiles
+        g / NCG, + G / NCG, ....  Per tile the workgroup loads the 16 rows of h3 once (one float4 per thread, loaded
+        a tile ahead), splits them into bf16 parts and writes them to LDS as the MFMA's B operand fragments (two
+        buffers, one barrier per tile); every wave reads its six fragments with 16-byte reads and stores its 64
+        columns of the 16 rows as one float4 per lane and column tile."""
+        CT = WS_COLS // 16
+        NCB = -(-NW // WS_COLS)
+        NCG = -(-NCB // 4)
+        TAILT = (NW % WS_COLS) // 16
+        KS = HL // 32
+        FR = KS * 3 * 64 * 8                                 # bf16 per tile of operand fragments
+        assert HL == 64, 'mlp_out stages one float4 of h3 per thread: HL must be 64'
+        F = [f'extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu({WS_WAVES}))) '
+             f'void {name}(const float* __restrict__ h3, const unsigned short* __restrict__ Wo, float* __restrict__ W0, '
+             'long long E, const int* __restrict__ rows, const int* __restrict__ count) {',
+             f'  __shared__ __align__(16) unsigned short frag[2][{FR}];',
+             '  const int t = threadIdx.x, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
+             '  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);',
+             '  const long long ncount = count ? (long long)count[0] : E;',
+             '  const long long T = (ncount + 15) / 16;',
+             '  const int nx8 = gridDim.x < 8 ? (int)gridDim.x : 8;        // XCDs the grid reaches (round-robin)',
+             '  const int xcd = (int)blockIdx.x % nx8;',
+             '  const int G = ((int)gridDim.x - xcd + nx8 - 1) / nx8;      // workgroups on this XCD',
+             '  const int g = (int)blockIdx.x / nx8;',
+             '  const long long t0 = T * xcd / nx8, Tx = T * (xcd + 1) / nx8 - t0;   // this XCD\'s tiles',
+             '  // G >= NCG: workgroup g keeps column group g % NCG and takes tiles g / NCG, + G / NCG, ... (the workgroups',
+             '  // past the last whole set of NCG idle); G < NCG: workgroup g takes column groups g, g + G, ... and every tile',
+             f'  const int nsub = G / {NCG};',
+             f'  if (nsub > 0 && g >= nsub * {NCG}) return;',
+             f'  const int cg0 = nsub > 0 ? g % {NCG} : g, cgs = nsub > 0 ? {NCG} : G;',
+             f'  const long long sub = nsub > 0 ? g / {NCG} : 0, step = nsub > 0 ? nsub : 1;',
+             '  if (sub >= Tx) return;',
+             '  // the staging thread\'s piece of a tile: slot t / 16, K positions 4 u .. 4 u + 3 (u = t % 16), i.e. half',
+             '  // u % 2 of lane group (u / 2) % 4\'s fragment at K step u / 8',
+             '  const int ps = t >> 4, pu = t & 15, pks = pu >> 3, pq = (pu >> 1) & 3, ph = pu & 1;',
+             f'  for (int cg = cg0; cg < {NCG}; cg += cgs) {{',
+             '    const int cb = 4 * cg + wave;                              // uniform; a block past NCB computes nothing',
+             f'    const bool act = cb < {NCB};',
+             f'    mh_bf8 a[{CT}][{KS}][3];',
+             '    if (act) {',
+             f'      const mh_u4* __restrict__ src = reinterpret_cast<const mh_u4*>(Wo) + (size_t)cb * {CT * KS * 3 * 64} + lane;']
+        F += [f'      a[{ct}][{ks}][{p}] = __builtin_bit_cast(mh_bf8, src[{((ct * KS + ks) * 3 + p) * 64}]);'
+              for ct in range(CT) for ks in range(KS) for p in range(3)]
+        F += ['    } else {']
+        F += [f'      a[{ct}][{ks}][{p}] = __builtin_bit_cast(mh_bf8, mh_u4{{0u, 0u, 0u, 0u}});'
+              for ct in range(CT) for ks in range(KS) for p in range(3)]
+        F += ['    }',
+              '    long long tt = sub;',
+              '    // a tile\'s staging piece and this lane\'s edge row, loaded a tile ahead (clamped: every load in range)',
+              '    auto piece = [&](long long tile) {',
+              '      const long long s2 = (t0 + tile) * 16 + ps;',
+              f'      return *reinterpret_cast<const mh_f4*>(h3 + (s2 < ncount ? s2 : ncount - 1) * {HL} + 4 * pu);',
+              '    };',
+              '    auto erow = [&](long long tile) {',
+              '      const long long s2 = (t0 + tile) * 16 + c16;',
+              '      const long long sc = s2 < ncount ? s2 : ncount - 1;',
+              '      return rows ? rows[sc] : (int)sc;',
+              '    };',
+              '    mh_f4 pc = piece(tt);',
+              '    int rc = erow(tt);',
+              '    int buf = 0;',
+              '    while (true) {',
+              '      const long long nx = tt + step;',
+              '      const long long tn = nx < Tx ? nx : tt;',
+              '      const mh_f4 pn = piece(tn);',
+              '      const int rn = erow(tn);',
+              '      // tile tt\'s piece, split exactly into three bf16 parts, into its fragments in LDS buffer buf',
+              '      {',
+              '        unsigned pk[3][2];',
+              '#pragma unroll',
+              '        for (int j = 0; j < 4; j += 2) {',
+              '          unsigned bb[2][3];',
+              '#pragma unroll',
+              '          for (int e = 0; e < 2; ++e) {',
+              '            const unsigned hbits = __float_as_uint(pc[j + e]) & 0xFFFF0000u;',
+              '            const float r1 = pc[j + e] - __uint_as_float(hbits);',
+              '            const unsigned mbits = __float_as_uint(r1) & 0xFFFF0000u;',
+              '            const float r2 = r1 - __uint_as_float(mbits);',
+              '            bb[e][0] = hbits >> 16;',
+              '            bb[e][1] = mbits >> 16;',
+              '            bb[e][2] = __float_as_uint(r2) >> 16;',
+              '          }',
+              '#pragma unroll',
+              '          for (int p = 0; p < 3; ++p) pk[p][j / 2] = bb[0][p] | (bb[1][p] << 16);',
+              '        }',
+              '#pragma unroll',
+              '        for (int p = 0; p < 3; ++p)',
+              '          *reinterpret_cast<uint2*>(&frag[buf][((pks * 3 + p) * 64 + pq * 16 + ps) * 8 + 4 * ph]) = '
+              'uint2{pk[p][0], pk[p][1]};',
+              '      }',
+              '      __syncthreads();',
+              '      if (act) {',
+              f'        mh_bf8 b[{KS}][3];']
+        F += [f'        b[{ks}][{p}] = *reinterpret_cast<const mh_bf8*>(&frag[buf][(({ks} * 3 + {p}) * 64 + lane) * 8]);'
+              for ks in range(KS) for p in range(3)]
+        F += [f'        mh_f4 acc[{CT}];'] + [f'        acc[{ct}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for ct in range(CT)]
+        for ks in range(KS):
+            for pa, pb in PAIRS:
+                for ct in range(CT):
+                    F.append(f'        acc[{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[{ct}][{ks}][{pa}], b[{ks}][{pb}], '
+                             f'acc[{ct}], 0, 0, 0);')
+        F += ['        if ((t0 + tt) * 16 + c16 < ncount) {',
+              f'          float* __restrict__ dst = W0 + (long long)rc * {NW} + cb * {WS_COLS} + 4 * q;']
+        for ct in range(CT):
+            guard = f'if (cb < {NCB - 1}) ' if TAILT and ct >= TAILT else ''
+            F.append(f'          {guard}*reinterpret_cast<mh_f4*>(dst + {16 * ct}) = acc[{ct}];')
+        F += ['        }',
+              '      }',
+              '      if (nx >= Tx) break;',
+              '      tt = nx;',
+              '      pc = pn;',
+              '      rc = rn;',
+              '      buf ^= 1;',
+              '    }',
+              '    __syncthreads();                     // every wave is done with the buffers before the next group',
+              '  }',
+              '}', '']
+        return F
+
     if second:
         L += fwd_kernel(spec.kname('mlp_jvp'), True) + bwd_kernel(spec.kname('mlp_bwd2'), True)
     else:
         L += fwd_kernel(spec.kname('mlp_fwd'), False) + bwd_kernel(spec.kname('mlp_bwd'), False)
         hidden_only()
+        L += h3_kernel(spec.kname('mlp_h3')) + out_kernel(spec.kname('mlp_out'))
     return '\n'.join(L)
 
 
 def packed_weights(spec):
     """Weight buffers: {'fwd': (hidden transposed fp32, output layer bf16 chunks), 'bwd': (hidden natural fp32,
     output layer bf16 chunks)}.  Hidden layer i is laid out as the kernel's LDS copy: natural [k][j + PAD] (the first
-    layer's K padded to a multiple of 4 with zero rows) or transposed [j][k + PAD].  The output layer W [HL, NW] is
+    layer's K padded to a multiple of 4 with zero rows) or transposed [j][k + TPAD] (TPAD0 for the first layer).  The output layer W [HL, NW] is
     split exactly into three bf16 parts (uint16 bit patterns) and cut into chunks of CH_FWD / CH_BWD columns (the last
     zero-padded): forward [chunk][3][HL / 8][CH_FWD][8] with K in the ``_kperm`` order, backward
     [chunk][3][CH_BWD / 8][HL][8] (16-byte groups of a row, rows innermost)."""
@@ -688,7 +856,7 @@ def packed_weights(spec):
         buf = np.zeros((r, c + PAD))
         buf[:A.shape[0], :c] = A
         nat[Lo['nat'][i]:Lo['nat'][i] + buf.size] = buf.reshape(-1)
-        bt = np.zeros((c, r + PAD))
+        bt = np.zeros((c, r + _tpad(i)))
         bt[:, :A.shape[0]] = A.T
         tr[Lo['tr'][i]:Lo['tr'][i] + bt.size] = bt.reshape(-1)
     HL, NW = spec.A[-1].shape
@@ -704,8 +872,16 @@ def packed_weights(spec):
     parts, n = padded(CH_BWD)
     bwd = np.stack([p.reshape(HL, n, CH_BWD).transpose(1, 0, 2) for p in parts], axis=1)
     bwd = bwd.reshape(n, 3, HL, CH_BWD // 8, 8).transpose(0, 1, 3, 2, 4)
+    # weight-stationary forward: [ncb][ct][ks][part][lane][8], lane = 16 q + c16 holding output column
+    # 64 cb + 16 ct + c16 at K positions 32 ks + 8 q .. + 7 (hidden features in the _kperm order)
+    ncb, KS = -(-NW // WS_COLS), HL // 32
+    w = np.zeros((HL, ncb * WS_COLS), dtype=np.float32)
+    w[:, :NW] = spec.A[-1][perm]                             # K position -> hidden feature, as mlp_h3 writes hb
+    ws = np.stack([p.reshape(KS, 4, 8, ncb, WS_COLS // 16, 16).transpose(3, 4, 0, 1, 5, 2)
+                   .reshape(ncb, WS_COLS // 16, KS, 64, 8) for p in bf16_split3(w)], axis=3)
     return {'fwd': (tr.astype(np.float32), np.ascontiguousarray(fwd).reshape(-1)),
-            'bwd': (nat.astype(np.float32), np.ascontiguousarray(bwd).reshape(-1))}
+            'bwd': (nat.astype(np.float32), np.ascontiguousarray(bwd).reshape(-1)),
+            'ws': np.ascontiguousarray(ws).reshape(-1)}
 
 
 _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. training on forces/stress or an '
@@ -729,8 +905,13 @@ def mlp_forward(op, ef, rows=None, count=None):
     rows are computed and written (the other rows of W0 are left unset)."""
     out = torch.empty(ef.shape[0], op.spec.hs[-1], device=ef.device, dtype=torch.float32)
     P = _native.ptr
-    _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd_rows, op.module.handle, P(ef), P(op.WhT),
-                   P(op.WlT), P(out), ef.shape[0], P(rows), P(count), _native.stream_of(ef))
+    if WS_FWD and op.spec.hs[-1] >= WS_MIN_COLS:
+        h3 = torch.empty(ef.shape[0], op.spec.hs[-2], device=ef.device, dtype=torch.float32)
+        _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd_ws, op.module.handle, P(ef), P(op.WhT),
+                       P(op.Wo), P(h3), P(out), ef.shape[0], P(rows), P(count), op.ncb, _native.stream_of(ef))
+    else:
+        _native.launch(f'mlp_fwd[{op.tag}]', _native.load().mh_mlp_fwd_rows, op.module.handle, P(ef), P(op.WhT),
+                       P(op.WlT), P(out), ef.shape[0], P(rows), P(count), _native.stream_of(ef))
     op.last_rows = count if count is not None else ef.shape[0]     # rows computed: device count or all
     return out
 
@@ -815,9 +996,13 @@ class HipRadialMLP(torch.nn.Module):
                 _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), BLOCK, 64 * NB_BWD),
                 _native.MH_MLP_HID: (self.spec.kname('mlp_hid'), BLOCK, 64 * NB_FWD),
                 _native.MH_MLP_HIDB: (self.spec.kname('mlp_hidb'), BLOCK, 64 * NB_BWD),
+                _native.MH_MLP_H3: (self.spec.kname('mlp_h3'), BLOCK, 64),
+                _native.MH_MLP_OUT: (self.spec.kname('mlp_out'), BLOCK, 1),
             })
+        self.ncb = -(-self.spec.hs[-1] // WS_COLS)
         pw = packed_weights(self.spec)
-        for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1])):
+        for name, arr in (('WhT', pw['fwd'][0]), ('WlT', pw['fwd'][1]), ('Wh', pw['bwd'][0]), ('Wl', pw['bwd'][1]),
+                          ('Wo', pw['ws'])):
             # the bf16 parts travel as int16 bit patterns (the kernels read them as raw 16-bit words)
             arr = arr.view(np.int16) if arr.dtype == np.uint16 else arr
             self.register_buffer(name, torch.from_numpy(np.ascontiguousarray(arr)).to(dev), persistent=False)

@@ -942,13 +942,61 @@ def test_radial_mlp_c_abi():
     gx = torch.empty_like(x)
     _native.check(lib.mh_mlp_bwd(op.module.handle, P(x), P(op.Wh), P(op.Wl), P(out), P(gx), e, st), 'mlp_bwd')
     torch.cuda.synchronize()
-    assert torch.equal(out, op(x))
+    assert _rel(out.double().cpu().numpy(), op(x).double().cpu().numpy()) < 2e-6     # the module's forward (mlp_out)
     # the backward is the adjoint of the Jacobian: <gx, dx> = <out, J dx> for a small step dx (finite difference)
     dx = 1e-3 * torch.randn_like(x)
     jdx = (op(x + dx) - op(x - dx)) / 2
     lhs, rhs = _dot(gx, dx), _dot(out, jdx)
     assert abs(lhs - rhs) <= 1e-3 * abs(rhs)
     assert lib.mh_mlp_fwd(op.module.handle, None, P(op.WhT), P(op.WlT), P(out), e, st) != 0
+    assert b'NULL' in lib.mh_last_error()
+
+
+@pytest.mark.parametrize('hidden,lmax', [('128x0e+128x1o', 3), ('32x0e+32x1o', 2)])
+def test_radial_mlp_weight_stationary_c_abi(hidden, lmax):
+    """mh_mlp_fwd_ws (hidden activations into a slot-ordered scratch, then the output layer with each wave's 64-column
+    block of split weights held in registers over the tiles of its XCD's share, four waves sharing each tile through
+    LDS) against the single-kernel
+    mh_mlp_fwd_rows and against float64 (MLPSpec.apply): every listed row to fp32 accuracy, every unlisted row left
+    untouched (a NaN sentinel survives), on ragged counts and slot counts (0, 1, 15, 17 ... rows; tiles of 16), with
+    and without a row list, for output widths with whole and partial 64-column blocks (1280, 512, 224, 96)."""
+    dev = _dev()
+    model = factory.make_model(hidden, lmax, 2, elements=factory.ELEMENTS_PTCOH)
+    lib, P = _native.load(), _native.ptr
+    rng = np.random.default_rng(29)
+    for li, blk in enumerate(model.interactions):
+        op = HipRadialMLP(blk.conv_tp_weights, device=dev)
+        nw, hl = op.hs[-1], op.hs[-2]
+        for e, cnt in ((1, 1), (17, 15), (17, 0), (1000, 1000), (3001, 1777), (3001, None)):
+            print(f'[case] weight-stationary MLP forward {hidden} layer {li}: E={e} count={cnt} (NW={nw})', flush=True)
+            x = torch.tensor(rng.normal(size=(e, op.hs[0])), dtype=torch.float32, device=dev)
+            st = _native.stream_of(x)
+            if cnt is None:
+                rows = count = None
+                listed = np.arange(e)
+            else:
+                perm = rng.permutation(e).astype(np.int32)
+                rows = torch.tensor(perm, device=dev)
+                count = torch.tensor([cnt], dtype=torch.int32, device=dev)
+                listed = perm[:cnt]
+            got = torch.full((e, nw), float('nan'), device=dev)
+            old = torch.full((e, nw), float('nan'), device=dev)
+            h3 = torch.empty(e, hl, device=dev)
+            _native.check(lib.mh_mlp_fwd_ws(op.module.handle, P(x), P(op.WhT), P(op.Wo), P(h3), P(got), e, P(rows),
+                                            P(count), op.ncb, st), 'mlp_fwd_ws')
+            _native.check(lib.mh_mlp_fwd_rows(op.module.handle, P(x), P(op.WhT), P(op.WlT), P(old), e, P(rows),
+                                              P(count), st), 'mlp_fwd_rows')
+            torch.cuda.synchronize()
+            g, o = got.cpu().numpy(), old.cpu().numpy()
+            unl = np.setdiff1d(np.arange(e), listed)
+            assert np.isnan(g[unl]).all()
+            if len(listed):
+                want = op.spec.apply(x.double().cpu().numpy()[listed])
+                assert _rel(g[listed].astype(np.float64), want) < MLP_TOL
+                assert _rel(g[listed].astype(np.float64), o[listed].astype(np.float64)) < 2e-6
+    assert lib.mh_mlp_fwd_ws(op.module.handle, P(x), P(op.WhT), P(op.Wo), P(h3), P(got), 5, None, None, 0, st) != 0
+    assert b'ncb' in lib.mh_last_error()
+    assert lib.mh_mlp_fwd_ws(op.module.handle, P(x), P(op.WhT), None, P(h3), P(got), 5, None, None, 1, st) != 0
     assert b'NULL' in lib.mh_last_error()
 
 
