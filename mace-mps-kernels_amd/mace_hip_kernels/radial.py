@@ -248,9 +248,10 @@ def _source(spec, second):
     lds_fwd = max(Lo['tr_size'], Lo['chunk_fwd'])        # floats; a bf16 chunk of n elements takes n / 2 floats
     lds_bwd = max(Lo['nat_size'], Lo['chunk_bwd'])
     L = [_native.device_header(),
-         '__device__ __forceinline__ float mlp_sig(float z) { return 1.f / (1.f + expf(-z)); }',
-         '// the logistic function on the hardware exp2 and reciprocal (about 1e-7 relative error; -z large: rcp(inf) = 0)',
-         '__device__ __forceinline__ float mlp_sigf(float z) {',
+         '// the logistic function 1 / (1 + e^-z) on the hardware exp2 (e^-z = 2^(-z log2 e)) and reciprocal: within',
+         '// about 1e-7 of the exact value (z very negative: 1 + inf, whose reciprocal is 0), and about 5 instructions',
+         '// where expf and an IEEE division take about 25',
+         '__device__ __forceinline__ float mlp_sig(float z) {',
          '  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * z));',
          '}', '']
     if second:
@@ -328,7 +329,7 @@ def _source(spec, second):
                   for st in range(K0S)]
         return P
 
-    def hidden_fwd(transposed, keep, tiles, dual=False, keep_t=False, sig='mlp_sig'):
+    def hidden_fwd(transposed, keep, tiles, dual=False, keep_t=False):
         """z_i and h_i = c_i silu(z_i) for every hidden layer on the fp32 MFMA, A operands from LDS (transposed
         layout: one b128 read per 4 MFMAs; natural layout: b32 reads), each A operand used for every edge tile in
         ``tiles``.  ``dual``: also the tangents zt_i (the same A operands applied to the input tangent xv / the
@@ -371,7 +372,7 @@ def _source(spec, second):
                     for o in range(T):
                         for r in range(4):
                             P.append(f'  h{i}_{b}[{o}][{r}] = {_lit(spec.c[i])} * z{i}_{b}[{o}][{r}] * '
-                                     f'{sig}(z{i}_{b}[{o}][{r}]);')
+                                     f'mlp_sig(z{i}_{b}[{o}][{r}]);')
             if dual and (i < nh - 1 or keep_t):
                 for b in tiles:
                     P.append(f'  mh_f4 ht{i}_{b}[{T}];')
@@ -691,8 +692,7 @@ def _source(spec, second):
         L.extend(H + ['}', ''])
 
     def h3_kernel(name):
-        """mlp_h3: slot i < count (edge rows[i]): the last hidden activations (SiLU on the hardware exp2 and
-        reciprocal, within about 1e-7 of the exact activation), fp32, into h3 [E][HL] at row i with
+        """mlp_h3: slot i < count (edge rows[i]): the last hidden activations, fp32, into h3 [E][HL] at row i with
         the features in the output layer's K order (_kperm: position 32 s + 8 q + 4 t + r holds feature
         32 s + 16 t + 4 q + r, which is what lane group q holds after the last hidden layer: two float4 stores per K
         step of 32)."""
@@ -701,7 +701,7 @@ def _source(spec, second):
         H += skip_block(1, zero_rows=False)
         H += xin(range(1))                   # the row's features are loaded while the weights are staged
         H += stage('Wh', Lo['tr_size']) + ['  __syncthreads();']
-        H += hidden_fwd(True, True, range(1), sig='mlp_sigf')
+        H += hidden_fwd(True, True, range(1))
         H += ['  if (do0) {']
         H += [f'    *reinterpret_cast<mh_f4*>(h3 + ej0 * {HL} + {32 * st + 4 * tt} + 8 * q) = h{nh - 1}_0[{2 * st + tt}];'
               for st in range(S) for tt in range(2)]
@@ -779,7 +779,9 @@ def _source(spec, second):
               '      const long long tn = nx < Tx ? nx : tt;',
               '      const mh_f4 pn = piece(tn);',
               '      const int rn = erow(tn);',
-              '      // tile tt\'s piece, split exactly into three bf16 parts, into its fragments in LDS buffer buf',
+              '      // tile tt\'s piece, split exactly into three bf16 parts, into its fragments in LDS buffer buf; lane',
+              '      // (q, c16) of fragment (ks, p) sits at q * 16 + (c16 ^ (8 ks + 2 q)): each half-wave\'s 8-byte writes',
+              '      // then hit 64 different banks, and each wave\'s 16-byte reads of a fragment stay one 1 KB block',
               '      {',
               '        unsigned pk[3][2];',
               '#pragma unroll',
@@ -800,14 +802,14 @@ def _source(spec, second):
               '        }',
               '#pragma unroll',
               '        for (int p = 0; p < 3; ++p)',
-              '          *reinterpret_cast<uint2*>(&frag[buf][((pks * 3 + p) * 64 + pq * 16 + ps) * 8 + 4 * ph]) = '
-              'uint2{pk[p][0], pk[p][1]};',
+              '          *reinterpret_cast<uint2*>(&frag[buf][((pks * 3 + p) * 64 + pq * 16 + (ps ^ (8 * pks + 2 * pq))) * 8 + '
+              '4 * ph]) = uint2{pk[p][0], pk[p][1]};',
               '      }',
               '      __syncthreads();',
               '      if (act) {',
               f'        mh_bf8 b[{KS}][3];']
-        F += [f'        b[{ks}][{p}] = *reinterpret_cast<const mh_bf8*>(&frag[buf][(({ks} * 3 + {p}) * 64 + lane) * 8]);'
-              for ks in range(KS) for p in range(3)]
+        F += [f'        b[{ks}][{p}] = *reinterpret_cast<const mh_bf8*>(&frag[buf][(({ks} * 3 + {p}) * 64 + q * 16 + '
+              f'(c16 ^ ({8 * ks} + 2 * q))) * 8]);' for ks in range(KS) for p in range(3)]
         F += [f'        mh_f4 acc[{CT}];'] + [f'        acc[{ct}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};' for ct in range(CT)]
         for ks in range(KS):
             for pa, pb in PAIRS:
