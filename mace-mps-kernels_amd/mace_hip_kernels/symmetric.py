@@ -296,6 +296,13 @@ STAGE_NPW = 2          # nodes per wave: every coefficient read from LDS feeds S
 STAGE_ROWS = 64        # coefficient rows per LDS chunk; two chunks resident (double buffer)
 STAGE_FENCE = 64       # rows between anti-hoisting fences in the staged walk (0: none; spills)
 SLOT_GROUP = STAGE_WAVES * STAGE_NPW     # node slots per workgroup of the staged kernels
+# Split staged kernels (opt-in, HipSymmetricContraction.split): STAGE_SPLIT groups of STAGE_WAVES waves per
+# workgroup, each walking its own share of the polynomial (a contiguous range of the trie root's children, about equal
+# in rows, the first group also the root's own terms) for the same SLOT_GROUP slots, with its own LDS double buffer;
+# the groups' partial sums meet in LDS in group order.  Twice the waves for graphs with few nodes, but not faster on
+# MI355X at 2,533 nodes (2.5 waves per SIMD unsplit): SC1 forward 24.2 -> 26.4 us, backward 33.0 -> 35.9 us; the
+# staged walk is bound by instruction issue per SIMD, not by latency (one node per wave, twice the waves: 29.8 us).
+STAGE_SPLIT = 2
 
 
 def walk_rows(spec):
@@ -313,9 +320,53 @@ def walk_rows(spec):
     return out
 
 
-def stage_chunks(spec, cr=None):
+def _subtree_rows(node):
+    return sum(M for _, _, M in node['terms']) + sum(_subtree_rows(k) for k in node['kids'].values())
+
+
+def split_tries(spec, split):
+    """The prefix trie cut into ``split`` pseudo-tries that share no rows: the root's children (in index order) in
+    contiguous ranges of about equal row counts, the root's own terms in the first.  Walking each evaluates its
+    terms with the same prefix products as the whole trie."""
+    root = _trie(spec)
+    kids = sorted(root['kids'])
+    sizes = [_subtree_rows(root['kids'][i]) for i in kids]
+    total = sum(sizes) + sum(M for _, _, M in root['terms'])
+    parts, cur, acc = [[] for _ in range(split)], 0, sum(M for _, _, M in root['terms'])
+    for i, sz in zip(kids, sizes):
+        # move on to the next group once this one holds its share of the rows (never past the last group)
+        if cur < split - 1 and parts[cur] and acc + sz / 2 > total * (cur + 1) / split:
+            cur += 1
+        parts[cur].append(i)
+        acc += sz
+    return [{'terms': root['terms'] if g == 0 else [], 'kids': {i: root['kids'][i] for i in parts[g]}}
+            for g in range(split)]
+
+
+def _walk_order(node):
+    out = []
+
+    def rec(nd):
+        for _, r0, M in nd['terms']:
+            out.extend(range(r0, r0 + M))
+        for i in sorted(nd['kids']):
+            rec(nd['kids'][i])
+    rec(node)
+    return out
+
+
+def walk_rows_split(spec, split):
+    """Per group of the split staged kernels, the table rows in the order its walk reads them."""
+    return [_walk_order(t) for t in split_tries(spec, split)]
+
+
+def stage_chunks(spec, cr=None, split=1):
+    """LDS chunks of the staged walk (split > 1: of the longest group's walk, which every group's table is padded
+    to)."""
     cr = STAGE_ROWS if cr is None else cr
-    return -(-spec.nrows // cr)
+    if split == 1:
+        return -(-spec.nrows // cr)
+    return max(-(-len(r) // cr) for r in walk_rows_split(spec, split))
 
 
 def pack_staged(spec, cr=None):
@@ -334,6 +385,21 @@ def pack_staged(spec, cr=None):
     return np.ascontiguousarray(buf.transpose(0, 3, 1, 4, 2))  # [e][cb][quad][lane][row in quad]
 
 
+def pack_staged_split(spec, split=STAGE_SPLIT, cr=None):
+    """The table of the split staged kernels: per (element, 64-channel block) the groups' tables one after the
+    other, each in its walk order and zero-padded to the same number of chunks, in pack_staged's chunk layout:
+    [n_elem][ncb][split][chunks · cr / 4][64][4]."""
+    cr = STAGE_ROWS if cr is None else cr
+    T = spec.T.numpy()
+    ne, R, C = T.shape
+    RP = stage_chunks(spec, cr, split) * cr
+    buf = np.zeros((ne, split, RP, spec.ncb * WAVE), dtype=np.float32)
+    for g, rows in enumerate(walk_rows_split(spec, split)):
+        buf[:, g, :len(rows), :C] = T[:, rows, :]
+    buf = buf.reshape(ne, split, RP // 4, 4, spec.ncb, WAVE)  # [e][g][quad][row in quad][cb][lane]
+    return np.ascontiguousarray(buf.transpose(0, 4, 1, 2, 5, 3))  # [e][cb][g][quad][lane][row in quad]
+
+
 class _Stage:
     """Coefficient reads of a staged walk.  Walk position w (row ``walk_rows[w]``) is read from LDS buffer
     (w // cr) % 2; every fourth position loads the lane's next quad.  Entering chunk k >= 1 stores the staged
@@ -341,18 +407,20 @@ class _Stage:
     every wave finished before the last barrier, then waits at the workgroup barrier and issues the global loads of
     chunk k + 1."""
 
-    def __init__(self, spec, cr, fence):
-        self.pos = {r: w for w, r in enumerate(walk_rows(spec))}
-        self.cr, self.fence, self.nchunk = cr, fence, stage_chunks(spec, cr)
+    def __init__(self, spec, cr, fence, rows=None, sl='sl'):
+        rows = walk_rows(spec) if rows is None else rows
+        self.pos = {r: w for w, r in enumerate(rows)}
+        self.cr, self.fence, self.nchunk = cr, fence, -(-len(rows) // cr)
         self.nst = cr // 16                   # 16-byte staging registers per thread (256 threads per chunk copy)
         self.sb = cr // 4 * WAVE              # quads per chunk
+        self.sl = sl                          # the LDS double buffer's name
         self.next, self.since = 0, 0
 
     def copy_in(self, k, ind):
         return [f'{ind}sg{v} = src[{k * self.sb} + t + {256 * v}];' for v in range(self.nst)]
 
     def store(self, k, ind):
-        return [f'{ind}sl[{(k % 2) * self.sb} + t + {256 * v}] = sg{v};' for v in range(self.nst)]
+        return [f'{ind}{self.sl}[{(k % 2) * self.sb} + t + {256 * v}] = sg{v};' for v in range(self.nst)]
 
     def prologue(self, ind):
         L = [f'{ind}mh_f4 ' + ', '.join(f'sg{v}' for v in range(self.nst)) + ';', f'{ind}mh_f4 tq;']
@@ -378,7 +446,7 @@ class _Stage:
                 for ci, ch in enumerate(chunks):
                     ops = ', '.join([f'"+v"({v})' for v in ch] + (['"+v"(lo)'] if ci == len(chunks) - 1 else []))
                     L.append(f'{ind}asm volatile("" : {ops});')
-            L.append(f'{ind}tq = sl[{(k % 2) * self.sb + (w % self.cr) // 4 * WAVE} + lo];')
+            L.append(f'{ind}tq = {self.sl}[{(k % 2) * self.sb + (w % self.cr) // 4 * WAVE} + lo];')
         return f'tq[{w % 4}]'
 
 
@@ -518,6 +586,149 @@ def _source_staged(spec, irreps=False, npw=None, cr=None, fence=None):
         L.append('  }')
     L += ['}', '']
     return '\n'.join(L)
+
+
+def split_fits(spec, split=STAGE_SPLIT, npw=None, cr=None):
+    """Whether the split staged kernels can exchange their partial sums through one group's LDS double buffer (the
+    backward's n_ell and the forward's output components per node, per wave)."""
+    npw = STAGE_NPW if npw is None else npw
+    cr = STAGE_ROWS if cr is None else cr
+    nout = sum(bl['M'] for bl in spec.blocks)
+    return split > 1 and STAGE_WAVES * npw * max(spec.n_ell, nout) * WAVE <= 2 * (cr // 4 * WAVE) * 4
+
+
+def _source_staged_split(spec, irreps=False, split=STAGE_SPLIT, npw=None, cr=None, fence=None):
+    """HIP source of the split staged kernels ``sc_fwds2`` / ``sc_bwds2`` (``i`` suffix: e3nn's irreps layout).
+    Workgroup = ``split`` groups of STAGE_WAVES waves on the same SLOT_GROUP slots and 64-channel block; group g walks
+    its part of the polynomial (``split_tries``) with its coefficient rows streamed through its own LDS double
+    buffer, exactly as the unsplit kernel walks the whole (the same staging, fences and per-node expressions).  All
+    groups pass the same number of barriers (a group with fewer chunks waits at the rest); after one more, which
+    every wave reaches only when its walk is done, the groups past the first leave their partial sums (outputs, or
+    x-gradients) in their LDS buffer, and after another the first group adds them in group order and stores.
+    ``grp`` is read as a scalar, so every branch on it is uniform per wave."""
+    npw = STAGE_NPW if npw is None else npw
+    cr = STAGE_ROWS if cr is None else cr
+    fence = STAGE_FENCE if fence is None else fence
+    assert cr % 16 == 0 and split_fits(spec, split, npw, cr)
+    C, n = spec.C, spec.n_ell
+    sfx = 'i' if irreps else ''
+    slots = STAGE_WAVES * npw
+    comp = []
+    if irreps:
+        o = 0
+        for d in spec.dims:
+            comp += [(o, d, m) for m in range(d)]
+            o += d
+
+    def xidx(node, i, ch):
+        if not irreps:
+            return f'((size_t)({node}) * C + {ch}) * N_ELL + {i}'
+        ok, d, m = comp[i]
+        return f'(size_t)({node}) * (C * N_ELL) + {C * ok} + {ch} * {d} + {m}'
+    tries = split_tries(spec, split)
+    rows = [_walk_order(t) for t in tries]
+    nchunk = stage_chunks(spec, cr, split)
+    sb = cr // 4 * WAVE
+    outs = [(bi, m) for bi, bl in enumerate(spec.blocks) for m in range(bl['M'])]
+    L = [_native.device_header(),
+         f'#define C {C}', f'#define NCB {spec.ncb}', f'#define N_ELL {n}', f'#define OUT_DIM {spec.out_dim}',
+         f'#define SLOTS {slots}', f'#define CHUNK_QUADS {sb}', f'#define NCHUNK {nchunk}', f'#define SPLIT {split}']
+
+    def head(name, extra_args):
+        H = [f'extern "C" __global__ __launch_bounds__({split * STAGE_WAVES * WAVE}) void {spec.kname(name + sfx)}('
+             'const float* __restrict__ X,',
+             '    const int* __restrict__ slots, const int* __restrict__ elem, const float* __restrict__ TS,',
+             f'    {extra_args}, int N) {{',
+             '  __shared__ mh_f4 sl[SPLIT * 2 * CHUNK_QUADS];',
+             f'  const int grp = __builtin_amdgcn_readfirstlane((int)threadIdx.x / {STAGE_WAVES * WAVE});',
+             f'  const int t = (int)threadIdx.x & {STAGE_WAVES * WAVE - 1}, wv = t >> 6;   // thread, wave in the group',
+             '  int lo = t & 63;',
+             '  const int q0 = blockIdx.x * SLOTS;',
+             '  const int s0 = slots[q0];',
+             '  if (s0 < 0) return;                       // past the last group (uniform over the workgroup)',
+             '  const int c = blockIdx.y * 64 + lo;',
+             '  const bool active = c < C;',
+             '  const int cc = active ? c : C - 1;',
+             '  mh_f4* __restrict__ slg = sl + grp * (2 * CHUNK_QUADS);',
+             '  const mh_f4* __restrict__ src = reinterpret_cast<const mh_f4*>(TS) +',
+             '      ((size_t)(elem[s0] * NCB + blockIdx.y) * SPLIT + grp) * (NCHUNK * CHUNK_QUADS);']
+        for j in range(npw):
+            H += [f'  const int m{j} = slots[q0 + wv * {npw} + {j}];',
+                  f'  const int n{j} = m{j} >= 0 ? m{j} : s0;             // empty slot: compute on s0, store nothing']
+            H += [f'  const float x{j}_{i} = X[{xidx(f"n{j}", i, "cc")}];' for i in range(n)]
+        return H
+
+    def groups(walk, acc_names):
+        """Each group's staged walk in a uniform branch, padded to NCHUNK barriers; then the partials of the groups
+        past the first into their LDS buffers (acc_names: the per-node accumulators, lane-contiguous rows)."""
+        G = []
+        for g in range(split):
+            st = _Stage(spec, cr, fence, rows=rows[g], sl='slg')
+            G.append(f'  {"if" if g == 0 else "else if"} (grp == {g}) {{')
+            G += st.prologue('    ')
+            walk(tries[g], G, '    ', st)
+            G += ['    __syncthreads();                      // (the longest group\'s remaining chunk boundaries)'] * \
+                (nchunk - st.nchunk)
+            G.append('  }')
+        G += ['  __syncthreads();                          // every wave done with its group\'s chunks',
+              '  if (grp > 0) {',
+              '    float* __restrict__ pp = reinterpret_cast<float*>(slg);']
+        G += [f'    pp[{k * WAVE} + (wv * {len(acc_names)}) * {WAVE} + lo] = {a};' for k, a in enumerate(acc_names)]
+        G += ['  }', '  __syncthreads();', '  if (grp != 0) return;']
+        for g in range(1, split):
+            G.append(f'  {{ const float* __restrict__ pp = reinterpret_cast<const float*>(sl + {g} * 2 * CHUNK_QUADS);')
+            G += [f'    {a} += pp[{k * WAVE} + (wv * {len(acc_names)}) * {WAVE} + lo];' for k, a in enumerate(acc_names)]
+            G.append('  }')
+        return G
+
+    # forward
+    L += head('sc_fwds2', 'float* __restrict__ out')
+    accs = [f'a{j}_{bi}_{m}' for j in range(npw) for bi, m in outs]
+    L += [f'  float {a} = 0.0f;' for a in accs]
+    L += groups(lambda node, G, ind, st: _fwd_walk_s(spec, node, 0, G, ind, st, npw), accs)
+    for j in range(npw):
+        L.append(f'  if (active && m{j} >= 0) {{')
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'    out[(size_t)n{j} * OUT_DIM + {bl["out_off"]} + c * {M} + {m}] = a{j}_{bi}_{m};'
+                  for m in range(M)]
+        L.append('  }')
+    L += ['}', '']
+    # backward
+    L += head('sc_bwds2', 'const float* __restrict__ G, float* __restrict__ GX')
+    for j in range(npw):
+        L += [f'  float d{j}_{i} = 0.0f;' for i in range(n)]
+        for bi, bl in enumerate(spec.blocks):
+            M = bl['M']
+            L += [f'  const float g{j}_{bi}_{m} = G[(size_t)n{j} * OUT_DIM + {bl["out_off"]} + cc * {M} + {m}];'
+                  for m in range(M)]
+
+    def bwd_walk(node, G_, ind, st):
+        G_.append(f'{ind}' + ' '.join(f'float G{j}_0 = 0.0f;' for j in range(npw)))
+        _bwd_walk_s(spec, node, 0, G_, ind, st, npw)
+        G_.append(f'{ind}' + ' '.join(f'(void)G{j}_0;' for j in range(npw)))
+    L += groups(bwd_walk, [f'd{j}_{i}' for j in range(npw) for i in range(n)])
+    for j in range(npw):
+        L.append(f'  if (active && m{j} >= 0) {{')
+        L += [f'    GX[{xidx(f"n{j}", i, "c")}] = d{j}_{i};' for i in range(n)]
+        L.append('  }')
+    L += ['}', '']
+    return '\n'.join(L)
+
+
+def split_usable(spec, split=STAGE_SPLIT):
+    """Whether the split staged kernels serve this contraction: the partial sums fit the LDS buffers and every
+    group has rows to walk."""
+    return split_fits(spec, split, STAGE_NPW, STAGE_ROWS) and all(walk_rows_split(spec, split))
+
+
+def source_split(spec, split=STAGE_SPLIT):
+    """HIP source of the module of the split staged kernels (both layouts when the input irreps are known)."""
+    src = _source_staged_split(spec, split=split)
+    if spec.dims is not None:
+        alt = _source_staged_split(spec, irreps=True, split=split)
+        src += '\n' + alt[alt.index('#define SLOTS'):]
+    return src
 
 
 def _source_layout(spec, group=None, irreps=False, second=False):
@@ -754,14 +965,15 @@ def element_index(node_attrs):
 
 def _sc_fwd(op, layout, kind, x, elem, order, slots):
     """Launch the contraction on contiguous x in ``layout`` ('mace' [N, C, n_ell] or 'irreps' [N, C n_ell]) with
-    the kernel family ``kind`` ('node', 'grouped' or 'staged')."""
+    the kernel family ``kind`` ('node', 'grouped', 'staged' or 'staged2')."""
     N = x.shape[0]
     out = torch.empty(N, op.spec.out_dim, device=x.device, dtype=torch.float32)
     lib, P = _native.load(), _native.ptr
     st = _native.stream_of(x)
-    if kind == 'staged':
-        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_staged, op.module.handle, P(x), P(slots), slots.numel(),
-                       P(elem), P(op.TS), P(out), N, int(layout == 'irreps'), st)
+    if kind in ('staged', 'staged2'):
+        m, ts = op.split_module() if kind == 'staged2' else (op.module, op.TS)
+        _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_staged, m.handle, P(x), P(slots), slots.numel(),
+                       P(elem), P(ts), P(out), N, int(layout == 'irreps'), st)
     elif layout == 'irreps':
         _native.launch(f'sc_fwd[{op.tag}]', lib.mh_sc_fwd_irreps, op.module.handle, P(x), P(elem),
                        P(order) if kind == 'grouped' else None, P(op.T), P(out), N, st)
@@ -778,9 +990,10 @@ def _sc_bwd(op, layout, kind, x, elem, order, slots, g):
     gx = torch.empty_like(x)
     lib, P = _native.load(), _native.ptr
     st, N = _native.stream_of(x), x.shape[0]
-    if kind == 'staged':
-        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_staged, op.module.handle, P(x), P(slots), slots.numel(),
-                       P(elem), P(op.TS), P(g), P(gx), N, int(layout == 'irreps'), st)
+    if kind in ('staged', 'staged2'):
+        m, ts = op.split_module() if kind == 'staged2' else (op.module, op.TS)
+        _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_staged, m.handle, P(x), P(slots), slots.numel(),
+                       P(elem), P(ts), P(g), P(gx), N, int(layout == 'irreps'), st)
     elif layout == 'irreps':
         _native.launch(f'sc_bwd[{op.tag}]', lib.mh_sc_bwd_irreps, op.module.handle, P(x), P(elem),
                        P(order) if kind == 'grouped' else None, P(op.T), P(g), P(gx), N, st)
@@ -906,16 +1119,38 @@ class HipSymmetricContraction(torch.nn.Module):
                     _native.MH_SC_BWD_SI: (self.spec.kname('sc_bwdsi'), sw, SLOT_GROUP, ncb),
                 })
             self.module = _native.Module(code, kinds)
+        self.register_buffer('TS2', None)        # the split kernels' table (split_module)
+        self._split = None
         self.irreps_in, self.irreps_out = sc.irreps_in, sc.irreps_out
         self.original = [sc]
         self.tag = 'sc'               # name used in launch timings (patch_model sets the module path)
         self.grouped = None           # True / False: force the grouped / per-node global-memory kernels
         self.staged = None            # None: by size (kernel_family); True: force the LDS-staged kernels
+        self.split = None             # True: the split staged kernels (split_module) in place of the staged ones
         self.last_layout = None       # input layout of the last call: 'mace' [N, C, n_ell] or 'irreps'
         # a backward under create_graph=True: raise (the reference's behaviour) unless this is set, in which case
         # the gradient is differentiable once more through the second-order kernels (second_module)
         self.double_backward = False
         self._second = None
+
+    def split_module(self):
+        """The module of the split staged kernels (the same entry points and kinds as the staged ones, bound to
+        ``sc_fwds2`` / ``sc_bwds2``) and its table, compiled and packed on first use."""
+        if self._split is None:
+            s = self.spec
+            if not split_usable(s):
+                raise ValueError('mace_hip_kernels: the split staged kernels do not serve this contraction')
+            self.TS2 = torch.from_numpy(pack_staged_split(s)).to(self.T.device)
+            code = _native.compile_source(source_split(s))
+            sw, ncb = STAGE_SPLIT * STAGE_WAVES * WAVE, s.ncb
+            kinds = {_native.MH_SC_FWD_S: (s.kname('sc_fwds2'), sw, SLOT_GROUP, ncb),
+                     _native.MH_SC_BWD_S: (s.kname('sc_bwds2'), sw, SLOT_GROUP, ncb)}
+            if s.dims is not None:
+                kinds.update({_native.MH_SC_FWD_SI: (s.kname('sc_fwds2i'), sw, SLOT_GROUP, ncb),
+                              _native.MH_SC_BWD_SI: (s.kname('sc_bwds2i'), sw, SLOT_GROUP, ncb)})
+            with torch.cuda.device(self.T.device):
+                self._split = _native.Module(code, kinds)
+        return self._split, self.TS2
 
     def second_module(self):
         """The module of the second-order kernels (``sc_jvp``, ``sc_bwd2``), compiled on first use."""
@@ -944,9 +1179,12 @@ class HipSymmetricContraction(torch.nn.Module):
         return waves >= 4 * _SIMDS[key]
 
     def kernel_family(self, n_nodes, device):
-        """'staged' (coefficient rows through LDS, SLOT_GROUP nodes of one element per workgroup), 'grouped' or
-        'node' (coefficients from global memory): ``staged`` / ``grouped`` force a family (``staged`` False: the
-        global-memory family that ``use_grouped`` picks), else the staged kernels."""
+        """'staged' (coefficient rows through LDS, SLOT_GROUP nodes of one element per workgroup), 'staged2' (the
+        same split over two groups of waves), 'grouped' or 'node' (coefficients from global memory): ``split`` /
+        ``staged`` / ``grouped`` force a family (``staged`` False: the global-memory family that ``use_grouped``
+        picks), else the staged kernels."""
+        if self.split:
+            return 'staged2'
         if self.staged:
             return 'staged'
         if self.grouped is not None:
@@ -959,7 +1197,7 @@ class HipSymmetricContraction(torch.nn.Module):
         if y.shape != (x.shape[0], self.spec.n_elem):
             raise ValueError(f'node_attrs must be [{x.shape[0]}, {self.spec.n_elem}], got {tuple(y.shape)}')
         elem, order = element_order(y)
-        slots = group_slots(y) if self.kernel_family(x.shape[0], x.device) == 'staged' else None
+        slots = group_slots(y) if self.kernel_family(x.shape[0], x.device) in ('staged', 'staged2') else None
         src = getattr(x, 'irreps_source', None)
         if src is not None and self.spec.dims is not None and src(self.spec.dims) is not None:
             # x is MACE's reshape_irreps of a tensor in e3nn's layout, not yet formed: read that tensor directly

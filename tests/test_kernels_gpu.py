@@ -419,12 +419,13 @@ def test_conv_deterministic_and_empty():
 SC_MODELS = [('32x0e+32x1o', 2, 2), ('128x0e+128x1o', 3, 3), ('64x0e', 2, 2), ('128x0e+128x1o+128x2e', 3, 3)]
 
 
-SC_FAMILIES = ['node', 'grouped', 'staged']
+SC_FAMILIES = ['node', 'grouped', 'staged', 'staged2']
 
 
 def _family(op, fam):
     """Force a kernel family of a HipSymmetricContraction."""
-    op.staged, op.grouped = (True, None) if fam == 'staged' else (False, fam == 'grouped')
+    op.split = fam == 'staged2'
+    op.staged, op.grouped = (True, None) if fam.startswith('staged') else (False, fam == 'grouped')
     return op
 
 
@@ -433,7 +434,8 @@ def _family(op, fam):
 def test_sc_fwd_bwd_vs_oracle(hidden, lmax, corr, family):
     """Every kernel family: one node per workgroup; element-grouped (GROUP nodes per workgroup, mixed groups at
     element boundaries, a partial last group); LDS-staged (SLOT_GROUP slots of one element per workgroup, padded
-    element runs, coefficient rows through LDS in chunks)."""
+    element runs, coefficient rows through LDS in chunks); the split LDS-staged kernels (the same with two groups of
+    waves per workgroup, each walking part of the polynomial)."""
     dev = _dev()
     model = factory.make_model(hidden, lmax, corr, elements=factory.ELEMENTS_PTCOH)
     rng = np.random.default_rng(4)
@@ -545,10 +547,10 @@ def test_sc_grouped_matches_per_node():
 
 @pytest.mark.parametrize('layout', [0, 1])
 def test_sc_staged_matches_per_node(layout):
-    """The LDS-staged kernels (mh_sc_fwd_staged / mh_sc_bwd_staged) against the per-node ones through the C ABI:
-    element runs of every length mod SLOT_GROUP (a single-node element, a run of exactly SLOT_GROUP, a long run
-    with a partial last group), an element with no nodes, both layouts, and slots from group_slots; then a second,
-    smaller call on the same module."""
+    """The LDS-staged kernels (mh_sc_fwd_staged / mh_sc_bwd_staged), unsplit and split, against the per-node ones
+    through the C ABI: element runs of every length mod SLOT_GROUP (a single-node element, a run of exactly
+    SLOT_GROUP, a long run with a partial last group), an element with no nodes, both layouts, and slots from
+    group_slots; then a second, smaller call on the same module."""
     from mace_hip_kernels import symmetric as hsym
     dev = _dev()
     model = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
@@ -579,14 +581,16 @@ def test_sc_staged_matches_per_node(layout):
                           lib.mh_sc_fwd(h, P(X), P(elem), P(op.T), P(out1), n, st), 'sc_fwd')
             _native.check(lib.mh_sc_bwd_irreps(h, P(Xl), P(elem), None, P(op.T), P(G), P(gx1), n, st) if layout else
                           lib.mh_sc_bwd(h, P(X), P(elem), P(op.T), P(G), P(gx1), n, st), 'sc_bwd')
-            out2, gx2 = torch.full_like(out1, float('nan')), torch.full_like(gx1, float('nan'))
-            _native.check(lib.mh_sc_fwd_staged(h, P(Xl), P(slots), slots.numel(), P(elem), P(op.TS), P(out2), n,
-                                               layout, st), 'sc_fwd_staged')
-            _native.check(lib.mh_sc_bwd_staged(h, P(Xl), P(slots), slots.numel(), P(elem), P(op.TS), P(G), P(gx2),
-                                               n, layout, st), 'sc_bwd_staged')
-            torch.cuda.synchronize()
-            assert _rel(out2.double().cpu().numpy(), out1.double().cpu().numpy()) < 1e-6
-            assert _rel(gx2.double().cpu().numpy(), gx1.double().cpu().numpy()) < 1e-6
+            ms, TS2 = op.split_module()
+            for hs, TS in ((h, op.TS), (ms.handle, TS2)):
+                out2, gx2 = torch.full_like(out1, float('nan')), torch.full_like(gx1, float('nan'))
+                _native.check(lib.mh_sc_fwd_staged(hs, P(Xl), P(slots), slots.numel(), P(elem), P(TS), P(out2), n,
+                                                   layout, st), 'sc_fwd_staged')
+                _native.check(lib.mh_sc_bwd_staged(hs, P(Xl), P(slots), slots.numel(), P(elem), P(TS), P(G),
+                                                   P(gx2), n, layout, st), 'sc_bwd_staged')
+                torch.cuda.synchronize()
+                assert _rel(out2.double().cpu().numpy(), out1.double().cpu().numpy()) < 1e-6
+                assert _rel(gx2.double().cpu().numpy(), gx1.double().cpu().numpy()) < 1e-6
         bad = lib.mh_sc_fwd_staged(h, P(Xl), P(slots), slots.numel() - 1, P(elem), P(op.TS), P(out2), n, layout, st)
         assert bad != 0 and b'multiple' in lib.mh_last_error()
 

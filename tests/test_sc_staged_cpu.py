@@ -38,18 +38,22 @@ static thread_local mh_dim3 threadIdx;
 static mh_dim3 blockIdx, gridDim;
 static std::barrier<>* g_bar;
 static inline void __syncthreads() { g_bar->arrive_and_wait(); }
+static inline int __builtin_amdgcn_readfirstlane(int v) { return v; }
 typedef float mh_f4 __attribute__((vector_size(16)));
 """
 
 
-def _cpu_library(spec, tmp_path, npw, cr):
-    src = hsym._source_staged(spec, npw=npw, cr=cr)
+def _cpu_library(spec, tmp_path, npw, cr, split=1):
+    gen = (lambda **kw: hsym._source_staged_split(spec, split=split, **kw)) if split > 1 else \
+        (lambda **kw: hsym._source_staged(spec, **kw))
+    src = gen(npw=npw, cr=cr)
     if spec.dims is not None:
-        alt = hsym._source_staged(spec, irreps=True, npw=npw, cr=cr)
+        alt = gen(irreps=True, npw=npw, cr=cr)
         src += '\n' + alt[alt.index('#define SLOTS'):]
     src = src[src.index('#define C '):]
     src = '\n'.join(l for l in src.split('\n') if 'asm volatile' not in l)
-    names = re.findall(r'void (sc_(?:fwds|bwds)i?_\w+)\(', src)
+    names = re.findall(r'void (sc_(?:fwds|bwds)2?i?_\w+)\(', src)
+    nthr = split * hsym.STAGE_WAVES * hsym.WAVE
     drivers = []
     for k in names:
         bwd = k.startswith('sc_bwds')
@@ -60,19 +64,20 @@ def _cpu_library(spec, tmp_path, npw, cr):
             f'extern "C" void run_{k}({params}, int nslots) {{\n'
             f'  for (int bx = 0; bx < nslots / SLOTS; ++bx) for (int by = 0; by < NCB; ++by) {{\n'
             f'    blockIdx.x = bx; blockIdx.y = by;\n'
-            f'    std::barrier<> bar({hsym.STAGE_WAVES * hsym.WAVE}); g_bar = &bar;\n'
+            f'    std::barrier<> bar({nthr}); g_bar = &bar;\n'
             f'    std::vector<std::thread> th;\n'
-            f'    for (int t = 0; t < {hsym.STAGE_WAVES * hsym.WAVE}; ++t)\n'
+            f'    for (int t = 0; t < {nthr}; ++t)\n'
             f'      th.emplace_back([=] {{ threadIdx.x = t; {k}({args}); }});\n'
             f'    for (auto& h : th) h.join();\n'
             f'  }}\n}}')
-    c = tmp_path / f'scs_{npw}_{cr}.cpp'
-    so = tmp_path / f'scs_{npw}_{cr}.so'
+    c = tmp_path / f'scs_{npw}_{cr}_{split}.cpp'
+    so = tmp_path / f'scs_{npw}_{cr}_{split}.so'
     c.write_text(SHIM + src + '\n' + '\n'.join(drivers))
     subprocess.run(['g++', '-O1', '-std=c++20', '-shared', '-fPIC', '-pthread', '-w', str(c), '-o', str(so)],
                    check=True)
     lib = ctypes.CDLL(str(so))
-    return lib, {('bwd' if k.startswith('sc_bwds') else 'fwd', 'i_c' in k): getattr(lib, f'run_{k}') for k in names}
+    return lib, {('bwd' if k.startswith('sc_bwds') else 'fwd', bool(re.match(r'sc_(fwd|bwd)s2?i_', k))):
+                 getattr(lib, f'run_{k}') for k in names}
 
 
 def _fp(a):
@@ -139,14 +144,22 @@ def test_pack_staged_layout():
 
 
 @pytest.mark.skipif(shutil.which('g++') is None, reason='needs g++')
-@pytest.mark.parametrize('hidden,lmax,corr,npw,cr', [('16x0e+16x1o', 2, 3, 2, 64), ('16x0e+16x1o', 2, 3, 1, 16),
-                                                     ('16x0e+16x1o+16x2e', 3, 2, 2, 32)])
-def test_staged_kernels_vs_oracle(hidden, lmax, corr, npw, cr, tmp_path):
+@pytest.mark.parametrize('hidden,lmax,corr,npw,cr,split', [('16x0e+16x1o', 2, 3, 2, 64, 1),
+                                                           ('16x0e+16x1o', 2, 3, 1, 16, 1),
+                                                           ('16x0e+16x1o+16x2e', 3, 2, 2, 32, 1),
+                                                           ('16x0e+16x1o', 2, 3, 2, 64, 2),
+                                                           ('16x0e+16x1o+16x2e', 3, 2, 2, 64, 2)])
+def test_staged_kernels_vs_oracle(hidden, lmax, corr, npw, cr, split, tmp_path):
+    """split > 1: the split kernels, whose wave groups walk disjoint parts of the polynomial with their own LDS
+    buffers, barrier counts padded to the longest group, and partial sums combined through LDS."""
     model = factory.make_model(hidden, lmax, corr, elements=factory.ELEMENTS_PTCOH)
     sc = model.products[0].symmetric_contractions
     spec = hsym.SCSpec(sc)
     assert hsym.stage_chunks(spec, cr) > 2                 # several chunk transitions
-    lib, fns = _cpu_library(spec, tmp_path, npw, cr)
+    if split > 1:                                           # several chunks per group
+        nch = [-(-len(r) // cr) for r in hsym.walk_rows_split(spec, split)]
+        assert min(nch) >= 2, nch
+    lib, fns = _cpu_library(spec, tmp_path, npw, cr, split)
     assert set(fns) == {('fwd', False), ('bwd', False), ('fwd', True), ('bwd', True)}
     rng = np.random.default_rng(5)
     gs = hsym.STAGE_WAVES * npw
@@ -162,7 +175,7 @@ def test_staged_kernels_vs_oracle(hidden, lmax, corr, npw, cr, tmp_path):
         want_gx += osc.poly_grad(tab, x, elem, g[:, off:off + C * M].reshape(n, C, M))
         off += C * M
     want_out = np.concatenate(want_out, axis=1)
-    TS = hsym.pack_staged(spec, cr)
+    TS = hsym.pack_staged(spec, cr) if split == 1 else hsym.pack_staged_split(spec, split, cr)
     el = elem.astype(np.int32)
     gf = g.astype(np.float32)
     slots = _slots_reference(elem, 4, gs)

@@ -94,9 +94,9 @@ def test_conv_factored_matches_plain_full_size(cfg4):
 
 
 def test_sc_families_match_per_node_full_size(cfg4):
-    """The three symmetric-contraction families at N = 20,000: the LDS-staged kernels (what the patched model
-    launches at this size) and the element-grouped ones against one node per workgroup (itself against the oracle
-    at small sizes), outputs and input gradients."""
+    """The four symmetric-contraction families at N = 20,000: the LDS-staged kernels (what the patched model
+    launches at this size), the split LDS-staged ones and the element-grouped ones against one node per workgroup
+    (itself against the oracle at small sizes), outputs and input gradients."""
     model, batch, meta = cfg4
     dev = torch.device('cuda:0')
     N = batch['positions'].shape[0]
@@ -109,15 +109,15 @@ def test_sc_families_match_per_node_full_size(cfg4):
         x = (0.5 * torch.randn(N, op.spec.C, op.spec.n_ell, generator=gen)).to(dev).requires_grad_(True)
         g = torch.randn(N, op.spec.out_dim, generator=gen).to(dev)
         got = {}
-        for fam, (staged, grouped) in (('staged', (True, None)), ('grouped', (False, True)),
-                                       ('node', (False, False))):
+        for fam, (staged, grouped, split) in (('staged', (True, None, None)), ('staged2', (None, None, True)),
+                                              ('grouped', (False, True, None)), ('node', (False, False, None))):
             print(f'[case] config 4 symmetric contraction {li}: {fam} kernels', flush=True)
-            op.staged, op.grouped = staged, grouped
+            op.staged, op.grouped, op.split = staged, grouped, split
             assert op.kernel_family(N, dev) == fam
             out = op(x, attrs)
             got[fam] = (out.detach(), torch.autograd.grad(out, x, g)[0])
             del out
-        for fam in ('staged', 'grouped'):
+        for fam in ('staged', 'staged2', 'grouped'):
             for u, v in zip(got[fam], got['node']):
                 assert _rel(u, v) < 1e-5, fam
 
