@@ -319,15 +319,18 @@ int mh_graph_build_noalloc(mh_module* m, const int64_t* edge_index, int64_t E, i
 
 /* Neighbour list of a batch of B structures (atoms ptr[b] .. ptr[b + 1] of pos [N, 3] float64, cell [B, 3, 3]
  * float64 with the lattice vectors as rows, pbc [B, 3] int32): every (sender i, receiver j, unit shift o) with
- * |pos[j] + o cell - pos[i]| < r_max (float64, no fused multiply-add), o over the translations ceil(r_max / h_k)
- * deep along each periodic direction (h_k the spacing of lattice planes k), without (i, i, 0); ordered by sender,
+ * |pos[j] + o cell - pos[i]| < r_max (float64, no fused multiply-add), o over the translations
+ * max(ceil(r_max / h_k), floor(r_max / h_k + s_k)) deep along each periodic direction (h_k the spacing of lattice
+ * planes k, s_k the span of the structure's fractional coordinates along k, so atoms outside the cell keep every
+ * edge; at most 64 deep), without (i, i, 0); ordered by sender,
  * then receiver, then o (lexicographic).  e_pad > 0: structure b's edges fill [b e_pad, (b + 1) e_pad) (e_total =
  * B e_pad), each sender's real edges followed by its share of padding edges (self-loops with unit shift (0, 0, kz),
  * kz = ceil((r_max + 1) / |c_2|), spread round-robin over the structure's atoms); a structure with more edges fills
  * its e_pad slots with e_pad of them.  e_pad == 0: the edges back to back, e_total their number.  Outputs: edge_index [2, e_total]
  * int64 (row 0 senders, row 1 receivers), unit_shifts and shifts (= unit_shifts cell) [e_total, 3] as float64
  * (out_f64) or float32, n_edges [B] int32 = each structure's real edge count (above e_pad when it overflowed; -1
- * when it needs padding and cannot have any: no atoms, or c_2 = 0; its slots then hold zero-length self-loops).
+ * when it needs padding and cannot have any: no atoms, or c_2 = 0, its slots then holding zero-length self-loops;
+ * -1 also when the image search was cut at 64 translations, atoms spread over more than 64 cells).
  * edge_index NULL: only n_edges (size the exact layout with it, then call again).  work: caller-owned device scratch
  * of mh_neighbour_list_work_size(B, N, e_total) bytes.  Device work only (no host synchronisation, no memset), so a
  * padded build can be captured in a HIP graph; deterministic.  Bind MH_NL_SETUP with 256 threads and rows_per_block
