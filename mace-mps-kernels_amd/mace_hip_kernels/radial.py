@@ -61,9 +61,15 @@ TPAD = 8             # and of their transposed layout (16-byte reads, rows of 64
 TPAD0 = 4            # the first layer's transposed rows (K = the padded input width, scalar reads: 8 + 4 words)
 # Waves per SIMD the forward and backward are compiled for (amdgpu_waves_per_eu; None: the compiler's choice).
 # Left to itself the compiler gives mlp_fwd 172 VGPRs + 48 AGPRs (2 waves per SIMD); asked for 3 it fits in 138
-# VGPRs without spills, mlp_bwd in 154.
+# VGPRs without spills, mlp_bwd in 168 (three VGPRs spilled).  mlp_bwd measured (config 2, layer 2 / layer 1, us in
+# the E+F call): 2 waves 158.3 / 78.4, 3 waves 144.0 / 72.4, 4 waves (128 VGPRs, no spills) 147.5 / 71.9.
 WAVES_FWD = 3
 WAVES_BWD = 3
+# Waves per workgroup of the first-order backward (16 edges each).  The workgroup streams the whole split output layer
+# through LDS, so more waves would amortise that staging over more edges, but every chunk's barrier then waits for
+# more waves: config 2, layer 2 / layer 1 in the E+F call, 4 waves 143.6 / 72.6 us, 6 waves 157.6 / 84.2, 8 waves
+# 172.1 / 84.0.
+WG_WAVES_BWD = 4
 # The forward as two kernels (mh_mlp_fwd_ws): the hidden layers of the listed rows into an [E, HL] scratch (mlp_h3),
 # then the output layer weight-stationary (mlp_out): a persistent grid whose waves each keep one block of WS_COLS
 # output columns of the split output layer in registers and walk the 16-edge tiles of their XCD's share, four waves
@@ -382,7 +388,7 @@ def _source(spec, second):
                                      f'zt{i}_{b}[{o}][{r}];')
         return P
 
-    def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None, reg='pre'):
+    def chunk_io(src, nx_elems, row_elems, rs, nrows, ind, store_base=None, reg='pre', nthreads=BLOCK):
         """Load (store_base None) or store this thread's 16-byte pieces of a bf16 chunk: piece f is part p, 8-element
         group c8, row rr of a [3][row_elems / 8][nrows][8] block at element offset nx_elems of ``src`` (rows
         innermost, so the eight lanes of one LDS write phase hit eight different rows: conflict-free for any row
@@ -390,19 +396,19 @@ def _source(spec, second):
         per_row = row_elems // 8
         total = NSPLIT * nrows * per_row
         P = []
-        for it in range(-(-total // BLOCK)):
-            exact = (it + 1) * BLOCK <= total
-            fx = f't + {it * BLOCK}' if exact else f'min(t + {it * BLOCK}, {total - 1})'
+        for it in range(-(-total // nthreads)):
+            exact = (it + 1) * nthreads <= total
+            fx = f't + {it * nthreads}' if exact else f'min(t + {it * nthreads}, {total - 1})'
             idx = [f'{ind}{{ const int f = {fx}, p = f / {nrows * per_row}, rem = f - p * {nrows * per_row},',
                    f'{ind}      c8 = rem / {nrows}, rr = rem - c8 * {nrows};']
             if store_base is None:
                 P += idx + [f'{ind}  {reg}{it} = *reinterpret_cast<const mh_u4*>({src} + (size_t){nx_elems} + '
                             f'(size_t)f * 8); }}']
             else:
-                guard = '' if exact else f'if (t + {it * BLOCK} < {total}) '
+                guard = '' if exact else f'if (t + {it * nthreads} < {total}) '
                 P += idx + [f'{ind}  {guard}*reinterpret_cast<mh_u4*>(&ldsb[{store_base} + p * {nrows * rs} + rr * {rs} + '
                             f'8 * c8]) = {reg}{it}; }}']
-        return P, -(-total // BLOCK)
+        return P, -(-total // nthreads)
 
     PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
 
@@ -562,15 +568,18 @@ def _source(spec, second):
         KS = CH // 32                                        # bf16 K steps per chunk
         NCHK = -(-NW // CH)
         TAIL = NW % CH != 0
+        wg = BLOCK // 64 if dual else WG_WAVES_BWD           # waves per workgroup
+        nt = 64 * wg
         B = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if dual else '') +
                  'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, const float* __restrict__ gW, '
-                 'float* __restrict__ gef, long long E', lds_bwd, nb, indexed=not dual, wpe=None if dual else WAVES_BWD)
+                 'float* __restrict__ gef, long long E', lds_bwd, nb, waves=wg, indexed=not dual,
+                 wpe=None if dual else WAVES_BWD)
         if not dual:
-            B += skip_block(nb, zero_rows=True)
+            B += skip_block(nb, zero_rows=True, waves=wg)
         for b in range(nb):
             B += [f'  mh_f4 dh{b}[{TL}][{ncb}];'] + [f'  dh{b}[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};'
                                                     for o in range(TL) for j in range(ncb)]
-        ld0, npre = chunk_io('Wl', 0, CH, RSB, HL, '  ')
+        ld0, npre = chunk_io('Wl', 0, CH, RSB, HL, '  ', nthreads=nt)
         B += [f'  mh_u4 {", ".join(f"pre{i}" for i in range(npre))};'] + ld0
         # columns past NW (the zero-padded tail of the last chunk) read a valid column and are zeroed
         gcol = (lambda c: f'min({c} + 8 * q, {NW - 8})') if TAIL else (lambda c: f'{c} + 8 * q')
@@ -587,13 +596,13 @@ def _source(spec, second):
         for b in range(nb):
             for d in range(GW_DIST):
                 B += gload(f'g{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
-        st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0')
+        st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0', nthreads=nt)
         B += st0 + ['  __syncthreads();']
         B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
               f'    const int base = (ch & 1) * {Lo["chunk_bwd"]}, nbase = {Lo["chunk_bwd"]} - base;',
               f'    const int nc = min(ch + 1, {NCHK - 1});',
               f'    const size_t nx = (size_t)nc * {NSPLIT * HL * CH};']
-        ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ')
+        ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ', nthreads=nt)
         B += ldn
         B += [f'    const int gc = min(ch + {GW_DIST}, {NCHK - 1}) * {CH};']
         for b in range(nb):
@@ -623,14 +632,14 @@ def _source(spec, second):
                     for d in range(GW_DIST - 1):
                         B += [f'    g{d}_{ks}_{h}_{b} = g{d + 1}_{ks}_{h}_{b};']
                     B += [f'    g{GW_DIST - 1}_{ks}_{h}_{b} = gn_{ks}_{h}_{b};']
-        stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase')
+        stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase', nthreads=nt)
         B += stn + ['    __syncthreads();', '  }']
         for b in range(nb):
             B += [f'  mh_f4 dhs_{b}[{TL}];'] + [f'  dhs_{b}[{o}] = ' + ' + '.join(f'dh{b}[{o}][{j}]' for j in range(ncb)) + ';'
                                                for o in range(TL)]
         # the hidden layers recomputed and walked back HIDDEN_TILES_BWD edge tiles at a time (each group in a scope of
         # its own, so the registers of its activations are free for the next)
-        B += stage('Wh', Lo['nat_size']) + ['  __syncthreads();']
+        B += stage('Wh', Lo['nat_size'], nthreads=nt) + ['  __syncthreads();']
         for g0 in range(0, nb, HIDDEN_TILES_BWD):
             grp = range(g0, min(nb, g0 + HIDDEN_TILES_BWD))
             B += ['  {'] + xin(grp)
@@ -995,7 +1004,7 @@ class HipRadialMLP(torch.nn.Module):
         with torch.cuda.device(dev):
             self.module = _native.Module(code, {
                 _native.MH_MLP_FWD: (self.spec.kname('mlp_fwd'), BLOCK, 64 * NB_FWD),
-                _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), BLOCK, 64 * NB_BWD),
+                _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), 64 * WG_WAVES_BWD, 16 * NB_BWD * WG_WAVES_BWD),
                 _native.MH_MLP_HID: (self.spec.kname('mlp_hid'), BLOCK, 64 * NB_FWD),
                 _native.MH_MLP_HIDB: (self.spec.kname('mlp_hidb'), BLOCK, 64 * NB_BWD),
                 _native.MH_MLP_H3: (self.spec.kname('mlp_h3'), BLOCK, 64),
