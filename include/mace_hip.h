@@ -111,7 +111,9 @@ enum mh_kernel_kind {
     MH_CONV_FWD_CR = 72, /* conv fwd, W0 * cutoff with W0 rows through a row map (cacheable loads)     */
     MH_MLP_H3 = 73,      /* radial MLP: last hidden activations of the listed rows, h3 [slot][HL]       */
     MH_MLP_OUT = 74,     /* its output layer, weight-stationary: persistent waves over 16-edge tiles    */
-    MH_NUM_KINDS = 75
+    MH_EDGE_FWD = 75,    /* edge geometry, spherical harmonics and radial embedding in one pass          */
+    MH_EDGE_BWD = 76,    /* the harmonics' and the embedding's backward in one pass                      */
+    MH_NUM_KINDS = 77
 };
 
 /* flags of mh_conv_bwd */
@@ -556,6 +558,16 @@ int mh_conv_bwd_mlp(mh_module* m, const float* x, const float* g, const float* Y
 int mh_emb_fwd(mh_module* m, const float* len, float* feats, float* cutoff, int64_t E, void* stream);
 int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float* gcutoff, float* glen, int64_t E,
                void* stream);
+/* The edge geometry, the spherical harmonics and the radial embedding of the same edges in one pass (a module
+ * generated by edgefeat.source(SHSpec, EmbSpec); bind MH_EDGE_FWD and MH_EDGE_BWD with 256 threads and 256 edges per
+ * block).  mh_edge_fwd writes what mh_geom_fwd, then mh_sh_fwd on its vectors and mh_emb_fwd on its lengths would:
+ * vec [E, 3], len [E], Y [E, DIM], feats [E, n], cutoff [E].  mh_edge_bwd writes what mh_sh_bwd and mh_emb_bwd would:
+ * gvec [E, 3] = (dY/dv)^T gY and glen [E] = dL/dlen from gfeats [E, n] and gcutoff [E] (gcutoff NULL: none).  No
+ * reference counterpart (these modules stay on e3nn / MACE there). */
+int mh_edge_fwd(mh_module* m, const float* pos, const int32_t* send, const int32_t* recv, const float* shifts,
+                float* vec, float* len, float* Y, float* feats, float* cutoff, int64_t E, void* stream);
+int mh_edge_bwd(mh_module* m, const float* vec, const float* len, const float* gY, const float* gfeats,
+                const float* gcutoff, float* gvec, float* glen, int64_t E, void* stream);
 
 /* Per-node permutation of N rows from e3nn's irreps layout (block l at off_l, index off_l + u (2l+1) + m) to
  * [mul, sum_l (2l+1)] (index u D + o_l + m), the block table compiled into the module; mh_perm_bwd applies the inverse

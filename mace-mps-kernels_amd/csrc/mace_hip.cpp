@@ -139,7 +139,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 37; }
+int mh_version(void) { return 38; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -932,6 +932,21 @@ int mh_emb_bwd(mh_module* m, const float* len, const float* gfeats, const float*
     if (E > 0 && (!len || !gfeats || !glen)) return fail(-1, "mh_emb_bwd: NULL len, gfeats or glen");
     void* args[] = {&len, &gfeats, &gcutoff, &glen, &E};
     return launch(m, MH_EMB_BWD, E, args, stream, "mh_emb_bwd");
+}
+
+int mh_edge_fwd(mh_module* m, const float* pos, const int32_t* send, const int32_t* recv, const float* shifts,
+                float* vec, float* len, float* Y, float* feats, float* cutoff, int64_t E, void* stream) {
+    if (E > 0 && (!pos || !send || !recv || !shifts || !vec || !len || !Y || !feats || !cutoff))
+        return fail(-1, "mh_edge_fwd: NULL operand");
+    void* args[] = {&pos, &send, &recv, &shifts, &vec, &len, &Y, &feats, &cutoff, &E};
+    return launch(m, MH_EDGE_FWD, E, args, stream, "mh_edge_fwd");
+}
+
+int mh_edge_bwd(mh_module* m, const float* vec, const float* len, const float* gY, const float* gfeats,
+                const float* gcutoff, float* gvec, float* glen, int64_t E, void* stream) {
+    if (E > 0 && (!vec || !len || !gY || !gfeats || !gvec || !glen)) return fail(-1, "mh_edge_bwd: NULL operand");
+    void* args[] = {&vec, &len, &gY, &gfeats, &gcutoff, &gvec, &glen, &E};
+    return launch(m, MH_EDGE_BWD, E, args, stream, "mh_edge_bwd");
 }
 
 int mh_perm_fwd(mh_module* m, const float* x, float* y, int32_t N, void* stream) {

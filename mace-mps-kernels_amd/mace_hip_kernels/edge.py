@@ -308,4 +308,6 @@ class HipSphericalHarmonics(torch.nn.Module):
         return self._second
 
     def forward(self, vec):
-        return _SHFn.apply(vec, self)
+        from . import edgefeat
+        Y = edgefeat.take_harmonics(self, vec)      # made in the geometry's pass (edgefeat), if it was
+        return Y if Y is not None else _SHFn.apply(vec, self)

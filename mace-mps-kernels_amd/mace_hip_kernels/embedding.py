@@ -263,7 +263,9 @@ class HipRadialEmbedding(torch.nn.Module):
         return self._second
 
     def forward(self, edge_lengths, *args, **kwargs):
-        feats, cut = _EmbFn.apply(edge_lengths, self)
+        from . import edgefeat
+        made = edgefeat.take_embedding(self, edge_lengths)     # made in the geometry's pass (edgefeat), if it was
+        feats, cut = made if made is not None else _EmbFn.apply(edge_lengths, self)
         # The cutoff is -0.0 exactly where r >= r_max (outside the envelope's support, where its derivative is zero)
         # and nonzero or +0.0 elsewhere; a patched convolution that receives this tensor unmodified (same version)
         # skips such edges in its backward (MH_CUT_MASKED).

@@ -41,6 +41,8 @@ BLOCK = 256
 _ACTIVE = contextvars.ContextVar('mace_hip_kernels_geometry', default=False)
 _PTR = contextvars.ContextVar('mace_hip_kernels_geometry_ptr', default=None)   # the batch's ptr during a forward
 _BATCH = contextvars.ContextVar('mace_hip_kernels_geometry_batch', default=None)  # the batch vector, likewise
+# (harmonics, embedding) drop-ins of the running forward whose outputs the geometry's forward makes too (edgefeat)
+_EDGE = contextvars.ContextVar('mace_hip_kernels_geometry_edge', default=None)
 FUNCTION = 'get_edge_vectors_and_lengths'
 DISPLACEMENT = 'get_symmetric_displacement'
 SCATTER = 'scatter_sum'
@@ -217,17 +219,22 @@ def _geom_bwd(vec, ln, gv, gl, gr, N, want_shifts):
 
 class _GeomFn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, positions, shifts, edge_index, double_backward=False):
+    def forward(ctx, positions, shifts, edge_index, double_backward=False, edge_ops=None):
         N, E = positions.shape[0], edge_index.shape[1]
         gr = _conv.graph_for(edge_index, N)
         p = positions.contiguous()
         sh = shifts.contiguous()
         vec = torch.empty(E, 3, device=p.device, dtype=torch.float32)
         ln = torch.empty(E, 1, device=p.device, dtype=torch.float32)
-        mod = _module(p.device)
-        _native.launch('geom_fwd', _native.load().mh_geom_fwd, mod.handle, _native.ptr(p), _native.ptr(gr.send),
-                       _native.ptr(gr.recv), _native.ptr(sh), _native.ptr(vec), _native.ptr(ln), E,
-                       _native.stream_of(p))
+        if edge_ops is not None:
+            # the harmonics and the embedding of the same edges in the same pass, left on vec for those modules
+            from . import edgefeat
+            edgefeat.forward_all(p, gr, sh, vec, ln, edge_ops)
+        else:
+            mod = _module(p.device)
+            _native.launch('geom_fwd', _native.load().mh_geom_fwd, mod.handle, _native.ptr(p), _native.ptr(gr.send),
+                           _native.ptr(gr.recv), _native.ptr(sh), _native.ptr(vec), _native.ptr(ln), E,
+                           _native.stream_of(p))
         ctx.save_for_backward(positions, shifts, vec, ln)
         ctx.gr, ctx.N, ctx.double_backward = gr, N, double_backward
         return vec, ln
@@ -242,7 +249,7 @@ class _GeomFn(torch.autograd.Function):
                                          ctx.needs_input_grad[1])
         else:
             gpos, gsh = _geom_bwd(vec, ln, gv, gl, ctx.gr, ctx.N, ctx.needs_input_grad[1])
-        return (gpos if ctx.needs_input_grad[0] else None), gsh, None, None
+        return (gpos if ctx.needs_input_grad[0] else None), gsh, None, None, None
 
 
 class _GeomAdjFn(torch.autograd.Function):
@@ -286,7 +293,7 @@ def edge_vectors_and_lengths(positions, edge_index, shifts):
     if positions.shape[-1] != 3 or shifts.shape != (edge_index.shape[1], 3):
         raise ValueError(f'positions [N, 3] and shifts [E, 3] expected, got {tuple(positions.shape)}, '
                          f'{tuple(shifts.shape)}')
-    return _GeomFn.apply(positions, shifts, edge_index, _ACTIVE.get() == 'double_backward')
+    return _GeomFn.apply(positions, shifts, edge_index, _ACTIVE.get() == 'double_backward', _EDGE.get())
 
 
 def _segsum(g, perm, seg, B):
@@ -462,8 +469,20 @@ def _wrap_scatter(orig):
     return scatter_sum
 
 
+def _edge_ops(model):
+    """(harmonics, embedding) of ``model`` when both are drop-ins and the fused edge pass is on, else None."""
+    from . import edgefeat
+    from .edge import HipSphericalHarmonics
+    from .embedding import HipRadialEmbedding
+    sh, emb = getattr(model, 'spherical_harmonics', None), getattr(model, 'radial_embedding', None)
+    if edgefeat.FUSE and isinstance(sh, HipSphericalHarmonics) and isinstance(emb, HipRadialEmbedding):
+        return sh, emb
+    return None
+
+
 def _forward_with_geometry(self, *args, **kwargs):
     token = _ACTIVE.set('double_backward' if getattr(self, '_mh_geometry_double_backward', False) else True)
+    token_edge = _EDGE.set(_edge_ops(self))
     data = args[0] if args else kwargs.get('data')
     token_ptr = _PTR.set(data.get('ptr') if isinstance(data, dict) else None)
     b = data.get('batch') if isinstance(data, dict) else None
@@ -473,6 +492,7 @@ def _forward_with_geometry(self, *args, **kwargs):
     finally:
         _BATCH.reset(token_batch)
         _PTR.reset(token_ptr)
+        _EDGE.reset(token_edge)
         _ACTIVE.reset(token)
 
 

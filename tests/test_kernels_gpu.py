@@ -1176,6 +1176,71 @@ def test_edge_geometry_vs_float64():
     assert _rel(got.double().cpu().numpy(), want.numpy()) < 1e-5
 
 
+def test_fused_edge_pass_c_abi():
+    """mh_edge_fwd / mh_edge_bwd (edge geometry, harmonics and embedding in one pass each way) against the separate
+    entry points on the same inputs (mh_geom_fwd, then mh_sh_fwd on its vectors and mh_emb_fwd on its lengths;
+    mh_sh_bwd and mh_emb_bwd): within 1e-6 relative, the cutoff's -0.0 marks in the same places, a zero-length
+    self-loop and an edge exactly at r_max, a ragged edge count, with and without a cutoff gradient; NULL operands
+    are rejected."""
+    from mace_hip_kernels import HipRadialEmbedding, HipSphericalHarmonics, edgefeat, geometry
+    dev = _dev()
+    print('[case] fused edge pass through the C ABI', flush=True)
+    model = factory.make_model('128x0e+128x1o', 3, 2, elements=factory.ELEMENTS_PTCOH)
+    sh = HipSphericalHarmonics(model.spherical_harmonics, device=dev)
+    emb = HipRadialEmbedding(model.radial_embedding, device=dev)
+    m = edgefeat.module(sh, emb, dev)
+    lib, P = _native.load(), _native.ptr
+    rng = np.random.default_rng(12)
+    N, E = 300, 40001
+    f = lambda a: torch.tensor(a, dtype=torch.float32, device=dev)  # noqa: E731
+    pos = f(rng.uniform(0.0, 12.0, size=(N, 3)))
+    send = torch.tensor(rng.integers(0, N, E), dtype=torch.int32, device=dev)
+    recv = torch.tensor(rng.integers(0, N, E), dtype=torch.int32, device=dev)
+    shifts = (rng.integers(-1, 2, size=(E, 3)) * 12.0).astype(np.float32)
+    send[0], recv[0] = 5, 5
+    shifts[0] = 0.0
+    send[1], recv[1] = 7, 7
+    shifts[1] = (emb.spec.r_max, 0.0, 0.0)
+    shifts = f(shifts)
+    st = _native.stream_of(pos)
+    out = [torch.empty(E, 3, device=dev), torch.empty(E, device=dev), torch.empty(E, sh.spec.dim, device=dev),
+           torch.empty(E, emb.spec.n, device=dev), torch.empty(E, device=dev)]
+    _native.check(lib.mh_edge_fwd(m.handle, P(pos), P(send), P(recv), P(shifts), *[P(t) for t in out], E, st),
+                  'edge_fwd')
+    vec, ln = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+    _native.check(lib.mh_geom_fwd(geometry._module(dev).handle, P(pos), P(send), P(recv), P(shifts), P(vec), P(ln),
+                                  E, st), 'geom_fwd')
+    Y = torch.empty(E, sh.spec.dim, device=dev)
+    _native.check(lib.mh_sh_fwd(sh.module.handle, P(vec), P(Y), E, st), 'sh_fwd')
+    feats, cut = torch.empty(E, emb.spec.n, device=dev), torch.empty(E, device=dev)
+    _native.check(lib.mh_emb_fwd(emb.module.handle, P(ln), P(feats), P(cut), E, st), 'emb_fwd')
+    torch.cuda.synchronize()
+
+    def same(got, want):                  # NaN in the same places (the features of a zero-length edge: 0 / 0)
+        gn, wn = torch.isnan(got), torch.isnan(want)
+        assert torch.equal(gn, wn)
+        return _rel(got[~gn].double().cpu().numpy(), want[~wn].double().cpu().numpy()) < 1e-6
+    for got, want in zip(out, (vec, ln, Y, feats, cut)):
+        assert same(got, want)
+    assert torch.equal(torch.signbit(out[4]) & (out[4] == 0), torch.signbit(cut) & (cut == 0))
+    assert bool(torch.signbit(out[4][1])) and float(out[4][1]) == 0.0 and float(out[1][0]) == 0.0
+    gY, gf, gc = torch.randn(E, sh.spec.dim, device=dev), torch.randn(E, emb.spec.n, device=dev), \
+        torch.randn(E, device=dev)
+    for with_cut in (True, False):
+        gv, gl = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+        _native.check(lib.mh_edge_bwd(m.handle, P(vec), P(ln), P(gY), P(gf), P(gc) if with_cut else None, P(gv),
+                                      P(gl), E, st), 'edge_bwd')
+        wv, wl = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+        _native.check(lib.mh_sh_bwd(sh.module.handle, P(vec), P(gY), P(wv), E, st), 'sh_bwd')
+        _native.check(lib.mh_emb_bwd(emb.module.handle, P(ln), P(gf), P(gc) if with_cut else None, P(wl), E, st),
+                      'emb_bwd')
+        torch.cuda.synchronize()
+        assert same(gv, wv) and same(gl, wl)
+    assert lib.mh_edge_fwd(m.handle, P(pos), P(send), P(recv), P(shifts), P(out[0]), None, P(out[2]), P(out[3]),
+                           P(out[4]), E, st) != 0
+    assert b'NULL' in lib.mh_last_error()
+
+
 def test_edge_geometry_only_while_a_patched_model_runs():
     """The edge-geometry route is taken inside a patched model's forward and nowhere else: an unpatched copy of the
     same model, run in the same process, launches no geometry kernel."""
@@ -1194,11 +1259,12 @@ def test_edge_geometry_only_while_a_patched_model_runs():
         with _native.timing() as tm:
             mdl(D.fresh(b), compute_force=True)
         tags = {t for t, *_ in tm.records}
-        assert ('geom_fwd' in tags) == expect and ('geom_bwd' in tags) == expect, tags
+        fwd = 'geom_fwd' in tags or any(t.startswith('edge_fwd') for t in tags)   # alone, or in the fused edge pass
+        assert fwd == expect and ('geom_bwd' in tags) == expect, tags
     assert 'edge_geometry' in unpatch_model(patched)
     with _native.timing() as tm:
         patched(D.fresh(b), compute_force=True)
-    assert not any(t.startswith('geom') for t, *_ in tm.records)
+    assert not any(t.startswith(('geom', 'edge_fwd', 'edge_bwd')) for t, *_ in tm.records)
 
 
 def test_structure_energy_sums():

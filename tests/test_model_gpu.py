@@ -280,10 +280,12 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
     assert sym[f'lin_fwd[{comp}]'] == ['lin_fwd_i2048_o2048_v4c'], sym
     assert sym[f'lin_bwd[{comp}]'] == ['lin_bwd_i2048_o2048_v4c'], sym
     assert not any(k.endswith(('[interactions.0.linear]', '[interactions.0.skip_tp]')) for k in sym), sym
-    for prefix in ('sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_', 'geom_fwd', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
+    # the edge geometry, harmonics and embedding forward as one pass (edge_fwd), their backward as edge_bwd + geom_bwd
+    for prefix in ('edge_fwd_', 'edge_bwd_', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
                    'ro_fwd_', 'ro_bwd_'):
         assert any(n.startswith(prefix) for n in flat), (prefix, flat)
-    assert not any(n.startswith(('perm_', 'conv_fwd_', 'conv_bwd_') + banned) for n in flat), flat
+    assert not any(n.startswith(('perm_', 'conv_fwd_', 'conv_bwd_', 'sh_fwd_', 'sh_bwd_', 'emb_fwd_', 'emb_bwd_',
+                                 'geom_fwd') + banned) for n in flat), flat
 
 
 def test_stress_path_segmented_sums():
@@ -301,6 +303,44 @@ def test_stress_path_segmented_sums():
     torch.cuda.synchronize()
     assert tm.symbols.get('geom_segsum') == ['geom_segsum'] and tm.summary()['geom_segsum'][0] == 2, tm.symbols
     _check(ref, met, batch, dev, np.diff(batch['ptr'].numpy()), stress=True)
+
+
+def test_fused_edge_pass_matches_separate_kernels(monkeypatch):
+    """The edge geometry, harmonics and embedding as one pass each way (edgefeat: edge_fwd / edge_bwd) against the
+    same model with the three drop-ins launched separately: E+F+stress of config 1 and the position gradient of a
+    force loss under double_backward (where the joint node's gradient is the modules' own second-order functions),
+    within 1e-6 relative; the fused call launches one edge_fwd and one edge_bwd and none of the separate kernels."""
+    from mace_hip_kernels import _native, edgefeat
+    dev = _dev()
+    print('[case] fused edge pass vs separate kernels (config 1, stress; force loss)', flush=True)
+    model, batch, _ = factory.workload(1)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    patch_model(met, verbose=False)
+    res = {}
+    for fuse in (True, False):
+        monkeypatch.setattr(edgefeat, 'FUSE', fuse)
+        _ef(met, batch, dev, torch.float32, stress=True)
+        with _native.timing() as tm:
+            res[fuse] = _ef(met, batch, dev, torch.float32, stress=True)
+        torch.cuda.synchronize()
+        tags = [t for t, *_ in tm.records]
+        if fuse:
+            assert sum(t.startswith('edge_fwd') for t in tags) == 1 and sum(t.startswith('edge_bwd') for t in tags) == 1
+            assert not any(t.startswith(('sh_', 'emb_')) or t == 'geom_fwd' for t in tags), tags
+        else:
+            assert not any(t.startswith('edge_') and t != 'edge_pairs' for t in tags), tags
+    for a, b in zip(res[True], res[False]):
+        assert np.abs(a - b).max() <= 1e-6 * max(np.abs(b).max(), 1e-6), (np.abs(a - b).max(), np.abs(b).max())
+    dbl = copy.deepcopy(model).to(dev, torch.float32)
+    patch_model(dbl, verbose=False, double_backward=True)
+    small = D.batch_graphs([D.graph_of(factory.make_structure(seed=9), 5.0)], factory.ELEMENTS_REF)
+    loss = {}
+    for fuse in (True, False):
+        monkeypatch.setattr(edgefeat, 'FUSE', fuse)
+        loss[fuse] = _force_loss(dbl, small, dev, torch.float32, wrt_positions=True)
+    for k in loss[False]:
+        a, b = loss[True][k], loss[False][k]
+        assert np.abs(a - b).max() <= 1e-6 * max(np.abs(b).max(), 1e-6), k
 
 
 def test_unsupported_block_is_skipped():
