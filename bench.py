@@ -180,7 +180,8 @@ def _kernel_table(met, batch, n_real_edges, summary, symbols):
             rows[f'ro_bwd[{m.tag}]'] = (bb, 0)
         elif isinstance(m, HipRadialMLP):
             # the rows the forward computed (a row list: the edges inside the cutoff's support, or of those one per
-            # edge and its reverse; without one every edge of the padded list) and the backward's (the support)
+            # edge and its reverse; without one every edge of the padded list) and the backward's (the support; its
+            # dL/dW0 rows are all read, and with the pairs of exact reverses one projection per shared row)
             s = m.spec
             E = batch['edge_index'].shape[1]
             last = getattr(m, 'last_rows', E)
@@ -189,7 +190,7 @@ def _kernel_table(met, batch, n_real_edges, summary, symbols):
             bf, _ = s.bytes(ef_rows)
             _, bb = s.bytes(eb_rows)
             rows[f'mlp_fwd[{m.tag}]'] = (bf, s.flops(ef_rows))
-            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(eb_rows))
+            rows[f'mlp_bwd[{m.tag}]'] = (bb, s.flops(ef_rows if getattr(m, 'bwd_paired', False) else eb_rows))
     # edge geometry: positions, shifts and the edge list in, vectors and lengths out; backward: vectors, lengths and
     # their gradients plus both CSRs in, the position gradient out
     E = batch['edge_index'].shape[1]

@@ -113,7 +113,8 @@ enum mh_kernel_kind {
     MH_MLP_OUT = 74,     /* its output layer, weight-stationary: persistent waves over 16-edge tiles    */
     MH_EDGE_FWD = 75,    /* edge geometry, spherical harmonics and radial embedding in one pass          */
     MH_EDGE_BWD = 76,    /* the harmonics' and the embedding's backward in one pass                      */
-    MH_NUM_KINDS = 77
+    MH_MLP_BWD_P = 77,   /* radial MLP backward over shared rows, an edge's and its partner's gW0 summed   */
+    MH_NUM_KINDS = 78
 };
 
 /* flags of mh_conv_bwd */
@@ -474,6 +475,17 @@ int mh_mlp_fwd_ws(mh_module* m, const float* ef, const float* WhT, const uint16_
                   int64_t E, const int32_t* rows, const int32_t* count, int32_t ncb, void* stream);
 int mh_mlp_bwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                     int64_t E, const int32_t* rows, const int32_t* count, void* stream);
+/* mh_mlp_bwd_rows over the rows mh_edge_pairs shares between an edge and its exact reverse: slot i < count[0]
+ * (edge e = rows[i], a row the forward computed) projects gW0[e] + gW0[partner[e]] when partner[e] >= 0 (the one
+ * edge that reads e's W0 row, from mh_edge_pairs with vec), else gW0[e]; gef[e] receives the row's gradient and
+ * every edge of the slots from count[0] on (the partners and the edges outside the support) a zero row.  The sum of
+ * the two edges' gef rows is what mh_mlp_bwd_rows gives them (to fp32 rounding), which is all that reaches the
+ * positions when the features are the same function of both edges' lengths and the two vectors are exact
+ * negations; the per-edge split is not kept.  rows, count and partner are required.  Bind MH_MLP_BWD_P as
+ * MH_MLP_BWD.  No reference counterpart. */
+int mh_mlp_bwd_pairs(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0,
+                     float* gef, int64_t E, const int32_t* rows, const int32_t* count, const int32_t* partner,
+                     void* stream);
 
 /* The edge rows of a cutoff column (cutoff [E] fp32): rows [E] int32 = the edges whose cutoff is not -0.0 exactly
  * (inside the cutoff envelope's support, as mace_hip_kernels' radial embedding marks it), in increasing order, then
@@ -494,13 +506,16 @@ int mh_edge_compact(mh_module* m, const float* cutoff, int64_t E, int32_t* rows,
  * count as they are).  srows / scount receive, from the same pass, what mh_edge_compact gives for the cutoff (the
  * edges inside the support first: mh_mlp_bwd_rows's list).  work: mh_edge_pairs_work_size(E) bytes of device
  * scratch.  Module of conv.graph_source(); bind MH_EDGE_PAIR with 256 threads and 4 nodes per block, MH_EDGE_COUNT
- * and MH_EDGE_PLACE as for mh_edge_compact.  Deterministic, no atomics, device work only.  No reference
- * counterpart. */
+ * and MH_EDGE_PLACE as for mh_edge_compact.  Deterministic, no atomics in global memory, device work only.
+ * vec [E, 3] fp32 (the edge vectors) and partner [E] int32, both NULL or both given: with them a partner must also be
+ * e's exact reverse (vec of the partner == -vec[e], component by component), every edge's row is read by at most
+ * one other edge, and partner[e2] = the edge that reads e2's row (-1: none), the map mh_mlp_bwd_pairs takes; a node
+ * with more than 2048 incoming edges then shares none of its rows.  No reference counterpart. */
 size_t mh_edge_pairs_work_size(int64_t E);
 int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff, const int32_t* rowptr_r,
                   const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* senders,
-                  const int32_t* receivers, int32_t N, int64_t E, int32_t* wrow, int32_t* rows, int32_t* count,
-                  int32_t* srows, int32_t* scount, void* work, void* stream);
+                  const int32_t* receivers, int32_t N, int64_t E, const float* vec, int32_t* wrow, int32_t* partner,
+                  int32_t* rows, int32_t* count, int32_t* srows, int32_t* scount, void* work, void* stream);
 
 /* Second derivatives of the radial MLP, behind a double backward (ev [E, n_basis] a direction of the features):
  * mh_mlp_jvp writes dW0 = (dW0/def) ev [E, n_out], the gradient of <ev, dL/def> with respect to gW0; mh_mlp_bwd2

@@ -139,7 +139,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 38; }
+int mh_version(void) { return 39; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -782,6 +782,15 @@ int mh_mlp_bwd_rows(mh_module* m, const float* ef, const float* Wh, const uint16
     return launch(m, MH_MLP_BWD, E, args, stream, "mh_mlp_bwd");
 }
 
+int mh_mlp_bwd_pairs(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0,
+                     float* gef, int64_t E, const int32_t* rows, const int32_t* count, const int32_t* partner,
+                     void* stream) {
+    if (E > 0 && (!ef || !Wh || !Wl || !gW0 || !gef || !rows || !partner)) return fail(-1, "mh_mlp_bwd_pairs: NULL operand");
+    if (!count) return fail(-1, "mh_mlp_bwd_pairs: NULL count");
+    void* args[] = {&ef, &Wh, &Wl, &gW0, &gef, &E, &rows, &count, &partner};
+    return launch(m, MH_MLP_BWD_P, E, args, stream, "mh_mlp_bwd_pairs");
+}
+
 int mh_mlp_bwd(mh_module* m, const float* ef, const float* Wh, const uint16_t* Wl, const float* gW0, float* gef,
                int64_t E, void* stream) {
     return mh_mlp_bwd_rows(m, ef, Wh, Wl, gW0, gef, E, nullptr, nullptr, stream);
@@ -814,19 +823,21 @@ size_t mh_edge_pairs_work_size(int64_t E) {
 
 int mh_edge_pairs(mh_module* m, const float* ef, int32_t nf, const float* cutoff, const int32_t* rowptr_r,
                   const int32_t* eids_r, const int32_t* rowptr_s, const int32_t* eids_s, const int32_t* senders,
-                  const int32_t* receivers, int32_t N, int64_t E, int32_t* wrow, int32_t* rows, int32_t* count,
-                  int32_t* srows, int32_t* scount, void* work, void* stream) {
+                  const int32_t* receivers, int32_t N, int64_t E, const float* vec, int32_t* wrow, int32_t* partner,
+                  int32_t* rows, int32_t* count, int32_t* srows, int32_t* scount, void* work, void* stream) {
     if (E < 0 || E >= 0x7fffffffLL || N < 0) return fail(-1, "mh_edge_pairs: bad size");
     if (nf < 1) return fail(-1, "mh_edge_pairs: nf must be at least 1");
     if (!count || !scount || !work ||
         (E > 0 && (!ef || !cutoff || !rowptr_r || !eids_r || !rowptr_s || !eids_s || !senders || !receivers ||
                    !wrow || !rows || !srows)))
         return fail(-1, "mh_edge_pairs: NULL operand");
+    if ((vec == nullptr) != (partner == nullptr))
+        return fail(-1, "mh_edge_pairs: vec and partner go together (both NULL or both given)");
     int32_t* keep = static_cast<int32_t*>(work);
     int32_t* bc = keep + (E > 0 ? E : 0);
     if (N > 0) {
         void* a0[] = {&ef, &nf, &cutoff, &rowptr_r, &eids_r, &rowptr_s, &eids_s, &senders, &receivers, &N, &wrow,
-                      &keep};
+                      &keep, &vec, &partner};
         int rc = launch(m, MH_EDGE_PAIR, N, a0, stream, "mh_edge_pairs");
         if (rc) return rc;
     }

@@ -169,7 +169,8 @@ def graph_source():
     (a hub node, or padding edges all sent to one node) is sorted in place by one workgroup (``csr_sort_long``: a
     bitonic network of ascending comparators, so comparators that reach past the segment's end are simply skipped,
     O(L log^2 L) work, in LDS up to SORT_LDS edges) and then copied."""
-    return _native.device_header() + f"#define RANK_MAX {RANK_MAX}\n#define SORT_LDS {SORT_LDS}\n" + r"""
+    return _native.device_header() + (f"#define RANK_MAX {RANK_MAX}\n#define SORT_LDS {SORT_LDS}\n"
+                                      f"#define PAIR_DEG_MAX {PAIR_DEG_MAX}\n") + r"""
 extern "C" __global__ __launch_bounds__(256) void csr_fill(int* __restrict__ cnt, int* __restrict__ bad, int n) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   if (i <= n) cnt[(long long)blockIdx.y * (n + 1) + i] = 0;
@@ -353,28 +354,45 @@ extern "C" __global__ __launch_bounds__(1024) void edge_place(const float* __res
 // Every other edge inside the support keeps its own row.  A partner always keeps its own row (its sender is the
 // smaller endpoint), so every row read through wrow is computed.  One wave per node s: the edges out of s one per
 // lane, the edges into s 64 at a time in registers, scanned by readlane.  Deterministic; no atomics.
+//
+// With vec (the edge vectors, [E][3]) and partner: a candidate must also be e's exact reverse, vec[e2] == -vec[e]
+// component by component, and each candidate is taken by one edge at most, so that partner[e2] = e names the one
+// edge that reads e2's row (-1: none).  Every such claim on an edge into s is made by s's own wave: the claims are
+// recorded in an LDS bitmap of s's incoming CSR positions (lanes of one round that want the same candidate: the
+// lowest lane takes it, the others search on), partner[] is written for the claims as they are made and with -1 for
+// every other edge into s at the end, each entry once.  A node with more than PAIR_DEG_MAX incoming edges makes no
+// claims (its edges keep their own rows).
 extern "C" __global__ __launch_bounds__(256) void edge_pair(const float* __restrict__ ef, int nf,
     const float* __restrict__ cut, const int* __restrict__ rowptr_r, const int* __restrict__ eids_r,
     const int* __restrict__ rowptr_s, const int* __restrict__ eids_s, const int* __restrict__ senders,
-    const int* __restrict__ receivers, int N, int* __restrict__ wrow, int* __restrict__ keep) {
-  const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int* __restrict__ receivers, int N, int* __restrict__ wrow, int* __restrict__ keep,
+    const float* __restrict__ vec, int* __restrict__ partner) {
+  __shared__ unsigned claimed[4][PAIR_DEG_MAX / 32];
+  const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   if (s >= N) return;
   const int a0 = rowptr_r[s], a1 = rowptr_r[s + 1];     // edges into s
   const int b0 = rowptr_s[s], b1 = rowptr_s[s + 1];     // edges out of s
+  const bool rev = partner != nullptr;                    // unique exact-reverse partners (wave-uniform)
+  const bool can = !rev || a1 - a0 <= PAIR_DEG_MAX;      // (wave-uniform)
+  if (rev)
+    for (int w = lane; w < PAIR_DEG_MAX / 32; w += 64) claimed[wv][w] = 0u;
   for (int pb = b0; pb < b1; pb += 64) {
     const int p = pb + lane;
     int e = 0, r = 0, w = 0, kp = 0;
     bool look = false;
+    float vx = 0.f, vy = 0.f, vz = 0.f;
     if (p < b1) {
       e = eids_s[p];
       r = receivers[e];
       w = e;
       kp = __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
-      look = kp && r < s;
+      look = kp && r < s && can;
+      if (rev) { vx = vec[3 * (size_t)e]; vy = vec[3 * (size_t)e + 1]; vz = vec[3 * (size_t)e + 2]; }
     }
     // Each round finds, per looking lane, the first edge from r into s at CSR position >= from (registers and
     // readlane only), then checks that candidate's cutoff and feature row with one round of loads; a lane whose
-    // candidate differs resumes after it (another image of the same pair), one with none stops.
+    // candidate differs (or, with partners, is taken) resumes after it (another image of the same pair), one with
+    // none stops.
     int from = a0;
     while (__any(look)) {
       int cand = -1;
@@ -387,20 +405,47 @@ extern "C" __global__ __launch_bounds__(256) void edge_pair(const float* __restr
           if (look && cand < 0 && s2 == r && qb + q >= from) cand = qb + q;
         }
       }
+      bool same = false;
+      int e2 = 0;
+      if (look && cand >= 0) {
+        e2 = eids_r[cand];
+        same = __float_as_uint(cut[e2]) != 0x80000000u;
+        for (int f = 0; f < nf; ++f)
+          same = same && __float_as_uint(ef[(size_t)e * nf + f]) == __float_as_uint(ef[(size_t)e2 * nf + f]);
+        if (rev)
+          same = same && vec[3 * (size_t)e2] == -vx && vec[3 * (size_t)e2 + 1] == -vy && vec[3 * (size_t)e2 + 2] == -vz;
+      }
+      if (rev) {
+        // one claim per candidate: not taken in an earlier round, and no lower lane of this round wants it
+        const int want = same ? cand - a0 : -1;
+        bool take = same && !(claimed[wv][want >> 5 & (PAIR_DEG_MAX / 32 - 1)] >> (want & 31) & 1u);
+        for (int j = 0; j < 64; ++j) {
+          const int wj = __builtin_amdgcn_readlane(want, j);
+          if (j < lane && wj == want) take = false;
+        }
+        if (take) {
+          atomicOr(&claimed[wv][want >> 5], 1u << (want & 31));
+          partner[e2] = e;
+        }
+        same = take;
+      }
       if (look) {
         if (cand < 0) {
           look = false;
+        } else if (same) {
+          w = e2; kp = 0; look = false;
         } else {
-          const int e2 = eids_r[cand];
-          bool same = __float_as_uint(cut[e2]) != 0x80000000u;
-          for (int f = 0; f < nf; ++f)
-            same = same && __float_as_uint(ef[(size_t)e * nf + f]) == __float_as_uint(ef[(size_t)e2 * nf + f]);
-          if (same) { w = e2; kp = 0; look = false; }
-          else from = cand + 1;
+          from = cand + 1;
         }
       }
     }
     if (p < b1) { wrow[e] = w; keep[e] = kp; }
+  }
+  if (rev) {
+    __builtin_amdgcn_wave_barrier();
+    for (int q = a0 + lane; q < a1; q += 64)
+      if (!can || !(claimed[wv][((q - a0) >> 5) & (PAIR_DEG_MAX / 32 - 1)] >> ((q - a0) & 31) & 1u))
+        partner[eids_r[q]] = -1;
   }
 }
 """
@@ -409,6 +454,7 @@ extern "C" __global__ __launch_bounds__(256) void edge_pair(const float* __restr
 RANK_MAX = 128             # longest segment ordered by counting in csr_rank; longer ones by csr_sort_long
 EC_EDGES = 4096            # edges per workgroup of mh_edge_compact's kernels (fixed in graph_source)
 SORT_LDS = 8192            # longest segment csr_sort_long sorts in LDS (longer: in place in global memory)
+PAIR_DEG_MAX = 2048        # incoming edges of a node up to which edge_pair records unique partners (a power of 2)
 _GRAPH_MODULES = {}        # device index -> module of the graph-build kernels
 
 
@@ -712,19 +758,26 @@ def support_rows(cut):
 # the deferred radial MLP computes one W0 row per pair of an edge and its reverse when their feature rows are equal
 # (support_pairs); off, one row per edge inside the cutoff's support
 PAIR_RADIAL = True
+# ... and, when only the sum of an edge's and its exact reverse's length gradients reaches the positions (features of
+# the patched geometry's lengths, shifts without gradient), the MLP's backward projects each shared row once from the
+# pair's summed dL/dW0 (conv_mlp.ConvRadialFn, mh_mlp_bwd_pairs)
+PAIR_GRADS = True
 
 
-def support_pairs(ef, cut, gr):
-    """(wrow int32 [E], rows int32 [E], count int32 [1]) of ``mh_edge_pairs`` for the MLP input rows ``ef`` [E, nf],
-    the cutoff column ``cut`` and the graph ``gr`` (both CSRs): edge e reads its W0 row at wrow[e], and rows[:count]
-    lists the edges whose rows the MLP computes (inside the cutoff's support, not mapped to a reverse edge with an
-    equal feature row).  Cached on the cutoff tensor for its version, the features' storage and version and the
-    graph, so both interaction layers (which share MACE's edge features and cutoff) pair the edges once per call;
-    the same launch also fills ``support_rows``'s cache for the cutoff."""
-    key = (cut._version, ef.data_ptr(), ef._version, gr)
+def support_pairs(ef, cut, gr, vec=None):
+    """(wrow int32 [E], rows int32 [E], count int32 [1], partner int32 [E] or None) of ``mh_edge_pairs`` for the MLP
+    input rows ``ef`` [E, nf], the cutoff column ``cut`` and the graph ``gr`` (both CSRs): edge e reads its W0 row at
+    wrow[e], and rows[:count] lists the edges whose rows the MLP computes (inside the cutoff's support, not mapped to
+    a reverse edge with an equal feature row).  With the edge vectors ``vec`` [E, 3] a partner must also be the exact
+    reverse (negated vector), each row is shared by one other edge at most, and ``partner[e]`` names it (-1: none):
+    the map of the paired MLP backward.  Cached on the cutoff tensor for its version, the features' and vectors'
+    storage and version and the graph, so both interaction layers (which share MACE's edge features and cutoff) pair
+    the edges once per call; the same launch also fills ``support_rows``'s cache for the cutoff."""
+    vkey = None if vec is None else (vec.data_ptr(), vec._version)
+    key = (cut._version, ef.data_ptr(), ef._version, gr, vkey)
     c = getattr(cut, '_mh_pairs', None)
     if c is not None and c[0] == key:
-        return c[1], c[2], c[3]
+        return c[1], c[2], c[3], c[4]
     E = cut.numel()
     efc = ef.reshape(E, -1).contiguous()
     cutf = cut.reshape(-1).contiguous()
@@ -735,14 +788,16 @@ def support_pairs(ef, cut, gr):
     count = torch.empty(1, dtype=torch.int32, device=dev)
     srows = torch.empty(E, dtype=torch.int32, device=dev)
     scount = torch.empty(1, dtype=torch.int32, device=dev)
+    vc = None if vec is None else vec.reshape(E, 3).contiguous()
+    partner = None if vec is None else torch.empty(E, dtype=torch.int32, device=dev)
     work = torch.empty(-(-lib.mh_edge_pairs_work_size(E) // 4), dtype=torch.int32, device=dev)
     (rowptr_r, eids_r), (rowptr_s, eids_s) = gr.by_recv(), gr.by_send()
     _native.launch('edge_pairs', lib.mh_edge_pairs, _graph_module(dev).handle, P(efc), efc.shape[1], P(cutf),
-                   P(rowptr_r), P(eids_r), P(rowptr_s), P(eids_s), P(gr.send), P(gr.recv), gr.n, E, P(wrow), P(rows),
-                   P(count), P(srows), P(scount), P(work), _native.stream_of(cutf))
-    cut._mh_pairs = (key, wrow, rows, count, efc)           # (efc keeps the keyed storage alive)
+                   P(rowptr_r), P(eids_r), P(rowptr_s), P(eids_s), P(gr.send), P(gr.recv), gr.n, E, P(vc), P(wrow),
+                   P(partner), P(rows), P(count), P(srows), P(scount), P(work), _native.stream_of(cutf))
+    cut._mh_pairs = (key, wrow, rows, count, partner, efc, vc)   # (efc, vc keep the keyed storage alive)
     cut._mh_rows = (cut._version, srows, scount)            # the support list came from the same pass
-    return wrow, rows, count
+    return wrow, rows, count, partner
 
 
 def _support_masked(cut):

@@ -662,12 +662,19 @@ class ConvRadialFn(torch.autograd.Function):
     feature rows are bitwise equal (``conv.support_pairs``; MACE's neighbour lists hold both directions at the same
     length, and the MLP row is a function of the feature row alone), and the convolution reads each edge's row
     through the pairing's row map: the forward's work and W0 stores halve, every value stays bitwise the same, and
-    the backward is unchanged (one dL/dW0 row per edge).  No double backward: the two-kernel modules take that
+    the backward keeps one dL/dW0 row per edge.  With ``conv.PAIR_GRADS``, when the edge features come from the
+    patched embedding of the patched geometry's lengths and the shifts need no gradient (``geometry.
+    lengths_pair_symmetric``: only the sum of an edge's and its exact reverse's length gradients reaches the
+    positions), the pairs are the exact reverses and the MLP's backward projects each shared row once, from the
+    pair's summed dL/dW0 rows (``mh_mlp_bwd_pairs``): half the projections; the pair's summed dL/d(edge features),
+    and so the forces, are those of the per-edge backward to fp32 rounding, while the split between the two edges
+    is not kept (the partner's row is zero).  No double backward: the two-kernel modules take that
     (``patch_model(double_backward=True)``)."""
 
     @staticmethod
     def forward(ctx, x, Y, ef, cut, edge_index, op):
         from . import conv as C
+        from .geometry import lengths_pair_symmetric
         from .radial import mlp_forward
         mlp = op.deferred_mlp()
         s = op.spec
@@ -686,11 +693,12 @@ class ConvRadialFn(torch.autograd.Function):
         masked = C._support_masked(cut) and op.skip_masked
         xc, Yc = x.contiguous(), Y.contiguous()
         efc, cutf = ef.reshape(E, -1).contiguous(), cut.reshape(-1).contiguous()
-        rows = count = wrow = None
+        rows = count = wrow = partner = frows = fcount = None
         gr = C.graph_for(edge_index, n)
         if masked and E >= C.EDGE_COMPACT_MIN:
             if C.PAIR_RADIAL:                       # (also lists the support: support_rows is then cached)
-                wrow, frows, fcount = C.support_pairs(efc, cut, gr)
+                vec = lengths_pair_symmetric(ef) if C.PAIR_GRADS else None
+                wrow, frows, fcount, partner = C.support_pairs(efc, cut, gr, vec)
             rows, count = C.support_rows(cut)
             if not C.PAIR_RADIAL:
                 frows, fcount = rows, count
@@ -706,13 +714,14 @@ class ConvRadialFn(torch.autograd.Function):
                        P(W0), P(rowptr), P(eids), P(gr.send), P(cutf), P(wrow), P(out), n, _native.stream_of(x))
         ctx.save_for_backward(xc, Yc, efc, cutf)
         ctx.W0, ctx.rows, ctx.count, ctx.masked, ctx.wrow = W0, rows, count, masked, wrow
+        ctx.pairs = (frows, fcount, partner) if partner is not None else None
         ctx.op, ctx.gr, ctx.shapes = op, gr, (ef.shape, cut.shape)
         return out
 
     @staticmethod
     def backward(ctx, g):
         from . import conv as C
-        from .radial import _mlp_bwd
+        from .radial import _mlp_bwd, _mlp_bwd_pairs
         if torch.is_grad_enabled():
             raise RuntimeError(_DOUBLE_BACKWARD)
         x, Y, ef, cut = ctx.saved_tensors
@@ -724,8 +733,14 @@ class ConvRadialFn(torch.autograd.Function):
         gx, gY, gW0, gcut = C._conv_grads(op, gr, g.contiguous(), x, Y, None, ctx.W0, cut, want_x,
                                           want_y or want_ef or want_cut, masked=ctx.masked, nozero=compact,
                                           wrow=ctx.wrow)
-        # per edge: every edge inside the support has its own dL/dW0 row, whatever row its W0 came from
-        gef = _mlp_bwd(op.deferred_mlp(), ef, gW0, ctx.rows, ctx.count) if want_ef else None
+        # every edge inside the support has its own dL/dW0 row, whatever row its W0 came from; with the pairs of
+        # exact reverses, one projection per shared row of the pair's summed dL/dW0
+        if not want_ef:
+            gef = None
+        elif ctx.pairs is not None:
+            gef = _mlp_bwd_pairs(op.deferred_mlp(), ef, gW0, *ctx.pairs)
+        else:
+            gef = _mlp_bwd(op.deferred_mlp(), ef, gW0, ctx.rows, ctx.count)
         ef_shape, cut_shape = ctx.shapes
         return (gx, gY if want_y else None, gef.view(ef_shape) if gef is not None else None,
                 gcut.view(cut_shape) if want_cut else None, None, None)

@@ -270,5 +270,10 @@ class HipRadialEmbedding(torch.nn.Module):
         # and nonzero or +0.0 elsewhere; a patched convolution that receives this tensor unmodified (same version)
         # skips such edges in its backward (MH_CUT_MASKED).
         cut._mh_support_mask = cut._version
+        from .geometry import lengths_pair_symmetric
+        vec = lengths_pair_symmetric(edge_lengths)
+        if vec is not None:
+            # each feature row is the same function of its edge's length alone
+            feats._mh_vec = (feats._version, vec, vec._version)
         return feats, cut
 

@@ -293,7 +293,24 @@ def edge_vectors_and_lengths(positions, edge_index, shifts):
     if positions.shape[-1] != 3 or shifts.shape != (edge_index.shape[1], 3):
         raise ValueError(f'positions [N, 3] and shifts [E, 3] expected, got {tuple(positions.shape)}, '
                          f'{tuple(shifts.shape)}')
-    return _GeomFn.apply(positions, shifts, edge_index, _ACTIVE.get() == 'double_backward', _EDGE.get())
+    vec, ln = _GeomFn.apply(positions, shifts, edge_index, _ACTIVE.get() == 'double_backward', _EDGE.get())
+    if not shifts.requires_grad:
+        # The lengths' one differentiable input is then the positions, through pos[recv] - pos[send] + shift: an edge
+        # and its exact reverse (negated vector) have equal lengths whose gradients reach the two end atoms along the
+        # same axis with opposite signs, so only the sum of the pair's length gradients reaches the positions.  A
+        # patched radial embedding passes this on to its features (lengths_pair_symmetric).
+        ln._mh_vec = (ln._version, vec, vec._version)
+    return vec, ln
+
+
+def lengths_pair_symmetric(t):
+    """The edge vectors behind ``t`` (edge lengths from ``edge_vectors_and_lengths``, or a patched radial
+    embedding's features of them) when only the sum of an edge's and its exact reverse's gradients in ``t`` reaches
+    any input (the shifts need no gradient), and ``t`` and the vectors are unmodified since; else None."""
+    m = getattr(t, '_mh_vec', None)
+    if m is None or m[0] != t._version or m[1]._version != m[2]:
+        return None
+    return m[1]
 
 
 def _segsum(g, perm, seg, B):

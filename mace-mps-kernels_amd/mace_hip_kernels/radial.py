@@ -43,6 +43,7 @@ NB_FWD = 1           # 16-edge tiles per wave in the forward (each LDS weight fr
 NB_BWD = 1           # and in the backward
 NB_JVP = 1           # and in the forward-mode derivative (twice the hidden registers of the forward)
 GW_DIST = 2          # chunks of dL/dW0 in flight ahead of the one being multiplied (backward)
+GW_DIST_P = 1        # the same for the paired backward (mlp_bwdp), whose chunks are two rows each
 PREFETCH = 2         # output-layer weight chunks in flight ahead of the one being multiplied
 HIDDEN_TILES_BWD = 1 # edge tiles whose hidden layers the backward recomputes together (register pressure)
 CH_FWD = 32          # output columns of the last layer per LDS chunk, forward (a multiple of 32)
@@ -267,13 +268,14 @@ def _source(spec, second):
               '__device__ __forceinline__ float mlp_d2(float z) { const float s = mlp_sig(z); '
               'return s * (1.f - s) * (2.f + z * (1.f - 2.f * s)); }', '']
 
-    def head(name, args, lds, nb, waves=BLOCK // 64, indexed=False, wpe=None):
+    def head(name, args, lds, nb, waves=BLOCK // 64, indexed=False, wpe=None, extra=''):
         """Kernel prologue: edge slot ej{b} of this lane in tile b (live{b}: a slot < E).  ``indexed``: two more
         arguments, ``rows`` (NULL, or the edge of each slot) and ``count`` (NULL, or the number of slots to compute:
         the rest are not computed, and a backward writes zero gradient rows for their edges); rowc{b} is the edge of
         slot ej{b} (clamped into range) and do{b} whether it is computed."""
         if indexed:
             args += ', const int* __restrict__ rows, const int* __restrict__ count'
+        args += extra                                    # parameters after the row list's (mlp_bwdp: partner)
         span = 16 * nb * waves
         occ = f' __attribute__((amdgpu_waves_per_eu({wpe})))' if wpe else ''
         P = [f'extern "C" __global__ __launch_bounds__({64 * waves}){occ} void {name}({args}) {{',
@@ -557,8 +559,11 @@ def _source(spec, second):
         return B
 
     # ------------------------------------------------------------------ backward
-    def bwd_kernel(name, dual):
-        """The backward (``dual``: the Hessian-vector product along ev)."""
+    def bwd_kernel(name, dual, paired=False):
+        """The backward (``dual``: the Hessian-vector product along ev; ``paired``: ``mlp_bwdp``, the row list's
+        slot i < count[0] (edge e = rows[i]) projects the sum of e's dL/dW0 row and that of partner[e] when
+        partner[e] >= 0, the edge that reads e's W0 row; the partner's own slot lies past count[0] and gets a zero
+        dL/d(edge features) row like every other uncomputed slot)."""
         # dL/dh_last = gW Wl^T first: K = the output columns, one bf16 step of 32 per chunk (lane group q: columns
         # 8 q .. 8 q + 7, two float4 loads of gW split into three bf16 parts); chunks of Wl [HL][CH] as bf16 rows of
         # CH + BPAD.  Then the hidden layers recomputed from the natural-layout fp32 weights and walked back.
@@ -570,12 +575,19 @@ def _source(spec, second):
         TAIL = NW % CH != 0
         wg = BLOCK // 64 if dual else WG_WAVES_BWD           # waves per workgroup
         nt = 64 * wg
+        dist = GW_DIST_P if paired else GW_DIST
         B = head(name, 'const float* __restrict__ ef, ' + ('const float* __restrict__ ev, ' if dual else '') +
                  'const float* __restrict__ Wh, const unsigned short* __restrict__ Wl, const float* __restrict__ gW, '
                  'float* __restrict__ gef, long long E', lds_bwd, nb, waves=wg, indexed=not dual,
-                 wpe=None if dual else WAVES_BWD)
+                 wpe=None if dual else WAVES_BWD, extra=', const int* __restrict__ partner' if paired else '')
         if not dual:
             B += skip_block(nb, zero_rows=True, waves=wg)
+        if paired:
+            # the partner's row when there is one (hp), else the slot's own row again, whose values are then dropped
+            for b in range(nb):
+                B += [f'  const int prr{b} = partner[rowc{b}];',
+                      f'  const bool hp{b} = do{b} && prr{b} >= 0;',
+                      f'  const long long prc{b} = hp{b} ? (long long)prr{b} : rowc{b};']
         for b in range(nb):
             B += [f'  mh_f4 dh{b}[{TL}][{ncb}];'] + [f'  dh{b}[{o}][{j}] = mh_f4{{0.f, 0.f, 0.f, 0.f}};'
                                                     for o in range(TL) for j in range(ncb)]
@@ -584,18 +596,28 @@ def _source(spec, second):
         # columns past NW (the zero-padded tail of the last chunk) read a valid column and are zeroed
         gcol = (lambda c: f'min({c} + 8 * q, {NW - 8})') if TAIL else (lambda c: f'{c} + 8 * q')
 
-        def gload(dst, c, b, decl):
+        def gload(dst, c, b, decl, row='rowc'):
             """dL/dW0 of edge tile b, columns c + 32 ks + 8 q .. + 7 for each K step ks, into dst_ks_{0,1}"""
             P = []
             for ks in range(KS):
                 col = gcol(f'{c} + {32 * ks}')
-                P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + rowc{b} * {NW} + {col});',
-                      f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + rowc{b} * {NW} + {col} + 4);']
+                P += [f'{decl}{dst}_{ks}_0_{b} = *reinterpret_cast<const mh_f4*>(gW + {row}{b} * {NW} + {col});',
+                      f'{decl}{dst}_{ks}_1_{b} = *reinterpret_cast<const mh_f4*>(gW + {row}{b} * {NW} + {col} + 4);']
             return P
-        # dL/dW0 of chunk ch + d sits in g{d}_* (d = 0 .. GW_DIST - 1) while chunk ch is multiplied
+
+        def fold(dst, src, b, decl):
+            """dst = src + (the partner's values when there is one), per K step and half"""
+            return [f'{decl}{dst}_{ks}_{h}_{b} = {src}_{ks}_{h}_{b} + (hp{b} ? {src}p_{ks}_{h}_{b} : '
+                    f'mh_f4{{0.f, 0.f, 0.f, 0.f}});' for ks in range(KS) for h in range(2)]
+        # dL/dW0 of chunk ch + d sits in g{d}_* (d = 0 .. dist - 1) while chunk ch is multiplied
         for b in range(nb):
-            for d in range(GW_DIST):
-                B += gload(f'g{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
+            for d in range(dist):
+                if paired:
+                    B += gload(f'gi{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
+                    B += gload(f'gi{d}p', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ', row='prc')
+                    B += fold(f'g{d}', f'gi{d}', b, '  mh_f4 ')
+                else:
+                    B += gload(f'g{d}', str(min(d, NCHK - 1) * CH), b, '  mh_f4 ')
         st0, _ = chunk_io('Wl', 0, CH, RSB, HL, '  ', store_base='0', nthreads=nt)
         B += st0 + ['  __syncthreads();']
         B += [f'  for (int ch = 0; ch < {NCHK}; ++ch) {{',
@@ -604,9 +626,11 @@ def _source(spec, second):
               f'    const size_t nx = (size_t)nc * {NSPLIT * HL * CH};']
         ldn, _ = chunk_io('Wl', 'nx', CH, RSB, HL, '    ', nthreads=nt)
         B += ldn
-        B += [f'    const int gc = min(ch + {GW_DIST}, {NCHK - 1}) * {CH};']
+        B += [f'    const int gc = min(ch + {dist}, {NCHK - 1}) * {CH};']
         for b in range(nb):
             B += gload('gn', 'gc', b, '    const mh_f4 ')
+            if paired:
+                B += gload('gnp', 'gc', b, '    const mh_f4 ', row='prc')
         B += ['    __builtin_amdgcn_sched_barrier(0);            // the next chunk\'s loads go out before the MFMAs']
         for ks in range(KS):
             for b in range(nb):
@@ -629,9 +653,12 @@ def _source(spec, second):
         for b in range(nb):
             for ks in range(KS):
                 for h in range(2):
-                    for d in range(GW_DIST - 1):
+                    for d in range(dist - 1):
                         B += [f'    g{d}_{ks}_{h}_{b} = g{d + 1}_{ks}_{h}_{b};']
-                    B += [f'    g{GW_DIST - 1}_{ks}_{h}_{b} = gn_{ks}_{h}_{b};']
+                    if not paired:
+                        B += [f'    g{dist - 1}_{ks}_{h}_{b} = gn_{ks}_{h}_{b};']
+            if paired:
+                B += fold(f'g{dist - 1}', 'gn', b, '    ')
         stn, _ = chunk_io('Wl', 0, CH, RSB, HL, '    ', store_base='nbase', nthreads=nt)
         B += stn + ['    __syncthreads();', '  }']
         for b in range(nb):
@@ -847,6 +874,7 @@ def _source(spec, second):
         L += fwd_kernel(spec.kname('mlp_jvp'), True) + bwd_kernel(spec.kname('mlp_bwd2'), True)
     else:
         L += fwd_kernel(spec.kname('mlp_fwd'), False) + bwd_kernel(spec.kname('mlp_bwd'), False)
+        L += bwd_kernel(spec.kname('mlp_bwdp'), False, paired=True)
         hidden_only()
         L += h3_kernel(spec.kname('mlp_h3')) + out_kernel(spec.kname('mlp_out'))
     return '\n'.join(L)
@@ -906,8 +934,22 @@ def _mlp_bwd(op, ef, g, rows=None, count=None):
     and their dL/dW0 rows are not read."""
     gx = torch.empty_like(ef)
     P = _native.ptr
+    op.bwd_paired = False
     _native.launch(f'mlp_bwd[{op.tag}]', _native.load().mh_mlp_bwd_rows, op.module.handle, P(ef), P(op.Wh), P(op.Wl),
                    P(g), P(gx), ef.shape[0], P(rows), P(count), _native.stream_of(ef))
+    return gx
+
+
+def _mlp_bwd_pairs(op, ef, g, rows, count, partner):
+    """dL/d(edge features) over the rows shared between an edge and its exact reverse (``conv.support_pairs`` with
+    the edge vectors): the row of each computed slot's edge e receives J(ef[e])^T (g[e] + g[partner[e]]) and every
+    other edge a zero row.  Each pair's two rows add up to what ``_mlp_bwd`` gives them; only that sum reaches the
+    positions (the two lengths are equal and their vectors opposite)."""
+    gx = torch.empty_like(ef)
+    P = _native.ptr
+    op.bwd_paired = True
+    _native.launch(f'mlp_bwd[{op.tag}]', _native.load().mh_mlp_bwd_pairs, op.module.handle, P(ef), P(op.Wh),
+                   P(op.Wl), P(g), P(gx), ef.shape[0], P(rows), P(count), P(partner), _native.stream_of(ef))
     return gx
 
 
@@ -1005,6 +1047,7 @@ class HipRadialMLP(torch.nn.Module):
             self.module = _native.Module(code, {
                 _native.MH_MLP_FWD: (self.spec.kname('mlp_fwd'), BLOCK, 64 * NB_FWD),
                 _native.MH_MLP_BWD: (self.spec.kname('mlp_bwd'), 64 * WG_WAVES_BWD, 16 * NB_BWD * WG_WAVES_BWD),
+                _native.MH_MLP_BWD_P: (self.spec.kname('mlp_bwdp'), 64 * WG_WAVES_BWD, 16 * NB_BWD * WG_WAVES_BWD),
                 _native.MH_MLP_HID: (self.spec.kname('mlp_hid'), BLOCK, 64 * NB_FWD),
                 _native.MH_MLP_HIDB: (self.spec.kname('mlp_hidb'), BLOCK, 64 * NB_BWD),
                 _native.MH_MLP_H3: (self.spec.kname('mlp_h3'), BLOCK, 64),

@@ -236,6 +236,15 @@ def test_edge_compaction_and_row_list_argument_checks():
     assert b'go together' in lib.mh_last_error()
     assert lib.mh_mlp_bwd_rows(None, P(8), P(8), P(8), P(8), P(8), 10, None, P(8), None) != 0
     assert b'go together' in lib.mh_last_error()
+    # the paired backward needs its row list, count and partner map
+    assert lib.mh_mlp_bwd_pairs(None, P(8), P(8), P(8), P(8), P(8), 10, P(8), P(8), None, None) != 0
+    assert b'mh_mlp_bwd_pairs: NULL' in lib.mh_last_error()
+    assert lib.mh_mlp_bwd_pairs(None, P(8), P(8), P(8), P(8), P(8), 10, P(8), None, P(8), None) != 0
+    assert b'NULL count' in lib.mh_last_error()
+    # the pairing's vectors and partner map go together
+    ops = [P(8)] * 7
+    assert lib.mh_edge_pairs(None, P(8), 8, *ops, 5, 10, P(8), P(8), None, P(8), P(8), P(8), P(8), P(8), None) != 0
+    assert b'vec and partner go together' in lib.mh_last_error()
     assert lib.mh_conv_bwd_recv(None, P(8), P(8), P(8), P(8), None, None, None, None, None, None, None, P(8), P(8),
                                 P(8), P(8), 10, _native.MH_WANT_GWY | _native.MH_CUT_NOZERO, None) != 0
     assert b'MH_CUT_NOZERO needs MH_CUT_MASKED' in lib.mh_last_error()

@@ -177,7 +177,8 @@ def test_edge_pairs_vs_definition(n, m):
     ei = torch.tensor(np.stack([s, r]), device=dev)
     gr = hconv.graph_for(ei, n)
     eft, ct = torch.tensor(ef, device=dev), torch.tensor(c, device=dev)
-    wrow, rows, count = hconv.support_pairs(eft, ct, gr)
+    wrow, rows, count, partner = hconv.support_pairs(eft, ct, gr)
+    assert partner is None
     want_w, keep = _pairs_numpy(s, r, ef, c)
     assert np.array_equal(wrow.cpu().numpy(), want_w)
     K = int(keep.sum())
@@ -197,6 +198,155 @@ def test_edge_pairs_vs_definition(n, m):
     assert int(scount.item()) == S
     got = srows.cpu().numpy()
     assert np.array_equal(got[:S], np.nonzero(inside)[0]) and np.array_equal(np.sort(got[S:]), np.nonzero(~inside)[0])
+
+
+def _reverse_graph(rng, n, m, nf, hub=0):
+    """Both directions of m node pairs with exactly negated vectors and equal feature rows, plus: reverse rows that
+    differ in one bit, pairs whose reverse vector is -0.0 where the edge's is +0.0 (equal values), a second image of
+    some pairs with its own vectors, edges with a pair's features but no reverse at all, exact duplicates of some
+    edges in both directions, self-loops, edges outside the cutoff's support, and (hub > 0) a last node with hub
+    incoming and outgoing edges.  Edge ids shuffled."""
+    a = rng.integers(0, n, size=m)
+    b = rng.integers(0, n, size=m)
+    f = rng.normal(size=(m, nf)).astype(np.float32)
+    v = rng.normal(size=(m, 3)).astype(np.float32)
+    v[: m // 10, 2] = 0.0
+    w = -v
+    w[: m // 20, 2] = 0.0                                 # +0.0 on both sides: still the exact reverse
+    k2, k3, kd = m // 8, m // 16, m // 32
+    v2 = (v[:k2] + np.float32(1.5)).astype(np.float32)   # a second image: the same features, other vectors
+    s = [a, b, a[:k2], b[:k2], a[:k3], a[:kd], b[:kd]]
+    r = [b, a, b[:k2], a[:k2], b[:k3], b[:kd], a[:kd]]
+    ef = [f, f, f[:k2], f[:k2], f[:k3], f[:kd], f[:kd]]
+    vec = [v, w, v2, -v2, rng.normal(size=(k3, 3)).astype(np.float32), v[:kd], w[:kd]]
+    if hub:
+        h = n - 1
+        src = rng.integers(0, n - 1, size=hub)
+        fh = rng.normal(size=(hub, nf)).astype(np.float32)
+        vh = rng.normal(size=(hub, 3)).astype(np.float32)
+        s += [src, np.full(hub, h)]
+        r += [np.full(hub, h), src]
+        ef += [fh, fh]
+        vec += [vh, -vh]
+    s, r, ef, vec = (np.concatenate(x) for x in (s, r, ef, vec))
+    flip = np.zeros(len(s), bool)
+    flip[m:2 * m] = rng.uniform(size=m) < 0.1
+    ef[flip, 0] = np.nextafter(ef[flip, 0], np.float32(np.inf))
+    c = rng.uniform(0.05, 1.0, size=len(s)).astype(np.float32)
+    c[rng.uniform(size=len(s)) < 0.1] = -0.0
+    loops = rng.uniform(size=len(s)) < 0.01
+    r[loops] = s[loops]
+    perm = rng.permutation(len(s))
+    return s[perm], r[perm], ef[perm], c[perm], vec[perm]
+
+
+def _reverse_pairs_numpy(s, r, ef, c, vec, deg_max):
+    """The exact-reverse pairing's definition: edges in id order; an edge s -> r inside the support with r < s (and s
+    with at most deg_max incoming edges) takes the first edge r -> s (by id) inside the support, not taken yet, whose
+    feature row is bitwise equal and whose vector is the negation of its own; partner[that edge] = the edge."""
+    E = len(s)
+    inside = ~(np.signbit(c) & (c == 0))
+    bits = ef.view(np.uint32)
+    indeg = np.bincount(r, minlength=max(s.max(), r.max()) + 1)
+    wrow, keep, partner = np.arange(E), inside.copy(), np.full(E, -1)
+    taken = np.zeros(E, bool)
+    for e in range(E):
+        if inside[e] and r[e] < s[e] and indeg[s[e]] <= deg_max:
+            for e2 in np.nonzero((s == r[e]) & (r == s[e]) & inside)[0]:
+                if not taken[e2] and np.array_equal(bits[e2], bits[e]) and np.all(vec[e2] == -vec[e]):
+                    wrow[e], keep[e], partner[e2], taken[e2] = e2, False, e, True
+                    break
+    return wrow, keep, partner
+
+
+@pytest.mark.parametrize('n,m,hub', [(50, 3000, 0), (400, 20000, 0), (300, 6000, 2100)])
+def test_edge_pairs_exact_reverses(n, m, hub):
+    """mh_edge_pairs with the edge vectors: partners are exact reverses, each row is shared by one edge at most,
+    and partner[] names that edge; against the definition, edge for edge."""
+    dev = _dev()
+    print(f'[case] exact-reverse edge pairs n={n} m={m} hub={hub}', flush=True)
+    rng = np.random.default_rng(n + m)
+    s, r, ef, c, vec = _reverse_graph(rng, n, m, 8, hub)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    gr = hconv.graph_for(ei, n)
+    eft, ct, vt = (torch.tensor(a, device=dev) for a in (ef, c, vec))
+    wrow, rows, count, partner = hconv.support_pairs(eft, ct, gr, vt)
+    want_w, keep, want_p = _reverse_pairs_numpy(s, r, ef, c, vec, hconv.PAIR_DEG_MAX)
+    got_w, got_p = wrow.cpu().numpy(), partner.cpu().numpy()
+    assert np.array_equal(got_w, want_w) and np.array_equal(got_p, want_p)
+    K = int(keep.sum())
+    assert int(count.item()) == K
+    assert np.array_equal(rows.cpu().numpy()[:K], np.nonzero(keep)[0])
+    mapped = np.nonzero(want_w != np.arange(len(s)))[0]
+    assert len(mapped) > m // 3 and np.array_equal(want_p[want_w[mapped]], mapped)
+    # a duplicate pair shares rows with the duplicate reverse, one each; the hub's edges share none
+    if hub:
+        h = n - 1
+        assert (got_w[(s == h) | (r == h)] == np.nonzero((s == h) | (r == h))[0]).all()
+    # the same inputs without vectors: the pairing by feature rows alone, cached separately
+    w2, _, _, p2 = hconv.support_pairs(eft, ct, gr)
+    assert p2 is None and np.array_equal(w2.cpu().numpy(), _pairs_numpy(s, r, ef, c)[0])
+
+
+@pytest.mark.parametrize('want_x', [True, False])
+def test_paired_gradients_sum_per_pair(monkeypatch, want_x):
+    """ConvRadialFn when the features are marked as a function of the lengths of exact-reverse edges
+    (conv.PAIR_GRADS): the MLP's backward projects each shared row once from the pair's summed dL/dW0
+    (mh_mlp_bwd_pairs).  Against the per-edge backward: output and every other gradient bitwise equal, dL/d(edge
+    features) equal on unpaired edges, the pair's sum on the kept edge (fp32 rounding) and zero on its partner."""
+    dev = _dev()
+    print(f'[case] paired radial gradients want_x={want_x}', flush=True)
+    op, mlp = _modules(dev)
+    rng = np.random.default_rng(11)
+    n = 900
+    s, r, ef, c, vec = _reverse_graph(rng, n, 20000, mlp.spec.hs[0])
+    E = len(s)
+    x = rng.normal(size=(n, op.spec.x_dim)).astype(np.float32)
+    Y = rng.normal(size=(E, op.spec.y_dim)).astype(np.float32)
+    g = torch.tensor(rng.normal(size=(n, op.spec.out_dim)).astype(np.float32), device=dev)
+    ei = torch.tensor(np.stack([s, r]), device=dev)
+    vt = torch.tensor(vec, device=dev)
+
+    def run(paired):
+        monkeypatch.setattr(hconv, 'PAIR_GRADS', paired)
+        op.defer_mlp(mlp)
+        mlp.fuse = True
+        t = lambda a, rg=True: torch.tensor(a, device=dev, requires_grad=rg)  # noqa: E731
+        xt, Yt, eft, ct = t(x, want_x), t(Y), t(ef), t(c[:, None])
+        ct._mh_support_mask = ct._version
+        eft._mh_vec = (eft._version, vt, vt._version)       # as the patched embedding marks its features
+        with _native.timing() as tm:
+            out = op(xt, Yt, mlp(eft) * ct, ei)
+            out.backward(g)
+        torch.cuda.synchronize()
+        return out.detach(), xt.grad, Yt.grad, eft.grad, ct.grad, tm.symbols
+
+    try:
+        one = run(False)
+        two = run(True)
+    finally:
+        op.defer_mlp(None)
+        mlp.fuse = False
+    for nm, a, b in zip(('out', 'gx', 'gY', 'gcut'), (one[0], one[1], one[2], one[4]), (two[0], two[1], two[2], two[4])):
+        if nm == 'gx' and not want_x:
+            assert a is None and b is None
+            continue
+        assert torch.equal(a, b), (nm, float((a - b).abs().max()))
+    assert one[5]['mlp_bwd[radial_mlp]'][0].startswith('mlp_bwd_'), one[5]
+    assert two[5]['mlp_bwd[radial_mlp]'][0].startswith('mlp_bwdp_'), two[5]
+    g1, g2 = one[3].cpu().numpy(), two[3].cpu().numpy()
+    gr = hconv.graph_for(ei, n)
+    wrow, _, _, partner = hconv.support_pairs(torch.tensor(ef, device=dev), torch.tensor(c[:, None], device=dev),
+                                              gr, vt)
+    p = partner.cpu().numpy()
+    kept = np.nonzero(p >= 0)[0]
+    part = p[kept]
+    assert len(kept) > 5000
+    scale = float(np.abs(g1).max())
+    assert np.abs(g2[kept] - (g1[kept] + g1[part])).max() <= 2e-6 * scale
+    assert (g2[part] == 0).all()
+    rest = np.setdiff1d(np.arange(E), np.concatenate([kept, part]))
+    assert np.array_equal(g2[rest], g1[rest])
 
 
 @pytest.mark.parametrize('want_x', [True, False])
@@ -250,6 +400,7 @@ def test_patched_model_pairs_bitwise(monkeypatch):
     model, batch, _ = factory.workload(2)
     b = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
     outs = []
+    monkeypatch.setattr(hconv, 'PAIR_GRADS', False)       # the per-edge backward: bitwise equal forces
     for paired in (False, True):
         monkeypatch.setattr(hconv, 'PAIR_RADIAL', paired)
         m = copy.deepcopy(model).to(dev)
@@ -259,3 +410,33 @@ def test_patched_model_pairs_bitwise(monkeypatch):
         outs.append((o['energy'].detach(), o['forces'].detach()))
     (e0, f0), (e1, f1) = outs
     assert torch.equal(e0, e1) and torch.equal(f0, f1), (float((e0 - e1).abs().max()), float((f0 - f1).abs().max()))
+
+
+def test_patched_model_paired_gradients(monkeypatch):
+    """config 2: the MLP backward over the pairs of exact reverses (conv.PAIR_GRADS, the default) against the
+    per-edge backward: energies bitwise equal, forces to fp32 rounding, and the paired kernel runs for both layers
+    with E+F but not with stress (the shifts then need a gradient of their own)."""
+    dev = _dev()
+    print('[case] patched model, paired radial gradients (config 2)', flush=True)
+    model, batch, _ = factory.workload(2)
+    b = {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in batch.items()}
+    outs = []
+    for paired in (False, True):
+        monkeypatch.setattr(hconv, 'PAIR_GRADS', paired)
+        m = copy.deepcopy(model).to(dev)
+        patch_model(m, verbose=False)
+        with _native.timing() as tm:
+            o = m(D.fresh(b), compute_force=True)
+        torch.cuda.synchronize()
+        names = [nm for tag, nms in tm.symbols.items() if tag.startswith('mlp_bwd[') for nm in nms]
+        assert len(names) == 2 and all(nm.startswith('mlp_bwdp_' if paired else 'mlp_bwd_') for nm in names), names
+        outs.append((o['energy'].detach(), o['forces'].detach()))
+        if paired:
+            with _native.timing() as tm:
+                m(D.fresh(b), compute_force=True, compute_stress=True)
+            torch.cuda.synchronize()
+            names = [nm for tag, nms in tm.symbols.items() if tag.startswith('mlp_bwd[') for nm in nms]
+            assert names and all(nm.startswith('mlp_bwd_') for nm in names), names
+    (e0, f0), (e1, f1) = outs
+    assert torch.equal(e0, e1), float((e0 - e1).abs().max())
+    assert float((f0 - f1).abs().max()) <= 1e-6 * max(1.0, float(f0.abs().max())), float((f0 - f1).abs().max())

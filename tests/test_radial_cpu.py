@@ -146,3 +146,44 @@ def test_fused_output_layer_packing():
                                 want = (A[16 * mt + i16, fs.korder[ki] * mul + 16 * ct + 4 * q + np.arange(4)]
                                         if ki < nk else np.zeros(4))
                                 assert np.array_equal(got[4 * t:4 * t + 4], want)
+
+
+def _kernel_params(src, name):
+    """Parameter names of the generated kernel ``name`` (in order)."""
+    i = src.index(f'void {name}(')
+    sig = src[i + len(name) + 6:src.index(')', i)]
+    return [p.strip().split()[-1].lstrip('*') for p in sig.split(',')]
+
+
+def _launcher_args(fn, array='args'):
+    """Argument names, in order, of the kernel-argument array ``array`` of the C entry point ``fn`` in
+    csrc/mace_hip.cpp."""
+    import os
+    import re
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    cpp = open(os.path.join(root, 'mace-mps-kernels_amd', 'csrc', 'mace_hip.cpp')).read()
+    i = cpp.index(f'\nint {fn}(')
+    body = cpp[i:cpp.index('\n}\n', i)]
+    return re.findall(r'&(\w+)', re.search(r'void\* ' + array + r'\[\] = \{([^}]*)\}', body).group(1))
+
+
+def test_kernel_parameters_follow_the_launchers_arguments():
+    """Every radial-MLP entry point passes its kernel arguments in the order of the generated kernel's parameters
+    (names as in the C source; gW0 is the kernels' gW, W0's WhT / Wh / Wl the weight buffers in order)."""
+    spec = radial.MLPSpec(factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+                          .interactions[1].conv_tp_weights)
+    src = radial.source(spec)
+    alias = {'gW0': 'gW'}
+    for fn, kern in (('mh_mlp_fwd_rows', 'mlp_fwd'), ('mh_mlp_bwd_rows', 'mlp_bwd'), ('mh_mlp_bwd_pairs', 'mlp_bwdp')):
+        got = [alias.get(a, a) for a in _launcher_args(fn)]
+        want = _kernel_params(src, spec.kname(kern))
+        assert len(got) == len(want), (fn, got, want)
+        for g, w in zip(got, want):
+            assert g == w or {g, w} <= {'Wh', 'WhT', 'Wl'}, (fn, got, want)
+
+
+def test_edge_pair_parameters_follow_the_launcher():
+    """mh_edge_pairs passes edge_pair's arguments in the kernel's parameter order (cutoff is the kernel's cut)."""
+    from mace_hip_kernels import conv
+    got = [{'cutoff': 'cut'}.get(a, a) for a in _launcher_args('mh_edge_pairs', 'a0')]
+    assert got == _kernel_params(conv.graph_source(), 'edge_pair'), got
