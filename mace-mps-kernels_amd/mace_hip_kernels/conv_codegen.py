@@ -62,8 +62,10 @@ FWD_PREFETCH = 1
 # Edges whose x and W slices the receiver-ordered backward has in flight ahead of the one being computed (1 or 2).
 # Measured on config 2 (isolated, layer 2): 290.7 us with one edge ahead, 295.7 us with two.
 BWD_PREFETCH = 1
-# The factored backward's per-edge cutoff: broadcast from a per-chunk register (True) or loaded per edge (False).
-BWD_CUT_BCAST = True
+# The factored backward's per-edge cutoff: broadcast from a per-chunk register (True) or loaded per edge (False, a
+# wave-uniform load).  Measured in config 2's E+F call, three alternating runs each: layer 1 backward 85.1-86.3 us
+# broadcast, 76.8-77.3 us loaded; layer 2 unchanged (231-233 us).
+BWD_CUT_BCAST = False
 # Fence the factored backward's ∂/∂c accumulator after every instruction: the per-instruction gW values are then
 # not scheduled together, 173 -> 155 VGPRs for the 1280-wide layer (3 waves per SIMD instead of 2; config 2,
 # layer 2 backward 241 -> 230 us).

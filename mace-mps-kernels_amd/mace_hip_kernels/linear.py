@@ -41,6 +41,11 @@ BLOCK = 256          # 4 waves
 WAVES = BLOCK // 64
 ROWS = 16            # rows (node, m) of an MFMA row tile
 NT = 1               # row tiles per wave, bf16 family: each LDS weight fragment feeds NT MFMAs
+WC_BF16 = 1          # column groups of waves, bf16 family: the workgroup's waves form (4 / WC) x WC, each wave
+                     # NT * WC row tiles by CT / WC column tiles of the workgroup's tile; 1: every wave takes all
+                     # columns.  Config 2's E+F call, all linears per call (two alternating runs): WC 1 240.5 / 246.1
+                     # us, 2 249.1 / 246.5 us (a third fewer LDS operand reads, twice the input splits per wave),
+                     # 4 287.8 / 288.2 us; results bitwise equal
 NT_ATTRS = 1         # the same for skip_tp (attribute terms)
 PREFETCH_BF16 = 2    # chunks whose global loads are in flight ahead of the one being multiplied (1, 2 or 4), bf16 family
 XPAD = 4             # floats of padding per LDS row of staged inputs
@@ -314,6 +319,8 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         TN, G = _group(l, NT)
         CW = _cw(mo, CW_BF16)
         CT = CW // 16
+        WCo = WC_BF16 if CT % WC_BF16 == 0 and WAVES % WC_BF16 == 0 else 1
+        TW, CTW = NT * WCo, CT // WCo                 # row tiles and column tiles per wave
         fn = f'{name}_b{o}'
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const unsigned short* __restrict__ W, float* __restrict__ out, int N, int group, int cg,',
@@ -341,14 +348,15 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         # attribute values a[n, v] of each thread's rows for the staged chunk (skip_tp): loaded with the chunk's other
         # operands and passed through LDS, so the MFMA body never waits on a global load
         SOFF = 2 * (XB + WB)
-        SB = NT * BLOCK if V else 0                  # floats per attribute buffer
+        SB = TW * BLOCK if V else 0                  # floats per attribute buffer
         lds = max(SOFF + 2 * SB, G * CW * D)
         lds_max = max(lds_max, lds)
         NXP = G * KC * D // 4                        # float4 pieces of a chunk's inputs
         NWP = 3 * CW * KC // 8                       # 16-byte pieces of a chunk's weights
         ix, iw = -(-NXP // BLOCK), -(-NWP // BLOCK)
         L += ['  const int wave = t >> 6, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
-              '  (void)lane;']
+              f'  const int wr = wave / {WCo}, cb = (wave % {WCo}) * {16 * CTW};   // row group, first column',
+              '  (void)lane; (void)cb;']
         if V:
             L += _mask_wave(V, 'g0', 'ng') if V <= 32 else _mask(V, 'g0', 'ng', ordered=True)
         else:
@@ -377,8 +385,8 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         # staging: thread piece it of the inputs is node nl = f / (8 D), float4 e = f % (8 D) of the node's run of
         # 32 d floats (channel-major, component-minor, as in e3nn's layout)
         # the lane's A rows: row c16 of each of its tiles (rows past the tile's nodes read row 0; never stored)
-        for tt in range(NT):
-            L += [f'  const int xr{tt} = {(tt) * TN * D} + wave * {NT * TN * D} + (c16 < {TN * D} ? c16 : 0);']
+        for tt in range(TW):
+            L += [f'  const int xr{tt} = {(tt) * TN * D} + wr * {TW * TN * D} + (c16 < {TN * D} ? c16 : 0);']
             if V:
                 L += [f'  const int an{tt} = nd(min(g0 + xr{tt} / {D}, N - 1));']
         # node of each of the thread's input pieces, once (the chunk loop's loads then depend on no index load;
@@ -391,13 +399,13 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
             L += [f'  mh_f4 {", ".join(f"px{S}{k}" for k in range(ix))};',
                   f'  mh_u4 {", ".join(f"pw{S}{k}" for k in range(iw))};']
             if V:
-                L += [f'  float {", ".join(f"ps{S}{tt}" for tt in range(NT))};']
+                L += [f'  float {", ".join(f"ps{S}{tt}" for tt in range(TW))};']
             L += [f'  auto load{S} = [&](int c) {{',
                   '    int oi, mi, uc, v, wo;',
                   '    where(c, oi, mi, uc, v, wo);',
                   '    (void)v;']
             if V:
-                L += [f'    ps{S}{tt} = attr[(size_t)an{tt} * {V} + v];' for tt in range(NT)]
+                L += [f'    ps{S}{tt} = attr[(size_t)an{tt} * {V} + v];' for tt in range(TW)]
             # float4 loads where every input block of this output block starts and ends on a 16-byte boundary (a
             # one-hot node embedding with, say, 89 elements does not): else four scalar loads
             vec = Din % 4 == 0 and all(in_blocks[i][2] % 4 == 0 and in_blocks[i][0] * D % 4 == 0 for i, _ in terms[o])
@@ -419,7 +427,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                   f'    float* __restrict__ xs = lds + buf * {XB};',
                   f'    unsigned short* __restrict__ ws = reinterpret_cast<unsigned short*>(lds + {2 * XB} + buf * {WB});']
             if V:
-                L += [f'    lds[{SOFF} + buf * {SB} + {tt * BLOCK} + t] = ps{S}{tt};' for tt in range(NT)]
+                L += [f'    lds[{SOFF} + buf * {SB} + {tt * BLOCK} + t] = ps{S}{tt};' for tt in range(TW)]
             for k in range(ix):
                 guard = '' if (k + 1) * BLOCK <= NXP else f'if (t + {k * BLOCK} < {NXP}) '
                 L += [f'    {guard}{{ const int f = t + {k * BLOCK}, nl = f / {8 * D}, e = f - nl * {8 * D};']
@@ -437,11 +445,11 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                       f'        k8 = r / {CW}, col = r - k8 * {CW};',
                       f'      *reinterpret_cast<mh_u4*>(ws + (p * {CW} + col) * {WS} + 8 * k8) = pw{S}{k}; }}']
             L += ['  };']
-        L += [f'  mh_f4 acc[{NT}][{CT}];',
+        L += [f'  mh_f4 acc[{TW}][{CTW}];',
               '#pragma unroll',
-              f'  for (int a = 0; a < {NT}; ++a)',
+              f'  for (int a = 0; a < {TW}; ++a)',
               '#pragma unroll',
-              f'    for (int b = 0; b < {CT}; ++b) acc[a][b] = mh_f4{{0.f, 0.f, 0.f, 0.f}};',
+              f'    for (int b = 0; b < {CTW}; ++b) acc[a][b] = mh_f4{{0.f, 0.f, 0.f, 0.f}};',
 ]
 
         def body(cc, buf):
@@ -455,7 +463,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
             return B + BODY + ['    }']
 
         BODY = []
-        for tt in range(NT):
+        for tt in range(TW):
             BODY += [f'    mh_bf8 a{tt}[3];',
                   '    {',
                   f'      const mh_f4 lo = *reinterpret_cast<const mh_f4*>(xs + xr{tt} * {XS} + 8 * q);',
@@ -468,12 +476,12 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
                 BODY += ['      const float v8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};']
             BODY += [f'      mh_split8(v8, a{tt});', '    }']
         PAIRS = [(0, 0), (0, 1), (1, 0), (0, 2), (1, 1), (2, 0)]
-        for ct in range(CT):
+        for ct in range(CTW):
             BODY += [f'    {{ mh_bf8 b[3];']
-            BODY += [f'      b[{p}] = *reinterpret_cast<const mh_bf8*>(ws + ({p * CW + 16 * ct} + c16) * {WS} + 8 * q);'
+            BODY += [f'      b[{p}] = *reinterpret_cast<const mh_bf8*>(ws + ({p * CW + 16 * ct} + cb + c16) * {WS} + 8 * q);'
                   for p in range(3)]
             for pa, pb in PAIRS:
-                for tt in range(NT):
+                for tt in range(TW):
                     BODY.append(f'      acc[{tt}][{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a{tt}[{pa}], b[{pb}], '
                              f'acc[{tt}][{ct}], 0, 0, 0);')
             BODY += ['    }']
@@ -505,15 +513,15 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         # epilogue: lane (c16, q) holds rows 4q + r, column 16 ct + c16 of each tile -> LDS [node][column][m] ->
         # coalesced float4 rows of CW d floats per node
         L += ['#pragma unroll',
-              f'  for (int tt = 0; tt < {NT}; ++tt)',
+              f'  for (int tt = 0; tt < {TW}; ++tt)',
               '#pragma unroll',
               '    for (int r = 0; r < 4; ++r) {',
               '      const int row = 4 * q + r;',
               f'      if (row < {TN * D}) {{',
-              f'        const int rr = tt * {TN * D} + wave * {NT * TN * D} + row, nl = rr / {D}, m = rr - nl * {D};',
+              f'        const int rr = tt * {TN * D} + wr * {TW * TN * D} + row, nl = rr / {D}, m = rr - nl * {D};',
               '#pragma unroll',
-              f'        for (int ct = 0; ct < {CT}; ++ct)',
-              f'          lds[(nl * {CW} + 16 * ct + c16) * {D} + m] = alpha * acc[tt][ct][r];',
+              f'        for (int ct = 0; ct < {CTW}; ++ct)',
+              f'          lds[(nl * {CW} + cb + 16 * ct + c16) * {D} + m] = alpha * acc[tt][ct][r];',
               '      }',
               '    }',
               '  __syncthreads();',
