@@ -81,6 +81,8 @@ WS_MIN_COLS = 1024   # ... for output layers at least this wide (config 2: layer
                      # E+F call; layer 1's 512 columns 39.5 -> 43.3 us, so the single kernel stays there)
 WS_COLS = 64         # output columns per wave of mlp_out (4 MFMA column tiles: 96 VGPRs of split weights)
 WS_WAVES = 3         # waves per SIMD mlp_out is compiled for
+WS_STAGE_OUT = True  # mlp_out's results through LDS, stored as whole 1 KB row pieces of the column group (output
+                     # widths that are a multiple of 256); False: every wave stores its own 16 rows x 64 bytes
 
 
 def _layers(mod):
@@ -761,10 +763,17 @@ def _source(spec, second):
         KS = HL // 32
         FR = KS * 3 * 64 * 8                                 # bf16 per tile of operand fragments
         assert HL == 64, 'mlp_out stages one float4 of h3 per thread: HL must be 64'
+        SO = WS_STAGE_OUT and NW % (4 * WS_COLS) == 0        # staged stores: whole 256-column groups only
+        OS = 4 * WS_COLS + 16                                # floats per staged row: 16 mod 64 banks apart
         F = [f'extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu({WS_WAVES}))) '
              f'void {name}(const float* __restrict__ h3, const unsigned short* __restrict__ Wo, float* __restrict__ W0, '
              'long long E, const int* __restrict__ rows, const int* __restrict__ count) {',
-             f'  __shared__ __align__(16) unsigned short frag[2][{FR}];',
+             f'  __shared__ __align__(16) unsigned short frag[2][{FR}];']
+        if SO:
+            # tile tt's 16 rows x 256 columns, written by the four waves, stored in the next iteration (after its
+            # barrier) as one 1 KB row piece per store instruction, wave w taking rows 4 w .. 4 w + 3
+            F += [f'  __shared__ __align__(16) float otile[2][16][{OS}];']
+        F += [
              '  const int t = threadIdx.x, lane = t & 63, q = lane >> 4, c16 = lane & 15;',
              '  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);',
              '  const long long ncount = count ? (long long)count[0] : E;',
@@ -809,7 +818,8 @@ def _source(spec, second):
               '    };',
               '    mh_f4 pc = piece(tt);',
               '    int rc = erow(tt);',
-              '    int buf = 0;',
+              '    int buf = 0;'] + (['    long long tp = -1;                   // the tile staged in buf ^ 1, stored next',
+                                     '    int rp = 0;'] if SO else []) + [
               '    while (true) {',
               '      const long long nx = tt + step;',
               '      const long long tn = nx < Tx ? nx : tt;',
@@ -852,21 +862,43 @@ def _source(spec, second):
                 for ct in range(CT):
                     F.append(f'        acc[{ct}] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[{ct}][{ks}][{pa}], b[{ks}][{pb}], '
                              f'acc[{ct}], 0, 0, 0);')
-        F += ['        if ((t0 + tt) * 16 + c16 < ncount) {',
-              f'          float* __restrict__ dst = W0 + (long long)rc * {NW} + cb * {WS_COLS} + 4 * q;']
-        for ct in range(CT):
-            guard = f'if (cb < {NCB - 1}) ' if TAILT and ct >= TAILT else ''
-            F.append(f'          {guard}*reinterpret_cast<mh_f4*>(dst + {16 * ct}) = acc[{ct}];')
+        if SO:
+            def store_rows(ind, ob, tile, rcv):
+                """Rows 4 wave .. 4 wave + 3 of staged tile ``tile`` (buffer ``ob``, lane edge rows ``rcv``)."""
+                R = []
+                for i in range(4):
+                    R += [f'{ind}{{ const int j = 4 * wave + {i};',
+                          f'{ind}  if ((t0 + {tile}) * 16 + j < ncount) {{',
+                          f'{ind}    const long long rj = __builtin_amdgcn_readlane({rcv}, j);',
+                          f'{ind}    *reinterpret_cast<mh_f4*>(W0 + rj * {NW} + cg * {4 * WS_COLS} + 4 * lane) = '
+                          f'*reinterpret_cast<const mh_f4*>(&otile[{ob}][j][4 * lane]);',
+                          f'{ind}  }}',
+                          f'{ind}}}']
+                return R
+            F += ['        {',
+                  '        if (tp >= 0) {                       // the previous tile, staged before this barrier']
+            F += store_rows('          ', 'buf ^ 1', 'tp', 'rp')
+            F += ['        }']
+            F += [f'        *reinterpret_cast<mh_f4*>(&otile[buf][c16][wave * {WS_COLS} + {16 * ct} + 4 * q]) = acc[{ct}];'
+                  for ct in range(CT)]
+        else:
+            F += ['        if ((t0 + tt) * 16 + c16 < ncount) {',
+                  f'          float* __restrict__ dst = W0 + (long long)rc * {NW} + cb * {WS_COLS} + 4 * q;']
+            for ct in range(CT):
+                guard = f'if (cb < {NCB - 1}) ' if TAILT and ct >= TAILT else ''
+                F.append(f'          {guard}*reinterpret_cast<mh_f4*>(dst + {16 * ct}) = acc[{ct}];')
         F += ['        }',
               '      }',
-              '      if (nx >= Tx) break;',
+              '      if (nx >= Tx) break;'] + (['      tp = tt;', '      rp = rc;'] if SO else []) + [
               '      tt = nx;',
               '      pc = pn;',
               '      rc = rn;',
               '      buf ^= 1;',
               '    }',
-              '    __syncthreads();                     // every wave is done with the buffers before the next group',
-              '  }',
+              '    __syncthreads();                     // every wave is done with the buffers before the next group']
+        if SO:
+            F += store_rows('    ', 'buf', 'tt', 'rc')       # the last tile (its staging complete at the barrier)
+        F += ['  }',
               '}', '']
         return F
 
