@@ -286,6 +286,19 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             if (isinstance(lin, HipNodeLinear) and isinstance(skp, HipNodeLinear) and lin.div_hint is not None
                     and not skp._composed and lin.spec.V == 0 and lin.spec.out_blocks == skp.spec.in_blocks):
                 skp.compose_after(lin)
+        # the node embedding's output reaches the first interaction block's linear_up alone when that block is
+        # MACE's RealAgnosticInteractionBlock (its skip_tp acts on the message; the residual block's skip_tp reads
+        # the node features too) and the model has no other embedding consumer: the two maps run as one composed
+        # launch
+        emb = getattr(getattr(model, 'node_embedding', None), 'linear', None)
+        blocks = list(getattr(model, 'interactions', []))
+        up = getattr(blocks[0], 'linear_up', None) if blocks else None
+        if (isinstance(emb, HipNodeLinear) and isinstance(up, HipNodeLinear)
+                and type(blocks[0]).__name__ == 'RealAgnosticInteractionBlock'
+                and not any(hasattr(model, k) for k in ('joint_embedding', 'embedding_readout'))
+                and emb.spec.V == 0 and up.spec.V == 0 and not up._composed and emb.spec.out_blocks == up.spec.in_blocks):
+            up.compose_after(emb)
+            emb.pend_hint = True
     if double_backward:                   # including modules patched by an earlier call
         if _geometry.installed(model):
             model._mh_geometry_double_backward = True

@@ -1021,6 +1021,9 @@ class HipNodeLinear(torch.nn.Module):
         self.double_backward = False
         # set by patch_model when the caller divides the output by a constant: forward then returns a PendingLinear
         self.div_hint = None
+        # set by patch_model when the output's one consumer runs it in composed form (compose_after): forward then
+        # returns a PendingLinear (any other use forms the output)
+        self.pend_hint = False
         # set by compose_after: the linear whose scaled output this module consumes (its output is then left
         # pending through the division) and the composed map that runs instead of the two
         self.compose_into = None
@@ -1049,7 +1052,9 @@ class HipNodeLinear(torch.nn.Module):
             op = self._composed[0]
             op.double_backward = self.double_backward
             return _LinFn.apply(x.x, attrs, op, x.scale)
-        if self.div_hint is not None and x.dtype == torch.float32:
+        if isinstance(x, Pending):
+            x = x.value()                      # formed here, under autograd, not inside _LinFn's forward
+        if (self.div_hint is not None or self.pend_hint) and x.dtype == torch.float32:
             return PendingLinear(x, attrs, self)
         return _LinFn.apply(x, attrs, self)
 

@@ -280,6 +280,9 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
     assert sym[f'lin_fwd[{comp}]'] == ['lin_fwd_i2048_o2048_v4c'], sym
     assert sym[f'lin_bwd[{comp}]'] == ['lin_bwd_i2048_o2048_v4c'], sym
     assert not any(k.endswith(('[interactions.0.linear]', '[interactions.0.skip_tp]')) for k in sym), sym
+    # the node embedding and the first block's linear_up, likewise (that block has no skip_tp)
+    assert sym['lin_fwd[node_embedding.linear+interactions.0.linear_up]'] == ['lin_fwd_i4_o128c'], sym
+    assert not any(k.endswith(('[node_embedding.linear]', '[interactions.0.linear_up]')) for k in sym), sym
     # the edge geometry, harmonics and embedding forward as one pass (edge_fwd), their backward as edge_bwd + geom_bwd
     for prefix in ('edge_fwd_', 'edge_bwd_', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
                    'ro_fwd_', 'ro_bwd_'):
