@@ -368,58 +368,92 @@ extern "C" __global__ __launch_bounds__(256) void edge_pair(const float* __restr
     const int* __restrict__ receivers, int N, int* __restrict__ wrow, int* __restrict__ keep,
     const float* __restrict__ vec, int* __restrict__ partner) {
   __shared__ unsigned claimed[4][PAIR_DEG_MAX / 32];
-  const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // node, ranges and loop bounds wave-uniform (readfirstlane: scalar registers and scalar branches)
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int s = blockIdx.x * 4 + wv;
   if (s >= N) return;
-  const int a0 = rowptr_r[s], a1 = rowptr_r[s + 1];     // edges into s
-  const int b0 = rowptr_s[s], b1 = rowptr_s[s + 1];     // edges out of s
+  const int a0 = __builtin_amdgcn_readfirstlane(rowptr_r[s]), a1 = __builtin_amdgcn_readfirstlane(rowptr_r[s + 1]);
+  const int b0 = __builtin_amdgcn_readfirstlane(rowptr_s[s]), b1 = __builtin_amdgcn_readfirstlane(rowptr_s[s + 1]);
   const bool rev = partner != nullptr;                    // unique exact-reverse partners (wave-uniform)
   const bool can = !rev || a1 - a0 <= PAIR_DEG_MAX;      // (wave-uniform)
   if (rev)
     for (int w = lane; w < PAIR_DEG_MAX / 32; w += 64) claimed[wv][w] = 0u;
+  // the first 64 edges into s (all of them for most nodes): edge ids and senders held in registers; their index
+  // loads go out together with those of the first 64 edges out of s (positions clamped into the ranges, the
+  // conditions wave-uniform), so the two chains share their round trips
+  // (one basic block for the common case: a wait-count pass merges branches conservatively)
+  int eid0 = 0, is0 = -1, eo0 = 0;
+  if (a1 > a0 && b1 > b0) {
+    eid0 = eids_r[min(a0 + lane, a1 - 1)];
+    eo0 = eids_s[min(b0 + lane, b1 - 1)];
+  } else if (a1 > a0) {
+    eid0 = eids_r[min(a0 + lane, a1 - 1)];
+  }
   for (int pb = b0; pb < b1; pb += 64) {
     const int p = pb + lane;
     int e = 0, r = 0, w = 0, kp = 0;
     bool look = false;
     float vx = 0.f, vy = 0.f, vz = 0.f;
+    unsigned ce = 0x80000000u;
     if (p < b1) {
-      e = eids_s[p];
+      e = pb == b0 ? eo0 : eids_s[p];
       r = receivers[e];
-      w = e;
-      kp = __float_as_uint(cut[e]) != 0x80000000u ? 1 : 0;
-      look = kp && r < s && can;
+      ce = __float_as_uint(cut[e]);
       if (rev) { vx = vec[3 * (size_t)e]; vy = vec[3 * (size_t)e + 1]; vz = vec[3 * (size_t)e + 2]; }
     }
+    if (pb == b0 && a1 > a0) is0 = senders[eid0];       // in flight with the loads above
+    if (p < b1) {                                        // (the loaded values used only after every load is out)
+      w = e;
+      kp = ce != 0x80000000u ? 1 : 0;
+      look = kp && r < s && can;
+    }
     // Each round finds, per looking lane, the first edge from r into s at CSR position >= from (registers and
-    // readlane only), then checks that candidate's cutoff and feature row with one round of loads; a lane whose
-    // candidate differs (or, with partners, is taken) resumes after it (another image of the same pair), one with
-    // none stops.
+    // readlane only), then checks that candidate's cutoff, feature row and vector with one round of loads (all
+    // issued before any is used: indices clamped in range instead of branches); a lane whose candidate differs (or,
+    // with partners, is taken) resumes after it (another image of the same pair), one with none stops.
     int from = a0;
     while (__any(look)) {
       int cand = -1;
       for (int qb = a0; qb < a1; qb += 64) {
-        int is = -1;
-        if (qb + lane < a1) is = senders[eids_r[qb + lane]];
+        int is = is0;
+        if (qb != a0) {
+          is = -1;
+          if (qb + lane < a1) is = senders[eids_r[qb + lane]];
+        }
         const int nq = min(64, a1 - qb);
         for (int q = 0; q < nq; ++q) {
           const int s2 = __builtin_amdgcn_readlane(is, q);
           if (look && cand < 0 && s2 == r && qb + q >= from) cand = qb + q;
+          if ((q & 7) == 7 && !__any(look && cand < 0)) break;     // every lane has its candidate
         }
+        if (!__any(look && cand < 0)) break;
       }
+      const int e2r = __shfl(eid0, (cand - a0) & 63);    // the candidate's edge id when among the first 64
       bool same = false;
       int e2 = 0;
       if (look && cand >= 0) {
-        e2 = eids_r[cand];
-        same = __float_as_uint(cut[e2]) != 0x80000000u;
-        for (int f = 0; f < nf; ++f)
-          same = same && __float_as_uint(ef[(size_t)e * nf + f]) == __float_as_uint(ef[(size_t)e2 * nf + f]);
-        if (rev)
-          same = same && vec[3 * (size_t)e2] == -vx && vec[3 * (size_t)e2 + 1] == -vy && vec[3 * (size_t)e2 + 2] == -vz;
+        e2 = cand < a0 + 64 ? e2r : eids_r[cand];
+        const unsigned c2 = __float_as_uint(cut[e2]);
+        const float* __restrict__ vb = rev ? vec : cut;  // without vectors: any valid address, result unused
+        const size_t vo = rev ? 3 * (size_t)e2 : 0;
+        const int vs = rev ? 1 : 0;
+        const float w0 = vb[vo], w1 = vb[vo + vs], w2 = vb[vo + 2 * vs];
+        unsigned d = 0u;                                  // bitwise difference of the two feature rows
+        for (int f0 = 0; f0 < nf; f0 += 8) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int f = min(f0 + j, nf - 1);
+            d |= __float_as_uint(ef[(size_t)e * nf + f]) ^ __float_as_uint(ef[(size_t)e2 * nf + f]);
+          }
+        }
+        same = c2 != 0x80000000u && d == 0u && (!rev || (w0 == -vx && w1 == -vy && w2 == -vz));
       }
       if (rev) {
         // one claim per candidate: not taken in an earlier round, and no lower lane of this round wants it
         const int want = same ? cand - a0 : -1;
         bool take = same && !(claimed[wv][want >> 5 & (PAIR_DEG_MAX / 32 - 1)] >> (want & 31) & 1u);
-        for (int j = 0; j < 64; ++j) {
+        const int nj = min(64, b1 - pb);                  // lanes holding an edge of this batch
+        for (int j = 0; j < nj; ++j) {
           const int wj = __builtin_amdgcn_readlane(want, j);
           if (j < lane && wj == want) take = false;
         }
@@ -445,7 +479,7 @@ extern "C" __global__ __launch_bounds__(256) void edge_pair(const float* __restr
     __builtin_amdgcn_wave_barrier();
     for (int q = a0 + lane; q < a1; q += 64)
       if (!can || !(claimed[wv][((q - a0) >> 5) & (PAIR_DEG_MAX / 32 - 1)] >> ((q - a0) & 31) & 1u))
-        partner[eids_r[q]] = -1;
+        partner[q < a0 + 64 ? eid0 : eids_r[q]] = -1;
   }
 }
 """
