@@ -583,6 +583,13 @@ int mh_edge_fwd(mh_module* m, const float* pos, const int32_t* send, const int32
                 float* vec, float* len, float* Y, float* feats, float* cutoff, int64_t E, void* stream);
 int mh_edge_bwd(mh_module* m, const float* vec, const float* len, const float* gY, const float* gfeats,
                 const float* gcutoff, float* gvec, float* glen, int64_t E, void* stream);
+/* mh_edge_bwd for outputs that two consumers read: gY2 [E, DIM], gfeats2 [E, n] and gcutoff2 [E] (each may be NULL)
+ * are a second consumer's gradients of the same outputs, added to the first's per element (gY + gY2, ...) before
+ * use, so that no separate sum of the two runs (the results are those of mh_edge_bwd on the sums).  No reference
+ * counterpart. */
+int mh_edge_bwd2(mh_module* m, const float* vec, const float* len, const float* gY, const float* gfeats,
+                 const float* gcutoff, const float* gY2, const float* gfeats2, const float* gcutoff2, float* gvec,
+                 float* glen, int64_t E, void* stream);
 
 /* Per-node permutation of N rows from e3nn's irreps layout (block l at off_l, index off_l + u (2l+1) + m) to
  * [mul, sum_l (2l+1)] (index u D + o_l + m), the block table compiled into the module; mh_perm_bwd applies the inverse

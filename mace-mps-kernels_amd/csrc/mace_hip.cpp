@@ -139,7 +139,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 39; }
+int mh_version(void) { return 40; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -953,11 +953,17 @@ int mh_edge_fwd(mh_module* m, const float* pos, const int32_t* send, const int32
     return launch(m, MH_EDGE_FWD, E, args, stream, "mh_edge_fwd");
 }
 
+int mh_edge_bwd2(mh_module* m, const float* vec, const float* len, const float* gY, const float* gfeats,
+                 const float* gcutoff, const float* gY2, const float* gfeats2, const float* gcutoff2, float* gvec,
+                 float* glen, int64_t E, void* stream) {
+    if (E > 0 && (!vec || !len || !gY || !gfeats || !gvec || !glen)) return fail(-1, "mh_edge_bwd: NULL operand");
+    void* args[] = {&vec, &len, &gY, &gfeats, &gcutoff, &gvec, &glen, &E, &gY2, &gfeats2, &gcutoff2};
+    return launch(m, MH_EDGE_BWD, E, args, stream, "mh_edge_bwd");
+}
+
 int mh_edge_bwd(mh_module* m, const float* vec, const float* len, const float* gY, const float* gfeats,
                 const float* gcutoff, float* gvec, float* glen, int64_t E, void* stream) {
-    if (E > 0 && (!vec || !len || !gY || !gfeats || !gvec || !glen)) return fail(-1, "mh_edge_bwd: NULL operand");
-    void* args[] = {&vec, &len, &gY, &gfeats, &gcutoff, &gvec, &glen, &E};
-    return launch(m, MH_EDGE_BWD, E, args, stream, "mh_edge_bwd");
+    return mh_edge_bwd2(m, vec, len, gY, gfeats, gcutoff, nullptr, nullptr, nullptr, gvec, glen, E, stream);
 }
 
 int mh_perm_fwd(mh_module* m, const float* x, float* y, int32_t N, void* stream) {

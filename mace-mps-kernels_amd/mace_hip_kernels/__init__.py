@@ -299,6 +299,12 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 and emb.spec.V == 0 and up.spec.V == 0 and not up._composed and emb.spec.out_blocks == up.spec.in_blocks):
             up.compose_after(emb)
             emb.pend_hint = True
+    # the patched convolutions share the patched edge pass's harmonics, features and cutoff: all but one read aliases
+    # with gradient slots of their own (edgefeat.slot), so that the edge pass's backward adds their gradients itself
+    sh_mod = getattr(model, 'spherical_harmonics', None)
+    if isinstance(sh_mod, HipSphericalHarmonics):
+        convs = [b for b in getattr(model, 'interactions', []) if isinstance(getattr(b, 'conv_tp', None), HipConvTP)]
+        sh_mod.slots = max(0, len(convs) - 1)
     if double_backward:                   # including modules patched by an earlier call
         if _geometry.installed(model):
             model._mh_geometry_double_backward = True

@@ -29,6 +29,7 @@ import numpy as np
 import torch
 
 from . import _native, neighbours
+from .pending import stash_owner
 from .conv_codegen import gxsum_block, source
 
 WAVE = 64
@@ -774,7 +775,8 @@ def support_rows(cut):
     """(rows int32 [E], count int32 [1]) of a cutoff column (``mh_edge_compact``): the edges inside the cutoff's
     support (cutoff not -0.0) in increasing order, then the others; count[0] = how many are inside.  Cached on the
     tensor for its current version, so the interaction layers sharing MACE's cutoff compact it once per call."""
-    c = getattr(cut, '_mh_rows', None)
+    owner = stash_owner(cut)
+    c = getattr(owner, '_mh_rows', None)
     if c is not None and c[0] == cut._version:
         return c[1], c[2]
     flat = cut.reshape(-1).contiguous()
@@ -785,7 +787,7 @@ def support_rows(cut):
     work = torch.empty(-(-lib.mh_edge_compact_work_size(E) // 4), dtype=torch.int32, device=cut.device)
     _native.launch('edge_compact', lib.mh_edge_compact, _graph_module(cut.device).handle, P(flat), E, P(rows),
                    P(count), P(work), _native.stream_of(flat))
-    cut._mh_rows = (cut._version, rows, count)
+    owner._mh_rows = (cut._version, rows, count)
     return rows, count
 
 
@@ -809,7 +811,8 @@ def support_pairs(ef, cut, gr, vec=None):
     the edges once per call; the same launch also fills ``support_rows``'s cache for the cutoff."""
     vkey = None if vec is None else (vec.data_ptr(), vec._version)
     key = (cut._version, ef.data_ptr(), ef._version, gr, vkey)
-    c = getattr(cut, '_mh_pairs', None)
+    owner = stash_owner(cut)
+    c = getattr(owner, '_mh_pairs', None)
     if c is not None and c[0] == key:
         return c[1], c[2], c[3], c[4]
     E = cut.numel()
@@ -829,15 +832,15 @@ def support_pairs(ef, cut, gr, vec=None):
     _native.launch('edge_pairs', lib.mh_edge_pairs, _graph_module(dev).handle, P(efc), efc.shape[1], P(cutf),
                    P(rowptr_r), P(eids_r), P(rowptr_s), P(eids_s), P(gr.send), P(gr.recv), gr.n, E, P(vc), P(wrow),
                    P(partner), P(rows), P(count), P(srows), P(scount), P(work), _native.stream_of(cutf))
-    cut._mh_pairs = (key, wrow, rows, count, partner, efc, vc)   # (efc, vc keep the keyed storage alive)
-    cut._mh_rows = (cut._version, srows, scount)            # the support list came from the same pass
+    owner._mh_pairs = (key, wrow, rows, count, partner, efc, vc)   # (efc, vc keep the keyed storage alive)
+    owner._mh_rows = (cut._version, srows, scount)            # the support list came from the same pass
     return wrow, rows, count, partner
 
 
 def _support_masked(cut):
     """Whether ``cut`` is a patched radial embedding's cutoff, unmodified since: -0.0 then marks exactly the edges
     outside the envelope's support, where the envelope's derivative is zero."""
-    return getattr(cut, '_mh_support_mask', None) == cut._version
+    return getattr(stash_owner(cut), '_mh_support_mask', None) == cut._version
 
 
 def _conv_grads(op, gr, g, x, Y, W, W0, cut, want_x, want_wy, masked=False, nozero=False, wrow=None):
@@ -1074,13 +1077,19 @@ class HipConvTP(torch.nn.Module):
 
     def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
         from .conv_mlp import ConvMLPFn, ConvRadialFn, FusedWeights
+        from .edgefeat import slot
+        # the patched edge pass's outputs shared by several convolutions: this one reads aliases with gradient slots
+        # of their own where the pass left them (their gradients then need no separate sum)
+        edge_attrs = slot(edge_attrs)
         if isinstance(tp_weights, FusedWeights):
             if self.fused is not None and tp_weights.mlp is self.fused_mlp():
                 # W = cutoff * MLP(edge_feats) formed inside the kernels: neither W nor its gradient is stored
-                return ConvMLPFn.apply(node_feats, edge_attrs, tp_weights.ef, tp_weights.cut, edge_index, self)
+                return ConvMLPFn.apply(node_feats, edge_attrs, slot(tp_weights.ef), slot(tp_weights.cut), edge_index,
+                                       self)
             if tp_weights.mlp is self.deferred_mlp():
                 # the MLP's kernels and this convolution's in one node: rows outside the cutoff's support skipped
-                return ConvRadialFn.apply(node_feats, edge_attrs, tp_weights.ef, tp_weights.cut, edge_index, self)
+                return ConvRadialFn.apply(node_feats, edge_attrs, slot(tp_weights.ef), slot(tp_weights.cut),
+                                          edge_index, self)
             tp_weights = tp_weights.value()
         if isinstance(tp_weights, CutoffProduct):
             # the radial MLP's output times the cutoff, never formed: the kernels take the two factors

@@ -14,6 +14,8 @@ gradient and dL/dlengths from the embedding's, in one pass (the statements of ``
 Outputs left on a tensor are taken only by the module they were made for, only once, and only while the tensor is
 unmodified (same version); any other call computes as before.
 """
+import weakref
+
 import torch
 
 from . import _native
@@ -59,18 +61,43 @@ def source(sh_spec, emb_spec):
     L += ind(em['head'], 4) + ['    cutoff[e] = cut;'] + ind(em['fwd'], 4)
     L += [f'    feats[e * {n} + {k}] = f{k};' for k in range(n)]
     L += ['  }', '}', '']
+    # gY2 / gfeats2 / gcut2 (each may be NULL): a second consumer's gradients of the same outputs, added to the
+    # first's per element as autograd would (a + b), so that no separate sum runs
     L += [f'extern "C" __global__ __launch_bounds__(BLOCK) void {kname(sh_spec, emb_spec, "edge_bwd")}(',
           '    const float* __restrict__ vec, const float* __restrict__ len, const float* __restrict__ gY,',
           '    const float* __restrict__ gfeats, const float* __restrict__ gcut, float* __restrict__ gvec,',
-          '    float* __restrict__ glen, long long E) {'] + idx
+          '    float* __restrict__ glen, long long E, const float* __restrict__ gY2,',
+          '    const float* __restrict__ gfeats2, const float* __restrict__ gcut2) {'] + idx
     L += ['  {                                         // dL/dvec from the harmonics\' gradient (sh_bwd)',
           '    const float vx = vec[3 * e], vy = vec[3 * e + 1], vz = vec[3 * e + 2];']
     L += ind(sh['head'], 4)
-    L += ['    const float* __restrict__ ge = gY + e * DIM;'] + [f'    const float g{c} = ge[{c}];' for c in range(dim)]
+    # one wave-uniform test per operand, each branch straight-line loads (a test per element would wait per element)
+    L += ['    const float* __restrict__ ge = gY + e * DIM;', f'    float {", ".join(f"g{c}" for c in range(dim))};',
+          '    if (gY2) {', '      const float* __restrict__ ge2 = gY2 + e * DIM;']
+    L += [f'      g{c} = ge[{c}] + ge2[{c}];' for c in range(dim)]
+    L += ['    } else {'] + [f'      g{c} = ge[{c}];' for c in range(dim)] + ['    }']
     L += ind(sh['bwd'], 4) + ['    gvec[3 * e] = ox; gvec[3 * e + 1] = oy; gvec[3 * e + 2] = oz;', '  }']
     L += ['  {                                         // dL/dlen from the embedding\'s gradients (emb_bwd)',
           '    const float x = len[e];']
-    L += ind(em['head'] + em['bwd'], 4) + ['    glen[e] = acc;', '  }', '}', '']
+    L += [f'    float {", ".join(f"gf{k}" for k in range(n))};', '    if (gfeats2) {']
+    L += [f'      gf{k} = gfeats[e * {n} + {k}] + gfeats2[e * {n} + {k}];' for k in range(n)]
+    L += ['    } else {'] + [f'      gf{k} = gfeats[e * {n} + {k}];' for k in range(n)] + ['    }']
+    L += ['    const bool hc = gcut || gcut2;',
+          '    float gc = 0.f;',
+          '    if (gcut && gcut2) gc = gcut[e] + gcut2[e];',
+          '    else if (gcut) gc = gcut[e];',
+          '    else if (gcut2) gc = gcut2[e];']
+    # the embedding's statements read gfeats[e * n + k] and gcut; here they read the summed values
+    bwd, hits = [], 0
+    for ln_ in em['bwd']:
+        new_ = ln_.replace('gcut ? gcut[e] * dcut : 0.f', 'hc ? gc * dcut : 0.f')
+        for k in range(n):
+            new_ = new_.replace(f'gfeats[e * {n} + {k}]', f'gf{k}')
+        hits += new_ != ln_
+        bwd.append(new_)
+    if hits != n + 1 or any('gfeats' in b or 'gcut' in b for b in bwd):
+        raise RuntimeError('edgefeat: the embedding\'s backward statements changed form')
+    L += ind(em['head'] + bwd, 4) + ['    glen[e] = acc;', '  }', '}', '']
     return '\n'.join(L)
 
 
@@ -107,47 +134,78 @@ def forward_all(pos, gr, shifts, vec, ln, ops):
     vec._mh_edge = (sh_op, emb_op, ln, Y, feats, cut, vec._version, ln._version)
 
 
-def _edge_bwd(sh_op, emb_op, vec, ln, gY, gf, gc):
+def _two(gs, shape):
+    """The gradients ``gs`` (Nones dropped) as at most two contiguous tensors of ``shape``; a third and further ones
+    (three or more consumers) are added to the second."""
+    gs = [g.reshape(shape).contiguous() for g in gs if g is not None]
+    if len(gs) > 2:
+        gs = [gs[0], sum(gs[2:], gs[1])]
+    return gs + [None] * (2 - len(gs))
+
+
+def _edge_bwd(sh_op, emb_op, vec, ln, gYs, gfs, gcs):
+    """(gvec, glen) of the joint node from the gradients its consumers gave each output (lists; None: none)."""
     E = vec.shape[0]
     dev = vec.device
-    gY = torch.zeros(E, sh_op.spec.dim, device=dev) if gY is None else gY.reshape(E, sh_op.spec.dim).contiguous()
-    gf = torch.zeros(E, emb_op.spec.n, device=dev) if gf is None else gf.reshape(E, emb_op.spec.n).contiguous()
-    gc = None if gc is None else gc.reshape(E).contiguous()
+    gY, gY2 = _two(gYs, (E, sh_op.spec.dim))
+    gf, gf2 = _two(gfs, (E, emb_op.spec.n))
+    gc, gc2 = _two(gcs, (E,))
+    gY = torch.zeros(E, sh_op.spec.dim, device=dev) if gY is None else gY
+    gf = torch.zeros(E, emb_op.spec.n, device=dev) if gf is None else gf
     gv = torch.empty(E, 3, device=dev, dtype=torch.float32)
     gl = torch.empty(E, 1, device=dev, dtype=torch.float32)
     P = _native.ptr
-    _native.launch(f'edge_bwd[{sh_op.tag}+{emb_op.tag}]', _native.load().mh_edge_bwd,
-                   module(sh_op, emb_op, dev).handle, P(vec), P(ln), P(gY), P(gf), P(gc), P(gv), P(gl), E,
-                   _native.stream_of(vec))
+    two = gY2 is not None or gf2 is not None or gc2 is not None
+    _native.launch(f'edge_bwd[{sh_op.tag}+{emb_op.tag}{"+slots" if two else ""}]', _native.load().mh_edge_bwd2,
+                   module(sh_op, emb_op, dev).handle, P(vec), P(ln), P(gY), P(gf), P(gc), P(gY2), P(gf2), P(gc2),
+                   P(gv), P(gl), E, _native.stream_of(vec))
     return gv, gl
 
 
 class _EdgeFeatFn(torch.autograd.Function):
     """(harmonics, features, cutoff) of (vectors, lengths), made by ``edge_fwd``: one node for the two modules, so
-    that their gradients arrive together and one ``edge_bwd`` serves both.  Under create_graph the gradient is the
-    two modules' own differentiable functions (``_SHAdjFn``, ``_EmbAdjFn``)."""
+    that their gradients arrive together and one ``edge_bwd`` serves both.  With ``nslot`` > 0 the node also returns
+    ``nslot`` aliases of the three (the same storage, outputs of their own) for the other patched consumers
+    (``slot``): each consumer's gradients then reach the node separately, and ``edge_bwd`` adds them as it loads them
+    instead of autograd summing each output's gradients in kernels of their own.  Under create_graph the gradient is
+    the two modules' own differentiable functions (``_SHAdjFn``, ``_EmbAdjFn``) of the summed gradients."""
 
     @staticmethod
-    def forward(ctx, vec, ln, made):
+    def forward(ctx, vec, ln, made, nslot):
         sh_op, emb_op, _, Y, feats, cut = made[:6]
         ctx.save_for_backward(vec, ln)
         ctx.sh_op, ctx.emb_op = sh_op, emb_op
-        return Y, feats, cut
+        extra = []
+        for _ in range(nslot):
+            extra += [Y.detach(), feats.detach(), cut.detach()]
+        return (Y, feats, cut, *extra)
 
     @staticmethod
-    def backward(ctx, gY, gf, gc):
+    def backward(ctx, gY, gf, gc, *extra):
         vec, ln = ctx.saved_tensors
         sh_op, emb_op = ctx.sh_op, ctx.emb_op
+        gYs, gfs, gcs = [gY, *extra[0::3]], [gf, *extra[1::3]], [gc, *extra[2::3]]
         if torch.is_grad_enabled():          # only true under create_graph=True
             if not sh_op.double_backward:
                 raise RuntimeError(_edge._DOUBLE_BACKWARD)
             if not emb_op.double_backward:
                 raise RuntimeError(_emb._DOUBLE_BACKWARD)
+            total = lambda gs: None if all(g is None for g in gs) else sum(g for g in gs if g is not None)  # noqa
+            gY, gf, gc = total(gYs), total(gfs), total(gcs)
             gv = None if gY is None else _edge._SHAdjFn.apply(gY, vec, sh_op)
             gl = None if gf is None and gc is None else _emb._EmbAdjFn.apply(gf, gc, ln, emb_op)
-            return gv, gl, None
-        gv, gl = _edge_bwd(sh_op, emb_op, vec, ln, gY, gf, gc)
-        return gv, gl.reshape(ln.shape), None
+            return gv, gl, None, None
+        gv, gl = _edge_bwd(sh_op, emb_op, vec, ln, gYs, gfs, gcs)
+        return gv, gl.reshape(ln.shape), None, None
+
+
+def slot(t):
+    """``t``, or the next alias of it that the joint node left for another patched consumer (same storage and
+    version counter, an output of its own, so that this consumer's gradient reaches the node separately)."""
+    s = getattr(t, '_mh_slots', None)
+    if s is None or s[0] != t._version or not s[1]:
+        return t
+    return s[1].pop(0)
 
 
 def take_harmonics(sh_op, vec):
@@ -160,7 +218,15 @@ def take_harmonics(sh_op, vec):
     ln = made[2]
     if ln._version != made[7]:
         return None
-    Y, feats, cut = _EdgeFeatFn.apply(vec, ln, made)
+    nslot = max(0, int(getattr(sh_op, 'slots', 0)))
+    outs = _EdgeFeatFn.apply(vec, ln, made, nslot)
+    Y, feats, cut = outs[:3]
+    for k, t in enumerate((Y, feats, cut)):
+        if nslot:
+            aliases = list(outs[3 + k::3])
+            for a in aliases:
+                a._mh_base = weakref.ref(t)        # (weak: no reference cycle through t's own stash)
+            t._mh_slots = (t._version, aliases)
     ln._mh_emb = (made[1], feats, cut, ln._version)
     return Y
 

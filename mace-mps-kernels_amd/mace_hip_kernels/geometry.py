@@ -307,7 +307,8 @@ def lengths_pair_symmetric(t):
     """The edge vectors behind ``t`` (edge lengths from ``edge_vectors_and_lengths``, or a patched radial
     embedding's features of them) when only the sum of an edge's and its exact reverse's gradients in ``t`` reaches
     any input (the shifts need no gradient), and ``t`` and the vectors are unmodified since; else None."""
-    m = getattr(t, '_mh_vec', None)
+    from .pending import stash_owner
+    m = getattr(stash_owner(t), '_mh_vec', None)
     if m is None or m[0] != t._version or m[1]._version != m[2]:
         return None
     return m[1]

@@ -52,3 +52,11 @@ class Pending(torch.Tensor):
         args = torch.utils._pytree.tree_map(real, args)
         kwargs = torch.utils._pytree.tree_map(real, kwargs or {})
         return func(*args, **kwargs)
+
+
+def stash_owner(t):
+    """The tensor whose attributes hold the per-call caches of ``t``: ``t`` itself or, for an alias that gives
+    another consumer a gradient slot of its own (``edgefeat.slot``), the tensor it aliases (held weakly)."""
+    ref = getattr(t, '_mh_base', None)
+    base = ref() if ref is not None else None
+    return t if base is None else base

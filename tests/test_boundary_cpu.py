@@ -248,6 +248,11 @@ def test_edge_compaction_and_row_list_argument_checks():
     assert lib.mh_conv_bwd_recv(None, P(8), P(8), P(8), P(8), None, None, None, None, None, None, None, P(8), P(8),
                                 P(8), P(8), 10, _native.MH_WANT_GWY | _native.MH_CUT_NOZERO, None) != 0
     assert b'MH_CUT_NOZERO needs MH_CUT_MASKED' in lib.mh_last_error()
+    # the edge pass's backward with a second consumer's gradients: those may be NULL, the first ones may not
+    assert lib.mh_edge_bwd2(None, P(8), P(8), None, P(8), None, P(8), P(8), P(8), P(8), P(8), 10, None) != 0
+    assert b'mh_edge_bwd: NULL' in lib.mh_last_error()
+    assert lib.mh_edge_bwd2(None, P(8), P(8), P(8), P(8), None, None, None, None, P(8), P(8), 10, None) != 0
+    assert b'null module' in lib.mh_last_error()
 
 
 def test_species_order_fallback_on_large_tables():

@@ -1236,6 +1236,30 @@ def test_fused_edge_pass_c_abi():
                       'emb_bwd')
         torch.cuda.synchronize()
         assert same(gv, wv) and same(gl, wl)
+    # a second consumer's gradients (mh_edge_bwd2): bitwise what mh_edge_bwd gives on the sums, each second operand
+    # also absent on its own (then the first one alone)
+    print('[case] fused edge backward with two gradient sets', flush=True)
+    nz = lambda t: t.nan_to_num(7.0)  # noqa: E731  (the zero-length self-loop's NaNs compared as a number)
+    g2 = (torch.randn(E, sh.spec.dim, device=dev), torch.randn(E, emb.spec.n, device=dev), torch.randn(E, device=dev))
+    for keep in ((1, 1, 1), (1, 0, 1), (0, 1, 0), (0, 0, 0)):
+        sec = [t if k else None for t, k in zip(g2, keep)]
+        gv, gl = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+        _native.check(lib.mh_edge_bwd2(m.handle, P(vec), P(ln), P(gY), P(gf), P(gc), *[P(t) for t in sec], P(gv),
+                                       P(gl), E, st), 'edge_bwd2')
+        tot = [a if b is None else a + b for a, b in zip((gY, gf, gc), sec)]
+        wv, wl = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+        _native.check(lib.mh_edge_bwd(m.handle, P(vec), P(ln), *[P(t) for t in tot], P(wv), P(wl), E, st),
+                      'edge_bwd')
+        torch.cuda.synchronize()
+        assert torch.equal(nz(gv), nz(wv)) and torch.equal(nz(gl), nz(wl)), keep
+    # the cutoff gradient given only as the second operand
+    gv, gl = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+    _native.check(lib.mh_edge_bwd2(m.handle, P(vec), P(ln), P(gY), P(gf), None, None, None, P(gc), P(gv), P(gl), E,
+                                   st), 'edge_bwd2')
+    wv, wl = torch.empty(E, 3, device=dev), torch.empty(E, device=dev)
+    _native.check(lib.mh_edge_bwd(m.handle, P(vec), P(ln), P(gY), P(gf), P(gc), P(wv), P(wl), E, st), 'edge_bwd')
+    torch.cuda.synchronize()
+    assert torch.equal(nz(gv), nz(wv)) and torch.equal(nz(gl), nz(wl))
     assert lib.mh_edge_fwd(m.handle, P(pos), P(send), P(recv), P(shifts), P(out[0]), None, P(out[2]), P(out[3]),
                            P(out[4]), E, st) != 0
     assert b'NULL' in lib.mh_last_error()

@@ -283,6 +283,8 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
     # the node embedding and the first block's linear_up, likewise (that block has no skip_tp)
     assert sym['lin_fwd[node_embedding.linear+interactions.0.linear_up]'] == ['lin_fwd_i4_o128c'], sym
     assert not any(k.endswith(('[node_embedding.linear]', '[interactions.0.linear_up]')) for k in sym), sym
+    # the two convolutions' gradients of the edge pass's shared outputs reach its backward separately, which adds them
+    assert any(k.startswith('edge_bwd[') and k.endswith('+slots]') for k in sym), sym
     # the edge geometry, harmonics and embedding forward as one pass (edge_fwd), their backward as edge_bwd + geom_bwd
     for prefix in ('edge_fwd_', 'edge_bwd_', 'geom_bwd', 'lin_fwd_', 'lin_bwd_',
                    'ro_fwd_', 'ro_bwd_'):
