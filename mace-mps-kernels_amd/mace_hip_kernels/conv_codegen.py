@@ -640,6 +640,9 @@ def _bwd_recv(G, gyr, pdecl, decl, copy, cut=False):
     return L
 
 
+GX_LIST = 256             # edges of a sender up to which conv_gxsum lists its unmasked edges in LDS first
+
+
 def gxsum_block(spec):
     """Threads of the dX-message reduction: one float4 column each, rounded up to whole waves."""
     return (spec.x_dim // 4 + WAVE - 1) // WAVE * WAVE
@@ -648,21 +651,64 @@ def gxsum_block(spec):
 def _gx_sum(spec):
     """gx[s] = Σ_{e ∈ CSR_send(s)} gxm[e], summed in CSR order (deterministic); one float4 column per thread.
     ``mask`` non-NULL: edges whose mask value is -0.0 exactly have no message (``conv_bwdrc`` with masked edges
-    writes none; it would be zero) and are left out, which leaves every sum unchanged.  Their rows are still loaded
-    (in bounds, contents unset) alongside the mask, and dropped by a select: waiting for the mask before issuing the
-    message loads would add a dependent L2 round trip per group of four edges."""
+    writes none; it would be zero) and are left out, which leaves every sum unchanged.  For a sender of at most
+    GX_LIST edges the first wave lists its unmasked edges in LDS (CSR order: a ballot prefix per 64 edges) after one
+    round of id and mask loads, and the sum then loads only their rows (the padding edges' unset rows, about a fifth
+    of config 2's, are not read).  A longer segment loads each row alongside its mask and drops masked ones by a
+    select (waiting for the mask before each row load would add a dependent round trip per group of four edges).
+    Skipping a masked edge and adding 0.0 for it give the same sum: the sum starts at +0.0 and never becomes -0.0."""
     assert spec.x_dim % 4 == 0
     return [
+        f'#define GX_LIST {GX_LIST}',
         f'extern "C" __global__ __launch_bounds__({gxsum_block(spec)}) void {spec.kname("conv_gxsum")}(',
         '    const float* __restrict__ gxm, const int* __restrict__ rowptr, const int* __restrict__ eids,',
         '    float* __restrict__ gx, int N, const float* __restrict__ mask) {',
+        '  __shared__ int live[GX_LIST];              // the sender\'s unmasked edges, CSR order',
+        '  __shared__ int nlive;',
         '  const int s = mh_xcd_block(blockIdx.x, gridDim.x);',
         '  const int t = threadIdx.x;',
-        '  if (s >= N || t >= X_DIM / 4) return;',
+        '  if (s >= N) return;                        // (whole workgroup: s is uniform)',
+        '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
+        '  if (mask && p1 - p0 <= GX_LIST) {',
+        '    if (t < 64) {',
+        '      int base = 0;',
+        '      for (int q = p0; q < p1; q += 64) {',
+        '        const int pp = q + t;',
+        '        int e = 0;',
+        '        bool k = false;',
+        '        if (pp < p1) { e = eids[pp]; k = __float_as_uint(mask[e]) != 0x80000000u; }',
+        '        const unsigned long long b = __ballot(k);',
+        '        if (k) live[base + __popcll(b & ((1ull << t) - 1ull))] = e;',
+        '        base += __popcll(b);',
+        '      }',
+        '      if (t == 0) nlive = base;',
+        '    }',
+        '    __syncthreads();',
+        '    if (t >= X_DIM / 4) return;',
+        '    const float4* __restrict__ src = reinterpret_cast<const float4*>(gxm) + t;',
+        '    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);',
+        '    const int n = nlive;',
+        '    int i = 0;',
+        '    for (; i + 4 <= n; i += 4) {',
+        '      const int e0 = live[i], e1 = live[i + 1], e2 = live[i + 2], e3 = live[i + 3];',
+        '      const float4 v0 = src[(size_t)e0 * (X_DIM / 4)], v1 = src[(size_t)e1 * (X_DIM / 4)];',
+        '      const float4 v2 = src[(size_t)e2 * (X_DIM / 4)], v3 = src[(size_t)e3 * (X_DIM / 4)];',
+        '      acc.x += v0.x; acc.y += v0.y; acc.z += v0.z; acc.w += v0.w;',
+        '      acc.x += v1.x; acc.y += v1.y; acc.z += v1.z; acc.w += v1.w;',
+        '      acc.x += v2.x; acc.y += v2.y; acc.z += v2.z; acc.w += v2.w;',
+        '      acc.x += v3.x; acc.y += v3.y; acc.z += v3.z; acc.w += v3.w;',
+        '    }',
+        '    for (; i < n; ++i) {',
+        '      const float4 v = src[(size_t)live[i] * (X_DIM / 4)];',
+        '      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;',
+        '    }',
+        '    reinterpret_cast<float4*>(gx)[(size_t)s * (X_DIM / 4) + t] = acc;',
+        '    return;',
+        '  }',
+        '  if (t >= X_DIM / 4) return;',
         '  const float4* __restrict__ src = reinterpret_cast<const float4*>(gxm) + t;',
         '  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);',
         '  float4 acc = z;',
-        '  const int p0 = rowptr[s], p1 = rowptr[s + 1];',
         '  int p = p0;',
         '  if (mask) {',
         '    for (; p + 4 <= p1; p += 4) {',
