@@ -48,6 +48,11 @@ WC_BF16 = 1          # column groups of waves, bf16 family: the workgroup's wave
                      # 4 287.8 / 288.2 us; results bitwise equal
 NT_ATTRS = 1         # the same for skip_tp (attribute terms)
 PREFETCH_BF16 = 2    # chunks whose global loads are in flight ahead of the one being multiplied (1, 2 or 4), bf16 family
+LIN_XCD = False      # node-group-major, XCD-contiguous workgroup order (see _block_map).  Measured slower: config
+                     # 2's call 1.131-1.134 -> 1.191 ms, the 5120 -> 2048 linear 41 -> 55 us, the composed
+                     # 2048 -> 2048 26.5 -> 37.5 us.  The weight chunks are the larger stream: in the hardware's
+                     # order (blockIdx.x fastest) the workgroups running together share one (block, column group)
+                     # slice of weights in L2, while their inputs come from memory once per column group
 XPAD = 4             # floats of padding per LDS row of staged inputs
 WPAD = 8             # bf16 of padding per LDS row of staged weights
 
@@ -299,6 +304,16 @@ def pack(blocks, terms, in_blocks, wmats, V):
     return flat, base, toffs
 
 
+def _block_map():
+    """The kernel's (node group, case) from its workgroup: with LIN_XCD from the dispatch position, node-group major
+    and XCD-contiguous (``mh_xcd_block``), so that the cases of one node group, which read the same input rows, run
+    one after another on one XCD and find those rows in its L2; else (blockIdx.x, blockIdx.y)."""
+    if not LIN_XCD:
+        return ['  const int group = blockIdx.x, y = blockIdx.y;']
+    return ['  const int P = mh_xcd_block(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);',
+            '  const int group = P / gridDim.y, y = P - group * gridDim.y;']
+
+
 def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     """HIP source of one direction.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x a
     group of nodes: four waves of NT row tiles, a row tile being 16 // d whole nodes (<= 16 rows (node, m)).
@@ -535,7 +550,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         cases.append((o, fn))
     gy = _grid_y(out_blocks, CW_BF16)
     VW = (V + 31) // 32
-    sw = ['  switch (blockIdx.y) {']
+    sw = ['  switch (y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
         sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha, order); break;')
@@ -551,8 +566,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
          f'  __shared__ __align__(16) float lds[{lds_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];',
-         '  (void)amask; (void)vlist;',
-         '  const int group = blockIdx.x;'] + sw + ['}', '']
+         '  (void)amask; (void)vlist;'] + _block_map() + sw + ['}', '']
     return fns + K
 
 
@@ -748,7 +762,7 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
     gy = _grid_y(out_blocks)
     cw_max = max(_cw(mo) for mo, *_ in out_blocks)
     VW = (V + 31) // 32
-    sw = ['  switch (blockIdx.y) {']
+    sw = ['  switch (y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
         sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order, alpha); break;')
@@ -758,8 +772,7 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
          '    const int* __restrict__ order, float alpha) {',
          f'  __shared__ float red[{4 * 16 * cw_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
-         f'  __shared__ int vlist[{V + 1}];',
-         '  const int group = blockIdx.x;'] + sw + ['}', '']
+         f'  __shared__ int vlist[{V + 1}];'] + _block_map() + sw + ['}', '']
     return fns + K
 
 
