@@ -646,7 +646,7 @@ def main():
         return
     if a.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py: this build runs on one GPU only (no multi-GPU path is built; batched structures would '
-              'shard as independent units, see DESIGN.md). Run with --gpus 1.', file=sys.stderr)
+              'shard as independent units, whole structures per GPU). Run with --gpus 1.', file=sys.stderr)
         sys.exit(2)
 
     import torch
