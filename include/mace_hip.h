@@ -432,6 +432,12 @@ int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, 
                float alpha, int32_t N, void* stream);
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,
                float alpha, int32_t N, void* stream);
+/* mh_lin_fwd with a residual: out = alpha * L(x) + res, res [N, Dout] (NULL: none), the addition done in the store
+ * (rounded as a separate multiply and add, so the result equals mh_lin_fwd's output plus res computed apart).  For
+ * callers that add a tensor of the output's shape to the map's output (MACE's product block:
+ * linear(node_feats) + sc), which then needs no addition kernel of its own.  No reference counterpart. */
+int mh_lin_fwd_res(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
+                   float alpha, const float* res, int32_t N, void* stream);
 
 /* Readout head e[n] = R(x[n]) for N nodes (x [N, D], e [N], fp32): MACE's LinearReadoutBlock (e = x_s . w) or
  * NonLinearReadoutBlock (e = w2 . (c silu(x_s W1))), x_s the scalar (0e) block of the node features; the weights,

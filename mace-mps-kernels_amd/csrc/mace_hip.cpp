@@ -139,7 +139,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 40; }
+int mh_version(void) { return 41; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -716,17 +716,23 @@ int mh_readout_bwd2(mh_module* m, const float* x, const float* v, const float* g
     return launch(m, MH_READOUT_BWD2, N, args, stream, "mh_readout_bwd2");
 }
 
+int mh_lin_fwd_res(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
+                   float alpha, const float* res, int32_t N, void* stream) {
+    if (N > 0 && (!x || !W || !out)) return fail(-1, "mh_lin_fwd: NULL x, W or out");
+    void* args[] = {&x, &attrs, &W, &out, &N, &order, &alpha, &res};
+    return launch(m, MH_LIN_FWD, N, args, stream, "mh_lin_fwd");
+}
+
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
                float alpha, int32_t N, void* stream) {
-    if (N > 0 && (!x || !W || !out)) return fail(-1, "mh_lin_fwd: NULL x, W or out");
-    void* args[] = {&x, &attrs, &W, &out, &N, &order, &alpha};
-    return launch(m, MH_LIN_FWD, N, args, stream, "mh_lin_fwd");
+    return mh_lin_fwd_res(m, x, attrs, W, out, order, alpha, nullptr, N, stream);
 }
 
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,
                float alpha, int32_t N, void* stream) {
     if (N > 0 && (!g || !Wt || !gx)) return fail(-1, "mh_lin_bwd: NULL g, Wt or gx");
-    void* args[] = {&g, &attrs, &Wt, &gx, &N, &order, &alpha};
+    const float* res = nullptr;
+    void* args[] = {&g, &attrs, &Wt, &gx, &N, &order, &alpha, &res};
     return launch(m, MH_LIN_BWD, N, args, stream, "mh_lin_bwd");
 }
 

@@ -299,6 +299,13 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
                 and emb.spec.V == 0 and up.spec.V == 0 and not up._composed and emb.spec.out_blocks == up.spec.in_blocks):
             up.compose_after(emb)
             emb.pend_hint = True
+        # a residual block's product returns linear(node_feats) + sc (MACE's EquivariantProductBasisBlock with the
+        # skip connection of RealAgnosticResidualInteractionBlock): the sum runs in the linear's store
+        for blk, prod in zip(blocks, getattr(model, 'products', [])):
+            plin = getattr(prod, 'linear', None)
+            if (isinstance(plin, HipNodeLinear) and plin.spec.V == 0 and plin.div_hint is None
+                    and type(blk).__name__ == 'RealAgnosticResidualInteractionBlock'):
+                plin.pend_hint = True
     # the patched convolutions share the patched edge pass's harmonics, features and cutoff: all but one read aliases
     # with gradient slots of their own (edgefeat.slot), so that the edge pass's backward adds their gradients itself
     sh_mod = getattr(model, 'spherical_harmonics', None)

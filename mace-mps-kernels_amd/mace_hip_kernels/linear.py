@@ -340,9 +340,9 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const unsigned short* __restrict__ W, float* __restrict__ out, int N, int group, int cg,',
              '    float* __restrict__ lds, unsigned* __restrict__ amask, int* __restrict__ vlist, float alpha,',
-             '    const int* __restrict__ order) {',
+             '    const int* __restrict__ order, const float* __restrict__ res) {',
              f'  auto nd = [&](int i) {{ return {"order ? order[i] : " if V else ""}i; }};   // node of position i',
-             '  (void)alpha; (void)order;',
+             '  (void)alpha; (void)order; (void)res;',
              f'  const int g0 = group * {G};                 // first node of the workgroup',
              '  if (g0 >= N) return;',
              f'  const int ng = min({G}, N - g0);',
@@ -350,7 +350,8 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
         if not terms[o]:
             L += [f'  for (int f = t; f < ng * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D};',
-                  f'    out[(size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
+                  f'    const size_t at = (size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + j;',
+                  '    out[at] = res ? 0.f + res[at] : 0.f;',
                   '  }', '}', '']
             fns += L
             cases.append((o, fn))
@@ -542,8 +543,13 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
               '  __syncthreads();',
               f'  for (int f = t; f < ng * {CW * D // 4}; f += {BLOCK}) {{',
               f'    const int nl = f / {CW * D // 4}, j = f - nl * {CW * D // 4};',
-              f'    *reinterpret_cast<mh_f4*>(out + (size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + 4 * j) = '
-              f'*reinterpret_cast<const mh_f4*>(lds + nl * {CW * D} + 4 * j);',
+              f'    const size_t at = (size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + 4 * j;',
+              f'    mh_f4 v = *reinterpret_cast<const mh_f4*>(lds + nl * {CW * D} + 4 * j);',
+              '    if (res) {',
+              '      const mh_f4 rv = *reinterpret_cast<const mh_f4*>(res + at);',
+              '      v = mh_f4{v[0] + rv[0], v[1] + rv[1], v[2] + rv[2], v[3] + rv[3]};',
+              '    }',
+              '    *reinterpret_cast<mh_f4*>(out + at) = v;',
               '  }',
               '}', '']
         fns += L
@@ -553,7 +559,8 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     sw = ['  switch (y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha, order); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, lds, amask, vlist, alpha, order, res); '
+                  'break;')
     sw += ['    default: break;', '  }']
     lds_max = max(lds_max, 4)
     # two workgroups per CU fit the LDS; keep the registers within two waves per SIMD as well (the second prefetch
@@ -561,7 +568,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
     occ = ' __attribute__((amdgpu_waves_per_eu(2)))' if PREFETCH_BF16 > 1 else ''
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}){occ} void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const unsigned short* __restrict__ W, float* __restrict__ out, int N,',
-         '    const int* __restrict__ order, float alpha) {',
+         '    const int* __restrict__ order, float alpha, const float* __restrict__ res) {',
          '  (void)order;',
          f'  __shared__ __align__(16) float lds[{lds_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
@@ -679,8 +686,9 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
         G = WAVES * TN if tiles else TN                       # nodes per workgroup
         L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
              '    const float* __restrict__ W, float* __restrict__ out, int N, int group, int cg, float* __restrict__ red,',
-             '    unsigned* __restrict__ amask, int* __restrict__ vlist, const int* __restrict__ order, float alpha) {',
-             '  (void)alpha;',
+             '    unsigned* __restrict__ amask, int* __restrict__ vlist, const int* __restrict__ order, float alpha,',
+             '    const float* __restrict__ res) {',
+             '  (void)alpha; (void)res;',
              f'  auto nd = [&](int i) {{ return {"order ? order[i] : " if V else ""}i; }};   // node of position i',
              '  (void)order;',
              f'  const int g0 = group * {G};                 // first node of the workgroup',
@@ -690,7 +698,8 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
         if not terms[o]:
             L += [f'  for (int f = t; f < ng * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D};',
-                  f'    out[(size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + j] = 0.f;',
+                  f'    const size_t at = (size_t)nd(g0 + nl) * {Dout} + {oo} + col0 * {D} + j;',
+                  '    out[at] = res ? 0.f + res[at] : 0.f;',
                   '  }', '}', '']
             fns += L
             cases.append((o, fn))
@@ -733,12 +742,25 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
                   '      const int row = 4 * q + r;',
                   f'      if (row < nn * {D}) {{']
             if D == 1 and CT == 4 and Dout % 4 == 0 and oo % 4 == 0:
-                L += [f'        *reinterpret_cast<float4*>(out + (size_t)nd(n0 + row) * {Dout} + {oo} + col0 + 4 * c16) =',
-                      '            make_float4(alpha * acc[0][r], alpha * acc[1][r], alpha * acc[2][r], alpha * acc[3][r]);']
+                L += [f'        const size_t at = (size_t)nd(n0 + row) * {Dout} + {oo} + col0 + 4 * c16;',
+                      '        float4 v = make_float4(alpha * acc[0][r], alpha * acc[1][r], alpha * acc[2][r], '
+                      'alpha * acc[3][r]);',
+                      '        if (res) {',
+                      '          const float4 rv = *reinterpret_cast<const float4*>(res + at);',
+                      '          v = make_float4(mh_mul_add(alpha, acc[0][r], rv.x), '
+                      'mh_mul_add(alpha, acc[1][r], rv.y),',
+                      '                          mh_mul_add(alpha, acc[2][r], rv.z), '
+                      'mh_mul_add(alpha, acc[3][r], rv.w));',
+                      '        }',
+                      '        *reinterpret_cast<float4*>(out + at) = v;']
             else:
                 L += [f'        const int nl = row / {D}, m = row - nl * {D};',
-                      f'        float* __restrict__ o = out + (size_t)nd(n0 + nl) * {Dout} + {oo} + m;']
-                L += [f'        o[(col0 + {CT} * c16 + {ct}) * {D}] = alpha * acc[{ct}][r];' for ct in range(CT)]
+                      f'        const size_t ob = (size_t)nd(n0 + nl) * {Dout} + {oo} + m;',
+                      '        float* __restrict__ o = out + ob;']
+                for ct in range(CT):
+                    L += [f'        {{ const size_t at = (size_t)(col0 + {CT} * c16 + {ct}) * {D};',
+                          f'          o[at] = res ? mh_mul_add(alpha, acc[{ct}][r], res[ob + at]) : '
+                          f'alpha * acc[{ct}][r]; }}']
             L += ['      }', '    }', '  }', '}', '']
         else:
             # sum of the four waves' partial tiles, then coalesced per-node stores
@@ -752,9 +774,10 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
                   f'  for (int f = t; f < nn * {CW * D}; f += {BLOCK}) {{',
                   f'    const int nl = f / {CW * D}, j = f - nl * {CW * D}, cc = j / {D}, m = j - cc * {D};',
                   f'    const int row = nl * {D} + m;',
-                  f'    out[(size_t)nd(n0 + nl) * {Dout} + {oo} + col0 * {D} + j] = alpha * ((red[row * {CW} + cc] + '
-                  f'red[(16 + row) * {CW} + cc])',
-                  f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]));',
+                  f'    const float sum = (red[row * {CW} + cc] + red[(16 + row) * {CW} + cc])',
+                  f'        + (red[(32 + row) * {CW} + cc] + red[(48 + row) * {CW} + cc]);',
+                  f'    const size_t at = (size_t)nd(n0 + nl) * {Dout} + {oo} + col0 * {D} + j;',
+                  '    out[at] = res ? mh_mul_add(alpha, sum, res[at]) : alpha * sum;',
                   '  }',
                   '}', '']
         fns += L
@@ -765,11 +788,11 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
     sw = ['  switch (y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order, alpha); break;')
+        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order, alpha, res); break;')
     sw += ['    default: break;', '  }']
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const float* __restrict__ W, float* __restrict__ out, int N,',
-         '    const int* __restrict__ order, float alpha) {',
+         '    const int* __restrict__ order, float alpha, const float* __restrict__ res) {',
          f'  __shared__ float red[{4 * 16 * cw_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];'] + _block_map() + sw + ['}', '']
@@ -847,7 +870,7 @@ def _kernel_scalar_bwd(spec):
     L = [f'extern "C" __global__ __launch_bounds__({SCALAR_BLOCK}) void {spec.kname("lin_bwd")}('
          'const float* __restrict__ g,',
          '    const float* __restrict__ attrs, const float* __restrict__ Wt, float* __restrict__ gx, int N,',
-         '    const int* __restrict__ order, float alpha) {',
+         '    const int* __restrict__ order, float alpha, const float* __restrict__ res) {',
          '  (void)order;',
          f'  const int q0 = blockIdx.x * {NB};',
          f'  for (int idx = threadIdx.x; idx < {NB * spec.Din}; idx += {SCALAR_BLOCK}) {{',
@@ -872,13 +895,23 @@ def _kernel_scalar_bwd(spec):
                 L += [f'      for (int w = 0; w < {mo}; ++w)',
                       f'        acc = fmaf(gr[{oo} + w * {d} + m], Wt[{woff} + w * {mi} + u], acc);']
         L.append('    }')
-    L += [f'    gx[(size_t)n * {spec.Din} + k] = alpha * acc;', '  }', '}', '']
+    L += [f'    const size_t at = (size_t)n * {spec.Din} + k;',
+          '    gx[at] = res ? mh_mul_add(alpha, acc, res[at]) : alpha * acc;', '  }', '}', '']
     return L
+
+
+# alpha * x + r rounded as a separate multiply and add (what adding r to the stored alpha * x gives), never fused
+MUL_ADD = r"""
+__device__ __forceinline__ float mh_mul_add(float a, float x, float r) {
+#pragma clang fp contract(off)
+  return a * x + r;
+}
+"""
 
 
 def source(spec):
     """HIP source of ``lin_fwd`` and ``lin_bwd`` for one module."""
-    L = [_native.device_header(), '']
+    L = [_native.device_header(), MUL_ADD, '']
     if use_bf16(spec):
         L += _kernel(spec.kname('lin_fwd'), spec.in_blocks, spec.out_blocks, spec.terms, spec.V, spec.Din, spec.Dout,
                      spec.pack_fwd[1], spec.pack_fwd[2])
@@ -917,8 +950,10 @@ _DOUBLE_BACKWARD = ('mace_hip_kernels: double backward (create_graph=True, e.g. 
 
 
 class _LinFn(torch.autograd.Function):
+    """out = scale * L(x, attrs) (+ res: a tensor of the output's shape added in the kernel's store)."""
+
     @staticmethod
-    def forward(ctx, x, attrs, op, scale=1.0):
+    def forward(ctx, x, attrs, op, scale=1.0, res=None):
         s = op.spec
         if x.dtype != torch.float32 or not x.is_cuda:
             raise TypeError('mace_hip_kernels: node linears expect float32 GPU input')
@@ -942,9 +977,14 @@ class _LinFn(torch.autograd.Function):
         if a2 is not None and N > 0:
             # MACE's node_attrs is also what the symmetric contraction sorts by element: share that order
             order = element_order(attrs)[1] if attrs.dim() == 2 else node_order(a2)
-        _native.launch(f'lin_fwd[{op.tag}]', _native.load().mh_lin_fwd, op.module.handle, _native.ptr(x2),
-                       _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), _native.ptr(order), scale, N,
-                       _native.stream_of(x2))
+        r2 = None
+        if res is not None:
+            if res.shape != (*lead, s.Dout) or res.dtype != torch.float32 or res.device != x.device:
+                raise ValueError(f'a residual must be float32 [..., {s.Dout}] like the output, got {tuple(res.shape)}')
+            r2 = res.reshape(N, s.Dout).contiguous()
+        _native.launch(f'lin_fwd[{op.tag}]', _native.load().mh_lin_fwd_res, op.module.handle, _native.ptr(x2),
+                       _native.ptr(a2), _native.ptr(op.W), _native.ptr(out), _native.ptr(order), scale,
+                       _native.ptr(r2), N, _native.stream_of(x2))
         if a2 is not None:
             ctx.save_for_backward(a2, order)
         ctx.op, ctx.lead, ctx.N, ctx.scale = op, lead, N, scale
@@ -953,16 +993,17 @@ class _LinFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         # node attributes are data (MACE's one-hot element encoding): no gradient flows to them, as in the
-        # symmetric contraction
+        # symmetric contraction; the residual's gradient is g itself
+        gres = g if len(ctx.needs_input_grad) > 4 and ctx.needs_input_grad[4] else None
         if not ctx.needs_input_grad[0]:
-            return None, None, None, None
+            return None, None, None, None, gres
         op = ctx.op
         a2, order = ctx.saved_tensors if ctx.saved_tensors else (None, None)
         if torch.is_grad_enabled():          # only true under create_graph=True
             if not op.double_backward:
                 raise RuntimeError(_DOUBLE_BACKWARD)
-            return _LinAdjFn.apply(g, a2, order, op, ctx.scale, ctx.lead), None, None, None
-        return _lin_bwd(op, g, a2, order, ctx.scale, ctx.lead), None, None, None
+            return _LinAdjFn.apply(g, a2, order, op, ctx.scale, ctx.lead), None, None, None, gres
+        return _lin_bwd(op, g, a2, order, ctx.scale, ctx.lead), None, None, None, gres
 
 
 def _lin_bwd(op, g, a2, order, scale, lead):
@@ -1034,8 +1075,9 @@ class HipNodeLinear(torch.nn.Module):
         self.double_backward = False
         # set by patch_model when the caller divides the output by a constant: forward then returns a PendingLinear
         self.div_hint = None
-        # set by patch_model when the output's one consumer runs it in composed form (compose_after): forward then
-        # returns a PendingLinear (any other use forms the output)
+        # set by patch_model when the output's one consumer runs it in composed form (compose_after) or adds a
+        # tensor to it (a residual block's product: linear(node_feats) + sc): forward then returns a PendingLinear
+        # (any other use forms the output)
         self.pend_hint = False
         # set by compose_after: the linear whose scaled output this module consumes (its output is then left
         # pending through the division) and the composed map that runs instead of the two
@@ -1073,6 +1115,7 @@ class HipNodeLinear(torch.nn.Module):
 
 
 _DIVS = {torch.Tensor.__truediv__, torch.Tensor.div, torch.div, torch.true_divide}
+_ADDS = {torch.Tensor.__add__, torch.Tensor.__radd__, torch.Tensor.add, torch.add}
 
 
 class PendingLinear(Pending):
@@ -1080,8 +1123,9 @@ class PendingLinear(Pending):
     ``self.linear(message) / self.avg_num_neighbors``), times ``scale``, not yet computed.  Dividing it by a Python
     number launches the kernel with the reciprocal folded into its stores (and the backward's), so no division
     kernel runs in either direction; when a patched module consumes the quotient in composed form
-    (``HipNodeLinear.compose_after``) the quotient stays pending for it.  Any other use computes the plain output
-    first."""
+    (``HipNodeLinear.compose_after``) the quotient stays pending for it.  Adding a float32 tensor of the same shape
+    (MACE's product block: ``self.linear(node_feats) + sc``) launches the kernel with that tensor added in its
+    stores.  Any other use computes the plain output first."""
 
     @staticmethod
     def __new__(cls, x, attrs, op, scale=1.0):
@@ -1095,6 +1139,14 @@ class PendingLinear(Pending):
 
     @classmethod
     def intercept(cls, func, args, kwargs):
+        if func in _ADDS and len(args) == 2 and not kwargs:
+            a, b = args
+            if isinstance(b, PendingLinear) and not isinstance(a, Pending):
+                a, b = b, a                    # (a + b and b + a are the same float32 sum)
+            if (isinstance(a, PendingLinear) and torch.is_tensor(b) and not isinstance(b, Pending)
+                    and tuple(b.shape) == tuple(a.shape) and b.dtype == torch.float32 and b.device == a.device):
+                # MACE's product block, linear(node_feats) + sc: the sum in the linear's store
+                return _LinFn.apply(a.x, a.attrs, a.op, a.scale, b)
         if (func in _DIVS and len(args) == 2 and not kwargs and isinstance(args[0], PendingLinear)
                 and isinstance(args[1], (int, float)) and not isinstance(args[1], bool) and args[1] != 0):
             p = args[0]

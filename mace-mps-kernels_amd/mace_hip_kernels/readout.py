@@ -22,6 +22,7 @@ import numpy as np
 import torch
 
 from . import _native
+from .pending import Pending
 
 LANES = 16           # lanes per node
 BLOCK = 256          # 16 nodes per workgroup
@@ -404,4 +405,6 @@ class HipReadout(torch.nn.Module):
         return self._second
 
     def forward(self, x, heads=None):
+        if isinstance(x, Pending):
+            x = x.value()                      # formed here, under autograd, not inside the Function's forward
         return _ReadoutFn.apply(x, self)

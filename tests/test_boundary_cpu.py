@@ -253,6 +253,9 @@ def test_edge_compaction_and_row_list_argument_checks():
     assert b'mh_edge_bwd: NULL' in lib.mh_last_error()
     assert lib.mh_edge_bwd2(None, P(8), P(8), P(8), P(8), None, None, None, None, P(8), P(8), 10, None) != 0
     assert b'null module' in lib.mh_last_error()
+    # the node linear with a residual: NULL x, W or out is an error (res may be NULL)
+    assert lib.mh_lin_fwd_res(None, None, None, P(8), P(8), None, 1.0, P(8), 10, None) != 0
+    assert b'mh_lin_fwd: NULL x, W or out' in lib.mh_last_error()
 
 
 def test_species_order_fallback_on_large_tables():

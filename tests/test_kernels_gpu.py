@@ -828,6 +828,50 @@ def test_node_linear_c_abi_and_errors():
     assert b'not bound' in lib.mh_last_error()
 
 
+def test_linear_residual_in_the_store():
+    """mh_lin_fwd_res (out = alpha L(x) + res, the addition in the kernel's store) equals mh_lin_fwd's output plus
+    res added apart, bitwise, on both kernel families (fp32: the product linears and skip_tp, with attributes;
+    bf16: the 5120 -> 2048 interaction linear) and for alpha != 1; the pending output of a linear with pend_hint plus
+    a same-shape tensor runs it (either operand order), with the residual's gradient g itself and the input's the
+    plain map's; other shapes form the plain output first."""
+    dev = _dev()
+    print('[case] node linear with a residual in its store', flush=True)
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    lib, P = _native.load(), _native.ptr
+    n = 611
+    for mod in (m.products[0].linear, m.products[1].linear, m.interactions[1].skip_tp, m.interactions[1].linear):
+        op = HipNodeLinear(mod, device=dev)
+        s = op.spec
+        x = torch.randn(n, s.Din, device=dev)
+        a = torch.eye(s.V, device=dev)[torch.randint(0, s.V, (n,), device=dev)] if s.V else None
+        res = torch.randn(n, s.Dout, device=dev)
+        st = _native.stream_of(x)
+        for alpha in (1.0, 0.3):
+            plain, got = torch.empty(n, s.Dout, device=dev), torch.empty(n, s.Dout, device=dev)
+            _native.check(lib.mh_lin_fwd(op.module.handle, P(x), P(a), P(op.W), P(plain), None, alpha, n, st), 'fwd')
+            _native.check(lib.mh_lin_fwd_res(op.module.handle, P(x), P(a), P(op.W), P(got), None, alpha, P(res), n,
+                                             st), 'fwd_res')
+            torch.cuda.synchronize()
+            assert torch.equal(got, plain + res), (mod.__class__.__name__, s.Din, s.Dout, alpha)
+    op = HipNodeLinear(m.products[1].linear, device=dev)
+    x = torch.randn(n, op.spec.Din, device=dev, requires_grad=True)
+    res = torch.randn(n, op.spec.Dout, device=dev, requires_grad=True)
+    g = torch.randn(n, op.spec.Dout, device=dev)
+    plain = op(x)
+    ref = plain + res
+    gx_ref, = torch.autograd.grad(ref, x, g)
+    op.pend_hint = True
+    for order in (0, 1):
+        pend = op(x)
+        assert type(pend).__name__ == 'PendingLinear'
+        y = pend + res if order == 0 else res + pend
+        assert type(y) is torch.Tensor and torch.equal(y, ref)
+        gx, gr = torch.autograd.grad(y, (x, res), g)
+        assert torch.equal(gx, gx_ref) and torch.equal(gr, g)
+    y = op(x) + res[:1]                          # broadcast: the plain output first, then torch's add
+    assert torch.equal(y, plain + res[:1])
+
+
 def test_linear_division_folded():
     """The interaction linear's output divided by avg_num_neighbors (MACE's block code) is computed with the division
     folded into the kernels: same values and input gradient as dividing the plain output, and any other use of the

@@ -280,7 +280,9 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
     assert sym[f'lin_fwd[{comp}]'] == ['lin_fwd_i2048_o2048_v4c'], sym
     assert sym[f'lin_bwd[{comp}]'] == ['lin_bwd_i2048_o2048_v4c'], sym
     assert not any(k.endswith(('[interactions.0.linear]', '[interactions.0.skip_tp]')) for k in sym), sym
-    # the node embedding and the first block's linear_up, likewise (that block has no skip_tp)
+    # a residual block's product adds its skip connection in the linear's store (pending output + sc)
+    assert met.products[1].linear.pend_hint and not met.products[0].linear.pend_hint
+    # the node embedding and the first block's linear_up, likewise (that block's skip_tp acts on the message)
     assert sym['lin_fwd[node_embedding.linear+interactions.0.linear_up]'] == ['lin_fwd_i4_o128c'], sym
     assert not any(k.endswith(('[node_embedding.linear]', '[interactions.0.linear_up]')) for k in sym), sym
     # the two convolutions' gradients of the edge pass's shared outputs reach its backward separately, which adds them
@@ -346,6 +348,24 @@ def test_fused_edge_pass_matches_separate_kernels(monkeypatch):
     for k in loss[False]:
         a, b = loss[True][k], loss[False][k]
         assert np.abs(a - b).max() <= 1e-6 * max(np.abs(b).max(), 1e-6), k
+
+
+def test_residual_product_sum_in_the_linear():
+    """A residual block's product, linear(node_feats) + sc, runs the sum in the linear's store (pend_hint): E, F and
+    stress of config 1 bitwise equal to the same patched model adding the two apart."""
+    dev = _dev()
+    print('[case] residual product sum in the linear (config 1, stress)', flush=True)
+    model, batch, _ = factory.workload(1)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    patch_model(met, verbose=False)
+    plin = met.products[1].linear
+    assert plin.pend_hint
+    res = {}
+    for hint in (True, False):
+        plin.pend_hint = hint
+        res[hint] = _ef(met, batch, dev, torch.float32, stress=True)
+    for a, b in zip(res[True], res[False]):
+        assert np.array_equal(a, b)
 
 
 def test_unsupported_block_is_skipped():
