@@ -114,7 +114,8 @@ enum mh_kernel_kind {
     MH_EDGE_FWD = 75,    /* edge geometry, spherical harmonics and radial embedding in one pass          */
     MH_EDGE_BWD = 76,    /* the harmonics' and the embedding's backward in one pass                      */
     MH_MLP_BWD_P = 77,   /* radial MLP backward over shared rows, an edge's and its partner's gW0 summed   */
-    MH_NUM_KINDS = 78
+    MH_LIN_BWD_SUM = 78, /* node linear backward over the sum of three gradients of its output               */
+    MH_NUM_KINDS = 79
 };
 
 /* flags of mh_conv_bwd */
@@ -438,6 +439,13 @@ int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt,
  * linear(node_feats) + sc), which then needs no addition kernel of its own.  No reference counterpart. */
 int mh_lin_fwd_res(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
                    float alpha, const float* res, int32_t N, void* stream);
+/* mh_lin_bwd over the sum of three gradients of the output, gx = alpha L^T ((g + g2) + g3), the sum formed as the
+ * kernel loads them (g, g2, g3 [N, Dout], none NULL), for an output read by three consumers that each give it a
+ * gradient (MACE's product output: the readout and the next interaction block's skip_tp and linear_up).  The module
+ * binds MH_LIN_BWD_SUM to the kernel `linear.source_sum` generates (fp32 family, as MH_LIN_BWD's grid).  No
+ * reference counterpart. */
+int mh_lin_bwd_sum(mh_module* m, const float* g, const float* g2, const float* g3, const float* attrs, const void* Wt,
+                   float* gx, const int32_t* order, float alpha, int32_t N, void* stream);
 
 /* Readout head e[n] = R(x[n]) for N nodes (x [N, D], e [N], fp32): MACE's LinearReadoutBlock (e = x_s . w) or
  * NonLinearReadoutBlock (e = w2 . (c silu(x_s W1))), x_s the scalar (0e) block of the node features; the weights,

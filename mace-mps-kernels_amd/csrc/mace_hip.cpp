@@ -139,7 +139,7 @@ extern "C" {
 
 const char* mh_last_error(void) { return g_err.c_str(); }
 
-int mh_version(void) { return 41; }
+int mh_version(void) { return 42; }
 
 int mh_launch_log(int enable) {
     std::lock_guard<std::mutex> lock(g_log_mu);
@@ -726,6 +726,14 @@ int mh_lin_fwd_res(mh_module* m, const float* x, const float* attrs, const void*
 int mh_lin_fwd(mh_module* m, const float* x, const float* attrs, const void* W, float* out, const int32_t* order,
                float alpha, int32_t N, void* stream) {
     return mh_lin_fwd_res(m, x, attrs, W, out, order, alpha, nullptr, N, stream);
+}
+
+int mh_lin_bwd_sum(mh_module* m, const float* g, const float* g2, const float* g3, const float* attrs, const void* Wt,
+                   float* gx, const int32_t* order, float alpha, int32_t N, void* stream) {
+    if (N > 0 && (!g || !g2 || !g3 || !Wt || !gx)) return fail(-1, "mh_lin_bwd_sum: NULL g, g2, g3, Wt or gx");
+    const float* res = nullptr;
+    void* args[] = {&g, &attrs, &Wt, &gx, &N, &order, &alpha, &res, &g2, &g3};
+    return launch(m, MH_LIN_BWD_SUM, N, args, stream, "mh_lin_bwd_sum");
 }
 
 int mh_lin_bwd(mh_module* m, const float* g, const float* attrs, const void* Wt, float* gx, const int32_t* order,

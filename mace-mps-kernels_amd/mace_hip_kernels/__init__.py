@@ -30,7 +30,7 @@ import torch
 
 from .conv import HipConvTP, conv_supported
 from .edge import HipSphericalHarmonics, sh_supported
-from .linear import HipNodeLinear, lin_supported
+from .linear import HipNodeLinear, lin_supported, use_bf16 as _lin_bf16
 from .radial import HipRadialMLP, mlp_supported
 from .embedding import HipRadialEmbedding, emb_supported
 from .layout import HipReshapeIrreps, reshape_supported
@@ -306,6 +306,20 @@ def patch_model(model, conv=True, symmetric=True, verbose=True, spherical_harmon
             if (isinstance(plin, HipNodeLinear) and plin.spec.V == 0 and plin.div_hint is None
                     and type(blk).__name__ == 'RealAgnosticResidualInteractionBlock'):
                 plin.pend_hint = True
+        # a product's output read by three patched consumers (its readout and the next residual block's skip_tp and
+        # linear_up): two of them read aliases with gradient slots of their own, and the product linear's backward
+        # adds the three gradients as it loads them (lin_bwds) instead of autograd adding them in two kernels
+        prods, heads = list(getattr(model, 'products', [])), list(getattr(model, 'readouts', []))
+        for i, prod in enumerate(prods[:-1]):
+            plin = getattr(prod, 'linear', None)
+            nxt = blocks[i + 1] if i + 1 < len(blocks) else None
+            cons = [heads[i] if i < len(heads) else None, getattr(nxt, 'skip_tp', None),
+                    getattr(nxt, 'linear_up', None)]
+            if (isinstance(plin, HipNodeLinear) and plin.spec.V == 0 and not plin.pend_hint and plin.div_hint is None
+                    and plin.compose_into is None and plin.spec.tiled_bwd and not _lin_bf16(plin.spec, True)
+                    and type(nxt).__name__ == 'RealAgnosticResidualInteractionBlock'
+                    and isinstance(cons[0], HipReadout) and all(isinstance(c, HipNodeLinear) for c in cons[1:])):
+                plin.slots = 2
     # the patched convolutions share the patched edge pass's harmonics, features and cutoff: all but one read aliases
     # with gradient slots of their own (edgefeat.slot), so that the edge pass's backward adds their gradients itself
     sh_mod = getattr(model, 'spherical_harmonics', None)

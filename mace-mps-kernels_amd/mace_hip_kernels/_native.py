@@ -27,9 +27,9 @@ MH_CONV_FWD, MH_CONV_BWD, MH_CONV_BWD_WY, MH_SC_FWD, MH_SC_BWD, MH_CONV_BWD_R, M
     MH_SC_BWD_SI, MH_NL_SETUP, MH_NL_ZERO, MH_NL_BINS, MH_NL_SCAN, MH_NL_PLACE, MH_NL_COUNT, MH_NL_OFFSETS, \
     MH_NL_FILL, MH_SPECIES_ORDER, MH_MLP_JVP, MH_MLP_BWD2, MH_GEOM_SEGSUM, MH_NL_BASES, MH_EDGE_COUNT, \
     MH_EDGE_PLACE, MH_GEOM_SEGSUM1, MH_EDGE_PAIR, MH_CONV_FWD_CR, MH_MLP_H3, MH_MLP_OUT, MH_EDGE_FWD, \
-    MH_EDGE_BWD, MH_MLP_BWD_P = range(78)
+    MH_EDGE_BWD, MH_MLP_BWD_P, MH_LIN_BWD_SUM = range(79)
 MH_WANT_GX, MH_WANT_GWY, MH_CUT_MASKED, MH_CUT_NOZERO = 1, 2, 4, 8
-ABI_VERSION = 41
+ABI_VERSION = 42
 
 # hipcc/hipRTC options for every generated layer: gfx950 code, -O3, and packed-FP32 instructions disabled.
 ARCH = os.environ.get('MACE_HIP_ARCH', 'gfx950')
@@ -63,6 +63,7 @@ _SIGS = {
     'mh_lin_fwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, ctypes.c_int, _P]),
     'mh_lin_bwd': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, ctypes.c_int, _P]),
     'mh_lin_fwd_res': (ctypes.c_int, [_P] * 6 + [ctypes.c_float, _P, ctypes.c_int, _P]),
+    'mh_lin_bwd_sum': (ctypes.c_int, [_P] * 8 + [ctypes.c_float, ctypes.c_int, _P]),
     'mh_readout_fwd': (ctypes.c_int, [_P] * 3 + [ctypes.c_int64, _P]),
     'mh_readout_bwd': (ctypes.c_int, [_P] * 4 + [ctypes.c_int64, _P]),
     'mh_mlp_fwd': (ctypes.c_int, [_P] * 5 + [ctypes.c_int64, _P]),

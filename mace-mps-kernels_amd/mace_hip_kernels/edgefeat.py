@@ -14,13 +14,12 @@ gradient and dL/dlengths from the embedding's, in one pass (the statements of ``
 Outputs left on a tensor are taken only by the module they were made for, only once, and only while the tensor is
 unmodified (same version); any other call computes as before.
 """
-import weakref
-
 import torch
 
 from . import _native
 from . import edge as _edge
 from . import embedding as _emb
+from .pending import set_slots, slot  # noqa: F401  (slot: the joint node's aliases, handed out)
 
 BLOCK = 256
 FUSE = True            # run the three forwards (and the two backwards) as one pass where a model allows it
@@ -199,13 +198,6 @@ class _EdgeFeatFn(torch.autograd.Function):
         return gv, gl.reshape(ln.shape), None, None
 
 
-def slot(t):
-    """``t``, or the next alias of it that the joint node left for another patched consumer (same storage and
-    version counter, an output of its own, so that this consumer's gradient reaches the node separately)."""
-    s = getattr(t, '_mh_slots', None)
-    if s is None or s[0] != t._version or not s[1]:
-        return t
-    return s[1].pop(0)
 
 
 def take_harmonics(sh_op, vec):
@@ -221,12 +213,9 @@ def take_harmonics(sh_op, vec):
     nslot = max(0, int(getattr(sh_op, 'slots', 0)))
     outs = _EdgeFeatFn.apply(vec, ln, made, nslot)
     Y, feats, cut = outs[:3]
-    for k, t in enumerate((Y, feats, cut)):
-        if nslot:
-            aliases = list(outs[3 + k::3])
-            for a in aliases:
-                a._mh_base = weakref.ref(t)        # (weak: no reference cycle through t's own stash)
-            t._mh_slots = (t._version, aliases)
+    if nslot:
+        for k, t in enumerate((Y, feats, cut)):
+            set_slots(t, outs[3 + k::3])
     ln._mh_emb = (made[1], feats, cut, ln._version)
     return Y
 

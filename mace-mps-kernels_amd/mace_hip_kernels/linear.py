@@ -31,7 +31,7 @@ import torch
 
 from . import _native
 from .symmetric import element_order
-from .pending import Pending
+from .pending import Pending, set_slots, slot
 
 KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
 CW_BF16 = 64         # output columns per workgroup of the bf16 family (64 or 128)
@@ -590,8 +590,9 @@ def _nodes_per_group(terms_o, in_blocks, V, l):
     return WAVES * tn if (terms_o and _tiles_mode(terms_o, in_blocks, V)) else tn
 
 
-def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH):
+def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH, nsum=1):
     """Register loads of chunk c of term i: A (x, times the attribute) and B (weights) in MFMA lane layout.
+    With ``nsum`` = 3, A is the sum (x + x2) + x3 of three inputs of x's shape, added as loaded.
 
     K order inside a chunk: lane group kq takes k = k0 + 8 kq + st at step st, so a lane's 8 values of x are
     consecutive (two float4 loads for scalars); column order inside a group of 16 columns: lane c16 takes the CT
@@ -600,7 +601,8 @@ def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH):
     vsel = f'vlist[1 + c / {NCH}]' if V else '0'
     vecx = D == 1 and Din % 4 == 0 and oi % 4 == 0 and mi % 8 == 0
     wt = {4: 'float4', 2: 'float2', 1: 'float'}[CT]
-    L = [f'__device__ __forceinline__ void {fn}_ld{i}(const float* __restrict__ x, const float* __restrict__ attr,',
+    xs3 = 'const float* __restrict__ x2, const float* __restrict__ x3, ' if nsum > 1 else ''
+    L = [f'__device__ __forceinline__ void {fn}_ld{i}(const float* __restrict__ x, {xs3}const float* __restrict__ attr,',
          '    const float* __restrict__ W, const int* __restrict__ vlist, const int* __restrict__ order, int n0, int col0,',
          '    int anl, int am,'
          f'    int q, int c16, int c, float (&ra)[{KC // 4}], float (&rb)[{KC // 4}][{CT}]) {{',
@@ -613,8 +615,15 @@ def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH):
     if vecx:
         # mi % 8 == 0: the lane's 8 channels are all in range or all out of range
         L += [f'  const bool okx = k0 < {mi};',
-              f'  const float4* __restrict__ xv = reinterpret_cast<const float4*>(xr + (okx ? k0 : 0));',
-              '  const float4 x0 = xv[0], x1 = xv[1];',
+              f'  const float4* __restrict__ xv = reinterpret_cast<const float4*>(xr + (okx ? k0 : 0));']
+        if nsum > 1:
+            L += [f'  const size_t xo = (size_t)nr * {Din} + {oi} + am + (okx ? k0 : 0);',
+                  '  const float4* __restrict__ xv2 = reinterpret_cast<const float4*>(x2 + xo);',
+                  '  const float4* __restrict__ xv3 = reinterpret_cast<const float4*>(x3 + xo);',
+                  '  const float4 x0 = (xv[0] + xv2[0]) + xv3[0], x1 = (xv[1] + xv2[1]) + xv3[1];']
+        else:
+            L += ['  const float4 x0 = xv[0], x1 = xv[1];']
+        L += [
               '  const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};']
     L += ['#pragma unroll',
           f'  for (int st = 0; st < {KC // 4}; ++st) {{',
@@ -624,8 +633,12 @@ def _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH):
     if vecx:
         L.append(f'    ra[st] = okx ? xs[st]{" * s" if V else ""} : 0.f;')
     else:
-        L += [f'    const float xa = xr[kc * {D}];',
-              f'    ra[st] = ok ? xa{" * s" if V else ""} : 0.f;']
+        if nsum > 1:
+            L += [f'    const size_t xo = (size_t)nr * {Din} + {oi} + am + (size_t)kc * {D};',
+                  f'    const float xa = (xr[kc * {D}] + x2[xo]) + x3[xo];']
+        else:
+            L += [f'    const float xa = xr[kc * {D}];']
+        L += [f'    ra[st] = ok ? xa{" * s" if V else ""} : 0.f;']
     L += [f'    const {wt} wv = *reinterpret_cast<const {wt}*>(W + {woff} + ((size_t)kc * {VV} + v) * {mo} + col0'
           f' + {CT} * c16);']
     comps = ['x', 'y', 'z', 'w'][:CT] if CT > 1 else [None]
@@ -662,7 +675,7 @@ def _kloop(ld, CT, first, step, count, ind):
     return L
 
 
-def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
+def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout, nsum=1):
     """HIP source of one direction on the fp32 matrix cores.  blockIdx.y selects (output block o, column group of CW channels), blockIdx.x a
     group of nodes.  A tile is TN = 16 // d whole nodes, i.e. <= 16 rows (node, m) — one MFMA row tile — and CW
     channels.  Each block runs in one of two modes (``_tiles_mode``):
@@ -674,8 +687,11 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
 
     K is walked in chunks c = (active attribute v, 32 input channels); operands are loaded straight into registers
     in the MFMA lane layout (16x16x4: lane (i, kq) = (lane % 16, lane / 16) holds A[i][4s + kq] and B[4s + kq][16 ct
-    + i]) with the next chunk in flight."""
+    + i]) with the next chunk in flight.  With ``nsum`` = 3 the input is the sum (x + x2) + x3 of three tensors of
+    its shape, added as loaded (``lin_bwds``: a backward over three consumers' gradients)."""
     fns, cases = [], []
+    xs3 = 'const float* __restrict__ x2, const float* __restrict__ x3, ' if nsum > 1 else ''
+    xa3 = 'x2, x3, ' if nsum > 1 else ''
     for o, (mo, l, oo, _) in enumerate(out_blocks):
         D = 2 * l + 1
         TN = ROWS // D
@@ -684,7 +700,7 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
         fn = f'{name}_b{o}'
         tiles = bool(terms[o]) and _tiles_mode(terms[o], in_blocks, V)
         G = WAVES * TN if tiles else TN                       # nodes per workgroup
-        L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, const float* __restrict__ attr,',
+        L = [f'__device__ __forceinline__ void {fn}(const float* __restrict__ x, {xs3}const float* __restrict__ attr,',
              '    const float* __restrict__ W, float* __restrict__ out, int N, int group, int cg, float* __restrict__ red,',
              '    unsigned* __restrict__ amask, int* __restrict__ vlist, const int* __restrict__ order, float alpha,',
              '    const float* __restrict__ res) {',
@@ -725,8 +741,8 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
             assert li == l
             NCH = -(-mi // KC)
             nchunks = f'nact * {NCH}' if V else f'{NCH}'
-            fns += _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH)
-            ld = f'{fn}_ld{i}(x, attr, W, vlist, order, nb, col0, anl, am, q, c16'
+            fns += _loader(fn, i, in_blocks, mi, oi, D, Din, V, woff, mo, CT, NCH, nsum)
+            ld = f'{fn}_ld{i}(x, {xa3}attr, W, vlist, order, nb, col0, anl, am, q, c16'
             if tiles:
                 L += ['  if (wlive) {', f'    const int nch = {nchunks};']
                 L += _kloop(ld, CT, '0', 1, 'nch', '    ')
@@ -788,11 +804,13 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout):
     sw = ['  switch (y) {']
     for y, (o, cg) in enumerate(gy):
         fn = dict(cases)[o]
-        sw.append(f'    case {y}: {fn}(x, attr, W, out, N, group, {cg}, red, amask, vlist, order, alpha, res); break;')
+        sw.append(f'    case {y}: {fn}(x, {xa3}attr, W, out, N, group, {cg}, red, amask, vlist, order, alpha, res); '
+                  'break;')
     sw += ['    default: break;', '  }']
     K = [f'extern "C" __global__ __launch_bounds__({BLOCK}) void {name}(const float* __restrict__ x,',
          '    const float* __restrict__ attr, const float* __restrict__ W, float* __restrict__ out, int N,',
-         '    const int* __restrict__ order, float alpha, const float* __restrict__ res) {',
+         '    const int* __restrict__ order, float alpha, const float* __restrict__ res'
+         + (', const float* __restrict__ x2, const float* __restrict__ x3' if nsum > 1 else '') + ') {',
          f'  __shared__ float red[{4 * 16 * cw_max}];',
          f'  __shared__ unsigned amask[{max(VW, 1)}];',
          f'  __shared__ int vlist[{V + 1}];'] + _block_map() + sw + ['}', '']
@@ -909,6 +927,14 @@ __device__ __forceinline__ float mh_mul_add(float a, float x, float r) {
 """
 
 
+def source_sum(spec):
+    """HIP source of ``lin_bwds``: ``lin_bwd`` of an fp32-family module over the sum of three gradients (its output
+    read by three consumers, each with a gradient slot of its own)."""
+    return '\n'.join([_native.device_header(), MUL_ADD, ''] +
+                     _kernel_f32(spec.kname('lin_bwds'), spec.out_blocks, spec.in_blocks, spec.bterms, spec.V,
+                                 spec.Dout, spec.Din, nsum=3))
+
+
 def source(spec):
     """HIP source of ``lin_fwd`` and ``lin_bwd`` for one module."""
     L = [_native.device_header(), MUL_ADD, '']
@@ -1006,6 +1032,40 @@ class _LinFn(torch.autograd.Function):
         return _lin_bwd(op, g, a2, order, ctx.scale, ctx.lead), None, None, None, gres
 
 
+class _LinSlotsFn(torch.autograd.Function):
+    """``_LinFn`` whose output also comes as ``nslot`` aliases (``set_slots``: the same storage, outputs of their
+    own), one for each further consumer: the consumers' gradients reach this node separately and, three of them,
+    are added by the backward kernel as it loads them (``mh_lin_bwd_sum``: (g + g2) + g3, in slot order) instead of
+    by autograd in kernels of their own."""
+
+    @staticmethod
+    def forward(ctx, x, attrs, op, nslot):
+        out = _LinFn.forward(ctx, x, attrs, op)
+        return (out, *[out.detach() for _ in range(nslot)])
+
+    @staticmethod
+    def backward(ctx, g, *extra):
+        none = (None, None, None, None)
+        gs = [t for t in (g, *extra) if t is not None]
+        if not ctx.needs_input_grad[0] or not gs:
+            return none
+        op = ctx.op
+        a2, order = ctx.saved_tensors if ctx.saved_tensors else (None, None)
+        if torch.is_grad_enabled() or len(gs) != 3:
+            total = gs[0]
+            for t in gs[1:]:
+                total = total + t
+            return (_LinFn.backward(ctx, total)[0], None, None, None)
+        s = op.spec
+        g3 = [t.reshape(-1, s.Dout).contiguous() for t in gs]
+        N = g3[0].shape[0]
+        gx = torch.empty(N, s.Din, device=g.device, dtype=torch.float32)
+        P = _native.ptr
+        _native.launch(f'lin_bwd[{op.tag}+sum]', _native.load().mh_lin_bwd_sum, op.sum_module().handle, P(g3[0]),
+                       P(g3[1]), P(g3[2]), P(a2), P(op.Wt), P(gx), P(order), ctx.scale, N, _native.stream_of(g3[0]))
+        return gx.reshape(*ctx.lead, s.Din), None, None, None
+
+
 def _lin_bwd(op, g, a2, order, scale, lead):
     """The input gradient L^T g [*lead, Din] of g [*lead, Dout] by the backward kernel."""
     s = op.spec
@@ -1084,6 +1144,25 @@ class HipNodeLinear(torch.nn.Module):
         self.compose_into = None
         self.compose_from = None
         self._composed = []
+        # set by patch_model when the output is read by three patched consumers (MACE's product output: the readout
+        # and the next block's skip_tp and linear_up): forward then leaves two aliases of the output for them
+        # (gradient slots of their own) and the backward adds the three gradients as it loads them (lin_bwds)
+        self.slots = 0
+        self._sum_module = None
+
+    def sum_module(self):
+        """The module of ``lin_bwds`` (the backward over three gradients), compiled on first use; fp32 family with
+        a tiled backward only."""
+        s = self.spec
+        if not s.tiled_bwd or use_bf16(s, True):
+            raise RuntimeError('lin_bwds is built for the fp32 family with a tiled backward only')
+        if self._sum_module is None:
+            code = _native.compile_source(source_sum(s))
+            with torch.cuda.device(self.Wt.device):
+                self._sum_module = _native.Module(code, {_native.MH_LIN_BWD_SUM: (
+                    s.kname('lin_bwds'), BLOCK, _f32_nodes_per_launch_group(s.in_blocks, s.bterms, s.out_blocks, s.V),
+                    len(_grid_y(s.in_blocks, 64)))})
+        return self._sum_module
 
     def compose_after(self, first):
         """Consume ``first``'s output in composed form: when this module is called on the pending output of
@@ -1109,8 +1188,13 @@ class HipNodeLinear(torch.nn.Module):
             return _LinFn.apply(x.x, attrs, op, x.scale)
         if isinstance(x, Pending):
             x = x.value()                      # formed here, under autograd, not inside _LinFn's forward
+        x = slot(x)
         if (self.div_hint is not None or self.pend_hint) and x.dtype == torch.float32:
             return PendingLinear(x, attrs, self)
+        if self.slots and x.dtype == torch.float32:
+            outs = _LinSlotsFn.apply(x, attrs, self, self.slots)
+            set_slots(outs[0], outs[1:])
+            return outs[0]
         return _LinFn.apply(x, attrs, self)
 
 

@@ -60,3 +60,21 @@ def stash_owner(t):
     ref = getattr(t, '_mh_base', None)
     base = ref() if ref is not None else None
     return t if base is None else base
+
+
+def set_slots(t, aliases):
+    """Leave ``aliases`` of ``t`` (outputs of the same autograd node, each a gradient slot of its own) for the next
+    consumers that call ``slot(t)``."""
+    import weakref
+    for a in aliases:
+        a._mh_base = weakref.ref(t)            # (weak: no reference cycle through t's own stash)
+    t._mh_slots = (t._version, list(aliases))
+
+
+def slot(t):
+    """``t``, or the next alias of it left by ``set_slots`` (same storage and version counter, an output of its own
+    node, so that this consumer's gradient reaches the node separately); ``t`` itself once none is left."""
+    s = getattr(t, '_mh_slots', None)
+    if s is None or s[0] != t._version or not s[1]:
+        return t
+    return s[1].pop(0)

@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import _native
-from .pending import Pending
+from .pending import Pending, slot
 
 LANES = 16           # lanes per node
 BLOCK = 256          # 16 nodes per workgroup
@@ -407,4 +407,4 @@ class HipReadout(torch.nn.Module):
     def forward(self, x, heads=None):
         if isinstance(x, Pending):
             x = x.value()                      # formed here, under autograd, not inside the Function's forward
-        return _ReadoutFn.apply(x, self)
+        return _ReadoutFn.apply(slot(x), self)

@@ -256,6 +256,8 @@ def test_edge_compaction_and_row_list_argument_checks():
     # the node linear with a residual: NULL x, W or out is an error (res may be NULL)
     assert lib.mh_lin_fwd_res(None, None, None, P(8), P(8), None, 1.0, P(8), 10, None) != 0
     assert b'mh_lin_fwd: NULL x, W or out' in lib.mh_last_error()
+    assert lib.mh_lin_bwd_sum(None, P(8), None, P(8), None, P(8), P(8), None, 1.0, 10, None) != 0
+    assert b'mh_lin_bwd_sum: NULL' in lib.mh_last_error()
 
 
 def test_species_order_fallback_on_large_tables():

@@ -872,6 +872,30 @@ def test_linear_residual_in_the_store():
     assert torch.equal(y, plain + res[:1])
 
 
+def test_linear_backward_over_three_gradients():
+    """mh_lin_bwd_sum (lin_bwds: the backward over (g + g2) + g3, added as loaded) equals mh_lin_bwd on that sum
+    formed apart, bitwise, for the fp32-family product linear; NULL gradients are rejected."""
+    dev = _dev()
+    print('[case] node linear backward over three gradients', flush=True)
+    m = factory.make_model('128x0e+128x1o', 3, 3, elements=factory.ELEMENTS_PTCOH)
+    op = HipNodeLinear(m.products[0].linear, device=dev)
+    s = op.spec
+    lib, P = _native.load(), _native.ptr
+    for n in (611, 5):
+        g = [torch.randn(n, s.Dout, device=dev) for _ in range(3)]
+        got, want = torch.empty(n, s.Din, device=dev), torch.empty(n, s.Din, device=dev)
+        st = _native.stream_of(g[0])
+        _native.check(lib.mh_lin_bwd_sum(op.sum_module().handle, P(g[0]), P(g[1]), P(g[2]), None, P(op.Wt), P(got),
+                                         None, 1.0, n, st), 'bwd_sum')
+        tot = (g[0] + g[1]) + g[2]
+        _native.check(lib.mh_lin_bwd(op.module.handle, P(tot), None, P(op.Wt), P(want), None, 1.0, n, st), 'bwd')
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), n
+    assert lib.mh_lin_bwd_sum(op.sum_module().handle, P(g[0]), None, P(g[2]), None, P(op.Wt), P(got), None, 1.0, 5,
+                              st) != 0
+    assert b'NULL' in lib.mh_last_error()
+
+
 def test_linear_division_folded():
     """The interaction linear's output divided by avg_num_neighbors (MACE's block code) is computed with the division
     folded into the kernels: same values and input gradient as dividing the plain output, and any other use of the

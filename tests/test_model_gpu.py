@@ -282,6 +282,9 @@ def test_patched_model_launches_the_fast_paths(fuse, monkeypatch):
     assert not any(k.endswith(('[interactions.0.linear]', '[interactions.0.skip_tp]')) for k in sym), sym
     # a residual block's product adds its skip connection in the linear's store (pending output + sc)
     assert met.products[1].linear.pend_hint and not met.products[0].linear.pend_hint
+    # the first product's output has three patched consumers: its backward adds their gradients as it loads them
+    assert met.products[0].linear.slots == 2
+    assert 'lin_bwd[products.0.linear+sum]' in sym and 'lin_bwd[products.0.linear]' not in sym, sym
     # the node embedding and the first block's linear_up, likewise (that block's skip_tp acts on the message)
     assert sym['lin_fwd[node_embedding.linear+interactions.0.linear_up]'] == ['lin_fwd_i4_o128c'], sym
     assert not any(k.endswith(('[node_embedding.linear]', '[interactions.0.linear_up]')) for k in sym), sym
@@ -366,6 +369,36 @@ def test_residual_product_sum_in_the_linear():
         res[hint] = _ef(met, batch, dev, torch.float32, stress=True)
     for a, b in zip(res[True], res[False]):
         assert np.array_equal(a, b)
+
+
+def test_product_output_gradient_slots():
+    """The first product's output read by three patched consumers through gradient slots (the product linear's
+    backward adds the three gradients as it loads them) against the same model summing them through autograd: E, F
+    and stress of config 1 within 1e-6 relative (the sum's order differs), and a force loss's position gradient under
+    double_backward (where the slots' gradients are summed by torch)."""
+    dev = _dev()
+    print('[case] product output gradient slots (config 1, stress; force loss)', flush=True)
+    model, batch, _ = factory.workload(1)
+    met = copy.deepcopy(model).to(dev, torch.float32)
+    patch_model(met, verbose=False)
+    plin = met.products[0].linear
+    assert plin.slots == 2
+    res = {}
+    for k in (2, 0):
+        plin.slots = k
+        res[k] = _ef(met, batch, dev, torch.float32, stress=True)
+    for a, b in zip(res[2], res[0]):
+        assert np.abs(a - b).max() <= 1e-6 * max(np.abs(b).max(), 1e-6), (np.abs(a - b).max(), np.abs(b).max())
+    dbl = copy.deepcopy(model).to(dev, torch.float32)
+    patch_model(dbl, verbose=False, double_backward=True)
+    small = D.batch_graphs([D.graph_of(factory.make_structure(seed=9), 5.0)], factory.ELEMENTS_REF)
+    loss = {}
+    for k in (2, 0):
+        dbl.products[0].linear.slots = k
+        loss[k] = _force_loss(dbl, small, dev, torch.float32, wrt_positions=True)
+    for key in loss[0]:
+        a, b = loss[2][key], loss[0][key]
+        assert np.abs(a - b).max() <= 1e-6 * max(np.abs(b).max(), 1e-6), key
 
 
 def test_unsupported_block_is_skipped():
