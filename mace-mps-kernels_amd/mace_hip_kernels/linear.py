@@ -53,6 +53,11 @@ LIN_XCD = False      # node-group-major, XCD-contiguous workgroup order (see _bl
                      # 2048 -> 2048 26.5 -> 37.5 us.  The weight chunks are the larger stream: in the hardware's
                      # order (blockIdx.x fastest) the workgroups running together share one (block, column group)
                      # slice of weights in L2, while their inputs come from memory once per column group
+TILES_MIN_CHUNKS = 8 # fp32 family: K chunks (32 input channels of one attribute) from which a block runs one tile per
+                     # wave over the whole K loop instead of splitting K over the workgroup's waves.  Config 2's E+F
+                     # call with 4 (the 128-channel maps on one tile per wave; two alternating runs each): the
+                     # 512 -> 512 forward 13.8 -> 16.5-21.6 us, lin_bwds 17.4 -> 20.4 us, all linears 242-244 ->
+                     # 253-269 us per call; results within the same parity
 XPAD = 4             # floats of padding per LDS row of staged inputs
 WPAD = 8             # bf16 of padding per LDS row of staged weights
 
@@ -582,7 +587,7 @@ def _kernel(name, in_blocks, out_blocks, terms, V, Din, Dout, base, toffs):
 def _tiles_mode(terms_o, in_blocks, V):
     """One tile per wave with the whole K loop (long K: the pipeline hides the load latency), or one tile per
     workgroup with K split over the waves (short K, or attribute terms: more waves in flight)."""
-    return V == 0 and sum(-(-in_blocks[i][0] // KC) for i, _ in terms_o) >= 8
+    return V == 0 and sum(-(-in_blocks[i][0] // KC) for i, _ in terms_o) >= TILES_MIN_CHUNKS
 
 
 def _nodes_per_group(terms_o, in_blocks, V, l):
