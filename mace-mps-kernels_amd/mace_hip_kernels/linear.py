@@ -35,6 +35,8 @@ from .pending import Pending, set_slots, slot
 
 KC = 32              # K per chunk: one bf16 MFMA step (input channels u of one attribute v)
 CW_BF16 = 64         # output columns per workgroup of the bf16 family (64 or 128)
+CW_F32 = 64          # and of the fp32 family (32 or 64).  Config 2's E+F call with 32 (two alternating runs each):
+                     # 1.118 -> 1.136-1.138 ms, the 512 -> 512 forward 14 -> 16 us, lin_bwds 17.4 -> 25.5 us
 BF16_MIN_OUT = 1024  # outputs (inputs, backward) from which a direction runs on the bf16 family (the config-2 call
                      # measured 2 us slower with the 512-wide maps on it, 4 us with every map)
 BLOCK = 256          # 4 waves
@@ -700,7 +702,7 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout, nsum=1):
     for o, (mo, l, oo, _) in enumerate(out_blocks):
         D = 2 * l + 1
         TN = ROWS // D
-        CW = _cw(mo)
+        CW = _cw(mo, CW_F32)
         CT = CW // 16
         fn = f'{name}_b{o}'
         tiles = bool(terms[o]) and _tiles_mode(terms[o], in_blocks, V)
@@ -803,8 +805,8 @@ def _kernel_f32(name, in_blocks, out_blocks, terms, V, Din, Dout, nsum=1):
                   '}', '']
         fns += L
         cases.append((o, fn))
-    gy = _grid_y(out_blocks)
-    cw_max = max(_cw(mo) for mo, *_ in out_blocks)
+    gy = _grid_y(out_blocks, CW_F32)
+    cw_max = max(_cw(mo, CW_F32) for mo, *_ in out_blocks)
     VW = (V + 31) // 32
     sw = ['  switch (y) {']
     for y, (o, cg) in enumerate(gy):
@@ -1117,11 +1119,11 @@ class HipNodeLinear(torch.nn.Module):
                         _f32_nodes_per_launch_group(blocks, terms, in_blocks, s.V))
             kernels = {_native.MH_LIN_FWD: (s.kname('lin_fwd'), BLOCK,
                                             group(s.out_blocks, s.terms, s.in_blocks, use_bf16(s)),
-                                            len(_grid_y(s.out_blocks, CW_BF16 if use_bf16(s) else 64)))}
+                                            len(_grid_y(s.out_blocks, CW_BF16 if use_bf16(s) else CW_F32)))}
             if s.tiled_bwd:
                 kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), BLOCK,
                                                group(s.in_blocks, s.bterms, s.out_blocks, use_bf16(s, True)),
-                                               len(_grid_y(s.in_blocks, CW_BF16 if use_bf16(s, True) else 64)))
+                                               len(_grid_y(s.in_blocks, CW_BF16 if use_bf16(s, True) else CW_F32)))
             else:
                 kernels[_native.MH_LIN_BWD] = (s.kname('lin_bwd'), SCALAR_BLOCK, _scalar_nodes(s))
             self.module = _native.Module(code, kernels)
@@ -1166,7 +1168,7 @@ class HipNodeLinear(torch.nn.Module):
             with torch.cuda.device(self.Wt.device):
                 self._sum_module = _native.Module(code, {_native.MH_LIN_BWD_SUM: (
                     s.kname('lin_bwds'), BLOCK, _f32_nodes_per_launch_group(s.in_blocks, s.bterms, s.out_blocks, s.V),
-                    len(_grid_y(s.in_blocks, 64)))})
+                    len(_grid_y(s.in_blocks, CW_F32)))})
         return self._sum_module
 
     def compose_after(self, first):
