@@ -320,3 +320,49 @@ def test_grad_needed_follows_the_engine():
     seen.clear()
     torch.autograd.grad(Probe.apply(a, p * 3).sum(), [a])
     assert seen == [(True, False)]
+
+
+def test_grad_needed_without_the_engine_query(monkeypatch):
+    """A torch without the engine query answers conservatively: every input gradient autograd asks for counts as
+    needed, and the gradients are still right (host logic, CPU)."""
+    monkeypatch.delattr(torch._C, '_will_engine_execute_node')
+    seen = []
+
+    class Probe(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, a, b):
+            ctx.save_for_backward(a, b)
+            return a * b
+
+        @staticmethod
+        def backward(ctx, g):
+            a, b = ctx.saved_tensors
+            seen.append((conv._grad_needed(ctx, 0), conv._grad_needed(ctx, 1)))
+            return g * b, g * a
+
+    x, p = torch.randn(3, requires_grad=True), torch.randn(3, requires_grad=True)
+    (gp,) = torch.autograd.grad(Probe.apply(x * 2, p * 3).sum(), [p])
+    assert seen == [(True, True)]                       # the unused branch is computed, not skipped
+    assert torch.allclose(gp, 3 * (x * 2).detach())
+    seen.clear()
+    Probe.apply(torch.randn(3), p * 3).sum().backward()
+    assert seen == [(False, True)]                      # needs_input_grad still decides first
+
+
+def test_factored_weights_or_the_plain_path():
+    """``W0 * cutoff`` is read from its autograd node; any other producer, or a node whose saved tensors are gone,
+    keeps the plain path (None) instead of failing (host logic, CPU)."""
+    E, nw = 5, 8
+    W0 = torch.randn(E, nw, requires_grad=True)
+    cut = torch.rand(E, 1, requires_grad=True)
+    W = W0 * cut
+    got = conv._factored_weights(W)
+    assert got is not None and torch.equal(got[0], W0) and torch.equal(got[1], cut)
+    assert conv._factored_weights(cut.reshape(E, 1) * W0) is not None          # either operand order
+    assert conv._factored_weights(W0 * 2.0) is None                          # scalar product
+    assert conv._factored_weights(W0 + cut) is None                          # another op
+    assert conv._factored_weights(W0.detach() * cut.detach()) is None        # no graph
+    assert conv._factored_weights(W0 * torch.rand(E, nw)) is None            # factor of the wrong shape
+    W2 = W0 * cut
+    W2.sum().backward()                                                      # saved tensors freed
+    assert conv._factored_weights(W2) is None
